@@ -1,0 +1,79 @@
+/*
+ * C-ABI of the MI355X (gfx950) chunked delta-rule backward library
+ * (librewy_hip.so).  Plain device pointers, sizes and a hipStream_t; no torch
+ * types.  Every entry point validates its arguments, enqueues work on `stream`,
+ * allocates nothing, and returns hipSuccess or the first HIP error.
+ *
+ * Layouts are FLA's T-major layouts, which the reference keeps:
+ *   q, k, w, qg, kg         bf16  [B, T, H, K]
+ *   v, v_new, dO, dR, dv    bf16  [B, T, H, V]
+ *   Aqk, Akk                fp32  [B, T, H, 64]   (row t holds row t mod 64 of its chunk)
+ *   h, dh (per chunk)       bf16  [B, T/64, H, K, V]
+ *   h0, dht, dh0            fp32  [B, H, K, V]
+ *   g (vector gate)         fp32  [B, T, H, K]    chunk-local cumsum in log2 units
+ *   g (scalar gate)         fp32  [B, T, H]       chunk-local cumsum in log2 units
+ *   beta                    fp32  [B, T, H]
+ *   b_gate / w_gate (GDN2)  bf16  [B, T, H, K] / [B, T, H, V]
+ * Supported shapes: K = V = 128, chunk = 64, T a positive multiple of 64.
+ * gate_mode: 0 = none (DeltaNet), 1 = scalar (GDN), 2 = vector (KDA, GDN2).
+ */
+#ifndef REWY_AMD_H
+#define REWY_AMD_H
+
+#include <hip/hip_runtime.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Reverse inter-chunk state recurrence.
+ * Replaces FLA chunk_gated_delta_rule_bwd_dhu(q,k,w,do,dv,g,gk,h0,dht,scale,...)
+ * -> (dh, dh0, dr) as called at reference src/fast_delta_rule/backends/backward.py:120-121,
+ * and ReWY's state_bwd (src/fast_delta_rule/kernels/vector_state_gpu.py:47-67).
+ *
+ * For gate_mode 2, q/k are the gate-weighted qg = q*exp2(g) and
+ * kg = k*exp2(g_last - g) (vector_state_gpu.py:1-6); for modes 0/1 they are the
+ * raw q/k and the kernel applies the scalar gate.  Exactly one of `aqk`
+ * (dv_local = Aqk^T dO is then formed in-kernel, FLA chunk_kda_bwd_dAv) or `dv`
+ * (a precomputed dv_local, FLA chunk_bwd_dv_local) must be non-null.
+ * dht and dh0 may be null.  value_block = 0 picks the value-tile width.
+ */
+hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const float* g,
+                         int gate_mode, const void* dO, const float* aqk, const void* dv,
+                         const float* dht, void* dh, void* dr, float* dh0, int B, int T, int H,
+                         int K, int V, int chunk, float scale, int value_block,
+                         hipStream_t stream);
+
+/*
+ * Chunk-parallel backward: residual-WY products (P = A^T dR, D, E-bar),
+ * dAqk, matrix intra, gate/beta epilogue and the in-chunk reverse cumsum of dg,
+ * one work-group per (chunk, head).
+ * Replaces, at the seams of reference backends/backward.py:18-25,44-49,
+ *   chunk_kda_bwd_wy_dqkg_fused  -> LocalBetaResidual (kernels/kda_residual_local_beta.py:8-23)
+ *   chunk_kda_bwd_intra          -> EndpointMatrixIntra (kernels/endpoint_intra.py:300-326)
+ *   chunk_gdn2_bwd_wy_dqkg_fused -> gdn2_consumer_fp32.residual (kernels/gdn2_consumer_fp32.py:76-86)
+ *   chunk_gdn2_bwd_intra         -> gdn2_consumer_fp32.matrix_intra (:89-98)
+ *   scalar_liveness_gpu.adjoint  (kernels/scalar_liveness_gpu.py:87-102, GDN/DeltaNet)
+ * and the dAqk output of FLA chunk_kda_bwd_dAv.
+ *
+ * Scalar-beta families pass beta/dbeta and null b_gate/w_gate/db/dw; GDN2
+ * passes b_gate/w_gate/db/dw (bf16) and null beta/dbeta.  Outputs dq, dk, dv
+ * (bf16) and db/dw (bf16) are the final gradients; dg (fp32, same shape as g)
+ * is the gradient of the raw per-token gate (natural-log units), i.e. after the
+ * in-chunk reverse cumsum.  dbeta (fp32) follows the reference's branch rule:
+ * sum_v(P*v_new)/beta where |beta| >= 1e-6, the direct VJP otherwise
+ * (kernels/kda_residual_tri_beta.py:50-60, kda_residual_local_beta_consumer.py:161-180).
+ */
+hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v, const void* v_new,
+                         const void* dO, const void* dR, const float* g, int gate_mode,
+                         const float* beta, const void* b_gate, const void* w_gate,
+                         const float* Akk, const void* h, const void* dh, void* dq, void* dk,
+                         void* dv, float* dg, float* dbeta, void* db, void* dw, int B, int T,
+                         int H, int K, int V, int chunk, float scale, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* REWY_AMD_H */

@@ -1,0 +1,360 @@
+// Reverse inter-chunk state recurrence of the chunked delta-rule backward.
+//
+// Replaces FLA's chunk_gated_delta_rule_bwd_dhu (called at reference
+// backends/backward.py:120-121 and inside chunk_kda_bwd) and ReWY's
+// vector_state_gpu.state_kernel (kernels/vector_state_gpu.py:12-43).  Per
+// (batch, head, value tile) and for chunk c = NT-1 .. 0:
+//
+//   dh_out[c] = dh                                   (bf16)
+//   dR_c      = kg_c dh + dv_local_c                 (bf16),  dv_local_c = Aqk_c^T dO_c
+//   dh        = diag(lambda_c) dh + scale qg_c^T dO_c - w_c^T dR_c
+//
+// and dh0 = dh at the end (fp32).  dh is a 128 x BV fp32 tile held in
+// accumulator registers for the whole sequence; every per-chunk operand is
+// staged in LDS in K-contiguous layout so that all contractions run on
+// v_mfma_f32_16x16x32_bf16.  Operands of the next chunk are fetched into
+// registers while the current chunk computes.
+#include "common.hpp"
+
+namespace rewy {
+
+enum GateMode { GATE_NONE = 0, GATE_SCALAR = 1, GATE_VECTOR = 2 };
+
+template <int BV, int GATE, bool DV_FROM_AQK>
+struct StateSmem {
+  static constexpr int LDK = KD + 8;   // pitch of [.][K] tiles
+  static constexpr int LDT = C + 8;    // pitch of [.][T] tiles
+  bf16 k[C][LDK];          // kg rows: A operand of kg * dh        (contraction over K)
+  bf16 qT[KD][LDT];        // qg^T:    A operand of qg^T dO         (contraction over T)
+  bf16 wT[KD][LDT];        // -w^T:    A operand of -w^T dR         (contraction over T)
+  bf16 aTh[C][LDT];        // Aqk^T hi: A operand of Aqk^T dO       (contraction over S)
+  bf16 aTl[C][LDT];        // Aqk^T lo
+  bf16 doT[BV][LDT];       // dO^T:    B operand (contraction over T)
+  bf16 dhT[BV][LDK];       // dh^T:    B operand of kg * dh
+  bf16 drT[BV][LDT];       // dR^T:    B operand of -w^T dR
+  float lam[KD];           // exp2(g_last) per key row
+  float gam[C];            // scalar gate: exp2(g_t)
+  float gkf[C];            // scalar gate: exp2(g_last - g_t)
+};
+
+template <int BV, int GATE, bool DV_FROM_AQK>
+__global__ __launch_bounds__(256) void state_bwd_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ w,
+    const float* __restrict__ g, const bf16* __restrict__ dO, const float* __restrict__ aqk,
+    const bf16* __restrict__ dv, const float* __restrict__ dht, bf16* __restrict__ dh_out,
+    bf16* __restrict__ dr_out, float* __restrict__ dh0, int T, int H, float scale) {
+  using S = StateSmem<BV, GATE, DV_FROM_AQK>;
+  __shared__ S sm;
+  constexpr int NVT = VD / BV;
+  constexpr int NCT = BV / 16;             // column tiles of the state
+  const int logical = xcd_logical_block();
+  const int vt = logical % NVT;
+  const int bh = logical / NVT;
+  const int b = bh / H, h = bh % H;
+  const int NT = T / C;
+  const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
+  const int v_base = vt * BV;
+
+  // ---- state accumulators: wave wv owns key rows [32 wv, 32 wv + 32) ----
+  f32x4 st[2][NCT];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      f32x4 a = zero4();
+      if (dht) {
+        const float* src = dht + (size_t)bh * KD * VD;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int kr = 32 * wv + 16 * rt + 4 * (l >> 4) + r;
+          a[r] = src[kr * VD + v_base + 16 * ct + (l & 15)];
+        }
+      }
+      st[rt][ct] = a;
+    }
+
+  // ---- register staging of one chunk's operands ----
+  // q/k/w: 64 rows x 128 bf16 = 1024 16-byte pieces -> 4 per thread
+  // Aqk:   64 rows x 64 fp32  = 1024 16-byte pieces -> 4 per thread
+  // dO:    64 rows x BV bf16  = 8*BV pieces          -> BV/32 per thread
+  constexpr int NDO = (C * BV / 8) / 256 > 0 ? (C * BV / 8) / 256 : 1;
+  uint4 rq[4], rk[4], rw[4], ra[4], rdo[NDO];
+  float rg_last = 0.f, rg_tok = 0.f;
+  const size_t row_stride_k = (size_t)H * KD;   // elements between tokens
+  const size_t row_stride_v = (size_t)H * VD;
+
+  auto load_chunk = [&](int c) {
+    const size_t tok0 = (size_t)b * T + (size_t)c * C;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + 256 * i;
+      const int t = p >> 4, k0 = (p & 15) * 8;
+      const size_t off = (tok0 + t) * row_stride_k + (size_t)h * KD + k0;
+      rq[i] = *reinterpret_cast<const uint4*>(q + off);
+      rk[i] = *reinterpret_cast<const uint4*>(k + off);
+      rw[i] = *reinterpret_cast<const uint4*>(w + off);
+      if constexpr (DV_FROM_AQK) {
+        const int s = p >> 4, t0 = (p & 15) * 4;
+        ra[i] = *reinterpret_cast<const uint4*>(aqk + ((tok0 + s) * H + h) * C + t0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NDO; ++i) {
+      const int p = tid + 256 * i;
+      if (p < C * BV / 8) {
+        const int t = p / (BV / 8), v0 = (p % (BV / 8)) * 8;
+        const size_t off = (tok0 + t) * row_stride_v + (size_t)h * VD + v_base + v0;
+        rdo[i] = *reinterpret_cast<const uint4*>(dO + off);
+      }
+    }
+    if constexpr (GATE == GATE_VECTOR) {
+      if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
+    } else if constexpr (GATE == GATE_SCALAR) {
+      if (tid < C) rg_tok = g[(tok0 + tid) * H + h];
+      rg_last = g[(tok0 + C - 1) * H + h];
+    }
+  };
+
+  // dv (precomputed dv_local) is added straight from global into the dR tile.
+  auto stage_chunk = [&]() {
+    if constexpr (GATE == GATE_VECTOR) {
+      if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
+    } else if constexpr (GATE == GATE_SCALAR) {
+      if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
+      if (tid < C) {
+        sm.gam[tid] = fast_exp2(rg_tok);
+        sm.gkf[tid] = fast_exp2(rg_last - rg_tok);
+      }
+    } else {
+      if (tid < KD) sm.lam[tid] = 1.f;
+    }
+    if constexpr (GATE == GATE_SCALAR) __syncthreads();  // gam / lam needed below
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + 256 * i;
+      const int t = p >> 4, k0 = (p & 15) * 8;
+      const bf16* pq = reinterpret_cast<const bf16*>(&rq[i]);
+      const bf16* pk = reinterpret_cast<const bf16*>(&rk[i]);
+      const bf16* pw = reinterpret_cast<const bf16*>(&rw[i]);
+      if constexpr (GATE == GATE_SCALAR) {
+        const float gq = sm.gam[t];
+        const float gk = sm.gkf[t];
+        bf16x8 kk;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          sm.qT[k0 + j][t] = to_bf16(to_f32(pq[j]) * gq);
+          kk[j] = to_bf16(to_f32(pk[j]) * gk);
+        }
+        *reinterpret_cast<bf16x8*>(&sm.k[t][k0]) = kk;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sm.qT[k0 + j][t] = pq[j];
+        *reinterpret_cast<uint4*>(&sm.k[t][k0]) = rk[i];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sm.wT[k0 + j][t] = to_bf16(-to_f32(pw[j]));
+      if constexpr (DV_FROM_AQK) {
+        const int s = p >> 4, t0 = (p & 15) * 4;
+        const float* pa = reinterpret_cast<const float*>(&ra[i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          bf16 hi, lo;
+          split_bf16(pa[j], hi, lo);
+          sm.aTh[t0 + j][s] = hi;
+          sm.aTl[t0 + j][s] = lo;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NDO; ++i) {
+      const int p = tid + 256 * i;
+      if (p < C * BV / 8) {
+        const int t = p / (BV / 8), v0 = (p % (BV / 8)) * 8;
+        const bf16* pd = reinterpret_cast<const bf16*>(&rdo[i]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sm.doT[v0 + j][t] = pd[j];
+      }
+    }
+  };
+
+  load_chunk(NT - 1);
+  for (int c = NT - 1; c >= 0; --c) {
+    __syncthreads();                       // previous chunk done with every LDS tile
+    stage_chunk();
+    if (c > 0) load_chunk(c - 1);          // prefetch; consumed next iteration
+    // dh (state at the end of chunk c) -> LDS, transposed, bf16
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        bf16x4 v4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[rt][ct][r]);
+        *reinterpret_cast<bf16x4*>(&sm.dhT[16 * ct + (l & 15)][32 * wv + 16 * rt + 4 * (l >> 4)]) = v4;
+      }
+    __syncthreads();
+
+    // X = qg^T dO (independent of dh)
+    f32x4 xq[2][NCT];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        f32x4 a = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          a = mfma(frag(&sm.qT[32 * wv + 16 * rt][32 * ks], S::LDT), frag(&sm.doT[16 * ct][32 * ks], S::LDT), a);
+        xq[rt][ct] = a;
+      }
+    // dR tile rows [16 wv, 16 wv + 16): kg dh + Aqk^T dO (+ dv)
+    f32x4 dr[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      f32x4 a = zero4();
+      if constexpr (DV_FROM_AQK) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const bf16x8 bo = frag(&sm.doT[16 * ct][32 * ks], S::LDT);
+          a = mfma(frag(&sm.aTh[16 * wv][32 * ks], S::LDT), bo, a);
+          a = mfma(frag(&sm.aTl[16 * wv][32 * ks], S::LDT), bo, a);
+        }
+      } else {
+        const size_t tok0 = (size_t)b * T + (size_t)c * C;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * wv + 4 * (l >> 4) + r;
+          a[r] = to_f32(dv[(tok0 + t) * row_stride_v + (size_t)h * VD + v_base + 16 * ct + (l & 15)]);
+        }
+      }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        a = mfma(frag(&sm.k[16 * wv][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), a);
+      dr[ct] = a;
+    }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      bf16x4 v4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v4[r] = to_bf16(dr[ct][r]);
+      *reinterpret_cast<bf16x4*>(&sm.drT[16 * ct + (l & 15)][16 * wv + 4 * (l >> 4)]) = v4;
+    }
+    __syncthreads();
+
+    // dh <- lambda * dh + scale * X - w^T dR
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        f32x4 a;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int kr = 32 * wv + 16 * rt + 4 * (l >> 4) + r;
+          a[r] = st[rt][ct][r] * sm.lam[kr] + scale * xq[rt][ct][r];
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          a = mfma(frag(&sm.wT[32 * wv + 16 * rt][32 * ks], S::LDT), frag(&sm.drT[16 * ct][32 * ks], S::LDT), a);
+        st[rt][ct] = a;
+      }
+
+    // global stores of dh[c] and dR_c from the transposed LDS copies
+    {
+      const size_t dh_base = (((size_t)b * NT + c) * H + h) * KD * VD;
+      constexpr int NP = KD * BV / 8;
+      for (int p = tid; p < NP; p += 256) {
+        const int kr = p / (BV / 8), v0 = (p % (BV / 8)) * 8;
+        bf16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = sm.dhT[v0 + j][kr];
+        *reinterpret_cast<bf16x8*>(dh_out + dh_base + (size_t)kr * VD + v_base + v0) = o;
+      }
+      const size_t tok0 = (size_t)b * T + (size_t)c * C;
+      constexpr int NR = C * BV / 8;
+      for (int p = tid; p < NR; p += 256) {
+        const int t = p / (BV / 8), v0 = (p % (BV / 8)) * 8;
+        bf16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = sm.drT[v0 + j][t];
+        *reinterpret_cast<bf16x8*>(dr_out + (tok0 + t) * row_stride_v + (size_t)h * VD + v_base + v0) = o;
+      }
+    }
+  }
+
+  if (dh0) {
+    float* dst = dh0 + (size_t)bh * KD * VD;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int kr = 32 * wv + 16 * rt + 4 * (l >> 4) + r;
+          dst[kr * VD + v_base + 16 * ct + (l & 15)] = st[rt][ct][r];
+        }
+  }
+}
+
+template <int BV, int GATE, bool AQK>
+static hipError_t launch_state(const void* q, const void* k, const void* w, const float* g,
+                               const void* dO, const float* aqk, const void* dv, const float* dht,
+                               void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
+                               hipStream_t stream) {
+  const int grid = B * H * (VD / BV);
+  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK>), dim3(grid), dim3(256), 0, stream,
+                     (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk,
+                     (const bf16*)dv, dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale);
+  return hipGetLastError();
+}
+
+template <int GATE, bool AQK>
+static hipError_t pick_bv(int bv, const void* q, const void* k, const void* w, const float* g,
+                          const void* dO, const float* aqk, const void* dv, const float* dht,
+                          void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
+                          hipStream_t s) {
+  switch (bv) {
+    case 16: return launch_state<16, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s);
+    case 32: return launch_state<32, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s);
+    case 64: return launch_state<64, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace rewy
+
+using namespace rewy;
+
+// Value-tile width chosen so that the grid fills the chip: the recurrence is
+// sequential over chunks, so parallelism is B*H*(V/BV) work-groups.
+static int default_bv(int B, int H) {
+  const int bh = B * H;
+  if (bh * 2 >= 256) return 64;
+  if (bh * 4 >= 256) return 32;
+  return 16;
+}
+
+extern "C" hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const float* g,
+                                    int gate_mode, const void* dO, const float* aqk, const void* dv,
+                                    const float* dht, void* dh, void* dr, float* dh0, int B, int T,
+                                    int H, int K, int V, int chunk, float scale, int value_block,
+                                    hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0)
+    return hipErrorInvalidValue;
+  if (!q || !k || !w || !dO || !dh || !dr) return hipErrorInvalidValue;
+  if ((aqk == nullptr) == (dv == nullptr)) return hipErrorInvalidValue;
+  if (gate_mode != GATE_NONE && g == nullptr) return hipErrorInvalidValue;
+  const int bv = value_block > 0 ? value_block : default_bv(B, H);
+  const bool from_aqk = aqk != nullptr;
+  switch (gate_mode) {
+    case GATE_NONE:
+      return from_aqk ? pick_bv<GATE_NONE, true>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream)
+                      : pick_bv<GATE_NONE, false>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream);
+    case GATE_SCALAR:
+      return from_aqk ? pick_bv<GATE_SCALAR, true>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream)
+                      : pick_bv<GATE_SCALAR, false>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream);
+    case GATE_VECTOR:
+      return from_aqk ? pick_bv<GATE_VECTOR, true>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream)
+                      : pick_bv<GATE_VECTOR, false>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}

@@ -1,0 +1,129 @@
+"""Host wrappers of the HIP entry points: validate, allocate outputs, launch on
+the current stream.
+
+Each wrapper checks dtype, device, contiguity and shape of every operand on
+the host before anything is enqueued, so a launch never sees an operand the
+kernel's indexing does not assume.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+GATE_NONE, GATE_SCALAR, GATE_VECTOR = 0, 1, 2
+K_SUPPORTED = V_SUPPORTED = 128
+CHUNK = 64
+
+
+def _need(x, name, dtype, shape, device):
+    if x is None:
+        raise ValueError(f"{name} is required")
+    if x.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {x.dtype}")
+    if tuple(x.shape) != tuple(shape):
+        raise ValueError(f"{name}: expected shape {tuple(shape)}, got {tuple(x.shape)}")
+    if x.device != device:
+        raise ValueError(f"{name}: expected device {device}, got {x.device}")
+    if not x.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return x
+
+
+def _dims(q):
+    if q.ndim != 4:
+        raise ValueError("q must be [B,T,H,K]")
+    B, T, H, K = q.shape
+    if K != K_SUPPORTED:
+        raise ValueError(f"K must be {K_SUPPORTED}")
+    if T <= 0 or T % CHUNK:
+        raise ValueError(f"T must be a positive multiple of {CHUNK}")
+    if q.device.type != "cuda":
+        raise ValueError("HIP backward requires a GPU tensor")
+    return B, T, H, K
+
+
+def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, want_dh0=True,
+              value_block=0):
+    """Reverse state recurrence.  Returns (dh [B,NT,H,K,V] bf16, dR [B,T,H,V] bf16, dh0 fp32|None)."""
+    B, T, H, K = _dims(q)
+    V = V_SUPPORTED
+    dev = q.device
+    bf, f32 = torch.bfloat16, torch.float32
+    for x, n in ((q, "q"), (k, "k"), (w, "w")):
+        _need(x, n, bf, (B, T, H, K), dev)
+    _need(dO, "dO", bf, (B, T, H, V), dev)
+    if gate_mode == GATE_VECTOR:
+        _need(g, "g", f32, (B, T, H, K), dev)
+    elif gate_mode == GATE_SCALAR:
+        _need(g, "g", f32, (B, T, H), dev)
+    elif gate_mode != GATE_NONE:
+        raise ValueError("gate_mode must be 0, 1 or 2")
+    if (aqk is None) == (dv is None):
+        raise ValueError("exactly one of aqk / dv is required")
+    if aqk is not None:
+        _need(aqk, "Aqk", f32, (B, T, H, CHUNK), dev)
+    if dv is not None:
+        _need(dv, "dv", bf, (B, T, H, V), dev)
+    if dht is not None:
+        _need(dht, "dht", f32, (B, H, K, V), dev)
+    if value_block not in (0, 16, 32, 64):
+        raise ValueError("value_block must be 0, 16, 32 or 64")
+    NT = T // CHUNK
+    dh = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
+    dr = torch.empty(B, T, H, V, device=dev, dtype=bf)
+    dh0 = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_dh0 else None
+    P = _lib.ptr
+    st = _lib.load().fdr_state_bwd(P(q), P(k), P(w), P(g), int(gate_mode), P(dO), P(aqk), P(dv),
+                                   P(dht), P(dh), P(dr), P(dh0), B, T, H, K, V, CHUNK,
+                                   float(scale), int(value_block), _lib.stream_handle(dev))
+    _lib.check(st, "fdr_state_bwd")
+    return dh, dr, dh0
+
+
+def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None, b=None, w=None):
+    """Fused residual-WY + matrix-intra + epilogue stage.
+
+    Returns dict(dq, dk, dv [bf16], dg [fp32, gate shape] | None, dbeta [fp32] | None,
+    db, dw [bf16] | None)."""
+    B, T, H, K = _dims(q)
+    V = V_SUPPORTED
+    dev = q.device
+    bf, f32 = torch.bfloat16, torch.float32
+    NT = T // CHUNK
+    for x, n in ((q, "q"), (k, "k")):
+        _need(x, n, bf, (B, T, H, K), dev)
+    for x, n in ((v, "v"), (v_new, "v_new"), (dO, "dO"), (dR, "dR")):
+        _need(x, n, bf, (B, T, H, V), dev)
+    _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
+    _need(h, "h", bf, (B, NT, H, K, V), dev)
+    _need(dh, "dh", bf, (B, NT, H, K, V), dev)
+    vec_b = b is not None
+    if vec_b:
+        if gate_mode != GATE_VECTOR:
+            raise ValueError("vector erase/write gates require a vector decay gate")
+        _need(b, "b", bf, (B, T, H, K), dev)
+        _need(w, "w", bf, (B, T, H, V), dev)
+    else:
+        _need(beta, "beta", f32, (B, T, H), dev)
+    if gate_mode == GATE_VECTOR:
+        _need(g, "g", f32, (B, T, H, K), dev)
+    elif gate_mode == GATE_SCALAR:
+        _need(g, "g", f32, (B, T, H), dev)
+    elif gate_mode != GATE_NONE:
+        raise ValueError("gate_mode must be 0, 1 or 2")
+    out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=bf),
+               dk=torch.empty(B, T, H, K, device=dev, dtype=bf),
+               dv=torch.empty(B, T, H, V, device=dev, dtype=bf),
+               dg=torch.empty_like(g) if gate_mode != GATE_NONE else None,
+               dbeta=None if vec_b else torch.empty(B, T, H, device=dev, dtype=f32),
+               db=torch.empty(B, T, H, K, device=dev, dtype=bf) if vec_b else None,
+               dw=torch.empty(B, T, H, V, device=dev, dtype=bf) if vec_b else None)
+    P = _lib.ptr
+    st = _lib.load().fdr_chunk_bwd(P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), int(gate_mode),
+                                   P(beta), P(b), P(w), P(Akk), P(h), P(dh), P(out["dq"]),
+                                   P(out["dk"]), P(out["dv"]), P(out["dg"]), P(out["dbeta"]),
+                                   P(out["db"]), P(out["dw"]), B, T, H, K, V, CHUNK, float(scale),
+                                   _lib.stream_handle(dev))
+    _lib.check(st, "fdr_chunk_bwd")
+    return out
