@@ -1,0 +1,221 @@
+"""Autograd contract and public ``chunk_*`` operators for both backends.
+
+One autograd Function serves the four families.  Its forward is this
+package's chunked forward (``rewy_amd.forward``) and saves FLA's tensor list
+(reference ``_compat/kda.py:120-144``: q, k, v, g_cumsum, beta, Aqk, Akk and,
+under full saving, w, u, qg, kg, v_new, h).  Its backward is chosen when the
+forward runs and stays bound to the Function afterwards (reference
+``docs/architecture.md``: "Its own autograd Function permanently selects its
+backward"):
+
+* ``optimized`` -> ``rewy_amd.backends.backward`` (HIP kernels, no fallback);
+* ``original``  -> ``rewy_amd.original.original_backward`` (PyTorch ops).
+
+The public functions keep the reference's signatures (``_compat/kda.py:214``,
+``_compat/gdn.py`` ``chunk_gated_delta_rule``, ``_compat/gdn2.py:205``,
+``_compat/delta.py``) and argument checks; options outside this build's
+envelope raise ``NotImplementedError``.
+"""
+from __future__ import annotations
+
+import torch
+
+from ..forward import chunk_forward
+
+
+def _l2norm(x, eps=1e-6):
+    xf = x.float()
+    return (xf * torch.rsqrt((xf * xf).sum(-1, keepdim=True) + eps)).to(x.dtype)
+
+
+class ChunkFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w,
+                initial_state):
+        o, final, sv = chunk_forward(op, q, k, v, g=g, beta=beta, b=b, w=w,
+                                     initial_state=initial_state, scale=scale,
+                                     output_final_state=output_final_state)
+        keep = full_saving and op in ("kda", "gdn2")
+        ctx.save_for_backward(q, k, v, sv["gc"], beta, b, w, sv["Aqk"], sv["Akk"], initial_state,
+                              *(sv[n] if keep else None for n in ("w", "u", "qg", "kg", "v_new", "h")))
+        ctx.op, ctx.backend, ctx.scale = op, backend, scale
+        ctx.g_dtype = None if g is None else g.dtype
+        ctx.has_h0 = initial_state is not None
+        return o, final
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        (q, k, v, gc, beta, b, w, Aqk, Akk, h0, w_wy, u_wy, qg, kg, v_new, h) = ctx.saved_tensors
+        op, scale = ctx.op, ctx.scale
+        if ctx.backend == "optimized":
+            from ..backends import backward as bw
+            if op == "kda":
+                dq, dk, dv, db, dg, dh0, _, _ = bw.kda_backward(
+                    q=q, k=k, v=v, beta=beta, Aqk=Aqk, Akk=Akk, scale=scale, initial_state=h0,
+                    do=do, dht=dht, g=gc, w=w_wy, u=u_wy, qg=qg, kg=kg, v_new=v_new, h=h)
+                dw = None
+            elif op == "gdn2":
+                dq, dk, dv, db, dw, dg, dh0, _, _ = bw.gdn2_backward(
+                    q=q, k=k, v=v, b=b, w_gate=w, Aqk=Aqk, Akk=Akk, scale=scale, initial_state=h0,
+                    do=do, dht=dht, g=gc, w_wy=w_wy, u_wy=u_wy, qg=qg, kg=kg, v_new=v_new, h=h)
+            elif op == "gdn":
+                dq, dk, dv, db, dg, dh0, _, _ = bw.gdn_backward(
+                    q=q, k=k, v=v, g=gc, beta=beta, A=Akk, scale=scale, initial_state=h0, do=do, dht=dht)
+                dw = None
+            else:
+                dq, dk, dv, db, dh0 = bw.delta_backward(
+                    q=q, k=k, v=v, beta=beta, A=Akk, scale=scale, initial_state=h0, do=do, dht=dht)
+                dg = dw = None
+        else:
+            from ..original import original_backward
+            saved = None if h is None else dict(w=w_wy, u=u_wy, qg=qg, kg=kg, v_new=v_new, h=h)
+            out = original_backward(op, q, k, v, gc, Akk, scale, h0, do, dht, beta=beta, b=b, w=w,
+                                    Aqk=Aqk if op in ("kda", "gdn2") else None, saved=saved)
+            dq, dk, dv, dg, dh0 = out["dq"], out["dk"], out["dv"], out["dg"], out["dh0"]
+            db = out["db"] if op == "gdn2" else out["dbeta"]
+            dw = out["dw"]
+        if not ctx.has_h0:
+            dh0 = None
+        cast = lambda x, ref: None if x is None or ref is None else x.to(ref.dtype)
+        gb = cast(db, b if op == "gdn2" else beta)
+        return (None, None, None, None, None, cast(dq, q), cast(dk, k), cast(dv, v),
+                None if dg is None else dg.to(ctx.g_dtype),
+                None if op == "gdn2" else gb, gb if op == "gdn2" else None, cast(dw, w), dh0)
+
+
+def _unsupported(name, **flags):
+    for key, value in flags.items():
+        if value:
+            raise NotImplementedError(f"{name}: {key} is not supported by this build")
+
+
+def _pad_time(xs, T):
+    """Zero-pad the time axis of [B,T,...] tensors up to a multiple of 64.  Zero
+    keys/values/gates leave the state untouched, so outputs of real tokens are
+    unchanged (used by the original backend for arbitrary T)."""
+    Tp = (T + 63) // 64 * 64
+    if Tp == T:
+        return xs, T
+    out = []
+    for x in xs:
+        if x is None:
+            out.append(None)
+            continue
+        pad = [0, 0] * (x.ndim - 2) + [0, Tp - T]
+        out.append(torch.nn.functional.pad(x, pad))
+    return out, Tp
+
+
+def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0):
+    T = q.shape[1]
+    if backend == "original" and T % 64:
+        (q, k, v, g, beta, b, w), _ = _pad_time((q, k, v, g, beta, b, w), T)
+        o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state,
+                                       q, k, v, g, beta, b, w, h0)
+        return o[:, :T], final
+    return ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g,
+                               beta, b, w, h0)
+
+
+def make_kda(backend):
+    def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=False,
+                  use_qk_l2norm_in_kernel=False, use_gate_in_kernel=False,
+                  use_beta_sigmoid_in_kernel=False, allow_neg_eigval=False, safe_gate=False,
+                  lower_bound=None, disable_recompute=False, return_intermediate_states=False,
+                  state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None, cp_context=None,
+                  use_graph=False, max_num_seqs=None, **kwargs):
+        """Kimi Delta Attention (per-channel vector gate); reference _compat/kda.py:214."""
+        _unsupported("chunk_kda", use_gate_in_kernel=use_gate_in_kernel, safe_gate=safe_gate,
+                     return_intermediate_states=return_intermediate_states,
+                     state_v_first=state_v_first, cu_seqlens=cu_seqlens is not None,
+                     cp_context=cp_context is not None, use_graph=use_graph)
+        if kwargs.get("chunk_size", 64) != 64:
+            raise ValueError("`chunk_size` must be 64 for this build")
+        if allow_neg_eigval and not use_beta_sigmoid_in_kernel:
+            raise ValueError("`allow_neg_eigval=True` requires `use_beta_sigmoid_in_kernel=True`.")
+        if initial_state is not None:
+            assert initial_state.dtype == torch.float32, "initial_state must be in float32."
+        B, T, H, K = q.shape
+        assert q.shape == k.shape, f"q and k must have the same shape, got q={q.shape} vs k={k.shape}"
+        assert g.shape == (B, T, H, K), f"g must have shape [B, T, H, K], got {list(g.shape)}"
+        assert beta.shape == (B, T, H), f"beta must have shape [B, T, H], got {list(beta.shape)}"
+        if use_qk_l2norm_in_kernel:
+            q, k = _l2norm(q), _l2norm(k)
+        if use_beta_sigmoid_in_kernel:
+            beta = beta.sigmoid() * (2.0 if allow_neg_eigval else 1.0)
+        scale = K ** -0.5 if scale is None else scale
+        return _apply("kda", backend, disable_recompute, scale, output_final_state, q, k, v, g, beta,
+                      None, None, initial_state)
+    return chunk_kda
+
+
+def make_gdn(backend):
+    def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
+                               output_final_state=False, use_qk_l2norm_in_kernel=False,
+                               use_beta_sigmoid_in_kernel=False, allow_neg_eigval=False,
+                               state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None,
+                               chunk_indices=None, cp_context=None, **kwargs):
+        """Gated DeltaNet (scalar gate); reference _compat/gdn.py chunk_gated_delta_rule."""
+        _unsupported("chunk_gated_delta_rule", state_v_first=state_v_first,
+                     cu_seqlens=cu_seqlens is not None, cp_context=cp_context is not None,
+                     use_gate_in_kernel=kwargs.get("use_gate_in_kernel", False))
+        if kwargs.get("chunk_size", 64) != 64:
+            raise ValueError("`chunk_size` must be 64 for this build")
+        if initial_state is not None:
+            assert initial_state.dtype == torch.float32, "initial_state must be in float32."
+        B, T, H, K = q.shape
+        assert g.shape == (B, T, H), f"g must have shape [B, T, H], got {list(g.shape)}"
+        if use_qk_l2norm_in_kernel:
+            q, k = _l2norm(q), _l2norm(k)
+        if use_beta_sigmoid_in_kernel:
+            beta = beta.sigmoid() * (2.0 if allow_neg_eigval else 1.0)
+        scale = K ** -0.5 if scale is None else scale
+        return _apply("gdn", backend, False, scale, output_final_state, q, k, v, g, beta, None, None,
+                      initial_state)
+    return chunk_gated_delta_rule
+
+
+def make_gdn2(backend):
+    def chunk_gdn2(q, k, v, g, b, w, scale=None, initial_state=None, output_final_state=False,
+                   use_qk_l2norm_in_kernel=False, use_gate_in_kernel=False, cu_seqlens=None,
+                   cu_seqlens_cpu=None, safe_gate=False, lower_bound=None, disable_recompute=False,
+                   return_intermediate_states=False, state_v_first=False, cp_context=None, **kwargs):
+        """Gated DeltaNet 2 (vector gate, channel-wise erase b and write w gates);
+        reference _compat/gdn2.py:205."""
+        _unsupported("chunk_gdn2", use_gate_in_kernel=use_gate_in_kernel, safe_gate=safe_gate,
+                     return_intermediate_states=return_intermediate_states,
+                     state_v_first=state_v_first, cu_seqlens=cu_seqlens is not None,
+                     cp_context=cp_context is not None)
+        if kwargs.get("chunk_size", 64) != 64:
+            raise ValueError("`chunk_size` must be 64 for GDN-2")
+        if initial_state is not None:
+            assert initial_state.dtype == torch.float32, "initial_state must be in float32."
+        assert q.shape == k.shape == g.shape, "q, k, g must have the same shape."
+        assert b.shape == q.shape, "b (channel-wise erase gate) must have shape [B, T, H, K]"
+        assert w.shape == v.shape, "w (channel-wise write gate) must have shape [B, T, H, V]"
+        if use_qk_l2norm_in_kernel:
+            q, k = _l2norm(q), _l2norm(k)
+        scale = k.shape[-1] ** -0.5 if scale is None else scale
+        return _apply("gdn2", backend, disable_recompute, scale, output_final_state, q, k, v, g, None,
+                      b, w, initial_state)
+    return chunk_gdn2
+
+
+def make_delta(backend):
+    def chunk_delta_rule(q, k, v, beta, scale=None, initial_state=None, output_final_state=False,
+                         use_qk_l2norm_in_kernel=False, cu_seqlens=None, cu_seqlens_cpu=None,
+                         **kwargs):
+        """DeltaNet (no gate); reference _compat/delta.py chunk_delta_rule."""
+        if "head_first" in kwargs:
+            raise DeprecationWarning("head_first has been removed. Inputs must be in `[B, T, H, ...]` format.")
+        _unsupported("chunk_delta_rule", cu_seqlens=cu_seqlens is not None)
+        if kwargs.get("chunk_size", 64) != 64:
+            raise ValueError("`chunk_size` must be 64 for this build")
+        assert q.dtype == k.dtype == v.dtype
+        assert len(beta.shape) == 3, "beta must be of shape (batch size, seq len, num of head)."
+        if use_qk_l2norm_in_kernel:
+            q, k = _l2norm(q), _l2norm(k)
+        scale = k.shape[-1] ** -0.5 if scale is None else scale
+        return _apply("delta", backend, False, scale, output_final_state, q, k, v, None, beta, None,
+                      None, initial_state)
+    return chunk_delta_rule

@@ -1,0 +1,144 @@
+"""Complete backward bindings on the gfx950 HIP kernels.
+
+Same callables, keyword signatures and return tuples as the reference's
+``backends/backward.py`` (``kda_backward`` :63-73, ``gdn2_backward`` :75-81,
+``gdn_backward`` :133, ``delta_backward`` :136), which are keyword-compatible
+with FLA's ``chunk_<op>_bwd``.  Each one runs
+
+  1. (recompute policy only) w, u, qg, kg, v_new, h from the saved tensors;
+  2. ``fdr_state_bwd``  -- reverse state recurrence with dv_local = Aqk^T dO fused in;
+  3. ``fdr_chunk_bwd``  -- residual-WY products, dAqk, matrix intra, gate/beta
+     epilogue and the in-chunk reverse cumsum of dg, one work-group per chunk.
+
+There is no fallback: a missing HIP library or an unsupported argument raises.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import ops
+from ..forward import recompute
+
+_UNSUPPORTED = ("cu_seqlens", "chunk_indices", "cp_context", "chunk_offsets")
+
+
+def _check_common(kind, kw):
+    for name in _UNSUPPORTED:
+        if kw.get(name) is not None:
+            raise NotImplementedError(f"{kind} HIP backward: {name} is not supported")
+    if kw.get("state_v_first", False):
+        raise NotImplementedError(f"{kind} HIP backward: state_v_first is not supported")
+    if kw.get("chunk_size", 64) != 64:
+        raise NotImplementedError(f"{kind} HIP backward: chunk_size must be 64")
+    if kw.get("use_gate_in_kernel", False):
+        raise NotImplementedError(f"{kind} HIP backward: use_gate_in_kernel is not supported")
+    if kw.get("safe_gate", False):
+        raise NotImplementedError(f"{kind} HIP backward: safe_gate is not supported")
+    if kw.get("use_graph", False):
+        raise NotImplementedError(f"{kind} HIP backward: use_graph is not supported")
+
+
+def _bf(x):
+    return x.to(torch.bfloat16).contiguous()
+
+
+def _f32(x):
+    return None if x is None else x.to(torch.float32).contiguous()
+
+
+def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, saved, **kw):
+    """Shared vector-gate (KDA / GDN2) backward."""
+    _check_common(op, kw)
+    q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
+    g = _f32(g)
+    Aqk, Akk = _f32(Aqk), _f32(Akk)
+    if saved.get("h") is None:
+        saved = recompute(op, q, k, v, g, Akk, initial_state=initial_state, **gates)
+    dh, dR, dh0 = ops.state_bwd(_bf(saved["qg"]), _bf(saved["kg"]), _bf(saved["w"]), g,
+                                ops.GATE_VECTOR, do, scale, aqk=Aqk, dht=_f32(dht),
+                                want_dh0=initial_state is not None)
+    out = ops.chunk_bwd(q, k, v, _bf(saved["v_new"]), do, dR, g, ops.GATE_VECTOR, Akk,
+                        _bf(saved["h"]), dh, scale, beta=_f32(gates.get("beta")),
+                        b=None if gates.get("b") is None else _bf(gates["b"]),
+                        w=None if gates.get("w") is None else _bf(gates["w"]))
+    return out, dh0
+
+
+def kda_backward(q, k, v, beta, Aqk, Akk, scale, initial_state, do, dht, g, g_org=None,
+                 state_v_first=False, cu_seqlens=None, chunk_indices=None, chunk_size=64,
+                 safe_gate=False, lower_bound=None, use_gate_in_kernel=False, A_log=None,
+                 dt_bias=None, disable_recompute=False, cp_context=None, w=None, u=None, qg=None,
+                 kg=None, v_new=None, h=None, use_graph=False, chunk_offsets=None):
+    """KDA backward -> (dq, dk, dv, db, dg, dh0, dA_log, ddt_bias)."""
+    from ..runtime import record
+    saved = dict(w=w, u=u, qg=qg, kg=kg, v_new=v_new, h=h)
+    out, dh0 = _vector("kda", q, k, v, dict(beta=beta), Aqk, Akk, scale, initial_state, do, dht, g,
+                       saved, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
+                       chunk_indices=chunk_indices, chunk_size=chunk_size, safe_gate=safe_gate,
+                       use_gate_in_kernel=use_gate_in_kernel, cp_context=cp_context,
+                       use_graph=use_graph, chunk_offsets=chunk_offsets)
+    record("kda", "optimized_backward")
+    return out["dq"], out["dk"], out["dv"], out["dbeta"], out["dg"], dh0, None, None
+
+
+def gdn2_backward(q, k, v, b, w_gate, Aqk, Akk, scale, initial_state, do, dht, g, g_org=None,
+                  cu_seqlens=None, chunk_indices=None, chunk_size=64, safe_gate=False,
+                  lower_bound=None, use_gate_in_kernel=False, A_log=None, dt_bias=None,
+                  state_v_first=False, w_wy=None, u_wy=None, qg=None, kg=None, v_new=None, h=None,
+                  disable_recompute=False, cp_context=None):
+    """GDN2 backward -> (dq, dk, dv, db, dw, dg, dh0, dA_log, ddt_bias)."""
+    from ..runtime import record
+    saved = dict(w=w_wy, u=u_wy, qg=qg, kg=kg, v_new=v_new, h=h)
+    out, dh0 = _vector("gdn2", q, k, v, dict(b=b, w=w_gate), Aqk, Akk, scale, initial_state, do, dht,
+                       g, saved, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
+                       chunk_indices=chunk_indices, chunk_size=chunk_size, safe_gate=safe_gate,
+                       use_gate_in_kernel=use_gate_in_kernel, cp_context=cp_context)
+    record("gdn2", "optimized_backward")
+    return out["dq"], out["dk"], out["dv"], out["db"], out["dw"], out["dg"], dh0, None, None
+
+
+def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, **kw):
+    """GDN / DeltaNet: recompute w, u, h, v_new, then the state and chunk kernels
+    (reference ``_scalar``, backends/backward.py:96-131)."""
+    from ..runtime import record
+    _check_common(op, kw)
+    q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
+    g = _f32(g)
+    A = _f32(A)
+    beta = _f32(beta)
+    saved = recompute(op, q, k, v, g, A, beta=beta, initial_state=initial_state)
+    gate = ops.GATE_SCALAR if op == "gdn" else ops.GATE_NONE
+    aqk = _aqk_scalar(q, k, g, scale)
+    dh, dR, dh0 = ops.state_bwd(q, k, _bf(saved["w"]), g, gate, do, scale, aqk=aqk, dht=_f32(dht),
+                                want_dh0=initial_state is not None)
+    out = ops.chunk_bwd(q, k, v, _bf(saved["v_new"]), do, dR, g, gate, A, _bf(saved["h"]), dh, scale,
+                        beta=beta)
+    record(op, "optimized_backward")
+    return out, dh0
+
+
+def _aqk_scalar(q, k, g, scale):
+    """Intra-chunk scores scale * tril(q k^T 2^(g_i - g_j)) for scalar/no gates."""
+    from ..forward import from_chunks, to_chunks
+    qc, kc = to_chunks(q.float()), to_chunks(k.float())
+    s = scale * qc @ kc.transpose(-1, -2)
+    C = s.shape[-1]
+    low = torch.tril(torch.ones(C, C, dtype=torch.bool, device=q.device))
+    if g is not None:
+        gc = to_chunks(g)
+        d = gc[..., :, None] - gc[..., None, :]
+        s = s * torch.exp2(torch.where(low, d, torch.full_like(d, -float("inf"))))
+    s = torch.where(low, s, torch.zeros((), device=q.device))
+    return from_chunks(s)
+
+
+def gdn_backward(q, k, v, g, beta, A, scale, initial_state, do, dht, **kw):
+    """GDN backward -> (dq, dk, dv, db, dg, dh0, None, None)."""
+    out, dh0 = _scalar("gdn", q, k, v, beta, A, scale, initial_state, do, dht, g, **kw)
+    return out["dq"], out["dk"], out["dv"], out["dbeta"], out["dg"], dh0, None, None
+
+
+def delta_backward(q, k, v, beta, A, scale, initial_state, do, dht, **kw):
+    """DeltaNet backward -> (dq, dk, dv, db, dh0)."""
+    out, dh0 = _scalar("delta", q, k, v, beta, A, scale, initial_state, do, dht, None, **kw)
+    return out["dq"], out["dk"], out["dv"], out["dbeta"], dh0

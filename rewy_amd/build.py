@@ -6,6 +6,7 @@ the shared library next to this file so it travels with the source tree.
 from __future__ import annotations
 
 import concurrent.futures as cf
+import json
 import os
 import shutil
 import subprocess
@@ -15,6 +16,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 OUT = HERE / "librewy_hip.so"
+MANIFEST = HERE / "librewy_hip.manifest.json"
 BUILD = HERE / "_build"
 ARCH = "gfx950"
 FLAGS = [
@@ -52,10 +54,13 @@ def build(verbose: bool = False) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr[-4000:]}")
     os.replace(tmp, OUT)
+    from rewy_amd.runtime import source_fingerprint
+    MANIFEST.write_text(json.dumps({"arch": ARCH, "sources": source_fingerprint()}, indent=1))
     if verbose:
         print(f"built {OUT} from {[s.name for s in sources]}", file=sys.stderr)
     return OUT
 
 
 if __name__ == "__main__":
+    sys.path.insert(0, str(HERE.parent))
     build(verbose=True)

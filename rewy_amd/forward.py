@@ -70,12 +70,72 @@ def _pair_products(q, k, bk, gcv, scale, want_qk=True):
     for sl in _slices(N, per):
         d = gcv[sl, :, None, :] - gcv[sl, None, :, :]
         f = torch.exp2(torch.where(low[None, :, :, None], d, torch.full_like(d, -float("inf"))))
-        kj = k[sl, None, :, :]
         if want_qk:
             Aqk[sl] = scale * torch.einsum("nik,nijk,njk->nij", q[sl], f, k[sl])
         Mkk[sl] = torch.einsum("nik,nijk,njk->nij", bk[sl], f, k[sl]) * (~torch.eye(C, dtype=torch.bool, device=k.device))
-        del d, f, kj
+        del d, f
     return Aqk, Mkk
+
+
+def _wy_scan(qf, kf, vf, gcv, bc, wc, Akk, initial_state, scale, Aqk=None, h_dtype=torch.bfloat16):
+    """WY factors and the forward state scan on chunked fp32 operands
+    ([B,H,NT,C,*]); also the output when Aqk is given."""
+    B, H, NT, C, K = kf.shape
+    V = vf.shape[-1]
+    dev = kf.device
+    gam = torch.exp2(gcv)
+    glast = gcv[..., -1:, :]
+    w_wy = Akk @ (bc * kf * gam)
+    u_wy = Akk @ (wc * vf)
+    qg = qf * gam
+    kg = kf * torch.exp2(glast - gcv)
+    lam = torch.exp2(glast[..., 0, :])                                 # [B,H,NT,K|1]
+    S = torch.zeros(B, H, K, V, device=dev) if initial_state is None else initial_state.float().clone()
+    hs = torch.empty(B, H, NT, K, V, device=dev, dtype=h_dtype)
+    vnew = torch.empty(B, H, NT, C, V, device=dev)
+    o = torch.empty(B, H, NT, C, V, device=dev) if Aqk is not None else None
+    for c in range(NT):
+        hb = S.to(h_dtype)
+        hs[:, :, c] = hb
+        Sc = hb.float()
+        vn = u_wy[:, :, c] - w_wy[:, :, c] @ Sc
+        vnew[:, :, c] = vn
+        if o is not None:
+            o[:, :, c] = scale * qg[:, :, c] @ Sc + Aqk[:, :, c] @ vn
+        S = lam[:, :, c, :, None] * S + kg[:, :, c].transpose(-1, -2) @ vn
+    return hs, vnew, w_wy, u_wy, qg, kg, S, o
+
+
+def _family_operands(op, q, k, v, gc, beta, b, w):
+    """Chunked fp32 operands: q, k, v, gate (log2 cumsum, [..,K] or [..,1]), b, w."""
+    B, T, H, K = q.shape
+    NT = T // CHUNK
+    qf, kf, vf = (to_chunks(x.float()) for x in (q, k, v))
+    if op == "delta":
+        gcv = torch.zeros(B, H, NT, CHUNK, 1, device=q.device)
+    elif op == "gdn":
+        gcv = to_chunks(gc)[..., None]
+    else:
+        gcv = to_chunks(gc)
+    if op == "gdn2":
+        bc, wc = to_chunks(b.float()), to_chunks(w.float())
+    else:
+        be = to_chunks(beta.float())[..., None]
+        bc, wc = be, be
+    return qf, kf, vf, gcv, bc, wc
+
+
+def recompute(op, q, k, v, gc, Akk, beta=None, b=None, w=None, initial_state=None):
+    """Recompute w, u, qg, kg, v_new and h from saved (q, k, v, gc, Akk, gates):
+    the recompute policy of FLA's chunk_<op>_bwd (recompute_w_u_fwd +
+    chunk_gated_delta_rule_fwd_h, reference backends/backward.py:110-118)."""
+    qf, kf, vf, gcv, bc, wc = _family_operands(op, q, k, v, gc, beta, b, w)
+    A = to_chunks(Akk)
+    hs, vnew, w_wy, u_wy, qg, kg, _, _ = _wy_scan(qf, kf, vf, gcv, bc, wc, A, initial_state, None)
+    bf = torch.bfloat16
+    return dict(w=from_chunks(w_wy).to(bf), u=from_chunks(u_wy).to(bf), qg=from_chunks(qg).to(bf),
+                kg=from_chunks(kg).to(bf), v_new=from_chunks(vnew).to(bf),
+                h=hs.permute(0, 2, 1, 3, 4).contiguous())
 
 
 def chunk_forward(op, q, k, v, g=None, beta=None, b=None, w=None, initial_state=None,
@@ -86,29 +146,13 @@ def chunk_forward(op, q, k, v, g=None, beta=None, b=None, w=None, initial_state=
     decay ([B,T,H] for gdn, [B,T,H,K] for kda/gdn2).  The saved dict holds the
     FLA-convention intermediates listed in the module docstring."""
     B, T, H, K = q.shape
-    V = v.shape[-1]
     C = chunk
-    assert T % C == 0, "T must be a multiple of the chunk size"
+    assert C == CHUNK and T % C == 0, "T must be a multiple of the 64-token chunk"
     dev = q.device
     scale = K ** -0.5 if scale is None else scale
     NT = T // C
-    qf, kf, vf = (to_chunks(x.float()) for x in (q, k, v))           # [B,H,NT,C,D]
-    if op == "delta":
-        gc = None
-        gcv = torch.zeros(B, H, NT, C, 1, device=dev)
-    elif op == "gdn":
-        gc = chunk_local_cumsum(g, C)                                  # [B,T,H]
-        gcv = to_chunks(gc)[..., None]                                 # [B,H,NT,C,1]
-    else:
-        gc = chunk_local_cumsum(g, C)                                  # [B,T,H,K]
-        gcv = to_chunks(gc)
-    if op == "gdn2":
-        bc, wc = to_chunks(b.float()), to_chunks(w.float())
-    else:
-        be = to_chunks(beta.float())[..., None]                        # [B,H,NT,C,1]
-        bc, wc = be, be
-    gam = torch.exp2(gcv)                                              # [B,H,NT,C,K|1]
-    glast = gcv[..., -1:, :]
+    gc = None if op == "delta" else chunk_local_cumsum(g, C)
+    qf, kf, vf, gcv, bc, wc = _family_operands(op, q, k, v, gc, beta, b, w)
     bk = bc * kf
     N = B * H * NT
     if op in ("kda", "gdn2"):
@@ -125,23 +169,8 @@ def chunk_forward(op, q, k, v, g=None, beta=None, b=None, w=None, initial_state=
         Mkk = torch.where(torch.tril(low, -1), Mkk, torch.zeros((), device=dev))
     eye = torch.eye(C, device=dev)
     Akk = torch.linalg.solve_triangular(eye + Mkk, eye.expand_as(Mkk), upper=False, unitriangular=True)
-    w_wy = Akk @ (bk * gam)
-    u_wy = Akk @ (wc * vf)
-    qg = qf * gam
-    kg = kf * torch.exp2(glast - gcv)
-    lam = torch.exp2(glast[..., 0, :])                                 # [B,H,NT,K|1]
-    S = torch.zeros(B, H, K, V, device=dev) if initial_state is None else initial_state.float().clone()
-    hs = torch.empty(B, H, NT, K, V, device=dev, dtype=torch.bfloat16 if save else torch.float32)
-    vnew = torch.empty(B, H, NT, C, V, device=dev)
-    o = torch.empty(B, H, NT, C, V, device=dev)
-    for c in range(NT):
-        hb = S.to(hs.dtype)
-        hs[:, :, c] = hb
-        Sc = hb.float()
-        vn = u_wy[:, :, c] - w_wy[:, :, c] @ Sc
-        vnew[:, :, c] = vn
-        o[:, :, c] = scale * qg[:, :, c] @ Sc + Aqk[:, :, c] @ vn
-        S = lam[:, :, c, :, None] * S + kg[:, :, c].transpose(-1, -2) @ vn
+    hs, vnew, w_wy, u_wy, qg, kg, S, o = _wy_scan(qf, kf, vf, gcv, bc, wc, Akk, initial_state, scale,
+                                                  Aqk=Aqk, h_dtype=torch.bfloat16 if save else torch.float32)
     out = from_chunks(o).to(q.dtype)
     final = S if output_final_state else None
     saved = None

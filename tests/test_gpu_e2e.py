@@ -1,0 +1,95 @@
+"""End-to-end gradients of the public operators on the GPU.
+
+The optimized (HIP) backward is compared with the fp64 oracle (token-recurrence
+pinned) at the reference's acceptance tolerances (validation.py:40-45 and
+:68: rel-L2 <= 0.008 for q/k/v/h0, <= 0.02 for g/beta/b/w) and with the
+original-formulation backend on the same inputs (test_accelerator.py:7-31).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import delta_oracle as O
+from tests._inputs import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+OPNAME = {"kda": "chunk_kda", "gdn": "chunk_gated_delta_rule", "gdn2": "chunk_gdn2", "delta": "chunk_delta_rule"}
+GRAD = {"q": "dq", "k": "dk", "v": "dv", "g": "dg", "beta": "dbeta", "b": "db", "w": "dw", "initial_state": "dh0"}
+
+
+def _run(op, xs, dO, backend, **kw):
+    import rewy_amd as fdr
+    dev = torch.device("cuda")
+    xg = {k: v.to(dev).requires_grad_() for k, v in xs.items()}
+    with fdr.use_backend(backend, ops=(op,)):
+        o, ht = getattr(fdr, OPNAME[op])(**xg, output_final_state=True, **kw)
+    dht = (torch.randn(ht.shape, generator=torch.Generator().manual_seed(9)) * 0.1).to(dev)
+    grads = torch.autograd.grad((o, ht), tuple(xg.values()), (dO.to(dev), dht))
+    torch.cuda.synchronize()
+    return dict(zip(xs, grads)), dht.cpu()
+
+
+@pytest.mark.parametrize("op,kw", [("kda", dict(disable_recompute=True)), ("kda", dict(disable_recompute=False)),
+                                   ("gdn", {}), ("gdn2", dict(disable_recompute=True)), ("delta", {})])
+@pytest.mark.parametrize("T", [128, 320])
+def test_public_backward_matches_oracle(op, kw, T):
+    import rewy_amd as fdr
+    print(f"\n[e2e] op={op} kw={kw} T={T}", flush=True)
+    xs, dO = make_inputs(op, 2, T, 2, seed=21, beta_zero_every=7 if op != "gdn2" else 0)
+    fdr.stats(reset=True)
+    got, dht = _run(op, xs, dO, "optimized", **kw)
+    fdr.assert_used((op,))
+    assert not any("fallback" in k or "rejected" in k for k in fdr.stats())
+    n = lambda x: None if x is None else x.detach().double().cpu().numpy()
+    ref = O.backward(op, n(xs["q"]), n(xs["k"]), n(xs["v"]), g=n(xs.get("g")), beta=n(xs.get("beta")),
+                     b=n(xs.get("b")), w=n(xs.get("w")), h0=n(xs["initial_state"]), dO=n(dO), dht=n(dht))
+    report = {}
+    for name, grad in got.items():
+        e = O.error(ref[GRAD[name]], n(grad), O.limit_for(GRAD[name]))
+        report[name] = (round(e["relative_l2"], 5), e["max_abs"])
+        assert e["passed"], (name, e)
+    print("rel-L2/max-abs vs oracle", report, flush=True)
+
+
+@pytest.mark.parametrize("op", ["kda", "gdn", "gdn2", "delta"])
+def test_optimized_matches_original_backend(op):
+    print(f"\n[e2e-orig] op={op}", flush=True)
+    xs, dO = make_inputs(op, 1, 256, 3, seed=33)
+    kw = dict(disable_recompute=True) if op in ("kda", "gdn2") else {}
+    a, _ = _run(op, xs, dO, "optimized", **kw)
+    b, _ = _run(op, xs, dO, "original", **kw)
+    for name in a:
+        e = O.error(b[name].double().cpu().numpy(), a[name].double().cpu().numpy(), O.limit_for(GRAD[name]))
+        assert e["passed"], (name, e)
+
+
+def test_backward_stays_bound_after_disable():
+    import rewy_amd as fdr
+    xs, dO = make_inputs("kda", 1, 128, 2, seed=3)
+    dev = torch.device("cuda")
+    xg = {k: v.to(dev).requires_grad_() for k, v in xs.items()}
+    fdr.stats(reset=True)
+    fdr.enable("optimized", ops=("kda",))
+    o, _ = fdr.chunk_kda(**xg)
+    fdr.disable()
+    torch.autograd.grad(o, tuple(xg.values()), dO.to(dev))
+    fdr.assert_used(("kda",))
+
+
+def test_rejection_and_visible_fallback():
+    import rewy_amd as fdr
+    xs, dO = make_inputs("kda", 1, 128, 2, seed=3)
+    dev = torch.device("cuda")
+    xg = {k: v[:, :65].contiguous().to(dev).requires_grad_() if v.ndim > 3 or k == "beta" else v.to(dev).requires_grad_()
+          for k, v in xs.items()}
+    with fdr.use_backend("optimized"):
+        with pytest.raises(RuntimeError, match="multiple of 64"):
+            fdr.chunk_kda(**xg)
+    fdr.stats(reset=True)
+    with fdr.use_backend("optimized", strict=False):
+        with pytest.warns(RuntimeWarning, match="using original"):
+            out, _ = fdr.chunk_kda(**xg)
+    out.float().sum().backward()
+    assert fdr.stats()["kda.fallback_forward"] == 1
+    assert fdr.stats().get("kda.optimized_backward", 0) == 0
