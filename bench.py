@@ -202,48 +202,45 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(xs, sv, dO, dh, dR, scale, NTt):
-    """fp64 oracle (numpy, one thread) of the timed stages on B=1, T=512, all heads,
-    scaled linearly to the full workload's chunk-head count."""
+def cpu_baseline(xs, sv, dO, dh, dR, scale, NTt, heads_per_piece=1):
+    """fp64 oracle (numpy, one thread) of the timed stages -- state recurrence and
+    chunk stage -- on a bounded sample (batch 0, all T, the first 8 heads, one
+    head at a time so the oracle's pairwise tensors stay small), scaled linearly
+    to the full workload's chunk-head count."""
     import numpy as np
     try:
         from threadpoolctl import threadpool_limits
     except ImportError:  # pragma: no cover
         threadpool_limits = None
     from oracle import delta_oracle as O
-    Ts = 512
-    n = lambda x: x[:1, :Ts].double().cpu().numpy()
-    nh = lambda x: x[:1, :Ts // 64].double().cpu().numpy()
-    H = xs["q"].shape[2]
-    inputs = dict(qg=n(sv["qg"]), kg=n(sv["kg"]), w=n(sv["w"]), gc=n(sv["gc"]), dO=n(dO),
-                  Aqk=n(sv["Aqk"]), q=n(xs["q"]), k=n(xs["k"]), v=n(xs["v"]), beta=n(xs["beta"]),
-                  Akk=n(sv["Akk"]), h=nh(sv["h"]), v_new=n(sv["v_new"]))
-    # the sample's terminal state gradient is the GPU's dh at the sample end
-    dht = dh[:1, Ts // 64 - 1].double().cpu().numpy() if Ts < xs["q"].shape[1] else None
-    sample_heads = 1 * H * (Ts // 64)
-
-    def run():
-        dvl = O.dv_local(inputs["Aqk"], inputs["dO"])
-        d_h, d_R, _ = O.stage_state_bwd(inputs["qg"], inputs["kg"], inputs["w"], inputs["gc"],
-                                        inputs["dO"], dvl, dht=dht, scale=scale)
-        O.stage_post("kda", inputs["q"], inputs["k"], inputs["v"], inputs["gc"], beta=inputs["beta"],
-                     Akk=inputs["Akk"], h=inputs["h"], dh=d_h, v_new=inputs["v_new"], dO=inputs["dO"],
-                     dR=d_R, scale=scale)
-
+    B, T, H = xs["q"].shape[:3]
+    heads = min(8, H)
+    sample_heads = heads * (T // 64)
     ctx = threadpool_limits(limits=1) if threadpool_limits else None
     if ctx:
         ctx.__enter__()
+    el = 0.0
     try:
-        t0 = time.perf_counter()
-        run()
-        el = time.perf_counter() - t0
+        for h0 in range(0, heads, heads_per_piece):
+            hs = slice(h0, h0 + heads_per_piece)
+            n = lambda x: x[:1, :, hs].double().cpu().numpy()
+            inp = dict(qg=n(sv["qg"]), kg=n(sv["kg"]), w=n(sv["w"]), gc=n(sv["gc"]), dO=n(dO),
+                       Aqk=n(sv["Aqk"]), q=n(xs["q"]), k=n(xs["k"]), v=n(xs["v"]), beta=n(xs["beta"]),
+                       Akk=n(sv["Akk"]), h=n(sv["h"]), v_new=n(sv["v_new"]))
+            t0 = time.perf_counter()
+            dvl = O.dv_local(inp["Aqk"], inp["dO"])
+            d_h, d_R, _ = O.stage_state_bwd(inp["qg"], inp["kg"], inp["w"], inp["gc"], inp["dO"], dvl,
+                                            scale=scale)
+            O.stage_post("kda", inp["q"], inp["k"], inp["v"], inp["gc"], beta=inp["beta"], Akk=inp["Akk"],
+                         h=inp["h"], dh=d_h, v_new=inp["v_new"], dO=inp["dO"], dR=d_R, scale=scale)
+            el += time.perf_counter() - t0
     finally:
         if ctx:
             ctx.__exit__(None, None, None)
     full_ms = el * 1e3 * NTt / sample_heads
     return {"value": round(full_ms, 1), "unit": "ms (full workload, extrapolated)", "cores": 1,
             "kind": "port",
-            "sample": f"fp64 numpy oracle (state recurrence + chunk stage) on B=1 T={Ts} H={H} "
+            "sample": f"fp64 numpy oracle (state recurrence + chunk stage), batch 0, T={T}, heads 0-{heads - 1} "
                       f"({sample_heads} of {NTt} chunk-heads), measured {el:.2f} s, scaled linearly"}
 
 
