@@ -28,9 +28,18 @@
 // Vector gates: the 2^(g_i-g_s) factors are applied through one anchor per
 // 16-row block (the block's gate centre when its span is < 80, in log2 units,
 // else the block's own top/bottom with an exact pairwise diagonal), the same
-// safety rule as the reference (endpoint_intra.py:98-102).  The intra operands
-// are split into bf16 hi + lo so each contraction runs as three bf16 MFMAs
-// with fp32 accumulation (the reference uses tf32x3 dots for these).
+// safety rule as the reference (endpoint_intra.py:98-102).  Scalar gates are
+// applied exactly to the 64x64 L and D tiles, so no Gram matrix is formed and
+// no anchor is needed.  The intra operands are split into bf16 hi + lo so each
+// contraction runs as three bf16 MFMAs with fp32 accumulation (the reference
+// uses tf32x3 dots for these).
+//
+// Work split: 8 waves; wave (cs, rh) owns the 32 columns [32 cs, 32 cs + 32)
+// (key or value) and the 32 rows [32 rh, 32 rh + 32) of every 64 x 128 tile.
+// Token-major inputs that are contracted over tokens are staged transposed
+// (token pairs packed into dwords, conflict-free); P and the L/D tiles are
+// produced by MFMAs whose accumulator layout stores contiguously into the
+// orientation the next contraction reads.
 #include "common.hpp"
 
 namespace rewy {
@@ -40,38 +49,48 @@ enum GateModeC { CG_NONE = 0, CG_SCALAR = 1, CG_VECTOR = 2 };
 namespace post {
 constexpr int LDT = 72;    // bf16 pitch of [.][64] tiles
 constexpr int LDV = 136;   // bf16 pitch of [.][128] tiles
-constexpr int LDG = 68;    // fp32 pitch of [128][64] gate tile
-// region A: phase 1 {A^T hi, A^T lo, dR^T}; phase 2+ {L hi, L lo, D hi, D lo}
-constexpr int OFF_AKTH = 0;
-constexpr int OFF_AKTL = OFF_AKTH + C * LDT * 2;
-constexpr int OFF_DRT = OFF_AKTL + C * LDT * 2;
-constexpr int OFF_LH = 0;
-constexpr int OFF_LL = OFF_LH + C * LDT * 2;
-constexpr int OFF_DH = OFF_LL + C * LDT * 2;
-constexpr int OFF_DL = OFF_DH + C * LDT * 2;
-constexpr int REGION_A = (OFF_DRT + KD * LDT * 2) > (OFF_DL + C * LDT * 2) ? (OFF_DRT + KD * LDT * 2)
-                                                                           : (OFF_DL + C * LDT * 2);
-// region B: phases 1-3 {P, R, dO}; phases 4+ {q^T, k^T, g^T, b^T}
-constexpr int OFF_P = REGION_A;
-constexpr int OFF_R = OFF_P + C * LDV * 2;
-constexpr int OFF_DO = OFF_R + C * LDV * 2;
-constexpr int END_B1 = OFF_DO + C * LDV * 2;
-constexpr int OFF_QT = REGION_A;
-constexpr int OFF_KT = OFF_QT + KD * LDT * 2;
-constexpr int OFF_GT = OFF_KT + KD * LDT * 2;
-constexpr int OFF_BT = OFF_GT + KD * LDG * 4;        // used by the vector-b family only
+constexpr int LDG = 68;    // fp32 pitch of the [128][64] gate tile
+constexpr int T64 = C * LDT * 2;     // bytes of one [64][72] bf16 tile
+constexpr int T128 = KD * LDT * 2;   // bytes of one [128][72] bf16 tile
+constexpr int R64 = C * LDV * 2;     // bytes of one [64][136] bf16 tile
 }  // namespace post
 
 template <int GATE, bool VEC_B>
 struct PostLayout {
-  static constexpr int END_B2 = post::OFF_BT + (VEC_B ? KD * post::LDT * 2 : 0);
-  static constexpr int END_B = END_B2 > post::END_B1 ? END_B2 : post::END_B1;
-  static constexpr int OFF_SMALL = END_B;
-  // small arrays (floats)
+  // region A.  phases 0-1: A^T hi/lo [t][s], dR^T [v][s].
+  //            phases 2+:  L, D row-major hi/lo, and (scalar beta) L^T, D^T hi/lo.
+  static constexpr bool LT_COPY = !VEC_B;
+  static constexpr int OFF_AKTH = 0, OFF_AKTL = post::T64, OFF_DRT = 2 * post::T64;
+  static constexpr int OFF_LRH = 0, OFF_LRL = post::T64, OFF_DRH = 2 * post::T64, OFF_DRL = 3 * post::T64;
+  static constexpr int OFF_LTH = 4 * post::T64, OFF_LTL = 5 * post::T64, OFF_DTH = 6 * post::T64,
+                       OFF_DTL = 7 * post::T64;
+  static constexpr int A1 = 2 * post::T64 + post::T128;
+  static constexpr int A2 = (LT_COPY ? 8 : 4) * post::T64;
+  static constexpr int REGION_A = A1 > A2 ? A1 : A2;
+  // region B.  phases 0-3: P, R, dO row-major.  phases 3+: q^T, k^T, g^T (, b^T).
+  static constexpr int OFF_P = REGION_A, OFF_R = REGION_A + post::R64, OFF_DO = REGION_A + 2 * post::R64;
+  static constexpr int OFF_QT = REGION_A, OFF_KT = REGION_A + post::T128, OFF_GT = REGION_A + 2 * post::T128;
+  static constexpr int OFF_BT = OFF_GT + KD * post::LDG * 4;
+  static constexpr int B1 = 3 * post::R64;
+  static constexpr int B2 = 2 * post::T128 + KD * post::LDG * 4 + (VEC_B ? post::T128 : 0);
+  static constexpr int OFF_SMALL = REGION_A + (B1 > B2 ? B1 : B2);
   static constexpr int S_BETA = 0, S_G = 64, S_DBA = 128, S_DBB = 192, S_DG = 256, S_COL = 320,
-                       S_TOT = 448, S_GL = 576, S_FLAG = 704, S_N = 708;
+                       S_TOT = 448, S_GL = 576, S_N = 704;
   static constexpr int BYTES = OFF_SMALL + S_N * 4;
+  static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
+
+__device__ __forceinline__ bf16x4 split_hi4(f32x4 x, bf16x4& lo) {
+  bf16x4 hi;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    bf16 h, l;
+    split_bf16(x[r], h, l);
+    hi[r] = h;
+    lo[r] = l;
+  }
+  return hi;
+}
 
 template <int GATE, bool VEC_B>
 __global__ __launch_bounds__(512) void chunk_bwd_kernel(
@@ -83,22 +102,30 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
     bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale) {
   using LY = PostLayout<GATE, VEC_B>;
-  using namespace post;
+  using post::LDT;
+  using post::LDV;
+  using post::LDG;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  bf16* akTh = reinterpret_cast<bf16*>(smem + OFF_AKTH);
-  bf16* akTl = reinterpret_cast<bf16*>(smem + OFF_AKTL);
-  bf16* drT = reinterpret_cast<bf16*>(smem + OFF_DRT);
-  bf16* Lh = reinterpret_cast<bf16*>(smem + OFF_LH);
-  bf16* Ll = reinterpret_cast<bf16*>(smem + OFF_LL);
-  bf16* Dh = reinterpret_cast<bf16*>(smem + OFF_DH);
-  bf16* Dl = reinterpret_cast<bf16*>(smem + OFF_DL);
-  bf16* sP = reinterpret_cast<bf16*>(smem + OFF_P);
-  bf16* sR = reinterpret_cast<bf16*>(smem + OFF_R);
-  bf16* sdO = reinterpret_cast<bf16*>(smem + OFF_DO);
-  bf16* qT = reinterpret_cast<bf16*>(smem + OFF_QT);
-  bf16* kT = reinterpret_cast<bf16*>(smem + OFF_KT);
-  float* gT = reinterpret_cast<float*>(smem + OFF_GT);
-  bf16* bT = reinterpret_cast<bf16*>(smem + OFF_BT);
+  auto B16 = [&](int off) { return reinterpret_cast<bf16*>(smem + off); };
+  auto U32 = [&](int off) { return reinterpret_cast<uint32_t*>(smem + off); };
+  bf16* akTh = B16(LY::OFF_AKTH);
+  bf16* akTl = B16(LY::OFF_AKTL);
+  bf16* drT = B16(LY::OFF_DRT);
+  bf16* Lrh = B16(LY::OFF_LRH);
+  bf16* Lrl = B16(LY::OFF_LRL);
+  bf16* Drh = B16(LY::OFF_DRH);
+  bf16* Drl = B16(LY::OFF_DRL);
+  bf16* Lth = B16(LY::OFF_LTH);
+  bf16* Ltl = B16(LY::OFF_LTL);
+  bf16* Dth = B16(LY::OFF_DTH);
+  bf16* Dtl = B16(LY::OFF_DTL);
+  bf16* sP = B16(LY::OFF_P);
+  bf16* sR = B16(LY::OFF_R);
+  bf16* sdO = B16(LY::OFF_DO);
+  bf16* qT = B16(LY::OFF_QT);
+  bf16* kT = B16(LY::OFF_KT);
+  float* gT = reinterpret_cast<float*>(smem + LY::OFF_GT);
+  bf16* bT = B16(LY::OFF_BT);
   float* small = reinterpret_cast<float*>(smem + LY::OFF_SMALL);
   float* sBeta = small + LY::S_BETA;   // scalar beta per row
   float* sG = small + LY::S_G;         // scalar gate per row (log2)
@@ -117,35 +144,30 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int cs = wv & 3;          // column strip: k (or v) in [32 cs, 32 cs + 32)
   const int rh = wv >> 2;         // row half: rows [32 rh, 32 rh + 32)
+  const int lc = l & 15, lg = l >> 4;
   const size_t tok0 = (size_t)b * T + (size_t)c * C;
   const size_t rsk = (size_t)H * KD, rsv = (size_t)H * VD, rsa = (size_t)H * C;
   const size_t hoff = (((size_t)b * NT + c) * H + h) * KD * VD;
-  const int lc = l & 15, lg = l >> 4;
+  const size_t kofs = tok0 * rsk + (size_t)h * KD;    // [t][k] tensors of this chunk-head
+  const size_t vofs = tok0 * rsv + (size_t)h * VD;    // [t][v] tensors
+  const bf16* vb = v + vofs;
 
   // ---------------- phase 0: stage A^T (hi/lo), dR^T, R, dO, beta, gates ----------------
   int any_fb = 0;
   {
+    {
+      const int p = tid;   // 512 pair pieces (32 row pairs x 16 column chunks)
+      const PairPieceF pa = load_pair_piece_f(akk + (tok0 * H + h) * C, rsa, p & 31, (p >> 5) * 4);
+      const PairPiece pd = load_pair_piece(dR + vofs, rsv, p & 31, (p >> 5) * 8);
+      store_pair_piece_split(U32(LY::OFF_AKTH), U32(LY::OFF_AKTL), LDT / 2, p & 31, (p >> 5) * 4, pa, 1.f);
+      store_pair_piece(U32(LY::OFF_DRT), LDT / 2, p & 31, (p >> 5) * 8, pd);
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int p = tid + 512 * i;                    // 1024 pieces each
-      const int s = p >> 4, c0 = (p & 15) * 4;        // A: row s, 4 floats of t
-      const float4 a4 = *reinterpret_cast<const float4*>(akk + (tok0 + s) * rsa + (size_t)h * C + c0);
-      const float av[4] = {a4.x, a4.y, a4.z, a4.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bf16 hi, lo;
-        split_bf16(av[j], hi, lo);
-        akTh[(c0 + j) * LDT + s] = hi;
-        akTl[(c0 + j) * LDT + s] = lo;
-      }
-      const int t = p >> 4, v0 = (p & 15) * 8;        // dR/R/dO: row t, 8 bf16 of v
-      const size_t off = (tok0 + t) * rsv + (size_t)h * VD + v0;
-      const uint4 d4 = *reinterpret_cast<const uint4*>(dR + off);
-      const bf16* pd = reinterpret_cast<const bf16*>(&d4);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) drT[(v0 + j) * LDT + t] = pd[j];
-      *reinterpret_cast<uint4*>(sR + t * LDV + v0) = *reinterpret_cast<const uint4*>(vnew + off);
-      *reinterpret_cast<uint4*>(sdO + t * LDV + v0) = *reinterpret_cast<const uint4*>(dO + off);
+      const int p = tid + 512 * i;
+      const int t = p >> 4, v0 = (p & 15) * 8;
+      *reinterpret_cast<uint4*>(sR + t * LDV + v0) = *reinterpret_cast<const uint4*>(vnew + vofs + (size_t)t * rsv + v0);
+      *reinterpret_cast<uint4*>(sdO + t * LDV + v0) = *reinterpret_cast<const uint4*>(dO + vofs + (size_t)t * rsv + v0);
     }
     int fb = 0;
     if (tid < C) {
@@ -162,7 +184,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     }
     if (tid < KD) {
       float gl = 0.f;
-      if constexpr (GATE == CG_VECTOR) gl = g[((tok0 + C - 1) * H + h) * KD + tid];
+      if constexpr (GATE == CG_VECTOR) gl = g[kofs + (size_t)(C - 1) * rsk + tid];
       else if constexpr (GATE == CG_SCALAR) gl = g[(tok0 + C - 1) * H + h];
       sGl[tid] = gl;
     }
@@ -170,52 +192,61 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   }
   const bool has_fb = !VEC_B && any_fb != 0;
 
-  // ---------------- phase 1: P = A^T dR ; dv ; sum_v P R ----------------
+  // ---------------- phase 1: P^T = dR^T A  (accumulator layout stores P row-major) ----------------
   {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int I = 2 * rh + rt;               // row tile (t)
+    for (int vt = 0; vt < 2; ++vt) {
+      const int vrow0 = 32 * cs + 16 * vt;
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const int vcol0 = 32 * cs + 16 * ct;
+      for (int tt = 0; tt < 2; ++tt) {
+        const int tcol0 = 32 * rh + 16 * tt;
         f32x4 acc = zero4();
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           if (ks == 0 && rh == 1) continue;    // A^T upper triangular: s < 32 <= t vanishes
-          const bf16x8 bd = frag(drT + vcol0 * LDT + 32 * ks, LDT);
-          acc = mfma(frag(akTh + (16 * I) * LDT + 32 * ks, LDT), bd, acc);
-          acc = mfma(frag(akTl + (16 * I) * LDT + 32 * ks, LDT), bd, acc);
+          const bf16x8 a = frag(drT + vrow0 * LDT + 32 * ks, LDT);
+          acc = mfma(a, frag(akTh + tcol0 * LDT + 32 * ks, LDT), acc);
+          acc = mfma(a, frag(akTl + tcol0 * LDT + 32 * ks, LDT), acc);
         }
-        const int vv = vcol0 + lc;
-        float rowpr[4], rowpv[4];
+        // lane: t = tcol0 + lc, v = vrow0 + 4 lg .. +3
+        const int t = tcol0 + lc;
+        const int v0 = vrow0 + 4 * lg;
+        bf16x4 p4;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 16 * I + 4 * lg + r;
-          const float pv = acc[r];
-          const bf16 pb = to_bf16(pv);
-          sP[t * LDV + vv] = pb;
-          const size_t off = (tok0 + t) * rsv + (size_t)h * VD + vv;
-          if constexpr (VEC_B) {
-            const float wg = to_f32(wgate[off]);
-            dv_out[off] = to_bf16(wg * pv);
-            dw_out[off] = to_bf16(to_f32(v[off]) * pv);
-            rowpr[r] = rowpv[r] = 0.f;
-          } else {
-            dv_out[off] = to_bf16(sBeta[t] * pv);
-            rowpr[r] = pv * to_f32(sR[t * LDV + vv]);
-            rowpv[r] = has_fb ? pv * to_f32(v[off]) : 0.f;
-          }
-        }
-        if constexpr (!VEC_B) {
+        for (int r = 0; r < 4; ++r) p4[r] = to_bf16(acc[r]);
+        *reinterpret_cast<bf16x4*>(sP + t * LDV + v0) = p4;
+        const size_t go = (size_t)t * rsv + v0;
+        if constexpr (VEC_B) {
+          const bf16x4 w4 = *reinterpret_cast<const bf16x4*>(wgate + vofs + go);
+          const bf16x4 x4 = *reinterpret_cast<const bf16x4*>(vb + go);
+          bf16x4 o1, o2;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float a = sum_row16(rowpr[r]);
-            const float bsum = sum_row16(rowpv[r]);
-            if (lc == 0) {
-              const int t = 16 * I + 4 * lg + r;
-              atomicAdd(&sDbA[t], a);
-              if (has_fb) atomicAdd(&sDbB[t], bsum);
-            }
+            o1[r] = to_bf16(to_f32(w4[r]) * acc[r]);
+            o2[r] = to_bf16(to_f32(x4[r]) * acc[r]);
+          }
+          *reinterpret_cast<bf16x4*>(dv_out + vofs + go) = o1;
+          *reinterpret_cast<bf16x4*>(dw_out + vofs + go) = o2;
+        } else {
+          const float be = sBeta[t];
+          const bf16x4 r4 = *reinterpret_cast<const bf16x4*>(sR + t * LDV + v0);
+          bf16x4 o1;
+          float pr = 0.f;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            o1[r] = to_bf16(be * acc[r]);
+            pr += acc[r] * to_f32(r4[r]);
+          }
+          *reinterpret_cast<bf16x4*>(dv_out + vofs + go) = o1;
+          pr = sum_lane_groups(pr);
+          if (lg == 0) atomicAdd(&sDbA[t], pr);
+          if (has_fb) {
+            const bf16x4 x4 = *reinterpret_cast<const bf16x4*>(vb + go);
+            float pv = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pv += acc[r] * to_f32(x4[r]);
+            pv = sum_lane_groups(pv);
+            if (lg == 0) atomicAdd(&sDbB[t], pv);
           }
         }
       }
@@ -234,14 +265,21 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
       fdh[ct][ks] = *reinterpret_cast<const bf16x8*>(dhst + o);
     }
 
-  // ---------------- phase 2: L = scale tril(dO R^T), D = -strict_tril(P R^T) ----------------
+  // ---------------- phase 2: L = scale tril(dO R^T), D = -strict_tril(P R^T), both orientations ----------------
   {
     const int I = wv >> 1;
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int J = 2 * (wv & 1) + jj;
-      f32x4 aL = zero4(), aD = zero4();
-      if (J <= I) {
+      // (a) tiles of L and D with rows i in block I, columns s in block J.  Their
+      //     accumulator layout stores contiguously as L^T[s][i], D^T[s][i], the
+      //     A operands of uk.
+      // (b) tiles of L^T and D^T with rows s in block I, columns i in block J:
+      //     they store contiguously as the row-major L[i][s], D[i][s].
+      f32x4 aL = zero4(), aD = zero4(), bL = zero4(), bD = zero4();
+      const bool lowerA = J <= I;      // (a) nonzero: s-block J <= i-block I
+      const bool lowerB = J >= I;      // (b) nonzero: i-block J >= s-block I
+      if (lowerA && LY::LT_COPY) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           const bf16x8 br = frag(sR + (16 * J) * LDV + 32 * ks, LDV);
@@ -249,46 +287,54 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
           aD = mfma(frag(sP + (16 * I) * LDV + 32 * ks, LDV), br, aD);
         }
       }
-      const int s = 16 * J + lc;
+      if (lowerB) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * I + 4 * lg + r;
-        float lv = (i >= s) ? scale * aL[r] : 0.f;
-        float dv_ = (i > s) ? -aD[r] : 0.f;
-        if constexpr (GATE == CG_SCALAR) {
-          const float f = (i >= s) ? fast_exp2(sG[i] - sG[s]) : 0.f;
-          lv *= f;
-          dv_ *= f;
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 ar = frag(sR + (16 * I) * LDV + 32 * ks, LDV);
+          bL = mfma(ar, frag(sdO + (16 * J) * LDV + 32 * ks, LDV), bL);
+          bD = mfma(ar, frag(sP + (16 * J) * LDV + 32 * ks, LDV), bD);
         }
-        bf16 hi, lo;
-        split_bf16(lv, hi, lo);
-        Lh[i * LDT + s] = hi;
-        Ll[i * LDT + s] = lo;
-        split_bf16(dv_, hi, lo);
-        Dh[i * LDT + s] = hi;
-        Dl[i * LDT + s] = lo;
       }
-    }
-  }
-
-  // prefetch q, k, g (and b) for the transposed staging after phase 3
-  uint4 rq[2], rk[2], rb[2];
-  float4 rg[4];
+      if constexpr (LY::LT_COPY) {
+        // (a): lane holds rows i = 16 I + 4 lg + r, column s = 16 J + lc
+        const int s = 16 * J + lc;
+        f32x4 lv, dv4;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int p = tid + 512 * i;
-    const int t = p >> 4, k0 = (p & 15) * 8;
-    const size_t off = (tok0 + t) * rsk + (size_t)h * KD + k0;
-    rq[i] = *reinterpret_cast<const uint4*>(q + off);
-    rk[i] = *reinterpret_cast<const uint4*>(k + off);
-    if constexpr (VEC_B) rb[i] = *reinterpret_cast<const uint4*>(bgate + off);
-  }
-  if constexpr (GATE == CG_VECTOR) {
+        for (int r = 0; r < 4; ++r) {
+          const int i = 16 * I + 4 * lg + r;
+          float f = 1.f;
+          if constexpr (GATE == CG_SCALAR) f = (i >= s) ? fast_exp2(sG[i] - sG[s]) : 0.f;
+          lv[r] = (i >= s) ? scale * aL[r] * f : 0.f;
+          dv4[r] = (i > s) ? -aD[r] * f : 0.f;
+        }
+        bf16x4 lo;
+        bf16x4 hi = split_hi4(lv, lo);
+        *reinterpret_cast<bf16x4*>(Lth + s * LDT + 16 * I + 4 * lg) = hi;
+        *reinterpret_cast<bf16x4*>(Ltl + s * LDT + 16 * I + 4 * lg) = lo;
+        hi = split_hi4(dv4, lo);
+        *reinterpret_cast<bf16x4*>(Dth + s * LDT + 16 * I + 4 * lg) = hi;
+        *reinterpret_cast<bf16x4*>(Dtl + s * LDT + 16 * I + 4 * lg) = lo;
+      }
+      {
+        // (b): lane holds rows s = 16 I + 4 lg + r, column i = 16 J + lc
+        const int i = 16 * J + lc;
+        f32x4 lv, dv4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = tid + 512 * i;              // 2048 pieces of 4 floats
-      const int t = p >> 5, k0 = (p & 31) * 4;
-      rg[i] = *reinterpret_cast<const float4*>(g + (tok0 + t) * rsk + (size_t)h * KD + k0);
+        for (int r = 0; r < 4; ++r) {
+          const int s = 16 * I + 4 * lg + r;
+          float f = 1.f;
+          if constexpr (GATE == CG_SCALAR) f = (i >= s) ? fast_exp2(sG[i] - sG[s]) : 0.f;
+          lv[r] = (i >= s) ? scale * bL[r] * f : 0.f;
+          dv4[r] = (i > s) ? -bD[r] * f : 0.f;
+        }
+        bf16x4 lo;
+        bf16x4 hi = split_hi4(lv, lo);
+        *reinterpret_cast<bf16x4*>(Lrh + i * LDT + 16 * I + 4 * lg) = hi;
+        *reinterpret_cast<bf16x4*>(Lrl + i * LDT + 16 * I + 4 * lg) = lo;
+        hi = split_hi4(dv4, lo);
+        *reinterpret_cast<bf16x4*>(Drh + i * LDT + 16 * I + 4 * lg) = hi;
+        *reinterpret_cast<bf16x4*>(Drl + i * LDT + 16 * I + 4 * lg) = lo;
+      }
     }
   }
 
@@ -323,29 +369,29 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
       }
     }
   }
-  __syncthreads();   // P, R, dO no longer needed: region B becomes q^T, k^T, g^T (, b^T)
+  // q, k, g (and b) for the transposed staging (issued before the barrier)
+  const PairPiece rq = load_pair_piece(q + kofs, rsk, tid & 31, (tid >> 5) * 8);
+  const PairPiece rk = load_pair_piece(k + kofs, rsk, tid & 31, (tid >> 5) * 8);
+  PairPiece rb;
+  if constexpr (VEC_B) rb = load_pair_piece(bgate + kofs, rsk, tid & 31, (tid >> 5) * 8);
+  float4 rg[4];
+  if constexpr (GATE == CG_VECTOR) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int p = tid + 512 * i;
-    const int t = p >> 4, k0 = (p & 15) * 8;
-    const bf16* pq = reinterpret_cast<const bf16*>(&rq[i]);
-    const bf16* pk = reinterpret_cast<const bf16*>(&rk[i]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      qT[(k0 + j) * LDT + t] = pq[j];
-      kT[(k0 + j) * LDT + t] = pk[j];
-    }
-    if constexpr (VEC_B) {
-      const bf16* pb = reinterpret_cast<const bf16*>(&rb[i]);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) bT[(k0 + j) * LDT + t] = pb[j];
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + 512 * i;              // 2048 pieces: token t, 4 columns; lanes run over t
+      rg[i] = *reinterpret_cast<const float4*>(g + kofs + (size_t)(p & 63) * rsk + (p >> 6) * 4);
     }
   }
+
+  __syncthreads();   // P, R, dO no longer needed: region B becomes q^T, k^T, g^T (, b^T)
+  store_pair_piece(U32(LY::OFF_QT), LDT / 2, tid & 31, (tid >> 5) * 8, rq);
+  store_pair_piece(U32(LY::OFF_KT), LDT / 2, tid & 31, (tid >> 5) * 8, rk);
+  if constexpr (VEC_B) store_pair_piece(U32(LY::OFF_BT), LDT / 2, tid & 31, (tid >> 5) * 8, rb);
   if constexpr (GATE == CG_VECTOR) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int p = tid + 512 * i;
-      const int t = p >> 5, k0 = (p & 31) * 4;
+      const int t = p & 63, k0 = (p >> 6) * 4;
       gT[(k0 + 0) * LDG + t] = rg[i].x;
       gT[(k0 + 1) * LDG + t] = rg[i].y;
       gT[(k0 + 2) * LDG + t] = rg[i].z;
@@ -354,40 +400,42 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   }
   __syncthreads();
 
-  // gate value at (row i, column kk)
-  auto gate_at = [&](int i, int kk) -> float {
-    if constexpr (GATE == CG_VECTOR) return gT[kk * LDG + i];
-    else if constexpr (GATE == CG_SCALAR) return sG[i];
-    else return 0.f;
-  };
-  auto b_at = [&](int i, int kk) -> float {
-    if constexpr (VEC_B) return to_f32(bT[kk * LDT + i]);
-    else return sBeta[i];
-  };
-
-  // ---------------- phase 4: state-gradient epilogue ----------------
-  // after this block: aq = dq, ak = dk, aw = dG (all per element, before intra)
+  // ---------------- phases 4-5: epilogue + matrix intra, one 16x16 tile at a time ----------------
   float colkdk[2] = {0.f, 0.f};
   float fbrow[2][4];
   f32x4 adb[2][2];     // vector-b family: db = k exp2(g) Eb + k ue
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const int I = 2 * rh + rt;
+    const int i0 = 16 * I + 4 * lg;          // this lane's first row in the tile
 #pragma unroll
     for (int r = 0; r < 4; ++r) fbrow[rt][r] = 0.f;
+    f32x4 be4 = zero4();
+    if constexpr (!VEC_B) be4 = *reinterpret_cast<const f32x4*>(sBeta + i0);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       const int kk = 32 * cs + 16 * ct + lc;
       const float gl = sGl[kk];
+      // per-element operands of this lane's 4 rows
+      f32x4 g4 = zero4();
+      if constexpr (GATE == CG_VECTOR) g4 = *reinterpret_cast<const f32x4*>(gT + kk * LDG + i0);
+      else if constexpr (GATE == CG_SCALAR) g4 = *reinterpret_cast<const f32x4*>(sG + i0);
+      const bf16x4 q4 = *reinterpret_cast<const bf16x4*>(qT + kk * LDT + i0);
+      const bf16x4 k4 = *reinterpret_cast<const bf16x4*>(kT + kk * LDT + i0);
+      f32x4 b4;
+      if constexpr (VEC_B) {
+        const bf16x4 bb4 = *reinterpret_cast<const bf16x4*>(bT + kk * LDT + i0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) b4[r] = to_f32(bb4[r]);
+      } else {
+        b4 = be4;
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 16 * I + 4 * lg + r;
-        const float gi = gate_at(i, kk);
+        const float gi = g4[r];
         const float gam = (GATE == CG_NONE) ? 1.f : fast_exp2(gi);
         const float kdec = (GATE == CG_NONE) ? 1.f : fast_exp2(gl - gi);
-        const float qv = to_f32(qT[kk * LDT + i]);
-        const float kv = to_f32(kT[kk * LDT + i]);
-        const float bv = b_at(i, kk);
+        const float qv = to_f32(q4[r]), kv = to_f32(k4[r]), bv = b4[r];
         const float dqv = aq[rt][ct][r] * gam * scale;
         const float dks = ak[rt][ct][r] * kdec;
         const float eb = -aw[rt][ct][r];
@@ -399,33 +447,21 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
         if constexpr (VEC_B) adb[rt][ct][r] = keb;
         else fbrow[rt][r] += keb;
       }
-    }
-  }
-  // column partial of k * dks from the upper row half -> LDS
-#pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
-    const float s = sum_lane_groups(colkdk[ct]);
-    colkdk[ct] = s;
-    if (rh == 0 && lg == 0) sCol[32 * cs + 16 * ct + lc] = s;
-  }
 
-  // ---------------- phase 5: matrix intra ----------------
-  f32x4 uq[2][2], ue[2][2], uk[2][2];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int I = 2 * rh + rt;
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const int kk = 32 * cs + 16 * ct + lc;     // this lane's column for B fragments
-      float aqa = 0.f, aka = 0.f;                 // anchors (log2) for the q side / k side
+      // ---- matrix intra for this tile ----
+      float aqa = 0.f, aka = 0.f;      // anchors (log2) of the q side / k side
       bool pair = false;
       if constexpr (GATE == CG_VECTOR) {
+        const f32x4* gr = reinterpret_cast<const f32x4*>(gT + kk * LDG + 16 * I);
         float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
-        for (int s = 0; s < 16; ++s) {
-          const float gs = gT[kk * LDG + 16 * I + s];
-          lo = fminf(lo, gs);
-          hi = fmaxf(hi, gs);
+        for (int x = 0; x < 4; ++x) {
+          const f32x4 gg = gr[x];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            lo = fminf(lo, gg[r]);
+            hi = fmaxf(hi, gg[r]);
+          }
         }
         pair = (hi - lo) >= 80.f;
         const float cen = 0.5f * (lo + hi);
@@ -433,29 +469,34 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
         aka = pair ? lo : cen;
       }
       f32x4 xq = zero4(), xe = zero4(), xk = zero4();
-      // uq / ue : s in [0, 16 (I+1))
-      for (int ks = 0; ks <= (I >> 1); ++ks) {
-        bf16x8 bh_, bl_;
+      // uq / ue : s in [0, 16 (I+1)), diagonal block excluded when pairwise
+      const int s_end = pair ? 16 * I : 16 * (I + 1);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks > (I >> 1)) break;
         const int s0 = 32 * ks + 8 * lg;
+        const bf16x8 k8 = *reinterpret_cast<const bf16x8*>(kT + kk * LDT + s0);
+        f32x4 ga = zero4(), gb = zero4();
+        if constexpr (GATE == CG_VECTOR) {
+          ga = *reinterpret_cast<const f32x4*>(gT + kk * LDG + s0);
+          gb = *reinterpret_cast<const f32x4*>(gT + kk * LDG + s0 + 4);
+        }
+        bf16x8 bh_, bl_;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int s = s0 + j;
-          bool ok = s < 16 * (I + 1);
-          if (pair && s >= 16 * I) ok = false;
-          float x = 0.f;
-          if (ok) {
-            x = to_f32(kT[kk * LDT + s]);
-            if constexpr (GATE == CG_VECTOR) x *= fast_exp2(aqa - gT[kk * LDG + s]);
-          }
+          const float gs = j < 4 ? ga[j] : gb[j - 4];
+          float x = to_f32(k8[j]);
+          if constexpr (GATE == CG_VECTOR) x *= fast_exp2(aqa - gs);
+          x = (s0 + j < s_end) ? x : 0.f;
           bf16 hh, ll;
           split_bf16(x, hh, ll);
           bh_[j] = hh;
           bl_[j] = ll;
         }
-        const bf16x8 lh = frag(Lh + (16 * I) * LDT + 32 * ks, LDT);
-        const bf16x8 ll2 = frag(Ll + (16 * I) * LDT + 32 * ks, LDT);
-        const bf16x8 dh2 = frag(Dh + (16 * I) * LDT + 32 * ks, LDT);
-        const bf16x8 dl2 = frag(Dl + (16 * I) * LDT + 32 * ks, LDT);
+        const bf16x8 lh = frag(Lrh + (16 * I) * LDT + 32 * ks, LDT);
+        const bf16x8 ll2 = frag(Lrl + (16 * I) * LDT + 32 * ks, LDT);
+        const bf16x8 dh2 = frag(Drh + (16 * I) * LDT + 32 * ks, LDT);
+        const bf16x8 dl2 = frag(Drl + (16 * I) * LDT + 32 * ks, LDT);
         xq = mfma(lh, bh_, xq);
         xq = mfma(lh, bl_, xq);
         xq = mfma(ll2, bh_, xq);
@@ -463,22 +504,40 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
         xe = mfma(dh2, bl_, xe);
         xe = mfma(dl2, bh_, xe);
       }
-      // uk : s in [16 I, 64); A operand = L^T / D^T rows i, read transposed
-      for (int ks = (I >> 1); ks < 2; ++ks) {
-        bf16x8 qh, ql, eh, el;
+      // uk : s in [16 I, 64), diagonal block excluded when pairwise
+      const int s_beg = pair ? 16 * (I + 1) : 16 * I;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks < (I >> 1)) continue;
         const int s0 = 32 * ks + 8 * lg;
+        const bf16x8 k8 = *reinterpret_cast<const bf16x8*>(kT + kk * LDT + s0);
+        const bf16x8 q8 = *reinterpret_cast<const bf16x8*>(qT + kk * LDT + s0);
+        f32x4 ga = zero4(), gb = zero4(), ba, bb;
+        if constexpr (GATE == CG_VECTOR) {
+          ga = *reinterpret_cast<const f32x4*>(gT + kk * LDG + s0);
+          gb = *reinterpret_cast<const f32x4*>(gT + kk * LDG + s0 + 4);
+        }
+        if constexpr (VEC_B) {
+          const bf16x8 b8 = *reinterpret_cast<const bf16x8*>(bT + kk * LDT + s0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            ba[r] = to_f32(b8[r]);
+            bb[r] = to_f32(b8[r + 4]);
+          }
+        } else {
+          ba = *reinterpret_cast<const f32x4*>(sBeta + s0);
+          bb = *reinterpret_cast<const f32x4*>(sBeta + s0 + 4);
+        }
+        bf16x8 qh, ql, eh, el;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int s = s0 + j;
-          bool ok = s >= 16 * I;
-          if (pair && s < 16 * (I + 1)) ok = false;
-          float xqv = 0.f, xev = 0.f;
-          if (ok) {
-            float f = 1.f;
-            if constexpr (GATE == CG_VECTOR) f = fast_exp2(gT[kk * LDG + s] - aka);
-            xqv = to_f32(qT[kk * LDT + s]) * f;
-            xev = to_f32(kT[kk * LDT + s]) * b_at(s, kk) * f;
-          }
+          const float gs = j < 4 ? ga[j] : gb[j - 4];
+          const float bs = j < 4 ? ba[j] : bb[j - 4];
+          float f = 1.f;
+          if constexpr (GATE == CG_VECTOR) f = fast_exp2(gs - aka);
+          const bool ok = s0 + j >= s_beg;
+          const float xqv = ok ? to_f32(q8[j]) * f : 0.f;
+          const float xev = ok ? to_f32(k8[j]) * bs * f : 0.f;
           bf16 hh, ll;
           split_bf16(xqv, hh, ll);
           qh[j] = hh;
@@ -488,15 +547,20 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
           el[j] = ll;
         }
         bf16x8 lth, ltl, dth, dtl;
-        {
+        if constexpr (LY::LT_COPY) {
+          lth = frag(Lth + (16 * I) * LDT + 32 * ks, LDT);
+          ltl = frag(Ltl + (16 * I) * LDT + 32 * ks, LDT);
+          dth = frag(Dth + (16 * I) * LDT + 32 * ks, LDT);
+          dtl = frag(Dtl + (16 * I) * LDT + 32 * ks, LDT);
+        } else {
           const int i = 16 * I + lc;
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const int s = s0 + j;
-            lth[j] = Lh[s * LDT + i];
-            ltl[j] = Ll[s * LDT + i];
-            dth[j] = Dh[s * LDT + i];
-            dtl[j] = Dl[s * LDT + i];
+            lth[j] = Lrh[s * LDT + i];
+            ltl[j] = Lrl[s * LDT + i];
+            dth[j] = Drh[s * LDT + i];
+            dtl[j] = Drl[s * LDT + i];
           }
         }
         xk = mfma(lth, qh, xk);
@@ -506,67 +570,70 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
         xk = mfma(dth, el, xk);
         xk = mfma(dtl, eh, xk);
       }
-      // output scaling and the exact pairwise diagonal block when the span is wide
+      if constexpr (GATE == CG_VECTOR) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * I + 4 * lg + r;
-        const int kc = kk;
-        if constexpr (GATE == CG_VECTOR) {
-          const float gi = gT[kc * LDG + i];
-          xq[r] *= fast_exp2(gi - aqa);
-          xe[r] *= fast_exp2(gi - aqa);
+        for (int r = 0; r < 4; ++r) {
+          const float gi = g4[r];
+          const float up = fast_exp2(gi - aqa);
+          xq[r] *= up;
+          xe[r] *= up;
           xk[r] *= fast_exp2(aka - gi);
-          if (pair) {
+        }
+        if (pair) {   // exact pairwise diagonal block (gate span >= 80 in log2 units)
+#pragma unroll 1
+          for (int r = 0; r < 4; ++r) {
+            const int i = i0 + r;
+            const float gi = gT[kk * LDG + i];
             float pq = 0.f, pe = 0.f, pk = 0.f;
+#pragma unroll 1
             for (int s = 16 * I; s < 16 * (I + 1); ++s) {
-              const float gs = gT[kc * LDG + s];
-              const float ksv = to_f32(kT[kc * LDT + s]);
+              const float gs = gT[kk * LDG + s];
+              const float ksv = to_f32(kT[kk * LDT + s]);
               if (s <= i) {
                 const float f = fast_exp2(gi - gs);
-                pq += (to_f32(Lh[i * LDT + s]) + to_f32(Ll[i * LDT + s])) * ksv * f;
-                if (s < i) pe += (to_f32(Dh[i * LDT + s]) + to_f32(Dl[i * LDT + s])) * ksv * f;
+                pq += (to_f32(Lrh[i * LDT + s]) + to_f32(Lrl[i * LDT + s])) * ksv * f;
+                if (s < i) pe += (to_f32(Drh[i * LDT + s]) + to_f32(Drl[i * LDT + s])) * ksv * f;
               }
               if (s >= i) {
                 const float f = fast_exp2(gs - gi);
-                const float lsi = to_f32(Lh[s * LDT + i]) + to_f32(Ll[s * LDT + i]);
-                const float dsi = to_f32(Dh[s * LDT + i]) + to_f32(Dl[s * LDT + i]);
-                pk += (lsi * to_f32(qT[kc * LDT + s]) + dsi * b_at(s, kc) * ksv) * f;
+                const float lsi = to_f32(Lrh[s * LDT + i]) + to_f32(Lrl[s * LDT + i]);
+                const float dsi = to_f32(Drh[s * LDT + i]) + to_f32(Drl[s * LDT + i]);
+                float bs;
+                if constexpr (VEC_B) bs = to_f32(bT[kk * LDT + s]);
+                else bs = sBeta[s];
+                pk += (lsi * to_f32(qT[kk * LDT + s]) + dsi * bs * ksv) * f;
               }
             }
-            xq[r] += pq;
-            xe[r] += pe;
-            xk[r] += pk;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              if (rr == r) {
+                xq[rr] += pq;
+                xe[rr] += pe;
+                xk[rr] += pk;
+              }
+            }
           }
         }
       }
-      uq[rt][ct] = xq;
-      ue[rt][ct] = xe;
-      uk[rt][ct] = xk;
-    }
-  }
-  __syncthreads();   // sCol visible
-
-  // ---------------- phase 6: combine, dbeta/db, last-row terms, reverse cumsum, store ----------------
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int I = 2 * rh + rt;
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const int kk = 32 * cs + 16 * ct + lc;
+      // ---- combine ----
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 16 * I + 4 * lg + r;
-        const float qv = to_f32(qT[kk * LDT + i]);
-        const float kv = to_f32(kT[kk * LDT + i]);
-        const float bv = b_at(i, kk);
-        const float xq = uq[rt][ct][r], xe = ue[rt][ct][r], xk = uk[rt][ct][r];
-        if constexpr (VEC_B) adb[rt][ct][r] += kv * xe;
-        aq[rt][ct][r] += xq;
-        ak[rt][ct][r] += bv * xe + xk;
-        aw[rt][ct][r] += qv * xq + kv * (bv * xe - xk);
-        if constexpr (!VEC_B) fbrow[rt][r] += xe * kv;
+        const float qv = to_f32(q4[r]), kv = to_f32(k4[r]), bv = b4[r];
+        aq[rt][ct][r] += xq[r];
+        ak[rt][ct][r] += bv * xe[r] + xk[r];
+        aw[rt][ct][r] += qv * xq[r] + kv * (bv * xe[r] - xk[r]);
+        if constexpr (VEC_B) adb[rt][ct][r] += kv * xe[r];
+        else fbrow[rt][r] += xe[r] * kv;
       }
+      __builtin_amdgcn_sched_barrier(0);   // keep the four tiles' live ranges apart
     }
+  }
+  // column partial of k * dks from the upper row half -> LDS
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    const float s = sum_lane_groups(colkdk[ct]);
+    colkdk[ct] = s;
+    if (rh == 0 && lg == 0) sCol[32 * cs + 16 * ct + lc] = s;
   }
   // fallback dbeta rows: direct terms sum_k (k exp2(g) Eb + k ue)
   if constexpr (!VEC_B) {
@@ -580,9 +647,10 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
         }
     }
   }
+  __syncthreads();   // sCol, sDbB visible
 
+  // ---------------- phase 6: last-row state terms, reverse cumsum, stores ----------------
   if constexpr (GATE == CG_VECTOR) {
-    // last-row state terms: dG[63][kk] += exp2(g_last) sum_v h dh + sum_rows k dks
     if (rh == 1) {
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
@@ -591,13 +659,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
         if (lg == 3) aw[1][ct][3] += term;
       }
     }
-  }
-
-  if constexpr (GATE == CG_VECTOR) {
-    // reverse cumsum over the 64 rows of each column
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
-      float carry = 0.f;                       // total of rows below, inside this row half
+      float carry = 0.f;                       // total of the rows below, inside this row half
 #pragma unroll
       for (int rt = 1; rt >= 0; --rt) {
         f32x4& x = aw[rt][ct];
@@ -605,16 +669,16 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
         x[1] += x[2];
         x[0] += x[1];
         const float tot = x[0];                // this lane group's 4-row total
-        const float t1 = __shfl(tot, (l & 15) + 16 * 1);
-        const float t2 = __shfl(tot, (l & 15) + 16 * 2);
-        const float t3 = __shfl(tot, (l & 15) + 16 * 3);
+        const float t0 = __shfl(tot, lc);
+        const float t1 = __shfl(tot, lc + 16);
+        const float t2 = __shfl(tot, lc + 32);
+        const float t3 = __shfl(tot, lc + 48);
         float below = carry;
         if (lg < 3) below += t3;
         if (lg < 2) below += t2;
         if (lg < 1) below += t1;
 #pragma unroll
         for (int r = 0; r < 4; ++r) x[r] += below;
-        const float t0 = __shfl(tot, (l & 15));
         carry += t0 + t1 + t2 + t3;
       }
       if (rh == 1 && lg == 0) sTot[32 * cs + 16 * ct + lc] = carry;
@@ -653,7 +717,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     __syncthreads();
   }
 
-  // stores of dq, dk (bf16) and the vector dg (fp32)
+  // stores of dq, dk (bf16), the vector dg (fp32) and db (bf16)
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const int I = 2 * rh + rt;
@@ -663,7 +727,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * I + 4 * lg + r;
-        const size_t off = (tok0 + i) * rsk + (size_t)h * KD + kk;
+        const size_t off = kofs + (size_t)i * rsk + kk;
         dq_out[off] = to_bf16(aq[rt][ct][r]);
         dk_out[off] = to_bf16(ak[rt][ct][r]);
         if constexpr (GATE == CG_VECTOR) dg_out[off] = aw[rt][ct][r];
@@ -671,7 +735,6 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
       }
     }
   }
-  __syncthreads();
   if (tid < C) {
     const size_t row = (tok0 + tid) * H + h;
     if constexpr (!VEC_B) {

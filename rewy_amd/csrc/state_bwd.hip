@@ -74,38 +74,42 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
     }
 
   // ---- register staging of one chunk's operands ----
-  // q/k/w: 64 rows x 128 bf16 = 1024 16-byte pieces -> 4 per thread
-  // Aqk:   64 rows x 64 fp32  = 1024 16-byte pieces -> 4 per thread
-  // dO:    64 rows x BV bf16  = 8*BV pieces          -> BV/32 per thread
-  constexpr int NDO = (C * BV / 8) / 256 > 0 ? (C * BV / 8) / 256 : 1;
-  uint4 rq[4], rk[4], rw[4], ra[4], rdo[NDO];
+  // kg rows (row-major copy):        1024 16-byte pieces, 4 per thread
+  // qg, w (transposed, token pairs):  512 pair pieces each, 2 per thread
+  // Aqk (transposed hi/lo):           512 pair pieces, 2 per thread
+  // dO (transposed):                  32 * BV / 8 pair pieces
+  constexpr int NDO = (32 * (BV / 8) + 255) / 256;
+  uint4 rk[4];
+  PairPiece rq[2], rw[2], rdo[NDO];
+  PairPieceF ra[2];
   float rg_last = 0.f, rg_tok = 0.f;
   const size_t row_stride_k = (size_t)H * KD;   // elements between tokens
   const size_t row_stride_v = (size_t)H * VD;
 
   auto load_chunk = [&](int c) {
     const size_t tok0 = (size_t)b * T + (size_t)c * C;
+    const bf16* qb = q + tok0 * row_stride_k + (size_t)h * KD;
+    const bf16* wb = w + tok0 * row_stride_k + (size_t)h * KD;
+    const bf16* kb = k + tok0 * row_stride_k + (size_t)h * KD;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int p = tid + 256 * i;
-      const int t = p >> 4, k0 = (p & 15) * 8;
-      const size_t off = (tok0 + t) * row_stride_k + (size_t)h * KD + k0;
-      rq[i] = *reinterpret_cast<const uint4*>(q + off);
-      rk[i] = *reinterpret_cast<const uint4*>(k + off);
-      rw[i] = *reinterpret_cast<const uint4*>(w + off);
-      if constexpr (DV_FROM_AQK) {
-        const int s = p >> 4, t0 = (p & 15) * 4;
-        ra[i] = *reinterpret_cast<const uint4*>(aqk + ((tok0 + s) * H + h) * C + t0);
-      }
+      rk[i] = *reinterpret_cast<const uint4*>(kb + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + 256 * i;
+      rq[i] = load_pair_piece(qb, row_stride_k, p & 31, (p >> 5) * 8);
+      rw[i] = load_pair_piece(wb, row_stride_k, p & 31, (p >> 5) * 8);
+      if constexpr (DV_FROM_AQK)
+        ra[i] = load_pair_piece_f(aqk + (tok0 * H + h) * C, (size_t)H * C, p & 31, (p >> 5) * 4);
     }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
       const int p = tid + 256 * i;
-      if (p < C * BV / 8) {
-        const int t = p / (BV / 8), v0 = (p % (BV / 8)) * 8;
-        const size_t off = (tok0 + t) * row_stride_v + (size_t)h * VD + v_base + v0;
-        rdo[i] = *reinterpret_cast<const uint4*>(dO + off);
-      }
+      if (p < 32 * (BV / 8))
+        rdo[i] = load_pair_piece(dO + tok0 * row_stride_v + (size_t)h * VD + v_base, row_stride_v, p & 31,
+                                 (p >> 5) * 8);
     }
     if constexpr (GATE == GATE_VECTOR) {
       if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
@@ -115,7 +119,6 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
     }
   };
 
-  // dv (precomputed dv_local) is added straight from global into the dR tile.
   auto stage_chunk = [&]() {
     if constexpr (GATE == GATE_VECTOR) {
       if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
@@ -128,52 +131,42 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
     } else {
       if (tid < KD) sm.lam[tid] = 1.f;
     }
-    if constexpr (GATE == GATE_SCALAR) __syncthreads();  // gam / lam needed below
+    if constexpr (GATE == GATE_SCALAR) __syncthreads();  // gam / gkf needed below
+    uint32_t* qT = reinterpret_cast<uint32_t*>(&sm.qT[0][0]);
+    uint32_t* wT = reinterpret_cast<uint32_t*>(&sm.wT[0][0]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int p = tid + 256 * i;
       const int t = p >> 4, k0 = (p & 15) * 8;
-      const bf16* pq = reinterpret_cast<const bf16*>(&rq[i]);
-      const bf16* pk = reinterpret_cast<const bf16*>(&rk[i]);
-      const bf16* pw = reinterpret_cast<const bf16*>(&rw[i]);
       if constexpr (GATE == GATE_SCALAR) {
-        const float gq = sm.gam[t];
+        const bf16* pk = reinterpret_cast<const bf16*>(&rk[i]);
         const float gk = sm.gkf[t];
         bf16x8 kk;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          sm.qT[k0 + j][t] = to_bf16(to_f32(pq[j]) * gq);
-          kk[j] = to_bf16(to_f32(pk[j]) * gk);
-        }
+        for (int j = 0; j < 8; ++j) kk[j] = to_bf16(to_f32(pk[j]) * gk);
         *reinterpret_cast<bf16x8*>(&sm.k[t][k0]) = kk;
       } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sm.qT[k0 + j][t] = pq[j];
         *reinterpret_cast<uint4*>(&sm.k[t][k0]) = rk[i];
       }
+    }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) sm.wT[k0 + j][t] = to_bf16(-to_f32(pw[j]));
-      if constexpr (DV_FROM_AQK) {
-        const int s = p >> 4, t0 = (p & 15) * 4;
-        const float* pa = reinterpret_cast<const float*>(&ra[i]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          bf16 hi, lo;
-          split_bf16(pa[j], hi, lo);
-          sm.aTh[t0 + j][s] = hi;
-          sm.aTl[t0 + j][s] = lo;
-        }
-      }
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + 256 * i;
+      const int tp = p & 31;
+      if constexpr (GATE == GATE_SCALAR)
+        store_pair_piece_scaled(qT, S::LDT / 2, tp, (p >> 5) * 8, rq[i], sm.gam[2 * tp], sm.gam[2 * tp + 1]);
+      else
+        store_pair_piece(qT, S::LDT / 2, tp, (p >> 5) * 8, rq[i]);
+      store_pair_piece_scaled(wT, S::LDT / 2, tp, (p >> 5) * 8, rw[i], -1.f, -1.f);
+      if constexpr (DV_FROM_AQK)
+        store_pair_piece_split(reinterpret_cast<uint32_t*>(&sm.aTh[0][0]), reinterpret_cast<uint32_t*>(&sm.aTl[0][0]),
+                               S::LDT / 2, tp, (p >> 5) * 4, ra[i], 1.f);
     }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
       const int p = tid + 256 * i;
-      if (p < C * BV / 8) {
-        const int t = p / (BV / 8), v0 = (p % (BV / 8)) * 8;
-        const bf16* pd = reinterpret_cast<const bf16*>(&rdo[i]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sm.doT[v0 + j][t] = pd[j];
-      }
+      if (p < 32 * (BV / 8))
+        store_pair_piece(reinterpret_cast<uint32_t*>(&sm.doT[0][0]), S::LDT / 2, p & 31, (p >> 5) * 8, rdo[i]);
     }
   };
 
@@ -262,7 +255,7 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
       const size_t dh_base = (((size_t)b * NT + c) * H + h) * KD * VD;
       constexpr int NP = KD * BV / 8;
       for (int p = tid; p < NP; p += 256) {
-        const int kr = p / (BV / 8), v0 = (p % (BV / 8)) * 8;
+        const int kr = p % KD, v0 = (p / KD) * 8;      // lanes run over rows: conflict-free LDS reads
         bf16x8 o;
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = sm.dhT[v0 + j][kr];
@@ -271,7 +264,7 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
       const size_t tok0 = (size_t)b * T + (size_t)c * C;
       constexpr int NR = C * BV / 8;
       for (int p = tid; p < NR; p += 256) {
-        const int t = p / (BV / 8), v0 = (p % (BV / 8)) * 8;
+        const int t = p % C, v0 = (p / C) * 8;
         bf16x8 o;
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = sm.drT[v0 + j][t];

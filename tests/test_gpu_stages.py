@@ -35,12 +35,16 @@ def _setup(op, B, T, H, seed, **kw):
     return xs, dO, sv
 
 
-@pytest.mark.parametrize("op", ["kda", "gdn", "delta", "gdn2"])
-@pytest.mark.parametrize("B,T,H", [(1, 128, 2), (2, 256, 3)])
-def test_state_and_chunk_kernels(op, B, T, H):
+CASES = [(op, shp, "default", 0) for op in ("kda", "gdn", "delta", "gdn2") for shp in ((1, 128, 2), (2, 256, 3))]
+CASES += [("kda", (1, 192, 2), "wide", 5), ("gdn2", (1, 192, 2), "wide", 0), ("gdn", (1, 128, 2), "default", 3)]
+
+
+@pytest.mark.parametrize("op,shape,gate,bz", CASES)
+def test_state_and_chunk_kernels(op, shape, gate, bz):
     from rewy_amd import ops
-    print(f"\n[stage] op={op} B={B} T={T} H={H}", flush=True)
-    xs, dO, sv = _setup(op, B, T, H, seed=11)
+    B, T, H = shape
+    print(f"\n[stage] op={op} B={B} T={T} H={H} gate={gate} beta_zero_every={bz}", flush=True)
+    xs, dO, sv = _setup(op, B, T, H, seed=11, gate=gate, beta_zero_every=bz)
     dev = torch.device("cuda")
     scale = sv["scale"]
     cu = lambda x: None if x is None else x.to(dev).contiguous()
