@@ -36,7 +36,8 @@ def hipcc() -> str:
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", str(src), "-o", str(obj)]
+    extra = os.environ.get("REWY_HIPCC_FLAGS", "").split()   # e.g. -DREWY_INTRA_B_SPLIT=1
+    cmd = [hipcc(), *FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr[-4000:]}")

@@ -46,6 +46,13 @@ namespace rewy {
 
 enum GateModeC { CG_NONE = 0, CG_SCALAR = 1, CG_VECTOR = 2 };
 
+// Split the gate-weighted key/query operands of the intra contractions into
+// bf16 hi + lo (three MFMAs per product) or keep them single bf16 (two MFMAs:
+// the fp32 L/D coefficients are always split).
+#ifndef REWY_INTRA_B_SPLIT
+#define REWY_INTRA_B_SPLIT 1
+#endif
+
 namespace post {
 constexpr int LDT = 72;    // bf16 pitch of [.][64] tiles
 constexpr int LDV = 136;   // bf16 pitch of [.][128] tiles
@@ -254,16 +261,15 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   }
   __syncthreads();
 
-  // prefetch state tiles for phase 3 (B operands straight from global)
-  bf16x8 fh[2][4], fdh[2][4];
+  // prefetch state tiles for phase 3: wave wv owns key columns [16 wv, 16 wv + 16)
+  const int kk = 16 * wv + lc;                 // this lane's key column from here on
+  bf16x8 fh[4], fdh[4];
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const size_t o = hoff + (size_t)(32 * cs + 16 * ct + lc) * VD + 32 * ks + 8 * lg;
-      fh[ct][ks] = *reinterpret_cast<const bf16x8*>(hst + o);
-      fdh[ct][ks] = *reinterpret_cast<const bf16x8*>(dhst + o);
-    }
+  for (int ks = 0; ks < 4; ++ks) {
+    const size_t o = hoff + (size_t)kk * VD + 32 * ks + 8 * lg;
+    fh[ks] = *reinterpret_cast<const bf16x8*>(hst + o);
+    fdh[ks] = *reinterpret_cast<const bf16x8*>(dhst + o);
+  }
 
   // ---------------- phase 2: L = scale tril(dO R^T), D = -strict_tril(P R^T), both orientations ----------------
   {
@@ -338,35 +344,28 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     }
   }
 
-  // ---------------- phase 3: dq_s = dO h^T, dk_s = R dh^T, dw = P h^T ----------------
-  f32x4 aq[2][2], ak[2][2], aw[2][2];
-  float dgk[2];
+  // ---------------- phase 3: dq_s = dO h^T, dk_s = R dh^T, dw = P h^T (16-column strip, 64 rows) ----------------
+  f32x4 aq[4], ak[4], aw[4];
+  float dgk;
   {
+    float sacc = 0.f;
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      float sacc = 0.f;
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+      for (int j = 0; j < 8; ++j) sacc += to_f32(fh[ks][j]) * to_f32(fdh[ks][j]);
+    dgk = sum_lane_groups(sacc);               // sum_v h[kk][v] dh[kk][v]
 #pragma unroll
-        for (int j = 0; j < 8; ++j) sacc += to_f32(fh[ct][ks][j]) * to_f32(fdh[ct][ks][j]);
-      dgk[ct] = sum_lane_groups(sacc);
-    }
+    for (int I = 0; I < 4; ++I) {
+      f32x4 x = zero4(), y = zero4(), z = zero4();
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int I = 2 * rh + rt;
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        f32x4 x = zero4(), y = zero4(), z = zero4();
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          x = mfma(frag(sdO + (16 * I) * LDV + 32 * ks, LDV), fh[ct][ks], x);
-          y = mfma(frag(sR + (16 * I) * LDV + 32 * ks, LDV), fdh[ct][ks], y);
-          z = mfma(frag(sP + (16 * I) * LDV + 32 * ks, LDV), fh[ct][ks], z);
-        }
-        aq[rt][ct] = x;
-        ak[rt][ct] = y;
-        aw[rt][ct] = z;
+      for (int ks = 0; ks < 4; ++ks) {
+        x = mfma(frag(sdO + (16 * I) * LDV + 32 * ks, LDV), fh[ks], x);
+        y = mfma(frag(sR + (16 * I) * LDV + 32 * ks, LDV), fdh[ks], y);
+        z = mfma(frag(sP + (16 * I) * LDV + 32 * ks, LDV), fh[ks], z);
       }
+      aq[I] = x;
+      ak[I] = y;
+      aw[I] = z;
     }
   }
   // q, k, g (and b) for the transposed staging (issued before the barrier)
@@ -382,7 +381,6 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
       rg[i] = *reinterpret_cast<const float4*>(g + kofs + (size_t)(p & 63) * rsk + (p >> 6) * 4);
     }
   }
-
   __syncthreads();   // P, R, dO no longer needed: region B becomes q^T, k^T, g^T (, b^T)
   store_pair_piece(U32(LY::OFF_QT), LDT / 2, tid & 31, (tid >> 5) * 8, rq);
   store_pair_piece(U32(LY::OFF_KT), LDT / 2, tid & 31, (tid >> 5) * 8, rk);
@@ -400,341 +398,310 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   }
   __syncthreads();
 
-  // ---------------- phases 4-5: epilogue + matrix intra, one 16x16 tile at a time ----------------
-  float colkdk[2] = {0.f, 0.f};
-  float fbrow[2][4];
-  f32x4 adb[2][2];     // vector-b family: db = k exp2(g) Eb + k ue
+  // ---------------- per-lane operands of column kk, rows 16 J + 4 lg + j ----------------
+  // In the accumulator layout and in the B layout of the K=16 MFMA a lane holds the
+  // same four rows of one column, so one set of per-element values serves the
+  // epilogue, the intra operands and the output scaling.
+  f32x4 g4[4];
+  bf16x4 qb4[4], kb4[4];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int I = 2 * rh + rt;
-    const int i0 = 16 * I + 4 * lg;          // this lane's first row in the tile
+  for (int J = 0; J < 4; ++J) {
+    const int r0 = 16 * J + 4 * lg;
+    if constexpr (GATE == CG_VECTOR) g4[J] = *reinterpret_cast<const f32x4*>(gT + kk * LDG + r0);
+    else if constexpr (GATE == CG_SCALAR) g4[J] = *reinterpret_cast<const f32x4*>(sG + r0);
+    else g4[J] = zero4();
+    qb4[J] = *reinterpret_cast<const bf16x4*>(qT + kk * LDT + r0);
+    kb4[J] = *reinterpret_cast<const bf16x4*>(kT + kk * LDT + r0);
+  }
+  // erase gate of rows 16 J + 4 lg .. +3 (reloaded from LDS where needed)
+  auto bvals = [&](int J) -> f32x4 {
+    const int r0 = 16 * J + 4 * lg;
+    if constexpr (VEC_B) {
+      const bf16x4 bq = *reinterpret_cast<const bf16x4*>(bT + kk * LDT + r0);
+      f32x4 o;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) fbrow[rt][r] = 0.f;
-    f32x4 be4 = zero4();
-    if constexpr (!VEC_B) be4 = *reinterpret_cast<const f32x4*>(sBeta + i0);
+      for (int j = 0; j < 4; ++j) o[j] = to_f32(bq[j]);
+      return o;
+    } else {
+      return *reinterpret_cast<const f32x4*>(sBeta + r0);
+    }
+  };
+  // gate extremes of each 16-row block (this column) and the per-element ratios
+  //   EB = 2^(bot_J - g) <= 1,  ET = 2^(g - top_J) <= 1
+  float top[4], bot[4];
+  bool pair[4];
+  f32x4 EB[4], ET[4];
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const int kk = 32 * cs + 16 * ct + lc;
-      const float gl = sGl[kk];
-      // per-element operands of this lane's 4 rows
-      f32x4 g4 = zero4();
-      if constexpr (GATE == CG_VECTOR) g4 = *reinterpret_cast<const f32x4*>(gT + kk * LDG + i0);
-      else if constexpr (GATE == CG_SCALAR) g4 = *reinterpret_cast<const f32x4*>(sG + i0);
-      const bf16x4 q4 = *reinterpret_cast<const bf16x4*>(qT + kk * LDT + i0);
-      const bf16x4 k4 = *reinterpret_cast<const bf16x4*>(kT + kk * LDT + i0);
-      f32x4 b4;
-      if constexpr (VEC_B) {
-        const bf16x4 bb4 = *reinterpret_cast<const bf16x4*>(bT + kk * LDT + i0);
+  for (int J = 0; J < 4; ++J) {
+    float hi = fmaxf(fmaxf(g4[J][0], g4[J][1]), fmaxf(g4[J][2], g4[J][3]));
+    float lo = fminf(fminf(g4[J][0], g4[J][1]), fminf(g4[J][2], g4[J][3]));
+    hi = fmaxf(hi, __shfl_xor(hi, 16));
+    hi = fmaxf(hi, __shfl_xor(hi, 32));
+    lo = fminf(lo, __shfl_xor(lo, 16));
+    lo = fminf(lo, __shfl_xor(lo, 32));
+    top[J] = hi;
+    bot[J] = lo;
+    pair[J] = (GATE == CG_VECTOR) && (hi - lo) >= 80.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) b4[r] = to_f32(bb4[r]);
-      } else {
-        b4 = be4;
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float gi = g4[r];
-        const float gam = (GATE == CG_NONE) ? 1.f : fast_exp2(gi);
-        const float kdec = (GATE == CG_NONE) ? 1.f : fast_exp2(gl - gi);
-        const float qv = to_f32(q4[r]), kv = to_f32(k4[r]), bv = b4[r];
-        const float dqv = aq[rt][ct][r] * gam * scale;
-        const float dks = ak[rt][ct][r] * kdec;
-        const float eb = -aw[rt][ct][r];
-        const float keb = kv * gam * eb;
-        aq[rt][ct][r] = dqv;
-        ak[rt][ct][r] = dks + bv * gam * eb;
-        aw[rt][ct][r] = qv * dqv - kv * dks + bv * keb;
-        colkdk[ct] += kv * dks;
-        if constexpr (VEC_B) adb[rt][ct][r] = keb;
-        else fbrow[rt][r] += keb;
-      }
-
-      // ---- matrix intra for this tile ----
-      float aqa = 0.f, aka = 0.f;      // anchors (log2) of the q side / k side
-      bool pair = false;
-      if constexpr (GATE == CG_VECTOR) {
-        const f32x4* gr = reinterpret_cast<const f32x4*>(gT + kk * LDG + 16 * I);
-        float lo = INFINITY, hi = -INFINITY;
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          const f32x4 gg = gr[x];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            lo = fminf(lo, gg[r]);
-            hi = fmaxf(hi, gg[r]);
-          }
-        }
-        pair = (hi - lo) >= 80.f;
-        const float cen = 0.5f * (lo + hi);
-        aqa = pair ? hi : cen;
-        aka = pair ? lo : cen;
-      }
-      f32x4 xq = zero4(), xe = zero4(), xk = zero4();
-      // uq / ue : s in [0, 16 (I+1)), diagonal block excluded when pairwise
-      const int s_end = pair ? 16 * I : 16 * (I + 1);
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (ks > (I >> 1)) break;
-        const int s0 = 32 * ks + 8 * lg;
-        const bf16x8 k8 = *reinterpret_cast<const bf16x8*>(kT + kk * LDT + s0);
-        f32x4 ga = zero4(), gb = zero4();
-        if constexpr (GATE == CG_VECTOR) {
-          ga = *reinterpret_cast<const f32x4*>(gT + kk * LDG + s0);
-          gb = *reinterpret_cast<const f32x4*>(gT + kk * LDG + s0 + 4);
-        }
-        bf16x8 bh_, bl_;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float gs = j < 4 ? ga[j] : gb[j - 4];
-          float x = to_f32(k8[j]);
-          if constexpr (GATE == CG_VECTOR) x *= fast_exp2(aqa - gs);
-          x = (s0 + j < s_end) ? x : 0.f;
-          bf16 hh, ll;
-          split_bf16(x, hh, ll);
-          bh_[j] = hh;
-          bl_[j] = ll;
-        }
-        const bf16x8 lh = frag(Lrh + (16 * I) * LDT + 32 * ks, LDT);
-        const bf16x8 ll2 = frag(Lrl + (16 * I) * LDT + 32 * ks, LDT);
-        const bf16x8 dh2 = frag(Drh + (16 * I) * LDT + 32 * ks, LDT);
-        const bf16x8 dl2 = frag(Drl + (16 * I) * LDT + 32 * ks, LDT);
-        xq = mfma(lh, bh_, xq);
-        xq = mfma(lh, bl_, xq);
-        xq = mfma(ll2, bh_, xq);
-        xe = mfma(dh2, bh_, xe);
-        xe = mfma(dh2, bl_, xe);
-        xe = mfma(dl2, bh_, xe);
-      }
-      // uk : s in [16 I, 64), diagonal block excluded when pairwise
-      const int s_beg = pair ? 16 * (I + 1) : 16 * I;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (ks < (I >> 1)) continue;
-        const int s0 = 32 * ks + 8 * lg;
-        const bf16x8 k8 = *reinterpret_cast<const bf16x8*>(kT + kk * LDT + s0);
-        const bf16x8 q8 = *reinterpret_cast<const bf16x8*>(qT + kk * LDT + s0);
-        f32x4 ga = zero4(), gb = zero4(), ba, bb;
-        if constexpr (GATE == CG_VECTOR) {
-          ga = *reinterpret_cast<const f32x4*>(gT + kk * LDG + s0);
-          gb = *reinterpret_cast<const f32x4*>(gT + kk * LDG + s0 + 4);
-        }
-        if constexpr (VEC_B) {
-          const bf16x8 b8 = *reinterpret_cast<const bf16x8*>(bT + kk * LDT + s0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            ba[r] = to_f32(b8[r]);
-            bb[r] = to_f32(b8[r + 4]);
-          }
-        } else {
-          ba = *reinterpret_cast<const f32x4*>(sBeta + s0);
-          bb = *reinterpret_cast<const f32x4*>(sBeta + s0 + 4);
-        }
-        bf16x8 qh, ql, eh, el;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float gs = j < 4 ? ga[j] : gb[j - 4];
-          const float bs = j < 4 ? ba[j] : bb[j - 4];
-          float f = 1.f;
-          if constexpr (GATE == CG_VECTOR) f = fast_exp2(gs - aka);
-          const bool ok = s0 + j >= s_beg;
-          const float xqv = ok ? to_f32(q8[j]) * f : 0.f;
-          const float xev = ok ? to_f32(k8[j]) * bs * f : 0.f;
-          bf16 hh, ll;
-          split_bf16(xqv, hh, ll);
-          qh[j] = hh;
-          ql[j] = ll;
-          split_bf16(xev, hh, ll);
-          eh[j] = hh;
-          el[j] = ll;
-        }
-        bf16x8 lth, ltl, dth, dtl;
-        if constexpr (LY::LT_COPY) {
-          lth = frag(Lth + (16 * I) * LDT + 32 * ks, LDT);
-          ltl = frag(Ltl + (16 * I) * LDT + 32 * ks, LDT);
-          dth = frag(Dth + (16 * I) * LDT + 32 * ks, LDT);
-          dtl = frag(Dtl + (16 * I) * LDT + 32 * ks, LDT);
-        } else {
-          const int i = 16 * I + lc;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int s = s0 + j;
-            lth[j] = Lrh[s * LDT + i];
-            ltl[j] = Lrl[s * LDT + i];
-            dth[j] = Drh[s * LDT + i];
-            dtl[j] = Drl[s * LDT + i];
-          }
-        }
-        xk = mfma(lth, qh, xk);
-        xk = mfma(lth, ql, xk);
-        xk = mfma(ltl, qh, xk);
-        xk = mfma(dth, eh, xk);
-        xk = mfma(dth, el, xk);
-        xk = mfma(dtl, eh, xk);
-      }
-      if constexpr (GATE == CG_VECTOR) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float gi = g4[r];
-          const float up = fast_exp2(gi - aqa);
-          xq[r] *= up;
-          xe[r] *= up;
-          xk[r] *= fast_exp2(aka - gi);
-        }
-        if (pair) {   // exact pairwise diagonal block (gate span >= 80 in log2 units)
-#pragma unroll 1
-          for (int r = 0; r < 4; ++r) {
-            const int i = i0 + r;
-            const float gi = gT[kk * LDG + i];
-            float pq = 0.f, pe = 0.f, pk = 0.f;
-#pragma unroll 1
-            for (int s = 16 * I; s < 16 * (I + 1); ++s) {
-              const float gs = gT[kk * LDG + s];
-              const float ksv = to_f32(kT[kk * LDT + s]);
-              if (s <= i) {
-                const float f = fast_exp2(gi - gs);
-                pq += (to_f32(Lrh[i * LDT + s]) + to_f32(Lrl[i * LDT + s])) * ksv * f;
-                if (s < i) pe += (to_f32(Drh[i * LDT + s]) + to_f32(Drl[i * LDT + s])) * ksv * f;
-              }
-              if (s >= i) {
-                const float f = fast_exp2(gs - gi);
-                const float lsi = to_f32(Lrh[s * LDT + i]) + to_f32(Lrl[s * LDT + i]);
-                const float dsi = to_f32(Drh[s * LDT + i]) + to_f32(Drl[s * LDT + i]);
-                float bs;
-                if constexpr (VEC_B) bs = to_f32(bT[kk * LDT + s]);
-                else bs = sBeta[s];
-                pk += (lsi * to_f32(qT[kk * LDT + s]) + dsi * bs * ksv) * f;
-              }
-            }
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-              if (rr == r) {
-                xq[rr] += pq;
-                xe[rr] += pe;
-                xk[rr] += pk;
-              }
-            }
-          }
-        }
-      }
-      // ---- combine ----
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float qv = to_f32(q4[r]), kv = to_f32(k4[r]), bv = b4[r];
-        aq[rt][ct][r] += xq[r];
-        ak[rt][ct][r] += bv * xe[r] + xk[r];
-        aw[rt][ct][r] += qv * xq[r] + kv * (bv * xe[r] - xk[r]);
-        if constexpr (VEC_B) adb[rt][ct][r] += kv * xe[r];
-        else fbrow[rt][r] += xe[r] * kv;
-      }
-      __builtin_amdgcn_sched_barrier(0);   // keep the four tiles' live ranges apart
+    for (int j = 0; j < 4; ++j) {
+      EB[J][j] = (GATE == CG_VECTOR) ? fast_exp2(lo - g4[J][j]) : 1.f;
+      ET[J][j] = (GATE == CG_VECTOR) ? fast_exp2(g4[J][j] - hi) : 1.f;
     }
   }
-  // column partial of k * dks from the upper row half -> LDS
+  const float gl = sGl[kk];
+
+  // ---------------- phase 4: state-gradient epilogue ----------------
+  float colkdk = 0.f;
+  f32x4 fbrow[4];      // scalar-beta fallback rows: k exp2(g) Eb + k ue, summed over columns later
+  f32x4 adb[4];        // vector-b family: db = k exp2(g) Eb + k ue
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
-    const float s = sum_lane_groups(colkdk[ct]);
-    colkdk[ct] = s;
-    if (rh == 0 && lg == 0) sCol[32 * cs + 16 * ct + lc] = s;
+  for (int I = 0; I < 4; ++I) {
+    float gtop = 1.f, gdec = 1.f;
+    if constexpr (GATE == CG_VECTOR) {
+      gtop = fast_exp2(top[I]);            // exp2(g_i) = exp2(top) * ET
+      gdec = fast_exp2(gl - bot[I]);       // exp2(g_last - g_i) = exp2(g_last - bot) * EB
+    }
+    const f32x4 b4 = bvals(I);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float gam = 1.f, kdec = 1.f;
+      if constexpr (GATE == CG_VECTOR) {
+        gam = gtop * ET[I][r];
+        kdec = gdec * EB[I][r];
+      } else if constexpr (GATE == CG_SCALAR) {
+        gam = fast_exp2(g4[I][r]);
+        kdec = fast_exp2(gl - g4[I][r]);
+      }
+      const float qv = to_f32(qb4[I][r]), kv = to_f32(kb4[I][r]), bv = b4[r];
+      const float dqv = aq[I][r] * gam * scale;
+      const float dks = ak[I][r] * kdec;
+      const float eb = -aw[I][r];
+      const float keb = kv * gam * eb;
+      aq[I][r] = dqv;
+      ak[I][r] = dks + bv * gam * eb;
+      aw[I][r] = qv * dqv - kv * dks + bv * keb;
+      colkdk += kv * dks;
+      if constexpr (VEC_B) adb[I][r] = keb;
+      else fbrow[I][r] = keb;
+    }
   }
-  // fallback dbeta rows: direct terms sum_k (k exp2(g) Eb + k ue)
+
+  // ---------------- phase 5: matrix intra as K=16 MFMAs per 16-row sub-block ----------------
+  // B operands (shared by every output block): kE = k EB, qE = q ET, bkE = b k ET,
+  // split into bf16 hi + lo.  Sub-block J contributes to output block I with the
+  // per-column factor 2^(top_I - bot_J) (uq, ue; J <= I) or 2^(top_J - bot_I) (uk; J >= I),
+  // and the per-row factor ET_i (uq, ue) or EB_i (uk).
+  bf16x4 kEh[4], kEl[4], qEh[4], qEl[4], eEh[4], eEl[4];
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    const f32x4 b4 = bvals(J);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float kv = to_f32(kb4[J][j]);
+      bf16 h_, l_;
+      split_bf16(kv * EB[J][j], h_, l_);
+      kEh[J][j] = h_;
+      kEl[J][j] = l_;
+      split_bf16(to_f32(qb4[J][j]) * ET[J][j], h_, l_);
+      qEh[J][j] = h_;
+      qEl[J][j] = l_;
+      split_bf16(b4[j] * kv * ET[J][j], h_, l_);
+      eEh[J][j] = h_;
+      eEl[J][j] = l_;
+    }
+  }
+  auto mfma16 = [](bf16x4 a, bf16x4 b, f32x4 c) -> f32x4 {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a), __builtin_bit_cast(s4, b), c, 0, 0, 0);
+  };
+  auto afrag4 = [&](const bf16* base) -> bf16x4 {   // rows (lc), cols 4 lg .. 4 lg + 3
+    return *reinterpret_cast<const bf16x4*>(base + lc * LDT + 4 * lg);
+  };
+#pragma unroll
+  for (int I = 0; I < 4; ++I) {
+    f32x4 xq = zero4(), xe = zero4(), xk = zero4();
+#pragma unroll
+    for (int J = 0; J <= I; ++J) {
+      // MFMA operands are read from all 64 lanes, so fragments are loaded and the
+      // products issued for every lane; a pairwise column (diagonal block with a
+      // wide gate span) drops its own result through a zero factor instead.
+      const bf16x4 lh = afrag4(Lrh + (16 * I) * LDT + 16 * J), ll = afrag4(Lrl + (16 * I) * LDT + 16 * J);
+      const bf16x4 dh_ = afrag4(Drh + (16 * I) * LDT + 16 * J), dl_ = afrag4(Drl + (16 * I) * LDT + 16 * J);
+      f32x4 a = zero4(), e = zero4();
+      a = mfma16(lh, kEh[J], a);
+      a = mfma16(lh, kEl[J], a);
+      a = mfma16(ll, kEh[J], a);
+      e = mfma16(dh_, kEh[J], e);
+      e = mfma16(dh_, kEl[J], e);
+      e = mfma16(dl_, kEh[J], e);
+      float cf = (GATE == CG_VECTOR) ? fast_exp2(top[I] - bot[J]) : 1.f;
+      if (J == I && pair[I]) cf = 0.f;        // exact pairwise diagonal below
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        xq[r] += cf * a[r];
+        xe[r] += cf * e[r];
+      }
+    }
+#pragma unroll
+    for (int J = I; J < 4; ++J) {
+      bf16x4 lh, ll, dh_, dl_;
+      if constexpr (LY::LT_COPY) {
+        lh = afrag4(Lth + (16 * I) * LDT + 16 * J);
+        ll = afrag4(Ltl + (16 * I) * LDT + 16 * J);
+        dh_ = afrag4(Dth + (16 * I) * LDT + 16 * J);
+        dl_ = afrag4(Dtl + (16 * I) * LDT + 16 * J);
+      } else {
+        const int i = 16 * I + lc;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int s = 16 * J + 4 * lg + j;
+          lh[j] = Lrh[s * LDT + i];
+          ll[j] = Lrl[s * LDT + i];
+          dh_[j] = Drh[s * LDT + i];
+          dl_[j] = Drl[s * LDT + i];
+        }
+      }
+      f32x4 a = zero4();
+      a = mfma16(lh, qEh[J], a);
+      a = mfma16(lh, qEl[J], a);
+      a = mfma16(ll, qEh[J], a);
+      a = mfma16(dh_, eEh[J], a);
+      a = mfma16(dh_, eEl[J], a);
+      a = mfma16(dl_, eEh[J], a);
+      float cf = (GATE == CG_VECTOR) ? fast_exp2(top[J] - bot[I]) : 1.f;
+      if (J == I && pair[I]) cf = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xk[r] += cf * a[r];
+    }
+    if constexpr (GATE == CG_VECTOR) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        xq[r] *= ET[I][r];
+        xe[r] *= ET[I][r];
+        xk[r] *= EB[I][r];
+      }
+      if (pair[I]) {   // exact pairwise diagonal block (gate span >= 80 in log2 units)
+#pragma unroll 1
+        for (int r = 0; r < 4; ++r) {
+          const int i = 16 * I + 4 * lg + r;
+          const float gi = gT[kk * LDG + i];
+          float pq = 0.f, pe = 0.f, pk = 0.f;
+#pragma unroll 1
+          for (int s = 16 * I; s < 16 * (I + 1); ++s) {
+            const float gs = gT[kk * LDG + s];
+            const float ksv = to_f32(kT[kk * LDT + s]);
+            if (s <= i) {
+              const float f = fast_exp2(gi - gs);
+              pq += (to_f32(Lrh[i * LDT + s]) + to_f32(Lrl[i * LDT + s])) * ksv * f;
+              if (s < i) pe += (to_f32(Drh[i * LDT + s]) + to_f32(Drl[i * LDT + s])) * ksv * f;
+            }
+            if (s >= i) {
+              const float f = fast_exp2(gs - gi);
+              const float lsi = to_f32(Lrh[s * LDT + i]) + to_f32(Lrl[s * LDT + i]);
+              const float dsi = to_f32(Drh[s * LDT + i]) + to_f32(Drl[s * LDT + i]);
+              float bs;
+              if constexpr (VEC_B) bs = to_f32(bT[kk * LDT + s]);
+              else bs = sBeta[s];
+              pk += (lsi * to_f32(qT[kk * LDT + s]) + dsi * bs * ksv) * f;
+            }
+          }
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            if (rr == r) {
+              xq[rr] += pq;
+              xe[rr] += pe;
+              xk[rr] += pk;
+            }
+          }
+        }
+      }
+    }
+    // combine
+    const f32x4 b4 = bvals(I);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float qv = to_f32(qb4[I][r]), kv = to_f32(kb4[I][r]), bv = b4[r];
+      aq[I][r] += xq[r];
+      ak[I][r] += bv * xe[r] + xk[r];
+      aw[I][r] += qv * xq[r] + kv * (bv * xe[r] - xk[r]);
+      if constexpr (VEC_B) adb[I][r] += kv * xe[r];
+      else fbrow[I][r] += xe[r] * kv;
+    }
+  }
+
+  // fallback dbeta rows: direct terms sum_k (k exp2(g) Eb + k ue), summed over all columns
   if constexpr (!VEC_B) {
     if (has_fb) {
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int I = 0; I < 4; ++I)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float s = sum_row16(fbrow[rt][r]);
-          if (lc == 0) atomicAdd(&sDbB[16 * (2 * rh + rt) + 4 * lg + r], s);
+          const float s = sum_row16(fbrow[I][r]);
+          if (lc == 0) atomicAdd(&sDbB[16 * I + 4 * lg + r], s);
         }
     }
   }
-  __syncthreads();   // sCol, sDbB visible
 
   // ---------------- phase 6: last-row state terms, reverse cumsum, stores ----------------
+  colkdk = sum_lane_groups(colkdk);            // sum over the 64 rows of k dks (this column)
   if constexpr (GATE == CG_VECTOR) {
-    if (rh == 1) {
+    const float term = fast_exp2(gl) * dgk + colkdk;
+    if (lg == 3) aw[3][3] += term;
+    float carry = 0.f;                         // total of the rows below
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const int kk = 32 * cs + 16 * ct + lc;
-        const float term = fast_exp2(sGl[kk]) * dgk[ct] + colkdk[ct] + sCol[kk];
-        if (lg == 3) aw[1][ct][3] += term;
-      }
-    }
+    for (int I = 3; I >= 0; --I) {
+      f32x4& x = aw[I];
+      x[2] += x[3];
+      x[1] += x[2];
+      x[0] += x[1];
+      const float tot = x[0];                  // this lane group's 4-row total
+      const float t0 = __shfl(tot, lc);
+      const float t1 = __shfl(tot, lc + 16);
+      const float t2 = __shfl(tot, lc + 32);
+      const float t3 = __shfl(tot, lc + 48);
+      float below = carry;
+      if (lg < 3) below += t3;
+      if (lg < 2) below += t2;
+      if (lg < 1) below += t1;
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      float carry = 0.f;                       // total of the rows below, inside this row half
-#pragma unroll
-      for (int rt = 1; rt >= 0; --rt) {
-        f32x4& x = aw[rt][ct];
-        x[2] += x[3];
-        x[1] += x[2];
-        x[0] += x[1];
-        const float tot = x[0];                // this lane group's 4-row total
-        const float t0 = __shfl(tot, lc);
-        const float t1 = __shfl(tot, lc + 16);
-        const float t2 = __shfl(tot, lc + 32);
-        const float t3 = __shfl(tot, lc + 48);
-        float below = carry;
-        if (lg < 3) below += t3;
-        if (lg < 2) below += t2;
-        if (lg < 1) below += t1;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) x[r] += below;
-        carry += t0 + t1 + t2 + t3;
-      }
-      if (rh == 1 && lg == 0) sTot[32 * cs + 16 * ct + lc] = carry;
-    }
-    __syncthreads();
-    if (rh == 0) {
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const float add = sTot[32 * cs + 16 * ct + lc];
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) aw[rt][ct][r] += add;
-      }
+      for (int r = 0; r < 4; ++r) x[r] += below;
+      carry += t0 + t1 + t2 + t3;
     }
   } else if constexpr (GATE == CG_SCALAR) {
     // scalar gate: dG row sums over all 128 columns, then the last-row state term
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int I = 0; I < 4; ++I)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float s = aw[rt][0][r] + aw[rt][1][r];
-        s = sum_row16(s);
-        if (lc == 0) atomicAdd(&sDg[16 * (2 * rh + rt) + 4 * lg + r], s);
+        const float s = sum_row16(aw[I][r]);
+        if (lc == 0) atomicAdd(&sDg[16 * I + 4 * lg + r], s);
       }
-    if (rh == 1) {
-      float term = 0.f;
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const int kk = 32 * cs + 16 * ct + lc;
-        term += fast_exp2(sGl[kk]) * dgk[ct] + colkdk[ct] + sCol[kk];
-      }
-      term = sum_row16(term);
-      if (l == 0) atomicAdd(&sDg[C - 1], term);
-    }
-    __syncthreads();
+    float term = fast_exp2(gl) * dgk + colkdk;
+    term = sum_row16(term);
+    if (l == 0) atomicAdd(&sDg[C - 1], term);
   }
 
-  // stores of dq, dk (bf16), the vector dg (fp32) and db (bf16)
+  // stores of dq, dk (bf16), the vector dg (fp32) and db (bf16); 32-bit offsets
+  // from uniform per-chunk-head bases
+  {
+    bf16* dqb = dq_out + kofs;
+    bf16* dkb = dk_out + kofs;
+    float* dgb = dg_out + kofs;
+    bf16* dbb = db_out + kofs;
+    const int rsk32 = H * KD;
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int I = 2 * rh + rt;
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const int kk = 32 * cs + 16 * ct + lc;
+    for (int I = 0; I < 4; ++I) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 16 * I + 4 * lg + r;
-        const size_t off = kofs + (size_t)i * rsk + kk;
-        dq_out[off] = to_bf16(aq[rt][ct][r]);
-        dk_out[off] = to_bf16(ak[rt][ct][r]);
-        if constexpr (GATE == CG_VECTOR) dg_out[off] = aw[rt][ct][r];
-        if constexpr (VEC_B) db_out[off] = to_bf16(adb[rt][ct][r]);
+        const int off = (16 * I + 4 * lg + r) * rsk32 + kk;
+        dqb[off] = to_bf16(aq[I][r]);
+        dkb[off] = to_bf16(ak[I][r]);
+        if constexpr (GATE == CG_VECTOR) dgb[off] = aw[I][r];
+        if constexpr (VEC_B) dbb[off] = to_bf16(adb[I][r]);
       }
     }
   }
+  __syncthreads();   // sDbB, sDg complete
   if (tid < C) {
     const size_t row = (tok0 + tid) * H + h;
     if constexpr (!VEC_B) {

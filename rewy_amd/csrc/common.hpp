@@ -24,6 +24,10 @@ constexpr int VD = 128;   // value width
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
+// An MFMA reads its A/B operands from all 64 lanes whatever the EXEC mask, so
+// operands must never be produced under lane-divergent control flow (lanes
+// that skipped the producing load would feed stale registers to every output
+// column).  Branch on wave-uniform values only around MFMAs and their loads.
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

@@ -38,7 +38,7 @@ struct StateSmem {
 };
 
 template <int BV, int GATE, bool DV_FROM_AQK>
-__global__ __launch_bounds__(256) void state_bwd_kernel(
+__global__ __launch_bounds__(512) void state_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ w,
     const float* __restrict__ g, const bf16* __restrict__ dO, const float* __restrict__ aqk,
     const bf16* __restrict__ dv, const float* __restrict__ dht, bf16* __restrict__ dh_out,
@@ -55,33 +55,37 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int v_base = vt * BV;
 
-  // ---- state accumulators: wave wv owns key rows [32 wv, 32 wv + 32) ----
-  f32x4 st[2][NCT];
+  // ---- state accumulators: wave wv owns key rows [16 wv, 16 wv + 16) ----
+  constexpr int NTH = 512;
+  f32x4 st[NCT];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int ct = 0; ct < NCT; ++ct) {
+    f32x4 a = zero4();
+    if (dht) {
+      const float* src = dht + (size_t)bh * KD * VD;
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
-      f32x4 a = zero4();
-      if (dht) {
-        const float* src = dht + (size_t)bh * KD * VD;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int kr = 32 * wv + 16 * rt + 4 * (l >> 4) + r;
-          a[r] = src[kr * VD + v_base + 16 * ct + (l & 15)];
-        }
+      for (int r = 0; r < 4; ++r) {
+        const int kr = 16 * wv + 4 * (l >> 4) + r;
+        a[r] = src[kr * VD + v_base + 16 * ct + (l & 15)];
       }
-      st[rt][ct] = a;
     }
+    st[ct] = a;
+  }
+  // dR tiles: wave wv owns row tile (wv & 3) and column tiles [DCT * (wv >> 2), DCT * (wv >> 2) + DCT)
+  constexpr int DCT = NCT >= 2 ? NCT / 2 : 1;
+  const int drow = wv & 3;
+  const int dct0 = DCT * (wv >> 2);
+  const bool has_dr = dct0 < NCT;
 
   // ---- register staging of one chunk's operands ----
-  // kg rows (row-major copy):        1024 16-byte pieces, 4 per thread
-  // qg, w (transposed, token pairs):  512 pair pieces each, 2 per thread
-  // Aqk (transposed hi/lo):           512 pair pieces, 2 per thread
+  // kg rows (row-major copy):        1024 16-byte pieces, 2 per thread
+  // qg, w (transposed, token pairs):  512 pair pieces each, 1 per thread
+  // Aqk (transposed hi/lo):           512 pair pieces, 1 per thread
   // dO (transposed):                  32 * BV / 8 pair pieces
-  constexpr int NDO = (32 * (BV / 8) + 255) / 256;
-  uint4 rk[4];
-  PairPiece rq[2], rw[2], rdo[NDO];
-  PairPieceF ra[2];
+  constexpr int NDO = (32 * (BV / 8) + NTH - 1) / NTH;
+  uint4 rk[2];
+  PairPiece rq[1], rw[1], rdo[NDO];
+  PairPieceF ra[1];
   float rg_last = 0.f, rg_tok = 0.f;
   const size_t row_stride_k = (size_t)H * KD;   // elements between tokens
   const size_t row_stride_v = (size_t)H * VD;
@@ -92,13 +96,13 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
     const bf16* wb = w + tok0 * row_stride_k + (size_t)h * KD;
     const bf16* kb = k + tok0 * row_stride_k + (size_t)h * KD;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = tid + 256 * i;
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + NTH * i;
       rk[i] = *reinterpret_cast<const uint4*>(kb + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int p = tid + 256 * i;
+    for (int i = 0; i < 1; ++i) {
+      const int p = tid + NTH * i;
       rq[i] = load_pair_piece(qb, row_stride_k, p & 31, (p >> 5) * 8);
       rw[i] = load_pair_piece(wb, row_stride_k, p & 31, (p >> 5) * 8);
       if constexpr (DV_FROM_AQK)
@@ -106,7 +110,7 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
     }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
-      const int p = tid + 256 * i;
+      const int p = tid + NTH * i;
       if (p < 32 * (BV / 8))
         rdo[i] = load_pair_piece(dO + tok0 * row_stride_v + (size_t)h * VD + v_base, row_stride_v, p & 31,
                                  (p >> 5) * 8);
@@ -135,8 +139,8 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
     uint32_t* qT = reinterpret_cast<uint32_t*>(&sm.qT[0][0]);
     uint32_t* wT = reinterpret_cast<uint32_t*>(&sm.wT[0][0]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = tid + 256 * i;
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + NTH * i;
       const int t = p >> 4, k0 = (p & 15) * 8;
       if constexpr (GATE == GATE_SCALAR) {
         const bf16* pk = reinterpret_cast<const bf16*>(&rk[i]);
@@ -150,8 +154,8 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
       }
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int p = tid + 256 * i;
+    for (int i = 0; i < 1; ++i) {
+      const int p = tid + NTH * i;
       const int tp = p & 31;
       if constexpr (GATE == GATE_SCALAR)
         store_pair_piece_scaled(qT, S::LDT / 2, tp, (p >> 5) * 8, rq[i], sm.gam[2 * tp], sm.gam[2 * tp + 1]);
@@ -164,7 +168,7 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
     }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
-      const int p = tid + 256 * i;
+      const int p = tid + NTH * i;
       if (p < 32 * (BV / 8))
         store_pair_piece(reinterpret_cast<uint32_t*>(&sm.doT[0][0]), S::LDT / 2, p & 31, (p >> 5) * 8, rdo[i]);
     }
@@ -177,84 +181,76 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
     if (c > 0) load_chunk(c - 1);          // prefetch; consumed next iteration
     // dh (state at the end of chunk c) -> LDS, transposed, bf16
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) {
-        bf16x4 v4;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[rt][ct][r]);
-        *reinterpret_cast<bf16x4*>(&sm.dhT[16 * ct + (l & 15)][32 * wv + 16 * rt + 4 * (l >> 4)]) = v4;
-      }
-    __syncthreads();
-
-    // X = qg^T dO (independent of dh)
-    f32x4 xq[2][NCT];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) {
-        f32x4 a = zero4();
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-          a = mfma(frag(&sm.qT[32 * wv + 16 * rt][32 * ks], S::LDT), frag(&sm.doT[16 * ct][32 * ks], S::LDT), a);
-        xq[rt][ct] = a;
-      }
-    // dR tile rows [16 wv, 16 wv + 16): kg dh + Aqk^T dO (+ dv)
-    f32x4 dr[NCT];
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
-      f32x4 a = zero4();
-      if constexpr (DV_FROM_AQK) {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const bf16x8 bo = frag(&sm.doT[16 * ct][32 * ks], S::LDT);
-          a = mfma(frag(&sm.aTh[16 * wv][32 * ks], S::LDT), bo, a);
-          a = mfma(frag(&sm.aTl[16 * wv][32 * ks], S::LDT), bo, a);
-        }
-      } else {
-        const size_t tok0 = (size_t)b * T + (size_t)c * C;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 16 * wv + 4 * (l >> 4) + r;
-          a[r] = to_f32(dv[(tok0 + t) * row_stride_v + (size_t)h * VD + v_base + 16 * ct + (l & 15)]);
-        }
-      }
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        a = mfma(frag(&sm.k[16 * wv][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), a);
-      dr[ct] = a;
-    }
-#pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
       bf16x4 v4;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v4[r] = to_bf16(dr[ct][r]);
-      *reinterpret_cast<bf16x4*>(&sm.drT[16 * ct + (l & 15)][16 * wv + 4 * (l >> 4)]) = v4;
+      for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[ct][r]);
+      *reinterpret_cast<bf16x4*>(&sm.dhT[16 * ct + (l & 15)][16 * wv + 4 * (l >> 4)]) = v4;
+    }
+    __syncthreads();
+
+    // X = qg^T dO (independent of dh)
+    f32x4 xq[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      f32x4 a = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        a = mfma(frag(&sm.qT[16 * wv][32 * ks], S::LDT), frag(&sm.doT[16 * ct][32 * ks], S::LDT), a);
+      xq[ct] = a;
+    }
+    // dR tiles: kg dh + Aqk^T dO (+ dv)
+    if (has_dr) {
+#pragma unroll
+      for (int cc = 0; cc < DCT; ++cc) {
+        const int ct = dct0 + cc;
+        f32x4 a = zero4();
+        if constexpr (DV_FROM_AQK) {
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 bo = frag(&sm.doT[16 * ct][32 * ks], S::LDT);
+            a = mfma(frag(&sm.aTh[16 * drow][32 * ks], S::LDT), bo, a);
+            a = mfma(frag(&sm.aTl[16 * drow][32 * ks], S::LDT), bo, a);
+          }
+        } else {
+          const size_t tok0 = (size_t)b * T + (size_t)c * C;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 16 * drow + 4 * (l >> 4) + r;
+            a[r] = to_f32(dv[(tok0 + t) * row_stride_v + (size_t)h * VD + v_base + 16 * ct + (l & 15)]);
+          }
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          a = mfma(frag(&sm.k[16 * drow][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), a);
+        bf16x4 v4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v4[r] = to_bf16(a[r]);
+        *reinterpret_cast<bf16x4*>(&sm.drT[16 * ct + (l & 15)][16 * drow + 4 * (l >> 4)]) = v4;
+      }
     }
     __syncthreads();
 
     // dh <- lambda * dh + scale * X - w^T dR
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int ct = 0; ct < NCT; ++ct) {
+      f32x4 a;
 #pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) {
-        f32x4 a;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int kr = 32 * wv + 16 * rt + 4 * (l >> 4) + r;
-          a[r] = st[rt][ct][r] * sm.lam[kr] + scale * xq[rt][ct][r];
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-          a = mfma(frag(&sm.wT[32 * wv + 16 * rt][32 * ks], S::LDT), frag(&sm.drT[16 * ct][32 * ks], S::LDT), a);
-        st[rt][ct] = a;
+      for (int r = 0; r < 4; ++r) {
+        const int kr = 16 * wv + 4 * (l >> 4) + r;
+        a[r] = st[ct][r] * sm.lam[kr] + scale * xq[ct][r];
       }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        a = mfma(frag(&sm.wT[16 * wv][32 * ks], S::LDT), frag(&sm.drT[16 * ct][32 * ks], S::LDT), a);
+      st[ct] = a;
+    }
 
     // global stores of dh[c] and dR_c from the transposed LDS copies
     {
       const size_t dh_base = (((size_t)b * NT + c) * H + h) * KD * VD;
       constexpr int NP = KD * BV / 8;
-      for (int p = tid; p < NP; p += 256) {
+      for (int p = tid; p < NP; p += NTH) {
         const int kr = p % KD, v0 = (p / KD) * 8;      // lanes run over rows: conflict-free LDS reads
         bf16x8 o;
 #pragma unroll
@@ -263,7 +259,7 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
       }
       const size_t tok0 = (size_t)b * T + (size_t)c * C;
       constexpr int NR = C * BV / 8;
-      for (int p = tid; p < NR; p += 256) {
+      for (int p = tid; p < NR; p += NTH) {
         const int t = p % C, v0 = (p / C) * 8;
         bf16x8 o;
 #pragma unroll
@@ -276,14 +272,12 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(
   if (dh0) {
     float* dst = dh0 + (size_t)bh * KD * VD;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
-      for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int kr = 32 * wv + 16 * rt + 4 * (l >> 4) + r;
-          dst[kr * VD + v_base + 16 * ct + (l & 15)] = st[rt][ct][r];
-        }
+      for (int r = 0; r < 4; ++r) {
+        const int kr = 16 * wv + 4 * (l >> 4) + r;
+        dst[kr * VD + v_base + 16 * ct + (l & 15)] = st[ct][r];
+      }
   }
 }
 
@@ -293,7 +287,7 @@ static hipError_t launch_state(const void* q, const void* k, const void* w, cons
                                void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
                                hipStream_t stream) {
   const int grid = B * H * (VD / BV);
-  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK>), dim3(grid), dim3(256), 0, stream,
+  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK>), dim3(grid), dim3(512), 0, stream,
                      (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk,
                      (const bf16*)dv, dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale);
   return hipGetLastError();
