@@ -67,6 +67,8 @@ def main():
     ap.add_argument("--config", default="kda", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-original", action="store_true", help="skip the torch original comparator")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device copy (reference kernel for the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); every GPU box in this "
@@ -74,6 +76,15 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.calibrate_copy:
+        n = 1 << 28                                   # 1 GiB of fp32
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_read": 4 * n, "calibrate_copy_bytes_written": 4 * n}))
+        return
     from rewy_amd import ops
     from rewy_amd.backends.backward import kda_backward
     from rewy_amd.forward import chunk_forward
@@ -193,13 +204,26 @@ def main():
         "kernels": {n: {kk: round(vv, 4) for kk, vv in d.items()} for n, d in kernels.items()},
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": dom_bytes},
+                     "traffic": measured_traffic(dom, args.config), "algorithmic_bytes_per_launch": dom_bytes},
         "original_torch_ms": None if t_orig is None else round(t_orig, 3),
         "speedup_vs_original_torch": None if t_orig is None else round(t_orig / ms, 2),
         "parity_vs_original": parity,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def measured_traffic(kernel, config):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (profiles/hbm_traffic.json, calibrated against a plain
+    copy of known size), or None when that workload was not profiled."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data[config][kernel]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(xs, sv, dO, dh, dR, scale, NTt, heads_per_piece=1):
@@ -214,16 +238,17 @@ def cpu_baseline(xs, sv, dO, dh, dR, scale, NTt, heads_per_piece=1):
         threadpool_limits = None
     from oracle import delta_oracle as O
     B, T, H = xs["q"].shape[:3]
-    heads = min(8, H)
-    sample_heads = heads * (T // 64)
+    heads = H
+    nb = min(B, 3)                               # batches 0..nb-1, every head: ~10 s of fp64 work
+    sample_heads = nb * heads * (T // 64)
     ctx = threadpool_limits(limits=1) if threadpool_limits else None
     if ctx:
         ctx.__enter__()
     el = 0.0
     try:
-        for h0 in range(0, heads, heads_per_piece):
+        for bb, h0 in [(bb, h0) for bb in range(nb) for h0 in range(0, heads, heads_per_piece)]:
             hs = slice(h0, h0 + heads_per_piece)
-            n = lambda x: x[:1, :, hs].double().cpu().numpy()
+            n = lambda x: x[bb:bb + 1, :, hs].double().cpu().numpy()
             inp = dict(qg=n(sv["qg"]), kg=n(sv["kg"]), w=n(sv["w"]), gc=n(sv["gc"]), dO=n(dO),
                        Aqk=n(sv["Aqk"]), q=n(xs["q"]), k=n(xs["k"]), v=n(xs["v"]), beta=n(xs["beta"]),
                        Akk=n(sv["Akk"]), h=n(sv["h"]), v_new=n(sv["v_new"]))
@@ -240,7 +265,7 @@ def cpu_baseline(xs, sv, dO, dh, dR, scale, NTt, heads_per_piece=1):
     full_ms = el * 1e3 * NTt / sample_heads
     return {"value": round(full_ms, 1), "unit": "ms (full workload, extrapolated)", "cores": 1,
             "kind": "port",
-            "sample": f"fp64 numpy oracle (state recurrence + chunk stage), batch 0, T={T}, heads 0-{heads - 1} "
+            "sample": f"fp64 numpy oracle (state recurrence + chunk stage), batches 0-{nb - 1}, T={T}, all {heads} heads "
                       f"({sample_heads} of {NTt} chunk-heads), measured {el:.2f} s, scaled linearly"}
 
 
