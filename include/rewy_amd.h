@@ -72,6 +72,32 @@ hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v, const void
                          void* dv, float* dg, float* dbeta, void* db, void* dw, int B, int T,
                          int H, int K, int V, int chunk, float scale, hipStream_t stream);
 
+/*
+ * Recompute of the WY factors inside the backward (recompute policy).
+ * Replaces FLA recompute_w_u_fwd (called at reference backends/backward.py:110-116):
+ *   w = Akk (b k 2^g), u = Akk (w_gate v)            -> bf16 [B,T,H,K] / [B,T,H,V]
+ * and optionally (vector gate) qg = q 2^g, kg = k 2^(g_last - g) (bf16), or
+ * (scalar / no gate) the intra-chunk scores Aqk = scale tril(q k^T 2^(g_i - g_s))
+ * (fp32 [B,T,H,64]) that FLA chunk_bwd_dv_local forms (backward.py:119).
+ * Scalar-beta families pass beta and null b_gate/w_gate; GDN2 passes b_gate/w_gate.
+ */
+hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const float* g,
+                          int gate_mode, const float* beta, const void* b_gate, const void* w_gate,
+                          const float* Akk, void* w, void* u, void* qg, void* kg, float* Aqk, int B,
+                          int T, int H, int K, int V, int chunk, float scale, hipStream_t stream);
+
+/*
+ * Forward state scan recomputed inside the backward.
+ * Replaces FLA chunk_gated_delta_rule_fwd_h(k, w, u, g, initial_state, ...) -> (h, v_new, final)
+ * as called at reference backends/backward.py:117-118:
+ *   h[c] = state at chunk start (bf16 [B,T/64,H,K,V]); v_new_c = u_c - w_c h_c (bf16);
+ *   state <- lambda_c state + kg_c^T v_new_c;  ht = final state (fp32, may be null).
+ * For gate_mode 2, `k` is the gate-weighted kg; for modes 0/1 it is the raw k.
+ */
+hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g, int gate_mode,
+                     const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int K,
+                     int V, int chunk, int value_block, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,7 +5,8 @@ Same callables, keyword signatures and return tuples as the reference's
 ``gdn_backward`` :133, ``delta_backward`` :136), which are keyword-compatible
 with FLA's ``chunk_<op>_bwd``.  Each one runs
 
-  1. (recompute policy only) w, u, qg, kg, v_new, h from the saved tensors;
+  1. (recompute policy) ``fdr_prepare_wu`` -- w, u (and qg, kg or Aqk) -- and
+     ``fdr_fwd_h`` -- h, v_new -- from the saved tensors;
   2. ``fdr_state_bwd``  -- reverse state recurrence with dv_local = Aqk^T dO fused in;
   3. ``fdr_chunk_bwd``  -- residual-WY products, dAqk, matrix intra, gate/beta
      epilogue and the in-chunk reverse cumsum of dg, one work-group per chunk.
@@ -17,7 +18,6 @@ from __future__ import annotations
 import torch
 
 from .. import ops
-from ..forward import recompute
 
 _UNSUPPORTED = ("cu_seqlens", "chunk_indices", "cp_context", "chunk_offsets")
 
@@ -53,7 +53,7 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     g = _f32(g)
     Aqk, Akk = _f32(Aqk), _f32(Akk)
     if saved.get("h") is None:
-        saved = recompute(op, q, k, v, g, Akk, initial_state=initial_state, **gates)
+        saved = _recompute_vector(q, k, v, g, Akk, initial_state, gates)
     dh, dR, dh0 = ops.state_bwd(_bf(saved["qg"]), _bf(saved["kg"]), _bf(saved["w"]), g,
                                 ops.GATE_VECTOR, do, scale, aqk=Aqk, dht=_f32(dht),
                                 want_dh0=initial_state is not None)
@@ -62,6 +62,16 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
                         b=None if gates.get("b") is None else _bf(gates["b"]),
                         w=None if gates.get("w") is None else _bf(gates["w"]))
     return out, dh0
+
+
+def _recompute_vector(q, k, v, g, Akk, initial_state, gates):
+    """w, u, qg, kg (fdr_prepare_wu) then h, v_new (fdr_fwd_h): the recompute policy."""
+    b = None if gates.get("b") is None else _bf(gates["b"])
+    w = None if gates.get("w") is None else _bf(gates["w"])
+    pre = ops.prepare_wu(k, v, Akk, ops.GATE_VECTOR, g=g, beta=_f32(gates.get("beta")), b=b, w=w, q=q,
+                         want_qkg=True)
+    h, v_new, _ = ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state))
+    return dict(w=pre["w"], u=pre["u"], qg=pre["qg"], kg=pre["kg"], v_new=v_new, h=h)
 
 
 def kda_backward(q, k, v, beta, Aqk, Akk, scale, initial_state, do, dht, g, g_org=None,
@@ -106,13 +116,12 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, **kw):
     g = _f32(g)
     A = _f32(A)
     beta = _f32(beta)
-    saved = recompute(op, q, k, v, g, A, beta=beta, initial_state=initial_state)
     gate = ops.GATE_SCALAR if op == "gdn" else ops.GATE_NONE
-    aqk = _aqk_scalar(q, k, g, scale)
-    dh, dR, dh0 = ops.state_bwd(q, k, _bf(saved["w"]), g, gate, do, scale, aqk=aqk, dht=_f32(dht),
+    pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, q=q, want_aqk=True, scale=scale)
+    h, v_new, _ = ops.fwd_h(k, pre["w"], pre["u"], g, gate, h0=_f32(initial_state))
+    dh, dR, dh0 = ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
                                 want_dh0=initial_state is not None)
-    out = ops.chunk_bwd(q, k, v, _bf(saved["v_new"]), do, dR, g, gate, A, _bf(saved["h"]), dh, scale,
-                        beta=beta)
+    out = ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta)
     record(op, "optimized_backward")
     return out, dh0
 

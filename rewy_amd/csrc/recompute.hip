@@ -1,0 +1,508 @@
+// Forward recomputation inside the backward (recompute policy).
+//
+// Replaces FLA's recompute_w_u_fwd and chunk_gated_delta_rule_fwd_h as called at
+// reference backends/backward.py:110-118 (GDN / DeltaNet always; KDA / GDN2 when
+// the forward did not save its intermediates), plus the intra-chunk scores of
+// FLA's chunk_bwd_dv_local for the scalar-gate families.
+//
+//   fdr_prepare_wu (one work-group per chunk-head):
+//     w   = Akk (b k 2^g)        bf16 [B,T,H,K]
+//     u   = Akk (w_gate v)       bf16 [B,T,H,V]
+//     qg  = q 2^g, kg = k 2^(g_last - g)           (vector gates, optional)
+//     Aqk = scale tril(q k^T 2^(g_i - g_s))        (scalar / no gate, optional)
+//   fdr_fwd_h (sequential over chunks, one work-group per (batch, head, value tile)):
+//     h_c -> h[c] (bf16); v_new_c = u_c - w_c h_c (bf16); h_{c+1} = lambda_c h_c + kg_c^T v_new_c
+//
+// The WY products are computed transposed (w^T = E^T A^T) so the accumulator
+// layout stores w and u contiguously; A and E are split into bf16 hi + lo so
+// the products are fp32-faithful.
+#include "common.hpp"
+
+namespace rewy {
+
+enum GateModeR { RG_NONE = 0, RG_SCALAR = 1, RG_VECTOR = 2 };
+
+namespace rec {
+constexpr int LDT = 72;
+constexpr int T128 = KD * LDT * 2;
+}
+
+// ------------------------------------------------------------------------------------------
+// fdr_prepare_wu
+// ------------------------------------------------------------------------------------------
+template <int GATE, bool VEC_B, bool WANT_QKG, bool WANT_AQK>
+__global__ __launch_bounds__(256) void prepare_wu_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
+    const bf16* __restrict__ wgate, const float* __restrict__ akk, bf16* __restrict__ w_out,
+    bf16* __restrict__ u_out, bf16* __restrict__ qg_out, bf16* __restrict__ kg_out,
+    float* __restrict__ aqk_out, int T, int H, float scale) {
+  using rec::LDT;
+  // E^T hi/lo [128][72], Z^T hi/lo [128][72] (Z = w_gate v), small gate arrays
+  __shared__ __attribute__((aligned(16))) bf16 eTh[KD][LDT];
+  __shared__ __attribute__((aligned(16))) bf16 eTl[KD][LDT];
+  __shared__ __attribute__((aligned(16))) bf16 zTh[VD][LDT];
+  __shared__ __attribute__((aligned(16))) bf16 zTl[VD][LDT];
+  __shared__ float sG[C];
+  __shared__ float sB[C];
+
+  const int NT = T / C;
+  const int blk = blockIdx.x;
+  const int c = blk % NT;
+  const int bh = blk / NT;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
+  const int lc = l & 15, lg = l >> 4;
+  const size_t tok0 = (size_t)b * T + (size_t)c * C;
+  const size_t rsk = (size_t)H * KD, rsv = (size_t)H * VD;
+  const size_t kofs = tok0 * rsk + (size_t)h * KD;
+  const size_t vofs = tok0 * rsv + (size_t)h * VD;
+
+  if (tid < C) {
+    const size_t row = (tok0 + tid) * H + h;
+    sG[tid] = (GATE == RG_SCALAR) ? g[row] : 0.f;
+    sB[tid] = VEC_B ? 0.f : beta[row];
+  }
+  __syncthreads();
+
+  // ---- stage E^T = (b k 2^g)^T and Z^T = (w_gate v)^T, split hi/lo, token pairs per dword ----
+  {
+    // 512 pair pieces (32 token pairs x 16 column chunks of 8) per matrix; 2 per thread
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + 256 * i;
+      const int tp = p & 31, c0 = (p >> 5) * 8;
+      const int t0 = 2 * tp;
+      const PairPiece pk = load_pair_piece(k + kofs, rsk, tp, c0);
+      const PairPiece pv = load_pair_piece(v + vofs, rsv, tp, c0);
+      const bf16* ka = reinterpret_cast<const bf16*>(&pk.a);
+      const bf16* kb = reinterpret_cast<const bf16*>(&pk.b);
+      const bf16* va = reinterpret_cast<const bf16*>(&pv.a);
+      const bf16* vb = reinterpret_cast<const bf16*>(&pv.b);
+      float ea[8], eb[8], za[8], zb[8];
+      float ga[8], gb[8], ba[8], bb[8], wa[8], wb[8];
+      if constexpr (GATE == RG_VECTOR) {
+        const float4 g0 = *reinterpret_cast<const float4*>(g + kofs + (size_t)t0 * rsk + c0);
+        const float4 g1 = *reinterpret_cast<const float4*>(g + kofs + (size_t)t0 * rsk + c0 + 4);
+        const float4 g2 = *reinterpret_cast<const float4*>(g + kofs + (size_t)(t0 + 1) * rsk + c0);
+        const float4 g3 = *reinterpret_cast<const float4*>(g + kofs + (size_t)(t0 + 1) * rsk + c0 + 4);
+        const float gg0[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float gg1[8] = {g2.x, g2.y, g2.z, g2.w, g3.x, g3.y, g3.z, g3.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          ga[j] = fast_exp2(gg0[j]);
+          gb[j] = fast_exp2(gg1[j]);
+        }
+      } else {
+        const float s0 = (GATE == RG_SCALAR) ? fast_exp2(sG[t0]) : 1.f;
+        const float s1 = (GATE == RG_SCALAR) ? fast_exp2(sG[t0 + 1]) : 1.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          ga[j] = s0;
+          gb[j] = s1;
+        }
+      }
+      if constexpr (VEC_B) {
+        const uint4 b0 = *reinterpret_cast<const uint4*>(bgate + kofs + (size_t)t0 * rsk + c0);
+        const uint4 b1 = *reinterpret_cast<const uint4*>(bgate + kofs + (size_t)(t0 + 1) * rsk + c0);
+        const uint4 w0 = *reinterpret_cast<const uint4*>(wgate + vofs + (size_t)t0 * rsv + c0);
+        const uint4 w1 = *reinterpret_cast<const uint4*>(wgate + vofs + (size_t)(t0 + 1) * rsv + c0);
+        const bf16* pb0 = reinterpret_cast<const bf16*>(&b0);
+        const bf16* pb1 = reinterpret_cast<const bf16*>(&b1);
+        const bf16* pw0 = reinterpret_cast<const bf16*>(&w0);
+        const bf16* pw1 = reinterpret_cast<const bf16*>(&w1);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          ba[j] = to_f32(pb0[j]);
+          bb[j] = to_f32(pb1[j]);
+          wa[j] = to_f32(pw0[j]);
+          wb[j] = to_f32(pw1[j]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          ba[j] = wa[j] = sB[t0];
+          bb[j] = wb[j] = sB[t0 + 1];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        ea[j] = ba[j] * to_f32(ka[j]) * ga[j];
+        eb[j] = bb[j] * to_f32(kb[j]) * gb[j];
+        za[j] = wa[j] * to_f32(va[j]);
+        zb[j] = wb[j] * to_f32(vb[j]);
+        bf16 ah, al, bh_, bl_;
+        split_bf16(ea[j], ah, al);
+        split_bf16(eb[j], bh_, bl_);
+        reinterpret_cast<uint32_t*>(&eTh[c0 + j][0])[tp] = pack2(ah, bh_);
+        reinterpret_cast<uint32_t*>(&eTl[c0 + j][0])[tp] = pack2(al, bl_);
+        split_bf16(za[j], ah, al);
+        split_bf16(zb[j], bh_, bl_);
+        reinterpret_cast<uint32_t*>(&zTh[c0 + j][0])[tp] = pack2(ah, bh_);
+        reinterpret_cast<uint32_t*>(&zTl[c0 + j][0])[tp] = pack2(al, bl_);
+      }
+    }
+  }
+
+  // ---- qg / kg (vector gates): elementwise, coalesced ----
+  if constexpr (WANT_QKG && GATE == RG_VECTOR) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + 256 * i;          // 1024 pieces of 8
+      const int t = p >> 4, c0 = (p & 15) * 8;
+      const uint4 qq = *reinterpret_cast<const uint4*>(q + kofs + (size_t)t * rsk + c0);
+      const uint4 kq = *reinterpret_cast<const uint4*>(k + kofs + (size_t)t * rsk + c0);
+      const float* gr = g + kofs + (size_t)t * rsk + c0;
+      const float* gl = g + kofs + (size_t)(C - 1) * rsk + c0;
+      const bf16* pq = reinterpret_cast<const bf16*>(&qq);
+      const bf16* pk = reinterpret_cast<const bf16*>(&kq);
+      bf16x8 oq, ok;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float gj = gr[j];
+        oq[j] = to_bf16(to_f32(pq[j]) * fast_exp2(gj));
+        ok[j] = to_bf16(to_f32(pk[j]) * fast_exp2(gl[j] - gj));
+      }
+      *reinterpret_cast<bf16x8*>(qg_out + kofs + (size_t)t * rsk + c0) = oq;
+      *reinterpret_cast<bf16x8*>(kg_out + kofs + (size_t)t * rsk + c0) = ok;
+    }
+  }
+  __syncthreads();
+
+  // ---- w^T = E^T A^T, u^T = Z^T A^T: B operand = A rows (t), contiguous s, straight from HBM ----
+  // wave wv: output rows (k or v) [32 wv, 32 wv + 32), all 64 token columns
+  {
+    bf16x8 ah[4][2], al[4][2];   // A rows t = 16 tt + lc, s = 32 ks + 8 lg .. +7
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const float* src = akk + ((tok0 + 16 * tt + lc) * H + h) * C + 32 * ks + 8 * lg;
+        const float4 x0 = *reinterpret_cast<const float4*>(src);
+        const float4 x1 = *reinterpret_cast<const float4*>(src + 4);
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          bf16 hh, ll;
+          split_bf16(xs[j], hh, ll);
+          ah[tt][ks][j] = hh;
+          al[tt][ks][j] = ll;
+        }
+      }
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+      const bf16(*srcH)[LDT] = which == 0 ? eTh : zTh;
+      const bf16(*srcL)[LDT] = which == 0 ? eTl : zTl;
+      bf16* dst = which == 0 ? w_out + kofs : u_out + vofs;
+      const size_t rs = which == 0 ? rsk : rsv;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int row0 = 32 * wv + 16 * rt;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 xh = frag(&srcH[row0][32 * ks], LDT);
+            const bf16x8 xl = frag(&srcL[row0][32 * ks], LDT);
+            acc = mfma(xh, ah[tt][ks], acc);
+            acc = mfma(xh, al[tt][ks], acc);
+            acc = mfma(xl, ah[tt][ks], acc);
+          }
+          // lane: token t = 16 tt + lc, columns row0 + 4 lg .. +3
+          bf16x4 o;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = to_bf16(acc[r]);
+          *reinterpret_cast<bf16x4*>(dst + (size_t)(16 * tt + lc) * rs + row0 + 4 * lg) = o;
+        }
+      }
+    }
+  }
+
+  // ---- Aqk = scale tril(q k^T 2^(g_i - g_s)) for the scalar / no-gate families ----
+  if constexpr (WANT_AQK) {
+    // wave wv: row tile I = wv, all four column tiles; operands straight from HBM
+    const int I = wv;
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      f32x4 acc = zero4();
+      if (J <= I) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(q + kofs + (size_t)(16 * I + lc) * rsk + 32 * ks + 8 * lg);
+          const bf16x8 bq = *reinterpret_cast<const bf16x8*>(k + kofs + (size_t)(16 * J + lc) * rsk + 32 * ks + 8 * lg);
+          acc = mfma(a, bq, acc);
+        }
+      }
+      const int s = 16 * J + lc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * I + 4 * lg + r;
+        float f = (i >= s) ? scale : 0.f;
+        if constexpr (GATE == RG_SCALAR) f = (i >= s) ? scale * fast_exp2(sG[i] - sG[s]) : 0.f;
+        aqk_out[((tok0 + i) * H + h) * C + s] = acc[r] * f;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// fdr_fwd_h
+// ------------------------------------------------------------------------------------------
+template <int BV, int GATE>
+struct FwdSmem {
+  static constexpr int LDK = KD + 8;
+  static constexpr int LDT = C + 8;
+  bf16 w[C][LDK];          // w rows: A operand of w h           (contraction over K)
+  bf16 kT[KD][LDT];        // kg^T:   A operand of kg^T v_new      (contraction over T)
+  bf16 hT[BV][LDK];        // h^T:    B operand of w h
+  bf16 vT[BV][LDT];        // v_new^T: B operand of kg^T v_new
+  float lam[KD];
+  float gam[C];
+  float gkf[C];
+};
+
+template <int BV, int GATE>
+__global__ __launch_bounds__(512) void fwd_h_kernel(
+    const bf16* __restrict__ k, const bf16* __restrict__ w, const bf16* __restrict__ u,
+    const float* __restrict__ g, const float* __restrict__ h0, bf16* __restrict__ h_out,
+    bf16* __restrict__ vnew_out, float* __restrict__ ht_out, int T, int H) {
+  using S = FwdSmem<BV, GATE>;
+  __shared__ S sm;
+  constexpr int NVT = VD / BV;
+  constexpr int NCT = BV / 16;
+  constexpr int NTH = 512;
+  const int logical = xcd_logical_block();
+  const int vt = logical % NVT;
+  const int bh = logical / NVT;
+  const int b = bh / H, h = bh % H;
+  const int NT = T / C;
+  const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
+  const int v_base = vt * BV;
+  const size_t rsk = (size_t)H * KD, rsv = (size_t)H * VD;
+
+  // state rows [16 wv, 16 wv + 16)
+  f32x4 st[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    f32x4 a = zero4();
+    if (h0) {
+      const float* src = h0 + (size_t)bh * KD * VD;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        a[r] = src[(16 * wv + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)];
+    }
+    st[ct] = a;
+  }
+  constexpr int DCT = NCT >= 2 ? NCT / 2 : 1;
+  const int drow = wv & 3;
+  const int dct0 = DCT * (wv >> 2);
+  const bool has_dr = dct0 < NCT;
+
+  uint4 rw[2];
+  PairPiece rk;
+  float rg_last = 0.f, rg_tok = 0.f;
+  auto load_chunk = [&](int c) {
+    const size_t tok0 = (size_t)b * T + (size_t)c * C;
+    const bf16* wb = w + tok0 * rsk + (size_t)h * KD;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + NTH * i;
+      rw[i] = *reinterpret_cast<const uint4*>(wb + (size_t)(p >> 4) * rsk + (p & 15) * 8);
+    }
+    rk = load_pair_piece(k + tok0 * rsk + (size_t)h * KD, rsk, tid & 31, (tid >> 5) * 8);
+    if constexpr (GATE == RG_VECTOR) {
+      if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
+    } else if constexpr (GATE == RG_SCALAR) {
+      if (tid < C) rg_tok = g[(tok0 + tid) * H + h];
+      rg_last = g[(tok0 + C - 1) * H + h];
+    }
+  };
+  auto stage_chunk = [&]() {
+    if constexpr (GATE == RG_VECTOR) {
+      if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
+    } else if constexpr (GATE == RG_SCALAR) {
+      if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
+      if (tid < C) sm.gkf[tid] = fast_exp2(rg_last - rg_tok);
+    } else {
+      if (tid < KD) sm.lam[tid] = 1.f;
+    }
+    if constexpr (GATE == RG_SCALAR) __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + NTH * i;
+      *reinterpret_cast<uint4*>(&sm.w[p >> 4][(p & 15) * 8]) = rw[i];
+    }
+    const int tp = tid & 31;
+    if constexpr (GATE == RG_SCALAR)
+      store_pair_piece_scaled(reinterpret_cast<uint32_t*>(&sm.kT[0][0]), S::LDT / 2, tp, (tid >> 5) * 8, rk,
+                              sm.gkf[2 * tp], sm.gkf[2 * tp + 1]);
+    else
+      store_pair_piece(reinterpret_cast<uint32_t*>(&sm.kT[0][0]), S::LDT / 2, tp, (tid >> 5) * 8, rk);
+  };
+
+  load_chunk(0);
+  for (int c = 0; c < NT; ++c) {
+    __syncthreads();
+    stage_chunk();
+    if (c + 1 < NT) load_chunk(c + 1);
+    const size_t tok0 = (size_t)b * T + (size_t)c * C;
+    // h_c -> LDS (transposed, bf16); the same rounded values feed w h, as stored
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      bf16x4 v4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[ct][r]);
+      *reinterpret_cast<bf16x4*>(&sm.hT[16 * ct + (l & 15)][16 * wv + 4 * (l >> 4)]) = v4;
+    }
+    __syncthreads();
+    // v_new tiles = u - w h
+    if (has_dr) {
+#pragma unroll
+      for (int cc = 0; cc < DCT; ++cc) {
+        const int ct = dct0 + cc;
+        f32x4 a;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * drow + 4 * (l >> 4) + r;
+          a[r] = -to_f32(u[(tok0 + t) * rsv + (size_t)h * VD + v_base + 16 * ct + (l & 15)]);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          a = mfma(frag(&sm.w[16 * drow][32 * ks], S::LDK), frag(&sm.hT[16 * ct][32 * ks], S::LDK), a);
+        bf16x4 v4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v4[r] = to_bf16(-a[r]);
+        *reinterpret_cast<bf16x4*>(&sm.vT[16 * ct + (l & 15)][16 * drow + 4 * (l >> 4)]) = v4;
+      }
+    }
+    __syncthreads();
+    // h <- lambda h + kg^T v_new
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      f32x4 a;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) a[r] = st[ct][r] * sm.lam[16 * wv + 4 * (l >> 4) + r];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        a = mfma(frag(&sm.kT[16 * wv][32 * ks], S::LDT), frag(&sm.vT[16 * ct][32 * ks], S::LDT), a);
+      st[ct] = a;
+    }
+    // stores of h_c and v_new_c from the transposed LDS copies (lanes run over rows)
+    {
+      const size_t hb = (((size_t)b * NT + c) * H + h) * KD * VD;
+      for (int p = tid; p < KD * BV / 8; p += NTH) {
+        const int kr = p % KD, v0 = (p / KD) * 8;
+        bf16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = sm.hT[v0 + j][kr];
+        *reinterpret_cast<bf16x8*>(h_out + hb + (size_t)kr * VD + v_base + v0) = o;
+      }
+      for (int p = tid; p < C * BV / 8; p += NTH) {
+        const int t = p % C, v0 = (p / C) * 8;
+        bf16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = sm.vT[v0 + j][t];
+        *reinterpret_cast<bf16x8*>(vnew_out + (tok0 + t) * rsv + (size_t)h * VD + v_base + v0) = o;
+      }
+    }
+  }
+  if (ht_out) {
+    float* dst = ht_out + (size_t)bh * KD * VD;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        dst[(16 * wv + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)] = st[ct][r];
+  }
+}
+
+template <int GATE, bool VEC_B, bool QKG, bool AQK>
+static hipError_t launch_prepare(const void* q, const void* k, const void* v, const float* g,
+                                 const float* beta, const void* bg, const void* wg, const float* akk,
+                                 void* w, void* u, void* qg, void* kg, float* aqk, int B, int T, int H,
+                                 float scale, hipStream_t s) {
+  hipLaunchKernelGGL((prepare_wu_kernel<GATE, VEC_B, QKG, AQK>), dim3(B * H * (T / C)), dim3(256), 0, s,
+                     (const bf16*)q, (const bf16*)k, (const bf16*)v, g, beta, (const bf16*)bg,
+                     (const bf16*)wg, akk, (bf16*)w, (bf16*)u, (bf16*)qg, (bf16*)kg, aqk, T, H, scale);
+  return hipGetLastError();
+}
+
+template <int BV, int GATE>
+static hipError_t launch_fwd_h(const void* k, const void* w, const void* u, const float* g, const float* h0,
+                               void* h, void* vnew, float* ht, int B, int T, int H, hipStream_t s) {
+  hipLaunchKernelGGL((fwd_h_kernel<BV, GATE>), dim3(B * H * (VD / BV)), dim3(512), 0, s, (const bf16*)k,
+                     (const bf16*)w, (const bf16*)u, g, h0, (bf16*)h, (bf16*)vnew, ht, T, H);
+  return hipGetLastError();
+}
+
+}  // namespace rewy
+
+using namespace rewy;
+
+extern "C" hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const float* g,
+                                     int gate_mode, const float* beta, const void* b_gate,
+                                     const void* w_gate, const float* Akk, void* w, void* u, void* qg,
+                                     void* kg, float* Aqk, int B, int T, int H, int K, int V, int chunk,
+                                     float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  if (!k || !v || !Akk || !w || !u) return hipErrorInvalidValue;
+  const bool vec_b = b_gate != nullptr;
+  if (vec_b && (!w_gate || gate_mode != RG_VECTOR)) return hipErrorInvalidValue;
+  if (!vec_b && !beta) return hipErrorInvalidValue;
+  if (gate_mode != RG_NONE && !g) return hipErrorInvalidValue;
+  const bool want_qkg = qg != nullptr || kg != nullptr;
+  if (want_qkg && (!qg || !kg || !q || gate_mode != RG_VECTOR)) return hipErrorInvalidValue;
+  const bool want_aqk = Aqk != nullptr;
+  if (want_aqk && (!q || gate_mode == RG_VECTOR)) return hipErrorInvalidValue;
+#define P_ARGS q, k, v, g, beta, b_gate, w_gate, Akk, w, u, qg, kg, Aqk, B, T, H, scale, stream
+  switch (gate_mode) {
+    case RG_NONE:
+      return want_aqk ? launch_prepare<RG_NONE, false, false, true>(P_ARGS)
+                      : launch_prepare<RG_NONE, false, false, false>(P_ARGS);
+    case RG_SCALAR:
+      return want_aqk ? launch_prepare<RG_SCALAR, false, false, true>(P_ARGS)
+                      : launch_prepare<RG_SCALAR, false, false, false>(P_ARGS);
+    case RG_VECTOR:
+      if (vec_b)
+        return want_qkg ? launch_prepare<RG_VECTOR, true, true, false>(P_ARGS)
+                        : launch_prepare<RG_VECTOR, true, false, false>(P_ARGS);
+      return want_qkg ? launch_prepare<RG_VECTOR, false, true, false>(P_ARGS)
+                      : launch_prepare<RG_VECTOR, false, false, false>(P_ARGS);
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef P_ARGS
+}
+
+static int fwd_default_bv(int B, int H) {
+  const int bh = B * H;
+  if (bh * 2 >= 256) return 64;
+  if (bh * 4 >= 256) return 32;
+  return 16;
+}
+
+extern "C" hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g, int gate_mode,
+                                const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int K,
+                                int V, int chunk, int value_block, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  if (!k || !w || !u || !h || !v_new) return hipErrorInvalidValue;
+  if (gate_mode != RG_NONE && !g) return hipErrorInvalidValue;
+  const int bv = value_block > 0 ? value_block : fwd_default_bv(B, H);
+#define F_ARGS k, w, u, g, h0, h, v_new, ht, B, T, H, stream
+#define F_BV(G)                                                     \
+  switch (bv) {                                                     \
+    case 16: return launch_fwd_h<16, G>(F_ARGS);                    \
+    case 32: return launch_fwd_h<32, G>(F_ARGS);                    \
+    case 64: return launch_fwd_h<64, G>(F_ARGS);                    \
+    default: return hipErrorInvalidValue;                           \
+  }
+  switch (gate_mode) {
+    case RG_NONE: F_BV(RG_NONE)
+    case RG_SCALAR: F_BV(RG_SCALAR)
+    case RG_VECTOR: F_BV(RG_VECTOR)
+    default: return hipErrorInvalidValue;
+  }
+#undef F_BV
+#undef F_ARGS
+}

@@ -127,3 +127,73 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
                                    _lib.stream_handle(dev))
     _lib.check(st, "fdr_chunk_bwd")
     return out
+
+
+def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, want_qkg=False,
+               want_aqk=False, scale=1.0):
+    """WY factors (and qg/kg or Aqk) of every chunk.  Returns dict(w, u, qg, kg, Aqk)."""
+    B, T, H, K = _dims(k)
+    V = V_SUPPORTED
+    dev = k.device
+    bf, f32 = torch.bfloat16, torch.float32
+    _need(k, "k", bf, (B, T, H, K), dev)
+    _need(v, "v", bf, (B, T, H, V), dev)
+    _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
+    if q is not None:
+        _need(q, "q", bf, (B, T, H, K), dev)
+    vec_b = b is not None
+    if vec_b:
+        _need(b, "b", bf, (B, T, H, K), dev)
+        _need(w, "w", bf, (B, T, H, V), dev)
+    else:
+        _need(beta, "beta", f32, (B, T, H), dev)
+    if gate_mode == GATE_VECTOR:
+        _need(g, "g", f32, (B, T, H, K), dev)
+    elif gate_mode == GATE_SCALAR:
+        _need(g, "g", f32, (B, T, H), dev)
+    elif gate_mode != GATE_NONE:
+        raise ValueError("gate_mode must be 0, 1 or 2")
+    if want_qkg and (q is None or gate_mode != GATE_VECTOR):
+        raise ValueError("qg/kg need q and a vector gate")
+    if want_aqk and (q is None or gate_mode == GATE_VECTOR):
+        raise ValueError("Aqk is produced here for scalar / no-gate families only")
+    out = dict(w=torch.empty(B, T, H, K, device=dev, dtype=bf), u=torch.empty(B, T, H, V, device=dev, dtype=bf),
+               qg=torch.empty(B, T, H, K, device=dev, dtype=bf) if want_qkg else None,
+               kg=torch.empty(B, T, H, K, device=dev, dtype=bf) if want_qkg else None,
+               Aqk=torch.empty(B, T, H, CHUNK, device=dev, dtype=f32) if want_aqk else None)
+    P = _lib.ptr
+    st = _lib.load().fdr_prepare_wu(P(q), P(k), P(v), P(g), int(gate_mode), P(beta), P(b), P(w), P(Akk),
+                                    P(out["w"]), P(out["u"]), P(out["qg"]), P(out["kg"]), P(out["Aqk"]),
+                                    B, T, H, K, V, CHUNK, float(scale), _lib.stream_handle(dev))
+    _lib.check(st, "fdr_prepare_wu")
+    return out
+
+
+def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0):
+    """Forward state scan.  Returns (h [B,NT,H,K,V] bf16, v_new [B,T,H,V] bf16, final fp32|None)."""
+    B, T, H, K = _dims(k)
+    V = V_SUPPORTED
+    dev = k.device
+    bf, f32 = torch.bfloat16, torch.float32
+    _need(k, "k", bf, (B, T, H, K), dev)
+    _need(w, "w", bf, (B, T, H, K), dev)
+    _need(u, "u", bf, (B, T, H, V), dev)
+    if gate_mode == GATE_VECTOR:
+        _need(g, "g", f32, (B, T, H, K), dev)
+    elif gate_mode == GATE_SCALAR:
+        _need(g, "g", f32, (B, T, H), dev)
+    elif gate_mode != GATE_NONE:
+        raise ValueError("gate_mode must be 0, 1 or 2")
+    if h0 is not None:
+        _need(h0, "h0", f32, (B, H, K, V), dev)
+    if value_block not in (0, 16, 32, 64):
+        raise ValueError("value_block must be 0, 16, 32 or 64")
+    NT = T // CHUNK
+    h = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
+    vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
+    ht = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_final else None
+    P = _lib.ptr
+    st = _lib.load().fdr_fwd_h(P(k), P(w), P(u), P(g), int(gate_mode), P(h0), P(h), P(vnew), P(ht), B, T, H,
+                               K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
+    _lib.check(st, "fdr_fwd_h")
+    return h, vnew, ht
