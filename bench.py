@@ -3,15 +3,18 @@
 Default workload: KDA (per-channel gate) chunk backward with full saving at
 B=8, T=4096, H=16, K=V=128, chunk 64 -- BASELINE.json configs[2], the
 configuration the headline metric names.  One "step" is one complete backward
-(state recurrence kernel + fused chunk kernel) over synthetic inputs already
-resident in HBM; the forward that produces the saved tensors runs once,
-outside the timed region.
+(every kernel of the path) over synthetic inputs already resident in HBM; the
+forward that produces the saved tensors runs once, outside the timed region.
+The default run also times the GDN backward (always recompute) at the same
+B=8, T=4096, H=16 (the metric's "KDA/GDN") and reports it under "secondary".
 
 Printed (one JSON line): backward ms per step, algorithmic TFLOP/s and its
-fraction of the bf16 MFMA peak, a roofline record for the dominant kernel
-(per-launch algorithmic bytes / HIP-event launch time), the same-GPU time of
-the original 7-product formulation (PyTorch ops) and a CPU baseline (the fp64
-oracle on a bounded sample, one thread).
+fraction of the bf16 MFMA peak, per-kernel HIP-event launch times, a roofline
+record for the dominant kernel (per-launch algorithmic bytes / launch time),
+the same-GPU time of the original 7-product formulation (PyTorch ops) and a
+CPU baseline (the fp64 oracle on a bounded sample, one thread).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config kda|gdn|gdn_cfg|gdn2|kda_long|delta]
 """
 from __future__ import annotations
 
@@ -28,15 +31,46 @@ METRIC = "delta-rule bwd ms + TFLOP/s (frac of MFMA peak), KDA/GDN B=8 T=4096 H=
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
-# per chunk-head (64 tokens x one head), K = V = 128 -- see DESIGN.md
 CONFIGS = {
+    # the headline
     "kda": dict(op="kda", B=8, T=4096, H=16, seed=2, gate="kda", h0=False, full_saving=True),
+    # GDN at the metric's shape, and BASELINE.json configs[1]
+    "gdn": dict(op="gdn", B=8, T=4096, H=16, seed=1, gate="gdn", h0=True, full_saving=False),
+    "gdn_cfg": dict(op="gdn", B=4, T=2048, H=16, seed=1, gate="gdn", h0=True, full_saving=False),
+    # native recomputation inside the backward
+    "gdn2": dict(op="gdn2", B=2, T=8192, H=32, seed=3, gate="gdn2", h0=True, full_saving=False),
+    # long context, 1024 sequential chunks
     "kda_long": dict(op="kda", B=1, T=65536, H=16, seed=4, gate="kda_long", h0=True, full_saving=True),
+    # BASELINE.json configs[0] shape (its CPU reference path is the oracle test suite)
+    "delta": dict(op="delta", B=1, T=256, H=2, seed=0, gate=None, h0=False, full_saving=False),
 }
-FLOP_STATE = 2 * (64 * 128 * 128 + 64 * 64 * 128 + 2 * 128 * 64 * 128)          # 7.34 MFLOP
-FLOP_CHUNK = 2 * (3 * 64 * 64 * 128 + 3 * 64 * 128 * 128 + 4 * 64 * 64 * 128)   # 13.63 MFLOP
-BYTES_STATE = 3 * 16384 + 16384 + 16384 + 512 + 32768 + 16384                   # qg,kg,w,dO,Aqk,g_last | dh,dR
-BYTES_CHUNK = (5 * 16384 + 32768 + 256 + 16384 + 2 * 32768) + (3 * 16384 + 32768 + 256)
+
+TILE = 64 * 128 * 2          # one [64][128] bf16 tile
+HS = 128 * 128 * 2           # one [128][128] bf16 state
+AT = 64 * 64 * 4             # one [64][64] fp32 matrix (Akk, Aqk)
+
+
+def kernel_costs(op, full_saving):
+    """Algorithmic (bytes, FLOPs) per chunk-head of every kernel the backward launches:
+    every operand read once, every result written once; dense GEMM flops."""
+    vec, vb = op in ("kda", "gdn2"), op == "gdn2"
+    g_b = 64 * 128 * 4 if vec else (64 * 4 if op == "gdn" else 0)
+    gl_b = 128 * 4 if vec else (4 if op == "gdn" else 0)
+    beta_b = 0 if vb else 64 * 4
+    gates_b = 2 * TILE if vb else beta_b
+    mm = lambda m, n, k: 2 * m * n * k
+    costs = {}
+    if not full_saving:
+        rd = 3 * TILE + g_b + gates_b + AT                      # q, k, v, g, beta|b,w, Akk
+        wr = 2 * TILE + (2 * TILE if vec else AT)               # w, u, (qg, kg | Aqk)
+        costs["fdr_prepare_wu"] = (rd + wr, 2 * mm(64, 128, 64) + (0 if vec else mm(64, 64, 128)))
+        costs["fdr_fwd_h"] = (3 * TILE + gl_b + (0 if vec else g_b) + HS + TILE, 2 * mm(64, 128, 128))
+    costs["fdr_state_bwd"] = (4 * TILE + AT + gl_b + (0 if vec else g_b) + HS + TILE,
+                              mm(64, 128, 128) + mm(64, 128, 64) + 2 * mm(128, 128, 64))
+    rd = 5 * TILE + g_b + gates_b + AT + 2 * HS + (TILE if vb else 0)
+    wr = 3 * TILE + g_b + (2 * TILE if vb else beta_b)
+    costs["fdr_chunk_bwd"] = (rd + wr, 3 * mm(64, 64, 128) + 3 * mm(64, 128, 128) + 4 * mm(64, 64, 128))
+    return costs
 
 
 def make_inputs(cfg, device):
@@ -48,15 +82,185 @@ def make_inputs(cfg, device):
     q = F.normalize(torch.randn(shape, generator=gen), dim=-1).bfloat16()
     k = F.normalize(torch.randn(shape, generator=gen), dim=-1).bfloat16()
     v = torch.randn(shape, generator=gen).bfloat16()
-    beta = torch.sigmoid(torch.randn(shape[:-1], generator=gen))
-    if cfg["gate"] == "kda_long":
-        g = F.logsigmoid(0.3 * torch.randn(shape, generator=gen) + 3)
+    xs = dict(q=q, k=k, v=v)
+    if cfg["op"] == "gdn2":
+        # BASELINE.json leaves GDN2's erase / write gates open: the reference's
+        # U(0.1, 0.9) bf16 (validation.py:17-18)
+        xs["b"] = (torch.rand(shape, generator=gen) * 0.8 + 0.1).bfloat16()
+        xs["w"] = (torch.rand(shape, generator=gen) * 0.8 + 0.1).bfloat16()
     else:
-        g = F.logsigmoid(torch.randn(shape, generator=gen)).clamp_min(-5)
-    h0 = torch.randn(B, H, K, K, generator=gen) * 0.02 if cfg["h0"] else None
+        xs["beta"] = torch.sigmoid(torch.randn(shape[:-1], generator=gen))
+    gate = cfg["gate"]
+    if gate == "kda":
+        xs["g"] = F.logsigmoid(torch.randn(shape, generator=gen)).clamp_min(-5)
+    elif gate == "kda_long":
+        xs["g"] = F.logsigmoid(0.3 * torch.randn(shape, generator=gen) + 3)
+    elif gate == "gdn2":
+        xs["g"] = F.logsigmoid(torch.randn(shape, generator=gen))
+    elif gate == "gdn":
+        xs["g"] = F.logsigmoid(torch.randn(shape[:-1], generator=gen) * 0.5 + 4)
+    xs["h0"] = torch.randn(B, H, K, K, generator=gen) * 0.02 if cfg["h0"] else None
     dO = torch.randn(shape, generator=gen).bfloat16()
-    dev = lambda x: None if x is None else x.to(device)
-    return dict(q=dev(q), k=dev(k), v=dev(v), beta=dev(beta), g=dev(g), h0=dev(h0)), dev(dO)
+    return {n: (None if x is None else x.to(device)) for n, x in xs.items()}, dO.to(device)
+
+
+def setup(cfg, device):
+    """Forward once (untimed).  Returns (xs, dO, saved, step, per-kernel launchers)."""
+    import torch
+    from rewy_amd import ops
+    from rewy_amd.backends import backward as bw
+    from rewy_amd.forward import chunk_forward
+    xs, dO = make_inputs(cfg, device)
+    op = cfg["op"]
+    with torch.no_grad():
+        _, _, sv = chunk_forward(op, xs["q"], xs["k"], xs["v"], g=xs.get("g"), beta=xs.get("beta"),
+                                 b=xs.get("b"), w=xs.get("w"), initial_state=xs["h0"])
+    torch.cuda.synchronize()
+    scale = sv["scale"]
+    keep = cfg["full_saving"]
+    saved = {n: (sv[n] if keep else None) for n in ("w", "u", "qg", "kg", "v_new", "h")}
+
+    if op == "kda":
+        def step():
+            return bw.kda_backward(q=xs["q"], k=xs["k"], v=xs["v"], beta=xs["beta"], Aqk=sv["Aqk"], Akk=sv["Akk"],
+                                   scale=scale, initial_state=xs["h0"], do=dO, dht=None, g=sv["gc"],
+                                   disable_recompute=keep, **saved)
+    elif op == "gdn2":
+        def step():
+            return bw.gdn2_backward(q=xs["q"], k=xs["k"], v=xs["v"], b=xs["b"], w_gate=xs["w"], Aqk=sv["Aqk"],
+                                    Akk=sv["Akk"], scale=scale, initial_state=xs["h0"], do=dO, dht=None,
+                                    g=sv["gc"], w_wy=saved["w"], u_wy=saved["u"], qg=saved["qg"],
+                                    kg=saved["kg"], v_new=saved["v_new"], h=saved["h"])
+    elif op == "gdn":
+        def step():
+            return bw.gdn_backward(q=xs["q"], k=xs["k"], v=xs["v"], g=sv["gc"], beta=xs["beta"], A=sv["Akk"],
+                                   scale=scale, initial_state=xs["h0"], do=dO, dht=None)
+    else:
+        def step():
+            return bw.delta_backward(q=xs["q"], k=xs["k"], v=xs["v"], beta=xs["beta"], A=sv["Akk"],
+                                     scale=scale, initial_state=xs["h0"], do=dO, dht=None)
+
+    gate = {"kda": ops.GATE_VECTOR, "gdn2": ops.GATE_VECTOR, "gdn": ops.GATE_SCALAR, "delta": ops.GATE_NONE}[op]
+    vec = gate == ops.GATE_VECTOR
+    g = sv["gc"]
+    kern = {}
+    if keep:
+        qs, ks, ws, aqk, h, v_new = sv["qg"], sv["kg"], sv["w"], sv["Aqk"], sv["h"], sv["v_new"]
+    else:
+        kern["fdr_prepare_wu"] = lambda: ops.prepare_wu(
+            xs["k"], xs["v"], sv["Akk"], gate, g=g, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"), q=xs["q"],
+            want_qkg=vec, want_aqk=not vec, scale=scale)
+        pre = kern["fdr_prepare_wu"]()
+        ks, qs, ws = (pre["kg"], pre["qg"], pre["w"]) if vec else (xs["k"], xs["q"], pre["w"])
+        aqk = sv["Aqk"] if vec else pre["Aqk"]
+        kern["fdr_fwd_h"] = lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"])
+        h, v_new, _ = kern["fdr_fwd_h"]()
+    kern["fdr_state_bwd"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
+                                                  want_dh0=xs["h0"] is not None)
+    dh, dR, _ = kern["fdr_state_bwd"]()
+    kern["fdr_chunk_bwd"] = lambda: ops.chunk_bwd(xs["q"], xs["k"], xs["v"], v_new, dO, dR, g, gate, sv["Akk"], h,
+                                                  dh, scale, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"))
+    return xs, dO, sv, step, kern, (dh, dR)
+
+
+def time_steps(step, steps, warmup):
+    """Synchronized wall clock around `steps` back-to-back steps (after `warmup`)."""
+    import torch
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
+def time_kernels(kern, reps):
+    """Average launch time of each kernel: HIP events recorded on the stream the
+    kernel is launched on (the current torch stream)."""
+    import torch
+    stream = torch.cuda.current_stream()
+    out = {}
+    for name, fn in kern.items():
+        fn()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in evs:
+            a.record(stream)
+            fn()
+            b.record(stream)
+        torch.cuda.synchronize()
+        out[name] = sum(a.elapsed_time(b) for a, b in evs) / reps
+    return out
+
+
+def measure(cfg, steps, warmup):
+    xs, dO, sv, step, kern, inter = setup(cfg, "cuda")
+    NTt = cfg["B"] * cfg["H"] * (cfg["T"] // 64)
+    ms = time_steps(step, steps, warmup)
+    kt = time_kernels(kern, max(5, steps))
+    costs = kernel_costs(cfg["op"], cfg["full_saving"])
+    kernels = {}
+    for n, t in kt.items():
+        by, fl = costs[n]
+        kernels[n] = dict(ms=round(t, 4), gbs=round(by * NTt / (t * 1e-3) / 1e9, 1),
+                          tflops=round(fl * NTt / (t * 1e-3) / 1e12, 2), bytes_per_launch=by * NTt)
+    flops = sum(c[1] for c in costs.values()) * NTt
+    return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9, kernels=kernels, NTt=NTt,
+                xs=xs, dO=dO, sv=sv, step=step, inter=inter)
+
+
+def measured_traffic(kernel, config):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (profiles/hbm_traffic.json, calibrated against a plain
+    copy of known size), or None when that workload was not profiled."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data[config][kernel]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(xs, sv, dO, scale, NTt, nb_max=3):
+    """fp64 oracle (numpy, one thread) of the two KDA stages -- state recurrence and
+    chunk stage -- on a bounded sample (batches 0..nb-1, all heads, one head at a
+    time so the oracle's pairwise tensors stay small), scaled linearly to the full
+    workload's chunk-head count."""
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    from oracle import delta_oracle as O
+    B, T, H = xs["q"].shape[:3]
+    nb = min(B, nb_max)
+    sample_heads = nb * H * (T // 64)
+    ctx = threadpool_limits(limits=1) if threadpool_limits else None
+    if ctx:
+        ctx.__enter__()
+    el = 0.0
+    try:
+        for bb in range(nb):
+            for hh in range(H):
+                n = lambda x: x[bb:bb + 1, :, hh:hh + 1].double().cpu().numpy()
+                inp = dict(qg=n(sv["qg"]), kg=n(sv["kg"]), w=n(sv["w"]), gc=n(sv["gc"]), dO=n(dO),
+                           Aqk=n(sv["Aqk"]), q=n(xs["q"]), k=n(xs["k"]), v=n(xs["v"]), beta=n(xs["beta"]),
+                           Akk=n(sv["Akk"]), h=n(sv["h"]), v_new=n(sv["v_new"]))
+                t0 = time.perf_counter()
+                dvl = O.dv_local(inp["Aqk"], inp["dO"])
+                d_h, d_R, _ = O.stage_state_bwd(inp["qg"], inp["kg"], inp["w"], inp["gc"], inp["dO"], dvl,
+                                                scale=scale)
+                O.stage_post("kda", inp["q"], inp["k"], inp["v"], inp["gc"], beta=inp["beta"], Akk=inp["Akk"],
+                             h=inp["h"], dh=d_h, v_new=inp["v_new"], dO=inp["dO"], dR=d_R, scale=scale)
+                el += time.perf_counter() - t0
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    return {"value": round(el * 1e3 * NTt / sample_heads, 1), "unit": "ms (full workload, extrapolated)",
+            "cores": 1, "kind": "port",
+            "sample": f"fp64 numpy oracle (state recurrence + chunk stage), batches 0-{nb - 1}, T={T}, all {H} "
+                      f"heads ({sample_heads} of {NTt} chunk-heads), measured {el:.2f} s, scaled linearly"}
 
 
 def main():
@@ -67,6 +271,7 @@ def main():
     ap.add_argument("--config", default="kda", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-original", action="store_true", help="skip the torch original comparator")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the GDN companion measurement")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (reference kernel for the HBM byte counters)")
     args = ap.parse_args()
@@ -85,104 +290,55 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes_read": 4 * n, "calibrate_copy_bytes_written": 4 * n}))
         return
-    from rewy_amd import ops
-    from rewy_amd.backends.backward import kda_backward
-    from rewy_amd.forward import chunk_forward
     from rewy_amd.runtime import check_baseline
-
     check_baseline()
+    torch.cuda.set_device(0)
     cfg = CONFIGS[args.config]
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    xs, dO = make_inputs(cfg, dev)
     B, T, H = cfg["B"], cfg["T"], cfg["H"]
-    NTt = B * H * (T // 64)
-    print(f"[bench] config={args.config} B={B} T={T} H={H} chunk-heads={NTt}", file=sys.stderr, flush=True)
-    with torch.no_grad():
-        _, _, sv = chunk_forward("kda", xs["q"], xs["k"], xs["v"], g=xs["g"], beta=xs["beta"],
-                                 initial_state=xs["h0"])
-    torch.cuda.synchronize()
-    scale = sv["scale"]
-    dht = None
-
-    def step():
-        return kda_backward(q=xs["q"], k=xs["k"], v=xs["v"], beta=xs["beta"], Aqk=sv["Aqk"],
-                            Akk=sv["Akk"], scale=scale, initial_state=xs["h0"], do=dO, dht=dht,
-                            g=sv["gc"], w=sv["w"], u=sv["u"], qg=sv["qg"], kg=sv["kg"],
-                            v_new=sv["v_new"], h=sv["h"], disable_recompute=True)
+    print(f"[bench] config={args.config} op={cfg['op']} B={B} T={T} H={H}", file=sys.stderr, flush=True)
+    res = measure(cfg, args.steps, args.warmup)
+    xs, dO, sv, NTt = res["xs"], res["dO"], res["sv"], res["NTt"]
 
     # ---- gradient check against the original formulation (same GPU, same inputs) ----
-    from rewy_amd.original import original_backward
-    got = step()
-    torch.cuda.synchronize()
-    parity = None
-    t_orig = None
-    if not args.no_original:
+    parity, t_orig = None, None
+    if not args.no_original and cfg["op"] == "kda":
+        from rewy_amd.original import original_backward
+        got = res["step"]()
+        saved = sv if cfg["full_saving"] else None
+
         def orig():
-            return original_backward("kda", xs["q"], xs["k"], xs["v"], sv["gc"], sv["Akk"], scale,
-                                     xs["h0"], dO, dht, beta=xs["beta"], Aqk=sv["Aqk"], saved=sv)
+            return original_backward("kda", xs["q"], xs["k"], xs["v"], sv["gc"], sv["Akk"], sv["scale"], xs["h0"],
+                                     dO, None, beta=xs["beta"], Aqk=sv["Aqk"], saved=saved)
         ref = orig()
         torch.cuda.synchronize()
         parity = {}
         for name, a, r in (("dq", got[0], ref["dq"]), ("dk", got[1], ref["dk"]), ("dv", got[2], ref["dv"]),
                            ("dbeta", got[3], ref["dbeta"]), ("dg", got[4], ref["dg"])):
             a, r = a.double(), r.double()
-            parity[name] = dict(rel_l2=float((a - r).norm() / r.norm().clamp_min(1e-30)),
+            parity[name] = dict(rel_l2=round(float((a - r).norm() / r.norm().clamp_min(1e-30)), 6),
                                 max_abs=float((a - r).abs().max()))
-        del ref
-        torch.cuda.synchronize()
-        n_orig = 3
-        t0 = time.perf_counter()
-        for _ in range(n_orig):
-            orig()
-        torch.cuda.synchronize()
-        t_orig = (time.perf_counter() - t0) / n_orig * 1e3
+        del ref, got
+        t_orig = time_steps(orig, 2, 1)
 
-    # ---- timed region: complete backward, W warmup + K steps ----
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) / args.steps * 1e3
-
-    # ---- per-kernel launch times with HIP events on the launch stream ----
-    stream = torch.cuda.current_stream(dev)
-    reps = max(5, args.steps)
-
-    def time_kernel(fn):
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for a, b in evs:
-            a.record(stream)
-            fn()
-            b.record(stream)
-        torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in evs) / reps
-
-    t_state = time_kernel(lambda: ops.state_bwd(sv["qg"], sv["kg"], sv["w"], sv["gc"], ops.GATE_VECTOR, dO,
-                                                scale, aqk=sv["Aqk"], dht=dht, want_dh0=xs["h0"] is not None))
-    dh, dR, _ = ops.state_bwd(sv["qg"], sv["kg"], sv["w"], sv["gc"], ops.GATE_VECTOR, dO, scale,
-                              aqk=sv["Aqk"], dht=dht, want_dh0=False)
-    t_chunk = time_kernel(lambda: ops.chunk_bwd(xs["q"], xs["k"], xs["v"], sv["v_new"], dO, dR, sv["gc"],
-                                                ops.GATE_VECTOR, sv["Akk"], sv["h"], dh, scale, beta=xs["beta"]))
-    kernels = {
-        "fdr_state_bwd": dict(ms=t_state, gbs=BYTES_STATE * NTt / (t_state * 1e-3) / 1e9,
-                              tflops=FLOP_STATE * NTt / (t_state * 1e-3) / 1e12),
-        "fdr_chunk_bwd": dict(ms=t_chunk, gbs=BYTES_CHUNK * NTt / (t_chunk * 1e-3) / 1e9,
-                              tflops=FLOP_CHUNK * NTt / (t_chunk * 1e-3) / 1e12),
-    }
-    dom = max(kernels, key=lambda n: kernels[n]["ms"])
-    dom_bytes = (BYTES_CHUNK if dom == "fdr_chunk_bwd" else BYTES_STATE) * NTt
-    achieved = kernels[dom]["gbs"]
-    flops = (FLOP_STATE + FLOP_CHUNK) * NTt
-    tflops = flops / (ms * 1e-3) / 1e12
-
-    # ---- CPU baseline: fp64 oracle of the same two stages on a bounded sample ----
     cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(xs, sv, dO, dh, dR, scale, NTt)
+    if not args.no_cpu and args.config == "kda":
+        cpu = cpu_baseline(xs, sv, dO, sv["scale"], NTt)
+
+    ms, tflops, kernels = res["ms"], res["tflops"], res["kernels"]
+    dom = max(kernels, key=lambda n: kernels[n]["ms"])
+    achieved = kernels[dom]["gbs"]
+    del res, xs, dO, sv
+    torch.cuda.empty_cache()
+
+    secondary = None
+    if args.config == "kda" and not args.no_secondary:
+        g = measure(CONFIGS["gdn"], max(5, args.steps // 2), 2)
+        secondary = {"gdn": {"workload": "gdn chunk backward (always recompute), B=8 T=4096 H=16 K=V=128",
+                             "ms": round(g["ms"], 4), "tflops": round(g["tflops"], 2),
+                             "mfma_peak_frac": round(g["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+                             "kernels": g["kernels"]}}
+        del g
+        torch.cuda.empty_cache()
 
     line = {
         "metric": METRIC,
@@ -196,77 +352,24 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (BASELINE.json distributions, seeded)",
-        "config": {"workload": f"{cfg['op']} chunk backward, full saving, B={B} T={T} H={H} K=V=128 chunk=64",
+        "data": "synthetic (BASELINE.json distributions, seeded); random inputs, no checkpoint",
+        "config": {"workload": f"{cfg['op']} chunk backward, {'full saving' if cfg['full_saving'] else 'recompute'}, "
+                               f"B={B} T={T} H={H} K=V=128 chunk=64",
                    "global_batch": B, "seq_len": T, "heads": H, "parallelism": "none (1 GPU)"},
         "tflops": round(tflops, 2),
         "mfma_peak_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-        "kernels": {n: {kk: round(vv, 4) for kk, vv in d.items()} for n, d in kernels.items()},
+        "kernels": kernels,
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(dom, args.config), "algorithmic_bytes_per_launch": dom_bytes},
+                     "traffic": measured_traffic(dom, args.config),
+                     "algorithmic_bytes_per_launch": kernels[dom]["bytes_per_launch"]},
         "original_torch_ms": None if t_orig is None else round(t_orig, 3),
         "speedup_vs_original_torch": None if t_orig is None else round(t_orig / ms, 2),
         "parity_vs_original": parity,
         "cpu_baseline": cpu,
+        "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
-
-
-def measured_traffic(kernel, config):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE passes (profiles/hbm_traffic.json, calibrated against a plain
-    copy of known size), or None when that workload was not profiled."""
-    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
-    try:
-        with open(path) as f:
-            data = json.load(f)
-        return data[config][kernel]["bytes_per_launch"]
-    except (OSError, KeyError, ValueError):
-        return None
-
-
-def cpu_baseline(xs, sv, dO, dh, dR, scale, NTt, heads_per_piece=1):
-    """fp64 oracle (numpy, one thread) of the timed stages -- state recurrence and
-    chunk stage -- on a bounded sample (batch 0, all T, the first 8 heads, one
-    head at a time so the oracle's pairwise tensors stay small), scaled linearly
-    to the full workload's chunk-head count."""
-    import numpy as np
-    try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_limits = None
-    from oracle import delta_oracle as O
-    B, T, H = xs["q"].shape[:3]
-    heads = H
-    nb = min(B, 3)                               # batches 0..nb-1, every head: ~10 s of fp64 work
-    sample_heads = nb * heads * (T // 64)
-    ctx = threadpool_limits(limits=1) if threadpool_limits else None
-    if ctx:
-        ctx.__enter__()
-    el = 0.0
-    try:
-        for bb, h0 in [(bb, h0) for bb in range(nb) for h0 in range(0, heads, heads_per_piece)]:
-            hs = slice(h0, h0 + heads_per_piece)
-            n = lambda x: x[bb:bb + 1, :, hs].double().cpu().numpy()
-            inp = dict(qg=n(sv["qg"]), kg=n(sv["kg"]), w=n(sv["w"]), gc=n(sv["gc"]), dO=n(dO),
-                       Aqk=n(sv["Aqk"]), q=n(xs["q"]), k=n(xs["k"]), v=n(xs["v"]), beta=n(xs["beta"]),
-                       Akk=n(sv["Akk"]), h=n(sv["h"]), v_new=n(sv["v_new"]))
-            t0 = time.perf_counter()
-            dvl = O.dv_local(inp["Aqk"], inp["dO"])
-            d_h, d_R, _ = O.stage_state_bwd(inp["qg"], inp["kg"], inp["w"], inp["gc"], inp["dO"], dvl,
-                                            scale=scale)
-            O.stage_post("kda", inp["q"], inp["k"], inp["v"], inp["gc"], beta=inp["beta"], Akk=inp["Akk"],
-                         h=inp["h"], dh=d_h, v_new=inp["v_new"], dO=inp["dO"], dR=d_R, scale=scale)
-            el += time.perf_counter() - t0
-    finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
-    full_ms = el * 1e3 * NTt / sample_heads
-    return {"value": round(full_ms, 1), "unit": "ms (full workload, extrapolated)", "cores": 1,
-            "kind": "port",
-            "sample": f"fp64 numpy oracle (state recurrence + chunk stage), batches 0-{nb - 1}, T={T}, all {heads} heads "
-                      f"({sample_heads} of {NTt} chunk-heads), measured {el:.2f} s, scaled linearly"}
 
 
 if __name__ == "__main__":
