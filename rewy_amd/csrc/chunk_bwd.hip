@@ -173,8 +173,8 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     for (int i = 0; i < 2; ++i) {
       const int p = tid + 512 * i;
       const int t = p >> 4, v0 = (p & 15) * 8;
-      *reinterpret_cast<uint4*>(sR + t * LDV + v0) = *reinterpret_cast<const uint4*>(vnew + vofs + (size_t)t * rsv + v0);
-      *reinterpret_cast<uint4*>(sdO + t * LDV + v0) = *reinterpret_cast<const uint4*>(dO + vofs + (size_t)t * rsv + v0);
+      *reinterpret_cast<u32x4*>(sR + t * LDV + v0) = *reinterpret_cast<const u32x4*>(vnew + vofs + (size_t)t * rsv + v0);
+      *reinterpret_cast<u32x4*>(sdO + t * LDV + v0) = *reinterpret_cast<const u32x4*>(dO + vofs + (size_t)t * rsv + v0);
     }
     int fb = 0;
     if (tid < C) {
@@ -373,12 +373,12 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   const PairPiece rk = load_pair_piece(k + kofs, rsk, tid & 31, (tid >> 5) * 8);
   PairPiece rb;
   if constexpr (VEC_B) rb = load_pair_piece(bgate + kofs, rsk, tid & 31, (tid >> 5) * 8);
-  float4 rg[4];
+  f32x4 rg[4];
   if constexpr (GATE == CG_VECTOR) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int p = tid + 512 * i;              // 2048 pieces: token t, 4 columns; lanes run over t
-      rg[i] = *reinterpret_cast<const float4*>(g + kofs + (size_t)(p & 63) * rsk + (p >> 6) * 4);
+      rg[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)(p & 63) * rsk + (p >> 6) * 4);
     }
   }
   __syncthreads();   // P, R, dO no longer needed: region B becomes q^T, k^T, g^T (, b^T)

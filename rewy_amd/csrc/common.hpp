@@ -16,6 +16,10 @@ typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// Native vector types for 16-byte register copies: HIP's uint4 / float4 are
+// structs whose copies lower to memcpy, which keeps them out of registers
+// (the backend then parks them in LDS or scratch).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int C = 64;     // chunk length
 constexpr int KD = 128;   // key width
@@ -89,13 +93,13 @@ __device__ __forceinline__ float sum_row16(float x) {
 // lanes of one LDS write cycle hit 32 consecutive dwords (no bank conflict).
 // ---------------------------------------------------------------------------
 struct PairPiece {
-  uint4 a, b;   // rows t and t+1, 8 bf16 each
+  u32x4 a, b;   // rows t and t+1, 8 bf16 each
 };
 
 __device__ __forceinline__ PairPiece load_pair_piece(const bf16* src, size_t ld, int tp, int c0) {
   PairPiece p;
-  p.a = *reinterpret_cast<const uint4*>(src + (size_t)(2 * tp) * ld + c0);
-  p.b = *reinterpret_cast<const uint4*>(src + (size_t)(2 * tp + 1) * ld + c0);
+  p.a = *reinterpret_cast<const u32x4*>(src + (size_t)(2 * tp) * ld + c0);
+  p.b = *reinterpret_cast<const u32x4*>(src + (size_t)(2 * tp + 1) * ld + c0);
   return p;
 }
 
@@ -128,13 +132,13 @@ __device__ __forceinline__ void store_pair_piece_scaled(uint32_t* dst, int pitch
 // fp32 piece: two consecutive tokens x 4 columns, split into bf16 hi / lo
 // transposed tiles (pair-packed dwords).
 struct PairPieceF {
-  float4 a, b;
+  f32x4 a, b;
 };
 
 __device__ __forceinline__ PairPieceF load_pair_piece_f(const float* src, size_t ld, int tp, int c0) {
   PairPieceF p;
-  p.a = *reinterpret_cast<const float4*>(src + (size_t)(2 * tp) * ld + c0);
-  p.b = *reinterpret_cast<const float4*>(src + (size_t)(2 * tp + 1) * ld + c0);
+  p.a = *reinterpret_cast<const f32x4*>(src + (size_t)(2 * tp) * ld + c0);
+  p.b = *reinterpret_cast<const f32x4*>(src + (size_t)(2 * tp + 1) * ld + c0);
   return p;
 }
 

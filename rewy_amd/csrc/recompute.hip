@@ -82,10 +82,10 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
       float ea[8], eb[8], za[8], zb[8];
       float ga[8], gb[8], ba[8], bb[8], wa[8], wb[8];
       if constexpr (GATE == RG_VECTOR) {
-        const float4 g0 = *reinterpret_cast<const float4*>(g + kofs + (size_t)t0 * rsk + c0);
-        const float4 g1 = *reinterpret_cast<const float4*>(g + kofs + (size_t)t0 * rsk + c0 + 4);
-        const float4 g2 = *reinterpret_cast<const float4*>(g + kofs + (size_t)(t0 + 1) * rsk + c0);
-        const float4 g3 = *reinterpret_cast<const float4*>(g + kofs + (size_t)(t0 + 1) * rsk + c0 + 4);
+        const f32x4 g0 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)t0 * rsk + c0);
+        const f32x4 g1 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)t0 * rsk + c0 + 4);
+        const f32x4 g2 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)(t0 + 1) * rsk + c0);
+        const f32x4 g3 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)(t0 + 1) * rsk + c0 + 4);
         const float gg0[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
         const float gg1[8] = {g2.x, g2.y, g2.z, g2.w, g3.x, g3.y, g3.z, g3.w};
 #pragma unroll
@@ -103,10 +103,10 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
         }
       }
       if constexpr (VEC_B) {
-        const uint4 b0 = *reinterpret_cast<const uint4*>(bgate + kofs + (size_t)t0 * rsk + c0);
-        const uint4 b1 = *reinterpret_cast<const uint4*>(bgate + kofs + (size_t)(t0 + 1) * rsk + c0);
-        const uint4 w0 = *reinterpret_cast<const uint4*>(wgate + vofs + (size_t)t0 * rsv + c0);
-        const uint4 w1 = *reinterpret_cast<const uint4*>(wgate + vofs + (size_t)(t0 + 1) * rsv + c0);
+        const u32x4 b0 = *reinterpret_cast<const u32x4*>(bgate + kofs + (size_t)t0 * rsk + c0);
+        const u32x4 b1 = *reinterpret_cast<const u32x4*>(bgate + kofs + (size_t)(t0 + 1) * rsk + c0);
+        const u32x4 w0 = *reinterpret_cast<const u32x4*>(wgate + vofs + (size_t)t0 * rsv + c0);
+        const u32x4 w1 = *reinterpret_cast<const u32x4*>(wgate + vofs + (size_t)(t0 + 1) * rsv + c0);
         const bf16* pb0 = reinterpret_cast<const bf16*>(&b0);
         const bf16* pb1 = reinterpret_cast<const bf16*>(&b1);
         const bf16* pw0 = reinterpret_cast<const bf16*>(&w0);
@@ -150,8 +150,8 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     for (int i = 0; i < 4; ++i) {
       const int p = tid + 256 * i;          // 1024 pieces of 8
       const int t = p >> 4, c0 = (p & 15) * 8;
-      const uint4 qq = *reinterpret_cast<const uint4*>(q + kofs + (size_t)t * rsk + c0);
-      const uint4 kq = *reinterpret_cast<const uint4*>(k + kofs + (size_t)t * rsk + c0);
+      const u32x4 qq = *reinterpret_cast<const u32x4*>(q + kofs + (size_t)t * rsk + c0);
+      const u32x4 kq = *reinterpret_cast<const u32x4*>(k + kofs + (size_t)t * rsk + c0);
       const float* gr = g + kofs + (size_t)t * rsk + c0;
       const float* gl = g + kofs + (size_t)(C - 1) * rsk + c0;
       const bf16* pq = reinterpret_cast<const bf16*>(&qq);
@@ -178,8 +178,8 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const float* src = akk + ((tok0 + 16 * tt + lc) * H + h) * C + 32 * ks + 8 * lg;
-        const float4 x0 = *reinterpret_cast<const float4*>(src);
-        const float4 x1 = *reinterpret_cast<const float4*>(src + 4);
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(src);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4);
         const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -299,23 +299,35 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
   const int dct0 = DCT * (wv >> 2);
   const bool has_dr = dct0 < NCT;
 
-  uint4 rw[2];
+  u32x4 rw[2];
   PairPiece rk;
+  bf16x4 ru[DCT];      // this lane's u values of its v_new tiles (prefetched)
+  bf16x4 uc[DCT];      // the same for the chunk being processed
   float rg_last = 0.f, rg_tok = 0.f;
   auto load_chunk = [&](int c) {
     const size_t tok0 = (size_t)b * T + (size_t)c * C;
     const bf16* wb = w + tok0 * rsk + (size_t)h * KD;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int p = tid + NTH * i;
-      rw[i] = *reinterpret_cast<const uint4*>(wb + (size_t)(p >> 4) * rsk + (p & 15) * 8);
-    }
-    rk = load_pair_piece(k + tok0 * rsk + (size_t)h * KD, rsk, tid & 31, (tid >> 5) * 8);
+    // gate first: its consumer (lambda) is the first thing staged
     if constexpr (GATE == RG_VECTOR) {
       if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
     } else if constexpr (GATE == RG_SCALAR) {
       if (tid < C) rg_tok = g[(tok0 + tid) * H + h];
       rg_last = g[(tok0 + C - 1) * H + h];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + NTH * i;
+      rw[i] = *reinterpret_cast<const u32x4*>(wb + (size_t)(p >> 4) * rsk + (p & 15) * 8);
+    }
+    rk = load_pair_piece(k + tok0 * rsk + (size_t)h * KD, rsk, tid & 31, (tid >> 5) * 8);
+    if (has_dr) {
+#pragma unroll
+      for (int cc = 0; cc < DCT; ++cc)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * drow + 4 * (l >> 4) + r;
+          ru[cc][r] = u[(tok0 + t) * rsv + (size_t)h * VD + v_base + 16 * (dct0 + cc) + (l & 15)];
+        }
     }
   };
   auto stage_chunk = [&]() {
@@ -329,9 +341,11 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     }
     if constexpr (GATE == RG_SCALAR) __syncthreads();
 #pragma unroll
+    for (int cc = 0; cc < DCT; ++cc) uc[cc] = ru[cc];
+#pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
-      *reinterpret_cast<uint4*>(&sm.w[p >> 4][(p & 15) * 8]) = rw[i];
+      *reinterpret_cast<u32x4*>(&sm.w[p >> 4][(p & 15) * 8]) = rw[i];
     }
     const int tp = tid & 31;
     if constexpr (GATE == RG_SCALAR)
@@ -363,10 +377,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
         const int ct = dct0 + cc;
         f32x4 a;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 16 * drow + 4 * (l >> 4) + r;
-          a[r] = -to_f32(u[(tok0 + t) * rsv + (size_t)h * VD + v_base + 16 * ct + (l & 15)]);
-        }
+        for (int r = 0; r < 4; ++r) a[r] = -to_f32(uc[cc][r]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
           a = mfma(frag(&sm.w[16 * drow][32 * ks], S::LDK), frag(&sm.hT[16 * ct][32 * ks], S::LDK), a);
@@ -391,14 +402,22 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     // stores of h_c and v_new_c from the transposed LDS copies (lanes run over rows)
     {
       const size_t hb = (((size_t)b * NT + c) * H + h) * KD * VD;
-      for (int p = tid; p < KD * BV / 8; p += NTH) {
+      // fixed trip counts keep the vector-memory wait counts static
+      constexpr int NP = KD * BV / 8, NR = C * BV / 8;
+#pragma unroll
+      for (int i = 0; i < (NP + NTH - 1) / NTH; ++i) {
+        const int p = tid + NTH * i;
+        if (NP % NTH != 0 && p >= NP) break;
         const int kr = p % KD, v0 = (p / KD) * 8;
         bf16x8 o;
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = sm.hT[v0 + j][kr];
         *reinterpret_cast<bf16x8*>(h_out + hb + (size_t)kr * VD + v_base + v0) = o;
       }
-      for (int p = tid; p < C * BV / 8; p += NTH) {
+#pragma unroll
+      for (int i = 0; i < (NR + NTH - 1) / NTH; ++i) {
+        const int p = tid + NTH * i;
+        if (NR % NTH != 0 && p >= NR) break;
         const int t = p % C, v0 = (p / C) * 8;
         bf16x8 o;
 #pragma unroll

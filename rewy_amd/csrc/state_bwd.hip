@@ -83,7 +83,7 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
   // Aqk (transposed hi/lo):           512 pair pieces, 1 per thread
   // dO (transposed):                  32 * BV / 8 pair pieces
   constexpr int NDO = (32 * (BV / 8) + NTH - 1) / NTH;
-  uint4 rk[2];
+  u32x4 rk[2];
   PairPiece rq[1], rw[1], rdo[NDO];
   PairPieceF ra[1];
   float rg_last = 0.f, rg_tok = 0.f;
@@ -95,10 +95,17 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
     const bf16* qb = q + tok0 * row_stride_k + (size_t)h * KD;
     const bf16* wb = w + tok0 * row_stride_k + (size_t)h * KD;
     const bf16* kb = k + tok0 * row_stride_k + (size_t)h * KD;
+    // gate first: its consumer (lambda) is the first thing staged
+    if constexpr (GATE == GATE_VECTOR) {
+      if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
+    } else if constexpr (GATE == GATE_SCALAR) {
+      if (tid < C) rg_tok = g[(tok0 + tid) * H + h];
+      rg_last = g[(tok0 + C - 1) * H + h];
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
-      rk[i] = *reinterpret_cast<const uint4*>(kb + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8);
+      rk[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8);
     }
 #pragma unroll
     for (int i = 0; i < 1; ++i) {
@@ -110,16 +117,10 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
     }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
-      const int p = tid + NTH * i;
-      if (p < 32 * (BV / 8))
-        rdo[i] = load_pair_piece(dO + tok0 * row_stride_v + (size_t)h * VD + v_base, row_stride_v, p & 31,
-                                 (p >> 5) * 8);
-    }
-    if constexpr (GATE == GATE_VECTOR) {
-      if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
-    } else if constexpr (GATE == GATE_SCALAR) {
-      if (tid < C) rg_tok = g[(tok0 + tid) * H + h];
-      rg_last = g[(tok0 + C - 1) * H + h];
+      // every lane loads (clamped to a valid piece) so the wait counts stay static
+      const int p = min(tid + NTH * i, 32 * (BV / 8) - 1);
+      rdo[i] = load_pair_piece(dO + tok0 * row_stride_v + (size_t)h * VD + v_base, row_stride_v, p & 31,
+                               (p >> 5) * 8);
     }
   };
 
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
         for (int j = 0; j < 8; ++j) kk[j] = to_bf16(to_f32(pk[j]) * gk);
         *reinterpret_cast<bf16x8*>(&sm.k[t][k0]) = kk;
       } else {
-        *reinterpret_cast<uint4*>(&sm.k[t][k0]) = rk[i];
+        *reinterpret_cast<u32x4*>(&sm.k[t][k0]) = rk[i];
       }
     }
 #pragma unroll
@@ -250,7 +251,12 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
     {
       const size_t dh_base = (((size_t)b * NT + c) * H + h) * KD * VD;
       constexpr int NP = KD * BV / 8;
-      for (int p = tid; p < NP; p += NTH) {
+      // fixed trip counts keep the vector-memory wait counts static, so the next
+      // chunk's staging waits only for its own loads, not for these stores
+#pragma unroll
+      for (int i = 0; i < (NP + NTH - 1) / NTH; ++i) {
+        const int p = tid + NTH * i;
+        if (NP % NTH != 0 && p >= NP) break;
         const int kr = p % KD, v0 = (p / KD) * 8;      // lanes run over rows: conflict-free LDS reads
         bf16x8 o;
 #pragma unroll
@@ -259,7 +265,10 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
       }
       const size_t tok0 = (size_t)b * T + (size_t)c * C;
       constexpr int NR = C * BV / 8;
-      for (int p = tid; p < NR; p += NTH) {
+#pragma unroll
+      for (int i = 0; i < (NR + NTH - 1) / NTH; ++i) {
+        const int p = tid + NTH * i;
+        if (NR % NTH != 0 && p >= NR) break;
         const int t = p % C, v0 = (p / C) * 8;
         bf16x8 o;
 #pragma unroll
