@@ -87,18 +87,6 @@ struct PostLayout {
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
-__device__ __forceinline__ bf16x4 split_hi4(f32x4 x, bf16x4& lo) {
-  bf16x4 hi;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    bf16 h, l;
-    split_bf16(x[r], h, l);
-    hi[r] = h;
-    lo[r] = l;
-  }
-  return hi;
-}
-
 template <int GATE, bool VEC_B>
 __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,

@@ -53,6 +53,19 @@ __device__ __forceinline__ void split_bf16(float x, bf16& hi, bf16& lo) {
   lo = to_bf16(x - to_f32(hi));
 }
 
+// hi + lo split of four fp32 values; returns hi, writes lo.
+__device__ __forceinline__ bf16x4 split_hi4(f32x4 x, bf16x4& lo) {
+  bf16x4 hi;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    bf16 h, l;
+    split_bf16(x[r], h, l);
+    hi[r] = h;
+    lo[r] = l;
+  }
+  return hi;
+}
+
 // 2^x on the hardware transcendental unit (no denormal-range fix-up: results
 // below 2^-126 flush to zero, which every use here tolerates).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -158,6 +171,72 @@ __device__ __forceinline__ void store_pair_piece_split(uint32_t* dhi, uint32_t* 
     dhi[(c0 + j) * pitch_dw + tp] = pack2(ah, bh);
     dlo[(c0 + j) * pitch_dw + tp] = pack2(al, bl);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Row-major LDS tiles read transposed.
+//
+// gfx950's ds_read_b64_tr_b16 lets each lane of a 16-lane group name an 8-byte
+// piece (4 bf16) and returns the group's 16 x 4 pieces transposed: lane i gets
+// element (i & 3) of the pieces named by lanes 4j + (i >> 2), j = 0..3.  With
+// lane s naming row r0 + (s >> 2), columns c0 + 4 (s & 3) .. +3 of a row-major
+// tile X[r][c], lane i receives X[r0 + j][c0 + i] for j = 0..3: four
+// consecutive rows of one column, i.e. an MFMA operand fragment whose
+// contraction index runs down the rows.  Token-major inputs can therefore be
+// staged exactly as they sit in HBM (coalesced 16-byte rows, one ds_write_b128
+// per piece) and still feed contractions over tokens.
+//
+// Tiles of CH 16-byte chunks per row are stored without padding; chunk c of
+// row r sits at chunk c ^ tr_swz<CH>(r).  The swizzle keeps the two chunks a
+// 16-lane group reads per row adjacent (it is even) and spreads the 8 rows one
+// half-wave reads (r0 + {0..3, 8..11} + 16 q) over distinct banks.
+template <int CH>
+__device__ __forceinline__ int tr_swz(int r) {
+  if constexpr (CH >= 16) return 2 * ((r & 3) | (((r >> 3) & 1) << 2));
+  else if constexpr (CH == 8) return 2 * (((r >> 1) & 1) | (((r >> 3) & 1) << 1));
+  else if constexpr (CH == 4) return 2 * ((r >> 3) & 1);
+  else return 0;
+}
+
+// element offset of (row r, column col) in a swizzled tile of CH chunks per row
+template <int CH>
+__device__ __forceinline__ int tr_off(int r, int col) {
+  return r * (CH * 8) + (((col >> 3) ^ tr_swz<CH>(r)) << 3) + (col & 7);
+}
+
+__device__ __forceinline__ bf16x4 ds_read_tr4(const bf16* p) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+// Operand fragment of a contraction over rows r0 .. r0 + 31 of a swizzled
+// row-major tile, for the 16 columns c0 .. c0 + 15 (lane l: column c0 + (l & 15),
+// rows r0 + 8 (l >> 4) .. + 7).  Serves as the A operand of X^T Y (output
+// rows = columns of X) and as the B operand of X^T Y (output columns =
+// columns of Y).
+template <int CH>
+__device__ __forceinline__ bf16x8 frag_tr(const bf16* tile, int r0, int c0) {
+  const int l = lane_id(), i = l & 15;
+  const int r = r0 + 8 * (l >> 4) + (i >> 2);
+  const int col = c0 + 4 * (i & 3);
+  const bf16x4 a = ds_read_tr4(tile + tr_off<CH>(r, col));
+  const bf16x4 b = ds_read_tr4(tile + tr_off<CH>(r + 4, col));
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// 16-byte piece (8 bf16) of row r, chunk c of a swizzled tile
+template <int CH>
+__device__ __forceinline__ void store_tr_chunk(bf16* tile, int r, int c, u32x4 v) {
+  *reinterpret_cast<u32x4*>(tile + r * (CH * 8) + ((c ^ tr_swz<CH>(r)) << 3)) = v;
+}
+
+// 8 bf16 of a 16-byte piece, each multiplied by `s` (row scaling on staging)
+__device__ __forceinline__ u32x4 scale_bf16x8(u32x4 v, float s) {
+  bf16x8 x = __builtin_bit_cast(bf16x8, v);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] = to_bf16(to_f32(x[j]) * s);
+  return __builtin_bit_cast(u32x4, x);
 }
 
 }  // namespace rewy

@@ -10,10 +10,12 @@
 //   dh        = diag(lambda_c) dh + scale qg_c^T dO_c - w_c^T dR_c
 //
 // and dh0 = dh at the end (fp32).  dh is a 128 x BV fp32 tile held in
-// accumulator registers for the whole sequence; every per-chunk operand is
-// staged in LDS in K-contiguous layout so that all contractions run on
-// v_mfma_f32_16x16x32_bf16.  Operands of the next chunk are fetched into
-// registers while the current chunk computes.
+// accumulator registers for the whole sequence; all contractions run on
+// v_mfma_f32_16x16x32_bf16.  Per-chunk operands are staged in LDS row-major,
+// as they sit in HBM (coalesced 16-byte loads, one ds_write_b128 per piece);
+// the contractions over tokens read them transposed with ds_read_b64_tr_b16.
+// Operands of the next chunk are fetched into registers while the current
+// chunk computes.
 #include "common.hpp"
 
 namespace rewy {
@@ -24,14 +26,15 @@ template <int BV, int GATE, bool DV_FROM_AQK>
 struct StateSmem {
   static constexpr int LDK = KD + 8;   // pitch of [.][K] tiles
   static constexpr int LDT = C + 8;    // pitch of [.][T] tiles
-  bf16 k[C][LDK];          // kg rows: A operand of kg * dh        (contraction over K)
-  bf16 qT[KD][LDT];        // qg^T:    A operand of qg^T dO         (contraction over T)
-  bf16 wT[KD][LDT];        // -w^T:    A operand of -w^T dR         (contraction over T)
-  bf16 aTh[C][LDT];        // Aqk^T hi: A operand of Aqk^T dO       (contraction over S)
-  bf16 aTl[C][LDT];        // Aqk^T lo
-  bf16 doT[BV][LDT];       // dO^T:    B operand (contraction over T)
+  static constexpr int CHV = BV / 8;   // 16-byte chunks per dO row
+  bf16 k[C][LDK];          // kg rows:  A operand of kg * dh           (contraction over K, row reads)
+  bf16 q[C * KD];          // qg rows:  A operand of qg^T dO           (over T, transposed reads)
+  bf16 w[C * KD];          // w rows:   A operand of w^T dR            (over T, transposed reads)
+  bf16 ah[C * C];          // Aqk rows [t][s] hi: A operand of Aqk^T dO (over T, transposed reads)
+  bf16 al[C * C];          // Aqk lo
+  bf16 dO[C * BV];         // dO rows [t][v]: B operand of both        (over T, transposed reads)
   bf16 dhT[BV][LDK];       // dh^T:    B operand of kg * dh
-  bf16 drT[BV][LDT];       // dR^T:    B operand of -w^T dR
+  bf16 drT[BV][LDT];       // dR^T:    B operand of w^T dR
   float lam[KD];           // exp2(g_last) per key row
   float gam[C];            // scalar gate: exp2(g_t)
   float gkf[C];            // scalar gate: exp2(g_last - g_t)
@@ -77,24 +80,21 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
   const int dct0 = DCT * (wv >> 2);
   const bool has_dr = dct0 < NCT;
 
-  // ---- register staging of one chunk's operands ----
-  // kg rows (row-major copy):        1024 16-byte pieces, 2 per thread
-  // qg, w (transposed, token pairs):  512 pair pieces each, 1 per thread
-  // Aqk (transposed hi/lo):           512 pair pieces, 1 per thread
-  // dO (transposed):                  32 * BV / 8 pair pieces
-  constexpr int NDO = (32 * (BV / 8) + NTH - 1) / NTH;
-  u32x4 rk[2];
-  PairPiece rq[1], rw[1], rdo[NDO];
-  PairPieceF ra[1];
+  // ---- register staging of one chunk's operands (lanes run along rows) ----
+  // kg, qg, w rows:  1024 16-byte pieces each, 2 per thread
+  // Aqk rows (fp32): 1024 16-byte pieces, 2 per thread
+  // dO rows:         8 * BV pieces
+  constexpr int CHV = S::CHV;
+  constexpr int NPD = C * CHV;
+  constexpr int NDO = (NPD + NTH - 1) / NTH;
+  u32x4 rk[2], rq[2], rw[2], rdo[NDO];
+  f32x4 ra[2];
   float rg_last = 0.f, rg_tok = 0.f;
   const size_t row_stride_k = (size_t)H * KD;   // elements between tokens
   const size_t row_stride_v = (size_t)H * VD;
 
   auto load_chunk = [&](int c) {
     const size_t tok0 = (size_t)b * T + (size_t)c * C;
-    const bf16* qb = q + tok0 * row_stride_k + (size_t)h * KD;
-    const bf16* wb = w + tok0 * row_stride_k + (size_t)h * KD;
-    const bf16* kb = k + tok0 * row_stride_k + (size_t)h * KD;
     // gate first: its consumer (lambda) is the first thing staged
     if constexpr (GATE == GATE_VECTOR) {
       if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
@@ -102,25 +102,23 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
       if (tid < C) rg_tok = g[(tok0 + tid) * H + h];
       rg_last = g[(tok0 + C - 1) * H + h];
     }
+    const size_t kofs = tok0 * row_stride_k + (size_t)h * KD;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
-      rk[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < 1; ++i) {
-      const int p = tid + NTH * i;
-      rq[i] = load_pair_piece(qb, row_stride_k, p & 31, (p >> 5) * 8);
-      rw[i] = load_pair_piece(wb, row_stride_k, p & 31, (p >> 5) * 8);
+      const size_t o = kofs + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8;
+      rk[i] = *reinterpret_cast<const u32x4*>(k + o);
+      rq[i] = *reinterpret_cast<const u32x4*>(q + o);
+      rw[i] = *reinterpret_cast<const u32x4*>(w + o);
       if constexpr (DV_FROM_AQK)
-        ra[i] = load_pair_piece_f(aqk + (tok0 * H + h) * C, (size_t)H * C, p & 31, (p >> 5) * 4);
+        ra[i] = *reinterpret_cast<const f32x4*>(aqk + ((tok0 + (p >> 4)) * H + h) * C + (p & 15) * 4);
     }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
       // every lane loads (clamped to a valid piece) so the wait counts stay static
-      const int p = min(tid + NTH * i, 32 * (BV / 8) - 1);
-      rdo[i] = load_pair_piece(dO + tok0 * row_stride_v + (size_t)h * VD + v_base, row_stride_v, p & 31,
-                               (p >> 5) * 8);
+      const int p = min(tid + NTH * i, NPD - 1);
+      rdo[i] = *reinterpret_cast<const u32x4*>(dO + (tok0 + p / CHV) * row_stride_v + (size_t)h * VD + v_base +
+                                               (p % CHV) * 8);
     }
   };
 
@@ -137,41 +135,29 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
       if (tid < KD) sm.lam[tid] = 1.f;
     }
     if constexpr (GATE == GATE_SCALAR) __syncthreads();  // gam / gkf needed below
-    uint32_t* qT = reinterpret_cast<uint32_t*>(&sm.qT[0][0]);
-    uint32_t* wT = reinterpret_cast<uint32_t*>(&sm.wT[0][0]);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
-      const int t = p >> 4, k0 = (p & 15) * 8;
+      const int t = p >> 4, ch = p & 15;
+      u32x4 kq = rk[i], qq = rq[i];
       if constexpr (GATE == GATE_SCALAR) {
-        const bf16* pk = reinterpret_cast<const bf16*>(&rk[i]);
-        const float gk = sm.gkf[t];
-        bf16x8 kk;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) kk[j] = to_bf16(to_f32(pk[j]) * gk);
-        *reinterpret_cast<bf16x8*>(&sm.k[t][k0]) = kk;
-      } else {
-        *reinterpret_cast<u32x4*>(&sm.k[t][k0]) = rk[i];
+        kq = scale_bf16x8(kq, sm.gkf[t]);
+        qq = scale_bf16x8(qq, sm.gam[t]);
       }
-    }
-#pragma unroll
-    for (int i = 0; i < 1; ++i) {
-      const int p = tid + NTH * i;
-      const int tp = p & 31;
-      if constexpr (GATE == GATE_SCALAR)
-        store_pair_piece_scaled(qT, S::LDT / 2, tp, (p >> 5) * 8, rq[i], sm.gam[2 * tp], sm.gam[2 * tp + 1]);
-      else
-        store_pair_piece(qT, S::LDT / 2, tp, (p >> 5) * 8, rq[i]);
-      store_pair_piece_scaled(wT, S::LDT / 2, tp, (p >> 5) * 8, rw[i], -1.f, -1.f);
-      if constexpr (DV_FROM_AQK)
-        store_pair_piece_split(reinterpret_cast<uint32_t*>(&sm.aTh[0][0]), reinterpret_cast<uint32_t*>(&sm.aTl[0][0]),
-                               S::LDT / 2, tp, (p >> 5) * 4, ra[i], 1.f);
+      *reinterpret_cast<u32x4*>(&sm.k[t][ch * 8]) = kq;
+      store_tr_chunk<16>(sm.q, t, ch, qq);
+      store_tr_chunk<16>(sm.w, t, ch, rw[i]);
+      if constexpr (DV_FROM_AQK) {
+        bf16x4 lo;
+        const bf16x4 hi = split_hi4(ra[i], lo);
+        *reinterpret_cast<bf16x4*>(sm.ah + tr_off<8>(t, ch * 4)) = hi;
+        *reinterpret_cast<bf16x4*>(sm.al + tr_off<8>(t, ch * 4)) = lo;
+      }
     }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
       const int p = tid + NTH * i;
-      if (p < 32 * (BV / 8))
-        store_pair_piece(reinterpret_cast<uint32_t*>(&sm.doT[0][0]), S::LDT / 2, p & 31, (p >> 5) * 8, rdo[i]);
+      if (NPD % NTH == 0 || p < NPD) store_tr_chunk<CHV>(sm.dO, p / CHV, p % CHV, rdo[i]);
     }
   };
 
@@ -197,7 +183,7 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
       f32x4 a = zero4();
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag(&sm.qT[16 * wv][32 * ks], S::LDT), frag(&sm.doT[16 * ct][32 * ks], S::LDT), a);
+        a = mfma(frag_tr<16>(sm.q, 32 * ks, 16 * wv), frag_tr<CHV>(sm.dO, 32 * ks, 16 * ct), a);
       xq[ct] = a;
     }
     // dR tiles: kg dh + Aqk^T dO (+ dv)
@@ -209,9 +195,9 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
         if constexpr (DV_FROM_AQK) {
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 bo = frag(&sm.doT[16 * ct][32 * ks], S::LDT);
-            a = mfma(frag(&sm.aTh[16 * drow][32 * ks], S::LDT), bo, a);
-            a = mfma(frag(&sm.aTl[16 * drow][32 * ks], S::LDT), bo, a);
+            const bf16x8 bo = frag_tr<CHV>(sm.dO, 32 * ks, 16 * ct);
+            a = mfma(frag_tr<8>(sm.ah, 32 * ks, 16 * drow), bo, a);
+            a = mfma(frag_tr<8>(sm.al, 32 * ks, 16 * drow), bo, a);
           }
         } else {
           const size_t tok0 = (size_t)b * T + (size_t)c * C;
@@ -232,19 +218,19 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
     }
     __syncthreads();
 
-    // dh <- lambda * dh + scale * X - w^T dR
+    // dh <- lambda * dh + scale * X - w^T dR   (accumulated negated: -a + w^T dR)
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
       f32x4 a;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int kr = 16 * wv + 4 * (l >> 4) + r;
-        a[r] = st[ct][r] * sm.lam[kr] + scale * xq[ct][r];
+        a[r] = -(st[ct][r] * sm.lam[kr] + scale * xq[ct][r]);
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag(&sm.wT[16 * wv][32 * ks], S::LDT), frag(&sm.drT[16 * ct][32 * ks], S::LDT), a);
-      st[ct] = a;
+        a = mfma(frag_tr<16>(sm.w, 32 * ks, 16 * wv), frag(&sm.drT[16 * ct][32 * ks], S::LDT), a);
+      st[ct] = -a;
     }
 
     // global stores of dh[c] and dR_c from the transposed LDS copies
