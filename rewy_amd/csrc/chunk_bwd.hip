@@ -56,7 +56,7 @@ enum GateModeC { CG_NONE = 0, CG_SCALAR = 1, CG_VECTOR = 2 };
 namespace post {
 constexpr int LDT = 72;    // bf16 pitch of [.][64] tiles
 constexpr int LDV = 136;   // bf16 pitch of [.][128] tiles
-constexpr int LDG = 68;    // fp32 pitch of the [128][64] gate tile
+constexpr int LDG = 132;   // fp32 pitch of the row-major [64][128] gate tile (rows 4 apart: distinct banks)
 constexpr int T64 = C * LDT * 2;     // bytes of one [64][72] bf16 tile
 constexpr int T128 = KD * LDT * 2;   // bytes of one [128][72] bf16 tile
 constexpr int R64 = C * LDV * 2;     // bytes of one [64][136] bf16 tile
@@ -64,22 +64,23 @@ constexpr int R64 = C * LDV * 2;     // bytes of one [64][136] bf16 tile
 
 template <int GATE, bool VEC_B>
 struct PostLayout {
-  // region A.  phases 0-1: A^T hi/lo [t][s], dR^T [v][s].
+  // region A.  phases 0-1: A hi/lo [s][t], dR [s][v] (row-major, swizzled, read transposed).
   //            phases 2+:  L, D row-major hi/lo, and (scalar beta) L^T, D^T hi/lo.
   static constexpr bool LT_COPY = !VEC_B;
-  static constexpr int OFF_AKTH = 0, OFF_AKTL = post::T64, OFF_DRT = 2 * post::T64;
+  static constexpr int OFF_AKTH = 0, OFF_AKTL = C * C * 2, OFF_DRT = 2 * C * C * 2;
   static constexpr int OFF_LRH = 0, OFF_LRL = post::T64, OFF_DRH = 2 * post::T64, OFF_DRL = 3 * post::T64;
   static constexpr int OFF_LTH = 4 * post::T64, OFF_LTL = 5 * post::T64, OFF_DTH = 6 * post::T64,
                        OFF_DTL = 7 * post::T64;
-  static constexpr int A1 = 2 * post::T64 + post::T128;
+  static constexpr int A1 = 2 * C * C * 2 + C * KD * 2;
   static constexpr int A2 = (LT_COPY ? 8 : 4) * post::T64;
   static constexpr int REGION_A = A1 > A2 ? A1 : A2;
-  // region B.  phases 0-3: P, R, dO row-major.  phases 3+: q^T, k^T, g^T (, b^T).
+  // region B.  phases 0-3: P, R, dO row-major.  phases 3+: q, k (, b) row-major swizzled, g row-major.
   static constexpr int OFF_P = REGION_A, OFF_R = REGION_A + post::R64, OFF_DO = REGION_A + 2 * post::R64;
-  static constexpr int OFF_QT = REGION_A, OFF_KT = REGION_A + post::T128, OFF_GT = REGION_A + 2 * post::T128;
-  static constexpr int OFF_BT = OFF_GT + KD * post::LDG * 4;
+  static constexpr int TQ = C * KD * 2;   // bytes of one swizzled [64][128] bf16 tile
+  static constexpr int OFF_QT = REGION_A, OFF_KT = REGION_A + TQ, OFF_GT = REGION_A + 2 * TQ;
+  static constexpr int OFF_BT = OFF_GT + C * post::LDG * 4;
   static constexpr int B1 = 3 * post::R64;
-  static constexpr int B2 = 2 * post::T128 + KD * post::LDG * 4 + (VEC_B ? post::T128 : 0);
+  static constexpr int B2 = 2 * TQ + C * post::LDG * 4 + (VEC_B ? TQ : 0);
   static constexpr int OFF_SMALL = REGION_A + (B1 > B2 ? B1 : B2);
   static constexpr int S_BETA = 0, S_G = 64, S_DBA = 128, S_DBB = 192, S_DG = 256, S_COL = 320,
                        S_TOT = 448, S_GL = 576, S_N = 704;
@@ -103,9 +104,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   extern __shared__ __attribute__((aligned(16))) char smem[];
   auto B16 = [&](int off) { return reinterpret_cast<bf16*>(smem + off); };
   auto U32 = [&](int off) { return reinterpret_cast<uint32_t*>(smem + off); };
-  bf16* akTh = B16(LY::OFF_AKTH);
-  bf16* akTl = B16(LY::OFF_AKTL);
-  bf16* drT = B16(LY::OFF_DRT);
+  bf16* sAh = B16(LY::OFF_AKTH);    // A rows [s][t], hi
+  bf16* sAl = B16(LY::OFF_AKTL);    // A rows, lo
+  bf16* sdR = B16(LY::OFF_DRT);     // dR rows [s][v]
   bf16* Lrh = B16(LY::OFF_LRH);
   bf16* Lrl = B16(LY::OFF_LRL);
   bf16* Drh = B16(LY::OFF_DRH);
@@ -117,10 +118,10 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   bf16* sP = B16(LY::OFF_P);
   bf16* sR = B16(LY::OFF_R);
   bf16* sdO = B16(LY::OFF_DO);
-  bf16* qT = B16(LY::OFF_QT);
-  bf16* kT = B16(LY::OFF_KT);
-  float* gT = reinterpret_cast<float*>(smem + LY::OFF_GT);
-  bf16* bT = B16(LY::OFF_BT);
+  bf16* sQ = B16(LY::OFF_QT);       // q rows [t][k] (swizzled)
+  bf16* sK = B16(LY::OFF_KT);       // k rows
+  float* sGr = reinterpret_cast<float*>(smem + LY::OFF_GT);   // g rows [t][k], pitch LDG
+  bf16* sB = B16(LY::OFF_BT);       // erase-gate rows (GDN2)
   float* small = reinterpret_cast<float*>(smem + LY::OFF_SMALL);
   float* sBeta = small + LY::S_BETA;   // scalar beta per row
   float* sG = small + LY::S_G;         // scalar gate per row (log2)
@@ -147,15 +148,20 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   const size_t vofs = tok0 * rsv + (size_t)h * VD;    // [t][v] tensors
   const bf16* vb = v + vofs;
 
-  // ---------------- phase 0: stage A^T (hi/lo), dR^T, R, dO, beta, gates ----------------
+  // ---------------- phase 0: stage A (hi/lo), dR, R, dO row-major; beta, gates ----------------
   int any_fb = 0;
   {
-    {
-      const int p = tid;   // 512 pair pieces (32 row pairs x 16 column chunks)
-      const PairPieceF pa = load_pair_piece_f(akk + (tok0 * H + h) * C, rsa, p & 31, (p >> 5) * 4);
-      const PairPiece pd = load_pair_piece(dR + vofs, rsv, p & 31, (p >> 5) * 8);
-      store_pair_piece_split(U32(LY::OFF_AKTH), U32(LY::OFF_AKTL), LDT / 2, p & 31, (p >> 5) * 4, pa, 1.f);
-      store_pair_piece(U32(LY::OFF_DRT), LDT / 2, p & 31, (p >> 5) * 8, pd);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + 512 * i;        // 1024 16-byte pieces per tile; lanes run along rows
+      const int t = p >> 4, ch = p & 15;
+      const f32x4 a = *reinterpret_cast<const f32x4*>(akk + (tok0 * H + h) * C + (size_t)t * rsa + 4 * ch);
+      const u32x4 d = *reinterpret_cast<const u32x4*>(dR + vofs + (size_t)t * rsv + 8 * ch);
+      bf16x4 lo;
+      const bf16x4 hi = split_hi4(a, lo);
+      *reinterpret_cast<bf16x4*>(sAh + tr_off<8>(t, 4 * ch)) = hi;
+      *reinterpret_cast<bf16x4*>(sAl + tr_off<8>(t, 4 * ch)) = lo;
+      store_tr_chunk<16>(sdR, t, ch, d);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -199,9 +205,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           if (ks == 0 && rh == 1) continue;    // A^T upper triangular: s < 32 <= t vanishes
-          const bf16x8 a = frag(drT + vrow0 * LDT + 32 * ks, LDT);
-          acc = mfma(a, frag(akTh + tcol0 * LDT + 32 * ks, LDT), acc);
-          acc = mfma(a, frag(akTl + tcol0 * LDT + 32 * ks, LDT), acc);
+          const bf16x8 a = frag_tr<16>(sdR, 32 * ks, vrow0);          // dR^T rows v, over s
+          acc = mfma(a, frag_tr<8>(sAh, 32 * ks, tcol0), acc);      // A[s][t] columns t, over s
+          acc = mfma(a, frag_tr<8>(sAl, 32 * ks, tcol0), acc);
         }
         // lane: t = tcol0 + lc, v = vrow0 + 4 lg .. +3
         const int t = tcol0 + lc;
@@ -356,32 +362,37 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
       aw[I] = z;
     }
   }
-  // q, k, g (and b) for the transposed staging (issued before the barrier)
-  const PairPiece rq = load_pair_piece(q + kofs, rsk, tid & 31, (tid >> 5) * 8);
-  const PairPiece rk = load_pair_piece(k + kofs, rsk, tid & 31, (tid >> 5) * 8);
-  PairPiece rb;
-  if constexpr (VEC_B) rb = load_pair_piece(bgate + kofs, rsk, tid & 31, (tid >> 5) * 8);
+  // q, k, g (and b) rows for the row-major staging (issued before the barrier)
+  u32x4 rq[2], rk[2], rb[2];
   f32x4 rg[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = tid + 512 * i;
+    const size_t o = kofs + (size_t)(p >> 4) * rsk + (p & 15) * 8;
+    rq[i] = *reinterpret_cast<const u32x4*>(q + o);
+    rk[i] = *reinterpret_cast<const u32x4*>(k + o);
+    if constexpr (VEC_B) rb[i] = *reinterpret_cast<const u32x4*>(bgate + o);
+  }
   if constexpr (GATE == CG_VECTOR) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int p = tid + 512 * i;              // 2048 pieces: token t, 4 columns; lanes run over t
-      rg[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)(p & 63) * rsk + (p >> 6) * 4);
+      const int p = tid + 512 * i;              // 2048 pieces: token p >> 5, 4 columns
+      rg[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)(p >> 5) * rsk + (p & 31) * 4);
     }
   }
-  __syncthreads();   // P, R, dO no longer needed: region B becomes q^T, k^T, g^T (, b^T)
-  store_pair_piece(U32(LY::OFF_QT), LDT / 2, tid & 31, (tid >> 5) * 8, rq);
-  store_pair_piece(U32(LY::OFF_KT), LDT / 2, tid & 31, (tid >> 5) * 8, rk);
-  if constexpr (VEC_B) store_pair_piece(U32(LY::OFF_BT), LDT / 2, tid & 31, (tid >> 5) * 8, rb);
+  __syncthreads();   // P, R, dO no longer needed: region B becomes q, k, g (, b)
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = tid + 512 * i;
+    store_tr_chunk<16>(sQ, p >> 4, p & 15, rq[i]);
+    store_tr_chunk<16>(sK, p >> 4, p & 15, rk[i]);
+    if constexpr (VEC_B) store_tr_chunk<16>(sB, p >> 4, p & 15, rb[i]);
+  }
   if constexpr (GATE == CG_VECTOR) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int p = tid + 512 * i;
-      const int t = p & 63, k0 = (p >> 6) * 4;
-      gT[(k0 + 0) * LDG + t] = rg[i].x;
-      gT[(k0 + 1) * LDG + t] = rg[i].y;
-      gT[(k0 + 2) * LDG + t] = rg[i].z;
-      gT[(k0 + 3) * LDG + t] = rg[i].w;
+      *reinterpret_cast<f32x4*>(sGr + (p >> 5) * LDG + (p & 31) * 4) = rg[i];
     }
   }
   __syncthreads();
@@ -395,17 +406,22 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
     const int r0 = 16 * J + 4 * lg;
-    if constexpr (GATE == CG_VECTOR) g4[J] = *reinterpret_cast<const f32x4*>(gT + kk * LDG + r0);
+    if constexpr (GATE == CG_VECTOR) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) g4[J][j] = sGr[(r0 + j) * LDG + kk];
+    }
     else if constexpr (GATE == CG_SCALAR) g4[J] = *reinterpret_cast<const f32x4*>(sG + r0);
     else g4[J] = zero4();
-    qb4[J] = *reinterpret_cast<const bf16x4*>(qT + kk * LDT + r0);
-    kb4[J] = *reinterpret_cast<const bf16x4*>(kT + kk * LDT + r0);
+    // transposed reads: rows r0 .. r0 + 3 of column kk
+    const int tro = tr_off<16>(r0 + (lc >> 2), 16 * wv + 4 * (lc & 3));
+    qb4[J] = ds_read_tr4(sQ + tro);
+    kb4[J] = ds_read_tr4(sK + tro);
   }
   // erase gate of rows 16 J + 4 lg .. +3 (reloaded from LDS where needed)
   auto bvals = [&](int J) -> f32x4 {
     const int r0 = 16 * J + 4 * lg;
     if constexpr (VEC_B) {
-      const bf16x4 bq = *reinterpret_cast<const bf16x4*>(bT + kk * LDT + r0);
+      const bf16x4 bq = ds_read_tr4(sB + tr_off<16>(r0 + (lc >> 2), 16 * wv + 4 * (lc & 3)));
       f32x4 o;
 #pragma unroll
       for (int j = 0; j < 4; ++j) o[j] = to_f32(bq[j]);
@@ -572,12 +588,12 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
 #pragma unroll 1
         for (int r = 0; r < 4; ++r) {
           const int i = 16 * I + 4 * lg + r;
-          const float gi = gT[kk * LDG + i];
+          const float gi = sGr[i * LDG + kk];
           float pq = 0.f, pe = 0.f, pk = 0.f;
 #pragma unroll 1
           for (int s = 16 * I; s < 16 * (I + 1); ++s) {
-            const float gs = gT[kk * LDG + s];
-            const float ksv = to_f32(kT[kk * LDT + s]);
+            const float gs = sGr[s * LDG + kk];
+            const float ksv = to_f32(sK[tr_off<16>(s, kk)]);
             if (s <= i) {
               const float f = fast_exp2(gi - gs);
               pq += (to_f32(Lrh[i * LDT + s]) + to_f32(Lrl[i * LDT + s])) * ksv * f;
@@ -588,9 +604,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
               const float lsi = to_f32(Lrh[s * LDT + i]) + to_f32(Lrl[s * LDT + i]);
               const float dsi = to_f32(Drh[s * LDT + i]) + to_f32(Drl[s * LDT + i]);
               float bs;
-              if constexpr (VEC_B) bs = to_f32(bT[kk * LDT + s]);
+              if constexpr (VEC_B) bs = to_f32(sB[tr_off<16>(s, kk)]);
               else bs = sBeta[s];
-              pk += (lsi * to_f32(qT[kk * LDT + s]) + dsi * bs * ksv) * f;
+              pk += (lsi * to_f32(sQ[tr_off<16>(s, kk)]) + dsi * bs * ksv) * f;
             }
           }
 #pragma unroll
