@@ -38,11 +38,11 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     bf16* __restrict__ u_out, bf16* __restrict__ qg_out, bf16* __restrict__ kg_out,
     float* __restrict__ aqk_out, int T, int H, float scale) {
   using rec::LDT;
-  // E^T hi/lo [128][72], Z^T hi/lo [128][72] (Z = w_gate v), small gate arrays
-  __shared__ __attribute__((aligned(16))) bf16 eTh[KD][LDT];
-  __shared__ __attribute__((aligned(16))) bf16 eTl[KD][LDT];
-  __shared__ __attribute__((aligned(16))) bf16 zTh[VD][LDT];
-  __shared__ __attribute__((aligned(16))) bf16 zTl[VD][LDT];
+  // E = b k 2^g and Z = w_gate v rows [t][.], split hi/lo, swizzled for transposed reads
+  __shared__ __attribute__((aligned(16))) bf16 eH[C * KD];
+  __shared__ __attribute__((aligned(16))) bf16 eL[C * KD];
+  __shared__ __attribute__((aligned(16))) bf16 zH[C * VD];
+  __shared__ __attribute__((aligned(16))) bf16 zL[C * VD];
   __shared__ float sG[C];
   __shared__ float sB[C];
 
@@ -65,83 +65,54 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
   }
   __syncthreads();
 
-  // ---- stage E^T = (b k 2^g)^T and Z^T = (w_gate v)^T, split hi/lo, token pairs per dword ----
-  {
-    // 512 pair pieces (32 token pairs x 16 column chunks of 8) per matrix; 2 per thread
+  // ---- stage E = b k 2^g and Z = w_gate v row-major (coalesced 16-byte rows), split hi/lo ----
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int p = tid + 256 * i;
-      const int tp = p & 31, c0 = (p >> 5) * 8;
-      const int t0 = 2 * tp;
-      const PairPiece pk = load_pair_piece(k + kofs, rsk, tp, c0);
-      const PairPiece pv = load_pair_piece(v + vofs, rsv, tp, c0);
-      const bf16* ka = reinterpret_cast<const bf16*>(&pk.a);
-      const bf16* kb = reinterpret_cast<const bf16*>(&pk.b);
-      const bf16* va = reinterpret_cast<const bf16*>(&pv.a);
-      const bf16* vb = reinterpret_cast<const bf16*>(&pv.b);
-      float ea[8], eb[8], za[8], zb[8];
-      float ga[8], gb[8], ba[8], bb[8], wa[8], wb[8];
-      if constexpr (GATE == RG_VECTOR) {
-        const f32x4 g0 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)t0 * rsk + c0);
-        const f32x4 g1 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)t0 * rsk + c0 + 4);
-        const f32x4 g2 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)(t0 + 1) * rsk + c0);
-        const f32x4 g3 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)(t0 + 1) * rsk + c0 + 4);
-        const float gg0[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-        const float gg1[8] = {g2.x, g2.y, g2.z, g2.w, g3.x, g3.y, g3.z, g3.w};
+  for (int i = 0; i < 4; ++i) {
+    const int p = tid + 256 * i;            // 1024 pieces of 8 columns: row p >> 4
+    const int t = p >> 4, ch = p & 15, c0 = 8 * ch;
+    const bf16x8 kx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(k + kofs + (size_t)t * rsk + c0));
+    const bf16x8 vx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(v + vofs + (size_t)t * rsv + c0));
+    float ge[8], be[8], we[8];
+    if constexpr (GATE == RG_VECTOR) {
+      const f32x4 g0 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)t * rsk + c0);
+      const f32x4 g1 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)t * rsk + c0 + 4);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          ga[j] = fast_exp2(gg0[j]);
-          gb[j] = fast_exp2(gg1[j]);
-        }
-      } else {
-        const float s0 = (GATE == RG_SCALAR) ? fast_exp2(sG[t0]) : 1.f;
-        const float s1 = (GATE == RG_SCALAR) ? fast_exp2(sG[t0 + 1]) : 1.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          ga[j] = s0;
-          gb[j] = s1;
-        }
+      for (int j = 0; j < 4; ++j) {
+        ge[j] = fast_exp2(g0[j]);
+        ge[j + 4] = fast_exp2(g1[j]);
       }
-      if constexpr (VEC_B) {
-        const u32x4 b0 = *reinterpret_cast<const u32x4*>(bgate + kofs + (size_t)t0 * rsk + c0);
-        const u32x4 b1 = *reinterpret_cast<const u32x4*>(bgate + kofs + (size_t)(t0 + 1) * rsk + c0);
-        const u32x4 w0 = *reinterpret_cast<const u32x4*>(wgate + vofs + (size_t)t0 * rsv + c0);
-        const u32x4 w1 = *reinterpret_cast<const u32x4*>(wgate + vofs + (size_t)(t0 + 1) * rsv + c0);
-        const bf16* pb0 = reinterpret_cast<const bf16*>(&b0);
-        const bf16* pb1 = reinterpret_cast<const bf16*>(&b1);
-        const bf16* pw0 = reinterpret_cast<const bf16*>(&w0);
-        const bf16* pw1 = reinterpret_cast<const bf16*>(&w1);
+    } else {
+      const float s0 = (GATE == RG_SCALAR) ? fast_exp2(sG[t]) : 1.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          ba[j] = to_f32(pb0[j]);
-          bb[j] = to_f32(pb1[j]);
-          wa[j] = to_f32(pw0[j]);
-          wb[j] = to_f32(pw1[j]);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          ba[j] = wa[j] = sB[t0];
-          bb[j] = wb[j] = sB[t0 + 1];
-        }
-      }
+      for (int j = 0; j < 8; ++j) ge[j] = s0;
+    }
+    if constexpr (VEC_B) {
+      const bf16x8 bx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(bgate + kofs + (size_t)t * rsk + c0));
+      const bf16x8 wx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(wgate + vofs + (size_t)t * rsv + c0));
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        ea[j] = ba[j] * to_f32(ka[j]) * ga[j];
-        eb[j] = bb[j] * to_f32(kb[j]) * gb[j];
-        za[j] = wa[j] * to_f32(va[j]);
-        zb[j] = wb[j] * to_f32(vb[j]);
-        bf16 ah, al, bh_, bl_;
-        split_bf16(ea[j], ah, al);
-        split_bf16(eb[j], bh_, bl_);
-        reinterpret_cast<uint32_t*>(&eTh[c0 + j][0])[tp] = pack2(ah, bh_);
-        reinterpret_cast<uint32_t*>(&eTl[c0 + j][0])[tp] = pack2(al, bl_);
-        split_bf16(za[j], ah, al);
-        split_bf16(zb[j], bh_, bl_);
-        reinterpret_cast<uint32_t*>(&zTh[c0 + j][0])[tp] = pack2(ah, bh_);
-        reinterpret_cast<uint32_t*>(&zTl[c0 + j][0])[tp] = pack2(al, bl_);
+        be[j] = to_f32(bx[j]);
+        we[j] = to_f32(wx[j]);
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) be[j] = we[j] = sB[t];
     }
+    bf16x8 eh, el, zh, zl;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      bf16 hh, ll;
+      split_bf16(be[j] * to_f32(kx[j]) * ge[j], hh, ll);
+      eh[j] = hh;
+      el[j] = ll;
+      split_bf16(we[j] * to_f32(vx[j]), hh, ll);
+      zh[j] = hh;
+      zl[j] = ll;
+    }
+    store_tr_chunk<16>(eH, t, ch, __builtin_bit_cast(u32x4, eh));
+    store_tr_chunk<16>(eL, t, ch, __builtin_bit_cast(u32x4, el));
+    store_tr_chunk<16>(zH, t, ch, __builtin_bit_cast(u32x4, zh));
+    store_tr_chunk<16>(zL, t, ch, __builtin_bit_cast(u32x4, zl));
   }
 
   // ---- qg / kg (vector gates): elementwise, coalesced ----
@@ -191,8 +162,8 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
       }
 #pragma unroll
     for (int which = 0; which < 2; ++which) {
-      const bf16(*srcH)[LDT] = which == 0 ? eTh : zTh;
-      const bf16(*srcL)[LDT] = which == 0 ? eTl : zTl;
+      const bf16* srcH = which == 0 ? eH : zH;
+      const bf16* srcL = which == 0 ? eL : zL;
       bf16* dst = which == 0 ? w_out + kofs : u_out + vofs;
       const size_t rs = which == 0 ? rsk : rsv;
 #pragma unroll
@@ -203,8 +174,8 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
           f32x4 acc = zero4();
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 xh = frag(&srcH[row0][32 * ks], LDT);
-            const bf16x8 xl = frag(&srcL[row0][32 * ks], LDT);
+            const bf16x8 xh = frag_tr<16>(srcH, 32 * ks, row0);   // E^T rows (k or v), over s
+            const bf16x8 xl = frag_tr<16>(srcL, 32 * ks, row0);
             acc = mfma(xh, ah[tt][ks], acc);
             acc = mfma(xh, al[tt][ks], acc);
             acc = mfma(xl, ah[tt][ks], acc);
@@ -254,7 +225,7 @@ struct FwdSmem {
   static constexpr int LDK = KD + 8;
   static constexpr int LDT = C + 8;
   bf16 w[C][LDK];          // w rows: A operand of w h           (contraction over K)
-  bf16 kT[KD][LDT];        // kg^T:   A operand of kg^T v_new      (contraction over T)
+  bf16 k[C * KD];          // kg rows (swizzled): A operand of kg^T v_new (over T, transposed reads)
   bf16 hT[BV][LDK];        // h^T:    B operand of w h
   bf16 vT[BV][LDT];        // v_new^T: B operand of kg^T v_new
   float lam[KD];
@@ -300,7 +271,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
   const bool has_dr = dct0 < NCT;
 
   u32x4 rw[2];
-  PairPiece rk;
+  u32x4 rk[2];
   bf16x4 ru[DCT];      // this lane's u values of its v_new tiles (prefetched)
   bf16x4 uc[DCT];      // the same for the chunk being processed
   float rg_last = 0.f, rg_tok = 0.f;
@@ -319,7 +290,11 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
       const int p = tid + NTH * i;
       rw[i] = *reinterpret_cast<const u32x4*>(wb + (size_t)(p >> 4) * rsk + (p & 15) * 8);
     }
-    rk = load_pair_piece(k + tok0 * rsk + (size_t)h * KD, rsk, tid & 31, (tid >> 5) * 8);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + NTH * i;
+      rk[i] = *reinterpret_cast<const u32x4*>(k + tok0 * rsk + (size_t)h * KD + (size_t)(p >> 4) * rsk + (p & 15) * 8);
+    }
     if (has_dr) {
 #pragma unroll
       for (int cc = 0; cc < DCT; ++cc)
@@ -347,12 +322,13 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
       const int p = tid + NTH * i;
       *reinterpret_cast<u32x4*>(&sm.w[p >> 4][(p & 15) * 8]) = rw[i];
     }
-    const int tp = tid & 31;
-    if constexpr (GATE == RG_SCALAR)
-      store_pair_piece_scaled(reinterpret_cast<uint32_t*>(&sm.kT[0][0]), S::LDT / 2, tp, (tid >> 5) * 8, rk,
-                              sm.gkf[2 * tp], sm.gkf[2 * tp + 1]);
-    else
-      store_pair_piece(reinterpret_cast<uint32_t*>(&sm.kT[0][0]), S::LDT / 2, tp, (tid >> 5) * 8, rk);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + NTH * i;
+      u32x4 kq = rk[i];
+      if constexpr (GATE == RG_SCALAR) kq = scale_bf16x8(kq, sm.gkf[p >> 4]);
+      store_tr_chunk<16>(sm.k, p >> 4, p & 15, kq);
+    }
   };
 
   load_chunk(0);
@@ -396,7 +372,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
       for (int r = 0; r < 4; ++r) a[r] = st[ct][r] * sm.lam[16 * wv + 4 * (l >> 4) + r];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag(&sm.kT[16 * wv][32 * ks], S::LDT), frag(&sm.vT[16 * ct][32 * ks], S::LDT), a);
+        a = mfma(frag_tr<16>(sm.k, 32 * ks, 16 * wv), frag(&sm.vT[16 * ct][32 * ks], S::LDT), a);
       st[ct] = a;
     }
     // stores of h_c and v_new_c from the transposed LDS copies (lanes run over rows)
