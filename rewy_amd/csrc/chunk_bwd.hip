@@ -66,7 +66,9 @@ template <int GATE, bool VEC_B>
 struct PostLayout {
   // region A.  phases 0-1: A hi/lo [s][t], dR [s][v] (row-major, swizzled, read transposed).
   //            phases 2+:  L, D row-major hi/lo, and (scalar beta) L^T, D^T hi/lo.
-  static constexpr bool LT_COPY = !VEC_B;
+  // Vector gates keep explicit L^T / D^T copies (fewer live registers in their
+  // intra phase); the scalar / no-gate families read L^T / D^T transposed.
+  static constexpr bool LT_COPY = GATE == CG_VECTOR;
   static constexpr int OFF_AKTH = 0, OFF_AKTL = C * C * 2, OFF_DRT = 2 * C * C * 2;
   static constexpr int OFF_LRH = 0, OFF_LRL = post::T64, OFF_DRH = 2 * post::T64, OFF_DRL = 3 * post::T64;
   static constexpr int OFF_LTH = 4 * post::T64, OFF_LTL = 5 * post::T64, OFF_DTH = 6 * post::T64,
@@ -555,15 +557,12 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
         dh_ = afrag4(Dth + (16 * I) * LDT + 16 * J);
         dl_ = afrag4(Dtl + (16 * I) * LDT + 16 * J);
       } else {
-        const int i = 16 * I + lc;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int s = 16 * J + 4 * lg + j;
-          lh[j] = Lrh[s * LDT + i];
-          ll[j] = Lrl[s * LDT + i];
-          dh_[j] = Drh[s * LDT + i];
-          dl_[j] = Drl[s * LDT + i];
-        }
+        // transposed reads of the row-major tiles: lane gets L[16 J + 4 lg + j][16 I + lc]
+        const int o = (16 * J + 4 * lg + (lc >> 2)) * LDT + 16 * I + 4 * (lc & 3);
+        lh = ds_read_tr4(Lrh + o);
+        ll = ds_read_tr4(Lrl + o);
+        dh_ = ds_read_tr4(Drh + o);
+        dl_ = ds_read_tr4(Drl + o);
       }
       f32x4 a = zero4();
       a = mfma16(lh, qEh[J], a);
