@@ -98,6 +98,29 @@ hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g
                      const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int K,
                      int V, int chunk, int value_block, hipStream_t stream);
 
+/*
+ * Standalone matrix intra (the intra-chunk VJP of a vector-gated chunk), in place.
+ * Replaces the reference's kernel-level seam chunk_<op>_bwd_intra
+ * (q, k, g, beta, dAqk, dAkk, dq, dk, db, dg) -> (dq, dk, db, dg):
+ *   KDA   EndpointMatrixIntra.__call__       kernels/endpoint_intra.py:300-326
+ *   GDN2  gdn2_consumer_fp32.matrix_intra    kernels/gdn2_consumer_fp32.py:89-98
+ * With L = tril(dAqk) (diagonal included), D = strict_tril(dAkk) and gates g in log2
+ * units (chunk-local cumsum):
+ *   uq = sum_{s<=i} L_is k_s 2^(g_i-g_s),  ue = sum_{s<i} D_is k_s 2^(g_i-g_s),
+ *   uk = sum_{s>=i} (L_si q_s + D_si b_s k_s) 2^(g_s-g_i)
+ *   dq += uq;  dk += b ue + uk;  dg += q uq + k (b ue - uk);  db += sum_k ue k  (scalar beta,
+ *   every row, or only |beta| < 1e-6 rows when beta_complete != 0, endpoint_intra.py:190-194)
+ *   or db += ue k  (GDN2's vector erase gate b_gate).
+ * q, k, b_gate bf16 [B,T,H,K]; g, dq, dk, dg fp32 [B,T,H,K]; beta, db fp32 [B,T,H] (scalar
+ * beta) or db fp32 [B,T,H,K] (b_gate non-null, beta null); dAqk, dAkk fp32 [B,T,H,64].
+ * dq, dk, db, dg are read and rewritten (the reference's dq2 aliases dq).  dg is the
+ * pre-cumsum gate gradient, as at the reference seam.
+ */
+hipError_t fdr_matrix_intra(const void* q, const void* k, const float* g, const float* beta,
+                            const void* b_gate, const float* dAqk, const float* dAkk, float* dq,
+                            float* dk, float* db, float* dg, int B, int T, int H, int K, int chunk,
+                            int beta_complete, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

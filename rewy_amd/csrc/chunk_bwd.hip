@@ -62,13 +62,13 @@ constexpr int T128 = KD * LDT * 2;   // bytes of one [128][72] bf16 tile
 constexpr int R64 = C * LDV * 2;     // bytes of one [64][136] bf16 tile
 }  // namespace post
 
-template <int GATE, bool VEC_B>
+template <int GATE, bool VEC_B, bool INTRA = false>
 struct PostLayout {
   // region A.  phases 0-1: A hi/lo [s][t], dR [s][v] (row-major, swizzled, read transposed).
   //            phases 2+:  L, D row-major hi/lo, and (scalar beta) L^T, D^T hi/lo.
   // Vector gates keep explicit L^T / D^T copies (fewer live registers in their
   // intra phase); the scalar / no-gate families read L^T / D^T transposed.
-  static constexpr bool LT_COPY = GATE == CG_VECTOR;
+  static constexpr bool LT_COPY = GATE == CG_VECTOR && !INTRA;
   static constexpr int OFF_AKTH = 0, OFF_AKTL = C * C * 2, OFF_DRT = 2 * C * C * 2;
   static constexpr int OFF_LRH = 0, OFF_LRL = post::T64, OFF_DRH = 2 * post::T64, OFF_DRL = 3 * post::T64;
   static constexpr int OFF_LTH = 4 * post::T64, OFF_LTL = 5 * post::T64, OFF_DTH = 6 * post::T64,
@@ -90,16 +90,21 @@ struct PostLayout {
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
-template <int GATE, bool VEC_B>
-__global__ __launch_bounds__(512) void chunk_bwd_kernel(
+// The body serves two kernels: the full chunk backward (INTRA = false) and the
+// standalone matrix intra (INTRA = true: L and D are given, the partial dq, dk,
+// dg, db are read-modify-written in fp32, no state terms and no cumsum).
+template <int GATE, bool VEC_B, bool INTRA>
+__device__ __forceinline__ void chunk_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
     const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
     const bf16* __restrict__ wgate, const float* __restrict__ akk, const bf16* __restrict__ hst,
     const bf16* __restrict__ dhst, bf16* __restrict__ dq_out, bf16* __restrict__ dk_out,
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
-    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale) {
-  using LY = PostLayout<GATE, VEC_B>;
+    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale,
+    const float* __restrict__ daqk, float* __restrict__ dq32, float* __restrict__ dk32,
+    float* __restrict__ db32, int beta_complete) {
+  using LY = PostLayout<GATE, VEC_B, INTRA>;
   using post::LDT;
   using post::LDV;
   using post::LDG;
@@ -152,7 +157,32 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
 
   // ---------------- phase 0: stage A (hi/lo), dR, R, dO row-major; beta, gates ----------------
   int any_fb = 0;
-  {
+  if constexpr (INTRA) {
+    // L = tril(dAqk) (diagonal included), D = strict_tril(dAkk), split hi/lo, row-major
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + 512 * i;        // 1024 pieces of 4 fp32: row p >> 4
+      const int row = p >> 4, c4 = (p & 15) * 4;
+      f32x4 a = *reinterpret_cast<const f32x4*>(daqk + (tok0 * H + h) * C + (size_t)row * rsa + c4);
+      f32x4 d = *reinterpret_cast<const f32x4*>(akk + (tok0 * H + h) * C + (size_t)row * rsa + c4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (c4 + j > row) a[j] = 0.f;
+        if (c4 + j >= row) d[j] = 0.f;
+      }
+      bf16x4 lo;
+      bf16x4 hi = split_hi4(a, lo);
+      *reinterpret_cast<bf16x4*>(Lrh + row * LDT + c4) = hi;
+      *reinterpret_cast<bf16x4*>(Lrl + row * LDT + c4) = lo;
+      hi = split_hi4(d, lo);
+      *reinterpret_cast<bf16x4*>(Drh + row * LDT + c4) = hi;
+      *reinterpret_cast<bf16x4*>(Drl + row * LDT + c4) = lo;
+    }
+    if (tid < C) {
+      if constexpr (!VEC_B) sBeta[tid] = beta[(tok0 + tid) * H + h];
+      sDbB[tid] = 0.f;
+    }
+  } else {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + 512 * i;        // 1024 16-byte pieces per tile; lanes run along rows
@@ -193,7 +223,13 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     }
     any_fb = __syncthreads_or(fb);   // block-uniform: some row has |beta| < 1e-6
   }
-  const bool has_fb = !VEC_B && any_fb != 0;
+  // the standalone intra adds the direct dbeta terms of every row
+  const bool has_fb = !VEC_B && (INTRA || any_fb != 0);
+  const int kk = 16 * wv + lc;                 // this lane's key column from phase 3 on
+  f32x4 aq[4], ak[4], aw[4];                   // dq, dk, dG of column kk, rows 16 I + 4 lg + r
+  float dgk = 0.f;
+
+  if constexpr (!INTRA) {
 
   // ---------------- phase 1: P^T = dR^T A  (accumulator layout stores P row-major) ----------------
   {
@@ -258,7 +294,6 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   __syncthreads();
 
   // prefetch state tiles for phase 3: wave wv owns key columns [16 wv, 16 wv + 16)
-  const int kk = 16 * wv + lc;                 // this lane's key column from here on
   bf16x8 fh[4], fdh[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
@@ -341,8 +376,6 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   }
 
   // ---------------- phase 3: dq_s = dO h^T, dk_s = R dh^T, dw = P h^T (16-column strip, 64 rows) ----------------
-  f32x4 aq[4], ak[4], aw[4];
-  float dgk;
   {
     float sacc = 0.f;
 #pragma unroll
@@ -364,6 +397,8 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
       aw[I] = z;
     }
   }
+  }   // !INTRA: phases 1-3
+
   // q, k, g (and b) rows for the row-major staging (issued before the barrier)
   u32x4 rq[2], rk[2], rb[2];
   f32x4 rg[4];
@@ -460,6 +495,21 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   float colkdk = 0.f;
   f32x4 fbrow[4];      // scalar-beta fallback rows: k exp2(g) Eb + k ue, summed over columns later
   f32x4 adb[4];        // vector-b family: db = k exp2(g) Eb + k ue
+  if constexpr (INTRA) {
+    // the partial gradients the intra terms are added to
+    const int rsk32 = H * KD;
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int off = (16 * I + 4 * lg + r) * rsk32 + kk;
+        aq[I][r] = dq32[kofs + off];
+        ak[I][r] = dk32[kofs + off];
+        aw[I][r] = dg_out[kofs + off];
+        if constexpr (VEC_B) adb[I][r] = db32[kofs + off];
+        else fbrow[I][r] = 0.f;
+      }
+  } else {
 #pragma unroll
   for (int I = 0; I < 4; ++I) {
     float gtop = 1.f, gdec = 1.f;
@@ -491,6 +541,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
       else fbrow[I][r] = keb;
     }
   }
+  }   // !INTRA: phase 4
 
   // ---------------- phase 5: matrix intra as K=16 MFMAs per 16-row sub-block ----------------
   // B operands (shared by every output block): kE = k EB, qE = q ET, bkE = b k ET,
@@ -646,6 +697,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   }
 
   // ---------------- phase 6: last-row state terms, reverse cumsum, stores ----------------
+  if constexpr (!INTRA) {
   colkdk = sum_lane_groups(colkdk);            // sum over the 64 rows of k dks (this column)
   if constexpr (GATE == CG_VECTOR) {
     const float term = fast_exp2(gl) * dgk + colkdk;
@@ -683,10 +735,23 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     term = sum_row16(term);
     if (l == 0) atomicAdd(&sDg[C - 1], term);
   }
+  }   // !INTRA: phase 6
 
   // stores of dq, dk (bf16), the vector dg (fp32) and db (bf16); 32-bit offsets
   // from uniform per-chunk-head bases
-  {
+  if constexpr (INTRA) {
+    const int rsk32 = H * KD;
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int off = (16 * I + 4 * lg + r) * rsk32 + kk;
+        dq32[kofs + off] = aq[I][r];
+        dk32[kofs + off] = ak[I][r];
+        dg_out[kofs + off] = aw[I][r];
+        if constexpr (VEC_B) db32[kofs + off] = adb[I][r];
+      }
+  } else {
     bf16* dqb = dq_out + kofs;
     bf16* dkb = dk_out + kofs;
     float* dgb = dg_out + kofs;
@@ -705,7 +770,14 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     }
   }
   __syncthreads();   // sDbB, sDg complete
-  if (tid < C) {
+  if (INTRA && tid < C) {
+    // endpoint_intra.py:190-194: every row, or only |beta| < 1e-6 rows when the
+    // residual producer already accounted for the rest (beta_complete)
+    if constexpr (!VEC_B) {
+      const size_t row = (tok0 + tid) * H + h;
+      if (!beta_complete || fabsf(sBeta[tid]) < 1e-6f) dbeta_out[row] += sDbB[tid];
+    }
+  } else if (tid < C) {
     const size_t row = (tok0 + tid) * H + h;
     if constexpr (!VEC_B) {
       const float be = sBeta[tid];
@@ -717,6 +789,32 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
       dg_out[row] = acc;
     }
   }
+}
+
+template <int GATE, bool VEC_B>
+__global__ __launch_bounds__(512) void chunk_bwd_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
+    const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
+    const bf16* __restrict__ wgate, const float* __restrict__ akk, const bf16* __restrict__ hst,
+    const bf16* __restrict__ dhst, bf16* __restrict__ dq_out, bf16* __restrict__ dk_out,
+    bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
+    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale) {
+  chunk_body<GATE, VEC_B, false>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
+                                 dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale, nullptr,
+                                 nullptr, nullptr, nullptr, 0);
+}
+
+template <bool VEC_B>
+__global__ __launch_bounds__(512) void matrix_intra_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ g,
+    const float* __restrict__ beta, const bf16* __restrict__ bgate, const float* __restrict__ daqk,
+    const float* __restrict__ dakk, float* __restrict__ dq, float* __restrict__ dk,
+    float* __restrict__ db, float* __restrict__ dg, int T, int H, int beta_complete) {
+  chunk_body<CG_VECTOR, VEC_B, true>(q, k, nullptr, nullptr, nullptr, nullptr, g, beta, bgate, nullptr, dakk,
+                                     nullptr, nullptr, nullptr, nullptr, nullptr, dg, VEC_B ? nullptr : db,
+                                     nullptr, nullptr, T, H, 1.f, daqk, dq, dk, VEC_B ? db : nullptr,
+                                     beta_complete);
 }
 
 template <int GATE, bool VEC_B>
@@ -772,4 +870,33 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
     default: return hipErrorInvalidValue;
   }
 #undef FDR_POST
+}
+
+template <bool VEC_B>
+static hipError_t launch_intra(const void* q, const void* k, const float* g, const float* beta,
+                               const void* bgate, const float* daqk, const float* dakk, float* dq,
+                               float* dk, float* db, float* dg, int B, int T, int H, int beta_complete,
+                               hipStream_t s) {
+  using LY = PostLayout<CG_VECTOR, VEC_B, true>;
+  auto kern = matrix_intra_kernel<VEC_B>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LY::BYTES);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k, g,
+                     beta, (const bf16*)bgate, daqk, dakk, dq, dk, db, dg, T, H, beta_complete);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t fdr_matrix_intra(const void* q, const void* k, const float* g, const float* beta,
+                                       const void* b_gate, const float* dAqk, const float* dAkk, float* dq,
+                                       float* dk, float* db, float* dg, int B, int T, int H, int K,
+                                       int chunk, int beta_complete, hipStream_t stream) {
+  if (K != KD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  if (!q || !k || !g || !dAqk || !dAkk || !dq || !dk || !db || !dg) return hipErrorInvalidValue;
+  if (b_gate) return launch_intra<true>(q, k, g, nullptr, b_gate, dAqk, dAkk, dq, dk, db, dg, B, T, H, 0, stream);
+  if (!beta) return hipErrorInvalidValue;
+  return launch_intra<false>(q, k, g, beta, nullptr, dAqk, dAkk, dq, dk, db, dg, B, T, H, beta_complete, stream);
 }

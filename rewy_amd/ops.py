@@ -197,3 +197,30 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0):
                                K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_h")
     return h, vnew, ht
+
+
+def matrix_intra(q, k, g, dAqk, dAkk, dq, dk, db, dg, beta=None, b=None, beta_complete=False):
+    """Matrix intra VJP added in place into fp32 (dq, dk, db, dg); returns them."""
+    B, T, H, K = _dims(q)
+    dev = q.device
+    bf, f32 = torch.bfloat16, torch.float32
+    _need(q, "q", bf, (B, T, H, K), dev)
+    _need(k, "k", bf, (B, T, H, K), dev)
+    _need(g, "g", f32, (B, T, H, K), dev)
+    _need(dAqk, "dAqk", f32, (B, T, H, CHUNK), dev)
+    _need(dAkk, "dAkk", f32, (B, T, H, CHUNK), dev)
+    for x, n in ((dq, "dq"), (dk, "dk"), (dg, "dg")):
+        _need(x, n, f32, (B, T, H, K), dev)
+    if (beta is None) == (b is None):
+        raise ValueError("exactly one of beta (scalar) / b (vector erase gate) is required")
+    if b is not None:
+        _need(b, "b", bf, (B, T, H, K), dev)
+        _need(db, "db", f32, (B, T, H, K), dev)
+    else:
+        _need(beta, "beta", f32, (B, T, H), dev)
+        _need(db, "db", f32, (B, T, H), dev)
+    P = _lib.ptr
+    st = _lib.load().fdr_matrix_intra(P(q), P(k), P(g), P(beta), P(b), P(dAqk), P(dAkk), P(dq), P(dk), P(db),
+                                      P(dg), B, T, H, K, CHUNK, int(bool(beta_complete)), _lib.stream_handle(dev))
+    _lib.check(st, "fdr_matrix_intra")
+    return dq, dk, db, dg

@@ -39,6 +39,11 @@ def test_entry_points_reject_unsupported_shapes_without_touching_the_gpu():
     # null pointers with a valid shape
     st = lib.fdr_chunk_bwd(*([None] * 7), 2, *([None] * 13), 1, 128, 1, 128, 128, 64, 1.0, None)
     assert st == HIP_ERROR_INVALID_VALUE
+    # matrix intra: chunk 32, then null operands
+    st = lib.fdr_matrix_intra(*([None] * 11), 1, 128, 1, 128, 32, 0, None)
+    assert st == HIP_ERROR_INVALID_VALUE
+    st = lib.fdr_matrix_intra(*([None] * 11), 1, 128, 1, 128, 64, 0, None)
+    assert st == HIP_ERROR_INVALID_VALUE
 
 
 def test_host_wrappers_validate_before_launch():
