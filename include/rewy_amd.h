@@ -121,6 +121,31 @@ hipError_t fdr_matrix_intra(const void* q, const void* k, const float* g, const 
                             float* dk, float* db, float* dg, int B, int T, int H, int K, int chunk,
                             int beta_complete, hipStream_t stream);
 
+/*
+ * Forward, chunk-parallel part 1: gate cumsum and the intra-chunk matrices.
+ * Replaces, per chunk-head, FLA's chunk_local_cumsum(g, scale=RCP_LN2) and the
+ * chunk_<op>_fwd_intra + solve_tril pair inside chunk_kda_fwd / chunk_gdn2_fwd /
+ * chunk_gated_delta_rule_fwd / chunk_delta_rule_fwd (reference _compat/kda.py:89-113,
+ * _compat/gdn.py:33-123, _compat/gdn2.py:87-108):
+ *   gc  = chunk-local cumsum(g) / ln 2            fp32, g's shape (g = raw natural-log decay)
+ *   Aqk = scale tril(q k^T 2^(g_i - g_s))          fp32 [B,T,H,64]
+ *   Akk = (I + strict_tril((b k) k^T 2^(g_i - g_s)))^-1   fp32 [B,T,H,64]
+ * b is beta (fp32 [B,T,H]) or GDN2's erase gate b_gate (bf16 [B,T,H,K]); gate_mode as above
+ * (g and gc null for gate_mode 0).
+ */
+hipError_t fdr_fwd_prepare(const void* q, const void* k, const float* g, int gate_mode,
+                           const float* beta, const void* b_gate, float* gc, float* Aqk, float* Akk,
+                           int B, int T, int H, int K, int chunk, float scale, hipStream_t stream);
+
+/*
+ * Forward, chunk-parallel part 2: the output.  Replaces FLA's chunk_fwd_o:
+ *   o_c = scale (q_c 2^gc_c) h_c + Aqk_c v_new_c      bf16 [B,T,H,V]
+ * with h (bf16 [B,T/64,H,K,V]) and v_new from fdr_fwd_h and Aqk from fdr_fwd_prepare.
+ */
+hipError_t fdr_fwd_o(const void* q, const float* gc, int gate_mode, const float* Aqk, const void* h,
+                     const void* v_new, void* o, int B, int T, int H, int K, int V, int chunk,
+                     float scale, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,7 +1,8 @@
 """Autograd contract and public ``chunk_*`` operators for both backends.
 
-One autograd Function serves the four families.  Its forward is this
-package's chunked forward (``rewy_amd.forward``) and saves FLA's tensor list
+One autograd Function serves the four families.  Its forward is the HIP
+forward (``rewy_amd.hip_forward``) for the optimized backend on a GPU and the
+PyTorch restatement (``rewy_amd.forward``) otherwise; it saves FLA's tensor list
 (reference ``_compat/kda.py:120-144``: q, k, v, g_cumsum, beta, Aqk, Akk and,
 under full saving, w, u, qg, kg, v_new, h).  Its backward is chosen when the
 forward runs and stays bound to the Function afterwards (reference
@@ -32,9 +33,15 @@ class ChunkFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w,
                 initial_state):
-        o, final, sv = chunk_forward(op, q, k, v, g=g, beta=beta, b=b, w=w,
-                                     initial_state=initial_state, scale=scale,
-                                     output_final_state=output_final_state)
+        if backend == "optimized" and q.is_cuda:
+            from ..hip_forward import chunk_forward_hip
+            o, final, sv = chunk_forward_hip(op, q, k, v, g=g, beta=beta, b=b, w=w,
+                                             initial_state=initial_state, scale=scale,
+                                             output_final_state=output_final_state)
+        else:
+            o, final, sv = chunk_forward(op, q, k, v, g=g, beta=beta, b=b, w=w,
+                                         initial_state=initial_state, scale=scale,
+                                         output_final_state=output_final_state)
         keep = full_saving and op in ("kda", "gdn2")
         ctx.save_for_backward(q, k, v, sv["gc"], beta, b, w, sv["Aqk"], sv["Akk"], initial_state,
                               *(sv[n] if keep else None for n in ("w", "u", "qg", "kg", "v_new", "h")))

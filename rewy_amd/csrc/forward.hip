@@ -1,0 +1,427 @@
+// Chunk-parallel pieces of the delta-rule forward.
+//
+// Replace, per chunk-head, the parts of FLA's chunk_kda_fwd / chunk_gdn2_fwd /
+// chunk_gated_delta_rule_fwd / chunk_delta_rule_fwd (reference
+// _compat/kda.py:89-113, _compat/gdn.py:33-123, _compat/gdn2.py:87-108) that
+// are not the state scan:
+//
+//   fdr_fwd_prepare (one work-group per chunk-head):
+//     gc  = chunk-local cumsum of the raw (natural-log) gate, times 1/ln 2   (FLA chunk_local_cumsum)
+//     Aqk = scale tril(q k^T 2^(g_i - g_s))                                 (diagonal included)
+//     Akk = (I + strict_tril((b k) k^T 2^(g_i - g_s)))^-1                  (FLA chunk_*_fwd_intra + solve_tril)
+//   fdr_fwd_o (one work-group per chunk-head):
+//     o   = scale (q 2^g) h_c + Aqk v_new                                   (FLA chunk_fwd_o)
+//
+// The state scan between them is fdr_fwd_h and the WY factors are
+// fdr_prepare_wu (recompute.hip).
+//
+// Gate products.  For rows i of 16-row block I and rows s of block J <= I the
+// per-channel factor 2^(g_i - g_s) is split at the anchor n = 16 I (the first
+// row of block I): q 2^(g_i - g_n) <= 1 and k 2^(g_n - g_s) (<= 1 for J < I),
+// both split into bf16 hi + lo so each 16 x 16 tile is three MFMAs per 32-wide
+// slice of K (fp32-faithful).  A diagonal block whose gate span reaches 100 in
+// log2 units (where the k-side factor could overflow) is evaluated pairwise in
+// fp32 instead.
+#include "common.hpp"
+
+namespace rewy {
+
+enum GateModeF { FG_NONE = 0, FG_SCALAR = 1, FG_VECTOR = 2 };
+
+namespace fwd {
+constexpr int LDK = KD + 8;     // bf16 pitch of the q, k, b rows
+constexpr int LDG = KD + 4;     // fp32 pitch of the gate rows
+constexpr int LDM = C + 4;      // fp32 pitch of the 64 x 64 matrices
+constexpr float RCP_LN2 = 1.4426950408889634f;
+constexpr float WIDE = 100.f;   // diagonal-block gate span that takes the pairwise path
+}  // namespace fwd
+
+template <int GATE, bool VEC_B>
+__global__ __launch_bounds__(512) void fwd_prepare_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ graw,
+    const float* __restrict__ beta, const bf16* __restrict__ bgate, float* __restrict__ gc_out,
+    float* __restrict__ aqk_out, float* __restrict__ akk_out, int T, int H, float scale) {
+  using fwd::LDG;
+  using fwd::LDK;
+  using fwd::LDM;
+  __shared__ __attribute__((aligned(16))) bf16 sq[C][LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sk[C][LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sb[VEC_B ? C : 1][LDK];
+  __shared__ __attribute__((aligned(16))) float sg[GATE == FG_VECTOR ? C : 1][LDG];
+  __shared__ float sgs[C];        // scalar gate (log2 cumsum) per row
+  __shared__ float sbeta[C];
+  __shared__ float sM[C][LDM];    // strict_tril(b k k^T 2^(g_i-g_s)), then the inverse
+  __shared__ float sX[C][LDM];    // (I + M)^-1
+  __shared__ int sWide[4];        // diagonal block I takes the pairwise path
+
+  const int blk = blockIdx.x;
+  const int NT = T / C;
+  const int c = blk % NT;
+  const int bh = blk / NT;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
+  const int lc = l & 15, lg = l >> 4;
+  const size_t tok0 = (size_t)b * T + (size_t)c * C;
+  const size_t rsk = (size_t)H * KD;
+  const size_t kofs = tok0 * rsk + (size_t)h * KD;
+  const size_t mofs = (tok0 * H + h) * C;      // [t][64] matrices of this chunk-head
+  const size_t rsm = (size_t)H * C;
+
+  // ---- stage q, k (, b) rows; gate cumsum ----
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = tid + 512 * i;
+    const int t = p >> 4, c8 = (p & 15) * 8;
+    *reinterpret_cast<u32x4*>(&sq[t][c8]) = *reinterpret_cast<const u32x4*>(q + kofs + (size_t)t * rsk + c8);
+    *reinterpret_cast<u32x4*>(&sk[t][c8]) = *reinterpret_cast<const u32x4*>(k + kofs + (size_t)t * rsk + c8);
+    if constexpr (VEC_B)
+      *reinterpret_cast<u32x4*>(&sb[t][c8]) = *reinterpret_cast<const u32x4*>(bgate + kofs + (size_t)t * rsk + c8);
+  }
+  if constexpr (!VEC_B) {
+    if (tid < C) sbeta[tid] = beta[(tok0 + tid) * H + h];
+  }
+  if constexpr (GATE == FG_VECTOR) {
+    // four threads per channel, 16 rows each: local sums, then the carries
+    const int col = tid & 127, part = tid >> 7;
+    float v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = graw[kofs + (size_t)(16 * part + r) * rsk + col];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) v[r] += v[r - 1];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sg[16 * part + r][col] = v[r];
+    __syncthreads();
+    float carry = 0.f;
+    for (int pp = 0; pp < part; ++pp) carry += sg[16 * pp + 15][col];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float x = (v[r] + carry) * fwd::RCP_LN2;
+      sg[16 * part + r][col] = x;
+      gc_out[kofs + (size_t)(16 * part + r) * rsk + col] = x;
+    }
+  } else if constexpr (GATE == FG_SCALAR) {
+    if (wv == 0) {
+      float x = graw[(tok0 + l) * H + h];
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float y = __shfl_up(x, d);
+        if (l >= d) x += y;
+      }
+      x *= fwd::RCP_LN2;
+      sgs[l] = x;
+      gc_out[(tok0 + l) * H + h] = x;
+    }
+  }
+  __syncthreads();
+
+  auto gate = [&](int t, int kc) -> float {
+    if constexpr (GATE == FG_VECTOR) return sg[t][kc];
+    else if constexpr (GATE == FG_SCALAR) return sgs[t];
+    else return 0.f;
+  };
+
+  // ---- wide diagonal blocks: gate span (over any channel) >= WIDE; one wave per block ----
+  // (the gates are cumsums of log decays, so a block's span is first row - last row)
+  if (wv < 4) {
+    const int I = wv;
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = l + 64 * j;
+      m = fmaxf(m, gate(16 * I, col) - gate(16 * I + 15, col));
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+    if (l == 0) sWide[I] = m >= fwd::WIDE;
+  }
+  __syncthreads();
+
+  // ---- 16 x 16 tiles (I, J), J <= I: Aqk and M by anchored MFMAs ----
+  // tile list: (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0) (3,1) (3,2) (3,3); wave w: tiles w, w + 8
+  for (int tix = wv; tix < 10; tix += 8) {
+    const int I = tix < 1 ? 0 : tix < 3 ? 1 : tix < 6 ? 2 : 3;
+    const int J = tix - (I * (I + 1)) / 2;
+    const bool pairwise = (J == I) && sWide[I];
+    const int n = 16 * I;                       // anchor row
+    f32x4 aqk = zero4(), mkk = zero4();
+    if (!pairwise) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int k0 = 32 * ks + 8 * lg;
+        const int ia = 16 * I + lc;             // A rows (i)
+        const int sb_ = 16 * J + lc;            // B columns (s)
+        bf16x8 qh, ql, bh_, bl, kh, kl;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int kc = k0 + j;
+          const float fa = fast_exp2(gate(ia, kc) - gate(n, kc));     // <= 1
+          const float fb = fast_exp2(gate(n, kc) - gate(sb_, kc));    // <= 1 off the diagonal
+          const float kia = to_f32(sk[ia][kc]);
+          const float bia = VEC_B ? to_f32(sb[ia][kc]) : sbeta[ia];
+          bf16 hh, ll;
+          split_bf16(to_f32(sq[ia][kc]) * fa, hh, ll);
+          qh[j] = hh;
+          ql[j] = ll;
+          split_bf16(bia * kia * fa, hh, ll);
+          bh_[j] = hh;
+          bl[j] = ll;
+          split_bf16(to_f32(sk[sb_][kc]) * fb, hh, ll);
+          kh[j] = hh;
+          kl[j] = ll;
+        }
+        aqk = mfma(qh, kh, aqk);
+        aqk = mfma(qh, kl, aqk);
+        aqk = mfma(ql, kh, aqk);
+        mkk = mfma(bh_, kh, mkk);
+        mkk = mfma(bh_, kl, mkk);
+        mkk = mfma(bl, kh, mkk);
+      }
+    } else {
+      // exact pairwise diagonal: lane (lg, lc) owns rows 16 I + 4 lg + r, column s = 16 I + lc
+      const int s = 16 * J + lc;
+#pragma unroll 1
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * I + 4 * lg + r;
+        float a = 0.f, m = 0.f;
+        if (s <= i) {
+#pragma unroll 4
+          for (int kc = 0; kc < KD; ++kc) {
+            const float f = fast_exp2(gate(i, kc) - gate(s, kc));
+            const float ks_ = to_f32(sk[s][kc]);
+            a += to_f32(sq[i][kc]) * ks_ * f;
+            const float bi = VEC_B ? to_f32(sb[i][kc]) : sbeta[i];
+            m += bi * to_f32(sk[i][kc]) * ks_ * f;
+          }
+        }
+        aqk[r] = a;
+        mkk[r] = m;
+      }
+    }
+    // lane: rows i = 16 I + 4 lg + r, column s = 16 J + lc
+    const int s = 16 * J + lc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * I + 4 * lg + r;
+      aqk_out[mofs + (size_t)i * rsm + s] = (s <= i) ? scale * aqk[r] : 0.f;
+      sM[i][s] = (s < i) ? mkk[r] : 0.f;
+    }
+  }
+  // zero upper tiles of Aqk and M (J > I)
+  for (int p = tid; p < 6 * 256; p += 512) {
+    const int tix = p >> 8, e = p & 255;
+    const int I = tix < 3 ? 0 : tix < 5 ? 1 : 2;
+    const int J = I + 1 + (tix - (I == 0 ? 0 : I == 1 ? 3 : 5));
+    const int i = 16 * I + (e >> 4), s = 16 * J + (e & 15);
+    aqk_out[mofs + (size_t)i * rsm + s] = 0.f;
+    sM[i][s] = 0.f;
+  }
+  __syncthreads();
+
+  // ---- inverse of the unit lower-triangular I + M (fp32) ----
+  // diagonal 16 x 16 blocks by forward substitution: wave 0, lane = (block, column)
+  if (wv == 0) {
+    const int B4 = lg, j = lc, base = 16 * B4;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float acc = (i == j) ? 1.f : 0.f;
+#pragma unroll
+      for (int m = 0; m < i; ++m) acc -= sM[base + i][base + m] * x[m];
+      x[i] = acc;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sX[base + i][base + j] = x[i];
+  }
+  // zero the strictly upper blocks of the inverse
+  for (int p = tid; p < 6 * 256; p += 512) {
+    const int tix = p >> 8, e = p & 255;
+    const int I = tix < 3 ? 0 : tix < 5 ? 1 : 2;
+    const int J = I + 1 + (tix - (I == 0 ? 0 : I == 1 ? 3 : 5));
+    sX[16 * I + (e >> 4)][16 * J + (e & 15)] = 0.f;
+  }
+  __syncthreads();
+  // block rows I = 1..3: X_IJ = -X_II sum_{m = J}^{I-1} M_Im X_mJ, one wave per block
+  for (int I = 1; I < 4; ++I) {
+    if (wv < I) {
+      const int J = wv;
+      // lane: rows 16 I + (l >> 2), columns 16 J + 4 (l & 3) .. + 3
+      const int ri = l >> 2, cj = 4 * (l & 3);
+      float tacc[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int m = 16 * J; m < 16 * I; ++m) {
+        const float mv = sM[16 * I + ri][m];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tacc[e] += mv * sX[m][16 * J + cj + e];
+      }
+      // X_IJ[r][c] = -sum_t X_II[r][t] T[t][c], with T exchanged between lanes
+      float xo[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        // T[t][cj + e] lives in lane (4 t + (l & 3))
+        float tv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tv[e] = __shfl(tacc[e], 4 * t + (l & 3));
+        const float xi = sX[16 * I + ri][16 * I + t];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xo[e] -= xi * tv[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sX[16 * I + ri][16 * J + cj + e] = xo[e];
+    }
+    __syncthreads();
+  }
+  // ---- Akk rows -> HBM ----
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = tid + 512 * i;
+    const int t = p >> 4, c4 = (p & 15) * 4;
+    *reinterpret_cast<f32x4*>(akk_out + mofs + (size_t)t * rsm + c4) =
+        f32x4{sX[t][c4], sX[t][c4 + 1], sX[t][c4 + 2], sX[t][c4 + 3]};
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// fdr_fwd_o:  o = scale (q 2^g) h_c + Aqk v_new
+// ------------------------------------------------------------------------------------------
+template <int GATE>
+__global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, const float* __restrict__ gc,
+                                                     const float* __restrict__ aqk, const bf16* __restrict__ hst,
+                                                     const bf16* __restrict__ vnew, bf16* __restrict__ o_out,
+                                                     int T, int H, float scale) {
+  using fwd::LDK;
+  __shared__ __attribute__((aligned(16))) bf16 sqg[C][LDK];       // scale q 2^g rows, hi
+  __shared__ __attribute__((aligned(16))) bf16 sqgl[C][LDK];      // lo
+  __shared__ __attribute__((aligned(16))) bf16 sah[C][C + 8];     // Aqk rows [i][s], hi
+  __shared__ __attribute__((aligned(16))) bf16 sal[C][C + 8];     // lo
+  __shared__ __attribute__((aligned(16))) bf16 sv[C * VD];        // v_new rows (swizzled)
+  __shared__ __attribute__((aligned(16))) bf16 shT[C * KD];       // 64 rows of h [k][v] (swizzled)
+  // (q h) contracts over K = the rows of h, read transposed; h is staged in two halves.
+  const int blk = blockIdx.x;
+  const int NT = T / C;
+  const int c = blk % NT;
+  const int bh = blk / NT;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
+  const int lc = l & 15, lg = l >> 4;
+  const size_t tok0 = (size_t)b * T + (size_t)c * C;
+  const size_t rsk = (size_t)H * KD;
+  const size_t kofs = tok0 * rsk + (size_t)h * KD;
+  const size_t mofs = (tok0 * H + h) * C;
+  const size_t rsm = (size_t)H * C;
+  const size_t hoff = (((size_t)b * NT + c) * H + h) * KD * VD;
+
+  // stage scale * q 2^g (hi/lo), Aqk (hi/lo), v_new
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = tid + 512 * i;
+    const int t = p >> 4, c8 = (p & 15) * 8;
+    const bf16x8 qx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(q + kofs + (size_t)t * rsk + c8));
+    bf16x8 hi, lo;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float f = scale;
+      if constexpr (GATE == FG_VECTOR) f *= fast_exp2(gc[kofs + (size_t)t * rsk + c8 + j]);
+      else if constexpr (GATE == FG_SCALAR) f *= fast_exp2(gc[(tok0 + t) * H + h]);
+      bf16 hh, ll;
+      split_bf16(to_f32(qx[j]) * f, hh, ll);
+      hi[j] = hh;
+      lo[j] = ll;
+    }
+    *reinterpret_cast<bf16x8*>(&sqg[t][c8]) = hi;
+    *reinterpret_cast<bf16x8*>(&sqgl[t][c8]) = lo;
+    store_tr_chunk<16>(sv, t, p & 15, *reinterpret_cast<const u32x4*>(vnew + kofs + (size_t)t * rsk + c8));
+    const int c4 = (p & 15) * 4;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(aqk + mofs + (size_t)t * rsm + c4);
+    bf16x4 alo;
+    const bf16x4 ahi = split_hi4(a, alo);
+    *reinterpret_cast<bf16x4*>(&sah[t][c4]) = ahi;
+    *reinterpret_cast<bf16x4*>(&sal[t][c4]) = alo;
+  }
+  // wave w: output rows 16 (w & 3) .. +16, columns 64 (w >> 2) .. +64 (4 tiles)
+  const int I = wv & 3, cb = 64 * (wv >> 2);
+  f32x4 acc[4] = {zero4(), zero4(), zero4(), zero4()};
+  for (int half = 0; half < 2; ++half) {
+    __syncthreads();
+    // h rows [64 half .. 64 half + 64)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + 512 * i;
+      const int r = p >> 4, c8 = (p & 15) * 8;
+      store_tr_chunk<16>(shT, r, p & 15, *reinterpret_cast<const u32x4*>(hst + hoff + (size_t)(64 * half + r) * VD + c8));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const bf16x8 ah = frag(&sqg[16 * I][64 * half + 32 * ks], LDK);
+      const bf16x8 al = frag(&sqgl[16 * I][64 * half + 32 * ks], LDK);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const bf16x8 bh_ = frag_tr<16>(shT, 32 * ks, cb + 16 * ct);   // h rows over K, columns v
+        acc[ct] = mfma(ah, bh_, acc[ct]);
+        acc[ct] = mfma(al, bh_, acc[ct]);
+      }
+    }
+  }
+  // Aqk v_new: A = Aqk rows i (s-contiguous), B = v_new rows read transposed
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const bf16x8 ah = frag(&sah[16 * I][32 * ks], C + 8);
+    const bf16x8 al = frag(&sal[16 * I][32 * ks], C + 8);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const bf16x8 bv = frag_tr<16>(sv, 32 * ks, cb + 16 * ct);
+      acc[ct] = mfma(ah, bv, acc[ct]);
+      acc[ct] = mfma(al, bv, acc[ct]);
+    }
+  }
+  // lane: rows 16 I + 4 lg + r, column cb + 16 ct + lc
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      o_out[kofs + (size_t)(16 * I + 4 * lg + r) * rsk + cb + 16 * ct + lc] = to_bf16(acc[ct][r]);
+}
+
+}  // namespace rewy
+
+using namespace rewy;
+
+extern "C" hipError_t fdr_fwd_prepare(const void* q, const void* k, const float* g, int gate_mode,
+                                      const float* beta, const void* b_gate, float* gc, float* Aqk, float* Akk,
+                                      int B, int T, int H, int K, int chunk, float scale, hipStream_t stream) {
+  if (K != KD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  if (!q || !k || !Aqk || !Akk) return hipErrorInvalidValue;
+  if (gate_mode != FG_NONE && (!g || !gc)) return hipErrorInvalidValue;
+  const bool vec_b = b_gate != nullptr;
+  if (vec_b && gate_mode != FG_VECTOR) return hipErrorInvalidValue;
+  if (!vec_b && !beta) return hipErrorInvalidValue;
+  const dim3 grid(B * H * (T / C)), block(512);
+#define FDR_PREP(G, VB)                                                                              \
+  hipLaunchKernelGGL((fwd_prepare_kernel<G, VB>), grid, block, 0, stream, (const bf16*)q, (const bf16*)k, \
+                     g, beta, (const bf16*)b_gate, gc, Aqk, Akk, T, H, scale)
+  if (vec_b) FDR_PREP(FG_VECTOR, true);
+  else if (gate_mode == FG_VECTOR) FDR_PREP(FG_VECTOR, false);
+  else if (gate_mode == FG_SCALAR) FDR_PREP(FG_SCALAR, false);
+  else if (gate_mode == FG_NONE) FDR_PREP(FG_NONE, false);
+  else return hipErrorInvalidValue;
+#undef FDR_PREP
+  return hipGetLastError();
+}
+
+extern "C" hipError_t fdr_fwd_o(const void* q, const float* gc, int gate_mode, const float* Aqk, const void* h,
+                                const void* v_new, void* o, int B, int T, int H, int K, int V, int chunk,
+                                float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  if (!q || !Aqk || !h || !v_new || !o) return hipErrorInvalidValue;
+  if (gate_mode != FG_NONE && !gc) return hipErrorInvalidValue;
+  const dim3 grid(B * H * (T / C)), block(512);
+#define FDR_O(G)                                                                                       \
+  hipLaunchKernelGGL((fwd_o_kernel<G>), grid, block, 0, stream, (const bf16*)q, gc, Aqk, (const bf16*)h, \
+                     (const bf16*)v_new, (bf16*)o, T, H, scale)
+  if (gate_mode == FG_VECTOR) FDR_O(FG_VECTOR);
+  else if (gate_mode == FG_SCALAR) FDR_O(FG_SCALAR);
+  else if (gate_mode == FG_NONE) FDR_O(FG_NONE);
+  else return hipErrorInvalidValue;
+#undef FDR_O
+  return hipGetLastError();
+}

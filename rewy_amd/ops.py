@@ -224,3 +224,56 @@ def matrix_intra(q, k, g, dAqk, dAkk, dq, dk, db, dg, beta=None, b=None, beta_co
                                       P(dg), B, T, H, K, CHUNK, int(bool(beta_complete)), _lib.stream_handle(dev))
     _lib.check(st, "fdr_matrix_intra")
     return dq, dk, db, dg
+
+
+def fwd_prepare(q, k, g, gate_mode, beta=None, b=None, scale=1.0):
+    """Forward intra matrices.  Returns (gc fp32 | None, Aqk fp32, Akk fp32)."""
+    B, T, H, K = _dims(q)
+    dev = q.device
+    bf, f32 = torch.bfloat16, torch.float32
+    _need(q, "q", bf, (B, T, H, K), dev)
+    _need(k, "k", bf, (B, T, H, K), dev)
+    if gate_mode == GATE_VECTOR:
+        _need(g, "g", f32, (B, T, H, K), dev)
+    elif gate_mode == GATE_SCALAR:
+        _need(g, "g", f32, (B, T, H), dev)
+    elif gate_mode != GATE_NONE:
+        raise ValueError("gate_mode must be 0, 1 or 2")
+    if b is not None:
+        if gate_mode != GATE_VECTOR:
+            raise ValueError("a vector erase gate needs a vector decay gate")
+        _need(b, "b", bf, (B, T, H, K), dev)
+    else:
+        _need(beta, "beta", f32, (B, T, H), dev)
+    gc = torch.empty_like(g) if gate_mode != GATE_NONE else None
+    Aqk = torch.empty(B, T, H, CHUNK, device=dev, dtype=f32)
+    Akk = torch.empty(B, T, H, CHUNK, device=dev, dtype=f32)
+    P = _lib.ptr
+    st = _lib.load().fdr_fwd_prepare(P(q), P(k), P(g), int(gate_mode), P(beta), P(b), P(gc), P(Aqk), P(Akk),
+                                     B, T, H, K, CHUNK, float(scale), _lib.stream_handle(dev))
+    _lib.check(st, "fdr_fwd_prepare")
+    return gc, Aqk, Akk
+
+
+def fwd_o(q, gc, gate_mode, Aqk, h, v_new, scale):
+    """Forward output o = scale (q 2^gc) h + Aqk v_new (bf16)."""
+    B, T, H, K = _dims(q)
+    V = V_SUPPORTED
+    dev = q.device
+    bf, f32 = torch.bfloat16, torch.float32
+    _need(q, "q", bf, (B, T, H, K), dev)
+    if gate_mode == GATE_VECTOR:
+        _need(gc, "gc", f32, (B, T, H, K), dev)
+    elif gate_mode == GATE_SCALAR:
+        _need(gc, "gc", f32, (B, T, H), dev)
+    elif gate_mode != GATE_NONE:
+        raise ValueError("gate_mode must be 0, 1 or 2")
+    _need(Aqk, "Aqk", f32, (B, T, H, CHUNK), dev)
+    _need(h, "h", bf, (B, T // CHUNK, H, K, V), dev)
+    _need(v_new, "v_new", bf, (B, T, H, V), dev)
+    o = torch.empty(B, T, H, V, device=dev, dtype=bf)
+    P = _lib.ptr
+    st = _lib.load().fdr_fwd_o(P(q), P(gc), int(gate_mode), P(Aqk), P(h), P(v_new), P(o), B, T, H, K, V, CHUNK,
+                               float(scale), _lib.stream_handle(dev))
+    _lib.check(st, "fdr_fwd_o")
+    return o
