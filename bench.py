@@ -105,16 +105,20 @@ def make_inputs(cfg, device):
 
 
 def setup(cfg, device):
-    """Forward once (untimed).  Returns (xs, dO, saved, step, per-kernel launchers)."""
+    """Forward once (untimed, the HIP forward).  Returns (xs, dO, saved, step,
+    per-kernel launchers, backward intermediates, forward callable)."""
     import torch
     from rewy_amd import ops
     from rewy_amd.backends import backward as bw
-    from rewy_amd.forward import chunk_forward
+    from rewy_amd.hip_forward import chunk_forward_hip
     xs, dO = make_inputs(cfg, device)
     op = cfg["op"]
-    with torch.no_grad():
-        _, _, sv = chunk_forward(op, xs["q"], xs["k"], xs["v"], g=xs.get("g"), beta=xs.get("beta"),
+
+    def forward():
+        return chunk_forward_hip(op, xs["q"], xs["k"], xs["v"], g=xs.get("g"), beta=xs.get("beta"),
                                  b=xs.get("b"), w=xs.get("w"), initial_state=xs["h0"])
+    with torch.no_grad():
+        _, _, sv = forward()
     torch.cuda.synchronize()
     scale = sv["scale"]
     keep = cfg["full_saving"]
@@ -160,7 +164,7 @@ def setup(cfg, device):
     dh, dR, _ = kern["fdr_state_bwd"]()
     kern["fdr_chunk_bwd"] = lambda: ops.chunk_bwd(xs["q"], xs["k"], xs["v"], v_new, dO, dR, g, gate, sv["Akk"], h,
                                                   dh, scale, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"))
-    return xs, dO, sv, step, kern, (dh, dR)
+    return xs, dO, sv, step, kern, (dh, dR), forward
 
 
 def time_steps(step, steps, warmup):
@@ -195,9 +199,10 @@ def time_kernels(kern, reps):
 
 
 def measure(cfg, steps, warmup):
-    xs, dO, sv, step, kern, inter = setup(cfg, "cuda")
+    xs, dO, sv, step, kern, inter, forward = setup(cfg, "cuda")
     NTt = cfg["B"] * cfg["H"] * (cfg["T"] // 64)
     ms = time_steps(step, steps, warmup)
+    fwd_ms = time_steps(forward, max(3, steps // 4), 1)
     kt = time_kernels(kern, max(5, steps))
     costs = kernel_costs(cfg["op"], cfg["full_saving"])
     kernels = {}
@@ -207,7 +212,7 @@ def measure(cfg, steps, warmup):
                           tflops=round(fl * NTt / (t * 1e-3) / 1e12, 2), bytes_per_launch=by * NTt)
     flops = sum(c[1] for c in costs.values()) * NTt
     return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9, kernels=kernels, NTt=NTt,
-                xs=xs, dO=dO, sv=sv, step=step, inter=inter)
+                xs=xs, dO=dO, sv=sv, step=step, inter=inter, fwd_ms=fwd_ms)
 
 
 def measured_traffic(kernel, config):
@@ -324,7 +329,7 @@ def main():
     if not args.no_cpu and args.config == "kda":
         cpu = cpu_baseline(xs, sv, dO, sv["scale"], NTt)
 
-    ms, tflops, kernels = res["ms"], res["tflops"], res["kernels"]
+    ms, tflops, kernels, res_fwd_ms = res["ms"], res["tflops"], res["kernels"], res["fwd_ms"]
     dom = max(kernels, key=lambda n: kernels[n]["ms"])
     achieved = kernels[dom]["gbs"]
     del res, xs, dO, sv
@@ -336,6 +341,7 @@ def main():
         secondary = {"gdn": {"workload": "gdn chunk backward (always recompute), B=8 T=4096 H=16 K=V=128",
                              "ms": round(g["ms"], 4), "tflops": round(g["tflops"], 2),
                              "mfma_peak_frac": round(g["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+                             "forward_hip_ms": round(g["fwd_ms"], 4),
                              "kernels": g["kernels"]}}
         del g
         torch.cuda.empty_cache()
@@ -363,6 +369,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(dom, args.config),
                      "algorithmic_bytes_per_launch": kernels[dom]["bytes_per_launch"]},
+        "forward_hip_ms": round(res_fwd_ms, 4),
         "original_torch_ms": None if t_orig is None else round(t_orig, 3),
         "speedup_vs_original_torch": None if t_orig is None else round(t_orig / ms, 2),
         "parity_vs_original": parity,
