@@ -132,12 +132,21 @@ def make_kda(backend):
                   state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None, cp_context=None,
                   use_graph=False, max_num_seqs=None, **kwargs):
         """Kimi Delta Attention (per-channel vector gate); reference _compat/kda.py:214."""
-        _unsupported("chunk_kda", use_gate_in_kernel=use_gate_in_kernel, safe_gate=safe_gate,
-                     return_intermediate_states=return_intermediate_states,
+        _unsupported("chunk_kda", return_intermediate_states=return_intermediate_states,
                      state_v_first=state_v_first, cu_seqlens=cu_seqlens is not None,
                      cp_context=cp_context is not None, use_graph=use_graph)
         if kwargs.get("chunk_size", 64) != 64:
             raise ValueError("`chunk_size` must be 64 for this build")
+        A_log = dt_bias = None
+        if use_gate_in_kernel:
+            A_log, dt_bias = kwargs.get("A_log"), kwargs.get("dt_bias")
+            if A_log is None and lower_bound is None:
+                raise ValueError("`A_log` must be provided when `use_gate_in_kernel=True` and `lower_bound` is not set.")
+        if safe_gate and use_gate_in_kernel:
+            if lower_bound is None:
+                raise ValueError("`lower_bound` must be specified when `safe_gate=True` and `use_gate_in_kernel=True`.")
+            if not (-5 <= lower_bound < 0):
+                raise ValueError(f"`lower_bound` must be in the safe range [-5, 0), got {lower_bound}.")
         if allow_neg_eigval and not use_beta_sigmoid_in_kernel:
             raise ValueError("`allow_neg_eigval=True` requires `use_beta_sigmoid_in_kernel=True`.")
         if initial_state is not None:
@@ -150,6 +159,11 @@ def make_kda(backend):
             q, k = _l2norm(q), _l2norm(k)
         if use_beta_sigmoid_in_kernel:
             beta = beta.sigmoid() * (2.0 if allow_neg_eigval else 1.0)
+        if use_gate_in_kernel:
+            # the fused activation as its own autograd node: g's gradient flows to
+            # g_raw, A_log and dt_bias (the reference's dA_log / ddt_bias outputs)
+            from ..gates import KDAGate
+            g = KDAGate.apply(g, A_log, dt_bias, lower_bound)
         scale = K ** -0.5 if scale is None else scale
         return _apply("kda", backend, disable_recompute, scale, output_final_state, q, k, v, g, beta,
                       None, None, initial_state)

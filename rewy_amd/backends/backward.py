@@ -30,7 +30,7 @@ def _check_common(kind, kw):
         raise NotImplementedError(f"{kind} HIP backward: state_v_first is not supported")
     if kw.get("chunk_size", 64) != 64:
         raise NotImplementedError(f"{kind} HIP backward: chunk_size must be 64")
-    if kw.get("use_gate_in_kernel", False):
+    if kw.get("use_gate_in_kernel", False) and kind != "kda":
         raise NotImplementedError(f"{kind} HIP backward: use_gate_in_kernel is not supported")
     if kw.get("safe_gate", False):
         raise NotImplementedError(f"{kind} HIP backward: safe_gate is not supported")
@@ -88,7 +88,12 @@ def kda_backward(q, k, v, beta, Aqk, Akk, scale, initial_state, do, dht, g, g_or
                        use_gate_in_kernel=use_gate_in_kernel, cp_context=cp_context,
                        use_graph=use_graph, chunk_offsets=chunk_offsets)
     record("kda", "optimized_backward")
-    return out["dq"], out["dk"], out["dv"], out["dbeta"], out["dg"], dh0, None, None
+    dg, dA_log, ddt_bias = out["dg"], None, None
+    if use_gate_in_kernel:
+        # g is the activated gate's cumsum; g_org the raw gate input (FLA convention)
+        from ..gates import kda_gate_bwd
+        dg, dA_log, ddt_bias = kda_gate_bwd(dg, g_org, A_log, dt_bias, lower_bound)
+    return out["dq"], out["dk"], out["dv"], out["dbeta"], dg, dh0, dA_log, ddt_bias
 
 
 def gdn2_backward(q, k, v, b, w_gate, Aqk, Akk, scale, initial_state, do, dht, g, g_org=None,

@@ -93,3 +93,35 @@ def test_rejection_and_visible_fallback():
     out.float().sum().backward()
     assert fdr.stats()["kda.fallback_forward"] == 1
     assert fdr.stats().get("kda.optimized_backward", 0) == 0
+
+
+@pytest.mark.parametrize("lower_bound", [None, -5.0])
+def test_kda_fused_gate_optimized_matches_original(lower_bound):
+    """use_gate_in_kernel=True (the gate activation feeding the HIP backward, dA_log /
+    ddt_bias through its explicit backward) against the original backend on the
+    same inputs; and the envelope: accepted for KDA, rejected for GDN / GDN2 with
+    the reference's reasons (runtime.py:97-98)."""
+    import rewy_amd as fdr
+    from rewy_amd.runtime import rejection_reason
+    print(f"\n[e2e] kda fused gate lower_bound={lower_bound}", flush=True)
+    xs, dO = make_inputs("kda", 2, 128, 2, seed=31)
+    gen = torch.Generator().manual_seed(5)
+    leaves = dict(g=torch.randn(2, 128, 2, 128, generator=gen), A_log=torch.randn(2, generator=gen) * 0.5,
+                  dt_bias=torch.randn(256, generator=gen) * 0.1)
+    dev = torch.device("cuda")
+    res = {}
+    for backend in ("optimized", "original"):
+        lv = {k: v.to(dev).requires_grad_() for k, v in leaves.items()}
+        with fdr.use_backend(backend, ops=("kda",)):
+            o, _ = fdr.chunk_kda(xs["q"].to(dev), xs["k"].to(dev), xs["v"].to(dev), lv["g"], xs["beta"].to(dev),
+                                 initial_state=xs["initial_state"].to(dev), use_gate_in_kernel=True,
+                                 A_log=lv["A_log"], dt_bias=lv["dt_bias"], lower_bound=lower_bound)
+        res[backend] = [x.detach().double().cpu().numpy() for x in torch.autograd.grad(o, list(lv.values()), dO.to(dev))]
+    for name, a, r in zip(leaves, res["optimized"], res["original"]):
+        e = O.error(r, a, 0.02)
+        print(name, e, flush=True)
+        assert e["passed"], (name, e)
+    q = xs["q"].to(dev)
+    assert rejection_reason("kda", dict(q=q, k=q, v=q, use_gate_in_kernel=True)) is None
+    assert rejection_reason("gdn", dict(q=q, k=q, v=q, use_gate_in_kernel=True)) == "GDN fused gate is not release-validated"
+    assert rejection_reason("gdn2", dict(q=q, k=q, v=q, use_gate_in_kernel=True)) == "GDN2 fused gate is not release-validated"
