@@ -113,15 +113,67 @@ def _pad_time(xs, T):
     return out, Tp
 
 
-def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0):
+def _run(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0):
     T = q.shape[1]
-    if backend == "original" and T % 64:
+    if T % 64:
         (q, k, v, g, beta, b, w), _ = _pad_time((q, k, v, g, beta, b, w), T)
         o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state,
                                        q, k, v, g, beta, b, w, h0)
         return o[:, :T], final
     return ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g,
                                beta, b, w, h0)
+
+
+def _unpack(x, bounds, Tp):
+    """Packed [1, T, ...] -> [N, Tp, ...], each sequence zero-padded to Tp."""
+    if x is None:
+        return None
+    rows = []
+    for s, e in bounds:
+        seq = x[:, s:e]
+        pad = [0, 0] * (x.ndim - 2) + [0, Tp - (e - s)]
+        rows.append(torch.nn.functional.pad(seq, pad))
+    return torch.cat(rows, 0)
+
+
+def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0,
+           state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None):
+    """Layout adapters around the chunk Function (all autograd-transparent torch ops):
+
+    * grouped value heads (HV = v.shape[2] > H): q and k are repeated over each
+      group of HV / H value heads (FLA's head map i_h = i_hv // (HV / H));
+    * ``state_v_first``: initial / final states are [N, HV, V, K] at the boundary;
+    * ``cu_seqlens`` (B = 1, packed): every sequence is zero-padded to the longest
+      one rounded up to a chunk and run as one batch row.  Zero keys, values and
+      log-gates leave the state untouched, so outputs, final states and gradients
+      of the real tokens are exact; padded positions are dropped."""
+    H, HV = q.shape[2], v.shape[2]
+    if HV != H:
+        if HV % H:
+            raise ValueError(f"num_v_heads (HV={HV}) must be divisible by num_qk_heads (H={H})")
+        q = q.repeat_interleave(HV // H, dim=2)
+        k = k.repeat_interleave(HV // H, dim=2)
+        if b is not None:
+            b = b.repeat_interleave(HV // H, dim=2)
+    if state_v_first and h0 is not None:
+        h0 = h0.transpose(-1, -2)
+    if cu_seqlens is None:
+        o, final = _run(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0)
+    else:
+        if q.shape[0] != 1:
+            raise ValueError(f"The batch size is expected to be 1 rather than {q.shape[0]} when using `cu_seqlens`.")
+        cu = (cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens).tolist()
+        bounds = list(zip(cu[:-1], cu[1:]))
+        if h0 is not None and h0.shape[0] != len(bounds):
+            raise ValueError(f"The number of initial states is expected to be equal to the number of input "
+                             f"sequences, i.e., {len(bounds)} rather than {h0.shape[0]}.")
+        Tp = max(64, -(-max(e - s for s, e in bounds) // 64) * 64)
+        xs = [_unpack(x, bounds, Tp) for x in (q, k, v, g, beta, b, w)]
+        o, final = _run(op, backend, full_saving, scale, output_final_state, *xs, h0)
+        o = torch.cat([o[i:i + 1, :e - s] for i, (s, e) in enumerate(bounds)], 1)
+    if state_v_first and final is not None:
+        final = final.transpose(-1, -2)
+    return o, final
 
 
 def make_kda(backend):
@@ -133,7 +185,6 @@ def make_kda(backend):
                   use_graph=False, max_num_seqs=None, **kwargs):
         """Kimi Delta Attention (per-channel vector gate); reference _compat/kda.py:214."""
         _unsupported("chunk_kda", return_intermediate_states=return_intermediate_states,
-                     state_v_first=state_v_first, cu_seqlens=cu_seqlens is not None,
                      cp_context=cp_context is not None, use_graph=use_graph)
         if kwargs.get("chunk_size", 64) != 64:
             raise ValueError("`chunk_size` must be 64 for this build")
@@ -152,9 +203,11 @@ def make_kda(backend):
         if initial_state is not None:
             assert initial_state.dtype == torch.float32, "initial_state must be in float32."
         B, T, H, K = q.shape
+        HV = v.shape[2]
         assert q.shape == k.shape, f"q and k must have the same shape, got q={q.shape} vs k={k.shape}"
-        assert g.shape == (B, T, H, K), f"g must have shape [B, T, H, K], got {list(g.shape)}"
-        assert beta.shape == (B, T, H), f"beta must have shape [B, T, H], got {list(beta.shape)}"
+        assert HV % H == 0, f"For GVA, num_v_heads (HV={HV}) must be evenly divisible by num_qk_heads (H={H})"
+        assert g.shape == (B, T, HV, K), f"g must have shape [B, T, HV, K]={[B, T, HV, K]}, got {list(g.shape)}"
+        assert beta.shape == (B, T, HV), f"beta must have shape [B, T, HV]={[B, T, HV]}, got {list(beta.shape)}"
         if use_qk_l2norm_in_kernel:
             q, k = _l2norm(q), _l2norm(k)
         if use_beta_sigmoid_in_kernel:
@@ -166,7 +219,8 @@ def make_kda(backend):
             g = KDAGate.apply(g, A_log, dt_bias, lower_bound)
         scale = K ** -0.5 if scale is None else scale
         return _apply("kda", backend, disable_recompute, scale, output_final_state, q, k, v, g, beta,
-                      None, None, initial_state)
+                      None, None, initial_state, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
+                      cu_seqlens_cpu=cu_seqlens_cpu)
     return chunk_kda
 
 
@@ -177,22 +231,24 @@ def make_gdn(backend):
                                state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None,
                                chunk_indices=None, cp_context=None, **kwargs):
         """Gated DeltaNet (scalar gate); reference _compat/gdn.py chunk_gated_delta_rule."""
-        _unsupported("chunk_gated_delta_rule", state_v_first=state_v_first,
-                     cu_seqlens=cu_seqlens is not None, cp_context=cp_context is not None,
+        _unsupported("chunk_gated_delta_rule", cp_context=cp_context is not None,
                      use_gate_in_kernel=kwargs.get("use_gate_in_kernel", False))
         if kwargs.get("chunk_size", 64) != 64:
             raise ValueError("`chunk_size` must be 64 for this build")
         if initial_state is not None:
             assert initial_state.dtype == torch.float32, "initial_state must be in float32."
         B, T, H, K = q.shape
-        assert g.shape == (B, T, H), f"g must have shape [B, T, H], got {list(g.shape)}"
+        HV = v.shape[2]
+        assert HV % H == 0, f"num_v_heads (HV={HV}) must be divisible by num_qk_heads (H={H})"
+        assert g.shape == (B, T, HV), f"g must have shape [B, T, HV], got {list(g.shape)}"
         if use_qk_l2norm_in_kernel:
             q, k = _l2norm(q), _l2norm(k)
         if use_beta_sigmoid_in_kernel:
             beta = beta.sigmoid() * (2.0 if allow_neg_eigval else 1.0)
         scale = K ** -0.5 if scale is None else scale
         return _apply("gdn", backend, False, scale, output_final_state, q, k, v, g, beta, None, None,
-                      initial_state)
+                      initial_state, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
+                      cu_seqlens_cpu=cu_seqlens_cpu)
     return chunk_gated_delta_rule
 
 
@@ -205,7 +261,6 @@ def make_gdn2(backend):
         reference _compat/gdn2.py:205."""
         _unsupported("chunk_gdn2", use_gate_in_kernel=use_gate_in_kernel, safe_gate=safe_gate,
                      return_intermediate_states=return_intermediate_states,
-                     state_v_first=state_v_first, cu_seqlens=cu_seqlens is not None,
                      cp_context=cp_context is not None)
         if kwargs.get("chunk_size", 64) != 64:
             raise ValueError("`chunk_size` must be 64 for GDN-2")
@@ -218,7 +273,8 @@ def make_gdn2(backend):
             q, k = _l2norm(q), _l2norm(k)
         scale = k.shape[-1] ** -0.5 if scale is None else scale
         return _apply("gdn2", backend, disable_recompute, scale, output_final_state, q, k, v, g, None,
-                      b, w, initial_state)
+                      b, w, initial_state, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
+                      cu_seqlens_cpu=cu_seqlens_cpu)
     return chunk_gdn2
 
 
@@ -229,7 +285,6 @@ def make_delta(backend):
         """DeltaNet (no gate); reference _compat/delta.py chunk_delta_rule."""
         if "head_first" in kwargs:
             raise DeprecationWarning("head_first has been removed. Inputs must be in `[B, T, H, ...]` format.")
-        _unsupported("chunk_delta_rule", cu_seqlens=cu_seqlens is not None)
         if kwargs.get("chunk_size", 64) != 64:
             raise ValueError("`chunk_size` must be 64 for this build")
         assert q.dtype == k.dtype == v.dtype
@@ -238,5 +293,5 @@ def make_delta(backend):
             q, k = _l2norm(q), _l2norm(k)
         scale = k.shape[-1] ** -0.5 if scale is None else scale
         return _apply("delta", backend, False, scale, output_final_state, q, k, v, None, beta, None,
-                      None, initial_state)
+                      None, initial_state, cu_seqlens=cu_seqlens, cu_seqlens_cpu=cu_seqlens_cpu)
     return chunk_delta_rule

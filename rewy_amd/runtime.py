@@ -12,6 +12,10 @@ Differences, all forced by the platform:
   part of this build;
 * ``check_baseline`` fingerprints this package's own HIP library against the
   sources it was built from (the reference fingerprints FLA's sources, :52-67).
+
+One deliberate widening: packed variable-length batches (``cu_seqlens``) are
+accepted by the optimized backend, which runs them as zero-padded batch rows
+(``_compat.api._apply``); the reference's envelope rejects them.
 """
 from collections import Counter
 from contextlib import contextmanager
@@ -120,12 +124,10 @@ def rejection_reason(op, arguments):
         return 'release envelope requires K=V=128'
     if q.shape != k.shape or k.shape[:3] != v.shape[:3]:
         return 'grouped heads or unequal q/k/v shapes'
-    if k.shape[1] < 64 or k.shape[1] % 64:
+    if arguments.get('cu_seqlens') is None and (k.shape[1] < 64 or k.shape[1] % 64):
         return 'sequence length must be a positive multiple of 64'
     if arguments.get('chunk_size', 64) != 64:
         return 'release envelope requires chunk_size=64'
-    if arguments.get('cu_seqlens') is not None:
-        return 'packed/variable sequences are not release-validated'
     if arguments.get('cp_context') is not None:
         return 'context parallelism is not release-validated'
     if arguments.get('safe_gate', False):
@@ -134,8 +136,6 @@ def rejection_reason(op, arguments):
         return 'static variable-length graph buffers are not supported'
     if arguments.get('return_intermediate_states', False):
         return 'intermediate inference states are not supported'
-    if arguments.get('state_v_first', False):
-        return 'state_v_first layout is not supported'
     scale = arguments.get('scale')
     if scale is not None and scale != k.shape[-1] ** -.5:
         return 'custom scale is not release-validated'
