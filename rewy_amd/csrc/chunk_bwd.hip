@@ -141,9 +141,11 @@ __device__ __forceinline__ void chunk_body(
 
   const int NT = T / C;
   const int blk = blockIdx.x;
-  const int c = blk % NT;
-  const int bh = blk / NT;
-  const int b = bh / H, h = bh % H;
+  // heads run fastest: work-groups in flight together read neighbouring heads of
+  // the same tokens, i.e. contiguous HBM rows
+  const int h = blk % H;
+  const int c = (blk / H) % NT;
+  const int b = blk / (H * NT);
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int cs = wv & 3;          // column strip: k (or v) in [32 cs, 32 cs + 32)
   const int rh = wv >> 2;         // row half: rows [32 rh, 32 rh + 32)

@@ -56,9 +56,11 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
 
   const int blk = blockIdx.x;
   const int NT = T / C;
-  const int c = blk % NT;
-  const int bh = blk / NT;
-  const int b = bh / H, h = bh % H;
+  // heads run fastest: work-groups in flight together read neighbouring heads of
+  // the same tokens, i.e. contiguous HBM rows
+  const int h = blk % H;
+  const int c = (blk / H) % NT;
+  const int b = blk / (H * NT);
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int lc = l & 15, lg = l >> 4;
   const size_t tok0 = (size_t)b * T + (size_t)c * C;
@@ -298,9 +300,11 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
   // (q h) contracts over K = the rows of h, read transposed; h is staged in two halves.
   const int blk = blockIdx.x;
   const int NT = T / C;
-  const int c = blk % NT;
-  const int bh = blk / NT;
-  const int b = bh / H, h = bh % H;
+  // heads run fastest: work-groups in flight together read neighbouring heads of
+  // the same tokens, i.e. contiguous HBM rows
+  const int h = blk % H;
+  const int c = (blk / H) % NT;
+  const int b = blk / (H * NT);
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int lc = l & 15, lg = l >> 4;
   const size_t tok0 = (size_t)b * T + (size_t)c * C;

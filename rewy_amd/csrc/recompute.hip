@@ -48,9 +48,11 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
 
   const int NT = T / C;
   const int blk = blockIdx.x;
-  const int c = blk % NT;
-  const int bh = blk / NT;
-  const int b = bh / H, h = bh % H;
+  // heads run fastest: work-groups in flight together read neighbouring heads of
+  // the same tokens, i.e. contiguous HBM rows
+  const int h = blk % H;
+  const int c = (blk / H) % NT;
+  const int b = blk / (H * NT);
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int lc = l & 15, lg = l >> 4;
   const size_t tok0 = (size_t)b * T + (size_t)c * C;
