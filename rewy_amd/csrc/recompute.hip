@@ -38,11 +38,12 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     bf16* __restrict__ u_out, bf16* __restrict__ qg_out, bf16* __restrict__ kg_out,
     float* __restrict__ aqk_out, int T, int H, float scale) {
   using rec::LDT;
-  // E = b k 2^g and Z = w_gate v rows [t][.], split hi/lo, swizzled for transposed reads
+  // E = b k 2^g and Z = w_gate v rows [t][.] in bf16 (rounded as FLA's recompute_w_u_fwd
+  // rounds k beta 2^g before its dot), swizzled for transposed reads; A rows hi/lo
   __shared__ __attribute__((aligned(16))) bf16 eH[C * KD];
-  __shared__ __attribute__((aligned(16))) bf16 eL[C * KD];
   __shared__ __attribute__((aligned(16))) bf16 zH[C * VD];
-  __shared__ __attribute__((aligned(16))) bf16 zL[C * VD];
+  __shared__ __attribute__((aligned(16))) bf16 sAh[C][LDT];
+  __shared__ __attribute__((aligned(16))) bf16 sAl[C][LDT];
   __shared__ float sG[C];
   __shared__ float sB[C];
 
@@ -67,7 +68,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
   }
   __syncthreads();
 
-  // ---- stage E = b k 2^g and Z = w_gate v row-major (coalesced 16-byte rows), split hi/lo ----
+  // ---- stage E = b k 2^g, Z = w_gate v (bf16) and A (hi/lo) row-major, coalesced 16-byte rows ----
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int p = tid + 256 * i;            // 1024 pieces of 8 columns: row p >> 4
@@ -100,21 +101,20 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) be[j] = we[j] = sB[t];
     }
-    bf16x8 eh, el, zh, zl;
+    bf16x8 eh, zh;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      bf16 hh, ll;
-      split_bf16(be[j] * to_f32(kx[j]) * ge[j], hh, ll);
-      eh[j] = hh;
-      el[j] = ll;
-      split_bf16(we[j] * to_f32(vx[j]), hh, ll);
-      zh[j] = hh;
-      zl[j] = ll;
+      eh[j] = to_bf16(be[j] * to_f32(kx[j]) * ge[j]);
+      zh[j] = to_bf16(we[j] * to_f32(vx[j]));
     }
     store_tr_chunk<16>(eH, t, ch, __builtin_bit_cast(u32x4, eh));
-    store_tr_chunk<16>(eL, t, ch, __builtin_bit_cast(u32x4, el));
     store_tr_chunk<16>(zH, t, ch, __builtin_bit_cast(u32x4, zh));
-    store_tr_chunk<16>(zL, t, ch, __builtin_bit_cast(u32x4, zl));
+    // A rows: 64 x 64 fp32 = 1024 pieces of 4, one per (i, thread) here
+    const f32x4 a4 = *reinterpret_cast<const f32x4*>(akk + ((tok0 + t) * H + h) * C + 4 * ch);
+    bf16x4 alo;
+    const bf16x4 ahi = split_hi4(a4, alo);
+    *reinterpret_cast<bf16x4*>(&sAh[t][4 * ch]) = ahi;
+    *reinterpret_cast<bf16x4*>(&sAl[t][4 * ch]) = alo;
   }
 
   // ---- qg / kg (vector gates): elementwise, coalesced ----
@@ -142,46 +142,26 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
   }
   __syncthreads();
 
-  // ---- w^T = E^T A^T, u^T = Z^T A^T: B operand = A rows (t), contiguous s, straight from HBM ----
+  // ---- w^T = E^T A^T, u^T = Z^T A^T: B operand = A rows (t), contiguous s, from LDS ----
   // wave wv: output rows (k or v) [32 wv, 32 wv + 32), all 64 token columns
   {
-    bf16x8 ah[4][2], al[4][2];   // A rows t = 16 tt + lc, s = 32 ks + 8 lg .. +7
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const float* src = akk + ((tok0 + 16 * tt + lc) * H + h) * C + 32 * ks + 8 * lg;
-        const f32x4 x0 = *reinterpret_cast<const f32x4*>(src);
-        const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4);
-        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          bf16 hh, ll;
-          split_bf16(xs[j], hh, ll);
-          ah[tt][ks][j] = hh;
-          al[tt][ks][j] = ll;
-        }
-      }
 #pragma unroll
     for (int which = 0; which < 2; ++which) {
       const bf16* srcH = which == 0 ? eH : zH;
-      const bf16* srcL = which == 0 ? eL : zL;
       bf16* dst = which == 0 ? w_out + kofs : u_out + vofs;
       const size_t rs = which == 0 ? rsk : rsv;
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         const int row0 = 32 * wv + 16 * rt;
+        const bf16x8 x0 = frag_tr<16>(srcH, 0, row0);    // E^T rows (k or v), over s
+        const bf16x8 x1 = frag_tr<16>(srcH, 32, row0);
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
           f32x4 acc = zero4();
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 xh = frag_tr<16>(srcH, 32 * ks, row0);   // E^T rows (k or v), over s
-            const bf16x8 xl = frag_tr<16>(srcL, 32 * ks, row0);
-            acc = mfma(xh, ah[tt][ks], acc);
-            acc = mfma(xh, al[tt][ks], acc);
-            acc = mfma(xl, ah[tt][ks], acc);
-          }
+          acc = mfma(x0, frag(&sAh[16 * tt][0], LDT), acc);
+          acc = mfma(x0, frag(&sAl[16 * tt][0], LDT), acc);
+          acc = mfma(x1, frag(&sAh[16 * tt][32], LDT), acc);
+          acc = mfma(x1, frag(&sAl[16 * tt][32], LDT), acc);
           // lane: token t = 16 tt + lc, columns row0 + 4 lg .. +3
           bf16x4 o;
 #pragma unroll
