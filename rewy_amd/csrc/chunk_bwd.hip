@@ -66,9 +66,9 @@ template <int GATE, bool VEC_B, bool INTRA = false>
 struct PostLayout {
   // region A.  phases 0-1: A hi/lo [s][t], dR [s][v] (row-major, swizzled, read transposed).
   //            phases 2+:  L, D row-major hi/lo, and (scalar beta) L^T, D^T hi/lo.
-  // Vector gates keep explicit L^T / D^T copies (fewer live registers in their
-  // intra phase); the scalar / no-gate families read L^T / D^T transposed.
-  static constexpr bool LT_COPY = GATE == CG_VECTOR && !INTRA;
+  // GDN2 keeps explicit L^T / D^T copies (measured faster for its register budget);
+  // the other families read L^T / D^T transposed from L / D.
+  static constexpr bool LT_COPY = GATE == CG_VECTOR && VEC_B && !INTRA;
   static constexpr int OFF_AKTH = 0, OFF_AKTL = C * C * 2, OFF_DRT = 2 * C * C * 2;
   static constexpr int OFF_LRH = 0, OFF_LRL = post::T64, OFF_DRH = 2 * post::T64, OFF_DRL = 3 * post::T64;
   static constexpr int OFF_LTH = 4 * post::T64, OFF_LTL = 5 * post::T64, OFF_DTH = 6 * post::T64,
