@@ -545,7 +545,61 @@ __device__ __forceinline__ void chunk_body(
   }
   }   // !INTRA: phase 4
 
-  // ---------------- phase 5: matrix intra as K=16 MFMAs per 16-row sub-block ----------------
+  // ---------------- phase 5: matrix intra ----------------
+  auto combine = [&](int I, const f32x4& xq, const f32x4& xe, const f32x4& xk) {
+    const f32x4 b4 = bvals(I);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float qv = to_f32(qb4[I][r]), kv = to_f32(kb4[I][r]), bv = b4[r];
+      aq[I][r] += xq[r];
+      ak[I][r] += bv * xe[r] + xk[r];
+      aw[I][r] += qv * xq[r] + kv * (bv * xe[r] - xk[r]);
+      if constexpr (VEC_B) adb[I][r] += kv * xe[r];
+      else fbrow[I][r] += xe[r] * kv;
+    }
+  };
+  if constexpr (GATE != CG_VECTOR) {
+    // Scalar / no gate: L and D already carry the gate (phase 2), so the intra
+    // products are plain triangular matmuls, K = 32 MFMAs with every operand read
+    // straight from LDS: uq = L k, ue = D k (rows i, s <= i), uk = L^T q + D^T (beta k)
+    // (s >= i); L^T and D^T come from transposed reads, k and q are exact bf16.
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      f32x4 xq = zero4(), xe = zero4(), xk = zero4();
+#pragma unroll
+      for (int ks = 0; ks <= (16 * I + 15) / 32; ++ks) {
+        const bf16x8 bk = frag_tr<16>(sK, 32 * ks, 16 * wv);
+        xq = mfma(frag(Lrh + (16 * I) * LDT + 32 * ks, LDT), bk, xq);
+        xq = mfma(frag(Lrl + (16 * I) * LDT + 32 * ks, LDT), bk, xq);
+        xe = mfma(frag(Drh + (16 * I) * LDT + 32 * ks, LDT), bk, xe);
+        xe = mfma(frag(Drl + (16 * I) * LDT + 32 * ks, LDT), bk, xe);
+      }
+#pragma unroll
+      for (int ks = (16 * I) / 32; ks < 2; ++ks) {
+        const bf16x8 bq = frag_tr<16>(sQ, 32 * ks, 16 * wv);
+        const bf16x8 bk = frag_tr<16>(sK, 32 * ks, 16 * wv);
+        bf16x8 bkh, bkl;                          // beta_s k_s, rows s = 32 ks + 8 lg + j
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          bf16 hh, ll;
+          split_bf16(sBeta[32 * ks + 8 * lg + j] * to_f32(bk[j]), hh, ll);
+          bkh[j] = hh;
+          bkl[j] = ll;
+        }
+        const bf16x8 lth = frag_tr_pitch(Lrh, LDT, 32 * ks, 16 * I);
+        const bf16x8 ltl = frag_tr_pitch(Lrl, LDT, 32 * ks, 16 * I);
+        const bf16x8 dth = frag_tr_pitch(Drh, LDT, 32 * ks, 16 * I);
+        const bf16x8 dtl = frag_tr_pitch(Drl, LDT, 32 * ks, 16 * I);
+        xk = mfma(lth, bq, xk);
+        xk = mfma(ltl, bq, xk);
+        xk = mfma(dth, bkh, xk);
+        xk = mfma(dth, bkl, xk);
+        xk = mfma(dtl, bkh, xk);
+      }
+      combine(I, xq, xe, xk);
+    }
+  } else {
+  // vector gates: K=16 MFMAs per 16-row sub-block
   // B operands (shared by every output block): kE = k EB, qE = q ET, bkE = b k ET,
   // split into bf16 hi + lo.  Sub-block J contributes to output block I with the
   // per-column factor 2^(top_I - bot_J) (uq, ue; J <= I) or 2^(top_J - bot_I) (uk; J >= I),
@@ -672,18 +726,10 @@ __device__ __forceinline__ void chunk_body(
         }
       }
     }
-    // combine
-    const f32x4 b4 = bvals(I);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float qv = to_f32(qb4[I][r]), kv = to_f32(kb4[I][r]), bv = b4[r];
-      aq[I][r] += xq[r];
-      ak[I][r] += bv * xe[r] + xk[r];
-      aw[I][r] += qv * xq[r] + kv * (bv * xe[r] - xk[r]);
-      if constexpr (VEC_B) adb[I][r] += kv * xe[r];
-      else fbrow[I][r] += xe[r] * kv;
-    }
+    combine(I, xq, xe, xk);
   }
+
+  }   // vector gates
 
   // fallback dbeta rows: direct terms sum_k (k exp2(g) Eb + k ue), summed over all columns
   if constexpr (!VEC_B) {

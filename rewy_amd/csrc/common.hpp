@@ -225,6 +225,16 @@ __device__ __forceinline__ bf16x8 frag_tr(const bf16* tile, int r0, int c0) {
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// The same fragment from a padded row-major tile of pitch ld elements.
+__device__ __forceinline__ bf16x8 frag_tr_pitch(const bf16* tile, int ld, int r0, int c0) {
+  const int l = lane_id(), i = l & 15;
+  const int r = r0 + 8 * (l >> 4) + (i >> 2);
+  const int col = c0 + 4 * (i & 3);
+  const bf16x4 a = ds_read_tr4(tile + r * ld + col);
+  const bf16x4 b = ds_read_tr4(tile + (r + 4) * ld + col);
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
 // 16-byte piece (8 bf16) of row r, chunk c of a swizzled tile
 template <int CH>
 __device__ __forceinline__ void store_tr_chunk(bf16* tile, int r, int c, u32x4 v) {
