@@ -46,6 +46,11 @@ namespace rewy {
 
 enum GateModeC { CG_NONE = 0, CG_SCALAR = 1, CG_VECTOR = 2 };
 
+// Persistent, prefetching chunk kernel wherever its LDS fits (all but GDN2)
+#ifndef REWY_CHUNK_PIPE
+#define REWY_CHUNK_PIPE 1
+#endif
+
 // Split the gate-weighted key/query operands of the intra contractions into
 // bf16 hi + lo (three MFMAs per product) or keep them single bf16 (two MFMAs:
 // the fp32 L/D coefficients are always split).
@@ -62,38 +67,109 @@ constexpr int T128 = KD * LDT * 2;   // bytes of one [128][72] bf16 tile
 constexpr int R64 = C * LDV * 2;     // bytes of one [64][136] bf16 tile
 }  // namespace post
 
-template <int GATE, bool VEC_B, bool INTRA = false>
+template <int GATE, bool VEC_B, bool INTRA = false, bool PIPE = false>
 struct PostLayout {
-  // region A.  phases 0-1: A hi/lo [s][t], dR [s][v] (row-major, swizzled, read transposed).
-  //            phases 2+:  L, D row-major hi/lo, and (scalar beta) L^T, D^T hi/lo.
+  // PIPE: dR, R and dO sit in a separate buffer of the persistent kernel, filled
+  // by direct HBM -> LDS copies while the previous chunk-head finishes.
+  // region A.  phases 0-1: A hi/lo [t][s] (and, unpipelined, dR swizzled).
+  //            phases 2+:  L, D row-major hi/lo, and (GDN2) L^T, D^T hi/lo.
   // GDN2 keeps explicit L^T / D^T copies (measured faster for its register budget);
   // the other families read L^T / D^T transposed from L / D.
   static constexpr bool LT_COPY = GATE == CG_VECTOR && VEC_B && !INTRA;
+  static constexpr int TQ = C * KD * 2;   // bytes of one swizzled [64][128] bf16 tile
   static constexpr int OFF_AKTH = 0, OFF_AKTL = C * C * 2, OFF_DRT = 2 * C * C * 2;
   static constexpr int OFF_LRH = 0, OFF_LRL = post::T64, OFF_DRH = 2 * post::T64, OFF_DRL = 3 * post::T64;
   static constexpr int OFF_LTH = 4 * post::T64, OFF_LTL = 5 * post::T64, OFF_DTH = 6 * post::T64,
                        OFF_DTL = 7 * post::T64;
-  static constexpr int A1 = 2 * C * C * 2 + C * KD * 2;
+  static constexpr int A1 = 2 * C * C * 2 + (PIPE ? 0 : TQ);
   static constexpr int A2 = (LT_COPY ? 8 : 4) * post::T64;
   static constexpr int REGION_A = A1 > A2 ? A1 : A2;
-  // region B.  phases 0-3: P, R, dO row-major.  phases 3+: q, k (, b) row-major swizzled, g row-major.
-  static constexpr int OFF_P = REGION_A, OFF_R = REGION_A + post::R64, OFF_DO = REGION_A + 2 * post::R64;
-  static constexpr int TQ = C * KD * 2;   // bytes of one swizzled [64][128] bf16 tile
+  // region B.  phases 0-3: P row-major (pitch LDV) (, unpipelined: R, dO swizzled).
+  //            phases 3+:  q, k (, b) swizzled, vector g row-major fp32.
+  static constexpr int OFF_P = REGION_A, OFF_R = REGION_A + post::R64, OFF_DO = OFF_R + TQ;
+  static constexpr int GT_BYTES = GATE == CG_VECTOR ? C * post::LDG * 4 : 0;
   static constexpr int OFF_QT = REGION_A, OFF_KT = REGION_A + TQ, OFF_GT = REGION_A + 2 * TQ;
-  static constexpr int OFF_BT = OFF_GT + C * post::LDG * 4;
-  static constexpr int B1 = 3 * post::R64;
-  static constexpr int B2 = 2 * TQ + C * post::LDG * 4 + (VEC_B ? TQ : 0);
+  static constexpr int OFF_BT = OFF_GT + GT_BYTES;
+  static constexpr int B1 = post::R64 + (PIPE ? 0 : 2 * TQ);
+  static constexpr int B2 = 2 * TQ + GT_BYTES + (VEC_B ? TQ : 0);
   static constexpr int OFF_SMALL = REGION_A + (B1 > B2 ? B1 : B2);
   static constexpr int S_BETA = 0, S_G = 64, S_DBA = 128, S_DBB = 192, S_DG = 256, S_COL = 320,
-                       S_TOT = 448, S_GL = 576, S_N = 704;
-  static constexpr int BYTES = OFF_SMALL + S_N * 4;
-  static_assert(BYTES <= 160 * 1024, "LDS budget");
+                       S_TOT = 448, S_GL = 576, S_ANY = 704, S_N = 712;
+  static constexpr int BYTES = OFF_SMALL + S_N * 4;        // dynamic LDS
+  static constexpr int X_BYTES = PIPE ? 3 * TQ : 0;        // static LDS of the persistent kernel
+  static constexpr bool FITS = BYTES + X_BYTES <= 160 * 1024;
+  static_assert(PIPE || FITS, "LDS budget");
 };
+
+// Position of one (batch, chunk, head) work item in the T-major tensors.  Heads
+// run fastest: work-groups in flight together read neighbouring heads of the
+// same tokens, i.e. contiguous HBM rows.
+struct ChunkItem {
+  int h, c, b;
+  size_t tok0, kofs, vofs, hoff, aofs;
+  __device__ __forceinline__ ChunkItem(int item, int T, int H) {
+    const int NT = T / C;
+    h = item % H;
+    c = (item / H) % NT;
+    b = item / (H * NT);
+    tok0 = (size_t)b * T + (size_t)c * C;
+    kofs = tok0 * H * KD + (size_t)h * KD;
+    vofs = tok0 * H * VD + (size_t)h * VD;
+    hoff = (((size_t)b * NT + c) * H + h) * KD * VD;
+    aofs = (tok0 * H + h) * C;
+  }
+};
+
+// Per-thread inputs of phase 0 that the persistent kernel fetches one item
+// ahead: A (fp32, [t][s] rows of 64; two 16-byte pieces, lanes along rows), and
+// beta, the scalar gate of row tid & 63 and the last-row gate of column tid & 127.
+// Loaded by every thread (clamped rows) so that no branch splits the vmcnt count.
+struct PhaseIn {
+  f32x4 a[2];
+  float beta, g, gl;
+};
+
+template <int GATE, bool VEC_B>
+__device__ __forceinline__ void load_phase_in(const float* __restrict__ akk, const float* __restrict__ beta,
+                                              const float* __restrict__ g, const ChunkItem& it, int H, int tid,
+                                              PhaseIn& pin) {
+  const size_t rsa = (size_t)H * C;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = tid + 512 * i;
+    pin.a[i] = *reinterpret_cast<const f32x4*>(akk + it.aofs + (size_t)(p >> 4) * rsa + 4 * (p & 15));
+  }
+  const size_t row = (it.tok0 + (tid & (C - 1))) * H + it.h;
+  pin.beta = 0.f;
+  pin.g = 0.f;
+  pin.gl = 0.f;
+  if constexpr (!VEC_B) pin.beta = beta[row];
+  if constexpr (GATE == CG_SCALAR) {
+    pin.g = g[row];
+    pin.gl = g[(it.tok0 + C - 1) * H + it.h];
+  } else if constexpr (GATE == CG_VECTOR) {
+    pin.gl = g[it.kofs + (size_t)(C - 1) * H * KD + (tid & (KD - 1))];
+  }
+}
+
+// dR, R = v_new and dO of one item into the swizzled [64][128] tiles x[0..2]:
+// wave w copies rows 8 w .. 8 w + 7 of each
+__device__ __forceinline__ void dma_x(bf16* xbuf, const bf16* __restrict__ dR, const bf16* __restrict__ vnew,
+                                      const bf16* __restrict__ dO, const ChunkItem& it, int H, int tid) {
+  const size_t rsv = (size_t)H * VD;
+  const int r0 = 8 * __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    dma_rows4(xbuf, r0 + 4 * j, dR + it.vofs, rsv, l);
+    dma_rows4(xbuf + C * KD, r0 + 4 * j, vnew + it.vofs, rsv, l);
+    dma_rows4(xbuf + 2 * C * KD, r0 + 4 * j, dO + it.vofs, rsv, l);
+  }
+}
 
 // The body serves two kernels: the full chunk backward (INTRA = false) and the
 // standalone matrix intra (INTRA = true: L and D are given, the partial dq, dk,
 // dg, db are read-modify-written in fp32, no state terms and no cumsum).
-template <int GATE, bool VEC_B, bool INTRA>
+template <int GATE, bool VEC_B, bool INTRA, bool PIPE = false>
 __device__ __forceinline__ void chunk_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
@@ -103,8 +179,8 @@ __device__ __forceinline__ void chunk_body(
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
     bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale,
     const float* __restrict__ daqk, float* __restrict__ dq32, float* __restrict__ dk32,
-    float* __restrict__ db32, int beta_complete) {
-  using LY = PostLayout<GATE, VEC_B, INTRA>;
+    float* __restrict__ db32, int beta_complete, int item, int next_item, bf16* xbuf, PhaseIn& pin) {
+  using LY = PostLayout<GATE, VEC_B, INTRA, PIPE>;
   using post::LDT;
   using post::LDV;
   using post::LDG;
@@ -113,7 +189,10 @@ __device__ __forceinline__ void chunk_body(
   auto U32 = [&](int off) { return reinterpret_cast<uint32_t*>(smem + off); };
   bf16* sAh = B16(LY::OFF_AKTH);    // A rows [s][t], hi
   bf16* sAl = B16(LY::OFF_AKTL);    // A rows, lo
-  bf16* sdR = B16(LY::OFF_DRT);     // dR rows [s][v]
+  // dR, R, dO rows [t][v], swizzled: the persistent kernel's prefetch buffer, or staged here
+  bf16* sdR = PIPE ? xbuf : B16(LY::OFF_DRT);
+  bf16* sR = PIPE ? xbuf + C * KD : B16(LY::OFF_R);
+  bf16* sdO = PIPE ? xbuf + 2 * C * KD : B16(LY::OFF_DO);
   bf16* Lrh = B16(LY::OFF_LRH);
   bf16* Lrl = B16(LY::OFF_LRL);
   bf16* Drh = B16(LY::OFF_DRH);
@@ -123,8 +202,6 @@ __device__ __forceinline__ void chunk_body(
   bf16* Dth = B16(LY::OFF_DTH);
   bf16* Dtl = B16(LY::OFF_DTL);
   bf16* sP = B16(LY::OFF_P);
-  bf16* sR = B16(LY::OFF_R);
-  bf16* sdO = B16(LY::OFF_DO);
   bf16* sQ = B16(LY::OFF_QT);       // q rows [t][k] (swizzled)
   bf16* sK = B16(LY::OFF_KT);       // k rows
   float* sGr = reinterpret_cast<float*>(smem + LY::OFF_GT);   // g rows [t][k], pitch LDG
@@ -138,23 +215,23 @@ __device__ __forceinline__ void chunk_body(
   float* sCol = small + LY::S_COL;     // [128] column partials from the upper row half
   float* sTot = small + LY::S_TOT;     // [128] column totals of the lower row half
   float* sGl = small + LY::S_GL;       // [128] last-row gate (log2) per column
+  int* sAny = reinterpret_cast<int*>(small + LY::S_ANY);   // [8] per-wave "some beta ~ 0" flags
 
-  const int NT = T / C;
-  const int blk = blockIdx.x;
-  // heads run fastest: work-groups in flight together read neighbouring heads of
-  // the same tokens, i.e. contiguous HBM rows
-  const int h = blk % H;
-  const int c = (blk / H) % NT;
-  const int b = blk / (H * NT);
-  const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
+  const ChunkItem pos(item, T, H);
+  const int h = pos.h;
+  // the lane index is made opaque per call so that a persistent caller's loop
+  // cannot hoist the (loop-invariant) LDS address arithmetic out of the body
+  int tid_o = threadIdx.x;
+  asm volatile("" : "+v"(tid_o));
+  const int tid = tid_o, l = tid_o & 63, wv = __builtin_amdgcn_readfirstlane(tid_o >> 6);
   const int cs = wv & 3;          // column strip: k (or v) in [32 cs, 32 cs + 32)
   const int rh = wv >> 2;         // row half: rows [32 rh, 32 rh + 32)
   const int lc = l & 15, lg = l >> 4;
-  const size_t tok0 = (size_t)b * T + (size_t)c * C;
+  const size_t tok0 = pos.tok0;
   const size_t rsk = (size_t)H * KD, rsv = (size_t)H * VD, rsa = (size_t)H * C;
-  const size_t hoff = (((size_t)b * NT + c) * H + h) * KD * VD;
-  const size_t kofs = tok0 * rsk + (size_t)h * KD;    // [t][k] tensors of this chunk-head
-  const size_t vofs = tok0 * rsv + (size_t)h * VD;    // [t][v] tensors
+  const size_t hoff = pos.hoff;
+  const size_t kofs = pos.kofs;    // [t][k] tensors of this chunk-head
+  const size_t vofs = pos.vofs;    // [t][v] tensors
   const bf16* vb = v + vofs;
 
   // ---------------- phase 0: stage A (hi/lo), dR, R, dO row-major; beta, gates ----------------
@@ -185,45 +262,40 @@ __device__ __forceinline__ void chunk_body(
       sDbB[tid] = 0.f;
     }
   } else {
+    if constexpr (!PIPE) load_phase_in<GATE, VEC_B>(akk, beta, g, pos, H, tid, pin);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + 512 * i;        // 1024 16-byte pieces per tile; lanes run along rows
       const int t = p >> 4, ch = p & 15;
-      const f32x4 a = *reinterpret_cast<const f32x4*>(akk + (tok0 * H + h) * C + (size_t)t * rsa + 4 * ch);
-      const u32x4 d = *reinterpret_cast<const u32x4*>(dR + vofs + (size_t)t * rsv + 8 * ch);
       bf16x4 lo;
-      const bf16x4 hi = split_hi4(a, lo);
+      const bf16x4 hi = split_hi4(pin.a[i], lo);
       *reinterpret_cast<bf16x4*>(sAh + tr_off<8>(t, 4 * ch)) = hi;
       *reinterpret_cast<bf16x4*>(sAl + tr_off<8>(t, 4 * ch)) = lo;
-      store_tr_chunk<16>(sdR, t, ch, d);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int p = tid + 512 * i;
-      const int t = p >> 4, v0 = (p & 15) * 8;
-      *reinterpret_cast<u32x4*>(sR + t * LDV + v0) = *reinterpret_cast<const u32x4*>(vnew + vofs + (size_t)t * rsv + v0);
-      *reinterpret_cast<u32x4*>(sdO + t * LDV + v0) = *reinterpret_cast<const u32x4*>(dO + vofs + (size_t)t * rsv + v0);
+      if constexpr (!PIPE) {
+        const size_t o = vofs + (size_t)t * rsv + 8 * ch;
+        store_tr_chunk<16>(sdR, t, ch, *reinterpret_cast<const u32x4*>(dR + o));
+        store_tr_chunk<16>(sR, t, ch, *reinterpret_cast<const u32x4*>(vnew + o));
+        store_tr_chunk<16>(sdO, t, ch, *reinterpret_cast<const u32x4*>(dO + o));
+      }
     }
     int fb = 0;
     if (tid < C) {
-      const size_t row = (tok0 + tid) * H + h;
       if constexpr (!VEC_B) {
-        const float be = beta[row];
-        sBeta[tid] = be;
-        fb = fabsf(be) < 1e-6f;
+        sBeta[tid] = pin.beta;
+        fb = fabsf(pin.beta) < 1e-6f;
       }
-      if constexpr (GATE == CG_SCALAR) sG[tid] = g[row];
+      if constexpr (GATE == CG_SCALAR) sG[tid] = pin.g;
       sDbA[tid] = 0.f;
       sDbB[tid] = 0.f;
       sDg[tid] = 0.f;
     }
-    if (tid < KD) {
-      float gl = 0.f;
-      if constexpr (GATE == CG_VECTOR) gl = g[kofs + (size_t)(C - 1) * rsk + tid];
-      else if constexpr (GATE == CG_SCALAR) gl = g[(tok0 + C - 1) * H + h];
-      sGl[tid] = gl;
-    }
-    any_fb = __syncthreads_or(fb);   // block-uniform: some row has |beta| < 1e-6
+    if (tid < KD) sGl[tid] = pin.gl;
+    // block-uniform: some row has |beta| < 1e-6 (one flag per wave, then a barrier)
+    const unsigned long long fbw = __ballot(fb);
+    if (l == 0) sAny[wv] = fbw != 0ull;
+    lds_barrier();
+#pragma unroll
+    for (int w = 0; w < 8; ++w) any_fb |= sAny[w];
   }
   // the standalone intra adds the direct dbeta terms of every row
   const bool has_fb = !VEC_B && (INTRA || any_fb != 0);
@@ -245,9 +317,9 @@ __device__ __forceinline__ void chunk_body(
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           if (ks == 0 && rh == 1) continue;    // A^T upper triangular: s < 32 <= t vanishes
-          const bf16x8 a = frag_tr<16>(sdR, 32 * ks, vrow0);          // dR^T rows v, over s
-          acc = mfma(a, frag_tr<8>(sAh, 32 * ks, tcol0), acc);      // A[s][t] columns t, over s
-          acc = mfma(a, frag_tr<8>(sAl, 32 * ks, tcol0), acc);
+          const bf16x8 a = frag_tr<16>(sdR, 32 * ks, vrow0, l);          // dR^T rows v, over s
+          acc = mfma(a, frag_tr<8>(sAh, 32 * ks, tcol0, l), acc);      // A[s][t] columns t, over s
+          acc = mfma(a, frag_tr<8>(sAl, 32 * ks, tcol0, l), acc);
         }
         // lane: t = tcol0 + lc, v = vrow0 + 4 lg .. +3
         const int t = tcol0 + lc;
@@ -270,7 +342,7 @@ __device__ __forceinline__ void chunk_body(
           *reinterpret_cast<bf16x4*>(dw_out + vofs + go) = o2;
         } else {
           const float be = sBeta[t];
-          const bf16x4 r4 = *reinterpret_cast<const bf16x4*>(sR + t * LDV + v0);
+          const bf16x4 r4 = *reinterpret_cast<const bf16x4*>(sR + tr_off<16>(t, v0));
           bf16x4 o1;
           float pr = 0.f;
 #pragma unroll
@@ -279,21 +351,21 @@ __device__ __forceinline__ void chunk_body(
             pr += acc[r] * to_f32(r4[r]);
           }
           *reinterpret_cast<bf16x4*>(dv_out + vofs + go) = o1;
-          pr = sum_lane_groups(pr);
+          pr = sum_lane_groups(pr, l);
           if (lg == 0) atomicAdd(&sDbA[t], pr);
           if (has_fb) {
             const bf16x4 x4 = *reinterpret_cast<const bf16x4*>(vb + go);
             float pv = 0.f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) pv += acc[r] * to_f32(x4[r]);
-            pv = sum_lane_groups(pv);
+            pv = sum_lane_groups(pv, l);
             if (lg == 0) atomicAdd(&sDbB[t], pv);
           }
         }
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // prefetch state tiles for phase 3: wave wv owns key columns [16 wv, 16 wv + 16)
   bf16x8 fh[4], fdh[4];
@@ -321,17 +393,17 @@ __device__ __forceinline__ void chunk_body(
       if (lowerA && LY::LT_COPY) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 br = frag(sR + (16 * J) * LDV + 32 * ks, LDV);
-          aL = mfma(frag(sdO + (16 * I) * LDV + 32 * ks, LDV), br, aL);
-          aD = mfma(frag(sP + (16 * I) * LDV + 32 * ks, LDV), br, aD);
+          const bf16x8 br = frag_row<16>(sR, 16 * J, 32 * ks, l);
+          aL = mfma(frag_row<16>(sdO, 16 * I, 32 * ks, l), br, aL);
+          aD = mfma(frag(sP + (16 * I) * LDV + 32 * ks, LDV, l), br, aD);
         }
       }
       if (lowerB) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 ar = frag(sR + (16 * I) * LDV + 32 * ks, LDV);
-          bL = mfma(ar, frag(sdO + (16 * J) * LDV + 32 * ks, LDV), bL);
-          bD = mfma(ar, frag(sP + (16 * J) * LDV + 32 * ks, LDV), bD);
+          const bf16x8 ar = frag_row<16>(sR, 16 * I, 32 * ks, l);
+          bL = mfma(ar, frag_row<16>(sdO, 16 * J, 32 * ks, l), bL);
+          bD = mfma(ar, frag(sP + (16 * J) * LDV + 32 * ks, LDV, l), bD);
         }
       }
       if constexpr (LY::LT_COPY) {
@@ -384,15 +456,15 @@ __device__ __forceinline__ void chunk_body(
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int j = 0; j < 8; ++j) sacc += to_f32(fh[ks][j]) * to_f32(fdh[ks][j]);
-    dgk = sum_lane_groups(sacc);               // sum_v h[kk][v] dh[kk][v]
+    dgk = sum_lane_groups(sacc, l);               // sum_v h[kk][v] dh[kk][v]
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       f32x4 x = zero4(), y = zero4(), z = zero4();
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        x = mfma(frag(sdO + (16 * I) * LDV + 32 * ks, LDV), fh[ks], x);
-        y = mfma(frag(sR + (16 * I) * LDV + 32 * ks, LDV), fdh[ks], y);
-        z = mfma(frag(sP + (16 * I) * LDV + 32 * ks, LDV), fh[ks], z);
+        x = mfma(frag_row<16>(sdO, 16 * I, 32 * ks, l), fh[ks], x);
+        y = mfma(frag_row<16>(sR, 16 * I, 32 * ks, l), fdh[ks], y);
+        z = mfma(frag(sP + (16 * I) * LDV + 32 * ks, LDV, l), fh[ks], z);
       }
       aq[I] = x;
       ak[I] = y;
@@ -419,7 +491,7 @@ __device__ __forceinline__ void chunk_body(
       rg[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)(p >> 5) * rsk + (p & 31) * 4);
     }
   }
-  __syncthreads();   // P, R, dO no longer needed: region B becomes q, k, g (, b)
+  lds_barrier();   // P, R, dO no longer needed: region B becomes q, k, g (, b)
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int p = tid + 512 * i;
@@ -434,7 +506,13 @@ __device__ __forceinline__ void chunk_body(
       *reinterpret_cast<f32x4*>(sGr + (p >> 5) * LDG + (p & 31) * 4) = rg[i];
     }
   }
-  __syncthreads();
+  lds_barrier();
+  // The next item's dR, R, dO stream into the prefetch buffer during phases 4-6
+  // (the last item re-fetches its own rows: harmless, and no branch splits the
+  // vmcnt count).  Issued after the barrier: a barrier's LDS fence waits for
+  // outstanding direct-to-LDS copies, and so does any LDS write the compiler
+  // cannot prove disjoint from them.
+  if constexpr (PIPE) dma_x(xbuf, dR, vnew, dO, ChunkItem(next_item >= 0 ? next_item : item, T, H), H, tid);
 
   // ---------------- per-lane operands of column kk, rows 16 J + 4 lg + j ----------------
   // In the accumulator layout and in the B layout of the K=16 MFMA a lane holds the
@@ -478,10 +556,10 @@ __device__ __forceinline__ void chunk_body(
   for (int J = 0; J < 4; ++J) {
     float hi = fmaxf(fmaxf(g4[J][0], g4[J][1]), fmaxf(g4[J][2], g4[J][3]));
     float lo = fminf(fminf(g4[J][0], g4[J][1]), fminf(g4[J][2], g4[J][3]));
-    hi = fmaxf(hi, __shfl_xor(hi, 16));
-    hi = fmaxf(hi, __shfl_xor(hi, 32));
-    lo = fminf(lo, __shfl_xor(lo, 16));
-    lo = fminf(lo, __shfl_xor(lo, 32));
+    hi = fmaxf(hi, lane_xor16(hi));
+    hi = fmaxf(hi, lane_read(hi, l ^ 32));
+    lo = fminf(lo, lane_xor16(lo));
+    lo = fminf(lo, lane_read(lo, l ^ 32));
     top[J] = hi;
     bot[J] = lo;
     pair[J] = (GATE == CG_VECTOR) && (hi - lo) >= 80.f;
@@ -568,16 +646,16 @@ __device__ __forceinline__ void chunk_body(
       f32x4 xq = zero4(), xe = zero4(), xk = zero4();
 #pragma unroll
       for (int ks = 0; ks <= (16 * I + 15) / 32; ++ks) {
-        const bf16x8 bk = frag_tr<16>(sK, 32 * ks, 16 * wv);
-        xq = mfma(frag(Lrh + (16 * I) * LDT + 32 * ks, LDT), bk, xq);
-        xq = mfma(frag(Lrl + (16 * I) * LDT + 32 * ks, LDT), bk, xq);
-        xe = mfma(frag(Drh + (16 * I) * LDT + 32 * ks, LDT), bk, xe);
-        xe = mfma(frag(Drl + (16 * I) * LDT + 32 * ks, LDT), bk, xe);
+        const bf16x8 bk = frag_tr<16>(sK, 32 * ks, 16 * wv, l);
+        xq = mfma(frag(Lrh + (16 * I) * LDT + 32 * ks, LDT, l), bk, xq);
+        xq = mfma(frag(Lrl + (16 * I) * LDT + 32 * ks, LDT, l), bk, xq);
+        xe = mfma(frag(Drh + (16 * I) * LDT + 32 * ks, LDT, l), bk, xe);
+        xe = mfma(frag(Drl + (16 * I) * LDT + 32 * ks, LDT, l), bk, xe);
       }
 #pragma unroll
       for (int ks = (16 * I) / 32; ks < 2; ++ks) {
-        const bf16x8 bq = frag_tr<16>(sQ, 32 * ks, 16 * wv);
-        const bf16x8 bk = frag_tr<16>(sK, 32 * ks, 16 * wv);
+        const bf16x8 bq = frag_tr<16>(sQ, 32 * ks, 16 * wv, l);
+        const bf16x8 bk = frag_tr<16>(sK, 32 * ks, 16 * wv, l);
         bf16x8 bkh, bkl;                          // beta_s k_s, rows s = 32 ks + 8 lg + j
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -586,10 +664,10 @@ __device__ __forceinline__ void chunk_body(
           bkh[j] = hh;
           bkl[j] = ll;
         }
-        const bf16x8 lth = frag_tr_pitch(Lrh, LDT, 32 * ks, 16 * I);
-        const bf16x8 ltl = frag_tr_pitch(Lrl, LDT, 32 * ks, 16 * I);
-        const bf16x8 dth = frag_tr_pitch(Drh, LDT, 32 * ks, 16 * I);
-        const bf16x8 dtl = frag_tr_pitch(Drl, LDT, 32 * ks, 16 * I);
+        const bf16x8 lth = frag_tr_pitch(Lrh, LDT, 32 * ks, 16 * I, l);
+        const bf16x8 ltl = frag_tr_pitch(Lrl, LDT, 32 * ks, 16 * I, l);
+        const bf16x8 dth = frag_tr_pitch(Drh, LDT, 32 * ks, 16 * I, l);
+        const bf16x8 dtl = frag_tr_pitch(Drl, LDT, 32 * ks, 16 * I, l);
         xk = mfma(lth, bq, xk);
         xk = mfma(ltl, bq, xk);
         xk = mfma(dth, bkh, xk);
@@ -746,7 +824,7 @@ __device__ __forceinline__ void chunk_body(
 
   // ---------------- phase 6: last-row state terms, reverse cumsum, stores ----------------
   if constexpr (!INTRA) {
-  colkdk = sum_lane_groups(colkdk);            // sum over the 64 rows of k dks (this column)
+  colkdk = sum_lane_groups(colkdk, l);            // sum over the 64 rows of k dks (this column)
   if constexpr (GATE == CG_VECTOR) {
     const float term = fast_exp2(gl) * dgk + colkdk;
     if (lg == 3) aw[3][3] += term;
@@ -758,10 +836,10 @@ __device__ __forceinline__ void chunk_body(
       x[1] += x[2];
       x[0] += x[1];
       const float tot = x[0];                  // this lane group's 4-row total
-      const float t0 = __shfl(tot, lc);
-      const float t1 = __shfl(tot, lc + 16);
-      const float t2 = __shfl(tot, lc + 32);
-      const float t3 = __shfl(tot, lc + 48);
+      const float t0 = lane_read(tot, lc);
+      const float t1 = lane_read(tot, lc + 16);
+      const float t2 = lane_read(tot, lc + 32);
+      const float t3 = lane_read(tot, lc + 48);
       float below = carry;
       if (lg < 3) below += t3;
       if (lg < 2) below += t2;
@@ -785,6 +863,12 @@ __device__ __forceinline__ void chunk_body(
   }
   }   // !INTRA: phase 6
 
+  if constexpr (PIPE) {
+    // the next item's prefetch (issued after phase 3) has landed in this wave's
+    // rows; its A goes to registers before this item's stores are issued
+    __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
+    load_phase_in<GATE, VEC_B>(akk, beta, g, ChunkItem(next_item >= 0 ? next_item : item, T, H), H, tid, pin);
+  }
   // stores of dq, dk (bf16), the vector dg (fp32) and db (bf16); 32-bit offsets
   // from uniform per-chunk-head bases
   if constexpr (INTRA) {
@@ -817,7 +901,7 @@ __device__ __forceinline__ void chunk_body(
       }
     }
   }
-  __syncthreads();   // sDbB, sDg complete
+  lds_barrier();   // sDbB, sDg complete
   if (INTRA && tid < C) {
     // endpoint_intra.py:190-194: every row, or only |beta| < 1e-6 rows when the
     // residual producer already accounted for the rest (beta_complete)
@@ -837,6 +921,9 @@ __device__ __forceinline__ void chunk_body(
       dg_out[row] = acc;
     }
   }
+  // persistent kernel: every wave's prefetch complete and this item's LDS reads
+  // done before the next item's phase 0
+  if constexpr (PIPE) lds_barrier();
 }
 
 template <int GATE, bool VEC_B>
@@ -848,9 +935,43 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     const bf16* __restrict__ dhst, bf16* __restrict__ dq_out, bf16* __restrict__ dk_out,
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
     bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale) {
+  PhaseIn pin;
   chunk_body<GATE, VEC_B, false>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
                                  dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale, nullptr,
-                                 nullptr, nullptr, nullptr, 0);
+                                 nullptr, nullptr, nullptr, 0, blockIdx.x, -1, nullptr, pin);
+}
+
+// Persistent form: one work-group per CU walks the items blockIdx.x, + gridDim.x, ...
+// and copies the next item's dR, R, dO straight into LDS (and its A into
+// registers) while the current one computes phases 4-6, so that HBM reads overlap
+// the intra and epilogue work instead of stalling the work-group.
+template <int GATE, bool VEC_B>
+__global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
+    const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
+    const bf16* __restrict__ wgate, const float* __restrict__ akk, const bf16* __restrict__ hst,
+    const bf16* __restrict__ dhst, bf16* __restrict__ dq_out, bf16* __restrict__ dk_out,
+    bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
+    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale, int items) {
+  __shared__ __attribute__((aligned(16))) bf16 xbuf[3 * C * KD];
+  PhaseIn pin;
+  int it = blockIdx.x;
+  if (it >= items) return;
+  {
+    const ChunkItem first(it, T, H);
+    dma_x(xbuf, dR, vnew, dO, first, H, threadIdx.x);
+    load_phase_in<GATE, VEC_B>(akk, beta, g, first, H, threadIdx.x, pin);
+    __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
+    lds_barrier();
+  }
+  for (; it < items; it += gridDim.x) {
+    const int nx = it + (int)gridDim.x;
+    chunk_body<GATE, VEC_B, false, true>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
+                                         dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale,
+                                         nullptr, nullptr, nullptr, nullptr, 0, it, nx < items ? nx : -1, xbuf,
+                                         pin);
+  }
 }
 
 template <bool VEC_B>
@@ -859,10 +980,11 @@ __global__ __launch_bounds__(512) void matrix_intra_kernel(
     const float* __restrict__ beta, const bf16* __restrict__ bgate, const float* __restrict__ daqk,
     const float* __restrict__ dakk, float* __restrict__ dq, float* __restrict__ dk,
     float* __restrict__ db, float* __restrict__ dg, int T, int H, int beta_complete) {
+  PhaseIn pin;
   chunk_body<CG_VECTOR, VEC_B, true>(q, k, nullptr, nullptr, nullptr, nullptr, g, beta, bgate, nullptr, dakk,
                                      nullptr, nullptr, nullptr, nullptr, nullptr, dg, VEC_B ? nullptr : db,
                                      nullptr, nullptr, T, H, 1.f, daqk, dq, dk, VEC_B ? db : nullptr,
-                                     beta_complete);
+                                     beta_complete, blockIdx.x, -1, nullptr, pin);
 }
 
 template <int GATE, bool VEC_B>
@@ -871,6 +993,27 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
                               const void* bgate, const void* wgate, const float* akk, const void* h,
                               const void* dh, void* dq, void* dk, void* dv, float* dg, float* dbeta,
                               void* db, void* dw, int B, int T, int H, float scale, hipStream_t s) {
+  const int items = B * H * (T / C);
+  using LP = PostLayout<GATE, VEC_B, false, true>;
+  if constexpr (LP::FITS && REWY_CHUNK_PIPE) {
+    auto kern = chunk_bwd_pipe_kernel<GATE, VEC_B>;
+    static bool attr_set = false;
+    if (!attr_set) {
+      hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LP::BYTES);
+      if (e != hipSuccess) return e;
+      attr_set = true;
+    }
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    const int grid = items < cus ? items : cus;   // one work-group per CU (LDS-bound)
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), LP::BYTES, s, (const bf16*)q, (const bf16*)k,
+                       (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta,
+                       (const bf16*)bgate, (const bf16*)wgate, akk, (const bf16*)h, (const bf16*)dh,
+                       (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, items);
+    return hipGetLastError();
+  }
   using LY = PostLayout<GATE, VEC_B>;
   auto kern = chunk_bwd_kernel<GATE, VEC_B>;
   static bool attr_set = false;
@@ -879,7 +1022,7 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  const int grid = B * H * (T / C);
+  const int grid = items;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta,
                      (const bf16*)bgate, (const bf16*)wgate, akk, (const bf16*)h, (const bf16*)dh,

@@ -39,8 +39,7 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
 // 8-element fragment of a K-contiguous tile whose row 0 / k 0 is at `base`.
-__device__ __forceinline__ bf16x8 frag(const bf16* base, int ld) {
-  const int l = lane_id();
+__device__ __forceinline__ bf16x8 frag(const bf16* base, int ld, int l = lane_id()) {
   return *reinterpret_cast<const bf16x8*>(base + (l & 15) * ld + 8 * (l >> 4));
 }
 
@@ -80,19 +79,48 @@ __device__ __forceinline__ int xcd_logical_block() {
   return (b % 8) * (n / 8) + b / 8;
 }
 
+// Work-group barrier that orders LDS only.  __syncthreads() fences every
+// address space, which makes each wave wait for all of its outstanding global
+// loads and stores (vmcnt 0) before the barrier; kernels whose waves share
+// only LDS use this one so that prefetches and output stores stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// DPP lane moves inside rows of 16 lanes: no LDS traffic, no address registers.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+// value of lane `src` (any lane of the wave)
+__device__ __forceinline__ float lane_read(float x, int src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src << 2, __builtin_bit_cast(int, x)));
+}
+
+// value of lane l ^ 16
+__device__ __forceinline__ float lane_xor16(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
+}
+
 // Sum over the 4 lane groups (lanes l, l^16, l^32, l^48) of a wave.
-__device__ __forceinline__ float sum_lane_groups(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
+__device__ __forceinline__ float sum_lane_groups(float x, int l = lane_id()) {
+  // xor 16 inside each 32-lane half (ds_swizzle bit mode: and 0x1f, xor 0x10)
+  x += lane_xor16(x);
+  x += lane_read(x, l ^ 32);
   return x;
 }
 
-// Sum over the 16 lanes of one lane group (the 16 columns of a C tile row).
+// Sum over the 16 lanes of one lane group (the 16 columns of a C tile row):
+// pairs, quads (quad_perm), then halves of 8 (row_half_mirror) and of 16
+// (row_mirror); every lane ends with the full sum.
 __device__ __forceinline__ float sum_row16(float x) {
-  x += __shfl_xor(x, 1);
-  x += __shfl_xor(x, 2);
-  x += __shfl_xor(x, 4);
-  x += __shfl_xor(x, 8);
+  x += dpp_mov<0xB1>(x);    // quad_perm [1, 0, 3, 2]
+  x += dpp_mov<0x4E>(x);    // quad_perm [2, 3, 0, 1]
+  x += dpp_mov<0x141>(x);   // row_half_mirror
+  x += dpp_mov<0x140>(x);   // row_mirror
   return x;
 }
 
@@ -188,11 +216,14 @@ __device__ __forceinline__ void store_pair_piece_split(uint32_t* dhi, uint32_t* 
 //
 // Tiles of CH 16-byte chunks per row are stored without padding; chunk c of
 // row r sits at chunk c ^ tr_swz<CH>(r).  The swizzle keeps the two chunks a
-// 16-lane group reads per row adjacent (it is even) and spreads the 8 rows one
-// half-wave reads (r0 + {0..3, 8..11} + 16 q) over distinct banks.
+// 16-lane group reads per row in one aligned pair (the pair index is XORed, the
+// chunk inside the pair at most swapped) and spreads the 8 rows one half-wave
+// reads (r0 + {0..3, 8..11} + 16 q) over distinct banks.  For CH = 16 it also
+// maps the same chunk of 16 consecutive rows to 16 distinct chunks, so row
+// fragments (frag_row: one 16-byte read per lane, 16 rows) are conflict-free too.
 template <int CH>
 __device__ __forceinline__ int tr_swz(int r) {
-  if constexpr (CH >= 16) return 2 * ((r & 3) | (((r >> 3) & 1) << 2));
+  if constexpr (CH >= 16) return (2 * (r & 3)) | ((r >> 2) & 1) | (((r >> 3) & 1) << 3);
   else if constexpr (CH == 8) return 2 * (((r >> 1) & 1) | (((r >> 3) & 1) << 1));
   else if constexpr (CH == 4) return 2 * ((r >> 3) & 1);
   else return 0;
@@ -210,14 +241,18 @@ __device__ __forceinline__ bf16x4 ds_read_tr4(const bf16* p) {
   return __builtin_bit_cast(bf16x4, v);
 }
 
+// The fragment helpers take the lane index as a defaulted argument so that a
+// persistent kernel can pass a per-iteration value (keeping the address
+// arithmetic inside its loop instead of hoisted and held in registers).
+
 // Operand fragment of a contraction over rows r0 .. r0 + 31 of a swizzled
 // row-major tile, for the 16 columns c0 .. c0 + 15 (lane l: column c0 + (l & 15),
 // rows r0 + 8 (l >> 4) .. + 7).  Serves as the A operand of X^T Y (output
 // rows = columns of X) and as the B operand of X^T Y (output columns =
 // columns of Y).
 template <int CH>
-__device__ __forceinline__ bf16x8 frag_tr(const bf16* tile, int r0, int c0) {
-  const int l = lane_id(), i = l & 15;
+__device__ __forceinline__ bf16x8 frag_tr(const bf16* tile, int r0, int c0, int l = lane_id()) {
+  const int i = l & 15;
   const int r = r0 + 8 * (l >> 4) + (i >> 2);
   const int col = c0 + 4 * (i & 3);
   const bf16x4 a = ds_read_tr4(tile + tr_off<CH>(r, col));
@@ -226,13 +261,33 @@ __device__ __forceinline__ bf16x8 frag_tr(const bf16* tile, int r0, int c0) {
 }
 
 // The same fragment from a padded row-major tile of pitch ld elements.
-__device__ __forceinline__ bf16x8 frag_tr_pitch(const bf16* tile, int ld, int r0, int c0) {
-  const int l = lane_id(), i = l & 15;
+__device__ __forceinline__ bf16x8 frag_tr_pitch(const bf16* tile, int ld, int r0, int c0, int l = lane_id()) {
+  const int i = l & 15;
   const int r = r0 + 8 * (l >> 4) + (i >> 2);
   const int col = c0 + 4 * (i & 3);
   const bf16x4 a = ds_read_tr4(tile + r * ld + col);
   const bf16x4 b = ds_read_tr4(tile + (r + 4) * ld + col);
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Row fragment of a swizzled tile: lane l reads row r0 + (l & 15), columns
+// c0 + 8 (l >> 4) .. + 7 (the A/B operand layout of the K = 32 MFMA with the
+// contraction running along the row).
+template <int CH>
+__device__ __forceinline__ bf16x8 frag_row(const bf16* tile, int r0, int c0, int l = lane_id()) {
+  return *reinterpret_cast<const bf16x8*>(tile + tr_off<CH>(r0 + (l & 15), c0 + 8 * (l >> 4)));
+}
+
+// Direct HBM -> LDS copy (no registers) of rows r0 .. r0 + 3 of a [.][128] bf16
+// tile whose rows sit `ld` elements apart in HBM, into the swizzled CH = 16
+// layout.  One wave instruction writes 1 KiB of LDS, lane l the 16 bytes at
+// l * 16 from the tile row r0, so the lane fetches the HBM chunk that the
+// swizzle places there.  r0 must be wave-uniform; completion is tracked by
+// vmcnt like any vector load.
+__device__ __forceinline__ void dma_rows4(bf16* tile, int r0, const bf16* src, size_t ld, int l = lane_id()) {
+  const int r = r0 + (l >> 4);
+  const bf16* s = src + (size_t)r * ld + 8 * ((l & 15) ^ tr_swz<16>(r));
+  __builtin_amdgcn_global_load_lds(s, (__attribute__((address_space(3))) void*)(tile + r0 * 128), 16, 0, 0);
 }
 
 // 16-byte piece (8 bf16) of row r, chunk c of a swizzled tile
