@@ -60,17 +60,15 @@ enum GateModeC { CG_NONE = 0, CG_SCALAR = 1, CG_VECTOR = 2 };
 
 namespace post {
 constexpr int LDT = 72;    // bf16 pitch of [.][64] tiles
-constexpr int LDV = 136;   // bf16 pitch of [.][128] tiles
-constexpr int LDG = 132;   // fp32 pitch of the row-major [64][128] gate tile (rows 4 apart: distinct banks)
 constexpr int T64 = C * LDT * 2;     // bytes of one [64][72] bf16 tile
 constexpr int T128 = KD * LDT * 2;   // bytes of one [128][72] bf16 tile
-constexpr int R64 = C * LDV * 2;     // bytes of one [64][136] bf16 tile
 }  // namespace post
 
 template <int GATE, bool VEC_B, bool INTRA = false, bool PIPE = false>
 struct PostLayout {
-  // PIPE: dR, R and dO sit in a separate buffer of the persistent kernel, filled
-  // by direct HBM -> LDS copies while the previous chunk-head finishes.
+  // PIPE (persistent kernel): dR, R, dO sit in a separate buffer X filled by
+  // direct HBM -> LDS copies while the previous chunk-head finishes, and q, k, g
+  // are copied the same way into region B at the start of the chunk-head.
   // region A.  phases 0-1: A hi/lo [t][s] (and, unpipelined, dR swizzled).
   //            phases 2+:  L, D row-major hi/lo, and (GDN2) L^T, D^T hi/lo.
   // GDN2 keeps explicit L^T / D^T copies (measured faster for its register budget);
@@ -84,22 +82,53 @@ struct PostLayout {
   static constexpr int A1 = 2 * C * C * 2 + (PIPE ? 0 : TQ);
   static constexpr int A2 = (LT_COPY ? 8 : 4) * post::T64;
   static constexpr int REGION_A = A1 > A2 ? A1 : A2;
-  // region B.  phases 0-3: P row-major (pitch LDV) (, unpipelined: R, dO swizzled).
-  //            phases 3+:  q, k (, b) swizzled, vector g row-major fp32.
-  static constexpr int OFF_P = REGION_A, OFF_R = REGION_A + post::R64, OFF_DO = OFF_R + TQ;
-  static constexpr int GT_BYTES = GATE == CG_VECTOR ? C * post::LDG * 4 : 0;
-  static constexpr int OFF_QT = REGION_A, OFF_KT = REGION_A + TQ, OFF_GT = REGION_A + 2 * TQ;
+  // region B (offsets from its start).  Unpipelined, phases 0-3: P, R, dO swizzled.
+  // Phases 3+ (from phase 0 when pipelined): q, k (, b) swizzled, vector g (fp32, g_off).
+  static constexpr int OFF_P = 0, OFF_R = TQ, OFF_DO = 2 * TQ;
+  static constexpr int GT_BYTES = GATE == CG_VECTOR ? C * KD * 4 : 0;
+  static constexpr int OFF_QT = 0, OFF_KT = TQ, OFF_GT = 2 * TQ;
   static constexpr int OFF_BT = OFF_GT + GT_BYTES;
-  static constexpr int B1 = post::R64 + (PIPE ? 0 : 2 * TQ);
+  static constexpr int B1 = PIPE ? 0 : 3 * TQ;
   static constexpr int B2 = 2 * TQ + GT_BYTES + (VEC_B ? TQ : 0);
-  static constexpr int OFF_SMALL = REGION_A + (B1 > B2 ? B1 : B2);
-  static constexpr int S_BETA = 0, S_G = 64, S_DBA = 128, S_DBB = 192, S_DG = 256, S_COL = 320,
-                       S_TOT = 448, S_GL = 576, S_ANY = 704, S_N = 712;
-  static constexpr int BYTES = OFF_SMALL + S_N * 4;        // dynamic LDS
-  static constexpr int X_BYTES = PIPE ? 3 * TQ : 0;        // static LDS of the persistent kernel
-  static constexpr bool FITS = BYTES + X_BYTES <= 160 * 1024;
+  static constexpr int REGION_B = B1 > B2 ? B1 : B2;
+  // small per-row arrays (floats)
+  static constexpr int S_BETA = 0, S_G = 64, S_DBA = 128, S_DBB = 384, S_DG = 448, S_GL = 960,
+                       S_ANY = 1088, S_N = 1096;
+  static constexpr int SMALL = S_N * 4;
+  static constexpr int X_BYTES = PIPE ? 3 * TQ : 0;
+  static constexpr int BYTES = REGION_A + REGION_B + SMALL + X_BYTES;
+  static constexpr bool FITS = BYTES <= 160 * 1024;
   static_assert(PIPE || FITS, "LDS budget");
 };
+
+// fp32 gate tile [64][128] without padding: the 16-byte chunk c of row r sits at
+// chunk c ^ 4 ((r >> 2) & 3), so the 4 rows 4 apart that one read of 16
+// consecutive columns touches fall on distinct banks.
+__device__ __forceinline__ int g_off(int r, int col) {
+  return r * KD + ((((col >> 2) ^ (((r >> 2) & 3) << 2))) << 2) + (col & 3);
+}
+
+// LDS stores the compiler does not see as such.  It orders every LDS write it
+// cannot prove disjoint from an outstanding direct-to-LDS copy behind that copy
+// (vmcnt); for the few writes whose alias information it loses (merged
+// stores), these keep the persistent kernel's copies in flight.  LDS accesses
+// complete in order, so the compiler's own lgkmcnt waits stay correct.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(size_t)(const __attribute__((address_space(3))) char*)p;
+}
+__device__ __forceinline__ void lds_st(float* p, float v) {
+  asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_st(bf16* p, bf16x4 v) {
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  asm volatile("ds_write_b64 %0, %1" ::"v"(lds_addr(p)), "v"(__builtin_bit_cast(u2, v)) : "memory");
+}
+
+// Work-group barrier for LDS only, written as one asm block: the compiler's
+// fences at a barrier wait for outstanding direct-to-LDS copies, which the
+// persistent kernel keeps in flight across barriers on purpose (each copy is
+// waited for explicitly, with vmcnt, before the barrier that publishes it).
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Position of one (batch, chunk, head) work item in the T-major tensors.  Heads
 // run fastest: work-groups in flight together read neighbouring heads of the
@@ -152,6 +181,44 @@ __device__ __forceinline__ void load_phase_in(const float* __restrict__ akk, con
   }
 }
 
+// A hi/lo into the [t][s] tiles read transposed by phase 1
+__device__ __forceinline__ void stage_akk(const PhaseIn& pin, bf16* sAh, bf16* sAl, int tid) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = tid + 512 * i;
+    const int t = p >> 4, ch = p & 15;
+    bf16x4 lo;
+    const bf16x4 hi = split_hi4(pin.a[i], lo);
+    *reinterpret_cast<bf16x4*>(sAh + tr_off<8>(t, 4 * ch)) = hi;
+    *reinterpret_cast<bf16x4*>(sAl + tr_off<8>(t, 4 * ch)) = lo;
+  }
+}
+
+// s_waitcnt immediate for vmcnt(n) alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14)
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// q, k of one item into swizzled [64][128] tiles, vector g into the g_off tile
+template <int GATE>
+__device__ __forceinline__ void dma_qkg(bf16* sQ, bf16* sK, float* sGr, const bf16* __restrict__ q,
+                                        const bf16* __restrict__ k, const float* __restrict__ g,
+                                        const ChunkItem& it, int H, int tid) {
+  const size_t rsk = (size_t)H * KD;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    dma_rows4(sQ, 8 * w + 4 * j, q + it.kofs, rsk, l);
+    dma_rows4(sK, 8 * w + 4 * j, k + it.kofs, rsk, l);
+  }
+  if constexpr (GATE == CG_VECTOR) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {       // 2 rows of 512 bytes per instruction
+      const int r0 = 8 * w + 2 * j, r = r0 + (l >> 5), pc = l & 31;
+      const float* src = g + it.kofs + (size_t)r * rsk + 4 * (pc ^ (((r >> 2) & 3) << 2));
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sGr + r0 * KD), 16, 0, 0);
+    }
+  }
+}
+
 // dR, R = v_new and dO of one item into the swizzled [64][128] tiles x[0..2]:
 // wave w copies rows 8 w .. 8 w + 7 of each
 __device__ __forceinline__ void dma_x(bf16* xbuf, const bf16* __restrict__ dR, const bf16* __restrict__ vnew,
@@ -179,20 +246,20 @@ __device__ __forceinline__ void chunk_body(
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
     bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale,
     const float* __restrict__ daqk, float* __restrict__ dq32, float* __restrict__ dk32,
-    float* __restrict__ db32, int beta_complete, int item, int next_item, bf16* xbuf, PhaseIn& pin) {
+    float* __restrict__ db32, int beta_complete, int item, int next_item, char* regA, char* regB,
+    float* small, bf16* xbuf, PhaseIn& pin) {
   using LY = PostLayout<GATE, VEC_B, INTRA, PIPE>;
   using post::LDT;
-  using post::LDV;
-  using post::LDG;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  auto B16 = [&](int off) { return reinterpret_cast<bf16*>(smem + off); };
-  auto U32 = [&](int off) { return reinterpret_cast<uint32_t*>(smem + off); };
+  auto B16 = [&](int off) { return reinterpret_cast<bf16*>(regA + off); };
+  auto B16b = [&](int off) { return reinterpret_cast<bf16*>(regB + off); };
   bf16* sAh = B16(LY::OFF_AKTH);    // A rows [s][t], hi
   bf16* sAl = B16(LY::OFF_AKTL);    // A rows, lo
   // dR, R, dO rows [t][v], swizzled: the persistent kernel's prefetch buffer, or staged here
   bf16* sdR = PIPE ? xbuf : B16(LY::OFF_DRT);
-  bf16* sR = PIPE ? xbuf + C * KD : B16(LY::OFF_R);
-  bf16* sdO = PIPE ? xbuf + 2 * C * KD : B16(LY::OFF_DO);
+  bf16* sR = PIPE ? xbuf + C * KD : B16b(LY::OFF_R);
+  bf16* sdO = PIPE ? xbuf + 2 * C * KD : B16b(LY::OFF_DO);
+  // P rows [t][v], swizzled: over dR once phase 1 has read it (persistent kernel)
+  bf16* sP = PIPE ? xbuf : B16b(LY::OFF_P);
   bf16* Lrh = B16(LY::OFF_LRH);
   bf16* Lrl = B16(LY::OFF_LRL);
   bf16* Drh = B16(LY::OFF_DRH);
@@ -201,19 +268,15 @@ __device__ __forceinline__ void chunk_body(
   bf16* Ltl = B16(LY::OFF_LTL);
   bf16* Dth = B16(LY::OFF_DTH);
   bf16* Dtl = B16(LY::OFF_DTL);
-  bf16* sP = B16(LY::OFF_P);
-  bf16* sQ = B16(LY::OFF_QT);       // q rows [t][k] (swizzled)
-  bf16* sK = B16(LY::OFF_KT);       // k rows
-  float* sGr = reinterpret_cast<float*>(smem + LY::OFF_GT);   // g rows [t][k], pitch LDG
-  bf16* sB = B16(LY::OFF_BT);       // erase-gate rows (GDN2)
-  float* small = reinterpret_cast<float*>(smem + LY::OFF_SMALL);
+  bf16* sQ = B16b(LY::OFF_QT);      // q rows [t][k] (swizzled)
+  bf16* sK = B16b(LY::OFF_KT);      // k rows
+  float* sGr = reinterpret_cast<float*>(regB + LY::OFF_GT);   // g rows [t][k] (g_off)
+  bf16* sB = B16b(LY::OFF_BT);      // erase-gate rows (GDN2)
   float* sBeta = small + LY::S_BETA;   // scalar beta per row
   float* sG = small + LY::S_G;         // scalar gate per row (log2)
-  float* sDbA = small + LY::S_DBA;     // sum_v P R           (beta != 0 rows)
+  float* sDbA = small + LY::S_DBA;     // [4][64] sum_v P R per column strip (beta != 0 rows)
   float* sDbB = small + LY::S_DBB;     // direct dbeta terms  (beta ~ 0 rows)
-  float* sDg = small + LY::S_DG;       // scalar gate: dG row sums
-  float* sCol = small + LY::S_COL;     // [128] column partials from the upper row half
-  float* sTot = small + LY::S_TOT;     // [128] column totals of the lower row half
+  float* sDg = small + LY::S_DG;       // [8][64] scalar gate: dG row sums per wave
   float* sGl = small + LY::S_GL;       // [128] last-row gate (log2) per column
   int* sAny = reinterpret_cast<int*>(small + LY::S_ANY);   // [8] per-wave "some beta ~ 0" flags
 
@@ -233,6 +296,19 @@ __device__ __forceinline__ void chunk_body(
   const size_t kofs = pos.kofs;    // [t][k] tensors of this chunk-head
   const size_t vofs = pos.vofs;    // [t][v] tensors
   const bf16* vb = v + vofs;
+  const int kk = 16 * wv + lc;                 // this lane's key column from phase 3 on
+  // state tiles for phase 3: wave wv owns key columns [16 wv, 16 wv + 16).  The
+  // persistent kernel loads them first, ahead of this item's q, k, g copies.
+  bf16x8 fh[4], fdh[4];
+  auto load_state = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const size_t o = hoff + (size_t)kk * VD + 32 * ks + 8 * lg;
+      fh[ks] = *reinterpret_cast<const bf16x8*>(hst + o);
+      fdh[ks] = *reinterpret_cast<const bf16x8*>(dhst + o);
+    }
+  };
+  if constexpr (PIPE) load_state();
 
   // ---------------- phase 0: stage A (hi/lo), dR, R, dO row-major; beta, gates ----------------
   int any_fb = 0;
@@ -262,15 +338,15 @@ __device__ __forceinline__ void chunk_body(
       sDbB[tid] = 0.f;
     }
   } else {
-    if constexpr (!PIPE) load_phase_in<GATE, VEC_B>(akk, beta, g, pos, H, tid, pin);
+    // (the persistent kernel stages A hi/lo at the end of the previous item)
+    if constexpr (!PIPE) {
+      load_phase_in<GATE, VEC_B>(akk, beta, g, pos, H, tid, pin);
+      stage_akk(pin, sAh, sAl, tid);
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + 512 * i;        // 1024 16-byte pieces per tile; lanes run along rows
       const int t = p >> 4, ch = p & 15;
-      bf16x4 lo;
-      const bf16x4 hi = split_hi4(pin.a[i], lo);
-      *reinterpret_cast<bf16x4*>(sAh + tr_off<8>(t, 4 * ch)) = hi;
-      *reinterpret_cast<bf16x4*>(sAl + tr_off<8>(t, 4 * ch)) = lo;
       if constexpr (!PIPE) {
         const size_t o = vofs + (size_t)t * rsv + 8 * ch;
         store_tr_chunk<16>(sdR, t, ch, *reinterpret_cast<const u32x4*>(dR + o));
@@ -285,21 +361,21 @@ __device__ __forceinline__ void chunk_body(
         fb = fabsf(pin.beta) < 1e-6f;
       }
       if constexpr (GATE == CG_SCALAR) sG[tid] = pin.g;
-      sDbA[tid] = 0.f;
       sDbB[tid] = 0.f;
-      sDg[tid] = 0.f;
     }
     if (tid < KD) sGl[tid] = pin.gl;
     // block-uniform: some row has |beta| < 1e-6 (one flag per wave, then a barrier)
     const unsigned long long fbw = __ballot(fb);
     if (l == 0) sAny[wv] = fbw != 0ull;
-    lds_barrier();
+    lds_sync();
 #pragma unroll
     for (int w = 0; w < 8; ++w) any_fb |= sAny[w];
+    // persistent kernel: this item's q, k, g stream into region B during phases
+    // 1-3 (issued after this phase's LDS writes, see dma_x's call below)
+    if constexpr (PIPE) dma_qkg<GATE>(sQ, sK, sGr, q, k, g, pos, H, tid);
   }
   // the standalone intra adds the direct dbeta terms of every row
   const bool has_fb = !VEC_B && (INTRA || any_fb != 0);
-  const int kk = 16 * wv + lc;                 // this lane's key column from phase 3 on
   f32x4 aq[4], ak[4], aw[4];                   // dq, dk, dG of column kk, rows 16 I + 4 lg + r
   float dgk = 0.f;
 
@@ -307,13 +383,19 @@ __device__ __forceinline__ void chunk_body(
 
   // ---------------- phase 1: P^T = dR^T A  (accumulator layout stores P row-major) ----------------
   {
+    // LDS writes of P wait until every wave has read dR (P takes its place when
+    // pipelined); the LDS partial sums of sum_v P R are plain stores (one per
+    // column strip), which keeps LDS atomics out of the prefetch window
+    f32x4 pacc[2][2];
+    float pra[2] = {0.f, 0.f};
 #pragma unroll
     for (int vt = 0; vt < 2; ++vt) {
       const int vrow0 = 32 * cs + 16 * vt;
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         const int tcol0 = 32 * rh + 16 * tt;
-        f32x4 acc = zero4();
+        f32x4& acc = pacc[vt][tt];
+        acc = zero4();
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           if (ks == 0 && rh == 1) continue;    // A^T upper triangular: s < 32 <= t vanishes
@@ -324,10 +406,6 @@ __device__ __forceinline__ void chunk_body(
         // lane: t = tcol0 + lc, v = vrow0 + 4 lg .. +3
         const int t = tcol0 + lc;
         const int v0 = vrow0 + 4 * lg;
-        bf16x4 p4;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) p4[r] = to_bf16(acc[r]);
-        *reinterpret_cast<bf16x4*>(sP + t * LDV + v0) = p4;
         const size_t go = (size_t)t * rsv + v0;
         if constexpr (VEC_B) {
           const bf16x4 w4 = *reinterpret_cast<const bf16x4*>(wgate + vofs + go);
@@ -351,8 +429,7 @@ __device__ __forceinline__ void chunk_body(
             pr += acc[r] * to_f32(r4[r]);
           }
           *reinterpret_cast<bf16x4*>(dv_out + vofs + go) = o1;
-          pr = sum_lane_groups(pr, l);
-          if (lg == 0) atomicAdd(&sDbA[t], pr);
+          pra[tt] += sum_lane_groups(pr, l);
           if (has_fb) {
             const bf16x4 x4 = *reinterpret_cast<const bf16x4*>(vb + go);
             float pv = 0.f;
@@ -364,17 +441,26 @@ __device__ __forceinline__ void chunk_body(
         }
       }
     }
-  }
-  lds_barrier();
-
-  // prefetch state tiles for phase 3: wave wv owns key columns [16 wv, 16 wv + 16)
-  bf16x8 fh[4], fdh[4];
+    if constexpr (!VEC_B) {
+      if (lg == 0) {
+        lds_st(sDbA + 64 * cs + 32 * rh + lc, pra[0]);
+        lds_st(sDbA + 64 * cs + 32 * rh + 16 + lc, pra[1]);
+      }
+    }
+    if constexpr (PIPE) lds_sync();       // dR read by every wave: P overwrites it
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const size_t o = hoff + (size_t)kk * VD + 32 * ks + 8 * lg;
-    fh[ks] = *reinterpret_cast<const bf16x8*>(hst + o);
-    fdh[ks] = *reinterpret_cast<const bf16x8*>(dhst + o);
+    for (int vt = 0; vt < 2; ++vt)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        bf16x4 p4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p4[r] = to_bf16(pacc[vt][tt][r]);
+        lds_st(sP + tr_off<16>(32 * rh + 16 * tt + lc, 32 * cs + 16 * vt + 4 * lg), p4);
+      }
   }
+  lds_sync();
+
+  if constexpr (!PIPE) load_state();
 
   // ---------------- phase 2: L = scale tril(dO R^T), D = -strict_tril(P R^T), both orientations ----------------
   {
@@ -395,7 +481,7 @@ __device__ __forceinline__ void chunk_body(
         for (int ks = 0; ks < 4; ++ks) {
           const bf16x8 br = frag_row<16>(sR, 16 * J, 32 * ks, l);
           aL = mfma(frag_row<16>(sdO, 16 * I, 32 * ks, l), br, aL);
-          aD = mfma(frag(sP + (16 * I) * LDV + 32 * ks, LDV, l), br, aD);
+          aD = mfma(frag_row<16>(sP, 16 * I, 32 * ks, l), br, aD);
         }
       }
       if (lowerB) {
@@ -403,7 +489,7 @@ __device__ __forceinline__ void chunk_body(
         for (int ks = 0; ks < 4; ++ks) {
           const bf16x8 ar = frag_row<16>(sR, 16 * I, 32 * ks, l);
           bL = mfma(ar, frag_row<16>(sdO, 16 * J, 32 * ks, l), bL);
-          bD = mfma(ar, frag(sP + (16 * J) * LDV + 32 * ks, LDV, l), bD);
+          bD = mfma(ar, frag_row<16>(sP, 16 * J, 32 * ks, l), bD);
         }
       }
       if constexpr (LY::LT_COPY) {
@@ -464,7 +550,7 @@ __device__ __forceinline__ void chunk_body(
       for (int ks = 0; ks < 4; ++ks) {
         x = mfma(frag_row<16>(sdO, 16 * I, 32 * ks, l), fh[ks], x);
         y = mfma(frag_row<16>(sR, 16 * I, 32 * ks, l), fdh[ks], y);
-        z = mfma(frag(sP + (16 * I) * LDV + 32 * ks, LDV, l), fh[ks], z);
+        z = mfma(frag_row<16>(sP, 16 * I, 32 * ks, l), fh[ks], z);
       }
       aq[I] = x;
       ak[I] = y;
@@ -473,46 +559,50 @@ __device__ __forceinline__ void chunk_body(
   }
   }   // !INTRA: phases 1-3
 
-  // q, k, g (and b) rows for the row-major staging (issued before the barrier)
-  u32x4 rq[2], rk[2], rb[2];
-  f32x4 rg[4];
+  if constexpr (PIPE) {
+    // q, k, g were copied into region B at the item start: each wave waits for
+    // its own copies, the barrier publishes them (and retires P, R, dO)
+    __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
+    lds_sync();
+    // The next item's dR, R, dO stream into X during phases 4-6 (the last item
+    // re-fetches its own rows: harmless, and no branch splits the vmcnt count).
+    dma_x(xbuf, dR, vnew, dO, ChunkItem(next_item >= 0 ? next_item : item, T, H), H, tid);
+  } else {
+    // q, k, g (and b) rows for the row-major staging (issued before the barrier)
+    u32x4 rq[2], rk[2], rb[2];
+    f32x4 rg[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int p = tid + 512 * i;
-    const size_t o = kofs + (size_t)(p >> 4) * rsk + (p & 15) * 8;
-    rq[i] = *reinterpret_cast<const u32x4*>(q + o);
-    rk[i] = *reinterpret_cast<const u32x4*>(k + o);
-    if constexpr (VEC_B) rb[i] = *reinterpret_cast<const u32x4*>(bgate + o);
-  }
-  if constexpr (GATE == CG_VECTOR) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = tid + 512 * i;              // 2048 pieces: token p >> 5, 4 columns
-      rg[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)(p >> 5) * rsk + (p & 31) * 4);
-    }
-  }
-  lds_barrier();   // P, R, dO no longer needed: region B becomes q, k, g (, b)
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int p = tid + 512 * i;
-    store_tr_chunk<16>(sQ, p >> 4, p & 15, rq[i]);
-    store_tr_chunk<16>(sK, p >> 4, p & 15, rk[i]);
-    if constexpr (VEC_B) store_tr_chunk<16>(sB, p >> 4, p & 15, rb[i]);
-  }
-  if constexpr (GATE == CG_VECTOR) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
       const int p = tid + 512 * i;
-      *reinterpret_cast<f32x4*>(sGr + (p >> 5) * LDG + (p & 31) * 4) = rg[i];
+      const size_t o = kofs + (size_t)(p >> 4) * rsk + (p & 15) * 8;
+      rq[i] = *reinterpret_cast<const u32x4*>(q + o);
+      rk[i] = *reinterpret_cast<const u32x4*>(k + o);
+      if constexpr (VEC_B) rb[i] = *reinterpret_cast<const u32x4*>(bgate + o);
     }
+    if constexpr (GATE == CG_VECTOR) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = tid + 512 * i;              // 2048 pieces: token p >> 5, 4 columns
+        rg[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)(p >> 5) * rsk + (p & 31) * 4);
+      }
+    }
+    lds_sync();   // P, R, dO no longer needed: region B becomes q, k, g (, b)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + 512 * i;
+      store_tr_chunk<16>(sQ, p >> 4, p & 15, rq[i]);
+      store_tr_chunk<16>(sK, p >> 4, p & 15, rk[i]);
+      if constexpr (VEC_B) store_tr_chunk<16>(sB, p >> 4, p & 15, rb[i]);
+    }
+    if constexpr (GATE == CG_VECTOR) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = tid + 512 * i;
+        *reinterpret_cast<f32x4*>(sGr + g_off(p >> 5, (p & 31) * 4)) = rg[i];
+      }
+    }
+    lds_sync();
   }
-  lds_barrier();
-  // The next item's dR, R, dO stream into the prefetch buffer during phases 4-6
-  // (the last item re-fetches its own rows: harmless, and no branch splits the
-  // vmcnt count).  Issued after the barrier: a barrier's LDS fence waits for
-  // outstanding direct-to-LDS copies, and so does any LDS write the compiler
-  // cannot prove disjoint from them.
-  if constexpr (PIPE) dma_x(xbuf, dR, vnew, dO, ChunkItem(next_item >= 0 ? next_item : item, T, H), H, tid);
 
   // ---------------- per-lane operands of column kk, rows 16 J + 4 lg + j ----------------
   // In the accumulator layout and in the B layout of the K=16 MFMA a lane holds the
@@ -525,7 +615,7 @@ __device__ __forceinline__ void chunk_body(
     const int r0 = 16 * J + 4 * lg;
     if constexpr (GATE == CG_VECTOR) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) g4[J][j] = sGr[(r0 + j) * LDG + kk];
+      for (int j = 0; j < 4; ++j) g4[J][j] = sGr[g_off(r0 + j, kk)];
     }
     else if constexpr (GATE == CG_SCALAR) g4[J] = *reinterpret_cast<const f32x4*>(sG + r0);
     else g4[J] = zero4();
@@ -772,11 +862,11 @@ __device__ __forceinline__ void chunk_body(
 #pragma unroll 1
         for (int r = 0; r < 4; ++r) {
           const int i = 16 * I + 4 * lg + r;
-          const float gi = sGr[i * LDG + kk];
+          const float gi = sGr[g_off(i, kk)];
           float pq = 0.f, pe = 0.f, pk = 0.f;
 #pragma unroll 1
           for (int s = 16 * I; s < 16 * (I + 1); ++s) {
-            const float gs = sGr[s * LDG + kk];
+            const float gs = sGr[g_off(s, kk)];
             const float ksv = to_f32(sK[tr_off<16>(s, kk)]);
             if (s <= i) {
               const float f = fast_exp2(gi - gs);
@@ -849,17 +939,17 @@ __device__ __forceinline__ void chunk_body(
       carry += t0 + t1 + t2 + t3;
     }
   } else if constexpr (GATE == CG_SCALAR) {
-    // scalar gate: dG row sums over all 128 columns, then the last-row state term
+    // scalar gate: dG row sums over this wave's 16 columns (one partial per wave),
+    // the last row adding the state term
+    const float term = sum_row16(fast_exp2(gl) * dgk + colkdk);
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float s = sum_row16(aw[I][r]);
-        if (lc == 0) atomicAdd(&sDg[16 * I + 4 * lg + r], s);
+        float s = sum_row16(aw[I][r]);
+        if (I == 3 && r == 3 && lg == 3) s += term;
+        if (lc == 0) lds_st(sDg + 64 * wv + 16 * I + 4 * lg + r, s);
       }
-    float term = fast_exp2(gl) * dgk + colkdk;
-    term = sum_row16(term);
-    if (l == 0) atomicAdd(&sDg[C - 1], term);
   }
   }   // !INTRA: phase 6
 
@@ -868,6 +958,7 @@ __device__ __forceinline__ void chunk_body(
     // rows; its A goes to registers before this item's stores are issued
     __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
     load_phase_in<GATE, VEC_B>(akk, beta, g, ChunkItem(next_item >= 0 ? next_item : item, T, H), H, tid, pin);
+    asm volatile("" ::: "memory");          // the loads stay ahead of the stores below
   }
   // stores of dq, dk (bf16), the vector dg (fp32) and db (bf16); 32-bit offsets
   // from uniform per-chunk-head bases
@@ -901,7 +992,16 @@ __device__ __forceinline__ void chunk_body(
       }
     }
   }
-  lds_barrier();   // sDbB, sDg complete
+  lds_sync();   // sDbB, sDg complete; every wave is past phase 5 (region A free)
+  if constexpr (PIPE) {
+    // The next item's A: wait for its loads (issued ahead of this item's stores,
+    // one store per row and output below) without waiting for the stores, and
+    // stage it into region A.
+    constexpr int STORES = 16 * (2 + (GATE == CG_VECTOR ? 1 : 0) + (VEC_B ? 1 : 0));
+    static_assert(STORES < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(STORES));
+    stage_akk(pin, sAh, sAl, tid);
+  }
   if (INTRA && tid < C) {
     // endpoint_intra.py:190-194: every row, or only |beta| < 1e-6 rows when the
     // residual producer already accounted for the rest (beta_complete)
@@ -913,17 +1013,26 @@ __device__ __forceinline__ void chunk_body(
     const size_t row = (tok0 + tid) * H + h;
     if constexpr (!VEC_B) {
       const float be = sBeta[tid];
-      dbeta_out[row] = fabsf(be) < 1e-6f ? sDbB[tid] : sDbA[tid] / be;
+      const float pr = (sDbA[tid] + sDbA[64 + tid]) + (sDbA[128 + tid] + sDbA[192 + tid]);
+      dbeta_out[row] = fabsf(be) < 1e-6f ? sDbB[tid] : pr / be;
     }
     if constexpr (GATE == CG_SCALAR) {
-      float acc = 0.f;
-      for (int s = C - 1; s >= tid; --s) acc += sDg[s];
-      dg_out[row] = acc;
+      // row sums over the 8 waves' partials, then the reverse cumsum over the
+      // 64 rows as a suffix scan across the lanes of wave 0
+      float x = 0.f;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) x += sDg[64 * w + tid];
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float y = lane_read(x, l + d < 64 ? l + d : 63);
+        if (l + d < 64) x += y;
+      }
+      dg_out[row] = x;
     }
   }
   // persistent kernel: every wave's prefetch complete and this item's LDS reads
   // done before the next item's phase 0
-  if constexpr (PIPE) lds_barrier();
+  if constexpr (PIPE) lds_sync();
 }
 
 template <int GATE, bool VEC_B>
@@ -935,16 +1044,21 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     const bf16* __restrict__ dhst, bf16* __restrict__ dq_out, bf16* __restrict__ dk_out,
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
     bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale) {
+  using LY = PostLayout<GATE, VEC_B>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
   chunk_body<GATE, VEC_B, false>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
                                  dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale, nullptr,
-                                 nullptr, nullptr, nullptr, 0, blockIdx.x, -1, nullptr, pin);
+                                 nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
+                                 reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, pin);
 }
 
 // Persistent form: one work-group per CU walks the items blockIdx.x, + gridDim.x, ...
-// and copies the next item's dR, R, dO straight into LDS (and its A into
-// registers) while the current one computes phases 4-6, so that HBM reads overlap
-// the intra and epilogue work instead of stalling the work-group.
+// Its LDS regions are separate static arrays (so the compiler can tell them
+// apart); the next item's dR, R, dO are copied straight into LDS (and its A and
+// per-row scalars into registers) while the current one computes phases 4-6, and
+// an item's q, k, g while it computes phases 0-3, so that HBM reads overlap the
+// matrix work instead of stalling the work-group.
 template <int GATE, bool VEC_B>
 __global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
@@ -954,7 +1068,11 @@ __global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
     const bf16* __restrict__ dhst, bf16* __restrict__ dq_out, bf16* __restrict__ dk_out,
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
     bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale, int items) {
+  using LY = PostLayout<GATE, VEC_B, false, true>;
   __shared__ __attribute__((aligned(16))) bf16 xbuf[3 * C * KD];
+  __shared__ __attribute__((aligned(16))) char regA[LY::REGION_A];
+  __shared__ __attribute__((aligned(16))) char regB[LY::REGION_B];
+  __shared__ __attribute__((aligned(16))) float small[LY::S_N];
   PhaseIn pin;
   int it = blockIdx.x;
   if (it >= items) return;
@@ -963,14 +1081,16 @@ __global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
     dma_x(xbuf, dR, vnew, dO, first, H, threadIdx.x);
     load_phase_in<GATE, VEC_B>(akk, beta, g, first, H, threadIdx.x, pin);
     __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
-    lds_barrier();
+    stage_akk(pin, reinterpret_cast<bf16*>(regA + LY::OFF_AKTH), reinterpret_cast<bf16*>(regA + LY::OFF_AKTL),
+              threadIdx.x);
+    lds_sync();
   }
   for (; it < items; it += gridDim.x) {
     const int nx = it + (int)gridDim.x;
     chunk_body<GATE, VEC_B, false, true>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
                                          dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale,
-                                         nullptr, nullptr, nullptr, nullptr, 0, it, nx < items ? nx : -1, xbuf,
-                                         pin);
+                                         nullptr, nullptr, nullptr, nullptr, 0, it, nx < items ? nx : -1, regA,
+                                         regB, small, xbuf, pin);
   }
 }
 
@@ -980,11 +1100,14 @@ __global__ __launch_bounds__(512) void matrix_intra_kernel(
     const float* __restrict__ beta, const bf16* __restrict__ bgate, const float* __restrict__ daqk,
     const float* __restrict__ dakk, float* __restrict__ dq, float* __restrict__ dk,
     float* __restrict__ db, float* __restrict__ dg, int T, int H, int beta_complete) {
+  using LY = PostLayout<CG_VECTOR, VEC_B, true>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
   chunk_body<CG_VECTOR, VEC_B, true>(q, k, nullptr, nullptr, nullptr, nullptr, g, beta, bgate, nullptr, dakk,
                                      nullptr, nullptr, nullptr, nullptr, nullptr, dg, VEC_B ? nullptr : db,
                                      nullptr, nullptr, T, H, 1.f, daqk, dq, dk, VEC_B ? db : nullptr,
-                                     beta_complete, blockIdx.x, -1, nullptr, pin);
+                                     beta_complete, blockIdx.x, -1, smem, smem + LY::REGION_A,
+                                     reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, pin);
 }
 
 template <int GATE, bool VEC_B>
@@ -995,20 +1118,14 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
                               void* db, void* dw, int B, int T, int H, float scale, hipStream_t s) {
   const int items = B * H * (T / C);
   using LP = PostLayout<GATE, VEC_B, false, true>;
-  if constexpr (LP::FITS && REWY_CHUNK_PIPE) {
-    auto kern = chunk_bwd_pipe_kernel<GATE, VEC_B>;
-    static bool attr_set = false;
-    if (!attr_set) {
-      hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LP::BYTES);
-      if (e != hipSuccess) return e;
-      attr_set = true;
-    }
+  if constexpr (LP::FITS && REWY_CHUNK_PIPE && (GATE != CG_VECTOR || REWY_CHUNK_PIPE > 1)) {
+    auto kern = chunk_bwd_pipe_kernel<GATE, VEC_B>;    // static LDS only
     int dev = 0, cus = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return e;
     const int grid = items < cus ? items : cus;   // one work-group per CU (LDS-bound)
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), LP::BYTES, s, (const bf16*)q, (const bf16*)k,
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), 0, s, (const bf16*)q, (const bf16*)k,
                        (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta,
                        (const bf16*)bgate, (const bf16*)wgate, akk, (const bf16*)h, (const bf16*)dh,
                        (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, items);
