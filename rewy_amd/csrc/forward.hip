@@ -92,10 +92,10 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
     for (int r = 1; r < 16; ++r) v[r] += v[r - 1];
 #pragma unroll
     for (int r = 0; r < 16; ++r) sg[16 * part + r][col] = v[r];
-    __syncthreads();
+    lds_barrier();
     float carry = 0.f;
     for (int pp = 0; pp < part; ++pp) carry += sg[16 * pp + 15][col];
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float x = (v[r] + carry) * fwd::RCP_LN2;
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
       gc_out[(tok0 + l) * H + h] = x;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   auto gate = [&](int t, int kc) -> float {
     if constexpr (GATE == FG_VECTOR) return sg[t][kc];
@@ -137,7 +137,7 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
     for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
     if (l == 0) sWide[I] = m >= fwd::WIDE;
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 16 x 16 tiles (I, J), J <= I: Aqk and M by anchored MFMAs ----
   // tile list: (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0) (3,1) (3,2) (3,3); wave w: tiles w, w + 8
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
     aqk_out[mofs + (size_t)i * rsm + s] = 0.f;
     sM[i][s] = 0.f;
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- inverse of the unit lower-triangular I + M (fp32) ----
   // diagonal 16 x 16 blocks by forward substitution: wave 0, lane = (block, column)
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
     const int J = I + 1 + (tix - (I == 0 ? 0 : I == 1 ? 3 : 5));
     sX[16 * I + (e >> 4)][16 * J + (e & 15)] = 0.f;
   }
-  __syncthreads();
+  lds_barrier();
   // block rows I = 1..3: X_IJ = -X_II sum_{m = J}^{I-1} M_Im X_mJ, one wave per block
   for (int I = 1; I < 4; ++I) {
     if (wv < I) {
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) sX[16 * I + ri][16 * J + cj + e] = xo[e];
     }
-    __syncthreads();
+    lds_barrier();
   }
   // ---- Akk rows -> HBM ----
 #pragma unroll
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
   const int I = wv & 3, cb = 64 * (wv >> 2);
   f32x4 acc[4] = {zero4(), zero4(), zero4(), zero4()};
   for (int half = 0; half < 2; ++half) {
-    __syncthreads();
+    lds_barrier();
     // h rows [64 half .. 64 half + 64)
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
       const int r = p >> 4, c8 = (p & 15) * 8;
       store_tr_chunk<16>(shT, r, p & 15, *reinterpret_cast<const u32x4*>(hst + hoff + (size_t)(64 * half + r) * VD + c8));
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const bf16x8 ah = frag(&sqg[16 * I][64 * half + 32 * ks], LDK);

@@ -66,7 +66,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     sG[tid] = (GATE == RG_SCALAR) ? g[row] : 0.f;
     sB[tid] = VEC_B ? 0.f : beta[row];
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- stage E = b k 2^g, Z = w_gate v (bf16) and A (hi/lo) row-major, coalesced 16-byte rows ----
 #pragma unroll
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
       *reinterpret_cast<bf16x8*>(kg_out + kofs + (size_t)t * rsk + c0) = ok;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- w^T = E^T A^T, u^T = Z^T A^T: B operand = A rows (t), contiguous s, from LDS ----
   // wave wv: output rows (k or v) [32 wv, 32 wv + 32), all 64 token columns
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     } else {
       if (tid < KD) sm.lam[tid] = 1.f;
     }
-    if constexpr (GATE == RG_SCALAR) __syncthreads();
+    if constexpr (GATE == RG_SCALAR) lds_barrier();
 #pragma unroll
     for (int cc = 0; cc < DCT; ++cc) uc[cc] = ru[cc];
 #pragma unroll
@@ -315,7 +315,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
 
   load_chunk(0);
   for (int c = 0; c < NT; ++c) {
-    __syncthreads();
+    lds_barrier();
     stage_chunk();
     if (c + 1 < NT) load_chunk(c + 1);
     const size_t tok0 = (size_t)b * T + (size_t)c * C;
@@ -327,7 +327,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
       for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[ct][r]);
       *reinterpret_cast<bf16x4*>(&sm.hT[16 * ct + (l & 15)][16 * wv + 4 * (l >> 4)]) = v4;
     }
-    __syncthreads();
+    lds_barrier();
     // v_new tiles = u - w h
     if (has_dr) {
 #pragma unroll
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
         *reinterpret_cast<bf16x4*>(&sm.vT[16 * ct + (l & 15)][16 * drow + 4 * (l >> 4)]) = v4;
       }
     }
-    __syncthreads();
+    lds_barrier();
     // h <- lambda h + kg^T v_new
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {

@@ -134,7 +134,7 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
     } else {
       if (tid < KD) sm.lam[tid] = 1.f;
     }
-    if constexpr (GATE == GATE_SCALAR) __syncthreads();  // gam / gkf needed below
+    if constexpr (GATE == GATE_SCALAR) lds_barrier();  // gam / gkf needed below
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
 
   load_chunk(NT - 1);
   for (int c = NT - 1; c >= 0; --c) {
-    __syncthreads();                       // previous chunk done with every LDS tile
+    lds_barrier();                       // previous chunk done with every LDS tile
     stage_chunk();
     if (c > 0) load_chunk(c - 1);          // prefetch; consumed next iteration
     // dh (state at the end of chunk c) -> LDS, transposed, bf16
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
       for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[ct][r]);
       *reinterpret_cast<bf16x4*>(&sm.dhT[16 * ct + (l & 15)][16 * wv + 4 * (l >> 4)]) = v4;
     }
-    __syncthreads();
+    lds_barrier();
 
     // X = qg^T dO (independent of dh)
     f32x4 xq[NCT];
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
         *reinterpret_cast<bf16x4*>(&sm.drT[16 * ct + (l & 15)][16 * drow + 4 * (l >> 4)]) = v4;
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // dh <- lambda * dh + scale * X - w^T dR   (accumulated negated: -a + w^T dR)
 #pragma unroll
