@@ -38,14 +38,20 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     bf16* __restrict__ u_out, bf16* __restrict__ qg_out, bf16* __restrict__ kg_out,
     float* __restrict__ aqk_out, int T, int H, float scale) {
   using rec::LDT;
-  // E = b k 2^g and Z = w_gate v rows [t][.] in bf16 (rounded as FLA's recompute_w_u_fwd
-  // rounds k beta 2^g before its dot), swizzled for transposed reads; A rows hi/lo
+  // Scalar or no gate with scalar beta: k is staged raw and E = (beta k) 2^g is formed
+  // per operand fragment (one factor pair per token row), so Aqk reads k from LDS too
+  // instead of re-fetching it from HBM.
+  constexpr bool RAWK = GATE != RG_VECTOR && !VEC_B;
+  // E = b k 2^g (or raw k) and Z = w_gate v rows [t][.] in bf16 (E rounded as FLA's
+  // recompute_w_u_fwd rounds k beta 2^g before its dot), swizzled for transposed reads;
+  // A rows hi/lo
   __shared__ __attribute__((aligned(16))) bf16 eH[C * KD];
   __shared__ __attribute__((aligned(16))) bf16 zH[C * VD];
   __shared__ __attribute__((aligned(16))) bf16 sAh[C][LDT];
   __shared__ __attribute__((aligned(16))) bf16 sAl[C][LDT];
   __shared__ float sG[C];
   __shared__ float sB[C];
+  __shared__ __attribute__((aligned(16))) float sGe[C];   // RAWK: 2^g per row
 
   const int NT = T / C;
   const int blk = blockIdx.x;
@@ -63,8 +69,10 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
 
   if (tid < C) {
     const size_t row = (tok0 + tid) * H + h;
-    sG[tid] = (GATE == RG_SCALAR) ? g[row] : 0.f;
+    const float gv = (GATE == RG_SCALAR) ? g[row] : 0.f;
+    sG[tid] = gv;
     sB[tid] = VEC_B ? 0.f : beta[row];
+    sGe[tid] = (GATE == RG_SCALAR) ? fast_exp2(gv) : 1.f;
   }
   lds_barrier();
 
@@ -104,7 +112,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     bf16x8 eh, zh;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      eh[j] = to_bf16(be[j] * to_f32(kx[j]) * ge[j]);
+      eh[j] = RAWK ? kx[j] : to_bf16(be[j] * to_f32(kx[j]) * ge[j]);
       zh[j] = to_bf16(we[j] * to_f32(vx[j]));
     }
     store_tr_chunk<16>(eH, t, ch, __builtin_bit_cast(u32x4, eh));
@@ -153,8 +161,17 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         const int row0 = 32 * wv + 16 * rt;
-        const bf16x8 x0 = frag_tr<16>(srcH, 0, row0);    // E^T rows (k or v), over s
-        const bf16x8 x1 = frag_tr<16>(srcH, 32, row0);
+        bf16x8 x0 = frag_tr<16>(srcH, 0, row0);    // E^T rows (k or v), over s
+        bf16x8 x1 = frag_tr<16>(srcH, 32, row0);
+        if (RAWK && which == 0) {
+          // element e of the fragment is token row 8 (l >> 4) + e (+ 32)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int t0 = 8 * lg + e, t1 = t0 + 32;
+            x0[e] = to_bf16(sB[t0] * to_f32(x0[e]) * sGe[t0]);
+            x1[e] = to_bf16(sB[t1] * to_f32(x1[e]) * sGe[t1]);
+          }
+        }
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
           f32x4 acc = zero4();
@@ -183,7 +200,9 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           const bf16x8 a = *reinterpret_cast<const bf16x8*>(q + kofs + (size_t)(16 * I + lc) * rsk + 32 * ks + 8 * lg);
-          const bf16x8 bq = *reinterpret_cast<const bf16x8*>(k + kofs + (size_t)(16 * J + lc) * rsk + 32 * ks + 8 * lg);
+          bf16x8 bq;
+          if constexpr (RAWK) bq = frag_row<16>(eH, 16 * J, 32 * ks);
+          else bq = *reinterpret_cast<const bf16x8*>(k + kofs + (size_t)(16 * J + lc) * rsk + 32 * ks + 8 * lg);
           acc = mfma(a, bq, acc);
         }
       }
