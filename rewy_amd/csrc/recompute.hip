@@ -67,6 +67,14 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
   const size_t kofs = tok0 * rsk + (size_t)h * KD;
   const size_t vofs = tok0 * rsv + (size_t)h * VD;
 
+  // Aqk's q fragments (wave wv: row tile wv), fetched first so their latency hides
+  // behind the staging and the w/u products
+  bf16x8 qa[4];
+  if constexpr (WANT_AQK) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qa[ks] = *reinterpret_cast<const bf16x8*>(q + kofs + (size_t)(16 * wv + lc) * rsk + 32 * ks + 8 * lg);
+  }
   if (tid < C) {
     const size_t row = (tok0 + tid) * H + h;
     const float gv = (GATE == RG_SCALAR) ? g[row] : 0.f;
@@ -191,7 +199,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
 
   // ---- Aqk = scale tril(q k^T 2^(g_i - g_s)) for the scalar / no-gate families ----
   if constexpr (WANT_AQK) {
-    // wave wv: row tile I = wv, all four column tiles; operands straight from HBM
+    // wave wv: row tile I = wv, all four column tiles
     const int I = wv;
 #pragma unroll
     for (int J = 0; J < 4; ++J) {
@@ -199,7 +207,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
       if (J <= I) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(q + kofs + (size_t)(16 * I + lc) * rsk + 32 * ks + 8 * lg);
+          const bf16x8 a = qa[ks];
           bf16x8 bq;
           if constexpr (RAWK) bq = frag_row<16>(eH, 16 * J, 32 * ks);
           else bq = *reinterpret_cast<const bf16x8*>(k + kofs + (size_t)(16 * J + lc) * rsk + 32 * ks + 8 * lg);
