@@ -79,6 +79,15 @@ __device__ __forceinline__ int xcd_logical_block() {
   return (b % 8) * (n / 8) + b / 8;
 }
 
+// Redefines a register in place (an empty asm that reads and writes it).  A value
+// loaded for the next loop iteration is settled at the end of the current one,
+// after that iteration's stores are issued: the compiler then waits for the load
+// there, with an exact vector-memory count, instead of at the first use after the
+// loop back-edge, where its count merge can degrade to vmcnt(0) and also wait for
+// every store.
+template <class T>
+__device__ __forceinline__ void settle(T& x) { asm volatile("" : "+v"(x) : : "memory"); }
+
 // Work-group barrier that orders LDS only.  __syncthreads() fences every
 // address space, which makes each wave wait for all of its outstanding global
 // loads and stores (vmcnt 0) before the barrier; kernels whose waves share

@@ -237,6 +237,7 @@ struct FwdSmem {
   bf16 k[C * KD];          // kg rows (swizzled): A operand of kg^T v_new (over T, transposed reads)
   bf16 hT[BV][LDK];        // h^T:    B operand of w h
   bf16 vT[BV][LDT];        // v_new^T: B operand of kg^T v_new
+  bf16 u[C * BV];          // u rows [t][v] (swizzled): read transposed in the accumulator layout
   float lam[KD];
   float gam[C];
   float gkf[C];
@@ -281,17 +282,22 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
 
   u32x4 rw[2];
   u32x4 rk[2];
-  bf16x4 ru[DCT];      // this lane's u values of its v_new tiles (prefetched)
-  bf16x4 uc[DCT];      // the same for the chunk being processed
+  // u rows: 16-byte pieces, every lane one or more (clamped, so the counts are static)
+  constexpr int CHV = BV / 8;
+  constexpr int NPU = C * CHV;
+  constexpr int NU = (NPU + NTH - 1) / NTH;
+  u32x4 ru[NU];
   float rg_last = 0.f, rg_tok = 0.f;
   auto load_chunk = [&](int c) {
     const size_t tok0 = (size_t)b * T + (size_t)c * C;
     const bf16* wb = w + tok0 * rsk + (size_t)h * KD;
-    // gate first: its consumer (lambda) is the first thing staged
+    // gate first: its consumer (lambda) is the first thing staged.  Every lane
+    // issues the same loads (clamped indices): no branch makes the vector-memory
+    // wait counts lane- or wave-dependent.
     if constexpr (GATE == RG_VECTOR) {
-      if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
+      rg_last = g[((tok0 + C - 1) * H + h) * KD + (tid & (KD - 1))];
     } else if constexpr (GATE == RG_SCALAR) {
-      if (tid < C) rg_tok = g[(tok0 + tid) * H + h];
+      rg_tok = g[(tok0 + (tid & (C - 1))) * H + h];
       rg_last = g[(tok0 + C - 1) * H + h];
     }
 #pragma unroll
@@ -304,14 +310,10 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
       const int p = tid + NTH * i;
       rk[i] = *reinterpret_cast<const u32x4*>(k + tok0 * rsk + (size_t)h * KD + (size_t)(p >> 4) * rsk + (p & 15) * 8);
     }
-    if (has_dr) {
 #pragma unroll
-      for (int cc = 0; cc < DCT; ++cc)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 16 * drow + 4 * (l >> 4) + r;
-          ru[cc][r] = u[(tok0 + t) * rsv + (size_t)h * VD + v_base + 16 * (dct0 + cc) + (l & 15)];
-        }
+    for (int i = 0; i < NU; ++i) {
+      const int p = min(tid + NTH * i, NPU - 1);
+      ru[i] = *reinterpret_cast<const u32x4*>(u + (tok0 + p / CHV) * rsv + (size_t)h * VD + v_base + (p % CHV) * 8);
     }
   };
   auto stage_chunk = [&]() {
@@ -325,7 +327,10 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     }
     if constexpr (GATE == RG_SCALAR) lds_barrier();
 #pragma unroll
-    for (int cc = 0; cc < DCT; ++cc) uc[cc] = ru[cc];
+    for (int i = 0; i < NU; ++i) {
+      const int p = tid + NTH * i;
+      if (NPU % NTH == 0 || p < NPU) store_tr_chunk<CHV>(sm.u, p / CHV, p % CHV, ru[i]);
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
@@ -340,11 +345,23 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     }
   };
 
+  auto settle_chunk = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      settle(rw[i]);
+      settle(rk[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < NU; ++i) settle(ru[i]);
+    settle(rg_last);
+    settle(rg_tok);
+  };
   load_chunk(0);
+  settle_chunk();
   for (int c = 0; c < NT; ++c) {
     lds_barrier();
     stage_chunk();
-    if (c + 1 < NT) load_chunk(c + 1);
+    load_chunk(c + 1 < NT ? c + 1 : c);    // (the last chunk re-fetches itself: no branch)
     const size_t tok0 = (size_t)b * T + (size_t)c * C;
     // h_c -> LDS (transposed, bf16); the same rounded values feed w h, as stored
 #pragma unroll
@@ -360,9 +377,12 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
 #pragma unroll
       for (int cc = 0; cc < DCT; ++cc) {
         const int ct = dct0 + cc;
+        // u rows 16 drow + 4 (l >> 4) .. + 3 of column 16 ct + (l & 15), transposed read
+        const int lc = l & 15;
+        const bf16x4 u4 = ds_read_tr4(sm.u + tr_off<CHV>(16 * drow + 4 * (l >> 4) + (lc >> 2), 16 * ct + 4 * (lc & 3)));
         f32x4 a;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) a[r] = -to_f32(uc[cc][r]);
+        for (int r = 0; r < 4; ++r) a[r] = -to_f32(u4[r]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
           a = mfma(frag(&sm.w[16 * drow][32 * ks], S::LDK), frag(&sm.hT[16 * ct][32 * ks], S::LDK), a);
@@ -387,12 +407,12 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     // stores of h_c and v_new_c from the transposed LDS copies (lanes run over rows)
     {
       const size_t hb = (((size_t)b * NT + c) * H + h) * KD * VD;
-      // fixed trip counts keep the vector-memory wait counts static
+      // Every lane issues the same number of stores (pieces beyond the tile are
+      // written twice, with the same data): static vector-memory wait counts.
       constexpr int NP = KD * BV / 8, NR = C * BV / 8;
 #pragma unroll
       for (int i = 0; i < (NP + NTH - 1) / NTH; ++i) {
-        const int p = tid + NTH * i;
-        if (NP % NTH != 0 && p >= NP) break;
+        const int p = (tid + NTH * i) % NP;
         const int kr = p % KD, v0 = (p / KD) * 8;
         bf16x8 o;
 #pragma unroll
@@ -401,8 +421,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
       }
 #pragma unroll
       for (int i = 0; i < (NR + NTH - 1) / NTH; ++i) {
-        const int p = tid + NTH * i;
-        if (NR % NTH != 0 && p >= NR) break;
+        const int p = (tid + NTH * i) % NR;
         const int t = p % C, v0 = (p / C) * 8;
         bf16x8 o;
 #pragma unroll
@@ -410,6 +429,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
         *reinterpret_cast<bf16x8*>(vnew_out + (tok0 + t) * rsv + (size_t)h * VD + v_base + v0) = o;
       }
     }
+    settle_chunk();    // the next chunk's operands, settled behind this chunk's stores
   }
   if (ht_out) {
     float* dst = ht_out + (size_t)bh * KD * VD;
