@@ -1110,6 +1110,40 @@ __global__ __launch_bounds__(512) void matrix_intra_kernel(
                                      reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, pin);
 }
 
+// Per-device, once: raise a kernel's dynamic-LDS limit (the attribute is held per
+// device).  Concurrent first calls may both set it, which is harmless.
+constexpr int kMaxDevices = 64;
+static hipError_t allow_dynamic_lds(const void* kern, int bytes, bool (&done)[kMaxDevices]) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  if (!done[dev]) {
+    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return e;
+    done[dev] = true;
+  }
+  return hipSuccess;
+}
+
+// compute units of the current device (cached per device)
+static hipError_t device_cus(int& cus) {
+  static int cached[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  if (cached[dev] == 0) {
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    if (n <= 0) return hipErrorInvalidDevice;
+    cached[dev] = n;
+  }
+  cus = cached[dev];
+  return hipSuccess;
+}
+
 template <int GATE, bool VEC_B>
 static hipError_t launch_post(const void* q, const void* k, const void* v, const void* vnew,
                               const void* dO, const void* dR, const float* g, const float* beta,
@@ -1120,9 +1154,8 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
   using LP = PostLayout<GATE, VEC_B, false, true>;
   if constexpr (LP::FITS && REWY_CHUNK_PIPE && (GATE != CG_VECTOR || REWY_CHUNK_PIPE > 1)) {
     auto kern = chunk_bwd_pipe_kernel<GATE, VEC_B>;    // static LDS only
-    int dev = 0, cus = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    int cus = 0;
+    const hipError_t e = device_cus(cus);
     if (e != hipSuccess) return e;
     const int grid = items < cus ? items : cus;   // one work-group per CU (LDS-bound)
     hipLaunchKernelGGL(kern, dim3(grid), dim3(512), 0, s, (const bf16*)q, (const bf16*)k,
@@ -1133,12 +1166,9 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
   }
   using LY = PostLayout<GATE, VEC_B>;
   auto kern = chunk_bwd_kernel<GATE, VEC_B>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LY::BYTES);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static bool attr_set[kMaxDevices] = {};
+  const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
+  if (e != hipSuccess) return e;
   const int grid = items;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta,
@@ -1187,12 +1217,9 @@ static hipError_t launch_intra(const void* q, const void* k, const float* g, con
                                hipStream_t s) {
   using LY = PostLayout<CG_VECTOR, VEC_B, true>;
   auto kern = matrix_intra_kernel<VEC_B>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LY::BYTES);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static bool attr_set[kMaxDevices] = {};
+  const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k, g,
                      beta, (const bf16*)bgate, daqk, dakk, dq, dk, db, dg, T, H, beta_complete);
   return hipGetLastError();
