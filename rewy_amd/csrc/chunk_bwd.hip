@@ -89,13 +89,14 @@ struct PostLayout {
   static constexpr int OFF_QT = 0, OFF_KT = TQ, OFF_GT = 2 * TQ;
   static constexpr int OFF_BT = OFF_GT + GT_BYTES;
   static constexpr int B1 = PIPE ? 0 : 3 * TQ;
-  static constexpr int B2 = 2 * TQ + GT_BYTES + (VEC_B ? TQ : 0);
+  // (pipelined: g in an array of its own, so its copies and q/k's are told apart)
+  static constexpr int B2 = 2 * TQ + (PIPE ? 0 : GT_BYTES) + (VEC_B ? TQ : 0);
   static constexpr int REGION_B = B1 > B2 ? B1 : B2;
   // small per-row arrays (floats)
   static constexpr int S_BETA = 0, S_G = 64, S_DBA = 128, S_DBB = 384, S_DG = 448, S_GL = 960,
                        S_ANY = 1088, S_N = 1096;
   static constexpr int SMALL = S_N * 4;
-  static constexpr int X_BYTES = PIPE ? 3 * TQ : 0;
+  static constexpr int X_BYTES = PIPE ? 3 * TQ + GT_BYTES : 0;
   static constexpr int BYTES = REGION_A + REGION_B + SMALL + X_BYTES;
   static constexpr bool FITS = BYTES <= 160 * 1024;
   static_assert(PIPE || FITS, "LDS budget");
@@ -108,26 +109,9 @@ __device__ __forceinline__ int g_off(int r, int col) {
   return r * KD + ((((col >> 2) ^ (((r >> 2) & 3) << 2))) << 2) + (col & 3);
 }
 
-// LDS stores the compiler does not see as such.  It orders every LDS write it
-// cannot prove disjoint from an outstanding direct-to-LDS copy behind that copy
-// (vmcnt); for the few writes whose alias information it loses (merged
-// stores), these keep the persistent kernel's copies in flight.  LDS accesses
-// complete in order, so the compiler's own lgkmcnt waits stay correct.
-__device__ __forceinline__ unsigned lds_addr(const void* p) {
-  return (unsigned)(size_t)(const __attribute__((address_space(3))) char*)p;
-}
-__device__ __forceinline__ void lds_st(float* p, float v) {
-  asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory");
-}
-__device__ __forceinline__ void lds_st(bf16* p, bf16x4 v) {
-  typedef unsigned u2 __attribute__((ext_vector_type(2)));
-  asm volatile("ds_write_b64 %0, %1" ::"v"(lds_addr(p)), "v"(__builtin_bit_cast(u2, v)) : "memory");
-}
-
-// Work-group barrier for LDS only, written as one asm block: the compiler's
-// fences at a barrier wait for outstanding direct-to-LDS copies, which the
-// persistent kernel keeps in flight across barriers on purpose (each copy is
-// waited for explicitly, with vmcnt, before the barrier that publishes it).
+// Work-group barrier for LDS only, written as one asm block: the persistent
+// kernel keeps direct-to-LDS copies in flight across barriers on purpose (each
+// copy is waited for explicitly, with vmcnt, before the barrier that publishes it).
 __device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Position of one (batch, chunk, head) work item in the T-major tensors.  Heads
@@ -214,7 +198,7 @@ __device__ __forceinline__ void dma_qkg(bf16* sQ, bf16* sK, float* sGr, const bf
     for (int j = 0; j < 4; ++j) {       // 2 rows of 512 bytes per instruction
       const int r0 = 8 * w + 2 * j, r = r0 + (l >> 5), pc = l & 31;
       const float* src = g + it.kofs + (size_t)r * rsk + 4 * (pc ^ (((r >> 2) & 3) << 2));
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sGr + r0 * KD), 16, 0, 0);
+      dma16(src, sGr + r0 * KD);
     }
   }
 }
@@ -247,7 +231,7 @@ __device__ __forceinline__ void chunk_body(
     bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale,
     const float* __restrict__ daqk, float* __restrict__ dq32, float* __restrict__ dk32,
     float* __restrict__ db32, int beta_complete, int item, int next_item, char* regA, char* regB,
-    float* small, bf16* xbuf, PhaseIn& pin) {
+    float* small, bf16* xbuf, float* gbuf, PhaseIn& pin) {
   using LY = PostLayout<GATE, VEC_B, INTRA, PIPE>;
   using post::LDT;
   auto B16 = [&](int off) { return reinterpret_cast<bf16*>(regA + off); };
@@ -270,7 +254,7 @@ __device__ __forceinline__ void chunk_body(
   bf16* Dtl = B16(LY::OFF_DTL);
   bf16* sQ = B16b(LY::OFF_QT);      // q rows [t][k] (swizzled)
   bf16* sK = B16b(LY::OFF_KT);      // k rows
-  float* sGr = reinterpret_cast<float*>(regB + LY::OFF_GT);   // g rows [t][k] (g_off)
+  float* sGr = PIPE ? gbuf : reinterpret_cast<float*>(regB + LY::OFF_GT);   // g rows [t][k] (g_off)
   bf16* sB = B16b(LY::OFF_BT);      // erase-gate rows (GDN2)
   float* sBeta = small + LY::S_BETA;   // scalar beta per row
   float* sG = small + LY::S_G;         // scalar gate per row (log2)
@@ -384,8 +368,7 @@ __device__ __forceinline__ void chunk_body(
   // ---------------- phase 1: P^T = dR^T A  (accumulator layout stores P row-major) ----------------
   {
     // LDS writes of P wait until every wave has read dR (P takes its place when
-    // pipelined); the LDS partial sums of sum_v P R are plain stores (one per
-    // column strip), which keeps LDS atomics out of the prefetch window
+    // pipelined); sum_v P R goes to one LDS partial per column strip
     f32x4 pacc[2][2];
     float pra[2] = {0.f, 0.f};
 #pragma unroll
@@ -443,8 +426,8 @@ __device__ __forceinline__ void chunk_body(
     }
     if constexpr (!VEC_B) {
       if (lg == 0) {
-        lds_st(sDbA + 64 * cs + 32 * rh + lc, pra[0]);
-        lds_st(sDbA + 64 * cs + 32 * rh + 16 + lc, pra[1]);
+        sDbA[64 * cs + 32 * rh + lc] = pra[0];
+        sDbA[64 * cs + 32 * rh + 16 + lc] = pra[1];
       }
     }
     if constexpr (PIPE) lds_sync();       // dR read by every wave: P overwrites it
@@ -455,7 +438,7 @@ __device__ __forceinline__ void chunk_body(
         bf16x4 p4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) p4[r] = to_bf16(pacc[vt][tt][r]);
-        lds_st(sP + tr_off<16>(32 * rh + 16 * tt + lc, 32 * cs + 16 * vt + 4 * lg), p4);
+        *reinterpret_cast<bf16x4*>(sP + tr_off<16>(32 * rh + 16 * tt + lc, 32 * cs + 16 * vt + 4 * lg)) = p4;
       }
   }
   lds_sync();
@@ -948,7 +931,7 @@ __device__ __forceinline__ void chunk_body(
       for (int r = 0; r < 4; ++r) {
         float s = sum_row16(aw[I][r]);
         if (I == 3 && r == 3 && lg == 3) s += term;
-        if (lc == 0) lds_st(sDg + 64 * wv + 16 * I + 4 * lg + r, s);
+        if (lc == 0) sDg[64 * wv + 16 * I + 4 * lg + r] = s;
       }
   }
   }   // !INTRA: phase 6
@@ -1050,15 +1033,16 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   chunk_body<GATE, VEC_B, false>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
                                  dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale, nullptr,
                                  nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
-                                 reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, pin);
+                                 reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin);
 }
 
 // Persistent form: one work-group per CU walks the items blockIdx.x, + gridDim.x, ...
-// Its LDS regions are separate static arrays (so the compiler can tell them
-// apart); the next item's dR, R, dO are copied straight into LDS (and its A and
-// per-row scalars into registers) while the current one computes phases 4-6, and
-// an item's q, k, g while it computes phases 0-3, so that HBM reads overlap the
-// matrix work instead of stalling the work-group.
+// The next item's dR, R, dO are copied straight into LDS (and its A and per-row
+// scalars into registers) while the current one computes phases 4-6, and an
+// item's q, k, g while it computes phases 0-3, so that HBM reads overlap the
+// matrix work instead of stalling the work-group.  Measured slower for KDA (its
+// chunk kernel is bound by HBM bandwidth, not by exposed latency), so KDA keeps
+// one work-group per chunk-head.
 template <int GATE, bool VEC_B>
 __global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
@@ -1073,6 +1057,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
   __shared__ __attribute__((aligned(16))) char regA[LY::REGION_A];
   __shared__ __attribute__((aligned(16))) char regB[LY::REGION_B];
   __shared__ __attribute__((aligned(16))) float small[LY::S_N];
+  __shared__ __attribute__((aligned(16))) float gbuf[LY::GT_BYTES > 0 ? C * KD : 4];
   PhaseIn pin;
   int it = blockIdx.x;
   if (it >= items) return;
@@ -1090,7 +1075,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
     chunk_body<GATE, VEC_B, false, true>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
                                          dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale,
                                          nullptr, nullptr, nullptr, nullptr, 0, it, nx < items ? nx : -1, regA,
-                                         regB, small, xbuf, pin);
+                                         regB, small, xbuf, gbuf, pin);
   }
 }
 
@@ -1107,7 +1092,7 @@ __global__ __launch_bounds__(512) void matrix_intra_kernel(
                                      nullptr, nullptr, nullptr, nullptr, nullptr, dg, VEC_B ? nullptr : db,
                                      nullptr, nullptr, T, H, 1.f, daqk, dq, dk, VEC_B ? db : nullptr,
                                      beta_complete, blockIdx.x, -1, smem, smem + LY::REGION_A,
-                                     reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, pin);
+                                     reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin);
 }
 
 // Per-device, once: raise a kernel's dynamic-LDS limit (the attribute is held per
@@ -1152,12 +1137,13 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
                               void* db, void* dw, int B, int T, int H, float scale, hipStream_t s) {
   const int items = B * H * (T / C);
   using LP = PostLayout<GATE, VEC_B, false, true>;
+  // persistent form for scalar / no gate (measured slower for KDA: see the kernel)
   if constexpr (LP::FITS && REWY_CHUNK_PIPE && (GATE != CG_VECTOR || REWY_CHUNK_PIPE > 1)) {
     auto kern = chunk_bwd_pipe_kernel<GATE, VEC_B>;    // static LDS only
     int cus = 0;
     const hipError_t e = device_cus(cus);
     if (e != hipSuccess) return e;
-    const int grid = items < cus ? items : cus;   // one work-group per CU (LDS-bound)
+    const int grid = items < cus ? items : cus;        // one work-group per CU (LDS-bound)
     hipLaunchKernelGGL(kern, dim3(grid), dim3(512), 0, s, (const bf16*)q, (const bf16*)k,
                        (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta,
                        (const bf16*)bgate, (const bf16*)wgate, akk, (const bf16*)h, (const bf16*)dh,

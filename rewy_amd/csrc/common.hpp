@@ -287,16 +287,28 @@ __device__ __forceinline__ bf16x8 frag_row(const bf16* tile, int r0, int c0, int
   return *reinterpret_cast<const bf16x8*>(tile + tr_off<CH>(r0 + (l & 15), c0 + 8 * (l >> 4)));
 }
 
-// Direct HBM -> LDS copy (no registers) of rows r0 .. r0 + 3 of a [.][128] bf16
-// tile whose rows sit `ld` elements apart in HBM, into the swizzled CH = 16
-// layout.  One wave instruction writes 1 KiB of LDS, lane l the 16 bytes at
-// l * 16 from the tile row r0, so the lane fetches the HBM chunk that the
-// swizzle places there.  r0 must be wave-uniform; completion is tracked by
-// vmcnt like any vector load.
+// Direct HBM -> LDS copy of 16 bytes per lane (gfx950 global_load_lds_dwordx4):
+// lane l's bytes land at lds_block + 16 l, lds_block wave-uniform (it goes to M0).
+// Written as asm so that the compiler does not track it: it would otherwise order
+// later LDS writes, and after a handful of copies every LDS access, behind all
+// outstanding copies.  The caller waits for the copy explicitly (vmcnt) before the
+// barrier that publishes it; the compiler's own vmcnt waits stay correct, only
+// more conservative, since completion is in order.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(size_t)(const __attribute__((address_space(3))) char*)p;
+}
+__device__ __forceinline__ void dma16(const void* src, const void* lds_block) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds_addr(lds_block)))
+               : "memory");
+}
+
+// Direct HBM -> LDS copy of rows r0 .. r0 + 3 of a [.][128] bf16 tile whose rows
+// sit `ld` elements apart in HBM, into the swizzled CH = 16 layout: lane l fetches
+// the HBM chunk that the swizzle places at byte 16 l of the 1 KiB block of rows
+// r0 .. r0 + 3.  r0 must be wave-uniform.
 __device__ __forceinline__ void dma_rows4(bf16* tile, int r0, const bf16* src, size_t ld, int l = lane_id()) {
   const int r = r0 + (l >> 4);
-  const bf16* s = src + (size_t)r * ld + 8 * ((l & 15) ^ tr_swz<16>(r));
-  __builtin_amdgcn_global_load_lds(s, (__attribute__((address_space(3))) void*)(tile + r0 * 128), 16, 0, 0);
+  dma16(src + (size_t)r * ld + 8 * ((l & 15) ^ tr_swz<16>(r)), tile + r0 * 128);
 }
 
 // 16-byte piece (8 bf16) of row r, chunk c of a swizzled tile
