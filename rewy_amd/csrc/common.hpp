@@ -134,83 +134,6 @@ __device__ __forceinline__ float sum_row16(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// Transposed staging of token-major tiles into K-contiguous LDS tiles.
-//
-// A bf16 tile src[t][c] (t = 0..63 tokens, row stride `ld` elements) is stored
-// as dst[c][t] (pitch P elements).  One piece = two consecutive tokens x 8
-// columns: two 16-byte global loads, repacked into 8 dwords that each hold the
-// (t, t+1) pair of one column.  Lanes run over token pairs first, so the 32
-// lanes of one LDS write cycle hit 32 consecutive dwords (no bank conflict).
-// ---------------------------------------------------------------------------
-struct PairPiece {
-  u32x4 a, b;   // rows t and t+1, 8 bf16 each
-};
-
-__device__ __forceinline__ PairPiece load_pair_piece(const bf16* src, size_t ld, int tp, int c0) {
-  PairPiece p;
-  p.a = *reinterpret_cast<const u32x4*>(src + (size_t)(2 * tp) * ld + c0);
-  p.b = *reinterpret_cast<const u32x4*>(src + (size_t)(2 * tp + 1) * ld + c0);
-  return p;
-}
-
-// dst is the LDS tile viewed as dwords; pitch_dw = P / 2.
-__device__ __forceinline__ void store_pair_piece(uint32_t* dst, int pitch_dw, int tp, int c0,
-                                                 const PairPiece& p) {
-  const uint32_t a[4] = {p.a.x, p.a.y, p.a.z, p.a.w};
-  const uint32_t b[4] = {p.b.x, p.b.y, p.b.z, p.b.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    dst[(c0 + 2 * j) * pitch_dw + tp] = (a[j] & 0xffffu) | (b[j] << 16);
-    dst[(c0 + 2 * j + 1) * pitch_dw + tp] = (a[j] >> 16) | (b[j] & 0xffff0000u);
-  }
-}
-
-// Same for a piece with a per-row scalar multiplier (scalar-gate families).
-__device__ __forceinline__ void store_pair_piece_scaled(uint32_t* dst, int pitch_dw, int tp, int c0,
-                                                        const PairPiece& p, float sa, float sb) {
-  const bf16* a = reinterpret_cast<const bf16*>(&p.a);
-  const bf16* b = reinterpret_cast<const bf16*>(&p.b);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const bf16 x = to_bf16(to_f32(a[j]) * sa);
-    const bf16 y = to_bf16(to_f32(b[j]) * sb);
-    dst[(c0 + j) * pitch_dw + tp] = (uint32_t)__builtin_bit_cast(uint16_t, x) |
-                                    ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
-  }
-}
-
-// fp32 piece: two consecutive tokens x 4 columns, split into bf16 hi / lo
-// transposed tiles (pair-packed dwords).
-struct PairPieceF {
-  f32x4 a, b;
-};
-
-__device__ __forceinline__ PairPieceF load_pair_piece_f(const float* src, size_t ld, int tp, int c0) {
-  PairPieceF p;
-  p.a = *reinterpret_cast<const f32x4*>(src + (size_t)(2 * tp) * ld + c0);
-  p.b = *reinterpret_cast<const f32x4*>(src + (size_t)(2 * tp + 1) * ld + c0);
-  return p;
-}
-
-__device__ __forceinline__ uint32_t pack2(bf16 lo16, bf16 hi16) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, lo16) | ((uint32_t)__builtin_bit_cast(uint16_t, hi16) << 16);
-}
-
-__device__ __forceinline__ void store_pair_piece_split(uint32_t* dhi, uint32_t* dlo, int pitch_dw, int tp,
-                                                       int c0, const PairPieceF& p, float mult) {
-  const float a[4] = {p.a.x, p.a.y, p.a.z, p.a.w};
-  const float b[4] = {p.b.x, p.b.y, p.b.z, p.b.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    bf16 ah, al, bh, bl;
-    split_bf16(a[j] * mult, ah, al);
-    split_bf16(b[j] * mult, bh, bl);
-    dhi[(c0 + j) * pitch_dw + tp] = pack2(ah, bh);
-    dlo[(c0 + j) * pitch_dw + tp] = pack2(al, bl);
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Row-major LDS tiles read transposed.
 //
 // gfx950's ds_read_b64_tr_b16 lets each lane of a 16-lane group name an 8-byte
