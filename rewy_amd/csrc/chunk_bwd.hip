@@ -89,7 +89,7 @@ struct PostLayout {
   static constexpr int OFF_QT = 0, OFF_KT = TQ, OFF_GT = 2 * TQ;
   static constexpr int OFF_BT = OFF_GT + GT_BYTES;
   static constexpr int B1 = PIPE ? 0 : 3 * TQ;
-  // (pipelined: g in an array of its own, so its copies and q/k's are told apart)
+  // (pipelined: g in an array of its own)
   static constexpr int B2 = 2 * TQ + (PIPE ? 0 : GT_BYTES) + (VEC_B ? TQ : 0);
   static constexpr int REGION_B = B1 > B2 ? B1 : B2;
   // small per-row arrays (floats)
