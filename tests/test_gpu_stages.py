@@ -37,6 +37,9 @@ def _setup(op, B, T, H, seed, **kw):
 
 CASES = [(op, shp, "default", 0) for op in ("kda", "gdn", "delta", "gdn2") for shp in ((1, 128, 2), (2, 256, 3))]
 CASES += [("kda", (1, 192, 2), "wide", 5), ("gdn2", (1, 192, 2), "wide", 0), ("gdn", (1, 128, 2), "default", 3)]
+# more chunk-heads than the GPU has CUs: the persistent scalar/no-gate chunk kernel walks
+# 1 or 2 chunk-heads per work-group (300 is not a multiple of the CU count)
+CASES += [("gdn", (1, 64 * 300, 1), "default", 7), ("delta", (2, 64 * 150, 1), "default", 0)]
 
 
 @pytest.mark.parametrize("op,shape,gate,bz", CASES)
