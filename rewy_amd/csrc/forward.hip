@@ -52,6 +52,7 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
   __shared__ float sbeta[C];
   __shared__ float sM[C][LDM];    // strict_tril(b k k^T 2^(g_i-g_s)), then the inverse
   __shared__ float sX[C][LDM];    // (I + M)^-1
+  __shared__ __attribute__((aligned(16))) float sT[32][36];    // products of the block inverse
   __shared__ int sWide[4];        // diagonal block I takes the pairwise path
 
   const int blk = blockIdx.x;
@@ -243,35 +244,52 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
     sX[16 * I + (e >> 4)][16 * J + (e & 15)] = 0.f;
   }
   lds_barrier();
-  // block rows I = 1..3: X_IJ = -X_II sum_{m = J}^{I-1} M_Im X_mJ, one wave per block
-  for (int I = 1; I < 4; ++I) {
-    if (wv < I) {
-      const int J = wv;
-      // lane: rows 16 I + (l >> 2), columns 16 J + 4 (l & 3) .. + 3
-      const int ri = l >> 2, cj = 4 * (l & 3);
-      float tacc[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int m = 16 * J; m < 16 * I; ++m) {
-        const float mv = sM[16 * I + ri][m];
+  // Off-diagonal blocks by doubling, [[A, 0], [C, D]]^-1 = [[A^-1, 0], [-D^-1 C A^-1, D^-1]]:
+  // first inside the two 32 x 32 diagonal blocks, then for the 64 x 64 whole (C = M off the
+  // diagonal).  Each product is spread over all 512 threads (one or two outputs each),
+  // with fixed trip counts (the zero upper parts of X and M are summed as zeros) and
+  // 16-byte reads of the row operand.
+  auto rowdot = [&](const float* row, const float* col, int pitch, int n) -> float {
+    float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) tacc[e] += mv * sX[m][16 * J + cj + e];
-      }
-      // X_IJ[r][c] = -sum_t X_II[r][t] T[t][c], with T exchanged between lanes
-      float xo[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        // T[t][cj + e] lives in lane (4 t + (l & 3))
-        float tv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) tv[e] = __shfl(tacc[e], 4 * t + (l & 3));
-        const float xi = sX[16 * I + ri][16 * I + t];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xo[e] -= xi * tv[e];
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sX[16 * I + ri][16 * J + cj + e] = xo[e];
+    for (int m = 0; m < 32; m += 4) {
+      if (m >= n) break;
+      const f32x4 r4 = *reinterpret_cast<const f32x4*>(row + m);
+      a0 += r4[0] * col[(m + 0) * pitch];
+      a1 += r4[1] * col[(m + 1) * pitch];
+      a0 += r4[2] * col[(m + 2) * pitch];
+      a1 += r4[3] * col[(m + 3) * pitch];
     }
-    lds_barrier();
+    return a0 + a1;
+  };
+  {
+    // P = M_{r,r-1} X_{r-1,r-1}, r = 1, 3
+    const int q2 = tid >> 8, e = tid & 255, i = e >> 4, j = e & 15;
+    const int cb = 32 * q2, rb = cb + 16;
+    sT[16 * q2 + i][j] = rowdot(&sM[rb + i][cb], &sX[cb][cb + j], fwd::LDM, 16);
   }
+  lds_barrier();
+  {
+    // X_{r,r-1} = -X_{r,r} P
+    const int q2 = tid >> 8, e = tid & 255, i = e >> 4, j = e & 15;
+    const int rb = 32 * q2 + 16;
+    sX[rb + i][rb - 16 + j] = -rowdot(&sX[rb + i][rb], &sT[16 * q2][j], 36, 16);
+  }
+  lds_barrier();
+  // T = M_BL X_TL (rows 32..63, columns 0..31)
+#pragma unroll
+  for (int k2 = 0; k2 < 2; ++k2) {
+    const int o = tid + 512 * k2, i = o >> 5, j = o & 31;
+    sT[i][j] = rowdot(&sM[32 + i][0], &sX[0][j], fwd::LDM, 32);
+  }
+  lds_barrier();
+  // X_BL = -X_BR T
+#pragma unroll
+  for (int k2 = 0; k2 < 2; ++k2) {
+    const int o = tid + 512 * k2, i = o >> 5, j = o & 31;
+    sX[32 + i][j] = -rowdot(&sX[32 + i][32], &sT[0][j], 36, 32);
+  }
+  lds_barrier();
   // ---- Akk rows -> HBM ----
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
