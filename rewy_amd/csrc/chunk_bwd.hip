@@ -34,8 +34,10 @@
 // contraction runs as three bf16 MFMAs with fp32 accumulation (the reference
 // uses tf32x3 dots for these).
 //
-// Work split: 8 waves; wave (cs, rh) owns the 32 columns [32 cs, 32 cs + 32)
-// (key or value) and the 32 rows [32 rh, 32 rh + 32) of every 64 x 128 tile.
+// Work split over 8 waves: in phase 1 wave (cs, th) owns the value rows
+// [32 cs, 32 cs + 32) and the token tiles th and 2 + th of P^T; in phase 2 each wave
+// two 16 x 16 tile pairs of L and D; from phase 3 on wave w owns the 16 key columns
+// [16 w, 16 w + 16) over all 64 rows.
 // Token-major inputs that are contracted over tokens are staged transposed
 // (token pairs packed into dwords, conflict-free); P and the L/D tiles are
 // produced by MFMAs whose accumulator layout stores contiguously into the
@@ -272,7 +274,7 @@ __device__ __forceinline__ void chunk_body(
   asm volatile("" : "+v"(tid_o));
   const int tid = tid_o, l = tid_o & 63, wv = __builtin_amdgcn_readfirstlane(tid_o >> 6);
   const int cs = wv & 3;          // column strip: k (or v) in [32 cs, 32 cs + 32)
-  const int rh = wv >> 2;         // row half: rows [32 rh, 32 rh + 32)
+  const int th = wv >> 2;         // phase 1: token tiles th and 2 + th
   const int lc = l & 15, lg = l >> 4;
   const size_t tok0 = pos.tok0;
   const size_t rsk = (size_t)H * KD, rsv = (size_t)H * VD, rsa = (size_t)H * C;
@@ -368,7 +370,9 @@ __device__ __forceinline__ void chunk_body(
   // ---------------- phase 1: P^T = dR^T A  (accumulator layout stores P row-major) ----------------
   {
     // LDS writes of P wait until every wave has read dR (P takes its place when
-    // pipelined); sum_v P R goes to one LDS partial per column strip
+    // pipelined); sum_v P R goes to one LDS partial per column strip.  Each wave
+    // takes one token tile from each half (t tiles th and 2 + th): the second half
+    // needs half the contraction (A^T is upper triangular), so the waves balance.
     f32x4 pacc[2][2];
     float pra[2] = {0.f, 0.f};
 #pragma unroll
@@ -376,12 +380,12 @@ __device__ __forceinline__ void chunk_body(
       const int vrow0 = 32 * cs + 16 * vt;
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        const int tcol0 = 32 * rh + 16 * tt;
+        const int tcol0 = 16 * th + 32 * tt;
         f32x4& acc = pacc[vt][tt];
         acc = zero4();
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          if (ks == 0 && rh == 1) continue;    // A^T upper triangular: s < 32 <= t vanishes
+          if (ks == 0 && tt == 1) continue;    // A^T upper triangular: s < 32 <= t vanishes
           const bf16x8 a = frag_tr<16>(sdR, 32 * ks, vrow0, l);          // dR^T rows v, over s
           acc = mfma(a, frag_tr<8>(sAh, 32 * ks, tcol0, l), acc);      // A[s][t] columns t, over s
           acc = mfma(a, frag_tr<8>(sAl, 32 * ks, tcol0, l), acc);
@@ -426,8 +430,8 @@ __device__ __forceinline__ void chunk_body(
     }
     if constexpr (!VEC_B) {
       if (lg == 0) {
-        sDbA[64 * cs + 32 * rh + lc] = pra[0];
-        sDbA[64 * cs + 32 * rh + 16 + lc] = pra[1];
+        sDbA[64 * cs + 16 * th + lc] = pra[0];
+        sDbA[64 * cs + 32 + 16 * th + lc] = pra[1];
       }
     }
     if constexpr (PIPE) lds_sync();       // dR read by every wave: P overwrites it
@@ -438,7 +442,7 @@ __device__ __forceinline__ void chunk_body(
         bf16x4 p4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) p4[r] = to_bf16(pacc[vt][tt][r]);
-        *reinterpret_cast<bf16x4*>(sP + tr_off<16>(32 * rh + 16 * tt + lc, 32 * cs + 16 * vt + 4 * lg)) = p4;
+        *reinterpret_cast<bf16x4*>(sP + tr_off<16>(16 * th + 32 * tt + lc, 32 * cs + 16 * vt + 4 * lg)) = p4;
       }
   }
   lds_sync();
