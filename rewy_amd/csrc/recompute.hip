@@ -239,8 +239,6 @@ struct FwdSmem {
   bf16 vT[BV][LDT];        // v_new^T: B operand of kg^T v_new
   bf16 u[C * BV];          // u rows [t][v] (swizzled): read transposed in the accumulator layout
   float lam[KD];
-  float gam[C];
-  float gkf[C];
 };
 
 template <int BV, int GATE>
@@ -287,7 +285,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
   constexpr int NPU = C * CHV;
   constexpr int NU = (NPU + NTH - 1) / NTH;
   u32x4 ru[NU];
-  float rg_last = 0.f, rg_tok = 0.f;
+  float rg_last = 0.f, rg_tok[2] = {0.f, 0.f};   // scalar gate: last row, the 2 rows this thread stages
   auto load_chunk = [&](int c) {
     const size_t tok0 = (size_t)b * T + (size_t)c * C;
     const bf16* wb = w + tok0 * rsk + (size_t)h * KD;
@@ -297,7 +295,8 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     if constexpr (GATE == RG_VECTOR) {
       rg_last = g[((tok0 + C - 1) * H + h) * KD + (tid & (KD - 1))];
     } else if constexpr (GATE == RG_SCALAR) {
-      rg_tok = g[(tok0 + (tid & (C - 1))) * H + h];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) rg_tok[i] = g[(tok0 + ((tid + NTH * i) >> 4)) * H + h];
       rg_last = g[(tok0 + C - 1) * H + h];
     }
 #pragma unroll
@@ -321,11 +320,9 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
       if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
     } else if constexpr (GATE == RG_SCALAR) {
       if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
-      if (tid < C) sm.gkf[tid] = fast_exp2(rg_last - rg_tok);
     } else {
       if (tid < KD) sm.lam[tid] = 1.f;
     }
-    if constexpr (GATE == RG_SCALAR) lds_barrier();
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
       const int p = tid + NTH * i;
@@ -340,7 +337,8 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
       u32x4 kq = rk[i];
-      if constexpr (GATE == RG_SCALAR) kq = scale_bf16x8(kq, sm.gkf[p >> 4]);
+      // scalar gate: kg = k 2^(g_last - g_t), the row's factor from registers
+      if constexpr (GATE == RG_SCALAR) kq = scale_bf16x8(kq, fast_exp2(rg_last - rg_tok[i]));
       store_tr_chunk<16>(sm.k, p >> 4, p & 15, kq);
     }
   };
@@ -354,7 +352,8 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
 #pragma unroll
     for (int i = 0; i < NU; ++i) settle(ru[i]);
     settle(rg_last);
-    settle(rg_tok);
+    settle(rg_tok[0]);
+    settle(rg_tok[1]);
   };
   load_chunk(0);
   settle_chunk();

@@ -36,8 +36,6 @@ struct StateSmem {
   bf16 dhT[BV][LDK];       // dh^T:    B operand of kg * dh
   bf16 drT[BV][LDT];       // dR^T:    B operand of w^T dR
   float lam[KD];           // exp2(g_last) per key row
-  float gam[C];            // scalar gate: exp2(g_t)
-  float gkf[C];            // scalar gate: exp2(g_last - g_t)
 };
 
 template <int BV, int GATE, bool DV_FROM_AQK>
@@ -89,7 +87,7 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
   constexpr int NDO = (NPD + NTH - 1) / NTH;
   u32x4 rk[2], rq[2], rw[2], rdo[NDO];
   f32x4 ra[2];
-  float rg_last = 0.f, rg_tok = 0.f;
+  float rg_last = 0.f, rg_tok[2] = {0.f, 0.f};   // scalar gate: last row, the 2 rows this thread stages
   const size_t row_stride_k = (size_t)H * KD;   // elements between tokens
   const size_t row_stride_v = (size_t)H * VD;
 
@@ -99,7 +97,8 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
     if constexpr (GATE == GATE_VECTOR) {
       if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
     } else if constexpr (GATE == GATE_SCALAR) {
-      if (tid < C) rg_tok = g[(tok0 + tid) * H + h];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) rg_tok[i] = g[(tok0 + ((tid + NTH * i) >> 4)) * H + h];
       rg_last = g[(tok0 + C - 1) * H + h];
     }
     const size_t kofs = tok0 * row_stride_k + (size_t)h * KD;
@@ -127,22 +126,18 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
       if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
     } else if constexpr (GATE == GATE_SCALAR) {
       if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
-      if (tid < C) {
-        sm.gam[tid] = fast_exp2(rg_tok);
-        sm.gkf[tid] = fast_exp2(rg_last - rg_tok);
-      }
     } else {
       if (tid < KD) sm.lam[tid] = 1.f;
     }
-    if constexpr (GATE == GATE_SCALAR) lds_barrier();  // gam / gkf needed below
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
       const int t = p >> 4, ch = p & 15;
       u32x4 kq = rk[i], qq = rq[i];
       if constexpr (GATE == GATE_SCALAR) {
-        kq = scale_bf16x8(kq, sm.gkf[t]);
-        qq = scale_bf16x8(qq, sm.gam[t]);
+        // scalar gate: kg = k 2^(g_last - g_t), qg = q 2^(g_t), the row's factors from registers
+        kq = scale_bf16x8(kq, fast_exp2(rg_last - rg_tok[i]));
+        qq = scale_bf16x8(qq, fast_exp2(rg_tok[i]));
       }
       *reinterpret_cast<u32x4*>(&sm.k[t][ch * 8]) = kq;
       store_tr_chunk<16>(sm.q, t, ch, qq);
