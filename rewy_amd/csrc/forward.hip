@@ -141,25 +141,25 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
   lds_barrier();
 
   // ---- 16 x 16 tiles (I, J), J <= I: Aqk and M by anchored MFMAs ----
-  // tile list: (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0) (3,1) (3,2) (3,3); wave w: tiles w, w + 8
-  for (int tix = wv; tix < 10; tix += 8) {
-    const int I = tix < 1 ? 0 : tix < 3 ? 1 : tix < 6 ? 2 : 3;
-    const int J = tix - (I * (I + 1)) / 2;
-    const bool pairwise = (J == I) && sWide[I];
+  // wave -> (row block I, first column block J0, tile count): the two waves with two tiles
+  // form the q / b k row operands of block I once for both; every wave has at most two.
+  {
+    const int I = wv == 0 || wv == 2 || wv == 3 ? 3 : wv == 1 || wv == 4 ? 2 : wv == 7 ? 0 : 1;
+    const int J0 = wv == 2 ? 2 : wv == 3 ? 3 : wv == 4 ? 2 : wv == 6 ? 1 : 0;
+    const int NJ = wv < 2 ? 2 : 1;
+    const bool pairwise = NJ == 1 && J0 == I && sWide[I];
     const int n = 16 * I;                       // anchor row
-    f32x4 aqk = zero4(), mkk = zero4();
+    f32x4 aqk[2] = {zero4(), zero4()}, mkk[2] = {zero4(), zero4()};
     if (!pairwise) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int k0 = 32 * ks + 8 * lg;
         const int ia = 16 * I + lc;             // A rows (i)
-        const int sb_ = 16 * J + lc;            // B columns (s)
-        bf16x8 qh, ql, bh_, bl, kh, kl;
+        bf16x8 qh, ql, bh_, bl;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int kc = k0 + j;
           const float fa = fast_exp2(gate(ia, kc) - gate(n, kc));     // <= 1
-          const float fb = fast_exp2(gate(n, kc) - gate(sb_, kc));    // <= 1 off the diagonal
           const float kia = to_f32(sk[ia][kc]);
           const float bia = VEC_B ? to_f32(sb[ia][kc]) : sbeta[ia];
           bf16 hh, ll;
@@ -169,20 +169,32 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
           split_bf16(bia * kia * fa, hh, ll);
           bh_[j] = hh;
           bl[j] = ll;
-          split_bf16(to_f32(sk[sb_][kc]) * fb, hh, ll);
-          kh[j] = hh;
-          kl[j] = ll;
         }
-        aqk = mfma(qh, kh, aqk);
-        aqk = mfma(qh, kl, aqk);
-        aqk = mfma(ql, kh, aqk);
-        mkk = mfma(bh_, kh, mkk);
-        mkk = mfma(bh_, kl, mkk);
-        mkk = mfma(bl, kh, mkk);
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          if (jj >= NJ) break;                  // wave-uniform
+          const int sb_ = 16 * (J0 + jj) + lc;  // B columns (s)
+          bf16x8 kh, kl;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int kc = k0 + j;
+            const float fb = fast_exp2(gate(n, kc) - gate(sb_, kc));  // <= 1 off the diagonal
+            bf16 hh, ll;
+            split_bf16(to_f32(sk[sb_][kc]) * fb, hh, ll);
+            kh[j] = hh;
+            kl[j] = ll;
+          }
+          aqk[jj] = mfma(qh, kh, aqk[jj]);
+          aqk[jj] = mfma(qh, kl, aqk[jj]);
+          aqk[jj] = mfma(ql, kh, aqk[jj]);
+          mkk[jj] = mfma(bh_, kh, mkk[jj]);
+          mkk[jj] = mfma(bh_, kl, mkk[jj]);
+          mkk[jj] = mfma(bl, kh, mkk[jj]);
+        }
       }
     } else {
       // exact pairwise diagonal: lane (lg, lc) owns rows 16 I + 4 lg + r, column s = 16 I + lc
-      const int s = 16 * J + lc;
+      const int s = 16 * I + lc;
 #pragma unroll 1
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * I + 4 * lg + r;
@@ -197,17 +209,21 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
             m += bi * to_f32(sk[i][kc]) * ks_ * f;
           }
         }
-        aqk[r] = a;
-        mkk[r] = m;
+        aqk[0][r] = a;
+        mkk[0][r] = m;
       }
     }
     // lane: rows i = 16 I + 4 lg + r, column s = 16 J + lc
-    const int s = 16 * J + lc;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * I + 4 * lg + r;
-      aqk_out[mofs + (size_t)i * rsm + s] = (s <= i) ? scale * aqk[r] : 0.f;
-      sM[i][s] = (s < i) ? mkk[r] : 0.f;
+    for (int jj = 0; jj < 2; ++jj) {
+      if (jj >= NJ) break;
+      const int s = 16 * (J0 + jj) + lc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * I + 4 * lg + r;
+        aqk_out[mofs + (size_t)i * rsm + s] = (s <= i) ? scale * aqk[jj][r] : 0.f;
+        sM[i][s] = (s < i) ? mkk[jj][r] : 0.f;
+      }
     }
   }
   // zero upper tiles of Aqk and M (J > I)
