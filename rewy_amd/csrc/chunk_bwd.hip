@@ -551,9 +551,9 @@ __device__ __forceinline__ void chunk_body(
     // its own copies, the barrier publishes them (and retires P, R, dO)
     __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
     lds_sync();
-    // The next item's dR, R, dO stream into X during phases 4-6 (the last item
-    // re-fetches its own rows: harmless, and no branch splits the vmcnt count).
-    dma_x(xbuf, dR, vnew, dO, ChunkItem(next_item >= 0 ? next_item : item, T, H), H, tid);
+    // The next item's dR, R, dO stream into X during phases 4-6 (the copies are
+    // asm, outside the compiler's wait counts, so the branch costs no precision).
+    if (next_item >= 0) dma_x(xbuf, dR, vnew, dO, ChunkItem(next_item, T, H), H, tid);
   } else {
     // q, k, g (and b) rows for the row-major staging (issued before the barrier)
     u32x4 rq[2], rk[2], rb[2];
