@@ -1,7 +1,9 @@
 // Chunk-parallel part of the delta-rule backward: residual-WY local products,
 // matrix intra (KDA/GDN2 vector gates, Gram-free scalar-gate form for GDN and
 // DeltaNet), state-gradient epilogue and the in-chunk reverse gate cumsum, fused
-// into one work-group per (chunk, head).
+// per (chunk, head): one work-group per chunk-head (KDA, GDN2), or one persistent
+// work-group per CU that walks chunk-heads with direct HBM -> LDS prefetch
+// (scalar / no gate).
 //
 // Replaces, for one 64-token chunk of one head, the reference's
 //   residual_tri_beta_producer        kernels/kda_residual_tri_beta.py:8-73
@@ -25,10 +27,10 @@
 //   dG = q dq - k dks + b k exp2(g) Eb + k (b ue - uk)  (+ last-row state terms)
 //   dg = reverse_cumsum(dG)
 //
-// Vector gates: the 2^(g_i-g_s) factors are applied through one anchor per
-// 16-row block (the block's gate centre when its span is < 80, in log2 units,
-// else the block's own top/bottom with an exact pairwise diagonal), the same
-// safety rule as the reference (endpoint_intra.py:98-102).  Scalar gates are
+// Vector gates: per column and 16-row block, 2^(g_i-g_s) = ET_i 2^(top_I - bot_J) EB_s
+// with ET = 2^(g - top) <= 1 and EB = 2^(bot - g) <= 1 taken at the blocks' gate
+// extremes; a diagonal block whose gate span reaches 80 (log2 units) is evaluated
+// pairwise instead, the reference's safety rule (endpoint_intra.py:98-102).  Scalar gates are
 // applied exactly to the 64x64 L and D tiles, so no Gram matrix is formed and
 // no anchor is needed.  The intra operands are split into bf16 hi + lo so each
 // contraction runs as three bf16 MFMAs with fp32 accumulation (the reference
@@ -36,28 +38,22 @@
 //
 // Work split over 8 waves: in phase 1 wave (cs, th) owns the value rows
 // [32 cs, 32 cs + 32) and the token tiles th and 2 + th of P^T; in phase 2 each wave
-// two 16 x 16 tile pairs of L and D; from phase 3 on wave w owns the 16 key columns
-// [16 w, 16 w + 16) over all 64 rows.
-// Token-major inputs that are contracted over tokens are staged transposed
-// (token pairs packed into dwords, conflict-free); P and the L/D tiles are
-// produced by MFMAs whose accumulator layout stores contiguously into the
-// orientation the next contraction reads.
+// computes two 16 x 16 tile pairs of L and D; from phase 3 on wave w owns the 16 key
+// columns [16 w, 16 w + 16) over all 64 rows.
+// Token-major inputs sit in LDS row-major as in HBM (XOR-swizzled 16-byte chunks);
+// contractions over tokens read them transposed (ds_read_b64_tr_b16).  P and the
+// L/D tiles are produced by MFMAs whose accumulator layout stores contiguously
+// into the orientation the next contraction reads.
 #include "common.hpp"
 
 namespace rewy {
 
 enum GateModeC { CG_NONE = 0, CG_SCALAR = 1, CG_VECTOR = 2 };
 
-// Persistent, prefetching chunk kernel wherever its LDS fits (all but GDN2)
+// Persistent, prefetching chunk kernel for the scalar / no-gate families (1), also
+// for KDA (2: measured slower, kept for A/B), or never (0)
 #ifndef REWY_CHUNK_PIPE
 #define REWY_CHUNK_PIPE 1
-#endif
-
-// Split the gate-weighted key/query operands of the intra contractions into
-// bf16 hi + lo (three MFMAs per product) or keep them single bf16 (two MFMAs:
-// the fp32 L/D coefficients are always split).
-#ifndef REWY_INTRA_B_SPLIT
-#define REWY_INTRA_B_SPLIT 1
 #endif
 
 namespace post {
