@@ -146,6 +146,71 @@ hipError_t fdr_fwd_o(const void* q, const float* gc, int gate_mode, const float*
                      const void* v_new, void* o, int B, int T, int H, int K, int V, int chunk,
                      float scale, hipStream_t stream);
 
+/*
+ * Affine-step form of the two state recurrences (for small B*H, where the
+ * sequential chain and not HBM sets the time).  The same results as
+ * fdr_state_bwd / fdr_fwd_h, split into chunk-parallel and sequential parts:
+ *
+ *   fdr_affine_prep_bwd:  M_c = w_c^T kg_c,  Y_c = scale qg_c^T dO_c - w_c^T dv_c
+ *                         (dv_c = Aqk_c^T dO_c written to dv_out, or dv_in given)
+ *   fdr_affine_prep_fwd:  N_c = kg_c^T w_c,  Z_c = kg_c^T u_c
+ *   fdr_affine_scan:      S <- diag(2^g_last) S - A_c S + Y_c, states[c] = S before step c
+ *                         (reverse = 1: c = NT-1 .. 0, the backward dh; 0: the forward h)
+ *   fdr_affine_side:      out_c = addend_c + sign * rowfac_t * (x_c states[c])
+ *                         (dR = dv + [2^(g_last - g_t)] k dh;  v_new = u - w h)
+ *
+ * Together they replace the reference's two state recurrences (see fdr_state_bwd
+ * and fdr_fwd_h: backends/backward.py:117-121, kernels/vector_state_gpu.py:47-67).
+ * `step` (bf16, B*NT*H*K*K elements) and `offset` (fp32, B*NT*H*K*V) are
+ * workspaces in this library's private fragment order, written by a prep call and
+ * read by a scan call.  Gate conventions as for fdr_state_bwd / fdr_fwd_h (for
+ * gate_mode 2, q/k are qg/kg).  A scan or side call takes one or two independent
+ * problems (a forward and a backward recurrence run side by side); value_block
+ * (16, 32 or 64) is the value-tile width of one scan work-group.
+ */
+typedef struct fdr_scan_problem {
+  const void* step;          /* bf16 workspace from a prep call */
+  const float* offset;       /* fp32 workspace from the same prep call */
+  const float* g;            /* gate cumsum (log2), null for gate_mode 0 */
+  const float* initial;      /* fp32 [B,H,K,V] or null (zero) */
+  void* states;              /* bf16 [B,T/64,H,K,V] */
+  float* final_state;        /* fp32 [B,H,K,V] or null */
+  int gate_mode;
+  int reverse;
+} fdr_scan_problem;
+
+typedef struct fdr_side_problem {
+  const void* x;             /* bf16 [B,T,H,K]: kg | k (backward), w (forward) */
+  const void* states;        /* bf16 [B,T/64,H,K,V] from fdr_affine_scan */
+  const void* addend;        /* bf16 [B,T,H,V]: dv_local (backward), u (forward) */
+  const float* row_gate;     /* scalar gate cumsum for the factor 2^(g_last - g_t), or null */
+  void* out;                 /* bf16 [B,T,H,V]: dR | v_new */
+  float sign;                /* +1 (backward) or -1 (forward) */
+} fdr_side_problem;
+
+hipError_t fdr_affine_prep_bwd(const void* q, const void* k, const void* w, const float* g, int gate_mode,
+                               const void* dO, const float* aqk, const void* dv_in, void* step,
+                               float* offset, void* dv_out, int B, int T, int H, int K, int V, int chunk,
+                               float scale, hipStream_t stream);
+
+hipError_t fdr_affine_prep_fwd(const void* k, const void* w, const void* u, const float* g, int gate_mode,
+                               void* step, float* offset, int B, int T, int H, int K, int V, int chunk,
+                               hipStream_t stream);
+
+/* fdr_affine_prep_bwd and fdr_affine_prep_fwd in one launch (the recompute policy's two
+ * recurrences, same gate_mode; k is kg for gate_mode 2, raw k otherwise). */
+hipError_t fdr_affine_prep_pair(const void* q, const void* k, const void* w, const void* u, const float* g,
+                                int gate_mode, const void* dO, const float* aqk, const void* dv_in,
+                                void* step_bwd, float* offset_bwd, void* dv_out, void* step_fwd,
+                                float* offset_fwd, int B, int T, int H, int K, int V, int chunk, float scale,
+                                hipStream_t stream);
+
+hipError_t fdr_affine_scan(const fdr_scan_problem* problems, int n_problems, int B, int T, int H, int K,
+                           int V, int chunk, int value_block, hipStream_t stream);
+
+hipError_t fdr_affine_side(const fdr_side_problem* problems, int n_problems, int B, int T, int H, int K,
+                           int V, int chunk, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

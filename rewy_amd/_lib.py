@@ -24,7 +24,31 @@ SIGNATURES = {
     "fdr_matrix_intra": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "fdr_fwd_prepare": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P],
     "fdr_fwd_o": [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
+    "fdr_affine_prep_bwd": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
+    "fdr_affine_prep_fwd": [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P],
+    "fdr_affine_prep_pair": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                             _F, _P],
+    "fdr_affine_scan": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
+    "fdr_affine_side": [_P, _I, _I, _I, _I, _I, _I, _I, _P],
 }
+
+
+class ScanProblem(ctypes.Structure):
+    """fdr_scan_problem (include/rewy_amd.h)."""
+    _fields_ = [("step", _P), ("offset", _P), ("g", _P), ("initial", _P), ("states", _P),
+                ("final_state", _P), ("gate_mode", _I), ("reverse", _I)]
+
+
+class SideProblem(ctypes.Structure):
+    """fdr_side_problem (include/rewy_amd.h)."""
+    _fields_ = [("x", _P), ("states", _P), ("addend", _P), ("row_gate", _P), ("out", _P), ("sign", _F)]
+
+
+def problems(struct, items):
+    """ctypes array of one or two problem structs (passed by pointer)."""
+    arr = (struct * len(items))(*items)
+    return arr, len(items)
+
 
 _lib = None
 

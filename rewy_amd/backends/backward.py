@@ -11,6 +11,11 @@ with FLA's ``chunk_<op>_bwd``.  Each one runs
   3. ``fdr_chunk_bwd``  -- residual-WY products, dAqk, matrix intra, gate/beta
      epilogue and the in-chunk reverse cumsum of dg, one work-group per chunk.
 
+When batch x heads is too small to fill the GPU and the sequence long, the two
+recurrences (steps 1b and 2) run instead in affine-step form (``ops.recurrences``,
+``fdr_affine_*``): chunk-parallel step matrices, one scan launch carrying both
+recurrences side by side, and a chunk-parallel pass for v_new and dR.
+
 There is no fallback: a missing HIP library or an unsupported argument raises.
 """
 from __future__ import annotations
@@ -52,11 +57,17 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
     g = _f32(g)
     Aqk, Akk = _f32(Aqk), _f32(Akk)
-    if saved.get("h") is None:
-        saved = _recompute_vector(q, k, v, g, Akk, initial_state, gates)
-    dh, dR, dh0 = ops.state_bwd(_bf(saved["qg"]), _bf(saved["kg"]), _bf(saved["w"]), g,
-                                ops.GATE_VECTOR, do, scale, aqk=Aqk, dht=_f32(dht),
-                                want_dh0=initial_state is not None)
+    if saved.get("h") is None and ops.affine_pays(q):
+        # recompute policy, few heads: both recurrences side by side in affine-step form
+        pre = _prepare_vector(k, v, g, Akk, gates, q)
+        h, v_new, dh, dR, dh0 = ops.recurrences(pre["qg"], pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR,
+                                                do, scale, aqk=Aqk, h0=_f32(initial_state), dht=_f32(dht),
+                                                want_dh0=initial_state is not None)
+        saved = dict(v_new=v_new, h=h)
+    else:
+        if saved.get("h") is None:
+            saved = _recompute_vector(q, k, v, g, Akk, initial_state, gates)
+        dh, dR, dh0 = _state_vector(saved, g, do, scale, Aqk, dht, initial_state)
     out = ops.chunk_bwd(q, k, v, _bf(saved["v_new"]), do, dR, g, ops.GATE_VECTOR, Akk,
                         _bf(saved["h"]), dh, scale, beta=_f32(gates.get("beta")),
                         b=None if gates.get("b") is None else _bf(gates["b"]),
@@ -64,12 +75,21 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     return out, dh0
 
 
-def _recompute_vector(q, k, v, g, Akk, initial_state, gates):
-    """w, u, qg, kg (fdr_prepare_wu) then h, v_new (fdr_fwd_h): the recompute policy."""
+def _state_vector(saved, g, do, scale, Aqk, dht, initial_state):
+    return ops.state_bwd(_bf(saved["qg"]), _bf(saved["kg"]), _bf(saved["w"]), g, ops.GATE_VECTOR, do, scale,
+                         aqk=Aqk, dht=_f32(dht), want_dh0=initial_state is not None)
+
+
+def _prepare_vector(k, v, g, Akk, gates, q):
     b = None if gates.get("b") is None else _bf(gates["b"])
     w = None if gates.get("w") is None else _bf(gates["w"])
-    pre = ops.prepare_wu(k, v, Akk, ops.GATE_VECTOR, g=g, beta=_f32(gates.get("beta")), b=b, w=w, q=q,
-                         want_qkg=True)
+    return ops.prepare_wu(k, v, Akk, ops.GATE_VECTOR, g=g, beta=_f32(gates.get("beta")), b=b, w=w, q=q,
+                          want_qkg=True)
+
+
+def _recompute_vector(q, k, v, g, Akk, initial_state, gates):
+    """w, u, qg, kg (fdr_prepare_wu) then h, v_new (fdr_fwd_h): the recompute policy."""
+    pre = _prepare_vector(k, v, g, Akk, gates, q)
     h, v_new, _ = ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state))
     return dict(w=pre["w"], u=pre["u"], qg=pre["qg"], kg=pre["kg"], v_new=v_new, h=h)
 
@@ -123,9 +143,15 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, **kw):
     beta = _f32(beta)
     gate = ops.GATE_SCALAR if op == "gdn" else ops.GATE_NONE
     pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, q=q, want_aqk=True, scale=scale)
-    h, v_new, _ = ops.fwd_h(k, pre["w"], pre["u"], g, gate, h0=_f32(initial_state))
-    dh, dR, dh0 = ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
-                                want_dh0=initial_state is not None)
+    if ops.affine_pays(q):
+        # few heads: both recurrences side by side in affine-step form
+        h, v_new, dh, dR, dh0 = ops.recurrences(q, k, pre["w"], pre["u"], g, gate, do, scale, aqk=pre["Aqk"],
+                                                h0=_f32(initial_state), dht=_f32(dht),
+                                                want_dh0=initial_state is not None)
+    else:
+        h, v_new, _ = ops.fwd_h(k, pre["w"], pre["u"], g, gate, h0=_f32(initial_state), method="direct")
+        dh, dR, dh0 = ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
+                                    want_dh0=initial_state is not None, method="direct")
     out = ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta)
     record(op, "optimized_backward")
     return out, dh0

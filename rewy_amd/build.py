@@ -36,7 +36,7 @@ def hipcc() -> str:
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    extra = os.environ.get("REWY_HIPCC_FLAGS", "").split()   # e.g. -DREWY_INTRA_B_SPLIT=1
+    extra = os.environ.get("REWY_HIPCC_FLAGS", "").split()   # e.g. -DREWY_CHUNK_PIPE=2
     cmd = [hipcc(), *FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

@@ -30,6 +30,34 @@ def _need(x, name, dtype, shape, device):
     return x
 
 
+# Affine-step recurrences pay off when B*H work-groups leave the GPU idle: the
+# direct kernels are then bound by their per-chunk latency.
+AFFINE_MAX_BH = 16
+AFFINE_MIN_CHUNKS = 8
+AFFINE_VALUE_BLOCK = 16
+
+
+def _use_affine(method, B, H, NT):
+    if method not in ("auto", "direct", "affine"):
+        raise ValueError('method must be "auto", "direct" or "affine"')
+    if method == "auto":
+        return B * H <= AFFINE_MAX_BH and NT >= AFFINE_MIN_CHUNKS
+    return method == "affine"
+
+
+def affine_pays(q):
+    """True when the affine-step recurrences are the faster choice for q's shape."""
+    B, T, H = q.shape[:3]
+    return _use_affine("auto", B, H, T // CHUNK)
+
+
+def _affine_workspace(B, NT, H, dev):
+    """Step matrices (bf16 K x K) and offsets (fp32 K x V) of every chunk-head."""
+    n = B * NT * H
+    return (torch.empty(n, K_SUPPORTED, K_SUPPORTED, device=dev, dtype=torch.bfloat16),
+            torch.empty(n, K_SUPPORTED, V_SUPPORTED, device=dev, dtype=torch.float32))
+
+
 def _dims(q):
     if q.ndim != 4:
         raise ValueError("q must be [B,T,H,K]")
@@ -44,8 +72,12 @@ def _dims(q):
 
 
 def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, want_dh0=True,
-              value_block=0):
-    """Reverse state recurrence.  Returns (dh [B,NT,H,K,V] bf16, dR [B,T,H,V] bf16, dh0 fp32|None)."""
+              value_block=0, method="auto"):
+    """Reverse state recurrence.  Returns (dh [B,NT,H,K,V] bf16, dR [B,T,H,V] bf16, dh0 fp32|None).
+
+    method "direct": one kernel (fdr_state_bwd); "affine": chunk-parallel step
+    matrices, a one-product-per-chunk scan and a chunk-parallel dR pass
+    (fdr_affine_*), faster when B*H is too small to fill the GPU; "auto" picks."""
     B, T, H, K = _dims(q)
     V = V_SUPPORTED
     dev = q.device
@@ -74,11 +106,89 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
     dr = torch.empty(B, T, H, V, device=dev, dtype=bf)
     dh0 = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_dh0 else None
     P = _lib.ptr
+    if _use_affine(method, B, H, NT):
+        vb = value_block or AFFINE_VALUE_BLOCK
+        step, offset = _affine_workspace(B, NT, H, dev)
+        dv_local = torch.empty(B, T, H, V, device=dev, dtype=bf) if aqk is not None else None
+        lib = _lib.load()
+        st = lib.fdr_affine_prep_bwd(P(q), P(k), P(w), P(g), int(gate_mode), P(dO), P(aqk), P(dv), P(step),
+                                     P(offset), P(dv_local), B, T, H, K, V, CHUNK, float(scale),
+                                     _lib.stream_handle(dev))
+        _lib.check(st, "fdr_affine_prep_bwd")
+        arr, n = _lib.problems(_lib.ScanProblem, [_lib.ScanProblem(
+            P(step), P(offset), P(g), P(dht), P(dh), P(dh0), int(gate_mode), 1)])
+        _lib.check(lib.fdr_affine_scan(arr, n, B, T, H, K, V, CHUNK, int(vb), _lib.stream_handle(dev)),
+                   "fdr_affine_scan")
+        arr, n = _lib.problems(_lib.SideProblem, [_lib.SideProblem(
+            P(k), P(dh), P(dv_local if dv is None else dv), P(g) if gate_mode == GATE_SCALAR else None,
+            P(dr), 1.0)])
+        _lib.check(lib.fdr_affine_side(arr, n, B, T, H, K, V, CHUNK, _lib.stream_handle(dev)), "fdr_affine_side")
+        return dh, dr, dh0
     st = _lib.load().fdr_state_bwd(P(q), P(k), P(w), P(g), int(gate_mode), P(dO), P(aqk), P(dv),
                                    P(dht), P(dh), P(dr), P(dh0), B, T, H, K, V, CHUNK,
                                    float(scale), int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_state_bwd")
     return dh, dr, dh0
+
+
+def recurrences(q, k, w, u, g, gate_mode, dO, scale, aqk=None, dv=None, h0=None, dht=None, want_dh0=True,
+                value_block=0):
+    """Both state recurrences of the recompute policy in one pass of the affine-step
+    kernels, the forward and the backward recurrence side by side (neither needs the
+    other's states).  q/k as for ``state_bwd`` (qg/kg for a vector gate); w, u from
+    ``prepare_wu``.  Returns (h, v_new, dh, dR, dh0|None), each as ``fwd_h`` /
+    ``state_bwd`` return them."""
+    B, T, H, K = _dims(q)
+    V = V_SUPPORTED
+    dev = q.device
+    bf, f32 = torch.bfloat16, torch.float32
+    for x, n in ((q, "q"), (k, "k"), (w, "w")):
+        _need(x, n, bf, (B, T, H, K), dev)
+    _need(u, "u", bf, (B, T, H, V), dev)
+    _need(dO, "dO", bf, (B, T, H, V), dev)
+    if gate_mode == GATE_VECTOR:
+        _need(g, "g", f32, (B, T, H, K), dev)
+    elif gate_mode == GATE_SCALAR:
+        _need(g, "g", f32, (B, T, H), dev)
+    elif gate_mode != GATE_NONE:
+        raise ValueError("gate_mode must be 0, 1 or 2")
+    if (aqk is None) == (dv is None):
+        raise ValueError("exactly one of aqk / dv is required")
+    if aqk is not None:
+        _need(aqk, "Aqk", f32, (B, T, H, CHUNK), dev)
+    if dv is not None:
+        _need(dv, "dv", bf, (B, T, H, V), dev)
+    for x, n in ((h0, "h0"), (dht, "dht")):
+        if x is not None:
+            _need(x, n, f32, (B, H, K, V), dev)
+    if value_block not in (0, 16, 32, 64):
+        raise ValueError("value_block must be 0, 16, 32 or 64")
+    vb = value_block or AFFINE_VALUE_BLOCK
+    NT = T // CHUNK
+    h = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
+    vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
+    dh = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
+    dr = torch.empty(B, T, H, V, device=dev, dtype=bf)
+    dh0 = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_dh0 else None
+    sb, ob = _affine_workspace(B, NT, H, dev)
+    sf, of = _affine_workspace(B, NT, H, dev)
+    dv_local = torch.empty(B, T, H, V, device=dev, dtype=bf) if aqk is not None else None
+    P = _lib.ptr
+    lib = _lib.load()
+    stream = _lib.stream_handle(dev)
+    _lib.check(lib.fdr_affine_prep_pair(P(q), P(k), P(w), P(u), P(g), int(gate_mode), P(dO), P(aqk), P(dv),
+                                        P(sb), P(ob), P(dv_local), P(sf), P(of), B, T, H, K, V, CHUNK,
+                                        float(scale), stream), "fdr_affine_prep_pair")
+    arr, n = _lib.problems(_lib.ScanProblem, [
+        _lib.ScanProblem(P(sb), P(ob), P(g), P(dht), P(dh), P(dh0), int(gate_mode), 1),
+        _lib.ScanProblem(P(sf), P(of), P(g), P(h0), P(h), None, int(gate_mode), 0)])
+    _lib.check(lib.fdr_affine_scan(arr, n, B, T, H, K, V, CHUNK, int(vb), stream), "fdr_affine_scan")
+    arr, n = _lib.problems(_lib.SideProblem, [
+        _lib.SideProblem(P(k), P(dh), P(dv_local if dv is None else dv),
+                         P(g) if gate_mode == GATE_SCALAR else None, P(dr), 1.0),
+        _lib.SideProblem(P(w), P(h), P(u), None, P(vnew), -1.0)])
+    _lib.check(lib.fdr_affine_side(arr, n, B, T, H, K, V, CHUNK, stream), "fdr_affine_side")
+    return h, vnew, dh, dr, dh0
 
 
 def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None, b=None, w=None):
@@ -169,8 +279,9 @@ def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, 
     return out
 
 
-def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0):
-    """Forward state scan.  Returns (h [B,NT,H,K,V] bf16, v_new [B,T,H,V] bf16, final fp32|None)."""
+def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, method="auto"):
+    """Forward state scan.  Returns (h [B,NT,H,K,V] bf16, v_new [B,T,H,V] bf16, final fp32|None).
+    ``method`` as for ``state_bwd``."""
     B, T, H, K = _dims(k)
     V = V_SUPPORTED
     dev = k.device
@@ -193,6 +304,20 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0):
     vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
     ht = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_final else None
     P = _lib.ptr
+    if _use_affine(method, B, H, NT):
+        vb = value_block or AFFINE_VALUE_BLOCK
+        step, offset = _affine_workspace(B, NT, H, dev)
+        lib = _lib.load()
+        st = lib.fdr_affine_prep_fwd(P(k), P(w), P(u), P(g), int(gate_mode), P(step), P(offset), B, T, H, K, V,
+                                     CHUNK, _lib.stream_handle(dev))
+        _lib.check(st, "fdr_affine_prep_fwd")
+        arr, n = _lib.problems(_lib.ScanProblem, [_lib.ScanProblem(
+            P(step), P(offset), P(g), P(h0), P(h), P(ht), int(gate_mode), 0)])
+        _lib.check(lib.fdr_affine_scan(arr, n, B, T, H, K, V, CHUNK, int(vb), _lib.stream_handle(dev)),
+                   "fdr_affine_scan")
+        arr, n = _lib.problems(_lib.SideProblem, [_lib.SideProblem(P(w), P(h), P(u), None, P(vnew), -1.0)])
+        _lib.check(lib.fdr_affine_side(arr, n, B, T, H, K, V, CHUNK, _lib.stream_handle(dev)), "fdr_affine_side")
+        return h, vnew, ht
     st = _lib.load().fdr_fwd_h(P(k), P(w), P(u), P(g), int(gate_mode), P(h0), P(h), P(vnew), P(ht), B, T, H,
                                K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_h")
