@@ -271,7 +271,7 @@ def cpu_baseline(xs, sv, dO, scale, NTt, nb_max=3):
 
 # The reference's published operator grid (B, T, H), K=V=128, chunk 64, and its H100
 # backward times in microseconds, original FLA -> ReWY, "complete low-level B including
-# recomputation" under CUDA-graph replay (benchmarks/data/h100_data.json:29-306).
+# recomputation" under CUDA-graph replay (benchmarks/data/h100_data.json:36-350).
 PAPER_GRID = [(1, 512, 4), (1, 2048, 4), (1, 8192, 4), (1, 2048, 16), (2, 2048, 16), (1, 8192, 16)]
 H100_US = {
     ("kda", "recompute"): ([89.3, 253.0, 917.2, 603.7, 1091.6, 2316.4], [64.3, 187.8, 742.6, 459.2, 807.4, 1746.9]),
