@@ -236,11 +236,14 @@ struct ScanArgs {
 // GATE is a template parameter so that the gate load is branch-free: a branch
 // around a load makes the compiler's wait counts path-dependent, and it then
 // waits for every outstanding load (the whole prefetch) at the join.
-template <int NCT, int D, int GATE>
-__global__ __launch_bounds__(512) void affine_scan_kernel(ScanArgs p0, ScanArgs p1, int nb0, int T, int H) {
+// NW waves, each owning RT = 8 / NW row tiles of 16 state rows (wave w: tiles w, w + NW, ...).
+// Every wave reads the whole bf16 state from LDS per chunk, so fewer waves read less.
+template <int NCT, int D, int GATE, int NW>
+__global__ __launch_bounds__(64 * NW) void affine_scan_kernel(ScanArgs p0, ScanArgs p1, int nb0, int T, int H) {
   constexpr int BV = 16 * NCT;
   constexpr int NVT = VD / BV;
   constexpr int LDK = KD + 8;
+  constexpr int RT = 8 / NW;
   __shared__ bf16 sT[2][BV][LDK];               // bf16 state, transposed: B operand of A_c S
   // consecutive logical blocks (the value tiles of one head) share an XCD, so the
   // step matrix every tile of a head reads comes from that XCD's L2 after the first
@@ -252,72 +255,111 @@ __global__ __launch_bounds__(512) void affine_scan_kernel(ScanArgs p0, ScanArgs 
   const int b = bh / H, h = bh % H;
   const int NT = T / C;
   const int l = lane_id(), wv = wave_id();
-  const int rt = wv;                            // state rows [16 wv, 16 wv + 16)
   const int v_base = vt * BV;
+  auto rowt = [&](int i) { return wv + NW * i; };
 
-  f32x4 st[NCT];
+  f32x4 st[RT][NCT];
 #pragma unroll
-  for (int ct = 0; ct < NCT; ++ct) {
-    f32x4 a = zero4();
-    if (p.s0) {
-      const float* src = p.s0 + (size_t)bh * KD * VD;
+  for (int i = 0; i < RT; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) a[r] = src[(16 * rt + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)];
+    for (int ct = 0; ct < NCT; ++ct) {
+      f32x4 a = zero4();
+      if (p.s0) {
+        const float* src = p.s0 + (size_t)bh * KD * VD;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a[r] = src[(16 * rowt(i) + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)];
+      }
+      st[i][ct] = a;
     }
-    st[ct] = a;
-  }
 
-  bf16x8 af[D][4];
-  f32x4 yf[D][NCT];
-  f32x4 gl[D];
+  bf16x8 af[D][RT][4];
+  f32x4 yf[D][RT][NCT];
+  f32x4 gl[D][RT];
   auto load = [&](int s, int c) {
     const size_t chh = ((size_t)b * NT + c) * H + h;
-    const bf16* ab = p.a + chh * A_FRAG + (size_t)(rt * 4) * 512 + l * 8;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) af[s][ks] = *reinterpret_cast<const bf16x8*>(ab + ks * 512);
-    const float* yb = p.y + chh * Y_FRAG + l * 4;
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct)
-      yf[s][ct] = *reinterpret_cast<const f32x4*>(yb + (((vt * NCT + ct) * 8 + rt) * 64) * 4);
     const size_t tl = (size_t)b * T + (size_t)c * C + C - 1;
-    if constexpr (GATE == AG_VECTOR) {
-      gl[s] = *reinterpret_cast<const f32x4*>(p.g + (tl * H + h) * KD + 16 * rt + 4 * (l >> 4));
-    } else if constexpr (GATE == AG_SCALAR) {
-      const float x = p.g[tl * H + h];
-      gl[s] = f32x4{x, x, x, x};
-    } else {
-      gl[s] = zero4();
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const bf16* ab = p.a + chh * A_FRAG + (size_t)(rowt(i) * 4) * 512 + l * 8;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) af[s][i][ks] = *reinterpret_cast<const bf16x8*>(ab + ks * 512);
+      const float* yb = p.y + chh * Y_FRAG + l * 4;
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        yf[s][i][ct] = *reinterpret_cast<const f32x4*>(yb + (((vt * NCT + ct) * 8 + rowt(i)) * 64) * 4);
+      if constexpr (GATE == AG_VECTOR) {
+        gl[s][i] = *reinterpret_cast<const f32x4*>(p.g + (tl * H + h) * KD + 16 * rowt(i) + 4 * (l >> 4));
+      } else if constexpr (GATE == AG_SCALAR) {
+        const float x = p.g[tl * H + h];
+        gl[s][i] = f32x4{x, x, x, x};
+      } else {
+        gl[s][i] = zero4();
+      }
     }
   };
   auto publish = [&](int buf) {
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
-      bf16x4 v4;
+    for (int i = 0; i < RT; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[ct][r]);
-      *reinterpret_cast<bf16x4*>(&sT[buf][16 * ct + (l & 15)][16 * rt + 4 * (l >> 4)]) = v4;
+      for (int ct = 0; ct < NCT; ++ct) {
+        bf16x4 v4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[i][ct][r]);
+        *reinterpret_cast<bf16x4*>(&sT[buf][16 * ct + (l & 15)][16 * rowt(i) + 4 * (l >> 4)]) = v4;
+      }
+  };
+  // Per chunk, in dependency order.  Before the barrier: the accumulator seed
+  // -(lam S + Y) (own registers only).  After it: the state's B fragments from LDS,
+  // the global store of S (bf16), two independent MFMA chains over K halves per
+  // tile, the next loads into the slot just consumed (issued while the MFMAs run),
+  // then the new state's bf16 copy into the other LDS buffer.
+  f32x4 seed[RT][NCT];
+  auto prepare = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      f32x4 lam;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lam[r] = fast_exp2(gl[s][i][r]);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) seed[i][ct][r] = -(st[i][ct][r] * lam[r] + yf[s][i][ct][r]);
     }
   };
-  // one step with slot s; sT[buf] holds bf16(S) (published by the barrier just passed)
-  auto step = [&](int s, int c, int buf) {
-    bf16* dst = p.s_out + (((size_t)b * NT + c) * H + h) * KD * VD;
+  auto step = [&](int s, int c, int buf, int c_next) {
+    bf16x8 bfr[NCT][4];
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        dst[(16 * rt + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)] = to_bf16(st[ct][r]);
-    f32x4 lam;
+      for (int ks = 0; ks < 4; ++ks) bfr[ct][ks] = frag(&sT[buf][16 * ct][32 * ks], LDK);
+    bf16* dst = p.s_out + (((size_t)b * NT + c) * H + h) * KD * VD;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) lam[r] = fast_exp2(gl[s][r]);
+    for (int i = 0; i < RT; ++i)
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
-      f32x4 a;
+      for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) a[r] = -(st[ct][r] * lam[r] + yf[s][ct][r]);
+        for (int r = 0; r < 4; ++r)
+          dst[(16 * rowt(i) + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)] = to_bf16(st[i][ct][r]);
+    f32x4 a0[RT][NCT], a1[RT][NCT];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) a = mfma(af[s][ks], frag(&sT[buf][16 * ct][32 * ks], LDK), a);
-      st[ct] = -a;
-    }
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        a0[i][ct] = mfma(af[s][i][0], bfr[ct][0], seed[i][ct]);
+        a1[i][ct] = mfma(af[s][i][2], bfr[ct][2], zero4());
+      }
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        a0[i][ct] = mfma(af[s][i][1], bfr[ct][1], a0[i][ct]);
+        a1[i][ct] = mfma(af[s][i][3], bfr[ct][3], a1[i][ct]);
+      }
+    if (c_next >= 0) load(s, c_next);
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) st[i][ct] = -(a0[i][ct] + a1[i][ct]);
     publish(buf ^ 1);
   };
 
@@ -329,8 +371,9 @@ __global__ __launch_bounds__(512) void affine_scan_kernel(ScanArgs p0, ScanArgs 
   const int rem = NT % D;
   for (int i = 0; i < rem; ++i) {
     load(0, c);
+    prepare(0);
     lds_barrier();
-    step(0, c, buf);
+    step(0, c, buf, -1);
     buf ^= 1;
     c += dir;
   }
@@ -340,19 +383,22 @@ __global__ __launch_bounds__(512) void affine_scan_kernel(ScanArgs p0, ScanArgs 
   for (int j = rem; j < NT; j += D) {
 #pragma unroll
     for (int s = 0; s < D; ++s) {
+      prepare(s);
       lds_barrier();
-      step(s, c, buf);
+      step(s, c, buf, clampc(c + dir * D));
       buf ^= 1;
-      load(s, clampc(c + dir * D));
       c += dir;
     }
   }
   if (p.s_final) {
     float* dst = p.s_final + (size_t)bh * KD * VD;
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct)
+    for (int i = 0; i < RT; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dst[(16 * rt + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)] = st[ct][r];
+      for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          dst[(16 * rowt(i) + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)] = st[i][ct][r];
   }
 }
 
@@ -425,10 +471,21 @@ __global__ __launch_bounds__(512) void affine_side_kernel(SideArgs p0, SideArgs 
   }
 }
 
+// chunks of step operands in flight per scan work-group
+#ifndef REWY_SCAN_DEPTH
+#define REWY_SCAN_DEPTH 4
+#endif
+// waves per scan work-group (8, 4 or 2)
+#ifndef REWY_SCAN_WAVES
+#define REWY_SCAN_WAVES 8
+#endif
+
 template <int NCT, int GATE>
 static hipError_t launch_scan(const ScanArgs& a0, const ScanArgs& a1, int n, int B, int T, int H, hipStream_t s) {
   const int nb = B * H * (VD / (16 * NCT));
-  hipLaunchKernelGGL((affine_scan_kernel<NCT, 4, GATE>), dim3(nb * n), dim3(512), 0, s, a0, a1, nb, T, H);
+  constexpr int NW = REWY_SCAN_WAVES;
+  hipLaunchKernelGGL((affine_scan_kernel<NCT, (NCT >= 4 ? 2 : REWY_SCAN_DEPTH), GATE, NW>), dim3(nb * n), dim3(64 * NW),
+                     0, s, a0, a1, nb, T, H);
   return hipGetLastError();
 }
 
