@@ -14,7 +14,7 @@ record for the dominant kernel (per-launch algorithmic bytes / launch time),
 the same-GPU time of the original 7-product formulation (PyTorch ops) and a
 CPU baseline (the fp64 oracle on a bounded sample, one thread).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config kda|gdn|gdn_cfg|gdn2|kda_long|delta]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config kda|gdn|gdn_cfg|gdn2|kda_long|delta|paper_delta_c2|paper_kda_c5]
     python bench.py --paper-grid      # the reference's published operator grid (one JSON line per family)
 """
 from __future__ import annotations
@@ -44,6 +44,9 @@ CONFIGS = {
     "kda_long": dict(op="kda", B=1, T=65536, H=16, seed=4, gate="kda_long", h0=True, full_saving=True),
     # BASELINE.json configs[0] shape (its CPU reference path is the oracle test suite)
     "delta": dict(op="delta", B=1, T=256, H=2, seed=0, gate=None, h0=False, full_saving=False),
+    # two cases of the reference's published operator grid (few heads: affine-step recurrences)
+    "paper_delta_c2": dict(op="delta", B=1, T=8192, H=4, seed=12, gate=None, h0=True, full_saving=False),
+    "paper_kda_c5": dict(op="kda", B=1, T=8192, H=16, seed=15, gate="kda", h0=False, full_saving=False),
 }
 
 TILE = 64 * 128 * 2          # one [64][128] bf16 tile
@@ -71,6 +74,11 @@ def kernel_costs(op, full_saving):
     rd = 5 * TILE + g_b + gates_b + AT + 2 * HS + (TILE if vb else 0)
     wr = 3 * TILE + g_b + (2 * TILE if vb else beta_b)
     costs["fdr_chunk_bwd"] = (rd + wr, 3 * mm(64, 64, 128) + 3 * mm(64, 128, 128) + 4 * mm(64, 64, 128))
+    # the affine-step launches compute the same recurrences: same operands and results
+    # (their private step-matrix workspace is not algorithmic traffic)
+    costs["affine_state"] = costs["fdr_state_bwd"]
+    if not full_saving:
+        costs["affine_recurrences"] = tuple(a + b for a, b in zip(costs["fdr_fwd_h"], costs["fdr_state_bwd"]))
     return costs
 
 
@@ -158,11 +166,23 @@ def setup(cfg, device):
         pre = kern["fdr_prepare_wu"]()
         ks, qs, ws = (pre["kg"], pre["qg"], pre["w"]) if vec else (xs["k"], xs["q"], pre["w"])
         aqk = sv["Aqk"] if vec else pre["Aqk"]
-        kern["fdr_fwd_h"] = lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"])
-        h, v_new, _ = kern["fdr_fwd_h"]()
-    kern["fdr_state_bwd"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
-                                                  want_dh0=xs["h0"] is not None)
-    dh, dR, _ = kern["fdr_state_bwd"]()
+    if ops.affine_pays(xs["q"]):
+        # few heads: the backend runs the recurrences in affine-step form (prep, scan, side launches)
+        if keep:
+            kern["affine_state"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
+                                                         want_dh0=xs["h0"] is not None, method="affine")
+            dh, dR, _ = kern["affine_state"]()
+        else:
+            kern["affine_recurrences"] = lambda: ops.recurrences(qs, ks, ws, pre["u"], g, gate, dO, scale, aqk=aqk,
+                                                                 h0=xs["h0"], want_dh0=xs["h0"] is not None)
+            h, v_new, dh, dR, _ = kern["affine_recurrences"]()
+    else:
+        if not keep:
+            kern["fdr_fwd_h"] = lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"], method="direct")
+            h, v_new, _ = kern["fdr_fwd_h"]()
+        kern["fdr_state_bwd"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
+                                                      want_dh0=xs["h0"] is not None, method="direct")
+        dh, dR, _ = kern["fdr_state_bwd"]()
     kern["fdr_chunk_bwd"] = lambda: ops.chunk_bwd(xs["q"], xs["k"], xs["v"], v_new, dO, dR, g, gate, sv["Akk"], h,
                                                   dh, scale, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"))
     return xs, dO, sv, step, kern, (dh, dR), forward
@@ -211,7 +231,7 @@ def measure(cfg, steps, warmup):
         by, fl = costs[n]
         kernels[n] = dict(ms=round(t, 4), gbs=round(by * NTt / (t * 1e-3) / 1e9, 1),
                           tflops=round(fl * NTt / (t * 1e-3) / 1e12, 2), bytes_per_launch=by * NTt)
-    flops = sum(c[1] for c in costs.values()) * NTt
+    flops = sum(costs[n][1] for n in kt) * NTt
     return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9, kernels=kernels, NTt=NTt,
                 xs=xs, dO=dO, sv=sv, step=step, inter=inter, fwd_ms=fwd_ms)
 
