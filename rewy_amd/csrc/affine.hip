@@ -52,7 +52,7 @@ struct PrepSmem {
       bf16 xq[C * KD];     // bwd: qg
     } in;
     bf16 m[KD][KD + 8];    // the K x K product, row-major, for the fragment-order store
-  } u;
+  } t;
   bf16 y0[C * VD];         // bwd: dO | fwd: u   (swizzled rows [t][v])
   bf16 dv[C * VD];         // bwd: dv_local, bf16 (swizzled rows)
   bf16 ah[C * C];          // bwd: Aqk hi, rows [t][s] (8-chunk swizzle)
@@ -112,11 +112,11 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
       kk = scale_bf16x8(kk, fast_exp2(glast - gt));      // kg = k 2^(g_last - g_t)
     }
     if constexpr (BWD) {
-      store_tr_chunk<16>(sm.u.in.xa, t, cc, ww);
-      store_tr_chunk<16>(sm.u.in.xb, t, cc, kk);
+      store_tr_chunk<16>(sm.t.in.xa, t, cc, ww);
+      store_tr_chunk<16>(sm.t.in.xb, t, cc, kk);
       u32x4 qq = *reinterpret_cast<const u32x4*>(q + o);
       if constexpr (GATE == AG_SCALAR) qq = scale_bf16x8(qq, fast_exp2(gt));   // qg = q 2^(g_t)
-      store_tr_chunk<16>(sm.u.in.xq, t, cc, qq);
+      store_tr_chunk<16>(sm.t.in.xq, t, cc, qq);
       if constexpr (DV_FROM_AQK) {
         const f32x4 a = *reinterpret_cast<const f32x4*>(aqk + ((tok0 + t) * H + h) * C + cc * 4);
         bf16x4 lo;
@@ -127,8 +127,8 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
         store_tr_chunk<16>(sm.dv, t, cc, *reinterpret_cast<const u32x4*>(dv_in + vofs + (size_t)t * rsv + cc * 8));
       }
     } else {
-      store_tr_chunk<16>(sm.u.in.xa, t, cc, kk);
-      store_tr_chunk<16>(sm.u.in.xb, t, cc, ww);
+      store_tr_chunk<16>(sm.t.in.xa, t, cc, kk);
+      store_tr_chunk<16>(sm.t.in.xb, t, cc, ww);
     }
     store_tr_chunk<16>(sm.y0, t, cc, *reinterpret_cast<const u32x4*>(y_src + vofs + (size_t)t * rsv + cc * 8));
   }
@@ -164,7 +164,7 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
   const int rt = wv;
   bf16x8 af[2];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) af[ks] = frag_tr<16>(sm.u.in.xa, 32 * ks, 16 * rt);
+  for (int ks = 0; ks < 2; ++ks) af[ks] = frag_tr<16>(sm.t.in.xa, 32 * ks, 16 * rt);
   f32x4 pm[8];
   float* ydst = y_frag + (size_t)ch * Y_FRAG;
 #pragma unroll
@@ -172,7 +172,7 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
     f32x4 a = zero4(), y = zero4();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      a = mfma(af[ks], frag_tr<16>(sm.u.in.xb, 32 * ks, 16 * ct), a);
+      a = mfma(af[ks], frag_tr<16>(sm.t.in.xb, 32 * ks, 16 * ct), a);
       if constexpr (BWD) {
         y = mfma(af[ks], frag_tr<16>(sm.dv, 32 * ks, 16 * ct), y);          // w^T dv
       } else {
@@ -183,7 +183,7 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
       f32x4 x = zero4();
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        x = mfma(frag_tr<16>(sm.u.in.xq, 32 * ks, 16 * rt), frag_tr<16>(sm.y0, 32 * ks, 16 * ct), x);
+        x = mfma(frag_tr<16>(sm.t.in.xq, 32 * ks, 16 * rt), frag_tr<16>(sm.y0, 32 * ks, 16 * ct), x);
 #pragma unroll
       for (int r = 0; r < 4; ++r) y[r] = scale * x[r] - y[r];
     }
@@ -194,7 +194,7 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
 #pragma unroll
   for (int ct = 0; ct < 8; ++ct)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sm.u.m[16 * rt + 4 * (l >> 4) + r][16 * ct + (l & 15)] = to_bf16(pm[ct][r]);
+    for (int r = 0; r < 4; ++r) sm.t.m[16 * rt + 4 * (l >> 4) + r][16 * ct + (l & 15)] = to_bf16(pm[ct][r]);
   lds_barrier();
   bf16* adst = a_frag + (size_t)ch * A_FRAG;
 #pragma unroll
@@ -202,7 +202,7 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
     const int p = tid + 512 * i;                  // block p >> 6 = rt' * 4 + ks, lane p & 63
     const int blk = p >> 6, L = p & 63;
     const int row = 16 * (blk >> 2) + (L & 15), col = 32 * (blk & 3) + 8 * (L >> 4);
-    *reinterpret_cast<u32x4*>(adst + (size_t)p * 8) = *reinterpret_cast<const u32x4*>(&sm.u.m[row][col]);
+    *reinterpret_cast<u32x4*>(adst + (size_t)p * 8) = *reinterpret_cast<const u32x4*>(&sm.t.m[row][col]);
   }
 }
 
@@ -237,7 +237,8 @@ struct ScanArgs {
 // around a load makes the compiler's wait counts path-dependent, and it then
 // waits for every outstanding load (the whole prefetch) at the join.
 // NW waves, each owning RT = 8 / NW row tiles of 16 state rows (wave w: tiles w, w + NW, ...).
-// Every wave reads the whole bf16 state from LDS per chunk, so fewer waves read less.
+// Every wave reads the whole bf16 state from LDS per chunk; fewer waves read less but each
+// runs a longer chain per chunk, and 8 measured fastest.
 template <int NCT, int D, int GATE, int NW>
 __global__ __launch_bounds__(64 * NW) void affine_scan_kernel(ScanArgs p0, ScanArgs p1, int nb0, int T, int H) {
   constexpr int BV = 16 * NCT;
