@@ -36,6 +36,30 @@ constexpr float RCP_LN2 = 1.4426950408889634f;
 constexpr float WIDE = 100.f;   // diagonal-block gate span that takes the pairwise path
 }  // namespace fwd
 
+// LDS of fwd_prepare: the staged rows and gates are dead once the 16 x 16 tiles are
+// formed, so the inverse's matrices reuse their bytes (KDA: 69 KiB, two work-groups per CU).
+template <int GATE, bool VEC_B>
+struct PrepareSmem {
+  struct In {
+    bf16 q[C][fwd::LDK];
+    bf16 k[C][fwd::LDK];
+    bf16 b[VEC_B ? C : 1][fwd::LDK];
+    float g[GATE == FG_VECTOR ? C : 1][fwd::LDG];
+  };
+  struct Inv {
+    float M[C][fwd::LDM];    // strict_tril(b k k^T 2^(g_i-g_s))
+    float X[C][fwd::LDM];    // (I + M)^-1
+    float T[32][36];         // products of the block inverse
+  };
+  union {
+    In in;
+    Inv inv;
+  };
+  float gs[C];               // scalar gate (log2 cumsum) per row
+  float beta[C];
+  int wide[4];               // diagonal block I takes the pairwise path
+};
+
 template <int GATE, bool VEC_B>
 __global__ __launch_bounds__(512) void fwd_prepare_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ graw,
@@ -44,16 +68,17 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
   using fwd::LDG;
   using fwd::LDK;
   using fwd::LDM;
-  __shared__ __attribute__((aligned(16))) bf16 sq[C][LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sk[C][LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sb[VEC_B ? C : 1][LDK];
-  __shared__ __attribute__((aligned(16))) float sg[GATE == FG_VECTOR ? C : 1][LDG];
-  __shared__ float sgs[C];        // scalar gate (log2 cumsum) per row
-  __shared__ float sbeta[C];
-  __shared__ float sM[C][LDM];    // strict_tril(b k k^T 2^(g_i-g_s)), then the inverse
-  __shared__ float sX[C][LDM];    // (I + M)^-1
-  __shared__ __attribute__((aligned(16))) float sT[32][36];    // products of the block inverse
-  __shared__ int sWide[4];        // diagonal block I takes the pairwise path
+  __shared__ __attribute__((aligned(16))) PrepareSmem<GATE, VEC_B> sm;
+  auto& sq = sm.in.q;
+  auto& sk = sm.in.k;
+  auto& sb = sm.in.b;
+  auto& sg = sm.in.g;
+  auto& sgs = sm.gs;
+  auto& sbeta = sm.beta;
+  auto& sM = sm.inv.M;
+  auto& sX = sm.inv.X;
+  auto& sT = sm.inv.T;
+  auto& sWide = sm.wide;
 
   const int blk = blockIdx.x;
   const int NT = T / C;
@@ -143,13 +168,14 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
   // ---- 16 x 16 tiles (I, J), J <= I: Aqk and M by anchored MFMAs ----
   // wave -> (row block I, first column block J0, tile count): the two waves with two tiles
   // form the q / b k row operands of block I once for both; every wave has at most two.
+  const int I = wv == 0 || wv == 2 || wv == 3 ? 3 : wv == 1 || wv == 4 ? 2 : wv == 7 ? 0 : 1;
+  const int J0 = wv == 2 ? 2 : wv == 3 ? 3 : wv == 4 ? 2 : wv == 6 ? 1 : 0;
+  const int NJ = wv < 2 ? 2 : 1;
+  f32x4 mkk[2] = {zero4(), zero4()};
   {
-    const int I = wv == 0 || wv == 2 || wv == 3 ? 3 : wv == 1 || wv == 4 ? 2 : wv == 7 ? 0 : 1;
-    const int J0 = wv == 2 ? 2 : wv == 3 ? 3 : wv == 4 ? 2 : wv == 6 ? 1 : 0;
-    const int NJ = wv < 2 ? 2 : 1;
     const bool pairwise = NJ == 1 && J0 == I && sWide[I];
     const int n = 16 * I;                       // anchor row
-    f32x4 aqk[2] = {zero4(), zero4()}, mkk[2] = {zero4(), zero4()};
+    f32x4 aqk[2] = {zero4(), zero4()};
     if (!pairwise) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
@@ -222,18 +248,38 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * I + 4 * lg + r;
         aqk_out[mofs + (size_t)i * rsm + s] = (s <= i) ? scale * aqk[jj][r] : 0.f;
-        sM[i][s] = (s < i) ? mkk[jj][r] : 0.f;
       }
     }
   }
-  // zero upper tiles of Aqk and M (J > I)
-  for (int p = tid; p < 6 * 256; p += 512) {
+  // zero upper tiles of Aqk (J > I)
+  auto upper = [](int p, int& i, int& s) {
     const int tix = p >> 8, e = p & 255;
-    const int I = tix < 3 ? 0 : tix < 5 ? 1 : 2;
-    const int J = I + 1 + (tix - (I == 0 ? 0 : I == 1 ? 3 : 5));
-    const int i = 16 * I + (e >> 4), s = 16 * J + (e & 15);
-    aqk_out[mofs + (size_t)i * rsm + s] = 0.f;
-    sM[i][s] = 0.f;
+    const int I_ = tix < 3 ? 0 : tix < 5 ? 1 : 2;
+    const int J = I_ + 1 + (tix - (I_ == 0 ? 0 : I_ == 1 ? 3 : 5));
+    i = 16 * I_ + (e >> 4);
+    s = 16 * J + (e & 15);
+  };
+  for (int p = tid; p < 6 * 256; p += 512) {
+    int i, s_;
+    upper(p, i, s_);
+    aqk_out[mofs + (size_t)i * rsm + s_] = 0.f;
+  }
+  lds_barrier();                                // staged rows and gates dead: M and X take their LDS
+  // M tiles from the accumulators (lane: rows i = 16 I + 4 lg + r, column s = 16 J + lc), upper tiles zero
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    if (jj >= NJ) break;
+    const int s_ = 16 * (J0 + jj) + lc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * I + 4 * lg + r;
+      sM[i][s_] = (s_ < i) ? mkk[jj][r] : 0.f;
+    }
+  }
+  for (int p = tid; p < 6 * 256; p += 512) {
+    int i, s_;
+    upper(p, i, s_);
+    sM[i][s_] = 0.f;
   }
   lds_barrier();
 
@@ -324,11 +370,11 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
                                                      const float* __restrict__ aqk, const bf16* __restrict__ hst,
                                                      const bf16* __restrict__ vnew, bf16* __restrict__ o_out,
                                                      int T, int H, float scale) {
-  using fwd::LDK;
-  __shared__ __attribute__((aligned(16))) bf16 sqg[C][LDK];       // scale q 2^g rows, hi
-  __shared__ __attribute__((aligned(16))) bf16 sqgl[C][LDK];      // lo
-  __shared__ __attribute__((aligned(16))) bf16 sah[C][C + 8];     // Aqk rows [i][s], hi
-  __shared__ __attribute__((aligned(16))) bf16 sal[C][C + 8];     // lo
+  // swizzled, unpadded tiles (80 KiB in all, so two work-groups share a CU)
+  __shared__ __attribute__((aligned(16))) bf16 sqg[C * KD];       // scale q 2^g rows [i][k], hi
+  __shared__ __attribute__((aligned(16))) bf16 sqgl[C * KD];      // lo
+  __shared__ __attribute__((aligned(16))) bf16 sah[C * C];        // Aqk rows [i][s], hi
+  __shared__ __attribute__((aligned(16))) bf16 sal[C * C];        // lo
   __shared__ __attribute__((aligned(16))) bf16 sv[C * VD];        // v_new rows (swizzled)
   __shared__ __attribute__((aligned(16))) bf16 shT[C * KD];       // 64 rows of h [k][v] (swizzled)
   // (q h) contracts over K = the rows of h, read transposed; h is staged in two halves.
@@ -365,15 +411,15 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
       hi[j] = hh;
       lo[j] = ll;
     }
-    *reinterpret_cast<bf16x8*>(&sqg[t][c8]) = hi;
-    *reinterpret_cast<bf16x8*>(&sqgl[t][c8]) = lo;
+    store_tr_chunk<16>(sqg, t, p & 15, __builtin_bit_cast(u32x4, hi));
+    store_tr_chunk<16>(sqgl, t, p & 15, __builtin_bit_cast(u32x4, lo));
     store_tr_chunk<16>(sv, t, p & 15, *reinterpret_cast<const u32x4*>(vnew + kofs + (size_t)t * rsk + c8));
     const int c4 = (p & 15) * 4;
     const f32x4 a = *reinterpret_cast<const f32x4*>(aqk + mofs + (size_t)t * rsm + c4);
     bf16x4 alo;
     const bf16x4 ahi = split_hi4(a, alo);
-    *reinterpret_cast<bf16x4*>(&sah[t][c4]) = ahi;
-    *reinterpret_cast<bf16x4*>(&sal[t][c4]) = alo;
+    *reinterpret_cast<bf16x4*>(sah + tr_off<8>(t, c4)) = ahi;
+    *reinterpret_cast<bf16x4*>(sal + tr_off<8>(t, c4)) = alo;
   }
   // wave w: output rows 16 (w & 3) .. +16, columns 64 (w >> 2) .. +64 (4 tiles)
   const int I = wv & 3, cb = 64 * (wv >> 2);
@@ -390,8 +436,8 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
     lds_barrier();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const bf16x8 ah = frag(&sqg[16 * I][64 * half + 32 * ks], LDK);
-      const bf16x8 al = frag(&sqgl[16 * I][64 * half + 32 * ks], LDK);
+      const bf16x8 ah = frag_row<16>(sqg, 16 * I, 64 * half + 32 * ks);
+      const bf16x8 al = frag_row<16>(sqgl, 16 * I, 64 * half + 32 * ks);
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
         const bf16x8 bh_ = frag_tr<16>(shT, 32 * ks, cb + 16 * ct);   // h rows over K, columns v
@@ -403,8 +449,8 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
   // Aqk v_new: A = Aqk rows i (s-contiguous), B = v_new rows read transposed
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    const bf16x8 ah = frag(&sah[16 * I][32 * ks], C + 8);
-    const bf16x8 al = frag(&sal[16 * I][32 * ks], C + 8);
+    const bf16x8 ah = frag_row<8>(sah, 16 * I, 32 * ks);
+    const bf16x8 al = frag_row<8>(sal, 16 * I, 32 * ks);
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       const bf16x8 bv = frag_tr<16>(sv, 32 * ks, cb + 16 * ct);
