@@ -32,7 +32,9 @@ def _run(op, xs, dO, backend, **kw):
 
 @pytest.mark.parametrize("op,kw", [("kda", dict(disable_recompute=True)), ("kda", dict(disable_recompute=False)),
                                    ("gdn", {}), ("gdn2", dict(disable_recompute=True)), ("delta", {})])
-@pytest.mark.parametrize("T", [128, 320])
+# T = 640: ten chunks at B*H = 4, so the forward and backward state recurrences take the
+# affine-step kernels (fewer chunks or more heads take the direct ones)
+@pytest.mark.parametrize("T", [128, 320, 640])
 def test_public_backward_matches_oracle(op, kw, T):
     import rewy_amd as fdr
     print(f"\n[e2e] op={op} kw={kw} T={T}", flush=True)
