@@ -44,19 +44,26 @@ constexpr int Y_FRAG = KD * VD;   // fp32 elements of one chunk-head's offset
 // ---------------------------------------------------------------------------
 // prep: step matrix and offset of every chunk-head
 // ---------------------------------------------------------------------------
+// 80 KiB, two work-groups per CU: the K x K product's staging reuses the inputs'
+// bytes after the last MFMA, and (backward with Aqk) kg is written over Aqk's hi / lo
+// split once dv_local is formed.
 struct PrepSmem {
   union {
     struct {
       bf16 xa[C * KD];     // A side of the K x K product, swizzled rows [t][k]: w (bwd) | kg (fwd)
-      bf16 xb[C * KD];     // B side: kg (bwd) | w (fwd)
       bf16 xq[C * KD];     // bwd: qg
+      bf16 y0[C * VD];     // bwd: dO | fwd: u   (swizzled rows [t][v])
+      bf16 dv[C * VD];     // bwd: dv_local, bf16 (swizzled rows)
     } in;
     bf16 m[KD][KD + 8];    // the K x K product, row-major, for the fragment-order store
   } t;
-  bf16 y0[C * VD];         // bwd: dO | fwd: u   (swizzled rows [t][v])
-  bf16 dv[C * VD];         // bwd: dv_local, bf16 (swizzled rows)
-  bf16 ah[C * C];          // bwd: Aqk hi, rows [t][s] (8-chunk swizzle)
-  bf16 al[C * C];          // bwd: Aqk lo
+  union {
+    struct {
+      bf16 ah[C * C];      // bwd: Aqk hi, rows [t][s] (8-chunk swizzle)
+      bf16 al[C * C];      // bwd: Aqk lo
+    } a;
+    bf16 xb[C * KD];       // B side of the K x K product: kg (bwd) | w (fwd)
+  } s;
 };
 
 struct PrepArgs {
@@ -97,6 +104,8 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
   const size_t kofs = tok0 * rsk + (size_t)h * KD, vofs = tok0 * rsv + (size_t)h * VD;
 
   // ---- stage: 1024 16-byte pieces per [64][128] tile, 2 per thread ----
+  constexpr bool KG_LATE = BWD && DV_FROM_AQK;   // kg waits in registers for Aqk's LDS
+  u32x4 kreg[2];
   float glast = 0.f;
   if constexpr (GATE == AG_SCALAR) glast = g[(tok0 + C - 1) * H + h];
 #pragma unroll
@@ -113,7 +122,8 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
     }
     if constexpr (BWD) {
       store_tr_chunk<16>(sm.t.in.xa, t, cc, ww);
-      store_tr_chunk<16>(sm.t.in.xb, t, cc, kk);
+      if constexpr (KG_LATE) kreg[i] = kk;
+      else store_tr_chunk<16>(sm.s.xb, t, cc, kk);
       u32x4 qq = *reinterpret_cast<const u32x4*>(q + o);
       if constexpr (GATE == AG_SCALAR) qq = scale_bf16x8(qq, fast_exp2(gt));   // qg = q 2^(g_t)
       store_tr_chunk<16>(sm.t.in.xq, t, cc, qq);
@@ -121,16 +131,16 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
         const f32x4 a = *reinterpret_cast<const f32x4*>(aqk + ((tok0 + t) * H + h) * C + cc * 4);
         bf16x4 lo;
         const bf16x4 hi = split_hi4(a, lo);
-        *reinterpret_cast<bf16x4*>(sm.ah + tr_off<8>(t, cc * 4)) = hi;
-        *reinterpret_cast<bf16x4*>(sm.al + tr_off<8>(t, cc * 4)) = lo;
+        *reinterpret_cast<bf16x4*>(sm.s.a.ah + tr_off<8>(t, cc * 4)) = hi;
+        *reinterpret_cast<bf16x4*>(sm.s.a.al + tr_off<8>(t, cc * 4)) = lo;
       } else {
-        store_tr_chunk<16>(sm.dv, t, cc, *reinterpret_cast<const u32x4*>(dv_in + vofs + (size_t)t * rsv + cc * 8));
+        store_tr_chunk<16>(sm.t.in.dv, t, cc, *reinterpret_cast<const u32x4*>(dv_in + vofs + (size_t)t * rsv + cc * 8));
       }
     } else {
       store_tr_chunk<16>(sm.t.in.xa, t, cc, kk);
-      store_tr_chunk<16>(sm.t.in.xb, t, cc, ww);
+      store_tr_chunk<16>(sm.s.xb, t, cc, ww);
     }
-    store_tr_chunk<16>(sm.y0, t, cc, *reinterpret_cast<const u32x4*>(y_src + vofs + (size_t)t * rsv + cc * 8));
+    store_tr_chunk<16>(sm.t.in.y0, t, cc, *reinterpret_cast<const u32x4*>(y_src + vofs + (size_t)t * rsv + cc * 8));
   }
   lds_barrier();
 
@@ -143,21 +153,24 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
       f32x4 a = zero4();
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8 bo = frag_tr<16>(sm.y0, 32 * ks, 16 * ct);
-        a = mfma(frag_tr<8>(sm.ah, 32 * ks, 16 * rt), bo, a);
-        a = mfma(frag_tr<8>(sm.al, 32 * ks, 16 * rt), bo, a);
+        const bf16x8 bo = frag_tr<16>(sm.t.in.y0, 32 * ks, 16 * ct);
+        a = mfma(frag_tr<8>(sm.s.a.ah, 32 * ks, 16 * rt), bo, a);
+        a = mfma(frag_tr<8>(sm.s.a.al, 32 * ks, 16 * rt), bo, a);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sm.dv[tr_off<16>(16 * rt + 4 * (l >> 4) + r, 16 * ct + (l & 15))] = to_bf16(a[r]);
+      for (int r = 0; r < 4; ++r)
+        sm.t.in.dv[tr_off<16>(16 * rt + 4 * (l >> 4) + r, 16 * ct + (l & 15))] = to_bf16(a[r]);
     }
-    lds_barrier();
+    lds_barrier();                               // dv complete, Aqk's hi / lo dead
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + 512 * i;
       const int t = p >> 4, cc = p & 15;
+      store_tr_chunk<16>(sm.s.xb, t, cc, kreg[i]);
       *reinterpret_cast<u32x4*>(dv_out + vofs + (size_t)t * rsv + cc * 8) =
-          *reinterpret_cast<const u32x4*>(sm.dv + tr_off<16>(t, cc * 8));
+          *reinterpret_cast<const u32x4*>(sm.t.in.dv + tr_off<16>(t, cc * 8));
     }
+    lds_barrier();
   }
 
   // ---- K x K product and offset: wave wv owns output rows [16 wv, 16 wv + 16) ----
@@ -172,25 +185,25 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
     f32x4 a = zero4(), y = zero4();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      a = mfma(af[ks], frag_tr<16>(sm.t.in.xb, 32 * ks, 16 * ct), a);
+      a = mfma(af[ks], frag_tr<16>(sm.s.xb, 32 * ks, 16 * ct), a);
       if constexpr (BWD) {
-        y = mfma(af[ks], frag_tr<16>(sm.dv, 32 * ks, 16 * ct), y);          // w^T dv
+        y = mfma(af[ks], frag_tr<16>(sm.t.in.dv, 32 * ks, 16 * ct), y);     // w^T dv
       } else {
-        y = mfma(af[ks], frag_tr<16>(sm.y0, 32 * ks, 16 * ct), y);          // kg^T u
+        y = mfma(af[ks], frag_tr<16>(sm.t.in.y0, 32 * ks, 16 * ct), y);     // kg^T u
       }
     }
     if constexpr (BWD) {
       f32x4 x = zero4();
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        x = mfma(frag_tr<16>(sm.t.in.xq, 32 * ks, 16 * rt), frag_tr<16>(sm.y0, 32 * ks, 16 * ct), x);
+        x = mfma(frag_tr<16>(sm.t.in.xq, 32 * ks, 16 * rt), frag_tr<16>(sm.t.in.y0, 32 * ks, 16 * ct), x);
 #pragma unroll
       for (int r = 0; r < 4; ++r) y[r] = scale * x[r] - y[r];
     }
     pm[ct] = a;
     *reinterpret_cast<f32x4*>(ydst + ((ct * 8 + rt) * 64 + l) * 4) = y;
   }
-  lds_barrier();                                  // every wave done with xa / xb / xq
+  lds_barrier();                                  // every wave done with the staged inputs
 #pragma unroll
   for (int ct = 0; ct < 8; ++ct)
 #pragma unroll
