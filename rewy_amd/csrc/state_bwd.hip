@@ -38,8 +38,10 @@ struct StateSmem {
   float lam[KD];           // exp2(g_last) per key row
 };
 
-template <int BV, int GATE, bool DV_FROM_AQK>
-__global__ __launch_bounds__(512) void state_bwd_kernel(
+// NW waves: 8 (wave w owns state rows [16 w, 16 w + 16), every value column) or 16
+// (row tile w % 8, half of the value columns).
+template <int BV, int GATE, bool DV_FROM_AQK, int NW>
+__global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ w,
     const float* __restrict__ g, const bf16* __restrict__ dO, const float* __restrict__ aqk,
     const bf16* __restrict__ dv, const float* __restrict__ dht, bf16* __restrict__ dh_out,
@@ -56,38 +58,43 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int v_base = vt * BV;
 
-  // ---- state accumulators: wave wv owns key rows [16 wv, 16 wv + 16) ----
-  constexpr int NTH = 512;
-  f32x4 st[NCT];
+  // ---- state accumulators: wave wv owns key rows [16 rt, 16 rt + 16), column tiles ct0 .. ----
+  constexpr int NTH = 64 * NW;
+  constexpr int CG = NW / 8;                // waves per row tile
+  constexpr int NCW = NCT / CG;             // column tiles per wave
+  static_assert(NCW >= 1, "value tile too narrow for the wave count");
+  const int rt = wv % 8, ct0 = NCW * (wv / 8);
+  f32x4 st[NCW];
 #pragma unroll
-  for (int ct = 0; ct < NCT; ++ct) {
+  for (int j = 0; j < NCW; ++j) {
     f32x4 a = zero4();
     if (dht) {
       const float* src = dht + (size_t)bh * KD * VD;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int kr = 16 * wv + 4 * (l >> 4) + r;
-        a[r] = src[kr * VD + v_base + 16 * ct + (l & 15)];
+        const int kr = 16 * rt + 4 * (l >> 4) + r;
+        a[r] = src[kr * VD + v_base + 16 * (ct0 + j) + (l & 15)];
       }
     }
-    st[ct] = a;
+    st[j] = a;
   }
   // dR tiles: wave wv owns row tile (wv & 3) and column tiles [DCT * (wv >> 2), DCT * (wv >> 2) + DCT)
-  constexpr int DCT = NCT >= 2 ? NCT / 2 : 1;
+  constexpr int DCT = 4 * NCT >= NW ? 4 * NCT / NW : 1;
   const int drow = wv & 3;
   const int dct0 = DCT * (wv >> 2);
   const bool has_dr = dct0 < NCT;
 
   // ---- register staging of one chunk's operands (lanes run along rows) ----
-  // kg, qg, w rows:  1024 16-byte pieces each, 2 per thread
-  // Aqk rows (fp32): 1024 16-byte pieces, 2 per thread
+  // kg, qg, w rows:  1024 16-byte pieces each, NPI per thread
+  // Aqk rows (fp32): 1024 16-byte pieces, NPI per thread
   // dO rows:         8 * BV pieces
+  constexpr int NPI = 1024 / NTH;
   constexpr int CHV = S::CHV;
   constexpr int NPD = C * CHV;
   constexpr int NDO = (NPD + NTH - 1) / NTH;
-  u32x4 rk[2], rq[2], rw[2], rdo[NDO];
-  f32x4 ra[2];
-  float rg_last = 0.f, rg_tok[2] = {0.f, 0.f};   // scalar gate: last row, the 2 rows this thread stages
+  u32x4 rk[NPI], rq[NPI], rw[NPI], rdo[NDO];
+  f32x4 ra[NPI];
+  float rg_last = 0.f, rg_tok[NPI];             // scalar gate: last row, the rows this thread stages
   const size_t row_stride_k = (size_t)H * KD;   // elements between tokens
   const size_t row_stride_v = (size_t)H * VD;
 
@@ -98,12 +105,12 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
       if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
     } else if constexpr (GATE == GATE_SCALAR) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) rg_tok[i] = g[(tok0 + ((tid + NTH * i) >> 4)) * H + h];
+      for (int i = 0; i < NPI; ++i) rg_tok[i] = g[(tok0 + ((tid + NTH * i) >> 4)) * H + h];
       rg_last = g[(tok0 + C - 1) * H + h];
     }
     const size_t kofs = tok0 * row_stride_k + (size_t)h * KD;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NPI; ++i) {
       const int p = tid + NTH * i;
       const size_t o = kofs + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8;
       rk[i] = *reinterpret_cast<const u32x4*>(k + o);
@@ -130,7 +137,7 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
       if (tid < KD) sm.lam[tid] = 1.f;
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NPI; ++i) {
       const int p = tid + NTH * i;
       const int t = p >> 4, ch = p & 15;
       u32x4 kq = rk[i], qq = rq[i];
@@ -163,23 +170,23 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
     if (c > 0) load_chunk(c - 1);          // prefetch; consumed next iteration
     // dh (state at the end of chunk c) -> LDS, transposed, bf16
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
+    for (int j = 0; j < NCW; ++j) {
       bf16x4 v4;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[ct][r]);
-      *reinterpret_cast<bf16x4*>(&sm.dhT[16 * ct + (l & 15)][16 * wv + 4 * (l >> 4)]) = v4;
+      for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[j][r]);
+      *reinterpret_cast<bf16x4*>(&sm.dhT[16 * (ct0 + j) + (l & 15)][16 * rt + 4 * (l >> 4)]) = v4;
     }
     lds_barrier();
 
     // X = qg^T dO (independent of dh)
-    f32x4 xq[NCT];
+    f32x4 xq[NCW];
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
+    for (int j = 0; j < NCW; ++j) {
       f32x4 a = zero4();
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag_tr<16>(sm.q, 32 * ks, 16 * wv), frag_tr<CHV>(sm.dO, 32 * ks, 16 * ct), a);
-      xq[ct] = a;
+        a = mfma(frag_tr<16>(sm.q, 32 * ks, 16 * rt), frag_tr<CHV>(sm.dO, 32 * ks, 16 * (ct0 + j)), a);
+      xq[j] = a;
     }
     // dR tiles: kg dh + Aqk^T dO (+ dv)
     if (has_dr) {
@@ -215,17 +222,17 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
 
     // dh <- lambda * dh + scale * X - w^T dR   (accumulated negated: -a + w^T dR)
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
+    for (int j = 0; j < NCW; ++j) {
       f32x4 a;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int kr = 16 * wv + 4 * (l >> 4) + r;
-        a[r] = -(st[ct][r] * sm.lam[kr] + scale * xq[ct][r]);
+        const int kr = 16 * rt + 4 * (l >> 4) + r;
+        a[r] = -(st[j][r] * sm.lam[kr] + scale * xq[j][r]);
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag_tr<16>(sm.w, 32 * ks, 16 * wv), frag(&sm.drT[16 * ct][32 * ks], S::LDT), a);
-      st[ct] = -a;
+        a = mfma(frag_tr<16>(sm.w, 32 * ks, 16 * rt), frag(&sm.drT[16 * (ct0 + j)][32 * ks], S::LDT), a);
+      st[j] = -a;
     }
 
     // global stores of dh[c] and dR_c from the transposed LDS copies
@@ -262,14 +269,20 @@ __global__ __launch_bounds__(512) void state_bwd_kernel(
   if (dh0) {
     float* dst = dh0 + (size_t)bh * KD * VD;
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct)
+    for (int j = 0; j < NCW; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int kr = 16 * wv + 4 * (l >> 4) + r;
-        dst[kr * VD + v_base + 16 * ct + (l & 15)] = st[ct][r];
+        const int kr = 16 * rt + 4 * (l >> 4) + r;
+        dst[kr * VD + v_base + 16 * (ct0 + j) + (l & 15)] = st[j][r];
       }
   }
 }
+
+// Waves per state work-group: 16 for 32-wide value tiles (4 % faster for GDN2's
+// 512 work-groups), 8 otherwise (16 measured within 2 % at 64-wide tiles; 16-wide
+// tiles have one column tile per row tile).
+template <int BV>
+constexpr int state_waves() { return BV == 32 ? 16 : 8; }
 
 template <int BV, int GATE, bool AQK>
 static hipError_t launch_state(const void* q, const void* k, const void* w, const float* g,
@@ -277,7 +290,8 @@ static hipError_t launch_state(const void* q, const void* k, const void* w, cons
                                void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
                                hipStream_t stream) {
   const int grid = B * H * (VD / BV);
-  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK>), dim3(grid), dim3(512), 0, stream,
+  constexpr int NW = state_waves<BV>();
+  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW>), dim3(grid), dim3(64 * NW), 0, stream,
                      (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk,
                      (const bf16*)dv, dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale);
   return hipGetLastError();

@@ -50,3 +50,30 @@ def test_prepare_wu_and_fwd_h(op, B, T, H):
     print("rel-L2 vs oracle", errs, flush=True)
     for name, e in errs.items():
         assert e < (5e-4 if name == "Aqk" else 1e-2), (name, errs)
+
+
+@pytest.mark.parametrize("op", ["kda", "gdn"])
+@pytest.mark.parametrize("vb", [16, 32, 64])
+def test_fwd_h_value_blocks(op, vb):
+    """Every value-tile width of the direct forward scan against the oracle."""
+    from rewy_amd import ops
+    from rewy_amd.forward import chunk_forward
+    B, T, H = 1, 256, 2
+    print(f"\n[fwd_h vb] op={op} value_block={vb}", flush=True)
+    xs, _ = make_inputs(op, B, T, H, seed=43)
+    _, _, sv = chunk_forward(op, xs["q"], xs["k"], xs["v"], g=xs.get("g"), beta=xs.get("beta"),
+                             initial_state=xs["initial_state"], output_final_state=True)
+    n = lambda x: None if x is None else x.double().numpy()
+    ref = O.forward(op, n(xs["q"]), n(xs["k"]), n(xs["v"]), g=n(xs.get("g")), beta=n(xs.get("beta")),
+                    h0=n(xs["initial_state"]))
+    dev = torch.device("cuda")
+    cu = lambda x: None if x is None else x.to(dev).contiguous()
+    kin = sv["kg"] if op == "kda" else xs["k"]
+    h, vnew, ht = ops.fwd_h(cu(kin), cu(sv["w"]), cu(sv["u"]), cu(sv["gc"]), GATE[op], h0=cu(xs["initial_state"]),
+                            want_final=True, value_block=vb, method="direct")
+    torch.cuda.synchronize()
+    errs = dict(h=_rel(n(h.cpu()), ref["h"]), v_new=_rel(n(vnew.cpu()), ref["v_new"]),
+                final=_rel(n(ht.cpu()), ref["final"]))
+    print("rel-L2 vs oracle", errs, flush=True)
+    for name, e in errs.items():
+        assert e < 1e-2, (name, errs)

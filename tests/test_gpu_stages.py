@@ -94,3 +94,35 @@ def test_state_and_chunk_kernels(op, shape, gate, bz):
     for name, e_ in errs.items():
         assert np.isfinite(_np(out[name])).all(), name
         assert e_ < (1e-2 if name in ("dq", "dk", "dv", "db", "dw") else 5e-3), (name, errs)
+
+
+@pytest.mark.parametrize("op", ["kda", "gdn", "delta"])
+@pytest.mark.parametrize("vb", [16, 32, 64])
+def test_state_kernel_value_blocks(op, vb):
+    """Every value-tile width of the direct state kernel (the default picks it from B*H;
+    32-wide tiles run 16 waves, the others 8) against the oracle."""
+    from rewy_amd import ops
+    B, T, H = 1, 256, 2
+    print(f"\n[state vb] op={op} value_block={vb}", flush=True)
+    xs, dO, sv = _setup(op, B, T, H, seed=41)
+    dev = torch.device("cuda")
+    cu = lambda x: None if x is None else x.to(dev).contiguous()
+    gc = sv["gc"]
+    if op == "kda":
+        qs, ks, oq, ok_, og = sv["qg"], sv["kg"], _np(sv["qg"]), _np(sv["kg"]), _np(gc)
+    else:
+        qs, ks = xs["q"], xs["k"]
+        gcn = np.zeros((B, T, H)) if gc is None else _np(gc)
+        G = O._to_chunks(gcn[..., None], 64)
+        oq = O._from_chunks(O._to_chunks(_np(xs["q"]), 64) * np.exp2(G))
+        ok_ = O._from_chunks(O._to_chunks(_np(xs["k"]), 64) * np.exp2(G[..., -1:, :] - G))
+        og = np.broadcast_to(gcn[..., None], (B, T, H, 128))
+    dht = torch.randn(B, H, 128, 128, generator=torch.Generator().manual_seed(4)) * 0.1
+    dh, dR, dh0 = ops.state_bwd(cu(qs), cu(ks), cu(sv["w"]), cu(gc), GATE[op], cu(dO), sv["scale"],
+                                aqk=cu(sv["Aqk"]), dht=cu(dht), value_block=vb, method="direct")
+    torch.cuda.synchronize()
+    odv = O.dv_local(_np(sv["Aqk"]), _np(dO))
+    rdh, rdR, rdh0 = O.stage_state_bwd(oq, ok_, _np(sv["w"]), og, _np(dO), odv, dht=_np(dht), scale=sv["scale"])
+    e = dict(dh=_rel(_np(dh), rdh), dR=_rel(_np(dR), rdR), dh0=_rel(_np(dh0), rdh0))
+    print("state", e, flush=True)
+    assert e["dh"] < 1e-2 and e["dR"] < 1e-2 and e["dh0"] < 5e-3, e
