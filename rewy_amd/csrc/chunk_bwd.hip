@@ -649,19 +649,16 @@ __device__ __forceinline__ void chunk_body(
   f32x4 fbrow[4];      // scalar-beta fallback rows: k exp2(g) Eb + k ue, summed over columns later
   f32x4 adb[4];        // vector-b family: db = k exp2(g) Eb + k ue
   if constexpr (INTRA) {
-    // the partial gradients the intra terms are added to
-    const int rsk32 = H * KD;
+    // the intra terms alone; the partial gradients are added at the stores (not held
+    // in registers through phase 5)
 #pragma unroll
-    for (int I = 0; I < 4; ++I)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int off = (16 * I + 4 * lg + r) * rsk32 + kk;
-        aq[I][r] = dq32[kofs + off];
-        ak[I][r] = dk32[kofs + off];
-        aw[I][r] = dg_out[kofs + off];
-        if constexpr (VEC_B) adb[I][r] = db32[kofs + off];
-        else fbrow[I][r] = 0.f;
-      }
+    for (int I = 0; I < 4; ++I) {
+      aq[I] = zero4();
+      ak[I] = zero4();
+      aw[I] = zero4();
+      if constexpr (VEC_B) adb[I] = zero4();
+      else fbrow[I] = zero4();
+    }
   } else {
 #pragma unroll
   for (int I = 0; I < 4; ++I) {
@@ -952,10 +949,10 @@ __device__ __forceinline__ void chunk_body(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int off = (16 * I + 4 * lg + r) * rsk32 + kk;
-        dq32[kofs + off] = aq[I][r];
-        dk32[kofs + off] = ak[I][r];
-        dg_out[kofs + off] = aw[I][r];
-        if constexpr (VEC_B) db32[kofs + off] = adb[I][r];
+        dq32[kofs + off] += aq[I][r];
+        dk32[kofs + off] += ak[I][r];
+        dg_out[kofs + off] += aw[I][r];
+        if constexpr (VEC_B) db32[kofs + off] += adb[I][r];
       }
   } else {
     bf16* dqb = dq_out + kofs;
