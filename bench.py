@@ -219,6 +219,9 @@ def time_kernels(kern, reps):
     return out
 
 
+SEQUENTIAL = ("fdr_state_bwd", "fdr_fwd_h", "affine_state", "affine_recurrences")
+
+
 def measure(cfg, steps, warmup):
     xs, dO, sv, step, kern, inter, forward = setup(cfg, "cuda")
     NTt = cfg["B"] * cfg["H"] * (cfg["T"] // 64)
@@ -231,9 +234,14 @@ def measure(cfg, steps, warmup):
         by, fl = costs[n]
         kernels[n] = dict(ms=round(t, 4), gbs=round(by * NTt / (t * 1e-3) / 1e9, 1),
                           tflops=round(fl * NTt / (t * 1e-3) / 1e12, 2), bytes_per_launch=by * NTt)
+        if n in SEQUENTIAL:
+            # the recurrences walk the chunks in order: time per chunk step
+            kernels[n]["us_per_chunk_step"] = round(t * 1e3 / (cfg["T"] // 64), 3)
     flops = sum(costs[n][1] for n in kt) * NTt
+    graph_us, graph_err = graph_time_us(step, max(10, steps))
     return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9, kernels=kernels, NTt=NTt,
-                xs=xs, dO=dO, sv=sv, step=step, inter=inter, fwd_ms=fwd_ms)
+                xs=xs, dO=dO, sv=sv, step=step, inter=inter, fwd_ms=fwd_ms, graph_ms=graph_us * 1e-3,
+                graph_err=graph_err)
 
 
 def measured_traffic(kernel, config):
@@ -432,6 +440,7 @@ def main():
         cpu = cpu_baseline(xs, sv, dO, sv["scale"], NTt)
 
     ms, tflops, kernels, res_fwd_ms = res["ms"], res["tflops"], res["kernels"], res["fwd_ms"]
+    graph_ms, graph_err = res["graph_ms"], res["graph_err"]
     dom = max(kernels, key=lambda n: kernels[n]["ms"])
     achieved = kernels[dom]["gbs"]
     del res, xs, dO, sv
@@ -444,6 +453,7 @@ def main():
                              "ms": round(g["ms"], 4), "tflops": round(g["tflops"], 2),
                              "mfma_peak_frac": round(g["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
                              "forward_hip_ms": round(g["fwd_ms"], 4),
+                             "graph_ms": round(g["graph_ms"], 4),
                              "kernels": g["kernels"]}}
         del g
         torch.cuda.empty_cache()
@@ -472,6 +482,10 @@ def main():
                      "traffic": measured_traffic(dom, args.config),
                      "algorithmic_bytes_per_launch": kernels[dom]["bytes_per_launch"]},
         "forward_hip_ms": round(res_fwd_ms, 4),
+        # one backward captured in a HIP graph and replayed (kernel-only, as the reference's
+        # low-level timing); the replay's gradients are checked against an eager call
+        "graph_ms": round(graph_ms, 4),
+        "graph_vs_eager_rel_l2": graph_err,
         "original_torch_ms": None if t_orig is None else round(t_orig, 3),
         "speedup_vs_original_torch": None if t_orig is None else round(t_orig / ms, 2),
         "parity_vs_original": parity,
