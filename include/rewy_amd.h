@@ -147,6 +147,30 @@ hipError_t fdr_fwd_o(const void* q, const float* gc, int gate_mode, const float*
                      float scale, hipStream_t stream);
 
 /*
+ * KDA's in-kernel gate activation (use_gate_in_kernel=True) and its backward, as the
+ * reference documents them (_compat/kda.py:250-294; dA_log / ddt_bias are the extra
+ * outputs of kda_backward, backends/backward.py:63-73):
+ *   no lower bound:    g = -exp(A_log[h]) * softplus(g_raw + dt_bias[h,k])
+ *   lower_bound, A_log: g = lower_bound * sigmoid(exp(A_log[h]) * (g_raw + dt_bias[h,k]))
+ *   lower_bound only:  g = lower_bound * sigmoid(g_raw + dt_bias[h,k])
+ * g_raw [B,T,H,K] fp32 (raw_is_bf16 = 0) or bf16 (1); A_log fp32 [H] (null only with a
+ * lower bound); dt_bias fp32 [H*K] or null; g fp32 [B,T,H,K].  The backward takes
+ * dg = dL/dg (fp32), writes dg_raw in g_raw's dtype and, where non-null, dA_log (fp32 [H])
+ * and ddt_bias (fp32 [H*K]); `workspace` holds fdr_kda_gate_workspace_bytes(B,T,H,K)
+ * bytes of per-block partial sums.  K must be 128.
+ */
+size_t fdr_kda_gate_workspace_bytes(int B, int T, int H, int K);
+
+hipError_t fdr_kda_gate_fwd(const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
+                            int has_lower_bound, float lower_bound, float* g, int B, int T, int H, int K,
+                            hipStream_t stream);
+
+hipError_t fdr_kda_gate_bwd(const float* dg, const void* g_raw, int raw_is_bf16, const float* A_log,
+                            const float* dt_bias, int has_lower_bound, float lower_bound, void* dg_raw,
+                            float* dA_log, float* ddt_bias, void* workspace, int B, int T, int H, int K,
+                            hipStream_t stream);
+
+/*
  * Affine-step form of the two state recurrences (for small B*H, where the
  * sequential chain and not HBM sets the time).  The same results as
  * fdr_state_bwd / fdr_fwd_h, split into chunk-parallel and sequential parts:

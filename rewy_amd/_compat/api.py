@@ -216,7 +216,9 @@ def make_kda(backend):
             # the fused activation as its own autograd node: g's gradient flows to
             # g_raw, A_log and dt_bias (the reference's dA_log / ddt_bias outputs)
             from ..gates import KDAGate
-            g = KDAGate.apply(g, A_log, dt_bias, lower_bound)
+            # the optimized backend runs the activation's HIP kernels on a GPU, the
+            # original backend the torch expressions
+            g = KDAGate.apply(g, A_log, dt_bias, lower_bound, backend == "optimized" and g.is_cuda)
         scale = K ** -0.5 if scale is None else scale
         return _apply("kda", backend, disable_recompute, scale, output_final_state, q, k, v, g, beta,
                       None, None, initial_state, state_v_first=state_v_first, cu_seqlens=cu_seqlens,

@@ -28,6 +28,8 @@ SIGNATURES = {
     "fdr_affine_prep_fwd": [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "fdr_affine_prep_pair": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
                              _F, _P],
+    "fdr_kda_gate_fwd": [_P, _I, _P, _P, _I, _F, _P, _I, _I, _I, _I, _P],
+    "fdr_kda_gate_bwd": [_P, _P, _I, _P, _P, _I, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "fdr_affine_scan": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
     "fdr_affine_side": [_P, _I, _I, _I, _I, _I, _I, _I, _P],
 }
@@ -70,6 +72,8 @@ def load():
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = ctypes.c_int
+        lib.fdr_kda_gate_workspace_bytes.argtypes = [_I, _I, _I, _I]
+        lib.fdr_kda_gate_workspace_bytes.restype = ctypes.c_size_t
         _lib = lib
     return _lib
 
