@@ -171,6 +171,19 @@ hipError_t fdr_kda_gate_bwd(const float* dg, const void* g_raw, int raw_is_bf16,
                             hipStream_t stream);
 
 /*
+ * q / k L2 normalisation over K = 128 (use_qk_l2norm_in_kernel=True, reference
+ * _compat/kda.py:202-206; FLA l2norm_fwd / l2norm_bwd), `rows` rows of 128 channels,
+ * bf16 (is_bf16 = 1) or fp32:
+ *   fwd: rstd = (sum x^2 + eps)^-1/2 (fp32 per row, may be null), y = x rstd
+ *   bwd: dx = rstd (dy - y (y . dy)) with y = x rstd
+ */
+hipError_t fdr_l2norm_fwd(const void* x, int is_bf16, void* y, float* rstd, long long rows, int K, float eps,
+                          hipStream_t stream);
+
+hipError_t fdr_l2norm_bwd(const void* x, int is_bf16, const float* rstd, const void* dy, void* dx,
+                          long long rows, int K, hipStream_t stream);
+
+/*
  * Affine-step form of the two state recurrences (for small B*H, where the
  * sequential chain and not HBM sets the time).  The same results as
  * fdr_state_bwd / fdr_fwd_h, split into chunk-parallel and sequential parts:

@@ -24,9 +24,10 @@ import torch
 from ..forward import chunk_forward
 
 
-def _l2norm(x, eps=1e-6):
-    xf = x.float()
-    return (xf * torch.rsqrt((xf * xf).sum(-1, keepdim=True) + eps)).to(x.dtype)
+def _l2norm(x, backend):
+    """q / k normalisation: HIP kernels for the optimized backend on a GPU, torch ops otherwise."""
+    from ..norm import l2norm
+    return l2norm(x, native=backend == "optimized" and x.is_cuda)
 
 
 class ChunkFunction(torch.autograd.Function):
@@ -209,7 +210,7 @@ def make_kda(backend):
         assert g.shape == (B, T, HV, K), f"g must have shape [B, T, HV, K]={[B, T, HV, K]}, got {list(g.shape)}"
         assert beta.shape == (B, T, HV), f"beta must have shape [B, T, HV]={[B, T, HV]}, got {list(beta.shape)}"
         if use_qk_l2norm_in_kernel:
-            q, k = _l2norm(q), _l2norm(k)
+            q, k = _l2norm(q, backend), _l2norm(k, backend)
         if use_beta_sigmoid_in_kernel:
             beta = beta.sigmoid() * (2.0 if allow_neg_eigval else 1.0)
         if use_gate_in_kernel:
@@ -244,7 +245,7 @@ def make_gdn(backend):
         assert HV % H == 0, f"num_v_heads (HV={HV}) must be divisible by num_qk_heads (H={H})"
         assert g.shape == (B, T, HV), f"g must have shape [B, T, HV], got {list(g.shape)}"
         if use_qk_l2norm_in_kernel:
-            q, k = _l2norm(q), _l2norm(k)
+            q, k = _l2norm(q, backend), _l2norm(k, backend)
         if use_beta_sigmoid_in_kernel:
             beta = beta.sigmoid() * (2.0 if allow_neg_eigval else 1.0)
         scale = K ** -0.5 if scale is None else scale
@@ -272,7 +273,7 @@ def make_gdn2(backend):
         assert b.shape == q.shape, "b (channel-wise erase gate) must have shape [B, T, H, K]"
         assert w.shape == v.shape, "w (channel-wise write gate) must have shape [B, T, H, V]"
         if use_qk_l2norm_in_kernel:
-            q, k = _l2norm(q), _l2norm(k)
+            q, k = _l2norm(q, backend), _l2norm(k, backend)
         scale = k.shape[-1] ** -0.5 if scale is None else scale
         return _apply("gdn2", backend, disable_recompute, scale, output_final_state, q, k, v, g, None,
                       b, w, initial_state, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
@@ -292,7 +293,7 @@ def make_delta(backend):
         assert q.dtype == k.dtype == v.dtype
         assert len(beta.shape) == 3, "beta must be of shape (batch size, seq len, num of head)."
         if use_qk_l2norm_in_kernel:
-            q, k = _l2norm(q), _l2norm(k)
+            q, k = _l2norm(q, backend), _l2norm(k, backend)
         scale = k.shape[-1] ** -0.5 if scale is None else scale
         return _apply("delta", backend, False, scale, output_final_state, q, k, v, None, beta, None,
                       None, initial_state, cu_seqlens=cu_seqlens, cu_seqlens_cpu=cu_seqlens_cpu)

@@ -30,6 +30,8 @@ SIGNATURES = {
                              _F, _P],
     "fdr_kda_gate_fwd": [_P, _I, _P, _P, _I, _F, _P, _I, _I, _I, _I, _P],
     "fdr_kda_gate_bwd": [_P, _P, _I, _P, _P, _I, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "fdr_l2norm_fwd": [_P, _I, _P, _P, ctypes.c_longlong, _I, _F, _P],
+    "fdr_l2norm_bwd": [_P, _I, _P, _P, _P, ctypes.c_longlong, _I, _P],
     "fdr_affine_scan": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
     "fdr_affine_side": [_P, _I, _I, _I, _I, _I, _I, _I, _P],
 }

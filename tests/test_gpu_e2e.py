@@ -66,6 +66,25 @@ def test_optimized_matches_original_backend(op):
         assert e["passed"], (name, e)
 
 
+@pytest.mark.parametrize("op", ["kda", "gdn", "gdn2", "delta"])
+def test_optimized_matches_original_with_l2norm_in_kernel(op):
+    """use_qk_l2norm_in_kernel: the optimized backend normalises q / k with the HIP
+    kernels, the original backend with torch ops; raw (unnormalised) q / k in."""
+    print(f"\n[e2e-l2norm] op={op}", flush=True)
+    xs, dO = make_inputs(op, 1, 192, 2, seed=35)
+    gen = torch.Generator().manual_seed(36)
+    xs["q"] = (torch.randn(xs["q"].shape, generator=gen) * 3).bfloat16()
+    xs["k"] = (torch.randn(xs["k"].shape, generator=gen) * 3).bfloat16()
+    kw = dict(use_qk_l2norm_in_kernel=True)
+    if op in ("kda", "gdn2"):
+        kw["disable_recompute"] = True
+    a, _ = _run(op, xs, dO, "optimized", **kw)
+    b, _ = _run(op, xs, dO, "original", **kw)
+    for name in a:
+        e = O.error(b[name].double().cpu().numpy(), a[name].double().cpu().numpy(), O.limit_for(GRAD[name]))
+        assert e["passed"], (name, e)
+
+
 def test_backward_stays_bound_after_disable():
     import rewy_amd as fdr
     xs, dO = make_inputs("kda", 1, 128, 2, seed=3)
