@@ -46,6 +46,28 @@ def test_entry_points_reject_unsupported_shapes_without_touching_the_gpu():
     assert st == HIP_ERROR_INVALID_VALUE
 
 
+def test_new_entry_points_reject_bad_arguments_without_touching_the_gpu():
+    from rewy_amd import _lib
+    lib = _lib.load()
+    # affine-step recurrences: K = 64; null operands; too many problems
+    st = lib.fdr_affine_prep_bwd(*([None] * 4), 0, *([None] * 6), 1, 128, 1, 64, 128, 64, 1.0, None)
+    assert st == HIP_ERROR_INVALID_VALUE
+    st = lib.fdr_affine_prep_fwd(*([None] * 4), 0, None, None, 1, 128, 1, 128, 128, 64, None)
+    assert st == HIP_ERROR_INVALID_VALUE
+    probs = (_lib.ScanProblem * 3)()
+    assert lib.fdr_affine_scan(probs, 3, 1, 128, 1, 128, 128, 64, 16, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fdr_affine_scan(probs, 1, 1, 128, 1, 128, 128, 64, 16, None) == HIP_ERROR_INVALID_VALUE  # null step
+    sides = (_lib.SideProblem * 1)()
+    assert lib.fdr_affine_side(sides, 1, 1, 100, 1, 128, 128, 64, None) == HIP_ERROR_INVALID_VALUE  # T % 64
+    # gate kernels: K = 64, then no A_log without a lower bound
+    st = lib.fdr_kda_gate_fwd(None, 0, None, None, 0, 0.0, None, 1, 64, 1, 64, None)
+    assert st == HIP_ERROR_INVALID_VALUE
+    assert lib.fdr_kda_gate_workspace_bytes(1, 64, 1, 64) == 0
+    # l2norm: no rows
+    assert lib.fdr_l2norm_fwd(None, 1, None, None, 0, 128, 1e-6, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fdr_l2norm_bwd(None, 1, None, None, None, 0, 128, None) == HIP_ERROR_INVALID_VALUE
+
+
 def test_host_wrappers_validate_before_launch():
     import torch
     from rewy_amd import ops
