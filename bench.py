@@ -350,7 +350,9 @@ def graph_time_us(step, reps):
 def paper_grid(reps):
     """One JSON line per (family, policy): this build's backward at each grid case next
     to the reference's published H100 numbers for the same case."""
+    import math
     import torch
+    summary = {}
     for (op, policy), (orig_us, rewy_us) in H100_US.items():
         ours, worst = [], 0.0
         for i, (B, T, H) in enumerate(PAPER_GRID):
@@ -369,6 +371,10 @@ def paper_grid(reps):
             "speedup_vs_h100_rewy": [round(r / o, 2) for r, o in zip(rewy_us, ours)],
             "graph_vs_eager_rel_l2_max": worst,
             "timing": f"HIP graph of one backward, {reps} replays between HIP events"}), flush=True)
+        summary[f"{op}/{policy}"] = round(math.exp(sum(math.log(r / o) for r, o in zip(rewy_us, ours)) / 6), 3)
+    # six-case geometric mean of (H100 ReWY time / this build's time), as the reference
+    # summarises its own grid (docs/results.md:31-34)
+    print(json.dumps({"paper_grid_geomean_speedup_vs_h100_rewy": summary}), flush=True)
 
 
 def main():
