@@ -4,7 +4,7 @@ TEST INFRASTRUCTURE ONLY.  Nothing in the product (``rewy_amd``) imports this
 module; only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU
 baseline leg may use it, and only as the checker.
 
-Conventions (FLA's, which the reference keeps -- SURVEY 8 layout notes):
+Conventions (FLA's, which the reference keeps):
 
 * tensors are T-major ``[B, T, H, D]``; per-chunk states are ``[B, NT, H, K, V]``;
 * ``g`` handed to the public operators is the per-token *natural-log* decay;
