@@ -238,7 +238,11 @@ def measure(cfg, steps, warmup):
             # the recurrences walk the chunks in order: time per chunk step
             kernels[n]["us_per_chunk_step"] = round(t * 1e3 / (cfg["T"] // 64), 3)
     flops = sum(costs[n][1] for n in kt) * NTt
-    graph_us, graph_err = graph_time_us(step, max(10, steps))
+    try:
+        graph_us, graph_err = graph_time_us(step, max(10, steps))
+    except RuntimeError as e:        # the headline figure does not depend on graph capture
+        print(f"[bench] HIP-graph timing skipped: {e}", file=sys.stderr, flush=True)
+        graph_us, graph_err = float("nan"), None
     return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9, kernels=kernels, NTt=NTt,
                 xs=xs, dO=dO, sv=sv, step=step, inter=inter, fwd_ms=fwd_ms, graph_ms=graph_us * 1e-3,
                 graph_err=graph_err)
@@ -459,7 +463,7 @@ def main():
                              "ms": round(g["ms"], 4), "tflops": round(g["tflops"], 2),
                              "mfma_peak_frac": round(g["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
                              "forward_hip_ms": round(g["fwd_ms"], 4),
-                             "graph_ms": round(g["graph_ms"], 4),
+                             "graph_ms": None if g["graph_ms"] != g["graph_ms"] else round(g["graph_ms"], 4),
                              "kernels": g["kernels"]}}
         del g
         torch.cuda.empty_cache()
@@ -490,7 +494,7 @@ def main():
         "forward_hip_ms": round(res_fwd_ms, 4),
         # one backward captured in a HIP graph and replayed (kernel-only, as the reference's
         # low-level timing); the replay's gradients are checked against an eager call
-        "graph_ms": round(graph_ms, 4),
+        "graph_ms": None if graph_ms != graph_ms else round(graph_ms, 4),
         "graph_vs_eager_rel_l2": graph_err,
         "original_torch_ms": None if t_orig is None else round(t_orig, 3),
         "speedup_vs_original_torch": None if t_orig is None else round(t_orig / ms, 2),
