@@ -171,6 +171,24 @@ hipError_t fdr_kda_gate_bwd(const float* dg, const void* g_raw, int raw_is_bf16,
                             hipStream_t stream);
 
 /*
+ * fdr_chunk_bwd for KDA (gate_mode 2, scalar beta) with the in-kernel gate's backward
+ * folded into the dg stores: instead of dg it writes dg_raw = dL/dg_raw (g_raw's dtype)
+ * and, where non-null, dA_log / ddt_bias, with the activation and arguments of
+ * fdr_kda_gate_bwd.  `workspace` holds fdr_chunk_bwd_gate_workspace_bytes(B, T, H) bytes
+ * of per-chunk partial sums.  Replaces the chunk stage plus the gate backward of the
+ * reference's kda_backward with use_gate_in_kernel (backends/backward.py:63-73).
+ */
+size_t fdr_chunk_bwd_gate_workspace_bytes(int B, int T, int H);
+
+hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, const void* v, const void* v_new, const void* dO,
+                                   const void* dR, const float* g, const float* beta, const float* Akk,
+                                   const void* h, const void* dh, void* dq, void* dk, void* dv, float* dbeta,
+                                   const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
+                                   int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
+                                   float* ddt_bias, void* workspace, int B, int T, int H, int K, int V, int chunk,
+                                   float scale, hipStream_t stream);
+
+/*
  * q / k L2 normalisation over K = 128 (use_qk_l2norm_in_kernel=True, reference
  * _compat/kda.py:202-206; FLA l2norm_fwd / l2norm_bwd), `rows` rows of 128 channels,
  * bf16 (is_bf16 = 1) or fp32:

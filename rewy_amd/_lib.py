@@ -32,6 +32,8 @@ SIGNATURES = {
     "fdr_kda_gate_bwd": [_P, _P, _I, _P, _P, _I, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "fdr_l2norm_fwd": [_P, _I, _P, _P, ctypes.c_longlong, _I, _F, _P],
     "fdr_l2norm_bwd": [_P, _I, _P, _P, _P, ctypes.c_longlong, _I, _P],
+    "fdr_chunk_bwd_gate_fold": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _F,
+                                _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_affine_scan": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
     "fdr_affine_side": [_P, _I, _I, _I, _I, _I, _I, _I, _P],
 }
@@ -76,6 +78,8 @@ def load():
             fn.restype = ctypes.c_int
         lib.fdr_kda_gate_workspace_bytes.argtypes = [_I, _I, _I, _I]
         lib.fdr_kda_gate_workspace_bytes.restype = ctypes.c_size_t
+        lib.fdr_chunk_bwd_gate_workspace_bytes.argtypes = [_I, _I, _I]
+        lib.fdr_chunk_bwd_gate_workspace_bytes.restype = ctypes.c_size_t
         _lib = lib
     return _lib
 

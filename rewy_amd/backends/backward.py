@@ -51,8 +51,8 @@ def _f32(x):
     return None if x is None else x.to(torch.float32).contiguous()
 
 
-def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, saved, **kw):
-    """Shared vector-gate (KDA / GDN2) backward."""
+def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, saved, gate_fold=None, **kw):
+    """Shared vector-gate (KDA / GDN2) backward.  ``gate_fold``: see ops.chunk_bwd."""
     _check_common(op, kw)
     q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
     g = _f32(g)
@@ -71,7 +71,7 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     out = ops.chunk_bwd(q, k, v, _bf(saved["v_new"]), do, dR, g, ops.GATE_VECTOR, Akk,
                         _bf(saved["h"]), dh, scale, beta=_f32(gates.get("beta")),
                         b=None if gates.get("b") is None else _bf(gates["b"]),
-                        w=None if gates.get("w") is None else _bf(gates["w"]))
+                        w=None if gates.get("w") is None else _bf(gates["w"]), gate_fold=gate_fold)
     return out, dh0
 
 
@@ -102,17 +102,17 @@ def kda_backward(q, k, v, beta, Aqk, Akk, scale, initial_state, do, dht, g, g_or
     """KDA backward -> (dq, dk, dv, db, dg, dh0, dA_log, ddt_bias)."""
     from ..runtime import record
     saved = dict(w=w, u=u, qg=qg, kg=kg, v_new=v_new, h=h)
+    # the in-kernel gate's backward rides in the chunk kernel's dg stores (one pass fewer
+    # over dg); g is the activated gate's cumsum, g_org the raw gate input (FLA convention)
+    fold = (dict(g_raw=g_org, A_log=A_log, dt_bias=dt_bias, lower_bound=lower_bound)
+            if use_gate_in_kernel else None)
     out, dh0 = _vector("kda", q, k, v, dict(beta=beta), Aqk, Akk, scale, initial_state, do, dht, g,
-                       saved, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
+                       saved, gate_fold=fold, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
                        chunk_indices=chunk_indices, chunk_size=chunk_size, safe_gate=safe_gate,
                        use_gate_in_kernel=use_gate_in_kernel, cp_context=cp_context,
                        use_graph=use_graph, chunk_offsets=chunk_offsets)
     record("kda", "optimized_backward")
-    dg, dA_log, ddt_bias = out["dg"], None, None
-    if use_gate_in_kernel:
-        # g is the activated gate's cumsum; g_org the raw gate input (FLA convention)
-        from ..gates import kda_gate_bwd
-        dg, dA_log, ddt_bias = kda_gate_bwd(dg, g_org, A_log, dt_bias, lower_bound)
+    dg, dA_log, ddt_bias = out["dg"], out.get("dA_log"), out.get("ddt_bias")
     return out["dq"], out["dk"], out["dv"], out["dbeta"], dg, dh0, dA_log, ddt_bias
 
 

@@ -215,10 +215,25 @@ __device__ __forceinline__ void dma_x(bf16* xbuf, const bf16* __restrict__ dR, c
   }
 }
 
+// KDA's in-kernel gate backward folded into the dg stores (use_gate_in_kernel): the
+// activation's gradient is applied to dg where it is formed, and ddt_bias / dA_log
+// partials are written per (batch, chunk) instead of the fp32 dg.
+struct GateFoldArgs {
+  const void* graw;      // raw gate input [B,T,H,K], fp32 or bf16
+  const float* A_log;    // [H] or null (lower_bound form without A_log)
+  const float* dt_bias;  // [H*K] or null
+  float lower_bound;
+  void* dx;              // dL/dg_raw, g_raw's dtype
+  float* part_dt;        // [B*NT][H*K]: sum over a chunk's rows of dx
+  float* part_da;        // [B*NT][H][8]: dA_log terms per chunk, head and column strip
+};
+
 // The body serves two kernels: the full chunk backward (INTRA = false) and the
 // standalone matrix intra (INTRA = true: L and D are given, the partial dq, dk,
 // dg, db are read-modify-written in fp32, no state terms and no cumsum).
-template <int GATE, bool VEC_B, bool INTRA, bool PIPE = false>
+// FOLD >= 0: the gate backward is folded in, bf16 g_raw if FOLD & 1, activation FOLD >> 1:
+// 0: -exp(A) softplus(x), 1: lb sigmoid(exp(A) x), 2: lb sigmoid(x).
+template <int GATE, bool VEC_B, bool INTRA, bool PIPE = false, int FOLD = -1>
 __device__ __forceinline__ void chunk_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
@@ -229,7 +244,7 @@ __device__ __forceinline__ void chunk_body(
     bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale,
     const float* __restrict__ daqk, float* __restrict__ dq32, float* __restrict__ dk32,
     float* __restrict__ db32, int beta_complete, int item, int next_item, char* regA, char* regB,
-    float* small, bf16* xbuf, float* gbuf, PhaseIn& pin) {
+    float* small, bf16* xbuf, float* gbuf, PhaseIn& pin, const GateFoldArgs* gf = nullptr) {
   using LY = PostLayout<GATE, VEC_B, INTRA, PIPE>;
   using post::LDT;
   auto B16 = [&](int off) { return reinterpret_cast<bf16*>(regA + off); };
@@ -967,9 +982,59 @@ __device__ __forceinline__ void chunk_body(
         const int off = (16 * I + 4 * lg + r) * rsk32 + kk;
         dqb[off] = to_bf16(aq[I][r]);
         dkb[off] = to_bf16(ak[I][r]);
-        if constexpr (GATE == CG_VECTOR) dgb[off] = aw[I][r];
+        if constexpr (GATE == CG_VECTOR && FOLD < 0) dgb[off] = aw[I][r];
         if constexpr (VEC_B) dbb[off] = to_bf16(adb[I][r]);
       }
+    }
+    if constexpr (FOLD >= 0) {
+      // dx = dg * d(activation)/dx at each row of this lane's column; the column's
+      // sum over the 64 rows (ddt_bias) and the dA_log terms go to per-chunk partials
+      constexpr int MODE = FOLD >> 1;
+      constexpr bool RB = FOLD & 1;
+      const int hh = pos.h, col = hh * KD + kk;
+      const size_t base = kofs + (size_t)(4 * lg) * rsk32 + kk;
+      float xr[4][4];
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const size_t o = base + (size_t)(16 * I + r) * rsk32;
+          if constexpr (RB) xr[I][r] = to_f32(reinterpret_cast<const bf16*>(gf->graw)[o]);
+          else xr[I][r] = reinterpret_cast<const float*>(gf->graw)[o];
+        }
+      const float bias = gf->dt_bias ? gf->dt_bias[col] : 0.f;
+      const float a = MODE == 2 ? 1.f : exp_f(gf->A_log[hh]);
+      const float lb = gf->lower_bound;
+      float sdt = 0.f, sda = 0.f;
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const size_t o = base + (size_t)(16 * I + r) * rsk32;
+          const float x = xr[I][r] + bias, d = aw[I][r];
+          float dx, tda;
+          if constexpr (MODE == 0) {
+            const float y = exp_f(x);
+            dx = -d * a * sigmoid_y(y);
+            tda = d * (-a * softplus_y(x, y));
+          } else {
+            const float sg = sigmoid_y(exp_f(a * x));
+            const float ds = d * lb * sg * (1.f - sg);
+            dx = ds * a;
+            tda = MODE == 1 ? ds * a * x : 0.f;
+          }
+          if constexpr (RB) reinterpret_cast<bf16*>(gf->dx)[o] = to_bf16(dx);
+          else reinterpret_cast<float*>(gf->dx)[o] = dx;
+          sdt += dx;
+          sda += tda;
+        }
+      }
+      sdt = sum_lane_groups(sdt, l);             // the column's 64 rows
+      sda = sum_row16(sum_lane_groups(sda, l));  // and the strip's 16 columns
+      const int NT = T / C;
+      const size_t blk = (size_t)pos.b * NT + pos.c;
+      if (lg == 0) gf->part_dt[blk * (H * KD) + col] = sdt;
+      if (l == 0) gf->part_da[(blk * H + hh) * 8 + wv] = sda;
     }
   }
   lds_sync();   // sDbB, sDg complete; every wave is past phase 5 (region A free)
@@ -1031,6 +1096,25 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
                                  dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale, nullptr,
                                  nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
                                  reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin);
+}
+
+// KDA with the gate backward folded into the dg stores (no dg output)
+template <int FOLD>
+__global__ __launch_bounds__(512) void chunk_bwd_fold_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
+    const float* __restrict__ g, const float* __restrict__ beta, const float* __restrict__ akk,
+    const bf16* __restrict__ hst, const bf16* __restrict__ dhst, bf16* __restrict__ dq_out,
+    bf16* __restrict__ dk_out, bf16* __restrict__ dv_out, float* __restrict__ dbeta_out, int T, int H,
+    float scale, GateFoldArgs gf) {
+  using LY = PostLayout<CG_VECTOR, false>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  PhaseIn pin;
+  chunk_body<CG_VECTOR, false, false, false, FOLD>(
+      q, k, v, vnew, dO, dR, g, beta, nullptr, nullptr, akk, hst, dhst, dq_out, dk_out, dv_out, nullptr, dbeta_out,
+      nullptr, nullptr, T, H, scale, nullptr, nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem,
+      smem + LY::REGION_A, reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
+      &gf);
 }
 
 // Persistent form: one work-group per CU walks the items blockIdx.x, + gridDim.x, ...
@@ -1191,6 +1275,53 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
     default: return hipErrorInvalidValue;
   }
 #undef FDR_POST
+}
+
+namespace rewy {
+// gates.hip: ddt_bias / dA_log as column sums of [nrows][HK] / [nrows][HK/K*G] partials
+hipError_t kda_gate_partials_sum(const float* part_dt, const float* part_da, int nrows, int HK, int G, float* ddt,
+                                 float* dA, hipStream_t s);
+}  // namespace rewy
+
+extern "C" size_t fdr_chunk_bwd_gate_workspace_bytes(int B, int T, int H) {
+  if (B <= 0 || T <= 0 || T % C || H <= 0) return 0;
+  const size_t nblk = (size_t)B * (T / C);
+  return nblk * ((size_t)H * KD + 8 * (size_t)H) * sizeof(float);
+}
+
+extern "C" hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, const void* v, const void* v_new,
+                                              const void* dO, const void* dR, const float* g, const float* beta,
+                                              const float* Akk, const void* h, const void* dh, void* dq, void* dk,
+                                              void* dv, float* dbeta, const void* g_raw, int raw_is_bf16,
+                                              const float* A_log, const float* dt_bias, int has_lower_bound,
+                                              float lower_bound, void* dg_raw, float* dA_log, float* ddt_bias,
+                                              void* workspace, int B, int T, int H, int K, int V, int chunk,
+                                              float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  if (!q || !k || !v || !v_new || !dO || !dR || !g || !beta || !Akk || !h || !dh || !dq || !dk || !dv || !dbeta)
+    return hipErrorInvalidValue;
+  if (!g_raw || !dg_raw || !workspace) return hipErrorInvalidValue;
+  const int mode = !has_lower_bound ? (A_log ? 0 : -1) : (A_log ? 1 : 2);
+  if (mode < 0) return hipErrorInvalidValue;
+  const int nblk = B * (T / C);
+  float* part_dt = reinterpret_cast<float*>(workspace);
+  float* part_da = part_dt + (size_t)nblk * H * KD;
+  const GateFoldArgs gf{g_raw, A_log, dt_bias, lower_bound, dg_raw, part_dt, part_da};
+  using LY = PostLayout<CG_VECTOR, false>;
+  const int fold = 2 * mode + (raw_is_bf16 ? 1 : 0);
+  using KernT = decltype(&chunk_bwd_fold_kernel<0>);
+  static const KernT kerns[6] = {chunk_bwd_fold_kernel<0>, chunk_bwd_fold_kernel<1>, chunk_bwd_fold_kernel<2>,
+                                 chunk_bwd_fold_kernel<3>, chunk_bwd_fold_kernel<4>, chunk_bwd_fold_kernel<5>};
+  const KernT kern = kerns[fold];
+  static bool attr_set[6][kMaxDevices] = {};
+  hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set[fold]);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, stream, (const bf16*)q, (const bf16*)k,
+                     (const bf16*)v, (const bf16*)v_new, (const bf16*)dO, (const bf16*)dR, g, beta, Akk,
+                     (const bf16*)h, (const bf16*)dh, (bf16*)dq, (bf16*)dk, (bf16*)dv, dbeta, T, H, scale, gf);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return kda_gate_partials_sum(part_dt, part_da, nblk, H * KD, 8, ddt_bias, dA_log, stream);
 }
 
 template <bool VEC_B>

@@ -79,6 +79,18 @@ __device__ __forceinline__ int xcd_logical_block() {
   return (b % 8) * (n / 8) + b / 8;
 }
 
+// e^x on the hardware exp2 unit
+__device__ __forceinline__ float exp_f(float x) { return fast_exp2(x * 1.4426950408889634f); }
+// softplus(x) = log(1 + e^x) from y = e^x: torch's threshold (x > 20 returns x), log1p's
+// accuracy for small y from its series (y < 2^-12: relative error < 2^-37), else log2(1 + y)
+__device__ __forceinline__ float softplus_y(float x, float y) {
+  if (x > 20.f) return x;
+  if (y < 2.44140625e-4f) return y * (1.f - 0.5f * y);
+  return __builtin_amdgcn_logf(1.f + y) * 0.6931471805599453f;
+}
+// sigmoid(x) = 1 / (1 + e^-x) from y = e^x (y = inf -> 1, y = 0 -> 0)
+__device__ __forceinline__ float sigmoid_y(float y) { return 1.f / (1.f + 1.f / y); }
+
 // Redefines a register in place (an empty asm that reads and writes it).  A value
 // loaded for the next loop iteration is settled at the end of the current one,
 // after that iteration's stores are issued: the compiler then waits for the load

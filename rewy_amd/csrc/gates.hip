@@ -19,17 +19,6 @@ namespace rewy {
 constexpr int GT_TOK = 128;        // tokens per work-group
 constexpr int GT_COLS = 2048;      // columns per work-group (256 threads x 8)
 
-// e^x on the hardware exp2 unit
-__device__ __forceinline__ float exp_f(float x) { return fast_exp2(x * 1.4426950408889634f); }
-// softplus(x) = log(1 + e^x) from y = e^x: torch's threshold (x > 20 returns x), log1p's
-// accuracy for small y from its series (y < 2^-12: relative error < 2^-37), else log2(1 + y)
-__device__ __forceinline__ float softplus_y(float x, float y) {
-  if (x > 20.f) return x;
-  if (y < 2.44140625e-4f) return y * (1.f - 0.5f * y);
-  return __builtin_amdgcn_logf(1.f + y) * 0.6931471805599453f;
-}
-// sigmoid(x) = 1 / (1 + e^-x) from y = e^x (y = inf -> 1, y = 0 -> 0)
-__device__ __forceinline__ float sigmoid_y(float y) { return 1.f / (1.f + 1.f / y); }
 __device__ __forceinline__ float softplus_f(float x) { return softplus_y(x, exp_f(x)); }
 __device__ __forceinline__ float sigmoid_f(float x) { return sigmoid_y(exp_f(x)); }
 
@@ -144,23 +133,60 @@ __global__ __launch_bounds__(256) void kda_gate_bwd_kernel(const float* __restri
   if (live && (threadIdx.x & 15) == 0) part_da[(size_t)blockIdx.x * (HK / KD) + h] = tot;
 }
 
-// sum the per-block partials: ddt [HK] and dA [H]
+// sum the per-block partials: ddt [HK] over nblk_dt rows, dA [H] over nblk_da rows
+// Column sums of the per-block partials: ddt[c] = sum_r part_dt[r][c] (HK columns) and
+// dA[h] = sum_r sum_{j<G} part_da[r][h G + j] (H G columns).  A work-group takes 16
+// columns and splits the rows over 16 slices (four independent accumulators per
+// lane, so loads stay in flight), then reduces the slices, and for dA each group of
+// G adjacent columns (G divides 16), through LDS.
 __global__ __launch_bounds__(256) void kda_gate_sum_kernel(const float* __restrict__ part_dt,
                                                            const float* __restrict__ part_da, float* __restrict__ ddt,
-                                                           float* __restrict__ dA, int nblk, int HK) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  const int H = HK / KD;
-  if (i < HK) {
-    if (!ddt) return;
-    float s = 0.f;
-    for (int b = 0; b < nblk; ++b) s += part_dt[(size_t)b * HK + i];
-    ddt[i] = s;
-  } else if (i < HK + H) {
-    if (!dA) return;
-    float s = 0.f;
-    for (int b = 0; b < nblk; ++b) s += part_da[(size_t)b * H + (i - HK)];
-    dA[i - HK] = s;
+                                                           float* __restrict__ dA, int nrows, int HK, int G) {
+  __shared__ float red[16][17];
+  __shared__ float tot[16];
+  const int H = HK / KD, dt_blocks = ddt ? HK / 16 : 0;
+  const bool is_dt = (int)blockIdx.x < dt_blocks;
+  const float* src = is_dt ? part_dt : part_da;
+  const int cols = is_dt ? HK : H * G;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int c = 16 * (is_dt ? blockIdx.x : blockIdx.x - dt_blocks) + tx;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (c < cols) {
+    int r = ty;
+    for (; r + 48 < nrows; r += 64) {
+      s0 += src[(size_t)r * cols + c];
+      s1 += src[(size_t)(r + 16) * cols + c];
+      s2 += src[(size_t)(r + 32) * cols + c];
+      s3 += src[(size_t)(r + 48) * cols + c];
+    }
+    for (; r < nrows; r += 16) s0 += src[(size_t)r * cols + c];
   }
+  red[ty][tx] = (s0 + s1) + (s2 + s3);
+  __syncthreads();
+  if (ty != 0) return;
+  float t = 0.f;
+#pragma unroll
+  for (int y = 0; y < 16; ++y) t += red[y][tx];
+  if (is_dt) {
+    if (c < cols) ddt[c] = t;
+    return;
+  }
+  tot[tx] = t;   // read back by lanes of this same wave: LDS operations of a wave stay in order
+  if (tx % G == 0 && c < cols) {
+    float u = 0.f;
+    for (int j = 0; j < G; ++j) u += tot[tx + j];
+    dA[c / G] = u;
+  }
+}
+
+// ddt_bias / dA_log from partials (also used by the chunk kernel's folded gate backward)
+hipError_t kda_gate_partials_sum(const float* part_dt, const float* part_da, int nrows, int HK, int G, float* ddt,
+                                 float* dA, hipStream_t s) {
+  if (!ddt && !dA) return hipSuccess;
+  if (G < 1 || 16 % G) return hipErrorInvalidValue;
+  const int blocks = (ddt ? HK / 16 : 0) + (dA ? (HK / KD * G + 15) / 16 : 0);
+  hipLaunchKernelGGL(kda_gate_sum_kernel, dim3(blocks), dim3(256), 0, s, part_dt, part_da, ddt, dA, nrows, HK, G);
+  return hipGetLastError();
 }
 
 template <bool BF16_IN>
@@ -234,10 +260,5 @@ extern "C" hipError_t fdr_kda_gate_bwd(const float* dg, const void* g_raw, int r
                              : gate_bwd_launch<false>(mode, dg, g_raw, A_log, dt_bias, lower_bound, dg_raw, part_dt,
                                                       part_da, N, HK, stream);
   if (e != hipSuccess) return e;
-  if (dA_log || ddt_bias) {
-    hipLaunchKernelGGL(kda_gate_sum_kernel, dim3((HK + H + 255) / 256), dim3(256), 0, stream, part_dt, part_da,
-                       ddt_bias, dA_log, nblk, HK);
-    return hipGetLastError();
-  }
-  return hipSuccess;
+  return kda_gate_partials_sum(part_dt, part_da, nblk, HK, 1, ddt_bias, dA_log, stream);
 }

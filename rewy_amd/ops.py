@@ -191,8 +191,13 @@ def recurrences(q, k, w, u, g, gate_mode, dO, scale, aqk=None, dv=None, h0=None,
     return h, vnew, dh, dr, dh0
 
 
-def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None, b=None, w=None):
+def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None, b=None, w=None,
+              gate_fold=None):
     """Fused residual-WY + matrix-intra + epilogue stage.
+
+    ``gate_fold`` (KDA only) = dict(g_raw, A_log, dt_bias, lower_bound): the in-kernel gate's
+    backward is applied where dg is formed; ``dg`` is then dL/dg_raw (g_raw's dtype) and the
+    result also holds ``dA_log`` / ``ddt_bias`` (fp32, or None).
 
     Returns dict(dq, dk, dv [bf16], dg [fp32, gate shape] | None, dbeta [fp32] | None,
     db, dw [bf16] | None)."""
@@ -222,6 +227,8 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
         _need(g, "g", f32, (B, T, H), dev)
     elif gate_mode != GATE_NONE:
         raise ValueError("gate_mode must be 0, 1 or 2")
+    if gate_fold is not None:
+        return _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, gate_fold)
     out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=bf),
                dk=torch.empty(B, T, H, K, device=dev, dtype=bf),
                dv=torch.empty(B, T, H, V, device=dev, dtype=bf),
@@ -236,6 +243,42 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
                                    P(out["db"]), P(out["dw"]), B, T, H, K, V, CHUNK, float(scale),
                                    _lib.stream_handle(dev))
     _lib.check(st, "fdr_chunk_bwd")
+    return out
+
+
+def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, fold):
+    """chunk_bwd (KDA) with the gate backward folded into the dg stores."""
+    B, T, H, K = q.shape
+    V = V_SUPPORTED
+    dev = q.device
+    bf, f32 = torch.bfloat16, torch.float32
+    if gate_mode != GATE_VECTOR or b is not None:
+        raise ValueError("the folded gate backward is KDA's (vector gate, scalar beta)")
+    g_raw, A_log, dt_bias, lb = fold["g_raw"], fold.get("A_log"), fold.get("dt_bias"), fold.get("lower_bound")
+    raw = g_raw if g_raw.dtype in (bf, f32) else g_raw.float()
+    raw = raw.contiguous()
+    _need(raw, "g_raw", raw.dtype, (B, T, H, K), dev)
+    if lb is None and A_log is None:
+        raise ValueError("A_log is required when lower_bound is not set")
+    a = None if A_log is None else _need(A_log.float().contiguous(), "A_log", f32, (H,), dev)
+    dt = None if dt_bias is None else _need(dt_bias.float().contiguous(), "dt_bias", f32, (H * K,), dev)
+    out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=bf),
+               dk=torch.empty(B, T, H, K, device=dev, dtype=bf),
+               dv=torch.empty(B, T, H, V, device=dev, dtype=bf),
+               dg=torch.empty(B, T, H, K, device=dev, dtype=raw.dtype),
+               dbeta=torch.empty(B, T, H, device=dev, dtype=f32), db=None, dw=None,
+               dA_log=torch.empty(H, device=dev, dtype=f32) if A_log is not None else None,
+               ddt_bias=torch.empty(H * K, device=dev, dtype=f32) if dt_bias is not None else None)
+    lib = _lib.load()
+    ws = torch.empty(max(1, lib.fdr_chunk_bwd_gate_workspace_bytes(B, T, H) // 4), device=dev, dtype=f32)
+    P = _lib.ptr
+    st = lib.fdr_chunk_bwd_gate_fold(P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), P(beta), P(Akk), P(h), P(dh),
+                                     P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), P(raw),
+                                     int(raw.dtype == bf), P(a), P(dt), int(lb is not None),
+                                     0.0 if lb is None else float(lb), P(out["dg"]), P(out["dA_log"]),
+                                     P(out["ddt_bias"]), P(ws), B, T, H, K, V, CHUNK, float(scale),
+                                     _lib.stream_handle(dev))
+    _lib.check(st, "fdr_chunk_bwd_gate_fold")
     return out
 
 
