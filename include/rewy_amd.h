@@ -46,6 +46,21 @@ hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const floa
                          hipStream_t stream);
 
 /*
+ * fdr_state_bwd over a variable-length batch: N sequences packed along T (B = 1),
+ * sequence n owning chunks [chunk_offsets[n], chunk_offsets[n+1]) -- every sequence
+ * starts on a chunk boundary and holds at least one chunk (pad with zero keys,
+ * values and gates, which leave the state untouched).  chunk_offsets: int32 [N+1],
+ * device memory, chunk_offsets[N] = T / 64.  dht / dh0 are per sequence
+ * [N,H,K,V]; dh is [T/64,H,K,V] in packed chunk order.  Replaces the reference's
+ * state_bwd with cu_seqlens / chunk_offsets (kernels/vector_state_gpu.py:47-67,
+ * FLA's prepare_chunk_offsets).
+ */
+hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, const float* g, int gate_mode,
+                                const void* dO, const float* aqk, const void* dv, const float* dht, void* dh,
+                                void* dr, float* dh0, const int* chunk_offsets, int N, int T, int H, int K,
+                                int V, int chunk, float scale, int value_block, hipStream_t stream);
+
+/*
  * Chunk-parallel backward: residual-WY products (P = A^T dR, D, E-bar),
  * dAqk, matrix intra, gate/beta epilogue and the in-chunk reverse cumsum of dg,
  * one work-group per (chunk, head).
@@ -97,6 +112,15 @@ hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const flo
 hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g, int gate_mode,
                      const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int K,
                      int V, int chunk, int value_block, hipStream_t stream);
+
+/*
+ * fdr_fwd_h over a variable-length batch, with the packing and chunk_offsets of
+ * fdr_state_bwd_varlen; h0 / ht per sequence [N,H,K,V].  Replaces FLA's
+ * chunk_gated_delta_rule_fwd_h with cu_seqlens (the recompute policy's call).
+ */
+hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const float* g, int gate_mode,
+                            const float* h0, void* h, void* v_new, float* ht, const int* chunk_offsets, int N,
+                            int T, int H, int K, int V, int chunk, int value_block, hipStream_t stream);
 
 /*
  * Standalone matrix intra (the intra-chunk VJP of a vector-gated chunk), in place.

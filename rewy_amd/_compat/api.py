@@ -33,12 +33,18 @@ def _l2norm(x, backend):
 class ChunkFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w,
-                initial_state):
+                initial_state, cu_seqlens=None):
+        # cu_seqlens (optimized backend on a GPU only): sequences packed on 64-token
+        # chunk boundaries, B = 1; the state scans restart at each sequence
+        ctx.cu_seqlens = cu_seqlens
         if backend == "optimized" and q.is_cuda:
             from ..hip_forward import chunk_forward_hip
             o, final, sv = chunk_forward_hip(op, q, k, v, g=g, beta=beta, b=b, w=w,
                                              initial_state=initial_state, scale=scale,
-                                             output_final_state=output_final_state)
+                                             output_final_state=output_final_state,
+                                             chunk_offsets=None if cu_seqlens is None else cu_seqlens // 64)
+        elif cu_seqlens is not None:
+            raise NotImplementedError("chunk-aligned packing is the optimized GPU path's layout")
         else:
             o, final, sv = chunk_forward(op, q, k, v, g=g, beta=beta, b=b, w=w,
                                          initial_state=initial_state, scale=scale,
@@ -57,22 +63,26 @@ class ChunkFunction(torch.autograd.Function):
         op, scale = ctx.op, ctx.scale
         if ctx.backend == "optimized":
             from ..backends import backward as bw
+            cu = ctx.cu_seqlens
             if op == "kda":
                 dq, dk, dv, db, dg, dh0, _, _ = bw.kda_backward(
                     q=q, k=k, v=v, beta=beta, Aqk=Aqk, Akk=Akk, scale=scale, initial_state=h0,
-                    do=do, dht=dht, g=gc, w=w_wy, u=u_wy, qg=qg, kg=kg, v_new=v_new, h=h)
+                    do=do, dht=dht, g=gc, w=w_wy, u=u_wy, qg=qg, kg=kg, v_new=v_new, h=h, cu_seqlens=cu)
                 dw = None
             elif op == "gdn2":
                 dq, dk, dv, db, dw, dg, dh0, _, _ = bw.gdn2_backward(
                     q=q, k=k, v=v, b=b, w_gate=w, Aqk=Aqk, Akk=Akk, scale=scale, initial_state=h0,
-                    do=do, dht=dht, g=gc, w_wy=w_wy, u_wy=u_wy, qg=qg, kg=kg, v_new=v_new, h=h)
+                    do=do, dht=dht, g=gc, w_wy=w_wy, u_wy=u_wy, qg=qg, kg=kg, v_new=v_new, h=h,
+                    cu_seqlens=cu)
             elif op == "gdn":
                 dq, dk, dv, db, dg, dh0, _, _ = bw.gdn_backward(
-                    q=q, k=k, v=v, g=gc, beta=beta, A=Akk, scale=scale, initial_state=h0, do=do, dht=dht)
+                    q=q, k=k, v=v, g=gc, beta=beta, A=Akk, scale=scale, initial_state=h0, do=do, dht=dht,
+                    cu_seqlens=cu)
                 dw = None
             else:
                 dq, dk, dv, db, dh0 = bw.delta_backward(
-                    q=q, k=k, v=v, beta=beta, A=Akk, scale=scale, initial_state=h0, do=do, dht=dht)
+                    q=q, k=k, v=v, beta=beta, A=Akk, scale=scale, initial_state=h0, do=do, dht=dht,
+                    cu_seqlens=cu)
                 dg = dw = None
         else:
             from ..original import original_backward
@@ -88,7 +98,7 @@ class ChunkFunction(torch.autograd.Function):
         gb = cast(db, b if op == "gdn2" else beta)
         return (None, None, None, None, None, cast(dq, q), cast(dk, k), cast(dv, v),
                 None if dg is None else dg.to(ctx.g_dtype),
-                None if op == "gdn2" else gb, gb if op == "gdn2" else None, cast(dw, w), dh0)
+                None if op == "gdn2" else gb, gb if op == "gdn2" else None, cast(dw, w), dh0, None)
 
 
 def _unsupported(name, **flags):
@@ -137,6 +147,15 @@ def _unpack(x, bounds, Tp):
     return torch.cat(rows, 0)
 
 
+def _pack_aligned(x, dst, Tp):
+    """[1, T, ...] packed sequences -> [1, Tp, ...]: token t moves to dst[t], every other
+    position is zero (each sequence padded at its end to whole chunks).  One scatter
+    (its gradient one gather), whatever the number of sequences."""
+    if x is None:
+        return None
+    return x.new_zeros((1, Tp) + tuple(x.shape[2:])).index_copy(1, dst, x)
+
+
 def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0,
            state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None):
     """Layout adapters around the chunk Function (all autograd-transparent torch ops):
@@ -144,10 +163,13 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
     * grouped value heads (HV = v.shape[2] > H): q and k are repeated over each
       group of HV / H value heads (FLA's head map i_h = i_hv // (HV / H));
     * ``state_v_first``: initial / final states are [N, HV, V, K] at the boundary;
-    * ``cu_seqlens`` (B = 1, packed): every sequence is zero-padded to the longest
-      one rounded up to a chunk and run as one batch row.  Zero keys, values and
-      log-gates leave the state untouched, so outputs, final states and gradients
-      of the real tokens are exact; padded positions are dropped."""
+    * ``cu_seqlens`` (B = 1, packed): on the optimized backend on a GPU every
+      sequence is zero-padded to whole 64-token chunks and the sequences stay packed
+      (the state scans restart at each sequence's first chunk: work scales with the
+      sum of the lengths); otherwise each is padded to the longest one and run as
+      one batch row.  Zero keys, values and log-gates leave the state untouched, so
+      outputs, final states and gradients of the real tokens are exact; padded
+      positions are dropped."""
     H, HV = q.shape[2], v.shape[2]
     if HV != H:
         if HV % H:
@@ -168,10 +190,25 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
         if h0 is not None and h0.shape[0] != len(bounds):
             raise ValueError(f"The number of initial states is expected to be equal to the number of input "
                              f"sequences, i.e., {len(bounds)} rather than {h0.shape[0]}.")
-        Tp = max(64, -(-max(e - s for s, e in bounds) // 64) * 64)
-        xs = [_unpack(x, bounds, Tp) for x in (q, k, v, g, beta, b, w)]
-        o, final = _run(op, backend, full_saving, scale, output_final_state, *xs, h0)
-        o = torch.cat([o[i:i + 1, :e - s] for i, (s, e) in enumerate(bounds)], 1)
+        aligned = all(s % 64 == 0 and e > s for s, e in bounds)
+        if backend == "optimized" and q.is_cuda and aligned:
+            # already on chunk boundaries: the kernels take the batch as it is
+            o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta,
+                                           b, w, h0, torch.tensor(cu, dtype=torch.int64))
+        elif backend == "optimized" and q.is_cuda:
+            lens = [max(64, -(-(e - s) // 64) * 64) for s, e in bounds]
+            cu_al = torch.tensor([0] + lens, dtype=torch.int64).cumsum(0)
+            seq = torch.tensor(cu, dtype=torch.int64)
+            n_of = torch.repeat_interleave(torch.arange(len(bounds)), seq[1:] - seq[:-1])
+            dst = (torch.arange(cu[-1]) - seq[n_of] + cu_al[n_of]).to(q.device)
+            xs = [_pack_aligned(x, dst, int(cu_al[-1])) for x in (q, k, v, g, beta, b, w)]
+            o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, *xs, h0, cu_al)
+            o = o.index_select(1, dst)
+        else:
+            Tp = max(64, -(-max(e - s for s, e in bounds) // 64) * 64)
+            xs = [_unpack(x, bounds, Tp) for x in (q, k, v, g, beta, b, w)]
+            o, final = _run(op, backend, full_saving, scale, output_final_state, *xs, h0)
+            o = torch.cat([o[i:i + 1, :e - s] for i, (s, e) in enumerate(bounds)], 1)
     if state_v_first and final is not None:
         final = final.transpose(-1, -2)
     return o, final

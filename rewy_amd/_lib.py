@@ -21,6 +21,9 @@ SIGNATURES = {
                       _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_prepare_wu": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_fwd_h": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
+    "fdr_state_bwd_varlen": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F,
+                             _I, _P],
+    "fdr_fwd_h_varlen": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
     "fdr_matrix_intra": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "fdr_fwd_prepare": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P],
     "fdr_fwd_o": [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],

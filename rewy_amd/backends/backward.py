@@ -24,7 +24,32 @@ import torch
 
 from .. import ops
 
-_UNSUPPORTED = ("cu_seqlens", "chunk_indices", "cp_context", "chunk_offsets")
+_UNSUPPORTED = ("cp_context",)
+
+
+def _varlen(q, kw):
+    """Chunk offsets of a packed variable-length batch (``cu_seqlens``, B = 1), or None.
+
+    The kernels take sequences that start on 64-token chunk boundaries (each padded
+    with zero keys, values and gates to a whole chunk, as the public operators do):
+    the state recurrences then restart at every sequence's first chunk and every other
+    kernel is chunk-local.  ``chunk_indices`` / ``chunk_offsets`` (FLA's, derived from
+    cu_seqlens) are implied by cu_seqlens here."""
+    cu = kw.get("cu_seqlens")
+    if cu is None:
+        if kw.get("chunk_indices") is not None or kw.get("chunk_offsets") is not None:
+            raise NotImplementedError("chunk_indices / chunk_offsets without cu_seqlens")
+        return None
+    B, T = q.shape[:2]
+    host = torch.as_tensor(cu).detach().to("cpu", torch.int64)
+    if B != 1:
+        raise ValueError(f"The batch size is expected to be 1 rather than {B} when using `cu_seqlens`.")
+    if host.ndim != 1 or host.numel() < 2 or int(host[0]) != 0 or int(host[-1]) != T:
+        raise ValueError("cu_seqlens must rise from 0 to T")
+    if bool((host % ops.CHUNK != 0).any()) or bool((host[1:] <= host[:-1]).any()):
+        raise NotImplementedError("HIP backward: every sequence of cu_seqlens must start on a 64-token chunk "
+                                  "boundary and be non-empty (pad each sequence to whole chunks)")
+    return host // ops.CHUNK
 
 
 def _check_common(kind, kw):
@@ -54,10 +79,11 @@ def _f32(x):
 def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, saved, gate_fold=None, **kw):
     """Shared vector-gate (KDA / GDN2) backward.  ``gate_fold``: see ops.chunk_bwd."""
     _check_common(op, kw)
+    co = _varlen(q, kw)
     q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
     g = _f32(g)
     Aqk, Akk = _f32(Aqk), _f32(Akk)
-    if saved.get("h") is None and ops.affine_pays(q):
+    if saved.get("h") is None and co is None and ops.affine_pays(q):
         # recompute policy, few heads: both recurrences side by side in affine-step form
         pre = _prepare_vector(k, v, g, Akk, gates, q)
         h, v_new, dh, dR, dh0 = ops.recurrences(pre["qg"], pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR,
@@ -66,8 +92,8 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
         saved = dict(v_new=v_new, h=h)
     else:
         if saved.get("h") is None:
-            saved = _recompute_vector(q, k, v, g, Akk, initial_state, gates)
-        dh, dR, dh0 = _state_vector(saved, g, do, scale, Aqk, dht, initial_state)
+            saved = _recompute_vector(q, k, v, g, Akk, initial_state, gates, co)
+        dh, dR, dh0 = _state_vector(saved, g, do, scale, Aqk, dht, initial_state, co)
     out = ops.chunk_bwd(q, k, v, _bf(saved["v_new"]), do, dR, g, ops.GATE_VECTOR, Akk,
                         _bf(saved["h"]), dh, scale, beta=_f32(gates.get("beta")),
                         b=None if gates.get("b") is None else _bf(gates["b"]),
@@ -75,9 +101,10 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     return out, dh0
 
 
-def _state_vector(saved, g, do, scale, Aqk, dht, initial_state):
+def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, co=None):
     return ops.state_bwd(_bf(saved["qg"]), _bf(saved["kg"]), _bf(saved["w"]), g, ops.GATE_VECTOR, do, scale,
-                         aqk=Aqk, dht=_f32(dht), want_dh0=initial_state is not None)
+                         aqk=Aqk, dht=_f32(dht), want_dh0=initial_state is not None,
+                         method="auto" if co is None else "direct", chunk_offsets=co)
 
 
 def _prepare_vector(k, v, g, Akk, gates, q):
@@ -87,10 +114,11 @@ def _prepare_vector(k, v, g, Akk, gates, q):
                           want_qkg=True)
 
 
-def _recompute_vector(q, k, v, g, Akk, initial_state, gates):
+def _recompute_vector(q, k, v, g, Akk, initial_state, gates, co=None):
     """w, u, qg, kg (fdr_prepare_wu) then h, v_new (fdr_fwd_h): the recompute policy."""
     pre = _prepare_vector(k, v, g, Akk, gates, q)
-    h, v_new, _ = ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state))
+    h, v_new, _ = ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
+                            method="auto" if co is None else "direct", chunk_offsets=co)
     return dict(w=pre["w"], u=pre["u"], qg=pre["qg"], kg=pre["kg"], v_new=v_new, h=h)
 
 
@@ -137,21 +165,23 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, **kw):
     (reference ``_scalar``, backends/backward.py:96-131)."""
     from ..runtime import record
     _check_common(op, kw)
+    co = _varlen(q, kw)
     q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
     g = _f32(g)
     A = _f32(A)
     beta = _f32(beta)
     gate = ops.GATE_SCALAR if op == "gdn" else ops.GATE_NONE
     pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, q=q, want_aqk=True, scale=scale)
-    if ops.affine_pays(q):
+    if co is None and ops.affine_pays(q):
         # few heads: both recurrences side by side in affine-step form
         h, v_new, dh, dR, dh0 = ops.recurrences(q, k, pre["w"], pre["u"], g, gate, do, scale, aqk=pre["Aqk"],
                                                 h0=_f32(initial_state), dht=_f32(dht),
                                                 want_dh0=initial_state is not None)
     else:
-        h, v_new, _ = ops.fwd_h(k, pre["w"], pre["u"], g, gate, h0=_f32(initial_state), method="direct")
+        h, v_new, _ = ops.fwd_h(k, pre["w"], pre["u"], g, gate, h0=_f32(initial_state), method="direct",
+                                chunk_offsets=co)
         dh, dR, dh0 = ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
-                                    want_dh0=initial_state is not None, method="direct")
+                                    want_dh0=initial_state is not None, method="direct", chunk_offsets=co)
     out = ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta)
     record(op, "optimized_backward")
     return out, dh0

@@ -245,7 +245,7 @@ template <int BV, int GATE>
 __global__ __launch_bounds__(512) void fwd_h_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ w, const bf16* __restrict__ u,
     const float* __restrict__ g, const float* __restrict__ h0, bf16* __restrict__ h_out,
-    bf16* __restrict__ vnew_out, float* __restrict__ ht_out, int T, int H) {
+    bf16* __restrict__ vnew_out, float* __restrict__ ht_out, int T, int H, const int* __restrict__ chunk_off) {
   using S = FwdSmem<BV, GATE>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
@@ -255,7 +255,10 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
   const int vt = logical % NVT;
   const int bh = logical / NVT;
   const int b = bh / H, h = bh % H;
-  const int NT = T / C;
+  // chunks [c0, c0 + NT) of the packed token axis: row b of T tokens, or sequence b of
+  // a variable-length batch (chunk_off: cumulative chunk counts, every count >= 1)
+  const int c0 = chunk_off ? chunk_off[b] : b * (T / C);
+  const int NT = chunk_off ? chunk_off[b + 1] - c0 : T / C;
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int v_base = vt * BV;
   const size_t rsk = (size_t)H * KD, rsv = (size_t)H * VD;
@@ -287,7 +290,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
   u32x4 ru[NU];
   float rg_last = 0.f, rg_tok[2] = {0.f, 0.f};   // scalar gate: last row, the 2 rows this thread stages
   auto load_chunk = [&](int c) {
-    const size_t tok0 = (size_t)b * T + (size_t)c * C;
+    const size_t tok0 = (size_t)(c0 + c) * C;
     const bf16* wb = w + tok0 * rsk + (size_t)h * KD;
     // gate first: its consumer (lambda) is the first thing staged.  Every lane
     // issues the same loads (clamped indices): no branch makes the vector-memory
@@ -361,7 +364,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     lds_barrier();
     stage_chunk();
     load_chunk(c + 1 < NT ? c + 1 : c);    // (the last chunk re-fetches itself: no branch)
-    const size_t tok0 = (size_t)b * T + (size_t)c * C;
+    const size_t tok0 = (size_t)(c0 + c) * C;
     // h_c -> LDS (transposed, bf16); the same rounded values feed w h, as stored
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
@@ -405,7 +408,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     }
     // stores of h_c and v_new_c from the transposed LDS copies (lanes run over rows)
     {
-      const size_t hb = (((size_t)b * NT + c) * H + h) * KD * VD;
+      const size_t hb = ((size_t)(c0 + c) * H + h) * KD * VD;
       // Every lane issues the same number of stores (pieces beyond the tile are
       // written twice, with the same data): static vector-memory wait counts.
       constexpr int NP = KD * BV / 8, NR = C * BV / 8;
@@ -453,9 +456,10 @@ static hipError_t launch_prepare(const void* q, const void* k, const void* v, co
 
 template <int BV, int GATE>
 static hipError_t launch_fwd_h(const void* k, const void* w, const void* u, const float* g, const float* h0,
-                               void* h, void* vnew, float* ht, int B, int T, int H, hipStream_t s) {
+                               void* h, void* vnew, float* ht, int B, int T, int H, hipStream_t s,
+                               const int* co) {
   hipLaunchKernelGGL((fwd_h_kernel<BV, GATE>), dim3(B * H * (VD / BV)), dim3(512), 0, s, (const bf16*)k,
-                     (const bf16*)w, (const bf16*)u, g, h0, (bf16*)h, (bf16*)vnew, ht, T, H);
+                     (const bf16*)w, (const bf16*)u, g, h0, (bf16*)h, (bf16*)vnew, ht, T, H, co);
   return hipGetLastError();
 }
 
@@ -505,14 +509,15 @@ static int fwd_default_bv(int B, int H) {
   return 16;
 }
 
-extern "C" hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g, int gate_mode,
-                                const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int K,
-                                int V, int chunk, int value_block, hipStream_t stream) {
+// B rows of T tokens, or (co) B sequences packed along T
+static hipError_t fwd_h_dispatch(const void* k, const void* w, const void* u, const float* g, int gate_mode,
+                                 const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int K,
+                                 int V, int chunk, int value_block, hipStream_t stream, const int* co) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
   if (!k || !w || !u || !h || !v_new) return hipErrorInvalidValue;
   if (gate_mode != RG_NONE && !g) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : fwd_default_bv(B, H);
-#define F_ARGS k, w, u, g, h0, h, v_new, ht, B, T, H, stream
+#define F_ARGS k, w, u, g, h0, h, v_new, ht, B, T, H, stream, co
 #define F_BV(G)                                                     \
   switch (bv) {                                                     \
     case 16: return launch_fwd_h<16, G>(F_ARGS);                    \
@@ -528,4 +533,20 @@ extern "C" hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, con
   }
 #undef F_BV
 #undef F_ARGS
+}
+
+extern "C" hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g, int gate_mode,
+                                const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int K,
+                                int V, int chunk, int value_block, hipStream_t stream) {
+  return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, B, T, H, K, V, chunk, value_block, stream,
+                        nullptr);
+}
+
+extern "C" hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const float* g, int gate_mode,
+                                       const float* h0, void* h, void* v_new, float* ht, const int* chunk_offsets,
+                                       int N, int T, int H, int K, int V, int chunk, int value_block,
+                                       hipStream_t stream) {
+  if (!chunk_offsets) return hipErrorInvalidValue;
+  return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, N, T, H, K, V, chunk, value_block, stream,
+                        chunk_offsets);
 }

@@ -45,7 +45,8 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ w,
     const float* __restrict__ g, const bf16* __restrict__ dO, const float* __restrict__ aqk,
     const bf16* __restrict__ dv, const float* __restrict__ dht, bf16* __restrict__ dh_out,
-    bf16* __restrict__ dr_out, float* __restrict__ dh0, int T, int H, float scale) {
+    bf16* __restrict__ dr_out, float* __restrict__ dh0, int T, int H, float scale,
+    const int* __restrict__ chunk_off) {
   using S = StateSmem<BV, GATE, DV_FROM_AQK>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
@@ -54,7 +55,10 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   const int vt = logical % NVT;
   const int bh = logical / NVT;
   const int b = bh / H, h = bh % H;
-  const int NT = T / C;
+  // chunks [c0, c0 + NT) of the packed token axis: row b of T tokens, or sequence b of
+  // a variable-length batch (chunk_off: cumulative chunk counts, every count >= 1)
+  const int c0 = chunk_off ? chunk_off[b] : b * (T / C);
+  const int NT = chunk_off ? chunk_off[b + 1] - c0 : T / C;
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int v_base = vt * BV;
 
@@ -99,7 +103,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   const size_t row_stride_v = (size_t)H * VD;
 
   auto load_chunk = [&](int c) {
-    const size_t tok0 = (size_t)b * T + (size_t)c * C;
+    const size_t tok0 = (size_t)(c0 + c) * C;
     // gate first: its consumer (lambda) is the first thing staged
     if constexpr (GATE == GATE_VECTOR) {
       if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
@@ -202,7 +206,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
             a = mfma(frag_tr<8>(sm.al, 32 * ks, 16 * drow), bo, a);
           }
         } else {
-          const size_t tok0 = (size_t)b * T + (size_t)c * C;
+          const size_t tok0 = (size_t)(c0 + c) * C;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int t = 16 * drow + 4 * (l >> 4) + r;
@@ -237,7 +241,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
 
     // global stores of dh[c] and dR_c from the transposed LDS copies
     {
-      const size_t dh_base = (((size_t)b * NT + c) * H + h) * KD * VD;
+      const size_t dh_base = ((size_t)(c0 + c) * H + h) * KD * VD;
       constexpr int NP = KD * BV / 8;
       // fixed trip counts keep the vector-memory wait counts static, so the next
       // chunk's staging waits only for its own loads, not for these stores
@@ -251,7 +255,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
         for (int j = 0; j < 8; ++j) o[j] = sm.dhT[v0 + j][kr];
         *reinterpret_cast<bf16x8*>(dh_out + dh_base + (size_t)kr * VD + v_base + v0) = o;
       }
-      const size_t tok0 = (size_t)b * T + (size_t)c * C;
+      const size_t tok0 = (size_t)(c0 + c) * C;
       constexpr int NR = C * BV / 8;
 #pragma unroll
       for (int i = 0; i < (NR + NTH - 1) / NTH; ++i) {
@@ -288,12 +292,12 @@ template <int BV, int GATE, bool AQK>
 static hipError_t launch_state(const void* q, const void* k, const void* w, const float* g,
                                const void* dO, const float* aqk, const void* dv, const float* dht,
                                void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
-                               hipStream_t stream) {
+                               hipStream_t stream, const int* chunk_off) {
   const int grid = B * H * (VD / BV);
   constexpr int NW = state_waves<BV>();
   hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW>), dim3(grid), dim3(64 * NW), 0, stream,
                      (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk,
-                     (const bf16*)dv, dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale);
+                     (const bf16*)dv, dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale, chunk_off);
   return hipGetLastError();
 }
 
@@ -301,11 +305,11 @@ template <int GATE, bool AQK>
 static hipError_t pick_bv(int bv, const void* q, const void* k, const void* w, const float* g,
                           const void* dO, const float* aqk, const void* dv, const float* dht,
                           void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
-                          hipStream_t s) {
+                          hipStream_t s, const int* co) {
   switch (bv) {
-    case 16: return launch_state<16, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s);
-    case 32: return launch_state<32, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s);
-    case 64: return launch_state<64, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s);
+    case 16: return launch_state<16, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co);
+    case 32: return launch_state<32, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co);
+    case 64: return launch_state<64, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co);
     default: return hipErrorInvalidValue;
   }
 }
@@ -323,11 +327,11 @@ static int default_bv(int B, int H) {
   return 16;
 }
 
-extern "C" hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const float* g,
-                                    int gate_mode, const void* dO, const float* aqk, const void* dv,
-                                    const float* dht, void* dh, void* dr, float* dh0, int B, int T,
-                                    int H, int K, int V, int chunk, float scale, int value_block,
-                                    hipStream_t stream) {
+// B rows of T tokens, or (chunk_off) B sequences packed along T
+static hipError_t state_dispatch(const void* q, const void* k, const void* w, const float* g, int gate_mode,
+                                 const void* dO, const float* aqk, const void* dv, const float* dht, void* dh,
+                                 void* dr, float* dh0, int B, int T, int H, int K, int V, int chunk, float scale,
+                                 int value_block, hipStream_t stream, const int* co) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0)
     return hipErrorInvalidValue;
   if (!q || !k || !w || !dO || !dh || !dr) return hipErrorInvalidValue;
@@ -335,17 +339,35 @@ extern "C" hipError_t fdr_state_bwd(const void* q, const void* k, const void* w,
   if (gate_mode != GATE_NONE && g == nullptr) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : default_bv(B, H);
   const bool from_aqk = aqk != nullptr;
+#define S_ARGS bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream, co
   switch (gate_mode) {
     case GATE_NONE:
-      return from_aqk ? pick_bv<GATE_NONE, true>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream)
-                      : pick_bv<GATE_NONE, false>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream);
+      return from_aqk ? pick_bv<GATE_NONE, true>(S_ARGS) : pick_bv<GATE_NONE, false>(S_ARGS);
     case GATE_SCALAR:
-      return from_aqk ? pick_bv<GATE_SCALAR, true>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream)
-                      : pick_bv<GATE_SCALAR, false>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream);
+      return from_aqk ? pick_bv<GATE_SCALAR, true>(S_ARGS) : pick_bv<GATE_SCALAR, false>(S_ARGS);
     case GATE_VECTOR:
-      return from_aqk ? pick_bv<GATE_VECTOR, true>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream)
-                      : pick_bv<GATE_VECTOR, false>(bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream);
+      return from_aqk ? pick_bv<GATE_VECTOR, true>(S_ARGS) : pick_bv<GATE_VECTOR, false>(S_ARGS);
     default:
       return hipErrorInvalidValue;
   }
+#undef S_ARGS
+}
+
+extern "C" hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const float* g,
+                                    int gate_mode, const void* dO, const float* aqk, const void* dv,
+                                    const float* dht, void* dh, void* dr, float* dh0, int B, int T,
+                                    int H, int K, int V, int chunk, float scale, int value_block,
+                                    hipStream_t stream) {
+  return state_dispatch(q, k, w, g, gate_mode, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, K, V, chunk, scale,
+                        value_block, stream, nullptr);
+}
+
+extern "C" hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, const float* g,
+                                           int gate_mode, const void* dO, const float* aqk, const void* dv,
+                                           const float* dht, void* dh, void* dr, float* dh0,
+                                           const int* chunk_offsets, int N, int T, int H, int K, int V,
+                                           int chunk, float scale, int value_block, hipStream_t stream) {
+  if (!chunk_offsets) return hipErrorInvalidValue;
+  return state_dispatch(q, k, w, g, gate_mode, dO, aqk, dv, dht, dh, dr, dh0, N, T, H, K, V, chunk, scale,
+                        value_block, stream, chunk_offsets);
 }

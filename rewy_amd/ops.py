@@ -58,6 +58,24 @@ def _affine_workspace(B, NT, H, dev):
             torch.empty(n, K_SUPPORTED, V_SUPPORTED, device=dev, dtype=torch.float32))
 
 
+def _chunk_offsets(chunk_offsets, B, T, dev):
+    """Validated (int32 device tensor, N) for a packed variable-length batch, or (None, B).
+
+    chunk_offsets[n] is the first chunk of sequence n (FLA's prepare_chunk_offsets over
+    chunk-aligned cu_seqlens): starts at 0, ends at T / 64, every sequence >= 1 chunk."""
+    if chunk_offsets is None:
+        return None, B
+    if B != 1:
+        raise ValueError("a variable-length batch is packed along T: B must be 1")
+    co = torch.as_tensor(chunk_offsets)
+    host = co.detach().to("cpu", torch.int64)
+    if host.ndim != 1 or host.numel() < 2:
+        raise ValueError("chunk_offsets must be [N+1] with N >= 1")
+    if int(host[0]) != 0 or int(host[-1]) != T // CHUNK or bool((host[1:] <= host[:-1]).any()):
+        raise ValueError(f"chunk_offsets must rise strictly from 0 to T/{CHUNK} = {T // CHUNK}")
+    return co.to(device=dev, dtype=torch.int32).contiguous(), host.numel() - 1
+
+
 def _dims(q):
     if q.ndim != 4:
         raise ValueError("q must be [B,T,H,K]")
@@ -72,8 +90,12 @@ def _dims(q):
 
 
 def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, want_dh0=True,
-              value_block=0, method="auto"):
+              value_block=0, method="auto", chunk_offsets=None):
     """Reverse state recurrence.  Returns (dh [B,NT,H,K,V] bf16, dR [B,T,H,V] bf16, dh0 fp32|None).
+
+    ``chunk_offsets`` (int [N+1]): B = 1 holds N sequences packed along T, sequence n on
+    chunks [chunk_offsets[n], chunk_offsets[n+1]); dht / dh0 are then [N,H,K,V] and the
+    direct kernel runs (fdr_state_bwd_varlen).
 
     method "direct": one kernel (fdr_state_bwd); "affine": chunk-parallel step
     matrices, a one-product-per-chunk scan and a chunk-parallel dR pass
@@ -97,15 +119,24 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
         _need(aqk, "Aqk", f32, (B, T, H, CHUNK), dev)
     if dv is not None:
         _need(dv, "dv", bf, (B, T, H, V), dev)
+    co, N = _chunk_offsets(chunk_offsets, B, T, dev)
     if dht is not None:
-        _need(dht, "dht", f32, (B, H, K, V), dev)
+        _need(dht, "dht", f32, (N, H, K, V), dev)
     if value_block not in (0, 16, 32, 64):
         raise ValueError("value_block must be 0, 16, 32 or 64")
     NT = T // CHUNK
     dh = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
     dr = torch.empty(B, T, H, V, device=dev, dtype=bf)
-    dh0 = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_dh0 else None
+    dh0 = torch.empty(N, H, K, V, device=dev, dtype=f32) if want_dh0 else None
     P = _lib.ptr
+    if co is not None:
+        if method == "affine":
+            raise ValueError("the affine-step form takes equal-length rows, not chunk_offsets")
+        st = _lib.load().fdr_state_bwd_varlen(P(q), P(k), P(w), P(g), int(gate_mode), P(dO), P(aqk), P(dv),
+                                              P(dht), P(dh), P(dr), P(dh0), P(co), N, T, H, K, V, CHUNK,
+                                              float(scale), int(value_block), _lib.stream_handle(dev))
+        _lib.check(st, "fdr_state_bwd_varlen")
+        return dh, dr, dh0
     if _use_affine(method, B, H, NT):
         vb = value_block or AFFINE_VALUE_BLOCK
         step, offset = _affine_workspace(B, NT, H, dev)
@@ -322,9 +353,10 @@ def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, 
     return out
 
 
-def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, method="auto"):
+def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, method="auto",
+          chunk_offsets=None):
     """Forward state scan.  Returns (h [B,NT,H,K,V] bf16, v_new [B,T,H,V] bf16, final fp32|None).
-    ``method`` as for ``state_bwd``."""
+    ``method`` and ``chunk_offsets`` as for ``state_bwd`` (h0 / final per sequence)."""
     B, T, H, K = _dims(k)
     V = V_SUPPORTED
     dev = k.device
@@ -338,15 +370,23 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
         _need(g, "g", f32, (B, T, H), dev)
     elif gate_mode != GATE_NONE:
         raise ValueError("gate_mode must be 0, 1 or 2")
+    co, N = _chunk_offsets(chunk_offsets, B, T, dev)
     if h0 is not None:
-        _need(h0, "h0", f32, (B, H, K, V), dev)
+        _need(h0, "h0", f32, (N, H, K, V), dev)
     if value_block not in (0, 16, 32, 64):
         raise ValueError("value_block must be 0, 16, 32 or 64")
     NT = T // CHUNK
     h = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
     vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
-    ht = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_final else None
+    ht = torch.empty(N, H, K, V, device=dev, dtype=f32) if want_final else None
     P = _lib.ptr
+    if co is not None:
+        if method == "affine":
+            raise ValueError("the affine-step form takes equal-length rows, not chunk_offsets")
+        st = _lib.load().fdr_fwd_h_varlen(P(k), P(w), P(u), P(g), int(gate_mode), P(h0), P(h), P(vnew), P(ht),
+                                          P(co), N, T, H, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
+        _lib.check(st, "fdr_fwd_h_varlen")
+        return h, vnew, ht
     if _use_affine(method, B, H, NT):
         vb = value_block or AFFINE_VALUE_BLOCK
         step, offset = _affine_workspace(B, NT, H, dev)

@@ -76,3 +76,22 @@ def test_host_wrappers_validate_before_launch():
         ops.state_bwd(q, q, q, None, 0, q, 1.0, dv=q)
     with pytest.raises(ValueError, match="multiple of 64"):
         ops.chunk_bwd(q[:, :100], q, q, q, q, q, None, 0, None, None, None, 1.0)
+
+
+def test_backward_varlen_seam_validation():
+    """cu_seqlens at the backward seam: chunk-aligned, non-empty sequences map to chunk
+    offsets; anything else is refused before any kernel runs."""
+    import pytest
+    import torch
+    from rewy_amd.backends.backward import _varlen
+    q = torch.zeros(1, 256, 1, 128)
+    assert _varlen(q, {}) is None
+    assert _varlen(q, dict(cu_seqlens=torch.tensor([0, 64, 256]))).tolist() == [0, 1, 4]
+    with pytest.raises(NotImplementedError, match="chunk"):
+        _varlen(q, dict(cu_seqlens=torch.tensor([0, 100, 256])))
+    with pytest.raises(NotImplementedError, match="chunk"):
+        _varlen(q, dict(cu_seqlens=torch.tensor([0, 64, 64, 256])))
+    with pytest.raises(ValueError, match="rise"):
+        _varlen(q, dict(cu_seqlens=torch.tensor([0, 64])))
+    with pytest.raises(NotImplementedError):
+        _varlen(q, dict(chunk_offsets=torch.tensor([0, 4])))
