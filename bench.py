@@ -381,6 +381,48 @@ def paper_grid(reps):
     print(json.dumps({"paper_grid_geomean_speedup_vs_h100_rewy": summary}), flush=True)
 
 
+VARLEN_LENS = [8192, 4096, 2048, 2048, 1024, 512, 300, 7000, 3000, 4548]   # 32768 tokens
+
+
+def varlen(steps, warmup):
+    """KDA forward + backward (public operator, recompute policy, H=16) on a ragged
+    packed batch: natively packed (cu_seqlens) vs the same sequences padded to the
+    longest and run as batch rows.  Synthetic inputs; one JSON line."""
+    import torch
+    import rewy_amd as fdr
+    H, dev = 16, torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    def inputs(B, T):
+        nrm = torch.nn.functional.normalize
+        q = nrm(torch.randn(B, T, H, 128, device=dev, generator=gen), dim=-1).bfloat16()
+        k = nrm(torch.randn(B, T, H, 128, device=dev, generator=gen), dim=-1).bfloat16()
+        v = torch.randn(B, T, H, 128, device=dev, generator=gen).bfloat16()
+        g = -torch.rand(B, T, H, 128, device=dev, generator=gen) * 0.1
+        beta = torch.rand(B, T, H, device=dev, generator=gen)
+        do = torch.randn(B, T, H, 128, device=dev, generator=gen).bfloat16()
+        return [x.requires_grad_() for x in (q, k, v, g, beta)], do
+
+    T, N, Tm = sum(VARLEN_LENS), len(VARLEN_LENS), max(VARLEN_LENS)
+    cu = torch.tensor([0] + VARLEN_LENS).cumsum(0).to(dev)
+    xs, do = inputs(1, T)
+    xp, dop = inputs(N, Tm)
+    res = {}
+    with fdr.use_backend("optimized", ops=("kda",)):
+        def packed():
+            o, _ = fdr.chunk_kda(*xs, cu_seqlens=cu)
+            return torch.autograd.grad(o, xs, do)
+
+        def padded():
+            o, _ = fdr.chunk_kda(*xp)
+            return torch.autograd.grad(o, xp, dop)
+        for name, fn in (("packed_ms", packed), ("padded_to_longest_ms", padded)):
+            print(f"[bench] varlen {name}", file=sys.stderr, flush=True)
+            res[name] = round(time_steps(fn, steps, warmup), 3)
+    print(json.dumps({"varlen": "kda forward+backward, recompute, H=16", "lens": VARLEN_LENS, "tokens": T,
+                      "padded_tokens": N * Tm, **res, "data": "synthetic"}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -394,6 +436,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true", help="skip the GDN companion measurement")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (reference kernel for the HBM byte counters)")
+    ap.add_argument("--varlen", action="store_true",
+                    help="time a ragged cu_seqlens batch packed natively vs padded to the longest instead")
     ap.add_argument("--paper-grid", action="store_true",
                     help="time the reference's published operator grid (HIP-graph replay) instead")
     args = ap.parse_args()
@@ -417,6 +461,9 @@ def main():
     torch.cuda.set_device(0)
     if args.paper_grid:
         paper_grid(max(args.steps, 20))
+        return
+    if args.varlen:
+        varlen(min(args.steps, 10), min(args.warmup, 3))
         return
     cfg = CONFIGS[args.config]
     B, T, H = cfg["B"], cfg["T"], cfg["H"]

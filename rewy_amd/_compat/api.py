@@ -147,13 +147,44 @@ def _unpack(x, bounds, Tp):
     return torch.cat(rows, 0)
 
 
-def _pack_aligned(x, dst, Tp):
-    """[1, T, ...] packed sequences -> [1, Tp, ...]: token t moves to dst[t], every other
-    position is zero (each sequence padded at its end to whole chunks).  One scatter
-    (its gradient one gather), whatever the number of sequences."""
-    if x is None:
-        return None
-    return x.new_zeros((1, Tp) + tuple(x.shape[2:])).index_copy(1, dst, x)
+class _PackAligned(torch.autograd.Function):
+    """[1, T, ...] packed sequences (bounds (s, e)) -> [1, Tp, ...] with sequence n at
+    token starts[n] and the tail of its last chunk zero.  Block copies both ways (one
+    read and one write per element; only the pad tails are filled)."""
+
+    @staticmethod
+    def forward(ctx, x, bounds, starts, Tp):
+        ctx.bounds, ctx.starts, ctx.T = bounds, starts, x.shape[1]
+        out = x.new_empty((1, Tp) + tuple(x.shape[2:]))
+        for (s, e), a, a_next in zip(bounds, starts, starts[1:] + [Tp]):
+            out[:, a:a + e - s].copy_(x[:, s:e])
+            out[:, a + e - s:a_next].zero_()
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        return _take(grad, ctx.bounds, ctx.starts), None, None, None
+
+
+class _UnpackAligned(torch.autograd.Function):
+    """The inverse gather: [1, Tp, ...] -> [1, T, ...] (the real tokens only)."""
+
+    @staticmethod
+    def forward(ctx, y, bounds, starts):
+        ctx.bounds, ctx.starts, ctx.Tp = bounds, starts, y.shape[1]
+        return _take(y, bounds, starts)
+
+    @staticmethod
+    def backward(ctx, grad):
+        return _PackAligned.apply(grad.contiguous(), ctx.bounds, ctx.starts, ctx.Tp), None, None
+
+
+def _take(y, bounds, starts):
+    return torch.cat([y[:, a:a + e - s] for (s, e), a in zip(bounds, starts)], 1)
+
+
+def _pack_aligned(x, bounds, starts, Tp):
+    return None if x is None else _PackAligned.apply(x.contiguous(), bounds, starts, Tp)
 
 
 def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0,
@@ -198,12 +229,10 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
         elif backend == "optimized" and q.is_cuda:
             lens = [max(64, -(-(e - s) // 64) * 64) for s, e in bounds]
             cu_al = torch.tensor([0] + lens, dtype=torch.int64).cumsum(0)
-            seq = torch.tensor(cu, dtype=torch.int64)
-            n_of = torch.repeat_interleave(torch.arange(len(bounds)), seq[1:] - seq[:-1])
-            dst = (torch.arange(cu[-1]) - seq[n_of] + cu_al[n_of]).to(q.device)
-            xs = [_pack_aligned(x, dst, int(cu_al[-1])) for x in (q, k, v, g, beta, b, w)]
+            starts = cu_al[:-1].tolist()
+            xs = [_pack_aligned(x, bounds, starts, int(cu_al[-1])) for x in (q, k, v, g, beta, b, w)]
             o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, *xs, h0, cu_al)
-            o = o.index_select(1, dst)
+            o = _UnpackAligned.apply(o, bounds, starts)
         else:
             Tp = max(64, -(-max(e - s for s, e in bounds) // 64) * 64)
             xs = [_unpack(x, bounds, Tp) for x in (q, k, v, g, beta, b, w)]
