@@ -41,6 +41,10 @@ CONFIGS = {
     # native recomputation inside the backward
     "gdn2": dict(op="gdn2", B=2, T=8192, H=32, seed=3, gate="gdn2", h0=True, full_saving=False),
     # long context, 1024 sequential chunks
+    # KDA with the in-kernel gate activation (use_gate_in_kernel: -exp(A_log) softplus(g_raw
+    # + dt_bias)): its backward rides in the chunk kernel (fdr_chunk_bwd_gate_fold)
+    "kda_gate": dict(op="kda", B=8, T=4096, H=16, seed=2, gate="kda", h0=False, full_saving=True,
+                     gate_in_kernel=True),
     "kda_long": dict(op="kda", B=1, T=65536, H=16, seed=4, gate="kda_long", h0=True, full_saving=True),
     # BASELINE.json configs[0] shape (its CPU reference path is the oracle test suite)
     "delta": dict(op="delta", B=1, T=256, H=2, seed=0, gate=None, h0=False, full_saving=False),
@@ -74,6 +78,8 @@ def kernel_costs(op, full_saving):
     rd = 5 * TILE + g_b + gates_b + AT + 2 * HS + (TILE if vb else 0)
     wr = 3 * TILE + g_b + (2 * TILE if vb else beta_b)
     costs["fdr_chunk_bwd"] = (rd + wr, 3 * mm(64, 64, 128) + 3 * mm(64, 128, 128) + 4 * mm(64, 64, 128))
+    # folded gate backward: g_raw read besides g, dL/dg_raw (fp32) written in place of dg
+    costs["fdr_chunk_bwd_gate_fold"] = (costs["fdr_chunk_bwd"][0] + g_b, costs["fdr_chunk_bwd"][1])
     # the affine-step launches compute the same recurrences: same operands and results
     # (their private step-matrix workspace is not algorithmic traffic)
     costs["affine_state"] = costs["fdr_state_bwd"]
@@ -133,11 +139,21 @@ def setup(cfg, device):
     keep = cfg["full_saving"]
     saved = {n: (sv[n] if keep else None) for n in ("w", "u", "qg", "kg", "v_new", "h")}
 
+    fold = None
+    if cfg.get("gate_in_kernel"):
+        gen = torch.Generator().manual_seed(cfg["seed"] + 100)
+        B, T, H = cfg["B"], cfg["T"], cfg["H"]
+        fold = dict(g_raw=torch.randn(B, T, H, 128, generator=gen).to(device),
+                    A_log=(torch.randn(H, generator=gen) * 0.5).to(device),
+                    dt_bias=(torch.randn(H * 128, generator=gen) * 0.5).to(device), lower_bound=None)
     if op == "kda":
+        gate_kw = {} if fold is None else dict(use_gate_in_kernel=True, g_org=fold["g_raw"], A_log=fold["A_log"],
+                                               dt_bias=fold["dt_bias"])
+
         def step():
             return bw.kda_backward(q=xs["q"], k=xs["k"], v=xs["v"], beta=xs["beta"], Aqk=sv["Aqk"], Akk=sv["Akk"],
                                    scale=scale, initial_state=xs["h0"], do=dO, dht=None, g=sv["gc"],
-                                   disable_recompute=keep, **saved)
+                                   disable_recompute=keep, **gate_kw, **saved)
     elif op == "gdn2":
         def step():
             return bw.gdn2_backward(q=xs["q"], k=xs["k"], v=xs["v"], b=xs["b"], w_gate=xs["w"], Aqk=sv["Aqk"],
@@ -183,8 +199,9 @@ def setup(cfg, device):
         kern["fdr_state_bwd"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
                                                       want_dh0=xs["h0"] is not None, method="direct")
         dh, dR, _ = kern["fdr_state_bwd"]()
-    kern["fdr_chunk_bwd"] = lambda: ops.chunk_bwd(xs["q"], xs["k"], xs["v"], v_new, dO, dR, g, gate, sv["Akk"], h,
-                                                  dh, scale, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"))
+    name = "fdr_chunk_bwd" if fold is None else "fdr_chunk_bwd_gate_fold"
+    kern[name] = lambda: ops.chunk_bwd(xs["q"], xs["k"], xs["v"], v_new, dO, dR, g, gate, sv["Akk"], h, dh, scale,
+                                       beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"), gate_fold=fold)
     return xs, dO, sv, step, kern, (dh, dR), forward
 
 
@@ -473,7 +490,7 @@ def main():
 
     # ---- gradient check against the original formulation (same GPU, same inputs) ----
     parity, t_orig = None, None
-    if not args.no_original and cfg["op"] == "kda":
+    if not args.no_original and cfg["op"] == "kda" and not cfg.get("gate_in_kernel"):
         from rewy_amd.original import original_backward
         got = res["step"]()
         saved = sv if cfg["full_saving"] else None
