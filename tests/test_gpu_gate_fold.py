@@ -19,13 +19,14 @@ def _rel(a, r):
 
 @pytest.mark.parametrize("mode", ["softplus", "bounded", "bounded_no_A"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(1, 128, 2), (2, 192, 3), (1, 512, 20)])
-def test_gate_fold_matches_two_pass(mode, dtype, shape):
+@pytest.mark.parametrize("shape,with_bias", [((1, 128, 2), True), ((2, 192, 3), True), ((1, 512, 20), True),
+                                              ((2, 192, 3), False)])
+def test_gate_fold_matches_two_pass(mode, dtype, shape, with_bias):
     from rewy_amd import ops
     from rewy_amd.forward import chunk_forward
     from rewy_amd.gates import kda_gate_bwd
     B, T, H = shape
-    print(f"\n[gate-fold] mode={mode} dtype={dtype} shape={shape}", flush=True)
+    print(f"\n[gate-fold] mode={mode} dtype={dtype} shape={shape} bias={with_bias}", flush=True)
     xs, dO = make_inputs("kda", B, T, H, seed=17)
     _, _, sv = chunk_forward("kda", xs["q"], xs["k"], xs["v"], g=xs["g"], beta=xs["beta"],
                              initial_state=xs["initial_state"])
@@ -34,7 +35,7 @@ def test_gate_fold_matches_two_pass(mode, dtype, shape):
     gen = torch.Generator().manual_seed(4)
     g_raw = (torch.randn(B, T, H, 128, generator=gen) * 3).to(dtype).to(dev)
     A = None if mode == "bounded_no_A" else (torch.randn(H, generator=gen) * 0.5).to(dev)
-    dt = (torch.randn(H * 128, generator=gen) * 0.5).to(dev)
+    dt = (torch.randn(H * 128, generator=gen) * 0.5).to(dev) if with_bias else None
     lb = None if mode == "softplus" else -5.0
     scale = sv["scale"]
     gc = cu(sv["gc"])
@@ -55,9 +56,13 @@ def test_gate_fold_matches_two_pass(mode, dtype, shape):
     assert (got["dA_log"] is None) == (r_A is None)
     if r_A is not None:
         assert _rel(got["dA_log"], r_A) < 1e-5, _rel(got["dA_log"], r_A)
-    assert _rel(got["ddt_bias"], r_dt) < 1e-5, _rel(got["ddt_bias"], r_dt)
+    assert (got["ddt_bias"] is None) == (r_dt is None)
+    if r_dt is not None:
+        assert _rel(got["ddt_bias"], r_dt) < 1e-5, _rel(got["ddt_bias"], r_dt)
     # a second call reuses nothing stale: the partial sums are rewritten, not accumulated
     again = ops.chunk_bwd(*args, beta=cu(xs["beta"]),
                           gate_fold=dict(g_raw=g_raw, A_log=A, dt_bias=dt, lower_bound=lb))
     torch.cuda.synchronize()
-    assert torch.equal(again["ddt_bias"], got["ddt_bias"])
+    assert torch.equal(again["dg"], got["dg"])
+    if r_dt is not None:
+        assert torch.equal(again["ddt_bias"], got["ddt_bias"])
