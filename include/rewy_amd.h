@@ -48,8 +48,8 @@ hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const floa
 /*
  * fdr_state_bwd over a variable-length batch: N sequences packed along T (B = 1),
  * sequence n owning chunks [chunk_offsets[n], chunk_offsets[n+1]) -- every sequence
- * starts on a chunk boundary and holds at least one chunk (pad with zero keys,
- * values and gates, which leave the state untouched).  chunk_offsets: int32 [N+1],
+ * starts on a chunk boundary (pad with zero keys, values and gates, which leave
+ * the state untouched); an empty sequence passes its state through (dh0 = dht).  chunk_offsets: int32 [N+1],
  * device memory, chunk_offsets[N] = T / 64.  dht / dh0 are per sequence
  * [N,H,K,V]; dh is [T/64,H,K,V] in packed chunk order.  Replaces the reference's
  * state_bwd with cu_seqlens / chunk_offsets (kernels/vector_state_gpu.py:47-67,

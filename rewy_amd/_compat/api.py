@@ -221,7 +221,7 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
         if h0 is not None and h0.shape[0] != len(bounds):
             raise ValueError(f"The number of initial states is expected to be equal to the number of input "
                              f"sequences, i.e., {len(bounds)} rather than {h0.shape[0]}.")
-        aligned = all(s % 64 == 0 and e > s for s, e in bounds)
+        aligned = all(s % 64 == 0 for s, e in bounds) and cu[-1] % 64 == 0
         if backend == "optimized" and q.is_cuda and aligned:
             # already on chunk boundaries: the kernels take the batch as it is
             o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta,

@@ -46,9 +46,11 @@ def _varlen(q, kw):
         raise ValueError(f"The batch size is expected to be 1 rather than {B} when using `cu_seqlens`.")
     if host.ndim != 1 or host.numel() < 2 or int(host[0]) != 0 or int(host[-1]) != T:
         raise ValueError("cu_seqlens must rise from 0 to T")
-    if bool((host % ops.CHUNK != 0).any()) or bool((host[1:] <= host[:-1]).any()):
+    if bool((host[1:] < host[:-1]).any()):
+        raise ValueError("cu_seqlens must not decrease")
+    if bool((host % ops.CHUNK != 0).any()):
         raise NotImplementedError("HIP backward: every sequence of cu_seqlens must start on a 64-token chunk "
-                                  "boundary and be non-empty (pad each sequence to whole chunks)")
+                                  "boundary (pad each sequence to whole chunks)")
     return host // ops.CHUNK
 
 

@@ -256,9 +256,10 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
   const int bh = logical / NVT;
   const int b = bh / H, h = bh % H;
   // chunks [c0, c0 + NT) of the packed token axis: row b of T tokens, or sequence b of
-  // a variable-length batch (chunk_off: cumulative chunk counts, every count >= 1)
-  const int c0 = chunk_off ? chunk_off[b] : b * (T / C);
-  const int NT = chunk_off ? chunk_off[b + 1] - c0 : T / C;
+  // a variable-length batch (chunk_off: cumulative chunk counts; clamped to the T / C
+  // chunks there are, an empty sequence passes its state through)
+  const int c0 = chunk_off ? min(max(chunk_off[b], 0), T / C) : b * (T / C);
+  const int NT = chunk_off ? max(min(chunk_off[b + 1], T / C) - c0, 0) : T / C;
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int v_base = vt * BV;
   const size_t rsk = (size_t)H * KD, rsv = (size_t)H * VD;
@@ -358,8 +359,10 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     settle(rg_tok[0]);
     settle(rg_tok[1]);
   };
-  load_chunk(0);
-  settle_chunk();
+  if (NT > 0) {
+    load_chunk(0);
+    settle_chunk();
+  }
   for (int c = 0; c < NT; ++c) {
     lds_barrier();
     stage_chunk();

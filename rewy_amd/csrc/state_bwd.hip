@@ -56,9 +56,10 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   const int bh = logical / NVT;
   const int b = bh / H, h = bh % H;
   // chunks [c0, c0 + NT) of the packed token axis: row b of T tokens, or sequence b of
-  // a variable-length batch (chunk_off: cumulative chunk counts, every count >= 1)
-  const int c0 = chunk_off ? chunk_off[b] : b * (T / C);
-  const int NT = chunk_off ? chunk_off[b + 1] - c0 : T / C;
+  // a variable-length batch (chunk_off: cumulative chunk counts; clamped to the T / C
+  // chunks there are, an empty sequence passes its state through)
+  const int c0 = chunk_off ? min(max(chunk_off[b], 0), T / C) : b * (T / C);
+  const int NT = chunk_off ? max(min(chunk_off[b + 1], T / C) - c0, 0) : T / C;
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int v_base = vt * BV;
 
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     }
   };
 
-  load_chunk(NT - 1);
+  if (NT > 0) load_chunk(NT - 1);
   for (int c = NT - 1; c >= 0; --c) {
     lds_barrier();                       // previous chunk done with every LDS tile
     stage_chunk();

@@ -62,7 +62,8 @@ def _chunk_offsets(chunk_offsets, B, T, dev):
     """Validated (int32 device tensor, N) for a packed variable-length batch, or (None, B).
 
     chunk_offsets[n] is the first chunk of sequence n (FLA's prepare_chunk_offsets over
-    chunk-aligned cu_seqlens): starts at 0, ends at T / 64, every sequence >= 1 chunk."""
+    chunk-aligned cu_seqlens): starts at 0, ends at T / 64, never decreases (an empty
+    sequence passes its state through: dh0 = dht, final = h0)."""
     if chunk_offsets is None:
         return None, B
     if B != 1:
@@ -71,8 +72,8 @@ def _chunk_offsets(chunk_offsets, B, T, dev):
     host = co.detach().to("cpu", torch.int64)
     if host.ndim != 1 or host.numel() < 2:
         raise ValueError("chunk_offsets must be [N+1] with N >= 1")
-    if int(host[0]) != 0 or int(host[-1]) != T // CHUNK or bool((host[1:] <= host[:-1]).any()):
-        raise ValueError(f"chunk_offsets must rise strictly from 0 to T/{CHUNK} = {T // CHUNK}")
+    if int(host[0]) != 0 or int(host[-1]) != T // CHUNK or bool((host[1:] < host[:-1]).any()):
+        raise ValueError(f"chunk_offsets must rise from 0 to T/{CHUNK} = {T // CHUNK}")
     return co.to(device=dev, dtype=torch.int32).contiguous(), host.numel() - 1
 
 

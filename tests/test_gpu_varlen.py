@@ -64,11 +64,29 @@ def test_chunk_offsets_are_validated():
     dev = torch.device("cuda")
     x = torch.zeros(1, 256, 1, 128, device=dev, dtype=torch.bfloat16)
     g = torch.zeros(1, 256, 1, 128, device=dev)
-    for bad in ([0, 2, 2, 4], [0, 3], [1, 4], [0, 4, 3, 4]):
+    for bad in ([0, 3], [1, 4], [0, 4, 3, 4], [0, 2, 1, 4]):
         with pytest.raises(ValueError, match="chunk_offsets"):
             ops.fwd_h(x, x, x, g, ops.GATE_VECTOR, chunk_offsets=torch.tensor(bad))
     with pytest.raises(ValueError, match="affine"):
         ops.fwd_h(x, x, x, g, ops.GATE_VECTOR, chunk_offsets=torch.tensor([0, 4]), method="affine")
+
+
+def test_empty_sequences_pass_their_state_through():
+    from rewy_amd import ops
+    dev = torch.device("cuda")
+    print("\n[varlen] empty sequences: offsets [0, 0, 2, 2, 4]", flush=True)
+    gen = torch.Generator().manual_seed(5)
+    r = lambda *s: (torch.randn(*s, generator=gen) * 0.1).to(dev)
+    x = r(1, 256, 2, 128).bfloat16()
+    g = -r(1, 256, 2, 128).abs()
+    h0, dht = r(4, 2, 128, 128), r(4, 2, 128, 128)
+    co = torch.tensor([0, 0, 2, 2, 4])
+    _, _, ht = ops.fwd_h(x, x, x, g, ops.GATE_VECTOR, h0=h0, want_final=True, chunk_offsets=co)
+    _, _, dh0 = ops.state_bwd(x, x, x, g, ops.GATE_VECTOR, x, 1.0, dv=x, dht=dht, chunk_offsets=co)
+    torch.cuda.synchronize()
+    for n in (0, 2):
+        assert torch.equal(ht[n], h0[n]) and torch.equal(dh0[n], dht[n]), n
+    assert not torch.equal(ht[1], h0[1]) and not torch.equal(dh0[3], dht[3])
 
 
 @pytest.mark.parametrize("op,recompute,lens", [("kda", False, [1, 64, 300, 129, 700]),

@@ -89,8 +89,9 @@ def test_backward_varlen_seam_validation():
     assert _varlen(q, dict(cu_seqlens=torch.tensor([0, 64, 256]))).tolist() == [0, 1, 4]
     with pytest.raises(NotImplementedError, match="chunk"):
         _varlen(q, dict(cu_seqlens=torch.tensor([0, 100, 256])))
-    with pytest.raises(NotImplementedError, match="chunk"):
-        _varlen(q, dict(cu_seqlens=torch.tensor([0, 64, 64, 256])))
+    assert _varlen(q, dict(cu_seqlens=torch.tensor([0, 64, 64, 256]))).tolist() == [0, 1, 1, 4]
+    with pytest.raises(ValueError, match="decrease"):
+        _varlen(q, dict(cu_seqlens=torch.tensor([0, 128, 64, 256])))
     with pytest.raises(ValueError, match="rise"):
         _varlen(q, dict(cu_seqlens=torch.tensor([0, 64])))
     with pytest.raises(NotImplementedError):
