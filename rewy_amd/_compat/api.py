@@ -33,10 +33,18 @@ def _l2norm(x, backend):
 class ChunkFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w,
-                initial_state, cu_seqlens=None):
+                initial_state, cu_seqlens=None, gate=None, A_log=None, dt_bias=None):
         # cu_seqlens (optimized backend on a GPU only): sequences packed on 64-token
-        # chunk boundaries, B = 1; the state scans restart at each sequence
-        ctx.cu_seqlens = cu_seqlens
+        # chunk boundaries, B = 1; the state scans restart at each sequence.
+        # gate = (lower_bound,) (KDA, optimized backend on a GPU, no padded tokens): g is the
+        # raw gate, activated here by the HIP gate kernel; its backward, with dA_log and
+        # ddt_bias, is folded into the chunk kernel
+        ctx.cu_seqlens, ctx.gate = cu_seqlens, gate
+        ctx.g_dtype = None if g is None else g.dtype
+        g_raw = None
+        if gate is not None:
+            from ..gates import kda_gate
+            g_raw, g = g, kda_gate(g, A_log, dt_bias, gate[0], native=True)
         if backend == "optimized" and q.is_cuda:
             from ..hip_forward import chunk_forward_hip
             o, final, sv = chunk_forward_hip(op, q, k, v, g=g, beta=beta, b=b, w=w,
@@ -51,23 +59,29 @@ class ChunkFunction(torch.autograd.Function):
                                          output_final_state=output_final_state)
         keep = full_saving and op in ("kda", "gdn2")
         ctx.save_for_backward(q, k, v, sv["gc"], beta, b, w, sv["Aqk"], sv["Akk"], initial_state,
-                              *(sv[n] if keep else None for n in ("w", "u", "qg", "kg", "v_new", "h")))
+                              *(sv[n] if keep else None for n in ("w", "u", "qg", "kg", "v_new", "h")),
+                              g_raw, A_log, dt_bias)
         ctx.op, ctx.backend, ctx.scale = op, backend, scale
-        ctx.g_dtype = None if g is None else g.dtype
         ctx.has_h0 = initial_state is not None
         return o, final
 
     @staticmethod
     def backward(ctx, do, dht):
-        (q, k, v, gc, beta, b, w, Aqk, Akk, h0, w_wy, u_wy, qg, kg, v_new, h) = ctx.saved_tensors
+        (q, k, v, gc, beta, b, w, Aqk, Akk, h0, w_wy, u_wy, qg, kg, v_new, h, g_raw, A_log,
+         dt_bias) = ctx.saved_tensors
+        dA_log = ddt_bias = None
         op, scale = ctx.op, ctx.scale
         if ctx.backend == "optimized":
             from ..backends import backward as bw
             cu = ctx.cu_seqlens
             if op == "kda":
-                dq, dk, dv, db, dg, dh0, _, _ = bw.kda_backward(
+                gate_kw = {} if ctx.gate is None else dict(
+                    use_gate_in_kernel=True, g_org=g_raw, A_log=A_log, lower_bound=ctx.gate[0],
+                    dt_bias=None if dt_bias is None else dt_bias.reshape(-1))
+                dq, dk, dv, db, dg, dh0, dA_log, ddt_bias = bw.kda_backward(
                     q=q, k=k, v=v, beta=beta, Aqk=Aqk, Akk=Akk, scale=scale, initial_state=h0,
-                    do=do, dht=dht, g=gc, w=w_wy, u=u_wy, qg=qg, kg=kg, v_new=v_new, h=h, cu_seqlens=cu)
+                    do=do, dht=dht, g=gc, w=w_wy, u=u_wy, qg=qg, kg=kg, v_new=v_new, h=h, cu_seqlens=cu,
+                    **gate_kw)
                 dw = None
             elif op == "gdn2":
                 dq, dk, dv, db, dw, dg, dh0, _, _ = bw.gdn2_backward(
@@ -98,7 +112,8 @@ class ChunkFunction(torch.autograd.Function):
         gb = cast(db, b if op == "gdn2" else beta)
         return (None, None, None, None, None, cast(dq, q), cast(dk, k), cast(dv, v),
                 None if dg is None else dg.to(ctx.g_dtype),
-                None if op == "gdn2" else gb, gb if op == "gdn2" else None, cast(dw, w), dh0, None)
+                None if op == "gdn2" else gb, gb if op == "gdn2" else None, cast(dw, w), dh0, None, None,
+                cast(dA_log, A_log), None if ddt_bias is None else ddt_bias.reshape(dt_bias.shape).to(dt_bias.dtype))
 
 
 def _unsupported(name, **flags):
@@ -188,7 +203,7 @@ def _pack_aligned(x, bounds, starts, Tp):
 
 
 def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0,
-           state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None):
+           state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None, gate_fold=None):
     """Layout adapters around the chunk Function (all autograd-transparent torch ops):
 
     * grouped value heads (HV = v.shape[2] > H): q and k are repeated over each
@@ -211,7 +226,12 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
             b = b.repeat_interleave(HV // H, dim=2)
     if state_v_first and h0 is not None:
         h0 = h0.transpose(-1, -2)
-    if cu_seqlens is None:
+    if gate_fold is not None:
+        # raw gate, no padded tokens (checked by the caller): the activation runs inside
+        lb, A_log, dt_bias = gate_fold
+        o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b,
+                                       w, h0, None, (lb,), A_log, dt_bias)
+    elif cu_seqlens is None:
         o, final = _run(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0)
     else:
         if q.shape[0] != 1:
@@ -279,17 +299,23 @@ def make_kda(backend):
             q, k = _l2norm(q, backend), _l2norm(k, backend)
         if use_beta_sigmoid_in_kernel:
             beta = beta.sigmoid() * (2.0 if allow_neg_eigval else 1.0)
+        fold = None
         if use_gate_in_kernel:
-            # the fused activation as its own autograd node: g's gradient flows to
-            # g_raw, A_log and dt_bias (the reference's dA_log / ddt_bias outputs)
-            from ..gates import KDAGate
-            # the optimized backend runs the activation's HIP kernels on a GPU, the
-            # original backend the torch expressions
-            g = KDAGate.apply(g, A_log, dt_bias, lower_bound, backend == "optimized" and g.is_cuda)
+            if backend == "optimized" and g.is_cuda and cu_seqlens is None and T % 64 == 0:
+                # no padded tokens: the activation runs inside the chunk Function and its
+                # backward (dg_raw, dA_log, ddt_bias) rides in the chunk kernel
+                fold = (lower_bound, A_log, dt_bias)
+            else:
+                # the fused activation as its own autograd node (padded tokens must keep a
+                # zero activated gate): g's gradient flows to g_raw, A_log and dt_bias
+                from ..gates import KDAGate
+                # the optimized backend runs the activation's HIP kernels on a GPU, the
+                # original backend the torch expressions
+                g = KDAGate.apply(g, A_log, dt_bias, lower_bound, backend == "optimized" and g.is_cuda)
         scale = K ** -0.5 if scale is None else scale
         return _apply("kda", backend, disable_recompute, scale, output_final_state, q, k, v, g, beta,
                       None, None, initial_state, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
-                      cu_seqlens_cpu=cu_seqlens_cpu)
+                      cu_seqlens_cpu=cu_seqlens_cpu, gate_fold=fold)
     return chunk_kda
 
 

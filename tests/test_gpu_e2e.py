@@ -117,27 +117,39 @@ def test_rejection_and_visible_fallback():
 
 
 @pytest.mark.parametrize("lower_bound", [None, -5.0])
-def test_kda_fused_gate_optimized_matches_original(lower_bound):
+# T = 128: the activation and its backward run inside the chunk Function (folded into the
+# chunk kernel); T = 192 with a ragged cu_seqlens pads sequence tails, so the gate stays an
+# autograd node of its own
+@pytest.mark.parametrize("T", [128, 192])
+def test_kda_fused_gate_optimized_matches_original(lower_bound, T):
     """use_gate_in_kernel=True (the gate activation feeding the HIP backward, dA_log /
     ddt_bias through its explicit backward) against the original backend on the
     same inputs; and the envelope: accepted for KDA, rejected for GDN / GDN2 with
     the reference's reasons (runtime.py:97-98)."""
     import rewy_amd as fdr
     from rewy_amd.runtime import rejection_reason
-    print(f"\n[e2e] kda fused gate lower_bound={lower_bound}", flush=True)
-    xs, dO = make_inputs("kda", 2, 128, 2, seed=31)
+    print(f"\n[e2e] kda fused gate lower_bound={lower_bound} T={T}", flush=True)
+    xs, dO = make_inputs("kda", 2, T, 2, seed=31)
     gen = torch.Generator().manual_seed(5)
-    leaves = dict(g=torch.randn(2, 128, 2, 128, generator=gen), A_log=torch.randn(2, generator=gen) * 0.5,
+    leaves = dict(g=torch.randn(2, T, 2, 128, generator=gen), A_log=torch.randn(2, generator=gen) * 0.5,
                   dt_bias=torch.randn(256, generator=gen) * 0.1)
     dev = torch.device("cuda")
     res = {}
     for backend in ("optimized", "original"):
         lv = {k: v.to(dev).requires_grad_() for k, v in leaves.items()}
         with fdr.use_backend(backend, ops=("kda",)):
-            o, _ = fdr.chunk_kda(xs["q"].to(dev), xs["k"].to(dev), xs["v"].to(dev), lv["g"], xs["beta"].to(dev),
-                                 initial_state=xs["initial_state"].to(dev), use_gate_in_kernel=True,
-                                 A_log=lv["A_log"], dt_bias=lv["dt_bias"], lower_bound=lower_bound)
-        res[backend] = [x.detach().double().cpu().numpy() for x in torch.autograd.grad(o, list(lv.values()), dO.to(dev))]
+            packed = dict(cu_seqlens=torch.tensor([0, 70, T], device=dev)) if T == 192 else {}
+            if packed:     # one packed row of two sequences, one initial state each
+                flat = lambda x: x.reshape(1, 2 * T, *x.shape[2:])
+                args = [flat(xs["q"].to(dev)), flat(xs["k"].to(dev)), flat(xs["v"].to(dev)), flat(lv["g"]),
+                        flat(xs["beta"].to(dev))]
+                packed["cu_seqlens"] = torch.tensor([0, 70, 2 * T], device=dev)
+            else:
+                args = [xs["q"].to(dev), xs["k"].to(dev), xs["v"].to(dev), lv["g"], xs["beta"].to(dev)]
+            o, _ = fdr.chunk_kda(*args, initial_state=xs["initial_state"].to(dev), use_gate_in_kernel=True,
+                                 A_log=lv["A_log"], dt_bias=lv["dt_bias"], lower_bound=lower_bound, **packed)
+        res[backend] = [x.detach().double().cpu().numpy()
+                        for x in torch.autograd.grad(o, list(lv.values()), dO.to(dev).reshape(o.shape))]
     for name, a, r in zip(leaves, res["optimized"], res["original"]):
         e = O.error(r, a, 0.02)
         print(name, e, flush=True)
