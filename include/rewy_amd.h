@@ -79,13 +79,18 @@ hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, con
  * in-chunk reverse cumsum.  dbeta (fp32) follows the reference's branch rule:
  * sum_v(P*v_new)/beta where |beta| >= 1e-6, the direct VJP otherwise
  * (kernels/kda_residual_tri_beta.py:50-60, kda_residual_local_beta_consumer.py:161-180).
+ * beta_sigmoid > 0 (scalar beta only): beta was activated in the forward as
+ * beta = beta_sigmoid * sigmoid(x) (use_beta_sigmoid_in_kernel, scale 2 with
+ * allow_neg_eigval; reference _compat/kda.py:202-206), and dbeta is written as dL/dx;
+ * 0 writes dL/dbeta.
  */
 hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v, const void* v_new,
                          const void* dO, const void* dR, const float* g, int gate_mode,
                          const float* beta, const void* b_gate, const void* w_gate,
                          const float* Akk, const void* h, const void* dh, void* dq, void* dk,
-                         void* dv, float* dg, float* dbeta, void* db, void* dw, int B, int T,
-                         int H, int K, int V, int chunk, float scale, hipStream_t stream);
+                         void* dv, float* dg, float* dbeta, float beta_sigmoid, void* db, void* dw,
+                         int B, int T, int H, int K, int V, int chunk, float scale,
+                         hipStream_t stream);
 
 /*
  * Recompute of the WY factors inside the backward (recompute policy).
@@ -199,18 +204,28 @@ hipError_t fdr_kda_gate_bwd(const float* dg, const void* g_raw, int raw_is_bf16,
  * folded into the dg stores: instead of dg it writes dg_raw = dL/dg_raw (g_raw's dtype)
  * and, where non-null, dA_log / ddt_bias, with the activation and arguments of
  * fdr_kda_gate_bwd.  `workspace` holds fdr_chunk_bwd_gate_workspace_bytes(B, T, H) bytes
- * of per-chunk partial sums.  Replaces the chunk stage plus the gate backward of the
- * reference's kda_backward with use_gate_in_kernel (backends/backward.py:63-73).
+ * of per-chunk partial sums.  beta_sigmoid as for fdr_chunk_bwd.  Replaces the chunk
+ * stage plus the gate backward of the reference's kda_backward with use_gate_in_kernel
+ * (backends/backward.py:63-73).
  */
 size_t fdr_chunk_bwd_gate_workspace_bytes(int B, int T, int H);
 
 hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, const void* v, const void* v_new, const void* dO,
                                    const void* dR, const float* g, const float* beta, const float* Akk,
                                    const void* h, const void* dh, void* dq, void* dk, void* dv, float* dbeta,
-                                   const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
+                                   float beta_sigmoid, const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
                                    int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
                                    float* ddt_bias, void* workspace, int B, int T, int H, int K, int V, int chunk,
                                    float scale, hipStream_t stream);
+
+/*
+ * beta = scale * sigmoid(x) over n elements (use_beta_sigmoid_in_kernel; scale 2 with
+ * allow_neg_eigval; reference _compat/kda.py:202-206, FLA fused_beta_sigmoid forward).
+ * x fp32 (is_bf16 = 0) or bf16 (1); beta fp32.  The backward is fdr_chunk_bwd's
+ * beta_sigmoid argument.
+ */
+hipError_t fdr_beta_sigmoid_fwd(const void* x, int is_bf16, float scale, float* beta, long long n,
+                                hipStream_t stream);
 
 /*
  * q / k L2 normalisation over K = 128 (use_qk_l2norm_in_kernel=True, reference

@@ -33,18 +33,30 @@ def _l2norm(x, backend):
 class ChunkFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w,
-                initial_state, cu_seqlens=None, gate=None, A_log=None, dt_bias=None):
+                initial_state, cu_seqlens=None, gate=None, A_log=None, dt_bias=None, beta_act=None):
         # cu_seqlens (optimized backend on a GPU only): sequences packed on 64-token
         # chunk boundaries, B = 1; the state scans restart at each sequence.
         # gate = (lower_bound,) (KDA, optimized backend on a GPU, no padded tokens): g is the
         # raw gate, activated here by the HIP gate kernel; its backward, with dA_log and
-        # ddt_bias, is folded into the chunk kernel
-        ctx.cu_seqlens, ctx.gate = cu_seqlens, gate
+        # ddt_bias, is folded into the chunk kernel.
+        # beta_act = s (scalar-beta families, optimized backend on a GPU): beta is the raw
+        # input, activated here as s * sigmoid(beta); its backward rides in the chunk
+        # kernel's dbeta stores.
+        native = backend == "optimized" and q.is_cuda
+        if gate is not None and not (native and op == "kda"):
+            raise ValueError("the folded gate is the optimized GPU path's (KDA, batches without padded tokens)")
+        if beta_act is not None and not (native and op != "gdn2"):
+            raise ValueError("the folded beta sigmoid is the optimized GPU path's (scalar beta)")
+        ctx.cu_seqlens, ctx.gate, ctx.beta_act = cu_seqlens, gate, beta_act
         ctx.g_dtype = None if g is None else g.dtype
+        ctx.beta_dtype = None if beta is None else beta.dtype
         g_raw = None
         if gate is not None:
             from ..gates import kda_gate
             g_raw, g = g, kda_gate(g, A_log, dt_bias, gate[0], native=True)
+        if beta_act is not None:
+            from ..gates import beta_sigmoid
+            beta = beta_sigmoid(beta, beta_act, native=True)
         if backend == "optimized" and q.is_cuda:
             from ..hip_forward import chunk_forward_hip
             o, final, sv = chunk_forward_hip(op, q, k, v, g=g, beta=beta, b=b, w=w,
@@ -74,6 +86,7 @@ class ChunkFunction(torch.autograd.Function):
         if ctx.backend == "optimized":
             from ..backends import backward as bw
             cu = ctx.cu_seqlens
+            bsig = ctx.beta_act or 0.0
             if op == "kda":
                 gate_kw = {} if ctx.gate is None else dict(
                     use_gate_in_kernel=True, g_org=g_raw, A_log=A_log, lower_bound=ctx.gate[0],
@@ -81,7 +94,7 @@ class ChunkFunction(torch.autograd.Function):
                 dq, dk, dv, db, dg, dh0, dA_log, ddt_bias = bw.kda_backward(
                     q=q, k=k, v=v, beta=beta, Aqk=Aqk, Akk=Akk, scale=scale, initial_state=h0,
                     do=do, dht=dht, g=gc, w=w_wy, u=u_wy, qg=qg, kg=kg, v_new=v_new, h=h, cu_seqlens=cu,
-                    **gate_kw)
+                    beta_sigmoid=bsig, **gate_kw)
                 dw = None
             elif op == "gdn2":
                 dq, dk, dv, db, dw, dg, dh0, _, _ = bw.gdn2_backward(
@@ -91,12 +104,12 @@ class ChunkFunction(torch.autograd.Function):
             elif op == "gdn":
                 dq, dk, dv, db, dg, dh0, _, _ = bw.gdn_backward(
                     q=q, k=k, v=v, g=gc, beta=beta, A=Akk, scale=scale, initial_state=h0, do=do, dht=dht,
-                    cu_seqlens=cu)
+                    cu_seqlens=cu, beta_sigmoid=bsig)
                 dw = None
             else:
                 dq, dk, dv, db, dh0 = bw.delta_backward(
                     q=q, k=k, v=v, beta=beta, A=Akk, scale=scale, initial_state=h0, do=do, dht=dht,
-                    cu_seqlens=cu)
+                    cu_seqlens=cu, beta_sigmoid=bsig)
                 dg = dw = None
         else:
             from ..original import original_backward
@@ -109,11 +122,12 @@ class ChunkFunction(torch.autograd.Function):
         if not ctx.has_h0:
             dh0 = None
         cast = lambda x, ref: None if x is None or ref is None else x.to(ref.dtype)
-        gb = cast(db, b if op == "gdn2" else beta)
+        gb = cast(db, b) if op == "gdn2" else (None if db is None else db.to(ctx.beta_dtype))
         return (None, None, None, None, None, cast(dq, q), cast(dk, k), cast(dv, v),
                 None if dg is None else dg.to(ctx.g_dtype),
                 None if op == "gdn2" else gb, gb if op == "gdn2" else None, cast(dw, w), dh0, None, None,
-                cast(dA_log, A_log), None if ddt_bias is None else ddt_bias.reshape(dt_bias.shape).to(dt_bias.dtype))
+                cast(dA_log, A_log), None if ddt_bias is None else ddt_bias.reshape(dt_bias.shape).to(dt_bias.dtype),
+                None)
 
 
 def _unsupported(name, **flags):
@@ -203,7 +217,7 @@ def _pack_aligned(x, bounds, starts, Tp):
 
 
 def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0,
-           state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None, gate_fold=None):
+           state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None, gate_fold=None, beta_act=None):
     """Layout adapters around the chunk Function (all autograd-transparent torch ops):
 
     * grouped value heads (HV = v.shape[2] > H): q and k are repeated over each
@@ -215,8 +229,35 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
       sum of the lengths); otherwise each is padded to the longest one and run as
       one batch row.  Zero keys, values and log-gates leave the state untouched, so
       outputs, final states and gradients of the real tokens are exact; padded
-      positions are dropped."""
+      positions are dropped.
+
+    ``gate_fold`` = (lower_bound, A_log, dt_bias) (KDA's raw gate) and ``beta_act`` = s
+    (raw beta, activated as s * sigmoid): on the optimized backend on a GPU, for
+    batches that need no padded tokens, the activations run inside the chunk Function
+    and their backward rides in the chunk kernel; otherwise they run here as autograd
+    nodes of their own (padded tokens must keep zero activated gates)."""
     H, HV = q.shape[2], v.shape[2]
+    native = backend == "optimized" and q.is_cuda
+    bounds = aligned = None
+    if cu_seqlens is not None:
+        if q.shape[0] != 1:
+            raise ValueError(f"The batch size is expected to be 1 rather than {q.shape[0]} when using `cu_seqlens`.")
+        cu = (cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens).tolist()
+        bounds = list(zip(cu[:-1], cu[1:]))
+        if h0 is not None and h0.shape[0] != len(bounds):
+            raise ValueError(f"The number of initial states is expected to be equal to the number of input "
+                             f"sequences, i.e., {len(bounds)} rather than {h0.shape[0]}.")
+        aligned = all(s % 64 == 0 for s, e in bounds) and cu[-1] % 64 == 0
+    unpadded = native and (aligned if cu_seqlens is not None else q.shape[1] % 64 == 0)
+    if gate_fold is not None and not unpadded:
+        from ..gates import KDAGate
+        lb, A_log, dt_bias = gate_fold
+        g = KDAGate.apply(g, A_log, dt_bias, lb, native)
+        gate_fold = None
+    if beta_act is not None and not unpadded:
+        from ..gates import beta_sigmoid
+        beta = beta_sigmoid(beta, beta_act, native=False)
+        beta_act = None
     if HV != H:
         if HV % H:
             raise ValueError(f"num_v_heads (HV={HV}) must be divisible by num_qk_heads (H={H})")
@@ -226,38 +267,29 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
             b = b.repeat_interleave(HV // H, dim=2)
     if state_v_first and h0 is not None:
         h0 = h0.transpose(-1, -2)
-    if gate_fold is not None:
-        # raw gate, no padded tokens (checked by the caller): the activation runs inside
-        lb, A_log, dt_bias = gate_fold
-        o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b,
-                                       w, h0, None, (lb,), A_log, dt_bias)
-    elif cu_seqlens is None:
-        o, final = _run(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0)
-    else:
-        if q.shape[0] != 1:
-            raise ValueError(f"The batch size is expected to be 1 rather than {q.shape[0]} when using `cu_seqlens`.")
-        cu = (cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens).tolist()
-        bounds = list(zip(cu[:-1], cu[1:]))
-        if h0 is not None and h0.shape[0] != len(bounds):
-            raise ValueError(f"The number of initial states is expected to be equal to the number of input "
-                             f"sequences, i.e., {len(bounds)} rather than {h0.shape[0]}.")
-        aligned = all(s % 64 == 0 for s, e in bounds) and cu[-1] % 64 == 0
-        if backend == "optimized" and q.is_cuda and aligned:
-            # already on chunk boundaries: the kernels take the batch as it is
-            o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta,
-                                           b, w, h0, torch.tensor(cu, dtype=torch.int64))
-        elif backend == "optimized" and q.is_cuda:
-            lens = [max(64, -(-(e - s) // 64) * 64) for s, e in bounds]
-            cu_al = torch.tensor([0] + lens, dtype=torch.int64).cumsum(0)
-            starts = cu_al[:-1].tolist()
-            xs = [_pack_aligned(x, bounds, starts, int(cu_al[-1])) for x in (q, k, v, g, beta, b, w)]
-            o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, *xs, h0, cu_al)
-            o = _UnpackAligned.apply(o, bounds, starts)
+    fold = (None, None, None) if gate_fold is None else ((gate_fold[0],), gate_fold[1], gate_fold[2])
+    if cu_seqlens is None:
+        if unpadded:
+            o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b,
+                                           w, h0, None, *fold, beta_act)
         else:
-            Tp = max(64, -(-max(e - s for s, e in bounds) // 64) * 64)
-            xs = [_unpack(x, bounds, Tp) for x in (q, k, v, g, beta, b, w)]
-            o, final = _run(op, backend, full_saving, scale, output_final_state, *xs, h0)
-            o = torch.cat([o[i:i + 1, :e - s] for i, (s, e) in enumerate(bounds)], 1)
+            o, final = _run(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0)
+    elif unpadded:
+        # already on chunk boundaries: the kernels take the batch as it is
+        o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta,
+                                       b, w, h0, torch.tensor(cu, dtype=torch.int64), *fold, beta_act)
+    elif native:
+        lens = [max(64, -(-(e - s) // 64) * 64) for s, e in bounds]
+        cu_al = torch.tensor([0] + lens, dtype=torch.int64).cumsum(0)
+        starts = cu_al[:-1].tolist()
+        xs = [_pack_aligned(x, bounds, starts, int(cu_al[-1])) for x in (q, k, v, g, beta, b, w)]
+        o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, *xs, h0, cu_al)
+        o = _UnpackAligned.apply(o, bounds, starts)
+    else:
+        Tp = max(64, -(-max(e - s for s, e in bounds) // 64) * 64)
+        xs = [_unpack(x, bounds, Tp) for x in (q, k, v, g, beta, b, w)]
+        o, final = _run(op, backend, full_saving, scale, output_final_state, *xs, h0)
+        o = torch.cat([o[i:i + 1, :e - s] for i, (s, e) in enumerate(bounds)], 1)
     if state_v_first and final is not None:
         final = final.transpose(-1, -2)
     return o, final
@@ -297,25 +329,24 @@ def make_kda(backend):
         assert beta.shape == (B, T, HV), f"beta must have shape [B, T, HV]={[B, T, HV]}, got {list(beta.shape)}"
         if use_qk_l2norm_in_kernel:
             q, k = _l2norm(q, backend), _l2norm(k, backend)
-        if use_beta_sigmoid_in_kernel:
-            beta = beta.sigmoid() * (2.0 if allow_neg_eigval else 1.0)
+        beta_act = (2.0 if allow_neg_eigval else 1.0) if use_beta_sigmoid_in_kernel else None
+        if beta_act is not None and backend != "optimized":
+            beta, beta_act = beta.sigmoid() * beta_act, None
         fold = None
         if use_gate_in_kernel:
-            if backend == "optimized" and g.is_cuda and cu_seqlens is None and T % 64 == 0:
-                # no padded tokens: the activation runs inside the chunk Function and its
-                # backward (dg_raw, dA_log, ddt_bias) rides in the chunk kernel
+            if backend == "optimized":
+                # the activation runs inside the chunk Function where no token is padded,
+                # its backward (dg_raw, dA_log, ddt_bias) riding in the chunk kernel
                 fold = (lower_bound, A_log, dt_bias)
             else:
-                # the fused activation as its own autograd node (padded tokens must keep a
-                # zero activated gate): g's gradient flows to g_raw, A_log and dt_bias
+                # the fused activation as its own autograd node: g's gradient flows to
+                # g_raw, A_log and dt_bias (torch expressions)
                 from ..gates import KDAGate
-                # the optimized backend runs the activation's HIP kernels on a GPU, the
-                # original backend the torch expressions
-                g = KDAGate.apply(g, A_log, dt_bias, lower_bound, backend == "optimized" and g.is_cuda)
+                g = KDAGate.apply(g, A_log, dt_bias, lower_bound, False)
         scale = K ** -0.5 if scale is None else scale
         return _apply("kda", backend, disable_recompute, scale, output_final_state, q, k, v, g, beta,
                       None, None, initial_state, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
-                      cu_seqlens_cpu=cu_seqlens_cpu, gate_fold=fold)
+                      cu_seqlens_cpu=cu_seqlens_cpu, gate_fold=fold, beta_act=beta_act)
     return chunk_kda
 
 
@@ -338,12 +369,13 @@ def make_gdn(backend):
         assert g.shape == (B, T, HV), f"g must have shape [B, T, HV], got {list(g.shape)}"
         if use_qk_l2norm_in_kernel:
             q, k = _l2norm(q, backend), _l2norm(k, backend)
-        if use_beta_sigmoid_in_kernel:
-            beta = beta.sigmoid() * (2.0 if allow_neg_eigval else 1.0)
+        beta_act = (2.0 if allow_neg_eigval else 1.0) if use_beta_sigmoid_in_kernel else None
+        if beta_act is not None and backend != "optimized":
+            beta, beta_act = beta.sigmoid() * beta_act, None
         scale = K ** -0.5 if scale is None else scale
         return _apply("gdn", backend, False, scale, output_final_state, q, k, v, g, beta, None, None,
                       initial_state, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
-                      cu_seqlens_cpu=cu_seqlens_cpu)
+                      cu_seqlens_cpu=cu_seqlens_cpu, beta_act=beta_act)
     return chunk_gated_delta_rule
 
 

@@ -17,7 +17,7 @@ _I = ctypes.c_int
 _F = ctypes.c_float
 SIGNATURES = {
     "fdr_state_bwd": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P],
-    "fdr_chunk_bwd": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+    "fdr_chunk_bwd": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P,
                       _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_prepare_wu": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_fwd_h": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
@@ -33,9 +33,10 @@ SIGNATURES = {
                              _F, _P],
     "fdr_kda_gate_fwd": [_P, _I, _P, _P, _I, _F, _P, _I, _I, _I, _I, _P],
     "fdr_kda_gate_bwd": [_P, _P, _I, _P, _P, _I, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "fdr_beta_sigmoid_fwd": [_P, _I, _F, _P, ctypes.c_longlong, _P],
     "fdr_l2norm_fwd": [_P, _I, _P, _P, ctypes.c_longlong, _I, _F, _P],
     "fdr_l2norm_bwd": [_P, _I, _P, _P, _P, ctypes.c_longlong, _I, _P],
-    "fdr_chunk_bwd_gate_fold": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _F,
+    "fdr_chunk_bwd_gate_fold": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _P, _P, _I, _F,
                                 _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_affine_scan": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
     "fdr_affine_side": [_P, _I, _I, _I, _I, _I, _I, _I, _P],

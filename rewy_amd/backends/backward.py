@@ -78,8 +78,9 @@ def _f32(x):
     return None if x is None else x.to(torch.float32).contiguous()
 
 
-def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, saved, gate_fold=None, **kw):
-    """Shared vector-gate (KDA / GDN2) backward.  ``gate_fold``: see ops.chunk_bwd."""
+def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, saved, gate_fold=None,
+            beta_sigmoid=0.0, **kw):
+    """Shared vector-gate (KDA / GDN2) backward.  ``gate_fold``, ``beta_sigmoid``: see ops.chunk_bwd."""
     _check_common(op, kw)
     co = _varlen(q, kw)
     q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
@@ -99,7 +100,8 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     out = ops.chunk_bwd(q, k, v, _bf(saved["v_new"]), do, dR, g, ops.GATE_VECTOR, Akk,
                         _bf(saved["h"]), dh, scale, beta=_f32(gates.get("beta")),
                         b=None if gates.get("b") is None else _bf(gates["b"]),
-                        w=None if gates.get("w") is None else _bf(gates["w"]), gate_fold=gate_fold)
+                        w=None if gates.get("w") is None else _bf(gates["w"]), gate_fold=gate_fold,
+                        beta_sigmoid=beta_sigmoid)
     return out, dh0
 
 
@@ -128,8 +130,12 @@ def kda_backward(q, k, v, beta, Aqk, Akk, scale, initial_state, do, dht, g, g_or
                  state_v_first=False, cu_seqlens=None, chunk_indices=None, chunk_size=64,
                  safe_gate=False, lower_bound=None, use_gate_in_kernel=False, A_log=None,
                  dt_bias=None, disable_recompute=False, cp_context=None, w=None, u=None, qg=None,
-                 kg=None, v_new=None, h=None, use_graph=False, chunk_offsets=None):
-    """KDA backward -> (dq, dk, dv, db, dg, dh0, dA_log, ddt_bias)."""
+                 kg=None, v_new=None, h=None, use_graph=False, chunk_offsets=None, beta_sigmoid=0.0):
+    """KDA backward -> (dq, dk, dv, db, dg, dh0, dA_log, ddt_bias).
+
+    ``beta_sigmoid`` (this build's addition, default off): s > 0 when ``beta`` is
+    s * sigmoid(beta_raw) activated in the forward; db is then dL/dbeta_raw, the fused
+    beta-sigmoid backward of reference _compat/kda.py:204-205 done in the chunk kernel."""
     from ..runtime import record
     saved = dict(w=w, u=u, qg=qg, kg=kg, v_new=v_new, h=h)
     # the in-kernel gate's backward rides in the chunk kernel's dg stores (one pass fewer
@@ -137,7 +143,7 @@ def kda_backward(q, k, v, beta, Aqk, Akk, scale, initial_state, do, dht, g, g_or
     fold = (dict(g_raw=g_org, A_log=A_log, dt_bias=dt_bias, lower_bound=lower_bound)
             if use_gate_in_kernel else None)
     out, dh0 = _vector("kda", q, k, v, dict(beta=beta), Aqk, Akk, scale, initial_state, do, dht, g,
-                       saved, gate_fold=fold, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
+                       saved, gate_fold=fold, beta_sigmoid=beta_sigmoid, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
                        chunk_indices=chunk_indices, chunk_size=chunk_size, safe_gate=safe_gate,
                        use_gate_in_kernel=use_gate_in_kernel, cp_context=cp_context,
                        use_graph=use_graph, chunk_offsets=chunk_offsets)
@@ -162,7 +168,7 @@ def gdn2_backward(q, k, v, b, w_gate, Aqk, Akk, scale, initial_state, do, dht, g
     return out["dq"], out["dk"], out["dv"], out["db"], out["dw"], out["dg"], dh0, None, None
 
 
-def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, **kw):
+def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid=0.0, **kw):
     """GDN / DeltaNet: recompute w, u, h, v_new, then the state and chunk kernels
     (reference ``_scalar``, backends/backward.py:96-131)."""
     from ..runtime import record
@@ -184,7 +190,7 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, **kw):
                                 chunk_offsets=co)
         dh, dR, dh0 = ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
                                     want_dh0=initial_state is not None, method="direct", chunk_offsets=co)
-    out = ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta)
+    out = ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta, beta_sigmoid=beta_sigmoid)
     record(op, "optimized_backward")
     return out, dh0
 

@@ -244,7 +244,8 @@ __device__ __forceinline__ void chunk_body(
     bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale,
     const float* __restrict__ daqk, float* __restrict__ dq32, float* __restrict__ dk32,
     float* __restrict__ db32, int beta_complete, int item, int next_item, char* regA, char* regB,
-    float* small, bf16* xbuf, float* gbuf, PhaseIn& pin, const GateFoldArgs* gf = nullptr) {
+    float* small, bf16* xbuf, float* gbuf, PhaseIn& pin, const GateFoldArgs* gf = nullptr,
+    float beta_sig = 0.f) {
   using LY = PostLayout<GATE, VEC_B, INTRA, PIPE>;
   using post::LDT;
   auto B16 = [&](int off) { return reinterpret_cast<bf16*>(regA + off); };
@@ -1059,7 +1060,11 @@ __device__ __forceinline__ void chunk_body(
     if constexpr (!VEC_B) {
       const float be = sBeta[tid];
       const float pr = (sDbA[tid] + sDbA[64 + tid]) + (sDbA[128 + tid] + sDbA[192 + tid]);
-      dbeta_out[row] = fabsf(be) < 1e-6f ? sDbB[tid] : pr / be;
+      float db = fabsf(be) < 1e-6f ? sDbB[tid] : pr / be;
+      // beta = s sigmoid(x) activated in the forward (use_beta_sigmoid_in_kernel):
+      // dL/dx = dL/dbeta * s sigmoid (1 - sigmoid) = dL/dbeta * beta (1 - beta / s)
+      if (beta_sig > 0.f) db *= be * (1.f - be / beta_sig);
+      dbeta_out[row] = db;
     }
     if constexpr (GATE == CG_SCALAR) {
       // row sums over the 8 waves' partials, then the reverse cumsum over the
@@ -1088,14 +1093,15 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     const bf16* __restrict__ wgate, const float* __restrict__ akk, const bf16* __restrict__ hst,
     const bf16* __restrict__ dhst, bf16* __restrict__ dq_out, bf16* __restrict__ dk_out,
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
-    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale) {
+    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale, float beta_sig) {
   using LY = PostLayout<GATE, VEC_B>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
   chunk_body<GATE, VEC_B, false>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
                                  dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale, nullptr,
                                  nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
-                                 reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin);
+                                 reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
+                                 nullptr, beta_sig);
 }
 
 // KDA with the gate backward folded into the dg stores (no dg output)
@@ -1106,7 +1112,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_fold_kernel(
     const float* __restrict__ g, const float* __restrict__ beta, const float* __restrict__ akk,
     const bf16* __restrict__ hst, const bf16* __restrict__ dhst, bf16* __restrict__ dq_out,
     bf16* __restrict__ dk_out, bf16* __restrict__ dv_out, float* __restrict__ dbeta_out, int T, int H,
-    float scale, GateFoldArgs gf) {
+    float scale, GateFoldArgs gf, float beta_sig) {
   using LY = PostLayout<CG_VECTOR, false>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
@@ -1114,7 +1120,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_fold_kernel(
       q, k, v, vnew, dO, dR, g, beta, nullptr, nullptr, akk, hst, dhst, dq_out, dk_out, dv_out, nullptr, dbeta_out,
       nullptr, nullptr, T, H, scale, nullptr, nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem,
       smem + LY::REGION_A, reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
-      &gf);
+      &gf, beta_sig);
 }
 
 // Persistent form: one work-group per CU walks the items blockIdx.x, + gridDim.x, ...
@@ -1132,7 +1138,8 @@ __global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
     const bf16* __restrict__ wgate, const float* __restrict__ akk, const bf16* __restrict__ hst,
     const bf16* __restrict__ dhst, bf16* __restrict__ dq_out, bf16* __restrict__ dk_out,
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
-    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale, int items) {
+    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale, int items,
+    float beta_sig) {
   using LY = PostLayout<GATE, VEC_B, false, true>;
   __shared__ __attribute__((aligned(16))) bf16 xbuf[3 * C * KD];
   __shared__ __attribute__((aligned(16))) char regA[LY::REGION_A];
@@ -1156,7 +1163,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
     chunk_body<GATE, VEC_B, false, true>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
                                          dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale,
                                          nullptr, nullptr, nullptr, nullptr, 0, it, nx < items ? nx : -1, regA,
-                                         regB, small, xbuf, gbuf, pin);
+                                         regB, small, xbuf, gbuf, pin, nullptr, beta_sig);
   }
 }
 
@@ -1215,7 +1222,8 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
                               const void* dO, const void* dR, const float* g, const float* beta,
                               const void* bgate, const void* wgate, const float* akk, const void* h,
                               const void* dh, void* dq, void* dk, void* dv, float* dg, float* dbeta,
-                              void* db, void* dw, int B, int T, int H, float scale, hipStream_t s) {
+                              void* db, void* dw, int B, int T, int H, float scale, float beta_sig,
+                              hipStream_t s) {
   const int items = B * H * (T / C);
   using LP = PostLayout<GATE, VEC_B, false, true>;
   // persistent form for scalar / no gate (measured slower for KDA: see the kernel)
@@ -1228,7 +1236,8 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
     hipLaunchKernelGGL(kern, dim3(grid), dim3(512), 0, s, (const bf16*)q, (const bf16*)k,
                        (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta,
                        (const bf16*)bgate, (const bf16*)wgate, akk, (const bf16*)h, (const bf16*)dh,
-                       (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, items);
+                       (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, items,
+                       beta_sig);
     return hipGetLastError();
   }
   using LY = PostLayout<GATE, VEC_B>;
@@ -1240,7 +1249,7 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
   hipLaunchKernelGGL(kern, dim3(grid), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta,
                      (const bf16*)bgate, (const bf16*)wgate, akk, (const bf16*)h, (const bf16*)dh,
-                     (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale);
+                     (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, beta_sig);
   return hipGetLastError();
 }
 
@@ -1252,11 +1261,12 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
                                     const void* dO, const void* dR, const float* g, int gate_mode,
                                     const float* beta, const void* b_gate, const void* w_gate,
                                     const float* Akk, const void* h, const void* dh, void* dq,
-                                    void* dk, void* dv, float* dg, float* dbeta, void* db, void* dw,
-                                    int B, int T, int H, int K, int V, int chunk, float scale,
-                                    hipStream_t stream) {
+                                    void* dk, void* dv, float* dg, float* dbeta, float beta_sigmoid,
+                                    void* db, void* dw, int B, int T, int H, int K, int V, int chunk,
+                                    float scale, hipStream_t stream) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0)
     return hipErrorInvalidValue;
+  if (!(beta_sigmoid >= 0.f) || (beta_sigmoid > 0.f && b_gate)) return hipErrorInvalidValue;
   if (!q || !k || !v || !v_new || !dO || !dR || !Akk || !h || !dh || !dq || !dk || !dv)
     return hipErrorInvalidValue;
   const bool vec_b = b_gate != nullptr;
@@ -1266,7 +1276,7 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
   if (vec_b && gate_mode != CG_VECTOR) return hipErrorInvalidValue;
 #define FDR_POST(G, VB)                                                                          \
   return launch_post<G, VB>(q, k, v, v_new, dO, dR, g, beta, b_gate, w_gate, Akk, h, dh, dq, dk, \
-                            dv, dg, dbeta, db, dw, B, T, H, scale, stream)
+                            dv, dg, dbeta, db, dw, B, T, H, scale, beta_sigmoid, stream)
   if (vec_b) { FDR_POST(CG_VECTOR, true); }
   switch (gate_mode) {
     case CG_NONE: FDR_POST(CG_NONE, false);
@@ -1289,21 +1299,22 @@ extern "C" size_t fdr_chunk_bwd_gate_workspace_bytes(int B, int T, int H) {
   return nblk * ((size_t)H * KD + 8 * (size_t)H) * sizeof(float);
 }
 
-extern "C" hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, const void* v, const void* v_new,
-                                              const void* dO, const void* dR, const float* g, const float* beta,
-                                              const float* Akk, const void* h, const void* dh, void* dq, void* dk,
-                                              void* dv, float* dbeta, const void* g_raw, int raw_is_bf16,
-                                              const float* A_log, const float* dt_bias, int has_lower_bound,
-                                              float lower_bound, void* dg_raw, float* dA_log, float* ddt_bias,
-                                              void* workspace, int B, int T, int H, int K, int V, int chunk,
-                                              float scale, hipStream_t stream) {
+static hipError_t gate_fold_launch(const void* q, const void* k, const void* v, const void* v_new, const void* dO,
+                                   const void* dR, const float* g, const float* beta, const float* Akk, const void* h,
+                                   const void* dh, void* dq, void* dk, void* dv, float* dbeta, float beta_sigmoid,
+                                   const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
+                                   int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
+                                   float* ddt_bias, void* workspace, int B, int T, int H, int K, int V, int chunk,
+                                   float scale, hipStream_t stream) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
   if (!q || !k || !v || !v_new || !dO || !dR || !g || !beta || !Akk || !h || !dh || !dq || !dk || !dv || !dbeta)
     return hipErrorInvalidValue;
-  if (!g_raw || !dg_raw || !workspace) return hipErrorInvalidValue;
+  if (!g_raw || !dg_raw || !workspace || !(beta_sigmoid >= 0.f)) return hipErrorInvalidValue;
   const int mode = !has_lower_bound ? (A_log ? 0 : -1) : (A_log ? 1 : 2);
   if (mode < 0) return hipErrorInvalidValue;
   const int nblk = B * (T / C);
+  // every partial below is written by the chunk kernel before the column sums read it:
+  // the workspace needs no clearing
   float* part_dt = reinterpret_cast<float*>(workspace);
   float* part_da = part_dt + (size_t)nblk * H * KD;
   const GateFoldArgs gf{g_raw, A_log, dt_bias, lower_bound, dg_raw, part_dt, part_da};
@@ -1318,10 +1329,24 @@ extern "C" hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, cons
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, stream, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, (const bf16*)v_new, (const bf16*)dO, (const bf16*)dR, g, beta, Akk,
-                     (const bf16*)h, (const bf16*)dh, (bf16*)dq, (bf16*)dk, (bf16*)dv, dbeta, T, H, scale, gf);
+                     (const bf16*)h, (const bf16*)dh, (bf16*)dq, (bf16*)dk, (bf16*)dv, dbeta, T, H, scale, gf,
+                     beta_sigmoid);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   return kda_gate_partials_sum(part_dt, part_da, nblk, H * KD, 8, ddt_bias, dA_log, stream);
+}
+
+extern "C" hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, const void* v, const void* v_new,
+                                              const void* dO, const void* dR, const float* g, const float* beta,
+                                              const float* Akk, const void* h, const void* dh, void* dq, void* dk,
+                                              void* dv, float* dbeta, float beta_sigmoid, const void* g_raw,
+                                              int raw_is_bf16, const float* A_log, const float* dt_bias,
+                                              int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
+                                              float* ddt_bias, void* workspace, int B, int T, int H, int K, int V,
+                                              int chunk, float scale, hipStream_t stream) {
+  return gate_fold_launch(q, k, v, v_new, dO, dR, g, beta, Akk, h, dh, dq, dk, dv, dbeta, beta_sigmoid, g_raw,
+                          raw_is_bf16, A_log, dt_bias, has_lower_bound, lower_bound, dg_raw, dA_log, ddt_bias,
+                          workspace, B, T, H, K, V, chunk, scale, stream);
 }
 
 template <bool VEC_B>
@@ -1349,3 +1374,4 @@ extern "C" hipError_t fdr_matrix_intra(const void* q, const void* k, const float
   if (!beta) return hipErrorInvalidValue;
   return launch_intra<false>(q, k, g, beta, nullptr, dAqk, dAkk, dq, dk, db, dg, B, T, H, beta_complete, stream);
 }
+

@@ -262,3 +262,28 @@ extern "C" hipError_t fdr_kda_gate_bwd(const float* dg, const void* g_raw, int r
   if (e != hipSuccess) return e;
   return kda_gate_partials_sum(part_dt, part_da, nblk, HK, 1, ddt_bias, dA_log, stream);
 }
+
+namespace rewy {
+// beta = s sigmoid(x) per token and head (use_beta_sigmoid_in_kernel); its backward
+// is folded into the chunk kernel's dbeta stores (fdr_chunk_bwd's beta_sigmoid)
+template <bool BF16_IN>
+__global__ __launch_bounds__(256) void beta_sigmoid_kernel(const void* __restrict__ x, float s,
+                                                           float* __restrict__ beta, long long n) {
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
+    const float xv = BF16_IN ? to_f32(reinterpret_cast<const bf16*>(x)[i]) : reinterpret_cast<const float*>(x)[i];
+    beta[i] = s * sigmoid_y(exp_f(xv));
+  }
+}
+}  // namespace rewy
+
+extern "C" hipError_t fdr_beta_sigmoid_fwd(const void* x, int is_bf16, float scale, float* beta, long long n,
+                                           hipStream_t stream) {
+  if (n <= 0 || !x || !beta || !(scale > 0.f)) return hipErrorInvalidValue;
+  const long long blocks = (n + 255) / 256;
+  const int grid = (int)(blocks < 8192 ? blocks : 8192);
+  if (is_bf16)
+    hipLaunchKernelGGL(beta_sigmoid_kernel<true>, dim3(grid), dim3(256), 0, stream, x, scale, beta, n);
+  else
+    hipLaunchKernelGGL(beta_sigmoid_kernel<false>, dim3(grid), dim3(256), 0, stream, x, scale, beta, n);
+  return hipGetLastError();
+}

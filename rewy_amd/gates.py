@@ -138,3 +138,22 @@ class KDAGate(torch.autograd.Function):
         g_raw, A_log, dt_bias = ctx.saved_tensors
         dx, dA, ddt = kda_gate_bwd(dg, g_raw, A_log, dt_bias, ctx.lower_bound, ctx.native)
         return dx, dA, ddt, None, None
+
+
+def beta_sigmoid(beta_raw, scale=1.0, native=None):
+    """beta = scale * sigmoid(beta_raw), fp32 (``use_beta_sigmoid_in_kernel``; scale 2 with
+    ``allow_neg_eigval``).  ``native`` (default: on a GPU) runs ``fdr_beta_sigmoid_fwd``;
+    the backward of the native path is folded into the chunk kernel (ops.chunk_bwd's
+    ``beta_sigmoid``)."""
+    if not _native(beta_raw, native):
+        return torch.sigmoid(beta_raw.float()) * scale
+    from . import _lib
+    x = beta_raw if beta_raw.dtype in (torch.float32, torch.bfloat16) else beta_raw.float()
+    x = x.contiguous()
+    out = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    if x.numel() == 0:
+        return out
+    st = _lib.load().fdr_beta_sigmoid_fwd(_lib.ptr(x), int(x.dtype == torch.bfloat16), float(scale), _lib.ptr(out),
+                                          x.numel(), _lib.stream_handle(x.device))
+    _lib.check(st, "fdr_beta_sigmoid_fwd")
+    return out

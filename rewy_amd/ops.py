@@ -224,12 +224,15 @@ def recurrences(q, k, w, u, g, gate_mode, dO, scale, aqk=None, dv=None, h0=None,
 
 
 def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None, b=None, w=None,
-              gate_fold=None):
+              gate_fold=None, beta_sigmoid=0.0):
     """Fused residual-WY + matrix-intra + epilogue stage.
 
     ``gate_fold`` (KDA only) = dict(g_raw, A_log, dt_bias, lower_bound): the in-kernel gate's
     backward is applied where dg is formed; ``dg`` is then dL/dg_raw (g_raw's dtype) and the
     result also holds ``dA_log`` / ``ddt_bias`` (fp32, or None).
+
+    ``beta_sigmoid`` = s > 0 (scalar beta): beta was activated as s * sigmoid(x) in the
+    forward, and ``dbeta`` is returned as dL/dx (the reference's fused beta-sigmoid backward).
 
     Returns dict(dq, dk, dv [bf16], dg [fp32, gate shape] | None, dbeta [fp32] | None,
     db, dw [bf16] | None)."""
@@ -259,8 +262,12 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
         _need(g, "g", f32, (B, T, H), dev)
     elif gate_mode != GATE_NONE:
         raise ValueError("gate_mode must be 0, 1 or 2")
+    beta_sigmoid = float(beta_sigmoid or 0.0)
+    if beta_sigmoid < 0 or (beta_sigmoid and vec_b):
+        raise ValueError("beta_sigmoid is a non-negative scale of a scalar beta")
     if gate_fold is not None:
-        return _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, gate_fold)
+        return _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, gate_fold,
+                                    beta_sigmoid)
     out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=bf),
                dk=torch.empty(B, T, H, K, device=dev, dtype=bf),
                dv=torch.empty(B, T, H, V, device=dev, dtype=bf),
@@ -271,14 +278,14 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
     P = _lib.ptr
     st = _lib.load().fdr_chunk_bwd(P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), int(gate_mode),
                                    P(beta), P(b), P(w), P(Akk), P(h), P(dh), P(out["dq"]),
-                                   P(out["dk"]), P(out["dv"]), P(out["dg"]), P(out["dbeta"]),
+                                   P(out["dk"]), P(out["dv"]), P(out["dg"]), P(out["dbeta"]), beta_sigmoid,
                                    P(out["db"]), P(out["dw"]), B, T, H, K, V, CHUNK, float(scale),
                                    _lib.stream_handle(dev))
     _lib.check(st, "fdr_chunk_bwd")
     return out
 
 
-def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, fold):
+def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, fold, beta_sigmoid=0.0):
     """chunk_bwd (KDA) with the gate backward folded into the dg stores."""
     B, T, H, K = q.shape
     V = V_SUPPORTED
@@ -305,7 +312,7 @@ def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale
     ws = torch.empty(max(1, lib.fdr_chunk_bwd_gate_workspace_bytes(B, T, H) // 4), device=dev, dtype=f32)
     P = _lib.ptr
     st = lib.fdr_chunk_bwd_gate_fold(P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), P(beta), P(Akk), P(h), P(dh),
-                                     P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), P(raw),
+                                     P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), beta_sigmoid, P(raw),
                                      int(raw.dtype == bf), P(a), P(dt), int(lb is not None),
                                      0.0 if lb is None else float(lb), P(out["dg"]), P(out["dA_log"]),
                                      P(out["ddt_bias"]), P(ws), B, T, H, K, V, CHUNK, float(scale),
