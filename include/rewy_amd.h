@@ -219,6 +219,29 @@ hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, const void* v, 
                                    float scale, hipStream_t stream);
 
 /*
+ * fdr_chunk_bwd_gate_fold without the workspace argument.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops or harnesses that forbid hipMalloc).  The per-chunk
+ * partial sums go to a fixed device array inside the library, FDR_NOALLOC_SCRATCH_BYTES
+ * (16 MiB) per GPU, held until the process ends; a problem whose
+ * fdr_chunk_bwd_gate_workspace_bytes(B, T, H) exceeds it is refused with
+ * hipErrorInvalidValue before anything is enqueued.  The function itself calls no
+ * allocator.  All calls on one GPU share that GPU's array: calls that overlap on one
+ * GPU (concurrent streams or host threads) race.  Nothing in the array needs
+ * clearing between calls.
+ */
+#define FDR_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+hipError_t fdr_chunk_bwd_gate_fold_noalloc(const void* q, const void* k, const void* v, const void* v_new,
+                                           const void* dO, const void* dR, const float* g, const float* beta,
+                                           const float* Akk, const void* h, const void* dh, void* dq, void* dk,
+                                           void* dv, float* dbeta, float beta_sigmoid, const void* g_raw,
+                                           int raw_is_bf16, const float* A_log, const float* dt_bias,
+                                           int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
+                                           float* ddt_bias, int B, int T, int H, int K, int V, int chunk,
+                                           float scale, hipStream_t stream);
+
+/*
  * beta = scale * sigmoid(x) over n elements (use_beta_sigmoid_in_kernel; scale 2 with
  * allow_neg_eigval; reference _compat/kda.py:202-206, FLA fused_beta_sigmoid forward).
  * x fp32 (is_bf16 = 0) or bf16 (1); beta fp32.  The backward is fdr_chunk_bwd's

@@ -45,6 +45,7 @@
 // L/D tiles are produced by MFMAs whose accumulator layout stores contiguously
 // into the orientation the next contraction reads.
 #include "common.hpp"
+#include "rewy_amd.h"
 
 namespace rewy {
 
@@ -1375,3 +1376,54 @@ extern "C" hipError_t fdr_matrix_intra(const void* q, const void* k, const float
   return launch_intra<false>(q, k, g, beta, nullptr, dAqk, dAkk, dq, dk, db, dg, B, T, H, beta_complete, stream);
 }
 
+// ---------------------------------------------------------------------------
+// fdr_chunk_bwd_gate_fold without a workspace argument, for callers that cannot
+// allocate (code under HIP graph capture, serving loops that forbid hipMalloc):
+// the per-chunk partials live in a file-scope device array of fixed size that every
+// GPU the library runs on holds until the process ends.  Calls that overlap on one
+// GPU share it and race; nothing in it needs clearing (the chunk kernel writes every
+// partial before the column sums read it).
+// ---------------------------------------------------------------------------
+#include <mutex>
+
+static __device__ __align__(256) char scratch[FDR_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex scratch_mu;
+void* scratch_dev[rewy::kMaxDevices];   // the array's device address, per device
+
+// Device address of `scratch` on the current device, looked up once per device
+// (the array's host-side name is not a device address).
+hipError_t scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= rewy::kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    scratch_dev[dev] = p;
+  }
+  *out = scratch_dev[dev];
+  return hipSuccess;
+}
+}  // namespace
+
+extern "C" hipError_t fdr_chunk_bwd_gate_fold_noalloc(
+    const void* q, const void* k, const void* v, const void* v_new, const void* dO, const void* dR, const float* g,
+    const float* beta, const float* Akk, const void* h, const void* dh, void* dq, void* dk, void* dv, float* dbeta,
+    float beta_sigmoid, const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
+    int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log, float* ddt_bias, int B, int T, int H,
+    int K, int V, int chunk, float scale, hipStream_t stream) {
+  const size_t need = fdr_chunk_bwd_gate_workspace_bytes(B, T, H);
+  if (need == 0 || need > FDR_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
+  void* ws = nullptr;
+  const hipError_t e = scratch_ptr(&ws);
+  if (e != hipSuccess) return e;
+  return gate_fold_launch(q, k, v, v_new, dO, dR, g, beta, Akk, h, dh, dq, dk, dv, dbeta, beta_sigmoid, g_raw,
+                          raw_is_bf16, A_log, dt_bias, has_lower_bound, lower_bound, dg_raw, dA_log, ddt_bias, ws, B,
+                          T, H, K, V, chunk, scale, stream);
+}

@@ -1,0 +1,88 @@
+"""fdr_chunk_bwd_gate_fold_noalloc (no workspace argument: the per-chunk partials sit in
+the library's fixed device array) against fdr_chunk_bwd_gate_fold with a caller-allocated
+workspace, through the C-ABI.  Both launch the same kernels, so every output must be
+bit-identical; two calls in a row, the second on a smaller problem (the array keeps the
+first call's partials, which the second must not read), then a size beyond the array's
+limit is refused."""
+import pytest
+import torch
+
+from tests._inputs import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+HIP_ERROR_INVALID_VALUE = 1
+
+
+def _lib():
+    from rewy_amd import _lib as L
+    return L, L.load()
+
+
+def _case(B, T, H, seed):
+    from rewy_amd import ops
+    from rewy_amd.forward import chunk_forward
+    xs, dO = make_inputs("kda", B, T, H, seed=seed)
+    _, _, sv = chunk_forward("kda", xs["q"], xs["k"], xs["v"], g=xs["g"], beta=xs["beta"],
+                             initial_state=xs["initial_state"])
+    dev = torch.device("cuda")
+    cu = lambda x: x.to(dev).contiguous()
+    gen = torch.Generator().manual_seed(seed + 1)
+    g_raw = (torch.randn(B, T, H, 128, generator=gen) * 3).to(dev)
+    A = (torch.randn(H, generator=gen) * 0.5).to(dev)
+    dt = (torch.randn(H * 128, generator=gen) * 0.5).to(dev)
+    gc = cu(sv["gc"])
+    dh, dR, _ = ops.state_bwd(cu(sv["qg"]), cu(sv["kg"]), cu(sv["w"]), gc, ops.GATE_VECTOR, cu(dO), sv["scale"],
+                              aqk=cu(sv["Aqk"]))
+    ins = [cu(xs["q"]), cu(xs["k"]), cu(xs["v"]), cu(sv["v_new"]), cu(dO), dR, gc, cu(xs["beta"]), cu(sv["Akk"]),
+           cu(sv["h"]), dh]
+    return ins, g_raw, A, dt, sv["scale"]
+
+
+def _outs(B, T, H, dev):
+    e = lambda *s: torch.full(s, float("nan"), device=dev)
+    return dict(dq=e(B, T, H, 128).bfloat16(), dk=e(B, T, H, 128).bfloat16(), dv=e(B, T, H, 128).bfloat16(),
+                dbeta=e(B, T, H), dg=e(B, T, H, 128), dA=e(H), ddt=e(H * 128))
+
+
+def _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc):
+    B, T, H = shape
+    dev = g_raw.device
+    out = _outs(B, T, H, dev)
+    P = L.ptr
+    head = [P(x) for x in ins] + [P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), 0.0, P(g_raw), 0,
+                                  P(A), P(dt), 0, 0.0, P(out["dg"]), P(out["dA"]), P(out["ddt"])]
+    tail = [B, T, H, 128, 128, 64, float(scale), L.stream_handle(dev)]
+    if noalloc:
+        st = lib.fdr_chunk_bwd_gate_fold_noalloc(*head, *tail)
+    else:
+        ws = torch.empty(lib.fdr_chunk_bwd_gate_workspace_bytes(B, T, H) // 4, device=dev)
+        st = lib.fdr_chunk_bwd_gate_fold(*head, P(ws), *tail)
+    torch.cuda.synchronize()
+    return st, out
+
+
+def test_noalloc_matches_workspace_entry_point():
+    L, lib = _lib()
+    for shape, seed in (((2, 256, 4), 3), ((1, 128, 2), 8)):
+        print(f"\n[no-alloc] shape={shape} seed={seed}", flush=True)
+        ins, g_raw, A, dt, scale = _case(*shape, seed)
+        st_ref, ref = _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc=False)
+        st_got, got = _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc=True)
+        assert st_ref == 0 and st_got == 0, (st_ref, st_got)
+        for name in ref:
+            assert torch.isfinite(got[name].float()).all(), name
+            assert torch.equal(got[name], ref[name]), name
+
+
+def test_noalloc_rejects_sizes_beyond_its_array():
+    L, lib = _lib()
+    dev = torch.device("cuda")
+    # B * T/64 * (H*128 + 8 H) * 4 bytes = 35.7 MB > 16 MiB for B=16, T=16384, H=16
+    B, T, H = 16, 16384, 16
+    assert lib.fdr_chunk_bwd_gate_workspace_bytes(B, T, H) > (16 << 20)
+    dummy = torch.empty(16, device=dev)
+    p = L.ptr(dummy)
+    st = lib.fdr_chunk_bwd_gate_fold_noalloc(*([p] * 15), 0.0, p, 0, p, None, 0, 0.0, p, p, None,
+                                             B, T, H, 128, 128, 64, 1.0, L.stream_handle(dev))
+    assert st == HIP_ERROR_INVALID_VALUE
