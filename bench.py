@@ -12,7 +12,8 @@ Printed (one JSON line): backward ms per step, algorithmic TFLOP/s and its
 fraction of the bf16 MFMA peak, per-kernel HIP-event launch times, a roofline
 record for the dominant kernel (per-launch algorithmic bytes / launch time),
 the same-GPU time of the original 7-product formulation (PyTorch ops) and a
-CPU baseline (the fp64 oracle on a bounded sample, one thread).
+CPU baseline (the same original formulation as torch ops in fp32 on the host's
+granted threads, bounded sample; the fp64 oracle on one thread beside it).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config kda|gdn|gdn_cfg|gdn2|kda_long|delta|paper_delta_c2|paper_kda_c5]
     python bench.py --paper-grid      # the reference's published operator grid (one JSON line per family)
@@ -279,7 +280,61 @@ def measured_traffic(kernel, config):
         return None
 
 
-def cpu_baseline(xs, sv, dO, scale, NTt, nb_max=3):
+def cpu_baseline(xs, sv, dO, scale, NTt, round_s=0.5, rounds=15):
+    """The reference's CPU comparison point as SURVEY'd for the large configs: the original
+    (7-product) chunk backward as torch ops -- dAv, the reverse state recurrence, the
+    7-product local WY and the pairwise intra (``rewy_amd.original.original_backward``) --
+    in fp32 on the host, every thread the box grants (OMP_NUM_THREADS; the reference
+    pins torch.set_num_threads).  Sample: batch 0, the first Hs heads, all T=4096 tokens,
+    Hs chosen so that one round takes ~round_s; timing as the reference's benchmark.py:8-50
+    (synchronized wall clock per sample, warm-up >= 6 rounds and >= 2 s, median of
+    `rounds`), scaled linearly to the full workload's chunk-heads."""
+    import statistics
+    import torch
+    from rewy_amd.original import original_backward
+    threads = min(int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count()), os.cpu_count())
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    B, T, H = xs["q"].shape[:3]
+    try:
+        def sample_inputs(hs):
+            # batch 0, heads 0..hs-1 ([B,T,H,...] tensors and [B,NT,H,K,V] states alike)
+            c = lambda x: x[:1, :, :hs].float().cpu().contiguous()
+            saved = dict(w=c(sv["w"]), u=c(sv["u"]), qg=c(sv["qg"]), kg=c(sv["kg"]), v_new=c(sv["v_new"]),
+                         h=c(sv["h"]))
+            return dict(q=c(xs["q"]), k=c(xs["k"]), v=c(xs["v"]), gc=c(sv["gc"]), Akk=c(sv["Akk"]),
+                        beta=c(xs["beta"]), Aqk=c(sv["Aqk"]), dO=c(dO), saved=saved)
+
+        def run(inp):
+            t0 = time.perf_counter()
+            out = original_backward("kda", inp["q"], inp["k"], inp["v"], inp["gc"], inp["Akk"], scale, None,
+                                    inp["dO"], None, beta=inp["beta"], Aqk=inp["Aqk"], saved=inp["saved"])
+            el = time.perf_counter() - t0
+            del out
+            return el
+        hs = 1
+        probe = run(sample_inputs(1))
+        hs = max(1, min(H, int(round_s / max(probe, 1e-6))))
+        inp = sample_inputs(hs)
+        start, warm = time.perf_counter(), 0
+        while warm < 6 or time.perf_counter() - start < 2:
+            run(inp)
+            warm += 1
+        times = [run(inp) for _ in range(rounds)]
+        med = statistics.median(times)
+    finally:
+        torch.set_num_threads(prev)
+    sample_heads = hs * (T // 64)
+    return {"value": round(med * 1e3 * NTt / sample_heads, 1), "unit": "ms (full workload, extrapolated)",
+            "cores": threads, "kind": "port", "dtype": "fp32",
+            "sample": f"original 7-product chunk backward (torch ops, fp32, {threads} threads): batch 0, heads "
+                      f"0-{hs - 1}, T={T} ({sample_heads} of {NTt} chunk-heads); median of {rounds} rounds "
+                      f"({med * 1e3:.1f} ms) after {warm} warm-up rounds, scaled linearly",
+            "protocol": "reference benchmark.py:8-50: synchronized wall clock per sample, >= 6 and >= 2 s "
+                        "warm-up, median"}
+
+
+def cpu_oracle_baseline(xs, sv, dO, scale, NTt, nb_max=1):
     """fp64 oracle (numpy, one thread) of the two KDA stages -- state recurrence and
     chunk stage -- on a bounded sample (batches 0..nb-1, all heads, one head at a
     time so the oracle's pairwise tensors stay small), scaled linearly to the full
@@ -314,7 +369,7 @@ def cpu_baseline(xs, sv, dO, scale, NTt, nb_max=3):
         if ctx:
             ctx.__exit__(None, None, None)
     return {"value": round(el * 1e3 * NTt / sample_heads, 1), "unit": "ms (full workload, extrapolated)",
-            "cores": 1, "kind": "port",
+            "cores": 1, "kind": "port", "dtype": "fp64",
             "sample": f"fp64 numpy oracle (state recurrence + chunk stage), batches 0-{nb - 1}, T={T}, all {H} "
                       f"heads ({sample_heads} of {NTt} chunk-heads), measured {el:.2f} s, scaled linearly"}
 
@@ -512,7 +567,10 @@ def main():
 
     cpu = None
     if not args.no_cpu and args.config == "kda":
+        print("[bench] CPU baseline (original formulation, fp32, all granted threads)", file=sys.stderr, flush=True)
         cpu = cpu_baseline(xs, sv, dO, sv["scale"], NTt)
+        print("[bench] CPU baseline (fp64 oracle, one thread)", file=sys.stderr, flush=True)
+        cpu["fp64_oracle_1core"] = cpu_oracle_baseline(xs, sv, dO, sv["scale"], NTt)
 
     ms, tflops, kernels, res_fwd_ms = res["ms"], res["tflops"], res["kernels"], res["fwd_ms"]
     graph_ms, graph_err = res["graph_ms"], res["graph_err"]
