@@ -84,6 +84,7 @@ def kernel_costs(op, full_saving):
     # the affine-step launches compute the same recurrences: same operands and results
     # (their private step-matrix workspace is not algorithmic traffic)
     costs["affine_state"] = costs["fdr_state_bwd"]
+    costs["segmented_state"] = costs["fdr_state_bwd"]
     if not full_saving:
         costs["affine_recurrences"] = tuple(a + b for a, b in zip(costs["fdr_fwd_h"], costs["fdr_state_bwd"]))
     return costs
@@ -183,7 +184,13 @@ def setup(cfg, device):
         pre = kern["fdr_prepare_wu"]()
         ks, qs, ws = (pre["kg"], pre["qg"], pre["w"]) if vec else (xs["k"], xs["q"], pre["w"])
         aqk = sv["Aqk"] if vec else pre["Aqk"]
-    if ops.affine_pays(xs["q"]):
+    NT = cfg["T"] // 64
+    if keep and ops._state_method("auto", cfg["B"], cfg["H"], NT) == "segmented":
+        # long rows, few heads: segment maps in parallel, a short chain, segments rerun
+        kern["segmented_state"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
+                                                        want_dh0=xs["h0"] is not None, method="segmented")
+        dh, dR, _ = kern["segmented_state"]()
+    elif ops.affine_pays(xs["q"]):
         # few heads: the backend runs the recurrences in affine-step form (prep, scan, side launches)
         if keep:
             kern["affine_state"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
@@ -238,7 +245,7 @@ def time_kernels(kern, reps):
     return out
 
 
-SEQUENTIAL = ("fdr_state_bwd", "fdr_fwd_h", "affine_state", "affine_recurrences")
+SEQUENTIAL = ("fdr_state_bwd", "fdr_fwd_h", "affine_state", "affine_recurrences", "segmented_state")
 
 
 def measure(cfg, steps, warmup):

@@ -61,6 +61,31 @@ hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, con
                                 int V, int chunk, float scale, int value_block, hipStream_t stream);
 
 /*
+ * fdr_state_bwd for long rows and few heads, in three launches with a short sequential
+ * part.  Each row's chunks are split into `segments` consecutive segments; the
+ * recurrence is affine in the state, so a segment maps the state at its end X to the
+ * state at its start as P X + Q (P: K x K, Q: K x V, fp32):
+ *   1. every segment's P and Q in parallel (the recurrence run on the identity without
+ *      source terms, and on zero with them);
+ *   2. per (row, head), sequentially over the row's segments from the last: the end
+ *      state of each segment (dht, or zero, for the last; P X + Q of the next otherwise),
+ *      and dh0;
+ *   3. every segment again from its end state, writing dh and dR (fdr_state_bwd's
+ *      kernel on segments).
+ * Same arguments and results as fdr_state_bwd (dh0 may be null); segments in
+ * [1, T/64]; value_block (0 = by the number of segment rows) is step 3's tile width.
+ * `workspace` holds fdr_state_bwd_segmented_workspace_bytes(B, H, segments) bytes.
+ * Replaces the reference's state recurrence (see fdr_state_bwd) where B*H work-groups
+ * leave the GPU idle and the sequence is long (the reference's long-context config).
+ */
+size_t fdr_state_bwd_segmented_workspace_bytes(int B, int H, int segments);
+
+hipError_t fdr_state_bwd_segmented(const void* q, const void* k, const void* w, const float* g, int gate_mode,
+                                   const void* dO, const float* aqk, const void* dv, const float* dht, void* dh,
+                                   void* dr, float* dh0, int B, int T, int H, int K, int V, int chunk, float scale,
+                                   int segments, int value_block, void* workspace, hipStream_t stream);
+
+/*
  * Chunk-parallel backward: residual-WY products (P = A^T dR, D, E-bar),
  * dAqk, matrix intra, gate/beta epilogue and the in-chunk reverse cumsum of dg,
  * one work-group per (chunk, head).

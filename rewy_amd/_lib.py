@@ -17,6 +17,8 @@ _I = ctypes.c_int
 _F = ctypes.c_float
 SIGNATURES = {
     "fdr_state_bwd": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P],
+    "fdr_state_bwd_segmented": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I,
+                                _I, _P, _P],
     "fdr_chunk_bwd": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P,
                       _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_prepare_wu": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
@@ -84,6 +86,8 @@ def load():
             fn.restype = ctypes.c_int
         lib.fdr_kda_gate_workspace_bytes.argtypes = [_I, _I, _I, _I]
         lib.fdr_kda_gate_workspace_bytes.restype = ctypes.c_size_t
+        lib.fdr_state_bwd_segmented_workspace_bytes.argtypes = [_I, _I, _I]
+        lib.fdr_state_bwd_segmented_workspace_bytes.restype = ctypes.c_size_t
         lib.fdr_chunk_bwd_gate_workspace_bytes.argtypes = [_I, _I, _I]
         lib.fdr_chunk_bwd_gate_workspace_bytes.restype = ctypes.c_size_t
         _lib = lib

@@ -37,6 +37,33 @@ AFFINE_MIN_CHUNKS = 8
 AFFINE_VALUE_BLOCK = 16
 
 
+# Segmented state recurrence (fdr_state_bwd_segmented): long rows whose B*H value-tile
+# work-groups leave most of the GPU idle.  Segments are sized so that the per-segment
+# maps fill the chip (P and Q tiles: 4 work-groups per segment-head at 64-wide tiles).
+SEG_MIN_CHUNKS = 256
+SEG_TARGET_GROUPS = 512
+SEG_MIN_LEN = 16
+
+
+def segments_for(B, H, NT):
+    """Segment count of the segmented form for B rows of NT chunks and H heads."""
+    s = max(1, SEG_TARGET_GROUPS // (4 * B * H))
+    return max(1, min(s, NT // SEG_MIN_LEN))
+
+
+def _state_method(method, B, H, NT):
+    """Which form of the backward state recurrence runs: direct, affine or segmented."""
+    if method not in ("auto", "direct", "affine", "segmented"):
+        raise ValueError('method must be "auto", "direct", "affine" or "segmented"')
+    if method != "auto":
+        return method
+    if NT >= SEG_MIN_CHUNKS and 2 * B * H < 256:
+        return "segmented"
+    if B * H <= AFFINE_MAX_BH and NT >= AFFINE_MIN_CHUNKS:
+        return "affine"
+    return "direct"
+
+
 def _use_affine(method, B, H, NT):
     if method not in ("auto", "direct", "affine"):
         raise ValueError('method must be "auto", "direct" or "affine"')
@@ -91,7 +118,7 @@ def _dims(q):
 
 
 def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, want_dh0=True,
-              value_block=0, method="auto", chunk_offsets=None):
+              value_block=0, method="auto", chunk_offsets=None, segments=0):
     """Reverse state recurrence.  Returns (dh [B,NT,H,K,V] bf16, dR [B,T,H,V] bf16, dh0 fp32|None).
 
     ``chunk_offsets`` (int [N+1]): B = 1 holds N sequences packed along T, sequence n on
@@ -100,7 +127,10 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
 
     method "direct": one kernel (fdr_state_bwd); "affine": chunk-parallel step
     matrices, a one-product-per-chunk scan and a chunk-parallel dR pass
-    (fdr_affine_*), faster when B*H is too small to fill the GPU; "auto" picks."""
+    (fdr_affine_*), faster when B*H is too small to fill the GPU; "segmented": every row
+    split into ``segments`` (0: ``segments_for``) whose affine maps are formed in parallel,
+    chained, and each segment rerun from its end state (fdr_state_bwd_segmented), for long
+    rows and few heads; "auto" picks."""
     B, T, H, K = _dims(q)
     V = V_SUPPORTED
     dev = q.device
@@ -138,7 +168,19 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
                                               float(scale), int(value_block), _lib.stream_handle(dev))
         _lib.check(st, "fdr_state_bwd_varlen")
         return dh, dr, dh0
-    if _use_affine(method, B, H, NT):
+    form = _state_method(method, B, H, NT)
+    if form == "segmented":
+        segs = int(segments) or segments_for(B, H, NT)
+        if not 1 <= segs <= NT:
+            raise ValueError(f"segments must be in [1, {NT}]")
+        lib = _lib.load()
+        ws = torch.empty(lib.fdr_state_bwd_segmented_workspace_bytes(B, H, segs) // 4, device=dev, dtype=f32)
+        st = lib.fdr_state_bwd_segmented(P(q), P(k), P(w), P(g), int(gate_mode), P(dO), P(aqk), P(dv), P(dht),
+                                         P(dh), P(dr), P(dh0), B, T, H, K, V, CHUNK, float(scale), segs,
+                                         int(value_block), P(ws), _lib.stream_handle(dev))
+        _lib.check(st, "fdr_state_bwd_segmented")
+        return dh, dr, dh0
+    if form == "affine":
         vb = value_block or AFFINE_VALUE_BLOCK
         step, offset = _affine_workspace(B, NT, H, dev)
         dv_local = torch.empty(B, T, H, V, device=dev, dtype=bf) if aqk is not None else None

@@ -74,3 +74,17 @@ def test_grouped_value_heads(op):
     gb = torch.autograd.grad(o2, [b["q"], b["k"]], dO)
     for x, y in zip(ga, gb):
         torch.testing.assert_close(x.float(), y.float().reshape(1, 128, 2, 2, 128).sum(3), rtol=1e-2, atol=1e-2)
+
+
+def test_state_recurrence_form_routing():
+    """Which form of the backward state recurrence the backend picks (host logic only):
+    segmented for long rows with few heads, affine for few heads and few chunks, direct
+    when B*H fills the GPU."""
+    from rewy_amd import ops
+    assert ops._state_method("auto", 1, 16, 1024) == "segmented"      # the long-context KDA config
+    assert ops._state_method("auto", 8, 16, 64) == "direct"           # the headline config
+    assert ops._state_method("auto", 2, 32, 128) == "direct"          # the GDN2 config
+    assert ops._state_method("auto", 1, 4, 128) == "affine"           # the reference's grid, few chunks
+    assert ops.segments_for(1, 16, 1024) == 8
+    assert ops.segments_for(1, 1, 40) == 2                             # segments of >= 16 chunks
+    assert ops._state_method("direct", 1, 16, 1024) == "direct"
