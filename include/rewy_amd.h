@@ -37,12 +37,14 @@ extern "C" {
  * raw q/k and the kernel applies the scalar gate.  Exactly one of `aqk`
  * (dv_local = Aqk^T dO is then formed in-kernel, FLA chunk_kda_bwd_dAv) or `dv`
  * (a precomputed dv_local, FLA chunk_bwd_dv_local) must be non-null.
- * dht and dh0 may be null.  value_block = 0 picks the value-tile width.
+ * dht and dh0 may be null.  value_block = 0 picks the value-tile width.  state_v_first != 0:
+ * dht and dh0 are [B,H,V,K] (FLA's state_v_first layout, reference vector_state_gpu.py:24-25);
+ * the per-chunk dh stays [B,T/64,H,K,V] (internal to the backward).
  */
 hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const float* g,
                          int gate_mode, const void* dO, const float* aqk, const void* dv,
-                         const float* dht, void* dh, void* dr, float* dh0, int B, int T, int H,
-                         int K, int V, int chunk, float scale, int value_block,
+                         const float* dht, void* dh, void* dr, float* dh0, int state_v_first, int B,
+                         int T, int H, int K, int V, int chunk, float scale, int value_block,
                          hipStream_t stream);
 
 /*
@@ -57,7 +59,7 @@ hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const floa
  */
 hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, const float* g, int gate_mode,
                                 const void* dO, const float* aqk, const void* dv, const float* dht, void* dh,
-                                void* dr, float* dh0, const int* chunk_offsets, int N, int T, int H, int K,
+                                void* dr, float* dh0, int state_v_first, const int* chunk_offsets, int N, int T, int H, int K,
                                 int V, int chunk, float scale, int value_block, hipStream_t stream);
 
 /*
@@ -82,7 +84,7 @@ size_t fdr_state_bwd_segmented_workspace_bytes(int B, int H, int segments);
 
 hipError_t fdr_state_bwd_segmented(const void* q, const void* k, const void* w, const float* g, int gate_mode,
                                    const void* dO, const float* aqk, const void* dv, const float* dht, void* dh,
-                                   void* dr, float* dh0, int B, int T, int H, int K, int V, int chunk, float scale,
+                                   void* dr, float* dh0, int state_v_first, int B, int T, int H, int K, int V, int chunk, float scale,
                                    int segments, int value_block, void* workspace, hipStream_t stream);
 
 /*
@@ -107,14 +109,16 @@ hipError_t fdr_state_bwd_segmented(const void* q, const void* k, const void* w, 
  * beta_sigmoid > 0 (scalar beta only): beta was activated in the forward as
  * beta = beta_sigmoid * sigmoid(x) (use_beta_sigmoid_in_kernel, scale 2 with
  * allow_neg_eigval; reference _compat/kda.py:202-206), and dbeta is written as dL/dx;
- * 0 writes dL/dbeta.
+ * 0 writes dL/dbeta.  h_v_first != 0 (gate_mode 2 only): the saved per-chunk states h are
+ * [B,T/64,H,V,K], as FLA's forward saves them under state_v_first (reference
+ * _compat/kda.py:485-493); dh is always this library's [B,T/64,H,K,V] from fdr_state_bwd.
  */
 hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v, const void* v_new,
                          const void* dO, const void* dR, const float* g, int gate_mode,
                          const float* beta, const void* b_gate, const void* w_gate,
                          const float* Akk, const void* h, const void* dh, void* dq, void* dk,
                          void* dv, float* dg, float* dbeta, float beta_sigmoid, void* db, void* dw,
-                         int B, int T, int H, int K, int V, int chunk, float scale,
+                         int h_v_first, int B, int T, int H, int K, int V, int chunk, float scale,
                          hipStream_t stream);
 
 /*
@@ -138,10 +142,11 @@ hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const flo
  *   h[c] = state at chunk start (bf16 [B,T/64,H,K,V]); v_new_c = u_c - w_c h_c (bf16);
  *   state <- lambda_c state + kg_c^T v_new_c;  ht = final state (fp32, may be null).
  * For gate_mode 2, `k` is the gate-weighted kg; for modes 0/1 it is the raw k.
+ * state_v_first != 0: h0 and ht are [B,H,V,K]; the per-chunk h stays [B,T/64,H,K,V].
  */
 hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g, int gate_mode,
-                     const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int K,
-                     int V, int chunk, int value_block, hipStream_t stream);
+                     const float* h0, void* h, void* v_new, float* ht, int state_v_first, int B, int T, int H,
+                     int K, int V, int chunk, int value_block, hipStream_t stream);
 
 /*
  * fdr_fwd_h over a variable-length batch, with the packing and chunk_offsets of
@@ -149,7 +154,8 @@ hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g
  * chunk_gated_delta_rule_fwd_h with cu_seqlens (the recompute policy's call).
  */
 hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const float* g, int gate_mode,
-                            const float* h0, void* h, void* v_new, float* ht, const int* chunk_offsets, int N,
+                            const float* h0, void* h, void* v_new, float* ht, int state_v_first,
+                            const int* chunk_offsets, int N,
                             int T, int H, int K, int V, int chunk, int value_block, hipStream_t stream);
 
 /*
@@ -229,7 +235,7 @@ hipError_t fdr_kda_gate_bwd(const float* dg, const void* g_raw, int raw_is_bf16,
  * folded into the dg stores: instead of dg it writes dg_raw = dL/dg_raw (g_raw's dtype)
  * and, where non-null, dA_log / ddt_bias, with the activation and arguments of
  * fdr_kda_gate_bwd.  `workspace` holds fdr_chunk_bwd_gate_workspace_bytes(B, T, H) bytes
- * of per-chunk partial sums.  beta_sigmoid as for fdr_chunk_bwd.  Replaces the chunk
+ * of per-chunk partial sums.  beta_sigmoid and h_v_first as for fdr_chunk_bwd.  Replaces the chunk
  * stage plus the gate backward of the reference's kda_backward with use_gate_in_kernel
  * (backends/backward.py:63-73).
  */
@@ -240,7 +246,8 @@ hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, const void* v, 
                                    const void* h, const void* dh, void* dq, void* dk, void* dv, float* dbeta,
                                    float beta_sigmoid, const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
                                    int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
-                                   float* ddt_bias, void* workspace, int B, int T, int H, int K, int V, int chunk,
+                                   float* ddt_bias, void* workspace, int h_v_first, int B, int T, int H, int K, int V,
+                                   int chunk,
                                    float scale, hipStream_t stream);
 
 /*
@@ -263,7 +270,7 @@ hipError_t fdr_chunk_bwd_gate_fold_noalloc(const void* q, const void* k, const v
                                            void* dv, float* dbeta, float beta_sigmoid, const void* g_raw,
                                            int raw_is_bf16, const float* A_log, const float* dt_bias,
                                            int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
-                                           float* ddt_bias, int B, int T, int H, int K, int V, int chunk,
+                                           float* ddt_bias, int h_v_first, int B, int T, int H, int K, int V, int chunk,
                                            float scale, hipStream_t stream);
 
 /*
@@ -319,6 +326,7 @@ typedef struct fdr_scan_problem {
   float* final_state;        /* fp32 [B,H,K,V] or null */
   int gate_mode;
   int reverse;
+  int state_v_first;         /* initial / final_state are [B,H,V,K] instead of [B,H,K,V] */
 } fdr_scan_problem;
 
 typedef struct fdr_side_problem {

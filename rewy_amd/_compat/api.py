@@ -33,7 +33,8 @@ def _l2norm(x, backend):
 class ChunkFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w,
-                initial_state, cu_seqlens=None, gate=None, A_log=None, dt_bias=None, beta_act=None):
+                initial_state, cu_seqlens=None, gate=None, A_log=None, dt_bias=None, beta_act=None,
+                state_v_first=False):
         # cu_seqlens (optimized backend on a GPU only): sequences packed on 64-token
         # chunk boundaries, B = 1; the state scans restart at each sequence.
         # gate = (lower_bound,) (KDA, optimized backend on a GPU, no padded tokens): g is the
@@ -42,12 +43,16 @@ class ChunkFunction(torch.autograd.Function):
         # beta_act = s (scalar-beta families, optimized backend on a GPU): beta is the raw
         # input, activated here as s * sigmoid(beta); its backward rides in the chunk
         # kernel's dbeta stores.
+        # state_v_first (optimized backend on a GPU): initial / final states are [N,H,V,K],
+        # read and written so by the kernels.
         native = backend == "optimized" and q.is_cuda
+        if state_v_first and not native:
+            raise ValueError("V-first states in the chunk Function are the optimized GPU path's")
         if gate is not None and not (native and op == "kda"):
             raise ValueError("the folded gate is the optimized GPU path's (KDA, batches without padded tokens)")
         if beta_act is not None and not (native and op != "gdn2"):
             raise ValueError("the folded beta sigmoid is the optimized GPU path's (scalar beta)")
-        ctx.cu_seqlens, ctx.gate, ctx.beta_act = cu_seqlens, gate, beta_act
+        ctx.cu_seqlens, ctx.gate, ctx.beta_act, ctx.vf = cu_seqlens, gate, beta_act, bool(state_v_first)
         ctx.g_dtype = None if g is None else g.dtype
         ctx.beta_dtype = None if beta is None else beta.dtype
         g_raw = None
@@ -62,7 +67,8 @@ class ChunkFunction(torch.autograd.Function):
             o, final, sv = chunk_forward_hip(op, q, k, v, g=g, beta=beta, b=b, w=w,
                                              initial_state=initial_state, scale=scale,
                                              output_final_state=output_final_state,
-                                             chunk_offsets=None if cu_seqlens is None else cu_seqlens // 64)
+                                             chunk_offsets=None if cu_seqlens is None else cu_seqlens // 64,
+                                             state_v_first=state_v_first)
         elif cu_seqlens is not None:
             raise NotImplementedError("chunk-aligned packing is the optimized GPU path's layout")
         else:
@@ -87,6 +93,8 @@ class ChunkFunction(torch.autograd.Function):
             from ..backends import backward as bw
             cu = ctx.cu_seqlens
             bsig = ctx.beta_act or 0.0
+            # the saved per-chunk h is this package's [B,NT,H,K,V] whatever the state layout
+            lay = dict(state_v_first=ctx.vf, saved_h_v_first=False) if ctx.vf else {}
             if op == "kda":
                 gate_kw = {} if ctx.gate is None else dict(
                     use_gate_in_kernel=True, g_org=g_raw, A_log=A_log, lower_bound=ctx.gate[0],
@@ -94,22 +102,22 @@ class ChunkFunction(torch.autograd.Function):
                 dq, dk, dv, db, dg, dh0, dA_log, ddt_bias = bw.kda_backward(
                     q=q, k=k, v=v, beta=beta, Aqk=Aqk, Akk=Akk, scale=scale, initial_state=h0,
                     do=do, dht=dht, g=gc, w=w_wy, u=u_wy, qg=qg, kg=kg, v_new=v_new, h=h, cu_seqlens=cu,
-                    beta_sigmoid=bsig, **gate_kw)
+                    beta_sigmoid=bsig, **lay, **gate_kw)
                 dw = None
             elif op == "gdn2":
                 dq, dk, dv, db, dw, dg, dh0, _, _ = bw.gdn2_backward(
                     q=q, k=k, v=v, b=b, w_gate=w, Aqk=Aqk, Akk=Akk, scale=scale, initial_state=h0,
                     do=do, dht=dht, g=gc, w_wy=w_wy, u_wy=u_wy, qg=qg, kg=kg, v_new=v_new, h=h,
-                    cu_seqlens=cu)
+                    cu_seqlens=cu, **lay)
             elif op == "gdn":
                 dq, dk, dv, db, dg, dh0, _, _ = bw.gdn_backward(
                     q=q, k=k, v=v, g=gc, beta=beta, A=Akk, scale=scale, initial_state=h0, do=do, dht=dht,
-                    cu_seqlens=cu, beta_sigmoid=bsig)
+                    cu_seqlens=cu, beta_sigmoid=bsig, state_v_first=ctx.vf)
                 dw = None
             else:
                 dq, dk, dv, db, dh0 = bw.delta_backward(
                     q=q, k=k, v=v, beta=beta, A=Akk, scale=scale, initial_state=h0, do=do, dht=dht,
-                    cu_seqlens=cu, beta_sigmoid=bsig)
+                    cu_seqlens=cu, beta_sigmoid=bsig, state_v_first=ctx.vf)
                 dg = dw = None
         else:
             from ..original import original_backward
@@ -127,7 +135,7 @@ class ChunkFunction(torch.autograd.Function):
                 None if dg is None else dg.to(ctx.g_dtype),
                 None if op == "gdn2" else gb, gb if op == "gdn2" else None, cast(dw, w), dh0, None, None,
                 cast(dA_log, A_log), None if ddt_bias is None else ddt_bias.reshape(dt_bias.shape).to(dt_bias.dtype),
-                None)
+                None, None)
 
 
 def _unsupported(name, **flags):
@@ -153,15 +161,16 @@ def _pad_time(xs, T):
     return out, Tp
 
 
-def _run(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0):
+def _run(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0, vf=False):
     T = q.shape[1]
+    extra = (None, None, None, None, None, vf)
     if T % 64:
         (q, k, v, g, beta, b, w), _ = _pad_time((q, k, v, g, beta, b, w), T)
         o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state,
-                                       q, k, v, g, beta, b, w, h0)
+                                       q, k, v, g, beta, b, w, h0, *extra)
         return o[:, :T], final
     return ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g,
-                               beta, b, w, h0)
+                               beta, b, w, h0, *extra)
 
 
 def _unpack(x, bounds, Tp):
@@ -265,32 +274,36 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
         k = k.repeat_interleave(HV // H, dim=2)
         if b is not None:
             b = b.repeat_interleave(HV // H, dim=2)
-    if state_v_first and h0 is not None:
+    # V-first states: read and written in that layout by the kernels on the optimized GPU
+    # path; transposed here for the torch paths
+    vf = bool(state_v_first) and native
+    if state_v_first and not vf and h0 is not None:
         h0 = h0.transpose(-1, -2)
     fold = (None, None, None) if gate_fold is None else ((gate_fold[0],), gate_fold[1], gate_fold[2])
     if cu_seqlens is None:
         if unpadded:
             o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b,
-                                           w, h0, None, *fold, beta_act)
+                                           w, h0, None, *fold, beta_act, vf)
         else:
-            o, final = _run(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0)
+            o, final = _run(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0, vf)
     elif unpadded:
         # already on chunk boundaries: the kernels take the batch as it is
         o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta,
-                                       b, w, h0, torch.tensor(cu, dtype=torch.int64), *fold, beta_act)
+                                       b, w, h0, torch.tensor(cu, dtype=torch.int64), *fold, beta_act, vf)
     elif native:
         lens = [max(64, -(-(e - s) // 64) * 64) for s, e in bounds]
         cu_al = torch.tensor([0] + lens, dtype=torch.int64).cumsum(0)
         starts = cu_al[:-1].tolist()
         xs = [_pack_aligned(x, bounds, starts, int(cu_al[-1])) for x in (q, k, v, g, beta, b, w)]
-        o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, *xs, h0, cu_al)
+        o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, *xs, h0, cu_al,
+                                       None, None, None, None, vf)
         o = _UnpackAligned.apply(o, bounds, starts)
     else:
         Tp = max(64, -(-max(e - s for s, e in bounds) // 64) * 64)
         xs = [_unpack(x, bounds, Tp) for x in (q, k, v, g, beta, b, w)]
         o, final = _run(op, backend, full_saving, scale, output_final_state, *xs, h0)
         o = torch.cat([o[i:i + 1, :e - s] for i, (s, e) in enumerate(bounds)], 1)
-    if state_v_first and final is not None:
+    if state_v_first and not vf and final is not None:
         final = final.transpose(-1, -2)
     return o, final
 

@@ -58,8 +58,6 @@ def _check_common(kind, kw):
     for name in _UNSUPPORTED:
         if kw.get(name) is not None:
             raise NotImplementedError(f"{kind} HIP backward: {name} is not supported")
-    if kw.get("state_v_first", False):
-        raise NotImplementedError(f"{kind} HIP backward: state_v_first is not supported")
     if kw.get("chunk_size", 64) != 64:
         raise NotImplementedError(f"{kind} HIP backward: chunk_size must be 64")
     if kw.get("use_gate_in_kernel", False) and kind != "kda":
@@ -79,9 +77,13 @@ def _f32(x):
 
 
 def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, saved, gate_fold=None,
-            beta_sigmoid=0.0, **kw):
-    """Shared vector-gate (KDA / GDN2) backward.  ``gate_fold``, ``beta_sigmoid``: see ops.chunk_bwd."""
+            beta_sigmoid=0.0, state_v_first=False, saved_h_v_first=None, **kw):
+    """Shared vector-gate (KDA / GDN2) backward.  ``gate_fold``, ``beta_sigmoid``: see ops.chunk_bwd.
+    ``state_v_first``: initial_state, dht and dh0 are [N,H,V,K], and so is a saved ``h``
+    unless ``saved_h_v_first`` says otherwise (the kernels read and write those layouts)."""
     _check_common(op, kw)
+    vf = bool(state_v_first)
+    hvf = vf if saved_h_v_first is None else bool(saved_h_v_first)
     co = _varlen(q, kw)
     q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
     g = _f32(g)
@@ -91,24 +93,24 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
         pre = _prepare_vector(k, v, g, Akk, gates, q)
         h, v_new, dh, dR, dh0 = ops.recurrences(pre["qg"], pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR,
                                                 do, scale, aqk=Aqk, h0=_f32(initial_state), dht=_f32(dht),
-                                                want_dh0=initial_state is not None)
-        saved = dict(v_new=v_new, h=h)
+                                                want_dh0=initial_state is not None, state_v_first=vf)
+        saved, hvf = dict(v_new=v_new, h=h), False
     else:
         if saved.get("h") is None:
-            saved = _recompute_vector(q, k, v, g, Akk, initial_state, gates, co)
-        dh, dR, dh0 = _state_vector(saved, g, do, scale, Aqk, dht, initial_state, co)
+            saved, hvf = _recompute_vector(q, k, v, g, Akk, initial_state, gates, co, vf), False
+        dh, dR, dh0 = _state_vector(saved, g, do, scale, Aqk, dht, initial_state, co, vf)
     out = ops.chunk_bwd(q, k, v, _bf(saved["v_new"]), do, dR, g, ops.GATE_VECTOR, Akk,
                         _bf(saved["h"]), dh, scale, beta=_f32(gates.get("beta")),
                         b=None if gates.get("b") is None else _bf(gates["b"]),
                         w=None if gates.get("w") is None else _bf(gates["w"]), gate_fold=gate_fold,
-                        beta_sigmoid=beta_sigmoid)
+                        beta_sigmoid=beta_sigmoid, h_v_first=hvf)
     return out, dh0
 
 
-def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, co=None):
+def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, co=None, vf=False):
     return ops.state_bwd(_bf(saved["qg"]), _bf(saved["kg"]), _bf(saved["w"]), g, ops.GATE_VECTOR, do, scale,
                          aqk=Aqk, dht=_f32(dht), want_dh0=initial_state is not None,
-                         method="auto" if co is None else "direct", chunk_offsets=co)
+                         method="auto" if co is None else "direct", chunk_offsets=co, state_v_first=vf)
 
 
 def _prepare_vector(k, v, g, Akk, gates, q):
@@ -118,11 +120,11 @@ def _prepare_vector(k, v, g, Akk, gates, q):
                           want_qkg=True)
 
 
-def _recompute_vector(q, k, v, g, Akk, initial_state, gates, co=None):
+def _recompute_vector(q, k, v, g, Akk, initial_state, gates, co=None, vf=False):
     """w, u, qg, kg (fdr_prepare_wu) then h, v_new (fdr_fwd_h): the recompute policy."""
     pre = _prepare_vector(k, v, g, Akk, gates, q)
     h, v_new, _ = ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
-                            method="auto" if co is None else "direct", chunk_offsets=co)
+                            method="auto" if co is None else "direct", chunk_offsets=co, state_v_first=vf)
     return dict(w=pre["w"], u=pre["u"], qg=pre["qg"], kg=pre["kg"], v_new=v_new, h=h)
 
 
@@ -130,8 +132,13 @@ def kda_backward(q, k, v, beta, Aqk, Akk, scale, initial_state, do, dht, g, g_or
                  state_v_first=False, cu_seqlens=None, chunk_indices=None, chunk_size=64,
                  safe_gate=False, lower_bound=None, use_gate_in_kernel=False, A_log=None,
                  dt_bias=None, disable_recompute=False, cp_context=None, w=None, u=None, qg=None,
-                 kg=None, v_new=None, h=None, use_graph=False, chunk_offsets=None, beta_sigmoid=0.0):
+                 kg=None, v_new=None, h=None, use_graph=False, chunk_offsets=None, beta_sigmoid=0.0,
+                 saved_h_v_first=None):
     """KDA backward -> (dq, dk, dv, db, dg, dh0, dA_log, ddt_bias).
+
+    ``state_v_first``: initial_state, dht, dh0 and a saved h in FLA's [.., V, K] layout, read
+    and written in place by the kernels.  ``saved_h_v_first`` (this build's addition, default:
+    follow state_v_first) states the layout of the saved h separately.
 
     ``beta_sigmoid`` (this build's addition, default off): s > 0 when ``beta`` is
     s * sigmoid(beta_raw) activated in the forward; db is then dL/dbeta_raw, the fused
@@ -143,7 +150,8 @@ def kda_backward(q, k, v, beta, Aqk, Akk, scale, initial_state, do, dht, g, g_or
     fold = (dict(g_raw=g_org, A_log=A_log, dt_bias=dt_bias, lower_bound=lower_bound)
             if use_gate_in_kernel else None)
     out, dh0 = _vector("kda", q, k, v, dict(beta=beta), Aqk, Akk, scale, initial_state, do, dht, g,
-                       saved, gate_fold=fold, beta_sigmoid=beta_sigmoid, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
+                       saved, gate_fold=fold, beta_sigmoid=beta_sigmoid, state_v_first=state_v_first,
+                       saved_h_v_first=saved_h_v_first, cu_seqlens=cu_seqlens,
                        chunk_indices=chunk_indices, chunk_size=chunk_size, safe_gate=safe_gate,
                        use_gate_in_kernel=use_gate_in_kernel, cp_context=cp_context,
                        use_graph=use_graph, chunk_offsets=chunk_offsets)
@@ -156,19 +164,20 @@ def gdn2_backward(q, k, v, b, w_gate, Aqk, Akk, scale, initial_state, do, dht, g
                   cu_seqlens=None, chunk_indices=None, chunk_size=64, safe_gate=False,
                   lower_bound=None, use_gate_in_kernel=False, A_log=None, dt_bias=None,
                   state_v_first=False, w_wy=None, u_wy=None, qg=None, kg=None, v_new=None, h=None,
-                  disable_recompute=False, cp_context=None):
-    """GDN2 backward -> (dq, dk, dv, db, dw, dg, dh0, dA_log, ddt_bias)."""
+                  disable_recompute=False, cp_context=None, saved_h_v_first=None):
+    """GDN2 backward -> (dq, dk, dv, db, dw, dg, dh0, dA_log, ddt_bias).  ``state_v_first`` and
+    ``saved_h_v_first`` as for kda_backward."""
     from ..runtime import record
     saved = dict(w=w_wy, u=u_wy, qg=qg, kg=kg, v_new=v_new, h=h)
     out, dh0 = _vector("gdn2", q, k, v, dict(b=b, w=w_gate), Aqk, Akk, scale, initial_state, do, dht,
-                       g, saved, state_v_first=state_v_first, cu_seqlens=cu_seqlens,
+                       g, saved, state_v_first=state_v_first, saved_h_v_first=saved_h_v_first, cu_seqlens=cu_seqlens,
                        chunk_indices=chunk_indices, chunk_size=chunk_size, safe_gate=safe_gate,
                        use_gate_in_kernel=use_gate_in_kernel, cp_context=cp_context)
     record("gdn2", "optimized_backward")
     return out["dq"], out["dk"], out["dv"], out["db"], out["dw"], out["dg"], dh0, None, None
 
 
-def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid=0.0, **kw):
+def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid=0.0, state_v_first=False, **kw):
     """GDN / DeltaNet: recompute w, u, h, v_new, then the state and chunk kernels
     (reference ``_scalar``, backends/backward.py:96-131)."""
     from ..runtime import record
@@ -184,12 +193,13 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
         # few heads: both recurrences side by side in affine-step form
         h, v_new, dh, dR, dh0 = ops.recurrences(q, k, pre["w"], pre["u"], g, gate, do, scale, aqk=pre["Aqk"],
                                                 h0=_f32(initial_state), dht=_f32(dht),
-                                                want_dh0=initial_state is not None)
+                                                want_dh0=initial_state is not None, state_v_first=state_v_first)
     else:
         h, v_new, _ = ops.fwd_h(k, pre["w"], pre["u"], g, gate, h0=_f32(initial_state), method="direct",
-                                chunk_offsets=co)
+                                chunk_offsets=co, state_v_first=state_v_first)
         dh, dR, dh0 = ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
-                                    want_dh0=initial_state is not None, method="direct", chunk_offsets=co)
+                                    want_dh0=initial_state is not None, method="auto" if co is None else "direct",
+                                    chunk_offsets=co, state_v_first=state_v_first)
     out = ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta, beta_sigmoid=beta_sigmoid)
     record(op, "optimized_backward")
     return out, dh0

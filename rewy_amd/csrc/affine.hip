@@ -244,6 +244,7 @@ struct ScanArgs {
   bf16* s_out;
   float* s_final;
   int reverse;
+  int vf;            // s0 / s_final in [V,K] (state_v_first) instead of [K,V]
 };
 
 // GATE is a template parameter so that the gate load is branch-free: a branch
@@ -280,8 +281,12 @@ __global__ __launch_bounds__(64 * NW) void affine_scan_kernel(ScanArgs p0, ScanA
       f32x4 a = zero4();
       if (p.s0) {
         const float* src = p.s0 + (size_t)bh * KD * VD;
+        const int col = v_base + 16 * ct + (l & 15);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) a[r] = src[(16 * rowt(i) + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)];
+        for (int r = 0; r < 4; ++r) {
+          const int kr = 16 * rowt(i) + 4 * (l >> 4) + r;
+          a[r] = src[p.vf ? col * KD + kr : kr * VD + col];
+        }
       }
       st[i][ct] = a;
     }
@@ -411,8 +416,10 @@ __global__ __launch_bounds__(64 * NW) void affine_scan_kernel(ScanArgs p0, ScanA
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          dst[(16 * rowt(i) + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)] = st[i][ct][r];
+        for (int r = 0; r < 4; ++r) {
+          const int kr = 16 * rowt(i) + 4 * (l >> 4) + r, col = v_base + 16 * ct + (l & 15);
+          dst[p.vf ? col * KD + kr : kr * VD + col] = st[i][ct][r];
+        }
   }
 }
 
@@ -603,7 +610,7 @@ extern "C" hipError_t fdr_affine_scan(const fdr_scan_problem* probs, int n_probl
     if (p.gate_mode < AG_NONE || p.gate_mode > AG_VECTOR || (p.gate_mode != AG_NONE && !p.g)) return hipErrorInvalidValue;
     if (p.gate_mode != probs[0].gate_mode) return hipErrorInvalidValue;    // one gate mode per launch
     a[i] = ScanArgs{(const bf16*)p.step, p.offset, p.g, p.initial, (bf16*)p.states, p.final_state,
-                    p.reverse ? 1 : 0};
+                    p.reverse ? 1 : 0, p.state_v_first ? 1 : 0};
   }
   if (n_problems == 1) a[1] = a[0];
   const int gate = probs[0].gate_mode;

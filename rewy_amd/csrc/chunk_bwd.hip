@@ -234,7 +234,8 @@ struct GateFoldArgs {
 // dg, db are read-modify-written in fp32, no state terms and no cumsum).
 // FOLD >= 0: the gate backward is folded in, bf16 g_raw if FOLD & 1, activation FOLD >> 1:
 // 0: -exp(A) softplus(x), 1: lb sigmoid(exp(A) x), 2: lb sigmoid(x).
-template <int GATE, bool VEC_B, bool INTRA, bool PIPE = false, int FOLD = -1>
+// HVF: the per-chunk states h are [V,K] (FLA's state_v_first layout) instead of [K,V].
+template <int GATE, bool VEC_B, bool INTRA, bool PIPE = false, int FOLD = -1, bool HVF = false>
 __device__ __forceinline__ void chunk_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
@@ -303,7 +304,13 @@ __device__ __forceinline__ void chunk_body(
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const size_t o = hoff + (size_t)kk * VD + 32 * ks + 8 * lg;
-      fh[ks] = *reinterpret_cast<const bf16x8*>(hst + o);
+      if constexpr (HVF) {
+        // h[v][k]: the 8 values of column kk this lane needs are KD apart
+#pragma unroll
+        for (int j = 0; j < 8; ++j) fh[ks][j] = hst[hoff + (size_t)(32 * ks + 8 * lg + j) * KD + kk];
+      } else {
+        fh[ks] = *reinterpret_cast<const bf16x8*>(hst + o);
+      }
       fdh[ks] = *reinterpret_cast<const bf16x8*>(dhst + o);
     }
   };
@@ -1086,7 +1093,7 @@ __device__ __forceinline__ void chunk_body(
   if constexpr (PIPE) lds_sync();
 }
 
-template <int GATE, bool VEC_B>
+template <int GATE, bool VEC_B, bool HVF = false>
 __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
@@ -1098,7 +1105,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
   using LY = PostLayout<GATE, VEC_B>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
-  chunk_body<GATE, VEC_B, false>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
+  chunk_body<GATE, VEC_B, false, false, -1, HVF>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
                                  dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale, nullptr,
                                  nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
                                  reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
@@ -1106,7 +1113,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
 }
 
 // KDA with the gate backward folded into the dg stores (no dg output)
-template <int FOLD>
+template <int FOLD, bool HVF = false>
 __global__ __launch_bounds__(512) void chunk_bwd_fold_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
@@ -1117,7 +1124,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_fold_kernel(
   using LY = PostLayout<CG_VECTOR, false>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
-  chunk_body<CG_VECTOR, false, false, false, FOLD>(
+  chunk_body<CG_VECTOR, false, false, false, FOLD, HVF>(
       q, k, v, vnew, dO, dR, g, beta, nullptr, nullptr, akk, hst, dhst, dq_out, dk_out, dv_out, nullptr, dbeta_out,
       nullptr, nullptr, T, H, scale, nullptr, nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem,
       smem + LY::REGION_A, reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
@@ -1218,7 +1225,7 @@ static hipError_t device_cus(int& cus) {
   return hipSuccess;
 }
 
-template <int GATE, bool VEC_B>
+template <int GATE, bool VEC_B, bool HVF = false>
 static hipError_t launch_post(const void* q, const void* k, const void* v, const void* vnew,
                               const void* dO, const void* dR, const float* g, const float* beta,
                               const void* bgate, const void* wgate, const float* akk, const void* h,
@@ -1228,7 +1235,7 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
   const int items = B * H * (T / C);
   using LP = PostLayout<GATE, VEC_B, false, true>;
   // persistent form for scalar / no gate (measured slower for KDA: see the kernel)
-  if constexpr (LP::FITS && REWY_CHUNK_PIPE && (GATE != CG_VECTOR || REWY_CHUNK_PIPE > 1)) {
+  if constexpr (!HVF && LP::FITS && REWY_CHUNK_PIPE && (GATE != CG_VECTOR || REWY_CHUNK_PIPE > 1)) {
     auto kern = chunk_bwd_pipe_kernel<GATE, VEC_B>;    // static LDS only
     int cus = 0;
     const hipError_t e = device_cus(cus);
@@ -1242,7 +1249,7 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
     return hipGetLastError();
   }
   using LY = PostLayout<GATE, VEC_B>;
-  auto kern = chunk_bwd_kernel<GATE, VEC_B>;
+  auto kern = chunk_bwd_kernel<GATE, VEC_B, HVF>;
   static bool attr_set[kMaxDevices] = {};
   const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
   if (e != hipSuccess) return e;
@@ -1263,8 +1270,8 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
                                     const float* beta, const void* b_gate, const void* w_gate,
                                     const float* Akk, const void* h, const void* dh, void* dq,
                                     void* dk, void* dv, float* dg, float* dbeta, float beta_sigmoid,
-                                    void* db, void* dw, int B, int T, int H, int K, int V, int chunk,
-                                    float scale, hipStream_t stream) {
+                                    void* db, void* dw, int h_v_first, int B, int T, int H, int K, int V,
+                                    int chunk, float scale, hipStream_t stream) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0)
     return hipErrorInvalidValue;
   if (!(beta_sigmoid >= 0.f) || (beta_sigmoid > 0.f && b_gate)) return hipErrorInvalidValue;
@@ -1275,14 +1282,20 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
   if (!vec_b && (!beta || !dbeta)) return hipErrorInvalidValue;
   if (gate_mode != CG_NONE && (!g || !dg)) return hipErrorInvalidValue;
   if (vec_b && gate_mode != CG_VECTOR) return hipErrorInvalidValue;
-#define FDR_POST(G, VB)                                                                          \
-  return launch_post<G, VB>(q, k, v, v_new, dO, dR, g, beta, b_gate, w_gate, Akk, h, dh, dq, dk, \
-                            dv, dg, dbeta, db, dw, B, T, H, scale, beta_sigmoid, stream)
-  if (vec_b) { FDR_POST(CG_VECTOR, true); }
+#define FDR_POST(G, VB, HV)                                                                     \
+  return launch_post<G, VB, HV>(q, k, v, v_new, dO, dR, g, beta, b_gate, w_gate, Akk, h, dh, dq, dk, \
+                                dv, dg, dbeta, db, dw, B, T, H, scale, beta_sigmoid, stream)
+  if (h_v_first) {
+    // [V,K] states come from a saved forward: the vector-gate families (full saving)
+    if (gate_mode != CG_VECTOR) return hipErrorInvalidValue;
+    if (vec_b) { FDR_POST(CG_VECTOR, true, true); }
+    FDR_POST(CG_VECTOR, false, true);
+  }
+  if (vec_b) { FDR_POST(CG_VECTOR, true, false); }
   switch (gate_mode) {
-    case CG_NONE: FDR_POST(CG_NONE, false);
-    case CG_SCALAR: FDR_POST(CG_SCALAR, false);
-    case CG_VECTOR: FDR_POST(CG_VECTOR, false);
+    case CG_NONE: FDR_POST(CG_NONE, false, false);
+    case CG_SCALAR: FDR_POST(CG_SCALAR, false, false);
+    case CG_VECTOR: FDR_POST(CG_VECTOR, false, false);
     default: return hipErrorInvalidValue;
   }
 #undef FDR_POST
@@ -1305,8 +1318,8 @@ static hipError_t gate_fold_launch(const void* q, const void* k, const void* v, 
                                    const void* dh, void* dq, void* dk, void* dv, float* dbeta, float beta_sigmoid,
                                    const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
                                    int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
-                                   float* ddt_bias, void* workspace, int B, int T, int H, int K, int V, int chunk,
-                                   float scale, hipStream_t stream) {
+                                   float* ddt_bias, void* workspace, int h_v_first, int B, int T, int H, int K, int V,
+                                   int chunk, float scale, hipStream_t stream) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
   if (!q || !k || !v || !v_new || !dO || !dR || !g || !beta || !Akk || !h || !dh || !dq || !dk || !dv || !dbeta)
     return hipErrorInvalidValue;
@@ -1320,12 +1333,15 @@ static hipError_t gate_fold_launch(const void* q, const void* k, const void* v, 
   float* part_da = part_dt + (size_t)nblk * H * KD;
   const GateFoldArgs gf{g_raw, A_log, dt_bias, lower_bound, dg_raw, part_dt, part_da};
   using LY = PostLayout<CG_VECTOR, false>;
-  const int fold = 2 * mode + (raw_is_bf16 ? 1 : 0);
+  const int fold = 2 * mode + (raw_is_bf16 ? 1 : 0) + (h_v_first ? 6 : 0);
   using KernT = decltype(&chunk_bwd_fold_kernel<0>);
-  static const KernT kerns[6] = {chunk_bwd_fold_kernel<0>, chunk_bwd_fold_kernel<1>, chunk_bwd_fold_kernel<2>,
-                                 chunk_bwd_fold_kernel<3>, chunk_bwd_fold_kernel<4>, chunk_bwd_fold_kernel<5>};
+  static const KernT kerns[12] = {
+      chunk_bwd_fold_kernel<0>,       chunk_bwd_fold_kernel<1>,       chunk_bwd_fold_kernel<2>,
+      chunk_bwd_fold_kernel<3>,       chunk_bwd_fold_kernel<4>,       chunk_bwd_fold_kernel<5>,
+      chunk_bwd_fold_kernel<0, true>, chunk_bwd_fold_kernel<1, true>, chunk_bwd_fold_kernel<2, true>,
+      chunk_bwd_fold_kernel<3, true>, chunk_bwd_fold_kernel<4, true>, chunk_bwd_fold_kernel<5, true>};
   const KernT kern = kerns[fold];
-  static bool attr_set[6][kMaxDevices] = {};
+  static bool attr_set[12][kMaxDevices] = {};
   hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set[fold]);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, stream, (const bf16*)q, (const bf16*)k,
@@ -1343,11 +1359,11 @@ extern "C" hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, cons
                                               void* dv, float* dbeta, float beta_sigmoid, const void* g_raw,
                                               int raw_is_bf16, const float* A_log, const float* dt_bias,
                                               int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
-                                              float* ddt_bias, void* workspace, int B, int T, int H, int K, int V,
-                                              int chunk, float scale, hipStream_t stream) {
+                                              float* ddt_bias, void* workspace, int h_v_first, int B, int T, int H,
+                                              int K, int V, int chunk, float scale, hipStream_t stream) {
   return gate_fold_launch(q, k, v, v_new, dO, dR, g, beta, Akk, h, dh, dq, dk, dv, dbeta, beta_sigmoid, g_raw,
                           raw_is_bf16, A_log, dt_bias, has_lower_bound, lower_bound, dg_raw, dA_log, ddt_bias,
-                          workspace, B, T, H, K, V, chunk, scale, stream);
+                          workspace, h_v_first, B, T, H, K, V, chunk, scale, stream);
 }
 
 template <bool VEC_B>
@@ -1416,14 +1432,14 @@ extern "C" hipError_t fdr_chunk_bwd_gate_fold_noalloc(
     const void* q, const void* k, const void* v, const void* v_new, const void* dO, const void* dR, const float* g,
     const float* beta, const float* Akk, const void* h, const void* dh, void* dq, void* dk, void* dv, float* dbeta,
     float beta_sigmoid, const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
-    int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log, float* ddt_bias, int B, int T, int H,
-    int K, int V, int chunk, float scale, hipStream_t stream) {
+    int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log, float* ddt_bias, int h_v_first, int B,
+    int T, int H, int K, int V, int chunk, float scale, hipStream_t stream) {
   const size_t need = fdr_chunk_bwd_gate_workspace_bytes(B, T, H);
   if (need == 0 || need > FDR_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
   void* ws = nullptr;
   const hipError_t e = scratch_ptr(&ws);
   if (e != hipSuccess) return e;
   return gate_fold_launch(q, k, v, v_new, dO, dR, g, beta, Akk, h, dh, dq, dk, dv, dbeta, beta_sigmoid, g_raw,
-                          raw_is_bf16, A_log, dt_bias, has_lower_bound, lower_bound, dg_raw, dA_log, ddt_bias, ws, B,
-                          T, H, K, V, chunk, scale, stream);
+                          raw_is_bf16, A_log, dt_bias, has_lower_bound, lower_bound, dg_raw, dA_log, ddt_bias, ws,
+                          h_v_first, B, T, H, K, V, chunk, scale, stream);
 }

@@ -245,7 +245,8 @@ template <int BV, int GATE>
 __global__ __launch_bounds__(512) void fwd_h_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ w, const bf16* __restrict__ u,
     const float* __restrict__ g, const float* __restrict__ h0, bf16* __restrict__ h_out,
-    bf16* __restrict__ vnew_out, float* __restrict__ ht_out, int T, int H, const int* __restrict__ chunk_off) {
+    bf16* __restrict__ vnew_out, float* __restrict__ ht_out, int T, int H, const int* __restrict__ chunk_off,
+    int vf) {
   using S = FwdSmem<BV, GATE>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
@@ -270,10 +271,13 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
   for (int ct = 0; ct < NCT; ++ct) {
     f32x4 a = zero4();
     if (h0) {
-      const float* src = h0 + (size_t)bh * KD * VD;
+      const float* src = h0 + (size_t)bh * KD * VD;     // [K,V] or, state_v_first (vf), [V,K]
+      const int col = v_base + 16 * ct + (l & 15);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        a[r] = src[(16 * wv + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)];
+      for (int r = 0; r < 4; ++r) {
+        const int kr = 16 * wv + 4 * (l >> 4) + r;
+        a[r] = src[vf ? col * KD + kr : kr * VD + col];
+      }
     }
     st[ct] = a;
   }
@@ -441,8 +445,10 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        dst[(16 * wv + 4 * (l >> 4) + r) * VD + v_base + 16 * ct + (l & 15)] = st[ct][r];
+      for (int r = 0; r < 4; ++r) {
+        const int kr = 16 * wv + 4 * (l >> 4) + r, col = v_base + 16 * ct + (l & 15);
+        dst[vf ? col * KD + kr : kr * VD + col] = st[ct][r];
+      }
   }
 }
 
@@ -460,9 +466,9 @@ static hipError_t launch_prepare(const void* q, const void* k, const void* v, co
 template <int BV, int GATE>
 static hipError_t launch_fwd_h(const void* k, const void* w, const void* u, const float* g, const float* h0,
                                void* h, void* vnew, float* ht, int B, int T, int H, hipStream_t s,
-                               const int* co) {
+                               const int* co, int vf) {
   hipLaunchKernelGGL((fwd_h_kernel<BV, GATE>), dim3(B * H * (VD / BV)), dim3(512), 0, s, (const bf16*)k,
-                     (const bf16*)w, (const bf16*)u, g, h0, (bf16*)h, (bf16*)vnew, ht, T, H, co);
+                     (const bf16*)w, (const bf16*)u, g, h0, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf);
   return hipGetLastError();
 }
 
@@ -515,12 +521,12 @@ static int fwd_default_bv(int B, int H) {
 // B rows of T tokens, or (co) B sequences packed along T
 static hipError_t fwd_h_dispatch(const void* k, const void* w, const void* u, const float* g, int gate_mode,
                                  const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int K,
-                                 int V, int chunk, int value_block, hipStream_t stream, const int* co) {
+                                 int V, int chunk, int value_block, hipStream_t stream, const int* co, int vf) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
   if (!k || !w || !u || !h || !v_new) return hipErrorInvalidValue;
   if (gate_mode != RG_NONE && !g) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : fwd_default_bv(B, H);
-#define F_ARGS k, w, u, g, h0, h, v_new, ht, B, T, H, stream, co
+#define F_ARGS k, w, u, g, h0, h, v_new, ht, B, T, H, stream, co, vf
 #define F_BV(G)                                                     \
   switch (bv) {                                                     \
     case 16: return launch_fwd_h<16, G>(F_ARGS);                    \
@@ -539,17 +545,17 @@ static hipError_t fwd_h_dispatch(const void* k, const void* w, const void* u, co
 }
 
 extern "C" hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g, int gate_mode,
-                                const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int K,
-                                int V, int chunk, int value_block, hipStream_t stream) {
+                                const float* h0, void* h, void* v_new, float* ht, int state_v_first, int B, int T,
+                                int H, int K, int V, int chunk, int value_block, hipStream_t stream) {
   return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, B, T, H, K, V, chunk, value_block, stream,
-                        nullptr);
+                        nullptr, state_v_first ? 1 : 0);
 }
 
 extern "C" hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const float* g, int gate_mode,
-                                       const float* h0, void* h, void* v_new, float* ht, const int* chunk_offsets,
-                                       int N, int T, int H, int K, int V, int chunk, int value_block,
-                                       hipStream_t stream) {
+                                       const float* h0, void* h, void* v_new, float* ht, int state_v_first,
+                                       const int* chunk_offsets, int N, int T, int H, int K, int V, int chunk,
+                                       int value_block, hipStream_t stream) {
   if (!chunk_offsets) return hipErrorInvalidValue;
   return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, N, T, H, K, V, chunk, value_block, stream,
-                        chunk_offsets);
+                        chunk_offsets, state_v_first ? 1 : 0);
 }

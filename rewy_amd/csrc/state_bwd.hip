@@ -51,7 +51,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     const float* __restrict__ g, const bf16* __restrict__ dO, const float* __restrict__ aqk,
     const bf16* __restrict__ dv, const float* __restrict__ dht, bf16* __restrict__ dh_out,
     bf16* __restrict__ dr_out, float* __restrict__ dh0, int T, int H, float scale,
-    const int* __restrict__ chunk_off, int segs) {
+    const int* __restrict__ chunk_off, int segs, int vf) {
   using S = StateSmem<BV, GATE, DV_FROM_AQK>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
@@ -90,10 +90,11 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     f32x4 a = zero4();
     if (dht) {
       const float* init = dht + (size_t)bh * KD * VD;
+      const int col = v_base + 16 * (ct0 + j) + (l & 15);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int kr = 16 * rt + 4 * (l >> 4) + r;
-        a[r] = init[kr * VD + v_base + 16 * (ct0 + j) + (l & 15)];
+        a[r] = init[vf ? col * KD + kr : kr * VD + col];     // [K,V] or, state_v_first, [V,K]
       }
     }
     st[j] = a;
@@ -292,8 +293,8 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     for (int j = 0; j < NCW; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int kr = 16 * rt + 4 * (l >> 4) + r;
-        dst[kr * VD + v_base + 16 * (ct0 + j) + (l & 15)] = st[j][r];
+        const int kr = 16 * rt + 4 * (l >> 4) + r, col = v_base + 16 * (ct0 + j) + (l & 15);
+        dst[vf ? col * KD + kr : kr * VD + col] = st[j][r];
       }
   }
 }
@@ -308,13 +309,13 @@ template <int BV, int GATE, bool AQK>
 static hipError_t launch_state(const void* q, const void* k, const void* w, const float* g,
                                const void* dO, const float* aqk, const void* dv, const float* dht,
                                void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
-                               hipStream_t stream, const int* chunk_off, int segs = 0) {
+                               hipStream_t stream, const int* chunk_off, int segs = 0, int vf = 0) {
   const int rows = segs > 0 ? B * segs : B;
   const int grid = rows * H * (VD / BV);
   constexpr int NW = state_waves<BV>();
   hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW>), dim3(grid), dim3(64 * NW), 0, stream,
                      (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk,
-                     (const bf16*)dv, dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale, chunk_off, segs);
+                     (const bf16*)dv, dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale, chunk_off, segs, vf);
   return hipGetLastError();
 }
 
@@ -322,11 +323,11 @@ template <int GATE, bool AQK>
 static hipError_t pick_bv(int bv, const void* q, const void* k, const void* w, const float* g,
                           const void* dO, const float* aqk, const void* dv, const float* dht,
                           void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
-                          hipStream_t s, const int* co) {
+                          hipStream_t s, const int* co, int vf) {
   switch (bv) {
-    case 16: return launch_state<16, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co);
-    case 32: return launch_state<32, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co);
-    case 64: return launch_state<64, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co);
+    case 16: return launch_state<16, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf);
+    case 32: return launch_state<32, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf);
+    case 64: return launch_state<64, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf);
     default: return hipErrorInvalidValue;
   }
 }
@@ -527,13 +528,23 @@ constexpr int COMB_COLS = 8;
 __global__ __launch_bounds__(256) void state_combine_kernel(const float* __restrict__ pbuf,
                                                             const float* __restrict__ qbuf,
                                                             const float* __restrict__ dht, float* __restrict__ xbuf,
-                                                            float* __restrict__ dh0, int segs, int H) {
+                                                            float* __restrict__ dh0, int segs, int H, int vf) {
   __shared__ float pt[KD][KD + 1];      // P^T of the current segment (odd pitch: transposed writes spread over banks)
   __shared__ f32x4 xs[KD][COMB_COLS / 4];
   const int bh = blockIdx.x, row = bh / H, h = bh % H;
   const int tid = threadIdx.x, r = tid >> 1, hc = tid & 1;
   const int col = COMB_COLS * blockIdx.y + 4 * hc;
-  f32x4 x = dht ? *reinterpret_cast<const f32x4*>(dht + ((size_t)bh * KD + r) * VD + col) : zero4();
+  // dht / dh0 are [K,V] or (vf, state_v_first) [V,K] per (row, head)
+  f32x4 x = zero4();
+  if (dht) {
+    const float* d = dht + (size_t)bh * KD * VD;
+    if (vf) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = d[(col + e) * KD + r];
+    } else {
+      x = *reinterpret_cast<const f32x4*>(d + r * VD + col);
+    }
+  }
   f32x4 pre[KD * KD / 4 / 256];
   auto fetch = [&](int sg) {
     const float* P = pbuf + (((size_t)row * segs + sg) * H + h) * KD * KD;
@@ -568,14 +579,22 @@ __global__ __launch_bounds__(256) void state_combine_kernel(const float* __restr
     __syncthreads();
     x = acc;
   }
-  if (dh0) *reinterpret_cast<f32x4*>(dh0 + ((size_t)bh * KD + r) * VD + col) = x;
+  if (dh0) {
+    float* d = dh0 + (size_t)bh * KD * VD;
+    if (vf) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d[(col + e) * KD + r] = x[e];
+    } else {
+      *reinterpret_cast<f32x4*>(d + r * VD + col) = x;
+    }
+  }
 }
 
 template <int GATE, bool AQK>
 static hipError_t launch_segmented(const void* q, const void* k, const void* w, const float* g, const void* dO,
                                    const float* aqk, const void* dv, const float* dht, void* dh, void* dr,
                                    float* dh0, int B, int T, int H, float scale, int segs, int bv, float* ws,
-                                   hipStream_t s) {
+                                   int vf, hipStream_t s) {
   const size_t n = (size_t)B * segs * H * KD * VD;
   float* pbuf = ws;
   float* qbuf = ws + n;
@@ -589,7 +608,7 @@ static hipError_t launch_segmented(const void* q, const void* k, const void* w, 
   if (e != hipSuccess) return e;
   // 2. end states of every segment, sequential over segments
   hipLaunchKernelGGL(state_combine_kernel, dim3(B * H, VD / COMB_COLS), dim3(256), 0, s, pbuf, qbuf, dht, xbuf, dh0,
-                     segs, H);
+                     segs, H, vf);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   // 3. every segment from its end state: dh per chunk and dR
@@ -621,7 +640,7 @@ static int default_bv(int B, int H) {
 static hipError_t state_dispatch(const void* q, const void* k, const void* w, const float* g, int gate_mode,
                                  const void* dO, const float* aqk, const void* dv, const float* dht, void* dh,
                                  void* dr, float* dh0, int B, int T, int H, int K, int V, int chunk, float scale,
-                                 int value_block, hipStream_t stream, const int* co) {
+                                 int value_block, hipStream_t stream, const int* co, int vf) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0)
     return hipErrorInvalidValue;
   if (!q || !k || !w || !dO || !dh || !dr) return hipErrorInvalidValue;
@@ -629,7 +648,7 @@ static hipError_t state_dispatch(const void* q, const void* k, const void* w, co
   if (gate_mode != GATE_NONE && g == nullptr) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : default_bv(B, H);
   const bool from_aqk = aqk != nullptr;
-#define S_ARGS bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream, co
+#define S_ARGS bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream, co, vf
   switch (gate_mode) {
     case GATE_NONE:
       return from_aqk ? pick_bv<GATE_NONE, true>(S_ARGS) : pick_bv<GATE_NONE, false>(S_ARGS);
@@ -645,21 +664,21 @@ static hipError_t state_dispatch(const void* q, const void* k, const void* w, co
 
 extern "C" hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const float* g,
                                     int gate_mode, const void* dO, const float* aqk, const void* dv,
-                                    const float* dht, void* dh, void* dr, float* dh0, int B, int T,
-                                    int H, int K, int V, int chunk, float scale, int value_block,
+                                    const float* dht, void* dh, void* dr, float* dh0, int state_v_first,
+                                    int B, int T, int H, int K, int V, int chunk, float scale, int value_block,
                                     hipStream_t stream) {
   return state_dispatch(q, k, w, g, gate_mode, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, K, V, chunk, scale,
-                        value_block, stream, nullptr);
+                        value_block, stream, nullptr, state_v_first ? 1 : 0);
 }
 
 extern "C" hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, const float* g,
                                            int gate_mode, const void* dO, const float* aqk, const void* dv,
-                                           const float* dht, void* dh, void* dr, float* dh0,
+                                           const float* dht, void* dh, void* dr, float* dh0, int state_v_first,
                                            const int* chunk_offsets, int N, int T, int H, int K, int V,
                                            int chunk, float scale, int value_block, hipStream_t stream) {
   if (!chunk_offsets) return hipErrorInvalidValue;
   return state_dispatch(q, k, w, g, gate_mode, dO, aqk, dv, dht, dh, dr, dh0, N, T, H, K, V, chunk, scale,
-                        value_block, stream, chunk_offsets);
+                        value_block, stream, chunk_offsets, state_v_first ? 1 : 0);
 }
 
 extern "C" size_t fdr_state_bwd_segmented_workspace_bytes(int B, int H, int segments) {
@@ -669,7 +688,8 @@ extern "C" size_t fdr_state_bwd_segmented_workspace_bytes(int B, int H, int segm
 
 extern "C" hipError_t fdr_state_bwd_segmented(const void* q, const void* k, const void* w, const float* g,
                                               int gate_mode, const void* dO, const float* aqk, const void* dv,
-                                              const float* dht, void* dh, void* dr, float* dh0, int B, int T, int H,
+                                              const float* dht, void* dh, void* dr, float* dh0, int state_v_first,
+                                              int B, int T, int H,
                                               int K, int V, int chunk, float scale, int segments, int value_block,
                                               void* workspace, hipStream_t stream) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
@@ -681,7 +701,7 @@ extern "C" hipError_t fdr_state_bwd_segmented(const void* q, const void* k, cons
   if (bv != 16 && bv != 32 && bv != 64) return hipErrorInvalidValue;
   float* ws = reinterpret_cast<float*>(workspace);
   const bool a = aqk != nullptr;
-#define SEG_ARGS q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, segments, bv, ws, stream
+#define SEG_ARGS q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, segments, bv, ws, state_v_first ? 1 : 0, stream
   switch (gate_mode) {
     case GATE_NONE: return a ? launch_segmented<GATE_NONE, true>(SEG_ARGS) : launch_segmented<GATE_NONE, false>(SEG_ARGS);
     case GATE_SCALAR:

@@ -118,12 +118,13 @@ def _dims(q):
 
 
 def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, want_dh0=True,
-              value_block=0, method="auto", chunk_offsets=None, segments=0):
+              value_block=0, method="auto", chunk_offsets=None, segments=0, state_v_first=False):
     """Reverse state recurrence.  Returns (dh [B,NT,H,K,V] bf16, dR [B,T,H,V] bf16, dh0 fp32|None).
 
     ``chunk_offsets`` (int [N+1]): B = 1 holds N sequences packed along T, sequence n on
     chunks [chunk_offsets[n], chunk_offsets[n+1]); dht / dh0 are then [N,H,K,V] and the
-    direct kernel runs (fdr_state_bwd_varlen).
+    direct kernel runs (fdr_state_bwd_varlen).  ``state_v_first``: dht and dh0 are [.., V, K]
+    (FLA's layout); the per-chunk dh is [B,NT,H,K,V] either way.
 
     method "direct": one kernel (fdr_state_bwd); "affine": chunk-parallel step
     matrices, a one-product-per-chunk scan and a chunk-parallel dR pass
@@ -156,6 +157,7 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
     if value_block not in (0, 16, 32, 64):
         raise ValueError("value_block must be 0, 16, 32 or 64")
     NT = T // CHUNK
+    vf = int(bool(state_v_first))
     dh = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
     dr = torch.empty(B, T, H, V, device=dev, dtype=bf)
     dh0 = torch.empty(N, H, K, V, device=dev, dtype=f32) if want_dh0 else None
@@ -164,7 +166,7 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
         if method == "affine":
             raise ValueError("the affine-step form takes equal-length rows, not chunk_offsets")
         st = _lib.load().fdr_state_bwd_varlen(P(q), P(k), P(w), P(g), int(gate_mode), P(dO), P(aqk), P(dv),
-                                              P(dht), P(dh), P(dr), P(dh0), P(co), N, T, H, K, V, CHUNK,
+                                              P(dht), P(dh), P(dr), P(dh0), vf, P(co), N, T, H, K, V, CHUNK,
                                               float(scale), int(value_block), _lib.stream_handle(dev))
         _lib.check(st, "fdr_state_bwd_varlen")
         return dh, dr, dh0
@@ -176,7 +178,7 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
         lib = _lib.load()
         ws = torch.empty(lib.fdr_state_bwd_segmented_workspace_bytes(B, H, segs) // 4, device=dev, dtype=f32)
         st = lib.fdr_state_bwd_segmented(P(q), P(k), P(w), P(g), int(gate_mode), P(dO), P(aqk), P(dv), P(dht),
-                                         P(dh), P(dr), P(dh0), B, T, H, K, V, CHUNK, float(scale), segs,
+                                         P(dh), P(dr), P(dh0), vf, B, T, H, K, V, CHUNK, float(scale), segs,
                                          int(value_block), P(ws), _lib.stream_handle(dev))
         _lib.check(st, "fdr_state_bwd_segmented")
         return dh, dr, dh0
@@ -190,7 +192,7 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
                                      _lib.stream_handle(dev))
         _lib.check(st, "fdr_affine_prep_bwd")
         arr, n = _lib.problems(_lib.ScanProblem, [_lib.ScanProblem(
-            P(step), P(offset), P(g), P(dht), P(dh), P(dh0), int(gate_mode), 1)])
+            P(step), P(offset), P(g), P(dht), P(dh), P(dh0), int(gate_mode), 1, vf)])
         _lib.check(lib.fdr_affine_scan(arr, n, B, T, H, K, V, CHUNK, int(vb), _lib.stream_handle(dev)),
                    "fdr_affine_scan")
         arr, n = _lib.problems(_lib.SideProblem, [_lib.SideProblem(
@@ -199,14 +201,14 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
         _lib.check(lib.fdr_affine_side(arr, n, B, T, H, K, V, CHUNK, _lib.stream_handle(dev)), "fdr_affine_side")
         return dh, dr, dh0
     st = _lib.load().fdr_state_bwd(P(q), P(k), P(w), P(g), int(gate_mode), P(dO), P(aqk), P(dv),
-                                   P(dht), P(dh), P(dr), P(dh0), B, T, H, K, V, CHUNK,
+                                   P(dht), P(dh), P(dr), P(dh0), vf, B, T, H, K, V, CHUNK,
                                    float(scale), int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_state_bwd")
     return dh, dr, dh0
 
 
 def recurrences(q, k, w, u, g, gate_mode, dO, scale, aqk=None, dv=None, h0=None, dht=None, want_dh0=True,
-                value_block=0):
+                value_block=0, state_v_first=False):
     """Both state recurrences of the recompute policy in one pass of the affine-step
     kernels, the forward and the backward recurrence side by side (neither needs the
     other's states).  q/k as for ``state_bwd`` (qg/kg for a vector gate); w, u from
@@ -254,8 +256,8 @@ def recurrences(q, k, w, u, g, gate_mode, dO, scale, aqk=None, dv=None, h0=None,
                                         P(sb), P(ob), P(dv_local), P(sf), P(of), B, T, H, K, V, CHUNK,
                                         float(scale), stream), "fdr_affine_prep_pair")
     arr, n = _lib.problems(_lib.ScanProblem, [
-        _lib.ScanProblem(P(sb), P(ob), P(g), P(dht), P(dh), P(dh0), int(gate_mode), 1),
-        _lib.ScanProblem(P(sf), P(of), P(g), P(h0), P(h), None, int(gate_mode), 0)])
+        _lib.ScanProblem(P(sb), P(ob), P(g), P(dht), P(dh), P(dh0), int(gate_mode), 1, int(bool(state_v_first))),
+        _lib.ScanProblem(P(sf), P(of), P(g), P(h0), P(h), None, int(gate_mode), 0, int(bool(state_v_first)))])
     _lib.check(lib.fdr_affine_scan(arr, n, B, T, H, K, V, CHUNK, int(vb), stream), "fdr_affine_scan")
     arr, n = _lib.problems(_lib.SideProblem, [
         _lib.SideProblem(P(k), P(dh), P(dv_local if dv is None else dv),
@@ -266,7 +268,7 @@ def recurrences(q, k, w, u, g, gate_mode, dO, scale, aqk=None, dv=None, h0=None,
 
 
 def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None, b=None, w=None,
-              gate_fold=None, beta_sigmoid=0.0):
+              gate_fold=None, beta_sigmoid=0.0, h_v_first=False):
     """Fused residual-WY + matrix-intra + epilogue stage.
 
     ``gate_fold`` (KDA only) = dict(g_raw, A_log, dt_bias, lower_bound): the in-kernel gate's
@@ -275,6 +277,7 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
 
     ``beta_sigmoid`` = s > 0 (scalar beta): beta was activated as s * sigmoid(x) in the
     forward, and ``dbeta`` is returned as dL/dx (the reference's fused beta-sigmoid backward).
+    ``h_v_first`` (vector gates): the saved per-chunk states ``h`` are [B,NT,H,V,K].
 
     Returns dict(dq, dk, dv [bf16], dg [fp32, gate shape] | None, dbeta [fp32] | None,
     db, dw [bf16] | None)."""
@@ -307,9 +310,12 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
     beta_sigmoid = float(beta_sigmoid or 0.0)
     if beta_sigmoid < 0 or (beta_sigmoid and vec_b):
         raise ValueError("beta_sigmoid is a non-negative scale of a scalar beta")
+    hvf = int(bool(h_v_first))
+    if hvf and gate_mode != GATE_VECTOR:
+        raise ValueError("[V,K] saved states come with the vector-gate families")
     if gate_fold is not None:
         return _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, gate_fold,
-                                    beta_sigmoid)
+                                    beta_sigmoid, hvf)
     out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=bf),
                dk=torch.empty(B, T, H, K, device=dev, dtype=bf),
                dv=torch.empty(B, T, H, V, device=dev, dtype=bf),
@@ -321,13 +327,14 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
     st = _lib.load().fdr_chunk_bwd(P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), int(gate_mode),
                                    P(beta), P(b), P(w), P(Akk), P(h), P(dh), P(out["dq"]),
                                    P(out["dk"]), P(out["dv"]), P(out["dg"]), P(out["dbeta"]), beta_sigmoid,
-                                   P(out["db"]), P(out["dw"]), B, T, H, K, V, CHUNK, float(scale),
+                                   P(out["db"]), P(out["dw"]), hvf, B, T, H, K, V, CHUNK, float(scale),
                                    _lib.stream_handle(dev))
     _lib.check(st, "fdr_chunk_bwd")
     return out
 
 
-def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, fold, beta_sigmoid=0.0):
+def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, fold, beta_sigmoid=0.0,
+                         hvf=0):
     """chunk_bwd (KDA) with the gate backward folded into the dg stores."""
     B, T, H, K = q.shape
     V = V_SUPPORTED
@@ -357,7 +364,7 @@ def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale
                                      P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), beta_sigmoid, P(raw),
                                      int(raw.dtype == bf), P(a), P(dt), int(lb is not None),
                                      0.0 if lb is None else float(lb), P(out["dg"]), P(out["dA_log"]),
-                                     P(out["ddt_bias"]), P(ws), B, T, H, K, V, CHUNK, float(scale),
+                                     P(out["ddt_bias"]), P(ws), hvf, B, T, H, K, V, CHUNK, float(scale),
                                      _lib.stream_handle(dev))
     _lib.check(st, "fdr_chunk_bwd_gate_fold")
     return out
@@ -404,7 +411,7 @@ def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, 
 
 
 def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, method="auto",
-          chunk_offsets=None):
+          chunk_offsets=None, state_v_first=False):
     """Forward state scan.  Returns (h [B,NT,H,K,V] bf16, v_new [B,T,H,V] bf16, final fp32|None).
     ``method`` and ``chunk_offsets`` as for ``state_bwd`` (h0 / final per sequence)."""
     B, T, H, K = _dims(k)
@@ -426,6 +433,7 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
     if value_block not in (0, 16, 32, 64):
         raise ValueError("value_block must be 0, 16, 32 or 64")
     NT = T // CHUNK
+    vf = int(bool(state_v_first))
     h = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
     vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
     ht = torch.empty(N, H, K, V, device=dev, dtype=f32) if want_final else None
@@ -434,7 +442,7 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
         if method == "affine":
             raise ValueError("the affine-step form takes equal-length rows, not chunk_offsets")
         st = _lib.load().fdr_fwd_h_varlen(P(k), P(w), P(u), P(g), int(gate_mode), P(h0), P(h), P(vnew), P(ht),
-                                          P(co), N, T, H, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
+                                          vf, P(co), N, T, H, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
         _lib.check(st, "fdr_fwd_h_varlen")
         return h, vnew, ht
     if _use_affine(method, B, H, NT):
@@ -445,13 +453,13 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
                                      CHUNK, _lib.stream_handle(dev))
         _lib.check(st, "fdr_affine_prep_fwd")
         arr, n = _lib.problems(_lib.ScanProblem, [_lib.ScanProblem(
-            P(step), P(offset), P(g), P(h0), P(h), P(ht), int(gate_mode), 0)])
+            P(step), P(offset), P(g), P(h0), P(h), P(ht), int(gate_mode), 0, vf)])
         _lib.check(lib.fdr_affine_scan(arr, n, B, T, H, K, V, CHUNK, int(vb), _lib.stream_handle(dev)),
                    "fdr_affine_scan")
         arr, n = _lib.problems(_lib.SideProblem, [_lib.SideProblem(P(w), P(h), P(u), None, P(vnew), -1.0)])
         _lib.check(lib.fdr_affine_side(arr, n, B, T, H, K, V, CHUNK, _lib.stream_handle(dev)), "fdr_affine_side")
         return h, vnew, ht
-    st = _lib.load().fdr_fwd_h(P(k), P(w), P(u), P(g), int(gate_mode), P(h0), P(h), P(vnew), P(ht), B, T, H,
+    st = _lib.load().fdr_fwd_h(P(k), P(w), P(u), P(g), int(gate_mode), P(h0), P(h), P(vnew), P(ht), vf, B, T, H,
                                K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_h")
     return h, vnew, ht

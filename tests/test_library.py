@@ -30,14 +30,14 @@ def test_entry_points_reject_unsupported_shapes_without_touching_the_gpu():
     from rewy_amd import _lib
     lib = _lib.load()
     # K = 64 (only 128 supported)
-    st = lib.fdr_state_bwd(None, None, None, None, 2, None, None, None, None, None, None, None,
+    st = lib.fdr_state_bwd(None, None, None, None, 2, None, None, None, None, None, None, None, 0,
                            1, 128, 1, 64, 128, 64, 1.0, 0, None)
     assert st == HIP_ERROR_INVALID_VALUE
     # T not a multiple of 64
-    st = lib.fdr_chunk_bwd(*([None] * 7), 2, *([None] * 11), 0.0, None, None, 1, 100, 1, 128, 128, 64, 1.0, None)
+    st = lib.fdr_chunk_bwd(*([None] * 7), 2, *([None] * 11), 0.0, None, None, 0, 1, 100, 1, 128, 128, 64, 1.0, None)
     assert st == HIP_ERROR_INVALID_VALUE
     # null pointers with a valid shape
-    st = lib.fdr_chunk_bwd(*([None] * 7), 2, *([None] * 11), 0.0, None, None, 1, 128, 1, 128, 128, 64, 1.0, None)
+    st = lib.fdr_chunk_bwd(*([None] * 7), 2, *([None] * 11), 0.0, None, None, 0, 1, 128, 1, 128, 128, 64, 1.0, None)
     assert st == HIP_ERROR_INVALID_VALUE
     # matrix intra: chunk 32, then null operands
     st = lib.fdr_matrix_intra(*([None] * 11), 1, 128, 1, 128, 32, 0, None)
