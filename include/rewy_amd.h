@@ -15,6 +15,11 @@
  *   beta                    fp32  [B, T, H]
  *   b_gate / w_gate (GDN2)  bf16  [B, T, H, K] / [B, T, H, V]
  * Supported shapes: K = V = 128, chunk = 64, T a positive multiple of 64.
+ * Grouped value heads (FLA's GVA, reference _compat/kda.py:485-493): where an entry point
+ * takes `qk_heads` (or `k_heads`), the raw q / k (and, for scalar gates, the q / k a state
+ * recurrence reads) have that many heads, [B,T,qk_heads,K], and value head h uses q / k head
+ * h / (H / qk_heads); every other per-head tensor has H heads.  0 means H.  The gradients
+ * dq / dk are written per value head ([B,T,H,K]); summing each group is the caller's.
  * gate_mode: 0 = none (DeltaNet), 1 = scalar (GDN), 2 = vector (KDA, GDN2).
  */
 #ifndef REWY_AMD_H
@@ -44,7 +49,7 @@ extern "C" {
 hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const float* g,
                          int gate_mode, const void* dO, const float* aqk, const void* dv,
                          const float* dht, void* dh, void* dr, float* dh0, int state_v_first, int B,
-                         int T, int H, int K, int V, int chunk, float scale, int value_block,
+                         int T, int H, int qk_heads, int K, int V, int chunk, float scale, int value_block,
                          hipStream_t stream);
 
 /*
@@ -59,7 +64,7 @@ hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const floa
  */
 hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, const float* g, int gate_mode,
                                 const void* dO, const float* aqk, const void* dv, const float* dht, void* dh,
-                                void* dr, float* dh0, int state_v_first, const int* chunk_offsets, int N, int T, int H, int K,
+                                void* dr, float* dh0, int state_v_first, const int* chunk_offsets, int N, int T, int H, int qk_heads, int K,
                                 int V, int chunk, float scale, int value_block, hipStream_t stream);
 
 /*
@@ -118,7 +123,7 @@ hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v, const void
                          const float* beta, const void* b_gate, const void* w_gate,
                          const float* Akk, const void* h, const void* dh, void* dq, void* dk,
                          void* dv, float* dg, float* dbeta, float beta_sigmoid, void* db, void* dw,
-                         int h_v_first, int B, int T, int H, int K, int V, int chunk, float scale,
+                         int h_v_first, int B, int T, int H, int qk_heads, int K, int V, int chunk, float scale,
                          hipStream_t stream);
 
 /*
@@ -133,7 +138,7 @@ hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v, const void
 hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const float* g,
                           int gate_mode, const float* beta, const void* b_gate, const void* w_gate,
                           const float* Akk, void* w, void* u, void* qg, void* kg, float* Aqk, int B,
-                          int T, int H, int K, int V, int chunk, float scale, hipStream_t stream);
+                          int T, int H, int qk_heads, int K, int V, int chunk, float scale, hipStream_t stream);
 
 /*
  * Forward state scan recomputed inside the backward.
@@ -145,7 +150,7 @@ hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const flo
  * state_v_first != 0: h0 and ht are [B,H,V,K]; the per-chunk h stays [B,T/64,H,K,V].
  */
 hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g, int gate_mode,
-                     const float* h0, void* h, void* v_new, float* ht, int state_v_first, int B, int T, int H,
+                     const float* h0, void* h, void* v_new, float* ht, int state_v_first, int B, int T, int H, int k_heads,
                      int K, int V, int chunk, int value_block, hipStream_t stream);
 
 /*
@@ -156,7 +161,7 @@ hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g
 hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const float* g, int gate_mode,
                             const float* h0, void* h, void* v_new, float* ht, int state_v_first,
                             const int* chunk_offsets, int N,
-                            int T, int H, int K, int V, int chunk, int value_block, hipStream_t stream);
+                            int T, int H, int k_heads, int K, int V, int chunk, int value_block, hipStream_t stream);
 
 /*
  * Standalone matrix intra (the intra-chunk VJP of a vector-gated chunk), in place.
@@ -178,7 +183,7 @@ hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const f
  */
 hipError_t fdr_matrix_intra(const void* q, const void* k, const float* g, const float* beta,
                             const void* b_gate, const float* dAqk, const float* dAkk, float* dq,
-                            float* dk, float* db, float* dg, int B, int T, int H, int K, int chunk,
+                            float* dk, float* db, float* dg, int B, int T, int H, int qk_heads, int K, int chunk,
                             int beta_complete, hipStream_t stream);
 
 /*
@@ -195,7 +200,7 @@ hipError_t fdr_matrix_intra(const void* q, const void* k, const float* g, const 
  */
 hipError_t fdr_fwd_prepare(const void* q, const void* k, const float* g, int gate_mode,
                            const float* beta, const void* b_gate, float* gc, float* Aqk, float* Akk,
-                           int B, int T, int H, int K, int chunk, float scale, hipStream_t stream);
+                           int B, int T, int H, int qk_heads, int K, int chunk, float scale, hipStream_t stream);
 
 /*
  * Forward, chunk-parallel part 2: the output.  Replaces FLA's chunk_fwd_o:
@@ -203,7 +208,7 @@ hipError_t fdr_fwd_prepare(const void* q, const void* k, const float* g, int gat
  * with h (bf16 [B,T/64,H,K,V]) and v_new from fdr_fwd_h and Aqk from fdr_fwd_prepare.
  */
 hipError_t fdr_fwd_o(const void* q, const float* gc, int gate_mode, const float* Aqk, const void* h,
-                     const void* v_new, void* o, int B, int T, int H, int K, int V, int chunk,
+                     const void* v_new, void* o, int B, int T, int H, int qk_heads, int K, int V, int chunk,
                      float scale, hipStream_t stream);
 
 /*
@@ -246,7 +251,7 @@ hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, const void* v, 
                                    const void* h, const void* dh, void* dq, void* dk, void* dv, float* dbeta,
                                    float beta_sigmoid, const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
                                    int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
-                                   float* ddt_bias, void* workspace, int h_v_first, int B, int T, int H, int K, int V,
+                                   float* ddt_bias, void* workspace, int h_v_first, int B, int T, int H, int qk_heads, int K, int V,
                                    int chunk,
                                    float scale, hipStream_t stream);
 
@@ -270,7 +275,7 @@ hipError_t fdr_chunk_bwd_gate_fold_noalloc(const void* q, const void* k, const v
                                            void* dv, float* dbeta, float beta_sigmoid, const void* g_raw,
                                            int raw_is_bf16, const float* A_log, const float* dt_bias,
                                            int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
-                                           float* ddt_bias, int h_v_first, int B, int T, int H, int K, int V, int chunk,
+                                           float* ddt_bias, int h_v_first, int B, int T, int H, int qk_heads, int K, int V, int chunk,
                                            float scale, hipStream_t stream);
 
 /*

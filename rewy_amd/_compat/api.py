@@ -229,8 +229,10 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
            state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None, gate_fold=None, beta_act=None):
     """Layout adapters around the chunk Function (all autograd-transparent torch ops):
 
-    * grouped value heads (HV = v.shape[2] > H): q and k are repeated over each
-      group of HV / H value heads (FLA's head map i_h = i_hv // (HV / H));
+    * grouped value heads (HV = v.shape[2] > H): the optimized GPU path hands q and k
+      over with their H heads and the kernels map value head i_hv to q / k head
+      i_hv // (HV / H) (FLA's head map; dq / dk summed over each group); the torch paths
+      repeat q and k over each group;
     * ``state_v_first``: initial / final states are [N, HV, V, K] at the boundary;
     * ``cu_seqlens`` (B = 1, packed): on the optimized backend on a GPU every
       sequence is zero-padded to whole 64-token chunks and the sequences stay packed
@@ -270,10 +272,12 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
     if HV != H:
         if HV % H:
             raise ValueError(f"num_v_heads (HV={HV}) must be divisible by num_qk_heads (H={H})")
-        q = q.repeat_interleave(HV // H, dim=2)
-        k = k.repeat_interleave(HV // H, dim=2)
-        if b is not None:
-            b = b.repeat_interleave(HV // H, dim=2)
+        if not (native and op in ("kda", "gdn", "delta")):
+            # the torch paths (and GDN2) take one q / k head per value head
+            q = q.repeat_interleave(HV // H, dim=2)
+            k = k.repeat_interleave(HV // H, dim=2)
+            if b is not None:
+                b = b.repeat_interleave(HV // H, dim=2)
     # V-first states: read and written in that layout by the kernels on the optimized GPU
     # path; transposed here for the torch paths
     vf = bool(state_v_first) and native

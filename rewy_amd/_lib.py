@@ -16,32 +16,31 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
 SIGNATURES = {
-    "fdr_state_bwd": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P],
-    "fdr_state_bwd_segmented": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
-                                _I, _I, _P, _P],
-    "fdr_chunk_bwd": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P,
-                      _I, _I, _I, _I, _I, _I, _I, _F, _P],
-    "fdr_prepare_wu": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
-    "fdr_fwd_h": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
-    "fdr_state_bwd_varlen": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,
-                             _F, _I, _P],
-    "fdr_fwd_h_varlen": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P],
-    "fdr_matrix_intra": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
-    "fdr_fwd_prepare": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P],
-    "fdr_fwd_o": [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
+    "fdr_state_bwd": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P],
+    "fdr_state_bwd_segmented": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I,
+                                _I, _P, _P],
+    "fdr_chunk_bwd": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I,
+                      _I, _I, _I, _I, _I, _I, _F, _P],
+    "fdr_prepare_wu": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P],
+    "fdr_fwd_h": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P],
+    "fdr_state_bwd_varlen": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _F,
+                             _I, _P],
+    "fdr_fwd_h_varlen": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
+    "fdr_matrix_intra": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
+    "fdr_fwd_prepare": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
+    "fdr_fwd_o": [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_affine_prep_bwd": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_affine_prep_fwd": [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P],
-    "fdr_affine_prep_pair": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
-                             _F, _P],
+    "fdr_affine_prep_pair": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_kda_gate_fwd": [_P, _I, _P, _P, _I, _F, _P, _I, _I, _I, _I, _P],
     "fdr_kda_gate_bwd": [_P, _P, _I, _P, _P, _I, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "fdr_beta_sigmoid_fwd": [_P, _I, _F, _P, ctypes.c_longlong, _P],
     "fdr_l2norm_fwd": [_P, _I, _P, _P, ctypes.c_longlong, _I, _F, _P],
     "fdr_l2norm_bwd": [_P, _I, _P, _P, _P, ctypes.c_longlong, _I, _P],
-    "fdr_chunk_bwd_gate_fold": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _P, _P, _I, _F,
-                                _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P],
+    "fdr_chunk_bwd_gate_fold": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _P, _P, _I,
+                                _F, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_chunk_bwd_gate_fold_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _P,
-                                        _P, _I, _F, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P],
+                                        _P, _I, _F, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_affine_scan": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
     "fdr_affine_side": [_P, _I, _I, _I, _I, _I, _I, _I, _P],
 }

@@ -72,6 +72,17 @@ def _bf(x):
     return x.to(torch.bfloat16).contiguous()
 
 
+def _group_sum(out, HQ):
+    """Grouped value heads: dq / dk come per value head; q / k's gradient is the sum over
+    each head's group (FLA's head map i_h = i_hv // (HV / H)), formed in fp32."""
+    for n in ("dq", "dk"):
+        x = out[n]
+        B, T, H, K = x.shape
+        if H != HQ:
+            out[n] = x.view(B, T, HQ, H // HQ, K).float().sum(3).to(x.dtype)
+    return out
+
+
 def _f32(x):
     return None if x is None else x.to(torch.float32).contiguous()
 
@@ -88,7 +99,7 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
     g = _f32(g)
     Aqk, Akk = _f32(Aqk), _f32(Akk)
-    if saved.get("h") is None and co is None and ops.affine_pays(q):
+    if saved.get("h") is None and co is None and ops.affine_pays(v):
         # recompute policy, few heads: both recurrences side by side in affine-step form
         pre = _prepare_vector(k, v, g, Akk, gates, q)
         h, v_new, dh, dR, dh0 = ops.recurrences(pre["qg"], pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR,
@@ -104,7 +115,7 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
                         b=None if gates.get("b") is None else _bf(gates["b"]),
                         w=None if gates.get("w") is None else _bf(gates["w"]), gate_fold=gate_fold,
                         beta_sigmoid=beta_sigmoid, h_v_first=hvf)
-    return out, dh0
+    return _group_sum(out, q.shape[2]), dh0
 
 
 def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, co=None, vf=False):
@@ -189,7 +200,7 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
     beta = _f32(beta)
     gate = ops.GATE_SCALAR if op == "gdn" else ops.GATE_NONE
     pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, q=q, want_aqk=True, scale=scale)
-    if co is None and ops.affine_pays(q):
+    if co is None and q.shape[2] == v.shape[2] and ops.affine_pays(v):
         # few heads: both recurrences side by side in affine-step form
         h, v_new, dh, dR, dh0 = ops.recurrences(q, k, pre["w"], pre["u"], g, gate, do, scale, aqk=pre["Aqk"],
                                                 h0=_f32(initial_state), dht=_f32(dht),
@@ -200,7 +211,8 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
         dh, dR, dh0 = ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
                                     want_dh0=initial_state is not None, method="auto" if co is None else "direct",
                                     chunk_offsets=co, state_v_first=state_v_first)
-    out = ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta, beta_sigmoid=beta_sigmoid)
+    out = _group_sum(ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta,
+                                   beta_sigmoid=beta_sigmoid), q.shape[2])
     record(op, "optimized_backward")
     return out, dh0
 

@@ -184,13 +184,14 @@ constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) 
 template <int GATE>
 __device__ __forceinline__ void dma_qkg(bf16* sQ, bf16* sK, float* sGr, const bf16* __restrict__ q,
                                         const bf16* __restrict__ k, const float* __restrict__ g,
-                                        const ChunkItem& it, int H, int tid) {
+                                        const ChunkItem& it, int H, int HQ, int tid) {
   const size_t rsk = (size_t)H * KD;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
+  const QKRows qr = qk_rows(it.tok0, it.h, H, HQ);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    dma_rows4(sQ, 8 * w + 4 * j, q + it.kofs, rsk, l);
-    dma_rows4(sK, 8 * w + 4 * j, k + it.kofs, rsk, l);
+    dma_rows4(sQ, 8 * w + 4 * j, q + qr.ofs, qr.rs, l);
+    dma_rows4(sK, 8 * w + 4 * j, k + qr.ofs, qr.rs, l);
   }
   if constexpr (GATE == CG_VECTOR) {
 #pragma unroll
@@ -247,7 +248,8 @@ __device__ __forceinline__ void chunk_body(
     const float* __restrict__ daqk, float* __restrict__ dq32, float* __restrict__ dk32,
     float* __restrict__ db32, int beta_complete, int item, int next_item, char* regA, char* regB,
     float* small, bf16* xbuf, float* gbuf, PhaseIn& pin, const GateFoldArgs* gf = nullptr,
-    float beta_sig = 0.f) {
+    float beta_sig = 0.f, int HQ = 0) {
+  if (HQ <= 0) HQ = H;
   using LY = PostLayout<GATE, VEC_B, INTRA, PIPE>;
   using post::LDT;
   auto B16 = [&](int off) { return reinterpret_cast<bf16*>(regA + off); };
@@ -378,7 +380,7 @@ __device__ __forceinline__ void chunk_body(
     for (int w = 0; w < 8; ++w) any_fb |= sAny[w];
     // persistent kernel: this item's q, k, g stream into region B during phases
     // 1-3 (issued after this phase's LDS writes, see dma_x's call below)
-    if constexpr (PIPE) dma_qkg<GATE>(sQ, sK, sGr, q, k, g, pos, H, tid);
+    if constexpr (PIPE) dma_qkg<GATE>(sQ, sK, sGr, q, k, g, pos, H, HQ, tid);
   }
   // the standalone intra adds the direct dbeta terms of every row
   const bool has_fb = !VEC_B && (INTRA || any_fb != 0);
@@ -578,12 +580,14 @@ __device__ __forceinline__ void chunk_body(
     // q, k, g (and b) rows for the row-major staging (issued before the barrier)
     u32x4 rq[2], rk[2], rb[2];
     f32x4 rg[4];
+    const QKRows qr = qk_rows(tok0, h, H, HQ);       // raw q / k (grouped value heads: HQ < H)
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + 512 * i;
       const size_t o = kofs + (size_t)(p >> 4) * rsk + (p & 15) * 8;
-      rq[i] = *reinterpret_cast<const u32x4*>(q + o);
-      rk[i] = *reinterpret_cast<const u32x4*>(k + o);
+      const size_t oq = qr.ofs + (size_t)(p >> 4) * qr.rs + (p & 15) * 8;
+      rq[i] = *reinterpret_cast<const u32x4*>(q + oq);
+      rk[i] = *reinterpret_cast<const u32x4*>(k + oq);
       if constexpr (VEC_B) rb[i] = *reinterpret_cast<const u32x4*>(bgate + o);
     }
     if constexpr (GATE == CG_VECTOR) {
@@ -1101,7 +1105,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     const bf16* __restrict__ wgate, const float* __restrict__ akk, const bf16* __restrict__ hst,
     const bf16* __restrict__ dhst, bf16* __restrict__ dq_out, bf16* __restrict__ dk_out,
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
-    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale, float beta_sig) {
+    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale, float beta_sig, int HQ) {
   using LY = PostLayout<GATE, VEC_B>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
@@ -1109,7 +1113,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
                                  dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale, nullptr,
                                  nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
                                  reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
-                                 nullptr, beta_sig);
+                                 nullptr, beta_sig, HQ);
 }
 
 // KDA with the gate backward folded into the dg stores (no dg output)
@@ -1120,7 +1124,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_fold_kernel(
     const float* __restrict__ g, const float* __restrict__ beta, const float* __restrict__ akk,
     const bf16* __restrict__ hst, const bf16* __restrict__ dhst, bf16* __restrict__ dq_out,
     bf16* __restrict__ dk_out, bf16* __restrict__ dv_out, float* __restrict__ dbeta_out, int T, int H,
-    float scale, GateFoldArgs gf, float beta_sig) {
+    float scale, GateFoldArgs gf, float beta_sig, int HQ) {
   using LY = PostLayout<CG_VECTOR, false>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
@@ -1128,7 +1132,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_fold_kernel(
       q, k, v, vnew, dO, dR, g, beta, nullptr, nullptr, akk, hst, dhst, dq_out, dk_out, dv_out, nullptr, dbeta_out,
       nullptr, nullptr, T, H, scale, nullptr, nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem,
       smem + LY::REGION_A, reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
-      &gf, beta_sig);
+      &gf, beta_sig, HQ);
 }
 
 // Persistent form: one work-group per CU walks the items blockIdx.x, + gridDim.x, ...
@@ -1147,7 +1151,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
     const bf16* __restrict__ dhst, bf16* __restrict__ dq_out, bf16* __restrict__ dk_out,
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
     bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale, int items,
-    float beta_sig) {
+    float beta_sig, int HQ) {
   using LY = PostLayout<GATE, VEC_B, false, true>;
   __shared__ __attribute__((aligned(16))) bf16 xbuf[3 * C * KD];
   __shared__ __attribute__((aligned(16))) char regA[LY::REGION_A];
@@ -1171,7 +1175,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
     chunk_body<GATE, VEC_B, false, true>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
                                          dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale,
                                          nullptr, nullptr, nullptr, nullptr, 0, it, nx < items ? nx : -1, regA,
-                                         regB, small, xbuf, gbuf, pin, nullptr, beta_sig);
+                                         regB, small, xbuf, gbuf, pin, nullptr, beta_sig, HQ);
   }
 }
 
@@ -1180,7 +1184,7 @@ __global__ __launch_bounds__(512) void matrix_intra_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ g,
     const float* __restrict__ beta, const bf16* __restrict__ bgate, const float* __restrict__ daqk,
     const float* __restrict__ dakk, float* __restrict__ dq, float* __restrict__ dk,
-    float* __restrict__ db, float* __restrict__ dg, int T, int H, int beta_complete) {
+    float* __restrict__ db, float* __restrict__ dg, int T, int H, int beta_complete, int HQ) {
   using LY = PostLayout<CG_VECTOR, VEC_B, true>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
@@ -1188,7 +1192,8 @@ __global__ __launch_bounds__(512) void matrix_intra_kernel(
                                      nullptr, nullptr, nullptr, nullptr, nullptr, dg, VEC_B ? nullptr : db,
                                      nullptr, nullptr, T, H, 1.f, daqk, dq, dk, VEC_B ? db : nullptr,
                                      beta_complete, blockIdx.x, -1, smem, smem + LY::REGION_A,
-                                     reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin);
+                                     reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
+                                     nullptr, 0.f, HQ);
 }
 
 // Per-device, once: raise a kernel's dynamic-LDS limit (the attribute is held per
@@ -1230,7 +1235,7 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
                               const void* dO, const void* dR, const float* g, const float* beta,
                               const void* bgate, const void* wgate, const float* akk, const void* h,
                               const void* dh, void* dq, void* dk, void* dv, float* dg, float* dbeta,
-                              void* db, void* dw, int B, int T, int H, float scale, float beta_sig,
+                              void* db, void* dw, int B, int T, int H, int HQ, float scale, float beta_sig,
                               hipStream_t s) {
   const int items = B * H * (T / C);
   using LP = PostLayout<GATE, VEC_B, false, true>;
@@ -1245,7 +1250,7 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
                        (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta,
                        (const bf16*)bgate, (const bf16*)wgate, akk, (const bf16*)h, (const bf16*)dh,
                        (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, items,
-                       beta_sig);
+                       beta_sig, HQ);
     return hipGetLastError();
   }
   using LY = PostLayout<GATE, VEC_B>;
@@ -1257,7 +1262,7 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
   hipLaunchKernelGGL(kern, dim3(grid), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta,
                      (const bf16*)bgate, (const bf16*)wgate, akk, (const bf16*)h, (const bf16*)dh,
-                     (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, beta_sig);
+                     (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, beta_sig, HQ);
   return hipGetLastError();
 }
 
@@ -1270,10 +1275,12 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
                                     const float* beta, const void* b_gate, const void* w_gate,
                                     const float* Akk, const void* h, const void* dh, void* dq,
                                     void* dk, void* dv, float* dg, float* dbeta, float beta_sigmoid,
-                                    void* db, void* dw, int h_v_first, int B, int T, int H, int K, int V,
-                                    int chunk, float scale, hipStream_t stream) {
+                                    void* db, void* dw, int h_v_first, int B, int T, int H, int qk_heads,
+                                    int K, int V, int chunk, float scale, hipStream_t stream) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0)
     return hipErrorInvalidValue;
+  const int HQ = qk_heads > 0 ? qk_heads : H;
+  if (H % HQ || (b_gate && HQ != H)) return hipErrorInvalidValue;
   if (!(beta_sigmoid >= 0.f) || (beta_sigmoid > 0.f && b_gate)) return hipErrorInvalidValue;
   if (!q || !k || !v || !v_new || !dO || !dR || !Akk || !h || !dh || !dq || !dk || !dv)
     return hipErrorInvalidValue;
@@ -1284,7 +1291,7 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
   if (vec_b && gate_mode != CG_VECTOR) return hipErrorInvalidValue;
 #define FDR_POST(G, VB, HV)                                                                     \
   return launch_post<G, VB, HV>(q, k, v, v_new, dO, dR, g, beta, b_gate, w_gate, Akk, h, dh, dq, dk, \
-                                dv, dg, dbeta, db, dw, B, T, H, scale, beta_sigmoid, stream)
+                                dv, dg, dbeta, db, dw, B, T, H, HQ, scale, beta_sigmoid, stream)
   if (h_v_first) {
     // [V,K] states come from a saved forward: the vector-gate families (full saving)
     if (gate_mode != CG_VECTOR) return hipErrorInvalidValue;
@@ -1318,9 +1325,11 @@ static hipError_t gate_fold_launch(const void* q, const void* k, const void* v, 
                                    const void* dh, void* dq, void* dk, void* dv, float* dbeta, float beta_sigmoid,
                                    const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
                                    int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
-                                   float* ddt_bias, void* workspace, int h_v_first, int B, int T, int H, int K, int V,
-                                   int chunk, float scale, hipStream_t stream) {
+                                   float* ddt_bias, void* workspace, int h_v_first, int B, int T, int H, int qk_heads,
+                                   int K, int V, int chunk, float scale, hipStream_t stream) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  const int HQ = qk_heads > 0 ? qk_heads : H;
+  if (H % HQ) return hipErrorInvalidValue;
   if (!q || !k || !v || !v_new || !dO || !dR || !g || !beta || !Akk || !h || !dh || !dq || !dk || !dv || !dbeta)
     return hipErrorInvalidValue;
   if (!g_raw || !dg_raw || !workspace || !(beta_sigmoid >= 0.f)) return hipErrorInvalidValue;
@@ -1347,7 +1356,7 @@ static hipError_t gate_fold_launch(const void* q, const void* k, const void* v, 
   hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, stream, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, (const bf16*)v_new, (const bf16*)dO, (const bf16*)dR, g, beta, Akk,
                      (const bf16*)h, (const bf16*)dh, (bf16*)dq, (bf16*)dk, (bf16*)dv, dbeta, T, H, scale, gf,
-                     beta_sigmoid);
+                     beta_sigmoid, HQ);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   return kda_gate_partials_sum(part_dt, part_da, nblk, H * KD, 8, ddt_bias, dA_log, stream);
@@ -1360,16 +1369,17 @@ extern "C" hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, cons
                                               int raw_is_bf16, const float* A_log, const float* dt_bias,
                                               int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
                                               float* ddt_bias, void* workspace, int h_v_first, int B, int T, int H,
-                                              int K, int V, int chunk, float scale, hipStream_t stream) {
+                                              int qk_heads, int K, int V, int chunk, float scale,
+                                              hipStream_t stream) {
   return gate_fold_launch(q, k, v, v_new, dO, dR, g, beta, Akk, h, dh, dq, dk, dv, dbeta, beta_sigmoid, g_raw,
                           raw_is_bf16, A_log, dt_bias, has_lower_bound, lower_bound, dg_raw, dA_log, ddt_bias,
-                          workspace, h_v_first, B, T, H, K, V, chunk, scale, stream);
+                          workspace, h_v_first, B, T, H, qk_heads, K, V, chunk, scale, stream);
 }
 
 template <bool VEC_B>
 static hipError_t launch_intra(const void* q, const void* k, const float* g, const float* beta,
                                const void* bgate, const float* daqk, const float* dakk, float* dq,
-                               float* dk, float* db, float* dg, int B, int T, int H, int beta_complete,
+                               float* dk, float* db, float* dg, int B, int T, int H, int HQ, int beta_complete,
                                hipStream_t s) {
   using LY = PostLayout<CG_VECTOR, VEC_B, true>;
   auto kern = matrix_intra_kernel<VEC_B>;
@@ -1377,19 +1387,21 @@ static hipError_t launch_intra(const void* q, const void* k, const float* g, con
   const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k, g,
-                     beta, (const bf16*)bgate, daqk, dakk, dq, dk, db, dg, T, H, beta_complete);
+                     beta, (const bf16*)bgate, daqk, dakk, dq, dk, db, dg, T, H, beta_complete, HQ);
   return hipGetLastError();
 }
 
 extern "C" hipError_t fdr_matrix_intra(const void* q, const void* k, const float* g, const float* beta,
                                        const void* b_gate, const float* dAqk, const float* dAkk, float* dq,
-                                       float* dk, float* db, float* dg, int B, int T, int H, int K,
+                                       float* dk, float* db, float* dg, int B, int T, int H, int qk_heads, int K,
                                        int chunk, int beta_complete, hipStream_t stream) {
   if (K != KD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
   if (!q || !k || !g || !dAqk || !dAkk || !dq || !dk || !db || !dg) return hipErrorInvalidValue;
-  if (b_gate) return launch_intra<true>(q, k, g, nullptr, b_gate, dAqk, dAkk, dq, dk, db, dg, B, T, H, 0, stream);
+  const int HQ = qk_heads > 0 ? qk_heads : H;
+  if (H % HQ || (b_gate && HQ != H)) return hipErrorInvalidValue;
+  if (b_gate) return launch_intra<true>(q, k, g, nullptr, b_gate, dAqk, dAkk, dq, dk, db, dg, B, T, H, HQ, 0, stream);
   if (!beta) return hipErrorInvalidValue;
-  return launch_intra<false>(q, k, g, beta, nullptr, dAqk, dAkk, dq, dk, db, dg, B, T, H, beta_complete, stream);
+  return launch_intra<false>(q, k, g, beta, nullptr, dAqk, dAkk, dq, dk, db, dg, B, T, H, HQ, beta_complete, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -1433,7 +1445,7 @@ extern "C" hipError_t fdr_chunk_bwd_gate_fold_noalloc(
     const float* beta, const float* Akk, const void* h, const void* dh, void* dq, void* dk, void* dv, float* dbeta,
     float beta_sigmoid, const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
     int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log, float* ddt_bias, int h_v_first, int B,
-    int T, int H, int K, int V, int chunk, float scale, hipStream_t stream) {
+    int T, int H, int qk_heads, int K, int V, int chunk, float scale, hipStream_t stream) {
   const size_t need = fdr_chunk_bwd_gate_workspace_bytes(B, T, H);
   if (need == 0 || need > FDR_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
   void* ws = nullptr;
@@ -1441,5 +1453,5 @@ extern "C" hipError_t fdr_chunk_bwd_gate_fold_noalloc(
   if (e != hipSuccess) return e;
   return gate_fold_launch(q, k, v, v_new, dO, dR, g, beta, Akk, h, dh, dq, dk, dv, dbeta, beta_sigmoid, g_raw,
                           raw_is_bf16, A_log, dt_bias, has_lower_bound, lower_bound, dg_raw, dA_log, ddt_bias, ws,
-                          h_v_first, B, T, H, K, V, chunk, scale, stream);
+                          h_v_first, B, T, H, qk_heads, K, V, chunk, scale, stream);
 }

@@ -79,6 +79,17 @@ __device__ __forceinline__ int xcd_logical_block() {
   return (b % 8) * (n / 8) + b / 8;
 }
 
+// q / k may have fewer heads (HQ) than the value side (H): grouped value heads, FLA's head
+// map i_h = i_hv / (H / HQ).  Offset of the row of token tok0 of q / k for value head h,
+// and the distance between consecutive tokens.
+struct QKRows {
+  size_t ofs, rs;
+};
+__device__ __forceinline__ QKRows qk_rows(size_t tok0, int h, int H, int HQ) {
+  const size_t rs = (size_t)HQ * KD;
+  return QKRows{tok0 * rs + (size_t)(h / (H / HQ)) * KD, rs};
+}
+
 // e^x on the hardware exp2 unit
 __device__ __forceinline__ float exp_f(float x) { return fast_exp2(x * 1.4426950408889634f); }
 // softplus(x) = log(1 + e^x) from y = e^x: torch's threshold (x > 20 returns x), log1p's

@@ -64,7 +64,7 @@ template <int GATE, bool VEC_B>
 __global__ __launch_bounds__(512) void fwd_prepare_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ graw,
     const float* __restrict__ beta, const bf16* __restrict__ bgate, float* __restrict__ gc_out,
-    float* __restrict__ aqk_out, float* __restrict__ akk_out, int T, int H, float scale) {
+    float* __restrict__ aqk_out, float* __restrict__ akk_out, int T, int H, int HQ, float scale) {
   using fwd::LDG;
   using fwd::LDK;
   using fwd::LDM;
@@ -94,14 +94,15 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
   const size_t kofs = tok0 * rsk + (size_t)h * KD;
   const size_t mofs = (tok0 * H + h) * C;      // [t][64] matrices of this chunk-head
   const size_t rsm = (size_t)H * C;
+  const QKRows qr = qk_rows(tok0, h, H, HQ);   // q / k rows (grouped value heads: HQ < H)
 
   // ---- stage q, k (, b) rows; gate cumsum ----
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int p = tid + 512 * i;
     const int t = p >> 4, c8 = (p & 15) * 8;
-    *reinterpret_cast<u32x4*>(&sq[t][c8]) = *reinterpret_cast<const u32x4*>(q + kofs + (size_t)t * rsk + c8);
-    *reinterpret_cast<u32x4*>(&sk[t][c8]) = *reinterpret_cast<const u32x4*>(k + kofs + (size_t)t * rsk + c8);
+    *reinterpret_cast<u32x4*>(&sq[t][c8]) = *reinterpret_cast<const u32x4*>(q + qr.ofs + (size_t)t * qr.rs + c8);
+    *reinterpret_cast<u32x4*>(&sk[t][c8]) = *reinterpret_cast<const u32x4*>(k + qr.ofs + (size_t)t * qr.rs + c8);
     if constexpr (VEC_B)
       *reinterpret_cast<u32x4*>(&sb[t][c8]) = *reinterpret_cast<const u32x4*>(bgate + kofs + (size_t)t * rsk + c8);
   }
@@ -369,7 +370,7 @@ template <int GATE>
 __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, const float* __restrict__ gc,
                                                      const float* __restrict__ aqk, const bf16* __restrict__ hst,
                                                      const bf16* __restrict__ vnew, bf16* __restrict__ o_out,
-                                                     int T, int H, float scale) {
+                                                     int T, int H, int HQ, float scale) {
   // swizzled, unpadded tiles (80 KiB in all, so two work-groups share a CU)
   __shared__ __attribute__((aligned(16))) bf16 sqg[C * KD];       // scale q 2^g rows [i][k], hi
   __shared__ __attribute__((aligned(16))) bf16 sqgl[C * KD];      // lo
@@ -399,7 +400,8 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
   for (int i = 0; i < 2; ++i) {
     const int p = tid + 512 * i;
     const int t = p >> 4, c8 = (p & 15) * 8;
-    const bf16x8 qx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(q + kofs + (size_t)t * rsk + c8));
+    const QKRows qr = qk_rows(tok0, h, H, HQ);
+    const bf16x8 qx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(q + qr.ofs + (size_t)t * qr.rs + c8));
     bf16x8 hi, lo;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -472,8 +474,11 @@ using namespace rewy;
 
 extern "C" hipError_t fdr_fwd_prepare(const void* q, const void* k, const float* g, int gate_mode,
                                       const float* beta, const void* b_gate, float* gc, float* Aqk, float* Akk,
-                                      int B, int T, int H, int K, int chunk, float scale, hipStream_t stream) {
+                                      int B, int T, int H, int qk_heads, int K, int chunk, float scale,
+                                      hipStream_t stream) {
   if (K != KD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  const int HQ = qk_heads > 0 ? qk_heads : H;
+  if (H % HQ || (b_gate && HQ != H)) return hipErrorInvalidValue;
   if (!q || !k || !Aqk || !Akk) return hipErrorInvalidValue;
   if (gate_mode != FG_NONE && (!g || !gc)) return hipErrorInvalidValue;
   const bool vec_b = b_gate != nullptr;
@@ -482,7 +487,7 @@ extern "C" hipError_t fdr_fwd_prepare(const void* q, const void* k, const float*
   const dim3 grid(B * H * (T / C)), block(512);
 #define FDR_PREP(G, VB)                                                                              \
   hipLaunchKernelGGL((fwd_prepare_kernel<G, VB>), grid, block, 0, stream, (const bf16*)q, (const bf16*)k, \
-                     g, beta, (const bf16*)b_gate, gc, Aqk, Akk, T, H, scale)
+                     g, beta, (const bf16*)b_gate, gc, Aqk, Akk, T, H, HQ, scale)
   if (vec_b) FDR_PREP(FG_VECTOR, true);
   else if (gate_mode == FG_VECTOR) FDR_PREP(FG_VECTOR, false);
   else if (gate_mode == FG_SCALAR) FDR_PREP(FG_SCALAR, false);
@@ -493,15 +498,17 @@ extern "C" hipError_t fdr_fwd_prepare(const void* q, const void* k, const float*
 }
 
 extern "C" hipError_t fdr_fwd_o(const void* q, const float* gc, int gate_mode, const float* Aqk, const void* h,
-                                const void* v_new, void* o, int B, int T, int H, int K, int V, int chunk,
-                                float scale, hipStream_t stream) {
+                                const void* v_new, void* o, int B, int T, int H, int qk_heads, int K, int V,
+                                int chunk, float scale, hipStream_t stream) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  const int HQ = qk_heads > 0 ? qk_heads : H;
+  if (H % HQ) return hipErrorInvalidValue;
   if (!q || !Aqk || !h || !v_new || !o) return hipErrorInvalidValue;
   if (gate_mode != FG_NONE && !gc) return hipErrorInvalidValue;
   const dim3 grid(B * H * (T / C)), block(512);
 #define FDR_O(G)                                                                                       \
   hipLaunchKernelGGL((fwd_o_kernel<G>), grid, block, 0, stream, (const bf16*)q, gc, Aqk, (const bf16*)h, \
-                     (const bf16*)v_new, (bf16*)o, T, H, scale)
+                     (const bf16*)v_new, (bf16*)o, T, H, HQ, scale)
   if (gate_mode == FG_VECTOR) FDR_O(FG_VECTOR);
   else if (gate_mode == FG_SCALAR) FDR_O(FG_SCALAR);
   else if (gate_mode == FG_NONE) FDR_O(FG_NONE);

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
     const bf16* __restrict__ wgate, const float* __restrict__ akk, bf16* __restrict__ w_out,
     bf16* __restrict__ u_out, bf16* __restrict__ qg_out, bf16* __restrict__ kg_out,
-    float* __restrict__ aqk_out, int T, int H, float scale) {
+    float* __restrict__ aqk_out, int T, int H, int HQ, float scale) {
   using rec::LDT;
   // Scalar or no gate with scalar beta: k is staged raw and E = (beta k) 2^g is formed
   // per operand fragment (one factor pair per token row), so Aqk reads k from LDS too
@@ -66,6 +66,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
   const size_t rsk = (size_t)H * KD, rsv = (size_t)H * VD;
   const size_t kofs = tok0 * rsk + (size_t)h * KD;
   const size_t vofs = tok0 * rsv + (size_t)h * VD;
+  const QKRows qr = qk_rows(tok0, h, H, HQ);   // raw q / k rows (grouped value heads: HQ < H)
 
   // Aqk's q fragments (wave wv: row tile wv), fetched first so their latency hides
   // behind the staging and the w/u products
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
   if constexpr (WANT_AQK) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      qa[ks] = *reinterpret_cast<const bf16x8*>(q + kofs + (size_t)(16 * wv + lc) * rsk + 32 * ks + 8 * lg);
+      qa[ks] = *reinterpret_cast<const bf16x8*>(q + qr.ofs + (size_t)(16 * wv + lc) * qr.rs + 32 * ks + 8 * lg);
   }
   if (tid < C) {
     const size_t row = (tok0 + tid) * H + h;
@@ -89,7 +90,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
   for (int i = 0; i < 4; ++i) {
     const int p = tid + 256 * i;            // 1024 pieces of 8 columns: row p >> 4
     const int t = p >> 4, ch = p & 15, c0 = 8 * ch;
-    const bf16x8 kx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(k + kofs + (size_t)t * rsk + c0));
+    const bf16x8 kx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(k + qr.ofs + (size_t)t * qr.rs + c0));
     const bf16x8 vx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(v + vofs + (size_t)t * rsv + c0));
     float ge[8], be[8], we[8];
     if constexpr (GATE == RG_VECTOR) {
@@ -139,8 +140,8 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     for (int i = 0; i < 4; ++i) {
       const int p = tid + 256 * i;          // 1024 pieces of 8
       const int t = p >> 4, c0 = (p & 15) * 8;
-      const u32x4 qq = *reinterpret_cast<const u32x4*>(q + kofs + (size_t)t * rsk + c0);
-      const u32x4 kq = *reinterpret_cast<const u32x4*>(k + kofs + (size_t)t * rsk + c0);
+      const u32x4 qq = *reinterpret_cast<const u32x4*>(q + qr.ofs + (size_t)t * qr.rs + c0);
+      const u32x4 kq = *reinterpret_cast<const u32x4*>(k + qr.ofs + (size_t)t * qr.rs + c0);
       const float* gr = g + kofs + (size_t)t * rsk + c0;
       const float* gl = g + kofs + (size_t)(C - 1) * rsk + c0;
       const bf16* pq = reinterpret_cast<const bf16*>(&qq);
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
           const bf16x8 a = qa[ks];
           bf16x8 bq;
           if constexpr (RAWK) bq = frag_row<16>(eH, 16 * J, 32 * ks);
-          else bq = *reinterpret_cast<const bf16x8*>(k + kofs + (size_t)(16 * J + lc) * rsk + 32 * ks + 8 * lg);
+          else bq = *reinterpret_cast<const bf16x8*>(k + qr.ofs + (size_t)(16 * J + lc) * qr.rs + 32 * ks + 8 * lg);
           acc = mfma(a, bq, acc);
         }
       }
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ w, const bf16* __restrict__ u,
     const float* __restrict__ g, const float* __restrict__ h0, bf16* __restrict__ h_out,
     bf16* __restrict__ vnew_out, float* __restrict__ ht_out, int T, int H, const int* __restrict__ chunk_off,
-    int vf) {
+    int vf, int HQ) {
   using S = FwdSmem<BV, GATE>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
@@ -315,7 +316,8 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
-      rk[i] = *reinterpret_cast<const u32x4*>(k + tok0 * rsk + (size_t)h * KD + (size_t)(p >> 4) * rsk + (p & 15) * 8);
+      const QKRows kr_ = qk_rows(tok0, h, H, HQ);     // k: raw (HQ heads) for scalar gates, kg (HQ = H) else
+      rk[i] = *reinterpret_cast<const u32x4*>(k + kr_.ofs + (size_t)(p >> 4) * kr_.rs + (p & 15) * 8);
     }
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
@@ -455,20 +457,20 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
 template <int GATE, bool VEC_B, bool QKG, bool AQK>
 static hipError_t launch_prepare(const void* q, const void* k, const void* v, const float* g,
                                  const float* beta, const void* bg, const void* wg, const float* akk,
-                                 void* w, void* u, void* qg, void* kg, float* aqk, int B, int T, int H,
+                                 void* w, void* u, void* qg, void* kg, float* aqk, int B, int T, int H, int HQ,
                                  float scale, hipStream_t s) {
   hipLaunchKernelGGL((prepare_wu_kernel<GATE, VEC_B, QKG, AQK>), dim3(B * H * (T / C)), dim3(256), 0, s,
                      (const bf16*)q, (const bf16*)k, (const bf16*)v, g, beta, (const bf16*)bg,
-                     (const bf16*)wg, akk, (bf16*)w, (bf16*)u, (bf16*)qg, (bf16*)kg, aqk, T, H, scale);
+                     (const bf16*)wg, akk, (bf16*)w, (bf16*)u, (bf16*)qg, (bf16*)kg, aqk, T, H, HQ, scale);
   return hipGetLastError();
 }
 
 template <int BV, int GATE>
 static hipError_t launch_fwd_h(const void* k, const void* w, const void* u, const float* g, const float* h0,
                                void* h, void* vnew, float* ht, int B, int T, int H, hipStream_t s,
-                               const int* co, int vf) {
+                               const int* co, int vf, int HQ) {
   hipLaunchKernelGGL((fwd_h_kernel<BV, GATE>), dim3(B * H * (VD / BV)), dim3(512), 0, s, (const bf16*)k,
-                     (const bf16*)w, (const bf16*)u, g, h0, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf);
+                     (const bf16*)w, (const bf16*)u, g, h0, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf, HQ);
   return hipGetLastError();
 }
 
@@ -479,9 +481,11 @@ using namespace rewy;
 extern "C" hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const float* g,
                                      int gate_mode, const float* beta, const void* b_gate,
                                      const void* w_gate, const float* Akk, void* w, void* u, void* qg,
-                                     void* kg, float* Aqk, int B, int T, int H, int K, int V, int chunk,
-                                     float scale, hipStream_t stream) {
+                                     void* kg, float* Aqk, int B, int T, int H, int qk_heads, int K, int V,
+                                     int chunk, float scale, hipStream_t stream) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  const int HQ = qk_heads > 0 ? qk_heads : H;
+  if (H % HQ || (b_gate && HQ != H)) return hipErrorInvalidValue;
   if (!k || !v || !Akk || !w || !u) return hipErrorInvalidValue;
   const bool vec_b = b_gate != nullptr;
   if (vec_b && (!w_gate || gate_mode != RG_VECTOR)) return hipErrorInvalidValue;
@@ -491,7 +495,7 @@ extern "C" hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v
   if (want_qkg && (!qg || !kg || !q || gate_mode != RG_VECTOR)) return hipErrorInvalidValue;
   const bool want_aqk = Aqk != nullptr;
   if (want_aqk && (!q || gate_mode == RG_VECTOR)) return hipErrorInvalidValue;
-#define P_ARGS q, k, v, g, beta, b_gate, w_gate, Akk, w, u, qg, kg, Aqk, B, T, H, scale, stream
+#define P_ARGS q, k, v, g, beta, b_gate, w_gate, Akk, w, u, qg, kg, Aqk, B, T, H, HQ, scale, stream
   switch (gate_mode) {
     case RG_NONE:
       return want_aqk ? launch_prepare<RG_NONE, false, false, true>(P_ARGS)
@@ -520,13 +524,16 @@ static int fwd_default_bv(int B, int H) {
 
 // B rows of T tokens, or (co) B sequences packed along T
 static hipError_t fwd_h_dispatch(const void* k, const void* w, const void* u, const float* g, int gate_mode,
-                                 const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int K,
-                                 int V, int chunk, int value_block, hipStream_t stream, const int* co, int vf) {
+                                 const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int HQ,
+                                 int K, int V, int chunk, int value_block, hipStream_t stream, const int* co,
+                                 int vf) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  if (HQ <= 0) HQ = H;
+  if (H % HQ) return hipErrorInvalidValue;
   if (!k || !w || !u || !h || !v_new) return hipErrorInvalidValue;
   if (gate_mode != RG_NONE && !g) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : fwd_default_bv(B, H);
-#define F_ARGS k, w, u, g, h0, h, v_new, ht, B, T, H, stream, co, vf
+#define F_ARGS k, w, u, g, h0, h, v_new, ht, B, T, H, stream, co, vf, HQ
 #define F_BV(G)                                                     \
   switch (bv) {                                                     \
     case 16: return launch_fwd_h<16, G>(F_ARGS);                    \
@@ -546,16 +553,16 @@ static hipError_t fwd_h_dispatch(const void* k, const void* w, const void* u, co
 
 extern "C" hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g, int gate_mode,
                                 const float* h0, void* h, void* v_new, float* ht, int state_v_first, int B, int T,
-                                int H, int K, int V, int chunk, int value_block, hipStream_t stream) {
-  return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, B, T, H, K, V, chunk, value_block, stream,
+                                int H, int k_heads, int K, int V, int chunk, int value_block, hipStream_t stream) {
+  return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, B, T, H, k_heads, K, V, chunk, value_block, stream,
                         nullptr, state_v_first ? 1 : 0);
 }
 
 extern "C" hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const float* g, int gate_mode,
                                        const float* h0, void* h, void* v_new, float* ht, int state_v_first,
-                                       const int* chunk_offsets, int N, int T, int H, int K, int V, int chunk,
-                                       int value_block, hipStream_t stream) {
+                                       const int* chunk_offsets, int N, int T, int H, int k_heads, int K, int V,
+                                       int chunk, int value_block, hipStream_t stream) {
   if (!chunk_offsets) return hipErrorInvalidValue;
-  return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, N, T, H, K, V, chunk, value_block, stream,
+  return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, N, T, H, k_heads, K, V, chunk, value_block, stream,
                         chunk_offsets, state_v_first ? 1 : 0);
 }

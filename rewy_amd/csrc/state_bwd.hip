@@ -51,7 +51,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     const float* __restrict__ g, const bf16* __restrict__ dO, const float* __restrict__ aqk,
     const bf16* __restrict__ dv, const float* __restrict__ dht, bf16* __restrict__ dh_out,
     bf16* __restrict__ dr_out, float* __restrict__ dh0, int T, int H, float scale,
-    const int* __restrict__ chunk_off, int segs, int vf) {
+    const int* __restrict__ chunk_off, int segs, int vf, int HQ) {
   using S = StateSmem<BV, GATE, DV_FROM_AQK>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
@@ -130,12 +130,15 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       rg_last = g[(tok0 + C - 1) * H + h];
     }
     const size_t kofs = tok0 * row_stride_k + (size_t)h * KD;
+    // q / k: raw (HQ heads, grouped value heads) for scalar / no gates, qg / kg (HQ = H) else
+    const QKRows qr = qk_rows(tok0, h, H, HQ);
 #pragma unroll
     for (int i = 0; i < NPI; ++i) {
       const int p = tid + NTH * i;
       const size_t o = kofs + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8;
-      rk[i] = *reinterpret_cast<const u32x4*>(k + o);
-      rq[i] = *reinterpret_cast<const u32x4*>(q + o);
+      const size_t oq = qr.ofs + (size_t)(p >> 4) * qr.rs + (p & 15) * 8;
+      rk[i] = *reinterpret_cast<const u32x4*>(k + oq);
+      rq[i] = *reinterpret_cast<const u32x4*>(q + oq);
       rw[i] = *reinterpret_cast<const u32x4*>(w + o);
       if constexpr (DV_FROM_AQK)
         ra[i] = *reinterpret_cast<const f32x4*>(aqk + ((tok0 + (p >> 4)) * H + h) * C + (p & 15) * 4);
@@ -309,13 +312,14 @@ template <int BV, int GATE, bool AQK>
 static hipError_t launch_state(const void* q, const void* k, const void* w, const float* g,
                                const void* dO, const float* aqk, const void* dv, const float* dht,
                                void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
-                               hipStream_t stream, const int* chunk_off, int segs = 0, int vf = 0) {
+                               hipStream_t stream, const int* chunk_off, int segs = 0, int vf = 0, int HQ = 0) {
   const int rows = segs > 0 ? B * segs : B;
   const int grid = rows * H * (VD / BV);
   constexpr int NW = state_waves<BV>();
   hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW>), dim3(grid), dim3(64 * NW), 0, stream,
                      (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk,
-                     (const bf16*)dv, dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale, chunk_off, segs, vf);
+                     (const bf16*)dv, dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale, chunk_off, segs, vf,
+                     HQ > 0 ? HQ : H);
   return hipGetLastError();
 }
 
@@ -323,11 +327,11 @@ template <int GATE, bool AQK>
 static hipError_t pick_bv(int bv, const void* q, const void* k, const void* w, const float* g,
                           const void* dO, const float* aqk, const void* dv, const float* dht,
                           void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
-                          hipStream_t s, const int* co, int vf) {
+                          hipStream_t s, const int* co, int vf, int HQ) {
   switch (bv) {
-    case 16: return launch_state<16, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf);
-    case 32: return launch_state<32, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf);
-    case 64: return launch_state<64, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf);
+    case 16: return launch_state<16, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, HQ);
+    case 32: return launch_state<32, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, HQ);
+    case 64: return launch_state<64, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, HQ);
     default: return hipErrorInvalidValue;
   }
 }
@@ -640,15 +644,17 @@ static int default_bv(int B, int H) {
 static hipError_t state_dispatch(const void* q, const void* k, const void* w, const float* g, int gate_mode,
                                  const void* dO, const float* aqk, const void* dv, const float* dht, void* dh,
                                  void* dr, float* dh0, int B, int T, int H, int K, int V, int chunk, float scale,
-                                 int value_block, hipStream_t stream, const int* co, int vf) {
+                                 int value_block, hipStream_t stream, const int* co, int vf, int HQ) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0)
     return hipErrorInvalidValue;
   if (!q || !k || !w || !dO || !dh || !dr) return hipErrorInvalidValue;
   if ((aqk == nullptr) == (dv == nullptr)) return hipErrorInvalidValue;
   if (gate_mode != GATE_NONE && g == nullptr) return hipErrorInvalidValue;
+  if (HQ <= 0) HQ = H;
+  if (H % HQ) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : default_bv(B, H);
   const bool from_aqk = aqk != nullptr;
-#define S_ARGS bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream, co, vf
+#define S_ARGS bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream, co, vf, HQ
   switch (gate_mode) {
     case GATE_NONE:
       return from_aqk ? pick_bv<GATE_NONE, true>(S_ARGS) : pick_bv<GATE_NONE, false>(S_ARGS);
@@ -665,20 +671,20 @@ static hipError_t state_dispatch(const void* q, const void* k, const void* w, co
 extern "C" hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const float* g,
                                     int gate_mode, const void* dO, const float* aqk, const void* dv,
                                     const float* dht, void* dh, void* dr, float* dh0, int state_v_first,
-                                    int B, int T, int H, int K, int V, int chunk, float scale, int value_block,
-                                    hipStream_t stream) {
+                                    int B, int T, int H, int qk_heads, int K, int V, int chunk, float scale,
+                                    int value_block, hipStream_t stream) {
   return state_dispatch(q, k, w, g, gate_mode, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, K, V, chunk, scale,
-                        value_block, stream, nullptr, state_v_first ? 1 : 0);
+                        value_block, stream, nullptr, state_v_first ? 1 : 0, qk_heads);
 }
 
 extern "C" hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, const float* g,
                                            int gate_mode, const void* dO, const float* aqk, const void* dv,
                                            const float* dht, void* dh, void* dr, float* dh0, int state_v_first,
-                                           const int* chunk_offsets, int N, int T, int H, int K, int V,
-                                           int chunk, float scale, int value_block, hipStream_t stream) {
+                                           const int* chunk_offsets, int N, int T, int H, int qk_heads, int K,
+                                           int V, int chunk, float scale, int value_block, hipStream_t stream) {
   if (!chunk_offsets) return hipErrorInvalidValue;
   return state_dispatch(q, k, w, g, gate_mode, dO, aqk, dv, dht, dh, dr, dh0, N, T, H, K, V, chunk, scale,
-                        value_block, stream, chunk_offsets, state_v_first ? 1 : 0);
+                        value_block, stream, chunk_offsets, state_v_first ? 1 : 0, qk_heads);
 }
 
 extern "C" size_t fdr_state_bwd_segmented_workspace_bytes(int B, int H, int segments) {

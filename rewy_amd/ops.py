@@ -72,9 +72,10 @@ def _use_affine(method, B, H, NT):
     return method == "affine"
 
 
-def affine_pays(q):
-    """True when the affine-step recurrences are the faster choice for q's shape."""
-    B, T, H = q.shape[:3]
+def affine_pays(x):
+    """True when the affine-step recurrences are the faster choice for the shape of x,
+    a [B, T, H, .] tensor with one head per state (value heads)."""
+    B, T, H = x.shape[:3]
     return _use_affine("auto", B, H, T // CHUNK)
 
 
@@ -102,6 +103,13 @@ def _chunk_offsets(chunk_offsets, B, T, dev):
     if int(host[0]) != 0 or int(host[-1]) != T // CHUNK or bool((host[1:] < host[:-1]).any()):
         raise ValueError(f"chunk_offsets must rise from 0 to T/{CHUNK} = {T // CHUNK}")
     return co.to(device=dev, dtype=torch.int32).contiguous(), host.numel() - 1
+
+
+def _group(H, HQ):
+    """Value heads H and q / k heads HQ (grouped value heads: H a multiple of HQ)."""
+    if HQ <= 0 or H % HQ:
+        raise ValueError(f"value heads ({H}) must be a multiple of the q/k heads ({HQ})")
+    return H, HQ
 
 
 def _dims(q):
@@ -132,12 +140,14 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
     split into ``segments`` (0: ``segments_for``) whose affine maps are formed in parallel,
     chained, and each segment rerun from its end state (fdr_state_bwd_segmented), for long
     rows and few heads; "auto" picks."""
-    B, T, H, K = _dims(q)
+    B, T, HQ, K = _dims(q)
+    H, HQ = _group(w.shape[2] if w is not None and w.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = q.device
     bf, f32 = torch.bfloat16, torch.float32
-    for x, n in ((q, "q"), (k, "k"), (w, "w")):
-        _need(x, n, bf, (B, T, H, K), dev)
+    for x, n in ((q, "q"), (k, "k")):
+        _need(x, n, bf, (B, T, HQ, K), dev)
+    _need(w, "w", bf, (B, T, H, K), dev)
     _need(dO, "dO", bf, (B, T, H, V), dev)
     if gate_mode == GATE_VECTOR:
         _need(g, "g", f32, (B, T, H, K), dev)
@@ -166,11 +176,15 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
         if method == "affine":
             raise ValueError("the affine-step form takes equal-length rows, not chunk_offsets")
         st = _lib.load().fdr_state_bwd_varlen(P(q), P(k), P(w), P(g), int(gate_mode), P(dO), P(aqk), P(dv),
-                                              P(dht), P(dh), P(dr), P(dh0), vf, P(co), N, T, H, K, V, CHUNK,
+                                              P(dht), P(dh), P(dr), P(dh0), vf, P(co), N, T, H, HQ, K, V, CHUNK,
                                               float(scale), int(value_block), _lib.stream_handle(dev))
         _lib.check(st, "fdr_state_bwd_varlen")
         return dh, dr, dh0
     form = _state_method(method, B, H, NT)
+    if HQ != H and form != "direct":
+        if method != "auto":
+            raise ValueError("grouped q/k heads take the direct state recurrence")
+        form = "direct"
     if form == "segmented":
         segs = int(segments) or segments_for(B, H, NT)
         if not 1 <= segs <= NT:
@@ -201,7 +215,7 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
         _lib.check(lib.fdr_affine_side(arr, n, B, T, H, K, V, CHUNK, _lib.stream_handle(dev)), "fdr_affine_side")
         return dh, dr, dh0
     st = _lib.load().fdr_state_bwd(P(q), P(k), P(w), P(g), int(gate_mode), P(dO), P(aqk), P(dv),
-                                   P(dht), P(dh), P(dr), P(dh0), vf, B, T, H, K, V, CHUNK,
+                                   P(dht), P(dh), P(dr), P(dh0), vf, B, T, H, HQ, K, V, CHUNK,
                                    float(scale), int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_state_bwd")
     return dh, dr, dh0
@@ -281,13 +295,14 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
 
     Returns dict(dq, dk, dv [bf16], dg [fp32, gate shape] | None, dbeta [fp32] | None,
     db, dw [bf16] | None)."""
-    B, T, H, K = _dims(q)
+    B, T, HQ, K = _dims(q)
+    H, HQ = _group(v.shape[2] if v is not None and v.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = q.device
     bf, f32 = torch.bfloat16, torch.float32
     NT = T // CHUNK
     for x, n in ((q, "q"), (k, "k")):
-        _need(x, n, bf, (B, T, H, K), dev)
+        _need(x, n, bf, (B, T, HQ, K), dev)
     for x, n in ((v, "v"), (v_new, "v_new"), (dO, "dO"), (dR, "dR")):
         _need(x, n, bf, (B, T, H, V), dev)
     _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
@@ -315,7 +330,7 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
         raise ValueError("[V,K] saved states come with the vector-gate families")
     if gate_fold is not None:
         return _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, gate_fold,
-                                    beta_sigmoid, hvf)
+                                    beta_sigmoid, hvf, H)
     out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=bf),
                dk=torch.empty(B, T, H, K, device=dev, dtype=bf),
                dv=torch.empty(B, T, H, V, device=dev, dtype=bf),
@@ -327,16 +342,17 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
     st = _lib.load().fdr_chunk_bwd(P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), int(gate_mode),
                                    P(beta), P(b), P(w), P(Akk), P(h), P(dh), P(out["dq"]),
                                    P(out["dk"]), P(out["dv"]), P(out["dg"]), P(out["dbeta"]), beta_sigmoid,
-                                   P(out["db"]), P(out["dw"]), hvf, B, T, H, K, V, CHUNK, float(scale),
+                                   P(out["db"]), P(out["dw"]), hvf, B, T, H, HQ, K, V, CHUNK, float(scale),
                                    _lib.stream_handle(dev))
     _lib.check(st, "fdr_chunk_bwd")
     return out
 
 
 def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, fold, beta_sigmoid=0.0,
-                         hvf=0):
+                         hvf=0, H=None):
     """chunk_bwd (KDA) with the gate backward folded into the dg stores."""
-    B, T, H, K = q.shape
+    B, T, HQ, K = q.shape
+    H = HQ if H is None else H
     V = V_SUPPORTED
     dev = q.device
     bf, f32 = torch.bfloat16, torch.float32
@@ -364,7 +380,7 @@ def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale
                                      P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), beta_sigmoid, P(raw),
                                      int(raw.dtype == bf), P(a), P(dt), int(lb is not None),
                                      0.0 if lb is None else float(lb), P(out["dg"]), P(out["dA_log"]),
-                                     P(out["ddt_bias"]), P(ws), hvf, B, T, H, K, V, CHUNK, float(scale),
+                                     P(out["ddt_bias"]), P(ws), hvf, B, T, H, HQ, K, V, CHUNK, float(scale),
                                      _lib.stream_handle(dev))
     _lib.check(st, "fdr_chunk_bwd_gate_fold")
     return out
@@ -373,15 +389,16 @@ def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale
 def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, want_qkg=False,
                want_aqk=False, scale=1.0):
     """WY factors (and qg/kg or Aqk) of every chunk.  Returns dict(w, u, qg, kg, Aqk)."""
-    B, T, H, K = _dims(k)
+    B, T, HQ, K = _dims(k)
+    H, HQ = _group(v.shape[2] if v is not None and v.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = k.device
     bf, f32 = torch.bfloat16, torch.float32
-    _need(k, "k", bf, (B, T, H, K), dev)
+    _need(k, "k", bf, (B, T, HQ, K), dev)
     _need(v, "v", bf, (B, T, H, V), dev)
     _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
     if q is not None:
-        _need(q, "q", bf, (B, T, H, K), dev)
+        _need(q, "q", bf, (B, T, HQ, K), dev)
     vec_b = b is not None
     if vec_b:
         _need(b, "b", bf, (B, T, H, K), dev)
@@ -405,7 +422,7 @@ def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, 
     P = _lib.ptr
     st = _lib.load().fdr_prepare_wu(P(q), P(k), P(v), P(g), int(gate_mode), P(beta), P(b), P(w), P(Akk),
                                     P(out["w"]), P(out["u"]), P(out["qg"]), P(out["kg"]), P(out["Aqk"]),
-                                    B, T, H, K, V, CHUNK, float(scale), _lib.stream_handle(dev))
+                                    B, T, H, HQ, K, V, CHUNK, float(scale), _lib.stream_handle(dev))
     _lib.check(st, "fdr_prepare_wu")
     return out
 
@@ -414,11 +431,12 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
           chunk_offsets=None, state_v_first=False):
     """Forward state scan.  Returns (h [B,NT,H,K,V] bf16, v_new [B,T,H,V] bf16, final fp32|None).
     ``method`` and ``chunk_offsets`` as for ``state_bwd`` (h0 / final per sequence)."""
-    B, T, H, K = _dims(k)
+    B, T, HQ, K = _dims(k)
+    H, HQ = _group(w.shape[2] if w is not None and w.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = k.device
     bf, f32 = torch.bfloat16, torch.float32
-    _need(k, "k", bf, (B, T, H, K), dev)
+    _need(k, "k", bf, (B, T, HQ, K), dev)
     _need(w, "w", bf, (B, T, H, K), dev)
     _need(u, "u", bf, (B, T, H, V), dev)
     if gate_mode == GATE_VECTOR:
@@ -442,10 +460,11 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
         if method == "affine":
             raise ValueError("the affine-step form takes equal-length rows, not chunk_offsets")
         st = _lib.load().fdr_fwd_h_varlen(P(k), P(w), P(u), P(g), int(gate_mode), P(h0), P(h), P(vnew), P(ht),
-                                          vf, P(co), N, T, H, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
+                                          vf, P(co), N, T, H, HQ, K, V, CHUNK, int(value_block),
+                                          _lib.stream_handle(dev))
         _lib.check(st, "fdr_fwd_h_varlen")
         return h, vnew, ht
-    if _use_affine(method, B, H, NT):
+    if _use_affine(method, B, H, NT) and HQ == H:
         vb = value_block or AFFINE_VALUE_BLOCK
         step, offset = _affine_workspace(B, NT, H, dev)
         lib = _lib.load()
@@ -459,7 +478,7 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
         arr, n = _lib.problems(_lib.SideProblem, [_lib.SideProblem(P(w), P(h), P(u), None, P(vnew), -1.0)])
         _lib.check(lib.fdr_affine_side(arr, n, B, T, H, K, V, CHUNK, _lib.stream_handle(dev)), "fdr_affine_side")
         return h, vnew, ht
-    st = _lib.load().fdr_fwd_h(P(k), P(w), P(u), P(g), int(gate_mode), P(h0), P(h), P(vnew), P(ht), vf, B, T, H,
+    st = _lib.load().fdr_fwd_h(P(k), P(w), P(u), P(g), int(gate_mode), P(h0), P(h), P(vnew), P(ht), vf, B, T, H, HQ,
                                K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_h")
     return h, vnew, ht
@@ -467,11 +486,12 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
 
 def matrix_intra(q, k, g, dAqk, dAkk, dq, dk, db, dg, beta=None, b=None, beta_complete=False):
     """Matrix intra VJP added in place into fp32 (dq, dk, db, dg); returns them."""
-    B, T, H, K = _dims(q)
+    B, T, HQ, K = _dims(q)
+    H, HQ = _group(dq.shape[2] if dq is not None and dq.ndim == 4 else HQ, HQ)
     dev = q.device
     bf, f32 = torch.bfloat16, torch.float32
-    _need(q, "q", bf, (B, T, H, K), dev)
-    _need(k, "k", bf, (B, T, H, K), dev)
+    _need(q, "q", bf, (B, T, HQ, K), dev)
+    _need(k, "k", bf, (B, T, HQ, K), dev)
     _need(g, "g", f32, (B, T, H, K), dev)
     _need(dAqk, "dAqk", f32, (B, T, H, CHUNK), dev)
     _need(dAkk, "dAkk", f32, (B, T, H, CHUNK), dev)
@@ -487,18 +507,20 @@ def matrix_intra(q, k, g, dAqk, dAkk, dq, dk, db, dg, beta=None, b=None, beta_co
         _need(db, "db", f32, (B, T, H), dev)
     P = _lib.ptr
     st = _lib.load().fdr_matrix_intra(P(q), P(k), P(g), P(beta), P(b), P(dAqk), P(dAkk), P(dq), P(dk), P(db),
-                                      P(dg), B, T, H, K, CHUNK, int(bool(beta_complete)), _lib.stream_handle(dev))
+                                      P(dg), B, T, H, HQ, K, CHUNK, int(bool(beta_complete)), _lib.stream_handle(dev))
     _lib.check(st, "fdr_matrix_intra")
     return dq, dk, db, dg
 
 
 def fwd_prepare(q, k, g, gate_mode, beta=None, b=None, scale=1.0):
     """Forward intra matrices.  Returns (gc fp32 | None, Aqk fp32, Akk fp32)."""
-    B, T, H, K = _dims(q)
+    B, T, HQ, K = _dims(q)
+    side = beta if beta is not None else b
+    H, HQ = _group(side.shape[2] if side is not None and side.ndim >= 3 else HQ, HQ)
     dev = q.device
     bf, f32 = torch.bfloat16, torch.float32
-    _need(q, "q", bf, (B, T, H, K), dev)
-    _need(k, "k", bf, (B, T, H, K), dev)
+    _need(q, "q", bf, (B, T, HQ, K), dev)
+    _need(k, "k", bf, (B, T, HQ, K), dev)
     if gate_mode == GATE_VECTOR:
         _need(g, "g", f32, (B, T, H, K), dev)
     elif gate_mode == GATE_SCALAR:
@@ -516,18 +538,19 @@ def fwd_prepare(q, k, g, gate_mode, beta=None, b=None, scale=1.0):
     Akk = torch.empty(B, T, H, CHUNK, device=dev, dtype=f32)
     P = _lib.ptr
     st = _lib.load().fdr_fwd_prepare(P(q), P(k), P(g), int(gate_mode), P(beta), P(b), P(gc), P(Aqk), P(Akk),
-                                     B, T, H, K, CHUNK, float(scale), _lib.stream_handle(dev))
+                                     B, T, H, HQ, K, CHUNK, float(scale), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_prepare")
     return gc, Aqk, Akk
 
 
 def fwd_o(q, gc, gate_mode, Aqk, h, v_new, scale):
     """Forward output o = scale (q 2^gc) h + Aqk v_new (bf16)."""
-    B, T, H, K = _dims(q)
+    B, T, HQ, K = _dims(q)
+    H, HQ = _group(Aqk.shape[2] if Aqk is not None and Aqk.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = q.device
     bf, f32 = torch.bfloat16, torch.float32
-    _need(q, "q", bf, (B, T, H, K), dev)
+    _need(q, "q", bf, (B, T, HQ, K), dev)
     if gate_mode == GATE_VECTOR:
         _need(gc, "gc", f32, (B, T, H, K), dev)
     elif gate_mode == GATE_SCALAR:
@@ -539,7 +562,7 @@ def fwd_o(q, gc, gate_mode, Aqk, h, v_new, scale):
     _need(v_new, "v_new", bf, (B, T, H, V), dev)
     o = torch.empty(B, T, H, V, device=dev, dtype=bf)
     P = _lib.ptr
-    st = _lib.load().fdr_fwd_o(P(q), P(gc), int(gate_mode), P(Aqk), P(h), P(v_new), P(o), B, T, H, K, V, CHUNK,
+    st = _lib.load().fdr_fwd_o(P(q), P(gc), int(gate_mode), P(Aqk), P(h), P(v_new), P(o), B, T, H, HQ, K, V, CHUNK,
                                float(scale), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_o")
     return o

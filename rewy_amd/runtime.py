@@ -17,7 +17,9 @@ Where the platform forces a difference:
 * ``check_baseline`` fingerprints this package's HIP library against the
   sources it was built from (the reference seals FLA's sources, :52-67);
 * packed variable-length batches (``cu_seqlens``) are accepted: the state
-  scans take per-sequence chunk offsets natively (the reference rejects them).
+  scans take per-sequence chunk offsets natively (the reference rejects them);
+* grouped value heads (HV a multiple of H) are accepted for KDA, GDN and DeltaNet:
+  the kernels map value heads to q / k heads themselves (the reference rejects them).
 """
 from collections import Counter
 from contextlib import contextmanager
@@ -153,6 +155,21 @@ def _not_rank4(torch, args):
     return not all(isinstance(t, torch.Tensor) and t.ndim == 4 for t in _qkv(args))
 
 
+# grouped value heads (HV a multiple of H) run natively for the families whose
+# reference operators define them (KDA, GDN; DeltaNet's kernels are GDN's without a gate)
+_GROUPED_OK = ('kda', 'gdn', 'delta')
+
+
+def _bad_heads(args):
+    q, k, v = _qkv(args)
+    if q.shape != k.shape or k.shape[:2] != v.shape[:2]:
+        return True
+    H, HV = k.shape[2], v.shape[2]
+    if HV == H:
+        return False
+    return args.get('_op') not in _GROUPED_OK or HV % H != 0
+
+
 def _bad_length(torch, args):
     if args.get('cu_seqlens') is not None:
         return False
@@ -171,8 +188,7 @@ _ENVELOPE = (
     Rule('mixed devices', lambda torch, a: a['k'].device != a['q'].device or a['v'].device != a['q'].device),
     Rule('release envelope uses BF16 q/k/v', lambda torch, a: any(t.dtype != torch.bfloat16 for t in _qkv(a))),
     Rule('release envelope requires K=V=128', lambda torch, a: (a['k'].shape[-1], a['v'].shape[-1]) != (128, 128)),
-    Rule('grouped heads or unequal q/k/v shapes',
-         lambda torch, a: a['q'].shape != a['k'].shape or a['k'].shape[:3] != a['v'].shape[:3]),
+    Rule('grouped heads or unequal q/k/v shapes', lambda torch, a: _bad_heads(a)),
     Rule('sequence length must be a positive multiple of 64', _bad_length),
     Rule('release envelope requires chunk_size=64', lambda torch, a: a.get('chunk_size', 64) != 64),
     Rule('context parallelism is not release-validated', lambda torch, a: a.get('cp_context') is not None),
@@ -192,6 +208,7 @@ _ENVELOPE = (
 def rejection_reason(op, arguments):
     """The first envelope rule the call breaks, or None when it is accepted."""
     import torch
+    arguments = dict(arguments, _op=op)
     for rule in _ENVELOPE:
         if op in rule.ops and rule.rejects(torch, arguments):
             return rule.message

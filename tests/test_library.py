@@ -31,18 +31,18 @@ def test_entry_points_reject_unsupported_shapes_without_touching_the_gpu():
     lib = _lib.load()
     # K = 64 (only 128 supported)
     st = lib.fdr_state_bwd(None, None, None, None, 2, None, None, None, None, None, None, None, 0,
-                           1, 128, 1, 64, 128, 64, 1.0, 0, None)
+                           1, 128, 1, 0, 64, 128, 64, 1.0, 0, None)
     assert st == HIP_ERROR_INVALID_VALUE
     # T not a multiple of 64
-    st = lib.fdr_chunk_bwd(*([None] * 7), 2, *([None] * 11), 0.0, None, None, 0, 1, 100, 1, 128, 128, 64, 1.0, None)
+    st = lib.fdr_chunk_bwd(*([None] * 7), 2, *([None] * 11), 0.0, None, None, 0, 1, 100, 1, 0, 128, 128, 64, 1.0, None)
     assert st == HIP_ERROR_INVALID_VALUE
     # null pointers with a valid shape
-    st = lib.fdr_chunk_bwd(*([None] * 7), 2, *([None] * 11), 0.0, None, None, 0, 1, 128, 1, 128, 128, 64, 1.0, None)
+    st = lib.fdr_chunk_bwd(*([None] * 7), 2, *([None] * 11), 0.0, None, None, 0, 1, 128, 1, 0, 128, 128, 64, 1.0, None)
     assert st == HIP_ERROR_INVALID_VALUE
     # matrix intra: chunk 32, then null operands
-    st = lib.fdr_matrix_intra(*([None] * 11), 1, 128, 1, 128, 32, 0, None)
+    st = lib.fdr_matrix_intra(*([None] * 11), 1, 128, 1, 0, 128, 32, 0, None)
     assert st == HIP_ERROR_INVALID_VALUE
-    st = lib.fdr_matrix_intra(*([None] * 11), 1, 128, 1, 128, 64, 0, None)
+    st = lib.fdr_matrix_intra(*([None] * 11), 1, 128, 1, 0, 128, 64, 0, None)
     assert st == HIP_ERROR_INVALID_VALUE
 
 
@@ -96,3 +96,35 @@ def test_backward_varlen_seam_validation():
         _varlen(q, dict(cu_seqlens=torch.tensor([0, 64])))
     with pytest.raises(NotImplementedError):
         _varlen(q, dict(chunk_offsets=torch.tensor([0, 4])))
+
+
+def _header_params():
+    """Parameter kinds of every declared entry point, read from the header text."""
+    text = (ROOT / "include" / "rewy_amd.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for name, params in re.findall(r"hipError_t\s+(fdr_\w+)\s*\(([^)]*)\)", text):
+        kinds = []
+        for prm in params.split(","):
+            prm = " ".join(prm.split())
+            if "*" in prm or prm.startswith("hipStream_t"):
+                kinds.append("P")
+            elif prm.startswith("float"):
+                kinds.append("F")
+            elif prm.startswith("long long"):
+                kinds.append("L")
+            elif prm.startswith("int"):
+                kinds.append("I")
+            else:
+                raise AssertionError(f"{name}: unknown parameter type {prm!r}")
+        out[name] = kinds
+    return out
+
+
+def test_ctypes_signatures_match_the_header_parameter_by_parameter():
+    import ctypes
+    from rewy_amd import _lib
+    kind = {ctypes.c_void_p: "P", ctypes.c_int: "I", ctypes.c_float: "F", ctypes.c_longlong: "L"}
+    for name, params in _header_params().items():
+        got = [kind[t] for t in _lib.SIGNATURES[name]]
+        assert got == params, (name, "".join(got), "".join(params))

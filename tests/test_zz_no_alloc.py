@@ -52,7 +52,7 @@ def _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc):
     P = L.ptr
     head = [P(x) for x in ins] + [P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), 0.0, P(g_raw), 0,
                                   P(A), P(dt), 0, 0.0, P(out["dg"]), P(out["dA"]), P(out["ddt"])]
-    tail = [0, B, T, H, 128, 128, 64, float(scale), L.stream_handle(dev)]
+    tail = [0, B, T, H, 0, 128, 128, 64, float(scale), L.stream_handle(dev)]
     if noalloc:
         st = lib.fdr_chunk_bwd_gate_fold_noalloc(*head, *tail)
     else:
@@ -84,5 +84,5 @@ def test_noalloc_rejects_sizes_beyond_its_array():
     dummy = torch.empty(16, device=dev)
     p = L.ptr(dummy)
     st = lib.fdr_chunk_bwd_gate_fold_noalloc(*([p] * 15), 0.0, p, 0, p, None, 0, 0.0, p, p, None, 0,
-                                             B, T, H, 128, 128, 64, 1.0, L.stream_handle(dev))
+                                             B, T, H, 0, 128, 128, 64, 1.0, L.stream_handle(dev))
     assert st == HIP_ERROR_INVALID_VALUE
