@@ -127,6 +127,23 @@ hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v, const void
                          hipStream_t stream);
 
 /*
+ * fdr_chunk_bwd for KDA (gate_mode 2, scalar beta, [K,V] states) in the original 7-product
+ * formulation of the local WY backward -- the products of reference
+ * benchmarks/data/intro_graph_data.json (FLA's prepare_wy_repr_bwd /
+ * chunk_kda_bwd_kernel_wy_dqkg_fused; readable port kernels/gdn_original_separate_npu.py:226-477):
+ *   W-bar = -dR h^T,  E-bar = A^T W-bar,  Z-bar = A^T dR,  T = dR Z^T + W-bar E^T,
+ *   J = A^T T,  D = -strict_tril(J A^T),  dbeta by its direct VJP on every row,
+ * with everything else (dAqk, the matrix intra, the epilogue and the reverse cumsum) as in
+ * fdr_chunk_bwd.  No counterpart in the reference as an entry point: it is the same-GPU
+ * comparator of the residual formulation (same kernel, same staging), the ablation the
+ * reference reports (tests/fixtures/a800_kda_timings.json).  Outputs as fdr_chunk_bwd's.
+ */
+hipError_t fdr_chunk_bwd_original(const void* q, const void* k, const void* v, const void* v_new, const void* dO,
+                                  const void* dR, const float* g, const float* beta, const float* Akk, const void* h,
+                                  const void* dh, void* dq, void* dk, void* dv, float* dg, float* dbeta, int B, int T,
+                                  int H, int K, int V, int chunk, float scale, hipStream_t stream);
+
+/*
  * Recompute of the WY factors inside the backward (recompute policy).
  * Replaces FLA recompute_w_u_fwd (called at reference backends/backward.py:110-116):
  *   w = Akk (b k 2^g), u = Akk (w_gate v)            -> bf16 [B,T,H,K] / [B,T,H,V]

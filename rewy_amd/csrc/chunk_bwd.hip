@@ -63,7 +63,7 @@ constexpr int T64 = C * LDT * 2;     // bytes of one [64][72] bf16 tile
 constexpr int T128 = KD * LDT * 2;   // bytes of one [128][72] bf16 tile
 }  // namespace post
 
-template <int GATE, bool VEC_B, bool INTRA = false, bool PIPE = false>
+template <int GATE, bool VEC_B, bool INTRA = false, bool PIPE = false, bool ORIG = false>
 struct PostLayout {
   // PIPE (persistent kernel): dR, R, dO sit in a separate buffer X filled by
   // direct HBM -> LDS copies while the previous chunk-head finishes, and q, k, g
@@ -96,7 +96,11 @@ struct PostLayout {
                        S_ANY = 1088, S_N = 1096;
   static constexpr int SMALL = S_N * 4;
   static constexpr int X_BYTES = PIPE ? 3 * TQ + GT_BYTES : 0;
-  static constexpr int BYTES = REGION_A + REGION_B + SMALL + X_BYTES;
+  // the original formulation's extra tiles: Z = beta v, E = beta k 2^g, W-bar (bf16 [64][128]);
+  // later T hi/lo over Z and J hi/lo over E ([64][64] each)
+  static constexpr int O_BYTES = ORIG ? 3 * TQ : 0;
+  static constexpr int OFF_O = REGION_A + REGION_B + SMALL;
+  static constexpr int BYTES = REGION_A + REGION_B + SMALL + X_BYTES + O_BYTES;
   static constexpr bool FITS = BYTES <= 160 * 1024;
   static_assert(PIPE || FITS, "LDS budget");
 };
@@ -236,7 +240,11 @@ struct GateFoldArgs {
 // FOLD >= 0: the gate backward is folded in, bf16 g_raw if FOLD & 1, activation FOLD >> 1:
 // 0: -exp(A) softplus(x), 1: lb sigmoid(exp(A) x), 2: lb sigmoid(x).
 // HVF: the per-chunk states h are [V,K] (FLA's state_v_first layout) instead of [K,V].
-template <int GATE, bool VEC_B, bool INTRA, bool PIPE = false, int FOLD = -1, bool HVF = false>
+// ORIG (KDA, comparator only): the local WY backward in the original 7-product formulation
+// (W-bar = -dR h^T, E-bar = A^T W-bar, Z-bar = A^T dR, T = dR Z^T + W-bar E^T, J = A^T T,
+// D = -strict_tril(J A^T); dbeta by its direct VJP on every row) in place of the residual
+// triple (P = A^T dR, D = -strict_tril(P R^T), E-bar = -P h^T).
+template <int GATE, bool VEC_B, bool INTRA, bool PIPE = false, int FOLD = -1, bool HVF = false, bool ORIG = false>
 __device__ __forceinline__ void chunk_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
@@ -250,7 +258,8 @@ __device__ __forceinline__ void chunk_body(
     float* small, bf16* xbuf, float* gbuf, PhaseIn& pin, const GateFoldArgs* gf = nullptr,
     float beta_sig = 0.f, int HQ = 0) {
   if (HQ <= 0) HQ = H;
-  using LY = PostLayout<GATE, VEC_B, INTRA, PIPE>;
+  using LY = PostLayout<GATE, VEC_B, INTRA, PIPE, ORIG>;
+  static_assert(!ORIG || (GATE == CG_VECTOR && !VEC_B && !INTRA && !PIPE), "original formulation: KDA only");
   using post::LDT;
   auto B16 = [&](int off) { return reinterpret_cast<bf16*>(regA + off); };
   auto B16b = [&](int off) { return reinterpret_cast<bf16*>(regB + off); };
@@ -378,12 +387,35 @@ __device__ __forceinline__ void chunk_body(
     lds_sync();
 #pragma unroll
     for (int w = 0; w < 8; ++w) any_fb |= sAny[w];
+    if constexpr (ORIG) {
+      // Z = beta v, E = beta k 2^g rows (bf16, swizzled) for T = dR Z^T + W-bar E^T
+      bf16* sZ = reinterpret_cast<bf16*>(regA + LY::OFF_O);
+      bf16* sE = sZ + C * KD;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int p = tid + 512 * i;
+        const int t = p >> 4, ch = p & 15;
+        const bf16x8 vv = *reinterpret_cast<const bf16x8*>(vb + (size_t)t * rsv + 8 * ch);
+        const bf16x8 kx = *reinterpret_cast<const bf16x8*>(k + kofs + (size_t)t * rsk + 8 * ch);
+        const f32x4 g0 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)t * rsk + 8 * ch);
+        const f32x4 g1 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)t * rsk + 8 * ch + 4);
+        const float be = sBeta[t];
+        bf16x8 z8, e8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          z8[j] = to_bf16(be * to_f32(vv[j]));
+          e8[j] = to_bf16(be * to_f32(kx[j]) * fast_exp2(j < 4 ? g0[j] : g1[j - 4]));
+        }
+        store_tr_chunk<16>(sZ, t, ch, __builtin_bit_cast(u32x4, z8));
+        store_tr_chunk<16>(sE, t, ch, __builtin_bit_cast(u32x4, e8));
+      }
+    }
     // persistent kernel: this item's q, k, g stream into region B during phases
     // 1-3 (issued after this phase's LDS writes, see dma_x's call below)
     if constexpr (PIPE) dma_qkg<GATE>(sQ, sK, sGr, q, k, g, pos, H, HQ, tid);
   }
   // the standalone intra adds the direct dbeta terms of every row
-  const bool has_fb = !VEC_B && (INTRA || any_fb != 0);
+  const bool has_fb = !VEC_B && (INTRA || ORIG || any_fb != 0);
   f32x4 aq[4], ak[4], aw[4];                   // dq, dk, dG of column kk, rows 16 I + 4 lg + r
   float dgk = 0.f;
 
@@ -471,8 +503,157 @@ __device__ __forceinline__ void chunk_body(
 
   if constexpr (!PIPE) load_state();
 
+  if constexpr (ORIG) {
+    // ---------------- original formulation: W-bar, E-bar, T, J (D follows in phase 2) ----------------
+    bf16* sZ = reinterpret_cast<bf16*>(regA + LY::OFF_O);
+    bf16* sE = sZ + C * KD;
+    bf16* sWb = sZ + 2 * C * KD;
+    bf16* sTh = sZ;                   // T hi/lo [64][64] over Z (after T is formed)
+    bf16* sTl = sZ + C * C;
+    bf16* sJh = sE;                   // J hi/lo [64][64] over E
+    bf16* sJl = sE + C * C;
+    // W-bar strip = -dR h^T (this wave's 16 key columns, all 64 rows)
+    f32x4 wb[4];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      f32x4 z = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) z = mfma(frag_row<16>(sdR, 16 * I, 32 * ks, l), fh[ks], z);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        wb[I][r] = -z[r];
+        sWb[tr_off<16>(16 * I + 4 * lg + r, kk)] = to_bf16(-z[r]);
+      }
+    }
+    // E-bar strip = A^T W-bar (rows s, over t >= s), K = 16 MFMAs: the accumulator layout of
+    // W-bar is the B layout; A^T's A operand is a transposed read of A's [t][s] rows.  The
+    // residual code carries aw = P h^T = -E-bar, so aw = -E-bar here.
+    auto mfma16 = [](bf16x4 a, bf16x4 b, f32x4 c) -> f32x4 {
+      typedef short s4 __attribute__((ext_vector_type(4)));
+      return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a), __builtin_bit_cast(s4, b), c, 0, 0, 0);
+    };
+    bf16x4 wh[4], wl[4];
+#pragma unroll
+    for (int J = 0; J < 4; ++J) wh[J] = split_hi4(wb[J], wl[J]);
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      f32x4 e = zero4();
+#pragma unroll
+      for (int J = I; J < 4; ++J) {
+        const int o = tr_off<8>(16 * J + 4 * lg + (lc >> 2), 16 * I + 4 * (lc & 3));
+        const bf16x4 ah = ds_read_tr4(sAh + o), al = ds_read_tr4(sAl + o);
+        e = mfma16(ah, wh[J], e);
+        e = mfma16(ah, wl[J], e);
+        e = mfma16(al, wh[J], e);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) aw[I][r] = -e[r];
+    }
+    lds_sync();                       // W-bar complete
+    // T = dR Z^T + W-bar E^T: wave (I = wv / 2) takes tiles (I, J) for J = 2 (wv & 1) + jj
+    const int I = wv >> 1;
+    f32x4 tt[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int J = 2 * (wv & 1) + jj;
+      f32x4 a = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        a = mfma(frag_row<16>(sdR, 16 * I, 32 * ks, l), frag_row<16>(sZ, 16 * J, 32 * ks, l), a);
+        a = mfma(frag_row<16>(sWb, 16 * I, 32 * ks, l), frag_row<16>(sE, 16 * J, 32 * ks, l), a);
+      }
+      tt[jj] = a;
+    }
+    lds_sync();                       // Z, E read: T hi/lo over Z
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int J = 2 * (wv & 1) + jj;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bf16 hh, ll;
+        split_bf16(tt[jj][r], hh, ll);
+        const int o = tr_off<8>(16 * I + 4 * lg + r, 16 * J + lc);
+        sTh[o] = hh;
+        sTl[o] = ll;
+      }
+    }
+    lds_sync();
+    // J = A^T T (rows s, over t >= s)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int Jc = 2 * (wv & 1) + jj;
+      f32x4 a = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (32 * ks + 31 < 16 * I) continue;      // A[t][s] = 0 for t < s
+        const bf16x8 ah = frag_tr<8>(sAh, 32 * ks, 16 * I, l), al = frag_tr<8>(sAl, 32 * ks, 16 * I, l);
+        const bf16x8 th = frag_tr<8>(sTh, 32 * ks, 16 * Jc, l), tl = frag_tr<8>(sTl, 32 * ks, 16 * Jc, l);
+        a = mfma(ah, th, a);
+        a = mfma(ah, tl, a);
+        a = mfma(al, th, a);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bf16 hh, ll;
+        split_bf16(a[r], hh, ll);
+        const int o = tr_off<8>(16 * I + 4 * lg + r, 16 * Jc + lc);
+        sJh[o] = hh;
+        sJl[o] = ll;
+      }
+    }
+    lds_sync();                       // J complete
+  }
+
   // ---------------- phase 2: L = scale tril(dO R^T), D = -strict_tril(P R^T), both orientations ----------------
-  {
+  if constexpr (ORIG) {
+    // L as in the residual code; D^T tiles from J A^T (rows s, columns i): A's rows s read
+    // along t, J's rows i along t.  Every wave reads A (region A) before any writes L / D
+    // there, hence the barrier between the products and the stores.
+    bf16* sJh = reinterpret_cast<bf16*>(regA + LY::OFF_O) + C * KD;
+    bf16* sJl = sJh + C * C;
+    const int I = wv >> 1;
+    f32x4 bLs[2], bDs[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int J = 2 * (wv & 1) + jj;
+      f32x4 bL = zero4(), bD = zero4();
+      if (J >= I) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          bL = mfma(frag_row<16>(sR, 16 * I, 32 * ks, l), frag_row<16>(sdO, 16 * J, 32 * ks, l), bL);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const bf16x8 ah = frag_row<8>(sAh, 16 * I, 32 * ks, l), al = frag_row<8>(sAl, 16 * I, 32 * ks, l);
+          const bf16x8 jh = frag_row<8>(sJh, 16 * J, 32 * ks, l), jl = frag_row<8>(sJl, 16 * J, 32 * ks, l);
+          bD = mfma(ah, jh, bD);
+          bD = mfma(ah, jl, bD);
+          bD = mfma(al, jh, bD);
+        }
+      }
+      bLs[jj] = bL;
+      bDs[jj] = bD;
+    }
+    lds_sync();
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int J = 2 * (wv & 1) + jj;
+      const int i = 16 * J + lc;
+      f32x4 lv, dv4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int s_ = 16 * I + 4 * lg + r;
+        lv[r] = (i >= s_) ? scale * bLs[jj][r] : 0.f;
+        dv4[r] = (i > s_) ? -bDs[jj][r] : 0.f;
+      }
+      bf16x4 lo;
+      bf16x4 hi = split_hi4(lv, lo);
+      *reinterpret_cast<bf16x4*>(Lrh + i * LDT + 16 * I + 4 * lg) = hi;
+      *reinterpret_cast<bf16x4*>(Lrl + i * LDT + 16 * I + 4 * lg) = lo;
+      hi = split_hi4(dv4, lo);
+      *reinterpret_cast<bf16x4*>(Drh + i * LDT + 16 * I + 4 * lg) = hi;
+      *reinterpret_cast<bf16x4*>(Drl + i * LDT + 16 * I + 4 * lg) = lo;
+    }
+  } else {
     const int I = wv >> 1;
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
@@ -542,7 +723,7 @@ __device__ __forceinline__ void chunk_body(
         *reinterpret_cast<bf16x4*>(Drl + i * LDT + 16 * I + 4 * lg) = lo;
       }
     }
-  }
+  }   // phase 2
 
   // ---------------- phase 3: dq_s = dO h^T, dk_s = R dh^T, dw = P h^T (16-column strip, 64 rows) ----------------
   {
@@ -559,11 +740,11 @@ __device__ __forceinline__ void chunk_body(
       for (int ks = 0; ks < 4; ++ks) {
         x = mfma(frag_row<16>(sdO, 16 * I, 32 * ks, l), fh[ks], x);
         y = mfma(frag_row<16>(sR, 16 * I, 32 * ks, l), fdh[ks], y);
-        z = mfma(frag_row<16>(sP, 16 * I, 32 * ks, l), fh[ks], z);
+        if constexpr (!ORIG) z = mfma(frag_row<16>(sP, 16 * I, 32 * ks, l), fh[ks], z);
       }
       aq[I] = x;
       ak[I] = y;
-      aw[I] = z;
+      if constexpr (!ORIG) aw[I] = z;
     }
   }
   }   // !INTRA: phases 1-3
@@ -1072,7 +1253,7 @@ __device__ __forceinline__ void chunk_body(
     if constexpr (!VEC_B) {
       const float be = sBeta[tid];
       const float pr = (sDbA[tid] + sDbA[64 + tid]) + (sDbA[128 + tid] + sDbA[192 + tid]);
-      float db = fabsf(be) < 1e-6f ? sDbB[tid] : pr / be;
+      float db = (ORIG || fabsf(be) < 1e-6f) ? sDbB[tid] : pr / be;
       // beta = s sigmoid(x) activated in the forward (use_beta_sigmoid_in_kernel):
       // dL/dx = dL/dbeta * s sigmoid (1 - sigmoid) = dL/dbeta * beta (1 - beta / s)
       if (beta_sig > 0.f) db *= be * (1.f - be / beta_sig);
@@ -1114,6 +1295,24 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
                                  nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
                                  reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
                                  nullptr, beta_sig, HQ);
+}
+
+// KDA in the original 7-product formulation (the same-GPU comparator, ORIG above)
+template <int DUMMY = 0>
+__global__ __launch_bounds__(512) void chunk_bwd_original_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
+    const float* __restrict__ g, const float* __restrict__ beta, const float* __restrict__ akk,
+    const bf16* __restrict__ hst, const bf16* __restrict__ dhst, bf16* __restrict__ dq_out,
+    bf16* __restrict__ dk_out, bf16* __restrict__ dv_out, float* __restrict__ dg_out,
+    float* __restrict__ dbeta_out, int T, int H, float scale) {
+  using LY = PostLayout<CG_VECTOR, false, false, false, true>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  PhaseIn pin;
+  chunk_body<CG_VECTOR, false, false, false, -1, false, true>(
+      q, k, v, vnew, dO, dR, g, beta, nullptr, nullptr, akk, hst, dhst, dq_out, dk_out, dv_out, dg_out, dbeta_out,
+      nullptr, nullptr, T, H, scale, nullptr, nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem,
+      smem + LY::REGION_A, reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin);
 }
 
 // KDA with the gate backward folded into the dg stores (no dg output)
@@ -1454,4 +1653,25 @@ extern "C" hipError_t fdr_chunk_bwd_gate_fold_noalloc(
   return gate_fold_launch(q, k, v, v_new, dO, dR, g, beta, Akk, h, dh, dq, dk, dv, dbeta, beta_sigmoid, g_raw,
                           raw_is_bf16, A_log, dt_bias, has_lower_bound, lower_bound, dg_raw, dA_log, ddt_bias, ws,
                           h_v_first, B, T, H, qk_heads, K, V, chunk, scale, stream);
+}
+
+extern "C" hipError_t fdr_chunk_bwd_original(const void* q, const void* k, const void* v, const void* v_new,
+                                             const void* dO, const void* dR, const float* g, const float* beta,
+                                             const float* Akk, const void* h, const void* dh, void* dq, void* dk,
+                                             void* dv, float* dg, float* dbeta, int B, int T, int H, int K, int V,
+                                             int chunk, float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  if (!q || !k || !v || !v_new || !dO || !dR || !g || !beta || !Akk || !h || !dh || !dq || !dk || !dv || !dg ||
+      !dbeta)
+    return hipErrorInvalidValue;
+  using LY = PostLayout<CG_VECTOR, false, false, false, true>;
+  static_assert(LY::BYTES <= 160 * 1024, "LDS budget");
+  auto kern = chunk_bwd_original_kernel<0>;
+  static bool attr_set[kMaxDevices] = {};
+  hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, stream, (const bf16*)q, (const bf16*)k,
+                     (const bf16*)v, (const bf16*)v_new, (const bf16*)dO, (const bf16*)dR, g, beta, Akk,
+                     (const bf16*)h, (const bf16*)dh, (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, T, H, scale);
+  return hipGetLastError();
 }

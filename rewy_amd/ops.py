@@ -348,6 +348,35 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
     return out
 
 
+def chunk_bwd_original(q, k, v, v_new, dO, dR, g, Akk, h, dh, scale, beta):
+    """KDA's chunk stage in the original 7-product formulation (fdr_chunk_bwd_original): the
+    same-GPU comparator of ``chunk_bwd``.  Returns dict(dq, dk, dv, dg, dbeta)."""
+    B, T, H, K = _dims(q)
+    V = V_SUPPORTED
+    dev = q.device
+    bf, f32 = torch.bfloat16, torch.float32
+    NT = T // CHUNK
+    for x, n in ((q, "q"), (k, "k")):
+        _need(x, n, bf, (B, T, H, K), dev)
+    for x, n in ((v, "v"), (v_new, "v_new"), (dO, "dO"), (dR, "dR")):
+        _need(x, n, bf, (B, T, H, V), dev)
+    _need(g, "g", f32, (B, T, H, K), dev)
+    _need(beta, "beta", f32, (B, T, H), dev)
+    _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
+    _need(h, "h", bf, (B, NT, H, K, V), dev)
+    _need(dh, "dh", bf, (B, NT, H, K, V), dev)
+    out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=bf), dk=torch.empty(B, T, H, K, device=dev, dtype=bf),
+               dv=torch.empty(B, T, H, V, device=dev, dtype=bf), dg=torch.empty_like(g),
+               dbeta=torch.empty(B, T, H, device=dev, dtype=f32))
+    P = _lib.ptr
+    st = _lib.load().fdr_chunk_bwd_original(P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), P(beta), P(Akk), P(h),
+                                            P(dh), P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dg"]),
+                                            P(out["dbeta"]), B, T, H, K, V, CHUNK, float(scale),
+                                            _lib.stream_handle(dev))
+    _lib.check(st, "fdr_chunk_bwd_original")
+    return out
+
+
 def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, fold, beta_sigmoid=0.0,
                          hvf=0, H=None):
     """chunk_bwd (KDA) with the gate backward folded into the dg stores."""
