@@ -21,6 +21,19 @@
  * h / (H / qk_heads); every other per-head tensor has H heads.  0 means H.  The gradients
  * dq / dk are written per value head ([B,T,H,K]); summing each group is the caller's.
  * gate_mode: 0 = none (DeltaNet), 1 = scalar (GDN), 2 = vector (KDA, GDN2).
+ *
+ * Variable-length batches (the `_varlen` entry points; FLA's IS_VARLEN indexing, which the
+ * reference's kernels take, e.g. kernels/endpoint_intra.py:58-63): B = 1 and N sequences
+ * packed along the token axis, sequence n on tokens [cu_seqlens[n], cu_seqlens[n+1]),
+ * starting anywhere.  Each sequence is cut into ceil(len / 64) chunks; the batch's chunks,
+ * num_chunks in all, are listed by chunk_indices[c] = (sequence, chunk of the sequence)
+ * (FLA prepare_chunk_indices) and a sequence's first chunk is chunk_offsets[n] (FLA
+ * prepare_chunk_offsets).  cu_seqlens, chunk_indices (int32 [num_chunks][2]) and
+ * chunk_offsets (int32 [N+1]) are device memory.  Token-indexed tensors have T =
+ * cu_seqlens[N] rows; per-chunk states have num_chunks chunks.  A sequence's last chunk
+ * may hold fewer than 64 tokens: its missing rows read as zero (a gate cumsum's as its
+ * last row) and are never written, so the results are those of the sequence zero-padded
+ * to whole chunks.  An empty sequence owns no chunk.
  */
 #ifndef REWY_AMD_H
 #define REWY_AMD_H
@@ -53,19 +66,20 @@ hipError_t fdr_state_bwd(const void* q, const void* k, const void* w, const floa
                          hipStream_t stream);
 
 /*
- * fdr_state_bwd over a variable-length batch: N sequences packed along T (B = 1),
- * sequence n owning chunks [chunk_offsets[n], chunk_offsets[n+1]) -- every sequence
- * starts on a chunk boundary (pad with zero keys, values and gates, which leave
- * the state untouched); an empty sequence passes its state through (dh0 = dht).  chunk_offsets: int32 [N+1],
- * device memory, chunk_offsets[N] = T / 64.  dht / dh0 are per sequence
- * [N,H,K,V]; dh is [T/64,H,K,V] in packed chunk order.  Replaces the reference's
+ * fdr_state_bwd over a variable-length batch (B = 1), sequence n owning chunks
+ * [chunk_offsets[n], chunk_offsets[n+1]) of num_chunks; an empty sequence passes its
+ * state through (dh0 = dht).  cu_seqlens null: every sequence starts on a 64-token
+ * boundary, chunk c on tokens [64 c, 64 c + 64) (T = 64 num_chunks); else the sequences
+ * start anywhere (the packing described at the top).  dht / dh0 are per sequence
+ * [N,H,K,V]; dh is [num_chunks,H,K,V] in packed chunk order.  Replaces the reference's
  * state_bwd with cu_seqlens / chunk_offsets (kernels/vector_state_gpu.py:47-67,
  * FLA's prepare_chunk_offsets).
  */
 hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, const float* g, int gate_mode,
                                 const void* dO, const float* aqk, const void* dv, const float* dht, void* dh,
-                                void* dr, float* dh0, int state_v_first, const int* chunk_offsets, int N, int T, int H, int qk_heads, int K,
-                                int V, int chunk, float scale, int value_block, hipStream_t stream);
+                                void* dr, float* dh0, int state_v_first, const int* chunk_offsets,
+                                const int* cu_seqlens, int N, int num_chunks, int H, int qk_heads, int K, int V,
+                                int chunk, float scale, int value_block, hipStream_t stream);
 
 /*
  * fdr_state_bwd for long rows and few heads, in three launches with a short sequential
@@ -126,6 +140,17 @@ hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v, const void
                          int h_v_first, int B, int T, int H, int qk_heads, int K, int V, int chunk, float scale,
                          hipStream_t stream);
 
+/* fdr_chunk_bwd over a variable-length batch whose sequences start anywhere (the packing
+ * described at the top; the reference's chunk-stage kernels with cu_seqlens / chunk_indices,
+ * e.g. kernels/endpoint_intra.py:58-63).  h, dh are [num_chunks,H,K,V] (or [V,K]). */
+hipError_t fdr_chunk_bwd_varlen(const void* q, const void* k, const void* v, const void* v_new, const void* dO,
+                                const void* dR, const float* g, int gate_mode, const float* beta,
+                                const void* b_gate, const void* w_gate, const float* Akk, const void* h,
+                                const void* dh, void* dq, void* dk, void* dv, float* dg, float* dbeta,
+                                float beta_sigmoid, void* db, void* dw, int h_v_first, const int* cu_seqlens,
+                                const int* chunk_indices, int num_chunks, int H, int qk_heads, int K, int V,
+                                int chunk, float scale, hipStream_t stream);
+
 /*
  * fdr_chunk_bwd for KDA (gate_mode 2, scalar beta, [K,V] states) in the original 7-product
  * formulation of the local WY backward -- the products of reference
@@ -157,6 +182,14 @@ hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const flo
                           const float* Akk, void* w, void* u, void* qg, void* kg, float* Aqk, int B,
                           int T, int H, int qk_heads, int K, int V, int chunk, float scale, hipStream_t stream);
 
+/* fdr_prepare_wu over a variable-length batch whose sequences start anywhere (the packing
+ * described at the top; FLA recompute_w_u_fwd with cu_seqlens / chunk_indices). */
+hipError_t fdr_prepare_wu_varlen(const void* q, const void* k, const void* v, const float* g, int gate_mode,
+                                 const float* beta, const void* b_gate, const void* w_gate, const float* Akk,
+                                 void* w, void* u, void* qg, void* kg, float* Aqk, const int* cu_seqlens,
+                                 const int* chunk_indices, int num_chunks, int H, int qk_heads, int K, int V,
+                                 int chunk, float scale, hipStream_t stream);
+
 /*
  * Forward state scan recomputed inside the backward.
  * Replaces FLA chunk_gated_delta_rule_fwd_h(k, w, u, g, initial_state, ...) -> (h, v_new, final)
@@ -171,14 +204,14 @@ hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, const float* g
                      int K, int V, int chunk, int value_block, hipStream_t stream);
 
 /*
- * fdr_fwd_h over a variable-length batch, with the packing and chunk_offsets of
+ * fdr_fwd_h over a variable-length batch, with the packing, chunk_offsets and cu_seqlens of
  * fdr_state_bwd_varlen; h0 / ht per sequence [N,H,K,V].  Replaces FLA's
  * chunk_gated_delta_rule_fwd_h with cu_seqlens (the recompute policy's call).
  */
 hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const float* g, int gate_mode,
                             const float* h0, void* h, void* v_new, float* ht, int state_v_first,
-                            const int* chunk_offsets, int N,
-                            int T, int H, int k_heads, int K, int V, int chunk, int value_block, hipStream_t stream);
+                            const int* chunk_offsets, const int* cu_seqlens, int N, int num_chunks, int H,
+                            int k_heads, int K, int V, int chunk, int value_block, hipStream_t stream);
 
 /*
  * Standalone matrix intra (the intra-chunk VJP of a vector-gated chunk), in place.
@@ -219,6 +252,13 @@ hipError_t fdr_fwd_prepare(const void* q, const void* k, const float* g, int gat
                            const float* beta, const void* b_gate, float* gc, float* Aqk, float* Akk,
                            int B, int T, int H, int qk_heads, int K, int chunk, float scale, hipStream_t stream);
 
+/* fdr_fwd_prepare over a variable-length batch whose sequences start anywhere (the packing
+ * described at the top; FLA's chunk_local_cumsum / fwd_intra / solve_tril with cu_seqlens). */
+hipError_t fdr_fwd_prepare_varlen(const void* q, const void* k, const float* g, int gate_mode, const float* beta,
+                                  const void* b_gate, float* gc, float* Aqk, float* Akk, const int* cu_seqlens,
+                                  const int* chunk_indices, int num_chunks, int H, int qk_heads, int K, int chunk,
+                                  float scale, hipStream_t stream);
+
 /*
  * Forward, chunk-parallel part 2: the output.  Replaces FLA's chunk_fwd_o:
  *   o_c = scale (q_c 2^gc_c) h_c + Aqk_c v_new_c      bf16 [B,T,H,V]
@@ -227,6 +267,13 @@ hipError_t fdr_fwd_prepare(const void* q, const void* k, const float* g, int gat
 hipError_t fdr_fwd_o(const void* q, const float* gc, int gate_mode, const float* Aqk, const void* h,
                      const void* v_new, void* o, int B, int T, int H, int qk_heads, int K, int V, int chunk,
                      float scale, hipStream_t stream);
+
+/* fdr_fwd_o over a variable-length batch whose sequences start anywhere (the packing
+ * described at the top; FLA chunk_fwd_o with cu_seqlens / chunk_indices). */
+hipError_t fdr_fwd_o_varlen(const void* q, const float* gc, int gate_mode, const float* Aqk, const void* h,
+                            const void* v_new, void* o, const int* cu_seqlens, const int* chunk_indices,
+                            int num_chunks, int H, int qk_heads, int K, int V, int chunk, float scale,
+                            hipStream_t stream);
 
 /*
  * KDA's in-kernel gate activation (use_gate_in_kernel=True) and its backward, as the

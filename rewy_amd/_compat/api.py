@@ -35,8 +35,9 @@ class ChunkFunction(torch.autograd.Function):
     def forward(ctx, op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w,
                 initial_state, cu_seqlens=None, gate=None, A_log=None, dt_bias=None, beta_act=None,
                 state_v_first=False):
-        # cu_seqlens (optimized backend on a GPU only): sequences packed on 64-token
-        # chunk boundaries, B = 1; the state scans restart at each sequence.
+        # cu_seqlens (optimized backend on a GPU only): B = 1 holds sequences packed along T,
+        # starting anywhere; every kernel takes the batch's chunk map and the state scans
+        # restart at each sequence.
         # gate = (lower_bound,) (KDA, optimized backend on a GPU, no padded tokens): g is the
         # raw gate, activated here by the HIP gate kernel; its backward, with dA_log and
         # ddt_bias, is folded into the chunk kernel.
@@ -49,10 +50,10 @@ class ChunkFunction(torch.autograd.Function):
         if state_v_first and not native:
             raise ValueError("V-first states in the chunk Function are the optimized GPU path's")
         if gate is not None and not (native and op == "kda"):
-            raise ValueError("the folded gate is the optimized GPU path's (KDA, batches without padded tokens)")
+            raise ValueError("the folded gate is the optimized GPU path's (KDA, chunk-aligned batches)")
         if beta_act is not None and not (native and op != "gdn2"):
             raise ValueError("the folded beta sigmoid is the optimized GPU path's (scalar beta)")
-        ctx.cu_seqlens, ctx.gate, ctx.beta_act, ctx.vf = cu_seqlens, gate, beta_act, bool(state_v_first)
+        ctx.gate, ctx.beta_act, ctx.vf = gate, beta_act, bool(state_v_first)
         ctx.g_dtype = None if g is None else g.dtype
         ctx.beta_dtype = None if beta is None else beta.dtype
         g_raw = None
@@ -64,14 +65,19 @@ class ChunkFunction(torch.autograd.Function):
             beta = beta_sigmoid(beta, beta_act, native=True)
         if backend == "optimized" and q.is_cuda:
             from ..hip_forward import chunk_forward_hip
+            from ..ops import Varlen
+            varlen = None if cu_seqlens is None else Varlen(cu_seqlens, q.device)
+            ctx.cu_seqlens = varlen            # the chunk map, reused by the backward
+            if gate is not None and varlen is not None and not varlen.aligned:
+                raise ValueError("the folded gate takes chunk-aligned sequences")
             o, final, sv = chunk_forward_hip(op, q, k, v, g=g, beta=beta, b=b, w=w,
                                              initial_state=initial_state, scale=scale,
-                                             output_final_state=output_final_state,
-                                             chunk_offsets=None if cu_seqlens is None else cu_seqlens // 64,
+                                             output_final_state=output_final_state, varlen=varlen,
                                              state_v_first=state_v_first)
         elif cu_seqlens is not None:
-            raise NotImplementedError("chunk-aligned packing is the optimized GPU path's layout")
+            raise NotImplementedError("packed cu_seqlens batches in the chunk Function are the optimized GPU path's")
         else:
+            ctx.cu_seqlens = None
             o, final, sv = chunk_forward(op, q, k, v, g=g, beta=beta, b=b, w=w,
                                          initial_state=initial_state, scale=scale,
                                          output_final_state=output_final_state)
@@ -185,46 +191,6 @@ def _unpack(x, bounds, Tp):
     return torch.cat(rows, 0)
 
 
-class _PackAligned(torch.autograd.Function):
-    """[1, T, ...] packed sequences (bounds (s, e)) -> [1, Tp, ...] with sequence n at
-    token starts[n] and the tail of its last chunk zero.  Block copies both ways (one
-    read and one write per element; only the pad tails are filled)."""
-
-    @staticmethod
-    def forward(ctx, x, bounds, starts, Tp):
-        ctx.bounds, ctx.starts, ctx.T = bounds, starts, x.shape[1]
-        out = x.new_empty((1, Tp) + tuple(x.shape[2:]))
-        for (s, e), a, a_next in zip(bounds, starts, starts[1:] + [Tp]):
-            out[:, a:a + e - s].copy_(x[:, s:e])
-            out[:, a + e - s:a_next].zero_()
-        return out
-
-    @staticmethod
-    def backward(ctx, grad):
-        return _take(grad, ctx.bounds, ctx.starts), None, None, None
-
-
-class _UnpackAligned(torch.autograd.Function):
-    """The inverse gather: [1, Tp, ...] -> [1, T, ...] (the real tokens only)."""
-
-    @staticmethod
-    def forward(ctx, y, bounds, starts):
-        ctx.bounds, ctx.starts, ctx.Tp = bounds, starts, y.shape[1]
-        return _take(y, bounds, starts)
-
-    @staticmethod
-    def backward(ctx, grad):
-        return _PackAligned.apply(grad.contiguous(), ctx.bounds, ctx.starts, ctx.Tp), None, None
-
-
-def _take(y, bounds, starts):
-    return torch.cat([y[:, a:a + e - s] for (s, e), a in zip(bounds, starts)], 1)
-
-
-def _pack_aligned(x, bounds, starts, Tp):
-    return None if x is None else _PackAligned.apply(x.contiguous(), bounds, starts, Tp)
-
-
 def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0,
            state_v_first=False, cu_seqlens=None, cu_seqlens_cpu=None, gate_fold=None, beta_act=None):
     """Layout adapters around the chunk Function (all autograd-transparent torch ops):
@@ -234,19 +200,21 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
       i_hv // (HV / H) (FLA's head map; dq / dk summed over each group); the torch paths
       repeat q and k over each group;
     * ``state_v_first``: initial / final states are [N, HV, V, K] at the boundary;
-    * ``cu_seqlens`` (B = 1, packed): on the optimized backend on a GPU every
-      sequence is zero-padded to whole 64-token chunks and the sequences stay packed
-      (the state scans restart at each sequence's first chunk: work scales with the
-      sum of the lengths); otherwise each is padded to the longest one and run as
-      one batch row.  Zero keys, values and log-gates leave the state untouched, so
-      outputs, final states and gradients of the real tokens are exact; padded
-      positions are dropped.
+    * ``cu_seqlens`` (B = 1, packed): on the optimized backend on a GPU the kernels take
+      the packed batch as it is, whatever the sequence lengths (each sequence's last chunk
+      may be partial; its missing rows read as zero and are never written; the state
+      scans restart at each sequence: work scales with the sum of the lengths);
+      otherwise each sequence is zero-padded to the longest one and run as one batch
+      row.  Zero keys, values and log-gates leave the state untouched, so outputs,
+      final states and gradients of the real tokens are exact; padded positions are
+      dropped.
 
     ``gate_fold`` = (lower_bound, A_log, dt_bias) (KDA's raw gate) and ``beta_act`` = s
-    (raw beta, activated as s * sigmoid): on the optimized backend on a GPU, for
-    batches that need no padded tokens, the activations run inside the chunk Function
-    and their backward rides in the chunk kernel; otherwise they run here as autograd
-    nodes of their own (padded tokens must keep zero activated gates)."""
+    (raw beta, activated as s * sigmoid): on the optimized backend on a GPU the
+    activations run inside the chunk Function and their backward rides in the chunk
+    kernel (the gate's only for chunk-aligned batches, which the folded kernel takes);
+    otherwise they run here as autograd nodes of their own (padded tokens must keep
+    zero activated gates)."""
     H, HV = q.shape[2], v.shape[2]
     native = backend == "optimized" and q.is_cuda
     bounds = aligned = None
@@ -259,8 +227,9 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
             raise ValueError(f"The number of initial states is expected to be equal to the number of input "
                              f"sequences, i.e., {len(bounds)} rather than {h0.shape[0]}.")
         aligned = all(s % 64 == 0 for s, e in bounds) and cu[-1] % 64 == 0
-    unpadded = native and (aligned if cu_seqlens is not None else q.shape[1] % 64 == 0)
-    if gate_fold is not None and not unpadded:
+    # no padded tokens anywhere: dense rows of whole chunks, or a packed batch (native)
+    unpadded = native and (cu_seqlens is not None or q.shape[1] % 64 == 0)
+    if gate_fold is not None and not (unpadded and (cu_seqlens is None or aligned)):
         from ..gates import KDAGate
         lb, A_log, dt_bias = gate_fold
         g = KDAGate.apply(g, A_log, dt_bias, lb, native)
@@ -291,17 +260,9 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
         else:
             o, final = _run(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta, b, w, h0, vf)
     elif unpadded:
-        # already on chunk boundaries: the kernels take the batch as it is
+        # packed natively: the kernels take the batch as it is
         o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta,
                                        b, w, h0, torch.tensor(cu, dtype=torch.int64), *fold, beta_act, vf)
-    elif native:
-        lens = [max(64, -(-(e - s) // 64) * 64) for s, e in bounds]
-        cu_al = torch.tensor([0] + lens, dtype=torch.int64).cumsum(0)
-        starts = cu_al[:-1].tolist()
-        xs = [_pack_aligned(x, bounds, starts, int(cu_al[-1])) for x in (q, k, v, g, beta, b, w)]
-        o, final = ChunkFunction.apply(op, backend, full_saving, scale, output_final_state, *xs, h0, cu_al,
-                                       None, None, None, None, vf)
-        o = _UnpackAligned.apply(o, bounds, starts)
     else:
         Tp = max(64, -(-max(e - s for s, e in bounds) // 64) * 64)
         xs = [_unpack(x, bounds, Tp) for x in (q, k, v, g, beta, b, w)]

@@ -28,30 +28,23 @@ _UNSUPPORTED = ("cp_context",)
 
 
 def _varlen(q, kw):
-    """Chunk offsets of a packed variable-length batch (``cu_seqlens``, B = 1), or None.
+    """The packed variable-length batch of ``cu_seqlens`` (B = 1) as an ``ops.Varlen``, or None.
 
-    The kernels take sequences that start on 64-token chunk boundaries (each padded
-    with zero keys, values and gates to a whole chunk, as the public operators do):
-    the state recurrences then restart at every sequence's first chunk and every other
-    kernel is chunk-local.  ``chunk_indices`` / ``chunk_offsets`` (FLA's, derived from
-    cu_seqlens) are implied by cu_seqlens here."""
+    Sequences start anywhere: every kernel takes the batch's chunk map (FLA's
+    chunk_indices / chunk_offsets, derived here from cu_seqlens; a sequence's last chunk
+    may be partial), and the state recurrences restart at every sequence's first chunk."""
     cu = kw.get("cu_seqlens")
     if cu is None:
         if kw.get("chunk_indices") is not None or kw.get("chunk_offsets") is not None:
             raise NotImplementedError("chunk_indices / chunk_offsets without cu_seqlens")
         return None
     B, T = q.shape[:2]
-    host = torch.as_tensor(cu).detach().to("cpu", torch.int64)
     if B != 1:
         raise ValueError(f"The batch size is expected to be 1 rather than {B} when using `cu_seqlens`.")
-    if host.ndim != 1 or host.numel() < 2 or int(host[0]) != 0 or int(host[-1]) != T:
+    vl = cu if isinstance(cu, ops.Varlen) else ops.Varlen(cu, q.device)
+    if vl.T != T:
         raise ValueError("cu_seqlens must rise from 0 to T")
-    if bool((host[1:] < host[:-1]).any()):
-        raise ValueError("cu_seqlens must not decrease")
-    if bool((host % ops.CHUNK != 0).any()):
-        raise NotImplementedError("HIP backward: every sequence of cu_seqlens must start on a 64-token chunk "
-                                  "boundary (pad each sequence to whole chunks)")
-    return host // ops.CHUNK
+    return vl
 
 
 def _check_common(kind, kw):
@@ -95,47 +88,56 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     _check_common(op, kw)
     vf = bool(state_v_first)
     hvf = vf if saved_h_v_first is None else bool(saved_h_v_first)
-    co = _varlen(q, kw)
+    vl = _varlen(q, kw)
     q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
     g = _f32(g)
     Aqk, Akk = _f32(Aqk), _f32(Akk)
-    if saved.get("h") is None and co is None and ops.affine_pays(v):
+    if saved.get("h") is None and vl is None and ops.affine_pays(v):
         # recompute policy, few heads: both recurrences side by side in affine-step form
-        pre = _prepare_vector(k, v, g, Akk, gates, q)
+        pre = _prepare_vector(k, v, g, Akk, gates, q, vl)
         h, v_new, dh, dR, dh0 = ops.recurrences(pre["qg"], pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR,
                                                 do, scale, aqk=Aqk, h0=_f32(initial_state), dht=_f32(dht),
                                                 want_dh0=initial_state is not None, state_v_first=vf)
         saved, hvf = dict(v_new=v_new, h=h), False
     else:
         if saved.get("h") is None:
-            saved, hvf = _recompute_vector(q, k, v, g, Akk, initial_state, gates, co, vf), False
-        dh, dR, dh0 = _state_vector(saved, g, do, scale, Aqk, dht, initial_state, co, vf)
+            saved, hvf = _recompute_vector(q, k, v, g, Akk, initial_state, gates, vl, vf), False
+        dh, dR, dh0 = _state_vector(saved, g, do, scale, Aqk, dht, initial_state, vl, vf)
+    # the folded gate backward takes chunk-aligned rows; a packed batch of sequences that
+    # start anywhere runs it after the chunk kernel (one elementwise pass over dg)
+    separate = gate_fold is not None and vl is not None and not vl.aligned
     out = ops.chunk_bwd(q, k, v, _bf(saved["v_new"]), do, dR, g, ops.GATE_VECTOR, Akk,
                         _bf(saved["h"]), dh, scale, beta=_f32(gates.get("beta")),
                         b=None if gates.get("b") is None else _bf(gates["b"]),
-                        w=None if gates.get("w") is None else _bf(gates["w"]), gate_fold=gate_fold,
-                        beta_sigmoid=beta_sigmoid, h_v_first=hvf)
+                        w=None if gates.get("w") is None else _bf(gates["w"]),
+                        gate_fold=None if separate else gate_fold, beta_sigmoid=beta_sigmoid, h_v_first=hvf,
+                        varlen=vl)
+    if separate:
+        from ..gates import kda_gate_bwd
+        out["dg"], out["dA_log"], out["ddt_bias"] = kda_gate_bwd(
+            out["dg"], gate_fold["g_raw"], gate_fold.get("A_log"), gate_fold.get("dt_bias"),
+            gate_fold.get("lower_bound"), native=True)
     return _group_sum(out, q.shape[2]), dh0
 
 
-def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, co=None, vf=False):
+def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, vl=None, vf=False):
     return ops.state_bwd(_bf(saved["qg"]), _bf(saved["kg"]), _bf(saved["w"]), g, ops.GATE_VECTOR, do, scale,
                          aqk=Aqk, dht=_f32(dht), want_dh0=initial_state is not None,
-                         method="auto" if co is None else "direct", chunk_offsets=co, state_v_first=vf)
+                         method="auto" if vl is None else "direct", varlen=vl, state_v_first=vf)
 
 
-def _prepare_vector(k, v, g, Akk, gates, q):
+def _prepare_vector(k, v, g, Akk, gates, q, vl=None):
     b = None if gates.get("b") is None else _bf(gates["b"])
     w = None if gates.get("w") is None else _bf(gates["w"])
     return ops.prepare_wu(k, v, Akk, ops.GATE_VECTOR, g=g, beta=_f32(gates.get("beta")), b=b, w=w, q=q,
-                          want_qkg=True)
+                          want_qkg=True, varlen=vl)
 
 
-def _recompute_vector(q, k, v, g, Akk, initial_state, gates, co=None, vf=False):
+def _recompute_vector(q, k, v, g, Akk, initial_state, gates, vl=None, vf=False):
     """w, u, qg, kg (fdr_prepare_wu) then h, v_new (fdr_fwd_h): the recompute policy."""
-    pre = _prepare_vector(k, v, g, Akk, gates, q)
+    pre = _prepare_vector(k, v, g, Akk, gates, q, vl)
     h, v_new, _ = ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
-                            method="auto" if co is None else "direct", chunk_offsets=co, state_v_first=vf)
+                            method="auto" if vl is None else "direct", varlen=vl, state_v_first=vf)
     return dict(w=pre["w"], u=pre["u"], qg=pre["qg"], kg=pre["kg"], v_new=v_new, h=h)
 
 
@@ -153,7 +155,10 @@ def kda_backward(q, k, v, beta, Aqk, Akk, scale, initial_state, do, dht, g, g_or
 
     ``beta_sigmoid`` (this build's addition, default off): s > 0 when ``beta`` is
     s * sigmoid(beta_raw) activated in the forward; db is then dL/dbeta_raw, the fused
-    beta-sigmoid backward of reference _compat/kda.py:204-205 done in the chunk kernel."""
+    beta-sigmoid backward of reference _compat/kda.py:204-205 done in the chunk kernel.
+
+    ``cu_seqlens``: a packed batch (B = 1) whose sequences start anywhere, or the
+    ``ops.Varlen`` chunk map built from it (the chunk Function passes the forward's)."""
     from ..runtime import record
     saved = dict(w=w, u=u, qg=qg, kg=kg, v_new=v_new, h=h)
     # the in-kernel gate's backward rides in the chunk kernel's dg stores (one pass fewer
@@ -193,26 +198,26 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
     (reference ``_scalar``, backends/backward.py:96-131)."""
     from ..runtime import record
     _check_common(op, kw)
-    co = _varlen(q, kw)
+    vl = _varlen(q, kw)
     q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
     g = _f32(g)
     A = _f32(A)
     beta = _f32(beta)
     gate = ops.GATE_SCALAR if op == "gdn" else ops.GATE_NONE
-    pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, q=q, want_aqk=True, scale=scale)
-    if co is None and q.shape[2] == v.shape[2] and ops.affine_pays(v):
+    pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, q=q, want_aqk=True, scale=scale, varlen=vl)
+    if vl is None and q.shape[2] == v.shape[2] and ops.affine_pays(v):
         # few heads: both recurrences side by side in affine-step form
         h, v_new, dh, dR, dh0 = ops.recurrences(q, k, pre["w"], pre["u"], g, gate, do, scale, aqk=pre["Aqk"],
                                                 h0=_f32(initial_state), dht=_f32(dht),
                                                 want_dh0=initial_state is not None, state_v_first=state_v_first)
     else:
         h, v_new, _ = ops.fwd_h(k, pre["w"], pre["u"], g, gate, h0=_f32(initial_state), method="direct",
-                                chunk_offsets=co, state_v_first=state_v_first)
+                                varlen=vl, state_v_first=state_v_first)
         dh, dR, dh0 = ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
-                                    want_dh0=initial_state is not None, method="auto" if co is None else "direct",
-                                    chunk_offsets=co, state_v_first=state_v_first)
+                                    want_dh0=initial_state is not None, method="auto" if vl is None else "direct",
+                                    varlen=vl, state_v_first=state_v_first)
     out = _group_sum(ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta,
-                                   beta_sigmoid=beta_sigmoid), q.shape[2])
+                                   beta_sigmoid=beta_sigmoid, varlen=vl), q.shape[2])
     record(op, "optimized_backward")
     return out, dh0
 

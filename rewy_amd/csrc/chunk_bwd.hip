@@ -120,15 +120,23 @@ __device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\
 // Position of one (batch, chunk, head) work item in the T-major tensors.  Heads
 // run fastest: work-groups in flight together read neighbouring heads of the
 // same tokens, i.e. contiguous HBM rows.
+// With cu_seqlens / chunk_indices (a packed variable-length batch: B = 1, T = 64 x the
+// chunk count) the chunk's first token and row count come from them; n = 64 otherwise.
 struct ChunkItem {
-  int h, c, b;
+  int h, c, b, n;
   size_t tok0, kofs, vofs, hoff, aofs;
-  __device__ __forceinline__ ChunkItem(int item, int T, int H) {
+  __device__ __forceinline__ ChunkItem(int item, int T, int H, const int* cu = nullptr, const int* ci = nullptr) {
     const int NT = T / C;
     h = item % H;
     c = (item / H) % NT;
     b = item / (H * NT);
+    n = C;
     tok0 = (size_t)b * T + (size_t)c * C;
+    if (cu) {
+      const Rows<true> r = chunk_rows<true>(cu, ci, b, c, T);
+      tok0 = r.tok0;
+      n = r.n;
+    }
     kofs = tok0 * H * KD + (size_t)h * KD;
     vofs = tok0 * H * VD + (size_t)h * VD;
     hoff = (((size_t)b * NT + c) * H + h) * KD * VD;
@@ -145,26 +153,28 @@ struct PhaseIn {
   float beta, g, gl;
 };
 
-template <int GATE, bool VEC_B>
+template <int GATE, bool VEC_B, bool MAP = false>
 __device__ __forceinline__ void load_phase_in(const float* __restrict__ akk, const float* __restrict__ beta,
                                               const float* __restrict__ g, const ChunkItem& it, int H, int tid,
                                               PhaseIn& pin) {
+  const Rows<MAP> rw{it.tok0, it.n};
   const size_t rsa = (size_t)H * C;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int p = tid + 512 * i;
-    pin.a[i] = *reinterpret_cast<const f32x4*>(akk + it.aofs + (size_t)(p >> 4) * rsa + 4 * (p & 15));
+    pin.a[i] = *reinterpret_cast<const f32x4*>(rw.src(akk + it.aofs + (size_t)(p >> 4) * rsa + 4 * (p & 15), p >> 4));
   }
-  const size_t row = (it.tok0 + (tid & (C - 1))) * H + it.h;
+  const int t = tid & (C - 1);
+  const size_t row = (it.tok0 + t) * H + it.h;
   pin.beta = 0.f;
   pin.g = 0.f;
   pin.gl = 0.f;
-  if constexpr (!VEC_B) pin.beta = beta[row];
+  if constexpr (!VEC_B) pin.beta = *rw.src(beta + row, t);
   if constexpr (GATE == CG_SCALAR) {
-    pin.g = g[row];
-    pin.gl = g[(it.tok0 + C - 1) * H + it.h];
+    pin.g = g[(it.tok0 + rw.clamp(t)) * H + it.h];
+    pin.gl = g[(it.tok0 + rw.clamp(C - 1)) * H + it.h];
   } else if constexpr (GATE == CG_VECTOR) {
-    pin.gl = g[it.kofs + (size_t)(C - 1) * H * KD + (tid & (KD - 1))];
+    pin.gl = g[it.kofs + (size_t)rw.clamp(C - 1) * H * KD + (tid & (KD - 1))];
   }
 }
 
@@ -244,7 +254,11 @@ struct GateFoldArgs {
 // (W-bar = -dR h^T, E-bar = A^T W-bar, Z-bar = A^T dR, T = dR Z^T + W-bar E^T, J = A^T T,
 // D = -strict_tril(J A^T); dbeta by its direct VJP on every row) in place of the residual
 // triple (P = A^T dR, D = -strict_tril(P R^T), E-bar = -P h^T).
-template <int GATE, bool VEC_B, bool INTRA, bool PIPE = false, int FOLD = -1, bool HVF = false, bool ORIG = false>
+// MAP: a packed variable-length batch whose sequences start anywhere (cu, ci: cu_seqlens and
+// chunk_indices); a sequence's last chunk may hold fewer than 64 rows, whose missing rows
+// read as zeros (the gate cumsum's as its last row) and are never written.
+template <int GATE, bool VEC_B, bool INTRA, bool PIPE = false, int FOLD = -1, bool HVF = false, bool ORIG = false,
+          bool MAP = false>
 __device__ __forceinline__ void chunk_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
@@ -256,10 +270,11 @@ __device__ __forceinline__ void chunk_body(
     const float* __restrict__ daqk, float* __restrict__ dq32, float* __restrict__ dk32,
     float* __restrict__ db32, int beta_complete, int item, int next_item, char* regA, char* regB,
     float* small, bf16* xbuf, float* gbuf, PhaseIn& pin, const GateFoldArgs* gf = nullptr,
-    float beta_sig = 0.f, int HQ = 0) {
+    float beta_sig = 0.f, int HQ = 0, const int* cu = nullptr, const int* ci = nullptr) {
   if (HQ <= 0) HQ = H;
   using LY = PostLayout<GATE, VEC_B, INTRA, PIPE, ORIG>;
   static_assert(!ORIG || (GATE == CG_VECTOR && !VEC_B && !INTRA && !PIPE), "original formulation: KDA only");
+  static_assert(!MAP || (!INTRA && !PIPE && !ORIG && FOLD < 0), "variable-length rows: the plain chunk kernel");
   using post::LDT;
   auto B16 = [&](int off) { return reinterpret_cast<bf16*>(regA + off); };
   auto B16b = [&](int off) { return reinterpret_cast<bf16*>(regB + off); };
@@ -291,7 +306,8 @@ __device__ __forceinline__ void chunk_body(
   float* sGl = small + LY::S_GL;       // [128] last-row gate (log2) per column
   int* sAny = reinterpret_cast<int*>(small + LY::S_ANY);   // [8] per-wave "some beta ~ 0" flags
 
-  const ChunkItem pos(item, T, H);
+  const ChunkItem pos = MAP ? ChunkItem(item, T, H, cu, ci) : ChunkItem(item, T, H);
+  const Rows<MAP> rw{pos.tok0, pos.n};
   const int h = pos.h;
   // the lane index is made opaque per call so that a persistent caller's loop
   // cannot hoist the (loop-invariant) LDS address arithmetic out of the body
@@ -357,7 +373,7 @@ __device__ __forceinline__ void chunk_body(
   } else {
     // (the persistent kernel stages A hi/lo at the end of the previous item)
     if constexpr (!PIPE) {
-      load_phase_in<GATE, VEC_B>(akk, beta, g, pos, H, tid, pin);
+      load_phase_in<GATE, VEC_B, MAP>(akk, beta, g, pos, H, tid, pin);
       stage_akk(pin, sAh, sAl, tid);
     }
 #pragma unroll
@@ -366,9 +382,9 @@ __device__ __forceinline__ void chunk_body(
       const int t = p >> 4, ch = p & 15;
       if constexpr (!PIPE) {
         const size_t o = vofs + (size_t)t * rsv + 8 * ch;
-        store_tr_chunk<16>(sdR, t, ch, *reinterpret_cast<const u32x4*>(dR + o));
-        store_tr_chunk<16>(sR, t, ch, *reinterpret_cast<const u32x4*>(vnew + o));
-        store_tr_chunk<16>(sdO, t, ch, *reinterpret_cast<const u32x4*>(dO + o));
+        store_tr_chunk<16>(sdR, t, ch, *reinterpret_cast<const u32x4*>(rw.src(dR + o, t)));
+        store_tr_chunk<16>(sR, t, ch, *reinterpret_cast<const u32x4*>(rw.src(vnew + o, t)));
+        store_tr_chunk<16>(sdO, t, ch, *reinterpret_cast<const u32x4*>(rw.src(dO + o, t)));
       }
     }
     int fb = 0;
@@ -449,16 +465,16 @@ __device__ __forceinline__ void chunk_body(
         const int v0 = vrow0 + 4 * lg;
         const size_t go = (size_t)t * rsv + v0;
         if constexpr (VEC_B) {
-          const bf16x4 w4 = *reinterpret_cast<const bf16x4*>(wgate + vofs + go);
-          const bf16x4 x4 = *reinterpret_cast<const bf16x4*>(vb + go);
+          const bf16x4 w4 = *reinterpret_cast<const bf16x4*>(rw.src(wgate + vofs + go, t));
+          const bf16x4 x4 = *reinterpret_cast<const bf16x4*>(rw.src(vb + go, t));
           bf16x4 o1, o2;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             o1[r] = to_bf16(to_f32(w4[r]) * acc[r]);
             o2[r] = to_bf16(to_f32(x4[r]) * acc[r]);
           }
-          *reinterpret_cast<bf16x4*>(dv_out + vofs + go) = o1;
-          *reinterpret_cast<bf16x4*>(dw_out + vofs + go) = o2;
+          *reinterpret_cast<bf16x4*>(rw.dst(dv_out + vofs + go, t)) = o1;
+          *reinterpret_cast<bf16x4*>(rw.dst(dw_out + vofs + go, t)) = o2;
         } else {
           const float be = sBeta[t];
           const bf16x4 r4 = *reinterpret_cast<const bf16x4*>(sR + tr_off<16>(t, v0));
@@ -469,10 +485,10 @@ __device__ __forceinline__ void chunk_body(
             o1[r] = to_bf16(be * acc[r]);
             pr += acc[r] * to_f32(r4[r]);
           }
-          *reinterpret_cast<bf16x4*>(dv_out + vofs + go) = o1;
+          *reinterpret_cast<bf16x4*>(rw.dst(dv_out + vofs + go, t)) = o1;
           pra[tt] += sum_lane_groups(pr, l);
           if (has_fb) {
-            const bf16x4 x4 = *reinterpret_cast<const bf16x4*>(vb + go);
+            const bf16x4 x4 = *reinterpret_cast<const bf16x4*>(rw.src(vb + go, t));
             float pv = 0.f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) pv += acc[r] * to_f32(x4[r]);
@@ -767,15 +783,15 @@ __device__ __forceinline__ void chunk_body(
       const int p = tid + 512 * i;
       const size_t o = kofs + (size_t)(p >> 4) * rsk + (p & 15) * 8;
       const size_t oq = qr.ofs + (size_t)(p >> 4) * qr.rs + (p & 15) * 8;
-      rq[i] = *reinterpret_cast<const u32x4*>(q + oq);
-      rk[i] = *reinterpret_cast<const u32x4*>(k + oq);
-      if constexpr (VEC_B) rb[i] = *reinterpret_cast<const u32x4*>(bgate + o);
+      rq[i] = *reinterpret_cast<const u32x4*>(rw.src(q + oq, p >> 4));
+      rk[i] = *reinterpret_cast<const u32x4*>(rw.src(k + oq, p >> 4));
+      if constexpr (VEC_B) rb[i] = *reinterpret_cast<const u32x4*>(rw.src(bgate + o, p >> 4));
     }
     if constexpr (GATE == CG_VECTOR) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int p = tid + 512 * i;              // 2048 pieces: token p >> 5, 4 columns
-        rg[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)(p >> 5) * rsk + (p & 31) * 4);
+        rg[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rw.clamp(p >> 5) * rsk + (p & 31) * 4);
       }
     }
     lds_sync();   // P, R, dO no longer needed: region B becomes q, k, g (, b)
@@ -1173,11 +1189,12 @@ __device__ __forceinline__ void chunk_body(
     for (int I = 0; I < 4; ++I) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int off = (16 * I + 4 * lg + r) * rsk32 + kk;
-        dqb[off] = to_bf16(aq[I][r]);
-        dkb[off] = to_bf16(ak[I][r]);
-        if constexpr (GATE == CG_VECTOR && FOLD < 0) dgb[off] = aw[I][r];
-        if constexpr (VEC_B) dbb[off] = to_bf16(adb[I][r]);
+        const int t = 16 * I + 4 * lg + r;
+        const int off = t * rsk32 + kk;
+        *rw.dst(dqb + off, t) = to_bf16(aq[I][r]);
+        *rw.dst(dkb + off, t) = to_bf16(ak[I][r]);
+        if constexpr (GATE == CG_VECTOR && FOLD < 0) *rw.dst(dgb + off, t) = aw[I][r];
+        if constexpr (VEC_B) *rw.dst(dbb + off, t) = to_bf16(adb[I][r]);
       }
     }
     if constexpr (FOLD >= 0) {
@@ -1257,7 +1274,7 @@ __device__ __forceinline__ void chunk_body(
       // beta = s sigmoid(x) activated in the forward (use_beta_sigmoid_in_kernel):
       // dL/dx = dL/dbeta * s sigmoid (1 - sigmoid) = dL/dbeta * beta (1 - beta / s)
       if (beta_sig > 0.f) db *= be * (1.f - be / beta_sig);
-      dbeta_out[row] = db;
+      *rw.dst(dbeta_out + row, tid) = db;
     }
     if constexpr (GATE == CG_SCALAR) {
       // row sums over the 8 waves' partials, then the reverse cumsum over the
@@ -1270,7 +1287,7 @@ __device__ __forceinline__ void chunk_body(
         const float y = lane_read(x, l + d < 64 ? l + d : 63);
         if (l + d < 64) x += y;
       }
-      dg_out[row] = x;
+      *rw.dst(dg_out + row, tid) = x;
     }
   }
   // persistent kernel: every wave's prefetch complete and this item's LDS reads
@@ -1278,7 +1295,7 @@ __device__ __forceinline__ void chunk_body(
   if constexpr (PIPE) lds_sync();
 }
 
-template <int GATE, bool VEC_B, bool HVF = false>
+template <int GATE, bool VEC_B, bool HVF = false, bool MAP = false>
 __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
@@ -1286,15 +1303,16 @@ __global__ __launch_bounds__(512) void chunk_bwd_kernel(
     const bf16* __restrict__ wgate, const float* __restrict__ akk, const bf16* __restrict__ hst,
     const bf16* __restrict__ dhst, bf16* __restrict__ dq_out, bf16* __restrict__ dk_out,
     bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out,
-    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale, float beta_sig, int HQ) {
+    bf16* __restrict__ db_out, bf16* __restrict__ dw_out, int T, int H, float scale, float beta_sig, int HQ,
+    const int* __restrict__ cu, const int* __restrict__ ci) {
   using LY = PostLayout<GATE, VEC_B>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
-  chunk_body<GATE, VEC_B, false, false, -1, HVF>(q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out,
-                                 dk_out, dv_out, dg_out, dbeta_out, db_out, dw_out, T, H, scale, nullptr,
-                                 nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
-                                 reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
-                                 nullptr, beta_sig, HQ);
+  chunk_body<GATE, VEC_B, false, false, -1, HVF, false, MAP>(
+      q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, dq_out, dk_out, dv_out, dg_out, dbeta_out, db_out,
+      dw_out, T, H, scale, nullptr, nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
+      reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin, nullptr, beta_sig, HQ, cu,
+      ci);
 }
 
 // KDA in the original 7-product formulation (the same-GPU comparator, ORIG above)
@@ -1435,9 +1453,23 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
                               const void* bgate, const void* wgate, const float* akk, const void* h,
                               const void* dh, void* dq, void* dk, void* dv, float* dg, float* dbeta,
                               void* db, void* dw, int B, int T, int H, int HQ, float scale, float beta_sig,
-                              hipStream_t s) {
+                              hipStream_t s, const int* cu = nullptr, const int* ci = nullptr) {
   const int items = B * H * (T / C);
   using LP = PostLayout<GATE, VEC_B, false, true>;
+  using LY = PostLayout<GATE, VEC_B>;
+  if (cu) {
+    // a packed variable-length batch (sequences starting anywhere): the plain kernel
+    auto kern = chunk_bwd_kernel<GATE, VEC_B, HVF, true>;
+    static bool attr_set[kMaxDevices] = {};
+    const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(items), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k,
+                       (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta,
+                       (const bf16*)bgate, (const bf16*)wgate, akk, (const bf16*)h, (const bf16*)dh,
+                       (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, beta_sig, HQ,
+                       cu, ci);
+    return hipGetLastError();
+  }
   // persistent form for scalar / no gate (measured slower for KDA: see the kernel)
   if constexpr (!HVF && LP::FITS && REWY_CHUNK_PIPE && (GATE != CG_VECTOR || REWY_CHUNK_PIPE > 1)) {
     auto kern = chunk_bwd_pipe_kernel<GATE, VEC_B>;    // static LDS only
@@ -1452,7 +1484,6 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
                        beta_sig, HQ);
     return hipGetLastError();
   }
-  using LY = PostLayout<GATE, VEC_B>;
   auto kern = chunk_bwd_kernel<GATE, VEC_B, HVF>;
   static bool attr_set[kMaxDevices] = {};
   const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
@@ -1461,7 +1492,8 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
   hipLaunchKernelGGL(kern, dim3(grid), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta,
                      (const bf16*)bgate, (const bf16*)wgate, akk, (const bf16*)h, (const bf16*)dh,
-                     (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, beta_sig, HQ);
+                     (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, beta_sig, HQ,
+                     nullptr, nullptr);
   return hipGetLastError();
 }
 
@@ -1469,15 +1501,13 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
 
 using namespace rewy;
 
-extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v, const void* v_new,
-                                    const void* dO, const void* dR, const float* g, int gate_mode,
-                                    const float* beta, const void* b_gate, const void* w_gate,
-                                    const float* Akk, const void* h, const void* dh, void* dq,
-                                    void* dk, void* dv, float* dg, float* dbeta, float beta_sigmoid,
-                                    void* db, void* dw, int h_v_first, int B, int T, int H, int qk_heads,
-                                    int K, int V, int chunk, float scale, hipStream_t stream) {
-  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0)
-    return hipErrorInvalidValue;
+// B rows of T tokens, or (cu, ci) a packed batch of T / 64 chunks
+static hipError_t chunk_bwd_dispatch(const void* q, const void* k, const void* v, const void* v_new, const void* dO,
+                                     const void* dR, const float* g, int gate_mode, const float* beta,
+                                     const void* b_gate, const void* w_gate, const float* Akk, const void* h,
+                                     const void* dh, void* dq, void* dk, void* dv, float* dg, float* dbeta,
+                                     float beta_sigmoid, void* db, void* dw, int h_v_first, int B, int T, int H,
+                                     int qk_heads, float scale, hipStream_t stream, const int* cu, const int* ci) {
   const int HQ = qk_heads > 0 ? qk_heads : H;
   if (H % HQ || (b_gate && HQ != H)) return hipErrorInvalidValue;
   if (!(beta_sigmoid >= 0.f) || (beta_sigmoid > 0.f && b_gate)) return hipErrorInvalidValue;
@@ -1490,7 +1520,7 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
   if (vec_b && gate_mode != CG_VECTOR) return hipErrorInvalidValue;
 #define FDR_POST(G, VB, HV)                                                                     \
   return launch_post<G, VB, HV>(q, k, v, v_new, dO, dR, g, beta, b_gate, w_gate, Akk, h, dh, dq, dk, \
-                                dv, dg, dbeta, db, dw, B, T, H, HQ, scale, beta_sigmoid, stream)
+                                dv, dg, dbeta, db, dw, B, T, H, HQ, scale, beta_sigmoid, stream, cu, ci)
   if (h_v_first) {
     // [V,K] states come from a saved forward: the vector-gate families (full saving)
     if (gate_mode != CG_VECTOR) return hipErrorInvalidValue;
@@ -1505,6 +1535,35 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
     default: return hipErrorInvalidValue;
   }
 #undef FDR_POST
+}
+
+extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v, const void* v_new,
+                                    const void* dO, const void* dR, const float* g, int gate_mode,
+                                    const float* beta, const void* b_gate, const void* w_gate,
+                                    const float* Akk, const void* h, const void* dh, void* dq,
+                                    void* dk, void* dv, float* dg, float* dbeta, float beta_sigmoid,
+                                    void* db, void* dw, int h_v_first, int B, int T, int H, int qk_heads,
+                                    int K, int V, int chunk, float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0)
+    return hipErrorInvalidValue;
+  return chunk_bwd_dispatch(q, k, v, v_new, dO, dR, g, gate_mode, beta, b_gate, w_gate, Akk, h, dh, dq, dk, dv, dg,
+                            dbeta, beta_sigmoid, db, dw, h_v_first, B, T, H, qk_heads, scale, stream, nullptr,
+                            nullptr);
+}
+
+extern "C" hipError_t fdr_chunk_bwd_varlen(const void* q, const void* k, const void* v, const void* v_new,
+                                           const void* dO, const void* dR, const float* g, int gate_mode,
+                                           const float* beta, const void* b_gate, const void* w_gate,
+                                           const float* Akk, const void* h, const void* dh, void* dq, void* dk,
+                                           void* dv, float* dg, float* dbeta, float beta_sigmoid, void* db,
+                                           void* dw, int h_v_first, const int* cu_seqlens,
+                                           const int* chunk_indices, int num_chunks, int H, int qk_heads, int K,
+                                           int V, int chunk, float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || num_chunks <= 0 || H <= 0 || !cu_seqlens || !chunk_indices)
+    return hipErrorInvalidValue;
+  return chunk_bwd_dispatch(q, k, v, v_new, dO, dR, g, gate_mode, beta, b_gate, w_gate, Akk, h, dh, dq, dk, dv, dg,
+                            dbeta, beta_sigmoid, db, dw, h_v_first, 1, num_chunks * C, H, qk_heads, scale, stream,
+                            cu_seqlens, chunk_indices);
 }
 
 namespace rewy {

@@ -90,6 +90,71 @@ __device__ __forceinline__ QKRows qk_rows(size_t tok0, int h, int H, int HQ) {
   return QKRows{tok0 * rs + (size_t)(h / (H / HQ)) * KD, rs};
 }
 
+// ---------------------------------------------------------------------------
+// Variable-length batches packed along the token axis (B = 1) whose sequences start
+// anywhere: FLA's IS_VARLEN indexing, cu_seqlens [N+1] token offsets and, for chunk c of
+// the batch, chunk_indices[c] = (sequence, chunk of that sequence).  The last chunk of a
+// sequence may hold fewer than 64 rows.  Its missing rows are masked: data rows load as
+// zeros (from a zero page), rows of a chunk-local gate cumsum load as the last row that
+// exists (the value a zero-padded row's cumsum continues with), and their stores go to a
+// sink page.  The arithmetic is then exactly that of the sequence zero-padded to whole
+// chunks, without the padded copy.  MAP = false is the dense layout (every chunk full),
+// for which every helper is the identity.
+// ---------------------------------------------------------------------------
+static __device__ __attribute__((aligned(64))) uint32_t zero_page[16];   // never written
+static __device__ __attribute__((aligned(64))) uint32_t sink_page[16];   // never read
+
+template <bool MAP>
+struct Rows {
+  size_t tok0;   // token of row 0
+  int n;         // rows that exist (C unless MAP)
+  __device__ __forceinline__ bool ok(int t) const {
+    if constexpr (MAP) return t < n;
+    else return true;
+  }
+  __device__ __forceinline__ int clamp(int t) const {
+    if constexpr (MAP) return t < n ? t : n - 1;
+    else return t;
+  }
+  // address of row t's element p for a load (the zero page for a missing row)
+  template <class X>
+  __device__ __forceinline__ const X* src(const X* p, int t) const {
+    if constexpr (MAP) return t < n ? p : reinterpret_cast<const X*>(zero_page);
+    else return p;
+  }
+  // address of row t's element p for a store (the sink page for a missing row)
+  template <class X>
+  __device__ __forceinline__ X* dst(X* p, int t) const {
+    if constexpr (MAP) return t < n ? p : reinterpret_cast<X*>(sink_page);
+    else return p;
+  }
+};
+
+// Rows of chunk c of batch row b (dense: T tokens per row), or (MAP) of chunk c of the
+// packed batch
+template <bool MAP>
+__device__ __forceinline__ Rows<MAP> chunk_rows(const int* cu, const int* ci, int b, int c, int T) {
+  if constexpr (MAP) {
+    const int s = ci[2 * c], j = ci[2 * c + 1];
+    const int t0 = cu[s] + C * j;
+    return Rows<MAP>{(size_t)t0, min(C, cu[s + 1] - t0)};
+  } else {
+    return Rows<MAP>{(size_t)b * T + (size_t)c * C, C};
+  }
+}
+
+// Rows of chunk j of sequence s of a packed batch: on 64-token boundaries
+// (cu == nullptr: the sequence's chunk j is batch chunk cglob) or (MAP) from cu_seqlens
+template <bool MAP>
+__device__ __forceinline__ Rows<MAP> seq_chunk_rows(const int* cu, int s, int j, int cglob) {
+  if constexpr (MAP) {
+    const int t0 = cu[s] + C * j;
+    return Rows<MAP>{(size_t)t0, min(C, cu[s + 1] - t0)};
+  } else {
+    return Rows<MAP>{(size_t)cglob * C, C};
+  }
+}
+
 // e^x on the hardware exp2 unit
 __device__ __forceinline__ float exp_f(float x) { return fast_exp2(x * 1.4426950408889634f); }
 // softplus(x) = log(1 + e^x) from y = e^x: torch's threshold (x > 20 returns x), log1p's

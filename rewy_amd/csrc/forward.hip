@@ -23,6 +23,7 @@
 // log2 units (where the k-side factor could overflow) is evaluated pairwise in
 // fp32 instead.
 #include "common.hpp"
+#include "rewy_amd.h"
 
 namespace rewy {
 
@@ -60,11 +61,12 @@ struct PrepareSmem {
   int wide[4];               // diagonal block I takes the pairwise path
 };
 
-template <int GATE, bool VEC_B>
+template <int GATE, bool VEC_B, bool MAP>
 __global__ __launch_bounds__(512) void fwd_prepare_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ graw,
     const float* __restrict__ beta, const bf16* __restrict__ bgate, float* __restrict__ gc_out,
-    float* __restrict__ aqk_out, float* __restrict__ akk_out, int T, int H, int HQ, float scale) {
+    float* __restrict__ aqk_out, float* __restrict__ akk_out, int T, int H, int HQ, float scale,
+    const int* __restrict__ cu, const int* __restrict__ ci) {
   using fwd::LDG;
   using fwd::LDK;
   using fwd::LDM;
@@ -89,7 +91,8 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
   const int b = blk / (H * NT);
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int lc = l & 15, lg = l >> 4;
-  const size_t tok0 = (size_t)b * T + (size_t)c * C;
+  const Rows<MAP> rw = chunk_rows<MAP>(cu, ci, b, c, T);
+  const size_t tok0 = rw.tok0;
   const size_t rsk = (size_t)H * KD;
   const size_t kofs = tok0 * rsk + (size_t)h * KD;
   const size_t mofs = (tok0 * H + h) * C;      // [t][64] matrices of this chunk-head
@@ -101,20 +104,23 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
   for (int i = 0; i < 2; ++i) {
     const int p = tid + 512 * i;
     const int t = p >> 4, c8 = (p & 15) * 8;
-    *reinterpret_cast<u32x4*>(&sq[t][c8]) = *reinterpret_cast<const u32x4*>(q + qr.ofs + (size_t)t * qr.rs + c8);
-    *reinterpret_cast<u32x4*>(&sk[t][c8]) = *reinterpret_cast<const u32x4*>(k + qr.ofs + (size_t)t * qr.rs + c8);
+    *reinterpret_cast<u32x4*>(&sq[t][c8]) =
+        *reinterpret_cast<const u32x4*>(rw.src(q + qr.ofs + (size_t)t * qr.rs + c8, t));
+    *reinterpret_cast<u32x4*>(&sk[t][c8]) =
+        *reinterpret_cast<const u32x4*>(rw.src(k + qr.ofs + (size_t)t * qr.rs + c8, t));
     if constexpr (VEC_B)
-      *reinterpret_cast<u32x4*>(&sb[t][c8]) = *reinterpret_cast<const u32x4*>(bgate + kofs + (size_t)t * rsk + c8);
+      *reinterpret_cast<u32x4*>(&sb[t][c8]) =
+          *reinterpret_cast<const u32x4*>(rw.src(bgate + kofs + (size_t)t * rsk + c8, t));
   }
   if constexpr (!VEC_B) {
-    if (tid < C) sbeta[tid] = beta[(tok0 + tid) * H + h];
+    if (tid < C) sbeta[tid] = *rw.src(beta + (tok0 + tid) * H + h, tid);
   }
   if constexpr (GATE == FG_VECTOR) {
     // four threads per channel, 16 rows each: local sums, then the carries
     const int col = tid & 127, part = tid >> 7;
     float v[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = graw[kofs + (size_t)(16 * part + r) * rsk + col];
+    for (int r = 0; r < 16; ++r) v[r] = *rw.src(graw + kofs + (size_t)(16 * part + r) * rsk + col, 16 * part + r);
 #pragma unroll
     for (int r = 1; r < 16; ++r) v[r] += v[r - 1];
 #pragma unroll
@@ -127,11 +133,11 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
     for (int r = 0; r < 16; ++r) {
       const float x = (v[r] + carry) * fwd::RCP_LN2;
       sg[16 * part + r][col] = x;
-      gc_out[kofs + (size_t)(16 * part + r) * rsk + col] = x;
+      *rw.dst(gc_out + kofs + (size_t)(16 * part + r) * rsk + col, 16 * part + r) = x;
     }
   } else if constexpr (GATE == FG_SCALAR) {
     if (wv == 0) {
-      float x = graw[(tok0 + l) * H + h];
+      float x = *rw.src(graw + (tok0 + l) * H + h, l);
 #pragma unroll
       for (int d = 1; d < 64; d <<= 1) {
         const float y = __shfl_up(x, d);
@@ -139,7 +145,7 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
       }
       x *= fwd::RCP_LN2;
       sgs[l] = x;
-      gc_out[(tok0 + l) * H + h] = x;
+      *rw.dst(gc_out + (tok0 + l) * H + h, l) = x;
     }
   }
   lds_barrier();
@@ -248,7 +254,7 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * I + 4 * lg + r;
-        aqk_out[mofs + (size_t)i * rsm + s] = (s <= i) ? scale * aqk[jj][r] : 0.f;
+        *rw.dst(aqk_out + mofs + (size_t)i * rsm + s, i) = (s <= i) ? scale * aqk[jj][r] : 0.f;
       }
     }
   }
@@ -263,7 +269,7 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
   for (int p = tid; p < 6 * 256; p += 512) {
     int i, s_;
     upper(p, i, s_);
-    aqk_out[mofs + (size_t)i * rsm + s_] = 0.f;
+    *rw.dst(aqk_out + mofs + (size_t)i * rsm + s_, i) = 0.f;
   }
   lds_barrier();                                // staged rows and gates dead: M and X take their LDS
   // M tiles from the accumulators (lane: rows i = 16 I + 4 lg + r, column s = 16 J + lc), upper tiles zero
@@ -358,7 +364,7 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
   for (int i = 0; i < 2; ++i) {
     const int p = tid + 512 * i;
     const int t = p >> 4, c4 = (p & 15) * 4;
-    *reinterpret_cast<f32x4*>(akk_out + mofs + (size_t)t * rsm + c4) =
+    *reinterpret_cast<f32x4*>(rw.dst(akk_out + mofs + (size_t)t * rsm + c4, t)) =
         f32x4{sX[t][c4], sX[t][c4 + 1], sX[t][c4 + 2], sX[t][c4 + 3]};
   }
 }
@@ -366,11 +372,12 @@ __global__ __launch_bounds__(512) void fwd_prepare_kernel(
 // ------------------------------------------------------------------------------------------
 // fdr_fwd_o:  o = scale (q 2^g) h_c + Aqk v_new
 // ------------------------------------------------------------------------------------------
-template <int GATE>
+template <int GATE, bool MAP>
 __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, const float* __restrict__ gc,
                                                      const float* __restrict__ aqk, const bf16* __restrict__ hst,
                                                      const bf16* __restrict__ vnew, bf16* __restrict__ o_out,
-                                                     int T, int H, int HQ, float scale) {
+                                                     int T, int H, int HQ, float scale,
+                                                     const int* __restrict__ cu, const int* __restrict__ ci) {
   // swizzled, unpadded tiles (80 KiB in all, so two work-groups share a CU)
   __shared__ __attribute__((aligned(16))) bf16 sqg[C * KD];       // scale q 2^g rows [i][k], hi
   __shared__ __attribute__((aligned(16))) bf16 sqgl[C * KD];      // lo
@@ -388,7 +395,8 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
   const int b = blk / (H * NT);
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int lc = l & 15, lg = l >> 4;
-  const size_t tok0 = (size_t)b * T + (size_t)c * C;
+  const Rows<MAP> rw = chunk_rows<MAP>(cu, ci, b, c, T);
+  const size_t tok0 = rw.tok0;
   const size_t rsk = (size_t)H * KD;
   const size_t kofs = tok0 * rsk + (size_t)h * KD;
   const size_t mofs = (tok0 * H + h) * C;
@@ -401,13 +409,14 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
     const int p = tid + 512 * i;
     const int t = p >> 4, c8 = (p & 15) * 8;
     const QKRows qr = qk_rows(tok0, h, H, HQ);
-    const bf16x8 qx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(q + qr.ofs + (size_t)t * qr.rs + c8));
+    const bf16x8 qx =
+        __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(rw.src(q + qr.ofs + (size_t)t * qr.rs + c8, t)));
     bf16x8 hi, lo;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float f = scale;
-      if constexpr (GATE == FG_VECTOR) f *= fast_exp2(gc[kofs + (size_t)t * rsk + c8 + j]);
-      else if constexpr (GATE == FG_SCALAR) f *= fast_exp2(gc[(tok0 + t) * H + h]);
+      if constexpr (GATE == FG_VECTOR) f *= fast_exp2(gc[kofs + (size_t)rw.clamp(t) * rsk + c8 + j]);
+      else if constexpr (GATE == FG_SCALAR) f *= fast_exp2(gc[(tok0 + rw.clamp(t)) * H + h]);
       bf16 hh, ll;
       split_bf16(to_f32(qx[j]) * f, hh, ll);
       hi[j] = hh;
@@ -415,9 +424,9 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
     }
     store_tr_chunk<16>(sqg, t, p & 15, __builtin_bit_cast(u32x4, hi));
     store_tr_chunk<16>(sqgl, t, p & 15, __builtin_bit_cast(u32x4, lo));
-    store_tr_chunk<16>(sv, t, p & 15, *reinterpret_cast<const u32x4*>(vnew + kofs + (size_t)t * rsk + c8));
+    store_tr_chunk<16>(sv, t, p & 15, *reinterpret_cast<const u32x4*>(rw.src(vnew + kofs + (size_t)t * rsk + c8, t)));
     const int c4 = (p & 15) * 4;
-    const f32x4 a = *reinterpret_cast<const f32x4*>(aqk + mofs + (size_t)t * rsm + c4);
+    const f32x4 a = *reinterpret_cast<const f32x4*>(rw.src(aqk + mofs + (size_t)t * rsm + c4, t));
     bf16x4 alo;
     const bf16x4 ahi = split_hi4(a, alo);
     *reinterpret_cast<bf16x4*>(sah + tr_off<8>(t, c4)) = ahi;
@@ -465,18 +474,19 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
   for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      o_out[kofs + (size_t)(16 * I + 4 * lg + r) * rsk + cb + 16 * ct + lc] = to_bf16(acc[ct][r]);
+      *rw.dst(o_out + kofs + (size_t)(16 * I + 4 * lg + r) * rsk + cb + 16 * ct + lc, 16 * I + 4 * lg + r) =
+          to_bf16(acc[ct][r]);
 }
 
 }  // namespace rewy
 
 using namespace rewy;
 
-extern "C" hipError_t fdr_fwd_prepare(const void* q, const void* k, const float* g, int gate_mode,
-                                      const float* beta, const void* b_gate, float* gc, float* Aqk, float* Akk,
-                                      int B, int T, int H, int qk_heads, int K, int chunk, float scale,
-                                      hipStream_t stream) {
-  if (K != KD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+// B rows of T tokens (cu == nullptr), or (cu, ci) a packed batch of NC chunks, T = NC * 64
+template <bool MAP>
+static hipError_t fwd_prepare_launch(const void* q, const void* k, const float* g, int gate_mode, const float* beta,
+                                     const void* b_gate, float* gc, float* Aqk, float* Akk, int B, int T, int H,
+                                     int qk_heads, float scale, hipStream_t stream, const int* cu, const int* ci) {
   const int HQ = qk_heads > 0 ? qk_heads : H;
   if (H % HQ || (b_gate && HQ != H)) return hipErrorInvalidValue;
   if (!q || !k || !Aqk || !Akk) return hipErrorInvalidValue;
@@ -485,9 +495,9 @@ extern "C" hipError_t fdr_fwd_prepare(const void* q, const void* k, const float*
   if (vec_b && gate_mode != FG_VECTOR) return hipErrorInvalidValue;
   if (!vec_b && !beta) return hipErrorInvalidValue;
   const dim3 grid(B * H * (T / C)), block(512);
-#define FDR_PREP(G, VB)                                                                              \
-  hipLaunchKernelGGL((fwd_prepare_kernel<G, VB>), grid, block, 0, stream, (const bf16*)q, (const bf16*)k, \
-                     g, beta, (const bf16*)b_gate, gc, Aqk, Akk, T, H, HQ, scale)
+#define FDR_PREP(G, VB)                                                                                 \
+  hipLaunchKernelGGL((fwd_prepare_kernel<G, VB, MAP>), grid, block, 0, stream, (const bf16*)q, (const bf16*)k, \
+                     g, beta, (const bf16*)b_gate, gc, Aqk, Akk, T, H, HQ, scale, cu, ci)
   if (vec_b) FDR_PREP(FG_VECTOR, true);
   else if (gate_mode == FG_VECTOR) FDR_PREP(FG_VECTOR, false);
   else if (gate_mode == FG_SCALAR) FDR_PREP(FG_SCALAR, false);
@@ -497,22 +507,59 @@ extern "C" hipError_t fdr_fwd_prepare(const void* q, const void* k, const float*
   return hipGetLastError();
 }
 
-extern "C" hipError_t fdr_fwd_o(const void* q, const float* gc, int gate_mode, const float* Aqk, const void* h,
-                                const void* v_new, void* o, int B, int T, int H, int qk_heads, int K, int V,
-                                int chunk, float scale, hipStream_t stream) {
-  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+template <bool MAP>
+static hipError_t fwd_o_launch(const void* q, const float* gc, int gate_mode, const float* Aqk, const void* h,
+                               const void* v_new, void* o, int B, int T, int H, int qk_heads, float scale,
+                               hipStream_t stream, const int* cu, const int* ci) {
   const int HQ = qk_heads > 0 ? qk_heads : H;
   if (H % HQ) return hipErrorInvalidValue;
   if (!q || !Aqk || !h || !v_new || !o) return hipErrorInvalidValue;
   if (gate_mode != FG_NONE && !gc) return hipErrorInvalidValue;
   const dim3 grid(B * H * (T / C)), block(512);
-#define FDR_O(G)                                                                                       \
-  hipLaunchKernelGGL((fwd_o_kernel<G>), grid, block, 0, stream, (const bf16*)q, gc, Aqk, (const bf16*)h, \
-                     (const bf16*)v_new, (bf16*)o, T, H, HQ, scale)
+#define FDR_O(G)                                                                                           \
+  hipLaunchKernelGGL((fwd_o_kernel<G, MAP>), grid, block, 0, stream, (const bf16*)q, gc, Aqk, (const bf16*)h, \
+                     (const bf16*)v_new, (bf16*)o, T, H, HQ, scale, cu, ci)
   if (gate_mode == FG_VECTOR) FDR_O(FG_VECTOR);
   else if (gate_mode == FG_SCALAR) FDR_O(FG_SCALAR);
   else if (gate_mode == FG_NONE) FDR_O(FG_NONE);
   else return hipErrorInvalidValue;
 #undef FDR_O
   return hipGetLastError();
+}
+
+extern "C" hipError_t fdr_fwd_prepare(const void* q, const void* k, const float* g, int gate_mode,
+                                      const float* beta, const void* b_gate, float* gc, float* Aqk, float* Akk,
+                                      int B, int T, int H, int qk_heads, int K, int chunk, float scale,
+                                      hipStream_t stream) {
+  if (K != KD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  return fwd_prepare_launch<false>(q, k, g, gate_mode, beta, b_gate, gc, Aqk, Akk, B, T, H, qk_heads, scale, stream,
+                                   nullptr, nullptr);
+}
+
+extern "C" hipError_t fdr_fwd_prepare_varlen(const void* q, const void* k, const float* g, int gate_mode,
+                                             const float* beta, const void* b_gate, float* gc, float* Aqk,
+                                             float* Akk, const int* cu_seqlens, const int* chunk_indices,
+                                             int num_chunks, int H, int qk_heads, int K, int chunk, float scale,
+                                             hipStream_t stream) {
+  if (K != KD || chunk != C || num_chunks <= 0 || H <= 0 || !cu_seqlens || !chunk_indices)
+    return hipErrorInvalidValue;
+  return fwd_prepare_launch<true>(q, k, g, gate_mode, beta, b_gate, gc, Aqk, Akk, 1, num_chunks * C, H, qk_heads,
+                                  scale, stream, cu_seqlens, chunk_indices);
+}
+
+extern "C" hipError_t fdr_fwd_o(const void* q, const float* gc, int gate_mode, const float* Aqk, const void* h,
+                                const void* v_new, void* o, int B, int T, int H, int qk_heads, int K, int V,
+                                int chunk, float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  return fwd_o_launch<false>(q, gc, gate_mode, Aqk, h, v_new, o, B, T, H, qk_heads, scale, stream, nullptr, nullptr);
+}
+
+extern "C" hipError_t fdr_fwd_o_varlen(const void* q, const float* gc, int gate_mode, const float* Aqk,
+                                       const void* h, const void* v_new, void* o, const int* cu_seqlens,
+                                       const int* chunk_indices, int num_chunks, int H, int qk_heads, int K, int V,
+                                       int chunk, float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || num_chunks <= 0 || H <= 0 || !cu_seqlens || !chunk_indices)
+    return hipErrorInvalidValue;
+  return fwd_o_launch<true>(q, gc, gate_mode, Aqk, h, v_new, o, 1, num_chunks * C, H, qk_heads, scale, stream,
+                            cu_seqlens, chunk_indices);
 }

@@ -17,6 +17,7 @@
 // layout stores w and u contiguously; A and E are split into bf16 hi + lo so
 // the products are fp32-faithful.
 #include "common.hpp"
+#include "rewy_amd.h"
 
 namespace rewy {
 
@@ -30,13 +31,14 @@ constexpr int T128 = KD * LDT * 2;
 // ------------------------------------------------------------------------------------------
 // fdr_prepare_wu
 // ------------------------------------------------------------------------------------------
-template <int GATE, bool VEC_B, bool WANT_QKG, bool WANT_AQK>
+template <int GATE, bool VEC_B, bool WANT_QKG, bool WANT_AQK, bool MAP>
 __global__ __launch_bounds__(256) void prepare_wu_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
     const bf16* __restrict__ wgate, const float* __restrict__ akk, bf16* __restrict__ w_out,
     bf16* __restrict__ u_out, bf16* __restrict__ qg_out, bf16* __restrict__ kg_out,
-    float* __restrict__ aqk_out, int T, int H, int HQ, float scale) {
+    float* __restrict__ aqk_out, int T, int H, int HQ, float scale, const int* __restrict__ cu,
+    const int* __restrict__ ci) {
   using rec::LDT;
   // Scalar or no gate with scalar beta: k is staged raw and E = (beta k) 2^g is formed
   // per operand fragment (one factor pair per token row), so Aqk reads k from LDS too
@@ -62,7 +64,8 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
   const int b = blk / (H * NT);
   const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int lc = l & 15, lg = l >> 4;
-  const size_t tok0 = (size_t)b * T + (size_t)c * C;
+  const Rows<MAP> rw = chunk_rows<MAP>(cu, ci, b, c, T);
+  const size_t tok0 = rw.tok0;
   const size_t rsk = (size_t)H * KD, rsv = (size_t)H * VD;
   const size_t kofs = tok0 * rsk + (size_t)h * KD;
   const size_t vofs = tok0 * rsv + (size_t)h * VD;
@@ -74,13 +77,14 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
   if constexpr (WANT_AQK) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      qa[ks] = *reinterpret_cast<const bf16x8*>(q + qr.ofs + (size_t)(16 * wv + lc) * qr.rs + 32 * ks + 8 * lg);
+      qa[ks] = *reinterpret_cast<const bf16x8*>(
+          rw.src(q + qr.ofs + (size_t)(16 * wv + lc) * qr.rs + 32 * ks + 8 * lg, 16 * wv + lc));
   }
   if (tid < C) {
     const size_t row = (tok0 + tid) * H + h;
-    const float gv = (GATE == RG_SCALAR) ? g[row] : 0.f;
+    const float gv = (GATE == RG_SCALAR) ? g[(tok0 + rw.clamp(tid)) * H + h] : 0.f;
     sG[tid] = gv;
-    sB[tid] = VEC_B ? 0.f : beta[row];
+    sB[tid] = VEC_B ? 0.f : *rw.src(beta + row, tid);
     sGe[tid] = (GATE == RG_SCALAR) ? fast_exp2(gv) : 1.f;
   }
   lds_barrier();
@@ -90,12 +94,14 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
   for (int i = 0; i < 4; ++i) {
     const int p = tid + 256 * i;            // 1024 pieces of 8 columns: row p >> 4
     const int t = p >> 4, ch = p & 15, c0 = 8 * ch;
-    const bf16x8 kx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(k + qr.ofs + (size_t)t * qr.rs + c0));
-    const bf16x8 vx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(v + vofs + (size_t)t * rsv + c0));
+    const bf16x8 kx =
+        __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(rw.src(k + qr.ofs + (size_t)t * qr.rs + c0, t)));
+    const bf16x8 vx =
+        __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(rw.src(v + vofs + (size_t)t * rsv + c0, t)));
     float ge[8], be[8], we[8];
     if constexpr (GATE == RG_VECTOR) {
-      const f32x4 g0 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)t * rsk + c0);
-      const f32x4 g1 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)t * rsk + c0 + 4);
+      const f32x4 g0 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rw.clamp(t) * rsk + c0);
+      const f32x4 g1 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rw.clamp(t) * rsk + c0 + 4);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         ge[j] = fast_exp2(g0[j]);
@@ -107,8 +113,10 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
       for (int j = 0; j < 8; ++j) ge[j] = s0;
     }
     if constexpr (VEC_B) {
-      const bf16x8 bx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(bgate + kofs + (size_t)t * rsk + c0));
-      const bf16x8 wx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(wgate + vofs + (size_t)t * rsv + c0));
+      const bf16x8 bx =
+          __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(rw.src(bgate + kofs + (size_t)t * rsk + c0, t)));
+      const bf16x8 wx =
+          __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(rw.src(wgate + vofs + (size_t)t * rsv + c0, t)));
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         be[j] = to_f32(bx[j]);
@@ -127,7 +135,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     store_tr_chunk<16>(eH, t, ch, __builtin_bit_cast(u32x4, eh));
     store_tr_chunk<16>(zH, t, ch, __builtin_bit_cast(u32x4, zh));
     // A rows: 64 x 64 fp32 = 1024 pieces of 4, one per (i, thread) here
-    const f32x4 a4 = *reinterpret_cast<const f32x4*>(akk + ((tok0 + t) * H + h) * C + 4 * ch);
+    const f32x4 a4 = *reinterpret_cast<const f32x4*>(rw.src(akk + ((tok0 + t) * H + h) * C + 4 * ch, t));
     bf16x4 alo;
     const bf16x4 ahi = split_hi4(a4, alo);
     *reinterpret_cast<bf16x4*>(&sAh[t][4 * ch]) = ahi;
@@ -140,10 +148,10 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     for (int i = 0; i < 4; ++i) {
       const int p = tid + 256 * i;          // 1024 pieces of 8
       const int t = p >> 4, c0 = (p & 15) * 8;
-      const u32x4 qq = *reinterpret_cast<const u32x4*>(q + qr.ofs + (size_t)t * qr.rs + c0);
-      const u32x4 kq = *reinterpret_cast<const u32x4*>(k + qr.ofs + (size_t)t * qr.rs + c0);
-      const float* gr = g + kofs + (size_t)t * rsk + c0;
-      const float* gl = g + kofs + (size_t)(C - 1) * rsk + c0;
+      const u32x4 qq = *reinterpret_cast<const u32x4*>(rw.src(q + qr.ofs + (size_t)t * qr.rs + c0, t));
+      const u32x4 kq = *reinterpret_cast<const u32x4*>(rw.src(k + qr.ofs + (size_t)t * qr.rs + c0, t));
+      const float* gr = g + kofs + (size_t)rw.clamp(t) * rsk + c0;
+      const float* gl = g + kofs + (size_t)rw.clamp(C - 1) * rsk + c0;
       const bf16* pq = reinterpret_cast<const bf16*>(&qq);
       const bf16* pk = reinterpret_cast<const bf16*>(&kq);
       bf16x8 oq, ok;
@@ -153,8 +161,8 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
         oq[j] = to_bf16(to_f32(pq[j]) * fast_exp2(gj));
         ok[j] = to_bf16(to_f32(pk[j]) * fast_exp2(gl[j] - gj));
       }
-      *reinterpret_cast<bf16x8*>(qg_out + kofs + (size_t)t * rsk + c0) = oq;
-      *reinterpret_cast<bf16x8*>(kg_out + kofs + (size_t)t * rsk + c0) = ok;
+      *reinterpret_cast<bf16x8*>(rw.dst(qg_out + kofs + (size_t)t * rsk + c0, t)) = oq;
+      *reinterpret_cast<bf16x8*>(rw.dst(kg_out + kofs + (size_t)t * rsk + c0, t)) = ok;
     }
   }
   lds_barrier();
@@ -192,7 +200,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
           bf16x4 o;
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[r] = to_bf16(acc[r]);
-          *reinterpret_cast<bf16x4*>(dst + (size_t)(16 * tt + lc) * rs + row0 + 4 * lg) = o;
+          *reinterpret_cast<bf16x4*>(rw.dst(dst + (size_t)(16 * tt + lc) * rs + row0 + 4 * lg, 16 * tt + lc)) = o;
         }
       }
     }
@@ -211,7 +219,9 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
           const bf16x8 a = qa[ks];
           bf16x8 bq;
           if constexpr (RAWK) bq = frag_row<16>(eH, 16 * J, 32 * ks);
-          else bq = *reinterpret_cast<const bf16x8*>(k + qr.ofs + (size_t)(16 * J + lc) * qr.rs + 32 * ks + 8 * lg);
+          else
+            bq = *reinterpret_cast<const bf16x8*>(
+                rw.src(k + qr.ofs + (size_t)(16 * J + lc) * qr.rs + 32 * ks + 8 * lg, 16 * J + lc));
           acc = mfma(a, bq, acc);
         }
       }
@@ -221,7 +231,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
         const int i = 16 * I + 4 * lg + r;
         float f = (i >= s) ? scale : 0.f;
         if constexpr (GATE == RG_SCALAR) f = (i >= s) ? scale * fast_exp2(sG[i] - sG[s]) : 0.f;
-        aqk_out[((tok0 + i) * H + h) * C + s] = acc[r] * f;
+        *rw.dst(aqk_out + ((tok0 + i) * H + h) * C + s, i) = acc[r] * f;
       }
     }
   }
@@ -242,12 +252,12 @@ struct FwdSmem {
   float lam[KD];
 };
 
-template <int BV, int GATE>
+template <int BV, int GATE, bool MAP>
 __global__ __launch_bounds__(512) void fwd_h_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ w, const bf16* __restrict__ u,
     const float* __restrict__ g, const float* __restrict__ h0, bf16* __restrict__ h_out,
     bf16* __restrict__ vnew_out, float* __restrict__ ht_out, int T, int H, const int* __restrict__ chunk_off,
-    int vf, int HQ) {
+    int vf, int HQ, const int* __restrict__ cu) {
   using S = FwdSmem<BV, GATE>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
@@ -296,33 +306,35 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
   u32x4 ru[NU];
   float rg_last = 0.f, rg_tok[2] = {0.f, 0.f};   // scalar gate: last row, the 2 rows this thread stages
   auto load_chunk = [&](int c) {
-    const size_t tok0 = (size_t)(c0 + c) * C;
+    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+    const size_t tok0 = rs_.tok0;
     const bf16* wb = w + tok0 * rsk + (size_t)h * KD;
     // gate first: its consumer (lambda) is the first thing staged.  Every lane
     // issues the same loads (clamped indices): no branch makes the vector-memory
     // wait counts lane- or wave-dependent.
     if constexpr (GATE == RG_VECTOR) {
-      rg_last = g[((tok0 + C - 1) * H + h) * KD + (tid & (KD - 1))];
+      rg_last = g[((tok0 + rs_.clamp(C - 1)) * H + h) * KD + (tid & (KD - 1))];
     } else if constexpr (GATE == RG_SCALAR) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) rg_tok[i] = g[(tok0 + ((tid + NTH * i) >> 4)) * H + h];
-      rg_last = g[(tok0 + C - 1) * H + h];
+      for (int i = 0; i < 2; ++i) rg_tok[i] = g[(tok0 + rs_.clamp((tid + NTH * i) >> 4)) * H + h];
+      rg_last = g[(tok0 + rs_.clamp(C - 1)) * H + h];
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
-      rw[i] = *reinterpret_cast<const u32x4*>(wb + (size_t)(p >> 4) * rsk + (p & 15) * 8);
+      rw[i] = *reinterpret_cast<const u32x4*>(rs_.src(wb + (size_t)(p >> 4) * rsk + (p & 15) * 8, p >> 4));
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
       const QKRows kr_ = qk_rows(tok0, h, H, HQ);     // k: raw (HQ heads) for scalar gates, kg (HQ = H) else
-      rk[i] = *reinterpret_cast<const u32x4*>(k + kr_.ofs + (size_t)(p >> 4) * kr_.rs + (p & 15) * 8);
+      rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + kr_.ofs + (size_t)(p >> 4) * kr_.rs + (p & 15) * 8, p >> 4));
     }
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
       const int p = min(tid + NTH * i, NPU - 1);
-      ru[i] = *reinterpret_cast<const u32x4*>(u + (tok0 + p / CHV) * rsv + (size_t)h * VD + v_base + (p % CHV) * 8);
+      ru[i] = *reinterpret_cast<const u32x4*>(
+          rs_.src(u + (tok0 + p / CHV) * rsv + (size_t)h * VD + v_base + (p % CHV) * 8, p / CHV));
     }
   };
   auto stage_chunk = [&]() {
@@ -373,7 +385,8 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     lds_barrier();
     stage_chunk();
     load_chunk(c + 1 < NT ? c + 1 : c);    // (the last chunk re-fetches itself: no branch)
-    const size_t tok0 = (size_t)(c0 + c) * C;
+    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+    const size_t tok0 = rs_.tok0;
     // h_c -> LDS (transposed, bf16); the same rounded values feed w h, as stored
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
@@ -437,7 +450,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
         bf16x8 o;
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = sm.vT[v0 + j][t];
-        *reinterpret_cast<bf16x8*>(vnew_out + (tok0 + t) * rsv + (size_t)h * VD + v_base + v0) = o;
+        *reinterpret_cast<bf16x8*>(rs_.dst(vnew_out + (tok0 + t) * rsv + (size_t)h * VD + v_base + v0, t)) = o;
       }
     }
     settle_chunk();    // the next chunk's operands, settled behind this chunk's stores
@@ -458,19 +471,27 @@ template <int GATE, bool VEC_B, bool QKG, bool AQK>
 static hipError_t launch_prepare(const void* q, const void* k, const void* v, const float* g,
                                  const float* beta, const void* bg, const void* wg, const float* akk,
                                  void* w, void* u, void* qg, void* kg, float* aqk, int B, int T, int H, int HQ,
-                                 float scale, hipStream_t s) {
-  hipLaunchKernelGGL((prepare_wu_kernel<GATE, VEC_B, QKG, AQK>), dim3(B * H * (T / C)), dim3(256), 0, s,
-                     (const bf16*)q, (const bf16*)k, (const bf16*)v, g, beta, (const bf16*)bg,
-                     (const bf16*)wg, akk, (bf16*)w, (bf16*)u, (bf16*)qg, (bf16*)kg, aqk, T, H, HQ, scale);
+                                 float scale, hipStream_t s, const int* cu, const int* ci) {
+#define P_LAUNCH(MAP)                                                                                            \
+  hipLaunchKernelGGL((prepare_wu_kernel<GATE, VEC_B, QKG, AQK, MAP>), dim3(B * H * (T / C)), dim3(256), 0, s,   \
+                     (const bf16*)q, (const bf16*)k, (const bf16*)v, g, beta, (const bf16*)bg, (const bf16*)wg, \
+                     akk, (bf16*)w, (bf16*)u, (bf16*)qg, (bf16*)kg, aqk, T, H, HQ, scale, cu, ci)
+  if (cu) P_LAUNCH(true);
+  else P_LAUNCH(false);
+#undef P_LAUNCH
   return hipGetLastError();
 }
 
 template <int BV, int GATE>
 static hipError_t launch_fwd_h(const void* k, const void* w, const void* u, const float* g, const float* h0,
                                void* h, void* vnew, float* ht, int B, int T, int H, hipStream_t s,
-                               const int* co, int vf, int HQ) {
-  hipLaunchKernelGGL((fwd_h_kernel<BV, GATE>), dim3(B * H * (VD / BV)), dim3(512), 0, s, (const bf16*)k,
-                     (const bf16*)w, (const bf16*)u, g, h0, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf, HQ);
+                               const int* co, int vf, int HQ, const int* cu) {
+#define F_LAUNCH(MAP)                                                                                            \
+  hipLaunchKernelGGL((fwd_h_kernel<BV, GATE, MAP>), dim3(B * H * (VD / BV)), dim3(512), 0, s, (const bf16*)k,     \
+                     (const bf16*)w, (const bf16*)u, g, h0, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf, HQ, cu)
+  if (cu) F_LAUNCH(true);
+  else F_LAUNCH(false);
+#undef F_LAUNCH
   return hipGetLastError();
 }
 
@@ -478,12 +499,11 @@ static hipError_t launch_fwd_h(const void* k, const void* w, const void* u, cons
 
 using namespace rewy;
 
-extern "C" hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const float* g,
-                                     int gate_mode, const float* beta, const void* b_gate,
-                                     const void* w_gate, const float* Akk, void* w, void* u, void* qg,
-                                     void* kg, float* Aqk, int B, int T, int H, int qk_heads, int K, int V,
-                                     int chunk, float scale, hipStream_t stream) {
-  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+// B rows of T tokens, or (cu, ci) a packed batch of T / 64 chunks
+static hipError_t prepare_dispatch(const void* q, const void* k, const void* v, const float* g, int gate_mode,
+                                   const float* beta, const void* b_gate, const void* w_gate, const float* Akk,
+                                   void* w, void* u, void* qg, void* kg, float* Aqk, int B, int T, int H,
+                                   int qk_heads, float scale, hipStream_t stream, const int* cu, const int* ci) {
   const int HQ = qk_heads > 0 ? qk_heads : H;
   if (H % HQ || (b_gate && HQ != H)) return hipErrorInvalidValue;
   if (!k || !v || !Akk || !w || !u) return hipErrorInvalidValue;
@@ -495,7 +515,7 @@ extern "C" hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v
   if (want_qkg && (!qg || !kg || !q || gate_mode != RG_VECTOR)) return hipErrorInvalidValue;
   const bool want_aqk = Aqk != nullptr;
   if (want_aqk && (!q || gate_mode == RG_VECTOR)) return hipErrorInvalidValue;
-#define P_ARGS q, k, v, g, beta, b_gate, w_gate, Akk, w, u, qg, kg, Aqk, B, T, H, HQ, scale, stream
+#define P_ARGS q, k, v, g, beta, b_gate, w_gate, Akk, w, u, qg, kg, Aqk, B, T, H, HQ, scale, stream, cu, ci
   switch (gate_mode) {
     case RG_NONE:
       return want_aqk ? launch_prepare<RG_NONE, false, false, true>(P_ARGS)
@@ -515,6 +535,28 @@ extern "C" hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v
 #undef P_ARGS
 }
 
+extern "C" hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const float* g,
+                                     int gate_mode, const float* beta, const void* b_gate,
+                                     const void* w_gate, const float* Akk, void* w, void* u, void* qg,
+                                     void* kg, float* Aqk, int B, int T, int H, int qk_heads, int K, int V,
+                                     int chunk, float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  return prepare_dispatch(q, k, v, g, gate_mode, beta, b_gate, w_gate, Akk, w, u, qg, kg, Aqk, B, T, H, qk_heads,
+                          scale, stream, nullptr, nullptr);
+}
+
+extern "C" hipError_t fdr_prepare_wu_varlen(const void* q, const void* k, const void* v, const float* g,
+                                            int gate_mode, const float* beta, const void* b_gate,
+                                            const void* w_gate, const float* Akk, void* w, void* u, void* qg,
+                                            void* kg, float* Aqk, const int* cu_seqlens, const int* chunk_indices,
+                                            int num_chunks, int H, int qk_heads, int K, int V, int chunk,
+                                            float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || num_chunks <= 0 || H <= 0 || !cu_seqlens || !chunk_indices)
+    return hipErrorInvalidValue;
+  return prepare_dispatch(q, k, v, g, gate_mode, beta, b_gate, w_gate, Akk, w, u, qg, kg, Aqk, 1, num_chunks * C, H,
+                          qk_heads, scale, stream, cu_seqlens, chunk_indices);
+}
+
 static int fwd_default_bv(int B, int H) {
   const int bh = B * H;
   if (bh * 2 >= 256) return 64;
@@ -522,18 +564,20 @@ static int fwd_default_bv(int B, int H) {
   return 16;
 }
 
-// B rows of T tokens, or (co) B sequences packed along T
+// B rows of T tokens, or (co) B sequences packed along T tokens on 64-token boundaries,
+// or (co, cu) B sequences packed anywhere along the token axis, in T / 64 chunks
 static hipError_t fwd_h_dispatch(const void* k, const void* w, const void* u, const float* g, int gate_mode,
                                  const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int HQ,
                                  int K, int V, int chunk, int value_block, hipStream_t stream, const int* co,
-                                 int vf) {
+                                 int vf, const int* cu) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
   if (HQ <= 0) HQ = H;
   if (H % HQ) return hipErrorInvalidValue;
   if (!k || !w || !u || !h || !v_new) return hipErrorInvalidValue;
   if (gate_mode != RG_NONE && !g) return hipErrorInvalidValue;
+  if (cu && !co) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : fwd_default_bv(B, H);
-#define F_ARGS k, w, u, g, h0, h, v_new, ht, B, T, H, stream, co, vf, HQ
+#define F_ARGS k, w, u, g, h0, h, v_new, ht, B, T, H, stream, co, vf, HQ, cu
 #define F_BV(G)                                                     \
   switch (bv) {                                                     \
     case 16: return launch_fwd_h<16, G>(F_ARGS);                    \
@@ -555,14 +599,15 @@ extern "C" hipError_t fdr_fwd_h(const void* k, const void* w, const void* u, con
                                 const float* h0, void* h, void* v_new, float* ht, int state_v_first, int B, int T,
                                 int H, int k_heads, int K, int V, int chunk, int value_block, hipStream_t stream) {
   return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, B, T, H, k_heads, K, V, chunk, value_block, stream,
-                        nullptr, state_v_first ? 1 : 0);
+                        nullptr, state_v_first ? 1 : 0, nullptr);
 }
 
 extern "C" hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const float* g, int gate_mode,
                                        const float* h0, void* h, void* v_new, float* ht, int state_v_first,
-                                       const int* chunk_offsets, int N, int T, int H, int k_heads, int K, int V,
-                                       int chunk, int value_block, hipStream_t stream) {
-  if (!chunk_offsets) return hipErrorInvalidValue;
-  return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, N, T, H, k_heads, K, V, chunk, value_block, stream,
-                        chunk_offsets, state_v_first ? 1 : 0);
+                                       const int* chunk_offsets, const int* cu_seqlens, int N, int num_chunks,
+                                       int H, int k_heads, int K, int V, int chunk, int value_block,
+                                       hipStream_t stream) {
+  if (!chunk_offsets || num_chunks <= 0) return hipErrorInvalidValue;
+  return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, N, num_chunks * C, H, k_heads, K, V, chunk,
+                        value_block, stream, chunk_offsets, state_v_first ? 1 : 0, cu_seqlens);
 }

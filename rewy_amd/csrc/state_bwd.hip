@@ -45,13 +45,13 @@ struct StateSmem {
 // Segmented form (segs > 0): row r of T tokens is split into `segs` segments of
 // consecutive chunks, work-group row b is segment b % segs of row b / segs, and dht holds
 // each segment's end state (from state_combine_kernel).
-template <int BV, int GATE, bool DV_FROM_AQK, int NW>
+template <int BV, int GATE, bool DV_FROM_AQK, int NW, bool MAP = false>
 __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ w,
     const float* __restrict__ g, const bf16* __restrict__ dO, const float* __restrict__ aqk,
     const bf16* __restrict__ dv, const float* __restrict__ dht, bf16* __restrict__ dh_out,
     bf16* __restrict__ dr_out, float* __restrict__ dh0, int T, int H, float scale,
-    const int* __restrict__ chunk_off, int segs, int vf, int HQ) {
+    const int* __restrict__ chunk_off, int segs, int vf, int HQ, const int* __restrict__ cu) {
   using S = StateSmem<BV, GATE, DV_FROM_AQK>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
@@ -120,14 +120,15 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   const size_t row_stride_v = (size_t)H * VD;
 
   auto load_chunk = [&](int c) {
-    const size_t tok0 = (size_t)(c0 + c) * C;
+    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+    const size_t tok0 = rs_.tok0;
     // gate first: its consumer (lambda) is the first thing staged
     if constexpr (GATE == GATE_VECTOR) {
-      if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
+      if (tid < KD) rg_last = g[((tok0 + rs_.clamp(C - 1)) * H + h) * KD + tid];
     } else if constexpr (GATE == GATE_SCALAR) {
 #pragma unroll
-      for (int i = 0; i < NPI; ++i) rg_tok[i] = g[(tok0 + ((tid + NTH * i) >> 4)) * H + h];
-      rg_last = g[(tok0 + C - 1) * H + h];
+      for (int i = 0; i < NPI; ++i) rg_tok[i] = g[(tok0 + rs_.clamp((tid + NTH * i) >> 4)) * H + h];
+      rg_last = g[(tok0 + rs_.clamp(C - 1)) * H + h];
     }
     const size_t kofs = tok0 * row_stride_k + (size_t)h * KD;
     // q / k: raw (HQ heads, grouped value heads) for scalar / no gates, qg / kg (HQ = H) else
@@ -137,18 +138,18 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       const int p = tid + NTH * i;
       const size_t o = kofs + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8;
       const size_t oq = qr.ofs + (size_t)(p >> 4) * qr.rs + (p & 15) * 8;
-      rk[i] = *reinterpret_cast<const u32x4*>(k + oq);
-      rq[i] = *reinterpret_cast<const u32x4*>(q + oq);
-      rw[i] = *reinterpret_cast<const u32x4*>(w + o);
+      rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + oq, p >> 4));
+      rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + oq, p >> 4));
+      rw[i] = *reinterpret_cast<const u32x4*>(rs_.src(w + o, p >> 4));
       if constexpr (DV_FROM_AQK)
-        ra[i] = *reinterpret_cast<const f32x4*>(aqk + ((tok0 + (p >> 4)) * H + h) * C + (p & 15) * 4);
+        ra[i] = *reinterpret_cast<const f32x4*>(rs_.src(aqk + ((tok0 + (p >> 4)) * H + h) * C + (p & 15) * 4, p >> 4));
     }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
       // every lane loads (clamped to a valid piece) so the wait counts stay static
       const int p = min(tid + NTH * i, NPD - 1);
-      rdo[i] = *reinterpret_cast<const u32x4*>(dO + (tok0 + p / CHV) * row_stride_v + (size_t)h * VD + v_base +
-                                               (p % CHV) * 8);
+      rdo[i] = *reinterpret_cast<const u32x4*>(
+          rs_.src(dO + (tok0 + p / CHV) * row_stride_v + (size_t)h * VD + v_base + (p % CHV) * 8, p / CHV));
     }
   };
 
@@ -226,11 +227,11 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
             a = mfma(frag_tr<8>(sm.al, 32 * ks, 16 * drow), bo, a);
           }
         } else {
-          const size_t tok0 = (size_t)(c0 + c) * C;
+          const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int t = 16 * drow + 4 * (l >> 4) + r;
-            a[r] = to_f32(dv[(tok0 + t) * row_stride_v + (size_t)h * VD + v_base + 16 * ct + (l & 15)]);
+            a[r] = to_f32(*rs_.src(dv + (rs_.tok0 + t) * row_stride_v + (size_t)h * VD + v_base + 16 * ct + (l & 15), t));
           }
         }
 #pragma unroll
@@ -275,7 +276,8 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
         for (int j = 0; j < 8; ++j) o[j] = sm.dhT[v0 + j][kr];
         *reinterpret_cast<bf16x8*>(dh_out + dh_base + (size_t)kr * VD + v_base + v0) = o;
       }
-      const size_t tok0 = (size_t)(c0 + c) * C;
+      const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+      const size_t tok0 = rs_.tok0;
       constexpr int NR = C * BV / 8;
 #pragma unroll
       for (int i = 0; i < (NR + NTH - 1) / NTH; ++i) {
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
         bf16x8 o;
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = sm.drT[v0 + j][t];
-        *reinterpret_cast<bf16x8*>(dr_out + (tok0 + t) * row_stride_v + (size_t)h * VD + v_base + v0) = o;
+        *reinterpret_cast<bf16x8*>(rs_.dst(dr_out + (tok0 + t) * row_stride_v + (size_t)h * VD + v_base + v0, t)) = o;
       }
     }
   }
@@ -312,14 +314,18 @@ template <int BV, int GATE, bool AQK>
 static hipError_t launch_state(const void* q, const void* k, const void* w, const float* g,
                                const void* dO, const float* aqk, const void* dv, const float* dht,
                                void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
-                               hipStream_t stream, const int* chunk_off, int segs = 0, int vf = 0, int HQ = 0) {
+                               hipStream_t stream, const int* chunk_off, int segs = 0, int vf = 0, int HQ = 0,
+                               const int* cu = nullptr) {
   const int rows = segs > 0 ? B * segs : B;
   const int grid = rows * H * (VD / BV);
   constexpr int NW = state_waves<BV>();
-  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW>), dim3(grid), dim3(64 * NW), 0, stream,
-                     (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk,
-                     (const bf16*)dv, dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale, chunk_off, segs, vf,
-                     HQ > 0 ? HQ : H);
+#define S_LAUNCH(MAP)                                                                                        \
+  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW, MAP>), dim3(grid), dim3(64 * NW), 0, stream,        \
+                     (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk, (const bf16*)dv, \
+                     dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale, chunk_off, segs, vf, HQ > 0 ? HQ : H, cu)
+  if (cu) S_LAUNCH(true);
+  else S_LAUNCH(false);
+#undef S_LAUNCH
   return hipGetLastError();
 }
 
@@ -327,13 +333,16 @@ template <int GATE, bool AQK>
 static hipError_t pick_bv(int bv, const void* q, const void* k, const void* w, const float* g,
                           const void* dO, const float* aqk, const void* dv, const float* dht,
                           void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
-                          hipStream_t s, const int* co, int vf, int HQ) {
+                          hipStream_t s, const int* co, int vf, int HQ, const int* cu) {
+#define S_BV(BV) \
+  launch_state<BV, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, HQ, cu)
   switch (bv) {
-    case 16: return launch_state<16, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, HQ);
-    case 32: return launch_state<32, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, HQ);
-    case 64: return launch_state<64, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, HQ);
+    case 16: return S_BV(16);
+    case 32: return S_BV(32);
+    case 64: return S_BV(64);
     default: return hipErrorInvalidValue;
   }
+#undef S_BV
 }
 
 // Segmented form, step 1: each segment's map from its end state X to its start state,
@@ -640,11 +649,13 @@ static int default_bv(int B, int H) {
   return 16;
 }
 
-// B rows of T tokens, or (chunk_off) B sequences packed along T
+// B rows of T tokens, (chunk_off) B sequences packed along T tokens on 64-token boundaries,
+// or (chunk_off, cu) B sequences packed anywhere along the token axis, in T / 64 chunks
 static hipError_t state_dispatch(const void* q, const void* k, const void* w, const float* g, int gate_mode,
                                  const void* dO, const float* aqk, const void* dv, const float* dht, void* dh,
                                  void* dr, float* dh0, int B, int T, int H, int K, int V, int chunk, float scale,
-                                 int value_block, hipStream_t stream, const int* co, int vf, int HQ) {
+                                 int value_block, hipStream_t stream, const int* co, int vf, int HQ,
+                                 const int* cu = nullptr) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0)
     return hipErrorInvalidValue;
   if (!q || !k || !w || !dO || !dh || !dr) return hipErrorInvalidValue;
@@ -652,9 +663,10 @@ static hipError_t state_dispatch(const void* q, const void* k, const void* w, co
   if (gate_mode != GATE_NONE && g == nullptr) return hipErrorInvalidValue;
   if (HQ <= 0) HQ = H;
   if (H % HQ) return hipErrorInvalidValue;
+  if (cu && !co) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : default_bv(B, H);
   const bool from_aqk = aqk != nullptr;
-#define S_ARGS bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream, co, vf, HQ
+#define S_ARGS bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream, co, vf, HQ, cu
   switch (gate_mode) {
     case GATE_NONE:
       return from_aqk ? pick_bv<GATE_NONE, true>(S_ARGS) : pick_bv<GATE_NONE, false>(S_ARGS);
@@ -680,11 +692,12 @@ extern "C" hipError_t fdr_state_bwd(const void* q, const void* k, const void* w,
 extern "C" hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, const float* g,
                                            int gate_mode, const void* dO, const float* aqk, const void* dv,
                                            const float* dht, void* dh, void* dr, float* dh0, int state_v_first,
-                                           const int* chunk_offsets, int N, int T, int H, int qk_heads, int K,
-                                           int V, int chunk, float scale, int value_block, hipStream_t stream) {
-  if (!chunk_offsets) return hipErrorInvalidValue;
-  return state_dispatch(q, k, w, g, gate_mode, dO, aqk, dv, dht, dh, dr, dh0, N, T, H, K, V, chunk, scale,
-                        value_block, stream, chunk_offsets, state_v_first ? 1 : 0, qk_heads);
+                                           const int* chunk_offsets, const int* cu_seqlens, int N, int num_chunks,
+                                           int H, int qk_heads, int K, int V, int chunk, float scale,
+                                           int value_block, hipStream_t stream) {
+  if (!chunk_offsets || num_chunks <= 0) return hipErrorInvalidValue;
+  return state_dispatch(q, k, w, g, gate_mode, dO, aqk, dv, dht, dh, dr, dh0, N, num_chunks * C, H, K, V, chunk,
+                        scale, value_block, stream, chunk_offsets, state_v_first ? 1 : 0, qk_heads, cu_seqlens);
 }
 
 extern "C" size_t fdr_state_bwd_segmented_workspace_bytes(int B, int H, int segments) {

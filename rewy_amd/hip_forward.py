@@ -23,10 +23,10 @@ GATE_MODE = {"delta": ops.GATE_NONE, "gdn": ops.GATE_SCALAR, "kda": ops.GATE_VEC
 
 
 def chunk_forward_hip(op, q, k, v, g=None, beta=None, b=None, w=None, initial_state=None, scale=None,
-                      output_final_state=False, chunk_offsets=None, state_v_first=False):
-    """``chunk_offsets``: B = 1 holds sequences packed on chunk boundaries (see
-    ``ops.state_bwd``); initial / final states are per sequence.  Every stage but the
-    state scan is chunk-local, so only ``fwd_h`` takes the offsets.  ``state_v_first``:
+                      output_final_state=False, varlen=None, state_v_first=False):
+    """``varlen`` (an ``ops.Varlen``): B = 1 holds sequences packed along T, starting
+    anywhere (FLA's cu_seqlens); initial / final states are per sequence, and every stage
+    takes the batch's chunk map (a sequence's last chunk may be partial).  ``state_v_first``:
     initial / final states are [N,H,V,K] (read and written so by ``fwd_h``); the saved
     per-chunk h stays [B,NT,H,K,V]."""
     B, T, H, K = q.shape
@@ -40,13 +40,13 @@ def chunk_forward_hip(op, q, k, v, g=None, beta=None, b=None, w=None, initial_st
     b = b.to(bf).contiguous() if vb else None
     w = w.to(bf).contiguous() if vb else None
     h0 = None if initial_state is None else initial_state.to(f32).contiguous()
-    gc, Aqk, Akk = ops.fwd_prepare(q, k, g, gm, beta=beta, b=b, scale=scale)
+    gc, Aqk, Akk = ops.fwd_prepare(q, k, g, gm, beta=beta, b=b, scale=scale, varlen=varlen)
     vec = gm == ops.GATE_VECTOR
-    wu = ops.prepare_wu(k, v, Akk, gm, g=gc, beta=beta, b=b, w=w, q=q, want_qkg=vec, scale=scale)
+    wu = ops.prepare_wu(k, v, Akk, gm, g=gc, beta=beta, b=b, w=w, q=q, want_qkg=vec, scale=scale, varlen=varlen)
     h, v_new, final = ops.fwd_h(wu["kg"] if vec else k, wu["w"], wu["u"], gc, gm, h0=h0,
-                                want_final=output_final_state, chunk_offsets=chunk_offsets,
-                                method="auto" if chunk_offsets is None else "direct", state_v_first=state_v_first)
-    o = ops.fwd_o(q, gc, gm, Aqk, h, v_new, scale)
+                                want_final=output_final_state, varlen=varlen,
+                                method="auto" if varlen is None else "direct", state_v_first=state_v_first)
+    o = ops.fwd_o(q, gc, gm, Aqk, h, v_new, scale, varlen=varlen)
     saved = dict(gc=gc, Aqk=Aqk, Akk=Akk, w=wu["w"], u=wu["u"], qg=wu["qg"], kg=wu["kg"], v_new=v_new, h=h,
                  scale=scale)
     return o, final, saved

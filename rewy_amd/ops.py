@@ -105,6 +105,60 @@ def _chunk_offsets(chunk_offsets, B, T, dev):
     return co.to(device=dev, dtype=torch.int32).contiguous(), host.numel() - 1
 
 
+class Varlen:
+    """A packed variable-length batch (B = 1): FLA's ``cu_seqlens`` [N+1] and what the kernels
+    take with it, on the device -- ``chunk_indices`` [NC, 2] (sequence, chunk of the sequence;
+    FLA prepare_chunk_indices) and ``chunk_offsets`` [N+1] (FLA prepare_chunk_offsets), each
+    sequence cut into ceil(len / 64) chunks.  Sequences start anywhere; when every one starts
+    on a 64-token boundary and T is a multiple of 64 (``aligned``) the dense kernels serve the
+    chunk-local stages and only the scans take the offsets."""
+
+    def __init__(self, cu_seqlens, device):
+        host = torch.as_tensor(cu_seqlens).detach().to("cpu", torch.int64)
+        if host.ndim != 1 or host.numel() < 2 or int(host[0]) != 0:
+            raise ValueError("cu_seqlens must be [N+1], starting at 0")
+        lens = host[1:] - host[:-1]
+        if bool((lens < 0).any()):
+            raise ValueError("cu_seqlens must not decrease")
+        nch = (lens + CHUNK - 1) // CHUNK
+        self.N = int(lens.numel())
+        self.T = int(host[-1])
+        self.NC = int(nch.sum())
+        if self.NC == 0:
+            raise ValueError("a variable-length batch needs at least one token")
+        self.aligned = bool((host % CHUNK == 0).all())
+        seq = torch.repeat_interleave(torch.arange(self.N), nch)
+        first = torch.cumsum(nch, 0) - nch
+        ci = torch.stack([seq, torch.arange(self.NC) - first[seq]], 1)
+        i32 = dict(device=device, dtype=torch.int32)
+        self.cu_seqlens = host.to(**i32)
+        self.chunk_indices = ci.to(**i32).contiguous()
+        self.chunk_offsets = torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(nch, 0)]).to(**i32)
+
+    def check(self, x):
+        if x.shape[0] != 1 or x.shape[1] != self.T:
+            raise ValueError(f"a variable-length batch is [1, {self.T}, ...], got {tuple(x.shape)}")
+
+
+def _rows(x, varlen):
+    """(B, T, H, K) of a token-major operand; T any length for a packed variable-length batch."""
+    if varlen is None:
+        return _dims(x)
+    if x.ndim != 4:
+        raise ValueError("q must be [B,T,H,K]")
+    varlen.check(x)
+    if x.shape[3] != K_SUPPORTED:
+        raise ValueError(f"K must be {K_SUPPORTED}")
+    if x.device.type != "cuda":
+        raise ValueError("HIP backward requires a GPU tensor")
+    return x.shape
+
+
+def _mapped(varlen):
+    """The variable-length batch when the chunk-local kernels need its row map, else None."""
+    return None if varlen is None or varlen.aligned else varlen
+
+
 def _group(H, HQ):
     """Value heads H and q / k heads HQ (grouped value heads: H a multiple of HQ)."""
     if HQ <= 0 or H % HQ:
@@ -126,12 +180,13 @@ def _dims(q):
 
 
 def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, want_dh0=True,
-              value_block=0, method="auto", chunk_offsets=None, segments=0, state_v_first=False):
+              value_block=0, method="auto", chunk_offsets=None, segments=0, state_v_first=False, varlen=None):
     """Reverse state recurrence.  Returns (dh [B,NT,H,K,V] bf16, dR [B,T,H,V] bf16, dh0 fp32|None).
 
     ``chunk_offsets`` (int [N+1]): B = 1 holds N sequences packed along T, sequence n on
     chunks [chunk_offsets[n], chunk_offsets[n+1]); dht / dh0 are then [N,H,K,V] and the
-    direct kernel runs (fdr_state_bwd_varlen).  ``state_v_first``: dht and dh0 are [.., V, K]
+    direct kernel runs (fdr_state_bwd_varlen).  ``varlen`` (a ``Varlen``): the same for
+    sequences starting anywhere (dh then has ``varlen.NC`` chunks).  ``state_v_first``: dht and dh0 are [.., V, K]
     (FLA's layout); the per-chunk dh is [B,NT,H,K,V] either way.
 
     method "direct": one kernel (fdr_state_bwd); "affine": chunk-parallel step
@@ -140,7 +195,7 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
     split into ``segments`` (0: ``segments_for``) whose affine maps are formed in parallel,
     chained, and each segment rerun from its end state (fdr_state_bwd_segmented), for long
     rows and few heads; "auto" picks."""
-    B, T, HQ, K = _dims(q)
+    B, T, HQ, K = _rows(q, varlen)
     H, HQ = _group(w.shape[2] if w is not None and w.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = q.device
@@ -161,12 +216,17 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
         _need(aqk, "Aqk", f32, (B, T, H, CHUNK), dev)
     if dv is not None:
         _need(dv, "dv", bf, (B, T, H, V), dev)
-    co, N = _chunk_offsets(chunk_offsets, B, T, dev)
+    if varlen is not None:
+        if chunk_offsets is not None:
+            raise ValueError("pass chunk_offsets or varlen, not both")
+        co, N, NT = varlen.chunk_offsets, varlen.N, varlen.NC
+    else:
+        co, N = _chunk_offsets(chunk_offsets, B, T, dev)
+        NT = T // CHUNK
     if dht is not None:
         _need(dht, "dht", f32, (N, H, K, V), dev)
     if value_block not in (0, 16, 32, 64):
         raise ValueError("value_block must be 0, 16, 32 or 64")
-    NT = T // CHUNK
     vf = int(bool(state_v_first))
     dh = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
     dr = torch.empty(B, T, H, V, device=dev, dtype=bf)
@@ -175,9 +235,11 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
     if co is not None:
         if method == "affine":
             raise ValueError("the affine-step form takes equal-length rows, not chunk_offsets")
+        cu = _mapped(varlen)
         st = _lib.load().fdr_state_bwd_varlen(P(q), P(k), P(w), P(g), int(gate_mode), P(dO), P(aqk), P(dv),
-                                              P(dht), P(dh), P(dr), P(dh0), vf, P(co), N, T, H, HQ, K, V, CHUNK,
-                                              float(scale), int(value_block), _lib.stream_handle(dev))
+                                              P(dht), P(dh), P(dr), P(dh0), vf, P(co),
+                                              None if cu is None else P(cu.cu_seqlens), N, NT, H, HQ, K, V,
+                                              CHUNK, float(scale), int(value_block), _lib.stream_handle(dev))
         _lib.check(st, "fdr_state_bwd_varlen")
         return dh, dr, dh0
     form = _state_method(method, B, H, NT)
@@ -282,7 +344,7 @@ def recurrences(q, k, w, u, g, gate_mode, dO, scale, aqk=None, dv=None, h0=None,
 
 
 def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None, b=None, w=None,
-              gate_fold=None, beta_sigmoid=0.0, h_v_first=False):
+              gate_fold=None, beta_sigmoid=0.0, h_v_first=False, varlen=None):
     """Fused residual-WY + matrix-intra + epilogue stage.
 
     ``gate_fold`` (KDA only) = dict(g_raw, A_log, dt_bias, lower_bound): the in-kernel gate's
@@ -292,15 +354,17 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
     ``beta_sigmoid`` = s > 0 (scalar beta): beta was activated as s * sigmoid(x) in the
     forward, and ``dbeta`` is returned as dL/dx (the reference's fused beta-sigmoid backward).
     ``h_v_first`` (vector gates): the saved per-chunk states ``h`` are [B,NT,H,V,K].
+    ``varlen`` (a ``Varlen``): a packed variable-length batch; h, dh have ``varlen.NC`` chunks.
 
     Returns dict(dq, dk, dv [bf16], dg [fp32, gate shape] | None, dbeta [fp32] | None,
     db, dw [bf16] | None)."""
-    B, T, HQ, K = _dims(q)
+    B, T, HQ, K = _rows(q, varlen)
     H, HQ = _group(v.shape[2] if v is not None and v.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = q.device
     bf, f32 = torch.bfloat16, torch.float32
-    NT = T // CHUNK
+    NT = T // CHUNK if varlen is None else varlen.NC
+    mv = _mapped(varlen)
     for x, n in ((q, "q"), (k, "k")):
         _need(x, n, bf, (B, T, HQ, K), dev)
     for x, n in ((v, "v"), (v_new, "v_new"), (dO, "dO"), (dR, "dR")):
@@ -329,6 +393,8 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
     if hvf and gate_mode != GATE_VECTOR:
         raise ValueError("[V,K] saved states come with the vector-gate families")
     if gate_fold is not None:
+        if mv is not None:
+            raise ValueError("the folded gate backward takes chunk-aligned rows")
         return _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, gate_fold,
                                     beta_sigmoid, hvf, H)
     out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=bf),
@@ -339,11 +405,15 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
                db=torch.empty(B, T, H, K, device=dev, dtype=bf) if vec_b else None,
                dw=torch.empty(B, T, H, V, device=dev, dtype=bf) if vec_b else None)
     P = _lib.ptr
-    st = _lib.load().fdr_chunk_bwd(P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), int(gate_mode),
-                                   P(beta), P(b), P(w), P(Akk), P(h), P(dh), P(out["dq"]),
-                                   P(out["dk"]), P(out["dv"]), P(out["dg"]), P(out["dbeta"]), beta_sigmoid,
-                                   P(out["db"]), P(out["dw"]), hvf, B, T, H, HQ, K, V, CHUNK, float(scale),
-                                   _lib.stream_handle(dev))
+    common = (P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), int(gate_mode), P(beta), P(b), P(w), P(Akk), P(h),
+              P(dh), P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dg"]), P(out["dbeta"]), beta_sigmoid,
+              P(out["db"]), P(out["dw"]), hvf)
+    if mv is not None:
+        st = _lib.load().fdr_chunk_bwd_varlen(*common, P(mv.cu_seqlens), P(mv.chunk_indices), mv.NC, H, HQ, K, V,
+                                              CHUNK, float(scale), _lib.stream_handle(dev))
+        _lib.check(st, "fdr_chunk_bwd_varlen")
+        return out
+    st = _lib.load().fdr_chunk_bwd(*common, B, T, H, HQ, K, V, CHUNK, float(scale), _lib.stream_handle(dev))
     _lib.check(st, "fdr_chunk_bwd")
     return out
 
@@ -416,9 +486,10 @@ def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale
 
 
 def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, want_qkg=False,
-               want_aqk=False, scale=1.0):
-    """WY factors (and qg/kg or Aqk) of every chunk.  Returns dict(w, u, qg, kg, Aqk)."""
-    B, T, HQ, K = _dims(k)
+               want_aqk=False, scale=1.0, varlen=None):
+    """WY factors (and qg/kg or Aqk) of every chunk.  Returns dict(w, u, qg, kg, Aqk).
+    ``varlen``: a packed variable-length batch (``Varlen``)."""
+    B, T, HQ, K = _rows(k, varlen)
     H, HQ = _group(v.shape[2] if v is not None and v.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = k.device
@@ -449,18 +520,24 @@ def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, 
                kg=torch.empty(B, T, H, K, device=dev, dtype=bf) if want_qkg else None,
                Aqk=torch.empty(B, T, H, CHUNK, device=dev, dtype=f32) if want_aqk else None)
     P = _lib.ptr
-    st = _lib.load().fdr_prepare_wu(P(q), P(k), P(v), P(g), int(gate_mode), P(beta), P(b), P(w), P(Akk),
-                                    P(out["w"]), P(out["u"]), P(out["qg"]), P(out["kg"]), P(out["Aqk"]),
-                                    B, T, H, HQ, K, V, CHUNK, float(scale), _lib.stream_handle(dev))
+    common = (P(q), P(k), P(v), P(g), int(gate_mode), P(beta), P(b), P(w), P(Akk), P(out["w"]), P(out["u"]),
+              P(out["qg"]), P(out["kg"]), P(out["Aqk"]))
+    mv = _mapped(varlen)
+    if mv is not None:
+        st = _lib.load().fdr_prepare_wu_varlen(*common, P(mv.cu_seqlens), P(mv.chunk_indices), mv.NC, H, HQ, K, V,
+                                               CHUNK, float(scale), _lib.stream_handle(dev))
+        _lib.check(st, "fdr_prepare_wu_varlen")
+        return out
+    st = _lib.load().fdr_prepare_wu(*common, B, T, H, HQ, K, V, CHUNK, float(scale), _lib.stream_handle(dev))
     _lib.check(st, "fdr_prepare_wu")
     return out
 
 
 def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, method="auto",
-          chunk_offsets=None, state_v_first=False):
+          chunk_offsets=None, state_v_first=False, varlen=None):
     """Forward state scan.  Returns (h [B,NT,H,K,V] bf16, v_new [B,T,H,V] bf16, final fp32|None).
-    ``method`` and ``chunk_offsets`` as for ``state_bwd`` (h0 / final per sequence)."""
-    B, T, HQ, K = _dims(k)
+    ``method``, ``chunk_offsets`` and ``varlen`` as for ``state_bwd`` (h0 / final per sequence)."""
+    B, T, HQ, K = _rows(k, varlen)
     H, HQ = _group(w.shape[2] if w is not None and w.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = k.device
@@ -474,12 +551,17 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
         _need(g, "g", f32, (B, T, H), dev)
     elif gate_mode != GATE_NONE:
         raise ValueError("gate_mode must be 0, 1 or 2")
-    co, N = _chunk_offsets(chunk_offsets, B, T, dev)
+    if varlen is not None:
+        if chunk_offsets is not None:
+            raise ValueError("pass chunk_offsets or varlen, not both")
+        co, N, NT = varlen.chunk_offsets, varlen.N, varlen.NC
+    else:
+        co, N = _chunk_offsets(chunk_offsets, B, T, dev)
+        NT = T // CHUNK
     if h0 is not None:
         _need(h0, "h0", f32, (N, H, K, V), dev)
     if value_block not in (0, 16, 32, 64):
         raise ValueError("value_block must be 0, 16, 32 or 64")
-    NT = T // CHUNK
     vf = int(bool(state_v_first))
     h = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
     vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
@@ -488,9 +570,10 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
     if co is not None:
         if method == "affine":
             raise ValueError("the affine-step form takes equal-length rows, not chunk_offsets")
+        cu = _mapped(varlen)
         st = _lib.load().fdr_fwd_h_varlen(P(k), P(w), P(u), P(g), int(gate_mode), P(h0), P(h), P(vnew), P(ht),
-                                          vf, P(co), N, T, H, HQ, K, V, CHUNK, int(value_block),
-                                          _lib.stream_handle(dev))
+                                          vf, P(co), None if cu is None else P(cu.cu_seqlens), N, NT, H, HQ, K, V,
+                                          CHUNK, int(value_block), _lib.stream_handle(dev))
         _lib.check(st, "fdr_fwd_h_varlen")
         return h, vnew, ht
     if _use_affine(method, B, H, NT) and HQ == H:
@@ -541,9 +624,10 @@ def matrix_intra(q, k, g, dAqk, dAkk, dq, dk, db, dg, beta=None, b=None, beta_co
     return dq, dk, db, dg
 
 
-def fwd_prepare(q, k, g, gate_mode, beta=None, b=None, scale=1.0):
-    """Forward intra matrices.  Returns (gc fp32 | None, Aqk fp32, Akk fp32)."""
-    B, T, HQ, K = _dims(q)
+def fwd_prepare(q, k, g, gate_mode, beta=None, b=None, scale=1.0, varlen=None):
+    """Forward intra matrices.  Returns (gc fp32 | None, Aqk fp32, Akk fp32).
+    ``varlen``: a packed variable-length batch (``Varlen``)."""
+    B, T, HQ, K = _rows(q, varlen)
     side = beta if beta is not None else b
     H, HQ = _group(side.shape[2] if side is not None and side.ndim >= 3 else HQ, HQ)
     dev = q.device
@@ -566,15 +650,22 @@ def fwd_prepare(q, k, g, gate_mode, beta=None, b=None, scale=1.0):
     Aqk = torch.empty(B, T, H, CHUNK, device=dev, dtype=f32)
     Akk = torch.empty(B, T, H, CHUNK, device=dev, dtype=f32)
     P = _lib.ptr
-    st = _lib.load().fdr_fwd_prepare(P(q), P(k), P(g), int(gate_mode), P(beta), P(b), P(gc), P(Aqk), P(Akk),
-                                     B, T, H, HQ, K, CHUNK, float(scale), _lib.stream_handle(dev))
+    common = (P(q), P(k), P(g), int(gate_mode), P(beta), P(b), P(gc), P(Aqk), P(Akk))
+    mv = _mapped(varlen)
+    if mv is not None:
+        st = _lib.load().fdr_fwd_prepare_varlen(*common, P(mv.cu_seqlens), P(mv.chunk_indices), mv.NC, H, HQ, K,
+                                                CHUNK, float(scale), _lib.stream_handle(dev))
+        _lib.check(st, "fdr_fwd_prepare_varlen")
+        return gc, Aqk, Akk
+    st = _lib.load().fdr_fwd_prepare(*common, B, T, H, HQ, K, CHUNK, float(scale), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_prepare")
     return gc, Aqk, Akk
 
 
-def fwd_o(q, gc, gate_mode, Aqk, h, v_new, scale):
-    """Forward output o = scale (q 2^gc) h + Aqk v_new (bf16)."""
-    B, T, HQ, K = _dims(q)
+def fwd_o(q, gc, gate_mode, Aqk, h, v_new, scale, varlen=None):
+    """Forward output o = scale (q 2^gc) h + Aqk v_new (bf16).  ``varlen``: a packed
+    variable-length batch (``Varlen``; h has ``varlen.NC`` chunks)."""
+    B, T, HQ, K = _rows(q, varlen)
     H, HQ = _group(Aqk.shape[2] if Aqk is not None and Aqk.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = q.device
@@ -587,11 +678,17 @@ def fwd_o(q, gc, gate_mode, Aqk, h, v_new, scale):
     elif gate_mode != GATE_NONE:
         raise ValueError("gate_mode must be 0, 1 or 2")
     _need(Aqk, "Aqk", f32, (B, T, H, CHUNK), dev)
-    _need(h, "h", bf, (B, T // CHUNK, H, K, V), dev)
+    _need(h, "h", bf, (B, T // CHUNK if varlen is None else varlen.NC, H, K, V), dev)
     _need(v_new, "v_new", bf, (B, T, H, V), dev)
     o = torch.empty(B, T, H, V, device=dev, dtype=bf)
     P = _lib.ptr
-    st = _lib.load().fdr_fwd_o(P(q), P(gc), int(gate_mode), P(Aqk), P(h), P(v_new), P(o), B, T, H, HQ, K, V, CHUNK,
-                               float(scale), _lib.stream_handle(dev))
+    common = (P(q), P(gc), int(gate_mode), P(Aqk), P(h), P(v_new), P(o))
+    mv = _mapped(varlen)
+    if mv is not None:
+        st = _lib.load().fdr_fwd_o_varlen(*common, P(mv.cu_seqlens), P(mv.chunk_indices), mv.NC, H, HQ, K, V, CHUNK,
+                                          float(scale), _lib.stream_handle(dev))
+        _lib.check(st, "fdr_fwd_o_varlen")
+        return o
+    st = _lib.load().fdr_fwd_o(*common, B, T, H, HQ, K, V, CHUNK, float(scale), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_o")
     return o

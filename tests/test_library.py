@@ -79,17 +79,24 @@ def test_host_wrappers_validate_before_launch():
 
 
 def test_backward_varlen_seam_validation():
-    """cu_seqlens at the backward seam: chunk-aligned, non-empty sequences map to chunk
-    offsets; anything else is refused before any kernel runs."""
+    """cu_seqlens at the backward seam: the packed batch's chunk map (FLA's
+    prepare_chunk_indices / prepare_chunk_offsets: each sequence cut into ceil(len / 64)
+    chunks, an empty one owning none), sequences starting anywhere; malformed offsets are
+    refused before any kernel runs."""
     import pytest
     import torch
     from rewy_amd.backends.backward import _varlen
     q = torch.zeros(1, 256, 1, 128)
     assert _varlen(q, {}) is None
-    assert _varlen(q, dict(cu_seqlens=torch.tensor([0, 64, 256]))).tolist() == [0, 1, 4]
-    with pytest.raises(NotImplementedError, match="chunk"):
-        _varlen(q, dict(cu_seqlens=torch.tensor([0, 100, 256])))
-    assert _varlen(q, dict(cu_seqlens=torch.tensor([0, 64, 64, 256]))).tolist() == [0, 1, 1, 4]
+    vl = _varlen(q, dict(cu_seqlens=torch.tensor([0, 64, 256])))
+    assert vl.aligned and vl.chunk_offsets.tolist() == [0, 1, 4] and vl.NC == 4
+    vl = _varlen(q, dict(cu_seqlens=torch.tensor([0, 100, 256])))
+    assert not vl.aligned and (vl.N, vl.NC, vl.T) == (2, 5, 256)
+    assert vl.chunk_offsets.tolist() == [0, 2, 5]
+    assert vl.chunk_indices.tolist() == [[0, 0], [0, 1], [1, 0], [1, 1], [1, 2]]
+    vl = _varlen(q, dict(cu_seqlens=torch.tensor([0, 64, 64, 65, 256])))
+    assert vl.chunk_offsets.tolist() == [0, 1, 1, 2, 5]
+    assert vl.chunk_indices.tolist() == [[0, 0], [2, 0], [3, 0], [3, 1], [3, 2]]
     with pytest.raises(ValueError, match="decrease"):
         _varlen(q, dict(cu_seqlens=torch.tensor([0, 128, 64, 256])))
     with pytest.raises(ValueError, match="rise"):
