@@ -71,8 +71,46 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
   const size_t vofs = tok0 * rsv + (size_t)h * VD;
   const QKRows qr = qk_rows(tok0, h, H, HQ);   // raw q / k rows (grouped value heads: HQ < H)
 
-  // Aqk's q fragments (wave wv: row tile wv), fetched first so their latency hides
-  // behind the staging and the w/u products
+  // Loads first, all in flight together: every row piece of E, Z and A with its rows' gate
+  // and beta (below), the row gate and beta that later phases read from LDS, then Aqk's q
+  // fragments (wave wv: row tile wv, used last).
+  const int trow = tid & (C - 1);
+  const float gv = (GATE == RG_SCALAR) ? g[(tok0 + rw.clamp(trow)) * H + h] : 0.f;
+  const float bv = VEC_B ? 0.f : *rw.src(beta + (tok0 + trow) * H + h, trow);
+  // ---- stage E = b k 2^g, Z = w_gate v (bf16) and A (hi/lo) row-major, coalesced 16-byte rows ----
+  // Every row piece this thread stages is fetched first (1024 pieces of 8 columns: row p >> 4,
+  // p = tid + 256 i), so the loads are in flight together instead of one round trip per piece.
+  // The qg / kg pieces (vector gates) are the same rows and columns: k and g serve both.
+  u32x4 rkx[4], rvx[4], rbx[4], rwx[4], rqx[4];
+  f32x4 ra4[4], rg0[4], rg1[4];
+  f32x4 rgl0, rgl1;
+  float rgs[4], rbs[4];      // scalar gate and beta of each piece's row
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = tid + 256 * i;
+    const int t = p >> 4, c0 = 8 * (p & 15);
+    rgs[i] = (GATE == RG_SCALAR) ? g[(tok0 + rw.clamp(t)) * H + h] : 0.f;
+    rbs[i] = VEC_B ? 0.f : *rw.src(beta + (tok0 + t) * H + h, t);
+    rkx[i] = *reinterpret_cast<const u32x4*>(rw.src(k + qr.ofs + (size_t)t * qr.rs + c0, t));
+    rvx[i] = *reinterpret_cast<const u32x4*>(rw.src(v + vofs + (size_t)t * rsv + c0, t));
+    ra4[i] = *reinterpret_cast<const f32x4*>(rw.src(akk + ((tok0 + t) * H + h) * C + 4 * (p & 15), t));
+    if constexpr (GATE == RG_VECTOR) {
+      rg0[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rw.clamp(t) * rsk + c0);
+      rg1[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rw.clamp(t) * rsk + c0 + 4);
+    }
+    if constexpr (VEC_B) {
+      rbx[i] = *reinterpret_cast<const u32x4*>(rw.src(bgate + kofs + (size_t)t * rsk + c0, t));
+      rwx[i] = *reinterpret_cast<const u32x4*>(rw.src(wgate + vofs + (size_t)t * rsv + c0, t));
+    }
+    if constexpr (WANT_QKG && GATE == RG_VECTOR)
+      rqx[i] = *reinterpret_cast<const u32x4*>(rw.src(q + qr.ofs + (size_t)t * qr.rs + c0, t));
+  }
+  if constexpr (WANT_QKG && GATE == RG_VECTOR) {
+    // g_last of this thread's 8 columns (the same for its four pieces)
+    const float* gl = g + kofs + (size_t)rw.clamp(C - 1) * rsk + 8 * (tid & 15);
+    rgl0 = *reinterpret_cast<const f32x4*>(gl);
+    rgl1 = *reinterpret_cast<const f32x4*>(gl + 4);
+  }
   bf16x8 qa[4];
   if constexpr (WANT_AQK) {
 #pragma unroll
@@ -80,43 +118,28 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
       qa[ks] = *reinterpret_cast<const bf16x8*>(
           rw.src(q + qr.ofs + (size_t)(16 * wv + lc) * qr.rs + 32 * ks + 8 * lg, 16 * wv + lc));
   }
-  if (tid < C) {
-    const size_t row = (tok0 + tid) * H + h;
-    const float gv = (GATE == RG_SCALAR) ? g[(tok0 + rw.clamp(tid)) * H + h] : 0.f;
-    sG[tid] = gv;
-    sB[tid] = VEC_B ? 0.f : *rw.src(beta + row, tid);
-    sGe[tid] = (GATE == RG_SCALAR) ? fast_exp2(gv) : 1.f;
-  }
-  lds_barrier();
 
-  // ---- stage E = b k 2^g, Z = w_gate v (bf16) and A (hi/lo) row-major, coalesced 16-byte rows ----
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int p = tid + 256 * i;            // 1024 pieces of 8 columns: row p >> 4
+    const int p = tid + 256 * i;
     const int t = p >> 4, ch = p & 15, c0 = 8 * ch;
-    const bf16x8 kx =
-        __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(rw.src(k + qr.ofs + (size_t)t * qr.rs + c0, t)));
-    const bf16x8 vx =
-        __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(rw.src(v + vofs + (size_t)t * rsv + c0, t)));
+    const bf16x8 kx = __builtin_bit_cast(bf16x8, rkx[i]);
+    const bf16x8 vx = __builtin_bit_cast(bf16x8, rvx[i]);
     float ge[8], be[8], we[8];
     if constexpr (GATE == RG_VECTOR) {
-      const f32x4 g0 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rw.clamp(t) * rsk + c0);
-      const f32x4 g1 = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rw.clamp(t) * rsk + c0 + 4);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        ge[j] = fast_exp2(g0[j]);
-        ge[j + 4] = fast_exp2(g1[j]);
+        ge[j] = fast_exp2(rg0[i][j]);
+        ge[j + 4] = fast_exp2(rg1[i][j]);
       }
     } else {
-      const float s0 = (GATE == RG_SCALAR) ? fast_exp2(sG[t]) : 1.f;
+      const float s0 = (GATE == RG_SCALAR) ? fast_exp2(rgs[i]) : 1.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) ge[j] = s0;
     }
     if constexpr (VEC_B) {
-      const bf16x8 bx =
-          __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(rw.src(bgate + kofs + (size_t)t * rsk + c0, t)));
-      const bf16x8 wx =
-          __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(rw.src(wgate + vofs + (size_t)t * rsv + c0, t)));
+      const bf16x8 bx = __builtin_bit_cast(bf16x8, rbx[i]);
+      const bf16x8 wx = __builtin_bit_cast(bf16x8, rwx[i]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         be[j] = to_f32(bx[j]);
@@ -124,7 +147,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) be[j] = we[j] = sB[t];
+      for (int j = 0; j < 8; ++j) be[j] = we[j] = rbs[i];
     }
     bf16x8 eh, zh;
 #pragma unroll
@@ -135,35 +158,29 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     store_tr_chunk<16>(eH, t, ch, __builtin_bit_cast(u32x4, eh));
     store_tr_chunk<16>(zH, t, ch, __builtin_bit_cast(u32x4, zh));
     // A rows: 64 x 64 fp32 = 1024 pieces of 4, one per (i, thread) here
-    const f32x4 a4 = *reinterpret_cast<const f32x4*>(rw.src(akk + ((tok0 + t) * H + h) * C + 4 * ch, t));
     bf16x4 alo;
-    const bf16x4 ahi = split_hi4(a4, alo);
+    const bf16x4 ahi = split_hi4(ra4[i], alo);
     *reinterpret_cast<bf16x4*>(&sAh[t][4 * ch]) = ahi;
     *reinterpret_cast<bf16x4*>(&sAl[t][4 * ch]) = alo;
-  }
-
-  // ---- qg / kg (vector gates): elementwise, coalesced ----
-  if constexpr (WANT_QKG && GATE == RG_VECTOR) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = tid + 256 * i;          // 1024 pieces of 8
-      const int t = p >> 4, c0 = (p & 15) * 8;
-      const u32x4 qq = *reinterpret_cast<const u32x4*>(rw.src(q + qr.ofs + (size_t)t * qr.rs + c0, t));
-      const u32x4 kq = *reinterpret_cast<const u32x4*>(rw.src(k + qr.ofs + (size_t)t * qr.rs + c0, t));
-      const float* gr = g + kofs + (size_t)rw.clamp(t) * rsk + c0;
-      const float* gl = g + kofs + (size_t)rw.clamp(C - 1) * rsk + c0;
-      const bf16* pq = reinterpret_cast<const bf16*>(&qq);
-      const bf16* pk = reinterpret_cast<const bf16*>(&kq);
+    // qg = q 2^g, kg = k 2^(g_last - g) (vector gates): elementwise, coalesced
+    if constexpr (WANT_QKG && GATE == RG_VECTOR) {
+      const bf16x8 qx = __builtin_bit_cast(bf16x8, rqx[i]);
       bf16x8 oq, ok;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float gj = gr[j];
-        oq[j] = to_bf16(to_f32(pq[j]) * fast_exp2(gj));
-        ok[j] = to_bf16(to_f32(pk[j]) * fast_exp2(gl[j] - gj));
+        const float gj = j < 4 ? rg0[i][j] : rg1[i][j - 4];
+        const float glj = j < 4 ? rgl0[j] : rgl1[j - 4];
+        oq[j] = to_bf16(to_f32(qx[j]) * fast_exp2(gj));
+        ok[j] = to_bf16(to_f32(kx[j]) * fast_exp2(glj - gj));
       }
       *reinterpret_cast<bf16x8*>(rw.dst(qg_out + kofs + (size_t)t * rsk + c0, t)) = oq;
       *reinterpret_cast<bf16x8*>(rw.dst(kg_out + kofs + (size_t)t * rsk + c0, t)) = ok;
     }
+  }
+  if (tid < C) {
+    sG[tid] = gv;
+    sB[tid] = bv;
+    sGe[tid] = (GATE == RG_SCALAR) ? fast_exp2(gv) : 1.f;
   }
   lds_barrier();
 
