@@ -523,6 +523,39 @@ def varlen(steps, warmup):
                       "padded_tokens": N * Tm, **res, "data": "synthetic"}), flush=True)
 
 
+def stream_probe(reps=5):
+    """The HBM rates plain streaming reaches here (fdr_stream_probe: 16-byte lanes, coalesced,
+    the access shape of the path's kernels), the practical ceiling of every kernel's roofline
+    fraction: 4 GiB read, 4 GiB written, 2 GiB copied (4 GiB moved); for each, the best over
+    grids of 1024-16384 work-groups and ``reps`` launches after warm-up."""
+    import torch
+    from rewy_amd import _lib
+    nbytes = 4 << 30
+    a = torch.ones(nbytes // 2, device="cuda", dtype=torch.bfloat16)
+    b = torch.empty_like(a)
+    sink = torch.empty(16384 * 4, device="cuda", dtype=torch.int32)
+    lib, P, s = _lib.load(), _lib.ptr, _lib.stream_handle(a.device)
+    legs = {"read": lambda gr: lib.fdr_stream_probe(0, P(a), P(sink), nbytes, gr, s),
+            "write": lambda gr: lib.fdr_stream_probe(1, None, P(b), nbytes, gr, s),
+            "copy": lambda gr: lib.fdr_stream_probe(2, P(a), P(b), nbytes // 2, gr, s)}
+    out = {}
+    for name, fn in legs.items():
+        best = float("inf")
+        for grid in (1024, 2048, 4096, 16384):
+            for _ in range(2):
+                _lib.check(fn(grid), "fdr_stream_probe")
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                fn(grid)
+                e1.record()
+                torch.cuda.synchronize()
+                best = min(best, e0.elapsed_time(e1))
+        out[name + "_TBps"] = round(nbytes / best / 1e9, 2)
+    print(json.dumps({"stream_probe": "fdr_stream_probe, 4 GiB moved per leg, best over grids and %d launches" % reps,
+                      **out, "peak_TBps": HBM_PEAK_GBS / 1000}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -536,6 +569,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true", help="skip the GDN companion measurement")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (reference kernel for the HBM byte counters)")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="only measure what plain streaming reaches on this GPU: 4 GiB read, write and copy")
     ap.add_argument("--varlen", action="store_true",
                     help="time a ragged cu_seqlens batch packed natively vs padded to the longest instead")
     ap.add_argument("--paper-grid", action="store_true",
@@ -555,6 +590,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes_read": 4 * n, "calibrate_copy_bytes_written": 4 * n}))
+        return
+    if args.stream_probe:
+        stream_probe()
         return
     from rewy_amd.runtime import check_baseline
     check_baseline()

@@ -430,6 +430,14 @@ hipError_t fdr_affine_scan(const fdr_scan_problem* problems, int n_problems, int
 hipError_t fdr_affine_side(const fdr_side_problem* problems, int n_problems, int B, int T, int H, int K,
                            int V, int chunk, hipStream_t stream);
 
+/*
+ * Diagnostics, no counterpart in the reference: plain HBM streaming with 16-byte lanes,
+ * the ceiling the path's roofline fractions are read against.  mode 0 reads `bytes` of src
+ * (dst receives grid x 16 bytes), 1 writes `bytes` of dst, 2 copies `bytes` src -> dst; `grid`
+ * work-groups of 256 threads stride over the buffer.
+ */
+hipError_t fdr_stream_probe(int mode, const void* src, void* dst, long long bytes, int grid, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
