@@ -307,6 +307,25 @@ def measured_traffic(kernel, config):
         return None
 
 
+def streaming_floor(kernel, config, kernel_ms):
+    """The kernel against what plain streaming reaches on this GPU: its measured reads and
+    writes (profiles/hbm_traffic.json counters) at the committed stream-probe rates
+    (bench.py --stream-probe), as a floor time and the fraction of that floor's rate the
+    kernel runs at; None when that workload was not profiled."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        cal, rates, k = data["_calibration"], data["_streaming"], data[config][kernel]
+        reads = k["FETCH_SIZE_KiB"] * 1024 * cal["fetch_factor"]
+        writes = k["WRITE_SIZE_KiB"] * 1024 * cal["write_factor"]
+    except (OSError, KeyError, ValueError):
+        return None
+    floor_ms = (reads / (rates["read_TBps"] * 1e12) + writes / (rates["write_TBps"] * 1e12)) * 1e3
+    return {"floor_ms": round(floor_ms, 4), "frac": round(floor_ms / kernel_ms, 3),
+            "read_TBps": rates["read_TBps"], "write_TBps": rates["write_TBps"], "probe": rates["command"]}
+
+
 def cpu_baseline(xs, sv, dO, scale, NTt, round_s=0.5, rounds=15):
     """The reference's CPU comparison point as SURVEY'd for the large configs: the original
     (7-product) chunk backward as torch ops -- dAv, the reverse state recurrence, the
@@ -707,7 +726,8 @@ def main():
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(dom, args.config),
-                     "algorithmic_bytes_per_launch": kernels[dom]["bytes_per_launch"]},
+                     "algorithmic_bytes_per_launch": kernels[dom]["bytes_per_launch"],
+                     "practical": streaming_floor(dom, args.config, kernels[dom]["ms"])},
         "forward_hip_ms": round(res_fwd_ms, 4),
         # one backward captured in a HIP graph and replayed (kernel-only, as the reference's
         # low-level timing); the replay's gradients are checked against an eager call
