@@ -116,23 +116,26 @@ def test_rejection_and_visible_fallback():
     assert fdr.stats().get("kda.optimized_backward", 0) == 0
 
 
-@pytest.mark.parametrize("lower_bound", [None, -5.0])
+@pytest.mark.parametrize("lower_bound,with_a_log", [(None, True), (-5.0, True), (-5.0, False)])
 # T = 128: the activation and its backward run inside the chunk Function (folded into the
-# chunk kernel); T = 192 with a ragged cu_seqlens pads sequence tails, so the gate stays an
-# autograd node of its own
+# chunk kernel); T = 192 with a ragged cu_seqlens (a partial chunk): the gate stays an autograd
+# node of its own
 @pytest.mark.parametrize("T", [128, 192])
-def test_kda_fused_gate_optimized_matches_original(lower_bound, T):
+def test_kda_fused_gate_optimized_matches_original(lower_bound, with_a_log, T):
     """use_gate_in_kernel=True (the gate activation feeding the HIP backward, dA_log /
     ddt_bias through its explicit backward) against the original backend on the
-    same inputs; and the envelope: accepted for KDA, rejected for GDN / GDN2 with
-    the reference's reasons (runtime.py:97-98)."""
+    same inputs: the output and every leaf's gradient (q, k, v, beta, g_raw, A_log, dt_bias);
+    the lower-bound form with and without A_log; and the envelope: accepted for KDA,
+    rejected for GDN / GDN2 with the reference's reasons (runtime.py:97-98)."""
     import rewy_amd as fdr
     from rewy_amd.runtime import rejection_reason
-    print(f"\n[e2e] kda fused gate lower_bound={lower_bound} T={T}", flush=True)
+    print(f"\n[e2e] kda fused gate lower_bound={lower_bound} A_log={with_a_log} T={T}", flush=True)
     xs, dO = make_inputs("kda", 2, T, 2, seed=31)
     gen = torch.Generator().manual_seed(5)
-    leaves = dict(g=torch.randn(2, T, 2, 128, generator=gen), A_log=torch.randn(2, generator=gen) * 0.5,
-                  dt_bias=torch.randn(256, generator=gen) * 0.1)
+    leaves = dict(q=xs["q"], k=xs["k"], v=xs["v"], beta=xs["beta"], g=torch.randn(2, T, 2, 128, generator=gen),
+                  A_log=torch.randn(2, generator=gen) * 0.5, dt_bias=torch.randn(256, generator=gen) * 0.1)
+    if not with_a_log:
+        del leaves["A_log"]
     dev = torch.device("cuda")
     res = {}
     for backend in ("optimized", "original"):
@@ -141,17 +144,16 @@ def test_kda_fused_gate_optimized_matches_original(lower_bound, T):
             packed = dict(cu_seqlens=torch.tensor([0, 70, T], device=dev)) if T == 192 else {}
             if packed:     # one packed row of two sequences, one initial state each
                 flat = lambda x: x.reshape(1, 2 * T, *x.shape[2:])
-                args = [flat(xs["q"].to(dev)), flat(xs["k"].to(dev)), flat(xs["v"].to(dev)), flat(lv["g"]),
-                        flat(xs["beta"].to(dev))]
+                args = [flat(lv["q"]), flat(lv["k"]), flat(lv["v"]), flat(lv["g"]), flat(lv["beta"])]
                 packed["cu_seqlens"] = torch.tensor([0, 70, 2 * T], device=dev)
             else:
-                args = [xs["q"].to(dev), xs["k"].to(dev), xs["v"].to(dev), lv["g"], xs["beta"].to(dev)]
+                args = [lv["q"], lv["k"], lv["v"], lv["g"], lv["beta"]]
             o, _ = fdr.chunk_kda(*args, initial_state=xs["initial_state"].to(dev), use_gate_in_kernel=True,
-                                 A_log=lv["A_log"], dt_bias=lv["dt_bias"], lower_bound=lower_bound, **packed)
-        res[backend] = [x.detach().double().cpu().numpy()
-                        for x in torch.autograd.grad(o, list(lv.values()), dO.to(dev).reshape(o.shape))]
-    for name, a, r in zip(leaves, res["optimized"], res["original"]):
-        e = O.error(r, a, 0.02)
+                                 A_log=lv.get("A_log"), dt_bias=lv["dt_bias"], lower_bound=lower_bound, **packed)
+        grads = torch.autograd.grad(o, list(lv.values()), dO.to(dev).reshape(o.shape))
+        res[backend] = [o.detach().double().cpu().numpy()] + [x.detach().double().cpu().numpy() for x in grads]
+    for name, a, r in zip(["o"] + list(leaves), res["optimized"], res["original"]):
+        e = O.error(r, a, 0.02 if name in ("g", "A_log", "dt_bias", "beta") else 0.008)
         print(name, e, flush=True)
         assert e["passed"], (name, e)
     q = xs["q"].to(dev)
