@@ -140,6 +140,26 @@ hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v, const void
                          int h_v_first, int B, int T, int H, int qk_heads, int K, int V, int chunk, float scale,
                          hipStream_t stream);
 
+/*
+ * KDA's kernel-level WY seam: FLA's chunk_kda_bwd_wy_dqkg_fused(q, k, v, v_new, g, beta, A,
+ * h, do, dh, dv, scale) -> (dq, dk, dv2, db, dg, dA), whose kernel the reference replaces by
+ * its residual producer/consumer (backends/backward.py:23-25, LocalBetaResidual,
+ * kernels/kda_residual_local_beta.py:8-23; the NPU wrapper's signature at
+ * kernels/kda_residual_npu_onchip.py:683-702).  Every term of fdr_chunk_bwd but the matrix
+ * intra: dq, dk fp32 [B,T,H,K] (per value head), dv bf16, dg fp32 before the in-chunk
+ * reverse cumsum, dbeta fp32 complete on rows with |beta| >= 1e-6 (the residual identity;
+ * the direct terms on the others, which fdr_matrix_intra with beta_complete completes), and
+ * dA fp32 [B,T,H,64] = D = -strict_tril(P R^T), the dAkk the intra consumes.  dR is the
+ * state recurrence's dR (FLA's dv after chunk_gated_delta_rule_bwd_dhu).  Then
+ * fdr_matrix_intra(..., dAqk, dA, dq, dk, dbeta, dg, beta_complete = 1) and the reverse
+ * cumsum of dg give fdr_chunk_bwd's gradients.
+ */
+hipError_t fdr_chunk_bwd_wy(const void* q, const void* k, const void* v, const void* v_new, const void* dO,
+                            const void* dR, const float* g, const float* beta, const float* Akk, const void* h,
+                            const void* dh, float* dq, float* dk, void* dv, float* dbeta, float* dg, float* dA,
+                            int h_v_first, int B, int T, int H, int qk_heads, int K, int V, int chunk, float scale,
+                            hipStream_t stream);
+
 /* fdr_chunk_bwd over a variable-length batch whose sequences start anywhere (the packing
  * described at the top; the reference's chunk-stage kernels with cu_seqlens / chunk_indices,
  * e.g. kernels/endpoint_intra.py:58-63).  h, dh are [num_chunks,H,K,V] (or [V,K]). */

@@ -34,6 +34,8 @@ SIGNATURES = {
     "fdr_chunk_bwd_varlen": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P,
                              _I, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_stream_probe": [_I, _P, _P, ctypes.c_longlong, _I, _P],
+    "fdr_chunk_bwd_wy": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                         _I, _I, _F, _P],
     "fdr_matrix_intra": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
     "fdr_fwd_prepare": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_fwd_o": [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P],

@@ -257,8 +257,11 @@ struct GateFoldArgs {
 // MAP: a packed variable-length batch whose sequences start anywhere (cu, ci: cu_seqlens and
 // chunk_indices); a sequence's last chunk may hold fewer than 64 rows, whose missing rows
 // read as zeros (the gate cumsum's as its last row) and are never written.
+// WY (KDA): the kernel-level WY seam alone -- every term but the matrix intra, dq / dk in fp32
+// (dq32, dk32), dg before the in-chunk reverse cumsum, dbeta complete for |beta| >= 1e-6 rows
+// (the direct terms otherwise), and dA = D, the gradient the intra consumes as dAkk.
 template <int GATE, bool VEC_B, bool INTRA, bool PIPE = false, int FOLD = -1, bool HVF = false, bool ORIG = false,
-          bool MAP = false>
+          bool MAP = false, bool WY = false>
 __device__ __forceinline__ void chunk_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
@@ -270,11 +273,13 @@ __device__ __forceinline__ void chunk_body(
     const float* __restrict__ daqk, float* __restrict__ dq32, float* __restrict__ dk32,
     float* __restrict__ db32, int beta_complete, int item, int next_item, char* regA, char* regB,
     float* small, bf16* xbuf, float* gbuf, PhaseIn& pin, const GateFoldArgs* gf = nullptr,
-    float beta_sig = 0.f, int HQ = 0, const int* cu = nullptr, const int* ci = nullptr) {
+    float beta_sig = 0.f, int HQ = 0, const int* cu = nullptr, const int* ci = nullptr, float* dA_wy = nullptr) {
   if (HQ <= 0) HQ = H;
   using LY = PostLayout<GATE, VEC_B, INTRA, PIPE, ORIG>;
   static_assert(!ORIG || (GATE == CG_VECTOR && !VEC_B && !INTRA && !PIPE), "original formulation: KDA only");
   static_assert(!MAP || (!INTRA && !PIPE && !ORIG && FOLD < 0), "variable-length rows: the plain chunk kernel");
+  static_assert(!WY || (GATE == CG_VECTOR && !VEC_B && !INTRA && !PIPE && !ORIG && FOLD < 0 && !MAP),
+                "the WY seam: KDA, dense rows");
   using post::LDT;
   auto B16 = [&](int off) { return reinterpret_cast<bf16*>(regA + off); };
   auto B16b = [&](int off) { return reinterpret_cast<bf16*>(regB + off); };
@@ -737,6 +742,8 @@ __device__ __forceinline__ void chunk_body(
         hi = split_hi4(dv4, lo);
         *reinterpret_cast<bf16x4*>(Drh + i * LDT + 16 * I + 4 * lg) = hi;
         *reinterpret_cast<bf16x4*>(Drl + i * LDT + 16 * I + 4 * lg) = lo;
+        // the WY seam's dA: row i, columns s = 16 I + 4 lg .. + 3 (zero on and above the diagonal)
+        if constexpr (WY) *reinterpret_cast<f32x4*>(dA_wy + (tok0 * H + h) * C + (size_t)i * rsa + 16 * I + 4 * lg) = dv4;
       }
     }
   }   // phase 2
@@ -919,6 +926,7 @@ __device__ __forceinline__ void chunk_body(
   }   // !INTRA: phase 4
 
   // ---------------- phase 5: matrix intra ----------------
+  if constexpr (!WY) {
   auto combine = [&](int I, const f32x4& xq, const f32x4& xe, const f32x4& xk) {
     const f32x4 b4 = bvals(I);
 #pragma unroll
@@ -1103,6 +1111,7 @@ __device__ __forceinline__ void chunk_body(
   }
 
   }   // vector gates
+  }   // !WY: phase 5
 
   // fallback dbeta rows: direct terms sum_k (k exp2(g) Eb + k ue), summed over all columns
   if constexpr (!VEC_B) {
@@ -1126,6 +1135,7 @@ __device__ __forceinline__ void chunk_body(
     float carry = 0.f;                         // total of the rows below
 #pragma unroll
     for (int I = 3; I >= 0; --I) {
+      if constexpr (WY) break;                 // the seam's dg stays before the cumsum
       f32x4& x = aw[I];
       x[2] += x[3];
       x[1] += x[2];
@@ -1191,8 +1201,13 @@ __device__ __forceinline__ void chunk_body(
       for (int r = 0; r < 4; ++r) {
         const int t = 16 * I + 4 * lg + r;
         const int off = t * rsk32 + kk;
-        *rw.dst(dqb + off, t) = to_bf16(aq[I][r]);
-        *rw.dst(dkb + off, t) = to_bf16(ak[I][r]);
+        if constexpr (WY) {
+          dq32[kofs + off] = aq[I][r];
+          dk32[kofs + off] = ak[I][r];
+        } else {
+          *rw.dst(dqb + off, t) = to_bf16(aq[I][r]);
+          *rw.dst(dkb + off, t) = to_bf16(ak[I][r]);
+        }
         if constexpr (GATE == CG_VECTOR && FOLD < 0) *rw.dst(dgb + off, t) = aw[I][r];
         if constexpr (VEC_B) *rw.dst(dbb + off, t) = to_bf16(adb[I][r]);
       }
@@ -1331,6 +1346,25 @@ __global__ __launch_bounds__(512) void chunk_bwd_original_kernel(
       q, k, v, vnew, dO, dR, g, beta, nullptr, nullptr, akk, hst, dhst, dq_out, dk_out, dv_out, dg_out, dbeta_out,
       nullptr, nullptr, T, H, scale, nullptr, nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem,
       smem + LY::REGION_A, reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin);
+}
+
+// KDA's kernel-level WY seam (every term but the matrix intra; see WY above)
+template <bool HVF>
+__global__ __launch_bounds__(512) void chunk_bwd_wy_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
+    const float* __restrict__ g, const float* __restrict__ beta, const float* __restrict__ akk,
+    const bf16* __restrict__ hst, const bf16* __restrict__ dhst, float* __restrict__ dq32, float* __restrict__ dk32,
+    bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out, float* __restrict__ dA,
+    int T, int H, float scale, int HQ) {
+  using LY = PostLayout<CG_VECTOR, false>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  PhaseIn pin;
+  chunk_body<CG_VECTOR, false, false, false, -1, HVF, false, false, true>(
+      q, k, v, vnew, dO, dR, g, beta, nullptr, nullptr, akk, hst, dhst, nullptr, nullptr, dv_out, dg_out, dbeta_out,
+      nullptr, nullptr, T, H, scale, nullptr, dq32, dk32, nullptr, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
+      reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin, nullptr, 0.f, HQ, nullptr,
+      nullptr, dA);
 }
 
 // KDA with the gate backward folded into the dg stores (no dg output)
@@ -1549,6 +1583,35 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
   return chunk_bwd_dispatch(q, k, v, v_new, dO, dR, g, gate_mode, beta, b_gate, w_gate, Akk, h, dh, dq, dk, dv, dg,
                             dbeta, beta_sigmoid, db, dw, h_v_first, B, T, H, qk_heads, scale, stream, nullptr,
                             nullptr);
+}
+
+extern "C" hipError_t fdr_chunk_bwd_wy(const void* q, const void* k, const void* v, const void* v_new,
+                                       const void* dO, const void* dR, const float* g, const float* beta,
+                                       const float* Akk, const void* h, const void* dh, float* dq, float* dk,
+                                       void* dv, float* dbeta, float* dg, float* dA, int h_v_first, int B, int T,
+                                       int H, int qk_heads, int K, int V, int chunk, float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  const int HQ = qk_heads > 0 ? qk_heads : H;
+  if (H % HQ) return hipErrorInvalidValue;
+  if (!q || !k || !v || !v_new || !dO || !dR || !g || !beta || !Akk || !h || !dh || !dq || !dk || !dv || !dbeta ||
+      !dg || !dA)
+    return hipErrorInvalidValue;
+  using LY = PostLayout<CG_VECTOR, false>;
+  const int items = B * H * (T / C);
+#define WY_LAUNCH(HV)                                                                                          \
+  {                                                                                                            \
+    auto kern = chunk_bwd_wy_kernel<HV>;                                                                       \
+    static bool attr_set[kMaxDevices] = {};                                                                    \
+    const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);                            \
+    if (e != hipSuccess) return e;                                                                             \
+    hipLaunchKernelGGL(kern, dim3(items), dim3(512), LY::BYTES, stream, (const bf16*)q, (const bf16*)k,         \
+                       (const bf16*)v, (const bf16*)v_new, (const bf16*)dO, (const bf16*)dR, g, beta, Akk,     \
+                       (const bf16*)h, (const bf16*)dh, dq, dk, (bf16*)dv, dg, dbeta, dA, T, H, scale, HQ);   \
+  }
+  if (h_v_first) WY_LAUNCH(true)
+  else WY_LAUNCH(false)
+#undef WY_LAUNCH
+  return hipGetLastError();
 }
 
 extern "C" hipError_t fdr_chunk_bwd_varlen(const void* q, const void* k, const void* v, const void* v_new,

@@ -418,6 +418,39 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
     return out
 
 
+def chunk_bwd_wy(q, k, v, v_new, dO, dR, g, Akk, h, dh, scale, beta, h_v_first=False):
+    """KDA's WY seam alone (fdr_chunk_bwd_wy): every term of ``chunk_bwd`` but the matrix
+    intra.  Returns dict(dq, dk [fp32], dv [bf16], dbeta [fp32, complete on |beta| >= 1e-6
+    rows], dg [fp32, before the in-chunk reverse cumsum], dA [fp32 [B,T,H,64], the intra's
+    dAkk])."""
+    B, T, HQ, K = _dims(q)
+    H, HQ = _group(v.shape[2] if v is not None and v.ndim == 4 else HQ, HQ)
+    V = V_SUPPORTED
+    dev = q.device
+    bf, f32 = torch.bfloat16, torch.float32
+    NT = T // CHUNK
+    for x, n in ((q, "q"), (k, "k")):
+        _need(x, n, bf, (B, T, HQ, K), dev)
+    for x, n in ((v, "v"), (v_new, "v_new"), (dO, "dO"), (dR, "dR")):
+        _need(x, n, bf, (B, T, H, V), dev)
+    _need(g, "g", f32, (B, T, H, K), dev)
+    _need(beta, "beta", f32, (B, T, H), dev)
+    _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
+    _need(h, "h", bf, (B, NT, H, K, V), dev)
+    _need(dh, "dh", bf, (B, NT, H, K, V), dev)
+    out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=f32), dk=torch.empty(B, T, H, K, device=dev, dtype=f32),
+               dv=torch.empty(B, T, H, V, device=dev, dtype=bf), dbeta=torch.empty(B, T, H, device=dev, dtype=f32),
+               dg=torch.empty(B, T, H, K, device=dev, dtype=f32),
+               dA=torch.empty(B, T, H, CHUNK, device=dev, dtype=f32))
+    P = _lib.ptr
+    st = _lib.load().fdr_chunk_bwd_wy(P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), P(beta), P(Akk), P(h), P(dh),
+                                      P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), P(out["dg"]),
+                                      P(out["dA"]), int(bool(h_v_first)), B, T, H, HQ, K, V, CHUNK, float(scale),
+                                      _lib.stream_handle(dev))
+    _lib.check(st, "fdr_chunk_bwd_wy")
+    return out
+
+
 def chunk_bwd_original(q, k, v, v_new, dO, dR, g, Akk, h, dh, scale, beta):
     """KDA's chunk stage in the original 7-product formulation (fdr_chunk_bwd_original): the
     same-GPU comparator of ``chunk_bwd``.  Returns dict(dq, dk, dv, dg, dbeta)."""
