@@ -59,9 +59,21 @@ HS = 128 * 128 * 2           # one [128][128] bf16 state
 AT = 64 * 64 * 4             # one [64][64] fp32 matrix (Akk, Aqk)
 
 
-def kernel_costs(op, full_saving):
+def inline_aqk(cfg):
+    """The scalar / no-gate backends' direct state recurrence forms Aqk from the raw q / k it
+    stages (as ``backends.backward._scalar`` decides): fdr_prepare_wu then reads no q and
+    writes no Aqk, and fdr_state_bwd reads no Aqk."""
+    from rewy_amd import ops
+    if cfg["full_saving"] or cfg["op"] not in ("gdn", "delta"):
+        return False
+    NT = cfg["T"] // 64
+    return not ops._use_affine("auto", cfg["B"], cfg["H"], NT) and ops.state_form(cfg["B"], cfg["H"], NT) == "direct"
+
+
+def kernel_costs(op, full_saving, inline=False):
     """Algorithmic (bytes, FLOPs) per chunk-head of every kernel the backward launches:
-    every operand read once, every result written once; dense GEMM flops."""
+    every operand read once, every result written once; dense GEMM flops.  ``inline``: the
+    state recurrence forms Aqk itself (see ``inline_aqk``)."""
     vec, vb = op in ("kda", "gdn2"), op == "gdn2"
     g_b = 64 * 128 * 4 if vec else (64 * 4 if op == "gdn" else 0)
     gl_b = 128 * 4 if vec else (4 if op == "gdn" else 0)
@@ -70,12 +82,13 @@ def kernel_costs(op, full_saving):
     mm = lambda m, n, k: 2 * m * n * k
     costs = {}
     if not full_saving:
-        rd = 3 * TILE + g_b + gates_b + AT                      # q, k, v, g, beta|b,w, Akk
-        wr = 2 * TILE + (2 * TILE if vec else AT)               # w, u, (qg, kg | Aqk)
-        costs["fdr_prepare_wu"] = (rd + wr, 2 * mm(64, 128, 64) + (0 if vec else mm(64, 64, 128)))
+        rd = (2 if inline else 3) * TILE + g_b + gates_b + AT   # (q,) k, v, g, beta|b,w, Akk
+        wr = 2 * TILE + (2 * TILE if vec else (0 if inline else AT))   # w, u, (qg, kg | Aqk)
+        costs["fdr_prepare_wu"] = (rd + wr, 2 * mm(64, 128, 64) + (0 if vec or inline else mm(64, 64, 128)))
         costs["fdr_fwd_h"] = (3 * TILE + gl_b + (0 if vec else g_b) + HS + TILE, 2 * mm(64, 128, 128))
-    costs["fdr_state_bwd"] = (4 * TILE + AT + gl_b + (0 if vec else g_b) + HS + TILE,
-                              mm(64, 128, 128) + mm(64, 128, 64) + 2 * mm(128, 128, 64))
+    costs["fdr_state_bwd"] = (4 * TILE + (0 if inline else AT) + gl_b + (0 if vec else g_b) + HS + TILE,
+                              mm(64, 128, 128) + mm(64, 128, 64) + 2 * mm(128, 128, 64)
+                              + (mm(64, 64, 128) if inline else 0))
     rd = 5 * TILE + g_b + gates_b + AT + 2 * HS + (TILE if vb else 0)
     wr = 3 * TILE + g_b + (2 * TILE if vb else beta_b)
     costs["fdr_chunk_bwd"] = (rd + wr, 3 * mm(64, 64, 128) + 3 * mm(64, 128, 128) + 4 * mm(64, 64, 128))
@@ -177,14 +190,15 @@ def setup(cfg, device):
     kern = {}
     if keep:
         qs, ks, ws, aqk, h, v_new = sv["qg"], sv["kg"], sv["w"], sv["Aqk"], sv["h"], sv["v_new"]
-    else:
+    NT = cfg["T"] // 64
+    inline = inline_aqk(cfg)
+    if not keep:
         kern["fdr_prepare_wu"] = lambda: ops.prepare_wu(
             xs["k"], xs["v"], sv["Akk"], gate, g=g, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"), q=xs["q"],
-            want_qkg=vec, want_aqk=not vec, scale=scale)
+            want_qkg=vec, want_aqk=not vec and not inline, scale=scale)
         pre = kern["fdr_prepare_wu"]()
         ks, qs, ws = (pre["kg"], pre["qg"], pre["w"]) if vec else (xs["k"], xs["q"], pre["w"])
         aqk = sv["Aqk"] if vec else pre["Aqk"]
-    NT = cfg["T"] // 64
     if keep and ops._state_method("auto", cfg["B"], cfg["H"], NT) == "segmented":
         # long rows, few heads: segment maps in parallel, a short chain, segments rerun
         kern["segmented_state"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
@@ -273,7 +287,7 @@ def measure(cfg, steps, warmup):
     ms = time_steps(step, steps, warmup, WARMUP_MIN_S, winfo)
     fwd_ms = time_steps(forward, max(3, steps // 4), 1)
     kt = time_kernels(kern, max(5, steps))
-    costs = kernel_costs(cfg["op"], cfg["full_saving"])
+    costs = kernel_costs(cfg["op"], cfg["full_saving"], inline_aqk(cfg))
     kernels = {}
     for n, t in kt.items():
         by, fl = costs[n]

@@ -204,8 +204,13 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
     A = _f32(A)
     beta = _f32(beta)
     gate = ops.GATE_SCALAR if op == "gdn" else ops.GATE_NONE
-    pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, q=q, want_aqk=True, scale=scale, varlen=vl)
-    if vl is None and q.shape[2] == v.shape[2] and ops.affine_pays(v):
+    affine = vl is None and q.shape[2] == v.shape[2] and ops.affine_pays(v)
+    # the direct state recurrence forms Aqk itself from the raw q / k it stages: fdr_prepare_wu
+    # then writes only w and u
+    inline = not affine and (vl is not None or ops.state_form(q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK)
+                             == "direct")
+    pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, q=q, want_aqk=not inline, scale=scale, varlen=vl)
+    if affine:
         # few heads: both recurrences side by side in affine-step form
         h, v_new, dh, dR, dh0 = ops.recurrences(q, k, pre["w"], pre["u"], g, gate, do, scale, aqk=pre["Aqk"],
                                                 h0=_f32(initial_state), dht=_f32(dht),
@@ -214,7 +219,8 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
         h, v_new, _ = ops.fwd_h(k, pre["w"], pre["u"], g, gate, h0=_f32(initial_state), method="direct",
                                 varlen=vl, state_v_first=state_v_first)
         dh, dR, dh0 = ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
-                                    want_dh0=initial_state is not None, method="auto" if vl is None else "direct",
+                                    want_dh0=initial_state is not None,
+                                    method="direct" if inline or vl is not None else "auto",
                                     varlen=vl, state_v_first=state_v_first)
     out = _group_sum(ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta,
                                    beta_sigmoid=beta_sigmoid, varlen=vl), q.shape[2])

@@ -23,7 +23,7 @@ namespace rewy {
 
 enum GateMode { GATE_NONE = 0, GATE_SCALAR = 1, GATE_VECTOR = 2 };
 
-template <int BV, int GATE, bool DV_FROM_AQK>
+template <int BV, int GATE, bool DV_FROM_AQK, bool INL = false>
 struct StateSmem {
   static constexpr int LDK = KD + 8;   // pitch of [.][K] tiles
   static constexpr int LDT = C + 8;    // pitch of [.][T] tiles
@@ -37,22 +37,31 @@ struct StateSmem {
   bf16 dhT[BV][LDK];       // dh^T:    B operand of kg * dh
   bf16 drT[BV][LDT];       // dR^T:    B operand of w^T dR
   float lam[KD];           // exp2(g_last) per key row
+  // in-kernel Aqk (INL, scalar / no gate): k and q are staged raw; qg^T dO is formed as
+  // q^T (2^g dO) and kg dh as 2^(g_last - g_t) (k dh)
+  bf16 dOg[(INL && GATE == GATE_SCALAR) ? C * BV : 1];   // 2^(g_t) dO rows (swizzled)
+  float gt[INL ? C + 1 : 1];                             // g_t per row, g_last at [C]
 };
 
 // NW waves: 8 (wave w owns state rows [16 w, 16 w + 16), every value column) or 16
 // (row tile w % 8, half of the value columns).
 //
+// INL (scalar / no gate, with DV_FROM_AQK): Aqk = scale tril(q k^T 2^(g_i - g_s)) is formed
+// in-kernel from the raw q / k each chunk stages anyway, instead of being read from HBM
+// (fdr_prepare_wu then need not write it).
+//
 // Segmented form (segs > 0): row r of T tokens is split into `segs` segments of
 // consecutive chunks, work-group row b is segment b % segs of row b / segs, and dht holds
 // each segment's end state (from state_combine_kernel).
-template <int BV, int GATE, bool DV_FROM_AQK, int NW, bool MAP = false>
+template <int BV, int GATE, bool DV_FROM_AQK, int NW, bool MAP = false, bool INL = false>
 __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ w,
     const float* __restrict__ g, const bf16* __restrict__ dO, const float* __restrict__ aqk,
     const bf16* __restrict__ dv, const float* __restrict__ dht, bf16* __restrict__ dh_out,
     bf16* __restrict__ dr_out, float* __restrict__ dh0, int T, int H, float scale,
     const int* __restrict__ chunk_off, int segs, int vf, int HQ, const int* __restrict__ cu) {
-  using S = StateSmem<BV, GATE, DV_FROM_AQK>;
+  static_assert(!INL || (DV_FROM_AQK && GATE != GATE_VECTOR), "in-kernel Aqk: scalar / no gate");
+  using S = StateSmem<BV, GATE, DV_FROM_AQK, INL>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
   constexpr int NCT = BV / 16;             // column tiles of the state
@@ -116,6 +125,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   u32x4 rk[NPI], rq[NPI], rw[NPI], rdo[NDO];
   f32x4 ra[NPI];
   float rg_last = 0.f, rg_tok[NPI];             // scalar gate: last row, the rows this thread stages
+  float rg_do[NDO];                             // INL, scalar gate: the gate of each dO piece's row
   const size_t row_stride_k = (size_t)H * KD;   // elements between tokens
   const size_t row_stride_v = (size_t)H * VD;
 
@@ -141,7 +151,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + oq, p >> 4));
       rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + oq, p >> 4));
       rw[i] = *reinterpret_cast<const u32x4*>(rs_.src(w + o, p >> 4));
-      if constexpr (DV_FROM_AQK)
+      if constexpr (DV_FROM_AQK && !INL)
         ra[i] = *reinterpret_cast<const f32x4*>(rs_.src(aqk + ((tok0 + (p >> 4)) * H + h) * C + (p & 15) * 4, p >> 4));
     }
 #pragma unroll
@@ -150,6 +160,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       const int p = min(tid + NTH * i, NPD - 1);
       rdo[i] = *reinterpret_cast<const u32x4*>(
           rs_.src(dO + (tok0 + p / CHV) * row_stride_v + (size_t)h * VD + v_base + (p % CHV) * 8, p / CHV));
+      if constexpr (INL && GATE == GATE_SCALAR) rg_do[i] = g[(tok0 + rs_.clamp(p / CHV)) * H + h];
     }
   };
 
@@ -166,7 +177,11 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       const int p = tid + NTH * i;
       const int t = p >> 4, ch = p & 15;
       u32x4 kq = rk[i], qq = rq[i];
-      if constexpr (GATE == GATE_SCALAR) {
+      if constexpr (INL) {
+        // raw k and q; the row gates go to LDS for the Aqk factors and the kg dh row scaling
+        if (ch == 0) sm.gt[t] = GATE == GATE_SCALAR ? rg_tok[i] : 0.f;
+        if (tid == 0) sm.gt[C] = rg_last;
+      } else if constexpr (GATE == GATE_SCALAR) {
         // scalar gate: kg = k 2^(g_last - g_t), qg = q 2^(g_t), the row's factors from registers
         kq = scale_bf16x8(kq, fast_exp2(rg_last - rg_tok[i]));
         qq = scale_bf16x8(qq, fast_exp2(rg_tok[i]));
@@ -174,7 +189,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       *reinterpret_cast<u32x4*>(&sm.k[t][ch * 8]) = kq;
       store_tr_chunk<16>(sm.q, t, ch, qq);
       store_tr_chunk<16>(sm.w, t, ch, rw[i]);
-      if constexpr (DV_FROM_AQK) {
+      if constexpr (DV_FROM_AQK && !INL) {
         bf16x4 lo;
         const bf16x4 hi = split_hi4(ra[i], lo);
         *reinterpret_cast<bf16x4*>(sm.ah + tr_off<8>(t, ch * 4)) = hi;
@@ -184,7 +199,11 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
       const int p = tid + NTH * i;
-      if (NPD % NTH == 0 || p < NPD) store_tr_chunk<CHV>(sm.dO, p / CHV, p % CHV, rdo[i]);
+      if (NPD % NTH == 0 || p < NPD) {
+        store_tr_chunk<CHV>(sm.dO, p / CHV, p % CHV, rdo[i]);
+        if constexpr (INL && GATE == GATE_SCALAR)
+          store_tr_chunk<CHV>(sm.dOg, p / CHV, p % CHV, scale_bf16x8(rdo[i], fast_exp2(rg_do[i])));
+      }
     }
   };
 
@@ -203,6 +222,35 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     }
     lds_barrier();
 
+    if constexpr (INL) {
+      // Aqk = scale tril(q k^T 2^(g_i - g_s)), as S^T = k q^T tiles (rows s, columns i), so that
+      // each lane's four rows s are four consecutive columns of Aqk's row i (hi / lo, as staged)
+#pragma unroll
+      for (int tt = wv; tt < 16; tt += NW) {
+        const int Is = tt >> 2, Ji = tt & 3;
+        f32x4 a = zero4();
+        if (Ji >= Is) {                      // wave-uniform: tiles above the diagonal are zero
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks)
+            a = mfma(frag(&sm.k[16 * Is][32 * ks], S::LDK), frag_row<16>(sm.q, 16 * Ji, 32 * ks), a);
+        }
+        const int i = 16 * Ji + (l & 15);
+        const float gi = sm.gt[i];
+        f32x4 v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int s_ = 16 * Is + 4 * (l >> 4) + r;
+          const float f = GATE == GATE_SCALAR ? scale * fast_exp2(gi - sm.gt[s_]) : scale;
+          v[r] = i >= s_ ? a[r] * f : 0.f;
+        }
+        bf16x4 lo;
+        const bf16x4 hi = split_hi4(v, lo);
+        *reinterpret_cast<bf16x4*>(sm.ah + tr_off<8>(i, 16 * Is + 4 * (l >> 4))) = hi;
+        *reinterpret_cast<bf16x4*>(sm.al + tr_off<8>(i, 16 * Is + 4 * (l >> 4))) = lo;
+      }
+      lds_barrier();
+    }
+
     // X = qg^T dO (independent of dh)
     f32x4 xq[NCW];
 #pragma unroll
@@ -210,7 +258,8 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       f32x4 a = zero4();
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag_tr<16>(sm.q, 32 * ks, 16 * rt), frag_tr<CHV>(sm.dO, 32 * ks, 16 * (ct0 + j)), a);
+        a = mfma(frag_tr<16>(sm.q, 32 * ks, 16 * rt),
+                 frag_tr<CHV>(INL && GATE == GATE_SCALAR ? sm.dOg : sm.dO, 32 * ks, 16 * (ct0 + j)), a);
       xq[j] = a;
     }
     // dR tiles: kg dh + Aqk^T dO (+ dv)
@@ -234,9 +283,19 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
             a[r] = to_f32(*rs_.src(dv + (rs_.tok0 + t) * row_stride_v + (size_t)h * VD + v_base + 16 * ct + (l & 15), t));
           }
         }
+        if constexpr (INL && GATE == GATE_SCALAR) {
+          // kg dh = 2^(g_last - g_t) (k dh), row t = 16 drow + 4 (l >> 4) + r
+          f32x4 b = zero4();
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          a = mfma(frag(&sm.k[16 * drow][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), a);
+          for (int ks = 0; ks < 4; ++ks)
+            b = mfma(frag(&sm.k[16 * drow][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), b);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) a[r] += b[r] * fast_exp2(sm.gt[C] - sm.gt[16 * drow + 4 * (l >> 4) + r]);
+        } else {
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks)
+            a = mfma(frag(&sm.k[16 * drow][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), a);
+        }
         bf16x4 v4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) v4[r] = to_bf16(a[r]);
@@ -310,7 +369,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
 template <int BV>
 constexpr int state_waves() { return BV == 32 ? 16 : 8; }
 
-template <int BV, int GATE, bool AQK>
+template <int BV, int GATE, bool AQK, bool INL = false>
 static hipError_t launch_state(const void* q, const void* k, const void* w, const float* g,
                                const void* dO, const float* aqk, const void* dv, const float* dht,
                                void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
@@ -320,7 +379,7 @@ static hipError_t launch_state(const void* q, const void* k, const void* w, cons
   const int grid = rows * H * (VD / BV);
   constexpr int NW = state_waves<BV>();
 #define S_LAUNCH(MAP)                                                                                        \
-  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW, MAP>), dim3(grid), dim3(64 * NW), 0, stream,        \
+  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW, MAP, INL>), dim3(grid), dim3(64 * NW), 0, stream,   \
                      (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk, (const bf16*)dv, \
                      dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale, chunk_off, segs, vf, HQ > 0 ? HQ : H, cu)
   if (cu) S_LAUNCH(true);
@@ -329,13 +388,13 @@ static hipError_t launch_state(const void* q, const void* k, const void* w, cons
   return hipGetLastError();
 }
 
-template <int GATE, bool AQK>
+template <int GATE, bool AQK, bool INL = false>
 static hipError_t pick_bv(int bv, const void* q, const void* k, const void* w, const float* g,
                           const void* dO, const float* aqk, const void* dv, const float* dht,
                           void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
                           hipStream_t s, const int* co, int vf, int HQ, const int* cu) {
 #define S_BV(BV) \
-  launch_state<BV, GATE, AQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, HQ, cu)
+  launch_state<BV, GATE, AQK, INL>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, HQ, cu)
   switch (bv) {
     case 16: return S_BV(16);
     case 32: return S_BV(32);
@@ -659,7 +718,10 @@ static hipError_t state_dispatch(const void* q, const void* k, const void* w, co
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0)
     return hipErrorInvalidValue;
   if (!q || !k || !w || !dO || !dh || !dr) return hipErrorInvalidValue;
-  if ((aqk == nullptr) == (dv == nullptr)) return hipErrorInvalidValue;
+  // neither Aqk nor dv: the scalar / no-gate families form Aqk in-kernel from the raw q / k
+  const bool inl = aqk == nullptr && dv == nullptr;
+  if (aqk && dv) return hipErrorInvalidValue;
+  if (inl && gate_mode == GATE_VECTOR) return hipErrorInvalidValue;
   if (gate_mode != GATE_NONE && g == nullptr) return hipErrorInvalidValue;
   if (HQ <= 0) HQ = H;
   if (H % HQ) return hipErrorInvalidValue;
@@ -669,8 +731,10 @@ static hipError_t state_dispatch(const void* q, const void* k, const void* w, co
 #define S_ARGS bv, q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, stream, co, vf, HQ, cu
   switch (gate_mode) {
     case GATE_NONE:
+      if (inl) return pick_bv<GATE_NONE, true, true>(S_ARGS);
       return from_aqk ? pick_bv<GATE_NONE, true>(S_ARGS) : pick_bv<GATE_NONE, false>(S_ARGS);
     case GATE_SCALAR:
+      if (inl) return pick_bv<GATE_SCALAR, true, true>(S_ARGS);
       return from_aqk ? pick_bv<GATE_SCALAR, true>(S_ARGS) : pick_bv<GATE_SCALAR, false>(S_ARGS);
     case GATE_VECTOR:
       return from_aqk ? pick_bv<GATE_VECTOR, true>(S_ARGS) : pick_bv<GATE_VECTOR, false>(S_ARGS);

@@ -64,6 +64,11 @@ def _state_method(method, B, H, NT):
     return "direct"
 
 
+def state_form(B, H, NT):
+    """The form ``state_bwd(method="auto")`` takes for B rows of NT chunks and H heads."""
+    return _state_method("auto", B, H, NT)
+
+
 def _use_affine(method, B, H, NT):
     if method not in ("auto", "direct", "affine"):
         raise ValueError('method must be "auto", "direct" or "affine"')
@@ -183,6 +188,10 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
               value_block=0, method="auto", chunk_offsets=None, segments=0, state_v_first=False, varlen=None):
     """Reverse state recurrence.  Returns (dh [B,NT,H,K,V] bf16, dR [B,T,H,V] bf16, dh0 fp32|None).
 
+    dv_local = Aqk^T dO comes from ``aqk``, or is given as ``dv``; with neither (scalar / no
+    gate, direct form), Aqk = scale tril(q k^T 2^(g_i - g_s)) is formed in-kernel from the raw
+    q / k the recurrence stages anyway.
+
     ``chunk_offsets`` (int [N+1]): B = 1 holds N sequences packed along T, sequence n on
     chunks [chunk_offsets[n], chunk_offsets[n+1]); dht / dh0 are then [N,H,K,V] and the
     direct kernel runs (fdr_state_bwd_varlen).  ``varlen`` (a ``Varlen``): the same for
@@ -210,8 +219,11 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
         _need(g, "g", f32, (B, T, H), dev)
     elif gate_mode != GATE_NONE:
         raise ValueError("gate_mode must be 0, 1 or 2")
-    if (aqk is None) == (dv is None):
-        raise ValueError("exactly one of aqk / dv is required")
+    inline = aqk is None and dv is None
+    if aqk is not None and dv is not None:
+        raise ValueError("pass at most one of aqk / dv")
+    if inline and gate_mode == GATE_VECTOR:
+        raise ValueError("Aqk is formed in-kernel for the scalar / no-gate families only: pass aqk")
     if aqk is not None:
         _need(aqk, "Aqk", f32, (B, T, H, CHUNK), dev)
     if dv is not None:
@@ -243,9 +255,9 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
         _lib.check(st, "fdr_state_bwd_varlen")
         return dh, dr, dh0
     form = _state_method(method, B, H, NT)
-    if HQ != H and form != "direct":
+    if (HQ != H or inline) and form != "direct":
         if method != "auto":
-            raise ValueError("grouped q/k heads take the direct state recurrence")
+            raise ValueError("grouped q/k heads and the in-kernel Aqk take the direct state recurrence")
         form = "direct"
     if form == "segmented":
         segs = int(segments) or segments_for(B, H, NT)
