@@ -60,9 +60,9 @@ AT = 64 * 64 * 4             # one [64][64] fp32 matrix (Akk, Aqk)
 
 
 def inline_aqk(cfg):
-    """The scalar / no-gate backends' direct state recurrence forms Aqk from the raw q / k it
-    stages (as ``backends.backward._scalar`` decides): fdr_prepare_wu then reads no q and
-    writes no Aqk, and fdr_state_bwd reads no Aqk."""
+    """The scalar / no-gate backends' direct path (as ``backends.backward._scalar`` decides):
+    w / u are formed in the forward scan's sweep (fdr_fwd_h_wy in place of fdr_prepare_wu +
+    fdr_fwd_h) and the state recurrence forms Aqk from the raw q / k it stages (no Aqk read)."""
     from rewy_amd import ops
     if cfg["full_saving"] or cfg["op"] not in ("gdn", "delta"):
         return False
@@ -82,10 +82,13 @@ def kernel_costs(op, full_saving, inline=False):
     mm = lambda m, n, k: 2 * m * n * k
     costs = {}
     if not full_saving:
-        rd = (2 if inline else 3) * TILE + g_b + gates_b + AT   # (q,) k, v, g, beta|b,w, Akk
-        wr = 2 * TILE + (2 * TILE if vec else (0 if inline else AT))   # w, u, (qg, kg | Aqk)
-        costs["fdr_prepare_wu"] = (rd + wr, 2 * mm(64, 128, 64) + (0 if vec or inline else mm(64, 64, 128)))
+        rd = 3 * TILE + g_b + gates_b + AT                      # q, k, v, g, beta|b,w, Akk
+        wr = 2 * TILE + (2 * TILE if vec else AT)               # w, u, (qg, kg | Aqk)
+        costs["fdr_prepare_wu"] = (rd + wr, 2 * mm(64, 128, 64) + (0 if vec else mm(64, 64, 128)))
         costs["fdr_fwd_h"] = (3 * TILE + gl_b + (0 if vec else g_b) + HS + TILE, 2 * mm(64, 128, 128))
+        # w / u formed in the forward scan's sweep: reads k, v, Akk, g, beta; writes w, h, v_new
+        costs["fdr_fwd_h_wy"] = (2 * TILE + AT + g_b + gates_b + TILE + HS + TILE,
+                                 2 * mm(64, 128, 64) + 2 * mm(64, 128, 128))
     costs["fdr_state_bwd"] = (4 * TILE + (0 if inline else AT) + gl_b + (0 if vec else g_b) + HS + TILE,
                               mm(64, 128, 128) + mm(64, 128, 64) + 2 * mm(128, 128, 64)
                               + (mm(64, 64, 128) if inline else 0))
@@ -192,10 +195,15 @@ def setup(cfg, device):
         qs, ks, ws, aqk, h, v_new = sv["qg"], sv["kg"], sv["w"], sv["Aqk"], sv["h"], sv["v_new"]
     NT = cfg["T"] // 64
     inline = inline_aqk(cfg)
-    if not keep:
+    if inline:
+        # w / u in the forward scan's sweep (fdr_fwd_h_wy), Aqk in the state recurrence
+        kern["fdr_fwd_h_wy"] = lambda: ops.fwd_h_wy(xs["k"], xs["v"], sv["Akk"], g, gate, xs["beta"], h0=xs["h0"])
+        ws, h, v_new, _ = kern["fdr_fwd_h_wy"]()
+        ks, qs, aqk = xs["k"], xs["q"], None
+    elif not keep:
         kern["fdr_prepare_wu"] = lambda: ops.prepare_wu(
             xs["k"], xs["v"], sv["Akk"], gate, g=g, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"), q=xs["q"],
-            want_qkg=vec, want_aqk=not vec and not inline, scale=scale)
+            want_qkg=vec, want_aqk=not vec, scale=scale)
         pre = kern["fdr_prepare_wu"]()
         ks, qs, ws = (pre["kg"], pre["qg"], pre["w"]) if vec else (xs["k"], xs["q"], pre["w"])
         aqk = sv["Aqk"] if vec else pre["Aqk"]
@@ -215,7 +223,7 @@ def setup(cfg, device):
                                                                  h0=xs["h0"], want_dh0=xs["h0"] is not None)
             h, v_new, dh, dR, _ = kern["affine_recurrences"]()
     else:
-        if not keep:
+        if not keep and not inline:
             kern["fdr_fwd_h"] = lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"], method="direct")
             h, v_new, _ = kern["fdr_fwd_h"]()
         kern["fdr_state_bwd"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,

@@ -234,6 +234,29 @@ hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const f
                             int k_heads, int K, int V, int chunk, int value_block, hipStream_t stream);
 
 /*
+ * The recompute pair fdr_prepare_wu + fdr_fwd_h in one sweep, for the scalar-gate and
+ * no-gate families (gate_mode 0 / 1; raw k, scalar beta [B,T,H] fp32, Akk fp32 [B,T,H,64]).
+ * Replaces FLA recompute_w_u_fwd(k, v, beta, A, g) -> (w, u) followed by
+ * chunk_gated_delta_rule_fwd_h(k, w, u, g, initial_state) -> (h, v_new, final), as called
+ * at reference backends/backward.py:110-118.  Writes w (bf16 [B,T,H,K], for the backward
+ * state pass), h, v_new and ht exactly as that pair writes them (w and u are formed with
+ * fdr_prepare_wu's products and roundings, bit for bit); u is never written.
+ * Other arguments as for fdr_fwd_h.
+ */
+hipError_t fdr_fwd_h_wy(const void* k, const void* v, const float* beta, const float* Akk, const float* g,
+                        int gate_mode, const float* h0, void* w, void* h, void* v_new, float* ht, int state_v_first,
+                        int B, int T, int H, int k_heads, int K, int V, int chunk, int value_block,
+                        hipStream_t stream);
+
+/* fdr_fwd_h_wy over a variable-length batch: packing, chunk_offsets and cu_seqlens as for
+ * fdr_fwd_h_varlen (FLA recompute_w_u_fwd + chunk_gated_delta_rule_fwd_h with cu_seqlens). */
+hipError_t fdr_fwd_h_wy_varlen(const void* k, const void* v, const float* beta, const float* Akk, const float* g,
+                               int gate_mode, const float* h0, void* w, void* h, void* v_new, float* ht,
+                               int state_v_first, const int* chunk_offsets, const int* cu_seqlens, int N,
+                               int num_chunks, int H, int k_heads, int K, int V, int chunk, int value_block,
+                               hipStream_t stream);
+
+/*
  * Standalone matrix intra (the intra-chunk VJP of a vector-gated chunk), in place.
  * Replaces the reference's kernel-level seam chunk_<op>_bwd_intra
  * (q, k, g, beta, dAqk, dAkk, dq, dk, db, dg) -> (dq, dk, db, dg):

@@ -205,11 +205,20 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
     beta = _f32(beta)
     gate = ops.GATE_SCALAR if op == "gdn" else ops.GATE_NONE
     affine = vl is None and q.shape[2] == v.shape[2] and ops.affine_pays(v)
-    # the direct state recurrence forms Aqk itself from the raw q / k it stages: fdr_prepare_wu
-    # then writes only w and u
+    # the direct state recurrence forms Aqk itself from the raw q / k it stages; w and u are then
+    # formed inside the forward scan's sweep (fdr_fwd_h_wy: u never leaves the chip)
     inline = not affine and (vl is not None or ops.state_form(q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK)
                              == "direct")
-    pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, q=q, want_aqk=not inline, scale=scale, varlen=vl)
+    if inline:
+        w, h, v_new, _ = ops.fwd_h_wy(k, v, A, g, gate, beta, h0=_f32(initial_state), varlen=vl,
+                                      state_v_first=state_v_first)
+        dh, dR, dh0 = ops.state_bwd(q, k, w, g, gate, do, scale, dht=_f32(dht), want_dh0=initial_state is not None,
+                                    method="direct", varlen=vl, state_v_first=state_v_first)
+        out = _group_sum(ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta,
+                                       beta_sigmoid=beta_sigmoid, varlen=vl), q.shape[2])
+        record(op, "optimized_backward")
+        return out, dh0
+    pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, q=q, want_aqk=True, scale=scale, varlen=vl)
     if affine:
         # few heads: both recurrences side by side in affine-step form
         h, v_new, dh, dR, dh0 = ops.recurrences(q, k, pre["w"], pre["u"], g, gate, do, scale, aqk=pre["Aqk"],
@@ -219,9 +228,8 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
         h, v_new, _ = ops.fwd_h(k, pre["w"], pre["u"], g, gate, h0=_f32(initial_state), method="direct",
                                 varlen=vl, state_v_first=state_v_first)
         dh, dR, dh0 = ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
-                                    want_dh0=initial_state is not None,
-                                    method="direct" if inline or vl is not None else "auto",
-                                    varlen=vl, state_v_first=state_v_first)
+                                    want_dh0=initial_state is not None, method="auto", varlen=vl,
+                                    state_v_first=state_v_first)
     out = _group_sum(ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta,
                                    beta_sigmoid=beta_sigmoid, varlen=vl), q.shape[2])
     record(op, "optimized_backward")

@@ -484,6 +484,298 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
   }
 }
 
+// ------------------------------------------------------------------------------------------
+// fdr_fwd_h_wy: fdr_prepare_wu's w / u folded into the fdr_fwd_h sweep (scalar / no gate)
+// ------------------------------------------------------------------------------------------
+// Each (batch, head, value tile) work-group forms, per chunk, w^T = E^T A^T (E = beta k 2^g,
+// every k row) and u^T = Z^T A^T (Z = beta v, its own value tile) with the MFMA sequence of
+// prepare_wu_kernel, so w and u are the bits that kernel writes; u stays in LDS and w is
+// written once (each value tile stores 64 / NVT of its rows) for the backward's state pass.
+// A chunk's w / u do not depend on the state: the extra products sit beside the scan's
+// dependent chain, and the launch replaces two (u written and read back, k read twice).
+template <int BV>
+struct FwdWySmem {
+  static constexpr int LDK = KD + 8;
+  static constexpr int LDT = C + 8;
+  bf16 w[C][LDK];          // w rows, formed here: A operand of w h, stored from here
+  bf16 e[C * KD];          // E = beta k 2^g rows (swizzled): read transposed for w^T = E^T A^T
+  bf16 k[C * KD];          // kg rows (swizzled): A operand of kg^T v_new
+  bf16 hT[BV][LDK];        // h^T: B operand of w h
+  bf16 vT[BV][LDT];        // v_new^T: B operand of kg^T v_new
+  bf16 z[C * BV];          // Z = beta v rows of this value tile (swizzled)
+  bf16 u[C * BV];          // u rows (swizzled): read transposed in the accumulator layout
+  bf16 ah[C][LDT];         // A rows, bf16 hi and lo
+  bf16 al[C][LDT];
+  float lam[KD];
+};
+
+template <int BV, int GATE, bool MAP>
+__global__ __launch_bounds__(512) void fwd_h_wy_kernel(
+    const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ beta,
+    const float* __restrict__ akk, const float* __restrict__ g, const float* __restrict__ h0,
+    bf16* __restrict__ w_out, bf16* __restrict__ h_out, bf16* __restrict__ vnew_out, float* __restrict__ ht_out,
+    int T, int H, const int* __restrict__ chunk_off, int vf, int HQ, const int* __restrict__ cu) {
+  static_assert(GATE != RG_VECTOR, "vector gates keep fdr_prepare_wu (qg / kg)");
+  using S = FwdWySmem<BV>;
+  __shared__ S sm;
+  constexpr int NVT = VD / BV;
+  constexpr int NCT = BV / 16;
+  constexpr int NTH = 512;
+  const int logical = xcd_logical_block();
+  const int vt = logical % NVT;
+  const int bh = logical / NVT;
+  const int b = bh / H, h = bh % H;
+  const int c0 = chunk_off ? min(max(chunk_off[b], 0), T / C) : b * (T / C);
+  const int NT = chunk_off ? max(min(chunk_off[b + 1], T / C) - c0, 0) : T / C;
+  const int tid = threadIdx.x, l = lane_id(), wv = wave_id();
+  const int lc = l & 15, lg = l >> 4;
+  const int v_base = vt * BV;
+  const size_t rsk = (size_t)H * KD, rsv = (size_t)H * VD;
+
+  // state rows [16 wv, 16 wv + 16)
+  f32x4 st[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    f32x4 a = zero4();
+    if (h0) {
+      const float* src = h0 + (size_t)bh * KD * VD;     // [K,V] or, state_v_first (vf), [V,K]
+      const int col = v_base + 16 * ct + lc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kr = 16 * wv + 4 * lg + r;
+        a[r] = src[vf ? col * KD + kr : kr * VD + col];
+      }
+    }
+    st[ct] = a;
+  }
+  constexpr int DCT = NCT >= 2 ? NCT / 2 : 1;
+  const int drow = wv & 3;
+  const int dct0 = DCT * (wv >> 2);
+  const bool has_dr = dct0 < NCT;
+
+  // the next chunk's operands: 2 pieces of 8 k columns, 2 of 4 A columns, the value tile's
+  // v pieces, and the gate / beta of each piece's row
+  constexpr int CHV = BV / 8;
+  constexpr int NPU = C * CHV;
+  constexpr int NU = (NPU + NTH - 1) / NTH;
+  u32x4 rk[2], rv[NU];
+  f32x4 ra[2];
+  float rg_last = 0.f, rg_tok[2] = {0.f, 0.f}, rb_tok[2], rb_v[NU];
+  auto load_chunk = [&](int c) {
+    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+    const size_t tok0 = rs_.tok0;
+    if constexpr (GATE == RG_SCALAR) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) rg_tok[i] = g[(tok0 + rs_.clamp((tid + NTH * i) >> 4)) * H + h];
+      rg_last = g[(tok0 + rs_.clamp(C - 1)) * H + h];
+    }
+    const QKRows kr_ = qk_rows(tok0, h, H, HQ);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + NTH * i, t = p >> 4;
+      rb_tok[i] = *rs_.src(beta + (tok0 + t) * H + h, t);
+      rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + kr_.ofs + (size_t)t * kr_.rs + (p & 15) * 8, t));
+      ra[i] = *reinterpret_cast<const f32x4*>(rs_.src(akk + ((tok0 + t) * H + h) * C + 4 * (p & 15), t));
+    }
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+      const int p = min(tid + NTH * i, NPU - 1), t = p / CHV;
+      rb_v[i] = *rs_.src(beta + (tok0 + t) * H + h, t);
+      rv[i] = *reinterpret_cast<const u32x4*>(rs_.src(v + (tok0 + t) * rsv + (size_t)h * VD + v_base + (p % CHV) * 8, t));
+    }
+  };
+  auto stage_chunk = [&]() {
+    if (tid < KD) sm.lam[tid] = GATE == RG_SCALAR ? fast_exp2(rg_last) : 1.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = tid + NTH * i;
+      const int t = p >> 4, ch = p & 15;
+      // E = (beta k) 2^g, rounded as prepare_wu_kernel rounds it; kg = k 2^(g_last - g)
+      const float ge = GATE == RG_SCALAR ? fast_exp2(rg_tok[i]) : 1.f;
+      const bf16x8 kx = __builtin_bit_cast(bf16x8, rk[i]);
+      bf16x8 eh;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) eh[j] = to_bf16(rb_tok[i] * to_f32(kx[j]) * ge);
+      store_tr_chunk<16>(sm.e, t, ch, __builtin_bit_cast(u32x4, eh));
+      u32x4 kq = rk[i];
+      if constexpr (GATE == RG_SCALAR) kq = scale_bf16x8(kq, fast_exp2(rg_last - rg_tok[i]));
+      store_tr_chunk<16>(sm.k, t, ch, kq);
+      bf16x4 alo;
+      const bf16x4 ahi = split_hi4(ra[i], alo);
+      *reinterpret_cast<bf16x4*>(&sm.ah[t][4 * ch]) = ahi;
+      *reinterpret_cast<bf16x4*>(&sm.al[t][4 * ch]) = alo;
+    }
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+      const int p = tid + NTH * i;
+      if (NPU % NTH == 0 || p < NPU) {
+        const bf16x8 vx = __builtin_bit_cast(bf16x8, rv[i]);
+        bf16x8 zh;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) zh[j] = to_bf16(rb_v[i] * to_f32(vx[j]));
+        store_tr_chunk<CHV>(sm.z, p / CHV, p % CHV, __builtin_bit_cast(u32x4, zh));
+      }
+    }
+  };
+  auto settle_chunk = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      settle(rk[i]);
+      settle(ra[i]);
+      settle(rb_tok[i]);
+      settle(rg_tok[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+      settle(rv[i]);
+      settle(rb_v[i]);
+    }
+    settle(rg_last);
+  };
+  if (NT > 0) {
+    load_chunk(0);
+    settle_chunk();
+  }
+  for (int c = 0; c < NT; ++c) {
+    lds_barrier();
+    stage_chunk();
+    load_chunk(c + 1 < NT ? c + 1 : c);    // (the last chunk re-fetches itself: no branch)
+    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+    const size_t tok0 = rs_.tok0;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      bf16x4 v4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[ct][r]);
+      *reinterpret_cast<bf16x4*>(&sm.hT[16 * ct + lc][16 * wv + 4 * lg]) = v4;
+    }
+    lds_barrier();
+    // w^T = E^T A^T: wave wv, k rows [16 wv, 16 wv + 16), all 64 tokens -> w rows in LDS
+    {
+      const int row0 = 16 * wv;
+      const bf16x8 x0 = frag_tr<16>(sm.e, 0, row0);
+      const bf16x8 x1 = frag_tr<16>(sm.e, 32, row0);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        f32x4 acc = zero4();
+        acc = mfma(x0, frag(&sm.ah[16 * tt][0], S::LDT), acc);
+        acc = mfma(x0, frag(&sm.al[16 * tt][0], S::LDT), acc);
+        acc = mfma(x1, frag(&sm.ah[16 * tt][32], S::LDT), acc);
+        acc = mfma(x1, frag(&sm.al[16 * tt][32], S::LDT), acc);
+        bf16x4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = to_bf16(acc[r]);
+        *reinterpret_cast<bf16x4*>(&sm.w[16 * tt + lc][row0 + 4 * lg]) = o;
+      }
+    }
+    // u^T = Z^T A^T of this value tile: (value row tile, token tile) pairs over the waves
+#pragma unroll
+    for (int ut = wv; ut < NCT * 4; ut += 8) {
+      const int rt = ut % NCT, tt = ut / NCT;
+      const bf16x8 x0 = frag_tr<CHV>(sm.z, 0, 16 * rt);
+      const bf16x8 x1 = frag_tr<CHV>(sm.z, 32, 16 * rt);
+      f32x4 acc = zero4();
+      acc = mfma(x0, frag(&sm.ah[16 * tt][0], S::LDT), acc);
+      acc = mfma(x0, frag(&sm.al[16 * tt][0], S::LDT), acc);
+      acc = mfma(x1, frag(&sm.ah[16 * tt][32], S::LDT), acc);
+      acc = mfma(x1, frag(&sm.al[16 * tt][32], S::LDT), acc);
+      bf16x4 o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = to_bf16(acc[r]);
+      *reinterpret_cast<bf16x4*>(sm.u + tr_off<CHV>(16 * tt + lc, 16 * rt + 4 * lg)) = o;
+    }
+    lds_barrier();
+    // w rows [64 vt / NVT, ...) of this chunk to HBM, 16-byte pieces (every lane stores:
+    // pieces beyond the share are written twice, with the same data)
+    {
+      constexpr int RW = C / NVT, NWP = RW * (KD / 8);
+#pragma unroll
+      for (int i = 0; i < (NWP + NTH - 1) / NTH; ++i) {
+        const int p = (tid + NTH * i) % NWP;
+        const int t = vt * RW + p / (KD / 8), c8 = 8 * (p % (KD / 8));
+        *reinterpret_cast<u32x4*>(rs_.dst(w_out + (tok0 + t) * rsk + (size_t)h * KD + c8, t)) =
+            *reinterpret_cast<const u32x4*>(&sm.w[t][c8]);
+      }
+    }
+    // v_new tiles = u - w h
+    if (has_dr) {
+#pragma unroll
+      for (int cc = 0; cc < DCT; ++cc) {
+        const int ct = dct0 + cc;
+        const bf16x4 u4 = ds_read_tr4(sm.u + tr_off<CHV>(16 * drow + 4 * lg + (lc >> 2), 16 * ct + 4 * (lc & 3)));
+        f32x4 a;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a[r] = -to_f32(u4[r]);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          a = mfma(frag(&sm.w[16 * drow][32 * ks], S::LDK), frag(&sm.hT[16 * ct][32 * ks], S::LDK), a);
+        bf16x4 v4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v4[r] = to_bf16(-a[r]);
+        *reinterpret_cast<bf16x4*>(&sm.vT[16 * ct + lc][16 * drow + 4 * lg]) = v4;
+      }
+    }
+    lds_barrier();
+    // h <- lambda h + kg^T v_new
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      f32x4 a;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) a[r] = st[ct][r] * sm.lam[16 * wv + 4 * lg + r];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        a = mfma(frag_tr<16>(sm.k, 32 * ks, 16 * wv), frag(&sm.vT[16 * ct][32 * ks], S::LDT), a);
+      st[ct] = a;
+    }
+    {
+      const size_t hb = ((size_t)(c0 + c) * H + h) * KD * VD;
+      constexpr int NP = KD * BV / 8, NR = C * BV / 8;
+#pragma unroll
+      for (int i = 0; i < (NP + NTH - 1) / NTH; ++i) {
+        const int p = (tid + NTH * i) % NP;
+        const int kr = p % KD, v0 = (p / KD) * 8;
+        bf16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = sm.hT[v0 + j][kr];
+        *reinterpret_cast<bf16x8*>(h_out + hb + (size_t)kr * VD + v_base + v0) = o;
+      }
+#pragma unroll
+      for (int i = 0; i < (NR + NTH - 1) / NTH; ++i) {
+        const int p = (tid + NTH * i) % NR;
+        const int t = p % C, v0 = (p / C) * 8;
+        bf16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = sm.vT[v0 + j][t];
+        *reinterpret_cast<bf16x8*>(rs_.dst(vnew_out + (tok0 + t) * rsv + (size_t)h * VD + v_base + v0, t)) = o;
+      }
+    }
+    settle_chunk();
+  }
+  if (ht_out) {
+    float* dst = ht_out + (size_t)bh * KD * VD;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kr = 16 * wv + 4 * lg + r, col = v_base + 16 * ct + lc;
+        dst[vf ? col * KD + kr : kr * VD + col] = st[ct][r];
+      }
+  }
+}
+
+template <int BV, int GATE>
+static hipError_t launch_fwd_h_wy(const void* k, const void* v, const float* beta, const float* akk, const float* g,
+                                  const float* h0, void* w, void* h, void* vnew, float* ht, int B, int T, int H,
+                                  hipStream_t s, const int* co, int vf, int HQ, const int* cu) {
+#define FW_LAUNCH(MAP)                                                                                           \
+  hipLaunchKernelGGL((fwd_h_wy_kernel<BV, GATE, MAP>), dim3(B * H * (VD / BV)), dim3(512), 0, s, (const bf16*)k, \
+                     (const bf16*)v, beta, akk, g, h0, (bf16*)w, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf, HQ, cu)
+  if (cu) FW_LAUNCH(true);
+  else FW_LAUNCH(false);
+#undef FW_LAUNCH
+  return hipGetLastError();
+}
+
 template <int GATE, bool VEC_B, bool QKG, bool AQK>
 static hipError_t launch_prepare(const void* q, const void* k, const void* v, const float* g,
                                  const float* beta, const void* bg, const void* wg, const float* akk,
@@ -627,4 +919,49 @@ extern "C" hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void*
   if (!chunk_offsets || num_chunks <= 0) return hipErrorInvalidValue;
   return fwd_h_dispatch(k, w, u, g, gate_mode, h0, h, v_new, ht, N, num_chunks * C, H, k_heads, K, V, chunk,
                         value_block, stream, chunk_offsets, state_v_first ? 1 : 0, cu_seqlens);
+}
+
+// B rows of T tokens, or (co[, cu]) B sequences packed along T tokens as for fwd_h_dispatch
+static hipError_t fwd_h_wy_dispatch(const void* k, const void* v, const float* beta, const float* Akk,
+                                    const float* g, int gate_mode, const float* h0, void* w, void* h, void* v_new,
+                                    float* ht, int B, int T, int H, int HQ, int K, int V, int chunk,
+                                    int value_block, hipStream_t stream, const int* co, int vf, const int* cu) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  if (HQ <= 0) HQ = H;
+  if (H % HQ) return hipErrorInvalidValue;
+  if (!k || !v || !beta || !Akk || !w || !h || !v_new) return hipErrorInvalidValue;
+  if (gate_mode != RG_NONE && gate_mode != RG_SCALAR) return hipErrorInvalidValue;
+  if (gate_mode == RG_SCALAR && !g) return hipErrorInvalidValue;
+  if (cu && !co) return hipErrorInvalidValue;
+  const int bv = value_block > 0 ? value_block : fwd_default_bv(B, H);
+#define FW_ARGS k, v, beta, Akk, g, h0, w, h, v_new, ht, B, T, H, stream, co, vf, HQ, cu
+#define FW_BV(G)                                                    \
+  switch (bv) {                                                     \
+    case 16: return launch_fwd_h_wy<16, G>(FW_ARGS);                \
+    case 32: return launch_fwd_h_wy<32, G>(FW_ARGS);                \
+    case 64: return launch_fwd_h_wy<64, G>(FW_ARGS);                \
+    default: return hipErrorInvalidValue;                           \
+  }
+  if (gate_mode == RG_SCALAR) FW_BV(RG_SCALAR)
+  FW_BV(RG_NONE)
+#undef FW_BV
+#undef FW_ARGS
+}
+
+extern "C" hipError_t fdr_fwd_h_wy(const void* k, const void* v, const float* beta, const float* Akk, const float* g,
+                                   int gate_mode, const float* h0, void* w, void* h, void* v_new, float* ht,
+                                   int state_v_first, int B, int T, int H, int k_heads, int K, int V, int chunk,
+                                   int value_block, hipStream_t stream) {
+  return fwd_h_wy_dispatch(k, v, beta, Akk, g, gate_mode, h0, w, h, v_new, ht, B, T, H, k_heads, K, V, chunk,
+                           value_block, stream, nullptr, state_v_first ? 1 : 0, nullptr);
+}
+
+extern "C" hipError_t fdr_fwd_h_wy_varlen(const void* k, const void* v, const float* beta, const float* Akk,
+                                          const float* g, int gate_mode, const float* h0, void* w, void* h,
+                                          void* v_new, float* ht, int state_v_first, const int* chunk_offsets,
+                                          const int* cu_seqlens, int N, int num_chunks, int H, int k_heads, int K,
+                                          int V, int chunk, int value_block, hipStream_t stream) {
+  if (!chunk_offsets || num_chunks <= 0) return hipErrorInvalidValue;
+  return fwd_h_wy_dispatch(k, v, beta, Akk, g, gate_mode, h0, w, h, v_new, ht, N, num_chunks * C, H, k_heads, K, V,
+                           chunk, value_block, stream, chunk_offsets, state_v_first ? 1 : 0, cu_seqlens);
 }

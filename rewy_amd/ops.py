@@ -641,6 +641,51 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
     return h, vnew, ht
 
 
+def fwd_h_wy(k, v, Akk, g, gate_mode, beta, h0=None, want_final=False, value_block=0, state_v_first=False,
+             varlen=None):
+    """``prepare_wu`` (w, u) and the direct ``fwd_h`` in one sweep (scalar / no gate: raw k,
+    scalar beta).  Returns (w [B,T,H,K] bf16, h, v_new, final|None) with the bits of that pair;
+    u is not materialized.  ``varlen`` as for ``fwd_h`` (h0 / final per sequence)."""
+    if gate_mode not in (GATE_NONE, GATE_SCALAR):
+        raise ValueError("fwd_h_wy takes the scalar / no-gate families (gate_mode 0 or 1)")
+    B, T, HQ, K = _rows(k, varlen)
+    H, HQ = _group(v.shape[2] if v.ndim == 4 else HQ, HQ)
+    V = V_SUPPORTED
+    dev = k.device
+    bf, f32 = torch.bfloat16, torch.float32
+    _need(k, "k", bf, (B, T, HQ, K), dev)
+    _need(v, "v", bf, (B, T, H, V), dev)
+    _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
+    _need(beta, "beta", f32, (B, T, H), dev)
+    if gate_mode == GATE_SCALAR:
+        _need(g, "g", f32, (B, T, H), dev)
+    if varlen is not None:
+        co, N, NT = varlen.chunk_offsets, varlen.N, varlen.NC
+    else:
+        co, N, NT = None, B, T // CHUNK
+    if h0 is not None:
+        _need(h0, "h0", f32, (N, H, K, V), dev)
+    if value_block not in (0, 16, 32, 64):
+        raise ValueError("value_block must be 0, 16, 32 or 64")
+    vf = int(bool(state_v_first))
+    w = torch.empty(B, T, H, K, device=dev, dtype=bf)
+    h = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
+    vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
+    ht = torch.empty(N, H, K, V, device=dev, dtype=f32) if want_final else None
+    P = _lib.ptr
+    if co is not None:
+        cu = _mapped(varlen)
+        st = _lib.load().fdr_fwd_h_wy_varlen(P(k), P(v), P(beta), P(Akk), P(g), int(gate_mode), P(h0), P(w), P(h),
+                                             P(vnew), P(ht), vf, P(co), None if cu is None else P(cu.cu_seqlens),
+                                             N, NT, H, HQ, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
+        _lib.check(st, "fdr_fwd_h_wy_varlen")
+    else:
+        st = _lib.load().fdr_fwd_h_wy(P(k), P(v), P(beta), P(Akk), P(g), int(gate_mode), P(h0), P(w), P(h), P(vnew),
+                                      P(ht), vf, B, T, H, HQ, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
+        _lib.check(st, "fdr_fwd_h_wy")
+    return w, h, vnew, ht
+
+
 def matrix_intra(q, k, g, dAqk, dAkk, dq, dk, db, dg, beta=None, b=None, beta_complete=False):
     """Matrix intra VJP added in place into fp32 (dq, dk, db, dg); returns them."""
     B, T, HQ, K = _dims(q)

@@ -31,10 +31,10 @@ def test_kernel_costs_match_the_quoted_figures():
     # the affine-step launches are costed as the recurrences they replace
     assert gdn["affine_recurrences"] == tuple(a + b for a, b in zip(gdn["fdr_fwd_h"], gdn["fdr_state_bwd"]))
     assert kda["affine_state"] == kda["fdr_state_bwd"]
-    # Aqk formed in the state recurrence: prepare_wu drops the q read and the Aqk write, the
-    # state kernel the Aqk read (and computes q k^T)
+    # Aqk formed in the state recurrence (no Aqk read; q k^T computed there), w / u in the
+    # forward scan's sweep: k, v, Akk, g, beta read, w, h, v_new written
     inl = bench.kernel_costs("gdn", False, inline=True)
-    assert inl["fdr_prepare_wu"][0] == gdn["fdr_prepare_wu"][0] - bench.TILE - bench.AT
+    assert inl["fdr_fwd_h_wy"][0] == 115_200
     assert inl["fdr_state_bwd"][0] == gdn["fdr_state_bwd"][0] - bench.AT
     assert inl["fdr_state_bwd"][1] == gdn["fdr_state_bwd"][1] + 2 * 64 * 64 * 128
     assert bench.inline_aqk(bench.CONFIGS["gdn"]) and not bench.inline_aqk(bench.CONFIGS["kda"])
