@@ -491,22 +491,22 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
 // every k row) and u^T = Z^T A^T (Z = beta v, its own value tile) with the MFMA sequence of
 // prepare_wu_kernel, so w and u are the bits that kernel writes; u stays in LDS and w is
 // written once (each value tile stores 64 / NVT of its rows) for the backward's state pass.
-// A chunk's w / u do not depend on the state: the extra products sit beside the scan's
-// dependent chain, and the launch replaces two (u written and read back, k read twice).
+// A chunk's w / u do not depend on the state: they are formed one chunk ahead, beside the
+// scan's dependent chain, and the launch replaces two (u written and read back, k read twice).
 template <int BV>
 struct FwdWySmem {
   static constexpr int LDK = KD + 8;
   static constexpr int LDT = C + 8;
-  bf16 w[C][LDK];          // w rows, formed here: A operand of w h, stored from here
-  bf16 e[C * KD];          // E = beta k 2^g rows (swizzled): read transposed for w^T = E^T A^T
-  bf16 k[C * KD];          // kg rows (swizzled): A operand of kg^T v_new
+  bf16 w[2][C][LDK];       // w rows of chunks c, c + 1 (by parity): A operand of w h, stored from here
+  bf16 u[2][C * BV];       // u rows (swizzled), chunks c, c + 1: read transposed in the accumulator layout
+  bf16 k[2][C * KD];       // kg rows (swizzled), chunks c, c + 1: A operand of kg^T v_new
+  bf16 e[C * KD];          // E = beta k 2^g rows of chunk c + 1 (swizzled): w^T = E^T A^T
   bf16 hT[BV][LDK];        // h^T: B operand of w h
   bf16 vT[BV][LDT];        // v_new^T: B operand of kg^T v_new
-  bf16 z[C * BV];          // Z = beta v rows of this value tile (swizzled)
-  bf16 u[C * BV];          // u rows (swizzled): read transposed in the accumulator layout
-  bf16 ah[C][LDT];         // A rows, bf16 hi and lo
+  bf16 z[C * BV];          // Z = beta v rows of chunk c + 1, this value tile (swizzled)
+  bf16 ah[C][LDT];         // A rows of chunk c + 1, bf16 hi and lo
   bf16 al[C][LDT];
-  float lam[KD];
+  float lam[2][KD];
 };
 
 template <int BV, int GATE, bool MAP>
@@ -553,8 +553,11 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
   const int dct0 = DCT * (wv >> 2);
   const bool has_dr = dct0 < NCT;
 
-  // the next chunk's operands: 2 pieces of 8 k columns, 2 of 4 A columns, the value tile's
-  // v pieces, and the gate / beta of each piece's row
+  // Pipeline: step c stages chunk c + 1 and forms its w / u after chunk c's state update
+  // (those products beside the update and the stores, off the scan's dependent chain);
+  // w, u, kg and lambda are double-buffered by chunk parity.  Registers: chunk c + 1's
+  // operands, loaded one step ahead -- 2 pieces of 8 k columns, 2 of 4 A columns, the value
+  // tile's v pieces, the gate / beta of each piece's row.
   constexpr int CHV = BV / 8;
   constexpr int NPU = C * CHV;
   constexpr int NU = (NPU + NTH - 1) / NTH;
@@ -584,8 +587,9 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       rv[i] = *reinterpret_cast<const u32x4*>(rs_.src(v + (tok0 + t) * rsv + (size_t)h * VD + v_base + (p % CHV) * 8, t));
     }
   };
-  auto stage_chunk = [&]() {
-    if (tid < KD) sm.lam[tid] = GATE == RG_SCALAR ? fast_exp2(rg_last) : 1.f;
+  // the registers' chunk into LDS: E, Z, A (hi / lo) for its w / u, kg and lambda into buffer `pb`
+  auto stage_chunk = [&](int pb) {
+    if (tid < KD) sm.lam[pb][tid] = GATE == RG_SCALAR ? fast_exp2(rg_last) : 1.f;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
@@ -599,7 +603,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       store_tr_chunk<16>(sm.e, t, ch, __builtin_bit_cast(u32x4, eh));
       u32x4 kq = rk[i];
       if constexpr (GATE == RG_SCALAR) kq = scale_bf16x8(kq, fast_exp2(rg_last - rg_tok[i]));
-      store_tr_chunk<16>(sm.k, t, ch, kq);
+      store_tr_chunk<16>(sm.k[pb], t, ch, kq);
       bf16x4 alo;
       const bf16x4 ahi = split_hi4(ra[i], alo);
       *reinterpret_cast<bf16x4*>(&sm.ah[t][4 * ch]) = ahi;
@@ -615,6 +619,42 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
         for (int j = 0; j < 8; ++j) zh[j] = to_bf16(rb_v[i] * to_f32(vx[j]));
         store_tr_chunk<CHV>(sm.z, p / CHV, p % CHV, __builtin_bit_cast(u32x4, zh));
       }
+    }
+  };
+  // w^T = E^T A^T (wave wv: k rows [16 wv, 16 wv + 16), all 64 tokens) and u^T = Z^T A^T
+  // ((value row tile, token tile) pairs over the waves) of the staged chunk, into buffer `pb`
+  auto form_wu = [&](int pb) {
+    {
+      const int row0 = 16 * wv;
+      const bf16x8 x0 = frag_tr<16>(sm.e, 0, row0);
+      const bf16x8 x1 = frag_tr<16>(sm.e, 32, row0);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        f32x4 acc = zero4();
+        acc = mfma(x0, frag(&sm.ah[16 * tt][0], S::LDT), acc);
+        acc = mfma(x0, frag(&sm.al[16 * tt][0], S::LDT), acc);
+        acc = mfma(x1, frag(&sm.ah[16 * tt][32], S::LDT), acc);
+        acc = mfma(x1, frag(&sm.al[16 * tt][32], S::LDT), acc);
+        bf16x4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = to_bf16(acc[r]);
+        *reinterpret_cast<bf16x4*>(&sm.w[pb][16 * tt + lc][row0 + 4 * lg]) = o;
+      }
+    }
+#pragma unroll
+    for (int ut = wv; ut < NCT * 4; ut += 8) {
+      const int rt = ut % NCT, tt = ut / NCT;
+      const bf16x8 x0 = frag_tr<CHV>(sm.z, 0, 16 * rt);
+      const bf16x8 x1 = frag_tr<CHV>(sm.z, 32, 16 * rt);
+      f32x4 acc = zero4();
+      acc = mfma(x0, frag(&sm.ah[16 * tt][0], S::LDT), acc);
+      acc = mfma(x0, frag(&sm.al[16 * tt][0], S::LDT), acc);
+      acc = mfma(x1, frag(&sm.ah[16 * tt][32], S::LDT), acc);
+      acc = mfma(x1, frag(&sm.al[16 * tt][32], S::LDT), acc);
+      bf16x4 o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = to_bf16(acc[r]);
+      *reinterpret_cast<bf16x4*>(sm.u[pb] + tr_off<CHV>(16 * tt + lc, 16 * rt + 4 * lg)) = o;
     }
   };
   auto settle_chunk = [&]() {
@@ -635,13 +675,16 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
   if (NT > 0) {
     load_chunk(0);
     settle_chunk();
+    stage_chunk(0);
+    load_chunk(NT > 1 ? 1 : 0);
+    lds_barrier();
+    form_wu(0);
+    settle_chunk();
   }
   for (int c = 0; c < NT; ++c) {
+    const int pb = c & 1;
     lds_barrier();
-    stage_chunk();
-    load_chunk(c + 1 < NT ? c + 1 : c);    // (the last chunk re-fetches itself: no branch)
-    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
-    const size_t tok0 = rs_.tok0;
+    // h_c -> LDS (transposed, bf16); the same rounded values feed w h, as stored
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
       bf16x4 v4;
@@ -649,44 +692,13 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[ct][r]);
       *reinterpret_cast<bf16x4*>(&sm.hT[16 * ct + lc][16 * wv + 4 * lg]) = v4;
     }
+    stage_chunk(pb ^ 1);                     // chunk c + 1 (the last step stages itself again: no branch)
+    load_chunk(c + 2 < NT ? c + 2 : NT - 1);
+    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+    const size_t tok0 = rs_.tok0;
     lds_barrier();
-    // w^T = E^T A^T: wave wv, k rows [16 wv, 16 wv + 16), all 64 tokens -> w rows in LDS
-    {
-      const int row0 = 16 * wv;
-      const bf16x8 x0 = frag_tr<16>(sm.e, 0, row0);
-      const bf16x8 x1 = frag_tr<16>(sm.e, 32, row0);
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        f32x4 acc = zero4();
-        acc = mfma(x0, frag(&sm.ah[16 * tt][0], S::LDT), acc);
-        acc = mfma(x0, frag(&sm.al[16 * tt][0], S::LDT), acc);
-        acc = mfma(x1, frag(&sm.ah[16 * tt][32], S::LDT), acc);
-        acc = mfma(x1, frag(&sm.al[16 * tt][32], S::LDT), acc);
-        bf16x4 o;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = to_bf16(acc[r]);
-        *reinterpret_cast<bf16x4*>(&sm.w[16 * tt + lc][row0 + 4 * lg]) = o;
-      }
-    }
-    // u^T = Z^T A^T of this value tile: (value row tile, token tile) pairs over the waves
-#pragma unroll
-    for (int ut = wv; ut < NCT * 4; ut += 8) {
-      const int rt = ut % NCT, tt = ut / NCT;
-      const bf16x8 x0 = frag_tr<CHV>(sm.z, 0, 16 * rt);
-      const bf16x8 x1 = frag_tr<CHV>(sm.z, 32, 16 * rt);
-      f32x4 acc = zero4();
-      acc = mfma(x0, frag(&sm.ah[16 * tt][0], S::LDT), acc);
-      acc = mfma(x0, frag(&sm.al[16 * tt][0], S::LDT), acc);
-      acc = mfma(x1, frag(&sm.ah[16 * tt][32], S::LDT), acc);
-      acc = mfma(x1, frag(&sm.al[16 * tt][32], S::LDT), acc);
-      bf16x4 o;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = to_bf16(acc[r]);
-      *reinterpret_cast<bf16x4*>(sm.u + tr_off<CHV>(16 * tt + lc, 16 * rt + 4 * lg)) = o;
-    }
-    lds_barrier();
-    // w rows [64 vt / NVT, ...) of this chunk to HBM, 16-byte pieces (every lane stores:
-    // pieces beyond the share are written twice, with the same data)
+    // w rows [64 vt / NVT, ...) of chunk c to HBM, 16-byte pieces (every lane stores: pieces
+    // beyond the share are written twice, with the same data)
     {
       constexpr int RW = C / NVT, NWP = RW * (KD / 8);
 #pragma unroll
@@ -694,7 +706,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
         const int p = (tid + NTH * i) % NWP;
         const int t = vt * RW + p / (KD / 8), c8 = 8 * (p % (KD / 8));
         *reinterpret_cast<u32x4*>(rs_.dst(w_out + (tok0 + t) * rsk + (size_t)h * KD + c8, t)) =
-            *reinterpret_cast<const u32x4*>(&sm.w[t][c8]);
+            *reinterpret_cast<const u32x4*>(&sm.w[pb][t][c8]);
       }
     }
     // v_new tiles = u - w h
@@ -702,13 +714,14 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
 #pragma unroll
       for (int cc = 0; cc < DCT; ++cc) {
         const int ct = dct0 + cc;
-        const bf16x4 u4 = ds_read_tr4(sm.u + tr_off<CHV>(16 * drow + 4 * lg + (lc >> 2), 16 * ct + 4 * (lc & 3)));
+        const bf16x4 u4 =
+            ds_read_tr4(sm.u[pb] + tr_off<CHV>(16 * drow + 4 * lg + (lc >> 2), 16 * ct + 4 * (lc & 3)));
         f32x4 a;
 #pragma unroll
         for (int r = 0; r < 4; ++r) a[r] = -to_f32(u4[r]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
-          a = mfma(frag(&sm.w[16 * drow][32 * ks], S::LDK), frag(&sm.hT[16 * ct][32 * ks], S::LDK), a);
+          a = mfma(frag(&sm.w[pb][16 * drow][32 * ks], S::LDK), frag(&sm.hT[16 * ct][32 * ks], S::LDK), a);
         bf16x4 v4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) v4[r] = to_bf16(-a[r]);
@@ -721,12 +734,13 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     for (int ct = 0; ct < NCT; ++ct) {
       f32x4 a;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) a[r] = st[ct][r] * sm.lam[16 * wv + 4 * lg + r];
+      for (int r = 0; r < 4; ++r) a[r] = st[ct][r] * sm.lam[pb][16 * wv + 4 * lg + r];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag_tr<16>(sm.k, 32 * ks, 16 * wv), frag(&sm.vT[16 * ct][32 * ks], S::LDT), a);
+        a = mfma(frag_tr<16>(sm.k[pb], 32 * ks, 16 * wv), frag(&sm.vT[16 * ct][32 * ks], S::LDT), a);
       st[ct] = a;
     }
+    form_wu(pb ^ 1);                         // chunk c + 1's w / u, beside the update and the stores
     {
       const size_t hb = ((size_t)(c0 + c) * H + h) * KD * VD;
       constexpr int NP = KD * BV / 8, NR = C * BV / 8;
