@@ -86,9 +86,10 @@ def kernel_costs(op, full_saving, inline=False):
         wr = 2 * TILE + (2 * TILE if vec else AT)               # w, u, (qg, kg | Aqk)
         costs["fdr_prepare_wu"] = (rd + wr, 2 * mm(64, 128, 64) + (0 if vec else mm(64, 64, 128)))
         costs["fdr_fwd_h"] = (3 * TILE + gl_b + (0 if vec else g_b) + HS + TILE, 2 * mm(64, 128, 128))
-        # w / u formed in the forward scan's sweep: reads k, v, Akk, g, beta; writes w, h, v_new
-        costs["fdr_fwd_h_wy"] = (2 * TILE + AT + g_b + gates_b + TILE + HS + TILE,
-                                 2 * mm(64, 128, 64) + 2 * mm(64, 128, 128))
+        # w / u formed in the forward scan's sweep: reads (q,) k, v, Akk, g, beta|b,w; writes
+        # w, (qg, kg,) h, v_new
+        costs["fdr_fwd_h_wy"] = ((3 if vec else 2) * TILE + AT + g_b + gates_b + TILE + (2 * TILE if vec else 0)
+                                 + HS + TILE, 2 * mm(64, 128, 64) + 2 * mm(64, 128, 128))
     costs["fdr_state_bwd"] = (4 * TILE + (0 if inline else AT) + gl_b + (0 if vec else g_b) + HS + TILE,
                               mm(64, 128, 128) + mm(64, 128, 64) + 2 * mm(128, 128, 64)
                               + (mm(64, 64, 128) if inline else 0))
@@ -195,11 +196,18 @@ def setup(cfg, device):
         qs, ks, ws, aqk, h, v_new = sv["qg"], sv["kg"], sv["w"], sv["Aqk"], sv["h"], sv["v_new"]
     NT = cfg["T"] // 64
     inline = inline_aqk(cfg)
-    if inline:
-        # w / u in the forward scan's sweep (fdr_fwd_h_wy), Aqk in the state recurrence
-        kern["fdr_fwd_h_wy"] = lambda: ops.fwd_h_wy(xs["k"], xs["v"], sv["Akk"], g, gate, xs["beta"], h0=xs["h0"])
-        ws, h, v_new, _ = kern["fdr_fwd_h_wy"]()
-        ks, qs, aqk = xs["k"], xs["q"], None
+    # the recompute policy's direct path (as the backends decide): w / u in the forward scan's
+    # sweep (fdr_fwd_h_wy); for the scalar / no-gate families Aqk in the state recurrence
+    fused = (not keep and not ops.affine_pays(xs["q"])
+             and (inline or (vec and ops.fwd_h_wy_pays(cfg["B"], cfg["H"], gate))))
+    if fused:
+        kern["fdr_fwd_h_wy"] = lambda: ops.fwd_h_wy(xs["k"], xs["v"], sv["Akk"], g, gate, beta=xs.get("beta"),
+                                                    q=xs["q"] if vec else None, b=xs.get("b"), w=xs.get("w"),
+                                                    h0=xs["h0"])
+        sw = kern["fdr_fwd_h_wy"]()
+        ws, h, v_new = sw["w"], sw["h"], sw["v_new"]
+        ks, qs = (sw["kg"], sw["qg"]) if vec else (xs["k"], xs["q"])
+        aqk = sv["Aqk"] if vec else None
     elif not keep:
         kern["fdr_prepare_wu"] = lambda: ops.prepare_wu(
             xs["k"], xs["v"], sv["Akk"], gate, g=g, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"), q=xs["q"],
@@ -223,7 +231,7 @@ def setup(cfg, device):
                                                                  h0=xs["h0"], want_dh0=xs["h0"] is not None)
             h, v_new, dh, dR, _ = kern["affine_recurrences"]()
     else:
-        if not keep and not inline:
+        if not keep and not fused:
             kern["fdr_fwd_h"] = lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"], method="direct")
             h, v_new, _ = kern["fdr_fwd_h"]()
         kern["fdr_state_bwd"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,

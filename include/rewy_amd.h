@@ -234,26 +234,30 @@ hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const f
                             int k_heads, int K, int V, int chunk, int value_block, hipStream_t stream);
 
 /*
- * The recompute pair fdr_prepare_wu + fdr_fwd_h in one sweep, for the scalar-gate and
- * no-gate families (gate_mode 0 / 1; raw k, scalar beta [B,T,H] fp32, Akk fp32 [B,T,H,64]).
- * Replaces FLA recompute_w_u_fwd(k, v, beta, A, g) -> (w, u) followed by
- * chunk_gated_delta_rule_fwd_h(k, w, u, g, initial_state) -> (h, v_new, final), as called
- * at reference backends/backward.py:110-118.  Writes w (bf16 [B,T,H,K], for the backward
- * state pass), h, v_new and ht exactly as that pair writes them (w and u are formed with
- * fdr_prepare_wu's products and roundings, bit for bit); u is never written.
- * Other arguments as for fdr_fwd_h.
+ * The recompute pair fdr_prepare_wu + fdr_fwd_h in one sweep.  Replaces FLA
+ * recompute_w_u_fwd(k, v, beta, A, g) -> (w, u) [, qg, kg] followed by
+ * chunk_gated_delta_rule_fwd_h(k, w, u, g, initial_state) -> (h, v_new, final), as called at
+ * reference backends/backward.py:110-118 (GDN / DeltaNet) and :44-49 (KDA / GDN2 when the
+ * forward did not save its intermediates).  Arguments as for fdr_prepare_wu (raw q / k,
+ * gate_mode 0/1/2, scalar beta or GDN2's b_gate / w_gate, Akk fp32) and fdr_fwd_h (h0, h,
+ * v_new, ht, state_v_first).  Writes w (bf16 [B,T,H,K], for the backward state pass), for
+ * gate_mode 2 qg and kg (bf16 [B,T,H,K]; null otherwise), h, v_new and ht, each exactly as
+ * the pair writes it: w and u are formed with fdr_prepare_wu's products and roundings, bit
+ * for bit.  u is never written.
  */
-hipError_t fdr_fwd_h_wy(const void* k, const void* v, const float* beta, const float* Akk, const float* g,
-                        int gate_mode, const float* h0, void* w, void* h, void* v_new, float* ht, int state_v_first,
-                        int B, int T, int H, int k_heads, int K, int V, int chunk, int value_block,
-                        hipStream_t stream);
+hipError_t fdr_fwd_h_wy(const void* q, const void* k, const void* v, const float* g, int gate_mode,
+                        const float* beta, const void* b_gate, const void* w_gate, const float* Akk,
+                        const float* h0, void* w, void* qg, void* kg, void* h, void* v_new, float* ht,
+                        int state_v_first, int B, int T, int H, int qk_heads, int K, int V, int chunk,
+                        int value_block, hipStream_t stream);
 
 /* fdr_fwd_h_wy over a variable-length batch: packing, chunk_offsets and cu_seqlens as for
  * fdr_fwd_h_varlen (FLA recompute_w_u_fwd + chunk_gated_delta_rule_fwd_h with cu_seqlens). */
-hipError_t fdr_fwd_h_wy_varlen(const void* k, const void* v, const float* beta, const float* Akk, const float* g,
-                               int gate_mode, const float* h0, void* w, void* h, void* v_new, float* ht,
+hipError_t fdr_fwd_h_wy_varlen(const void* q, const void* k, const void* v, const float* g, int gate_mode,
+                               const float* beta, const void* b_gate, const void* w_gate, const float* Akk,
+                               const float* h0, void* w, void* qg, void* kg, void* h, void* v_new, float* ht,
                                int state_v_first, const int* chunk_offsets, const int* cu_seqlens, int N,
-                               int num_chunks, int H, int k_heads, int K, int V, int chunk, int value_block,
+                               int num_chunks, int H, int qk_heads, int K, int V, int chunk, int value_block,
                                hipStream_t stream);
 
 /*

@@ -5,14 +5,16 @@ Same callables, keyword signatures and return tuples as the reference's
 ``gdn_backward`` :133, ``delta_backward`` :136), which are keyword-compatible
 with FLA's ``chunk_<op>_bwd``.  Each one runs
 
-  1. (recompute policy) ``fdr_prepare_wu`` -- w, u (and qg, kg or Aqk) -- and
-     ``fdr_fwd_h`` -- h, v_new -- from the saved tensors;
-  2. ``fdr_state_bwd``  -- reverse state recurrence with dv_local = Aqk^T dO fused in;
+  1. (recompute policy) ``fdr_fwd_h_wy`` -- w (and qg, kg), h, v_new from the saved
+     tensors, w / u formed inside the forward scan (``fdr_prepare_wu`` + ``fdr_fwd_h`` for a
+     vector gate whose value tiles are narrower than 64, see ``ops.fwd_h_wy_pays``);
+  2. ``fdr_state_bwd``  -- reverse state recurrence with dv_local = Aqk^T dO fused in (for
+     the scalar / no-gate families Aqk formed in-kernel from q, k);
   3. ``fdr_chunk_bwd``  -- residual-WY products, dAqk, matrix intra, gate/beta
      epilogue and the in-chunk reverse cumsum of dg, one work-group per chunk.
 
 When batch x heads is too small to fill the GPU and the sequence long, the two
-recurrences (steps 1b and 2) run instead in affine-step form (``ops.recurrences``,
+recurrences run instead in affine-step form (after ``fdr_prepare_wu``: w, u and qg, kg or Aqk) (``ops.recurrences``,
 ``fdr_affine_*``): chunk-parallel step matrices, one scan launch carrying both
 recurrences side by side, and a chunk-parallel pass for v_new and dR.
 
@@ -134,11 +136,19 @@ def _prepare_vector(k, v, g, Akk, gates, q, vl=None):
 
 
 def _recompute_vector(q, k, v, g, Akk, initial_state, gates, vl=None, vf=False):
-    """w, u, qg, kg (fdr_prepare_wu) then h, v_new (fdr_fwd_h): the recompute policy."""
+    """The recompute policy: w, qg, kg, h, v_new -- in one sweep (fdr_fwd_h_wy: w / u formed
+    inside the forward scan, u never written) when that pays, else fdr_prepare_wu then fdr_fwd_h."""
+    N = q.shape[0] if vl is None else vl.N
+    if ops.fwd_h_wy_pays(N, v.shape[2], ops.GATE_VECTOR):
+        b = None if gates.get("b") is None else _bf(gates["b"])
+        w = None if gates.get("w") is None else _bf(gates["w"])
+        sw = ops.fwd_h_wy(k, v, Akk, g, ops.GATE_VECTOR, beta=_f32(gates.get("beta")), q=q, b=b, w=w,
+                          h0=_f32(initial_state), varlen=vl, state_v_first=vf)
+        return dict(w=sw["w"], qg=sw["qg"], kg=sw["kg"], v_new=sw["v_new"], h=sw["h"])
     pre = _prepare_vector(k, v, g, Akk, gates, q, vl)
     h, v_new, _ = ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
-                            method="auto" if vl is None else "direct", varlen=vl, state_v_first=vf)
-    return dict(w=pre["w"], u=pre["u"], qg=pre["qg"], kg=pre["kg"], v_new=v_new, h=h)
+                            method="direct", varlen=vl, state_v_first=vf)
+    return dict(w=pre["w"], qg=pre["qg"], kg=pre["kg"], v_new=v_new, h=h)
 
 
 def kda_backward(q, k, v, beta, Aqk, Akk, scale, initial_state, do, dht, g, g_org=None,
@@ -210,8 +220,8 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
     inline = not affine and (vl is not None or ops.state_form(q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK)
                              == "direct")
     if inline:
-        w, h, v_new, _ = ops.fwd_h_wy(k, v, A, g, gate, beta, h0=_f32(initial_state), varlen=vl,
-                                      state_v_first=state_v_first)
+        sw = ops.fwd_h_wy(k, v, A, g, gate, beta=beta, h0=_f32(initial_state), varlen=vl, state_v_first=state_v_first)
+        w, h, v_new = sw["w"], sw["h"], sw["v_new"]
         dh, dR, dh0 = ops.state_bwd(q, k, w, g, gate, do, scale, dht=_f32(dht), want_dh0=initial_state is not None,
                                     method="direct", varlen=vl, state_v_first=state_v_first)
         out = _group_sum(ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta,

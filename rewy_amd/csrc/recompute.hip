@@ -500,27 +500,31 @@ struct FwdWySmem {
   bf16 w[2][C][LDK];       // w rows of chunks c, c + 1 (by parity): A operand of w h, stored from here
   bf16 u[2][C * BV];       // u rows (swizzled), chunks c, c + 1: read transposed in the accumulator layout
   bf16 k[2][C * KD];       // kg rows (swizzled), chunks c, c + 1: A operand of kg^T v_new
-  bf16 e[C * KD];          // E = beta k 2^g rows of chunk c + 1 (swizzled): w^T = E^T A^T
+  bf16 e[C * KD];          // E = b k 2^g rows of chunk c + 1 (swizzled): w^T = E^T A^T
   bf16 hT[BV][LDK];        // h^T: B operand of w h
   bf16 vT[BV][LDT];        // v_new^T: B operand of kg^T v_new
-  bf16 z[C * BV];          // Z = beta v rows of chunk c + 1, this value tile (swizzled)
+  bf16 z[C * BV];          // Z = w_gate v rows of chunk c + 1, this value tile (swizzled)
   bf16 ah[C][LDT];         // A rows of chunk c + 1, bf16 hi and lo
   bf16 al[C][LDT];
   float lam[2][KD];
 };
 
-template <int BV, int GATE, bool MAP>
+template <int BV, int GATE, bool VEC_B, bool MAP>
 __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
-    const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ beta,
-    const float* __restrict__ akk, const float* __restrict__ g, const float* __restrict__ h0,
-    bf16* __restrict__ w_out, bf16* __restrict__ h_out, bf16* __restrict__ vnew_out, float* __restrict__ ht_out,
-    int T, int H, const int* __restrict__ chunk_off, int vf, int HQ, const int* __restrict__ cu) {
-  static_assert(GATE != RG_VECTOR, "vector gates keep fdr_prepare_wu (qg / kg)");
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
+    const bf16* __restrict__ wgate, const float* __restrict__ akk, const float* __restrict__ h0,
+    bf16* __restrict__ w_out, bf16* __restrict__ qg_out, bf16* __restrict__ kg_out, bf16* __restrict__ h_out,
+    bf16* __restrict__ vnew_out, float* __restrict__ ht_out, int T, int H, const int* __restrict__ chunk_off,
+    int vf, int HQ, const int* __restrict__ cu) {
+  static_assert(!VEC_B || GATE == RG_VECTOR, "vector b / w_gate come with the vector gate (GDN2)");
+  constexpr bool VEC = GATE == RG_VECTOR;
   using S = FwdWySmem<BV>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
   constexpr int NCT = BV / 16;
   constexpr int NTH = 512;
+  constexpr int RW = C / NVT;          // rows of w (and qg, kg) this value tile stores
   const int logical = xcd_logical_block();
   const int vt = logical % NVT;
   const int bh = logical / NVT;
@@ -553,57 +557,94 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
   const int dct0 = DCT * (wv >> 2);
   const bool has_dr = dct0 < NCT;
 
-  // Pipeline: step c stages chunk c + 1 and forms its w / u after chunk c's state update
-  // (those products beside the update and the stores, off the scan's dependent chain);
-  // w, u, kg and lambda are double-buffered by chunk parity.  Registers: chunk c + 1's
-  // operands, loaded one step ahead -- 2 pieces of 8 k columns, 2 of 4 A columns, the value
-  // tile's v pieces, the gate / beta of each piece's row.
+  // Pipeline: step c stages chunk c + 1 beside its v_new product and forms chunk c + 1's
+  // w / u beside its state update and stores, off the scan's dependent chain; w, u, kg and
+  // lambda are double-buffered by chunk parity.  Registers hold chunk c + 1's operands,
+  // loaded one step ahead: per piece p = tid + 512 i (row p >> 4, columns 8 (p & 15) ..) the
+  // k (, q, g, b) pieces and 4 A columns, the value tile's v (, w_gate) pieces, and the gate /
+  // beta scalars of those rows.
   constexpr int CHV = BV / 8;
   constexpr int NPU = C * CHV;
   constexpr int NU = (NPU + NTH - 1) / NTH;
-  u32x4 rk[2], rv[NU];
-  f32x4 ra[2];
-  float rg_last = 0.f, rg_tok[2] = {0.f, 0.f}, rb_tok[2], rb_v[NU];
+  u32x4 rk[2], rq[2], rb[2], rv[NU], rwg[NU];
+  f32x4 ra[2], rg0[2], rg1[2], rgl0, rgl1;
+  float rg_last = 0.f, rg_tok[2] = {0.f, 0.f}, rb_tok[2] = {0.f, 0.f}, rb_v[NU];
   auto load_chunk = [&](int c) {
     const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
     const size_t tok0 = rs_.tok0;
+    const size_t kofs = tok0 * rsk + (size_t)h * KD;
     if constexpr (GATE == RG_SCALAR) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) rg_tok[i] = g[(tok0 + rs_.clamp((tid + NTH * i) >> 4)) * H + h];
       rg_last = g[(tok0 + rs_.clamp(C - 1)) * H + h];
+    } else if constexpr (VEC) {
+      // lambda's column (tid < KD), and g_last of this thread's 8 columns (both pieces)
+      rg_last = g[kofs + (size_t)rs_.clamp(C - 1) * rsk + (tid & (KD - 1))];
+      const float* gl = g + kofs + (size_t)rs_.clamp(C - 1) * rsk + 8 * (tid & 15);
+      rgl0 = *reinterpret_cast<const f32x4*>(gl);
+      rgl1 = *reinterpret_cast<const f32x4*>(gl + 4);
     }
     const QKRows kr_ = qk_rows(tok0, h, H, HQ);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int p = tid + NTH * i, t = p >> 4;
-      rb_tok[i] = *rs_.src(beta + (tok0 + t) * H + h, t);
-      rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + kr_.ofs + (size_t)t * kr_.rs + (p & 15) * 8, t));
+      const int p = tid + NTH * i, t = p >> 4, c8 = 8 * (p & 15);
+      if constexpr (VEC) {
+        rg0[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8);
+        rg1[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8 + 4);
+        rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + kr_.ofs + (size_t)t * kr_.rs + c8, t));
+      }
+      if constexpr (VEC_B) rb[i] = *reinterpret_cast<const u32x4*>(rs_.src(bgate + kofs + (size_t)t * rsk + c8, t));
+      else rb_tok[i] = *rs_.src(beta + (tok0 + t) * H + h, t);
+      rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + kr_.ofs + (size_t)t * kr_.rs + c8, t));
       ra[i] = *reinterpret_cast<const f32x4*>(rs_.src(akk + ((tok0 + t) * H + h) * C + 4 * (p & 15), t));
     }
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
       const int p = min(tid + NTH * i, NPU - 1), t = p / CHV;
-      rb_v[i] = *rs_.src(beta + (tok0 + t) * H + h, t);
-      rv[i] = *reinterpret_cast<const u32x4*>(rs_.src(v + (tok0 + t) * rsv + (size_t)h * VD + v_base + (p % CHV) * 8, t));
+      const size_t vo = (tok0 + t) * rsv + (size_t)h * VD + v_base + (p % CHV) * 8;
+      if constexpr (VEC_B) rwg[i] = *reinterpret_cast<const u32x4*>(rs_.src(wgate + vo, t));
+      else rb_v[i] = *rs_.src(beta + (tok0 + t) * H + h, t);
+      rv[i] = *reinterpret_cast<const u32x4*>(rs_.src(v + vo, t));
     }
   };
-  // the registers' chunk into LDS: E, Z, A (hi / lo) for its w / u, kg and lambda into buffer `pb`
-  auto stage_chunk = [&](int pb) {
-    if (tid < KD) sm.lam[pb][tid] = GATE == RG_SCALAR ? fast_exp2(rg_last) : 1.f;
+  // the registers' chunk (c) into LDS: E, Z, A (hi / lo) for its w / u, kg and lambda into
+  // buffer `pb`; vector gates also store its qg and kg rows of this value tile's share
+  auto stage_chunk = [&](int pb, int c) {
+    if (tid < KD) sm.lam[pb][tid] = GATE == RG_NONE ? 1.f : fast_exp2(rg_last);
+    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+    const size_t kofs = rs_.tok0 * rsk + (size_t)h * KD;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
       const int t = p >> 4, ch = p & 15;
-      // E = (beta k) 2^g, rounded as prepare_wu_kernel rounds it; kg = k 2^(g_last - g)
-      const float ge = GATE == RG_SCALAR ? fast_exp2(rg_tok[i]) : 1.f;
+      // E = (b k) 2^g and kg = k 2^(g_last - g), each rounded as prepare_wu_kernel rounds it
       const bf16x8 kx = __builtin_bit_cast(bf16x8, rk[i]);
-      bf16x8 eh;
+      bf16x8 eh, kg;
+      if constexpr (VEC) {
+        const bf16x8 qx = __builtin_bit_cast(bf16x8, rq[i]);
+        const bf16x8 bx = __builtin_bit_cast(bf16x8, rb[i]);
+        bf16x8 qg;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) eh[j] = to_bf16(rb_tok[i] * to_f32(kx[j]) * ge);
+        for (int j = 0; j < 8; ++j) {
+          const float gj = j < 4 ? rg0[i][j] : rg1[i][j - 4];
+          const float glj = j < 4 ? rgl0[j] : rgl1[j - 4];
+          const float be = VEC_B ? to_f32(bx[j]) : rb_tok[i];
+          eh[j] = to_bf16(be * to_f32(kx[j]) * fast_exp2(gj));
+          qg[j] = to_bf16(to_f32(qx[j]) * fast_exp2(gj));
+          kg[j] = to_bf16(to_f32(kx[j]) * fast_exp2(glj - gj));
+        }
+        if (t / RW == vt) {       // (wave-uniform: a wave's 64 pieces are 4 whole rows)
+          *reinterpret_cast<bf16x8*>(rs_.dst(qg_out + kofs + (size_t)t * rsk + 8 * ch, t)) = qg;
+          *reinterpret_cast<bf16x8*>(rs_.dst(kg_out + kofs + (size_t)t * rsk + 8 * ch, t)) = kg;
+        }
+      } else {
+        const float ge = GATE == RG_SCALAR ? fast_exp2(rg_tok[i]) : 1.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) eh[j] = to_bf16(rb_tok[i] * to_f32(kx[j]) * ge);
+        kg = GATE == RG_SCALAR ? __builtin_bit_cast(bf16x8, scale_bf16x8(rk[i], fast_exp2(rg_last - rg_tok[i]))) : kx;
+      }
       store_tr_chunk<16>(sm.e, t, ch, __builtin_bit_cast(u32x4, eh));
-      u32x4 kq = rk[i];
-      if constexpr (GATE == RG_SCALAR) kq = scale_bf16x8(kq, fast_exp2(rg_last - rg_tok[i]));
-      store_tr_chunk<16>(sm.k[pb], t, ch, kq);
+      store_tr_chunk<16>(sm.k[pb], t, ch, __builtin_bit_cast(u32x4, kg));
       bf16x4 alo;
       const bf16x4 ahi = split_hi4(ra[i], alo);
       *reinterpret_cast<bf16x4*>(&sm.ah[t][4 * ch]) = ahi;
@@ -614,9 +655,10 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       const int p = tid + NTH * i;
       if (NPU % NTH == 0 || p < NPU) {
         const bf16x8 vx = __builtin_bit_cast(bf16x8, rv[i]);
+        const bf16x8 wx = __builtin_bit_cast(bf16x8, rwg[i]);
         bf16x8 zh;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) zh[j] = to_bf16(rb_v[i] * to_f32(vx[j]));
+        for (int j = 0; j < 8; ++j) zh[j] = to_bf16((VEC_B ? to_f32(wx[j]) : rb_v[i]) * to_f32(vx[j]));
         store_tr_chunk<CHV>(sm.z, p / CHV, p % CHV, __builtin_bit_cast(u32x4, zh));
       }
     }
@@ -662,20 +704,31 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     for (int i = 0; i < 2; ++i) {
       settle(rk[i]);
       settle(ra[i]);
-      settle(rb_tok[i]);
-      settle(rg_tok[i]);
+      if constexpr (VEC) {
+        settle(rq[i]);
+        settle(rg0[i]);
+        settle(rg1[i]);
+      }
+      if constexpr (VEC_B) settle(rb[i]);
+      else settle(rb_tok[i]);
+      if constexpr (GATE == RG_SCALAR) settle(rg_tok[i]);
     }
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
       settle(rv[i]);
-      settle(rb_v[i]);
+      if constexpr (VEC_B) settle(rwg[i]);
+      else settle(rb_v[i]);
+    }
+    if constexpr (VEC) {
+      settle(rgl0);
+      settle(rgl1);
     }
     settle(rg_last);
   };
   if (NT > 0) {
     load_chunk(0);
     settle_chunk();
-    stage_chunk(0);
+    stage_chunk(0, 0);
     load_chunk(NT > 1 ? 1 : 0);
     lds_barrier();
     form_wu(0);
@@ -692,15 +745,16 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[ct][r]);
       *reinterpret_cast<bf16x4*>(&sm.hT[16 * ct + lc][16 * wv + 4 * lg]) = v4;
     }
-    stage_chunk(pb ^ 1);                     // chunk c + 1 (the last step stages itself again: no branch)
+    lds_barrier();
+    const int cn = c + 1 < NT ? c + 1 : c;   // (the last step stages itself again: no branch)
+    stage_chunk(pb ^ 1, cn);
     load_chunk(c + 2 < NT ? c + 2 : NT - 1);
     const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
     const size_t tok0 = rs_.tok0;
-    lds_barrier();
     // w rows [64 vt / NVT, ...) of chunk c to HBM, 16-byte pieces (every lane stores: pieces
     // beyond the share are written twice, with the same data)
     {
-      constexpr int RW = C / NVT, NWP = RW * (KD / 8);
+      constexpr int NWP = RW * (KD / 8);
 #pragma unroll
       for (int i = 0; i < (NWP + NTH - 1) / NTH; ++i) {
         const int p = (tid + NTH * i) % NWP;
@@ -777,13 +831,15 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
   }
 }
 
-template <int BV, int GATE>
-static hipError_t launch_fwd_h_wy(const void* k, const void* v, const float* beta, const float* akk, const float* g,
-                                  const float* h0, void* w, void* h, void* vnew, float* ht, int B, int T, int H,
+template <int BV, int GATE, bool VEC_B>
+static hipError_t launch_fwd_h_wy(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                                  const void* bg, const void* wg, const float* akk, const float* h0, void* w,
+                                  void* qg, void* kg, void* h, void* vnew, float* ht, int B, int T, int H,
                                   hipStream_t s, const int* co, int vf, int HQ, const int* cu) {
-#define FW_LAUNCH(MAP)                                                                                           \
-  hipLaunchKernelGGL((fwd_h_wy_kernel<BV, GATE, MAP>), dim3(B * H * (VD / BV)), dim3(512), 0, s, (const bf16*)k, \
-                     (const bf16*)v, beta, akk, g, h0, (bf16*)w, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf, HQ, cu)
+#define FW_LAUNCH(MAP)                                                                                             \
+  hipLaunchKernelGGL((fwd_h_wy_kernel<BV, GATE, VEC_B, MAP>), dim3(B * H * (VD / BV)), dim3(512), 0, s,            \
+                     (const bf16*)q, (const bf16*)k, (const bf16*)v, g, beta, (const bf16*)bg, (const bf16*)wg, akk, \
+                     h0, (bf16*)w, (bf16*)qg, (bf16*)kg, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf, HQ, cu)
   if (cu) FW_LAUNCH(true);
   else FW_LAUNCH(false);
 #undef FW_LAUNCH
@@ -936,46 +992,59 @@ extern "C" hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void*
 }
 
 // B rows of T tokens, or (co[, cu]) B sequences packed along T tokens as for fwd_h_dispatch
-static hipError_t fwd_h_wy_dispatch(const void* k, const void* v, const float* beta, const float* Akk,
-                                    const float* g, int gate_mode, const float* h0, void* w, void* h, void* v_new,
-                                    float* ht, int B, int T, int H, int HQ, int K, int V, int chunk,
-                                    int value_block, hipStream_t stream, const int* co, int vf, const int* cu) {
+static hipError_t fwd_h_wy_dispatch(const void* q, const void* k, const void* v, const float* g, int gate_mode,
+                                    const float* beta, const void* b_gate, const void* w_gate, const float* Akk,
+                                    const float* h0, void* w, void* qg, void* kg, void* h, void* v_new, float* ht,
+                                    int B, int T, int H, int HQ, int K, int V, int chunk, int value_block,
+                                    hipStream_t stream, const int* co, int vf, const int* cu) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
   if (HQ <= 0) HQ = H;
   if (H % HQ) return hipErrorInvalidValue;
-  if (!k || !v || !beta || !Akk || !w || !h || !v_new) return hipErrorInvalidValue;
-  if (gate_mode != RG_NONE && gate_mode != RG_SCALAR) return hipErrorInvalidValue;
-  if (gate_mode == RG_SCALAR && !g) return hipErrorInvalidValue;
+  if (!k || !v || !Akk || !w || !h || !v_new) return hipErrorInvalidValue;
+  const bool vec_b = b_gate != nullptr;
+  if (vec_b && (!w_gate || gate_mode != RG_VECTOR || HQ != H)) return hipErrorInvalidValue;
+  if (!vec_b && !beta) return hipErrorInvalidValue;
+  if (gate_mode != RG_NONE && !g) return hipErrorInvalidValue;
+  if (gate_mode == RG_VECTOR && (!q || !qg || !kg)) return hipErrorInvalidValue;
   if (cu && !co) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : fwd_default_bv(B, H);
-#define FW_ARGS k, v, beta, Akk, g, h0, w, h, v_new, ht, B, T, H, stream, co, vf, HQ, cu
-#define FW_BV(G)                                                    \
+#define FW_ARGS q, k, v, g, beta, b_gate, w_gate, Akk, h0, w, qg, kg, h, v_new, ht, B, T, H, stream, co, vf, HQ, cu
+#define FW_BV(G, VB)                                                \
   switch (bv) {                                                     \
-    case 16: return launch_fwd_h_wy<16, G>(FW_ARGS);                \
-    case 32: return launch_fwd_h_wy<32, G>(FW_ARGS);                \
-    case 64: return launch_fwd_h_wy<64, G>(FW_ARGS);                \
+    case 16: return launch_fwd_h_wy<16, G, VB>(FW_ARGS);            \
+    case 32: return launch_fwd_h_wy<32, G, VB>(FW_ARGS);            \
+    case 64: return launch_fwd_h_wy<64, G, VB>(FW_ARGS);            \
     default: return hipErrorInvalidValue;                           \
   }
-  if (gate_mode == RG_SCALAR) FW_BV(RG_SCALAR)
-  FW_BV(RG_NONE)
+  switch (gate_mode) {
+    case RG_NONE: FW_BV(RG_NONE, false)
+    case RG_SCALAR: FW_BV(RG_SCALAR, false)
+    case RG_VECTOR:
+      if (vec_b) FW_BV(RG_VECTOR, true)
+      FW_BV(RG_VECTOR, false)
+    default: return hipErrorInvalidValue;
+  }
 #undef FW_BV
 #undef FW_ARGS
 }
 
-extern "C" hipError_t fdr_fwd_h_wy(const void* k, const void* v, const float* beta, const float* Akk, const float* g,
-                                   int gate_mode, const float* h0, void* w, void* h, void* v_new, float* ht,
-                                   int state_v_first, int B, int T, int H, int k_heads, int K, int V, int chunk,
+extern "C" hipError_t fdr_fwd_h_wy(const void* q, const void* k, const void* v, const float* g, int gate_mode,
+                                   const float* beta, const void* b_gate, const void* w_gate, const float* Akk,
+                                   const float* h0, void* w, void* qg, void* kg, void* h, void* v_new, float* ht,
+                                   int state_v_first, int B, int T, int H, int qk_heads, int K, int V, int chunk,
                                    int value_block, hipStream_t stream) {
-  return fwd_h_wy_dispatch(k, v, beta, Akk, g, gate_mode, h0, w, h, v_new, ht, B, T, H, k_heads, K, V, chunk,
-                           value_block, stream, nullptr, state_v_first ? 1 : 0, nullptr);
+  return fwd_h_wy_dispatch(q, k, v, g, gate_mode, beta, b_gate, w_gate, Akk, h0, w, qg, kg, h, v_new, ht, B, T, H,
+                           qk_heads, K, V, chunk, value_block, stream, nullptr, state_v_first ? 1 : 0, nullptr);
 }
 
-extern "C" hipError_t fdr_fwd_h_wy_varlen(const void* k, const void* v, const float* beta, const float* Akk,
-                                          const float* g, int gate_mode, const float* h0, void* w, void* h,
+extern "C" hipError_t fdr_fwd_h_wy_varlen(const void* q, const void* k, const void* v, const float* g, int gate_mode,
+                                          const float* beta, const void* b_gate, const void* w_gate,
+                                          const float* Akk, const float* h0, void* w, void* qg, void* kg, void* h,
                                           void* v_new, float* ht, int state_v_first, const int* chunk_offsets,
-                                          const int* cu_seqlens, int N, int num_chunks, int H, int k_heads, int K,
+                                          const int* cu_seqlens, int N, int num_chunks, int H, int qk_heads, int K,
                                           int V, int chunk, int value_block, hipStream_t stream) {
   if (!chunk_offsets || num_chunks <= 0) return hipErrorInvalidValue;
-  return fwd_h_wy_dispatch(k, v, beta, Akk, g, gate_mode, h0, w, h, v_new, ht, N, num_chunks * C, H, k_heads, K, V,
-                           chunk, value_block, stream, chunk_offsets, state_v_first ? 1 : 0, cu_seqlens);
+  return fwd_h_wy_dispatch(q, k, v, g, gate_mode, beta, b_gate, w_gate, Akk, h0, w, qg, kg, h, v_new, ht, N,
+                           num_chunks * C, H, qk_heads, K, V, chunk, value_block, stream, chunk_offsets,
+                           state_v_first ? 1 : 0, cu_seqlens);
 }

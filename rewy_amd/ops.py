@@ -641,24 +641,45 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
     return h, vnew, ht
 
 
-def fwd_h_wy(k, v, Akk, g, gate_mode, beta, h0=None, want_final=False, value_block=0, state_v_first=False,
-             varlen=None):
-    """``prepare_wu`` (w, u) and the direct ``fwd_h`` in one sweep (scalar / no gate: raw k,
-    scalar beta).  Returns (w [B,T,H,K] bf16, h, v_new, final|None) with the bits of that pair;
-    u is not materialized.  ``varlen`` as for ``fwd_h`` (h0 / final per sequence)."""
-    if gate_mode not in (GATE_NONE, GATE_SCALAR):
-        raise ValueError("fwd_h_wy takes the scalar / no-gate families (gate_mode 0 or 1)")
+def fwd_h_wy_pays(N, H, gate_mode):
+    """Whether ``fwd_h_wy`` beats ``prepare_wu`` + ``fwd_h`` for N rows (sequences) of H heads.
+    Each value-tile work-group forms the whole w (and, for a vector gate, every qg / kg / E
+    exponential) of its chunk: with 64-wide tiles (2 N H >= 256 work-groups) that is paid
+    twice per head and the fused sweep wins for every family; with narrower tiles it is paid
+    4-8 times, which the scalar / no-gate families still absorb and the vector gates do not."""
+    return gate_mode != GATE_VECTOR or 2 * N * H >= 256
+
+
+def fwd_h_wy(k, v, Akk, g, gate_mode, beta=None, q=None, b=None, w=None, h0=None, want_final=False,
+             value_block=0, state_v_first=False, varlen=None):
+    """``prepare_wu`` (w, u; qg, kg for a vector gate) and the direct ``fwd_h`` in one sweep.
+    Operands as for ``prepare_wu`` (raw q / k; scalar beta, or GDN2's b and w_gate).  Returns
+    dict(w, qg, kg, h, v_new, final) with the bits of that pair (qg / kg None unless
+    gate_mode 2, final None unless want_final); u is not materialized.  ``varlen`` as for
+    ``fwd_h`` (h0 / final per sequence)."""
     B, T, HQ, K = _rows(k, varlen)
     H, HQ = _group(v.shape[2] if v.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = k.device
     bf, f32 = torch.bfloat16, torch.float32
+    vec = gate_mode == GATE_VECTOR
     _need(k, "k", bf, (B, T, HQ, K), dev)
     _need(v, "v", bf, (B, T, H, V), dev)
     _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
-    _need(beta, "beta", f32, (B, T, H), dev)
-    if gate_mode == GATE_SCALAR:
+    if b is not None:
+        if not vec or HQ != H:
+            raise ValueError("b / w_gate (GDN2) take the vector gate and one q/k head per value head")
+        _need(b, "b", bf, (B, T, H, K), dev)
+        _need(w, "w_gate", bf, (B, T, H, V), dev)
+    else:
+        _need(beta, "beta", f32, (B, T, H), dev)
+    if vec:
+        _need(g, "g", f32, (B, T, H, K), dev)
+        _need(q, "q", bf, (B, T, HQ, K), dev)
+    elif gate_mode == GATE_SCALAR:
         _need(g, "g", f32, (B, T, H), dev)
+    elif gate_mode != GATE_NONE:
+        raise ValueError("gate_mode must be 0, 1 or 2")
     if varlen is not None:
         co, N, NT = varlen.chunk_offsets, varlen.N, varlen.NC
     else:
@@ -668,22 +689,24 @@ def fwd_h_wy(k, v, Akk, g, gate_mode, beta, h0=None, want_final=False, value_blo
     if value_block not in (0, 16, 32, 64):
         raise ValueError("value_block must be 0, 16, 32 or 64")
     vf = int(bool(state_v_first))
-    w = torch.empty(B, T, H, K, device=dev, dtype=bf)
+    wo = torch.empty(B, T, H, K, device=dev, dtype=bf)
+    qg = torch.empty(B, T, H, K, device=dev, dtype=bf) if vec else None
+    kg = torch.empty(B, T, H, K, device=dev, dtype=bf) if vec else None
     h = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
     vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
     ht = torch.empty(N, H, K, V, device=dev, dtype=f32) if want_final else None
     P = _lib.ptr
+    args = (P(q if vec else None), P(k), P(v), P(g), int(gate_mode), P(beta), P(b), P(w), P(Akk), P(h0), P(wo),
+            P(qg), P(kg), P(h), P(vnew), P(ht), vf)
     if co is not None:
         cu = _mapped(varlen)
-        st = _lib.load().fdr_fwd_h_wy_varlen(P(k), P(v), P(beta), P(Akk), P(g), int(gate_mode), P(h0), P(w), P(h),
-                                             P(vnew), P(ht), vf, P(co), None if cu is None else P(cu.cu_seqlens),
-                                             N, NT, H, HQ, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
+        st = _lib.load().fdr_fwd_h_wy_varlen(*args, P(co), None if cu is None else P(cu.cu_seqlens), N, NT, H, HQ,
+                                             K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
         _lib.check(st, "fdr_fwd_h_wy_varlen")
     else:
-        st = _lib.load().fdr_fwd_h_wy(P(k), P(v), P(beta), P(Akk), P(g), int(gate_mode), P(h0), P(w), P(h), P(vnew),
-                                      P(ht), vf, B, T, H, HQ, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
+        st = _lib.load().fdr_fwd_h_wy(*args, B, T, H, HQ, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
         _lib.check(st, "fdr_fwd_h_wy")
-    return w, h, vnew, ht
+    return dict(w=wo, qg=qg, kg=kg, h=h, v_new=vnew, final=ht)
 
 
 def matrix_intra(q, k, g, dAqk, dAkk, dq, dk, db, dg, beta=None, b=None, beta_complete=False):
