@@ -32,7 +32,8 @@ struct StateSmem {
   bf16 q[C * KD];          // qg rows:  A operand of qg^T dO           (over T, transposed reads)
   bf16 w[C * KD];          // w rows:   A operand of w^T dR            (over T, transposed reads)
   bf16 ah[C * C];          // Aqk rows [t][s] hi: A operand of Aqk^T dO (over T, transposed reads)
-  bf16 al[C * C];          // Aqk lo
+  bf16 al[INL ? 8 : C * C];   // Aqk lo (the in-kernel Aqk is one bf16; 16 bytes keep the
+                              // tiles after it 16-byte aligned)
   bf16 dO[C * BV];         // dO rows [t][v]: B operand of both        (over T, transposed reads)
   bf16 dhT[BV][LDK];       // dh^T:    B operand of kg * dh
   bf16 drT[BV][LDT];       // dR^T:    B operand of w^T dR
@@ -48,7 +49,8 @@ struct StateSmem {
 //
 // INL (scalar / no gate, with DV_FROM_AQK): Aqk = scale tril(q k^T 2^(g_i - g_s)) is formed
 // in-kernel from the raw q / k each chunk stages anyway, instead of being read from HBM
-// (fdr_prepare_wu then need not write it).
+// (fdr_prepare_wu then need not write it), and held as one bf16 for Aqk^T dO, as the
+// reference's call for these families (FLA chunk_bwd_dv_local) rounds it.
 //
 // Segmented form (segs > 0): row r of T tokens is split into `segs` segments of
 // consecutive chunks, work-group row b is segment b % segs of row b / segs, and dht holds
@@ -243,10 +245,12 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
           const float f = GATE == GATE_SCALAR ? scale * fast_exp2(gi - sm.gt[s_]) : scale;
           v[r] = i >= s_ ? a[r] * f : 0.f;
         }
-        bf16x4 lo;
-        const bf16x4 hi = split_hi4(v, lo);
+        // one bf16 Aqk, as FLA's chunk_bwd_dv_local rounds A before its dot with dO (the
+        // read-Aqk form keeps an fp32-faithful hi / lo pair)
+        bf16x4 hi;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hi[r] = to_bf16(v[r]);
         *reinterpret_cast<bf16x4*>(sm.ah + tr_off<8>(i, 16 * Is + 4 * (l >> 4))) = hi;
-        *reinterpret_cast<bf16x4*>(sm.al + tr_off<8>(i, 16 * Is + 4 * (l >> 4))) = lo;
       }
       lds_barrier();
     }
@@ -273,7 +277,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
           for (int ks = 0; ks < 2; ++ks) {
             const bf16x8 bo = frag_tr<CHV>(sm.dO, 32 * ks, 16 * ct);
             a = mfma(frag_tr<8>(sm.ah, 32 * ks, 16 * drow), bo, a);
-            a = mfma(frag_tr<8>(sm.al, 32 * ks, 16 * drow), bo, a);
+            if constexpr (!INL) a = mfma(frag_tr<8>(sm.al, 32 * ks, 16 * drow), bo, a);
           }
         } else {
           const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);

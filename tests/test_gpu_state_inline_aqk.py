@@ -1,6 +1,7 @@
 """The reverse state recurrence forming Aqk itself (scalar / no gate: fdr_state_bwd with
 neither aqk nor dv).  Aqk = scale tril(q k^T 2^(g_i - g_s)) is formed per chunk from the raw
-q / k the recurrence stages, kg dh as 2^(g_last - g_t) (k dh) and qg^T dO as q^T (2^g dO):
+q / k the recurrence stages (one bf16 tile, as FLA's chunk_bwd_dv_local rounds it), kg dh as
+2^(g_last - g_t) (k dh) and qg^T dO as q^T (2^g dO):
 against the fp64 oracle (its Aqk formed in fp64 from the same q, k, g) at the tolerances of
 the stage tests (rel-L2 1e-2 for the bf16 dh / dR, 5e-3 for the fp32 dh0), for GDN and
 DeltaNet, grouped q / k heads, every value-tile width and a packed batch whose sequences
