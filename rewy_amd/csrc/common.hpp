@@ -290,6 +290,19 @@ __device__ __forceinline__ bf16x8 frag_tr_pitch(const bf16* tile, int ld, int r0
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// Rows r0 .. r0 + 7 of column c0 + (l & 15) of a padded row-major tile of pitch ld elements
+// (r0 may differ between the four 16-lane groups): the 16-byte piece a lane stores when a
+// tile held transposed in LDS goes out row by row, two transposed reads instead of eight
+// 2-byte ones.
+__device__ __forceinline__ bf16x8 col8_tr(const bf16* tile, int ld, int r0, int c0, int l = lane_id()) {
+  const int i = l & 15;
+  const int r = r0 + (i >> 2);
+  const int col = c0 + 4 * (i & 3);
+  const bf16x4 a = ds_read_tr4(tile + r * ld + col);
+  const bf16x4 b = ds_read_tr4(tile + (r + 4) * ld + col);
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
 // Row fragment of a swizzled tile: lane l reads row r0 + (l & 15), columns
 // c0 + 8 (l >> 4) .. + 7 (the A/B operand layout of the K = 32 MFMA with the
 // contraction running along the row).

@@ -448,25 +448,24 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     // stores of h_c and v_new_c from the transposed LDS copies (lanes run over rows)
     {
       const size_t hb = ((size_t)(c0 + c) * H + h) * KD * VD;
-      // Every lane issues the same number of stores (pieces beyond the tile are
-      // written twice, with the same data): static vector-memory wait counts.
-      constexpr int NP = KD * BV / 8, NR = C * BV / 8;
+      // Every lane issues the same number of stores (tasks beyond the tile are written
+      // twice, with the same data): static vector-memory wait counts.
+      // per wave task a block of 16 columns (h rows k / v_new rows t) by 32 value rows, 16-lane
+      // group g taking 8 of them (two transposed reads per 16-byte piece)
+      constexpr int RB = BV / 8, RQ = RB >= 4 ? RB / 4 : 1, NW = NTH / 64;
+      constexpr int NTK = (KD / 16) * RQ, NTR = (C / 16) * RQ;
 #pragma unroll
-      for (int i = 0; i < (NP + NTH - 1) / NTH; ++i) {
-        const int p = (tid + NTH * i) % NP;
-        const int kr = p % KD, v0 = (p / KD) * 8;
-        bf16x8 o;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = sm.hT[v0 + j][kr];
-        *reinterpret_cast<bf16x8*>(h_out + hb + (size_t)kr * VD + v_base + v0) = o;
+      for (int i = 0; i < (NTK + NW - 1) / NW; ++i) {
+        const int tk = (wv + NW * i) % NTK;
+        const int kr0 = 16 * (tk % (KD / 16)), v0 = 8 * ((4 * (tk / (KD / 16)) + (l >> 4)) % RB);
+        const bf16x8 o = col8_tr(&sm.hT[0][0], S::LDK, v0, kr0, l);
+        *reinterpret_cast<bf16x8*>(h_out + hb + (size_t)(kr0 + (l & 15)) * VD + v_base + v0) = o;
       }
 #pragma unroll
-      for (int i = 0; i < (NR + NTH - 1) / NTH; ++i) {
-        const int p = (tid + NTH * i) % NR;
-        const int t = p % C, v0 = (p / C) * 8;
-        bf16x8 o;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = sm.vT[v0 + j][t];
+      for (int i = 0; i < (NTR + NW - 1) / NW; ++i) {
+        const int tk = (wv + NW * i) % NTR;
+        const int t0 = 16 * (tk % (C / 16)), t = t0 + (l & 15), v0 = 8 * ((4 * (tk / (C / 16)) + (l >> 4)) % RB);
+        const bf16x8 o = col8_tr(&sm.vT[0][0], S::LDT, v0, t0, l);
         *reinterpret_cast<bf16x8*>(rs_.dst(vnew_out + (tok0 + t) * rsv + (size_t)h * VD + v_base + v0, t)) = o;
       }
     }
@@ -797,23 +796,22 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     form_wu(pb ^ 1);                         // chunk c + 1's w / u, beside the update and the stores
     {
       const size_t hb = ((size_t)(c0 + c) * H + h) * KD * VD;
-      constexpr int NP = KD * BV / 8, NR = C * BV / 8;
+      // per wave task a block of 16 columns (h rows k / v_new rows t) by 32 value rows, 16-lane
+      // group g taking 8 of them (two transposed reads per 16-byte piece)
+      constexpr int RB = BV / 8, RQ = RB >= 4 ? RB / 4 : 1, NW = NTH / 64;
+      constexpr int NTK = (KD / 16) * RQ, NTR = (C / 16) * RQ;
 #pragma unroll
-      for (int i = 0; i < (NP + NTH - 1) / NTH; ++i) {
-        const int p = (tid + NTH * i) % NP;
-        const int kr = p % KD, v0 = (p / KD) * 8;
-        bf16x8 o;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = sm.hT[v0 + j][kr];
-        *reinterpret_cast<bf16x8*>(h_out + hb + (size_t)kr * VD + v_base + v0) = o;
+      for (int i = 0; i < (NTK + NW - 1) / NW; ++i) {
+        const int tk = (wv + NW * i) % NTK;
+        const int kr0 = 16 * (tk % (KD / 16)), v0 = 8 * ((4 * (tk / (KD / 16)) + (l >> 4)) % RB);
+        const bf16x8 o = col8_tr(&sm.hT[0][0], S::LDK, v0, kr0, l);
+        *reinterpret_cast<bf16x8*>(h_out + hb + (size_t)(kr0 + (l & 15)) * VD + v_base + v0) = o;
       }
 #pragma unroll
-      for (int i = 0; i < (NR + NTH - 1) / NTH; ++i) {
-        const int p = (tid + NTH * i) % NR;
-        const int t = p % C, v0 = (p / C) * 8;
-        bf16x8 o;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = sm.vT[v0 + j][t];
+      for (int i = 0; i < (NTR + NW - 1) / NW; ++i) {
+        const int tk = (wv + NW * i) % NTR;
+        const int t0 = 16 * (tk % (C / 16)), t = t0 + (l & 15), v0 = 8 * ((4 * (tk / (C / 16)) + (l >> 4)) % RB);
+        const bf16x8 o = col8_tr(&sm.vT[0][0], S::LDT, v0, t0, l);
         *reinterpret_cast<bf16x8*>(rs_.dst(vnew_out + (tok0 + t) * rsv + (size_t)h * VD + v_base + v0, t)) = o;
       }
     }

@@ -323,33 +323,35 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       st[j] = -a;
     }
 
-    // global stores of dh[c] and dR_c from the transposed LDS copies
+    // global stores of dh[c] and dR_c from the transposed LDS copies: per wave task a block of
+    // 16 columns (dh rows k / dR rows t) by 32 value rows, 16-lane group g taking 8 of them
+    // (two transposed reads per 16-byte piece; narrower tiles repeat a group's rows, with
+    // the same data).  Fixed trip counts keep the vector-memory wait counts static, so the
+    // next chunk's staging waits only for its own loads, not for these stores; waves beyond
+    // the tasks skip (wave-uniform).
     {
+      constexpr int RB = BV / 8;                          // 8-row blocks of the value tile
+      constexpr int RQ = RB >= 4 ? RB / 4 : 1;            // quads of them
+      const int g4 = l >> 4;
       const size_t dh_base = ((size_t)(c0 + c) * H + h) * KD * VD;
-      constexpr int NP = KD * BV / 8;
-      // fixed trip counts keep the vector-memory wait counts static, so the next
-      // chunk's staging waits only for its own loads, not for these stores
+      constexpr int NTK = (KD / 16) * RQ;
 #pragma unroll
-      for (int i = 0; i < (NP + NTH - 1) / NTH; ++i) {
-        const int p = tid + NTH * i;
-        if (NP % NTH != 0 && p >= NP) break;
-        const int kr = p % KD, v0 = (p / KD) * 8;      // lanes run over rows: conflict-free LDS reads
-        bf16x8 o;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = sm.dhT[v0 + j][kr];
-        *reinterpret_cast<bf16x8*>(dh_out + dh_base + (size_t)kr * VD + v_base + v0) = o;
+      for (int i = 0; i < (NTK + NW - 1) / NW; ++i) {
+        const int tk = wv + NW * i;
+        if (NTK % NW != 0 && tk >= NTK) break;
+        const int kr0 = 16 * (tk % (KD / 16)), v0 = 8 * ((4 * (tk / (KD / 16)) + g4) % RB);
+        const bf16x8 o = col8_tr(&sm.dhT[0][0], S::LDK, v0, kr0, l);
+        *reinterpret_cast<bf16x8*>(dh_out + dh_base + (size_t)(kr0 + (l & 15)) * VD + v_base + v0) = o;
       }
       const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
       const size_t tok0 = rs_.tok0;
-      constexpr int NR = C * BV / 8;
+      constexpr int NTR = (C / 16) * RQ;
 #pragma unroll
-      for (int i = 0; i < (NR + NTH - 1) / NTH; ++i) {
-        const int p = tid + NTH * i;
-        if (NR % NTH != 0 && p >= NR) break;
-        const int t = p % C, v0 = (p / C) * 8;
-        bf16x8 o;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = sm.drT[v0 + j][t];
+      for (int i = 0; i < (NTR + NW - 1) / NW; ++i) {
+        const int tk = wv + NW * i;
+        if (NTR % NW != 0 && tk >= NTR) break;
+        const int t = 16 * (tk % (C / 16)) + (l & 15), v0 = 8 * ((4 * (tk / (C / 16)) + g4) % RB);
+        const bf16x8 o = col8_tr(&sm.drT[0][0], S::LDT, v0, t - (l & 15), l);
         *reinterpret_cast<bf16x8*>(rs_.dst(dr_out + (tok0 + t) * row_stride_v + (size_t)h * VD + v_base + v0, t)) = o;
       }
     }
