@@ -45,8 +45,8 @@ constexpr int Y_FRAG = KD * VD;   // fp32 elements of one chunk-head's offset
 // prep: step matrix and offset of every chunk-head
 // ---------------------------------------------------------------------------
 // 80 KiB, two work-groups per CU: the K x K product's staging reuses the inputs'
-// bytes after the last MFMA, and (backward with Aqk) kg is written over Aqk's hi / lo
-// split once dv_local is formed.
+// bytes after the last MFMA, and (backward with Aqk) kg is written over Aqk's bf16 tile
+// once dv_local is formed.
 struct PrepSmem {
   union {
     struct {
@@ -59,8 +59,7 @@ struct PrepSmem {
   } t;
   union {
     struct {
-      bf16 ah[C * C];      // bwd: Aqk hi, rows [t][s] (8-chunk swizzle)
-      bf16 al[C * C];      // bwd: Aqk lo
+      bf16 ah[C * C];      // bwd: Aqk (bf16), rows [t][s] (8-chunk swizzle)
     } a;
     bf16 xb[C * KD];       // B side of the K x K product: kg (bwd) | w (fwd)
   } s;
@@ -128,11 +127,13 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
       if constexpr (GATE == AG_SCALAR) qq = scale_bf16x8(qq, fast_exp2(gt));   // qg = q 2^(g_t)
       store_tr_chunk<16>(sm.t.in.xq, t, cc, qq);
       if constexpr (DV_FROM_AQK) {
+        // Aqk as one bf16, the precision of the reference's dv_local (FLA's dAv rounds A to
+        // the dO dtype before its dot: kernels/kda_residual_npu_onchip.py:114-116)
         const f32x4 a = *reinterpret_cast<const f32x4*>(aqk + ((tok0 + t) * H + h) * C + cc * 4);
-        bf16x4 lo;
-        const bf16x4 hi = split_hi4(a, lo);
+        bf16x4 hi;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hi[r] = to_bf16(a[r]);
         *reinterpret_cast<bf16x4*>(sm.s.a.ah + tr_off<8>(t, cc * 4)) = hi;
-        *reinterpret_cast<bf16x4*>(sm.s.a.al + tr_off<8>(t, cc * 4)) = lo;
       } else {
         store_tr_chunk<16>(sm.t.in.dv, t, cc, *reinterpret_cast<const u32x4*>(dv_in + vofs + (size_t)t * rsv + cc * 8));
       }
@@ -155,13 +156,12 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
       for (int ks = 0; ks < 2; ++ks) {
         const bf16x8 bo = frag_tr<16>(sm.t.in.y0, 32 * ks, 16 * ct);
         a = mfma(frag_tr<8>(sm.s.a.ah, 32 * ks, 16 * rt), bo, a);
-        a = mfma(frag_tr<8>(sm.s.a.al, 32 * ks, 16 * rt), bo, a);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         sm.t.in.dv[tr_off<16>(16 * rt + 4 * (l >> 4) + r, 16 * ct + (l & 15))] = to_bf16(a[r]);
     }
-    lds_barrier();                               // dv complete, Aqk's hi / lo dead
+    lds_barrier();                               // dv complete, Aqk dead
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + 512 * i;

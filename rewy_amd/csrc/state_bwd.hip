@@ -31,9 +31,7 @@ struct StateSmem {
   bf16 k[C][LDK];          // kg rows:  A operand of kg * dh           (contraction over K, row reads)
   bf16 q[C * KD];          // qg rows:  A operand of qg^T dO           (over T, transposed reads)
   bf16 w[C * KD];          // w rows:   A operand of w^T dR            (over T, transposed reads)
-  bf16 ah[C * C];          // Aqk rows [t][s] hi: A operand of Aqk^T dO (over T, transposed reads)
-  bf16 al[INL ? 8 : C * C];   // Aqk lo (the in-kernel Aqk is one bf16; 16 bytes keep the
-                              // tiles after it 16-byte aligned)
+  bf16 ah[C * C];          // Aqk rows [t][s], bf16: A operand of Aqk^T dO (over T, transposed reads)
   bf16 dO[C * BV];         // dO rows [t][v]: B operand of both        (over T, transposed reads)
   bf16 dhT[BV][LDK];       // dh^T:    B operand of kg * dh
   bf16 drT[BV][LDT];       // dR^T:    B operand of w^T dR
@@ -192,10 +190,12 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       store_tr_chunk<16>(sm.q, t, ch, qq);
       store_tr_chunk<16>(sm.w, t, ch, rw[i]);
       if constexpr (DV_FROM_AQK && !INL) {
-        bf16x4 lo;
-        const bf16x4 hi = split_hi4(ra[i], lo);
+        // Aqk as one bf16, the precision of the reference's dv_local (FLA's dAv rounds A to
+        // the dO dtype before its dot: kernels/kda_residual_npu_onchip.py:114-116)
+        bf16x4 hi;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hi[r] = to_bf16(ra[i][r]);
         *reinterpret_cast<bf16x4*>(sm.ah + tr_off<8>(t, ch * 4)) = hi;
-        *reinterpret_cast<bf16x4*>(sm.al + tr_off<8>(t, ch * 4)) = lo;
       }
     }
 #pragma unroll
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
 
     if constexpr (INL) {
       // Aqk = scale tril(q k^T 2^(g_i - g_s)), as S^T = k q^T tiles (rows s, columns i), so that
-      // each lane's four rows s are four consecutive columns of Aqk's row i (hi / lo, as staged)
+      // each lane's four rows s are four consecutive columns of Aqk's row i (as the read form stages it)
 #pragma unroll
       for (int tt = wv; tt < 16; tt += NW) {
         const int Is = tt >> 2, Ji = tt & 3;
@@ -245,8 +245,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
           const float f = GATE == GATE_SCALAR ? scale * fast_exp2(gi - sm.gt[s_]) : scale;
           v[r] = i >= s_ ? a[r] * f : 0.f;
         }
-        // one bf16 Aqk, as FLA's chunk_bwd_dv_local rounds A before its dot with dO (the
-        // read-Aqk form keeps an fp32-faithful hi / lo pair)
+        // one bf16 Aqk, as FLA's chunk_bwd_dv_local rounds A before its dot with dO
         bf16x4 hi;
 #pragma unroll
         for (int r = 0; r < 4; ++r) hi[r] = to_bf16(v[r]);
@@ -277,7 +276,6 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
           for (int ks = 0; ks < 2; ++ks) {
             const bf16x8 bo = frag_tr<CHV>(sm.dO, 32 * ks, 16 * ct);
             a = mfma(frag_tr<8>(sm.ah, 32 * ks, 16 * drow), bo, a);
-            if constexpr (!INL) a = mfma(frag_tr<8>(sm.al, 32 * ks, 16 * drow), bo, a);
           }
         } else {
           const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
@@ -424,8 +422,7 @@ struct XferSmem {
   bf16 k[C][LDK];
   bf16 q[C * KD];
   bf16 w[C * KD];
-  bf16 ah[C * C];
-  bf16 al[C * C];
+  bf16 ah[C * C];          // Aqk rows [t][s], bf16
   bf16 dO[C * 64];         // the Q half's 64 value columns
   bf16 dhT[128][LDK];      // state^T: columns 0-63 of P's half, 64-127 of Q's
   bf16 drT[128][LDT];
@@ -504,10 +501,10 @@ __global__ __launch_bounds__(512) void state_xfer_kernel(
       store_tr_chunk<16>(sm.q, t, ch, qq);
       store_tr_chunk<16>(sm.w, t, ch, rw[i]);
       if constexpr (DV_FROM_AQK) {
-        bf16x4 lo;
-        const bf16x4 hi = split_hi4(ra[i], lo);
+        bf16x4 hi;                           // one bf16 Aqk, as the direct kernel
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hi[r] = to_bf16(ra[i][r]);
         *reinterpret_cast<bf16x4*>(sm.ah + tr_off<8>(t, ch * 4)) = hi;
-        *reinterpret_cast<bf16x4*>(sm.al + tr_off<8>(t, ch * 4)) = lo;
       }
     }
     static_assert(NPD == NTH, "one dO piece per thread");
@@ -548,7 +545,6 @@ __global__ __launch_bounds__(512) void state_xfer_kernel(
           for (int ks = 0; ks < 2; ++ks) {
             const bf16x8 bo = frag_tr<CHV>(sm.dO, 32 * ks, 16 * cc);
             a = mfma(frag_tr<8>(sm.ah, 32 * ks, 16 * drow), bo, a);
-            a = mfma(frag_tr<8>(sm.al, 32 * ks, 16 * drow), bo, a);
           }
         } else {
           const size_t tok0 = (size_t)(c0 + c) * C;
