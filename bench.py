@@ -82,9 +82,9 @@ def kernel_costs(op, full_saving, inline=False):
     mm = lambda m, n, k: 2 * m * n * k
     costs = {}
     if not full_saving:
-        rd = 3 * TILE + g_b + gates_b + AT                      # q, k, v, g, beta|b,w, Akk
-        wr = 2 * TILE + (2 * TILE if vec else AT)               # w, u, (qg, kg | Aqk)
-        costs["fdr_prepare_wu"] = (rd + wr, 2 * mm(64, 128, 64) + (0 if vec else mm(64, 64, 128)))
+        rd = (2 if inline else 3) * TILE + g_b + gates_b + AT   # (q,) k, v, g, beta|b,w, Akk
+        wr = 2 * TILE + (2 * TILE if vec else (0 if inline else AT))   # w, u, (qg, kg | Aqk)
+        costs["fdr_prepare_wu"] = (rd + wr, 2 * mm(64, 128, 64) + (0 if vec or inline else mm(64, 64, 128)))
         costs["fdr_fwd_h"] = (3 * TILE + gl_b + (0 if vec else g_b) + HS + TILE, 2 * mm(64, 128, 128))
         # w / u formed in the forward scan's sweep: reads (q,) k, v, Akk, g, beta|b,w; writes
         # w, (qg, kg,) h, v_new
@@ -198,8 +198,8 @@ def setup(cfg, device):
     inline = inline_aqk(cfg)
     # the recompute policy's direct path (as the backends decide): w / u in the forward scan's
     # sweep (fdr_fwd_h_wy); for the scalar / no-gate families Aqk in the state recurrence
-    fused = (not keep and not ops.affine_pays(xs["q"])
-             and (inline or (vec and ops.fwd_h_wy_pays(cfg["B"], cfg["H"], gate))))
+    fused = (not keep and not ops.affine_pays(xs["q"]) and (inline or vec)
+             and ops.fwd_h_wy_pays(cfg["B"], cfg["H"], gate))
     if fused:
         kern["fdr_fwd_h_wy"] = lambda: ops.fwd_h_wy(xs["k"], xs["v"], sv["Akk"], g, gate, beta=xs.get("beta"),
                                                     q=xs["q"] if vec else None, b=xs.get("b"), w=xs.get("w"),
@@ -211,7 +211,7 @@ def setup(cfg, device):
     elif not keep:
         kern["fdr_prepare_wu"] = lambda: ops.prepare_wu(
             xs["k"], xs["v"], sv["Akk"], gate, g=g, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"), q=xs["q"],
-            want_qkg=vec, want_aqk=not vec, scale=scale)
+            want_qkg=vec, want_aqk=not vec and not inline, scale=scale)
         pre = kern["fdr_prepare_wu"]()
         ks, qs, ws = (pre["kg"], pre["qg"], pre["w"]) if vec else (xs["k"], xs["q"], pre["w"])
         aqk = sv["Aqk"] if vec else pre["Aqk"]

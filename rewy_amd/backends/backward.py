@@ -216,12 +216,20 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
     gate = ops.GATE_SCALAR if op == "gdn" else ops.GATE_NONE
     affine = vl is None and q.shape[2] == v.shape[2] and ops.affine_pays(v)
     # the direct state recurrence forms Aqk itself from the raw q / k it stages; w and u are then
-    # formed inside the forward scan's sweep (fdr_fwd_h_wy: u never leaves the chip)
+    # formed inside the forward scan's sweep where that pays (fdr_fwd_h_wy: u never leaves the
+    # chip), else by fdr_prepare_wu without Aqk
     inline = not affine and (vl is not None or ops.state_form(q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK)
                              == "direct")
     if inline:
-        sw = ops.fwd_h_wy(k, v, A, g, gate, beta=beta, h0=_f32(initial_state), varlen=vl, state_v_first=state_v_first)
-        w, h, v_new = sw["w"], sw["h"], sw["v_new"]
+        if ops.fwd_h_wy_pays(q.shape[0] if vl is None else vl.N, v.shape[2], gate):
+            sw = ops.fwd_h_wy(k, v, A, g, gate, beta=beta, h0=_f32(initial_state), varlen=vl,
+                              state_v_first=state_v_first)
+            w, h, v_new = sw["w"], sw["h"], sw["v_new"]
+        else:
+            pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, varlen=vl)
+            w = pre["w"]
+            h, v_new, _ = ops.fwd_h(k, w, pre["u"], g, gate, h0=_f32(initial_state), method="direct", varlen=vl,
+                                    state_v_first=state_v_first)
         dh, dR, dh0 = ops.state_bwd(q, k, w, g, gate, do, scale, dht=_f32(dht), want_dh0=initial_state is not None,
                                     method="direct", varlen=vl, state_v_first=state_v_first)
         out = _group_sum(ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta,

@@ -644,10 +644,13 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
 def fwd_h_wy_pays(N, H, gate_mode):
     """Whether ``fwd_h_wy`` beats ``prepare_wu`` + ``fwd_h`` for N rows (sequences) of H heads.
     Each value-tile work-group forms the whole w (and, for a vector gate, every qg / kg / E
-    exponential) of its chunk: with 64-wide tiles (2 N H >= 256 work-groups) that is paid
-    twice per head and the fused sweep wins for every family; with narrower tiles it is paid
-    4-8 times, which the scalar / no-gate families still absorb and the vector gates do not."""
-    return gate_mode != GATE_VECTOR or 2 * N * H >= 256
+    exponential) of its chunk, so that work is repeated once per value tile of a head.  The
+    default tiles are 64 wide from 2 N H >= 256 work-groups, 32 wide from 4 N H >= 256, else
+    16 wide.  Measured: at 64-wide tiles the sweep wins for every family; at 32-wide ones the
+    scalar / no-gate families still win and the vector gates lose; at 16-wide ones all lose."""
+    if gate_mode == GATE_VECTOR:
+        return 2 * N * H >= 256
+    return 4 * N * H >= 256
 
 
 def fwd_h_wy(k, v, Akk, g, gate_mode, beta=None, q=None, b=None, w=None, h0=None, want_final=False,

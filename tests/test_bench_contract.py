@@ -35,6 +35,7 @@ def test_kernel_costs_match_the_quoted_figures():
     # forward scan's sweep: k, v, Akk, g, beta read, w, h, v_new written
     inl = bench.kernel_costs("gdn", False, inline=True)
     assert inl["fdr_fwd_h_wy"][0] == 115_200
+    assert inl["fdr_prepare_wu"][0] == gdn["fdr_prepare_wu"][0] - bench.TILE - bench.AT
     assert inl["fdr_state_bwd"][0] == gdn["fdr_state_bwd"][0] - bench.AT
     assert inl["fdr_state_bwd"][1] == gdn["fdr_state_bwd"][1] + 2 * 64 * 64 * 128
     assert bench.inline_aqk(bench.CONFIGS["gdn"]) and not bench.inline_aqk(bench.CONFIGS["kda"])
