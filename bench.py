@@ -375,9 +375,8 @@ def cpu_baseline(xs, sv, dO, scale, NTt, round_s=0.5, rounds=15):
     try:
         def sample_inputs(hs):
             # batch 0, heads 0..hs-1 ([B,T,H,...] tensors and [B,NT,H,K,V] states alike)
-            c = lambda x: x[:1, :, :hs].float().cpu().contiguous()
-            saved = dict(w=c(sv["w"]), u=c(sv["u"]), qg=c(sv["qg"]), kg=c(sv["kg"]), v_new=c(sv["v_new"]),
-                         h=c(sv["h"]))
+            c = lambda x: None if x is None else x[:1, :, :hs].float().cpu().contiguous()
+            saved = {n: c(sv[n]) for n in ("w", "u", "qg", "kg", "v_new", "h")}
             return dict(q=c(xs["q"]), k=c(xs["k"]), v=c(xs["v"]), gc=c(sv["gc"]), Akk=c(sv["Akk"]),
                         beta=c(xs["beta"]), Aqk=c(sv["Aqk"]), dO=c(dO), saved=saved)
 

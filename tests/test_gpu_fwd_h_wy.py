@@ -133,3 +133,26 @@ def test_recompute_backward_equals_full_saving(op):
             assert a is None
             continue
         assert torch.equal(a, r), (i, float((a.float() - r.float()).abs().max()))
+
+
+@pytest.mark.parametrize("op", ["gdn", "kda", "gdn2"])
+def test_hip_forward_fused_scan_equals_the_pair(op):
+    """The HIP forward with steps 2-3 as one sweep (fdr_fwd_h_wy) against the same forward with
+    fdr_prepare_wu + fdr_fwd_h: o, the final state and every saved tensor but u, bit for bit"""
+    from rewy_amd.hip_forward import chunk_forward_hip
+    B, T, H = 8, 128, 16
+    print(f"\n[fwd_h_wy] HIP forward {op} fused vs pair", flush=True)
+    dev = torch.device("cuda")
+    xs, _ = make_inputs(op, B, T, H, seed=67)
+    xs = {n: x.to(dev) for n, x in xs.items()}
+    run = lambda fuse: chunk_forward_hip(op, xs["q"], xs["k"], xs["v"], g=xs.get("g"), beta=xs.get("beta"),
+                                         b=xs.get("b"), w=xs.get("w"), initial_state=xs["initial_state"],
+                                         output_final_state=True, fuse_scan=fuse)
+    o1, f1, s1 = run(True)
+    o0, f0, s0 = run(False)
+    torch.cuda.synchronize()
+    assert s1["u"] is None
+    assert torch.equal(o1, o0) and torch.equal(f1, f0)
+    for n in ("w", "qg", "kg", "h", "v_new"):
+        if s0[n] is not None:
+            assert torch.equal(s1[n], s0[n]), n
