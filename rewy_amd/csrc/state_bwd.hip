@@ -28,10 +28,14 @@ struct StateSmem {
   static constexpr int LDK = KD + 8;   // pitch of [.][K] tiles
   static constexpr int LDT = C + 8;    // pitch of [.][T] tiles
   static constexpr int CHV = BV / 8;   // 16-byte chunks per dO row
-  bf16 k[C][LDK];          // kg rows:  A operand of kg * dh           (contraction over K, row reads)
-  bf16 q[C * KD];          // qg rows:  A operand of qg^T dO           (over T, transposed reads)
+  // (INL at 64-wide tiles: k, q, Aqk and the row gates double-buffered by chunk parity -- see
+  // the kernel)
+  static constexpr bool SP = INL && BV == 64;
+  static constexpr int NB = SP ? 2 : 1;
+  bf16 k[NB][C][LDK];      // kg rows:  A operand of kg * dh           (contraction over K, row reads)
+  bf16 q[NB][C * KD];      // qg rows:  A operand of qg^T dO           (over T, transposed reads)
   bf16 w[C * KD];          // w rows:   A operand of w^T dR            (over T, transposed reads)
-  bf16 ah[C * C];          // Aqk rows [t][s], bf16: A operand of Aqk^T dO (over T, transposed reads)
+  bf16 ah[NB][C * C];      // Aqk rows [t][s], bf16: A operand of Aqk^T dO (over T, transposed reads)
   bf16 dO[C * BV];         // dO rows [t][v]: B operand of both        (over T, transposed reads)
   bf16 dhT[BV][LDK];       // dh^T:    B operand of kg * dh
   bf16 drT[BV][LDT];       // dR^T:    B operand of w^T dR
@@ -39,7 +43,7 @@ struct StateSmem {
   // in-kernel Aqk (INL, scalar / no gate): k and q are staged raw; qg^T dO is formed as
   // q^T (2^g dO) and kg dh as 2^(g_last - g_t) (k dh)
   bf16 dOg[(INL && GATE == GATE_SCALAR) ? C * BV : 1];   // 2^(g_t) dO rows (swizzled)
-  float gt[INL ? C + 1 : 1];                             // g_t per row, g_last at [C]
+  float gt[NB][INL ? C + 1 : 1];                         // g_t per row, g_last at [C]
 };
 
 // NW waves: 8 (wave w owns state rows [16 w, 16 w + 16), every value column) or 16
@@ -177,43 +181,164 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       const int p = tid + NTH * i;
       const int t = p >> 4, ch = p & 15;
       u32x4 kq = rk[i], qq = rq[i];
-      if constexpr (INL) {
-        // raw k and q; the row gates go to LDS for the Aqk factors and the kg dh row scaling
-        if (ch == 0) sm.gt[t] = GATE == GATE_SCALAR ? rg_tok[i] : 0.f;
-        if (tid == 0) sm.gt[C] = rg_last;
-      } else if constexpr (GATE == GATE_SCALAR) {
+      if constexpr (GATE == GATE_SCALAR) {
         // scalar gate: kg = k 2^(g_last - g_t), qg = q 2^(g_t), the row's factors from registers
         kq = scale_bf16x8(kq, fast_exp2(rg_last - rg_tok[i]));
         qq = scale_bf16x8(qq, fast_exp2(rg_tok[i]));
       }
-      *reinterpret_cast<u32x4*>(&sm.k[t][ch * 8]) = kq;
-      store_tr_chunk<16>(sm.q, t, ch, qq);
+      *reinterpret_cast<u32x4*>(&sm.k[0][t][ch * 8]) = kq;
+      store_tr_chunk<16>(sm.q[0], t, ch, qq);
       store_tr_chunk<16>(sm.w, t, ch, rw[i]);
-      if constexpr (DV_FROM_AQK && !INL) {
+      if constexpr (DV_FROM_AQK) {
         // Aqk as one bf16, the precision of the reference's dv_local (FLA's dAv rounds A to
         // the dO dtype before its dot: kernels/kda_residual_npu_onchip.py:114-116)
         bf16x4 hi;
 #pragma unroll
         for (int r = 0; r < 4; ++r) hi[r] = to_bf16(ra[i][r]);
-        *reinterpret_cast<bf16x4*>(sm.ah + tr_off<8>(t, ch * 4)) = hi;
+        *reinterpret_cast<bf16x4*>(sm.ah[0] + tr_off<8>(t, ch * 4)) = hi;
       }
+    }
+#pragma unroll
+    for (int i = 0; i < NDO; ++i) {
+      const int p = tid + NTH * i;
+      if (NPD % NTH == 0 || p < NPD) store_tr_chunk<CHV>(sm.dO, p / CHV, p % CHV, rdo[i]);
+    }
+  };
+
+
+  // In-kernel Aqk (INL): two load / stage groups, A (a chunk's raw k, q and row gates, g_last
+  // included) and B (w, dO and 2^g dO).  At 64-wide tiles (SP) group A is staged one step ahead
+  // into the parity buffer the chunk will read, so that its S = q k^T tiles are formed in the
+  // step before -- after that step's state update, beside its stores, off the dependent chain
+  // (registers at the start of step c: B holds chunk c, A chunk c - 1).  Narrower tiles (16
+  // waves at 32-wide ones) measured slower so: they stage both groups of chunk c at step c and
+  // form its S tiles before its dR.
+  constexpr bool SP = S::SP;
+  auto load_A = [&](int c) {
+    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+    const size_t tok0 = rs_.tok0;
+    if constexpr (GATE == GATE_SCALAR) {
+#pragma unroll
+      for (int i = 0; i < NPI; ++i) rg_tok[i] = g[(tok0 + rs_.clamp((tid + NTH * i) >> 4)) * H + h];
+      rg_last = g[(tok0 + rs_.clamp(C - 1)) * H + h];
+    }
+    const QKRows qr = qk_rows(tok0, h, H, HQ);
+#pragma unroll
+    for (int i = 0; i < NPI; ++i) {
+      const int p = tid + NTH * i;
+      const size_t oq = qr.ofs + (size_t)(p >> 4) * qr.rs + (p & 15) * 8;
+      rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + oq, p >> 4));
+      rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + oq, p >> 4));
+    }
+  };
+  auto load_B = [&](int c) {
+    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+    const size_t tok0 = rs_.tok0;
+    const size_t kofs = tok0 * row_stride_k + (size_t)h * KD;
+#pragma unroll
+    for (int i = 0; i < NPI; ++i) {
+      const int p = tid + NTH * i;
+      rw[i] = *reinterpret_cast<const u32x4*>(rs_.src(w + kofs + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8, p >> 4));
+    }
+#pragma unroll
+    for (int i = 0; i < NDO; ++i) {
+      const int p = min(tid + NTH * i, NPD - 1);
+      rdo[i] = *reinterpret_cast<const u32x4*>(
+          rs_.src(dO + (tok0 + p / CHV) * row_stride_v + (size_t)h * VD + v_base + (p % CHV) * 8, p / CHV));
+      if constexpr (GATE == GATE_SCALAR) rg_do[i] = g[(tok0 + rs_.clamp(p / CHV)) * H + h];
+    }
+  };
+  // group A of the registers' chunk into parity buffer `pb`: raw k and q, the row gates
+  auto stage_A = [&](int pb) {
+#pragma unroll
+    for (int i = 0; i < NPI; ++i) {
+      const int p = tid + NTH * i;
+      const int t = p >> 4, ch = p & 15;
+      if (ch == 0) sm.gt[pb][t] = GATE == GATE_SCALAR ? rg_tok[i] : 0.f;
+      *reinterpret_cast<u32x4*>(&sm.k[pb][t][ch * 8]) = rk[i];
+      store_tr_chunk<16>(sm.q[pb], t, ch, rq[i]);
+    }
+    if (tid == 0) sm.gt[pb][C] = GATE == GATE_SCALAR ? rg_last : 0.f;
+  };
+  auto stage_B = [&]() {
+#pragma unroll
+    for (int i = 0; i < NPI; ++i) {
+      const int p = tid + NTH * i;
+      store_tr_chunk<16>(sm.w, p >> 4, p & 15, rw[i]);
     }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
       const int p = tid + NTH * i;
       if (NPD % NTH == 0 || p < NPD) {
         store_tr_chunk<CHV>(sm.dO, p / CHV, p % CHV, rdo[i]);
-        if constexpr (INL && GATE == GATE_SCALAR)
+        if constexpr (GATE == GATE_SCALAR)
           store_tr_chunk<CHV>(sm.dOg, p / CHV, p % CHV, scale_bf16x8(rdo[i], fast_exp2(rg_do[i])));
       }
     }
   };
+  // Aqk = scale tril(q k^T 2^(g_i - g_s)) of the chunk in buffer `pb`, as S^T = k q^T tiles
+  // (rows s, columns i), so that each lane's four rows s are four consecutive columns of Aqk's
+  // row i (as the read form stages it); one bf16, as FLA's chunk_bwd_dv_local rounds A before
+  // its dot with dO
+  auto form_S = [&](int pb) {
+#pragma unroll
+    for (int tt = wv; tt < 16; tt += NW) {
+      const int Is = tt >> 2, Ji = tt & 3;
+      f32x4 a = zero4();
+      if (Ji >= Is) {                      // wave-uniform: tiles above the diagonal are zero
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          a = mfma(frag(&sm.k[pb][16 * Is][32 * ks], S::LDK), frag_row<16>(sm.q[pb], 16 * Ji, 32 * ks), a);
+      }
+      const int i = 16 * Ji + (l & 15);
+      const float gi = sm.gt[pb][i];
+      bf16x4 hi;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int s_ = 16 * Is + 4 * (l >> 4) + r;
+        const float f = GATE == GATE_SCALAR ? scale * fast_exp2(gi - sm.gt[pb][s_]) : scale;
+        hi[r] = to_bf16(i >= s_ ? a[r] * f : 0.f);
+      }
+      *reinterpret_cast<bf16x4*>(sm.ah[pb] + tr_off<8>(i, 16 * Is + 4 * (l >> 4))) = hi;
+    }
+  };
 
-  if (NT > 0) load_chunk(NT - 1);
+  if constexpr (SP) {
+    if (NT > 0) {
+      load_A(NT - 1);
+      load_B(NT - 1);
+      stage_A((NT - 1) & 1);
+      load_A(NT > 1 ? NT - 2 : 0);
+      lds_barrier();
+      form_S((NT - 1) & 1);
+    }
+  } else if constexpr (INL) {
+    if (NT > 0) {
+      load_A(NT - 1);
+      load_B(NT - 1);
+    }
+  } else {
+    if (NT > 0) load_chunk(NT - 1);
+  }
   for (int c = NT - 1; c >= 0; --c) {
+    const int pb = SP ? (c & 1) : 0;     // this chunk's k / q / Aqk / gate buffer
     lds_barrier();                       // previous chunk done with every LDS tile
-    stage_chunk();
-    if (c > 0) load_chunk(c - 1);          // prefetch; consumed next iteration
+    if constexpr (SP) {
+      stage_B();                           // chunk c
+      stage_A(pb ^ 1);                     // chunk c - 1 (the last step stages chunk 0 again)
+      load_B(c > 0 ? c - 1 : 0);
+      load_A(c > 1 ? c - 2 : 0);
+    } else if constexpr (INL) {
+      stage_B();
+      stage_A(0);
+      if (c > 0) {
+        load_A(c - 1);
+        load_B(c - 1);
+      }
+    } else {
+      stage_chunk();
+      if (c > 0) load_chunk(c - 1);          // prefetch; consumed next iteration
+    }
     // dh (state at the end of chunk c) -> LDS, transposed, bf16
 #pragma unroll
     for (int j = 0; j < NCW; ++j) {
@@ -224,33 +349,8 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     }
     lds_barrier();
 
-    if constexpr (INL) {
-      // Aqk = scale tril(q k^T 2^(g_i - g_s)), as S^T = k q^T tiles (rows s, columns i), so that
-      // each lane's four rows s are four consecutive columns of Aqk's row i (as the read form stages it)
-#pragma unroll
-      for (int tt = wv; tt < 16; tt += NW) {
-        const int Is = tt >> 2, Ji = tt & 3;
-        f32x4 a = zero4();
-        if (Ji >= Is) {                      // wave-uniform: tiles above the diagonal are zero
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks)
-            a = mfma(frag(&sm.k[16 * Is][32 * ks], S::LDK), frag_row<16>(sm.q, 16 * Ji, 32 * ks), a);
-        }
-        const int i = 16 * Ji + (l & 15);
-        const float gi = sm.gt[i];
-        f32x4 v;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int s_ = 16 * Is + 4 * (l >> 4) + r;
-          const float f = GATE == GATE_SCALAR ? scale * fast_exp2(gi - sm.gt[s_]) : scale;
-          v[r] = i >= s_ ? a[r] * f : 0.f;
-        }
-        // one bf16 Aqk, as FLA's chunk_bwd_dv_local rounds A before its dot with dO
-        bf16x4 hi;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) hi[r] = to_bf16(v[r]);
-        *reinterpret_cast<bf16x4*>(sm.ah + tr_off<8>(i, 16 * Is + 4 * (l >> 4))) = hi;
-      }
+    if constexpr (INL && !SP) {
+      form_S(0);
       lds_barrier();
     }
 
@@ -261,7 +361,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       f32x4 a = zero4();
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag_tr<16>(sm.q, 32 * ks, 16 * rt),
+        a = mfma(frag_tr<16>(sm.q[pb], 32 * ks, 16 * rt),
                  frag_tr<CHV>(INL && GATE == GATE_SCALAR ? sm.dOg : sm.dO, 32 * ks, 16 * (ct0 + j)), a);
       xq[j] = a;
     }
@@ -275,7 +375,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
             const bf16x8 bo = frag_tr<CHV>(sm.dO, 32 * ks, 16 * ct);
-            a = mfma(frag_tr<8>(sm.ah, 32 * ks, 16 * drow), bo, a);
+            a = mfma(frag_tr<8>(sm.ah[pb], 32 * ks, 16 * drow), bo, a);
           }
         } else {
           const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
@@ -290,13 +390,13 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
           f32x4 b = zero4();
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks)
-            b = mfma(frag(&sm.k[16 * drow][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), b);
+            b = mfma(frag(&sm.k[pb][16 * drow][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), b);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) a[r] += b[r] * fast_exp2(sm.gt[C] - sm.gt[16 * drow + 4 * (l >> 4) + r]);
+          for (int r = 0; r < 4; ++r) a[r] += b[r] * fast_exp2(sm.gt[pb][C] - sm.gt[pb][16 * drow + 4 * (l >> 4) + r]);
         } else {
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks)
-            a = mfma(frag(&sm.k[16 * drow][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), a);
+            a = mfma(frag(&sm.k[pb][16 * drow][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), a);
         }
         bf16x4 v4;
 #pragma unroll
@@ -307,19 +407,21 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     lds_barrier();
 
     // dh <- lambda * dh + scale * X - w^T dR   (accumulated negated: -a + w^T dR)
+    const float lam_inl = INL && GATE == GATE_SCALAR ? fast_exp2(sm.gt[pb][C]) : 1.f;
 #pragma unroll
     for (int j = 0; j < NCW; ++j) {
       f32x4 a;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int kr = 16 * rt + 4 * (l >> 4) + r;
-        a[r] = -(st[j][r] * sm.lam[kr] + scale * xq[j][r]);
+        a[r] = -(st[j][r] * (INL ? lam_inl : sm.lam[kr]) + scale * xq[j][r]);
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
         a = mfma(frag_tr<16>(sm.w, 32 * ks, 16 * rt), frag(&sm.drT[16 * (ct0 + j)][32 * ks], S::LDT), a);
       st[j] = -a;
     }
+    if constexpr (SP) form_S(pb ^ 1);      // chunk c - 1's Aqk, beside the stores
 
     // global stores of dh[c] and dR_c from the transposed LDS copies: per wave task a block of
     // 16 columns (dh rows k / dR rows t) by 32 value rows, 16-lane group g taking 8 of them
