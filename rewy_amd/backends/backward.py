@@ -139,7 +139,7 @@ def _recompute_vector(q, k, v, g, Akk, initial_state, gates, vl=None, vf=False):
     """The recompute policy: w, qg, kg, h, v_new -- in one sweep (fdr_fwd_h_wy: w / u formed
     inside the forward scan, u never written) when that pays, else fdr_prepare_wu then fdr_fwd_h."""
     N = q.shape[0] if vl is None else vl.N
-    if ops.fwd_h_wy_pays(N, v.shape[2], ops.GATE_VECTOR):
+    if ops.fwd_h_wy_pays(N, v.shape[2], ops.GATE_VECTOR, vl):
         b = None if gates.get("b") is None else _bf(gates["b"])
         w = None if gates.get("w") is None else _bf(gates["w"])
         sw = ops.fwd_h_wy(k, v, Akk, g, ops.GATE_VECTOR, beta=_f32(gates.get("beta")), q=q, b=b, w=w,
@@ -221,7 +221,7 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
     inline = not affine and (vl is not None or ops.state_form(q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK)
                              == "direct")
     if inline:
-        if ops.fwd_h_wy_pays(q.shape[0] if vl is None else vl.N, v.shape[2], gate):
+        if ops.fwd_h_wy_pays(q.shape[0] if vl is None else vl.N, v.shape[2], gate, vl):
             sw = ops.fwd_h_wy(k, v, A, g, gate, beta=beta, h0=_f32(initial_state), varlen=vl,
                               state_v_first=state_v_first)
             w, h, v_new = sw["w"], sw["h"], sw["v_new"]

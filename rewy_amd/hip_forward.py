@@ -47,7 +47,7 @@ def chunk_forward_hip(op, q, k, v, g=None, beta=None, b=None, w=None, initial_st
     vec = gm == ops.GATE_VECTOR
     N, H = (B if varlen is None else varlen.N), v.shape[2]
     if fuse_scan is None:
-        fuse_scan = not ops._use_affine("auto", N, H, T // ops.CHUNK) and ops.fwd_h_wy_pays(N, H, gm)
+        fuse_scan = not ops._use_affine("auto", N, H, T // ops.CHUNK) and ops.fwd_h_wy_pays(N, H, gm, varlen)
     if fuse_scan:
         wu = ops.fwd_h_wy(k, v, Akk, gc, gm, beta=beta, q=q if vec else None, b=b, w=w, h0=h0,
                           want_final=output_final_state, varlen=varlen, state_v_first=state_v_first)

@@ -129,6 +129,7 @@ class Varlen:
         self.N = int(lens.numel())
         self.T = int(host[-1])
         self.NC = int(nch.sum())
+        self.max_chunks = int(nch.max())
         if self.NC == 0:
             raise ValueError("a variable-length batch needs at least one token")
         self.aligned = bool((host % CHUNK == 0).all())
@@ -641,13 +642,20 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
     return h, vnew, ht
 
 
-def fwd_h_wy_pays(N, H, gate_mode):
+def fwd_h_wy_pays(N, H, gate_mode, varlen=None):
     """Whether ``fwd_h_wy`` beats ``prepare_wu`` + ``fwd_h`` for N rows (sequences) of H heads.
     Each value-tile work-group forms the whole w (and, for a vector gate, every qg / kg / E
     exponential) of its chunk, so that work is repeated once per value tile of a head.  The
     default tiles are 64 wide from 2 N H >= 256 work-groups, 32 wide from 4 N H >= 256, else
     16 wide.  Measured: at 64-wide tiles the sweep wins for every family; at 32-wide ones the
-    scalar / no-gate families still win and the vector gates lose; at 16-wide ones all lose."""
+    scalar / no-gate families still win and the vector gates lose; at 16-wide ones all lose.
+    A packed batch (``varlen``) scans for as long as its longest sequence, which then carries
+    the sweep's extra work on every one of its chunks while the pair's ``prepare_wu`` spreads
+    it over all chunks: it takes the sweep only when its sequences are near one length
+    (longest x N <= 1.5 x all chunks; ten sequences of 300-8192 tokens measured 3.86 ms fused
+    vs 3.64 ms with the pair)."""
+    if varlen is not None and varlen.max_chunks * varlen.N > 1.5 * varlen.NC:
+        return False
     if gate_mode == GATE_VECTOR:
         return 2 * N * H >= 256
     return 4 * N * H >= 256

@@ -135,3 +135,20 @@ def test_ctypes_signatures_match_the_header_parameter_by_parameter():
     for name, params in _header_params().items():
         got = [kind[t] for t in _lib.SIGNATURES[name]]
         assert got == params, (name, "".join(got), "".join(params))
+
+
+def test_fused_scan_rule():
+    """ops.fwd_h_wy_pays: by value-tile width (64-wide from 2 N H >= 256 work-groups, 32-wide
+    from 4 N H >= 256) and, for a packed batch, by how far its longest sequence sets the scan"""
+    import torch
+    from rewy_amd import ops
+    V, S, N0 = ops.GATE_VECTOR, ops.GATE_SCALAR, ops.GATE_NONE
+    assert ops.fwd_h_wy_pays(8, 16, V) and ops.fwd_h_wy_pays(8, 16, S)
+    assert not ops.fwd_h_wy_pays(2, 32, V) and ops.fwd_h_wy_pays(2, 32, S)      # 32-wide tiles
+    assert not ops.fwd_h_wy_pays(2, 16, S) and not ops.fwd_h_wy_pays(2, 16, N0)  # 16-wide tiles
+    even = ops.Varlen([0, 4096, 8192, 12288, 16384, 20480, 24576, 28672, 32768], "cpu")
+    skewed = ops.Varlen(torch.tensor([0, 8192, 4096, 2048, 2048, 1024, 512, 300, 7000, 3000, 4548]).cumsum(0),
+                        "cpu")
+    assert even.max_chunks == 64 and skewed.max_chunks == 128 and skewed.NC == 514
+    assert ops.fwd_h_wy_pays(even.N, 16, V, even)
+    assert not ops.fwd_h_wy_pays(skewed.N, 16, V, skewed)
