@@ -621,7 +621,8 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       bf16x8 eh, kg;
       if constexpr (VEC) {
         const bf16x8 qx = __builtin_bit_cast(bf16x8, rq[i]);
-        const bf16x8 bx = __builtin_bit_cast(bf16x8, rb[i]);
+        bf16x8 bx = {};
+        if constexpr (VEC_B) bx = __builtin_bit_cast(bf16x8, rb[i]);
         bf16x8 qg;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -654,10 +655,15 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       const int p = tid + NTH * i;
       if (NPU % NTH == 0 || p < NPU) {
         const bf16x8 vx = __builtin_bit_cast(bf16x8, rv[i]);
-        const bf16x8 wx = __builtin_bit_cast(bf16x8, rwg[i]);
         bf16x8 zh;
+        if constexpr (VEC_B) {
+          const bf16x8 wx = __builtin_bit_cast(bf16x8, rwg[i]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) zh[j] = to_bf16((VEC_B ? to_f32(wx[j]) : rb_v[i]) * to_f32(vx[j]));
+          for (int j = 0; j < 8; ++j) zh[j] = to_bf16(to_f32(wx[j]) * to_f32(vx[j]));
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) zh[j] = to_bf16(rb_v[i] * to_f32(vx[j]));
+        }
         store_tr_chunk<CHV>(sm.z, p / CHV, p % CHV, __builtin_bit_cast(u32x4, zh));
       }
     }
