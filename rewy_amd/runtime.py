@@ -16,8 +16,8 @@ Where the platform forces a difference:
   7-product formulation (``rewy_amd.original``) instead of FLA;
 * ``check_baseline`` fingerprints this package's HIP library against the
   sources it was built from (the reference seals FLA's sources, :52-67);
-* packed variable-length batches (``cu_seqlens``) are accepted: the state
-  scans take per-sequence chunk offsets natively (the reference rejects them);
+* packed variable-length batches (``cu_seqlens``) are accepted: every kernel takes
+  the batch's chunk map, sequences starting anywhere (the reference rejects them);
 * grouped value heads (HV a multiple of H) are accepted for KDA, GDN and DeltaNet:
   the kernels map value heads to q / k heads themselves (the reference rejects them).
 """
