@@ -32,14 +32,17 @@ struct StateSmem {
   // the kernel)
   static constexpr bool SP = INL && BV == 64;
   static constexpr int NB = SP ? 2 : 1;
+  // Outside SP the tiles a step's tail reads (dh^T for the stores, w and lambda for the
+  // update) are double-buffered by chunk parity instead, so a step starts without a barrier
+  static constexpr int ND = SP ? 1 : 2;
   bf16 k[NB][C][LDK];      // kg rows:  A operand of kg * dh           (contraction over K, row reads)
   bf16 q[NB][C * KD];      // qg rows:  A operand of qg^T dO           (over T, transposed reads)
-  bf16 w[C * KD];          // w rows:   A operand of w^T dR            (over T, transposed reads)
+  bf16 w[ND][C * KD];      // w rows:   A operand of w^T dR            (over T, transposed reads)
   bf16 ah[NB][C * C];      // Aqk rows [t][s], bf16: A operand of Aqk^T dO (over T, transposed reads)
   bf16 dO[C * BV];         // dO rows [t][v]: B operand of both        (over T, transposed reads)
-  bf16 dhT[BV][LDK];       // dh^T:    B operand of kg * dh
+  bf16 dhT[ND][BV][LDK];   // dh^T:    B operand of kg * dh
   bf16 drT[BV][LDT];       // dR^T:    B operand of w^T dR
-  float lam[KD];           // exp2(g_last) per key row
+  float lam[ND][KD];       // exp2(g_last) per key row
   // in-kernel Aqk (INL, scalar / no gate): k and q are staged raw; qg^T dO is formed as
   // q^T (2^g dO) and kg dh as 2^(g_last - g_t) (k dh)
   bf16 dOg[(INL && GATE == GATE_SCALAR) ? C * BV : 1];   // 2^(g_t) dO rows (swizzled)
@@ -168,13 +171,13 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     }
   };
 
-  auto stage_chunk = [&]() {
+  auto stage_chunk = [&](int db) {
     if constexpr (GATE == GATE_VECTOR) {
-      if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
+      if (tid < KD) sm.lam[db][tid] = fast_exp2(rg_last);
     } else if constexpr (GATE == GATE_SCALAR) {
-      if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
+      if (tid < KD) sm.lam[db][tid] = fast_exp2(rg_last);
     } else {
-      if (tid < KD) sm.lam[tid] = 1.f;
+      if (tid < KD) sm.lam[db][tid] = 1.f;
     }
 #pragma unroll
     for (int i = 0; i < NPI; ++i) {
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       }
       *reinterpret_cast<u32x4*>(&sm.k[0][t][ch * 8]) = kq;
       store_tr_chunk<16>(sm.q[0], t, ch, qq);
-      store_tr_chunk<16>(sm.w, t, ch, rw[i]);
+      store_tr_chunk<16>(sm.w[db], t, ch, rw[i]);
       if constexpr (DV_FROM_AQK) {
         // Aqk as one bf16, the precision of the reference's dv_local (FLA's dAv rounds A to
         // the dO dtype before its dot: kernels/kda_residual_npu_onchip.py:114-116)
@@ -260,11 +263,11 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     }
     if (tid == 0) sm.gt[pb][C] = GATE == GATE_SCALAR ? rg_last : 0.f;
   };
-  auto stage_B = [&]() {
+  auto stage_B = [&](int db) {
 #pragma unroll
     for (int i = 0; i < NPI; ++i) {
       const int p = tid + NTH * i;
-      store_tr_chunk<16>(sm.w, p >> 4, p & 15, rw[i]);
+      store_tr_chunk<16>(sm.w[db], p >> 4, p & 15, rw[i]);
     }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
@@ -322,21 +325,25 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   }
   for (int c = NT - 1; c >= 0; --c) {
     const int pb = SP ? (c & 1) : 0;     // this chunk's k / q / Aqk / gate buffer
-    lds_barrier();                       // previous chunk done with every LDS tile
+    const int db = S::ND == 2 ? (c & 1) : 0;   // and its dh^T / w / lambda buffer
+    // SP: the previous chunk done with every LDS tile.  Otherwise every tile written before
+    // the next barrier was last read before the previous chunk's last barrier, or has a
+    // buffer of its own (dh^T, w, lambda), so no barrier is needed here.
+    if constexpr (SP) lds_barrier();
     if constexpr (SP) {
-      stage_B();                           // chunk c
+      stage_B(0);                          // chunk c
       stage_A(pb ^ 1);                     // chunk c - 1 (the last step stages chunk 0 again)
       load_B(c > 0 ? c - 1 : 0);
       load_A(c > 1 ? c - 2 : 0);
     } else if constexpr (INL) {
-      stage_B();
+      stage_B(db);
       stage_A(0);
       if (c > 0) {
         load_A(c - 1);
         load_B(c - 1);
       }
     } else {
-      stage_chunk();
+      stage_chunk(db);
       if (c > 0) load_chunk(c - 1);          // prefetch; consumed next iteration
     }
     // dh (state at the end of chunk c) -> LDS, transposed, bf16
@@ -345,7 +352,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       bf16x4 v4;
 #pragma unroll
       for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[j][r]);
-      *reinterpret_cast<bf16x4*>(&sm.dhT[16 * (ct0 + j) + (l & 15)][16 * rt + 4 * (l >> 4)]) = v4;
+      *reinterpret_cast<bf16x4*>(&sm.dhT[db][16 * (ct0 + j) + (l & 15)][16 * rt + 4 * (l >> 4)]) = v4;
     }
     lds_barrier();
 
@@ -390,13 +397,13 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
           f32x4 b = zero4();
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks)
-            b = mfma(frag(&sm.k[pb][16 * drow][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), b);
+            b = mfma(frag(&sm.k[pb][16 * drow][32 * ks], S::LDK), frag(&sm.dhT[db][16 * ct][32 * ks], S::LDK), b);
 #pragma unroll
           for (int r = 0; r < 4; ++r) a[r] += b[r] * fast_exp2(sm.gt[pb][C] - sm.gt[pb][16 * drow + 4 * (l >> 4) + r]);
         } else {
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks)
-            a = mfma(frag(&sm.k[pb][16 * drow][32 * ks], S::LDK), frag(&sm.dhT[16 * ct][32 * ks], S::LDK), a);
+            a = mfma(frag(&sm.k[pb][16 * drow][32 * ks], S::LDK), frag(&sm.dhT[db][16 * ct][32 * ks], S::LDK), a);
         }
         bf16x4 v4;
 #pragma unroll
@@ -404,21 +411,22 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
         *reinterpret_cast<bf16x4*>(&sm.drT[16 * ct + (l & 15)][16 * drow + 4 * (l >> 4)]) = v4;
       }
     }
+    // (read before the barrier: without SP the next chunk's staging may overwrite the gates)
+    const float lam_inl = INL && GATE == GATE_SCALAR ? fast_exp2(sm.gt[pb][C]) : 1.f;
     lds_barrier();
 
     // dh <- lambda * dh + scale * X - w^T dR   (accumulated negated: -a + w^T dR)
-    const float lam_inl = INL && GATE == GATE_SCALAR ? fast_exp2(sm.gt[pb][C]) : 1.f;
 #pragma unroll
     for (int j = 0; j < NCW; ++j) {
       f32x4 a;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int kr = 16 * rt + 4 * (l >> 4) + r;
-        a[r] = -(st[j][r] * (INL ? lam_inl : sm.lam[kr]) + scale * xq[j][r]);
+        a[r] = -(st[j][r] * (INL ? lam_inl : sm.lam[db][kr]) + scale * xq[j][r]);
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag_tr<16>(sm.w, 32 * ks, 16 * rt), frag(&sm.drT[16 * (ct0 + j)][32 * ks], S::LDT), a);
+        a = mfma(frag_tr<16>(sm.w[db], 32 * ks, 16 * rt), frag(&sm.drT[16 * (ct0 + j)][32 * ks], S::LDT), a);
       st[j] = -a;
     }
     if constexpr (SP) form_S(pb ^ 1);      // chunk c - 1's Aqk, beside the stores
@@ -440,7 +448,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
         const int tk = wv + NW * i;
         if (NTK % NW != 0 && tk >= NTK) break;
         const int kr0 = 16 * (tk % (KD / 16)), v0 = 8 * ((4 * (tk / (KD / 16)) + g4) % RB);
-        const bf16x8 o = col8_tr(&sm.dhT[0][0], S::LDK, v0, kr0, l);
+        const bf16x8 o = col8_tr(&sm.dhT[db][0][0], S::LDK, v0, kr0, l);
         *reinterpret_cast<bf16x8*>(dh_out + dh_base + (size_t)(kr0 + (l & 15)) * VD + v_base + v0) = o;
       }
       const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
