@@ -261,12 +261,14 @@ template <int BV, int GATE>
 struct FwdSmem {
   static constexpr int LDK = KD + 8;
   static constexpr int LDT = C + 8;
+  // kg, h^T and lambda, which a step's tail reads (the update, the stores), per chunk parity,
+  // so a step starts without a barrier
   bf16 w[C][LDK];          // w rows: A operand of w h           (contraction over K)
-  bf16 k[C * KD];          // kg rows (swizzled): A operand of kg^T v_new (over T, transposed reads)
-  bf16 hT[BV][LDK];        // h^T:    B operand of w h
+  bf16 k[2][C * KD];       // kg rows (swizzled): A operand of kg^T v_new (over T, transposed reads)
+  bf16 hT[2][BV][LDK];     // h^T:    B operand of w h
   bf16 vT[BV][LDT];        // v_new^T: B operand of kg^T v_new
   bf16 u[C * BV];          // u rows [t][v] (swizzled): read transposed in the accumulator layout
-  float lam[KD];
+  float lam[2][KD];
 };
 
 template <int BV, int GATE, bool MAP>
@@ -354,13 +356,13 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
           rs_.src(u + (tok0 + p / CHV) * rsv + (size_t)h * VD + v_base + (p % CHV) * 8, p / CHV));
     }
   };
-  auto stage_chunk = [&]() {
+  auto stage_chunk = [&](int db) {
     if constexpr (GATE == RG_VECTOR) {
-      if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
+      if (tid < KD) sm.lam[db][tid] = fast_exp2(rg_last);
     } else if constexpr (GATE == RG_SCALAR) {
-      if (tid < KD) sm.lam[tid] = fast_exp2(rg_last);
+      if (tid < KD) sm.lam[db][tid] = fast_exp2(rg_last);
     } else {
-      if (tid < KD) sm.lam[tid] = 1.f;
+      if (tid < KD) sm.lam[db][tid] = 1.f;
     }
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
@@ -378,7 +380,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
       u32x4 kq = rk[i];
       // scalar gate: kg = k 2^(g_last - g_t), the row's factor from registers
       if constexpr (GATE == RG_SCALAR) kq = scale_bf16x8(kq, fast_exp2(rg_last - rg_tok[i]));
-      store_tr_chunk<16>(sm.k, p >> 4, p & 15, kq);
+      store_tr_chunk<16>(sm.k[db], p >> 4, p & 15, kq);
     }
   };
 
@@ -399,8 +401,10 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     settle_chunk();
   }
   for (int c = 0; c < NT; ++c) {
-    lds_barrier();
-    stage_chunk();
+    // no barrier: w and u were last read before the previous step's last barrier, and kg,
+    // h^T and lambda have a buffer per chunk parity
+    const int db = c & 1;
+    stage_chunk(db);
     load_chunk(c + 1 < NT ? c + 1 : c);    // (the last chunk re-fetches itself: no branch)
     const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
     const size_t tok0 = rs_.tok0;
@@ -410,7 +414,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
       bf16x4 v4;
 #pragma unroll
       for (int r = 0; r < 4; ++r) v4[r] = to_bf16(st[ct][r]);
-      *reinterpret_cast<bf16x4*>(&sm.hT[16 * ct + (l & 15)][16 * wv + 4 * (l >> 4)]) = v4;
+      *reinterpret_cast<bf16x4*>(&sm.hT[db][16 * ct + (l & 15)][16 * wv + 4 * (l >> 4)]) = v4;
     }
     lds_barrier();
     // v_new tiles = u - w h
@@ -426,7 +430,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
         for (int r = 0; r < 4; ++r) a[r] = -to_f32(u4[r]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
-          a = mfma(frag(&sm.w[16 * drow][32 * ks], S::LDK), frag(&sm.hT[16 * ct][32 * ks], S::LDK), a);
+          a = mfma(frag(&sm.w[16 * drow][32 * ks], S::LDK), frag(&sm.hT[db][16 * ct][32 * ks], S::LDK), a);
         bf16x4 v4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) v4[r] = to_bf16(-a[r]);
@@ -439,10 +443,10 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
     for (int ct = 0; ct < NCT; ++ct) {
       f32x4 a;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) a[r] = st[ct][r] * sm.lam[16 * wv + 4 * (l >> 4) + r];
+      for (int r = 0; r < 4; ++r) a[r] = st[ct][r] * sm.lam[db][16 * wv + 4 * (l >> 4) + r];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag_tr<16>(sm.k, 32 * ks, 16 * wv), frag(&sm.vT[16 * ct][32 * ks], S::LDT), a);
+        a = mfma(frag_tr<16>(sm.k[db], 32 * ks, 16 * wv), frag(&sm.vT[16 * ct][32 * ks], S::LDT), a);
       st[ct] = a;
     }
     // stores of h_c and v_new_c from the transposed LDS copies (lanes run over rows)
@@ -458,7 +462,7 @@ __global__ __launch_bounds__(512) void fwd_h_kernel(
       for (int i = 0; i < (NTK + NW - 1) / NW; ++i) {
         const int tk = (wv + NW * i) % NTK;
         const int kr0 = 16 * (tk % (KD / 16)), v0 = 8 * ((4 * (tk / (KD / 16)) + (l >> 4)) % RB);
-        const bf16x8 o = col8_tr(&sm.hT[0][0], S::LDK, v0, kr0, l);
+        const bf16x8 o = col8_tr(&sm.hT[db][0][0], S::LDK, v0, kr0, l);
         *reinterpret_cast<bf16x8*>(h_out + hb + (size_t)(kr0 + (l & 15)) * VD + v_base + v0) = o;
       }
 #pragma unroll
