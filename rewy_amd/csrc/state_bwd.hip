@@ -531,12 +531,12 @@ struct XferSmem {
   static constexpr int LDT = C + 8;
   bf16 k[C][LDK];
   bf16 q[C * KD];
-  bf16 w[C * KD];
+  bf16 w[2][C * KD];       // per chunk parity (read by the update, after a step's last barrier)
   bf16 ah[C * C];          // Aqk rows [t][s], bf16
   bf16 dO[C * 64];         // the Q half's 64 value columns
   bf16 dhT[128][LDK];      // state^T: columns 0-63 of P's half, 64-127 of Q's
   bf16 drT[128][LDT];
-  float lam[KD];
+  float lam[2][KD];        // per chunk parity, as w
 };
 
 template <int GATE, bool DV_FROM_AQK>
@@ -596,8 +596,8 @@ __global__ __launch_bounds__(512) void state_xfer_kernel(
     }
     rdo = *reinterpret_cast<const u32x4*>(dO + (tok0 + tid / CHV) * rsv + (size_t)h * VD + base + (tid % CHV) * 8);
   };
-  auto stage_chunk = [&]() {
-    if (tid < KD) sm.lam[tid] = GATE == GATE_NONE ? 1.f : fast_exp2(rg_last);
+  auto stage_chunk = [&](int db) {
+    if (tid < KD) sm.lam[db][tid] = GATE == GATE_NONE ? 1.f : fast_exp2(rg_last);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i;
@@ -609,7 +609,7 @@ __global__ __launch_bounds__(512) void state_xfer_kernel(
       }
       *reinterpret_cast<u32x4*>(&sm.k[t][ch * 8]) = kq;
       store_tr_chunk<16>(sm.q, t, ch, qq);
-      store_tr_chunk<16>(sm.w, t, ch, rw[i]);
+      store_tr_chunk<16>(sm.w[db], t, ch, rw[i]);
       if constexpr (DV_FROM_AQK) {
         bf16x4 hi;                           // one bf16 Aqk, as the direct kernel
 #pragma unroll
@@ -623,8 +623,11 @@ __global__ __launch_bounds__(512) void state_xfer_kernel(
 
   if (NT > 0) load_chunk(NT - 1);
   for (int c = NT - 1; c >= 0; --c) {
-    lds_barrier();
-    stage_chunk();
+    // no barrier: every tile written before the next one was last read before the previous
+    // step's last barrier (nothing per chunk is stored), except w and lambda, which the update
+    // reads after it and which have a buffer per chunk parity
+    const int db = c & 1;
+    stage_chunk(db);
     if (c > 0) load_chunk(c - 1);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -680,11 +683,11 @@ __global__ __launch_bounds__(512) void state_xfer_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int kr = 16 * rt + 4 * (l >> 4) + r;
-        a[r] = -(st[j][r] * sm.lam[kr] + (j >= 4 ? scale * xq[j - 4][r] : 0.f));
+        a[r] = -(st[j][r] * sm.lam[db][kr] + (j >= 4 ? scale * xq[j - 4][r] : 0.f));
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag_tr<16>(sm.w, 32 * ks, 16 * rt), frag(&sm.drT[16 * j][32 * ks], S::LDT), a);
+        a = mfma(frag_tr<16>(sm.w[db], 32 * ks, 16 * rt), frag(&sm.drT[16 * j][32 * ks], S::LDT), a);
       st[j] = -a;
     }
   }
