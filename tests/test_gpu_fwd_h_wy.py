@@ -64,14 +64,15 @@ def test_fwd_h_wy_state_layouts_and_grouped_heads(op, vf):
     _both(op, a, vf=vf, h0=h0)
 
 
+@pytest.mark.parametrize("vb", [0, 64])
 @pytest.mark.parametrize("lens", [[128, 64, 256], [100, 37, 0, 64, 1, 150]])
 @pytest.mark.parametrize("op", ["gdn", "delta", "kda", "gdn2"])
-def test_fwd_h_wy_packed(op, lens):
+def test_fwd_h_wy_packed(op, lens, vb):
     """gc and Akk from the HIP forward of the packed batch itself (per-sequence chunk-local
     gate cumsums: a vector gate's 2^(g_last - g) is bounded only then)"""
     from rewy_amd import ops
     from rewy_amd.hip_forward import chunk_forward_hip
-    print(f"\n[fwd_h_wy] packed op={op} lens={lens}", flush=True)
+    print(f"\n[fwd_h_wy] packed op={op} lens={lens} vb={vb}", flush=True)
     T = sum(lens)
     dev = torch.device("cuda")
     xs, _ = make_inputs(op, 1, T, 2, seed=63)
@@ -82,7 +83,7 @@ def test_fwd_h_wy_packed(op, lens):
     a = dict(q=xs["q"], k=xs["k"], v=xs["v"], A=sv["Akk"], g=sv["gc"] if op != "delta" else None,
              beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"))
     h0 = (torch.randn(len(lens), 2, 128, 128, generator=torch.Generator().manual_seed(64)) * 0.05).to(dev)
-    _both(op, a, varlen=vl, h0=h0)
+    _both(op, a, vb=vb, varlen=vl, h0=h0)
 
 
 def test_fwd_h_wy_against_the_oracle():

@@ -118,3 +118,47 @@ def test_inline_aqk_packed_unaligned(op):
         e = float((a.double() - b.double()).norm() / b.double().norm().clamp_min(1e-30))
         print(n, e, flush=True)
         assert e <= tol, (n, e)
+
+
+@pytest.mark.parametrize("op", ["gdn", "delta"])
+@pytest.mark.parametrize("vb", [16, 32, 64])
+def test_inline_aqk_packed_every_tile_width(op, vb):
+    """The in-kernel-Aqk recurrence on a packed batch whose sequences start anywhere, at every
+    value-tile width (64-wide tiles form each chunk's Aqk one step ahead): against the same
+    batch zero-padded to whole chunks on the dense kernel with chunk offsets.  DeltaNet bit for
+    bit; GDN within rel-L2 1e-4 (g_last, as above)."""
+    from rewy_amd import ops
+    from tests.test_gpu_varlen_unaligned import LENS, _pad, _unpad
+    print(f"\n[inline-aqk] packed every tile width op={op} vb={vb}", flush=True)
+    lens, H = LENS, 2
+    T = sum(lens)
+    dev = torch.device("cuda")
+    gen = torch.Generator().manual_seed(46)
+    bf = torch.bfloat16
+    q = torch.nn.functional.normalize(torch.randn(1, T, H, 128, generator=gen), dim=-1).to(bf)
+    k = torch.nn.functional.normalize(torch.randn(1, T, H, 128, generator=gen), dim=-1).to(bf)
+    w = (torch.randn(1, T, H, 128, generator=gen) * 0.1).to(bf)
+    dO = torch.randn(1, T, H, 128, generator=gen).to(bf)
+    dht = torch.randn(len(lens), H, 128, 128, generator=gen) * 0.05
+    g = None
+    if op == "gdn":
+        # chunk-local cumsum (log2) of each sequence's decays, the padded rows adding zero
+        inc = torch.nn.functional.logsigmoid(torch.randn(1, T, H, generator=gen) * 0.5 + 4)
+        inc_p = _pad(inc, lens)
+        g_p = inc_p.view(1, -1, 64, H).cumsum(2).view(1, -1, H) / 0.6931471805599453
+        g = _unpad(g_p, lens).contiguous()
+    cu = lambda x: None if x is None else x.to(dev).contiguous()
+    gate = GATE[op]
+    vl = ops.Varlen(torch.tensor([0] + lens).cumsum(0), dev)
+    vl_p = ops.Varlen(torch.tensor([0] + [-(-L // 64) * 64 for L in lens]).cumsum(0), dev)
+    got = ops.state_bwd(cu(q), cu(k), cu(w), cu(g), gate, cu(dO), 0.088, dht=cu(dht), value_block=vb,
+                        method="direct", varlen=vl)
+    P = lambda x: None if x is None else cu(_pad(x, lens))
+    ref = ops.state_bwd(P(q), P(k), P(w), None if g is None else cu(g_p), gate, P(dO), 0.088, dht=cu(dht),
+                        value_block=vb, method="direct", varlen=vl_p)
+    torch.cuda.synchronize()
+    tol = 0.0 if op == "delta" else 1e-4
+    for n, a, b in (("dh", got[0], ref[0]), ("dR", got[1], _unpad(ref[1], lens)), ("dh0", got[2], ref[2])):
+        e = float((a.double() - b.double()).norm() / b.double().norm().clamp_min(1e-30))
+        print(n, e, flush=True)
+        assert e <= tol, (n, e)
