@@ -218,64 +218,72 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   // form its S tiles before its dR.
   constexpr bool SP = S::SP;
   auto load_A = [&](int c) {
-    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
-    const size_t tok0 = rs_.tok0;
-    if constexpr (GATE == GATE_SCALAR) {
+    if constexpr (INL) {
+      const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+      const size_t tok0 = rs_.tok0;
+      if constexpr (GATE == GATE_SCALAR) {
 #pragma unroll
-      for (int i = 0; i < NPI; ++i) rg_tok[i] = g[(tok0 + rs_.clamp((tid + NTH * i) >> 4)) * H + h];
-      rg_last = g[(tok0 + rs_.clamp(C - 1)) * H + h];
-    }
-    const QKRows qr = qk_rows(tok0, h, H, HQ);
+        for (int i = 0; i < NPI; ++i) rg_tok[i] = g[(tok0 + rs_.clamp((tid + NTH * i) >> 4)) * H + h];
+        rg_last = g[(tok0 + rs_.clamp(C - 1)) * H + h];
+      }
+      const QKRows qr = qk_rows(tok0, h, H, HQ);
 #pragma unroll
-    for (int i = 0; i < NPI; ++i) {
-      const int p = tid + NTH * i;
-      const size_t oq = qr.ofs + (size_t)(p >> 4) * qr.rs + (p & 15) * 8;
-      rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + oq, p >> 4));
-      rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + oq, p >> 4));
+      for (int i = 0; i < NPI; ++i) {
+        const int p = tid + NTH * i;
+        const size_t oq = qr.ofs + (size_t)(p >> 4) * qr.rs + (p & 15) * 8;
+        rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + oq, p >> 4));
+        rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + oq, p >> 4));
+      }
     }
   };
   auto load_B = [&](int c) {
-    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
-    const size_t tok0 = rs_.tok0;
-    const size_t kofs = tok0 * row_stride_k + (size_t)h * KD;
+    if constexpr (INL) {
+      const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+      const size_t tok0 = rs_.tok0;
+      const size_t kofs = tok0 * row_stride_k + (size_t)h * KD;
 #pragma unroll
-    for (int i = 0; i < NPI; ++i) {
-      const int p = tid + NTH * i;
-      rw[i] = *reinterpret_cast<const u32x4*>(rs_.src(w + kofs + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8, p >> 4));
-    }
+      for (int i = 0; i < NPI; ++i) {
+        const int p = tid + NTH * i;
+        rw[i] = *reinterpret_cast<const u32x4*>(rs_.src(w + kofs + (size_t)(p >> 4) * row_stride_k + (p & 15) * 8, p >> 4));
+      }
 #pragma unroll
-    for (int i = 0; i < NDO; ++i) {
-      const int p = min(tid + NTH * i, NPD - 1);
-      rdo[i] = *reinterpret_cast<const u32x4*>(
-          rs_.src(dO + (tok0 + p / CHV) * row_stride_v + (size_t)h * VD + v_base + (p % CHV) * 8, p / CHV));
-      if constexpr (GATE == GATE_SCALAR) rg_do[i] = g[(tok0 + rs_.clamp(p / CHV)) * H + h];
+      for (int i = 0; i < NDO; ++i) {
+        const int p = min(tid + NTH * i, NPD - 1);
+        rdo[i] = *reinterpret_cast<const u32x4*>(
+            rs_.src(dO + (tok0 + p / CHV) * row_stride_v + (size_t)h * VD + v_base + (p % CHV) * 8, p / CHV));
+        if constexpr (GATE == GATE_SCALAR) rg_do[i] = g[(tok0 + rs_.clamp(p / CHV)) * H + h];
+      }
     }
   };
   // group A of the registers' chunk into parity buffer `pb`: raw k and q, the row gates
   auto stage_A = [&](int pb) {
+    if constexpr (INL) {
 #pragma unroll
-    for (int i = 0; i < NPI; ++i) {
-      const int p = tid + NTH * i;
-      const int t = p >> 4, ch = p & 15;
-      if (ch == 0) sm.gt[pb][t] = GATE == GATE_SCALAR ? rg_tok[i] : 0.f;
-      *reinterpret_cast<u32x4*>(&sm.k[pb][t][ch * 8]) = rk[i];
-      store_tr_chunk<16>(sm.q[pb], t, ch, rq[i]);
+      for (int i = 0; i < NPI; ++i) {
+        const int p = tid + NTH * i;
+        const int t = p >> 4, ch = p & 15;
+        if (ch == 0) sm.gt[pb][t] = GATE == GATE_SCALAR ? rg_tok[i] : 0.f;
+        *reinterpret_cast<u32x4*>(&sm.k[pb][t][ch * 8]) = rk[i];
+        store_tr_chunk<16>(sm.q[pb], t, ch, rq[i]);
+      }
+      if (tid == 0) sm.gt[pb][C] = GATE == GATE_SCALAR ? rg_last : 0.f;
     }
-    if (tid == 0) sm.gt[pb][C] = GATE == GATE_SCALAR ? rg_last : 0.f;
   };
   auto stage_B = [&](int db) {
+    if constexpr (INL) {
 #pragma unroll
-    for (int i = 0; i < NPI; ++i) {
-      const int p = tid + NTH * i;
-      store_tr_chunk<16>(sm.w[db], p >> 4, p & 15, rw[i]);
-    }
+      for (int i = 0; i < NPI; ++i) {
+        const int p = tid + NTH * i;
+        store_tr_chunk<16>(sm.w[db], p >> 4, p & 15, rw[i]);
+      }
 #pragma unroll
-    for (int i = 0; i < NDO; ++i) {
-      const int p = tid + NTH * i;
-      if (NPD % NTH == 0 || p < NPD) {
-        store_tr_chunk<CHV>(sm.dO, p / CHV, p % CHV, rdo[i]);
-        if constexpr (GATE == GATE_SCALAR)
-          store_tr_chunk<CHV>(sm.dOg, p / CHV, p % CHV, scale_bf16x8(rdo[i], fast_exp2(rg_do[i])));
+      for (int i = 0; i < NDO; ++i) {
+        const int p = tid + NTH * i;
+        if (NPD % NTH == 0 || p < NPD) {
+          store_tr_chunk<CHV>(sm.dO, p / CHV, p % CHV, rdo[i]);
+          if constexpr (GATE == GATE_SCALAR)
+            store_tr_chunk<CHV>(sm.dOg, p / CHV, p % CHV, scale_bf16x8(rdo[i], fast_exp2(rg_do[i])));
+        }
       }
     }
   };
@@ -284,25 +292,27 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   // row i (as the read form stages it); one bf16, as FLA's chunk_bwd_dv_local rounds A before
   // its dot with dO
   auto form_S = [&](int pb) {
+    if constexpr (INL) {
 #pragma unroll
-    for (int tt = wv; tt < 16; tt += NW) {
-      const int Is = tt >> 2, Ji = tt & 3;
-      f32x4 a = zero4();
-      if (Ji >= Is) {                      // wave-uniform: tiles above the diagonal are zero
+      for (int tt = wv; tt < 16; tt += NW) {
+        const int Is = tt >> 2, Ji = tt & 3;
+        f32x4 a = zero4();
+        if (Ji >= Is) {                      // wave-uniform: tiles above the diagonal are zero
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          a = mfma(frag(&sm.k[pb][16 * Is][32 * ks], S::LDK), frag_row<16>(sm.q[pb], 16 * Ji, 32 * ks), a);
+          for (int ks = 0; ks < 4; ++ks)
+            a = mfma(frag(&sm.k[pb][16 * Is][32 * ks], S::LDK), frag_row<16>(sm.q[pb], 16 * Ji, 32 * ks), a);
+        }
+        const int i = 16 * Ji + (l & 15);
+        const float gi = sm.gt[pb][i];
+        bf16x4 hi;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int s_ = 16 * Is + 4 * (l >> 4) + r;
+          const float f = GATE == GATE_SCALAR ? scale * fast_exp2(gi - sm.gt[pb][s_]) : scale;
+          hi[r] = to_bf16(i >= s_ ? a[r] * f : 0.f);
+        }
+        *reinterpret_cast<bf16x4*>(sm.ah[pb] + tr_off<8>(i, 16 * Is + 4 * (l >> 4))) = hi;
       }
-      const int i = 16 * Ji + (l & 15);
-      const float gi = sm.gt[pb][i];
-      bf16x4 hi;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int s_ = 16 * Is + 4 * (l >> 4) + r;
-        const float f = GATE == GATE_SCALAR ? scale * fast_exp2(gi - sm.gt[pb][s_]) : scale;
-        hi[r] = to_bf16(i >= s_ ? a[r] * f : 0.f);
-      }
-      *reinterpret_cast<bf16x4*>(sm.ah[pb] + tr_off<8>(i, 16 * Is + 4 * (l >> 4))) = hi;
     }
   };
 
