@@ -367,6 +367,24 @@ hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, const void* v, 
                                    float scale, hipStream_t stream);
 
 /*
+ * fdr_chunk_bwd_gate_fold over a packed variable-length batch whose sequences start
+ * anywhere (cu_seqlens, chunk_indices and num_chunks as for fdr_chunk_bwd_varlen; rows
+ * past a sequence's end are neither read nor written and add nothing to dA_log /
+ * ddt_bias).  `workspace` holds fdr_chunk_bwd_gate_workspace_bytes(1, 64 * num_chunks, H)
+ * bytes.  Replaces the chunk stage plus the gate backward of the reference's kda_backward
+ * with use_gate_in_kernel and cu_seqlens (backends/backward.py:63-73).
+ */
+hipError_t fdr_chunk_bwd_gate_fold_varlen(const void* q, const void* k, const void* v, const void* v_new,
+                                          const void* dO, const void* dR, const float* g, const float* beta,
+                                          const float* Akk, const void* h, const void* dh, void* dq, void* dk,
+                                          void* dv, float* dbeta, float beta_sigmoid, const void* g_raw,
+                                          int raw_is_bf16, const float* A_log, const float* dt_bias,
+                                          int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
+                                          float* ddt_bias, void* workspace, int h_v_first, const int* cu_seqlens,
+                                          const int* chunk_indices, int num_chunks, int H, int qk_heads, int K,
+                                          int V, int chunk, float scale, hipStream_t stream);
+
+/*
  * fdr_chunk_bwd_gate_fold without the workspace argument.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under HIP
  * graph capture, serving loops or harnesses that forbid hipMalloc).  The per-chunk

@@ -50,7 +50,7 @@ class ChunkFunction(torch.autograd.Function):
         if state_v_first and not native:
             raise ValueError("V-first states in the chunk Function are the optimized GPU path's")
         if gate is not None and not (native and op == "kda"):
-            raise ValueError("the folded gate is the optimized GPU path's (KDA, chunk-aligned batches)")
+            raise ValueError("the folded gate is the optimized GPU path's (KDA)")
         if beta_act is not None and not (native and op != "gdn2"):
             raise ValueError("the folded beta sigmoid is the optimized GPU path's (scalar beta)")
         ctx.gate, ctx.beta_act, ctx.vf = gate, beta_act, bool(state_v_first)
@@ -68,8 +68,6 @@ class ChunkFunction(torch.autograd.Function):
             from ..ops import Varlen
             varlen = None if cu_seqlens is None else Varlen(cu_seqlens, q.device)
             ctx.cu_seqlens = varlen            # the chunk map, reused by the backward
-            if gate is not None and varlen is not None and not varlen.aligned:
-                raise ValueError("the folded gate takes chunk-aligned sequences")
             o, final, sv = chunk_forward_hip(op, q, k, v, g=g, beta=beta, b=b, w=w,
                                              initial_state=initial_state, scale=scale,
                                              output_final_state=output_final_state, varlen=varlen,
@@ -212,12 +210,11 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
     ``gate_fold`` = (lower_bound, A_log, dt_bias) (KDA's raw gate) and ``beta_act`` = s
     (raw beta, activated as s * sigmoid): on the optimized backend on a GPU the
     activations run inside the chunk Function and their backward rides in the chunk
-    kernel (the gate's only for chunk-aligned batches, which the folded kernel takes);
-    otherwise they run here as autograd nodes of their own (padded tokens must keep
+    kernel; otherwise they run here as autograd nodes of their own (padded tokens must keep
     zero activated gates)."""
     H, HV = q.shape[2], v.shape[2]
     native = backend == "optimized" and q.is_cuda
-    bounds = aligned = None
+    bounds = None
     if cu_seqlens is not None:
         if q.shape[0] != 1:
             raise ValueError(f"The batch size is expected to be 1 rather than {q.shape[0]} when using `cu_seqlens`.")
@@ -226,10 +223,9 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
         if h0 is not None and h0.shape[0] != len(bounds):
             raise ValueError(f"The number of initial states is expected to be equal to the number of input "
                              f"sequences, i.e., {len(bounds)} rather than {h0.shape[0]}.")
-        aligned = all(s % 64 == 0 for s, e in bounds) and cu[-1] % 64 == 0
     # no padded tokens anywhere: dense rows of whole chunks, or a packed batch (native)
     unpadded = native and (cu_seqlens is not None or q.shape[1] % 64 == 0)
-    if gate_fold is not None and not (unpadded and (cu_seqlens is None or aligned)):
+    if gate_fold is not None and not unpadded:
         from ..gates import KDAGate
         lb, A_log, dt_bias = gate_fold
         g = KDAGate.apply(g, A_log, dt_bias, lb, native)

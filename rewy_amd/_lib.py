@@ -53,6 +53,8 @@ SIGNATURES = {
     "fdr_l2norm_bwd": [_P, _I, _P, _P, _P, ctypes.c_longlong, _I, _P],
     "fdr_chunk_bwd_gate_fold": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _P, _P, _I,
                                 _F, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P],
+    "fdr_chunk_bwd_gate_fold_varlen": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _P,
+                                       _P, _I, _F, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_chunk_bwd_gate_fold_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _P,
                                         _P, _I, _F, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_affine_scan": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P],

@@ -105,20 +105,11 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
         if saved.get("h") is None:
             saved, hvf = _recompute_vector(q, k, v, g, Akk, initial_state, gates, vl, vf), False
         dh, dR, dh0 = _state_vector(saved, g, do, scale, Aqk, dht, initial_state, vl, vf)
-    # the folded gate backward takes chunk-aligned rows; a packed batch of sequences that
-    # start anywhere runs it after the chunk kernel (one elementwise pass over dg)
-    separate = gate_fold is not None and vl is not None and not vl.aligned
     out = ops.chunk_bwd(q, k, v, _bf(saved["v_new"]), do, dR, g, ops.GATE_VECTOR, Akk,
                         _bf(saved["h"]), dh, scale, beta=_f32(gates.get("beta")),
                         b=None if gates.get("b") is None else _bf(gates["b"]),
                         w=None if gates.get("w") is None else _bf(gates["w"]),
-                        gate_fold=None if separate else gate_fold, beta_sigmoid=beta_sigmoid, h_v_first=hvf,
-                        varlen=vl)
-    if separate:
-        from ..gates import kda_gate_bwd
-        out["dg"], out["dA_log"], out["ddt_bias"] = kda_gate_bwd(
-            out["dg"], gate_fold["g_raw"], gate_fold.get("A_log"), gate_fold.get("dt_bias"),
-            gate_fold.get("lower_bound"), native=True)
+                        gate_fold=gate_fold, beta_sigmoid=beta_sigmoid, h_v_first=hvf, varlen=vl)
     return _group_sum(out, q.shape[2]), dh0
 
 

@@ -277,7 +277,7 @@ __device__ __forceinline__ void chunk_body(
   if (HQ <= 0) HQ = H;
   using LY = PostLayout<GATE, VEC_B, INTRA, PIPE, ORIG>;
   static_assert(!ORIG || (GATE == CG_VECTOR && !VEC_B && !INTRA && !PIPE), "original formulation: KDA only");
-  static_assert(!MAP || (!INTRA && !PIPE && !ORIG && FOLD < 0), "variable-length rows: the plain chunk kernel");
+  static_assert(!MAP || (!INTRA && !PIPE && !ORIG), "variable-length rows: the plain and the gate-fold chunk kernels");
   static_assert(!WY || (GATE == CG_VECTOR && !VEC_B && !INTRA && !PIPE && !ORIG && FOLD < 0 && !MAP),
                 "the WY seam: KDA, dense rows");
   using post::LDT;
@@ -1225,8 +1225,9 @@ __device__ __forceinline__ void chunk_body(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const size_t o = base + (size_t)(16 * I + r) * rsk32;
-          if constexpr (RB) xr[I][r] = to_f32(reinterpret_cast<const bf16*>(gf->graw)[o]);
-          else xr[I][r] = reinterpret_cast<const float*>(gf->graw)[o];
+          const int t = 16 * I + 4 * lg + r;
+          if constexpr (RB) xr[I][r] = to_f32(*rw.src(reinterpret_cast<const bf16*>(gf->graw) + o, t));
+          else xr[I][r] = *rw.src(reinterpret_cast<const float*>(gf->graw) + o, t);
         }
       const float bias = gf->dt_bias ? gf->dt_bias[col] : 0.f;
       const float a = MODE == 2 ? 1.f : exp_f(gf->A_log[hh]);
@@ -1249,8 +1250,9 @@ __device__ __forceinline__ void chunk_body(
             dx = ds * a;
             tda = MODE == 1 ? ds * a * x : 0.f;
           }
-          if constexpr (RB) reinterpret_cast<bf16*>(gf->dx)[o] = to_bf16(dx);
-          else reinterpret_cast<float*>(gf->dx)[o] = dx;
+          if constexpr (RB) *rw.dst(reinterpret_cast<bf16*>(gf->dx) + o, 16 * I + 4 * lg + r) = to_bf16(dx);
+          else *rw.dst(reinterpret_cast<float*>(gf->dx) + o, 16 * I + 4 * lg + r) = dx;
+          if (!rw.ok(16 * I + 4 * lg + r)) dx = tda = 0.f;   // rows past a sequence's end
           sdt += dx;
           sda += tda;
         }
@@ -1367,23 +1369,25 @@ __global__ __launch_bounds__(512) void chunk_bwd_wy_kernel(
       nullptr, dA);
 }
 
-// KDA with the gate backward folded into the dg stores (no dg output)
-template <int FOLD, bool HVF = false>
+// KDA with the gate backward folded into the dg stores (no dg output); MAP: a packed
+// variable-length batch (cu, ci as for chunk_bwd_kernel)
+template <int FOLD, bool HVF = false, bool MAP = false>
 __global__ __launch_bounds__(512) void chunk_bwd_fold_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
     const float* __restrict__ g, const float* __restrict__ beta, const float* __restrict__ akk,
     const bf16* __restrict__ hst, const bf16* __restrict__ dhst, bf16* __restrict__ dq_out,
     bf16* __restrict__ dk_out, bf16* __restrict__ dv_out, float* __restrict__ dbeta_out, int T, int H,
-    float scale, GateFoldArgs gf, float beta_sig, int HQ) {
+    float scale, GateFoldArgs gf, float beta_sig, int HQ, const int* __restrict__ cu,
+    const int* __restrict__ ci) {
   using LY = PostLayout<CG_VECTOR, false>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
-  chunk_body<CG_VECTOR, false, false, false, FOLD, HVF>(
+  chunk_body<CG_VECTOR, false, false, false, FOLD, HVF, false, MAP>(
       q, k, v, vnew, dO, dR, g, beta, nullptr, nullptr, akk, hst, dhst, dq_out, dk_out, dv_out, nullptr, dbeta_out,
       nullptr, nullptr, T, H, scale, nullptr, nullptr, nullptr, nullptr, 0, blockIdx.x, -1, smem,
       smem + LY::REGION_A, reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
-      &gf, beta_sig, HQ);
+      &gf, beta_sig, HQ, cu, ci);
 }
 
 // Persistent form: one work-group per CU walks the items blockIdx.x, + gridDim.x, ...
@@ -1647,7 +1651,8 @@ static hipError_t gate_fold_launch(const void* q, const void* k, const void* v, 
                                    const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
                                    int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log,
                                    float* ddt_bias, void* workspace, int h_v_first, int B, int T, int H, int qk_heads,
-                                   int K, int V, int chunk, float scale, hipStream_t stream) {
+                                   int K, int V, int chunk, float scale, hipStream_t stream,
+                                   const int* cu = nullptr, const int* ci = nullptr) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
   const int HQ = qk_heads > 0 ? qk_heads : H;
   if (H % HQ) return hipErrorInvalidValue;
@@ -1663,21 +1668,22 @@ static hipError_t gate_fold_launch(const void* q, const void* k, const void* v, 
   float* part_da = part_dt + (size_t)nblk * H * KD;
   const GateFoldArgs gf{g_raw, A_log, dt_bias, lower_bound, dg_raw, part_dt, part_da};
   using LY = PostLayout<CG_VECTOR, false>;
-  const int fold = 2 * mode + (raw_is_bf16 ? 1 : 0) + (h_v_first ? 6 : 0);
+  const int fold = 2 * mode + (raw_is_bf16 ? 1 : 0) + (h_v_first ? 6 : 0) + (cu ? 12 : 0);
   using KernT = decltype(&chunk_bwd_fold_kernel<0>);
-  static const KernT kerns[12] = {
-      chunk_bwd_fold_kernel<0>,       chunk_bwd_fold_kernel<1>,       chunk_bwd_fold_kernel<2>,
-      chunk_bwd_fold_kernel<3>,       chunk_bwd_fold_kernel<4>,       chunk_bwd_fold_kernel<5>,
-      chunk_bwd_fold_kernel<0, true>, chunk_bwd_fold_kernel<1, true>, chunk_bwd_fold_kernel<2, true>,
-      chunk_bwd_fold_kernel<3, true>, chunk_bwd_fold_kernel<4, true>, chunk_bwd_fold_kernel<5, true>};
+#define FOLD_KERNS(HV, M)                                                                                     \
+  chunk_bwd_fold_kernel<0, HV, M>, chunk_bwd_fold_kernel<1, HV, M>, chunk_bwd_fold_kernel<2, HV, M>,          \
+      chunk_bwd_fold_kernel<3, HV, M>, chunk_bwd_fold_kernel<4, HV, M>, chunk_bwd_fold_kernel<5, HV, M>
+  static const KernT kerns[24] = {FOLD_KERNS(false, false), FOLD_KERNS(true, false), FOLD_KERNS(false, true),
+                                  FOLD_KERNS(true, true)};
+#undef FOLD_KERNS
   const KernT kern = kerns[fold];
-  static bool attr_set[12][kMaxDevices] = {};
+  static bool attr_set[24][kMaxDevices] = {};
   hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set[fold]);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, stream, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, (const bf16*)v_new, (const bf16*)dO, (const bf16*)dR, g, beta, Akk,
                      (const bf16*)h, (const bf16*)dh, (bf16*)dq, (bf16*)dk, (bf16*)dv, dbeta, T, H, scale, gf,
-                     beta_sigmoid, HQ);
+                     beta_sigmoid, HQ, cu, ci);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   return kda_gate_partials_sum(part_dt, part_da, nblk, H * KD, 8, ddt_bias, dA_log, stream);
@@ -1695,6 +1701,20 @@ extern "C" hipError_t fdr_chunk_bwd_gate_fold(const void* q, const void* k, cons
   return gate_fold_launch(q, k, v, v_new, dO, dR, g, beta, Akk, h, dh, dq, dk, dv, dbeta, beta_sigmoid, g_raw,
                           raw_is_bf16, A_log, dt_bias, has_lower_bound, lower_bound, dg_raw, dA_log, ddt_bias,
                           workspace, h_v_first, B, T, H, qk_heads, K, V, chunk, scale, stream);
+}
+
+extern "C" hipError_t fdr_chunk_bwd_gate_fold_varlen(
+    const void* q, const void* k, const void* v, const void* v_new, const void* dO, const void* dR, const float* g,
+    const float* beta, const float* Akk, const void* h, const void* dh, void* dq, void* dk, void* dv, float* dbeta,
+    float beta_sigmoid, const void* g_raw, int raw_is_bf16, const float* A_log, const float* dt_bias,
+    int has_lower_bound, float lower_bound, void* dg_raw, float* dA_log, float* ddt_bias, void* workspace,
+    int h_v_first, const int* cu_seqlens, const int* chunk_indices, int num_chunks, int H, int qk_heads, int K,
+    int V, int chunk, float scale, hipStream_t stream) {
+  if (num_chunks <= 0 || !cu_seqlens || !chunk_indices) return hipErrorInvalidValue;
+  return gate_fold_launch(q, k, v, v_new, dO, dR, g, beta, Akk, h, dh, dq, dk, dv, dbeta, beta_sigmoid, g_raw,
+                          raw_is_bf16, A_log, dt_bias, has_lower_bound, lower_bound, dg_raw, dA_log, ddt_bias,
+                          workspace, h_v_first, 1, num_chunks * C, H, qk_heads, K, V, chunk, scale, stream,
+                          cu_seqlens, chunk_indices);
 }
 
 template <bool VEC_B>

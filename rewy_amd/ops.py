@@ -406,10 +406,8 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
     if hvf and gate_mode != GATE_VECTOR:
         raise ValueError("[V,K] saved states come with the vector-gate families")
     if gate_fold is not None:
-        if mv is not None:
-            raise ValueError("the folded gate backward takes chunk-aligned rows")
         return _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, gate_fold,
-                                    beta_sigmoid, hvf, H)
+                                    beta_sigmoid, hvf, H, mv)
     out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=bf),
                dk=torch.empty(B, T, H, K, device=dev, dtype=bf),
                dv=torch.empty(B, T, H, V, device=dev, dtype=bf),
@@ -494,8 +492,9 @@ def chunk_bwd_original(q, k, v, v_new, dO, dR, g, Akk, h, dh, scale, beta):
 
 
 def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta, b, fold, beta_sigmoid=0.0,
-                         hvf=0, H=None):
-    """chunk_bwd (KDA) with the gate backward folded into the dg stores."""
+                         hvf=0, H=None, mv=None):
+    """chunk_bwd (KDA) with the gate backward folded into the dg stores; ``mv``: a packed
+    batch whose sequences start anywhere (a mapped ``Varlen``)."""
     B, T, HQ, K = q.shape
     H = HQ if H is None else H
     V = V_SUPPORTED
@@ -519,13 +518,20 @@ def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale
                dA_log=torch.empty(H, device=dev, dtype=f32) if A_log is not None else None,
                ddt_bias=torch.empty(H * K, device=dev, dtype=f32) if dt_bias is not None else None)
     lib = _lib.load()
-    ws = torch.empty(max(1, lib.fdr_chunk_bwd_gate_workspace_bytes(B, T, H) // 4), device=dev, dtype=f32)
     P = _lib.ptr
-    st = lib.fdr_chunk_bwd_gate_fold(P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), P(beta), P(Akk), P(h), P(dh),
-                                     P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), beta_sigmoid, P(raw),
-                                     int(raw.dtype == bf), P(a), P(dt), int(lb is not None),
-                                     0.0 if lb is None else float(lb), P(out["dg"]), P(out["dA_log"]),
-                                     P(out["ddt_bias"]), P(ws), hvf, B, T, H, HQ, K, V, CHUNK, float(scale),
+    args = (P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), P(beta), P(Akk), P(h), P(dh), P(out["dq"]),
+            P(out["dk"]), P(out["dv"]), P(out["dbeta"]), beta_sigmoid, P(raw), int(raw.dtype == bf), P(a), P(dt),
+            int(lb is not None), 0.0 if lb is None else float(lb), P(out["dg"]), P(out["dA_log"]),
+            P(out["ddt_bias"]))
+    if mv is not None:
+        ws = torch.empty(max(1, lib.fdr_chunk_bwd_gate_workspace_bytes(1, CHUNK * mv.NC, H) // 4), device=dev,
+                         dtype=f32)
+        st = lib.fdr_chunk_bwd_gate_fold_varlen(*args, P(ws), hvf, P(mv.cu_seqlens), P(mv.chunk_indices), mv.NC, H,
+                                                HQ, K, V, CHUNK, float(scale), _lib.stream_handle(dev))
+        _lib.check(st, "fdr_chunk_bwd_gate_fold_varlen")
+        return out
+    ws = torch.empty(max(1, lib.fdr_chunk_bwd_gate_workspace_bytes(B, T, H) // 4), device=dev, dtype=f32)
+    st = lib.fdr_chunk_bwd_gate_fold(*args, P(ws), hvf, B, T, H, HQ, K, V, CHUNK, float(scale),
                                      _lib.stream_handle(dev))
     _lib.check(st, "fdr_chunk_bwd_gate_fold")
     return out

@@ -117,9 +117,9 @@ def test_rejection_and_visible_fallback():
 
 
 @pytest.mark.parametrize("lower_bound,with_a_log", [(None, True), (-5.0, True), (-5.0, False)])
-# T = 128: the activation and its backward run inside the chunk Function (folded into the
-# chunk kernel); T = 192 with a ragged cu_seqlens (a partial chunk): the gate stays an autograd
-# node of its own
+# the activation and its backward run inside the chunk Function (folded into the chunk
+# kernel): T = 128 dense rows; T = 192 as one packed row with a ragged cu_seqlens (partial
+# chunks, fdr_chunk_bwd_gate_fold_varlen)
 @pytest.mark.parametrize("T", [128, 192])
 def test_kda_fused_gate_optimized_matches_original(lower_bound, with_a_log, T):
     """use_gate_in_kernel=True (the gate activation feeding the HIP backward, dA_log /
