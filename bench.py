@@ -52,6 +52,8 @@ CONFIGS = {
     # two cases of the reference's published operator grid (few heads: affine-step recurrences)
     "paper_delta_c2": dict(op="delta", B=1, T=8192, H=4, seed=12, gate=None, h0=True, full_saving=False),
     "paper_kda_c5": dict(op="kda", B=1, T=8192, H=16, seed=15, gate="kda", h0=False, full_saving=False),
+    "paper_delta_c5": dict(op="delta", B=1, T=8192, H=16, seed=15, gate=None, h0=True, full_saving=False),
+    "paper_gdn_c5": dict(op="gdn", B=1, T=8192, H=16, seed=15, gate="gdn", h0=True, full_saving=False),
 }
 
 TILE = 64 * 128 * 2          # one [64][128] bf16 tile
@@ -217,6 +219,14 @@ def setup(cfg, device):
         aqk = sv["Aqk"] if vec else pre["Aqk"]
     if keep and ops._state_method("auto", cfg["B"], cfg["H"], NT) == "segmented":
         # long rows, few heads: segment maps in parallel, a short chain, segments rerun
+        kern["segmented_state"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
+                                                        want_dh0=xs["h0"] is not None, method="segmented")
+        dh, dR, _ = kern["segmented_state"]()
+    elif not keep and ops.side_by_side_pays(cfg["B"], cfg["H"], NT):
+        # few heads, long rows: the forward scan beside the segmented state recurrence (two
+        # streams in the backend; timed here one at a time)
+        kern["fdr_fwd_h"] = lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"], method="direct")
+        h, v_new, _ = kern["fdr_fwd_h"]()
         kern["segmented_state"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
                                                         want_dh0=xs["h0"] is not None, method="segmented")
         dh, dR, _ = kern["segmented_state"]()

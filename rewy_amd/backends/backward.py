@@ -17,6 +17,9 @@ When batch x heads is too small to fill the GPU and the sequence long, the two
 recurrences run instead in affine-step form (after ``fdr_prepare_wu``: w, u and qg, kg or Aqk) (``ops.recurrences``,
 ``fdr_affine_*``): chunk-parallel step matrices, one scan launch carrying both
 recurrences side by side, and a chunk-parallel pass for v_new and dR.
+With a few more heads and long rows the recompute policy runs the forward scan
+(``fdr_fwd_h``) on the current stream beside the segmented backward state recurrence
+(``fdr_state_bwd_segmented``) on a second stream (``ops.side_by_side_pays``).
 
 There is no fallback: a missing HIP library or an unsupported argument raises.
 """
@@ -82,6 +85,33 @@ def _f32(x):
     return None if x is None else x.to(torch.float32).contiguous()
 
 
+_SIDE = {}
+
+
+def _side_by_side(first, second):
+    """first() enqueued on the current stream while second() is enqueued on a side stream
+    that waits only for the work enqueued before first(); the current stream then waits for
+    the side stream.  For two independent recurrences that each leave most of the GPU idle
+    (few heads, long rows: the forward scan of the recompute policy beside the segmented
+    backward state recurrence).  first() is enqueued first so that its few long-lived
+    work-groups are placed before second()'s launches fill the GPU (the other way round,
+    the scan's work-groups waited for free CUs and the scan took 2.4x as long).  The tensors
+    that second() returns are marked as used by the current stream."""
+    cur = torch.cuda.current_stream()
+    side = _SIDE.get(cur.device)
+    if side is None:
+        side = _SIDE[cur.device] = torch.cuda.Stream(cur.device)    # default priority
+    side.wait_stream(cur)
+    a = first()
+    with torch.cuda.stream(side):
+        b = second()
+    cur.wait_stream(side)
+    for t in b:
+        if torch.is_tensor(t):
+            t.record_stream(cur)
+    return a, b
+
+
 def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, saved, gate_fold=None,
             beta_sigmoid=0.0, state_v_first=False, saved_h_v_first=None, **kw):
     """Shared vector-gate (KDA / GDN2) backward.  ``gate_fold``, ``beta_sigmoid``: see ops.chunk_bwd.
@@ -101,6 +131,16 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
                                                 do, scale, aqk=Aqk, h0=_f32(initial_state), dht=_f32(dht),
                                                 want_dh0=initial_state is not None, state_v_first=vf)
         saved, hvf = dict(v_new=v_new, h=h), False
+    elif saved.get("h") is None and vl is None and ops.side_by_side_pays(q.shape[0], v.shape[2],
+                                                                        q.shape[1] // ops.CHUNK):
+        # recompute policy, few heads, long rows: the forward scan beside the segmented
+        # backward state recurrence
+        pre = _prepare_vector(k, v, g, Akk, gates, q, vl)
+        (h, v_new, _), (dh, dR, dh0) = _side_by_side(
+            lambda: ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
+                              method="direct", state_v_first=vf),
+            lambda: _state_vector(pre, g, do, scale, Aqk, dht, initial_state, vl, vf, method="segmented"))
+        saved, hvf = dict(v_new=v_new, h=h), False
     else:
         if saved.get("h") is None:
             saved, hvf = _recompute_vector(q, k, v, g, Akk, initial_state, gates, vl, vf), False
@@ -113,10 +153,10 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     return _group_sum(out, q.shape[2]), dh0
 
 
-def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, vl=None, vf=False):
+def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, vl=None, vf=False, method="auto"):
     return ops.state_bwd(_bf(saved["qg"]), _bf(saved["kg"]), _bf(saved["w"]), g, ops.GATE_VECTOR, do, scale,
                          aqk=Aqk, dht=_f32(dht), want_dh0=initial_state is not None,
-                         method="auto" if vl is None else "direct", varlen=vl, state_v_first=vf)
+                         method=method if vl is None else "direct", varlen=vl, state_v_first=vf)
 
 
 def _prepare_vector(k, v, g, Akk, gates, q, vl=None):
@@ -234,11 +274,24 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
                                                 h0=_f32(initial_state), dht=_f32(dht),
                                                 want_dh0=initial_state is not None, state_v_first=state_v_first)
     else:
-        h, v_new, _ = ops.fwd_h(k, pre["w"], pre["u"], g, gate, h0=_f32(initial_state), method="direct",
-                                varlen=vl, state_v_first=state_v_first)
-        dh, dR, dh0 = ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
-                                    want_dh0=initial_state is not None, method="auto", varlen=vl,
-                                    state_v_first=state_v_first)
+        # (grouped q / k heads take the direct state recurrence)
+        sbs = (vl is None and q.shape[2] == v.shape[2]
+               and ops.side_by_side_pays(q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK))
+        method = "segmented" if sbs else "auto"
+
+        def scan():
+            return ops.fwd_h(k, pre["w"], pre["u"], g, gate, h0=_f32(initial_state), method="direct",
+                             varlen=vl, state_v_first=state_v_first)
+
+        def state():
+            return ops.state_bwd(q, k, pre["w"], g, gate, do, scale, aqk=pre["Aqk"], dht=_f32(dht),
+                                 want_dh0=initial_state is not None, method=method, varlen=vl,
+                                 state_v_first=state_v_first)
+        if sbs:
+            (h, v_new, _), (dh, dR, dh0) = _side_by_side(scan, state)
+        else:
+            h, v_new, _ = scan()
+            dh, dR, dh0 = state()
     out = _group_sum(ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta,
                                    beta_sigmoid=beta_sigmoid, varlen=vl), q.shape[2])
     record(op, "optimized_backward")

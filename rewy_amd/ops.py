@@ -64,6 +64,26 @@ def _state_method(method, B, H, NT):
     return "direct"
 
 
+# Recompute policy, few heads: the forward scan (direct) on a side stream beside the
+# segmented backward state recurrence (the two are independent and each leaves most of
+# the GPU idle), in place of the affine-step pair or the direct kernels one after the other.
+SIDE_BY_SIDE = True
+SBS_MIN_BH = 8
+SBS_MIN_WORK = 1024       # B * H * NT
+
+
+def side_by_side_pays(B, H, NT):
+    """True when the recompute policy runs the forward scan beside the segmented state
+    recurrence for B rows of NT chunks and H heads (dense rows).  Measured crossovers
+    (DeltaNet / GDN): it beats the affine-step pair from B*H*NT = 1024 at B*H >= 8 (B*H = 16,
+    NT = 128: 405 vs 503 us) but not at B*H = 4 (NT = 128: 205 vs 160 us); with more heads
+    the direct kernels win until the segmented form's own threshold."""
+    BH = B * H
+    if not SIDE_BY_SIDE or BH < SBS_MIN_BH or 2 * BH >= 256 or BH * NT < SBS_MIN_WORK:
+        return False
+    return BH <= AFFINE_MAX_BH or NT >= SEG_MIN_CHUNKS
+
+
 def state_form(B, H, NT):
     """The form ``state_bwd(method="auto")`` takes for B rows of NT chunks and H heads."""
     return _state_method("auto", B, H, NT)
@@ -79,9 +99,10 @@ def _use_affine(method, B, H, NT):
 
 def affine_pays(x):
     """True when the affine-step recurrences are the faster choice for the shape of x,
-    a [B, T, H, .] tensor with one head per state (value heads)."""
+    a [B, T, H, .] tensor with one head per state (value heads), for the recompute policy
+    (both recurrences)."""
     B, T, H = x.shape[:3]
-    return _use_affine("auto", B, H, T // CHUNK)
+    return _use_affine("auto", B, H, T // CHUNK) and not side_by_side_pays(B, H, T // CHUNK)
 
 
 def _affine_workspace(B, NT, H, dev):

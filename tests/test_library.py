@@ -152,3 +152,18 @@ def test_fused_scan_rule():
     assert even.max_chunks == 64 and skewed.max_chunks == 128 and skewed.NC == 514
     assert ops.fwd_h_wy_pays(even.N, 16, V, even)
     assert not ops.fwd_h_wy_pays(skewed.N, 16, V, skewed)
+
+
+def test_side_by_side_rule():
+    """ops.side_by_side_pays (recompute policy: the forward scan beside the segmented state
+    recurrence) against the measured crossovers, and affine_pays stepping aside for it."""
+    import torch
+    from rewy_amd import ops
+    sbs = ops.side_by_side_pays
+    assert sbs(1, 16, 128) and sbs(1, 8, 128) and sbs(1, 16, 64)       # grid case 5 and its kin
+    assert not sbs(1, 4, 128) and not sbs(1, 16, 32) and not sbs(1, 8, 64)   # the affine pair wins
+    assert not sbs(2, 16, 128) and sbs(2, 16, 256)     # direct kernels until the segmented threshold
+    assert not sbs(8, 16, 512)                         # the direct kernels fill the GPU
+    meta = lambda B, T, H: torch.empty(B, T, H, 1, device="meta")
+    assert not ops.affine_pays(meta(1, 8192, 16)) and ops.affine_pays(meta(1, 8192, 4))
+    assert ops.affine_pays(meta(1, 2048, 16))
