@@ -131,14 +131,17 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
                                                 do, scale, aqk=Aqk, h0=_f32(initial_state), dht=_f32(dht),
                                                 want_dh0=initial_state is not None, state_v_first=vf)
         saved, hvf = dict(v_new=v_new, h=h), False
-    elif saved.get("h") is None and vl is None and ops.side_by_side_pays(q.shape[0], v.shape[2],
-                                                                        q.shape[1] // ops.CHUNK):
-        # recompute policy, few heads, long rows: the forward scan beside the segmented
-        # backward state recurrence
+    elif saved.get("h") is None and (
+            (vl is None and ops.side_by_side_pays(q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK))
+            or (vl is not None and ops.SIDE_BY_SIDE
+                and not ops.fwd_h_wy_pays(vl.N, v.shape[2], ops.GATE_VECTOR, vl))):
+        # recompute policy: the forward scan beside the backward state recurrence, for few
+        # heads and long rows (segmented recurrence) and for packed batches the fused sweep
+        # does not take (their short sequences leave CUs idle while the longest runs)
         pre = _prepare_vector(k, v, g, Akk, gates, q, vl)
         (h, v_new, _), (dh, dR, dh0) = _side_by_side(
             lambda: ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
-                              method="direct", state_v_first=vf),
+                              method="direct", varlen=vl, state_v_first=vf),
             lambda: _state_vector(pre, g, do, scale, Aqk, dht, initial_state, vl, vf, method="segmented"))
         saved, hvf = dict(v_new=v_new, h=h), False
     else:
@@ -252,6 +255,7 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
     inline = not affine and (vl is not None or ops.state_form(q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK)
                              == "direct")
     if inline:
+        pre = None
         if ops.fwd_h_wy_pays(q.shape[0] if vl is None else vl.N, v.shape[2], gate, vl):
             sw = ops.fwd_h_wy(k, v, A, g, gate, beta=beta, h0=_f32(initial_state), varlen=vl,
                               state_v_first=state_v_first)
@@ -259,10 +263,22 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
         else:
             pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, varlen=vl)
             w = pre["w"]
-            h, v_new, _ = ops.fwd_h(k, w, pre["u"], g, gate, h0=_f32(initial_state), method="direct", varlen=vl,
-                                    state_v_first=state_v_first)
-        dh, dR, dh0 = ops.state_bwd(q, k, w, g, gate, do, scale, dht=_f32(dht), want_dh0=initial_state is not None,
-                                    method="direct", varlen=vl, state_v_first=state_v_first)
+
+        def state():
+            return ops.state_bwd(q, k, w, g, gate, do, scale, dht=_f32(dht), want_dh0=initial_state is not None,
+                                 method="direct", varlen=vl, state_v_first=state_v_first)
+
+        def scan():
+            return ops.fwd_h(k, w, pre["u"], g, gate, h0=_f32(initial_state), method="direct", varlen=vl,
+                             state_v_first=state_v_first)
+        if pre is None:
+            dh, dR, dh0 = state()
+        elif vl is not None and ops.SIDE_BY_SIDE:
+            # a packed batch: its short sequences leave CUs idle while the longest runs
+            (h, v_new, _), (dh, dR, dh0) = _side_by_side(scan, state)
+        else:
+            h, v_new, _ = scan()
+            dh, dR, dh0 = state()
         out = _group_sum(ops.chunk_bwd(q, k, v, v_new, do, dR, g, gate, A, h, dh, scale, beta=beta,
                                        beta_sigmoid=beta_sigmoid, varlen=vl), q.shape[2])
         record(op, "optimized_backward")

@@ -92,8 +92,11 @@ struct PostLayout {
   static constexpr int B2 = 2 * TQ + (PIPE ? 0 : GT_BYTES) + (VEC_B ? TQ : 0);
   static constexpr int REGION_B = B1 > B2 ? B1 : B2;
   // small per-row arrays (floats)
-  static constexpr int S_BETA = 0, S_G = 64, S_DBA = 128, S_DBB = 384, S_DG = 448, S_GL = 960,
-                       S_ANY = 1088, S_N = 1096;
+  // S_FB (scalar beta): the direct dbeta terms of |beta| < 1e-6 rows as per-wave partials,
+  // [8][64] from phase 1 (one per column strip and value tile) then [8][64] from phase 5,
+  // summed in a fixed order (no LDS atomics: the result does not depend on wave timing)
+  static constexpr int S_BETA = 0, S_G = 64, S_DBA = 128, S_DG = 448, S_GL = 960, S_ANY = 1088, S_FB = 1096,
+                       S_N = S_FB + (VEC_B ? 0 : 16 * 64);
   static constexpr int SMALL = S_N * 4;
   static constexpr int X_BYTES = PIPE ? 3 * TQ + GT_BYTES : 0;
   // the original formulation's extra tiles: Z = beta v, E = beta k 2^g, W-bar (bf16 [64][128]);
@@ -306,7 +309,7 @@ __device__ __forceinline__ void chunk_body(
   float* sBeta = small + LY::S_BETA;   // scalar beta per row
   float* sG = small + LY::S_G;         // scalar gate per row (log2)
   float* sDbA = small + LY::S_DBA;     // [4][64] sum_v P R per column strip (beta != 0 rows)
-  float* sDbB = small + LY::S_DBB;     // direct dbeta terms  (beta ~ 0 rows)
+  float* sFb = small + LY::S_FB;       // direct dbeta terms (beta ~ 0 rows), per-wave partials
   float* sDg = small + LY::S_DG;       // [8][64] scalar gate: dG row sums per wave
   float* sGl = small + LY::S_GL;       // [128] last-row gate (log2) per column
   int* sAny = reinterpret_cast<int*>(small + LY::S_ANY);   // [8] per-wave "some beta ~ 0" flags
@@ -373,7 +376,6 @@ __device__ __forceinline__ void chunk_body(
     }
     if (tid < C) {
       if constexpr (!VEC_B) sBeta[tid] = beta[(tok0 + tid) * H + h];
-      sDbB[tid] = 0.f;
     }
   } else {
     // (the persistent kernel stages A hi/lo at the end of the previous item)
@@ -399,7 +401,6 @@ __device__ __forceinline__ void chunk_body(
         fb = fabsf(pin.beta) < 1e-6f;
       }
       if constexpr (GATE == CG_SCALAR) sG[tid] = pin.g;
-      sDbB[tid] = 0.f;
     }
     if (tid < KD) sGl[tid] = pin.gl;
     // block-uniform: some row has |beta| < 1e-6 (one flag per wave, then a barrier)
@@ -498,7 +499,7 @@ __device__ __forceinline__ void chunk_body(
 #pragma unroll
             for (int r = 0; r < 4; ++r) pv += acc[r] * to_f32(x4[r]);
             pv = sum_lane_groups(pv, l);
-            if (lg == 0) atomicAdd(&sDbB[t], pv);
+            if (lg == 0) sFb[64 * (2 * cs + vt) + t] = pv;
           }
         }
       }
@@ -1121,7 +1122,7 @@ __device__ __forceinline__ void chunk_body(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float s = sum_row16(fbrow[I][r]);
-          if (lc == 0) atomicAdd(&sDbB[16 * I + 4 * lg + r], s);
+          if (lc == 0) sFb[512 + 64 * wv + 16 * I + 4 * lg + r] = s;
         }
     }
   }
@@ -1265,7 +1266,7 @@ __device__ __forceinline__ void chunk_body(
       if (l == 0) gf->part_da[(blk * H + hh) * 8 + wv] = sda;
     }
   }
-  lds_sync();   // sDbB, sDg complete; every wave is past phase 5 (region A free)
+  lds_sync();   // sFb, sDg complete; every wave is past phase 5 (region A free)
   if constexpr (PIPE) {
     // The next item's A: wait for its loads (issued ahead of this item's stores,
     // one store per row and output below) without waiting for the stores, and
@@ -1275,19 +1276,32 @@ __device__ __forceinline__ void chunk_body(
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(STORES));
     stage_akk(pin, sAh, sAl, tid);
   }
+  // the fallback rows' direct dbeta: phase-1 partials (one per column strip and value tile),
+  // then phase 5's (one per wave), in a fixed order; only where written (has_fb, uniform)
+  float fbs = 0.f;
+  if constexpr (!VEC_B) {
+    if (has_fb && tid < C) {
+      if constexpr (!INTRA) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) fbs += sFb[64 * j + tid];
+      }
+#pragma unroll
+      for (int w = 0; w < 8; ++w) fbs += sFb[512 + 64 * w + tid];
+    }
+  }
   if (INTRA && tid < C) {
     // endpoint_intra.py:190-194: every row, or only |beta| < 1e-6 rows when the
     // residual producer already accounted for the rest (beta_complete)
     if constexpr (!VEC_B) {
       const size_t row = (tok0 + tid) * H + h;
-      if (!beta_complete || fabsf(sBeta[tid]) < 1e-6f) dbeta_out[row] += sDbB[tid];
+      if (!beta_complete || fabsf(sBeta[tid]) < 1e-6f) dbeta_out[row] += fbs;
     }
   } else if (tid < C) {
     const size_t row = (tok0 + tid) * H + h;
     if constexpr (!VEC_B) {
       const float be = sBeta[tid];
       const float pr = (sDbA[tid] + sDbA[64 + tid]) + (sDbA[128 + tid] + sDbA[192 + tid]);
-      float db = (ORIG || fabsf(be) < 1e-6f) ? sDbB[tid] : pr / be;
+      float db = (ORIG || fabsf(be) < 1e-6f) ? fbs : pr / be;
       // beta = s sigmoid(x) activated in the forward (use_beta_sigmoid_in_kernel):
       // dL/dx = dL/dbeta * s sigmoid (1 - sigmoid) = dL/dbeta * beta (1 - beta / s)
       if (beta_sig > 0.f) db *= be * (1.f - be / beta_sig);

@@ -64,9 +64,12 @@ def _state_method(method, B, H, NT):
     return "direct"
 
 
-# Recompute policy, few heads: the forward scan (direct) on a side stream beside the
-# segmented backward state recurrence (the two are independent and each leaves most of
-# the GPU idle), in place of the affine-step pair or the direct kernels one after the other.
+# Recompute policy: the forward scan (direct) and the backward state recurrence are
+# independent.  With few heads and long rows the scan runs beside the segmented recurrence
+# (each leaves most of the GPU idle), in place of the affine-step pair or the direct
+# kernels one after the other; a packed batch that the fused sweep (fwd_h_wy_pays) does
+# not take runs the scan beside the direct recurrence (its short sequences leave CUs idle
+# while the longest one runs).  SIDE_BY_SIDE switches both off.
 SIDE_BY_SIDE = True
 SBS_MIN_BH = 8
 SBS_MIN_WORK = 1024       # B * H * NT

@@ -108,3 +108,43 @@ def test_side_by_side_under_graph_capture(op):
             assert torch.equal(a, r), (op, rep, i)
         run()                     # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("op", ["kda", "gdn", "delta"])
+def test_side_by_side_on_a_packed_batch(op, monkeypatch):
+    """A skewed packed batch (sequences starting anywhere, one long, several short): the scan
+    beside the direct state recurrence gives the gradients of the same launches on one stream,
+    bit for bit."""
+    from rewy_amd import ops
+    from rewy_amd.backends import backward as bw
+    from rewy_amd.hip_forward import chunk_forward_hip
+    lens, H = [2048, 100, 300, 64, 577], 4
+    T = sum(lens)
+    print(f"\n[side-by-side packed] op={op} lens={lens} H={H}", flush=True)
+    dev = torch.device("cuda")
+    xs, dO = make_inputs(op, 1, T, H, seed=43)
+    xs = {n: v.to(dev) for n, v in xs.items() if n != "initial_state"}
+    dO = dO.to(dev)
+    cu = torch.tensor([0] + lens).cumsum(0).to(dev)
+    vl = ops.Varlen(cu, dev)
+    assert not ops.fwd_h_wy_pays(vl.N, H, ops.GATE_VECTOR if op == "kda" else ops.GATE_SCALAR, vl)
+    _, _, sv = chunk_forward_hip(op, xs["q"], xs["k"], xs["v"], g=xs.get("g"), beta=xs["beta"], varlen=vl)
+    common = dict(q=xs["q"], k=xs["k"], v=xs["v"], scale=sv["scale"], initial_state=None, do=dO, dht=None,
+                  cu_seqlens=cu)
+    if op == "kda":
+        run = lambda: bw.kda_backward(beta=xs["beta"], Aqk=sv["Aqk"], Akk=sv["Akk"], g=sv["gc"], **common)[:5]
+    elif op == "gdn":
+        run = lambda: bw.gdn_backward(g=sv["gc"], beta=xs["beta"], A=sv["Akk"], **common)[:5]
+    else:
+        run = lambda: bw.delta_backward(beta=xs["beta"], A=sv["Akk"], **common)[:4]
+    calls = []
+    real = bw._side_by_side
+    monkeypatch.setattr(bw, "_side_by_side", lambda a, b: (calls.append(1), real(a, b))[1])
+    got = [x.clone() for x in run()]
+    torch.cuda.synchronize()
+    assert calls, "the side-by-side form did not run"
+    monkeypatch.setattr(bw, "_side_by_side", lambda a, b: (a(), b()))
+    one = run()
+    torch.cuda.synchronize()
+    for i, (a, r) in enumerate(zip(got, one)):
+        assert torch.equal(a, r), (op, i)
