@@ -124,20 +124,20 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     q, k, v, do = _bf(q), _bf(k), _bf(v), _bf(do)
     g = _f32(g)
     Aqk, Akk = _f32(Aqk), _f32(Akk)
-    if saved.get("h") is None and vl is None and ops.affine_pays(v):
-        # recompute policy, few heads: both recurrences side by side in affine-step form
+    recompute = saved.get("h") is None
+    N, H, NT = (q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK) if vl is None else (vl.N, v.shape[2], vl.NC)
+    if recompute and vl is None and ops.affine_pays(v):
+        # few heads: both recurrences side by side in affine-step form
         pre = _prepare_vector(k, v, g, Akk, gates, q, vl)
         h, v_new, dh, dR, dh0 = ops.recurrences(pre["qg"], pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR,
                                                 do, scale, aqk=Aqk, h0=_f32(initial_state), dht=_f32(dht),
                                                 want_dh0=initial_state is not None, state_v_first=vf)
         saved, hvf = dict(v_new=v_new, h=h), False
-    elif saved.get("h") is None and (
-            (vl is None and ops.side_by_side_pays(q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK))
-            or (vl is not None and ops.SIDE_BY_SIDE
-                and not ops.fwd_h_wy_pays(vl.N, v.shape[2], ops.GATE_VECTOR, vl))):
-        # recompute policy: the forward scan beside the backward state recurrence, for few
-        # heads and long rows (segmented recurrence) and for packed batches the fused sweep
-        # does not take (their short sequences leave CUs idle while the longest runs)
+    elif recompute and (ops.side_by_side_pays(N, H, NT) if vl is None else
+                        ops.SIDE_BY_SIDE and not ops.fwd_h_wy_pays(N, H, ops.GATE_VECTOR, vl)):
+        # the forward scan on one stream beside the backward state recurrence on another:
+        # few heads and long rows (the segmented recurrence), or a packed batch the fused
+        # sweep does not take (its short sequences leave CUs idle while the longest runs)
         pre = _prepare_vector(k, v, g, Akk, gates, q, vl)
         (h, v_new, _), (dh, dR, dh0) = _side_by_side(
             lambda: ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
@@ -145,7 +145,7 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
             lambda: _state_vector(pre, g, do, scale, Aqk, dht, initial_state, vl, vf, method="segmented"))
         saved, hvf = dict(v_new=v_new, h=h), False
     else:
-        if saved.get("h") is None:
+        if recompute:
             saved, hvf = _recompute_vector(q, k, v, g, Akk, initial_state, gates, vl, vf), False
         dh, dR, dh0 = _state_vector(saved, g, do, scale, Aqk, dht, initial_state, vl, vf)
     out = ops.chunk_bwd(q, k, v, _bf(saved["v_new"]), do, dR, g, ops.GATE_VECTOR, Akk,
