@@ -129,10 +129,10 @@ __device__ __forceinline__ void prep_body(PrepSmem& sm, const PrepArgs& pa, int 
       if constexpr (DV_FROM_AQK) {
         // Aqk as one bf16, the precision of the reference's dv_local (FLA's dAv rounds A to
         // the dO dtype before its dot: kernels/kda_residual_npu_onchip.py:114-116)
-        const f32x4 a = *reinterpret_cast<const f32x4*>(aqk + ((tok0 + t) * H + h) * C + cc * 4);
+        const f32x4 a = *reinterpret_cast<const f32x4*>(tril_src(aqk + ((tok0 + t) * H + h) * C + cc * 4, t, cc));
         bf16x4 hi;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) hi[r] = to_bf16(a[r]);
+        for (int r = 0; r < 4; ++r) hi[r] = to_bf16(tril_elem(a[r], t, 4 * cc + r));
         *reinterpret_cast<bf16x4*>(sm.s.a.ah + tr_off<8>(t, cc * 4)) = hi;
       } else {
         store_tr_chunk<16>(sm.t.in.dv, t, cc, *reinterpret_cast<const u32x4*>(dv_in + vofs + (size_t)t * rsv + cc * 8));

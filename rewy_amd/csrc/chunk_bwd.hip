@@ -165,7 +165,8 @@ __device__ __forceinline__ void load_phase_in(const float* __restrict__ akk, con
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int p = tid + 512 * i;
-    pin.a[i] = *reinterpret_cast<const f32x4*>(rw.src(akk + it.aofs + (size_t)(p >> 4) * rsa + 4 * (p & 15), p >> 4));
+    pin.a[i] = *reinterpret_cast<const f32x4*>(
+        tril_src(rw.src(akk + it.aofs + (size_t)(p >> 4) * rsa + 4 * (p & 15), p >> 4), p >> 4, p & 15));
   }
   const int t = tid & (C - 1);
   const size_t row = (it.tok0 + t) * H + it.h;
@@ -188,7 +189,7 @@ __device__ __forceinline__ void stage_akk(const PhaseIn& pin, bf16* sAh, bf16* s
     const int p = tid + 512 * i;
     const int t = p >> 4, ch = p & 15;
     bf16x4 lo;
-    const bf16x4 hi = split_hi4(pin.a[i], lo);
+    const bf16x4 hi = split_hi4(tril_piece(pin.a[i], t, ch), lo);
     *reinterpret_cast<bf16x4*>(sAh + tr_off<8>(t, 4 * ch)) = hi;
     *reinterpret_cast<bf16x4*>(sAl + tr_off<8>(t, 4 * ch)) = lo;
   }

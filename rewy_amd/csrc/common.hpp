@@ -104,6 +104,22 @@ __device__ __forceinline__ QKRows qk_rows(size_t tok0, int h, int H, int HQ) {
 static __device__ __attribute__((aligned(64))) uint32_t zero_page[16];   // never written
 static __device__ __attribute__((aligned(64))) uint32_t sink_page[16];   // never read
 
+// Piece (row t, columns 4 ch .. 4 ch + 3) of a lower-triangular [64][64] fp32 matrix (Aqk,
+// and Akk = (I + M)^-1, zero above the diagonal): a piece wholly above the diagonal is read
+// from the zero page (no HBM traffic, ~6 of its 16 KiB per chunk-head), and tril_elem /
+// tril_piece zero the elements above the diagonal, the reference's causal mask on Aqk before
+// its dot (kernels/kda_residual_npu_onchip.py:114); the kernels already treat Akk as lower
+// triangular (they skip its upper blocks' products).
+__device__ __forceinline__ const float* tril_src(const float* p, int t, int ch) {
+  return 4 * ch <= t ? p : reinterpret_cast<const float*>(zero_page);
+}
+__device__ __forceinline__ float tril_elem(float x, int t, int col) { return col <= t ? x : 0.f; }
+__device__ __forceinline__ f32x4 tril_piece(f32x4 a, int t, int ch) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) a[r] = tril_elem(a[r], t, 4 * ch + r);
+  return a;
+}
+
 template <bool MAP>
 struct Rows {
   size_t tok0;   // token of row 0

@@ -426,7 +426,10 @@ __global__ __launch_bounds__(512) void fwd_o_kernel(const bf16* __restrict__ q, 
     store_tr_chunk<16>(sqgl, t, p & 15, __builtin_bit_cast(u32x4, lo));
     store_tr_chunk<16>(sv, t, p & 15, *reinterpret_cast<const u32x4*>(rw.src(vnew + kofs + (size_t)t * rsk + c8, t)));
     const int c4 = (p & 15) * 4;
-    const f32x4 a = *reinterpret_cast<const f32x4*>(rw.src(aqk + mofs + (size_t)t * rsm + c4, t));
+    // causal: pieces above the diagonal are not fetched, elements above it are zero
+    f32x4 a = *reinterpret_cast<const f32x4*>(tril_src(rw.src(aqk + mofs + (size_t)t * rsm + c4, t), t, p & 15));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a[r] = tril_elem(a[r], t, c4 + r);
     bf16x4 alo;
     const bf16x4 ahi = split_hi4(a, alo);
     *reinterpret_cast<bf16x4*>(sah + tr_off<8>(t, c4)) = ahi;

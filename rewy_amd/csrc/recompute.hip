@@ -93,7 +93,8 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     rbs[i] = VEC_B ? 0.f : *rw.src(beta + (tok0 + t) * H + h, t);
     rkx[i] = *reinterpret_cast<const u32x4*>(rw.src(k + qr.ofs + (size_t)t * qr.rs + c0, t));
     rvx[i] = *reinterpret_cast<const u32x4*>(rw.src(v + vofs + (size_t)t * rsv + c0, t));
-    ra4[i] = *reinterpret_cast<const f32x4*>(rw.src(akk + ((tok0 + t) * H + h) * C + 4 * (p & 15), t));
+    ra4[i] = *reinterpret_cast<const f32x4*>(tril_src(rw.src(akk + ((tok0 + t) * H + h) * C + 4 * (p & 15), t), t,
+                                                      p & 15));
     if constexpr (GATE == RG_VECTOR) {
       rg0[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rw.clamp(t) * rsk + c0);
       rg1[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rw.clamp(t) * rsk + c0 + 4);
@@ -159,7 +160,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     store_tr_chunk<16>(zH, t, ch, __builtin_bit_cast(u32x4, zh));
     // A rows: 64 x 64 fp32 = 1024 pieces of 4, one per (i, thread) here
     bf16x4 alo;
-    const bf16x4 ahi = split_hi4(ra4[i], alo);
+    const bf16x4 ahi = split_hi4(tril_piece(ra4[i], t, ch), alo);
     *reinterpret_cast<bf16x4*>(&sAh[t][4 * ch]) = ahi;
     *reinterpret_cast<bf16x4*>(&sAl[t][4 * ch]) = alo;
     // qg = q 2^g, kg = k 2^(g_last - g) (vector gates): elementwise, coalesced
@@ -599,7 +600,8 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       if constexpr (VEC_B) rb[i] = *reinterpret_cast<const u32x4*>(rs_.src(bgate + kofs + (size_t)t * rsk + c8, t));
       else rb_tok[i] = *rs_.src(beta + (tok0 + t) * H + h, t);
       rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + kr_.ofs + (size_t)t * kr_.rs + c8, t));
-      ra[i] = *reinterpret_cast<const f32x4*>(rs_.src(akk + ((tok0 + t) * H + h) * C + 4 * (p & 15), t));
+      ra[i] = *reinterpret_cast<const f32x4*>(tril_src(rs_.src(akk + ((tok0 + t) * H + h) * C + 4 * (p & 15), t),
+                                                       t, p & 15));
     }
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
@@ -650,7 +652,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       store_tr_chunk<16>(sm.e, t, ch, __builtin_bit_cast(u32x4, eh));
       store_tr_chunk<16>(sm.k[pb], t, ch, __builtin_bit_cast(u32x4, kg));
       bf16x4 alo;
-      const bf16x4 ahi = split_hi4(ra[i], alo);
+      const bf16x4 ahi = split_hi4(tril_piece(ra[i], t, ch), alo);
       *reinterpret_cast<bf16x4*>(&sm.ah[t][4 * ch]) = ahi;
       *reinterpret_cast<bf16x4*>(&sm.al[t][4 * ch]) = alo;
     }

@@ -159,7 +159,8 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + oq, p >> 4));
       rw[i] = *reinterpret_cast<const u32x4*>(rs_.src(w + o, p >> 4));
       if constexpr (DV_FROM_AQK && !INL)
-        ra[i] = *reinterpret_cast<const f32x4*>(rs_.src(aqk + ((tok0 + (p >> 4)) * H + h) * C + (p & 15) * 4, p >> 4));
+        ra[i] = *reinterpret_cast<const f32x4*>(
+            tril_src(rs_.src(aqk + ((tok0 + (p >> 4)) * H + h) * C + (p & 15) * 4, p >> 4), p >> 4, p & 15));
     }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
@@ -197,7 +198,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
         // the dO dtype before its dot: kernels/kda_residual_npu_onchip.py:114-116)
         bf16x4 hi;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) hi[r] = to_bf16(ra[i][r]);
+        for (int r = 0; r < 4; ++r) hi[r] = to_bf16(tril_elem(ra[i][r], t, 4 * ch + r));
         *reinterpret_cast<bf16x4*>(sm.ah[0] + tr_off<8>(t, ch * 4)) = hi;
       }
     }
@@ -602,7 +603,8 @@ __global__ __launch_bounds__(512) void state_xfer_kernel(
       rq[i] = *reinterpret_cast<const u32x4*>(q + o);
       rw[i] = *reinterpret_cast<const u32x4*>(w + o);
       if constexpr (DV_FROM_AQK)
-        ra[i] = *reinterpret_cast<const f32x4*>(aqk + ((tok0 + (p >> 4)) * H + h) * C + (p & 15) * 4);
+        ra[i] = *reinterpret_cast<const f32x4*>(
+            tril_src(aqk + ((tok0 + (p >> 4)) * H + h) * C + (p & 15) * 4, p >> 4, p & 15));
     }
     rdo = *reinterpret_cast<const u32x4*>(dO + (tok0 + tid / CHV) * rsv + (size_t)h * VD + base + (tid % CHV) * 8);
   };
@@ -623,7 +625,7 @@ __global__ __launch_bounds__(512) void state_xfer_kernel(
       if constexpr (DV_FROM_AQK) {
         bf16x4 hi;                           // one bf16 Aqk, as the direct kernel
 #pragma unroll
-        for (int r = 0; r < 4; ++r) hi[r] = to_bf16(ra[i][r]);
+        for (int r = 0; r < 4; ++r) hi[r] = to_bf16(tril_elem(ra[i][r], t, 4 * ch + r));
         *reinterpret_cast<bf16x4*>(sm.ah + tr_off<8>(t, ch * 4)) = hi;
       }
     }
