@@ -367,7 +367,7 @@ def streaming_floor(kernel, config, kernel_ms):
 
 
 def cpu_baseline(xs, sv, dO, scale, NTt, round_s=0.5, rounds=15):
-    """The reference's CPU comparison point as SURVEY'd for the large configs: the original
+    """The reference's CPU comparison point for the large configs: the original
     (7-product) chunk backward as torch ops -- dAv, the reverse state recurrence, the
     7-product local WY and the pairwise intra (``rewy_amd.original.original_backward``) --
     in fp32 on the host, every thread the box grants (OMP_NUM_THREADS; the reference
