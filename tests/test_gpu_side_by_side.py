@@ -148,3 +148,46 @@ def test_side_by_side_on_a_packed_batch(op, monkeypatch):
     torch.cuda.synchronize()
     for i, (a, r) in enumerate(zip(got, one)):
         assert torch.equal(a, r), (op, i)
+
+
+@pytest.mark.parametrize("op", ["kda", "gdn"])
+def test_side_by_side_with_grouped_heads_and_v_first_states(op, monkeypatch):
+    """The side-by-side form with grouped value heads (q / k with 4 heads, 8 value heads) and
+    V-first states: KDA takes it (its q / k head map is the prepare kernel's); GDN, whose
+    segmented recurrence reads raw q / k per value head, keeps the direct kernels.  Both
+    against the direct kernels one after the other (rel-L2 <= 1e-2 per gradient)."""
+    from rewy_amd import ops
+    from rewy_amd.backends import backward as bw
+    from rewy_amd.hip_forward import chunk_forward_hip
+    HV, G = 8, 2
+    print(f"\n[side-by-side gva+vf] op={op} B={B} T={T} HV={HV} G={G}", flush=True)
+    dev = torch.device("cuda")
+    xs, dO = make_inputs(op, B, T, HV, seed=47)
+    xs = {n: v.to(dev) for n, v in xs.items()}
+    xs["q"] = xs["q"][:, :, ::G].contiguous()
+    xs["k"] = xs["k"][:, :, 1::G].contiguous()
+    h0 = xs["initial_state"].transpose(-1, -2).contiguous()           # [N, HV, V, K]
+    dO = dO.to(dev)
+    _, _, sv = chunk_forward_hip(op, xs["q"], xs["k"], xs["v"], g=xs.get("g"), beta=xs["beta"], initial_state=h0,
+                                 state_v_first=True)
+    dht = torch.randn(B, HV, 128, 128, generator=torch.Generator().manual_seed(5)).mul(0.1).to(dev)
+    common = dict(q=xs["q"], k=xs["k"], v=xs["v"], scale=sv["scale"], initial_state=h0, do=dO, dht=dht,
+                  state_v_first=True)
+    if op == "kda":
+        run = lambda: bw.kda_backward(beta=xs["beta"], Aqk=sv["Aqk"], Akk=sv["Akk"], g=sv["gc"], **common)[:6]
+    else:
+        run = lambda: bw.gdn_backward(g=sv["gc"], beta=xs["beta"], A=sv["Akk"], **common)[:6]
+    calls = []
+    real = bw._side_by_side
+    monkeypatch.setattr(bw, "_side_by_side", lambda a, b: (calls.append(1), real(a, b))[1])
+    got = [x.clone() for x in run()]
+    torch.cuda.synchronize()
+    assert bool(calls) == (op == "kda"), calls
+    monkeypatch.setattr(ops, "SIDE_BY_SIDE", False)
+    monkeypatch.setattr(ops, "AFFINE_MAX_BH", -1)
+    ref = run()
+    torch.cuda.synchronize()
+    for i, (a, r) in enumerate(zip(got, ref)):
+        e = _rel(a, r)
+        print(op, i, f"{e:.2e}", flush=True)
+        assert e < 1e-2, (op, i, e)
