@@ -23,6 +23,8 @@ def make_inputs(op, B, T, H, K=128, seed=0, gate="default", h0=True, beta_zero_e
     elif op in ("kda", "gdn2"):
         if gate == "wide":
             xs["g"] = F.logsigmoid(torch.randn(shape, generator=g_) * 3 - 4)
+        elif gate == "mild":      # long-memory gates (BASELINE.json's kda_long draw)
+            xs["g"] = F.logsigmoid(torch.randn(shape, generator=g_) * 0.3 + 3)
         else:
             xs["g"] = F.logsigmoid(torch.randn(shape, generator=g_)).clamp_min(-5)
     if h0:

@@ -31,7 +31,9 @@ def _call(op):
     from rewy_amd.backends import backward as bw
     from rewy_amd.hip_forward import chunk_forward_hip
     dev = torch.device("cuda")
-    xs, dO = make_inputs(op, B, T, H, seed=41)
+    # long-memory gates for the vector families, so that the segment maps carry the state
+    # across segments (with the default gates it decays to nothing within a chunk)
+    xs, dO = make_inputs(op, B, T, H, seed=41, gate="mild" if op in ("kda", "gdn2") else "default")
     xs = {n: (None if v is None else v.to(dev)) for n, v in xs.items()}
     dO = dO.to(dev)
     _, _, sv = chunk_forward_hip(op, xs["q"], xs["k"], xs["v"], g=xs.get("g"), beta=xs.get("beta"),
