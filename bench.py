@@ -105,6 +105,7 @@ def kernel_costs(op, full_saving, inline=False):
     costs["affine_state"] = costs["fdr_state_bwd"]
     costs["segmented_state"] = costs["fdr_state_bwd"]
     if not full_saving:
+        costs["paired_recurrences"] = tuple(a + b for a, b in zip(costs["fdr_fwd_h"], costs["fdr_state_bwd"]))
         costs["affine_recurrences"] = tuple(a + b for a, b in zip(costs["fdr_fwd_h"], costs["fdr_state_bwd"]))
     return costs
 
@@ -217,7 +218,17 @@ def setup(cfg, device):
         pre = kern["fdr_prepare_wu"]()
         ks, qs, ws = (pre["kg"], pre["qg"], pre["w"]) if vec else (xs["k"], xs["q"], pre["w"])
         aqk = sv["Aqk"] if vec else pre["Aqk"]
-    if keep and ops._state_method("auto", cfg["B"], cfg["H"], NT) == "segmented":
+    vb_pair = 0 if keep else ops.paired_tile(cfg["B"], cfg["H"], NT, gate)
+    if vb_pair:
+        # vector gates, batch x heads too small for one recurrence to fill the GPU: the state
+        # recurrence and the forward scan side by side (two streams, as the backend runs them)
+        from rewy_amd.backends.backward import _side_by_side
+        kern["paired_recurrences"] = lambda: _side_by_side(
+            lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk, want_dh0=xs["h0"] is not None,
+                                  method="direct", value_block=vb_pair),
+            lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"], method="direct", value_block=vb_pair))
+        (dh, dR, _), (h, v_new, _) = kern["paired_recurrences"]()
+    elif keep and ops._state_method("auto", cfg["B"], cfg["H"], NT) == "segmented":
         # long rows, few heads: segment maps in parallel, a short chain, segments rerun
         kern["segmented_state"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
                                                         want_dh0=xs["h0"] is not None, method="segmented")
@@ -303,7 +314,8 @@ def time_kernels(kern, reps):
     return out
 
 
-SEQUENTIAL = ("fdr_state_bwd", "fdr_fwd_h", "affine_state", "affine_recurrences", "segmented_state")
+SEQUENTIAL = ("fdr_state_bwd", "fdr_fwd_h", "affine_state", "affine_recurrences", "segmented_state",
+              "paired_recurrences")
 
 
 def measure(cfg, steps, warmup):

@@ -17,6 +17,9 @@ When batch x heads is too small to fill the GPU and the sequence long, the two
 recurrences run instead in affine-step form (after ``fdr_prepare_wu``: w, u and qg, kg or Aqk) (``ops.recurrences``,
 ``fdr_affine_*``): chunk-parallel step matrices, one scan launch carrying both
 recurrences side by side, and a chunk-parallel pass for v_new and dR.
+For vector gates with 24 <= batch x heads < 128 the recompute policy runs the direct backward
+state recurrence and the direct forward scan side by side on two streams, at a value-tile
+width that gives each at most half the CUs (``ops.paired_tile``).
 With a few more heads and long rows the recompute policy runs the forward scan
 (``fdr_fwd_h``) on the current stream beside the segmented backward state recurrence
 (``fdr_state_bwd_segmented``) on a second stream (``ops.side_by_side_pays``).
@@ -24,6 +27,8 @@ With a few more heads and long rows the recompute policy runs the forward scan
 There is no fallback: a missing HIP library or an unsupported argument raises.
 """
 from __future__ import annotations
+
+import threading
 
 import torch
 
@@ -86,6 +91,7 @@ def _f32(x):
 
 
 _SIDE = {}
+_SIDE_LOCK = threading.Lock()
 
 
 def _side_by_side(first, second):
@@ -96,11 +102,20 @@ def _side_by_side(first, second):
     backward state recurrence).  first() is enqueued first so that its few long-lived
     work-groups are placed before second()'s launches fill the GPU (the other way round,
     the scan's work-groups waited for free CUs and the scan took 2.4x as long).  The tensors
-    that second() returns are marked as used by the current stream."""
+    that second() returns are marked as used by the current stream.
+
+    Lifetimes: second() reads tensors allocated on the current stream.  The join
+    (``cur.wait_stream(side)``) is enqueued before this function returns, so memory that
+    the caller frees afterwards can only be reused by work ordered after the side stream's
+    kernels.  A caller must not free an input of second() before this function returns.
+    The side streams are created once per device, under a lock."""
     cur = torch.cuda.current_stream()
     side = _SIDE.get(cur.device)
     if side is None:
-        side = _SIDE[cur.device] = torch.cuda.Stream(cur.device)    # default priority
+        with _SIDE_LOCK:
+            side = _SIDE.get(cur.device)
+            if side is None:
+                side = _SIDE[cur.device] = torch.cuda.Stream(cur.device)    # default priority
     side.wait_stream(cur)
     a = first()
     with torch.cuda.stream(side):
@@ -133,6 +148,18 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
                                                 do, scale, aqk=Aqk, h0=_f32(initial_state), dht=_f32(dht),
                                                 want_dh0=initial_state is not None, state_v_first=vf)
         saved, hvf = dict(v_new=v_new, h=h), False
+    elif recompute and vl is None and ops.paired_tile(N, H, NT, ops.GATE_VECTOR):
+        # batch x heads too small for one direct recurrence to fill the GPU: the backward
+        # state recurrence and the forward scan side by side, both direct, at a value-tile
+        # width that gives each launch at most half the CUs
+        vb = ops.paired_tile(N, H, NT, ops.GATE_VECTOR)
+        pre = _prepare_vector(k, v, g, Akk, gates, q, vl)
+        (dh, dR, dh0), (h, v_new, _) = _side_by_side(
+            lambda: _state_vector(pre, g, do, scale, Aqk, dht, initial_state, vl, vf, method="direct",
+                                  value_block=vb),
+            lambda: ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
+                              method="direct", value_block=vb, state_v_first=vf))
+        saved, hvf = dict(v_new=v_new, h=h), False
     elif recompute and (ops.side_by_side_pays(N, H, NT) if vl is None else
                         ops.SIDE_BY_SIDE and not ops.fwd_h_wy_pays(N, H, ops.GATE_VECTOR, vl)):
         # the forward scan on one stream beside the backward state recurrence on another:
@@ -156,9 +183,9 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     return _group_sum(out, q.shape[2]), dh0
 
 
-def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, vl=None, vf=False, method="auto"):
+def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, vl=None, vf=False, method="auto", value_block=0):
     return ops.state_bwd(_bf(saved["qg"]), _bf(saved["kg"]), _bf(saved["w"]), g, ops.GATE_VECTOR, do, scale,
-                         aqk=Aqk, dht=_f32(dht), want_dh0=initial_state is not None,
+                         aqk=Aqk, dht=_f32(dht), want_dh0=initial_state is not None, value_block=value_block,
                          method=method if vl is None else "direct", varlen=vl, state_v_first=vf)
 
 

@@ -1,0 +1,123 @@
+"""The recompute policy's paired direct recurrences (vector gates, 24 <= B*H < 128): the
+direct backward state recurrence (fdr_state_bwd) on the current stream beside the direct
+forward scan (fdr_fwd_h) on a second stream, both at the value-tile width
+``ops.paired_tile`` picks (32 at B*H = 32, 64 at B*H = 48).  For KDA and GDN2:
+
+* the public autograd backward (recompute policy) against the fp64 oracle at the
+  reference's acceptance tolerances (validation.py:40-45, :68);
+* the same gradients, bit for bit, as the same launches enqueued on one stream;
+* against the policy switched off (the pair one after the other at the default tile
+  width): rel-L2 <= 1e-5, the tile width changing no arithmetic of a value column;
+* captured in a HIP graph and replayed three times with eager work between the replays.
+"""
+import pytest
+import torch
+
+from oracle import delta_oracle as O
+from tests._inputs import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+OPNAME = {"kda": "chunk_kda", "gdn2": "chunk_gdn2"}
+GRAD = {"q": "dq", "k": "dk", "v": "dv", "g": "dg", "beta": "dbeta", "b": "db", "w": "dw", "initial_state": "dh0"}
+SHAPES = [(2, 512, 16, 32), (1, 256, 48, 64)]     # B, T, H, the tile width paired_tile picks
+
+
+def _rel(a, r):
+    a, r = a.double(), r.double()
+    return float((a - r).norm() / r.norm().clamp_min(1e-30))
+
+
+def _seam(op, B, T, H):
+    """The backward seam of `op` (recompute policy) on fixed inputs, as a closure."""
+    from rewy_amd.backends import backward as bw
+    from rewy_amd.hip_forward import chunk_forward_hip
+    dev = torch.device("cuda")
+    xs, dO = make_inputs(op, B, T, H, seed=51, gate="mild")
+    xs = {n: (None if v is None else v.to(dev)) for n, v in xs.items()}
+    dO = dO.to(dev)
+    _, _, sv = chunk_forward_hip(op, xs["q"], xs["k"], xs["v"], g=xs.get("g"), beta=xs.get("beta"),
+                                 b=xs.get("b"), w=xs.get("w"), initial_state=xs["initial_state"])
+    dht = torch.randn(B, H, 128, 128, generator=torch.Generator().manual_seed(5)).mul(0.1).to(dev)
+    common = dict(q=xs["q"], k=xs["k"], v=xs["v"], scale=sv["scale"], initial_state=xs["initial_state"], do=dO,
+                  dht=dht, Aqk=sv["Aqk"], Akk=sv["Akk"], g=sv["gc"])
+    if op == "kda":
+        return lambda: bw.kda_backward(beta=xs["beta"], **common)[:6]
+    return lambda: bw.gdn2_backward(b=xs["b"], w_gate=xs["w"], **common)[:7]
+
+
+@pytest.mark.parametrize("B,T,H,vb", SHAPES)
+@pytest.mark.parametrize("op", ["kda", "gdn2"])
+def test_paired_public_backward_matches_oracle(op, B, T, H, vb, monkeypatch):
+    import rewy_amd as fdr
+    from rewy_amd import ops
+    from rewy_amd.backends import backward as bw
+    print(f"\n[paired] op={op} B={B} T={T} H={H}", flush=True)
+    assert ops.paired_tile(B, H, T // 64, ops.GATE_VECTOR) == vb
+    calls = []
+    real = bw._side_by_side
+    monkeypatch.setattr(bw, "_side_by_side", lambda a, b: (calls.append(1), real(a, b))[1])
+    xs, dO = make_inputs(op, B, T, H, seed=52, gate="mild")
+    dev = torch.device("cuda")
+    xg = {k: v.to(dev).requires_grad_() for k, v in xs.items()}
+    with fdr.use_backend("optimized", ops=(op,)):
+        o, ht = getattr(fdr, OPNAME[op])(**xg, output_final_state=True, disable_recompute=False)
+    dht = (torch.randn(ht.shape, generator=torch.Generator().manual_seed(9)) * 0.1).to(dev)
+    grads = torch.autograd.grad((o, ht), tuple(xg.values()), (dO.to(dev), dht))
+    torch.cuda.synchronize()
+    assert calls, "the paired recurrences did not run"
+    n = lambda x: None if x is None else x.detach().double().cpu().numpy()
+    ref = O.backward(op, n(xs["q"]), n(xs["k"]), n(xs["v"]), g=n(xs.get("g")), beta=n(xs.get("beta")),
+                     b=n(xs.get("b")), w=n(xs.get("w")), h0=n(xs["initial_state"]), dO=n(dO), dht=n(dht))
+    report = {}
+    for name, grad in zip(xs, grads):
+        e = O.error(ref[GRAD[name]], n(grad), O.limit_for(GRAD[name]))
+        report[name] = round(e["relative_l2"], 5)
+        assert e["passed"], (name, e)
+    print("rel-L2 vs oracle", report, flush=True)
+
+
+@pytest.mark.parametrize("B,T,H,vb", SHAPES)
+@pytest.mark.parametrize("op", ["kda", "gdn2"])
+def test_paired_equals_one_stream_and_policy_off(op, B, T, H, vb, monkeypatch):
+    from rewy_amd import ops
+    from rewy_amd.backends import backward as bw
+    print(f"\n[paired-streams] op={op} B={B} T={T} H={H}", flush=True)
+    run = _seam(op, B, T, H)
+    got = [x.clone() for x in run()]
+    monkeypatch.setattr(bw, "_side_by_side", lambda first, second: (first(), second()))
+    one = run()
+    torch.cuda.synchronize()
+    for i, (a, r) in enumerate(zip(got, one)):
+        assert torch.equal(a, r), (op, i)
+    monkeypatch.undo()
+    monkeypatch.setattr(ops, "PAIRED", False)
+    off = run()
+    torch.cuda.synchronize()
+    for i, (a, r) in enumerate(zip(got, off)):
+        e = _rel(a, r)
+        assert e <= 1e-5, (op, i, e)
+
+
+@pytest.mark.parametrize("op", ["kda", "gdn2"])
+def test_paired_under_graph_capture(op):
+    B, T, H, _ = SHAPES[0]
+    print(f"\n[paired-graph] op={op} B={B} T={T} H={H}", flush=True)
+    run = _seam(op, B, T, H)
+    eager = [x.clone() for x in run()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        held = run()
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (a, r) in enumerate(zip(held, eager)):
+            assert torch.equal(a, r), (op, rep, i)
+        run()          # eager work between the replays
+        torch.cuda.synchronize()

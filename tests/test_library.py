@@ -167,3 +167,18 @@ def test_side_by_side_rule():
     meta = lambda B, T, H: torch.empty(B, T, H, 1, device="meta")
     assert not ops.affine_pays(meta(1, 8192, 16)) and ops.affine_pays(meta(1, 8192, 4))
     assert ops.affine_pays(meta(1, 2048, 16))
+
+
+def test_paired_rule():
+    """ops.paired_tile (recompute policy, vector gates: the direct state recurrence beside the
+    direct forward scan): the narrowest of 32 / 64 at which each launch holds <= 128
+    work-groups, for 24 <= B*H < 128 only, and never for scalar / no gates."""
+    from rewy_amd import ops
+    V, S = ops.GATE_VECTOR, ops.GATE_SCALAR
+    assert ops.paired_tile(2, 32, 128, V) == 64          # GDN2 configs[3]
+    assert ops.paired_tile(2, 16, 64, V) == 32 and ops.paired_tile(1, 24, 256, V) == 32
+    assert ops.paired_tile(1, 48, 128, V) == 64
+    assert ops.paired_tile(1, 16, 512, V) == 0           # few heads: affine / side-by-side forms
+    assert ops.paired_tile(8, 16, 64, V) == 0            # the fused sweep fills the GPU
+    assert ops.paired_tile(1, 96, 64, V) == 0            # 64-wide tiles would need 192 CUs each
+    assert ops.paired_tile(2, 32, 128, S) == 0
