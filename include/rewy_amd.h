@@ -160,6 +160,45 @@ hipError_t fdr_chunk_bwd_wy(const void* q, const void* k, const void* v, const v
                             int h_v_first, int B, int T, int H, int qk_heads, int K, int V, int chunk, float scale,
                             hipStream_t stream);
 
+/* fdr_chunk_bwd_wy over a packed variable-length batch whose sequences start anywhere (the
+ * packing described at the top; the reference seam's cu_seqlens / chunk_indices,
+ * kernels/kda_residual_npu_onchip.py:683-702).  h, dh are [num_chunks,H,K,V] (h [V,K] when
+ * h_v_first); rows past a sequence's end are neither read nor written. */
+hipError_t fdr_chunk_bwd_wy_varlen(const void* q, const void* k, const void* v, const void* v_new, const void* dO,
+                                   const void* dR, const float* g, const float* beta, const float* Akk,
+                                   const void* h, const void* dh, float* dq, float* dk, void* dv, float* dbeta,
+                                   float* dg, float* dA, int h_v_first, const int* cu_seqlens,
+                                   const int* chunk_indices, int num_chunks, int H, int qk_heads, int K, int V,
+                                   int chunk, float scale, hipStream_t stream);
+
+/*
+ * GDN2's kernel-level WY seam: FLA's chunk_gdn2_bwd_wy_dqkg_fused as the reference replaces it
+ * (backends/backward.py:43-47: gdn2_consumer_fp32.residual, kernels/gdn2_consumer_fp32.py:76-86,
+ * whose joint consumer, :8-75, the intra seam then runs).  The reference's producer computes
+ * P = A^T dR, dv2 = w_gate P, dw = v P and DM = -strict_tril(P R^T); its joint consumer the
+ * state terms, the gate epilogue and the matrix intra.  Here every term but the matrix intra:
+ * dq, dk fp32 [B,T,H,K], dv bf16 [B,T,H,V] (complete), db fp32 [B,T,H,K] (without the intra's
+ * ue k), dw bf16 [B,T,H,V] (complete), dg fp32 before the in-chunk reverse cumsum (the last-row
+ * state term included), dA fp32 [B,T,H,64] = DM.  Then fdr_matrix_intra(..., b_gate, dAqk,
+ * dA, dq, dk, db, dg) and the reverse cumsum of dg give fdr_chunk_bwd's gradients.  q and k
+ * have one head per value head (H).
+ */
+hipError_t fdr_gdn2_chunk_bwd_wy(const void* q, const void* k, const void* v, const void* v_new, const void* dO,
+                                 const void* dR, const float* g, const void* b_gate, const void* w_gate,
+                                 const float* Akk, const void* h, const void* dh, float* dq, float* dk, void* dv,
+                                 float* db, void* dw, float* dg, float* dA, int h_v_first, int B, int T, int H, int K,
+                                 int V, int chunk, float scale, hipStream_t stream);
+
+/* fdr_gdn2_chunk_bwd_wy over a packed variable-length batch (gdn2_consumer_fp32.py:76-80's
+ * cu_seqlens / chunk_indices), laid out as for fdr_chunk_bwd_wy_varlen. */
+hipError_t fdr_gdn2_chunk_bwd_wy_varlen(const void* q, const void* k, const void* v, const void* v_new,
+                                        const void* dO, const void* dR, const float* g, const void* b_gate,
+                                        const void* w_gate, const float* Akk, const void* h, const void* dh,
+                                        float* dq, float* dk, void* dv, float* db, void* dw, float* dg, float* dA,
+                                        int h_v_first, const int* cu_seqlens, const int* chunk_indices,
+                                        int num_chunks, int H, int K, int V, int chunk, float scale,
+                                        hipStream_t stream);
+
 /* fdr_chunk_bwd over a variable-length batch whose sequences start anywhere (the packing
  * described at the top; the reference's chunk-stage kernels with cu_seqlens / chunk_indices,
  * e.g. kernels/endpoint_intra.py:58-63).  h, dh are [num_chunks,H,K,V] (or [V,K]). */
@@ -282,6 +321,15 @@ hipError_t fdr_matrix_intra(const void* q, const void* k, const float* g, const 
                             const void* b_gate, const float* dAqk, const float* dAkk, float* dq,
                             float* dk, float* db, float* dg, int B, int T, int H, int qk_heads, int K, int chunk,
                             int beta_complete, hipStream_t stream);
+
+/* fdr_matrix_intra over a packed variable-length batch whose sequences start anywhere (the
+ * reference seam's cu_seqlens / chunk_indices, kernels/endpoint_intra.py:318-321,
+ * gdn2_consumer_fp32.py:91-94).  Rows past a sequence's end are neither read nor written. */
+hipError_t fdr_matrix_intra_varlen(const void* q, const void* k, const float* g, const float* beta,
+                                   const void* b_gate, const float* dAqk, const float* dAkk, float* dq, float* dk,
+                                   float* db, float* dg, const int* cu_seqlens, const int* chunk_indices,
+                                   int num_chunks, int H, int qk_heads, int K, int chunk, int beta_complete,
+                                   hipStream_t stream);
 
 /*
  * Forward, chunk-parallel part 1: gate cumsum and the intra-chunk matrices.

@@ -44,6 +44,8 @@
 // contractions over tokens read them transposed (ds_read_b64_tr_b16).  P and the
 // L/D tiles are produced by MFMAs whose accumulator layout stores contiguously
 // into the orientation the next contraction reads.
+#include <atomic>
+
 #include "common.hpp"
 #include "rewy_amd.h"
 
@@ -281,9 +283,9 @@ __device__ __forceinline__ void chunk_body(
   if (HQ <= 0) HQ = H;
   using LY = PostLayout<GATE, VEC_B, INTRA, PIPE, ORIG>;
   static_assert(!ORIG || (GATE == CG_VECTOR && !VEC_B && !INTRA && !PIPE), "original formulation: KDA only");
-  static_assert(!MAP || (!INTRA && !PIPE && !ORIG), "variable-length rows: the plain and the gate-fold chunk kernels");
-  static_assert(!WY || (GATE == CG_VECTOR && !VEC_B && !INTRA && !PIPE && !ORIG && FOLD < 0 && !MAP),
-                "the WY seam: KDA, dense rows");
+  static_assert(!MAP || (!PIPE && !ORIG), "variable-length rows: the plain, gate-fold, intra and WY kernels");
+  static_assert(!WY || (GATE == CG_VECTOR && !INTRA && !PIPE && !ORIG && FOLD < 0),
+                "the WY seam: KDA and GDN2");
   using post::LDT;
   auto B16 = [&](int off) { return reinterpret_cast<bf16*>(regA + off); };
   auto B16b = [&](int off) { return reinterpret_cast<bf16*>(regB + off); };
@@ -360,8 +362,10 @@ __device__ __forceinline__ void chunk_body(
     for (int i = 0; i < 2; ++i) {
       const int p = tid + 512 * i;        // 1024 pieces of 4 fp32: row p >> 4
       const int row = p >> 4, c4 = (p & 15) * 4;
-      f32x4 a = *reinterpret_cast<const f32x4*>(daqk + (tok0 * H + h) * C + (size_t)row * rsa + c4);
-      f32x4 d = *reinterpret_cast<const f32x4*>(akk + (tok0 * H + h) * C + (size_t)row * rsa + c4);
+      // (a packed batch's missing rows read as zeros; their columns lie above the diagonal
+      // of every row that exists)
+      f32x4 a = *reinterpret_cast<const f32x4*>(rw.src(daqk + (tok0 * H + h) * C + (size_t)row * rsa + c4, row));
+      f32x4 d = *reinterpret_cast<const f32x4*>(rw.src(akk + (tok0 * H + h) * C + (size_t)row * rsa + c4, row));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if (c4 + j > row) a[j] = 0.f;
@@ -376,7 +380,7 @@ __device__ __forceinline__ void chunk_body(
       *reinterpret_cast<bf16x4*>(Drl + row * LDT + c4) = lo;
     }
     if (tid < C) {
-      if constexpr (!VEC_B) sBeta[tid] = beta[(tok0 + tid) * H + h];
+      if constexpr (!VEC_B) sBeta[tid] = *rw.src(beta + (tok0 + tid) * H + h, tid);
     }
   } else {
     // (the persistent kernel stages A hi/lo at the end of the previous item)
@@ -745,7 +749,8 @@ __device__ __forceinline__ void chunk_body(
         *reinterpret_cast<bf16x4*>(Drh + i * LDT + 16 * I + 4 * lg) = hi;
         *reinterpret_cast<bf16x4*>(Drl + i * LDT + 16 * I + 4 * lg) = lo;
         // the WY seam's dA: row i, columns s = 16 I + 4 lg .. + 3 (zero on and above the diagonal)
-        if constexpr (WY) *reinterpret_cast<f32x4*>(dA_wy + (tok0 * H + h) * C + (size_t)i * rsa + 16 * I + 4 * lg) = dv4;
+        if constexpr (WY)
+          *reinterpret_cast<f32x4*>(rw.dst(dA_wy + (tok0 * H + h) * C + (size_t)i * rsa + 16 * I + 4 * lg, i)) = dv4;
       }
     }
   }   // phase 2
@@ -1185,7 +1190,9 @@ __device__ __forceinline__ void chunk_body(
     for (int I = 0; I < 4; ++I)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int off = (16 * I + 4 * lg + r) * rsk32 + kk;
+        const int t = 16 * I + 4 * lg + r;
+        const int off = t * rsk32 + kk;
+        if (!rw.ok(t)) continue;            // a packed batch's missing rows
         dq32[kofs + off] += aq[I][r];
         dk32[kofs + off] += ak[I][r];
         dg_out[kofs + off] += aw[I][r];
@@ -1204,14 +1211,17 @@ __device__ __forceinline__ void chunk_body(
         const int t = 16 * I + 4 * lg + r;
         const int off = t * rsk32 + kk;
         if constexpr (WY) {
-          dq32[kofs + off] = aq[I][r];
-          dk32[kofs + off] = ak[I][r];
+          *rw.dst(dq32 + kofs + off, t) = aq[I][r];
+          *rw.dst(dk32 + kofs + off, t) = ak[I][r];
         } else {
           *rw.dst(dqb + off, t) = to_bf16(aq[I][r]);
           *rw.dst(dkb + off, t) = to_bf16(ak[I][r]);
         }
         if constexpr (GATE == CG_VECTOR && FOLD < 0) *rw.dst(dgb + off, t) = aw[I][r];
-        if constexpr (VEC_B) *rw.dst(dbb + off, t) = to_bf16(adb[I][r]);
+        if constexpr (VEC_B) {
+          if constexpr (WY) *rw.dst(db32 + kofs + off, t) = adb[I][r];   // the intra adds ue k
+          else *rw.dst(dbb + off, t) = to_bf16(adb[I][r]);
+        }
       }
     }
     if constexpr (FOLD >= 0) {
@@ -1295,7 +1305,7 @@ __device__ __forceinline__ void chunk_body(
     // residual producer already accounted for the rest (beta_complete)
     if constexpr (!VEC_B) {
       const size_t row = (tok0 + tid) * H + h;
-      if (!beta_complete || fabsf(sBeta[tid]) < 1e-6f) dbeta_out[row] += fbs;
+      if (rw.ok(tid) && (!beta_complete || fabsf(sBeta[tid]) < 1e-6f)) dbeta_out[row] += fbs;
     }
   } else if (tid < C) {
     const size_t row = (tok0 + tid) * H + h;
@@ -1365,23 +1375,27 @@ __global__ __launch_bounds__(512) void chunk_bwd_original_kernel(
       smem + LY::REGION_A, reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin);
 }
 
-// KDA's kernel-level WY seam (every term but the matrix intra; see WY above)
-template <bool HVF>
+// The kernel-level WY seams (every term but the matrix intra; see WY above): KDA (scalar
+// beta) and GDN2 (VEC_B: erase gate b, write gate w; db in fp32 for the intra to complete,
+// dw complete); MAP: a packed variable-length batch (cu, ci as for chunk_bwd_kernel)
+template <bool VEC_B, bool HVF, bool MAP>
 __global__ __launch_bounds__(512) void chunk_bwd_wy_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ vnew, const bf16* __restrict__ dO, const bf16* __restrict__ dR,
-    const float* __restrict__ g, const float* __restrict__ beta, const float* __restrict__ akk,
-    const bf16* __restrict__ hst, const bf16* __restrict__ dhst, float* __restrict__ dq32, float* __restrict__ dk32,
-    bf16* __restrict__ dv_out, float* __restrict__ dg_out, float* __restrict__ dbeta_out, float* __restrict__ dA,
-    int T, int H, float scale, int HQ) {
-  using LY = PostLayout<CG_VECTOR, false>;
+    const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
+    const bf16* __restrict__ wgate, const float* __restrict__ akk, const bf16* __restrict__ hst,
+    const bf16* __restrict__ dhst, float* __restrict__ dq32, float* __restrict__ dk32, bf16* __restrict__ dv_out,
+    float* __restrict__ dg_out, float* __restrict__ dbeta_out, float* __restrict__ db32, bf16* __restrict__ dw_out,
+    float* __restrict__ dA, int T, int H, float scale, int HQ, const int* __restrict__ cu,
+    const int* __restrict__ ci) {
+  using LY = PostLayout<CG_VECTOR, VEC_B>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
-  chunk_body<CG_VECTOR, false, false, false, -1, HVF, false, false, true>(
-      q, k, v, vnew, dO, dR, g, beta, nullptr, nullptr, akk, hst, dhst, nullptr, nullptr, dv_out, dg_out, dbeta_out,
-      nullptr, nullptr, T, H, scale, nullptr, dq32, dk32, nullptr, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
-      reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin, nullptr, 0.f, HQ, nullptr,
-      nullptr, dA);
+  chunk_body<CG_VECTOR, VEC_B, false, false, -1, HVF, false, MAP, true>(
+      q, k, v, vnew, dO, dR, g, beta, bgate, wgate, akk, hst, dhst, nullptr, nullptr, dv_out, dg_out, dbeta_out,
+      nullptr, dw_out, T, H, scale, nullptr, dq32, dk32, db32, 0, blockIdx.x, -1, smem, smem + LY::REGION_A,
+      reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin, nullptr, 0.f, HQ, cu,
+      ci, dA);
 }
 
 // KDA with the gate backward folded into the dg stores (no dg output); MAP: a packed
@@ -1449,54 +1463,56 @@ __global__ __launch_bounds__(512) void chunk_bwd_pipe_kernel(
   }
 }
 
-template <bool VEC_B>
+template <bool VEC_B, bool MAP = false>
 __global__ __launch_bounds__(512) void matrix_intra_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ g,
     const float* __restrict__ beta, const bf16* __restrict__ bgate, const float* __restrict__ daqk,
     const float* __restrict__ dakk, float* __restrict__ dq, float* __restrict__ dk,
-    float* __restrict__ db, float* __restrict__ dg, int T, int H, int beta_complete, int HQ) {
+    float* __restrict__ db, float* __restrict__ dg, int T, int H, int beta_complete, int HQ,
+    const int* __restrict__ cu, const int* __restrict__ ci) {
   using LY = PostLayout<CG_VECTOR, VEC_B, true>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PhaseIn pin;
-  chunk_body<CG_VECTOR, VEC_B, true>(q, k, nullptr, nullptr, nullptr, nullptr, g, beta, bgate, nullptr, dakk,
-                                     nullptr, nullptr, nullptr, nullptr, nullptr, dg, VEC_B ? nullptr : db,
-                                     nullptr, nullptr, T, H, 1.f, daqk, dq, dk, VEC_B ? db : nullptr,
-                                     beta_complete, blockIdx.x, -1, smem, smem + LY::REGION_A,
-                                     reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin,
-                                     nullptr, 0.f, HQ);
+  chunk_body<CG_VECTOR, VEC_B, true, false, -1, false, false, MAP>(
+      q, k, nullptr, nullptr, nullptr, nullptr, g, beta, bgate, nullptr, dakk, nullptr, nullptr, nullptr, nullptr,
+      nullptr, dg, VEC_B ? nullptr : db, nullptr, nullptr, T, H, 1.f, daqk, dq, dk, VEC_B ? db : nullptr,
+      beta_complete, blockIdx.x, -1, smem, smem + LY::REGION_A,
+      reinterpret_cast<float*>(smem + LY::REGION_A + LY::REGION_B), nullptr, nullptr, pin, nullptr, 0.f, HQ, cu, ci);
 }
 
 // Per-device, once: raise a kernel's dynamic-LDS limit (the attribute is held per
-// device).  Concurrent first calls may both set it, which is harmless.
+// device).  The flags are atomics: concurrent first calls from several host threads may
+// both set the attribute (idempotent), and neither reads a torn flag.
 constexpr int kMaxDevices = 64;
-static hipError_t allow_dynamic_lds(const void* kern, int bytes, bool (&done)[kMaxDevices]) {
+using LdsFlags = std::atomic<bool>[kMaxDevices];
+static hipError_t allow_dynamic_lds(const void* kern, int bytes, LdsFlags& done) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  if (!done[dev]) {
+  if (!done[dev].load(std::memory_order_acquire)) {
     e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (e != hipSuccess) return e;
-    done[dev] = true;
+    done[dev].store(true, std::memory_order_release);
   }
   return hipSuccess;
 }
 
 // compute units of the current device (cached per device)
 static hipError_t device_cus(int& cus) {
-  static int cached[kMaxDevices] = {};
+  static std::atomic<int> cached[kMaxDevices] = {};
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return e;
     if (n <= 0) return hipErrorInvalidDevice;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  cus = cached[dev];
+  cus = n;
   return hipSuccess;
 }
 
@@ -1513,7 +1529,7 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
   if (cu) {
     // a packed variable-length batch (sequences starting anywhere): the plain kernel
     auto kern = chunk_bwd_kernel<GATE, VEC_B, HVF, true>;
-    static bool attr_set[kMaxDevices] = {};
+    static LdsFlags attr_set = {};
     const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(items), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k,
@@ -1538,7 +1554,7 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
     return hipGetLastError();
   }
   auto kern = chunk_bwd_kernel<GATE, VEC_B, HVF>;
-  static bool attr_set[kMaxDevices] = {};
+  static LdsFlags attr_set = {};
   const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
   if (e != hipSuccess) return e;
   const int grid = items;
@@ -1604,33 +1620,95 @@ extern "C" hipError_t fdr_chunk_bwd(const void* q, const void* k, const void* v,
                             nullptr);
 }
 
+template <bool VEC_B, bool HVF, bool MAP>
+static hipError_t launch_wy(const void* q, const void* k, const void* v, const void* v_new, const void* dO,
+                            const void* dR, const float* g, const float* beta, const void* b_gate,
+                            const void* w_gate, const float* Akk, const void* h, const void* dh, float* dq,
+                            float* dk, void* dv, float* dbeta, float* db, void* dw, float* dg, float* dA, int items,
+                            int T, int H, int HQ, float scale, const int* cu, const int* ci, hipStream_t stream) {
+  using LY = PostLayout<CG_VECTOR, VEC_B>;
+  auto kern = chunk_bwd_wy_kernel<VEC_B, HVF, MAP>;
+  static LdsFlags attr_set = {};
+  const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(items), dim3(512), LY::BYTES, stream, (const bf16*)q, (const bf16*)k, (const bf16*)v,
+                     (const bf16*)v_new, (const bf16*)dO, (const bf16*)dR, g, beta, (const bf16*)b_gate,
+                     (const bf16*)w_gate, Akk, (const bf16*)h, (const bf16*)dh, dq, dk, (bf16*)dv, dg, dbeta, db,
+                     (bf16*)dw, dA, T, H, scale, HQ, cu, ci);
+  return hipGetLastError();
+}
+
+// KDA (beta) or GDN2 (b_gate, w_gate) WY seam over B rows of T tokens, or (cu, ci) a packed
+// batch of T / 64 chunks
+static hipError_t wy_dispatch(const void* q, const void* k, const void* v, const void* v_new, const void* dO,
+                              const void* dR, const float* g, const float* beta, const void* b_gate,
+                              const void* w_gate, const float* Akk, const void* h, const void* dh, float* dq,
+                              float* dk, void* dv, float* dbeta, float* db, void* dw, float* dg, float* dA,
+                              int h_v_first, int B, int T, int H, int HQ, float scale, const int* cu, const int* ci,
+                              hipStream_t stream) {
+  if (T <= 0 || T % C || B <= 0 || H <= 0 || H % HQ) return hipErrorInvalidValue;
+  if (!q || !k || !v || !v_new || !dO || !dR || !g || !Akk || !h || !dh || !dq || !dk || !dv || !dg || !dA)
+    return hipErrorInvalidValue;
+  const bool vb = b_gate != nullptr;
+  if (vb ? (!w_gate || !db || !dw || HQ != H) : (!beta || !dbeta)) return hipErrorInvalidValue;
+  const int items = B * H * (T / C);
+#define W_ARGS q, k, v, v_new, dO, dR, g, beta, b_gate, w_gate, Akk, h, dh, dq, dk, dv, dbeta, db, dw, dg, dA, items, \
+               T, H, HQ, scale, cu, ci, stream
+#define W_MAP(VB, HV) return cu ? launch_wy<VB, HV, true>(W_ARGS) : launch_wy<VB, HV, false>(W_ARGS);
+  if (vb) {
+    if (h_v_first) W_MAP(true, true) else W_MAP(true, false)
+  }
+  if (h_v_first) W_MAP(false, true) else W_MAP(false, false)
+#undef W_MAP
+#undef W_ARGS
+}
+
 extern "C" hipError_t fdr_chunk_bwd_wy(const void* q, const void* k, const void* v, const void* v_new,
                                        const void* dO, const void* dR, const float* g, const float* beta,
                                        const float* Akk, const void* h, const void* dh, float* dq, float* dk,
                                        void* dv, float* dbeta, float* dg, float* dA, int h_v_first, int B, int T,
                                        int H, int qk_heads, int K, int V, int chunk, float scale, hipStream_t stream) {
-  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
-  const int HQ = qk_heads > 0 ? qk_heads : H;
-  if (H % HQ) return hipErrorInvalidValue;
-  if (!q || !k || !v || !v_new || !dO || !dR || !g || !beta || !Akk || !h || !dh || !dq || !dk || !dv || !dbeta ||
-      !dg || !dA)
+  if (K != KD || V != VD || chunk != C) return hipErrorInvalidValue;
+  return wy_dispatch(q, k, v, v_new, dO, dR, g, beta, nullptr, nullptr, Akk, h, dh, dq, dk, dv, dbeta, nullptr,
+                     nullptr, dg, dA, h_v_first, B, T, H, qk_heads > 0 ? qk_heads : H, scale, nullptr, nullptr, stream);
+}
+
+extern "C" hipError_t fdr_chunk_bwd_wy_varlen(const void* q, const void* k, const void* v, const void* v_new,
+                                              const void* dO, const void* dR, const float* g, const float* beta,
+                                              const float* Akk, const void* h, const void* dh, float* dq, float* dk,
+                                              void* dv, float* dbeta, float* dg, float* dA, int h_v_first,
+                                              const int* cu_seqlens, const int* chunk_indices, int num_chunks, int H,
+                                              int qk_heads, int K, int V, int chunk, float scale,
+                                              hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || num_chunks <= 0 || !cu_seqlens || !chunk_indices)
     return hipErrorInvalidValue;
-  using LY = PostLayout<CG_VECTOR, false>;
-  const int items = B * H * (T / C);
-#define WY_LAUNCH(HV)                                                                                          \
-  {                                                                                                            \
-    auto kern = chunk_bwd_wy_kernel<HV>;                                                                       \
-    static bool attr_set[kMaxDevices] = {};                                                                    \
-    const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);                            \
-    if (e != hipSuccess) return e;                                                                             \
-    hipLaunchKernelGGL(kern, dim3(items), dim3(512), LY::BYTES, stream, (const bf16*)q, (const bf16*)k,         \
-                       (const bf16*)v, (const bf16*)v_new, (const bf16*)dO, (const bf16*)dR, g, beta, Akk,     \
-                       (const bf16*)h, (const bf16*)dh, dq, dk, (bf16*)dv, dg, dbeta, dA, T, H, scale, HQ);   \
-  }
-  if (h_v_first) WY_LAUNCH(true)
-  else WY_LAUNCH(false)
-#undef WY_LAUNCH
-  return hipGetLastError();
+  return wy_dispatch(q, k, v, v_new, dO, dR, g, beta, nullptr, nullptr, Akk, h, dh, dq, dk, dv, dbeta, nullptr,
+                     nullptr, dg, dA, h_v_first, 1, num_chunks * C, H, qk_heads > 0 ? qk_heads : H, scale,
+                     cu_seqlens, chunk_indices, stream);
+}
+
+extern "C" hipError_t fdr_gdn2_chunk_bwd_wy(const void* q, const void* k, const void* v, const void* v_new,
+                                            const void* dO, const void* dR, const float* g, const void* b_gate,
+                                            const void* w_gate, const float* Akk, const void* h, const void* dh,
+                                            float* dq, float* dk, void* dv, float* db, void* dw, float* dg, float* dA,
+                                            int h_v_first, int B, int T, int H, int K, int V, int chunk, float scale,
+                                            hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || !b_gate) return hipErrorInvalidValue;
+  return wy_dispatch(q, k, v, v_new, dO, dR, g, nullptr, b_gate, w_gate, Akk, h, dh, dq, dk, dv, nullptr, db, dw, dg,
+                     dA, h_v_first, B, T, H, H, scale, nullptr, nullptr, stream);
+}
+
+extern "C" hipError_t fdr_gdn2_chunk_bwd_wy_varlen(const void* q, const void* k, const void* v, const void* v_new,
+                                                   const void* dO, const void* dR, const float* g, const void* b_gate,
+                                                   const void* w_gate, const float* Akk, const void* h,
+                                                   const void* dh, float* dq, float* dk, void* dv, float* db,
+                                                   void* dw, float* dg, float* dA, int h_v_first,
+                                                   const int* cu_seqlens, const int* chunk_indices, int num_chunks,
+                                                   int H, int K, int V, int chunk, float scale, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || !b_gate || num_chunks <= 0 || !cu_seqlens || !chunk_indices)
+    return hipErrorInvalidValue;
+  return wy_dispatch(q, k, v, v_new, dO, dR, g, nullptr, b_gate, w_gate, Akk, h, dh, dq, dk, dv, nullptr, db, dw, dg,
+                     dA, h_v_first, 1, num_chunks * C, H, H, scale, cu_seqlens, chunk_indices, stream);
 }
 
 extern "C" hipError_t fdr_chunk_bwd_varlen(const void* q, const void* k, const void* v, const void* v_new,
@@ -1692,7 +1770,7 @@ static hipError_t gate_fold_launch(const void* q, const void* k, const void* v, 
                                   FOLD_KERNS(true, true)};
 #undef FOLD_KERNS
   const KernT kern = kerns[fold];
-  static bool attr_set[24][kMaxDevices] = {};
+  static LdsFlags attr_set[24] = {};
   hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set[fold]);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, stream, (const bf16*)q, (const bf16*)k,
@@ -1732,19 +1810,31 @@ extern "C" hipError_t fdr_chunk_bwd_gate_fold_varlen(
                           cu_seqlens, chunk_indices);
 }
 
-template <bool VEC_B>
+template <bool VEC_B, bool MAP>
 static hipError_t launch_intra(const void* q, const void* k, const float* g, const float* beta,
                                const void* bgate, const float* daqk, const float* dakk, float* dq,
                                float* dk, float* db, float* dg, int B, int T, int H, int HQ, int beta_complete,
-                               hipStream_t s) {
+                               const int* cu, const int* ci, hipStream_t s) {
   using LY = PostLayout<CG_VECTOR, VEC_B, true>;
-  auto kern = matrix_intra_kernel<VEC_B>;
-  static bool attr_set[kMaxDevices] = {};
+  auto kern = matrix_intra_kernel<VEC_B, MAP>;
+  static LdsFlags attr_set = {};
   const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k, g,
-                     beta, (const bf16*)bgate, daqk, dakk, dq, dk, db, dg, T, H, beta_complete, HQ);
+                     beta, (const bf16*)bgate, daqk, dakk, dq, dk, db, dg, T, H, beta_complete, HQ, cu, ci);
   return hipGetLastError();
+}
+
+static hipError_t intra_dispatch(const void* q, const void* k, const float* g, const float* beta,
+                                 const void* b_gate, const float* dAqk, const float* dAkk, float* dq, float* dk,
+                                 float* db, float* dg, int B, int T, int H, int HQ, int beta_complete,
+                                 const int* cu, const int* ci, hipStream_t s) {
+  if (H % HQ || (b_gate && HQ != H)) return hipErrorInvalidValue;
+  if (!b_gate && !beta) return hipErrorInvalidValue;
+#define I_ARGS q, k, g, beta, b_gate, dAqk, dAkk, dq, dk, db, dg, B, T, H, HQ, beta_complete, cu, ci, s
+  if (b_gate) return cu ? launch_intra<true, true>(I_ARGS) : launch_intra<true, false>(I_ARGS);
+  return cu ? launch_intra<false, true>(I_ARGS) : launch_intra<false, false>(I_ARGS);
+#undef I_ARGS
 }
 
 extern "C" hipError_t fdr_matrix_intra(const void* q, const void* k, const float* g, const float* beta,
@@ -1754,10 +1844,20 @@ extern "C" hipError_t fdr_matrix_intra(const void* q, const void* k, const float
   if (K != KD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
   if (!q || !k || !g || !dAqk || !dAkk || !dq || !dk || !db || !dg) return hipErrorInvalidValue;
   const int HQ = qk_heads > 0 ? qk_heads : H;
-  if (H % HQ || (b_gate && HQ != H)) return hipErrorInvalidValue;
-  if (b_gate) return launch_intra<true>(q, k, g, nullptr, b_gate, dAqk, dAkk, dq, dk, db, dg, B, T, H, HQ, 0, stream);
-  if (!beta) return hipErrorInvalidValue;
-  return launch_intra<false>(q, k, g, beta, nullptr, dAqk, dAkk, dq, dk, db, dg, B, T, H, HQ, beta_complete, stream);
+  return intra_dispatch(q, k, g, b_gate ? nullptr : beta, b_gate, dAqk, dAkk, dq, dk, db, dg, B, T, H, HQ,
+                        b_gate ? 0 : beta_complete, nullptr, nullptr, stream);
+}
+
+extern "C" hipError_t fdr_matrix_intra_varlen(const void* q, const void* k, const float* g, const float* beta,
+                                              const void* b_gate, const float* dAqk, const float* dAkk, float* dq,
+                                              float* dk, float* db, float* dg, const int* cu_seqlens,
+                                              const int* chunk_indices, int num_chunks, int H, int qk_heads, int K,
+                                              int chunk, int beta_complete, hipStream_t stream) {
+  if (K != KD || chunk != C || num_chunks <= 0 || H <= 0 || !cu_seqlens || !chunk_indices) return hipErrorInvalidValue;
+  if (!q || !k || !g || !dAqk || !dAkk || !dq || !dk || !db || !dg) return hipErrorInvalidValue;
+  const int HQ = qk_heads > 0 ? qk_heads : H;
+  return intra_dispatch(q, k, g, b_gate ? nullptr : beta, b_gate, dAqk, dAkk, dq, dk, db, dg, 1, num_chunks * C, H,
+                        HQ, b_gate ? 0 : beta_complete, cu_seqlens, chunk_indices, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -1824,7 +1924,7 @@ extern "C" hipError_t fdr_chunk_bwd_original(const void* q, const void* k, const
   using LY = PostLayout<CG_VECTOR, false, false, false, true>;
   static_assert(LY::BYTES <= 160 * 1024, "LDS budget");
   auto kern = chunk_bwd_original_kernel<0>;
-  static bool attr_set[kMaxDevices] = {};
+  static LdsFlags attr_set = {};
   hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, stream, (const bf16*)q, (const bf16*)k,

@@ -480,35 +480,73 @@ def chunk_bwd(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale, beta=None
     return out
 
 
-def chunk_bwd_wy(q, k, v, v_new, dO, dR, g, Akk, h, dh, scale, beta, h_v_first=False):
-    """KDA's WY seam alone (fdr_chunk_bwd_wy): every term of ``chunk_bwd`` but the matrix
-    intra.  Returns dict(dq, dk [fp32], dv [bf16], dbeta [fp32, complete on |beta| >= 1e-6
-    rows], dg [fp32, before the in-chunk reverse cumsum], dA [fp32 [B,T,H,64], the intra's
-    dAkk])."""
-    B, T, HQ, K = _dims(q)
+def chunk_bwd_wy(q, k, v, v_new, dO, dR, g, Akk, h, dh, scale, beta=None, h_v_first=False, b=None, w=None,
+                 varlen=None):
+    """The WY seam alone: every term of ``chunk_bwd`` but the matrix intra.  KDA (``beta``,
+    fdr_chunk_bwd_wy) returns dict(dq, dk [fp32], dv [bf16], dbeta [fp32, complete on
+    |beta| >= 1e-6 rows], dg [fp32, before the in-chunk reverse cumsum], dA [fp32
+    [B,T,H,64], the intra's dAkk]); GDN2 (``b``, ``w``: erase and write gates,
+    fdr_gdn2_chunk_bwd_wy) returns dict(dq, dk, dv, db [fp32, without the intra's ue k],
+    dw [bf16], dg, dA).  ``varlen``: a packed variable-length batch (``Varlen``; h, dh then
+    have ``varlen.NC`` chunks)."""
+    B, T, HQ, K = _rows(q, varlen)
     H, HQ = _group(v.shape[2] if v is not None and v.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = q.device
     bf, f32 = torch.bfloat16, torch.float32
-    NT = T // CHUNK
+    NT = T // CHUNK if varlen is None else varlen.NC
+    if varlen is None and T % CHUNK:
+        raise ValueError("T must be a multiple of 64 (pass cu_seqlens for ragged rows)")
     for x, n in ((q, "q"), (k, "k")):
         _need(x, n, bf, (B, T, HQ, K), dev)
     for x, n in ((v, "v"), (v_new, "v_new"), (dO, "dO"), (dR, "dR")):
         _need(x, n, bf, (B, T, H, V), dev)
     _need(g, "g", f32, (B, T, H, K), dev)
-    _need(beta, "beta", f32, (B, T, H), dev)
+    vec_b = b is not None
+    if vec_b == (beta is not None):
+        raise ValueError("exactly one of beta (KDA) / b, w (GDN2) is required")
+    if vec_b:
+        if HQ != H:
+            raise ValueError("GDN2 takes one q/k head per value head")
+        _need(b, "b", bf, (B, T, H, K), dev)
+        _need(w, "w", bf, (B, T, H, V), dev)
+    else:
+        _need(beta, "beta", f32, (B, T, H), dev)
     _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
-    _need(h, "h", bf, (B, NT, H, K, V), dev)
+    _need(h, "h", bf, (B, NT, H, V, K) if h_v_first else (B, NT, H, K, V), dev)
     _need(dh, "dh", bf, (B, NT, H, K, V), dev)
     out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=f32), dk=torch.empty(B, T, H, K, device=dev, dtype=f32),
-               dv=torch.empty(B, T, H, V, device=dev, dtype=bf), dbeta=torch.empty(B, T, H, device=dev, dtype=f32),
-               dg=torch.empty(B, T, H, K, device=dev, dtype=f32),
+               dv=torch.empty(B, T, H, V, device=dev, dtype=bf), dg=torch.empty(B, T, H, K, device=dev, dtype=f32),
                dA=torch.empty(B, T, H, CHUNK, device=dev, dtype=f32))
+    if vec_b:
+        out["db"] = torch.empty(B, T, H, K, device=dev, dtype=f32)
+        out["dw"] = torch.empty(B, T, H, V, device=dev, dtype=bf)
+    else:
+        out["dbeta"] = torch.empty(B, T, H, device=dev, dtype=f32)
     P = _lib.ptr
-    st = _lib.load().fdr_chunk_bwd_wy(P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g), P(beta), P(Akk), P(h), P(dh),
-                                      P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), P(out["dg"]),
-                                      P(out["dA"]), int(bool(h_v_first)), B, T, H, HQ, K, V, CHUNK, float(scale),
-                                      _lib.stream_handle(dev))
+    lib = _lib.load()
+    hv = int(bool(h_v_first))
+    head = (P(q), P(k), P(v), P(v_new), P(dO), P(dR), P(g))
+    mv = _mapped(varlen)
+    if vec_b:
+        tail = (P(Akk), P(h), P(dh), P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["db"]), P(out["dw"]),
+                P(out["dg"]), P(out["dA"]), hv)
+        if mv is not None:
+            st = lib.fdr_gdn2_chunk_bwd_wy_varlen(*head, P(b), P(w), *tail, P(mv.cu_seqlens), P(mv.chunk_indices),
+                                                  mv.NC, H, K, V, CHUNK, float(scale), _lib.stream_handle(dev))
+        else:
+            st = lib.fdr_gdn2_chunk_bwd_wy(*head, P(b), P(w), *tail, B, T, H, K, V, CHUNK, float(scale),
+                                           _lib.stream_handle(dev))
+        _lib.check(st, "fdr_gdn2_chunk_bwd_wy")
+        return out
+    tail = (P(Akk), P(h), P(dh), P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), P(out["dg"]),
+            P(out["dA"]), hv)
+    if mv is not None:
+        st = lib.fdr_chunk_bwd_wy_varlen(*head, P(beta), *tail, P(mv.cu_seqlens), P(mv.chunk_indices), mv.NC, H,
+                                         HQ, K, V, CHUNK, float(scale), _lib.stream_handle(dev))
+    else:
+        st = lib.fdr_chunk_bwd_wy(*head, P(beta), *tail, B, T, H, HQ, K, V, CHUNK, float(scale),
+                                  _lib.stream_handle(dev))
     _lib.check(st, "fdr_chunk_bwd_wy")
     return out
 
@@ -777,9 +815,12 @@ def fwd_h_wy(k, v, Akk, g, gate_mode, beta=None, q=None, b=None, w=None, h0=None
     return dict(w=wo, qg=qg, kg=kg, h=h, v_new=vnew, final=ht)
 
 
-def matrix_intra(q, k, g, dAqk, dAkk, dq, dk, db, dg, beta=None, b=None, beta_complete=False):
-    """Matrix intra VJP added in place into fp32 (dq, dk, db, dg); returns them."""
-    B, T, HQ, K = _dims(q)
+def matrix_intra(q, k, g, dAqk, dAkk, dq, dk, db, dg, beta=None, b=None, beta_complete=False, varlen=None):
+    """Matrix intra VJP added in place into fp32 (dq, dk, db, dg); returns them.  ``varlen``:
+    a packed variable-length batch (``Varlen``)."""
+    B, T, HQ, K = _rows(q, varlen)
+    if varlen is None and T % CHUNK:
+        raise ValueError("T must be a multiple of 64 (pass cu_seqlens for ragged rows)")
     H, HQ = _group(dq.shape[2] if dq is not None and dq.ndim == 4 else HQ, HQ)
     dev = q.device
     bf, f32 = torch.bfloat16, torch.float32
@@ -799,6 +840,13 @@ def matrix_intra(q, k, g, dAqk, dAkk, dq, dk, db, dg, beta=None, b=None, beta_co
         _need(beta, "beta", f32, (B, T, H), dev)
         _need(db, "db", f32, (B, T, H), dev)
     P = _lib.ptr
+    mv = _mapped(varlen)
+    if mv is not None:
+        st = _lib.load().fdr_matrix_intra_varlen(P(q), P(k), P(g), P(beta), P(b), P(dAqk), P(dAkk), P(dq), P(dk),
+                                                 P(db), P(dg), P(mv.cu_seqlens), P(mv.chunk_indices), mv.NC, H, HQ,
+                                                 K, CHUNK, int(bool(beta_complete)), _lib.stream_handle(dev))
+        _lib.check(st, "fdr_matrix_intra_varlen")
+        return dq, dk, db, dg
     st = _lib.load().fdr_matrix_intra(P(q), P(k), P(g), P(beta), P(b), P(dAqk), P(dAkk), P(dq), P(dk), P(db),
                                       P(dg), B, T, H, HQ, K, CHUNK, int(bool(beta_complete)), _lib.stream_handle(dev))
     _lib.check(st, "fdr_matrix_intra")

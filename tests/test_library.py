@@ -182,3 +182,30 @@ def test_paired_rule():
     assert ops.paired_tile(8, 16, 64, V) == 0            # the fused sweep fills the GPU
     assert ops.paired_tile(1, 96, 64, V) == 0            # 64-wide tiles would need 192 CUs each
     assert ops.paired_tile(2, 32, 128, S) == 0
+
+
+def test_kernel_seams_validate_before_launch():
+    """The kernel-level seams (state, WY, intra) reject what they do not take before any
+    GPU work: chunk_indices without cu_seqlens, chunk_indices that do not match cu_seqlens,
+    both gate kinds at once, other chunk sizes."""
+    import pytest
+    import torch
+    from rewy_amd.backends.intra import chunk_gdn2_bwd_intra
+    from rewy_amd.backends.state import chunk_gated_delta_rule_bwd_dhu
+    from rewy_amd.backends.wy import chunk_gdn2_bwd_wy_dqkg_fused, chunk_kda_bwd_wy_dqkg_fused
+    x = torch.zeros(1, 100, 2, 128)
+    ci = torch.zeros(2, 2, dtype=torch.int32)
+    cu = torch.tensor([0, 30, 100], dtype=torch.int32)
+    with pytest.raises(NotImplementedError):
+        chunk_kda_bwd_wy_dqkg_fused(x, x, x, x, x, x[..., 0], x, x, x, x, x, chunk_indices=ci)
+    with pytest.raises(ValueError, match="chunk_indices must be"):
+        chunk_gdn2_bwd_wy_dqkg_fused(x, x, x, x, x, x, x, x, x, x, x, x, cu_seqlens=cu,
+                                     chunk_indices=torch.zeros(4, 2, dtype=torch.int32))
+    with pytest.raises(NotImplementedError):
+        chunk_gdn2_bwd_intra(x, x, x, x, x, x, x, x, x, x, chunk_size=32)
+    with pytest.raises(ValueError, match="at most one"):
+        chunk_gated_delta_rule_bwd_dhu(x, x, x, x, x, g=x[..., 0], gk=x)
+    with pytest.raises(ValueError, match="batch size"):
+        chunk_gated_delta_rule_bwd_dhu(torch.zeros(2, 100, 2, 128), x, x, x, x, cu_seqlens=cu)
+    with pytest.raises(ValueError, match="GPU"):       # shapes pass; no device to run on
+        chunk_gated_delta_rule_bwd_dhu(x, x, x, x, x, gk=x, cu_seqlens=cu)
