@@ -378,15 +378,15 @@ def streaming_floor(kernel, config, kernel_ms):
             "read_TBps": rates["read_TBps"], "write_TBps": rates["write_TBps"], "probe": rates["command"]}
 
 
-def cpu_baseline(xs, sv, dO, scale, NTt, round_s=0.5, rounds=15):
+def cpu_baseline(xs, sv, dO, scale, NTt, rounds=5, warmup=2):
     """The reference's CPU comparison point for the large configs: the original
     (7-product) chunk backward as torch ops -- dAv, the reverse state recurrence, the
     7-product local WY and the pairwise intra (``rewy_amd.original.original_backward``) --
     in fp32 on the host, every thread the box grants (OMP_NUM_THREADS; the reference
-    pins torch.set_num_threads).  Sample: batch 0, the first Hs heads, all T=4096 tokens,
-    Hs chosen so that one round takes ~round_s; timing as the reference's benchmark.py:8-50
-    (synchronized wall clock per sample, warm-up >= 6 rounds and >= 2 s, median of
-    `rounds`), scaled linearly to the full workload's chunk-heads."""
+    pins torch.set_num_threads).  Sample: batch row 0 whole (every head, all T tokens:
+    1,024 of the headline's 8,192 chunk-heads); timing as the reference's benchmark.py:8-50
+    (synchronized wall clock per sample, median of `rounds`) after `warmup` rounds, scaled
+    linearly to the full workload's chunk-heads."""
     import statistics
     import torch
     from rewy_amd.original import original_backward
@@ -409,14 +409,10 @@ def cpu_baseline(xs, sv, dO, scale, NTt, round_s=0.5, rounds=15):
             el = time.perf_counter() - t0
             del out
             return el
-        hs = 1
-        probe = run(sample_inputs(1))
-        hs = max(1, min(H, int(round_s / max(probe, 1e-6))))
+        hs = H          # one whole batch row: every head, every chunk
         inp = sample_inputs(hs)
-        start, warm = time.perf_counter(), 0
-        while warm < 6 or time.perf_counter() - start < 2:
+        for _ in range(warmup):
             run(inp)
-            warm += 1
         times = [run(inp) for _ in range(rounds)]
         med = statistics.median(times)
     finally:
@@ -426,9 +422,9 @@ def cpu_baseline(xs, sv, dO, scale, NTt, round_s=0.5, rounds=15):
             "cores": threads, "kind": "port", "dtype": "fp32",
             "sample": f"original 7-product chunk backward (torch ops, fp32, {threads} threads): batch 0, heads "
                       f"0-{hs - 1}, T={T} ({sample_heads} of {NTt} chunk-heads); median of {rounds} rounds "
-                      f"({med * 1e3:.1f} ms) after {warm} warm-up rounds, scaled linearly",
-            "protocol": "reference benchmark.py:8-50: synchronized wall clock per sample, >= 6 and >= 2 s "
-                        "warm-up, median"}
+                      f"({med * 1e3:.1f} ms) after {warmup} warm-up rounds, scaled linearly",
+            "protocol": "reference benchmark.py:8-50: synchronized wall clock per sample, median (warm-up "
+                        f"{warmup} rounds: the host needs no clock settling, and a round is ~2 s)"}
 
 
 def cpu_oracle_baseline(xs, sv, dO, scale, NTt, nb_max=1):
@@ -469,6 +465,90 @@ def cpu_oracle_baseline(xs, sv, dO, scale, NTt, nb_max=1):
             "cores": 1, "kind": "port", "dtype": "fp64",
             "sample": f"fp64 numpy oracle (state recurrence + chunk stage), batches 0-{nb - 1}, T={T}, all {H} "
                       f"heads ({sample_heads} of {NTt} chunk-heads), measured {el:.2f} s, scaled linearly"}
+
+
+def paired_protocol(cand, orig, rounds=10, tol=None):
+    """The reference's paired timing (benchmark.py:21-46): a gradient check of the candidate
+    against the original formulation first (rel-L2 <= 0.008, 0.02 for the gate / beta
+    gradients; a failure raises), then warm-up rounds of both (>= 6 and >= 2 s), then
+    `rounds` rounds in alternating ABBA / BAAB order, each sample a synchronized wall clock
+    around one backward; medians and the speed-up of their ratio."""
+    import statistics
+    import torch
+    names = ("dq", "dk", "dv", "dbeta", "dg", "dh0")
+    checks = {}
+    for n, a, r in zip(names, cand(), orig()):
+        if not (torch.is_tensor(a) and torch.is_tensor(r)):
+            continue
+        a, r = a.double(), r.double()
+        lim = 0.02 if n in ("dbeta", "dg") else 0.008
+        rel = float((a - r).norm() / r.norm().clamp_min(1e-30))
+        checks[n] = {"relative_l2": round(rel, 6), "limit": lim, "passed": rel <= lim}
+    if not all(c["passed"] for c in checks.values()):
+        raise RuntimeError(f"Gradient check failed: {checks}")
+    fns = {"original": orig, "optimized": cand}
+
+    def sample(name):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = fns[name]()
+        torch.cuda.synchronize()
+        el = (time.perf_counter() - t0) * 1e3
+        del out
+        return el
+    start, warm = time.perf_counter(), 0
+    while warm < 6 or time.perf_counter() - start < 2:
+        for n in ("original", "optimized"):
+            sample(n)
+        warm += 1
+    samples, orders = {"original": [], "optimized": []}, []
+    for r in range(rounds):
+        order = ["original", "optimized"] if r % 2 == 0 else ["optimized", "original"]
+        order = order + order[::-1]
+        orders.append("".join("A" if o == "original" else "B" for o in order))
+        for n in order:
+            samples[n].append(sample(n))
+    med = {n: statistics.median(v) for n, v in samples.items()}
+    return {"protocol": "reference benchmark.py:21-46: gradient check, >= 6 rounds and >= 2 s warm-up, "
+                        f"{rounds} rounds ABBA/BAAB, synchronized wall clock per backward, medians",
+            "A": "original formulation (HIP, 7-product local WY)", "B": "residual formulation (HIP)",
+            "warmup_rounds": warm, "rounds": rounds, "orders": orders,
+            "median_ms": {n: round(v, 4) for n, v in med.items()},
+            "samples_ms": {n: [round(x, 4) for x in v] for n, v in samples.items()},
+            "speedup": round(med["original"] / med["optimized"], 3), "correctness": checks}
+
+
+def reference_cpu_path(rounds=5):
+    """The reference's own CPU path at BASELINE.json configs[0] (DeltaNet, B=1 T=256 H=2,
+    K=V=128): the fp64 token recurrence plus its autograd backward (validation.py:23-38,
+    restated as oracle.delta_oracle.torch_token_recurrence) on the host's granted threads,
+    timed as the reference times (synchronized wall clock, median), beside the HIP backward
+    of the same config on this GPU."""
+    import statistics
+    import torch
+    from oracle import delta_oracle as O
+    from tests._inputs import make_inputs
+    threads = min(int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count()), os.cpu_count())
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        xs, dO = make_inputs("delta", 1, 256, 2, seed=0)
+        t = {n: x.double().requires_grad_() for n, x in xs.items()}
+        dO = dO.double()
+
+        def run():
+            t0 = time.perf_counter()
+            o, _ = O.torch_token_recurrence("delta", t)
+            torch.autograd.grad(o, tuple(t.values()), dO)
+            return (time.perf_counter() - t0) * 1e3
+        run()
+        times = [run() for _ in range(rounds)]
+    finally:
+        torch.set_num_threads(prev)
+    return {"config": "BASELINE.json configs[0]: DeltaNet B=1 T=256 H=2 K=V=128", "value":
+            round(statistics.median(times), 2), "unit": "ms per forward + backward (fp64 token recurrence, "
+            "torch autograd)", "cores": threads, "kind": "port", "dtype": "fp64",
+            "sample": f"the whole config, median of {rounds} runs after one warm-up run"}
 
 
 # The reference's published operator grid (B, T, H), K=V=128, chunk 64, and its H100
@@ -682,7 +762,7 @@ def main():
     # ---- the original 7-product formulation on the same GPU: the same state kernel and the
     # same chunk kernel built with the original local WY (fdr_chunk_bwd_original), timed as
     # the headline; gradients checked against the PyTorch original backend ----
-    parity, orig = None, None
+    parity, orig, paired = None, None, None
     if cfg["op"] == "kda" and cfg["full_saving"] and not cfg.get("gate_in_kernel"):
         from rewy_amd import ops
 
@@ -704,6 +784,8 @@ def main():
         for name, a, r in zip(("dq", "dk", "dv", "dbeta", "dg"), got, ref_hip):
             a, r = a.double(), r.double()
             gap[name] = round(float((a - r).norm() / r.norm().clamp_min(1e-30)), 6)
+        print("[bench] paired protocol (original vs residual, HIP)", file=sys.stderr, flush=True)
+        paired = paired_protocol(res["step"], orig_step)
         orig = {"ms": round(o_ms, 4), "chunk_kernel_ms": round(o_kern, 4),
                 "speedup_of_residual": round(o_ms / res["ms"], 3),
                 "rel_l2_residual_vs_original": gap,
@@ -731,6 +813,9 @@ def main():
         cpu = cpu_baseline(xs, sv, dO, sv["scale"], NTt)
         print("[bench] CPU baseline (fp64 oracle, one thread)", file=sys.stderr, flush=True)
         cpu["fp64_oracle_1core"] = cpu_oracle_baseline(xs, sv, dO, sv["scale"], NTt)
+        print("[bench] the reference's CPU path at configs[0] (fp64 token recurrence + autograd)", file=sys.stderr,
+              flush=True)
+        cpu["reference_cpu_path"] = reference_cpu_path()
 
     ms, tflops, kernels, res_fwd_ms = res["ms"], res["tflops"], res["kernels"], res["fwd_ms"]
     warm_run = res["warmup_steps_run"]
@@ -751,6 +836,19 @@ def main():
                              "kernels": g["kernels"]}}
         del g
         torch.cuda.empty_cache()
+        # the other BASELINE.json configs (parity-test cases), timed the same way
+        for name, idx in (("delta", 0), ("gdn_cfg", 1), ("gdn2", 3), ("kda_long", 4)):
+            c = CONFIGS[name]
+            print(f"[bench] configs[{idx}]: {name}", file=sys.stderr, flush=True)
+            g = measure(c, args.steps, args.warmup)
+            secondary[name] = {"workload": f"BASELINE.json configs[{idx}]: {c['op']} chunk backward, "
+                                           f"{'full saving' if c['full_saving'] else 'recompute'}, "
+                                           f"B={c['B']} T={c['T']} H={c['H']}",
+                               "ms": round(g["ms"], 4), "tflops": round(g["tflops"], 2),
+                               "graph_ms": None if g["graph_ms"] != g["graph_ms"] else round(g["graph_ms"], 4),
+                               "kernels": {n: k["ms"] for n, k in g["kernels"].items()}}
+            del g
+            torch.cuda.empty_cache()
 
     line = {
         "metric": METRIC,
@@ -787,6 +885,8 @@ def main():
         # the original 7-product formulation, same GPU, same kernels otherwise (HIP)
         "original_formulation_hip": orig,
         "speedup_vs_original_formulation": None if orig is None else orig["speedup_of_residual"],
+        # the same pair timed as the reference's benchmark.py does (paired ABBA/BAAB rounds)
+        "paired_vs_original": paired,
         # gradients against the PyTorch original backend (fp32 torch ops)
         "parity_vs_original": parity,
         "cpu_baseline": cpu,

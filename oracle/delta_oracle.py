@@ -29,6 +29,9 @@ Functions and what pins them (see ``tests/test_oracle.py``):
 
 * ``recurrence``              -- textbook statement; pinned by torch fp64 autograd
                                  and by the chunked forward.
+* ``torch_token_recurrence``  -- the reference's CPU path (``validation.py:23-38``) in
+                                 torch, batched; pinned by equality of its fp64
+                                 autograd with ``backward``.
 * ``chunk_pullback``          -- closed-form single-chunk backward, restating
                                  ``check_manuscript_math.py:21-54``; pinned by
                                  complex-step differentiation of ``recurrence``.
@@ -67,6 +70,32 @@ def recurrence(q, k, v, g, b, w, S0, scale=1.0):
         S = S + np.outer(k[t], r)
         out.append(scale * (S.T @ q[t]))
     return np.asarray(out), S
+
+
+def torch_token_recurrence(op, xs):
+    """The reference's CPU path (validation.py:23-38): the token recurrence of ``op`` over a
+    batch in torch (any dtype; fp64 there), differentiable by autograd.  ``xs``: q, k, v
+    [B,T,H,K], initial_state [B,H,K,V], g (natural log; [B,T,H] for gdn, [B,T,H,K] for kda /
+    gdn2, absent for delta), beta [B,T,H] or (gdn2) b [B,T,H,K], w [B,T,H,V].  Returns (o, S_T).
+    Pinned against ``backward`` (complex-step pinned) by tests/test_oracle.py."""
+    import torch
+    q, k, v = xs["q"], xs["k"], xs["v"]
+    S = xs["initial_state"]
+    ys = []
+    for i in range(k.shape[1]):
+        if op != "delta":
+            gi = xs["g"][:, i]
+            if op == "gdn":
+                gi = gi[..., None]
+            S = S * gi.exp()[..., None]
+        kt = k[:, i]
+        if op == "gdn2":
+            r = xs["w"][:, i] * v[:, i] - torch.einsum("bhk,bhkv->bhv", xs["b"][:, i] * kt, S)
+        else:
+            r = xs["beta"][:, i, ..., None] * (v[:, i] - torch.einsum("bhk,bhkv->bhv", kt, S))
+        S = S + kt[..., None] * r[..., None, :]
+        ys.append(torch.einsum("bhk,bhkv->bhv", q[:, i] * q.shape[-1] ** -.5, S))
+    return torch.stack(ys, 1), S
 
 
 def recurrence_objective(q, k, v, g, b, w, S0, dO, dS, scale=1.0):

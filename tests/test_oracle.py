@@ -126,23 +126,7 @@ def test_backward_matches_torch_autograd_of_token_recurrence(family):
     out = O.backward(family, n(xs["q"]), n(xs["k"]), n(xs["v"]), g=n(xs.get("g")), beta=n(xs.get("beta")),
                      b=n(xs.get("b")), w=n(xs.get("w")), h0=n(xs["initial_state"]), dO=n(dO), dht=None)
     t = {k: v.double().clone().requires_grad_() for k, v in xs.items()}
-    q, k, v = t["q"], t["k"], t["v"]
-    S = t["initial_state"]
-    ys = []
-    for i in range(q.shape[1]):
-        if family != "delta":
-            gi = t["g"][:, i]
-            if family == "gdn":
-                gi = gi[..., None]
-            S = S * gi.exp()[..., None]
-        kt = k[:, i]
-        if family == "gdn2":
-            r = t["w"][:, i] * v[:, i] - torch.einsum("bhk,bhkv->bhv", t["b"][:, i] * kt, S)
-        else:
-            r = t["beta"][:, i, ..., None] * (v[:, i] - torch.einsum("bhk,bhkv->bhv", kt, S))
-        S = S + kt[..., None] * r[..., None, :]
-        ys.append(torch.einsum("bhk,bhkv->bhv", q[:, i] * q.shape[-1] ** -.5, S))
-    o = torch.stack(ys, 1)
+    o, _ = O.torch_token_recurrence(family, t)
     grads = torch.autograd.grad(o, tuple(t.values()), dO.double())
     names = {"q": "dq", "k": "dk", "v": "dv", "g": "dg", "beta": "dbeta", "b": "db", "w": "dw",
              "initial_state": "dh0"}
