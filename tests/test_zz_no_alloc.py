@@ -3,7 +3,9 @@ the library's fixed device array) against fdr_chunk_bwd_gate_fold with a caller-
 workspace, through the C-ABI.  Both launch the same kernels, so every output must be
 bit-identical; two calls in a row, the second on a smaller problem (the array keeps the
 first call's partials, which the second must not read), then a size beyond the array's
-limit is refused."""
+limit is refused.  Also with V-first saved states (h_v_first = 1), and captured in a HIP
+graph after one eager call (the per-device set-up happens on that call): three replays, with
+eager work between them, each bit-identical to the workspace entry point."""
 import pytest
 import torch
 
@@ -45,20 +47,21 @@ def _outs(B, T, H, dev):
                 dbeta=e(B, T, H), dg=e(B, T, H, 128), dA=e(H), ddt=e(H * 128))
 
 
-def _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc):
+def _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc, hvf=0, out=None, sync=True):
     B, T, H = shape
     dev = g_raw.device
-    out = _outs(B, T, H, dev)
+    out = _outs(B, T, H, dev) if out is None else out
     P = L.ptr
     head = [P(x) for x in ins] + [P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dbeta"]), 0.0, P(g_raw), 0,
                                   P(A), P(dt), 0, 0.0, P(out["dg"]), P(out["dA"]), P(out["ddt"])]
-    tail = [0, B, T, H, 0, 128, 128, 64, float(scale), L.stream_handle(dev)]
+    tail = [hvf, B, T, H, 0, 128, 128, 64, float(scale), L.stream_handle(dev)]
     if noalloc:
         st = lib.fdr_chunk_bwd_gate_fold_noalloc(*head, *tail)
     else:
         ws = torch.empty(lib.fdr_chunk_bwd_gate_workspace_bytes(B, T, H) // 4, device=dev)
         st = lib.fdr_chunk_bwd_gate_fold(*head, P(ws), *tail)
-    torch.cuda.synchronize()
+    if sync:
+        torch.cuda.synchronize()
     return st, out
 
 
@@ -86,3 +89,46 @@ def test_noalloc_rejects_sizes_beyond_its_array():
     st = lib.fdr_chunk_bwd_gate_fold_noalloc(*([p] * 15), 0.0, p, 0, p, None, 0, 0.0, p, p, None, 0,
                                              B, T, H, 0, 128, 128, 64, 1.0, L.stream_handle(dev))
     assert st == HIP_ERROR_INVALID_VALUE
+
+
+def test_noalloc_with_v_first_states():
+    L, lib = _lib()
+    shape = (1, 192, 3)
+    print(f"\n[no-alloc] h_v_first shape={shape}", flush=True)
+    ins, g_raw, A, dt, scale = _case(*shape, 11)
+    ins[9] = ins[9].transpose(-1, -2).contiguous()          # saved h as [B,NT,H,V,K]
+    st_ref, ref = _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc=False, hvf=1)
+    st_got, got = _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc=True, hvf=1)
+    assert st_ref == 0 and st_got == 0, (st_ref, st_got)
+    for name in ref:
+        assert torch.equal(got[name], ref[name]), name
+
+
+def test_noalloc_under_graph_capture():
+    L, lib = _lib()
+    shape = (2, 128, 2)
+    print(f"\n[no-alloc] graph capture shape={shape}", flush=True)
+    ins, g_raw, A, dt, scale = _case(*shape, 12)
+    st_ref, ref = _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc=False)
+    assert st_ref == 0
+    st, _ = _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc=True)      # eager first call
+    assert st == 0
+    out = _outs(*shape, g_raw.device)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            # the library launches on the stream it is given: the capturing one
+            st, _ = _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc=True, out=out, sync=False)
+    torch.cuda.current_stream().wait_stream(side)
+    assert st == 0
+    for rep in range(3):
+        for x in out.values():
+            x.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for name in ref:
+            assert torch.equal(out[name], ref[name]), (rep, name)
+        st, _ = _call(L, lib, ins, g_raw, A, dt, scale, (1, 128, 2), noalloc=True)   # eager work between
+        assert st == 0
