@@ -601,6 +601,39 @@ def graph_time_us(step, reps):
     return us, worst
 
 
+def graph_vs_eager(config, reps=100):
+    """The headline backward as eager launches and as HIP-graph replays, one after the other
+    (for a kernel trace: kernel durations and the gaps between them in each regime), with
+    HIP-event times per step of each, in alternating rounds."""
+    import torch
+    cfg = CONFIGS[config]
+    xs, dO, sv, step, kern, inter, fwd = setup(cfg, "cuda")
+    time_steps(step, 50, 40, WARMUP_MIN_S)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(20):
+        graph.replay()
+    torch.cuda.synchronize()
+
+    def ev(fn, n):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+    rounds = [{"eager_ms": round(ev(step, reps), 4), "graph_ms": round(ev(graph.replay, reps), 4)} for _ in range(3)]
+    print(json.dumps({"graph_vs_eager": config, "steps_per_round": reps, "rounds": rounds}), flush=True)
+
+
 def paper_grid(reps):
     """One JSON line per (family, policy): this build's backward at each grid case next
     to the reference's published H100 numbers for the same case."""
@@ -723,6 +756,8 @@ def main():
                     help="only measure what plain streaming reaches on this GPU: 4 GiB read, write and copy")
     ap.add_argument("--varlen", action="store_true",
                     help="time a ragged cu_seqlens batch packed natively vs padded to the longest instead")
+    ap.add_argument("--graph-vs-eager", action="store_true",
+                    help="time --config's backward as eager launches and as HIP-graph replays (for a kernel trace)")
     ap.add_argument("--paper-grid", action="store_true",
                     help="time the reference's published operator grid (HIP-graph replay) instead")
     args = ap.parse_args()
@@ -749,6 +784,9 @@ def main():
     torch.cuda.set_device(0)
     if args.paper_grid:
         paper_grid(max(args.steps, 20))
+        return
+    if args.graph_vs_eager:
+        graph_vs_eager(args.config)
         return
     if args.varlen:
         varlen(min(args.steps, 10), min(args.warmup, 3))

@@ -122,10 +122,15 @@ def check(status: int, what: str):
 
 
 def ptr(t):
-    """Device pointer of a tensor (or None)."""
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    """Device pointer of a tensor as an int (or None: a null pointer); the c_void_p argtypes
+    convert it at the call."""
+    return None if t is None else t.data_ptr()
 
 
 def stream_handle(device):
+    """The current HIP stream of ``device`` (torch's, so the kernels order with torch's own
+    work), as a raw handle.  The raw lookup costs ~0.3 us against ~5 us for
+    torch.cuda.current_stream(device), which tiny backwards pay four times per call."""
     import torch
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
