@@ -69,6 +69,9 @@ def inline_aqk(cfg):
     if cfg["full_saving"] or cfg["op"] not in ("gdn", "delta"):
         return False
     NT = cfg["T"] // 64
+    gate = ops.GATE_SCALAR if cfg["op"] == "gdn" else ops.GATE_NONE
+    if ops.paired_tile(cfg["B"], cfg["H"], NT, gate):
+        return True
     return not ops._use_affine("auto", cfg["B"], cfg["H"], NT) and ops.state_form(cfg["B"], cfg["H"], NT) == "direct"
 
 
@@ -220,8 +223,8 @@ def setup(cfg, device):
         aqk = sv["Aqk"] if vec else pre["Aqk"]
     vb_pair = 0 if keep else ops.paired_tile(cfg["B"], cfg["H"], NT, gate)
     if vb_pair:
-        # vector gates, batch x heads too small for one recurrence to fill the GPU: the state
-        # recurrence and the forward scan side by side (two streams, as the backend runs them)
+        # batch x heads too small for one recurrence to fill the GPU: the state recurrence and
+        # the forward scan side by side (two streams, as the backend runs them)
         from rewy_amd.backends.backward import _side_by_side
         kern["paired_recurrences"] = lambda: _side_by_side(
             lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk, want_dh0=xs["h0"] is not None,

@@ -17,9 +17,10 @@ When batch x heads is too small to fill the GPU and the sequence long, the two
 recurrences run instead in affine-step form (after ``fdr_prepare_wu``: w, u and qg, kg or Aqk) (``ops.recurrences``,
 ``fdr_affine_*``): chunk-parallel step matrices, one scan launch carrying both
 recurrences side by side, and a chunk-parallel pass for v_new and dR.
-For vector gates with 24 <= batch x heads < 128 the recompute policy runs the direct backward
-state recurrence and the direct forward scan side by side on two streams, at a value-tile
-width that gives each at most half the CUs (``ops.paired_tile``).
+With 24 <= batch x heads where the fused sweep does not pay (vector gates below 128, scalar /
+no gate below 64) the recompute policy runs the direct backward state recurrence and the
+direct forward scan side by side on two streams, at a value-tile width that gives each at
+most half the CUs (``ops.paired_tile``).
 With a few more heads and long rows the recompute policy runs the forward scan
 (``fdr_fwd_h``) on the current stream beside the segmented backward state recurrence
 (``fdr_state_bwd_segmented``) on a second stream (``ops.side_by_side_pays``).
@@ -276,11 +277,13 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
     beta = _f32(beta)
     gate = ops.GATE_SCALAR if op == "gdn" else ops.GATE_NONE
     affine = vl is None and q.shape[2] == v.shape[2] and ops.affine_pays(v)
+    # mid-size batch x heads: the direct recurrences side by side (ops.paired_tile)
+    vb = 0 if vl is not None else ops.paired_tile(q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK, gate)
     # the direct state recurrence forms Aqk itself from the raw q / k it stages; w and u are then
     # formed inside the forward scan's sweep where that pays (fdr_fwd_h_wy: u never leaves the
     # chip), else by fdr_prepare_wu without Aqk
-    inline = not affine and (vl is not None or ops.state_form(q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK)
-                             == "direct")
+    inline = vb > 0 or (not affine and (vl is not None or ops.state_form(q.shape[0], v.shape[2],
+                                                                          q.shape[1] // ops.CHUNK) == "direct"))
     if inline:
         pre = None
         if ops.fwd_h_wy_pays(q.shape[0] if vl is None else vl.N, v.shape[2], gate, vl):
@@ -293,13 +296,16 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
 
         def state():
             return ops.state_bwd(q, k, w, g, gate, do, scale, dht=_f32(dht), want_dh0=initial_state is not None,
-                                 method="direct", varlen=vl, state_v_first=state_v_first)
+                                 method="direct", varlen=vl, state_v_first=state_v_first, value_block=vb)
 
         def scan():
             return ops.fwd_h(k, w, pre["u"], g, gate, h0=_f32(initial_state), method="direct", varlen=vl,
-                             state_v_first=state_v_first)
+                             state_v_first=state_v_first, value_block=vb)
         if pre is None:
             dh, dR, dh0 = state()
+        elif vb:
+            # the state recurrence (the longer chain) first, the scan on the side stream
+            (dh, dR, dh0), (h, v_new, _) = _side_by_side(state, scan)
         elif vl is not None and ops.SIDE_BY_SIDE:
             # a packed batch: its short sequences leave CUs idle while the longest runs
             (h, v_new, _), (dh, dR, dh0) = _side_by_side(scan, state)

@@ -1,7 +1,8 @@
-"""The recompute policy's paired direct recurrences (vector gates, 24 <= B*H < 128): the
-direct backward state recurrence (fdr_state_bwd) on the current stream beside the direct
-forward scan (fdr_fwd_h) on a second stream, both at the value-tile width
-``ops.paired_tile`` picks (32 at B*H = 32, 64 at B*H = 48).  For KDA and GDN2:
+"""The recompute policy's paired direct recurrences (B*H >= 24 where the fused sweep does not
+pay): the direct backward state recurrence (fdr_state_bwd) on the current stream beside the
+direct forward scan (fdr_fwd_h) on a second stream, both at the value-tile width
+``ops.paired_tile`` picks (32 at B*H = 32, 64 at B*H = 48).  For all four families (the
+scalar / no-gate ones with the state recurrence forming Aqk itself):
 
 * the public autograd backward (recompute policy) against the fp64 oracle at the
   reference's acceptance tolerances (validation.py:40-45, :68);
@@ -18,7 +19,9 @@ from tests._inputs import make_inputs
 
 pytestmark = pytest.mark.gpu
 
-OPNAME = {"kda": "chunk_kda", "gdn2": "chunk_gdn2"}
+OPNAME = {"kda": "chunk_kda", "gdn2": "chunk_gdn2", "gdn": "chunk_gated_delta_rule", "delta": "chunk_delta_rule"}
+OPS = ["kda", "gdn2", "gdn", "delta"]
+GATE = {"kda": 2, "gdn2": 2, "gdn": 1, "delta": 0}
 GRAD = {"q": "dq", "k": "dk", "v": "dv", "g": "dg", "beta": "dbeta", "b": "db", "w": "dw", "initial_state": "dh0"}
 SHAPES = [(2, 512, 16, 32), (1, 256, 48, 64)]     # B, T, H, the tile width paired_tile picks
 
@@ -33,35 +36,41 @@ def _seam(op, B, T, H):
     from rewy_amd.backends import backward as bw
     from rewy_amd.hip_forward import chunk_forward_hip
     dev = torch.device("cuda")
-    xs, dO = make_inputs(op, B, T, H, seed=51, gate="mild")
+    xs, dO = make_inputs(op, B, T, H, seed=51, gate="mild" if op in ("kda", "gdn2") else "default")
     xs = {n: (None if v is None else v.to(dev)) for n, v in xs.items()}
     dO = dO.to(dev)
     _, _, sv = chunk_forward_hip(op, xs["q"], xs["k"], xs["v"], g=xs.get("g"), beta=xs.get("beta"),
                                  b=xs.get("b"), w=xs.get("w"), initial_state=xs["initial_state"])
     dht = torch.randn(B, H, 128, 128, generator=torch.Generator().manual_seed(5)).mul(0.1).to(dev)
     common = dict(q=xs["q"], k=xs["k"], v=xs["v"], scale=sv["scale"], initial_state=xs["initial_state"], do=dO,
-                  dht=dht, Aqk=sv["Aqk"], Akk=sv["Akk"], g=sv["gc"])
+                  dht=dht)
     if op == "kda":
-        return lambda: bw.kda_backward(beta=xs["beta"], **common)[:6]
-    return lambda: bw.gdn2_backward(b=xs["b"], w_gate=xs["w"], **common)[:7]
+        return lambda: bw.kda_backward(beta=xs["beta"], Aqk=sv["Aqk"], Akk=sv["Akk"], g=sv["gc"], **common)[:6]
+    if op == "gdn2":
+        return lambda: bw.gdn2_backward(b=xs["b"], w_gate=xs["w"], Aqk=sv["Aqk"], Akk=sv["Akk"], g=sv["gc"],
+                                        **common)[:7]
+    if op == "gdn":
+        return lambda: bw.gdn_backward(g=sv["gc"], beta=xs["beta"], A=sv["Akk"], **common)[:6]
+    return lambda: bw.delta_backward(beta=xs["beta"], A=sv["Akk"], **common)
 
 
 @pytest.mark.parametrize("B,T,H,vb", SHAPES)
-@pytest.mark.parametrize("op", ["kda", "gdn2"])
+@pytest.mark.parametrize("op", OPS)
 def test_paired_public_backward_matches_oracle(op, B, T, H, vb, monkeypatch):
     import rewy_amd as fdr
     from rewy_amd import ops
     from rewy_amd.backends import backward as bw
     print(f"\n[paired] op={op} B={B} T={T} H={H}", flush=True)
-    assert ops.paired_tile(B, H, T // 64, ops.GATE_VECTOR) == vb
+    assert ops.paired_tile(B, H, T // 64, GATE[op]) == vb
     calls = []
     real = bw._side_by_side
     monkeypatch.setattr(bw, "_side_by_side", lambda a, b: (calls.append(1), real(a, b))[1])
-    xs, dO = make_inputs(op, B, T, H, seed=52, gate="mild")
+    xs, dO = make_inputs(op, B, T, H, seed=52, gate="mild" if op in ("kda", "gdn2") else "default")
     dev = torch.device("cuda")
     xg = {k: v.to(dev).requires_grad_() for k, v in xs.items()}
+    kw = dict(disable_recompute=False) if op in ("kda", "gdn2") else {}
     with fdr.use_backend("optimized", ops=(op,)):
-        o, ht = getattr(fdr, OPNAME[op])(**xg, output_final_state=True, disable_recompute=False)
+        o, ht = getattr(fdr, OPNAME[op])(**xg, output_final_state=True, **kw)
     dht = (torch.randn(ht.shape, generator=torch.Generator().manual_seed(9)) * 0.1).to(dev)
     grads = torch.autograd.grad((o, ht), tuple(xg.values()), (dO.to(dev), dht))
     torch.cuda.synchronize()
@@ -78,7 +87,7 @@ def test_paired_public_backward_matches_oracle(op, B, T, H, vb, monkeypatch):
 
 
 @pytest.mark.parametrize("B,T,H,vb", SHAPES)
-@pytest.mark.parametrize("op", ["kda", "gdn2"])
+@pytest.mark.parametrize("op", OPS)
 def test_paired_equals_one_stream_and_policy_off(op, B, T, H, vb, monkeypatch):
     from rewy_amd import ops
     from rewy_amd.backends import backward as bw
@@ -99,7 +108,7 @@ def test_paired_equals_one_stream_and_policy_off(op, B, T, H, vb, monkeypatch):
         assert e <= 1e-5, (op, i, e)
 
 
-@pytest.mark.parametrize("op", ["kda", "gdn2"])
+@pytest.mark.parametrize("op", ["kda", "gdn"])
 def test_paired_under_graph_capture(op):
     B, T, H, _ = SHAPES[0]
     print(f"\n[paired-graph] op={op} B={B} T={T} H={H}", flush=True)
