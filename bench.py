@@ -75,10 +75,21 @@ def inline_aqk(cfg):
     return not ops._use_affine("auto", cfg["B"], cfg["H"], NT) and ops.state_form(cfg["B"], cfg["H"], NT) == "direct"
 
 
-def kernel_costs(op, full_saving, inline=False):
+def folds_u(cfg):
+    """The recompute policy's paired recurrences with u formed inside the scan (as
+    ``backends.backward`` decides)."""
+    from rewy_amd import ops
+    gate = {"kda": ops.GATE_VECTOR, "gdn2": ops.GATE_VECTOR, "gdn": ops.GATE_SCALAR, "delta": ops.GATE_NONE}[cfg["op"]]
+    return (not cfg["full_saving"] and ops.PAIRED_U
+            and bool(ops.paired_tile(cfg["B"], cfg["H"], cfg["T"] // 64, gate)))
+
+
+def kernel_costs(op, full_saving, inline=False, fold_u=False):
     """Algorithmic (bytes, FLOPs) per chunk-head of every kernel the backward launches:
     every operand read once, every result written once; dense GEMM flops.  ``inline``: the
-    state recurrence forms Aqk itself (see ``inline_aqk``)."""
+    state recurrence forms Aqk itself (see ``inline_aqk``).  ``fold_u``: the paired
+    recurrences' scan forms u itself (fdr_fwd_h_u), so prepare_wu neither reads v (nor GDN2's
+    write gate) nor writes u."""
     vec, vb = op in ("kda", "gdn2"), op == "gdn2"
     g_b = 64 * 128 * 4 if vec else (64 * 4 if op == "gdn" else 0)
     gl_b = 128 * 4 if vec else (4 if op == "gdn" else 0)
@@ -101,6 +112,12 @@ def kernel_costs(op, full_saving, inline=False):
     rd = 5 * TILE + g_b + gates_b + AT + 2 * HS + (TILE if vb else 0)
     wr = 3 * TILE + g_b + (2 * TILE if vb else beta_b)
     costs["fdr_chunk_bwd"] = (rd + wr, 3 * mm(64, 64, 128) + 3 * mm(64, 128, 128) + 4 * mm(64, 64, 128))
+    if not full_saving and fold_u:
+        by, fl = costs["fdr_prepare_wu"]
+        costs["fdr_prepare_wu"] = (by - TILE - (TILE if vb else 0) - TILE, fl - mm(64, 128, 64))
+        # the scan reads v (, w_gate | beta) and Akk in place of u, and forms u
+        by, fl = costs["fdr_fwd_h"]
+        costs["fdr_fwd_h_u"] = (by + (TILE if vb else 64 * 4) + AT, fl + mm(64, 128, 64))
     # folded gate backward: g_raw read besides g, dL/dg_raw (fp32) written in place of dg
     costs["fdr_chunk_bwd_gate_fold"] = (costs["fdr_chunk_bwd"][0] + g_b, costs["fdr_chunk_bwd"][1])
     # the affine-step launches compute the same recurrences: same operands and results
@@ -108,7 +125,8 @@ def kernel_costs(op, full_saving, inline=False):
     costs["affine_state"] = costs["fdr_state_bwd"]
     costs["segmented_state"] = costs["fdr_state_bwd"]
     if not full_saving:
-        costs["paired_recurrences"] = tuple(a + b for a, b in zip(costs["fdr_fwd_h"], costs["fdr_state_bwd"]))
+        scan = "fdr_fwd_h_u" if fold_u else "fdr_fwd_h"
+        costs["paired_recurrences"] = tuple(a + b for a, b in zip(costs[scan], costs["fdr_state_bwd"]))
         costs["affine_recurrences"] = tuple(a + b for a, b in zip(costs["fdr_fwd_h"], costs["fdr_state_bwd"]))
     return costs
 
@@ -214,14 +232,15 @@ def setup(cfg, device):
         ws, h, v_new = sw["w"], sw["h"], sw["v_new"]
         ks, qs = (sw["kg"], sw["qg"]) if vec else (xs["k"], xs["q"])
         aqk = sv["Aqk"] if vec else None
-    elif not keep:
+    vb_pair = 0 if keep else ops.paired_tile(cfg["B"], cfg["H"], NT, gate)
+    fold_u = bool(vb_pair) and ops.PAIRED_U
+    if not keep and not fused:
         kern["fdr_prepare_wu"] = lambda: ops.prepare_wu(
             xs["k"], xs["v"], sv["Akk"], gate, g=g, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"), q=xs["q"],
-            want_qkg=vec, want_aqk=not vec and not inline, scale=scale)
+            want_qkg=vec, want_aqk=not vec and not inline, scale=scale, want_u=not fold_u)
         pre = kern["fdr_prepare_wu"]()
         ks, qs, ws = (pre["kg"], pre["qg"], pre["w"]) if vec else (xs["k"], xs["q"], pre["w"])
         aqk = sv["Aqk"] if vec else pre["Aqk"]
-    vb_pair = 0 if keep else ops.paired_tile(cfg["B"], cfg["H"], NT, gate)
     if vb_pair:
         # batch x heads too small for one recurrence to fill the GPU: the state recurrence and
         # the forward scan side by side (two streams, as the backend runs them)
@@ -229,7 +248,9 @@ def setup(cfg, device):
         kern["paired_recurrences"] = lambda: _side_by_side(
             lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk, want_dh0=xs["h0"] is not None,
                                   method="direct", value_block=vb_pair),
-            lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"], method="direct", value_block=vb_pair))
+            (lambda: ops.fwd_h_u(ks, ws, xs["v"], sv["Akk"], g, gate, beta=xs.get("beta"), w_gate=xs.get("w"),
+                                 h0=xs["h0"], value_block=vb_pair)) if fold_u else
+            (lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"], method="direct", value_block=vb_pair)))
         (dh, dR, _), (h, v_new, _) = kern["paired_recurrences"]()
     elif keep and ops._state_method("auto", cfg["B"], cfg["H"], NT) == "segmented":
         # long rows, few heads: segment maps in parallel, a short chain, segments rerun
@@ -328,7 +349,7 @@ def measure(cfg, steps, warmup):
     ms = time_steps(step, steps, warmup, WARMUP_MIN_S, winfo)
     fwd_ms = time_steps(forward, max(3, steps // 4), 1)
     kt = time_kernels(kern, max(5, steps))
-    costs = kernel_costs(cfg["op"], cfg["full_saving"], inline_aqk(cfg))
+    costs = kernel_costs(cfg["op"], cfg["full_saving"], inline_aqk(cfg), folds_u(cfg))
     kernels = {}
     for n, t in kt.items():
         by, fl = costs[n]

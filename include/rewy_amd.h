@@ -235,6 +235,8 @@ hipError_t fdr_chunk_bwd_original(const void* q, const void* k, const void* v, c
  * (scalar / no gate) the intra-chunk scores Aqk = scale tril(q k^T 2^(g_i - g_s))
  * (fp32 [B,T,H,64]) that FLA chunk_bwd_dv_local forms (backward.py:119).
  * Scalar-beta families pass beta and null b_gate/w_gate; GDN2 passes b_gate/w_gate.
+ * u = nullptr writes w (and qg, kg) only, for fdr_fwd_h_u, which forms u itself (vector gates
+ * with qg / kg; scalar / no gates without Aqk); v and w_gate are then not read.
  */
 hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const float* g,
                           int gate_mode, const float* beta, const void* b_gate, const void* w_gate,
@@ -271,6 +273,21 @@ hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const f
                             const float* h0, void* h, void* v_new, float* ht, int state_v_first,
                             const int* chunk_offsets, const int* cu_seqlens, int N, int num_chunks, int H,
                             int k_heads, int K, int V, int chunk, int value_block, hipStream_t stream);
+
+/*
+ * The forward scan of fdr_fwd_h with u formed in-kernel: FLA's recompute_w_u_fwd's u
+ * (u = Akk (beta v), or Akk (w_gate v) for GDN2) folded into chunk_gated_delta_rule_fwd_h
+ * (reference backends/backward.py:110-118), for the recompute policy's paired recurrences,
+ * where fdr_prepare_wu (with u = nullptr) writes w (and qg, kg) but not u.  k is kg for a vector
+ * gate (one row per value head), raw k otherwise (k_heads q/k heads); w as fdr_prepare_wu
+ * writes it; v bf16 [B,T,H,V]; beta fp32 [B,T,H], or w_gate bf16 [B,T,H,V] (vector gate only);
+ * Akk fp32 [B,T,H,64].  u is formed with fdr_prepare_wu's MFMA sequence and roundings, so h,
+ * v_new and ht are the bits of fdr_prepare_wu + fdr_fwd_h.  value_block as for fdr_fwd_h.
+ */
+hipError_t fdr_fwd_h_u(const void* k, const void* w, const void* v, const float* g, int gate_mode,
+                       const float* beta, const void* w_gate, const float* Akk, const float* h0, void* h,
+                       void* v_new, float* ht, int state_v_first, int B, int T, int H, int k_heads, int K, int V,
+                       int chunk, int value_block, hipStream_t stream);
 
 /*
  * The recompute pair fdr_prepare_wu + fdr_fwd_h in one sweep.  Replaces FLA

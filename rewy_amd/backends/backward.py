@@ -154,12 +154,19 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
         # state recurrence and the forward scan side by side, both direct, at a value-tile
         # width that gives each launch at most half the CUs
         vb = ops.paired_tile(N, H, NT, ops.GATE_VECTOR)
-        pre = _prepare_vector(k, v, g, Akk, gates, q, vl)
+        fold_u = ops.PAIRED_U
+        pre = _prepare_vector(k, v, g, Akk, gates, q, vl, want_u=not fold_u)
+
+        def scan():
+            if fold_u:      # u formed inside the scan (prepare_wu wrote w, qg, kg only)
+                return ops.fwd_h_u(pre["kg"], pre["w"], v, Akk, g, ops.GATE_VECTOR, beta=_f32(gates.get("beta")),
+                                   w_gate=None if gates.get("w") is None else _bf(gates["w"]),
+                                   h0=_f32(initial_state), value_block=vb, state_v_first=vf)
+            return ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
+                             method="direct", value_block=vb, state_v_first=vf)
         (dh, dR, dh0), (h, v_new, _) = _side_by_side(
             lambda: _state_vector(pre, g, do, scale, Aqk, dht, initial_state, vl, vf, method="direct",
-                                  value_block=vb),
-            lambda: ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
-                              method="direct", value_block=vb, state_v_first=vf))
+                                  value_block=vb), scan)
         saved, hvf = dict(v_new=v_new, h=h), False
     elif recompute and (ops.side_by_side_pays(N, H, NT) if vl is None else
                         ops.SIDE_BY_SIDE and not ops.fwd_h_wy_pays(N, H, ops.GATE_VECTOR, vl)):
@@ -190,11 +197,11 @@ def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, vl=None, vf=Fals
                          method=method if vl is None else "direct", varlen=vl, state_v_first=vf)
 
 
-def _prepare_vector(k, v, g, Akk, gates, q, vl=None):
+def _prepare_vector(k, v, g, Akk, gates, q, vl=None, want_u=True):
     b = None if gates.get("b") is None else _bf(gates["b"])
     w = None if gates.get("w") is None else _bf(gates["w"])
     return ops.prepare_wu(k, v, Akk, ops.GATE_VECTOR, g=g, beta=_f32(gates.get("beta")), b=b, w=w, q=q,
-                          want_qkg=True, varlen=vl)
+                          want_qkg=True, varlen=vl, want_u=want_u)
 
 
 def _recompute_vector(q, k, v, g, Akk, initial_state, gates, vl=None, vf=False):
@@ -291,7 +298,8 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
                               state_v_first=state_v_first)
             w, h, v_new = sw["w"], sw["h"], sw["v_new"]
         else:
-            pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, varlen=vl)
+            # paired (vb): u formed inside the scan where ops.PAIRED_U holds
+            pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, varlen=vl, want_u=not (vb and ops.PAIRED_U))
             w = pre["w"]
 
         def state():
@@ -299,6 +307,9 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
                                  method="direct", varlen=vl, state_v_first=state_v_first, value_block=vb)
 
         def scan():
+            if pre["u"] is None:
+                return ops.fwd_h_u(k, w, v, A, g, gate, beta=beta, h0=_f32(initial_state), value_block=vb,
+                                   state_v_first=state_v_first)
             return ops.fwd_h(k, w, pre["u"], g, gate, h0=_f32(initial_state), method="direct", varlen=vl,
                              state_v_first=state_v_first, value_block=vb)
         if pre is None:

@@ -31,7 +31,7 @@ constexpr int T128 = KD * LDT * 2;
 // ------------------------------------------------------------------------------------------
 // fdr_prepare_wu
 // ------------------------------------------------------------------------------------------
-template <int GATE, bool VEC_B, bool WANT_QKG, bool WANT_AQK, bool MAP>
+template <int GATE, bool VEC_B, bool WANT_QKG, bool WANT_AQK, bool MAP, bool WANT_U = true>
 __global__ __launch_bounds__(256) void prepare_wu_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     rgs[i] = (GATE == RG_SCALAR) ? g[(tok0 + rw.clamp(t)) * H + h] : 0.f;
     rbs[i] = VEC_B ? 0.f : *rw.src(beta + (tok0 + t) * H + h, t);
     rkx[i] = *reinterpret_cast<const u32x4*>(rw.src(k + qr.ofs + (size_t)t * qr.rs + c0, t));
-    rvx[i] = *reinterpret_cast<const u32x4*>(rw.src(v + vofs + (size_t)t * rsv + c0, t));
+    if constexpr (WANT_U) rvx[i] = *reinterpret_cast<const u32x4*>(rw.src(v + vofs + (size_t)t * rsv + c0, t));
     ra4[i] = *reinterpret_cast<const f32x4*>(tril_src(rw.src(akk + ((tok0 + t) * H + h) * C + 4 * (p & 15), t), t,
                                                       p & 15));
     if constexpr (GATE == RG_VECTOR) {
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     }
     if constexpr (VEC_B) {
       rbx[i] = *reinterpret_cast<const u32x4*>(rw.src(bgate + kofs + (size_t)t * rsk + c0, t));
-      rwx[i] = *reinterpret_cast<const u32x4*>(rw.src(wgate + vofs + (size_t)t * rsv + c0, t));
+      if constexpr (WANT_U) rwx[i] = *reinterpret_cast<const u32x4*>(rw.src(wgate + vofs + (size_t)t * rsv + c0, t));
     }
     if constexpr (WANT_QKG && GATE == RG_VECTOR)
       rqx[i] = *reinterpret_cast<const u32x4*>(rw.src(q + qr.ofs + (size_t)t * qr.rs + c0, t));
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     const int p = tid + 256 * i;
     const int t = p >> 4, ch = p & 15, c0 = 8 * ch;
     const bf16x8 kx = __builtin_bit_cast(bf16x8, rkx[i]);
-    const bf16x8 vx = __builtin_bit_cast(bf16x8, rvx[i]);
+    const bf16x8 vx = WANT_U ? __builtin_bit_cast(bf16x8, rvx[i]) : bf16x8{};
     float ge[8], be[8], we[8];
     if constexpr (GATE == RG_VECTOR) {
 #pragma unroll
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
     }
     if constexpr (VEC_B) {
       const bf16x8 bx = __builtin_bit_cast(bf16x8, rbx[i]);
-      const bf16x8 wx = __builtin_bit_cast(bf16x8, rwx[i]);
+      const bf16x8 wx = WANT_U ? __builtin_bit_cast(bf16x8, rwx[i]) : bf16x8{};
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         be[j] = to_f32(bx[j]);
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
       zh[j] = to_bf16(we[j] * to_f32(vx[j]));
     }
     store_tr_chunk<16>(eH, t, ch, __builtin_bit_cast(u32x4, eh));
-    store_tr_chunk<16>(zH, t, ch, __builtin_bit_cast(u32x4, zh));
+    if constexpr (WANT_U) store_tr_chunk<16>(zH, t, ch, __builtin_bit_cast(u32x4, zh));
     // A rows: 64 x 64 fp32 = 1024 pieces of 4, one per (i, thread) here
     bf16x4 alo;
     const bf16x4 ahi = split_hi4(tril_piece(ra4[i], t, ch), alo);
@@ -187,9 +187,10 @@ __global__ __launch_bounds__(256) void prepare_wu_kernel(
 
   // ---- w^T = E^T A^T, u^T = Z^T A^T: B operand = A rows (t), contiguous s, from LDS ----
   // wave wv: output rows (k or v) [32 wv, 32 wv + 32), all 64 token columns
+  // (!WANT_U: w only; the forward scan that reads w forms u itself, fdr_fwd_h_u)
   {
 #pragma unroll
-    for (int which = 0; which < 2; ++which) {
+    for (int which = 0; which < (WANT_U ? 2 : 1); ++which) {
       const bf16* srcH = which == 0 ? eH : zH;
       bf16* dst = which == 0 ? w_out + kofs : u_out + vofs;
       const size_t rs = which == 0 ? rsk : rsv;
@@ -513,14 +514,17 @@ struct FwdWySmem {
   float lam[2][KD];
 };
 
-template <int BV, int GATE, bool VEC_B, bool MAP>
+// WG (fdr_fwd_h_u): w is given (w_in, as fdr_prepare_wu wrote it) and only u is formed here;
+// k is then kg for a vector gate (as fdr_fwd_h takes it), raw k otherwise, and nothing but h,
+// v_new (and the final state) is written.
+template <int BV, int GATE, bool VEC_B, bool MAP, bool WG = false>
 __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
     const bf16* __restrict__ wgate, const float* __restrict__ akk, const float* __restrict__ h0,
     bf16* __restrict__ w_out, bf16* __restrict__ qg_out, bf16* __restrict__ kg_out, bf16* __restrict__ h_out,
     bf16* __restrict__ vnew_out, float* __restrict__ ht_out, int T, int H, const int* __restrict__ chunk_off,
-    int vf, int HQ, const int* __restrict__ cu) {
+    int vf, int HQ, const int* __restrict__ cu, const bf16* __restrict__ w_in = nullptr) {
   static_assert(!VEC_B || GATE == RG_VECTOR, "vector b / w_gate come with the vector gate (GDN2)");
   constexpr bool VEC = GATE == RG_VECTOR;
   using S = FwdWySmem<BV>;
@@ -584,21 +588,28 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     } else if constexpr (VEC) {
       // lambda's column (tid < KD), and g_last of this thread's 8 columns (both pieces)
       rg_last = g[kofs + (size_t)rs_.clamp(C - 1) * rsk + (tid & (KD - 1))];
-      const float* gl = g + kofs + (size_t)rs_.clamp(C - 1) * rsk + 8 * (tid & 15);
-      rgl0 = *reinterpret_cast<const f32x4*>(gl);
-      rgl1 = *reinterpret_cast<const f32x4*>(gl + 4);
+      if constexpr (!WG) {
+        const float* gl = g + kofs + (size_t)rs_.clamp(C - 1) * rsk + 8 * (tid & 15);
+        rgl0 = *reinterpret_cast<const f32x4*>(gl);
+        rgl1 = *reinterpret_cast<const f32x4*>(gl + 4);
+      }
     }
-    const QKRows kr_ = qk_rows(tok0, h, H, HQ);
+    // (WG with a vector gate: k is kg, one row per value head)
+    const QKRows kr_ = (WG && VEC) ? QKRows{kofs, rsk} : qk_rows(tok0, h, H, HQ);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i, t = p >> 4, c8 = 8 * (p & 15);
-      if constexpr (VEC) {
-        rg0[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8);
-        rg1[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8 + 4);
-        rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + kr_.ofs + (size_t)t * kr_.rs + c8, t));
+      if constexpr (WG) {
+        rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(w_in + kofs + (size_t)t * rsk + c8, t));   // w rows
+      } else {
+        if constexpr (VEC) {
+          rg0[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8);
+          rg1[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8 + 4);
+          rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + kr_.ofs + (size_t)t * kr_.rs + c8, t));
+        }
+        if constexpr (VEC_B) rb[i] = *reinterpret_cast<const u32x4*>(rs_.src(bgate + kofs + (size_t)t * rsk + c8, t));
+        else rb_tok[i] = *rs_.src(beta + (tok0 + t) * H + h, t);
       }
-      if constexpr (VEC_B) rb[i] = *reinterpret_cast<const u32x4*>(rs_.src(bgate + kofs + (size_t)t * rsk + c8, t));
-      else rb_tok[i] = *rs_.src(beta + (tok0 + t) * H + h, t);
       rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + kr_.ofs + (size_t)t * kr_.rs + c8, t));
       ra[i] = *reinterpret_cast<const f32x4*>(tril_src(rs_.src(akk + ((tok0 + t) * H + h) * C + 4 * (p & 15), t),
                                                        t, p & 15));
@@ -625,7 +636,11 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       // E = (b k) 2^g and kg = k 2^(g_last - g), each rounded as prepare_wu_kernel rounds it
       const bf16x8 kx = __builtin_bit_cast(bf16x8, rk[i]);
       bf16x8 eh, kg;
-      if constexpr (VEC) {
+      if constexpr (WG) {
+        // w and kg as given (the scalar gate's kg formed as fdr_fwd_h forms it); no E
+        *reinterpret_cast<u32x4*>(&sm.w[pb][t][8 * ch]) = rq[i];
+        kg = GATE == RG_SCALAR ? __builtin_bit_cast(bf16x8, scale_bf16x8(rk[i], fast_exp2(rg_last - rg_tok[i]))) : kx;
+      } else if constexpr (VEC) {
         const bf16x8 qx = __builtin_bit_cast(bf16x8, rq[i]);
         bf16x8 bx = {};
         if constexpr (VEC_B) bx = __builtin_bit_cast(bf16x8, rb[i]);
@@ -649,7 +664,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
         for (int j = 0; j < 8; ++j) eh[j] = to_bf16(rb_tok[i] * to_f32(kx[j]) * ge);
         kg = GATE == RG_SCALAR ? __builtin_bit_cast(bf16x8, scale_bf16x8(rk[i], fast_exp2(rg_last - rg_tok[i]))) : kx;
       }
-      store_tr_chunk<16>(sm.e, t, ch, __builtin_bit_cast(u32x4, eh));
+      if constexpr (!WG) store_tr_chunk<16>(sm.e, t, ch, __builtin_bit_cast(u32x4, eh));
       store_tr_chunk<16>(sm.k[pb], t, ch, __builtin_bit_cast(u32x4, kg));
       bf16x4 alo;
       const bf16x4 ahi = split_hi4(tril_piece(ra[i], t, ch), alo);
@@ -677,7 +692,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
   // w^T = E^T A^T (wave wv: k rows [16 wv, 16 wv + 16), all 64 tokens) and u^T = Z^T A^T
   // ((value row tile, token tile) pairs over the waves) of the staged chunk, into buffer `pb`
   auto form_wu = [&](int pb) {
-    {
+    if constexpr (!WG) {
       const int row0 = 16 * wv;
       const bf16x8 x0 = frag_tr<16>(sm.e, 0, row0);
       const bf16x8 x1 = frag_tr<16>(sm.e, 32, row0);
@@ -715,13 +730,17 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     for (int i = 0; i < 2; ++i) {
       settle(rk[i]);
       settle(ra[i]);
-      if constexpr (VEC) {
+      if constexpr (WG) {
         settle(rq[i]);
-        settle(rg0[i]);
-        settle(rg1[i]);
+      } else {
+        if constexpr (VEC) {
+          settle(rq[i]);
+          settle(rg0[i]);
+          settle(rg1[i]);
+        }
+        if constexpr (VEC_B) settle(rb[i]);
+        else settle(rb_tok[i]);
       }
-      if constexpr (VEC_B) settle(rb[i]);
-      else settle(rb_tok[i]);
       if constexpr (GATE == RG_SCALAR) settle(rg_tok[i]);
     }
 #pragma unroll
@@ -730,7 +749,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       if constexpr (VEC_B) settle(rwg[i]);
       else settle(rb_v[i]);
     }
-    if constexpr (VEC) {
+    if constexpr (VEC && !WG) {
       settle(rgl0);
       settle(rgl1);
     }
@@ -763,8 +782,8 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
     const size_t tok0 = rs_.tok0;
     // w rows [64 vt / NVT, ...) of chunk c to HBM, 16-byte pieces (every lane stores: pieces
-    // beyond the share are written twice, with the same data)
-    {
+    // beyond the share are written twice, with the same data); WG: w came from HBM
+    if constexpr (!WG) {
       constexpr int NWP = RW * (KD / 8);
 #pragma unroll
       for (int i = 0; i < (NWP + NTH - 1) / NTH; ++i) {
@@ -841,28 +860,30 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
   }
 }
 
-template <int BV, int GATE, bool VEC_B>
+template <int BV, int GATE, bool VEC_B, bool WG = false>
 static hipError_t launch_fwd_h_wy(const void* q, const void* k, const void* v, const float* g, const float* beta,
                                   const void* bg, const void* wg, const float* akk, const float* h0, void* w,
                                   void* qg, void* kg, void* h, void* vnew, float* ht, int B, int T, int H,
-                                  hipStream_t s, const int* co, int vf, int HQ, const int* cu) {
+                                  hipStream_t s, const int* co, int vf, int HQ, const int* cu,
+                                  const void* w_in = nullptr) {
 #define FW_LAUNCH(MAP)                                                                                             \
-  hipLaunchKernelGGL((fwd_h_wy_kernel<BV, GATE, VEC_B, MAP>), dim3(B * H * (VD / BV)), dim3(512), 0, s,            \
+  hipLaunchKernelGGL((fwd_h_wy_kernel<BV, GATE, VEC_B, MAP, WG>), dim3(B * H * (VD / BV)), dim3(512), 0, s,        \
                      (const bf16*)q, (const bf16*)k, (const bf16*)v, g, beta, (const bf16*)bg, (const bf16*)wg, akk, \
-                     h0, (bf16*)w, (bf16*)qg, (bf16*)kg, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf, HQ, cu)
+                     h0, (bf16*)w, (bf16*)qg, (bf16*)kg, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf, HQ, cu,        \
+                     (const bf16*)w_in)
   if (cu) FW_LAUNCH(true);
   else FW_LAUNCH(false);
 #undef FW_LAUNCH
   return hipGetLastError();
 }
 
-template <int GATE, bool VEC_B, bool QKG, bool AQK>
+template <int GATE, bool VEC_B, bool QKG, bool AQK, bool WU = true>
 static hipError_t launch_prepare(const void* q, const void* k, const void* v, const float* g,
                                  const float* beta, const void* bg, const void* wg, const float* akk,
                                  void* w, void* u, void* qg, void* kg, float* aqk, int B, int T, int H, int HQ,
                                  float scale, hipStream_t s, const int* cu, const int* ci) {
 #define P_LAUNCH(MAP)                                                                                            \
-  hipLaunchKernelGGL((prepare_wu_kernel<GATE, VEC_B, QKG, AQK, MAP>), dim3(B * H * (T / C)), dim3(256), 0, s,   \
+  hipLaunchKernelGGL((prepare_wu_kernel<GATE, VEC_B, QKG, AQK, MAP, WU>), dim3(B * H * (T / C)), dim3(256), 0, s, \
                      (const bf16*)q, (const bf16*)k, (const bf16*)v, g, beta, (const bf16*)bg, (const bf16*)wg, \
                      akk, (bf16*)w, (bf16*)u, (bf16*)qg, (bf16*)kg, aqk, T, H, HQ, scale, cu, ci)
   if (cu) P_LAUNCH(true);
@@ -895,7 +916,7 @@ static hipError_t prepare_dispatch(const void* q, const void* k, const void* v, 
                                    int qk_heads, float scale, hipStream_t stream, const int* cu, const int* ci) {
   const int HQ = qk_heads > 0 ? qk_heads : H;
   if (H % HQ || (b_gate && HQ != H)) return hipErrorInvalidValue;
-  if (!k || !v || !Akk || !w || !u) return hipErrorInvalidValue;
+  if (!k || !Akk || !w) return hipErrorInvalidValue;
   const bool vec_b = b_gate != nullptr;
   if (vec_b && (!w_gate || gate_mode != RG_VECTOR)) return hipErrorInvalidValue;
   if (!vec_b && !beta) return hipErrorInvalidValue;
@@ -905,6 +926,20 @@ static hipError_t prepare_dispatch(const void* q, const void* k, const void* v, 
   const bool want_aqk = Aqk != nullptr;
   if (want_aqk && (!q || gate_mode == RG_VECTOR)) return hipErrorInvalidValue;
 #define P_ARGS q, k, v, g, beta, b_gate, w_gate, Akk, w, u, qg, kg, Aqk, B, T, H, HQ, scale, stream, cu, ci
+  if (!u) {
+    // w (and qg, kg) only, for the forward scan that forms u itself (fdr_fwd_h_u): vector gates
+    // with qg / kg, or scalar / no gates without Aqk
+    if (want_aqk || (gate_mode == RG_VECTOR) != want_qkg) return hipErrorInvalidValue;
+    switch (gate_mode) {
+      case RG_NONE: return launch_prepare<RG_NONE, false, false, false, false>(P_ARGS);
+      case RG_SCALAR: return launch_prepare<RG_SCALAR, false, false, false, false>(P_ARGS);
+      case RG_VECTOR:
+        return vec_b ? launch_prepare<RG_VECTOR, true, true, false, false>(P_ARGS)
+                     : launch_prepare<RG_VECTOR, false, true, false, false>(P_ARGS);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (!v) return hipErrorInvalidValue;
   switch (gate_mode) {
     case RG_NONE:
       return want_aqk ? launch_prepare<RG_NONE, false, false, true>(P_ARGS)
@@ -1045,6 +1080,53 @@ extern "C" hipError_t fdr_fwd_h_wy(const void* q, const void* k, const void* v, 
                                    int value_block, hipStream_t stream) {
   return fwd_h_wy_dispatch(q, k, v, g, gate_mode, beta, b_gate, w_gate, Akk, h0, w, qg, kg, h, v_new, ht, B, T, H,
                            qk_heads, K, V, chunk, value_block, stream, nullptr, state_v_first ? 1 : 0, nullptr);
+}
+
+// The forward scan with u formed in-kernel from v (and beta or w_gate) and Akk, w given:
+// B rows of T tokens, or (co[, cu]) packed sequences as for fwd_h_dispatch
+static hipError_t fwd_h_u_dispatch(const void* k, const void* w, const void* v, const float* g, int gate_mode,
+                                   const float* beta, const void* w_gate, const float* Akk, const float* h0, void* h,
+                                   void* v_new, float* ht, int B, int T, int H, int HQ, int K, int V, int chunk,
+                                   int value_block, hipStream_t stream, const int* co, int vf, const int* cu) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  if (HQ <= 0) HQ = H;
+  if (H % HQ) return hipErrorInvalidValue;
+  if (!k || !w || !v || !Akk || !h || !v_new) return hipErrorInvalidValue;
+  const bool vec_b = w_gate != nullptr;
+  if (vec_b && gate_mode != RG_VECTOR) return hipErrorInvalidValue;
+  if (!vec_b && !beta) return hipErrorInvalidValue;
+  if (gate_mode == RG_VECTOR && HQ != H) return hipErrorInvalidValue;   // k is kg, per value head
+  if (gate_mode != RG_NONE && !g) return hipErrorInvalidValue;
+  if (cu && !co) return hipErrorInvalidValue;
+  const int bv = value_block > 0 ? value_block : fwd_default_bv(B, H);
+  // (b_gate is not read in this mode: only u's Z = w_gate v; a non-null pointer selects VEC_B)
+#define FU_ARGS nullptr, k, v, g, beta, w_gate, w_gate, Akk, h0, nullptr, nullptr, nullptr, h, v_new, ht, B, T, H, \
+                stream, co, vf, HQ, cu, w
+#define FU_BV(G, VB)                                                \
+  switch (bv) {                                                     \
+    case 16: return launch_fwd_h_wy<16, G, VB, true>(FU_ARGS);      \
+    case 32: return launch_fwd_h_wy<32, G, VB, true>(FU_ARGS);      \
+    case 64: return launch_fwd_h_wy<64, G, VB, true>(FU_ARGS);      \
+    default: return hipErrorInvalidValue;                           \
+  }
+  switch (gate_mode) {
+    case RG_NONE: FU_BV(RG_NONE, false)
+    case RG_SCALAR: FU_BV(RG_SCALAR, false)
+    case RG_VECTOR:
+      if (vec_b) FU_BV(RG_VECTOR, true)
+      FU_BV(RG_VECTOR, false)
+    default: return hipErrorInvalidValue;
+  }
+#undef FU_BV
+#undef FU_ARGS
+}
+
+extern "C" hipError_t fdr_fwd_h_u(const void* k, const void* w, const void* v, const float* g, int gate_mode,
+                                  const float* beta, const void* w_gate, const float* Akk, const float* h0, void* h,
+                                  void* v_new, float* ht, int state_v_first, int B, int T, int H, int k_heads, int K,
+                                  int V, int chunk, int value_block, hipStream_t stream) {
+  return fwd_h_u_dispatch(k, w, v, g, gate_mode, beta, w_gate, Akk, h0, h, v_new, ht, B, T, H, k_heads, K, V, chunk,
+                          value_block, stream, nullptr, state_v_first ? 1 : 0, nullptr);
 }
 
 extern "C" hipError_t fdr_fwd_h_wy_varlen(const void* q, const void* k, const void* v, const float* g, int gate_mode,

@@ -94,6 +94,8 @@ def side_by_side_pays(B, H, NT):
 # per CU.
 PAIRED = True
 PAIRED_MIN_BH = 24
+# ... with u formed inside the scan (fwd_h_u) instead of written by prepare_wu and read back
+PAIRED_U = True
 
 
 def paired_tile(B, H, NT, gate_mode):
@@ -628,9 +630,10 @@ def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale
 
 
 def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, want_qkg=False,
-               want_aqk=False, scale=1.0, varlen=None):
+               want_aqk=False, scale=1.0, varlen=None, want_u=True):
     """WY factors (and qg/kg or Aqk) of every chunk.  Returns dict(w, u, qg, kg, Aqk).
-    ``varlen``: a packed variable-length batch (``Varlen``)."""
+    ``varlen``: a packed variable-length batch (``Varlen``).  ``want_u=False``: w (and qg, kg)
+    only, for ``fwd_h_u`` (u None; v and the write gate are not read)."""
     B, T, HQ, K = _rows(k, varlen)
     H, HQ = _group(v.shape[2] if v is not None and v.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
@@ -657,7 +660,10 @@ def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, 
         raise ValueError("qg/kg need q and a vector gate")
     if want_aqk and (q is None or gate_mode == GATE_VECTOR):
         raise ValueError("Aqk is produced here for scalar / no-gate families only")
-    out = dict(w=torch.empty(B, T, H, K, device=dev, dtype=bf), u=torch.empty(B, T, H, V, device=dev, dtype=bf),
+    if not want_u and (want_aqk or want_qkg != (gate_mode == GATE_VECTOR) or varlen is not None):
+        raise ValueError("want_u=False takes qg / kg for a vector gate, no Aqk, dense rows")
+    out = dict(w=torch.empty(B, T, H, K, device=dev, dtype=bf),
+               u=torch.empty(B, T, H, V, device=dev, dtype=bf) if want_u else None,
                qg=torch.empty(B, T, H, K, device=dev, dtype=bf) if want_qkg else None,
                kg=torch.empty(B, T, H, K, device=dev, dtype=bf) if want_qkg else None,
                Aqk=torch.empty(B, T, H, CHUNK, device=dev, dtype=f32) if want_aqk else None)
@@ -735,6 +741,51 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
     st = _lib.load().fdr_fwd_h(P(k), P(w), P(u), P(g), int(gate_mode), P(h0), P(h), P(vnew), P(ht), vf, B, T, H, HQ,
                                K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_h")
+    return h, vnew, ht
+
+
+def fwd_h_u(k, w, v, Akk, g, gate_mode, beta=None, w_gate=None, h0=None, want_final=False, value_block=0,
+            state_v_first=False):
+    """``fwd_h`` with u formed in-kernel (fdr_fwd_h_u): u = Akk (beta v), or Akk (w_gate v) for
+    GDN2, from the same MFMA sequence as ``prepare_wu``, so h, v_new and the final state are
+    the bits of ``prepare_wu`` + ``fwd_h``.  k is kg for a vector gate, raw k otherwise; w as
+    ``prepare_wu(..., want_u=False)`` returns it.  Returns (h, v_new, final|None)."""
+    B, T, HQ, K = _dims(k)
+    H, HQ = _group(w.shape[2] if w is not None and w.ndim == 4 else HQ, HQ)
+    V = V_SUPPORTED
+    dev = k.device
+    bf, f32 = torch.bfloat16, torch.float32
+    _need(k, "k", bf, (B, T, HQ, K), dev)
+    _need(w, "w", bf, (B, T, H, K), dev)
+    _need(v, "v", bf, (B, T, H, V), dev)
+    _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
+    if gate_mode == GATE_VECTOR:
+        if HQ != H:
+            raise ValueError("a vector gate's kg has one row per value head")
+        _need(g, "g", f32, (B, T, H, K), dev)
+    elif gate_mode == GATE_SCALAR:
+        _need(g, "g", f32, (B, T, H), dev)
+    elif gate_mode != GATE_NONE:
+        raise ValueError("gate_mode must be 0, 1 or 2")
+    if w_gate is not None:
+        if gate_mode != GATE_VECTOR:
+            raise ValueError("w_gate (GDN2) takes the vector gate")
+        _need(w_gate, "w_gate", bf, (B, T, H, V), dev)
+    else:
+        _need(beta, "beta", f32, (B, T, H), dev)
+    if h0 is not None:
+        _need(h0, "h0", f32, (B, H, K, V), dev)
+    if value_block not in (0, 16, 32, 64):
+        raise ValueError("value_block must be 0, 16, 32 or 64")
+    NT = T // CHUNK
+    h = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
+    vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
+    ht = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_final else None
+    P = _lib.ptr
+    st = _lib.load().fdr_fwd_h_u(P(k), P(w), P(v), P(g), int(gate_mode), P(beta), P(w_gate), P(Akk), P(h0), P(h),
+                                 P(vnew), P(ht), int(bool(state_v_first)), B, T, H, HQ, K, V, CHUNK, int(value_block),
+                                 _lib.stream_handle(dev))
+    _lib.check(st, "fdr_fwd_h_u")
     return h, vnew, ht
 
 

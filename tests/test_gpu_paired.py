@@ -6,7 +6,8 @@ scalar / no-gate ones with the state recurrence forming Aqk itself):
 
 * the public autograd backward (recompute policy) against the fp64 oracle at the
   reference's acceptance tolerances (validation.py:40-45, :68);
-* the same gradients, bit for bit, as the same launches enqueued on one stream;
+* the same gradients, bit for bit, as the same launches enqueued on one stream, and as the
+  scan reading a u that prepare_wu wrote (``ops.PAIRED_U`` off: the scan forms u itself);
 * against the policy switched off (the pair one after the other at the default tile
   width): rel-L2 <= 1e-5, the tile width changing no arithmetic of a value column;
 * captured in a HIP graph and replayed three times with eager work between the replays.
@@ -100,6 +101,12 @@ def test_paired_equals_one_stream_and_policy_off(op, B, T, H, vb, monkeypatch):
     for i, (a, r) in enumerate(zip(got, one)):
         assert torch.equal(a, r), (op, i)
     monkeypatch.undo()
+    # u written by prepare_wu and read by fdr_fwd_h instead of formed in the scan: the same bits
+    monkeypatch.setattr(ops, "PAIRED_U", False)
+    unfolded = run()
+    torch.cuda.synchronize()
+    for i, (a, r) in enumerate(zip(got, unfolded)):
+        assert torch.equal(a, r), (op, "PAIRED_U", i)
     monkeypatch.setattr(ops, "PAIRED", False)
     off = run()
     torch.cuda.synchronize()
