@@ -223,7 +223,7 @@ def setup(cfg, device):
     # the recompute policy's direct path (as the backends decide): w / u in the forward scan's
     # sweep (fdr_fwd_h_wy); for the scalar / no-gate families Aqk in the state recurrence
     fused = (not keep and not ops.affine_pays(xs["q"]) and (inline or vec)
-             and ops.fwd_h_wy_pays(cfg["B"], cfg["H"], gate))
+             and ops.fwd_h_wy_pays(cfg["B"], cfg["H"], gate) and not ops.paired_tile(cfg["B"], cfg["H"], NT, gate))
     if fused:
         kern["fdr_fwd_h_wy"] = lambda: ops.fwd_h_wy(xs["k"], xs["v"], sv["Akk"], g, gate, beta=xs.get("beta"),
                                                     q=xs["q"] if vec else None, b=xs.get("b"), w=xs.get("w"),

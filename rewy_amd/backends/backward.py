@@ -17,10 +17,9 @@ When batch x heads is too small to fill the GPU and the sequence long, the two
 recurrences run instead in affine-step form (after ``fdr_prepare_wu``: w, u and qg, kg or Aqk) (``ops.recurrences``,
 ``fdr_affine_*``): chunk-parallel step matrices, one scan launch carrying both
 recurrences side by side, and a chunk-parallel pass for v_new and dR.
-With 24 <= batch x heads where the fused sweep does not pay (vector gates below 128, scalar /
-no gate below 64) the recompute policy runs the direct backward state recurrence and the
-direct forward scan side by side on two streams, at a value-tile width that gives each at
-most half the CUs (``ops.paired_tile``).
+With 24 <= batch x heads <= 64 the recompute policy runs the direct backward state recurrence
+and the direct forward scan side by side on two streams, at a value-tile width that gives
+each at most half the CUs (``ops.paired_tile``).
 With a few more heads and long rows the recompute policy runs the forward scan
 (``fdr_fwd_h``) on the current stream beside the segmented backward state recurrence
 (``fdr_state_bwd_segmented``) on a second stream (``ops.side_by_side_pays``).
@@ -293,7 +292,7 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
                                                                           q.shape[1] // ops.CHUNK) == "direct"))
     if inline:
         pre = None
-        if ops.fwd_h_wy_pays(q.shape[0] if vl is None else vl.N, v.shape[2], gate, vl):
+        if not vb and ops.fwd_h_wy_pays(q.shape[0] if vl is None else vl.N, v.shape[2], gate, vl):
             sw = ops.fwd_h_wy(k, v, A, g, gate, beta=beta, h0=_f32(initial_state), varlen=vl,
                               state_v_first=state_v_first)
             w, h, v_new = sw["w"], sw["h"], sw["v_new"]

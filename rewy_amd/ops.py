@@ -87,11 +87,10 @@ def side_by_side_pays(B, H, NT):
     return BH <= AFFINE_MAX_BH or NT >= SEG_MIN_CHUNKS
 
 
-# Paired direct recurrences (recompute policy, the prepare_wu + fwd_h pair): when batch x
-# heads is too small for one direct recurrence to fill the GPU and the fused sweep does not
-# pay, the forward scan and the backward state recurrence run side by side at a common
-# value-tile width chosen so that the two launches together hold at most one work-group
-# per CU.
+# Paired direct recurrences (recompute policy): when batch x heads is too small for one
+# direct recurrence to fill the GPU, the forward scan and the backward state recurrence run
+# side by side at a common value-tile width chosen so that the two launches together hold
+# at most one work-group per CU.
 PAIRED = True
 PAIRED_MIN_BH = 24
 # ... with u formed inside the scan (fwd_h_u) instead of written by prepare_wu and read back
@@ -100,16 +99,17 @@ PAIRED_U = True
 
 def paired_tile(B, H, NT, gate_mode):
     """Value-tile width at which the recompute policy runs ``fwd_h`` and ``state_bwd`` (both
-    direct) side by side, or 0 when it runs them otherwise.  Taken with B H >= 24 where the
-    fused sweep does not pay (``fwd_h_wy_pays``: vector gates below B H = 128, scalar / no
-    gate below 64): the narrowest of 32 / 64 at which each launch has at most 128
-    work-groups.  Measured (MI355X, both recurrences, prepare_wu's outputs given): GDN2 B=2
-    T=8192 H=32 0.451 ms paired at 64-wide tiles vs 0.544 one after the other at 32-wide;
-    B=2 T=4096 H=16 0.177 (32-wide) vs 0.231; B=1 T=8192 H=48 0.443 vs 0.543; B=1 T=16384 H=24
-    0.639 (32-wide) vs 0.905 direct one after the other.  DeltaNet B=2 T=2048 H=16, the whole
-    backward as a graph replay: 148.6 us paired (32-wide) vs 178.4 us."""
+    direct) side by side, or 0 when it runs them otherwise: for 24 <= B H <= 64, the
+    narrowest of 32 / 64 at which each launch has at most 128 work-groups (the two together
+    one per CU).  Measured (MI355X): GDN2 B=2 T=8192 H=32 both recurrences 0.451 ms paired at
+    64-wide tiles vs 0.544 one after the other at 32-wide; B=2 T=4096 H=16 0.177 (32-wide) vs
+    0.231; B=1 T=8192 H=48 0.443 vs 0.543; B=1 T=16384 H=24 0.639 (32-wide) vs 0.905.  The
+    scalar / no-gate families, whose fused sweep (``fwd_h_wy_pays``) runs from B H = 64: GDN
+    B=4 T=2048 H=16 backward 0.288 ms paired (64-wide, u formed in the scan) vs 0.311 with the
+    sweep, DeltaNet same shape 0.261 vs 0.279; DeltaNet B=2 T=2048 H=16 (graph replay)
+    148.6 us paired (32-wide) vs 178.4 us."""
     BH = B * H
-    if not PAIRED or BH < PAIRED_MIN_BH or NT < 1 or fwd_h_wy_pays(B, H, gate_mode):
+    if not PAIRED or BH < PAIRED_MIN_BH or NT < 1:
         return 0
     for vb in (32, 64):
         if BH * (V_SUPPORTED // vb) <= 128:

@@ -172,8 +172,7 @@ def test_side_by_side_rule():
 def test_paired_rule():
     """ops.paired_tile (recompute policy, vector gates: the direct state recurrence beside the
     direct forward scan): the narrowest of 32 / 64 at which each launch holds <= 128
-    work-groups, for B*H >= 24 where the fused sweep does not pay (vector gates below 128,
-    scalar / no gate below 64)."""
+    work-groups, for 24 <= B*H <= 64."""
     from rewy_amd import ops
     V, S = ops.GATE_VECTOR, ops.GATE_SCALAR
     assert ops.paired_tile(2, 32, 128, V) == 64          # GDN2 configs[3]
@@ -182,8 +181,9 @@ def test_paired_rule():
     assert ops.paired_tile(1, 16, 512, V) == 0           # few heads: affine / side-by-side forms
     assert ops.paired_tile(8, 16, 64, V) == 0            # the fused sweep fills the GPU
     assert ops.paired_tile(1, 96, 64, V) == 0            # 64-wide tiles would need 192 CUs each
-    assert ops.paired_tile(2, 32, 128, S) == 0          # the scalar families' fused sweep pays from 64
+    assert ops.paired_tile(2, 32, 128, S) == 64 and ops.paired_tile(4, 16, 32, S) == 64   # before the fused sweep
     assert ops.paired_tile(2, 16, 32, S) == 32 and ops.paired_tile(1, 48, 64, ops.GATE_NONE) == 64
+    assert ops.paired_tile(8, 16, 64, S) == 0
 
 
 def test_kernel_seams_validate_before_launch():
