@@ -19,7 +19,7 @@
 // per-channel factor 2^(g_i - g_s) is split at the anchor n = 16 I (the first
 // row of block I): q 2^(g_i - g_n) <= 1 and k 2^(g_n - g_s) (<= 1 for J < I),
 // both split into bf16 hi + lo so each 16 x 16 tile is three MFMAs per 32-wide
-// slice of K (fp32-faithful).  A diagonal block whose gate span reaches 100 in
+// slice of K (16-bit operand mantissas, the lo x lo term dropped).  A diagonal block whose gate span reaches 100 in
 // log2 units (where the k-side factor could overflow) is evaluated pairwise in
 // fp32 instead.
 #include "common.hpp"

@@ -14,8 +14,8 @@
 //     h_c -> h[c] (bf16); v_new_c = u_c - w_c h_c (bf16); h_{c+1} = lambda_c h_c + kg_c^T v_new_c
 //
 // The WY products are computed transposed (w^T = E^T A^T) so the accumulator
-// layout stores w and u contiguously; A and E are split into bf16 hi + lo so
-// the products are fp32-faithful.
+// layout stores w and u contiguously; A and E are split into bf16 hi + lo (16
+// mantissa bits each; three MFMAs per product, the lo x lo term dropped).
 #include "common.hpp"
 #include "rewy_amd.h"
 
