@@ -218,6 +218,10 @@ def _apply(op, backend, full_saving, scale, output_final_state, q, k, v, g, beta
     if cu_seqlens is not None:
         if q.shape[0] != 1:
             raise ValueError(f"The batch size is expected to be 1 rather than {q.shape[0]} when using `cu_seqlens`.")
+        # The chunk map is built on the host, as FLA's prepare_chunk_indices(cu_seqlens, chunk,
+        # cu_seqlens_cpu) builds it (reference _compat/gdn.py:166): a caller that passes
+        # cu_seqlens_cpu spares the one device-to-host copy of cu_seqlens per call, which the
+        # map's construction otherwise needs.
         cu = (cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens).tolist()
         bounds = list(zip(cu[:-1], cu[1:]))
         if h0 is not None and h0.shape[0] != len(bounds):
