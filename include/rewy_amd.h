@@ -482,6 +482,16 @@ hipError_t fdr_beta_sigmoid_fwd(const void* x, int is_bf16, float scale, float* 
                                 hipStream_t stream);
 
 /*
+ * Grouped value heads: dq / dk summed over each q / k head's group of value heads.
+ * x bf16 [rows, heads, group, K] (the chunk kernels' per-value-head dq or dk, rows = B*T,
+ * heads = the q / k heads H, group = HV / H), out bf16 [rows, heads, K]:
+ *   out[r, h, :] = bf16(sum_j x[r, h, j, :]), in fp32, j ascending.
+ * Replaces the reshape-and-sum over FLA's per-value-head dq / dk (FLA's head map
+ * i_h = i_hv // (HV / H); the reference's GVA path, runtime.py:85, leaves it to torch).
+ */
+hipError_t fdr_group_sum(const void* x, void* out, long long rows, int heads, int group, int K, hipStream_t stream);
+
+/*
  * q / k L2 normalisation over K = 128 (use_qk_l2norm_in_kernel=True, reference
  * _compat/kda.py:202-206; FLA l2norm_fwd / l2norm_bwd), `rows` rows of 128 channels,
  * bf16 (is_bf16 = 1) or fp32:

@@ -57,6 +57,7 @@ SIGNATURES = {
     "fdr_kda_gate_fwd": [_P, _I, _P, _P, _I, _F, _P, _I, _I, _I, _I, _P],
     "fdr_kda_gate_bwd": [_P, _P, _I, _P, _P, _I, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "fdr_beta_sigmoid_fwd": [_P, _I, _F, _P, ctypes.c_longlong, _P],
+    "fdr_group_sum": [_P, _P, ctypes.c_longlong, _I, _I, _I, _P],
     "fdr_l2norm_fwd": [_P, _I, _P, _P, ctypes.c_longlong, _I, _F, _P],
     "fdr_l2norm_bwd": [_P, _I, _P, _P, _P, ctypes.c_longlong, _I, _P],
     "fdr_chunk_bwd_gate_fold": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _P, _P, _I,

@@ -77,12 +77,13 @@ def _bf(x):
 
 def _group_sum(out, HQ):
     """Grouped value heads: dq / dk come per value head; q / k's gradient is the sum over
-    each head's group (FLA's head map i_h = i_hv // (HV / H)), formed in fp32."""
+    each head's group (FLA's head map i_h = i_hv // (HV / H)), formed in fp32 in one pass
+    (fdr_group_sum)."""
     for n in ("dq", "dk"):
         x = out[n]
-        B, T, H, K = x.shape
-        if H != HQ:
-            out[n] = x.view(B, T, HQ, H // HQ, K).float().sum(3).to(x.dtype)
+        if x.shape[2] != HQ:
+            out[n] = ops.group_sum(x.contiguous(), HQ) if x.dtype == torch.bfloat16 else \
+                x.view(*x.shape[:2], HQ, x.shape[2] // HQ, x.shape[3]).float().sum(3).to(x.dtype)
     return out
 
 

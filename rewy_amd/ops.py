@@ -744,6 +744,23 @@ def fwd_h(k, w, u, g, gate_mode, h0=None, want_final=False, value_block=0, metho
     return h, vnew, ht
 
 
+def group_sum(x, HQ):
+    """dq / dk of grouped value heads summed over each q / k head's group (fdr_group_sum):
+    x bf16 [B, T, HV, K] with HV = G HQ, value head j of group h at h G + j (FLA's head map);
+    returns bf16 [B, T, HQ, K], each sum in fp32."""
+    B, T, HV, K = x.shape
+    if HV % HQ:
+        raise ValueError(f"value heads ({HV}) must be a multiple of the q/k heads ({HQ})")
+    _need(x, "x", torch.bfloat16, (B, T, HV, K), x.device)
+    if K != K_SUPPORTED:
+        raise ValueError(f"K must be {K_SUPPORTED}")
+    out = torch.empty(B, T, HQ, K, device=x.device, dtype=torch.bfloat16)
+    P = _lib.ptr
+    _lib.check(_lib.load().fdr_group_sum(P(x), P(out), B * T, HQ, HV // HQ, K, _lib.stream_handle(x.device)),
+               "fdr_group_sum")
+    return out
+
+
 def fwd_h_u(k, w, v, Akk, g, gate_mode, beta=None, w_gate=None, h0=None, want_final=False, value_block=0,
             state_v_first=False):
     """``fwd_h`` with u formed in-kernel (fdr_fwd_h_u): u = Akk (beta v), or Akk (w_gate v) for
