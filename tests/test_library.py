@@ -211,3 +211,23 @@ def test_kernel_seams_validate_before_launch():
         chunk_gated_delta_rule_bwd_dhu(torch.zeros(2, 100, 2, 128), x, x, x, x, cu_seqlens=cu)
     with pytest.raises(ValueError, match="GPU"):       # shapes pass; no device to run on
         chunk_gated_delta_rule_bwd_dhu(x, x, x, x, x, gk=x, cu_seqlens=cu)
+
+
+def test_seam_and_pairing_entry_points_reject_bad_arguments_without_touching_the_gpu():
+    """The kernel-level seams' packed-batch forms, GDN2's WY seam, the scan that forms u
+    itself and the GVA group sum validate their shapes and pointers before any launch."""
+    from rewy_amd import _lib
+    lib = _lib.load()
+    # K = 64 everywhere (only 128 supported), or no chunks / no row map
+    assert lib.fdr_fwd_h_u(*([None] * 4), 2, *([None] * 7), 0, 1, 128, 1, 1, 64, 128, 64, 0,
+                           None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fdr_fwd_h_u(*([None] * 4), 2, *([None] * 7), 0, 1, 128, 1, 1, 128, 128, 64, 0,
+                           None) == HIP_ERROR_INVALID_VALUE            # null operands
+    assert lib.fdr_group_sum(None, None, 16, 2, 2, 64, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fdr_group_sum(None, None, 0, 2, 2, 128, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fdr_gdn2_chunk_bwd_wy(*([None] * 19), 0, 1, 128, 1, 64, 128, 64, 1.0, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fdr_gdn2_chunk_bwd_wy_varlen(*([None] * 19), 0, None, None, 2, 1, 128, 128, 64, 1.0,
+                                            None) == HIP_ERROR_INVALID_VALUE   # no row map
+    assert lib.fdr_chunk_bwd_wy_varlen(*([None] * 17), 0, None, None, 2, 1, 1, 128, 128, 64, 1.0,
+                                       None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fdr_matrix_intra_varlen(*([None] * 13), 0, 1, 1, 128, 64, 0, None) == HIP_ERROR_INVALID_VALUE
