@@ -132,3 +132,46 @@ def test_noalloc_under_graph_capture():
             assert torch.equal(out[name], ref[name]), (rep, name)
         st, _ = _call(L, lib, ins, g_raw, A, dt, scale, (1, 128, 2), noalloc=True)   # eager work between
         assert st == 0
+
+
+_FIRST_CALL_CAPTURED = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from tests.test_zz_no_alloc import _case, _call, _outs, _lib
+L, lib = _lib()
+shape = (1, 128, 2)
+ins, g_raw, A, dt, scale = _case(*shape, 13)
+torch.cuda.synchronize()
+out = _outs(*shape, g_raw.device)
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.stream(side):
+    with torch.cuda.graph(graph, stream=side):
+        # the entry point's first call in this process: its per-device set-up runs under capture
+        st, _ = _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc=True, out=out, sync=False)
+torch.cuda.current_stream().wait_stream(side)
+assert st == 0, st
+st_ref, ref = _call(L, lib, ins, g_raw, A, dt, scale, shape, noalloc=False)   # after the capture
+assert st_ref == 0
+for rep in range(2):
+    graph.replay()
+    torch.cuda.synchronize()
+    for name in ref:
+        assert torch.equal(out[name], ref[name]), (rep, name)
+print("first call under capture: ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """The entry point's per-device set-up (the symbol lookup and the kernels' LDS attribute)
+    on its first call in a fresh process, made while a HIP graph is being captured."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("\n[no-alloc] first call under capture (fresh process)", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED, root], capture_output=True, text=True,
+                       timeout=240, cwd=root)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "first call under capture: ok" in r.stdout
