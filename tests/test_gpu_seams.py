@@ -3,8 +3,8 @@
 * ``backends.state.chunk_gated_delta_rule_bwd_dhu`` (FLA's name; the reference's GDN2
   replacement ``kernels/vector_state_gpu.py:47-67``) against the fp64 oracle's
   ``stage_state_bwd`` for the vector gate (gk, gate-weighted q / k), the scalar gate (g, raw
-  q / k) and no gate, K-first and V-first states; with cu_seqlens against the same sequences
-  run one at a time as dense rows.
+  q / k) and no gate, K-first and V-first states; with cu_seqlens (a one-token and an empty
+  sequence among them) against the same sequences run one at a time as dense rows.
 * ``backends.wy.chunk_gdn2_bwd_wy_dqkg_fused`` (the reference's ``gdn2_consumer_fp32.residual``)
   composed with ``backends.intra.chunk_gdn2_bwd_intra`` and the in-chunk reverse cumsum of dg,
   as FLA's chunk_gdn2_bwd composes them, against the fused chunk kernel; and its own terms
@@ -65,7 +65,7 @@ def test_state_seam_matches_the_oracle(op, vf):
 
 def test_state_seam_packed_batch_matches_rows_one_at_a_time():
     from rewy_amd.backends.state import chunk_gated_delta_rule_bwd_dhu
-    lens = [100, 64, 230]
+    lens = [100, 0, 64, 1, 230]          # an empty sequence passes its state through
     cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
     Tt, H = int(cu[-1]), 2
     print(f"\n[seam state varlen] lens={lens}", flush=True)
@@ -92,6 +92,9 @@ def test_state_seam_packed_batch_matches_rows_one_at_a_time():
         a, b = int(cu[s]), int(cu[s + 1])
         nc = (n + 63) // 64
         pad = nc * 64 - n
+        if n == 0:
+            assert torch.equal(dh0[s].cpu(), dht[s]), s
+            continue
 
         def seq(x):
             y = x[:, a:b]
@@ -224,7 +227,7 @@ def _packed_and_padded(op, lens, H, seed):
 def test_wy_and_intra_seams_on_a_packed_batch(op):
     from rewy_amd.backends.intra import chunk_gdn2_bwd_intra, chunk_kda_bwd_intra
     from rewy_amd.backends.wy import chunk_gdn2_bwd_wy_dqkg_fused, chunk_kda_bwd_wy_dqkg_fused
-    lens, H = [150, 64, 37, 200], 2
+    lens, H = [150, 64, 0, 37, 1, 200], 2
     print(f"\n[seam varlen] op={op} lens={lens}", flush=True)
     d, scale, cu, pack, pack_chunks = _packed_and_padded(op, lens, H, 65)
     Bp, Tp = d["q"].shape[:2]
