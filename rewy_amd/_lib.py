@@ -135,4 +135,7 @@ def stream_handle(device):
     torch.cuda.current_stream(device), which tiny backwards pay four times per call."""
     import torch
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    return torch._C._cuda_getCurrentRawStream(idx)
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)     # torch's own fast path
+    if raw is None:
+        return torch.cuda.current_stream(idx).cuda_stream
+    return raw(idx)
