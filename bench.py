@@ -84,12 +84,14 @@ def folds_u(cfg):
             and bool(ops.paired_tile(cfg["B"], cfg["H"], cfg["T"] // 64, gate)))
 
 
-def kernel_costs(op, full_saving, inline=False, fold_u=False):
+def kernel_costs(op, full_saving, inline=False, fold_u=False, raw=False):
     """Algorithmic (bytes, FLOPs) per chunk-head of every kernel the backward launches:
     every operand read once, every result written once; dense GEMM flops.  ``inline``: the
     state recurrence forms Aqk itself (see ``inline_aqk``).  ``fold_u``: the paired
     recurrences' scan forms u itself (fdr_fwd_h_u), so prepare_wu neither reads v (nor GDN2's
-    write gate) nor writes u."""
+    write gate) nor writes u.  ``raw`` (with ``fold_u``, vector gates): both recurrences form
+    qg / kg from the raw q / k and the gate tile, so prepare_wu neither reads q nor writes qg /
+    kg, and each recurrence reads g."""
     vec, vb = op in ("kda", "gdn2"), op == "gdn2"
     g_b = 64 * 128 * 4 if vec else (64 * 4 if op == "gdn" else 0)
     gl_b = 128 * 4 if vec else (4 if op == "gdn" else 0)
@@ -118,6 +120,11 @@ def kernel_costs(op, full_saving, inline=False, fold_u=False):
         # the scan reads v (, w_gate | beta) and Akk in place of u, and forms u
         by, fl = costs["fdr_fwd_h"]
         costs["fdr_fwd_h_u"] = (by + (TILE if vb else 64 * 4) + AT, fl + mm(64, 128, 64))
+        if raw and vec:
+            by, fl = costs["fdr_prepare_wu"]
+            costs["fdr_prepare_wu"] = (by - 3 * TILE, fl)
+            costs["fdr_fwd_h_u"] = (costs["fdr_fwd_h_u"][0] + g_b, costs["fdr_fwd_h_u"][1])
+            costs["fdr_state_bwd"] = (costs["fdr_state_bwd"][0] + g_b, costs["fdr_state_bwd"][1])
     # folded gate backward: g_raw read besides g, dL/dg_raw (fp32) written in place of dg
     costs["fdr_chunk_bwd_gate_fold"] = (costs["fdr_chunk_bwd"][0] + g_b, costs["fdr_chunk_bwd"][1])
     # the affine-step launches compute the same recurrences: same operands and results
@@ -234,12 +241,13 @@ def setup(cfg, device):
         aqk = sv["Aqk"] if vec else None
     vb_pair = 0 if keep else ops.paired_tile(cfg["B"], cfg["H"], NT, gate)
     fold_u = bool(vb_pair) and ops.PAIRED_U
+    raw = fold_u and vec and ops.PAIRED_RAW
     if not keep and not fused:
         kern["fdr_prepare_wu"] = lambda: ops.prepare_wu(
             xs["k"], xs["v"], sv["Akk"], gate, g=g, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"), q=xs["q"],
-            want_qkg=vec, want_aqk=not vec and not inline, scale=scale, want_u=not fold_u)
+            want_qkg=vec and not raw, want_aqk=not vec and not inline, scale=scale, want_u=not fold_u)
         pre = kern["fdr_prepare_wu"]()
-        ks, qs, ws = (pre["kg"], pre["qg"], pre["w"]) if vec else (xs["k"], xs["q"], pre["w"])
+        ks, qs, ws = (pre["kg"], pre["qg"], pre["w"]) if vec and not raw else (xs["k"], xs["q"], pre["w"])
         aqk = sv["Aqk"] if vec else pre["Aqk"]
     if vb_pair:
         # batch x heads too small for one recurrence to fill the GPU: the state recurrence and
@@ -247,8 +255,8 @@ def setup(cfg, device):
         from rewy_amd.backends.backward import _side_by_side
         kern["paired_recurrences"] = lambda: _side_by_side(
             lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk, want_dh0=xs["h0"] is not None,
-                                  method="direct", value_block=vb_pair),
-            (lambda: ops.fwd_h_u(ks, ws, xs["v"], sv["Akk"], g, gate, beta=xs.get("beta"), w_gate=xs.get("w"),
+                                  method="direct", value_block=vb_pair, raw_qk=raw),
+            (lambda: ops.fwd_h_u(xs["k"], ws, xs["v"], sv["Akk"], g, gate, beta=xs.get("beta"), w_gate=xs.get("w"),
                                  h0=xs["h0"], value_block=vb_pair)) if fold_u else
             (lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"], method="direct", value_block=vb_pair)))
         (dh, dR, _), (h, v_new, _) = kern["paired_recurrences"]()
@@ -349,7 +357,8 @@ def measure(cfg, steps, warmup):
     ms = time_steps(step, steps, warmup, WARMUP_MIN_S, winfo)
     fwd_ms = time_steps(forward, max(3, steps // 4), 1)
     kt = time_kernels(kern, max(5, steps))
-    costs = kernel_costs(cfg["op"], cfg["full_saving"], inline_aqk(cfg), folds_u(cfg))
+    costs = kernel_costs(cfg["op"], cfg["full_saving"], inline_aqk(cfg), folds_u(cfg),
+                         folds_u(cfg) and ops.PAIRED_RAW)
     kernels = {}
     for n, t in kt.items():
         by, fl = costs[n]

@@ -82,6 +82,19 @@ hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, con
                                 int chunk, float scale, int value_block, hipStream_t stream);
 
 /*
+ * fdr_state_bwd for a vector gate with the raw q and k (qk_heads q / k heads, FLA's head map for
+ * grouped value heads): qg = q 2^g and kg = k 2^(g_last - g) are formed in-kernel as each chunk
+ * is staged, with fdr_prepare_wu's roundings, from the gate tile g (fp32 [B,T,H,K], log2-unit
+ * chunk-local cumsum), so dh, dR and dh0 are the bits of fdr_prepare_wu's qg / kg then
+ * fdr_state_bwd.  For the recompute policy's paired recurrences, where fdr_prepare_wu then
+ * writes w only.  Dv_local from aqk (fp32 [B,T,H,64]); dense rows only.
+ */
+hipError_t fdr_state_bwd_raw_qk(const void* q, const void* k, const void* w, const float* g, const void* dO,
+                                const float* aqk, const float* dht, void* dh, void* dr, float* dh0,
+                                int state_v_first, int B, int T, int H, int qk_heads, int K, int V, int chunk,
+                                float scale, int value_block, hipStream_t stream);
+
+/*
  * fdr_state_bwd for long rows and few heads, in three launches with a short sequential
  * part.  Each row's chunks are split into `segments` consecutive segments; the
  * recurrence is affine in the state, so a segment maps the state at its end X to the
@@ -235,8 +248,8 @@ hipError_t fdr_chunk_bwd_original(const void* q, const void* k, const void* v, c
  * (scalar / no gate) the intra-chunk scores Aqk = scale tril(q k^T 2^(g_i - g_s))
  * (fp32 [B,T,H,64]) that FLA chunk_bwd_dv_local forms (backward.py:119).
  * Scalar-beta families pass beta and null b_gate/w_gate; GDN2 passes b_gate/w_gate.
- * u = nullptr writes w (and qg, kg) only, for fdr_fwd_h_u, which forms u itself (vector gates
- * with qg / kg; scalar / no gates without Aqk); v and w_gate are then not read.
+ * u = nullptr writes w (and, vector gates, optionally qg, kg) only, for fdr_fwd_h_u, which
+ * forms u itself (no Aqk); v and w_gate are then not read.
  */
 hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const float* g,
                           int gate_mode, const float* beta, const void* b_gate, const void* w_gate,
@@ -278,9 +291,9 @@ hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const f
  * The forward scan of fdr_fwd_h with u formed in-kernel: FLA's recompute_w_u_fwd's u
  * (u = Akk (beta v), or Akk (w_gate v) for GDN2) folded into chunk_gated_delta_rule_fwd_h
  * (reference backends/backward.py:110-118), for the recompute policy's paired recurrences,
- * where fdr_prepare_wu (with u = nullptr) writes w (and qg, kg) but not u.  k is kg for a vector
- * gate (one row per value head), raw k otherwise (k_heads q/k heads); w as fdr_prepare_wu
- * writes it; v bf16 [B,T,H,V]; beta fp32 [B,T,H], or w_gate bf16 [B,T,H,V] (vector gate only);
+ * where fdr_prepare_wu (with u = nullptr) writes w but not u.  k is the raw k (k_heads q/k
+ * heads); a vector gate's kg = k 2^(g_last - g) is formed in-kernel with fdr_prepare_wu's
+ * rounding, as fdr_state_bwd_raw_qk forms it; w as fdr_prepare_wu writes it; v bf16 [B,T,H,V]; beta fp32 [B,T,H], or w_gate bf16 [B,T,H,V] (vector gate only);
  * Akk fp32 [B,T,H,64].  u is formed with fdr_prepare_wu's MFMA sequence and roundings, so h,
  * v_new and ht are the bits of fdr_prepare_wu + fdr_fwd_h.  value_block as for fdr_fwd_h.
  */

@@ -155,18 +155,25 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
         # width that gives each launch at most half the CUs
         vb = ops.paired_tile(N, H, NT, ops.GATE_VECTOR)
         fold_u = ops.PAIRED_U
-        pre = _prepare_vector(k, v, g, Akk, gates, q, vl, want_u=not fold_u)
+        raw = fold_u and ops.PAIRED_RAW
+        pre = _prepare_vector(k, v, g, Akk, gates, q, vl, want_u=not fold_u, want_qkg=not raw)
+
+        def state():
+            if raw:         # qg / kg formed as the state recurrence stages each chunk
+                return ops.state_bwd(q, k, pre["w"], g, ops.GATE_VECTOR, do, scale, aqk=Aqk, dht=_f32(dht),
+                                     want_dh0=initial_state is not None, value_block=vb, method="direct",
+                                     state_v_first=vf, raw_qk=True)
+            return _state_vector(pre, g, do, scale, Aqk, dht, initial_state, vl, vf, method="direct",
+                                 value_block=vb)
 
         def scan():
-            if fold_u:      # u formed inside the scan (prepare_wu wrote w, qg, kg only)
-                return ops.fwd_h_u(pre["kg"], pre["w"], v, Akk, g, ops.GATE_VECTOR, beta=_f32(gates.get("beta")),
+            if fold_u:      # u and kg formed inside the scan (prepare_wu wrote w and perhaps qg, kg)
+                return ops.fwd_h_u(k, pre["w"], v, Akk, g, ops.GATE_VECTOR, beta=_f32(gates.get("beta")),
                                    w_gate=None if gates.get("w") is None else _bf(gates["w"]),
                                    h0=_f32(initial_state), value_block=vb, state_v_first=vf)
             return ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
                              method="direct", value_block=vb, state_v_first=vf)
-        (dh, dR, dh0), (h, v_new, _) = _side_by_side(
-            lambda: _state_vector(pre, g, do, scale, Aqk, dht, initial_state, vl, vf, method="direct",
-                                  value_block=vb), scan)
+        (dh, dR, dh0), (h, v_new, _) = _side_by_side(state, scan)
         saved, hvf = dict(v_new=v_new, h=h), False
     elif recompute and (ops.side_by_side_pays(N, H, NT) if vl is None else
                         ops.SIDE_BY_SIDE and not ops.fwd_h_wy_pays(N, H, ops.GATE_VECTOR, vl)):
@@ -197,11 +204,11 @@ def _state_vector(saved, g, do, scale, Aqk, dht, initial_state, vl=None, vf=Fals
                          method=method if vl is None else "direct", varlen=vl, state_v_first=vf)
 
 
-def _prepare_vector(k, v, g, Akk, gates, q, vl=None, want_u=True):
+def _prepare_vector(k, v, g, Akk, gates, q, vl=None, want_u=True, want_qkg=True):
     b = None if gates.get("b") is None else _bf(gates["b"])
     w = None if gates.get("w") is None else _bf(gates["w"])
     return ops.prepare_wu(k, v, Akk, ops.GATE_VECTOR, g=g, beta=_f32(gates.get("beta")), b=b, w=w, q=q,
-                          want_qkg=True, varlen=vl, want_u=want_u)
+                          want_qkg=want_qkg, varlen=vl, want_u=want_u)
 
 
 def _recompute_vector(q, k, v, g, Akk, initial_state, gates, vl=None, vf=False):

@@ -515,8 +515,8 @@ struct FwdWySmem {
 };
 
 // WG (fdr_fwd_h_u): w is given (w_in, as fdr_prepare_wu wrote it) and only u is formed here;
-// k is then kg for a vector gate (as fdr_fwd_h takes it), raw k otherwise, and nothing but h,
-// v_new (and the final state) is written.
+// k is the raw k (a vector gate's kg = k 2^(g_last - g) formed here, rounded as
+// prepare_wu_kernel rounds it), and nothing but h, v_new (and the final state) is written.
 template <int BV, int GATE, bool VEC_B, bool MAP, bool WG = false>
 __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
@@ -588,19 +588,20 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     } else if constexpr (VEC) {
       // lambda's column (tid < KD), and g_last of this thread's 8 columns (both pieces)
       rg_last = g[kofs + (size_t)rs_.clamp(C - 1) * rsk + (tid & (KD - 1))];
-      if constexpr (!WG) {
-        const float* gl = g + kofs + (size_t)rs_.clamp(C - 1) * rsk + 8 * (tid & 15);
-        rgl0 = *reinterpret_cast<const f32x4*>(gl);
-        rgl1 = *reinterpret_cast<const f32x4*>(gl + 4);
-      }
+      const float* gl = g + kofs + (size_t)rs_.clamp(C - 1) * rsk + 8 * (tid & 15);
+      rgl0 = *reinterpret_cast<const f32x4*>(gl);
+      rgl1 = *reinterpret_cast<const f32x4*>(gl + 4);
     }
-    // (WG with a vector gate: k is kg, one row per value head)
-    const QKRows kr_ = (WG && VEC) ? QKRows{kofs, rsk} : qk_rows(tok0, h, H, HQ);
+    const QKRows kr_ = qk_rows(tok0, h, H, HQ);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i, t = p >> 4, c8 = 8 * (p & 15);
       if constexpr (WG) {
         rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(w_in + kofs + (size_t)t * rsk + c8, t));   // w rows
+        if constexpr (VEC) {
+          rg0[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8);
+          rg1[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8 + 4);
+        }
       } else {
         if constexpr (VEC) {
           rg0[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8);
@@ -637,9 +638,18 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       const bf16x8 kx = __builtin_bit_cast(bf16x8, rk[i]);
       bf16x8 eh, kg;
       if constexpr (WG) {
-        // w and kg as given (the scalar gate's kg formed as fdr_fwd_h forms it); no E
+        // w as given, kg formed (the scalar gate's as fdr_fwd_h forms it); no E
         *reinterpret_cast<u32x4*>(&sm.w[pb][t][8 * ch]) = rq[i];
-        kg = GATE == RG_SCALAR ? __builtin_bit_cast(bf16x8, scale_bf16x8(rk[i], fast_exp2(rg_last - rg_tok[i]))) : kx;
+        if constexpr (VEC) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float gj = j < 4 ? rg0[i][j] : rg1[i][j - 4];
+            const float glj = j < 4 ? rgl0[j] : rgl1[j - 4];
+            kg[j] = to_bf16(to_f32(kx[j]) * fast_exp2(glj - gj));
+          }
+        } else {
+          kg = GATE == RG_SCALAR ? __builtin_bit_cast(bf16x8, scale_bf16x8(rk[i], fast_exp2(rg_last - rg_tok[i]))) : kx;
+        }
       } else if constexpr (VEC) {
         const bf16x8 qx = __builtin_bit_cast(bf16x8, rq[i]);
         bf16x8 bx = {};
@@ -927,15 +937,18 @@ static hipError_t prepare_dispatch(const void* q, const void* k, const void* v, 
   if (want_aqk && (!q || gate_mode == RG_VECTOR)) return hipErrorInvalidValue;
 #define P_ARGS q, k, v, g, beta, b_gate, w_gate, Akk, w, u, qg, kg, Aqk, B, T, H, HQ, scale, stream, cu, ci
   if (!u) {
-    // w (and qg, kg) only, for the forward scan that forms u itself (fdr_fwd_h_u): vector gates
-    // with qg / kg, or scalar / no gates without Aqk
-    if (want_aqk || (gate_mode == RG_VECTOR) != want_qkg) return hipErrorInvalidValue;
+    // w (and, vector gates, optionally qg, kg) only, for the forward scan that forms u itself
+    // (fdr_fwd_h_u); no Aqk
+    if (want_aqk) return hipErrorInvalidValue;
     switch (gate_mode) {
       case RG_NONE: return launch_prepare<RG_NONE, false, false, false, false>(P_ARGS);
       case RG_SCALAR: return launch_prepare<RG_SCALAR, false, false, false, false>(P_ARGS);
       case RG_VECTOR:
-        return vec_b ? launch_prepare<RG_VECTOR, true, true, false, false>(P_ARGS)
-                     : launch_prepare<RG_VECTOR, false, true, false, false>(P_ARGS);
+        if (vec_b)
+          return want_qkg ? launch_prepare<RG_VECTOR, true, true, false, false>(P_ARGS)
+                          : launch_prepare<RG_VECTOR, true, false, false, false>(P_ARGS);
+        return want_qkg ? launch_prepare<RG_VECTOR, false, true, false, false>(P_ARGS)
+                        : launch_prepare<RG_VECTOR, false, false, false, false>(P_ARGS);
       default: return hipErrorInvalidValue;
     }
   }
@@ -1095,7 +1108,6 @@ static hipError_t fwd_h_u_dispatch(const void* k, const void* w, const void* v, 
   const bool vec_b = w_gate != nullptr;
   if (vec_b && gate_mode != RG_VECTOR) return hipErrorInvalidValue;
   if (!vec_b && !beta) return hipErrorInvalidValue;
-  if (gate_mode == RG_VECTOR && HQ != H) return hipErrorInvalidValue;   // k is kg, per value head
   if (gate_mode != RG_NONE && !g) return hipErrorInvalidValue;
   if (cu && !co) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : fwd_default_bv(B, H);

@@ -60,7 +60,10 @@ struct StateSmem {
 // Segmented form (segs > 0): row r of T tokens is split into `segs` segments of
 // consecutive chunks, work-group row b is segment b % segs of row b / segs, and dht holds
 // each segment's end state (from state_combine_kernel).
-template <int BV, int GATE, bool DV_FROM_AQK, int NW, bool MAP = false, bool INL = false>
+// RAWQK (vector gate, dense rows): q and k are the raw ones (q/k heads HQ), and qg = q 2^g,
+// kg = k 2^(g_last - g) are formed while the chunk is staged, with fdr_prepare_wu's roundings,
+// from the gate tile the chunk loads beside them, so no qg / kg need be written for this pass.
+template <int BV, int GATE, bool DV_FROM_AQK, int NW, bool MAP = false, bool INL = false, bool RAWQK = false>
 __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ w,
     const float* __restrict__ g, const bf16* __restrict__ dO, const float* __restrict__ aqk,
@@ -68,6 +71,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     bf16* __restrict__ dr_out, float* __restrict__ dh0, int T, int H, float scale,
     const int* __restrict__ chunk_off, int segs, int vf, int HQ, const int* __restrict__ cu) {
   static_assert(!INL || (DV_FROM_AQK && GATE != GATE_VECTOR), "in-kernel Aqk: scalar / no gate");
+  static_assert(!RAWQK || (GATE == GATE_VECTOR && !INL && !MAP), "raw q / k: the vector gate, dense rows");
   using S = StateSmem<BV, GATE, DV_FROM_AQK, INL>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
@@ -133,6 +137,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   f32x4 ra[NPI];
   float rg_last = 0.f, rg_tok[NPI];             // scalar gate: last row, the rows this thread stages
   float rg_do[NDO];                             // INL, scalar gate: the gate of each dO piece's row
+  f32x4 rgp0[NPI], rgp1[NPI], rgl0, rgl1;       // RAWQK: each piece's 8 gates, g_last of its 8 columns
   const size_t row_stride_k = (size_t)H * KD;   // elements between tokens
   const size_t row_stride_v = (size_t)H * VD;
 
@@ -148,8 +153,21 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       rg_last = g[(tok0 + rs_.clamp(C - 1)) * H + h];
     }
     const size_t kofs = tok0 * row_stride_k + (size_t)h * KD;
-    // q / k: raw (HQ heads, grouped value heads) for scalar / no gates, qg / kg (HQ = H) else
+    // q / k: raw (HQ heads, grouped value heads) for scalar / no gates and RAWQK, qg / kg
+    // (HQ = H) else
     const QKRows qr = qk_rows(tok0, h, H, HQ);
+    if constexpr (RAWQK) {
+      const float* gl = g + kofs + (size_t)rs_.clamp(C - 1) * row_stride_k + 8 * (tid & 15);
+      rgl0 = *reinterpret_cast<const f32x4*>(gl);
+      rgl1 = *reinterpret_cast<const f32x4*>(gl + 4);
+#pragma unroll
+      for (int i = 0; i < NPI; ++i) {
+        const int p = tid + NTH * i;
+        const float* gp = g + kofs + (size_t)rs_.clamp(p >> 4) * row_stride_k + (p & 15) * 8;
+        rgp0[i] = *reinterpret_cast<const f32x4*>(gp);
+        rgp1[i] = *reinterpret_cast<const f32x4*>(gp + 4);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NPI; ++i) {
       const int p = tid + NTH * i;
@@ -185,6 +203,20 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       const int p = tid + NTH * i;
       const int t = p >> 4, ch = p & 15;
       u32x4 kq = rk[i], qq = rq[i];
+      if constexpr (RAWQK) {
+        // qg = q 2^g, kg = k 2^(g_last - g), rounded as fdr_prepare_wu rounds them
+        const bf16x8 kx = __builtin_bit_cast(bf16x8, rk[i]), qx = __builtin_bit_cast(bf16x8, rq[i]);
+        bf16x8 ko, qo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float gj = j < 4 ? rgp0[i][j] : rgp1[i][j - 4];
+          const float glj = j < 4 ? rgl0[j] : rgl1[j - 4];
+          qo[j] = to_bf16(to_f32(qx[j]) * fast_exp2(gj));
+          ko[j] = to_bf16(to_f32(kx[j]) * fast_exp2(glj - gj));
+        }
+        kq = __builtin_bit_cast(u32x4, ko);
+        qq = __builtin_bit_cast(u32x4, qo);
+      }
       if constexpr (GATE == GATE_SCALAR) {
         // scalar gate: kg = k 2^(g_last - g_t), qg = q 2^(g_t), the row's factors from registers
         kq = scale_bf16x8(kq, fast_exp2(rg_last - rg_tok[i]));
@@ -494,7 +526,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
 template <int BV>
 constexpr int state_waves() { return BV == 32 ? 16 : 8; }
 
-template <int BV, int GATE, bool AQK, bool INL = false>
+template <int BV, int GATE, bool AQK, bool INL = false, bool RAWQK = false>
 static hipError_t launch_state(const void* q, const void* k, const void* w, const float* g,
                                const void* dO, const float* aqk, const void* dv, const float* dht,
                                void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
@@ -504,22 +536,24 @@ static hipError_t launch_state(const void* q, const void* k, const void* w, cons
   const int grid = rows * H * (VD / BV);
   constexpr int NW = state_waves<BV>();
 #define S_LAUNCH(MAP)                                                                                        \
-  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW, MAP, INL>), dim3(grid), dim3(64 * NW), 0, stream,   \
+  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW, MAP, INL, RAWQK>), dim3(grid), dim3(64 * NW), 0, stream, \
                      (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk, (const bf16*)dv, \
                      dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale, chunk_off, segs, vf, HQ > 0 ? HQ : H, cu)
-  if (cu) S_LAUNCH(true);
+  if constexpr (RAWQK) S_LAUNCH(false);     // (dense rows only)
+  else if (cu) S_LAUNCH(true);
   else S_LAUNCH(false);
 #undef S_LAUNCH
   return hipGetLastError();
 }
 
-template <int GATE, bool AQK, bool INL = false>
+template <int GATE, bool AQK, bool INL = false, bool RAWQK = false>
 static hipError_t pick_bv(int bv, const void* q, const void* k, const void* w, const float* g,
                           const void* dO, const float* aqk, const void* dv, const float* dht,
                           void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
                           hipStream_t s, const int* co, int vf, int HQ, const int* cu) {
 #define S_BV(BV) \
-  launch_state<BV, GATE, AQK, INL>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, HQ, cu)
+  launch_state<BV, GATE, AQK, INL, RAWQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, \
+                                          HQ, cu)
   switch (bv) {
     case 16: return S_BV(16);
     case 32: return S_BV(32);
@@ -878,6 +912,19 @@ extern "C" hipError_t fdr_state_bwd(const void* q, const void* k, const void* w,
                                     int value_block, hipStream_t stream) {
   return state_dispatch(q, k, w, g, gate_mode, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, K, V, chunk, scale,
                         value_block, stream, nullptr, state_v_first ? 1 : 0, qk_heads);
+}
+
+extern "C" hipError_t fdr_state_bwd_raw_qk(const void* q, const void* k, const void* w, const float* g,
+                                           const void* dO, const float* aqk, const float* dht, void* dh, void* dr,
+                                           float* dh0, int state_v_first, int B, int T, int H, int qk_heads, int K,
+                                           int V, int chunk, float scale, int value_block, hipStream_t stream) {
+  if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
+  if (!q || !k || !w || !g || !dO || !aqk || !dh || !dr) return hipErrorInvalidValue;
+  const int HQ = qk_heads > 0 ? qk_heads : H;
+  if (H % HQ) return hipErrorInvalidValue;
+  const int bv = value_block > 0 ? value_block : default_bv(B, H);
+  return pick_bv<GATE_VECTOR, true, false, true>(bv, q, k, w, g, dO, aqk, nullptr, dht, dh, dr, dh0, B, T, H, scale,
+                                                stream, nullptr, state_v_first ? 1 : 0, HQ, nullptr);
 }
 
 extern "C" hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, const float* g,

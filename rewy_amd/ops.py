@@ -95,6 +95,9 @@ PAIRED = True
 PAIRED_MIN_BH = 24
 # ... with u formed inside the scan (fwd_h_u) instead of written by prepare_wu and read back
 PAIRED_U = True
+# ... and, vector gates, with qg / kg formed from the raw q / k where each recurrence stages a
+# chunk (fdr_state_bwd_raw_qk, fwd_h_u) instead of written by prepare_wu and read back
+PAIRED_RAW = True
 
 
 def paired_tile(B, H, NT, gate_mode):
@@ -240,7 +243,8 @@ def _dims(q):
 
 
 def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, want_dh0=True,
-              value_block=0, method="auto", chunk_offsets=None, segments=0, state_v_first=False, varlen=None):
+              value_block=0, method="auto", chunk_offsets=None, segments=0, state_v_first=False, varlen=None,
+              raw_qk=False):
     """Reverse state recurrence.  Returns (dh [B,NT,H,K,V] bf16, dR [B,T,H,V] bf16, dh0 fp32|None).
 
     dv_local = Aqk^T dO comes from ``aqk``, or is given as ``dv``; with neither (scalar / no
@@ -258,7 +262,11 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
     (fdr_affine_*), faster when B*H is too small to fill the GPU; "segmented": every row
     split into ``segments`` (0: ``segments_for``) whose affine maps are formed in parallel,
     chained, and each segment rerun from its end state (fdr_state_bwd_segmented), for long
-    rows and few heads; "auto" picks."""
+    rows and few heads; "auto" picks.
+
+    ``raw_qk`` (vector gate, ``aqk``, dense rows, direct form): q and k are the raw ones and
+    qg = q 2^g, kg = k 2^(g_last - g) are formed in-kernel with ``prepare_wu``'s roundings
+    (fdr_state_bwd_raw_qk), so the result is the bits of ``prepare_wu``'s qg / kg then this."""
     B, T, HQ, K = _rows(q, varlen)
     H, HQ = _group(w.shape[2] if w is not None and w.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
@@ -299,6 +307,14 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
     dr = torch.empty(B, T, H, V, device=dev, dtype=bf)
     dh0 = torch.empty(N, H, K, V, device=dev, dtype=f32) if want_dh0 else None
     P = _lib.ptr
+    if raw_qk:
+        if gate_mode != GATE_VECTOR or aqk is None or co is not None or method not in ("auto", "direct"):
+            raise ValueError("raw_qk takes a vector gate, aqk, dense rows and the direct form")
+        st = _lib.load().fdr_state_bwd_raw_qk(P(q), P(k), P(w), P(g), P(dO), P(aqk), P(dht), P(dh), P(dr), P(dh0),
+                                              vf, B, T, H, HQ, K, V, CHUNK, float(scale), int(value_block),
+                                              _lib.stream_handle(dev))
+        _lib.check(st, "fdr_state_bwd_raw_qk")
+        return dh, dr, dh0
     if co is not None:
         if method == "affine":
             raise ValueError("the affine-step form takes equal-length rows, not chunk_offsets")
@@ -632,8 +648,8 @@ def _chunk_bwd_gate_fold(q, k, v, v_new, dO, dR, g, gate_mode, Akk, h, dh, scale
 def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, want_qkg=False,
                want_aqk=False, scale=1.0, varlen=None, want_u=True):
     """WY factors (and qg/kg or Aqk) of every chunk.  Returns dict(w, u, qg, kg, Aqk).
-    ``varlen``: a packed variable-length batch (``Varlen``).  ``want_u=False``: w (and qg, kg)
-    only, for ``fwd_h_u`` (u None; v and the write gate are not read)."""
+    ``varlen``: a packed variable-length batch (``Varlen``).  ``want_u=False``: w (and, vector
+    gates, optionally qg, kg) only, for ``fwd_h_u`` (u None; v and the write gate are not read)."""
     B, T, HQ, K = _rows(k, varlen)
     H, HQ = _group(v.shape[2] if v is not None and v.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
@@ -660,8 +676,8 @@ def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, 
         raise ValueError("qg/kg need q and a vector gate")
     if want_aqk and (q is None or gate_mode == GATE_VECTOR):
         raise ValueError("Aqk is produced here for scalar / no-gate families only")
-    if not want_u and (want_aqk or want_qkg != (gate_mode == GATE_VECTOR) or varlen is not None):
-        raise ValueError("want_u=False takes qg / kg for a vector gate, no Aqk, dense rows")
+    if not want_u and (want_aqk or varlen is not None):
+        raise ValueError("want_u=False takes no Aqk and dense rows")
     out = dict(w=torch.empty(B, T, H, K, device=dev, dtype=bf),
                u=torch.empty(B, T, H, V, device=dev, dtype=bf) if want_u else None,
                qg=torch.empty(B, T, H, K, device=dev, dtype=bf) if want_qkg else None,
@@ -765,7 +781,8 @@ def fwd_h_u(k, w, v, Akk, g, gate_mode, beta=None, w_gate=None, h0=None, want_fi
             state_v_first=False):
     """``fwd_h`` with u formed in-kernel (fdr_fwd_h_u): u = Akk (beta v), or Akk (w_gate v) for
     GDN2, from the same MFMA sequence as ``prepare_wu``, so h, v_new and the final state are
-    the bits of ``prepare_wu`` + ``fwd_h``.  k is kg for a vector gate, raw k otherwise; w as
+    the bits of ``prepare_wu`` + ``fwd_h``.  k is the raw k (a vector gate's kg formed in-kernel
+    with ``prepare_wu``'s rounding); w as
     ``prepare_wu(..., want_u=False)`` returns it.  Returns (h, v_new, final|None)."""
     B, T, HQ, K = _dims(k)
     H, HQ = _group(w.shape[2] if w is not None and w.ndim == 4 else HQ, HQ)
@@ -777,8 +794,6 @@ def fwd_h_u(k, w, v, Akk, g, gate_mode, beta=None, w_gate=None, h0=None, want_fi
     _need(v, "v", bf, (B, T, H, V), dev)
     _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
     if gate_mode == GATE_VECTOR:
-        if HQ != H:
-            raise ValueError("a vector gate's kg has one row per value head")
         _need(g, "g", f32, (B, T, H, K), dev)
     elif gate_mode == GATE_SCALAR:
         _need(g, "g", f32, (B, T, H), dev)

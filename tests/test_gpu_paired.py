@@ -6,8 +6,10 @@ scalar / no-gate ones with the state recurrence forming Aqk itself):
 
 * the public autograd backward (recompute policy) against the fp64 oracle at the
   reference's acceptance tolerances (validation.py:40-45, :68);
-* the same gradients, bit for bit, as the same launches enqueued on one stream, and as the
-  scan reading a u that prepare_wu wrote (``ops.PAIRED_U`` off: the scan forms u itself);
+* the same gradients, bit for bit, as the same launches enqueued on one stream, as the two
+  recurrences reading the qg / kg that prepare_wu wrote (``ops.PAIRED_RAW`` off: they form
+  them from the raw q / k), and as the scan reading a u that prepare_wu wrote
+  (``ops.PAIRED_U`` off: the scan forms u itself);
 * against the policy switched off (the pair one after the other at the default tile
   width): rel-L2 <= 1e-5, the tile width changing no arithmetic of a value column;
 * captured in a HIP graph and replayed three times with eager work between the replays.
@@ -100,6 +102,14 @@ def test_paired_equals_one_stream_and_policy_off(op, B, T, H, vb, monkeypatch):
     torch.cuda.synchronize()
     for i, (a, r) in enumerate(zip(got, one)):
         assert torch.equal(a, r), (op, i)
+    monkeypatch.undo()
+    # vector gates: qg / kg written by prepare_wu and read back instead of formed in the two
+    # recurrences: the same bits
+    monkeypatch.setattr(ops, "PAIRED_RAW", False)
+    written = run()
+    torch.cuda.synchronize()
+    for i, (a, r) in enumerate(zip(got, written)):
+        assert torch.equal(a, r), (op, "PAIRED_RAW", i)
     monkeypatch.undo()
     # u written by prepare_wu and read by fdr_fwd_h instead of formed in the scan: the same bits
     monkeypatch.setattr(ops, "PAIRED_U", False)
