@@ -84,14 +84,15 @@ def folds_u(cfg):
             and bool(ops.paired_tile(cfg["B"], cfg["H"], cfg["T"] // 64, gate)))
 
 
-def kernel_costs(op, full_saving, inline=False, fold_u=False, raw=False):
+def kernel_costs(op, full_saving, inline=False, fold_u=False, raw=False, formw=False):
     """Algorithmic (bytes, FLOPs) per chunk-head of every kernel the backward launches:
     every operand read once, every result written once; dense GEMM flops.  ``inline``: the
     state recurrence forms Aqk itself (see ``inline_aqk``).  ``fold_u``: the paired
     recurrences' scan forms u itself (fdr_fwd_h_u), so prepare_wu neither reads v (nor GDN2's
     write gate) nor writes u.  ``raw`` (with ``fold_u``, vector gates): both recurrences form
     qg / kg from the raw q / k and the gate tile, so prepare_wu neither reads q nor writes qg /
-    kg, and each recurrence reads g."""
+    kg, and each recurrence reads g.  ``formw`` (with ``raw``): both recurrences form w too
+    (reading Akk and beta | b in place of w), and prepare_wu does not run."""
     vec, vb = op in ("kda", "gdn2"), op == "gdn2"
     g_b = 64 * 128 * 4 if vec else (64 * 4 if op == "gdn" else 0)
     gl_b = 128 * 4 if vec else (4 if op == "gdn" else 0)
@@ -125,6 +126,11 @@ def kernel_costs(op, full_saving, inline=False, fold_u=False, raw=False):
             costs["fdr_prepare_wu"] = (by - 3 * TILE, fl)
             costs["fdr_fwd_h_u"] = (costs["fdr_fwd_h_u"][0] + g_b, costs["fdr_fwd_h_u"][1])
             costs["fdr_state_bwd"] = (costs["fdr_state_bwd"][0] + g_b, costs["fdr_state_bwd"][1])
+            if formw:
+                del costs["fdr_prepare_wu"]
+                wb = AT + (TILE if vb else 64 * 4) - TILE       # Akk, b | beta in place of w
+                for n in ("fdr_fwd_h_u", "fdr_state_bwd"):
+                    costs[n] = (costs[n][0] + wb, costs[n][1] + mm(64, 128, 64))
     # folded gate backward: g_raw read besides g, dL/dg_raw (fp32) written in place of dg
     costs["fdr_chunk_bwd_gate_fold"] = (costs["fdr_chunk_bwd"][0] + g_b, costs["fdr_chunk_bwd"][1])
     # the affine-step launches compute the same recurrences: same operands and results
@@ -242,7 +248,11 @@ def setup(cfg, device):
     vb_pair = 0 if keep else ops.paired_tile(cfg["B"], cfg["H"], NT, gate)
     fold_u = bool(vb_pair) and ops.PAIRED_U
     raw = fold_u and vec and ops.PAIRED_RAW
-    if not keep and not fused:
+    formw = raw and ops.PAIRED_FORMW and cfg["op"] == "gdn2" and vb_pair == 64
+    if formw:
+        # (the paired recurrences form w, qg, kg and u themselves: no prepare_wu)
+        ks, qs, ws, aqk = xs["k"], xs["q"], None, sv["Aqk"]
+    elif not keep and not fused:
         kern["fdr_prepare_wu"] = lambda: ops.prepare_wu(
             xs["k"], xs["v"], sv["Akk"], gate, g=g, beta=xs.get("beta"), b=xs.get("b"), w=xs.get("w"), q=xs["q"],
             want_qkg=vec and not raw, want_aqk=not vec and not inline, scale=scale, want_u=not fold_u)
@@ -255,8 +265,10 @@ def setup(cfg, device):
         from rewy_amd.backends.backward import _side_by_side
         kern["paired_recurrences"] = lambda: _side_by_side(
             lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk, want_dh0=xs["h0"] is not None,
-                                  method="direct", value_block=vb_pair, raw_qk=raw),
+                                  method="direct", value_block=vb_pair, raw_qk=raw,
+                                  **(dict(beta=xs.get("beta"), b=xs.get("b"), Akk=sv["Akk"]) if formw else {})),
             (lambda: ops.fwd_h_u(xs["k"], ws, xs["v"], sv["Akk"], g, gate, beta=xs.get("beta"), w_gate=xs.get("w"),
+                                 b=xs.get("b"),
                                  h0=xs["h0"], value_block=vb_pair)) if fold_u else
             (lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"], method="direct", value_block=vb_pair)))
         (dh, dR, _), (h, v_new, _) = kern["paired_recurrences"]()
@@ -357,8 +369,10 @@ def measure(cfg, steps, warmup):
     ms = time_steps(step, steps, warmup, WARMUP_MIN_S, winfo)
     fwd_ms = time_steps(forward, max(3, steps // 4), 1)
     kt = time_kernels(kern, max(5, steps))
-    costs = kernel_costs(cfg["op"], cfg["full_saving"], inline_aqk(cfg), folds_u(cfg),
-                         folds_u(cfg) and ops.PAIRED_RAW)
+    raw = folds_u(cfg) and ops.PAIRED_RAW
+    costs = kernel_costs(cfg["op"], cfg["full_saving"], inline_aqk(cfg), folds_u(cfg), raw,
+                         raw and ops.PAIRED_FORMW and cfg["op"] == "gdn2"
+                         and ops.paired_tile(cfg["B"], cfg["H"], cfg["T"] // 64, ops.GATE_VECTOR) == 64)
     kernels = {}
     for n, t in kt.items():
         by, fl = costs[n]

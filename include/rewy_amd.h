@@ -86,13 +86,18 @@ hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, con
  * grouped value heads): qg = q 2^g and kg = k 2^(g_last - g) are formed in-kernel as each chunk
  * is staged, with fdr_prepare_wu's roundings, from the gate tile g (fp32 [B,T,H,K], log2-unit
  * chunk-local cumsum), so dh, dR and dh0 are the bits of fdr_prepare_wu's qg / kg then
- * fdr_state_bwd.  For the recompute policy's paired recurrences, where fdr_prepare_wu then
- * writes w only.  Dv_local from aqk (fp32 [B,T,H,64]); dense rows only.
+ * fdr_state_bwd.  w as fdr_prepare_wu writes it, or NULL: then w = Akk (b k 2^g) is formed
+ * in-kernel too, with fdr_prepare_wu's MFMA sequence and roundings, from Akk (fp32 [B,T,H,64])
+ * and beta (fp32 [B,T,H], KDA) or b_gate (bf16 [B,T,H,K], GDN2; qk_heads = H) -- exactly one of
+ * the two; both are ignored when w is given.  For the recompute policy's paired recurrences,
+ * where fdr_prepare_wu then need not run at all.  Dv_local from aqk (fp32 [B,T,H,64]); dense
+ * rows only.
  */
-hipError_t fdr_state_bwd_raw_qk(const void* q, const void* k, const void* w, const float* g, const void* dO,
-                                const float* aqk, const float* dht, void* dh, void* dr, float* dh0,
-                                int state_v_first, int B, int T, int H, int qk_heads, int K, int V, int chunk,
-                                float scale, int value_block, hipStream_t stream);
+hipError_t fdr_state_bwd_raw_qk(const void* q, const void* k, const void* w, const float* g, const float* beta,
+                                const void* b_gate, const float* Akk, const void* dO, const float* aqk,
+                                const float* dht, void* dh, void* dr, float* dh0, int state_v_first, int B, int T,
+                                int H, int qk_heads, int K, int V, int chunk, float scale, int value_block,
+                                hipStream_t stream);
 
 /*
  * fdr_state_bwd for long rows and few heads, in three launches with a short sequential
@@ -293,14 +298,17 @@ hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const f
  * (reference backends/backward.py:110-118), for the recompute policy's paired recurrences,
  * where fdr_prepare_wu (with u = nullptr) writes w but not u.  k is the raw k (k_heads q/k
  * heads); a vector gate's kg = k 2^(g_last - g) is formed in-kernel with fdr_prepare_wu's
- * rounding, as fdr_state_bwd_raw_qk forms it; w as fdr_prepare_wu writes it; v bf16 [B,T,H,V]; beta fp32 [B,T,H], or w_gate bf16 [B,T,H,V] (vector gate only);
+ * rounding, as fdr_state_bwd_raw_qk forms it; w as fdr_prepare_wu writes it, or NULL: then
+ * w = Akk (beta k 2^g | b_gate k 2^g) is formed in-kernel too, with fdr_prepare_wu's MFMA
+ * sequence and roundings (b_gate bf16 [B,T,H,K], GDN2 with k_heads = H; it is read only
+ * then), and fdr_prepare_wu need not run at all; v bf16 [B,T,H,V]; beta fp32 [B,T,H], or w_gate bf16 [B,T,H,V] (vector gate only);
  * Akk fp32 [B,T,H,64].  u is formed with fdr_prepare_wu's MFMA sequence and roundings, so h,
  * v_new and ht are the bits of fdr_prepare_wu + fdr_fwd_h.  value_block as for fdr_fwd_h.
  */
 hipError_t fdr_fwd_h_u(const void* k, const void* w, const void* v, const float* g, int gate_mode,
-                       const float* beta, const void* w_gate, const float* Akk, const float* h0, void* h,
-                       void* v_new, float* ht, int state_v_first, int B, int T, int H, int k_heads, int K, int V,
-                       int chunk, int value_block, hipStream_t stream);
+                       const float* beta, const void* b_gate, const void* w_gate, const float* Akk, const float* h0,
+                       void* h, void* v_new, float* ht, int state_v_first, int B, int T, int H, int k_heads, int K,
+                       int V, int chunk, int value_block, hipStream_t stream);
 
 /*
  * The recompute pair fdr_prepare_wu + fdr_fwd_h in one sweep.  Replaces FLA

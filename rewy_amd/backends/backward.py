@@ -156,20 +156,25 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
         vb = ops.paired_tile(N, H, NT, ops.GATE_VECTOR)
         fold_u = ops.PAIRED_U
         raw = fold_u and ops.PAIRED_RAW
-        pre = _prepare_vector(k, v, g, Akk, gates, q, vl, want_u=not fold_u, want_qkg=not raw)
+        formw = raw and ops.PAIRED_FORMW and gates.get("b") is not None and vb == 64
+        bgate = None if gates.get("b") is None else _bf(gates["b"])
+        # (formw: w formed in both recurrences as well, so no prepare_wu at all)
+        pre = (dict(w=None) if formw else
+               _prepare_vector(k, v, g, Akk, gates, q, vl, want_u=not fold_u, want_qkg=not raw))
 
         def state():
-            if raw:         # qg / kg formed as the state recurrence stages each chunk
+            if raw:         # qg / kg (and w) formed as the state recurrence stages each chunk
                 return ops.state_bwd(q, k, pre["w"], g, ops.GATE_VECTOR, do, scale, aqk=Aqk, dht=_f32(dht),
                                      want_dh0=initial_state is not None, value_block=vb, method="direct",
-                                     state_v_first=vf, raw_qk=True)
+                                     state_v_first=vf, raw_qk=True, beta=_f32(gates.get("beta")), b=bgate,
+                                     Akk=Akk)
             return _state_vector(pre, g, do, scale, Aqk, dht, initial_state, vl, vf, method="direct",
                                  value_block=vb)
 
         def scan():
-            if fold_u:      # u and kg formed inside the scan (prepare_wu wrote w and perhaps qg, kg)
+            if fold_u:      # u and kg (and w) formed inside the scan
                 return ops.fwd_h_u(k, pre["w"], v, Akk, g, ops.GATE_VECTOR, beta=_f32(gates.get("beta")),
-                                   w_gate=None if gates.get("w") is None else _bf(gates["w"]),
+                                   w_gate=None if gates.get("w") is None else _bf(gates["w"]), b=bgate,
                                    h0=_f32(initial_state), value_block=vb, state_v_first=vf)
             return ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
                              method="direct", value_block=vb, state_v_first=vf)

@@ -517,7 +517,9 @@ struct FwdWySmem {
 // WG (fdr_fwd_h_u): w is given (w_in, as fdr_prepare_wu wrote it) and only u is formed here;
 // k is the raw k (a vector gate's kg = k 2^(g_last - g) formed here, rounded as
 // prepare_wu_kernel rounds it), and nothing but h, v_new (and the final state) is written.
-template <int BV, int GATE, bool VEC_B, bool MAP, bool WG = false>
+// NOST (fdr_fwd_h_u with w NULL): w, u and kg all formed here, and again only h, v_new (and
+// the final state) written: no q read, no w / qg / kg stored.
+template <int BV, int GATE, bool VEC_B, bool MAP, bool WG = false, bool NOST = false>
 __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
@@ -526,6 +528,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     bf16* __restrict__ vnew_out, float* __restrict__ ht_out, int T, int H, const int* __restrict__ chunk_off,
     int vf, int HQ, const int* __restrict__ cu, const bf16* __restrict__ w_in = nullptr) {
   static_assert(!VEC_B || GATE == RG_VECTOR, "vector b / w_gate come with the vector gate (GDN2)");
+  static_assert(!(WG && NOST), "w given or formed, not both");
   constexpr bool VEC = GATE == RG_VECTOR;
   using S = FwdWySmem<BV>;
   __shared__ S sm;
@@ -606,7 +609,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
         if constexpr (VEC) {
           rg0[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8);
           rg1[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8 + 4);
-          rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + kr_.ofs + (size_t)t * kr_.rs + c8, t));
+          if constexpr (!NOST) rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + kr_.ofs + (size_t)t * kr_.rs + c8, t));
         }
         if constexpr (VEC_B) rb[i] = *reinterpret_cast<const u32x4*>(rs_.src(bgate + kofs + (size_t)t * rsk + c8, t));
         else rb_tok[i] = *rs_.src(beta + (tok0 + t) * H + h, t);
@@ -651,7 +654,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
           kg = GATE == RG_SCALAR ? __builtin_bit_cast(bf16x8, scale_bf16x8(rk[i], fast_exp2(rg_last - rg_tok[i]))) : kx;
         }
       } else if constexpr (VEC) {
-        const bf16x8 qx = __builtin_bit_cast(bf16x8, rq[i]);
+        const bf16x8 qx = NOST ? bf16x8{} : __builtin_bit_cast(bf16x8, rq[i]);
         bf16x8 bx = {};
         if constexpr (VEC_B) bx = __builtin_bit_cast(bf16x8, rb[i]);
         bf16x8 qg;
@@ -661,10 +664,10 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
           const float glj = j < 4 ? rgl0[j] : rgl1[j - 4];
           const float be = VEC_B ? to_f32(bx[j]) : rb_tok[i];
           eh[j] = to_bf16(be * to_f32(kx[j]) * fast_exp2(gj));
-          qg[j] = to_bf16(to_f32(qx[j]) * fast_exp2(gj));
+          if constexpr (!NOST) qg[j] = to_bf16(to_f32(qx[j]) * fast_exp2(gj));
           kg[j] = to_bf16(to_f32(kx[j]) * fast_exp2(glj - gj));
         }
-        if (t / RW == vt) {       // (wave-uniform: a wave's 64 pieces are 4 whole rows)
+        if (!NOST && t / RW == vt) {       // (wave-uniform: a wave's 64 pieces are 4 whole rows)
           *reinterpret_cast<bf16x8*>(rs_.dst(qg_out + kofs + (size_t)t * rsk + 8 * ch, t)) = qg;
           *reinterpret_cast<bf16x8*>(rs_.dst(kg_out + kofs + (size_t)t * rsk + 8 * ch, t)) = kg;
         }
@@ -742,9 +745,13 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       settle(ra[i]);
       if constexpr (WG) {
         settle(rq[i]);
+        if constexpr (VEC) {
+          settle(rg0[i]);
+          settle(rg1[i]);
+        }
       } else {
         if constexpr (VEC) {
-          settle(rq[i]);
+          if constexpr (!NOST) settle(rq[i]);
           settle(rg0[i]);
           settle(rg1[i]);
         }
@@ -759,7 +766,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       if constexpr (VEC_B) settle(rwg[i]);
       else settle(rb_v[i]);
     }
-    if constexpr (VEC && !WG) {
+    if constexpr (VEC) {
       settle(rgl0);
       settle(rgl1);
     }
@@ -793,7 +800,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     const size_t tok0 = rs_.tok0;
     // w rows [64 vt / NVT, ...) of chunk c to HBM, 16-byte pieces (every lane stores: pieces
     // beyond the share are written twice, with the same data); WG: w came from HBM
-    if constexpr (!WG) {
+    if constexpr (!WG && !NOST) {
       constexpr int NWP = RW * (KD / 8);
 #pragma unroll
       for (int i = 0; i < (NWP + NTH - 1) / NTH; ++i) {
@@ -870,14 +877,14 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
   }
 }
 
-template <int BV, int GATE, bool VEC_B, bool WG = false>
+template <int BV, int GATE, bool VEC_B, bool WG = false, bool NOST = false>
 static hipError_t launch_fwd_h_wy(const void* q, const void* k, const void* v, const float* g, const float* beta,
                                   const void* bg, const void* wg, const float* akk, const float* h0, void* w,
                                   void* qg, void* kg, void* h, void* vnew, float* ht, int B, int T, int H,
                                   hipStream_t s, const int* co, int vf, int HQ, const int* cu,
                                   const void* w_in = nullptr) {
 #define FW_LAUNCH(MAP)                                                                                             \
-  hipLaunchKernelGGL((fwd_h_wy_kernel<BV, GATE, VEC_B, MAP, WG>), dim3(B * H * (VD / BV)), dim3(512), 0, s,        \
+  hipLaunchKernelGGL((fwd_h_wy_kernel<BV, GATE, VEC_B, MAP, WG, NOST>), dim3(B * H * (VD / BV)), dim3(512), 0, s,  \
                      (const bf16*)q, (const bf16*)k, (const bf16*)v, g, beta, (const bf16*)bg, (const bf16*)wg, akk, \
                      h0, (bf16*)w, (bf16*)qg, (bf16*)kg, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf, HQ, cu,        \
                      (const bf16*)w_in)
@@ -1098,28 +1105,34 @@ extern "C" hipError_t fdr_fwd_h_wy(const void* q, const void* k, const void* v, 
 // The forward scan with u formed in-kernel from v (and beta or w_gate) and Akk, w given:
 // B rows of T tokens, or (co[, cu]) packed sequences as for fwd_h_dispatch
 static hipError_t fwd_h_u_dispatch(const void* k, const void* w, const void* v, const float* g, int gate_mode,
-                                   const float* beta, const void* w_gate, const float* Akk, const float* h0, void* h,
-                                   void* v_new, float* ht, int B, int T, int H, int HQ, int K, int V, int chunk,
-                                   int value_block, hipStream_t stream, const int* co, int vf, const int* cu) {
+                                   const float* beta, const void* b_gate, const void* w_gate, const float* Akk,
+                                   const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int HQ,
+                                   int K, int V, int chunk, int value_block, hipStream_t stream, const int* co, int vf,
+                                   const int* cu) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
   if (HQ <= 0) HQ = H;
   if (H % HQ) return hipErrorInvalidValue;
-  if (!k || !w || !v || !Akk || !h || !v_new) return hipErrorInvalidValue;
+  if (!k || !v || !Akk || !h || !v_new) return hipErrorInvalidValue;
   const bool vec_b = w_gate != nullptr;
   if (vec_b && gate_mode != RG_VECTOR) return hipErrorInvalidValue;
   if (!vec_b && !beta) return hipErrorInvalidValue;
+  if (!w && vec_b && (!b_gate || HQ != H)) return hipErrorInvalidValue;   // E = (b k) 2^g needs b
   if (gate_mode != RG_NONE && !g) return hipErrorInvalidValue;
   if (cu && !co) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : fwd_default_bv(B, H);
-  // (b_gate is not read in this mode: only u's Z = w_gate v; a non-null pointer selects VEC_B)
-#define FU_ARGS nullptr, k, v, g, beta, w_gate, w_gate, Akk, h0, nullptr, nullptr, nullptr, h, v_new, ht, B, T, H, \
-                stream, co, vf, HQ, cu, w
-#define FU_BV(G, VB)                                                \
-  switch (bv) {                                                     \
-    case 16: return launch_fwd_h_wy<16, G, VB, true>(FU_ARGS);      \
-    case 32: return launch_fwd_h_wy<32, G, VB, true>(FU_ARGS);      \
-    case 64: return launch_fwd_h_wy<64, G, VB, true>(FU_ARGS);      \
-    default: return hipErrorInvalidValue;                           \
+  // w given: b_gate is not read (only u's Z = w_gate v; a non-null pointer selects VEC_B);
+  // w NULL: w formed too (NOST), from b_gate (GDN2) or beta
+#define FU_ARGS nullptr, k, v, g, beta, w ? w_gate : b_gate, w_gate, Akk, h0, nullptr, nullptr, nullptr, h, v_new, ht, \
+                B, T, H, stream, co, vf, HQ, cu, w
+#define FU_BV(G, VB)                                                                          \
+  switch (bv) {                                                                               \
+    case 16: return w ? launch_fwd_h_wy<16, G, VB, true>(FU_ARGS)                             \
+                      : launch_fwd_h_wy<16, G, VB, false, true>(FU_ARGS);                     \
+    case 32: return w ? launch_fwd_h_wy<32, G, VB, true>(FU_ARGS)                             \
+                      : launch_fwd_h_wy<32, G, VB, false, true>(FU_ARGS);                     \
+    case 64: return w ? launch_fwd_h_wy<64, G, VB, true>(FU_ARGS)                             \
+                      : launch_fwd_h_wy<64, G, VB, false, true>(FU_ARGS);                     \
+    default: return hipErrorInvalidValue;                                                     \
   }
   switch (gate_mode) {
     case RG_NONE: FU_BV(RG_NONE, false)
@@ -1134,11 +1147,11 @@ static hipError_t fwd_h_u_dispatch(const void* k, const void* w, const void* v, 
 }
 
 extern "C" hipError_t fdr_fwd_h_u(const void* k, const void* w, const void* v, const float* g, int gate_mode,
-                                  const float* beta, const void* w_gate, const float* Akk, const float* h0, void* h,
-                                  void* v_new, float* ht, int state_v_first, int B, int T, int H, int k_heads, int K,
-                                  int V, int chunk, int value_block, hipStream_t stream) {
-  return fwd_h_u_dispatch(k, w, v, g, gate_mode, beta, w_gate, Akk, h0, h, v_new, ht, B, T, H, k_heads, K, V, chunk,
-                          value_block, stream, nullptr, state_v_first ? 1 : 0, nullptr);
+                                  const float* beta, const void* b_gate, const void* w_gate, const float* Akk,
+                                  const float* h0, void* h, void* v_new, float* ht, int state_v_first, int B, int T,
+                                  int H, int k_heads, int K, int V, int chunk, int value_block, hipStream_t stream) {
+  return fwd_h_u_dispatch(k, w, v, g, gate_mode, beta, b_gate, w_gate, Akk, h0, h, v_new, ht, B, T, H, k_heads, K, V,
+                          chunk, value_block, stream, nullptr, state_v_first ? 1 : 0, nullptr);
 }
 
 extern "C" hipError_t fdr_fwd_h_wy_varlen(const void* q, const void* k, const void* v, const float* g, int gate_mode,

@@ -23,7 +23,7 @@ namespace rewy {
 
 enum GateMode { GATE_NONE = 0, GATE_SCALAR = 1, GATE_VECTOR = 2 };
 
-template <int BV, int GATE, bool DV_FROM_AQK, bool INL = false>
+template <int BV, int GATE, bool DV_FROM_AQK, bool INL = false, int FW = 0>
 struct StateSmem {
   static constexpr int LDK = KD + 8;   // pitch of [.][K] tiles
   static constexpr int LDT = C + 8;    // pitch of [.][T] tiles
@@ -37,7 +37,8 @@ struct StateSmem {
   static constexpr int ND = SP ? 1 : 2;
   bf16 k[NB][C][LDK];      // kg rows:  A operand of kg * dh           (contraction over K, row reads)
   bf16 q[NB][C * KD];      // qg rows:  A operand of qg^T dO           (over T, transposed reads)
-  bf16 w[ND][C * KD];      // w rows:   A operand of w^T dR            (over T, transposed reads)
+  // (FW: w formed in-kernel between a step's two barriers, so one buffer)
+  bf16 w[FW ? 1 : ND][C * KD];   // w rows: A operand of w^T dR      (over T, transposed reads)
   bf16 ah[NB][C * C];      // Aqk rows [t][s], bf16: A operand of Aqk^T dO (over T, transposed reads)
   bf16 dO[C * BV];         // dO rows [t][v]: B operand of both        (over T, transposed reads)
   bf16 dhT[ND][BV][LDK];   // dh^T:    B operand of kg * dh
@@ -47,6 +48,12 @@ struct StateSmem {
   // q^T (2^g dO) and kg dh as 2^(g_last - g_t) (k dh)
   bf16 dOg[(INL && GATE == GATE_SCALAR) ? C * BV : 1];   // 2^(g_t) dO rows (swizzled)
   float gt[NB][INL ? C + 1 : 1];                         // g_t per row, g_last at [C]
+  // FW: E = (b k) 2^g rows (swizzled) and Akk hi / lo, the operands of w^T = E^T Akk^T
+  // (16-byte aligned: they follow the 2- and 4-byte scalars above, and a 16-byte LDS read
+  // from an address that is not measured 4x slower over the whole recurrence)
+  alignas(16) bf16 e[FW ? C * KD : 1];
+  alignas(16) bf16 akh[FW ? C : 1][LDT];
+  alignas(16) bf16 akl[FW ? C : 1][LDT];
 };
 
 // NW waves: 8 (wave w owns state rows [16 w, 16 w + 16), every value column) or 16
@@ -63,16 +70,23 @@ struct StateSmem {
 // RAWQK (vector gate, dense rows): q and k are the raw ones (q/k heads HQ), and qg = q 2^g,
 // kg = k 2^(g_last - g) are formed while the chunk is staged, with fdr_prepare_wu's roundings,
 // from the gate tile the chunk loads beside them, so no qg / kg need be written for this pass.
-template <int BV, int GATE, bool DV_FROM_AQK, int NW, bool MAP = false, bool INL = false, bool RAWQK = false>
+// FW (with RAWQK; 1: scalar beta, 2: GDN2's vector b): w is not read either but formed as
+// fdr_prepare_wu forms it, w^T = E^T Akk^T with E = (b k) 2^g and Akk split bf16 hi + lo, the
+// same MFMA sequence and roundings, between the step's two barriers.
+template <int BV, int GATE, bool DV_FROM_AQK, int NW, bool MAP = false, bool INL = false, bool RAWQK = false,
+          int FW = 0>
 __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ w,
     const float* __restrict__ g, const bf16* __restrict__ dO, const float* __restrict__ aqk,
     const bf16* __restrict__ dv, const float* __restrict__ dht, bf16* __restrict__ dh_out,
     bf16* __restrict__ dr_out, float* __restrict__ dh0, int T, int H, float scale,
-    const int* __restrict__ chunk_off, int segs, int vf, int HQ, const int* __restrict__ cu) {
+    const int* __restrict__ chunk_off, int segs, int vf, int HQ, const int* __restrict__ cu,
+    const float* __restrict__ beta = nullptr, const bf16* __restrict__ bgate = nullptr,
+    const float* __restrict__ akk = nullptr) {
   static_assert(!INL || (DV_FROM_AQK && GATE != GATE_VECTOR), "in-kernel Aqk: scalar / no gate");
   static_assert(!RAWQK || (GATE == GATE_VECTOR && !INL && !MAP), "raw q / k: the vector gate, dense rows");
-  using S = StateSmem<BV, GATE, DV_FROM_AQK, INL>;
+  static_assert(!FW || RAWQK, "w formed in-kernel: with the raw q / k");
+  using S = StateSmem<BV, GATE, DV_FROM_AQK, INL, FW>;
   __shared__ S sm;
   constexpr int NVT = VD / BV;
   constexpr int NCT = BV / 16;             // column tiles of the state
@@ -138,6 +152,9 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   float rg_last = 0.f, rg_tok[NPI];             // scalar gate: last row, the rows this thread stages
   float rg_do[NDO];                             // INL, scalar gate: the gate of each dO piece's row
   f32x4 rgp0[NPI], rgp1[NPI], rgl0, rgl1;       // RAWQK: each piece's 8 gates, g_last of its 8 columns
+  u32x4 rbx[NPI];                               // FW = 2: b pieces
+  float rbs[NPI];                               // FW = 1: beta of each piece's row
+  f32x4 rak[NPI];                               // FW: Akk pieces
   const size_t row_stride_k = (size_t)H * KD;   // elements between tokens
   const size_t row_stride_v = (size_t)H * VD;
 
@@ -175,7 +192,14 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       const size_t oq = qr.ofs + (size_t)(p >> 4) * qr.rs + (p & 15) * 8;
       rk[i] = *reinterpret_cast<const u32x4*>(rs_.src(k + oq, p >> 4));
       rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(q + oq, p >> 4));
-      rw[i] = *reinterpret_cast<const u32x4*>(rs_.src(w + o, p >> 4));
+      if constexpr (FW) {
+        rak[i] = *reinterpret_cast<const f32x4*>(
+            tril_src(rs_.src(akk + ((tok0 + (p >> 4)) * H + h) * C + (p & 15) * 4, p >> 4), p >> 4, p & 15));
+        if constexpr (FW == 2) rbx[i] = *reinterpret_cast<const u32x4*>(rs_.src(bgate + o, p >> 4));
+        else rbs[i] = *rs_.src(beta + (tok0 + (p >> 4)) * H + h, p >> 4);
+      } else {
+        rw[i] = *reinterpret_cast<const u32x4*>(rs_.src(w + o, p >> 4));
+      }
       if constexpr (DV_FROM_AQK && !INL)
         ra[i] = *reinterpret_cast<const f32x4*>(
             tril_src(rs_.src(aqk + ((tok0 + (p >> 4)) * H + h) * C + (p & 15) * 4, p >> 4), p >> 4, p & 15));
@@ -216,6 +240,21 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
         }
         kq = __builtin_bit_cast(u32x4, ko);
         qq = __builtin_bit_cast(u32x4, qo);
+        if constexpr (FW) {
+          // E = (b k) 2^g and Akk hi / lo, rounded as fdr_prepare_wu rounds them
+          bf16x8 eh;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float gj = j < 4 ? rgp0[i][j] : rgp1[i][j - 4];
+            const float be = FW == 2 ? to_f32(__builtin_bit_cast(bf16x8, rbx[i])[j]) : rbs[i];
+            eh[j] = to_bf16(be * to_f32(kx[j]) * fast_exp2(gj));
+          }
+          store_tr_chunk<16>(sm.e, t, ch, __builtin_bit_cast(u32x4, eh));
+          bf16x4 alo;
+          const bf16x4 ahi = split_hi4(tril_piece(rak[i], t, ch), alo);
+          *reinterpret_cast<bf16x4*>(&sm.akh[t][4 * ch]) = ahi;
+          *reinterpret_cast<bf16x4*>(&sm.akl[t][4 * ch]) = alo;
+        }
       }
       if constexpr (GATE == GATE_SCALAR) {
         // scalar gate: kg = k 2^(g_last - g_t), qg = q 2^(g_t), the row's factors from registers
@@ -224,7 +263,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       }
       *reinterpret_cast<u32x4*>(&sm.k[0][t][ch * 8]) = kq;
       store_tr_chunk<16>(sm.q[0], t, ch, qq);
-      store_tr_chunk<16>(sm.w[db], t, ch, rw[i]);
+      if constexpr (!FW) store_tr_chunk<16>(sm.w[db], t, ch, rw[i]);
       if constexpr (DV_FROM_AQK) {
         // Aqk as one bf16, the precision of the reference's dv_local (FLA's dAv rounds A to
         // the dO dtype before its dot: kernels/kda_residual_npu_onchip.py:114-116)
@@ -404,6 +443,30 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       lds_barrier();
     }
 
+    // FW: w^T = E^T Akk^T of chunk c (the MFMA sequence of fdr_prepare_wu), for the update
+    // after the next barrier: wave w takes token tile w % 4 and 32 / NW key-row tiles, so that
+    // it reads one token tile's Akk hi / lo fragments and the E fragments of its key rows
+    if constexpr (FW) {
+      constexpr int TPW = 32 / NW;
+      const int tt = wv % 4;
+      const bf16x8 ah0 = frag(&sm.akh[16 * tt][0], S::LDT), al0 = frag(&sm.akl[16 * tt][0], S::LDT);
+      const bf16x8 ah1 = frag(&sm.akh[16 * tt][32], S::LDT), al1 = frag(&sm.akl[16 * tt][32], S::LDT);
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        const int row0 = 16 * (TPW * (wv / 4) + i);
+        const bf16x8 x0 = frag_tr<16>(sm.e, 0, row0);
+        const bf16x8 x1 = frag_tr<16>(sm.e, 32, row0);
+        f32x4 acc = zero4();
+        acc = mfma(x0, ah0, acc);
+        acc = mfma(x0, al0, acc);
+        acc = mfma(x1, ah1, acc);
+        acc = mfma(x1, al1, acc);
+        bf16x4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = to_bf16(acc[r]);
+        *reinterpret_cast<bf16x4*>(sm.w[0] + tr_off<16>(16 * tt + (l & 15), row0 + 4 * (l >> 4))) = o;
+      }
+    }
     // X = qg^T dO (independent of dh)
     f32x4 xq[NCW];
 #pragma unroll
@@ -469,7 +532,8 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        a = mfma(frag_tr<16>(sm.w[db], 32 * ks, 16 * rt), frag(&sm.drT[16 * (ct0 + j)][32 * ks], S::LDT), a);
+        a = mfma(frag_tr<16>(sm.w[FW ? 0 : db], 32 * ks, 16 * rt), frag(&sm.drT[16 * (ct0 + j)][32 * ks], S::LDT),
+                 a);
       st[j] = -a;
     }
     if constexpr (SP) form_S(pb ^ 1);      // chunk c - 1's Aqk, beside the stores
@@ -526,19 +590,22 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
 template <int BV>
 constexpr int state_waves() { return BV == 32 ? 16 : 8; }
 
-template <int BV, int GATE, bool AQK, bool INL = false, bool RAWQK = false>
+template <int BV, int GATE, bool AQK, bool INL = false, bool RAWQK = false, int FW = 0>
 static hipError_t launch_state(const void* q, const void* k, const void* w, const float* g,
                                const void* dO, const float* aqk, const void* dv, const float* dht,
                                void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
                                hipStream_t stream, const int* chunk_off, int segs = 0, int vf = 0, int HQ = 0,
-                               const int* cu = nullptr) {
+                               const int* cu = nullptr, const float* beta = nullptr, const void* bg = nullptr,
+                               const float* akk = nullptr) {
   const int rows = segs > 0 ? B * segs : B;
   const int grid = rows * H * (VD / BV);
-  constexpr int NW = state_waves<BV>();
+  // (FW at 32-wide tiles: 8 waves; 16 under their 128-register cap spill)
+  constexpr int NW = FW ? 8 : state_waves<BV>();
 #define S_LAUNCH(MAP)                                                                                        \
-  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW, MAP, INL, RAWQK>), dim3(grid), dim3(64 * NW), 0, stream, \
-                     (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk, (const bf16*)dv, \
-                     dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale, chunk_off, segs, vf, HQ > 0 ? HQ : H, cu)
+  hipLaunchKernelGGL((state_bwd_kernel<BV, GATE, AQK, NW, MAP, INL, RAWQK, FW>), dim3(grid), dim3(64 * NW), 0,   \
+                     stream, (const bf16*)q, (const bf16*)k, (const bf16*)w, g, (const bf16*)dO, aqk,              \
+                     (const bf16*)dv, dht, (bf16*)dh, (bf16*)dr, dh0, T, H, scale, chunk_off, segs, vf,            \
+                     HQ > 0 ? HQ : H, cu, beta, (const bf16*)bg, akk)
   if constexpr (RAWQK) S_LAUNCH(false);     // (dense rows only)
   else if (cu) S_LAUNCH(true);
   else S_LAUNCH(false);
@@ -546,14 +613,15 @@ static hipError_t launch_state(const void* q, const void* k, const void* w, cons
   return hipGetLastError();
 }
 
-template <int GATE, bool AQK, bool INL = false, bool RAWQK = false>
+template <int GATE, bool AQK, bool INL = false, bool RAWQK = false, int FW = 0>
 static hipError_t pick_bv(int bv, const void* q, const void* k, const void* w, const float* g,
                           const void* dO, const float* aqk, const void* dv, const float* dht,
                           void* dh, void* dr, float* dh0, int B, int T, int H, float scale,
-                          hipStream_t s, const int* co, int vf, int HQ, const int* cu) {
+                          hipStream_t s, const int* co, int vf, int HQ, const int* cu, const float* beta = nullptr,
+                          const void* bg = nullptr, const float* akk = nullptr) {
 #define S_BV(BV) \
-  launch_state<BV, GATE, AQK, INL, RAWQK>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, vf, \
-                                          HQ, cu)
+  launch_state<BV, GATE, AQK, INL, RAWQK, FW>(q, k, w, g, dO, aqk, dv, dht, dh, dr, dh0, B, T, H, scale, s, co, 0, \
+                                              vf, HQ, cu, beta, bg, akk)
   switch (bv) {
     case 16: return S_BV(16);
     case 32: return S_BV(32);
@@ -915,16 +983,25 @@ extern "C" hipError_t fdr_state_bwd(const void* q, const void* k, const void* w,
 }
 
 extern "C" hipError_t fdr_state_bwd_raw_qk(const void* q, const void* k, const void* w, const float* g,
+                                           const float* beta, const void* b_gate, const float* Akk,
                                            const void* dO, const float* aqk, const float* dht, void* dh, void* dr,
                                            float* dh0, int state_v_first, int B, int T, int H, int qk_heads, int K,
                                            int V, int chunk, float scale, int value_block, hipStream_t stream) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
-  if (!q || !k || !w || !g || !dO || !aqk || !dh || !dr) return hipErrorInvalidValue;
+  if (!q || !k || !g || !dO || !aqk || !dh || !dr) return hipErrorInvalidValue;
   const int HQ = qk_heads > 0 ? qk_heads : H;
   if (H % HQ) return hipErrorInvalidValue;
   const int bv = value_block > 0 ? value_block : default_bv(B, H);
-  return pick_bv<GATE_VECTOR, true, false, true>(bv, q, k, w, g, dO, aqk, nullptr, dht, dh, dr, dh0, B, T, H, scale,
-                                                stream, nullptr, state_v_first ? 1 : 0, HQ, nullptr);
+  const int vf = state_v_first ? 1 : 0;
+  if (w) return pick_bv<GATE_VECTOR, true, false, true>(bv, q, k, w, g, dO, aqk, nullptr, dht, dh, dr, dh0, B, T, H,
+                                                       scale, stream, nullptr, vf, HQ, nullptr);
+  // w formed in-kernel from Akk and beta (scalar per row) or b_gate (GDN2, [B,T,H,K])
+  if (!Akk || (beta == nullptr) == (b_gate == nullptr) || (b_gate && HQ != H)) return hipErrorInvalidValue;
+  if (b_gate)
+    return pick_bv<GATE_VECTOR, true, false, true, 2>(bv, q, k, nullptr, g, dO, aqk, nullptr, dht, dh, dr, dh0, B, T,
+                                                      H, scale, stream, nullptr, vf, HQ, nullptr, nullptr, b_gate, Akk);
+  return pick_bv<GATE_VECTOR, true, false, true, 1>(bv, q, k, nullptr, g, dO, aqk, nullptr, dht, dh, dr, dh0, B, T, H,
+                                                    scale, stream, nullptr, vf, HQ, nullptr, beta, nullptr, Akk);
 }
 
 extern "C" hipError_t fdr_state_bwd_varlen(const void* q, const void* k, const void* w, const float* g,

@@ -98,6 +98,11 @@ PAIRED_U = True
 # ... and, vector gates, with qg / kg formed from the raw q / k where each recurrence stages a
 # chunk (fdr_state_bwd_raw_qk, fwd_h_u) instead of written by prepare_wu and read back
 PAIRED_RAW = True
+# ... and, GDN2 (a vector b) at 64-wide tiles, w formed in both recurrences too (w = Akk (b k 2^g)
+# from the same staged k and gate tile), so that fdr_prepare_wu does not run at all.  (KDA's
+# prepare, with a scalar beta, and GDN2's at B*H = 32 cost less than forming w adds to the state
+# recurrence's step: not taken there.)
+PAIRED_FORMW = True
 
 
 def paired_tile(B, H, NT, gate_mode):
@@ -244,7 +249,7 @@ def _dims(q):
 
 def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, want_dh0=True,
               value_block=0, method="auto", chunk_offsets=None, segments=0, state_v_first=False, varlen=None,
-              raw_qk=False):
+              raw_qk=False, beta=None, b=None, Akk=None):
     """Reverse state recurrence.  Returns (dh [B,NT,H,K,V] bf16, dR [B,T,H,V] bf16, dh0 fp32|None).
 
     dv_local = Aqk^T dO comes from ``aqk``, or is given as ``dv``; with neither (scalar / no
@@ -266,15 +271,28 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
 
     ``raw_qk`` (vector gate, ``aqk``, dense rows, direct form): q and k are the raw ones and
     qg = q 2^g, kg = k 2^(g_last - g) are formed in-kernel with ``prepare_wu``'s roundings
-    (fdr_state_bwd_raw_qk), so the result is the bits of ``prepare_wu``'s qg / kg then this."""
+    (fdr_state_bwd_raw_qk), so the result is the bits of ``prepare_wu``'s qg / kg then this.
+    With ``raw_qk``, w may be None: then w = Akk (beta k 2^g), or Akk (b k 2^g) for GDN2, is
+    formed in-kernel as ``prepare_wu`` forms it (``Akk`` and one of ``beta`` / ``b``)."""
     B, T, HQ, K = _rows(q, varlen)
-    H, HQ = _group(w.shape[2] if w is not None and w.ndim == 4 else HQ, HQ)
+    H, HQ = _group(w.shape[2] if w is not None and w.ndim == 4 else dO.shape[2], HQ)
     V = V_SUPPORTED
     dev = q.device
     bf, f32 = torch.bfloat16, torch.float32
     for x, n in ((q, "q"), (k, "k")):
         _need(x, n, bf, (B, T, HQ, K), dev)
-    _need(w, "w", bf, (B, T, H, K), dev)
+    if w is not None:
+        _need(w, "w", bf, (B, T, H, K), dev)
+    else:
+        if not raw_qk:
+            raise ValueError("w is formed in-kernel only with raw_qk")
+        _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
+        if (beta is None) == (b is None):
+            raise ValueError("w formed in-kernel: pass exactly one of beta / b")
+        if b is not None:
+            _need(b, "b", bf, (B, T, H, K), dev)
+        else:
+            _need(beta, "beta", f32, (B, T, H), dev)
     _need(dO, "dO", bf, (B, T, H, V), dev)
     if gate_mode == GATE_VECTOR:
         _need(g, "g", f32, (B, T, H, K), dev)
@@ -310,9 +328,11 @@ def state_bwd(q, k, w, g, gate_mode, dO, scale, aqk=None, dv=None, dht=None, wan
     if raw_qk:
         if gate_mode != GATE_VECTOR or aqk is None or co is not None or method not in ("auto", "direct"):
             raise ValueError("raw_qk takes a vector gate, aqk, dense rows and the direct form")
-        st = _lib.load().fdr_state_bwd_raw_qk(P(q), P(k), P(w), P(g), P(dO), P(aqk), P(dht), P(dh), P(dr), P(dh0),
-                                              vf, B, T, H, HQ, K, V, CHUNK, float(scale), int(value_block),
-                                              _lib.stream_handle(dev))
+        formw = w is None
+        st = _lib.load().fdr_state_bwd_raw_qk(P(q), P(k), P(w), P(g), P(beta if formw else None),
+                                              P(b if formw else None), P(Akk if formw else None), P(dO), P(aqk),
+                                              P(dht), P(dh), P(dr), P(dh0), vf, B, T, H, HQ, K, V, CHUNK,
+                                              float(scale), int(value_block), _lib.stream_handle(dev))
         _lib.check(st, "fdr_state_bwd_raw_qk")
         return dh, dr, dh0
     if co is not None:
@@ -778,19 +798,23 @@ def group_sum(x, HQ):
 
 
 def fwd_h_u(k, w, v, Akk, g, gate_mode, beta=None, w_gate=None, h0=None, want_final=False, value_block=0,
-            state_v_first=False):
+            state_v_first=False, b=None):
     """``fwd_h`` with u formed in-kernel (fdr_fwd_h_u): u = Akk (beta v), or Akk (w_gate v) for
     GDN2, from the same MFMA sequence as ``prepare_wu``, so h, v_new and the final state are
     the bits of ``prepare_wu`` + ``fwd_h``.  k is the raw k (a vector gate's kg formed in-kernel
-    with ``prepare_wu``'s rounding); w as
-    ``prepare_wu(..., want_u=False)`` returns it.  Returns (h, v_new, final|None)."""
+    with ``prepare_wu``'s rounding); w as ``prepare_wu(..., want_u=False)`` returns it, or None:
+    then w = Akk (beta k 2^g), or Akk (b k 2^g) for GDN2 (``b``), is formed in-kernel too, as
+    ``prepare_wu`` forms it.  Returns (h, v_new, final|None)."""
     B, T, HQ, K = _dims(k)
-    H, HQ = _group(w.shape[2] if w is not None and w.ndim == 4 else HQ, HQ)
+    H, HQ = _group(v.shape[2] if v is not None and v.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
     dev = k.device
     bf, f32 = torch.bfloat16, torch.float32
     _need(k, "k", bf, (B, T, HQ, K), dev)
-    _need(w, "w", bf, (B, T, H, K), dev)
+    if w is not None:
+        _need(w, "w", bf, (B, T, H, K), dev)
+    elif w_gate is not None:
+        _need(b, "b", bf, (B, T, H, K), dev)
     _need(v, "v", bf, (B, T, H, V), dev)
     _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
     if gate_mode == GATE_VECTOR:
@@ -814,9 +838,9 @@ def fwd_h_u(k, w, v, Akk, g, gate_mode, beta=None, w_gate=None, h0=None, want_fi
     vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
     ht = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_final else None
     P = _lib.ptr
-    st = _lib.load().fdr_fwd_h_u(P(k), P(w), P(v), P(g), int(gate_mode), P(beta), P(w_gate), P(Akk), P(h0), P(h),
-                                 P(vnew), P(ht), int(bool(state_v_first)), B, T, H, HQ, K, V, CHUNK, int(value_block),
-                                 _lib.stream_handle(dev))
+    st = _lib.load().fdr_fwd_h_u(P(k), P(w), P(v), P(g), int(gate_mode), P(beta), P(b if w is None else None),
+                                 P(w_gate), P(Akk), P(h0), P(h), P(vnew), P(ht), int(bool(state_v_first)), B, T, H,
+                                 HQ, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_h_u")
     return h, vnew, ht
 

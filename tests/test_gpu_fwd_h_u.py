@@ -3,8 +3,9 @@ itself) and fdr_prepare_wu without u (and without qg / kg), the pair the paired 
 run, against fdr_prepare_wu + fdr_fwd_h: w, qg, kg of the prepare modes and h, v_new, the
 final state of the two scans bit for bit (u and kg are formed with prepare_wu's MFMA sequence
 and roundings), for the four families, every tile width, V-first states and grouped q / k
-heads.  Likewise fdr_state_bwd_raw_qk (qg / kg formed in the state recurrence) against
-fdr_prepare_wu's qg / kg then fdr_state_bwd."""
+heads; and with w formed in the scan as well (w = NULL: no fdr_prepare_wu).  Likewise
+fdr_state_bwd_raw_qk (qg / kg, and with w = NULL w, formed in the state recurrence) against
+fdr_prepare_wu's qg / kg / w then fdr_state_bwd."""
 import pytest
 import torch
 
@@ -59,6 +60,12 @@ def test_fwd_h_u_equals_prepare_then_fwd_h(op, vb):
         torch.cuda.synchronize()
         for n, a, r in zip(("h", "v_new", "final"), got, ref):
             assert torch.equal(a, r), (op, vb, vf, n)
+        # w formed in the scan too (no prepare_wu)
+        got = ops.fwd_h_u(d["k"], None, d["v"], d["Akk"], d["gc"], gate, beta=d.get("beta"), w_gate=d.get("w"),
+                          b=d.get("b"), h0=h0, want_final=True, value_block=vb, state_v_first=vf)
+        torch.cuda.synchronize()
+        for n, a, r in zip(("h", "v_new", "final"), got, ref):
+            assert torch.equal(a, r), (op, vb, vf, "w formed", n)
 
 
 @pytest.mark.parametrize("op", ["kda", "gdn", "delta"])
@@ -74,10 +81,11 @@ def test_fwd_h_u_grouped_heads(op):
     assert torch.equal(part["w"], full["w"])
     ref = ops.fwd_h(full["kg"] if vec else d["k"], full["w"], full["u"], d["gc"], gate, h0=d["initial_state"],
                     method="direct")
-    got = ops.fwd_h_u(d["k"], part["w"], d["v"], d["Akk"], d["gc"], gate, beta=d["beta"], h0=d["initial_state"])
-    torch.cuda.synchronize()
-    for n, a, r in zip(("h", "v_new"), got[:2], ref[:2]):
-        assert torch.equal(a, r), (op, n)
+    for w in (part["w"], None):
+        got = ops.fwd_h_u(d["k"], w, d["v"], d["Akk"], d["gc"], gate, beta=d["beta"], h0=d["initial_state"])
+        torch.cuda.synchronize()
+        for n, a, r in zip(("h", "v_new"), got[:2], ref[:2]):
+            assert torch.equal(a, r), (op, w is None, n)
 
 
 @pytest.mark.parametrize("vb", [16, 32, 64])
@@ -97,6 +105,9 @@ def test_state_bwd_raw_qk_equals_prepared_qg_kg(op, HQ, vb):
         common = dict(aqk=d["Aqk"], dht=dht, want_dh0=True, value_block=vb, method="direct", state_v_first=vf)
         ref = ops.state_bwd(pre["qg"], pre["kg"], pre["w"], d["gc"], 2, dO, 0.088, **common)
         got = ops.state_bwd(d["q"], d["k"], pre["w"], d["gc"], 2, dO, 0.088, raw_qk=True, **common)
+        formed = ops.state_bwd(d["q"], d["k"], None, d["gc"], 2, dO, 0.088, raw_qk=True, beta=d.get("beta"),
+                               b=d.get("b"), Akk=d["Akk"], **common)
         torch.cuda.synchronize()
-        for n, a, r in zip(("dh", "dR", "dh0"), got, ref):
+        for n, a, f, r in zip(("dh", "dR", "dh0"), got, formed, ref):
             assert torch.equal(a, r), (op, HQ, vb, vf, n)
+            assert torch.equal(f, r), (op, HQ, vb, vf, "w formed", n)

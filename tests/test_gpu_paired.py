@@ -7,8 +7,8 @@ scalar / no-gate ones with the state recurrence forming Aqk itself):
 * the public autograd backward (recompute policy) against the fp64 oracle at the
   reference's acceptance tolerances (validation.py:40-45, :68);
 * the same gradients, bit for bit, as the same launches enqueued on one stream, as the two
-  recurrences reading the qg / kg that prepare_wu wrote (``ops.PAIRED_RAW`` off: they form
-  them from the raw q / k), and as the scan reading a u that prepare_wu wrote
+  recurrences reading the w (``ops.PAIRED_FORMW`` off, GDN2) and the qg / kg (``ops.PAIRED_RAW``
+  off) that prepare_wu wrote instead of forming them from the raw q / k, and as the scan reading a u that prepare_wu wrote
   (``ops.PAIRED_U`` off: the scan forms u itself);
 * against the policy switched off (the pair one after the other at the default tile
   width): rel-L2 <= 1e-5, the tile width changing no arithmetic of a value column;
@@ -105,6 +105,11 @@ def test_paired_equals_one_stream_and_policy_off(op, B, T, H, vb, monkeypatch):
     monkeypatch.undo()
     # vector gates: qg / kg written by prepare_wu and read back instead of formed in the two
     # recurrences: the same bits
+    monkeypatch.setattr(ops, "PAIRED_FORMW", False)
+    prepared = run()
+    torch.cuda.synchronize()
+    for i, (a, r) in enumerate(zip(got, prepared)):
+        assert torch.equal(a, r), (op, "PAIRED_FORMW", i)
     monkeypatch.setattr(ops, "PAIRED_RAW", False)
     written = run()
     torch.cuda.synchronize()
