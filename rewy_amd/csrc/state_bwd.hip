@@ -161,9 +161,12 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   auto load_chunk = [&](int c) {
     const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
     const size_t tok0 = rs_.tok0;
-    // gate first: its consumer (lambda) is the first thing staged
+    // gate first: its consumer (lambda) is the first thing staged.  Every lane issues the same
+    // loads (clamped indices): a branch here would make the vector-memory wait counts lane-
+    // dependent, and the wait before staging would then fall to vmcnt(0) -- waiting also for
+    // the previous step's dh / dR stores, issued after these loads
     if constexpr (GATE == GATE_VECTOR) {
-      if (tid < KD) rg_last = g[((tok0 + rs_.clamp(C - 1)) * H + h) * KD + tid];
+      rg_last = g[((tok0 + rs_.clamp(C - 1)) * H + h) * KD + (tid & (KD - 1))];
     } else if constexpr (GATE == GATE_SCALAR) {
 #pragma unroll
       for (int i = 0; i < NPI; ++i) rg_tok[i] = g[(tok0 + rs_.clamp((tid + NTH * i) >> 4)) * H + h];
@@ -388,6 +391,44 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     }
   };
 
+  // global stores of dh[c] and dR_c from the transposed LDS copies: per wave task a block of
+  // 16 columns (dh rows k / dR rows t) by 32 value rows, 16-lane group g taking 8 of them
+  // (two transposed reads per 16-byte piece; narrower tiles repeat a group's rows, and waves
+  // beyond the tasks repeat a task, with the same data).  Every wave issues the same number
+  // of stores, and the loop is entered with as many (sink: to the sink page) issued after the
+  // first chunk's loads as each step issues after the next chunk's: the vector-memory wait
+  // counts are then the same on both paths into a step, so its staging waits only for its
+  // own loads, not for the previous step's stores.  (Sink stores: one 16-byte slot each, at
+  // most 3 per step here, so that none overwrites another and is dropped.)
+  static_assert((KD / 16) * (BV >= 32 ? BV / 32 : 1) <= 2 * NW && (C / 16) * (BV >= 32 ? BV / 32 : 1) <= NW,
+                "at most 3 stores per step, one sink-page slot each");
+  auto store_tiles = [&](int c, int db, bool sink) {
+    constexpr int RB = BV / 8;                          // 8-row blocks of the value tile
+    constexpr int RQ = RB >= 4 ? RB / 4 : 1;            // quads of them
+    const int g4 = l >> 4;
+    const size_t dh_base = ((size_t)(c0 + c) * H + h) * KD * VD;
+    constexpr int NTK = (KD / 16) * RQ;
+#pragma unroll
+    for (int i = 0; i < (NTK + NW - 1) / NW; ++i) {
+      const int tk = (wv + NW * i) % NTK;
+      const int kr0 = 16 * (tk % (KD / 16)), v0 = 8 * ((4 * (tk / (KD / 16)) + g4) % RB);
+      const bf16x8 o = col8_tr(&sm.dhT[db][0][0], S::LDK, v0, kr0, l);
+      bf16* dst = dh_out + dh_base + (size_t)(kr0 + (l & 15)) * VD + v_base + v0;
+      *reinterpret_cast<bf16x8*>(sink ? reinterpret_cast<bf16*>(sink_page + 4 * i) : dst) = o;
+    }
+    const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
+    const size_t tok0 = rs_.tok0;
+    constexpr int NTR = (C / 16) * RQ;
+#pragma unroll
+    for (int i = 0; i < (NTR + NW - 1) / NW; ++i) {
+      const int tk = (wv + NW * i) % NTR;
+      const int t = 16 * (tk % (C / 16)) + (l & 15), v0 = 8 * ((4 * (tk / (C / 16)) + g4) % RB);
+      const bf16x8 o = col8_tr(&sm.drT[0][0], S::LDT, v0, t - (l & 15), l);
+      bf16* dst = rs_.dst(dr_out + (tok0 + t) * row_stride_v + (size_t)h * VD + v_base + v0, t);
+      *reinterpret_cast<bf16x8*>(sink ? reinterpret_cast<bf16*>(sink_page + 4 * ((NTK + NW - 1) / NW + i)) : dst) = o;
+    }
+  };
+
   if constexpr (SP) {
     if (NT > 0) {
       load_A(NT - 1);
@@ -405,6 +446,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
   } else {
     if (NT > 0) load_chunk(NT - 1);
   }
+  if (NT > 0) store_tiles(NT - 1, 0, true);
   for (int c = NT - 1; c >= 0; --c) {
     const int pb = SP ? (c & 1) : 0;     // this chunk's k / q / Aqk / gate buffer
     const int db = S::ND == 2 ? (c & 1) : 0;   // and its dh^T / w / lambda buffer
@@ -538,38 +580,7 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     }
     if constexpr (SP) form_S(pb ^ 1);      // chunk c - 1's Aqk, beside the stores
 
-    // global stores of dh[c] and dR_c from the transposed LDS copies: per wave task a block of
-    // 16 columns (dh rows k / dR rows t) by 32 value rows, 16-lane group g taking 8 of them
-    // (two transposed reads per 16-byte piece; narrower tiles repeat a group's rows, with
-    // the same data).  Fixed trip counts keep the vector-memory wait counts static, so the
-    // next chunk's staging waits only for its own loads, not for these stores; waves beyond
-    // the tasks skip (wave-uniform).
-    {
-      constexpr int RB = BV / 8;                          // 8-row blocks of the value tile
-      constexpr int RQ = RB >= 4 ? RB / 4 : 1;            // quads of them
-      const int g4 = l >> 4;
-      const size_t dh_base = ((size_t)(c0 + c) * H + h) * KD * VD;
-      constexpr int NTK = (KD / 16) * RQ;
-#pragma unroll
-      for (int i = 0; i < (NTK + NW - 1) / NW; ++i) {
-        const int tk = wv + NW * i;
-        if (NTK % NW != 0 && tk >= NTK) break;
-        const int kr0 = 16 * (tk % (KD / 16)), v0 = 8 * ((4 * (tk / (KD / 16)) + g4) % RB);
-        const bf16x8 o = col8_tr(&sm.dhT[db][0][0], S::LDK, v0, kr0, l);
-        *reinterpret_cast<bf16x8*>(dh_out + dh_base + (size_t)(kr0 + (l & 15)) * VD + v_base + v0) = o;
-      }
-      const Rows<MAP> rs_ = seq_chunk_rows<MAP>(cu, b, c, c0 + c);
-      const size_t tok0 = rs_.tok0;
-      constexpr int NTR = (C / 16) * RQ;
-#pragma unroll
-      for (int i = 0; i < (NTR + NW - 1) / NW; ++i) {
-        const int tk = wv + NW * i;
-        if (NTR % NW != 0 && tk >= NTR) break;
-        const int t = 16 * (tk % (C / 16)) + (l & 15), v0 = 8 * ((4 * (tk / (C / 16)) + g4) % RB);
-        const bf16x8 o = col8_tr(&sm.drT[0][0], S::LDT, v0, t - (l & 15), l);
-        *reinterpret_cast<bf16x8*>(rs_.dst(dr_out + (tok0 + t) * row_stride_v + (size_t)h * VD + v_base + v0, t)) = o;
-      }
-    }
+    store_tiles(c, db, false);
   }
 
   if (dh0) {
@@ -690,7 +701,7 @@ __global__ __launch_bounds__(512) void state_xfer_kernel(
   auto load_chunk = [&](int c) {
     const size_t tok0 = (size_t)(c0 + c) * C;
     if constexpr (GATE == GATE_VECTOR) {
-      if (tid < KD) rg_last = g[((tok0 + C - 1) * H + h) * KD + tid];
+      rg_last = g[((tok0 + C - 1) * H + h) * KD + (tid & (KD - 1))];     // (every lane: static wait counts)
     } else if constexpr (GATE == GATE_SCALAR) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) rg_tok[i] = g[(tok0 + ((tid + NTH * i) >> 4)) * H + h];
