@@ -84,6 +84,18 @@ def folds_u(cfg):
             and bool(ops.paired_tile(cfg["B"], cfg["H"], cfg["T"] // 64, gate)))
 
 
+def pair_forms(cfg):
+    """(raw, formw) of the paired recurrences, as ``backends.backward`` decides: qg / kg formed
+    from the raw q / k (vector gates), and w formed in both recurrences too (GDN2 at 64-wide
+    tiles)."""
+    from rewy_amd import ops
+    if not folds_u(cfg) or cfg["op"] not in ("kda", "gdn2"):
+        return False, False
+    raw = ops.PAIRED_RAW
+    vb = ops.paired_tile(cfg["B"], cfg["H"], cfg["T"] // 64, ops.GATE_VECTOR)
+    return raw, raw and ops.PAIRED_FORMW and cfg["op"] == "gdn2" and vb == 64
+
+
 def kernel_costs(op, full_saving, inline=False, fold_u=False, raw=False, formw=False):
     """Algorithmic (bytes, FLOPs) per chunk-head of every kernel the backward launches:
     every operand read once, every result written once; dense GEMM flops.  ``inline``: the
@@ -247,8 +259,7 @@ def setup(cfg, device):
         aqk = sv["Aqk"] if vec else None
     vb_pair = 0 if keep else ops.paired_tile(cfg["B"], cfg["H"], NT, gate)
     fold_u = bool(vb_pair) and ops.PAIRED_U
-    raw = fold_u and vec and ops.PAIRED_RAW
-    formw = raw and ops.PAIRED_FORMW and cfg["op"] == "gdn2" and vb_pair == 64
+    raw, formw = pair_forms(cfg) if fold_u else (False, False)
     if formw:
         # (the paired recurrences form w, qg, kg and u themselves: no prepare_wu)
         ks, qs, ws, aqk = xs["k"], xs["q"], None, sv["Aqk"]
@@ -369,10 +380,7 @@ def measure(cfg, steps, warmup):
     ms = time_steps(step, steps, warmup, WARMUP_MIN_S, winfo)
     fwd_ms = time_steps(forward, max(3, steps // 4), 1)
     kt = time_kernels(kern, max(5, steps))
-    raw = folds_u(cfg) and ops.PAIRED_RAW
-    costs = kernel_costs(cfg["op"], cfg["full_saving"], inline_aqk(cfg), folds_u(cfg), raw,
-                         raw and ops.PAIRED_FORMW and cfg["op"] == "gdn2"
-                         and ops.paired_tile(cfg["B"], cfg["H"], cfg["T"] // 64, ops.GATE_VECTOR) == 64)
+    costs = kernel_costs(cfg["op"], cfg["full_saving"], inline_aqk(cfg), folds_u(cfg), *pair_forms(cfg))
     kernels = {}
     for n, t in kt.items():
         by, fl = costs[n]

@@ -48,3 +48,19 @@ def test_paper_grid_tables_are_complete():
         assert op in bench.PAPER_GATE and policy in ("recompute", "all")
         assert len(orig) == len(rewy) == 6
         assert all(o > r > 0 for o, r in zip(orig, rewy))     # ReWY beat FLA in every published case
+
+
+def test_every_config_is_costed_as_its_backward_runs():
+    """The cost model of every bench config, with the paired recurrences' in-kernel forms as
+    the backend picks them (pure host logic: ``pair_forms`` and ``kernel_costs``)."""
+    import bench
+    for name, cfg in bench.CONFIGS.items():
+        raw, formw = bench.pair_forms(cfg)
+        costs = bench.kernel_costs(cfg["op"], cfg["full_saving"], bench.inline_aqk(cfg), bench.folds_u(cfg), raw,
+                                   formw)
+        assert all(b > 0 and f > 0 for b, f in costs.values()), name
+        assert formw <= raw
+        assert ("fdr_prepare_wu" in costs) == (not cfg["full_saving"] and not formw), name
+    # GDN2 B=2 T=8192 H=32 (64-wide paired tiles): w, qg, kg and u formed in the recurrences
+    assert bench.pair_forms(bench.CONFIGS["gdn2"]) == (True, True)
+    assert bench.pair_forms(bench.CONFIGS["kda"]) == (False, False)          # full saving
