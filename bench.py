@@ -86,14 +86,14 @@ def folds_u(cfg):
 
 def pair_forms(cfg):
     """(raw, formw) of the paired recurrences, as ``backends.backward`` decides: qg / kg formed
-    from the raw q / k (vector gates), and w formed in both recurrences too (GDN2 at 64-wide
-    tiles)."""
+    from the raw q / k (vector gates at 64-wide tiles), and w formed in both recurrences too
+    (GDN2 there)."""
     from rewy_amd import ops
-    if not folds_u(cfg) or cfg["op"] not in ("kda", "gdn2"):
+    if not folds_u(cfg) or cfg["op"] not in ("kda", "gdn2"):  # (vector gates only)
         return False, False
-    raw = ops.PAIRED_RAW
     vb = ops.paired_tile(cfg["B"], cfg["H"], cfg["T"] // 64, ops.GATE_VECTOR)
-    return raw, raw and ops.PAIRED_FORMW and cfg["op"] == "gdn2" and vb == 64
+    raw = ops.PAIRED_RAW and vb == 64
+    return raw, raw and ops.PAIRED_FORMW and cfg["op"] == "gdn2"
 
 
 def kernel_costs(op, full_saving, inline=False, fold_u=False, raw=False, formw=False):
@@ -279,7 +279,7 @@ def setup(cfg, device):
                                   method="direct", value_block=vb_pair, raw_qk=raw,
                                   **(dict(beta=xs.get("beta"), b=xs.get("b"), Akk=sv["Akk"]) if formw else {})),
             (lambda: ops.fwd_h_u(xs["k"], ws, xs["v"], sv["Akk"], g, gate, beta=xs.get("beta"), w_gate=xs.get("w"),
-                                 b=xs.get("b"),
+                                 b=xs.get("b"), kg=ks if vec and not raw else None,
                                  h0=xs["h0"], value_block=vb_pair)) if fold_u else
             (lambda: ops.fwd_h(ks, ws, pre["u"], g, gate, h0=xs["h0"], method="direct", value_block=vb_pair)))
         (dh, dR, _), (h, v_new, _) = kern["paired_recurrences"]()

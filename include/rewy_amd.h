@@ -301,11 +301,13 @@ hipError_t fdr_fwd_h_varlen(const void* k, const void* w, const void* u, const f
  * rounding, as fdr_state_bwd_raw_qk forms it; w as fdr_prepare_wu writes it, or NULL: then
  * w = Akk (beta k 2^g | b_gate k 2^g) is formed in-kernel too, with fdr_prepare_wu's MFMA
  * sequence and roundings (b_gate bf16 [B,T,H,K], GDN2 with k_heads = H; it is read only
- * then), and fdr_prepare_wu need not run at all; v bf16 [B,T,H,V]; beta fp32 [B,T,H], or w_gate bf16 [B,T,H,V] (vector gate only);
+ * then), and fdr_prepare_wu need not run at all.  kg (vector gate, w given; may be NULL):
+ * fdr_prepare_wu's kg [B,T,H,K], read instead of formed (k is then not read) -- cheaper at narrow
+ * value tiles, where every tile would form it again; v bf16 [B,T,H,V]; beta fp32 [B,T,H], or w_gate bf16 [B,T,H,V] (vector gate only);
  * Akk fp32 [B,T,H,64].  u is formed with fdr_prepare_wu's MFMA sequence and roundings, so h,
  * v_new and ht are the bits of fdr_prepare_wu + fdr_fwd_h.  value_block as for fdr_fwd_h.
  */
-hipError_t fdr_fwd_h_u(const void* k, const void* w, const void* v, const float* g, int gate_mode,
+hipError_t fdr_fwd_h_u(const void* k, const void* kg, const void* w, const void* v, const float* g, int gate_mode,
                        const float* beta, const void* b_gate, const void* w_gate, const float* Akk, const float* h0,
                        void* h, void* v_new, float* ht, int state_v_first, int B, int T, int H, int k_heads, int K,
                        int V, int chunk, int value_block, hipStream_t stream);

@@ -155,8 +155,8 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
         # width that gives each launch at most half the CUs
         vb = ops.paired_tile(N, H, NT, ops.GATE_VECTOR)
         fold_u = ops.PAIRED_U
-        raw = fold_u and ops.PAIRED_RAW
-        formw = raw and ops.PAIRED_FORMW and gates.get("b") is not None and vb == 64
+        raw = fold_u and ops.PAIRED_RAW and vb == 64
+        formw = raw and ops.PAIRED_FORMW and gates.get("b") is not None
         bgate = None if gates.get("b") is None else _bf(gates["b"])
         # (formw: w formed in both recurrences as well, so no prepare_wu at all)
         pre = (dict(w=None) if formw else
@@ -172,10 +172,11 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
                                  value_block=vb)
 
         def scan():
-            if fold_u:      # u and kg (and w) formed inside the scan
+            if fold_u:      # u (and kg, w) formed inside the scan
                 return ops.fwd_h_u(k, pre["w"], v, Akk, g, ops.GATE_VECTOR, beta=_f32(gates.get("beta")),
                                    w_gate=None if gates.get("w") is None else _bf(gates["w"]), b=bgate,
-                                   h0=_f32(initial_state), value_block=vb, state_v_first=vf)
+                                   h0=_f32(initial_state), value_block=vb, state_v_first=vf,
+                                   kg=None if raw else pre["kg"])
             return ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
                              method="direct", value_block=vb, state_v_first=vf)
         (dh, dR, dh0), (h, v_new, _) = _side_by_side(state, scan)

@@ -519,7 +519,9 @@ struct FwdWySmem {
 // prepare_wu_kernel rounds it), and nothing but h, v_new (and the final state) is written.
 // NOST (fdr_fwd_h_u with w NULL): w, u and kg all formed here, and again only h, v_new (and
 // the final state) written: no q read, no w / qg / kg stored.
-template <int BV, int GATE, bool VEC_B, bool MAP, bool WG = false, bool NOST = false>
+// KGIN (WG, vector gate): k is kg as fdr_prepare_wu wrote it (one row per value head), read
+// instead of formed -- at narrow value tiles, where every tile would form it again.
+template <int BV, int GATE, bool VEC_B, bool MAP, bool WG = false, bool NOST = false, bool KGIN = false>
 __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const bf16* __restrict__ bgate,
@@ -529,6 +531,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     int vf, int HQ, const int* __restrict__ cu, const bf16* __restrict__ w_in = nullptr) {
   static_assert(!VEC_B || GATE == RG_VECTOR, "vector b / w_gate come with the vector gate (GDN2)");
   static_assert(!(WG && NOST), "w given or formed, not both");
+  static_assert(!KGIN || (WG && GATE == RG_VECTOR), "kg read: the vector gate's u-only scan");
   constexpr bool VEC = GATE == RG_VECTOR;
   using S = FwdWySmem<BV>;
   __shared__ S sm;
@@ -591,17 +594,19 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
     } else if constexpr (VEC) {
       // lambda's column (tid < KD), and g_last of this thread's 8 columns (both pieces)
       rg_last = g[kofs + (size_t)rs_.clamp(C - 1) * rsk + (tid & (KD - 1))];
-      const float* gl = g + kofs + (size_t)rs_.clamp(C - 1) * rsk + 8 * (tid & 15);
-      rgl0 = *reinterpret_cast<const f32x4*>(gl);
-      rgl1 = *reinterpret_cast<const f32x4*>(gl + 4);
+      if constexpr (!KGIN) {
+        const float* gl = g + kofs + (size_t)rs_.clamp(C - 1) * rsk + 8 * (tid & 15);
+        rgl0 = *reinterpret_cast<const f32x4*>(gl);
+        rgl1 = *reinterpret_cast<const f32x4*>(gl + 4);
+      }
     }
-    const QKRows kr_ = qk_rows(tok0, h, H, HQ);
+    const QKRows kr_ = KGIN ? QKRows{kofs, rsk} : qk_rows(tok0, h, H, HQ);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = tid + NTH * i, t = p >> 4, c8 = 8 * (p & 15);
       if constexpr (WG) {
         rq[i] = *reinterpret_cast<const u32x4*>(rs_.src(w_in + kofs + (size_t)t * rsk + c8, t));   // w rows
-        if constexpr (VEC) {
+        if constexpr (VEC && !KGIN) {
           rg0[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8);
           rg1[i] = *reinterpret_cast<const f32x4*>(g + kofs + (size_t)rs_.clamp(t) * rsk + c8 + 4);
         }
@@ -643,7 +648,9 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       if constexpr (WG) {
         // w as given, kg formed (the scalar gate's as fdr_fwd_h forms it); no E
         *reinterpret_cast<u32x4*>(&sm.w[pb][t][8 * ch]) = rq[i];
-        if constexpr (VEC) {
+        if constexpr (KGIN) {
+          kg = kx;
+        } else if constexpr (VEC) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const float gj = j < 4 ? rg0[i][j] : rg1[i][j - 4];
@@ -745,7 +752,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       settle(ra[i]);
       if constexpr (WG) {
         settle(rq[i]);
-        if constexpr (VEC) {
+        if constexpr (VEC && !KGIN) {
           settle(rg0[i]);
           settle(rg1[i]);
         }
@@ -766,7 +773,7 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
       if constexpr (VEC_B) settle(rwg[i]);
       else settle(rb_v[i]);
     }
-    if constexpr (VEC) {
+    if constexpr (VEC && !KGIN) {
       settle(rgl0);
       settle(rgl1);
     }
@@ -877,14 +884,15 @@ __global__ __launch_bounds__(512) void fwd_h_wy_kernel(
   }
 }
 
-template <int BV, int GATE, bool VEC_B, bool WG = false, bool NOST = false>
+template <int BV, int GATE, bool VEC_B, bool WG = false, bool NOST = false, bool KGIN = false>
 static hipError_t launch_fwd_h_wy(const void* q, const void* k, const void* v, const float* g, const float* beta,
                                   const void* bg, const void* wg, const float* akk, const float* h0, void* w,
                                   void* qg, void* kg, void* h, void* vnew, float* ht, int B, int T, int H,
                                   hipStream_t s, const int* co, int vf, int HQ, const int* cu,
                                   const void* w_in = nullptr) {
 #define FW_LAUNCH(MAP)                                                                                             \
-  hipLaunchKernelGGL((fwd_h_wy_kernel<BV, GATE, VEC_B, MAP, WG, NOST>), dim3(B * H * (VD / BV)), dim3(512), 0, s,  \
+  hipLaunchKernelGGL((fwd_h_wy_kernel<BV, GATE, VEC_B, MAP, WG, NOST, KGIN>), dim3(B * H * (VD / BV)), dim3(512), 0, \
+                     s,                                                                                           \
                      (const bf16*)q, (const bf16*)k, (const bf16*)v, g, beta, (const bf16*)bg, (const bf16*)wg, akk, \
                      h0, (bf16*)w, (bf16*)qg, (bf16*)kg, (bf16*)h, (bf16*)vnew, ht, T, H, co, vf, HQ, cu,        \
                      (const bf16*)w_in)
@@ -1104,14 +1112,19 @@ extern "C" hipError_t fdr_fwd_h_wy(const void* q, const void* k, const void* v, 
 
 // The forward scan with u formed in-kernel from v (and beta or w_gate) and Akk, w given:
 // B rows of T tokens, or (co[, cu]) packed sequences as for fwd_h_dispatch
-static hipError_t fwd_h_u_dispatch(const void* k, const void* w, const void* v, const float* g, int gate_mode,
-                                   const float* beta, const void* b_gate, const void* w_gate, const float* Akk,
-                                   const float* h0, void* h, void* v_new, float* ht, int B, int T, int H, int HQ,
-                                   int K, int V, int chunk, int value_block, hipStream_t stream, const int* co, int vf,
-                                   const int* cu) {
+static hipError_t fwd_h_u_dispatch(const void* k, const void* kg, const void* w, const void* v, const float* g,
+                                   int gate_mode, const float* beta, const void* b_gate, const void* w_gate,
+                                   const float* Akk, const float* h0, void* h, void* v_new, float* ht, int B, int T,
+                                   int H, int HQ, int K, int V, int chunk, int value_block, hipStream_t stream,
+                                   const int* co, int vf, const int* cu) {
   if (K != KD || V != VD || chunk != C || T <= 0 || T % C || B <= 0 || H <= 0) return hipErrorInvalidValue;
   if (HQ <= 0) HQ = H;
   if (H % HQ) return hipErrorInvalidValue;
+  if (kg && (gate_mode != RG_VECTOR || !w)) return hipErrorInvalidValue;   // kg read: vector gate, w given
+  if (kg) {
+    k = kg;            // one row per value head
+    HQ = H;
+  }
   if (!k || !v || !Akk || !h || !v_new) return hipErrorInvalidValue;
   const bool vec_b = w_gate != nullptr;
   if (vec_b && gate_mode != RG_VECTOR) return hipErrorInvalidValue;
@@ -1134,6 +1147,17 @@ static hipError_t fwd_h_u_dispatch(const void* k, const void* w, const void* v, 
                       : launch_fwd_h_wy<64, G, VB, false, true>(FU_ARGS);                     \
     default: return hipErrorInvalidValue;                                                     \
   }
+#define FU_KG(VB)                                                                             \
+  switch (bv) {                                                                               \
+    case 16: return launch_fwd_h_wy<16, RG_VECTOR, VB, true, false, true>(FU_ARGS);          \
+    case 32: return launch_fwd_h_wy<32, RG_VECTOR, VB, true, false, true>(FU_ARGS);          \
+    case 64: return launch_fwd_h_wy<64, RG_VECTOR, VB, true, false, true>(FU_ARGS);          \
+    default: return hipErrorInvalidValue;                                                     \
+  }
+  if (kg) {
+    if (vec_b) FU_KG(true)
+    FU_KG(false)
+  }
   switch (gate_mode) {
     case RG_NONE: FU_BV(RG_NONE, false)
     case RG_SCALAR: FU_BV(RG_SCALAR, false)
@@ -1142,16 +1166,18 @@ static hipError_t fwd_h_u_dispatch(const void* k, const void* w, const void* v, 
       FU_BV(RG_VECTOR, false)
     default: return hipErrorInvalidValue;
   }
+#undef FU_KG
 #undef FU_BV
 #undef FU_ARGS
 }
 
-extern "C" hipError_t fdr_fwd_h_u(const void* k, const void* w, const void* v, const float* g, int gate_mode,
-                                  const float* beta, const void* b_gate, const void* w_gate, const float* Akk,
-                                  const float* h0, void* h, void* v_new, float* ht, int state_v_first, int B, int T,
-                                  int H, int k_heads, int K, int V, int chunk, int value_block, hipStream_t stream) {
-  return fwd_h_u_dispatch(k, w, v, g, gate_mode, beta, b_gate, w_gate, Akk, h0, h, v_new, ht, B, T, H, k_heads, K, V,
-                          chunk, value_block, stream, nullptr, state_v_first ? 1 : 0, nullptr);
+extern "C" hipError_t fdr_fwd_h_u(const void* k, const void* kg, const void* w, const void* v, const float* g,
+                                  int gate_mode, const float* beta, const void* b_gate, const void* w_gate,
+                                  const float* Akk, const float* h0, void* h, void* v_new, float* ht, int state_v_first,
+                                  int B, int T, int H, int k_heads, int K, int V, int chunk, int value_block,
+                                  hipStream_t stream) {
+  return fwd_h_u_dispatch(k, kg, w, v, g, gate_mode, beta, b_gate, w_gate, Akk, h0, h, v_new, ht, B, T, H, k_heads,
+                          K, V, chunk, value_block, stream, nullptr, state_v_first ? 1 : 0, nullptr);
 }
 
 extern "C" hipError_t fdr_fwd_h_wy_varlen(const void* q, const void* k, const void* v, const float* g, int gate_mode,

@@ -393,12 +393,13 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
 
   // global stores of dh[c] and dR_c from the transposed LDS copies: per wave task a block of
   // 16 columns (dh rows k / dR rows t) by 32 value rows, 16-lane group g taking 8 of them
-  // (two transposed reads per 16-byte piece; narrower tiles repeat a group's rows, and waves
-  // beyond the tasks repeat a task, with the same data).  Every wave issues the same number
-  // of stores, and the loop is entered with as many (sink: to the sink page) issued after the
-  // first chunk's loads as each step issues after the next chunk's: the vector-memory wait
-  // counts are then the same on both paths into a step, so its staging waits only for its
-  // own loads, not for the previous step's stores.  (Sink stores: one 16-byte slot each, at
+  // (two transposed reads per 16-byte piece; narrower tiles repeat a group's rows, with the
+  // same data; waves beyond the tasks skip, wave-uniform).  The loop is entered with as many
+  // stores (sink: to the sink page) issued after the first chunk's loads as each step issues
+  // after the next chunk's: where every wave has a task (64-wide tiles), the vector-memory wait
+  // counts are then the same on both paths into a step, so its staging waits only for its own
+  // loads, not for the previous step's stores.  (Narrower tiles keep waves without a task: a
+  // split of each task over more waves, to keep the counts static there, measured slower.)  (Sink stores: one 16-byte slot each, at
   // most 3 per step here, so that none overwrites another and is dropped.)
   static_assert((KD / 16) * (BV >= 32 ? BV / 32 : 1) <= 2 * NW && (C / 16) * (BV >= 32 ? BV / 32 : 1) <= NW,
                 "at most 3 stores per step, one sink-page slot each");
@@ -410,7 +411,8 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     constexpr int NTK = (KD / 16) * RQ;
 #pragma unroll
     for (int i = 0; i < (NTK + NW - 1) / NW; ++i) {
-      const int tk = (wv + NW * i) % NTK;
+      const int tk = wv + NW * i;
+      if (NTK % NW != 0 && tk >= NTK) break;
       const int kr0 = 16 * (tk % (KD / 16)), v0 = 8 * ((4 * (tk / (KD / 16)) + g4) % RB);
       const bf16x8 o = col8_tr(&sm.dhT[db][0][0], S::LDK, v0, kr0, l);
       bf16* dst = dh_out + dh_base + (size_t)(kr0 + (l & 15)) * VD + v_base + v0;
@@ -421,7 +423,8 @@ __global__ __launch_bounds__(64 * NW) void state_bwd_kernel(
     constexpr int NTR = (C / 16) * RQ;
 #pragma unroll
     for (int i = 0; i < (NTR + NW - 1) / NW; ++i) {
-      const int tk = (wv + NW * i) % NTR;
+      const int tk = wv + NW * i;
+      if (NTR % NW != 0 && tk >= NTR) break;
       const int t = 16 * (tk % (C / 16)) + (l & 15), v0 = 8 * ((4 * (tk / (C / 16)) + g4) % RB);
       const bf16x8 o = col8_tr(&sm.drT[0][0], S::LDT, v0, t - (l & 15), l);
       bf16* dst = rs_.dst(dr_out + (tok0 + t) * row_stride_v + (size_t)h * VD + v_base + v0, t);

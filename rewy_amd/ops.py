@@ -95,8 +95,10 @@ PAIRED = True
 PAIRED_MIN_BH = 24
 # ... with u formed inside the scan (fwd_h_u) instead of written by prepare_wu and read back
 PAIRED_U = True
-# ... and, vector gates, with qg / kg formed from the raw q / k where each recurrence stages a
-# chunk (fdr_state_bwd_raw_qk, fwd_h_u) instead of written by prepare_wu and read back
+# ... and, vector gates at 64-wide tiles, with qg / kg formed from the raw q / k where each
+# recurrence stages a chunk (fdr_state_bwd_raw_qk, fwd_h_u) instead of written by prepare_wu and
+# read back.  (At 32-wide tiles every one of a head's four value tiles would form them again:
+# measured slower there.)
 PAIRED_RAW = True
 # ... and, GDN2 (a vector b) at 64-wide tiles, w formed in both recurrences too (w = Akk (b k 2^g)
 # from the same staged k and gate tile), so that fdr_prepare_wu does not run at all.  (KDA's
@@ -798,13 +800,14 @@ def group_sum(x, HQ):
 
 
 def fwd_h_u(k, w, v, Akk, g, gate_mode, beta=None, w_gate=None, h0=None, want_final=False, value_block=0,
-            state_v_first=False, b=None):
+            state_v_first=False, b=None, kg=None):
     """``fwd_h`` with u formed in-kernel (fdr_fwd_h_u): u = Akk (beta v), or Akk (w_gate v) for
     GDN2, from the same MFMA sequence as ``prepare_wu``, so h, v_new and the final state are
     the bits of ``prepare_wu`` + ``fwd_h``.  k is the raw k (a vector gate's kg formed in-kernel
     with ``prepare_wu``'s rounding); w as ``prepare_wu(..., want_u=False)`` returns it, or None:
     then w = Akk (beta k 2^g), or Akk (b k 2^g) for GDN2 (``b``), is formed in-kernel too, as
-    ``prepare_wu`` forms it.  Returns (h, v_new, final|None)."""
+    ``prepare_wu`` forms it.  ``kg`` (vector gate, w given): ``prepare_wu``'s kg, read instead
+    of formed (k is then not read).  Returns (h, v_new, final|None)."""
     B, T, HQ, K = _dims(k)
     H, HQ = _group(v.shape[2] if v is not None and v.ndim == 4 else HQ, HQ)
     V = V_SUPPORTED
@@ -815,6 +818,10 @@ def fwd_h_u(k, w, v, Akk, g, gate_mode, beta=None, w_gate=None, h0=None, want_fi
         _need(w, "w", bf, (B, T, H, K), dev)
     elif w_gate is not None:
         _need(b, "b", bf, (B, T, H, K), dev)
+    if kg is not None:
+        if gate_mode != GATE_VECTOR or w is None:
+            raise ValueError("kg is read for a vector gate with w given")
+        _need(kg, "kg", bf, (B, T, H, K), dev)
     _need(v, "v", bf, (B, T, H, V), dev)
     _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
     if gate_mode == GATE_VECTOR:
@@ -838,7 +845,7 @@ def fwd_h_u(k, w, v, Akk, g, gate_mode, beta=None, w_gate=None, h0=None, want_fi
     vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
     ht = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_final else None
     P = _lib.ptr
-    st = _lib.load().fdr_fwd_h_u(P(k), P(w), P(v), P(g), int(gate_mode), P(beta), P(b if w is None else None),
+    st = _lib.load().fdr_fwd_h_u(P(k), P(kg), P(w), P(v), P(g), int(gate_mode), P(beta), P(b if w is None else None),
                                  P(w_gate), P(Akk), P(h0), P(h), P(vnew), P(ht), int(bool(state_v_first)), B, T, H,
                                  HQ, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_h_u")

@@ -60,6 +60,13 @@ def test_fwd_h_u_equals_prepare_then_fwd_h(op, vb):
         torch.cuda.synchronize()
         for n, a, r in zip(("h", "v_new", "final"), got, ref):
             assert torch.equal(a, r), (op, vb, vf, n)
+        if vec:     # kg read as prepare_wu wrote it
+            got = ops.fwd_h_u(d["k"], part["w"], d["v"], d["Akk"], d["gc"], gate, beta=d.get("beta"),
+                              w_gate=d.get("w"), h0=h0, want_final=True, value_block=vb, state_v_first=vf,
+                              kg=full["kg"])
+            torch.cuda.synchronize()
+            for n, a, r in zip(("h", "v_new", "final"), got, ref):
+                assert torch.equal(a, r), (op, vb, vf, "kg read", n)
         # w formed in the scan too (no prepare_wu)
         got = ops.fwd_h_u(d["k"], None, d["v"], d["Akk"], d["gc"], gate, beta=d.get("beta"), w_gate=d.get("w"),
                           b=d.get("b"), h0=h0, want_final=True, value_block=vb, state_v_first=vf)

@@ -219,9 +219,9 @@ def test_seam_and_pairing_entry_points_reject_bad_arguments_without_touching_the
     from rewy_amd import _lib
     lib = _lib.load()
     # K = 64 everywhere (only 128 supported), or no chunks / no row map
-    assert lib.fdr_fwd_h_u(*([None] * 4), 2, *([None] * 8), 0, 1, 128, 1, 1, 64, 128, 64, 0,
+    assert lib.fdr_fwd_h_u(*([None] * 5), 2, *([None] * 8), 0, 1, 128, 1, 1, 64, 128, 64, 0,
                            None) == HIP_ERROR_INVALID_VALUE
-    assert lib.fdr_fwd_h_u(*([None] * 4), 2, *([None] * 8), 0, 1, 128, 1, 1, 128, 128, 64, 0,
+    assert lib.fdr_fwd_h_u(*([None] * 5), 2, *([None] * 8), 0, 1, 128, 1, 1, 128, 128, 64, 0,
                            None) == HIP_ERROR_INVALID_VALUE            # null operands
     assert lib.fdr_state_bwd_raw_qk(*([None] * 13), 0, 1, 128, 1, 1, 64, 128, 64, 1.0, 0,
                                     None) == HIP_ERROR_INVALID_VALUE   # K = 64
