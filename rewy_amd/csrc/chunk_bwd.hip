@@ -54,9 +54,13 @@ namespace rewy {
 enum GateModeC { CG_NONE = 0, CG_SCALAR = 1, CG_VECTOR = 2 };
 
 // Persistent, prefetching chunk kernel for the scalar / no-gate families (1), also
-// for KDA (2: measured slower, kept for A/B), or never (0)
+// for KDA (2), or never (0, the default).  It had taken GDN's chunk kernel from 0.57 to
+// 0.44 ms when the one-work-group-per-chunk-head form waited for every load at each barrier;
+// since that form's LDS-only barriers and heads-fastest item order it is the faster one for
+// every family and size measured (GDN B=8 T=4096 H=16 chunk kernel 442 vs 449 us, B=1 T=2048
+// H=16 DeltaNet backward 116 vs 120 us under graph replay): kept as a build option for A/B.
 #ifndef REWY_CHUNK_PIPE
-#define REWY_CHUNK_PIPE 1
+#define REWY_CHUNK_PIPE 0
 #endif
 
 namespace post {
