@@ -1,5 +1,6 @@
 """The C-ABI library: loads, exports every symbol include/rewy_amd.h declares,
 and validates arguments on the host (no GPU needed for any of these calls)."""
+import ctypes
 import re
 from pathlib import Path
 
@@ -229,6 +230,19 @@ def test_seam_and_pairing_entry_points_reject_bad_arguments_without_touching_the
                                     None) == HIP_ERROR_INVALID_VALUE   # null operands
     assert lib.fdr_state_bwd_raw_qk(*([None] * 13), 0, 1, 100, 1, 1, 128, 128, 64, 1.0, 0,
                                     None) == HIP_ERROR_INVALID_VALUE   # T not whole chunks
+    fake = ctypes.c_void_p(256)          # never dereferenced: each call is rejected before any launch
+    # fdr_fwd_h_u: kg is read only for a vector gate with w given
+    assert lib.fdr_fwd_h_u(fake, fake, fake, fake, fake, 1, fake, None, None, fake, None, fake, fake, None, 0, 1, 128,
+                           1, 1, 128, 128, 64, 0, None) == HIP_ERROR_INVALID_VALUE     # scalar gate
+    assert lib.fdr_fwd_h_u(fake, fake, None, fake, fake, 2, fake, None, None, fake, None, fake, fake, None, 0, 1, 128,
+                           1, 1, 128, 128, 64, 0, None) == HIP_ERROR_INVALID_VALUE     # w NULL
+    # fdr_state_bwd_raw_qk with w formed: exactly one of beta / b_gate, and Akk
+    assert lib.fdr_state_bwd_raw_qk(fake, fake, None, fake, fake, fake, fake, fake, fake, None, fake, fake, None, 0,
+                                    1, 128, 1, 1, 128, 128, 64, 1.0, 0, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fdr_state_bwd_raw_qk(fake, fake, None, fake, None, None, fake, fake, fake, None, fake, fake, None, 0,
+                                    1, 128, 1, 1, 128, 128, 64, 1.0, 0, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fdr_state_bwd_raw_qk(fake, fake, None, fake, fake, None, None, fake, fake, None, fake, fake, None, 0,
+                                    1, 128, 1, 1, 128, 128, 64, 1.0, 0, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fdr_group_sum(None, None, 16, 2, 2, 64, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fdr_group_sum(None, None, 0, 2, 2, 128, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fdr_gdn2_chunk_bwd_wy(*([None] * 19), 0, 1, 128, 1, 64, 128, 64, 1.0, None) == HIP_ERROR_INVALID_VALUE
