@@ -72,6 +72,8 @@ def _check_common(kind, kw):
 
 
 def _bf(x):
+    if x.dtype is torch.bfloat16 and x.is_contiguous():      # (the common case, without a call into torch)
+        return x
     return x.to(torch.bfloat16).contiguous()
 
 
@@ -88,7 +90,9 @@ def _group_sum(out, HQ):
 
 
 def _f32(x):
-    return None if x is None else x.to(torch.float32).contiguous()
+    if x is None or (x.dtype is torch.float32 and x.is_contiguous()):
+        return x
+    return x.to(torch.float32).contiguous()
 
 
 _SIDE = {}
