@@ -152,3 +152,44 @@ def test_paired_under_graph_capture(op):
             assert torch.equal(a, r), (op, rep, i)
         run()          # eager work between the replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("op,HV,HQ", [("kda", 48, 12), ("kda", 32, 8), ("gdn", 48, 12), ("gdn2", 48, 48)])
+def test_paired_grouped_heads_and_absent_states(op, HV, HQ, monkeypatch):
+    """Grouped value heads (q / k with HQ heads) through the paired recurrences -- the raw q / k
+    forms at 64-wide tiles, prepare_wu's qg / kg at 32-wide ones -- and GDN2's prepare-free form
+    with no initial state and no final-state gradient: the public backward against the
+    policy switched off (the recurrences one after the other), rel-L2 <= 1e-5."""
+    import rewy_amd as fdr
+    from rewy_amd import ops
+    B, T = 1, 256
+    print(f"\n[paired-gva] op={op} HV={HV} HQ={HQ}", flush=True)
+    assert ops.paired_tile(B, HV, T // 64, GATE[op])
+    xs, dO = make_inputs(op, B, T, HV, seed=53, gate="mild" if op in ("kda", "gdn2") else "default",
+                         h0=op != "gdn2")
+    if HQ != HV:
+        xs["q"], xs["k"] = xs["q"][:, :, ::HV // HQ].contiguous(), xs["k"][:, :, ::HV // HQ].contiguous()
+    dev = torch.device("cuda")
+    kw = dict(disable_recompute=False) if op in ("kda", "gdn2") else {}
+
+    def run():
+        xg = {n: v.to(dev).requires_grad_() for n, v in xs.items()}
+        with fdr.use_backend("optimized", ops=(op,)):
+            o, ht = getattr(fdr, OPNAME[op])(**xg, output_final_state=True, **kw)
+        outs = (o,) if op == "gdn2" else (o, ht)      # gdn2: no final-state gradient
+        gouts = (dO.to(dev),) if op == "gdn2" else (dO.to(dev), torch.full_like(ht, 0.01))
+        grads = torch.autograd.grad(outs, tuple(xg.values()), gouts)
+        torch.cuda.synchronize()
+        return grads
+
+    from rewy_amd.backends import backward as bw
+    calls = []
+    real = bw._side_by_side
+    monkeypatch.setattr(bw, "_side_by_side", lambda a, b: (calls.append(1), real(a, b))[1])
+    got = run()
+    assert calls, "the paired recurrences did not run"
+    monkeypatch.setattr(ops, "PAIRED", False)
+    off = run()
+    for name, a, r in zip(xs, got, off):
+        e = _rel(a, r)
+        assert e <= 1e-5, (op, name, e)
