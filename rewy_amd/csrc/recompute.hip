@@ -12,6 +12,9 @@
 //     Aqk = scale tril(q k^T 2^(g_i - g_s))        (scalar / no gate, optional)
 //   fdr_fwd_h (sequential over chunks, one work-group per (batch, head, value tile)):
 //     h_c -> h[c] (bf16); v_new_c = u_c - w_c h_c (bf16); h_{c+1} = lambda_c h_c + kg_c^T v_new_c
+//   fdr_fwd_h_wy: the two in one sweep (w, u formed one chunk ahead inside the scan);
+//   fdr_fwd_h_u: the same sweep storing only h / v_new, with w read (or formed) and u and
+//     a vector gate's kg formed (or kg read) -- the paired recurrences' scan
 //
 // The WY products are computed transposed (w^T = E^T A^T) so the accumulator
 // layout stores w and u contiguously; A and E are split into bf16 hi + lo (16

@@ -15,7 +15,8 @@
 // as they sit in HBM (coalesced 16-byte loads, one ds_write_b128 per piece);
 // the contractions over tokens read them transposed with ds_read_b64_tr_b16.
 // Operands of the next chunk are fetched into registers while the current
-// chunk computes.
+// chunk computes.  qg / kg (and w) may instead be formed from the raw q / k (and
+// Akk, beta | b) as each chunk is staged: fdr_state_bwd_raw_qk.
 #include "common.hpp"
 #include "rewy_amd.h"
 
