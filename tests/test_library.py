@@ -251,3 +251,20 @@ def test_seam_and_pairing_entry_points_reject_bad_arguments_without_touching_the
     assert lib.fdr_chunk_bwd_wy_varlen(*([None] * 17), 0, None, None, 2, 1, 1, 128, 128, 64, 1.0,
                                        None) == HIP_ERROR_INVALID_VALUE
     assert lib.fdr_matrix_intra_varlen(*([None] * 13), 0, 1, 1, 128, 64, 0, None) == HIP_ERROR_INVALID_VALUE
+
+
+def test_integration_guide_ctypes_lines_match_the_bindings():
+    """Every `lib.<entry>.argtypes = ...` line INTEGRATION.md shows a maintainer is the
+    signature this package binds (rewy_amd/_lib.py), which test_header_and_ctypes_table_agree ties
+    to include/rewy_amd.h."""
+    import ctypes
+    from rewy_amd import _lib
+    env = {"P": ctypes.c_void_p, "I": ctypes.c_int, "F": ctypes.c_float, "ctypes": ctypes}
+    pat = re.compile(r"lib\.(fdr_\w+)\.argtypes = (\[[^`]*?\](?:\s*[\*\+]\s*(?:\d+|\[[^`\]]*\]))*)")
+    seen = 0
+    for line in (ROOT / "INTEGRATION.md").read_text().splitlines():
+        for name, expr in pat.findall(line):
+            assert name in _lib.SIGNATURES, name
+            assert list(eval(expr, env)) == list(_lib.SIGNATURES[name]), name
+            seen += 1
+    assert seen >= 10
