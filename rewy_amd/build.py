@@ -25,9 +25,6 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", str(HERE.parent / "include"),
 ]
-# per-source extras: the KDA chunk kernel with LLVM's max-ilp machine scheduler (measured faster
-# for it, slower for the other families' chunk kernels, which chunk_bwd.hip builds)
-FILE_FLAGS = {"chunk_bwd_kda.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
 
 
 def hipcc() -> str:
@@ -40,7 +37,7 @@ def hipcc() -> str:
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
     extra = os.environ.get("REWY_HIPCC_FLAGS", "").split()   # e.g. -DREWY_CHUNK_PIPE=2
-    cmd = [hipcc(), *FLAGS, *FILE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr[-4000:]}")

@@ -49,14 +49,6 @@
 #include "common.hpp"
 #include "rewy_amd.h"
 
-// chunk_bwd_kda.hip includes this file with REWY_CHUNK_KDA_TU = 1 to build only the KDA kernel
-// (vector gate, scalar beta, K-first states, dense rows; launch_chunk_kda) in a translation unit
-// of its own, which build.py compiles with LLVM's max-ilp machine scheduler: measured 2 % faster
-// for that kernel (542.6 vs 554.5 us at B=8 T=4096 H=16) and 1-2 % slower for GDN's and GDN2's.
-#ifndef REWY_CHUNK_KDA_TU
-#define REWY_CHUNK_KDA_TU 0
-#endif
-
 namespace rewy {
 
 enum GateModeC { CG_NONE = 0, CG_SCALAR = 1, CG_VECTOR = 2 };
@@ -1528,31 +1520,6 @@ static hipError_t device_cus(int& cus) {
   return hipSuccess;
 }
 
-// The KDA kernel of fdr_chunk_bwd on dense rows (defined in chunk_bwd_kda.hip's unit)
-hipError_t launch_chunk_kda(const void* q, const void* k, const void* v, const void* vnew, const void* dO,
-                            const void* dR, const float* g, const float* beta, const float* akk, const void* h,
-                            const void* dh, void* dq, void* dk, void* dv, float* dg, float* dbeta, int B, int T,
-                            int H, int HQ, float scale, float beta_sig, hipStream_t s);
-
-#if REWY_CHUNK_KDA_TU
-hipError_t launch_chunk_kda(const void* q, const void* k, const void* v, const void* vnew, const void* dO,
-                            const void* dR, const float* g, const float* beta, const float* akk, const void* h,
-                            const void* dh, void* dq, void* dk, void* dv, float* dg, float* dbeta, int B, int T,
-                            int H, int HQ, float scale, float beta_sig, hipStream_t s) {
-  using LY = PostLayout<CG_VECTOR, false>;
-  auto kern = chunk_bwd_kernel<CG_VECTOR, false, false>;
-  static LdsFlags attr_set = {};
-  const hipError_t e = allow_dynamic_lds((const void*)kern, LY::BYTES, attr_set);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(B * H * (T / C)), dim3(512), LY::BYTES, s, (const bf16*)q, (const bf16*)k,
-                     (const bf16*)v, (const bf16*)vnew, (const bf16*)dO, (const bf16*)dR, g, beta, nullptr, nullptr,
-                     akk, (const bf16*)h, (const bf16*)dh, (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, nullptr,
-                     nullptr, T, H, scale, beta_sig, HQ, nullptr, nullptr);
-  return hipGetLastError();
-}
-}  // namespace rewy
-#else
-
 template <int GATE, bool VEC_B, bool HVF = false>
 static hipError_t launch_post(const void* q, const void* k, const void* v, const void* vnew,
                               const void* dO, const void* dR, const float* g, const float* beta,
@@ -1589,10 +1556,6 @@ static hipError_t launch_post(const void* q, const void* k, const void* v, const
                        (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, (bf16*)db, (bf16*)dw, T, H, scale, items,
                        beta_sig, HQ);
     return hipGetLastError();
-  }
-  if constexpr (GATE == CG_VECTOR && !VEC_B && !HVF) {
-    return launch_chunk_kda(q, k, v, vnew, dO, dR, g, beta, akk, h, dh, dq, dk, dv, dg, dbeta, B, T, H, HQ, scale,
-                            beta_sig, s);
   }
   auto kern = chunk_bwd_kernel<GATE, VEC_B, HVF>;
   static LdsFlags attr_set = {};
@@ -1973,5 +1936,3 @@ extern "C" hipError_t fdr_chunk_bwd_original(const void* q, const void* k, const
                      (const bf16*)h, (const bf16*)dh, (bf16*)dq, (bf16*)dk, (bf16*)dv, dg, dbeta, T, H, scale);
   return hipGetLastError();
 }
-
-#endif  // REWY_CHUNK_KDA_TU
