@@ -146,14 +146,7 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
     Aqk, Akk = _f32(Aqk), _f32(Akk)
     recompute = saved.get("h") is None
     N, H, NT = (q.shape[0], v.shape[2], q.shape[1] // ops.CHUNK) if vl is None else (vl.N, v.shape[2], vl.NC)
-    if recompute and vl is None and ops.affine_pays(v):
-        # few heads: both recurrences side by side in affine-step form
-        pre = _prepare_vector(k, v, g, Akk, gates, q, vl)
-        h, v_new, dh, dR, dh0 = ops.recurrences(pre["qg"], pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR,
-                                                do, scale, aqk=Aqk, h0=_f32(initial_state), dht=_f32(dht),
-                                                want_dh0=initial_state is not None, state_v_first=vf)
-        saved, hvf = dict(v_new=v_new, h=h), False
-    elif recompute and vl is None and ops.paired_tile(N, H, NT, ops.GATE_VECTOR):
+    if recompute and vl is None and ops.paired_tile(N, H, NT, ops.GATE_VECTOR):
         # batch x heads too small for one direct recurrence to fill the GPU: the backward
         # state recurrence and the forward scan side by side, both direct, at a value-tile
         # width that gives each launch at most half the CUs
@@ -184,6 +177,13 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
             return ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
                              method="direct", value_block=vb, state_v_first=vf)
         (dh, dR, dh0), (h, v_new, _) = _side_by_side(state, scan)
+        saved, hvf = dict(v_new=v_new, h=h), False
+    elif recompute and vl is None and ops.affine_pays(v):
+        # few heads: both recurrences side by side in affine-step form
+        pre = _prepare_vector(k, v, g, Akk, gates, q, vl)
+        h, v_new, dh, dR, dh0 = ops.recurrences(pre["qg"], pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR,
+                                                do, scale, aqk=Aqk, h0=_f32(initial_state), dht=_f32(dht),
+                                                want_dh0=initial_state is not None, state_v_first=vf)
         saved, hvf = dict(v_new=v_new, h=h), False
     elif recompute and (ops.side_by_side_pays(N, H, NT) if vl is None else
                         ops.SIDE_BY_SIDE and not ops.fwd_h_wy_pays(N, H, ops.GATE_VECTOR, vl)):

@@ -96,6 +96,10 @@ def side_by_side_pays(B, H, NT):
 # at most one work-group per CU.
 PAIRED = True
 PAIRED_MIN_BH = 24
+# ... and at B*H = 16 (128 work-groups each at 16-wide tiles) for rows of at most 64 chunks,
+# where the pair beats the affine-step form (below that B*H, and on longer rows, it does not)
+PAIRED16_MIN_BH = 16
+PAIRED16_MAX_NT = 64
 # ... with u formed inside the scan (fwd_h_u) instead of written by prepare_wu and read back
 PAIRED_U = True
 # ... and, vector gates at 64-wide tiles, with qg / kg formed from the raw q / k where each
@@ -114,19 +118,27 @@ def paired_tile(B, H, NT, gate_mode):
     """Value-tile width at which the recompute policy runs ``fwd_h`` and ``state_bwd`` (both
     direct) side by side, or 0 when it runs them otherwise: for 24 <= B H <= 64, the
     narrowest of 32 / 64 at which each launch has at most 128 work-groups (the two together
-    one per CU).  Measured (MI355X): GDN2 B=2 T=8192 H=32 both recurrences 0.451 ms paired at
+    one per CU); at B H = 16, 16-wide tiles for rows of at most 64 chunks.  Measured (MI355X):
+    GDN2 B=2 T=8192 H=32 both recurrences 0.451 ms paired at
     64-wide tiles vs 0.544 one after the other at 32-wide; B=2 T=4096 H=16 0.177 (32-wide) vs
     0.231; B=1 T=8192 H=48 0.443 vs 0.543; B=1 T=16384 H=24 0.639 (32-wide) vs 0.905.  The
     scalar / no-gate families, whose fused sweep (``fwd_h_wy_pays``) runs from B H = 64: GDN
     B=4 T=2048 H=16 backward 0.288 ms paired (64-wide, u formed in the scan) vs 0.311 with the
     sweep, DeltaNet same shape 0.261 vs 0.279; DeltaNet B=2 T=2048 H=16 (graph replay)
-    148.6 us paired (32-wide) vs 178.4 us."""
+    148.6 us paired (32-wide) vs 178.4 us.  At B H = 16 against the affine-step form (graph
+    replay, backward): B=1 T=2048 H=16 DeltaNet 97 vs 112 us, GDN 113 vs 117, KDA 112 vs 129,
+    GDN2 122 vs 138; T=4096 DeltaNet 179 vs 199, KDA 226 vs 236 (GDN, GDN2 within 1.5 %);
+    T=8192 GDN 447 vs 421 (so not past 64 chunks); B H = 4 the affine-step form by 12-60 %."""
     BH = B * H
-    if not PAIRED or BH < PAIRED_MIN_BH or NT < 1:
+    if not PAIRED or NT < 1:
         return 0
-    for vb in (32, 64):
-        if BH * (V_SUPPORTED // vb) <= 128:
-            return vb
+    if BH >= PAIRED_MIN_BH:
+        for vb in (32, 64):
+            if BH * (V_SUPPORTED // vb) <= 128:
+                return vb
+        return 0
+    if BH >= PAIRED16_MIN_BH and BH * (V_SUPPORTED // 16) <= 128 and NT <= PAIRED16_MAX_NT:
+        return 16
     return 0
 
 

@@ -1,7 +1,7 @@
 """The recompute policy's paired direct recurrences (B*H >= 24 where the fused sweep does not
-pay): the direct backward state recurrence (fdr_state_bwd) on the current stream beside the
-direct forward scan (fdr_fwd_h) on a second stream, both at the value-tile width
-``ops.paired_tile`` picks (32 at B*H = 32, 64 at B*H = 48).  For all four families (the
+pay, and B*H = 16 on rows of at most 64 chunks): the direct backward state recurrence
+(fdr_state_bwd) on the current stream beside the direct forward scan (fdr_fwd_h) on a second stream, both at the value-tile width
+``ops.paired_tile`` picks (32 at B*H = 32, 64 at B*H = 48, 16 at B*H = 16 with few chunks).  For all four families (the
 scalar / no-gate ones with the state recurrence forming Aqk itself):
 
 * the public autograd backward (recompute policy) against the fp64 oracle at the
@@ -26,7 +26,7 @@ OPNAME = {"kda": "chunk_kda", "gdn2": "chunk_gdn2", "gdn": "chunk_gated_delta_ru
 OPS = ["kda", "gdn2", "gdn", "delta"]
 GATE = {"kda": 2, "gdn2": 2, "gdn": 1, "delta": 0}
 GRAD = {"q": "dq", "k": "dk", "v": "dv", "g": "dg", "beta": "dbeta", "b": "db", "w": "dw", "initial_state": "dh0"}
-SHAPES = [(2, 512, 16, 32), (1, 256, 48, 64)]     # B, T, H, the tile width paired_tile picks
+SHAPES = [(2, 512, 16, 32), (1, 256, 48, 64), (1, 512, 16, 16)]    # B, T, H, the tile width paired_tile picks
 
 
 def _rel(a, r):
@@ -123,6 +123,8 @@ def test_paired_equals_one_stream_and_policy_off(op, B, T, H, vb, monkeypatch):
     for i, (a, r) in enumerate(zip(got, unfolded)):
         assert torch.equal(a, r), (op, "PAIRED_U", i)
     monkeypatch.setattr(ops, "PAIRED", False)
+    # (B*H = 16 would take the affine-step form, whose rounding differs: the direct kernels)
+    monkeypatch.setattr(ops, "AFFINE_MAX_BH", -1)
     off = run()
     torch.cuda.synchronize()
     for i, (a, r) in enumerate(zip(got, off)):
