@@ -313,6 +313,35 @@ hipError_t fdr_fwd_h_u(const void* k, const void* kg, const void* w, const void*
                        int V, int chunk, int value_block, hipStream_t stream);
 
 /*
+ * fdr_state_bwd (direct) and fdr_fwd_h_u in one launch: the reverse state recurrence and the
+ * forward scan forming u, independent of each other, run side by side -- work-groups
+ * [0, n) the state recurrence's, [n, 2n) the scan's, n = B H V / value_block each -- with
+ * the same kernels' code, so every output is the bits of the two calls.  This build's own
+ * composition (no counterpart in the reference, which runs FLA's chunk_gated_delta_rule_fwd_h
+ * and its state kernel one after the other, backends/backward.py:117-121): for batch x heads
+ * too small for one recurrence to fill the GPU, where two launches on two streams would pay
+ * their fork and join.  Dense rows; value_block 16, 32 or 64 (required).
+ *   q, k: the state recurrence's q / k -- raw (qk_heads heads) for gate_mode 0 / 1 and with
+ *         raw_qk, else fdr_prepare_wu's qg / kg [B,T,H,K];
+ *   k_scan: the raw k (qk_heads heads) the scan forms kg / E from; kg: fdr_prepare_wu's kg,
+ *         read by the scan instead (vector gate without raw_qk; k_scan is then not read);
+ *   w: fdr_prepare_wu's w, or NULL (vector gate with raw_qk: w formed in both, from beta or
+ *      b_gate, as fdr_state_bwd_raw_qk / fdr_fwd_h_u form it);
+ *   gate_mode 0 / 1: aqk NULL (Aqk formed by the state recurrence), w given, raw_qk 0;
+ *   gate_mode 2: aqk given; raw_qk only at value_block 64;
+ *   beta fp32 [B,T,H] or GDN2's w_gate bf16 [B,T,H,V] (and b_gate when w is NULL);
+ *   v, Akk, h0 (may be null), h, v_new, ht (may be null): as fdr_fwd_h_u;
+ *   dO, dht (may be null), dh, dr, dh0 (may be null), scale: as fdr_state_bwd.
+ */
+hipError_t fdr_paired_recurrences(const void* q, const void* k, const void* w, const void* k_scan, const void* kg,
+                                  const float* g, int gate_mode, const float* beta, const void* b_gate,
+                                  const void* w_gate, const void* v, const float* Akk, const float* aqk,
+                                  const void* dO, const float* dht, const float* h0, void* dh, void* dr, float* dh0,
+                                  void* h, void* v_new, float* ht, int raw_qk, int state_v_first, int B, int T, int H,
+                                  int qk_heads, int K, int V, int chunk, float scale, int value_block,
+                                  hipStream_t stream);
+
+/*
  * The recompute pair fdr_prepare_wu + fdr_fwd_h in one sweep.  Replaces FLA
  * recompute_w_u_fwd(k, v, beta, A, g) -> (w, u) [, qg, kg] followed by
  * chunk_gated_delta_rule_fwd_h(k, w, u, g, initial_state) -> (h, v_new, final), as called at

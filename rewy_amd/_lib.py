@@ -26,6 +26,7 @@ SIGNATURES = {
     "fdr_prepare_wu": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P],
     "fdr_fwd_h": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P],
     "fdr_fwd_h_u": [_P] * 5 + [_I] + [_P] * 8 + [_I] * 9 + [_P],
+    "fdr_paired_recurrences": [_P] * 6 + [_I] + [_P] * 15 + [_I] * 9 + [_F, _I, _P],
     "fdr_state_bwd_varlen": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
                              _I, _P],
     "fdr_fwd_h_varlen": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P],

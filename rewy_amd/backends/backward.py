@@ -176,7 +176,15 @@ def _vector(op, q, k, v, gates, Aqk, Akk, scale, initial_state, do, dht, g, save
                                    kg=None if raw else pre["kg"])
             return ops.fwd_h(pre["kg"], pre["w"], pre["u"], g, ops.GATE_VECTOR, h0=_f32(initial_state),
                              method="direct", value_block=vb, state_v_first=vf)
-        (dh, dR, dh0), (h, v_new, _) = _side_by_side(state, scan)
+        if fold_u and ops.PAIRED_ONE_LAUNCH:
+            # both in one launch (the same kernels' bodies, no second stream)
+            (dh, dR, dh0), (h, v_new, _) = ops.paired_recurrences(
+                q, k, pre["w"], g, ops.GATE_VECTOR, do, scale, v, Akk, vb, aqk=Aqk, beta=_f32(gates.get("beta")),
+                b=bgate, w_gate=None if gates.get("w") is None else _bf(gates["w"]),
+                qg=None if raw else pre["qg"], kg=None if raw else pre["kg"], raw_qk=raw, h0=_f32(initial_state),
+                dht=_f32(dht), want_dh0=initial_state is not None, state_v_first=vf)
+        else:
+            (dh, dR, dh0), (h, v_new, _) = _side_by_side(state, scan)
         saved, hvf = dict(v_new=v_new, h=h), False
     elif recompute and vl is None and ops.affine_pays(v):
         # few heads: both recurrences side by side in affine-step form
@@ -331,6 +339,11 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
                              state_v_first=state_v_first, value_block=vb)
         if pre is None:
             dh, dR, dh0 = state()
+        elif vb and pre["u"] is None and ops.PAIRED_ONE_LAUNCH:
+            # both recurrences in one launch (the same kernels' bodies, no second stream)
+            (dh, dR, dh0), (h, v_new, _) = ops.paired_recurrences(
+                q, k, w, g, gate, do, scale, v, A, vb, beta=beta, h0=_f32(initial_state), dht=_f32(dht),
+                want_dh0=initial_state is not None, state_v_first=state_v_first)
         elif vb:
             # the state recurrence (the longer chain) first, the scan on the side stream
             (dh, dR, dh0), (h, v_new, _) = _side_by_side(state, scan)

@@ -100,6 +100,9 @@ PAIRED_MIN_BH = 24
 # where the pair beats the affine-step form (below that B*H, and on longer rows, it does not)
 PAIRED16_MIN_BH = 16
 PAIRED16_MAX_NT = 64
+# ... as one launch (fdr_paired_recurrences) instead of two kernels on two streams joined by
+# events, whose fork and join cost ~25 us of host time per backward
+PAIRED_ONE_LAUNCH = True
 # ... with u formed inside the scan (fwd_h_u) instead of written by prepare_wu and read back
 PAIRED_U = True
 # ... and, vector gates at 64-wide tiles, with qg / kg formed from the raw q / k where each
@@ -865,6 +868,75 @@ def fwd_h_u(k, w, v, Akk, g, gate_mode, beta=None, w_gate=None, h0=None, want_fi
                                  HQ, K, V, CHUNK, int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_fwd_h_u")
     return h, vnew, ht
+
+
+def paired_recurrences(q, k, w, g, gate_mode, dO, scale, v, Akk, value_block, aqk=None, beta=None, b=None,
+                       w_gate=None, qg=None, kg=None, raw_qk=False, h0=None, dht=None, want_dh0=True,
+                       state_v_first=False):
+    """``state_bwd`` (direct) and ``fwd_h_u`` in one launch (fdr_paired_recurrences): the
+    state recurrence's work-groups and the scan's side by side, with the same bits as the two
+    calls.  q / k are the raw ones (the scan's k).  Scalar / no gate: w as ``prepare_wu``
+    writes it, Aqk formed by the state recurrence (``aqk`` None).  Vector gate: ``aqk``, and
+    either ``qg`` / ``kg`` / ``w`` as ``prepare_wu`` wrote them (the state reads them, the scan
+    reads kg), or ``raw_qk`` at 64-wide tiles (qg / kg formed in both; w given, or None to form
+    it from ``beta`` or GDN2's ``b``).  GDN2 passes ``w_gate``, the others ``beta``.
+    Returns ((dh, dR, dh0|None), (h, v_new, None))."""
+    B, T, HQ, K = _dims(q)
+    H, HQ = _group(v.shape[2] if v.ndim == 4 else HQ, HQ)
+    V = V_SUPPORTED
+    dev = q.device
+    bf, f32 = torch.bfloat16, torch.float32
+    for x, n in ((q, "q"), (k, "k")):
+        _need(x, n, bf, (B, T, HQ, K), dev)
+    _need(v, "v", bf, (B, T, H, V), dev)
+    _need(dO, "dO", bf, (B, T, H, V), dev)
+    _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
+    if gate_mode == GATE_VECTOR:
+        _need(g, "g", f32, (B, T, H, K), dev)
+        _need(aqk, "Aqk", f32, (B, T, H, CHUNK), dev)
+    elif gate_mode in (GATE_SCALAR, GATE_NONE):
+        if gate_mode == GATE_SCALAR:
+            _need(g, "g", f32, (B, T, H), dev)
+        if aqk is not None or raw_qk or qg is not None or kg is not None:
+            raise ValueError("scalar / no gate: the raw q / k, Aqk formed in-kernel")
+    else:
+        raise ValueError("gate_mode must be 0, 1 or 2")
+    if w is not None:
+        _need(w, "w", bf, (B, T, H, K), dev)
+    elif not raw_qk or gate_mode != GATE_VECTOR:
+        raise ValueError("w is formed in-kernel only with raw_qk")
+    if w_gate is not None:
+        if gate_mode != GATE_VECTOR:
+            raise ValueError("w_gate (GDN2) takes the vector gate")
+        _need(w_gate, "w_gate", bf, (B, T, H, V), dev)
+        if w is None:
+            _need(b, "b", bf, (B, T, H, K), dev)
+    else:
+        _need(beta, "beta", f32, (B, T, H), dev)
+    if gate_mode == GATE_VECTOR and not raw_qk:
+        _need(qg, "qg", bf, (B, T, H, K), dev)
+        _need(kg, "kg", bf, (B, T, H, K), dev)
+    if value_block not in (16, 32, 64) or (raw_qk and value_block != 64):
+        raise ValueError("value_block must be 16, 32 or 64 (64 with raw_qk)")
+    if h0 is not None:
+        _need(h0, "h0", f32, (B, H, K, V), dev)
+    if dht is not None:
+        _need(dht, "dht", f32, (B, H, K, V), dev)
+    NT = T // CHUNK
+    dh = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
+    dr = torch.empty(B, T, H, V, device=dev, dtype=bf)
+    dh0 = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_dh0 else None
+    h = torch.empty(B, NT, H, K, V, device=dev, dtype=bf)
+    vnew = torch.empty(B, T, H, V, device=dev, dtype=bf)
+    P = _lib.ptr
+    prepared = gate_mode == GATE_VECTOR and not raw_qk
+    st = _lib.load().fdr_paired_recurrences(
+        P(qg if prepared else q), P(kg if prepared else k), P(w), P(k), P(kg if prepared else None), P(g),
+        int(gate_mode), P(beta), P(b if w is None else None), P(w_gate), P(v), P(Akk), P(aqk), P(dO), P(dht), P(h0),
+        P(dh), P(dr), P(dh0), P(h), P(vnew), None, int(bool(raw_qk)), int(bool(state_v_first)), B, T, H, HQ, K, V,
+        CHUNK, float(scale), int(value_block), _lib.stream_handle(dev))
+    _lib.check(st, "fdr_paired_recurrences")
+    return (dh, dr, dh0), (h, vnew, None)
 
 
 def fwd_h_wy_pays(N, H, gate_mode, varlen=None):

@@ -6,7 +6,9 @@ scalar / no-gate ones with the state recurrence forming Aqk itself):
 
 * the public autograd backward (recompute policy) against the fp64 oracle at the
   reference's acceptance tolerances (validation.py:40-45, :68);
-* the same gradients, bit for bit, as the same launches enqueued on one stream, as the two
+* the same gradients, bit for bit, whether the two recurrences run as one launch
+  (fdr_paired_recurrences, ``ops.PAIRED_ONE_LAUNCH``) or as two launches on two streams, as
+  the same launches enqueued on one stream, as the two
   recurrences reading the w (``ops.PAIRED_FORMW`` off, GDN2) and the qg / kg (``ops.PAIRED_RAW``
   off) that prepare_wu wrote instead of forming them from the raw q / k, and as the scan reading a u that prepare_wu wrote
   (``ops.PAIRED_U`` off: the scan forms u itself);
@@ -27,6 +29,17 @@ OPS = ["kda", "gdn2", "gdn", "delta"]
 GATE = {"kda": 2, "gdn2": 2, "gdn": 1, "delta": 0}
 GRAD = {"q": "dq", "k": "dk", "v": "dv", "g": "dg", "beta": "dbeta", "b": "db", "w": "dw", "initial_state": "dh0"}
 SHAPES = [(2, 512, 16, 32), (1, 256, 48, 64), (1, 512, 16, 16)]    # B, T, H, the tile width paired_tile picks
+
+
+def _count_pairs(monkeypatch):
+    """Count the paired recurrences: one launch (ops.paired_recurrences) or two streams."""
+    from rewy_amd import ops
+    from rewy_amd.backends import backward as bw
+    calls = []
+    real_sbs, real_one = bw._side_by_side, ops.paired_recurrences
+    monkeypatch.setattr(bw, "_side_by_side", lambda a, b: (calls.append("streams"), real_sbs(a, b))[1])
+    monkeypatch.setattr(ops, "paired_recurrences", lambda *a, **k: (calls.append("one"), real_one(*a, **k))[1])
+    return calls
 
 
 def _rel(a, r):
@@ -65,9 +78,7 @@ def test_paired_public_backward_matches_oracle(op, B, T, H, vb, monkeypatch):
     from rewy_amd.backends import backward as bw
     print(f"\n[paired] op={op} B={B} T={T} H={H}", flush=True)
     assert ops.paired_tile(B, H, T // 64, GATE[op]) == vb
-    calls = []
-    real = bw._side_by_side
-    monkeypatch.setattr(bw, "_side_by_side", lambda a, b: (calls.append(1), real(a, b))[1])
+    calls = _count_pairs(monkeypatch)
     xs, dO = make_inputs(op, B, T, H, seed=52, gate="mild" if op in ("kda", "gdn2") else "default")
     dev = torch.device("cuda")
     xg = {k: v.to(dev).requires_grad_() for k, v in xs.items()}
@@ -77,7 +88,7 @@ def test_paired_public_backward_matches_oracle(op, B, T, H, vb, monkeypatch):
     dht = (torch.randn(ht.shape, generator=torch.Generator().manual_seed(9)) * 0.1).to(dev)
     grads = torch.autograd.grad((o, ht), tuple(xg.values()), (dO.to(dev), dht))
     torch.cuda.synchronize()
-    assert calls, "the paired recurrences did not run"
+    assert calls == ["one"], calls
     n = lambda x: None if x is None else x.detach().double().cpu().numpy()
     ref = O.backward(op, n(xs["q"]), n(xs["k"]), n(xs["v"]), g=n(xs.get("g")), beta=n(xs.get("beta")),
                      b=n(xs.get("b")), w=n(xs.get("w")), h0=n(xs["initial_state"]), dO=n(dO), dht=n(dht))
@@ -97,6 +108,12 @@ def test_paired_equals_one_stream_and_policy_off(op, B, T, H, vb, monkeypatch):
     print(f"\n[paired-streams] op={op} B={B} T={T} H={H}", flush=True)
     run = _seam(op, B, T, H)
     got = [x.clone() for x in run()]
+    # the two recurrences as two launches on two streams (fdr_state_bwd*, fdr_fwd_h_u)
+    monkeypatch.setattr(ops, "PAIRED_ONE_LAUNCH", False)
+    two = run()
+    torch.cuda.synchronize()
+    for i, (a, r) in enumerate(zip(got, two)):
+        assert torch.equal(a, r), (op, "two launches", i)
     monkeypatch.setattr(bw, "_side_by_side", lambda first, second: (first(), second()))
     one = run()
     torch.cuda.synchronize()
@@ -184,12 +201,9 @@ def test_paired_grouped_heads_and_absent_states(op, HV, HQ, monkeypatch):
         torch.cuda.synchronize()
         return grads
 
-    from rewy_amd.backends import backward as bw
-    calls = []
-    real = bw._side_by_side
-    monkeypatch.setattr(bw, "_side_by_side", lambda a, b: (calls.append(1), real(a, b))[1])
+    calls = _count_pairs(monkeypatch)
     got = run()
-    assert calls, "the paired recurrences did not run"
+    assert calls == ["one"], calls
     monkeypatch.setattr(ops, "PAIRED", False)
     off = run()
     for name, a, r in zip(xs, got, off):
