@@ -270,9 +270,16 @@ def setup(cfg, device):
         pre = kern["fdr_prepare_wu"]()
         ks, qs, ws = (pre["kg"], pre["qg"], pre["w"]) if vec and not raw else (xs["k"], xs["q"], pre["w"])
         aqk = sv["Aqk"] if vec else pre["Aqk"]
-    if vb_pair:
+    if vb_pair and fold_u and ops.PAIRED_ONE_LAUNCH:
         # batch x heads too small for one recurrence to fill the GPU: the state recurrence and
-        # the forward scan side by side (two streams, as the backend runs them)
+        # the forward scan side by side in one launch (fdr_paired_recurrences), as the backend runs them
+        kern["paired_recurrences"] = lambda: ops.paired_recurrences(
+            xs["q"], xs["k"], ws, g, gate, dO, scale, xs["v"], sv["Akk"], vb_pair, aqk=aqk if vec else None,
+            beta=xs.get("beta"), b=xs.get("b"), w_gate=xs.get("w"), qg=qs if vec and not raw else None,
+            kg=ks if vec and not raw else None, raw_qk=raw, h0=xs["h0"], want_dh0=xs["h0"] is not None)
+        (dh, dR, _), (h, v_new, _) = kern["paired_recurrences"]()
+    elif vb_pair:
+        # (two launches on two streams, as the backend runs them with ops.PAIRED_ONE_LAUNCH off)
         from rewy_amd.backends.backward import _side_by_side
         kern["paired_recurrences"] = lambda: _side_by_side(
             lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk, want_dh0=xs["h0"] is not None,

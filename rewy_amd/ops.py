@@ -96,9 +96,12 @@ def side_by_side_pays(B, H, NT):
 # at most one work-group per CU.
 PAIRED = True
 PAIRED_MIN_BH = 24
-# ... and at B*H = 16 (128 work-groups each at 16-wide tiles) for rows of at most 64 chunks,
-# where the pair beats the affine-step form (below that B*H, and on longer rows, it does not)
-PAIRED16_MIN_BH = 16
+# ... and at 16-wide tiles for B*H <= 16 (at most 128 work-groups each) on short rows, where
+# the pair (one launch) beats the affine-step form and the direct recurrences one after the
+# other: rows of at most 8 chunks at any such B*H, 32 from B*H = 12, 64 at B*H = 16
+PAIRED16_SHORT_NT = 8
+PAIRED16_MID_BH = 12
+PAIRED16_MID_NT = 32
 PAIRED16_MAX_NT = 64
 # ... as one launch (fdr_paired_recurrences) instead of two kernels on two streams joined by
 # events, whose fork and join cost ~25 us of host time per backward
@@ -121,7 +124,7 @@ def paired_tile(B, H, NT, gate_mode):
     """Value-tile width at which the recompute policy runs ``fwd_h`` and ``state_bwd`` (both
     direct) side by side, or 0 when it runs them otherwise: for 24 <= B H <= 64, the
     narrowest of 32 / 64 at which each launch has at most 128 work-groups (the two together
-    one per CU); at B H = 16, 16-wide tiles for rows of at most 64 chunks.  Measured (MI355X):
+    one per CU); for B H <= 16, 16-wide tiles on short rows (``PAIRED16_*``).  Measured (MI355X):
     GDN2 B=2 T=8192 H=32 both recurrences 0.451 ms paired at
     64-wide tiles vs 0.544 one after the other at 32-wide; B=2 T=4096 H=16 0.177 (32-wide) vs
     0.231; B=1 T=8192 H=48 0.443 vs 0.543; B=1 T=16384 H=24 0.639 (32-wide) vs 0.905.  The
@@ -131,7 +134,11 @@ def paired_tile(B, H, NT, gate_mode):
     148.6 us paired (32-wide) vs 178.4 us.  At B H = 16 against the affine-step form (graph
     replay, backward): B=1 T=2048 H=16 DeltaNet 97 vs 112 us, GDN 113 vs 117, KDA 112 vs 129,
     GDN2 122 vs 138; T=4096 DeltaNet 179 vs 199, KDA 226 vs 236 (GDN, GDN2 within 1.5 %);
-    T=8192 GDN 447 vs 421 (so not past 64 chunks); B H = 4 the affine-step form by 12-60 %."""
+    T=8192 GDN 447 vs 421 (so not past 64 chunks).  As one launch (``PAIRED_ONE_LAUNCH``), graph
+    replay: rows of 4-8 chunks at B H = 1-8 DeltaNet 25.5-37.0 vs 30.3-46.0 us, KDA 31.1-38.8 vs
+    35.3-50.6 (configs[0], B=1 T=256 H=2: DeltaNet 30.0 vs 36.7); 16 chunks at B H = 12 DeltaNet
+    55.5 vs 57.5, 32 chunks KDA 102.5 vs 107.6; but 16-24 chunks at B H = 2-8 DeltaNet 50.7-67.2 vs
+    46.4-61.6 and 32 chunks at B H = 4-8 72-83 vs 61-72 (the affine-step form's cheaper steps)."""
     BH = B * H
     if not PAIRED or NT < 1:
         return 0
@@ -140,7 +147,8 @@ def paired_tile(B, H, NT, gate_mode):
             if BH * (V_SUPPORTED // vb) <= 128:
                 return vb
         return 0
-    if BH >= PAIRED16_MIN_BH and BH * (V_SUPPORTED // 16) <= 128 and NT <= PAIRED16_MAX_NT:
+    if BH * (V_SUPPORTED // 16) <= 128 and (NT <= PAIRED16_SHORT_NT or (BH >= PAIRED16_MID_BH and NT <= PAIRED16_MID_NT)
+                                             or (BH == 16 and NT <= PAIRED16_MAX_NT)):
         return 16
     return 0
 

@@ -3,8 +3,8 @@
 ``backends.backward`` picks, by batch x heads and chunk count, among the affine-step
 recurrences (few heads), the forward scan beside the segmented state recurrence (few heads,
 long rows), the paired direct recurrences at 32- or 64-wide tiles (24 <= B*H <= 64, with the
-vector gates' in-kernel qg / kg / w at 64-wide tiles) or 16-wide ones (B*H = 16, at most 64
-chunks), and the fused forward sweep or the
+vector gates' in-kernel qg / kg / w at 64-wide tiles) or 16-wide ones (B*H <= 16 on short
+rows), and the fused forward sweep or the
 plain direct recurrences (B*H >= 65).  One case on each side of each switch, odd head counts
 included, every family, both KDA policies: every (batch row, head) pair is independent end to
 end, so two heads of each batch (the first and the last) are checked against the oracle run
@@ -34,7 +34,10 @@ CASES = [  # op, B, T, H, full saving
     ("delta", 1, 4096, 16, False),    # 16 heads, 64 chunks: paired, 16-wide
     ("gdn", 1, 4160, 16, False),      # 16 heads, 65 chunks: the scan beside the segmented recurrence
     ("kda", 2, 512, 8, False),        # B*H = 16, 8 chunks: paired, 16-wide, vector gate
-    ("kda", 1, 1024, 15, False),      # 15 heads: affine-step
+    ("kda", 1, 1024, 15, False),      # 15 heads, 16 chunks: paired, 16-wide
+    ("kda", 1, 2048, 8, False),       # 8 heads, 32 chunks: affine-step
+    ("delta", 1, 256, 2, False),      # configs[0], 4 chunks: paired, 16-wide
+    ("gdn2", 1, 576, 4, False),       # 4 heads, 9 chunks: affine-step
     ("delta", 8, 256, 16, False),     # 128: the fused sweep
     ("kda", 8, 256, 16, False),       # 128, vector gate
 ]
