@@ -173,7 +173,8 @@ def test_paired_under_graph_capture(op):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("op,HV,HQ", [("kda", 48, 12), ("kda", 32, 8), ("gdn", 48, 12), ("gdn2", 48, 48)])
+@pytest.mark.parametrize("op,HV,HQ", [("kda", 48, 12), ("kda", 32, 8), ("gdn", 48, 12), ("gdn2", 48, 48),
+                                       ("kda", 16, 4), ("delta", 8, 2)])
 def test_paired_grouped_heads_and_absent_states(op, HV, HQ, monkeypatch):
     """Grouped value heads (q / k with HQ heads) through the paired recurrences -- the raw q / k
     forms at 64-wide tiles, prepare_wu's qg / kg at 32-wide ones -- and GDN2's prepare-free form

@@ -38,6 +38,9 @@ CASES = [  # op, B, T, H, full saving
     ("kda", 1, 2048, 8, False),       # 8 heads, 32 chunks: affine-step
     ("delta", 1, 256, 2, False),      # configs[0], 4 chunks: paired, 16-wide
     ("gdn2", 1, 576, 4, False),       # 4 heads, 9 chunks: affine-step
+    ("gdn2", 1, 128, 1, False),       # one head, 2 chunks: paired, 16-wide
+    ("gdn", 1, 2048, 12, False),      # 12 heads, 32 chunks: paired, 16-wide
+    ("delta", 1, 2112, 12, False),    # 12 heads, 33 chunks: affine-step
     ("delta", 8, 256, 16, False),     # 128: the fused sweep
     ("kda", 8, 256, 16, False),       # 128, vector gate
 ]
