@@ -17,9 +17,10 @@ When batch x heads is too small to fill the GPU and the sequence long, the two
 recurrences run instead in affine-step form (after ``fdr_prepare_wu``: w, u and qg, kg or Aqk) (``ops.recurrences``,
 ``fdr_affine_*``): chunk-parallel step matrices, one scan launch carrying both
 recurrences side by side, and a chunk-parallel pass for v_new and dR.
-With 24 <= batch x heads <= 64 the recompute policy runs the direct backward state recurrence
-and the direct forward scan side by side on two streams, at a value-tile width that gives
-each at most half the CUs (``ops.paired_tile``).
+With 24 <= batch x heads <= 64, and on short rows at batch x heads <= 16, the recompute policy
+runs the direct backward state recurrence and the direct forward scan side by side in one
+launch (``fdr_paired_recurrences``), at a value-tile width that gives each at most half the
+CUs (``ops.paired_tile``).
 With a few more heads and long rows the recompute policy runs the forward scan
 (``fdr_fwd_h``) on the current stream beside the segmented backward state recurrence
 (``fdr_state_bwd_segmented``) on a second stream (``ops.side_by_side_pays``).
