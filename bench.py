@@ -70,8 +70,9 @@ def inline_aqk(cfg):
         return False
     NT = cfg["T"] // 64
     gate = ops.GATE_SCALAR if cfg["op"] == "gdn" else ops.GATE_NONE
-    if ops.paired_tile(cfg["B"], cfg["H"], NT, gate):
-        return True
+    vb = ops.paired_tile(cfg["B"], cfg["H"], NT, gate)
+    if vb:
+        return vb > ops.PAIRED_AQK_MAX_VB     # (narrower tiles read the Aqk prepare_wu writes)
     return not ops._use_affine("auto", cfg["B"], cfg["H"], NT) and ops.state_form(cfg["B"], cfg["H"], NT) == "direct"
 
 
@@ -274,7 +275,7 @@ def setup(cfg, device):
         # batch x heads too small for one recurrence to fill the GPU: the state recurrence and
         # the forward scan side by side in one launch (fdr_paired_recurrences), as the backend runs them
         kern["paired_recurrences"] = lambda: ops.paired_recurrences(
-            xs["q"], xs["k"], ws, g, gate, dO, scale, xs["v"], sv["Akk"], vb_pair, aqk=aqk if vec else None,
+            xs["q"], xs["k"], ws, g, gate, dO, scale, xs["v"], sv["Akk"], vb_pair, aqk=aqk,
             beta=xs.get("beta"), b=xs.get("b"), w_gate=xs.get("w"), qg=qs if vec and not raw else None,
             kg=ks if vec and not raw else None, raw_qk=raw, h0=xs["h0"], want_dh0=xs["h0"] is not None)
         (dh, dR, _), (h, v_new, _) = kern["paired_recurrences"]()

@@ -324,13 +324,17 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
                               state_v_first=state_v_first)
             w, h, v_new = sw["w"], sw["h"], sw["v_new"]
         else:
-            # paired (vb): u formed inside the scan where ops.PAIRED_U holds
-            pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, varlen=vl, want_u=not (vb and ops.PAIRED_U))
+            # paired (vb): u formed inside the scan where ops.PAIRED_U holds; at narrow value tiles
+            # Aqk written here for the state recurrence (ops.PAIRED_AQK_MAX_VB)
+            aqk_pre = 0 < vb <= ops.PAIRED_AQK_MAX_VB
+            pre = ops.prepare_wu(k, v, A, gate, g=g, beta=beta, varlen=vl, want_u=not (vb and ops.PAIRED_U),
+                                 q=q if aqk_pre else None, want_aqk=aqk_pre, scale=scale)
             w = pre["w"]
 
         def state():
-            return ops.state_bwd(q, k, w, g, gate, do, scale, dht=_f32(dht), want_dh0=initial_state is not None,
-                                 method="direct", varlen=vl, state_v_first=state_v_first, value_block=vb)
+            return ops.state_bwd(q, k, w, g, gate, do, scale, aqk=None if pre is None else pre.get("Aqk"),
+                                 dht=_f32(dht), want_dh0=initial_state is not None, method="direct", varlen=vl,
+                                 state_v_first=state_v_first, value_block=vb)
 
         def scan():
             if pre["u"] is None:
@@ -343,8 +347,8 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
         elif vb and pre["u"] is None and ops.PAIRED_ONE_LAUNCH:
             # both recurrences in one launch (the same kernels' bodies, no second stream)
             (dh, dR, dh0), (h, v_new, _) = ops.paired_recurrences(
-                q, k, w, g, gate, do, scale, v, A, vb, beta=beta, h0=_f32(initial_state), dht=_f32(dht),
-                want_dh0=initial_state is not None, state_v_first=state_v_first)
+                q, k, w, g, gate, do, scale, v, A, vb, aqk=pre.get("Aqk"), beta=beta, h0=_f32(initial_state),
+                dht=_f32(dht), want_dh0=initial_state is not None, state_v_first=state_v_first)
         elif vb:
             # the state recurrence (the longer chain) first, the scan on the side stream
             (dh, dR, dh0), (h, v_new, _) = _side_by_side(state, scan)

@@ -116,8 +116,12 @@ extern "C" hipError_t fdr_paired_recurrences(
   PairScan f{(const bf16*)k_scan, (const bf16*)v, g, beta, (const bf16*)(w ? w_gate : b_gate),
              (const bf16*)w_gate, Akk, h0, (bf16*)h, (bf16*)v_new, ht, (const bf16*)w, HQ};
   if (gate_mode != GATE_VECTOR) {
-    // scalar / no gate: raw q / k, Aqk formed by the state recurrence, w given
-    if (aqk || !w || raw_qk || kg || !k_scan) return hipErrorInvalidValue;
+    // scalar / no gate: raw q / k, w given; Aqk formed by the state recurrence, or read
+    if (!w || raw_qk || kg || !k_scan) return hipErrorInvalidValue;
+    if (aqk) {
+      if (gate_mode == GATE_SCALAR) P_BV(GATE_SCALAR, false, false, 0, false, true, false, false)
+      P_BV(GATE_NONE, false, false, 0, false, true, false, false)
+    }
     if (gate_mode == GATE_SCALAR) P_BV(GATE_SCALAR, true, false, 0, false, true, false, false)
     P_BV(GATE_NONE, true, false, 0, false, true, false, false)
   }

@@ -574,12 +574,15 @@ static hipError_t prepare_dispatch(const void* q, const void* k, const void* v, 
   if (want_aqk && (!q || gate_mode == RG_VECTOR)) return hipErrorInvalidValue;
 #define P_ARGS q, k, v, g, beta, b_gate, w_gate, Akk, w, u, qg, kg, Aqk, B, T, H, HQ, scale, stream, cu, ci
   if (!u) {
-    // w (and, vector gates, optionally qg, kg) only, for the forward scan that forms u itself
-    // (fdr_fwd_h_u); no Aqk
-    if (want_aqk) return hipErrorInvalidValue;
+    // w (and, vector gates, optionally qg, kg; scalar / no gate, optionally Aqk) only, for the
+    // forward scan that forms u itself (fdr_fwd_h_u)
     switch (gate_mode) {
-      case RG_NONE: return launch_prepare<RG_NONE, false, false, false, false>(P_ARGS);
-      case RG_SCALAR: return launch_prepare<RG_SCALAR, false, false, false, false>(P_ARGS);
+      case RG_NONE:
+        return want_aqk ? launch_prepare<RG_NONE, false, false, true, false>(P_ARGS)
+                        : launch_prepare<RG_NONE, false, false, false, false>(P_ARGS);
+      case RG_SCALAR:
+        return want_aqk ? launch_prepare<RG_SCALAR, false, false, true, false>(P_ARGS)
+                        : launch_prepare<RG_SCALAR, false, false, false, false>(P_ARGS);
       case RG_VECTOR:
         if (vec_b)
           return want_qkg ? launch_prepare<RG_VECTOR, true, true, false, false>(P_ARGS)

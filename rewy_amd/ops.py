@@ -106,6 +106,12 @@ PAIRED16_MAX_NT = 96
 # ... as one launch (fdr_paired_recurrences) instead of two kernels on two streams joined by
 # events, whose fork and join cost ~25 us of host time per backward
 PAIRED_ONE_LAUNCH = True
+# ... and, scalar / no gate at value tiles up to this width, Aqk written by fdr_prepare_wu and
+# read by the state recurrence instead of formed there: at narrow tiles every one of a head's
+# value-tile work-groups would form the whole Aqk again on its step chain (GDN B=1 T=2048 H=16
+# 100.5 vs 113.5 us, B=2 T=2048 H=16 146.0 vs 153.4, B=1 T=6144 H=16 296 vs 339, DeltaNet B=1
+# T=2048 H=16 92.1 vs 97.7; at 64-wide tiles, GDN B=4 T=2048 H=16, 271.3 vs 268.4)
+PAIRED_AQK_MAX_VB = 32
 # ... with u formed inside the scan (fwd_h_u) instead of written by prepare_wu and read back
 PAIRED_U = True
 # ... and, vector gates at 64-wide tiles, with qg / kg formed from the raw q / k where each
@@ -727,8 +733,8 @@ def prepare_wu(k, v, Akk, gate_mode, g=None, beta=None, b=None, w=None, q=None, 
         raise ValueError("qg/kg need q and a vector gate")
     if want_aqk and (q is None or gate_mode == GATE_VECTOR):
         raise ValueError("Aqk is produced here for scalar / no-gate families only")
-    if not want_u and (want_aqk or varlen is not None):
-        raise ValueError("want_u=False takes no Aqk and dense rows")
+    if not want_u and varlen is not None:
+        raise ValueError("want_u=False takes dense rows")
     out = dict(w=torch.empty(B, T, H, K, device=dev, dtype=bf),
                u=torch.empty(B, T, H, V, device=dev, dtype=bf) if want_u else None,
                qg=torch.empty(B, T, H, K, device=dev, dtype=bf) if want_qkg else None,
@@ -908,8 +914,10 @@ def paired_recurrences(q, k, w, g, gate_mode, dO, scale, v, Akk, value_block, aq
     elif gate_mode in (GATE_SCALAR, GATE_NONE):
         if gate_mode == GATE_SCALAR:
             _need(g, "g", f32, (B, T, H), dev)
-        if aqk is not None or raw_qk or qg is not None or kg is not None:
-            raise ValueError("scalar / no gate: the raw q / k, Aqk formed in-kernel")
+        if raw_qk or qg is not None or kg is not None:
+            raise ValueError("scalar / no gate: the raw q / k")
+        if aqk is not None:
+            _need(aqk, "Aqk", f32, (B, T, H, CHUNK), dev)
     else:
         raise ValueError("gate_mode must be 0, 1 or 2")
     if w is not None:

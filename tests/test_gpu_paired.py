@@ -13,7 +13,9 @@ scalar / no-gate ones with the state recurrence forming Aqk itself):
   off) that prepare_wu wrote instead of forming them from the raw q / k, and as the scan reading a u that prepare_wu wrote
   (``ops.PAIRED_U`` off: the scan forms u itself);
 * against the policy switched off (the pair one after the other at the default tile
-  width): rel-L2 <= 1e-5, the tile width changing no arithmetic of a value column;
+  width): rel-L2 <= 1e-5, the tile width changing no arithmetic of a value column (5e-3 for the
+  scalar / no-gate families at narrow tiles, where the pair reads the Aqk fdr_prepare_wu writes
+  instead of forming it);
 * captured in a HIP graph and replayed three times with eager work between the replays.
 """
 import pytest
@@ -144,9 +146,13 @@ def test_paired_equals_one_stream_and_policy_off(op, B, T, H, vb, monkeypatch):
     monkeypatch.setattr(ops, "AFFINE_MAX_BH", -1)
     off = run()
     torch.cuda.synchronize()
+    # (scalar / no gate at tiles up to ops.PAIRED_AQK_MAX_VB: the pair's state recurrence reads
+    # the Aqk fdr_prepare_wu writes, the unpaired one forms Aqk itself -- two bf16 roundings of
+    # the same scores; both are held to the oracle in test_paired_public_backward_matches_oracle)
+    tol = 5e-3 if GATE[op] != 2 and vb <= ops.PAIRED_AQK_MAX_VB else 1e-5
     for i, (a, r) in enumerate(zip(got, off)):
         e = _rel(a, r)
-        assert e <= 1e-5, (op, i, e)
+        assert e <= tol, (op, i, e)
 
 
 @pytest.mark.parametrize("op", ["kda", "gdn"])

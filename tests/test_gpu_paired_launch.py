@@ -1,6 +1,7 @@
 """fdr_paired_recurrences (the state recurrence and the scan forming u in one launch) against
 its two halves run as separate launches -- fdr_state_bwd / fdr_state_bwd_raw_qk and
-fdr_fwd_h_u -- bit for bit: every family, value tiles 16 / 32 / 64, the vector gates with
+fdr_fwd_h_u -- bit for bit: every family (the scalar / no-gate ones forming Aqk, or reading the
+Aqk fdr_prepare_wu writes), value tiles 16 / 32 / 64, the vector gates with
 prepared qg / kg / w and with raw q / k (w given or formed), grouped q / k heads, V-first
 states, with and without the initial / final states; and the host-side argument rules."""
 import pytest
@@ -67,6 +68,19 @@ def test_one_launch_equals_the_two_launches(op, HQ, vb):
                                              d["Akk"], vb, **pk)
                 torch.cuda.synchronize()
                 _check(got, ref, tag)
+                # Aqk written by prepare_wu (with or without u: the same w and Aqk) and read
+                wa = ops.prepare_wu(d["k"], d["v"], d["Akk"], gate, g=d["gc"], beta=d["beta"], q=d["q"],
+                                    want_aqk=True, scale=0.088, want_u=False)
+                full = ops.prepare_wu(d["k"], d["v"], d["Akk"], gate, g=d["gc"], beta=d["beta"], q=d["q"],
+                                      want_aqk=True, scale=0.088)
+                torch.cuda.synchronize()
+                assert torch.equal(wa["w"], pre["w"]) and torch.equal(wa["Aqk"], full["Aqk"]), tag
+                ref = (ops.state_bwd(d["q"], d["k"], pre["w"], d["gc"], gate, d["dO"], 0.088, aqk=wa["Aqk"], **st),
+                       ref[1])
+                got = ops.paired_recurrences(d["q"], d["k"], pre["w"], d["gc"], gate, d["dO"], 0.088, d["v"],
+                                             d["Akk"], vb, aqk=wa["Aqk"], **pk)
+                torch.cuda.synchronize()
+                _check(got, ref, tag + ("aqk read",))
                 continue
             # qg / kg / w as prepare_wu wrote them
             ref = (ops.state_bwd(pre["qg"], pre["kg"], pre["w"], d["gc"], gate, d["dO"], 0.088, aqk=d["Aqk"], **st),
@@ -108,9 +122,9 @@ def test_argument_rules():
                                raw_qk=True, **base)
     with pytest.raises(ValueError):        # prepared qg / kg required without raw_qk
         ops.paired_recurrences(d["q"], d["k"], pre["w"], d["gc"], 2, d["dO"], 0.1, d["v"], d["Akk"], 32, **base)
-    with pytest.raises(ValueError):        # the scalar families form Aqk in-kernel
+    with pytest.raises(ValueError):        # the scalar families take the raw q / k only
         ops.paired_recurrences(d["q"], d["k"], pre["w"], d["gc"][..., 0].contiguous(), 1, d["dO"], 0.1, d["v"],
-                               d["Akk"], 32, **base)
+                               d["Akk"], 32, raw_qk=True, **base)
     # the library's own checks, below the Python ones
     P = _lib.ptr
     lib = _lib.load()
