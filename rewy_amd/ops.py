@@ -98,11 +98,11 @@ PAIRED = True
 PAIRED_MIN_BH = 24
 # ... and at 16-wide tiles for B*H <= 16 (at most 128 work-groups each) on short rows, where
 # the pair (one launch) beats the affine-step form and the direct recurrences one after the
-# other: rows of at most 8 chunks at any such B*H, 32 from B*H = 12, 96 at B*H = 16
+# other: rows of at most 8 chunks at any such B*H, 32 from B*H = 12, 128 at B*H = 16
 PAIRED16_SHORT_NT = 8
 PAIRED16_MID_BH = 12
 PAIRED16_MID_NT = 32
-PAIRED16_MAX_NT = 96
+PAIRED16_MAX_NT = 128
 # ... as one launch (fdr_paired_recurrences) instead of two kernels on two streams joined by
 # events, whose fork and join cost ~25 us of host time per backward
 PAIRED_ONE_LAUNCH = True
@@ -146,8 +146,8 @@ def paired_tile(B, H, NT, gate_mode):
     55.5 vs 57.5, 32 chunks KDA 102.5 vs 107.6; but 16-24 chunks at B H = 2-8 DeltaNet 50.7-67.2 vs
     46.4-61.6 and 32 chunks at B H = 4-8 72-83 vs 61-72 (the affine-step form's cheaper steps).
     At B H = 16 against the scan beside the segmented recurrence: 96 chunks DeltaNet 282 vs 323 us,
-    GDN 333 vs 343, KDA 340 vs 376, GDN2 378 vs 408; 128 chunks DeltaNet 381 vs 394, KDA 456 vs 462,
-    but GDN 443 vs 422 and GDN2 517 vs 507 (so not past 96 chunks)."""
+    GDN 333 vs 343, KDA 340 vs 376, GDN2 378 vs 408; 128 chunks (GDN / DeltaNet reading Aqk)
+    DeltaNet 379 vs 389, GDN 409 vs 419, KDA 457 vs 473, GDN2 518 vs 511 (eager all 3-9 % faster)."""
     BH = B * H
     if not PAIRED or NT < 1:
         return 0

@@ -32,8 +32,8 @@ CASES = [  # op, B, T, H, full saving
     ("kda", 1, 4096, 4, False),       # 4 heads, 64 chunks: affine-step or segmented
     ("gdn2", 1, 2048, 16, False),     # 16 heads, 32 chunks: paired, 16-wide
     ("delta", 1, 4096, 16, False),    # 16 heads, 64 chunks: paired, 16-wide
-    ("gdn", 1, 6144, 16, False),      # 16 heads, 96 chunks: paired, 16-wide
-    ("gdn", 1, 6208, 16, False),      # 16 heads, 97 chunks: the scan beside the segmented recurrence
+    ("gdn", 1, 8192, 16, False),      # 16 heads, 128 chunks: paired, 16-wide
+    ("gdn", 1, 8256, 16, False),      # 16 heads, 129 chunks: the scan beside the segmented recurrence
     ("kda", 2, 512, 8, False),        # B*H = 16, 8 chunks: paired, 16-wide, vector gate
     ("kda", 1, 1024, 15, False),      # 15 heads, 16 chunks: paired, 16-wide
     ("kda", 1, 2048, 8, False),       # 8 heads, 32 chunks: affine-step

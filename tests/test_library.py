@@ -179,17 +179,17 @@ def test_paired_rule():
     assert ops.paired_tile(2, 32, 128, V) == 64          # GDN2 configs[3]
     assert ops.paired_tile(2, 16, 64, V) == 32 and ops.paired_tile(1, 24, 256, V) == 32
     assert ops.paired_tile(1, 48, 128, V) == 64
-    assert ops.paired_tile(1, 16, 512, V) == 0           # few heads: affine / side-by-side forms
+    assert ops.paired_tile(1, 16, 512, V) == 0           # few heads, long rows: the side-by-side form
     assert ops.paired_tile(8, 16, 64, V) == 0            # the fused sweep fills the GPU
     assert ops.paired_tile(1, 96, 64, V) == 0            # 64-wide tiles would need 192 CUs each
     assert ops.paired_tile(2, 32, 128, S) == 64 and ops.paired_tile(4, 16, 32, S) == 64   # before the fused sweep
     assert ops.paired_tile(2, 16, 32, S) == 32 and ops.paired_tile(1, 48, 64, ops.GATE_NONE) == 64
     assert ops.paired_tile(8, 16, 64, S) == 0
-    # B*H <= 16: 16-wide tiles on rows of <= 8 chunks, <= 32 from B*H = 12, <= 96 at 16
+    # B*H <= 16: 16-wide tiles on rows of <= 8 chunks, <= 32 from B*H = 12, <= 128 at 16
     assert ops.paired_tile(1, 16, 32, V) == 16 and ops.paired_tile(2, 8, 64, S) == 16
     assert ops.paired_tile(1, 16, 8, ops.GATE_NONE) == 16 and ops.paired_tile(1, 2, 4, ops.GATE_NONE) == 16
-    assert ops.paired_tile(1, 16, 97, S) == 0 and ops.paired_tile(1, 15, 32, V) == 16
-    assert ops.paired_tile(1, 16, 96, V) == 16
+    assert ops.paired_tile(1, 16, 129, S) == 0 and ops.paired_tile(1, 15, 32, V) == 16
+    assert ops.paired_tile(1, 16, 128, V) == 16
     assert ops.paired_tile(1, 12, 33, V) == 0 and ops.paired_tile(1, 8, 16, V) == 0
     assert ops.paired_tile(1, 4, 32, V) == 0 and ops.paired_tile(1, 1, 8, S) == 16
 
