@@ -304,7 +304,7 @@ def setup(cfg, device):
         kern["segmented_state"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,
                                                         want_dh0=xs["h0"] is not None, method="segmented")
         dh, dR, _ = kern["segmented_state"]()
-    elif ops.affine_pays(xs["q"]):
+    elif (ops._state_method("auto", cfg["B"], cfg["H"], NT) == "affine") if keep else ops.affine_pays(xs["q"]):
         # few heads: the backend runs the recurrences in affine-step form (prep, scan, side launches)
         if keep:
             kern["affine_state"] = lambda: ops.state_bwd(qs, ks, ws, g, gate, dO, scale, aqk=aqk,

@@ -37,6 +37,12 @@ def _need(x, name, dtype, shape, device):
 # direct kernels are then bound by their per-chunk latency.
 AFFINE_MAX_BH = 16
 AFFINE_MIN_CHUNKS = 8
+# ... for the backward state recurrence alone (full saving: no forward scan beside it), from
+# more chunks: up to 16 the direct kernel's two launches fewer outweigh its longer steps
+# (graph replay, KDA: B=1 H=4 8 chunks 33.2 vs 37.6 us, 12 chunks 39.4 vs 41.5, 16 chunks 45.6 vs
+# 45.7; H=16 8 chunks 37.0 vs 42.6, 16 chunks 51.5 vs 53.7; GDN2 alike; 32 chunks the affine-step
+# form, 57.2 vs 74.3 and 89.4 vs 91.8)
+AFFINE_STATE_MIN_CHUNKS = 17
 AFFINE_VALUE_BLOCK = 16
 
 
@@ -62,7 +68,7 @@ def _state_method(method, B, H, NT):
         return method
     if NT >= SEG_MIN_CHUNKS and 2 * B * H < 256:
         return "segmented"
-    if B * H <= AFFINE_MAX_BH and NT >= AFFINE_MIN_CHUNKS:
+    if B * H <= AFFINE_MAX_BH and NT >= AFFINE_STATE_MIN_CHUNKS:
         return "affine"
     return "direct"
 

@@ -32,8 +32,9 @@ def _run(op, xs, dO, backend, **kw):
 
 @pytest.mark.parametrize("op,kw", [("kda", dict(disable_recompute=True)), ("kda", dict(disable_recompute=False)),
                                    ("gdn", {}), ("gdn2", dict(disable_recompute=True)), ("delta", {})])
-# T = 640: ten chunks at B*H = 4, so the forward and backward state recurrences take the
-# affine-step kernels (at most 8 chunks take the paired direct recurrences, in one launch)
+# T = 640: ten chunks at B*H = 4, so the recompute policy's forward and backward state
+# recurrences take the affine-step kernels (at most 8 chunks take the paired direct recurrences,
+# in one launch; the full-saving policy's state recurrence alone is direct up to 16 chunks)
 @pytest.mark.parametrize("T", [128, 320, 640])
 def test_public_backward_matches_oracle(op, kw, T):
     import rewy_amd as fdr

@@ -28,6 +28,8 @@ CASES = [  # op, B, T, H, full saving
     ("kda", 1, 256, 65, False),       # 65: the fused sweep or the direct pair, vector gate
     ("gdn2", 4, 256, 16, False),      # 64: paired, 64-wide, prepare-free
     ("kda", 4, 256, 16, True),        # full saving at 64
+    ("kda", 1, 1024, 4, True),        # full saving, 4 heads, 16 chunks: the direct state recurrence
+    ("gdn2", 1, 1088, 4, True),       # full saving, 4 heads, 17 chunks: affine-step
     ("gdn", 1, 1024, 8, False),       # 8 heads, 16 chunks
     ("kda", 1, 4096, 4, False),       # 4 heads, 64 chunks: affine-step or segmented
     ("gdn2", 1, 2048, 16, False),     # 16 heads, 32 chunks: paired, 16-wide

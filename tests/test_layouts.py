@@ -85,6 +85,8 @@ def test_state_recurrence_form_routing():
     assert ops._state_method("auto", 8, 16, 64) == "direct"           # the headline config
     assert ops._state_method("auto", 2, 32, 128) == "direct"          # the GDN2 config
     assert ops._state_method("auto", 1, 4, 128) == "affine"           # the reference's grid, few chunks
+    assert ops._state_method("auto", 1, 4, 17) == "affine"
+    assert ops._state_method("auto", 1, 16, 16) == "direct"           # short rows: two launches fewer
     assert ops.segments_for(1, 16, 1024) == 8
     assert ops.segments_for(1, 1, 40) == 2                             # segments of >= 16 chunks
     assert ops._state_method("direct", 1, 16, 1024) == "direct"
