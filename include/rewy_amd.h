@@ -327,7 +327,8 @@ hipError_t fdr_fwd_h_u(const void* k, const void* kg, const void* w, const void*
  *         read by the scan instead (vector gate without raw_qk; k_scan is then not read);
  *   w: fdr_prepare_wu's w, or NULL (vector gate with raw_qk: w formed in both, from beta or
  *      b_gate, as fdr_state_bwd_raw_qk / fdr_fwd_h_u form it);
- *   gate_mode 0 / 1: aqk NULL (Aqk formed by the state recurrence), w given, raw_qk 0;
+ *   gate_mode 0 / 1: w given, raw_qk 0; aqk NULL (Aqk formed by the state recurrence) or
+ *      fdr_prepare_wu's Aqk (read, as fdr_state_bwd reads it);
  *   gate_mode 2: aqk given; raw_qk only at value_block 64;
  *   beta fp32 [B,T,H] or GDN2's w_gate bf16 [B,T,H,V] (and b_gate when w is NULL);
  *   v, Akk, h0 (may be null), h, v_new, ht (may be null): as fdr_fwd_h_u;

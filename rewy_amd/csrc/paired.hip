@@ -22,7 +22,7 @@ struct PairState {
   const bf16* w;        // null: formed in-kernel (raw vector gate, FW)
   const float* g;
   const bf16* dO;
-  const float* aqk;     // null: formed in-kernel (scalar / no gate, INL)
+  const float* aqk;     // null: formed in-kernel (scalar / no gate, INL); else read
   const float* dht;
   bf16* dh;
   bf16* dr;
