@@ -253,8 +253,8 @@ hipError_t fdr_chunk_bwd_original(const void* q, const void* k, const void* v, c
  * (scalar / no gate) the intra-chunk scores Aqk = scale tril(q k^T 2^(g_i - g_s))
  * (fp32 [B,T,H,64]) that FLA chunk_bwd_dv_local forms (backward.py:119).
  * Scalar-beta families pass beta and null b_gate/w_gate; GDN2 passes b_gate/w_gate.
- * u = nullptr writes w (and, vector gates, optionally qg, kg) only, for fdr_fwd_h_u, which
- * forms u itself (no Aqk); v and w_gate are then not read.
+ * u = nullptr writes w (and optionally qg, kg for the vector gates, Aqk for gate_mode 0 / 1)
+ * only, for fdr_fwd_h_u, which forms u itself; v and w_gate are then not read.
  */
 hipError_t fdr_prepare_wu(const void* q, const void* k, const void* v, const float* g,
                           int gate_mode, const float* beta, const void* b_gate, const void* w_gate,
