@@ -250,6 +250,23 @@ def test_seam_and_pairing_entry_points_reject_bad_arguments_without_touching_the
                                     1, 128, 1, 1, 128, 128, 64, 1.0, 0, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fdr_state_bwd_raw_qk(fake, fake, None, fake, fake, None, None, fake, fake, None, fake, fake, None, 0,
                                     1, 128, 1, 1, 128, 128, 64, 1.0, 0, None) == HIP_ERROR_INVALID_VALUE
+    # fdr_paired_recurrences (q, k, w, k_scan, kg, g, gate, beta, b_gate, w_gate, v, Akk, aqk, dO, dht,
+    # h0, dh, dr, dh0, h, v_new, ht, raw_qk, vf, B, T, H, qk_heads, K, V, chunk, scale, value_block, stream)
+    def paired(w=fake, kg=fake, gate=2, beta=fake, b_gate=None, w_gate=None, aqk=fake, raw=0, vb=32, T=128):
+        return lib.fdr_paired_recurrences(fake, fake, w, fake, kg, fake, gate, beta, b_gate, w_gate, fake, fake, aqk,
+                                          fake, None, None, fake, fake, None, fake, fake, None, raw, 0, 1, T, 2, 2,
+                                          128, 128, 64, 1.0, vb, None)
+    assert paired(vb=48) == HIP_ERROR_INVALID_VALUE                     # tile width
+    assert paired(T=100) == HIP_ERROR_INVALID_VALUE                     # T not whole chunks
+    assert paired(kg=None) == HIP_ERROR_INVALID_VALUE                   # vector gate, prepared: kg required
+    assert paired(aqk=None) == HIP_ERROR_INVALID_VALUE                  # vector gate: Aqk required
+    assert paired(raw=1) == HIP_ERROR_INVALID_VALUE                     # raw q / k: not with kg ...
+    assert paired(raw=1, kg=None, vb=32) == HIP_ERROR_INVALID_VALUE     # ... and only at 64-wide tiles
+    assert paired(raw=1, kg=None, w=None, beta=None, b_gate=None, w_gate=fake,
+                  vb=64) == HIP_ERROR_INVALID_VALUE                     # GDN2 with w formed: b_gate required
+    assert paired(gate=1, kg=None, w=None) == HIP_ERROR_INVALID_VALUE   # scalar gate: w required
+    assert paired(gate=1, kg=None, raw=1) == HIP_ERROR_INVALID_VALUE    # scalar gate: no raw_qk
+    assert paired(gate=1, w_gate=fake) == HIP_ERROR_INVALID_VALUE       # w_gate only with the vector gate
     assert lib.fdr_group_sum(None, None, 16, 2, 2, 64, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fdr_group_sum(None, None, 0, 2, 2, 128, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fdr_gdn2_chunk_bwd_wy(*([None] * 19), 0, 1, 128, 1, 64, 128, 64, 1.0, None) == HIP_ERROR_INVALID_VALUE
