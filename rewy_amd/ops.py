@@ -101,14 +101,13 @@ def side_by_side_pays(B, H, NT):
 # side by side at a common value-tile width chosen so that the two launches together hold
 # at most one work-group per CU.
 PAIRED = True
-PAIRED_MIN_BH = 24
+PAIRED_MIN_BH = 17
 # ... and at 16-wide tiles for B*H <= 16 (at most 128 work-groups each) on short rows, where
 # the pair (one launch) beats the affine-step form and the direct recurrences one after the
-# other: rows of at most 8 chunks at any such B*H, 32 from B*H = 12, 128 at B*H = 16
+# other: rows of at most 8 chunks at any such B*H, of at most 128 from B*H = 12
 PAIRED16_SHORT_NT = 8
 PAIRED16_MID_BH = 12
-PAIRED16_MID_NT = 32
-PAIRED16_MAX_NT = 128
+PAIRED16_MID_NT = 128
 # ... as one launch (fdr_paired_recurrences) instead of two kernels on two streams joined by
 # events, whose fork and join cost ~25 us of host time per backward
 PAIRED_ONE_LAUNCH = True
@@ -134,7 +133,7 @@ PAIRED_FORMW = True
 
 def paired_tile(B, H, NT, gate_mode):
     """Value-tile width at which the recompute policy runs ``fwd_h`` and ``state_bwd`` (both
-    direct) side by side, or 0 when it runs them otherwise: for 24 <= B H <= 64, the
+    direct) side by side, or 0 when it runs them otherwise: for 17 <= B H <= 64, the
     narrowest of 32 / 64 at which each launch has at most 128 work-groups (the two together
     one per CU); for B H <= 16, 16-wide tiles on short rows (``PAIRED16_*``).  Measured (MI355X):
     GDN2 B=2 T=8192 H=32 both recurrences 0.451 ms paired at
@@ -153,7 +152,11 @@ def paired_tile(B, H, NT, gate_mode):
     46.4-61.6 and 32 chunks at B H = 4-8 72-83 vs 61-72 (the affine-step form's cheaper steps).
     At B H = 16 against the scan beside the segmented recurrence: 96 chunks DeltaNet 282 vs 323 us,
     GDN 333 vs 343, KDA 340 vs 376, GDN2 378 vs 408; 128 chunks (GDN / DeltaNet reading Aqk)
-    DeltaNet 379 vs 389, GDN 409 vs 419, KDA 457 vs 473, GDN2 518 vs 511 (eager all 3-9 % faster)."""
+    DeltaNet 379 vs 389, GDN 409 vs 419, KDA 457 vs 473, GDN2 518 vs 511 (eager all 3-9 % faster);
+    B H = 12, 64 chunks: DeltaNet 160 vs 204, KDA 187 vs 206; 128 chunks: GDN 358 vs 379, KDA 399 vs
+    408.  B H = 17-23 at 32-wide tiles, against the recurrences one after the other: B=1 T=2048
+    H=20 DeltaNet 118 vs 156 us, GDN 129 vs 179, KDA 136 vs 171, GDN2 153 vs 189; KDA T=4096 H=18
+    259 vs 320."""
     BH = B * H
     if not PAIRED or NT < 1:
         return 0
@@ -162,8 +165,7 @@ def paired_tile(B, H, NT, gate_mode):
             if BH * (V_SUPPORTED // vb) <= 128:
                 return vb
         return 0
-    if BH * (V_SUPPORTED // 16) <= 128 and (NT <= PAIRED16_SHORT_NT or (BH >= PAIRED16_MID_BH and NT <= PAIRED16_MID_NT)
-                                             or (BH == 16 and NT <= PAIRED16_MAX_NT)):
+    if BH * (V_SUPPORTED // 16) <= 128 and (NT <= PAIRED16_SHORT_NT or (BH >= PAIRED16_MID_BH and NT <= PAIRED16_MID_NT)):
         return 16
     return 0
 

@@ -2,7 +2,7 @@
 
 ``backends.backward`` picks, by batch x heads and chunk count, among the affine-step
 recurrences (few heads), the forward scan beside the segmented state recurrence (few heads,
-long rows), the paired direct recurrences at 32- or 64-wide tiles (24 <= B*H <= 64, with the
+long rows), the paired direct recurrences at 32- or 64-wide tiles (17 <= B*H <= 64, with the
 vector gates' in-kernel qg / kg / w at 64-wide tiles) or 16-wide ones (B*H <= 16 on short
 rows), and the fused forward sweep or the
 plain direct recurrences (B*H >= 65).  One case on each side of each switch, odd head counts
@@ -22,6 +22,8 @@ OPNAME = {"kda": "chunk_kda", "gdn": "chunk_gated_delta_rule", "gdn2": "chunk_gd
 GRAD = {"q": "dq", "k": "dk", "v": "dv", "g": "dg", "beta": "dbeta", "b": "db", "w": "dw", "initial_state": "dh0"}
 CASES = [  # op, B, T, H, full saving
     ("kda", 2, 256, 12, False),       # B*H = 24: paired, 32-wide, kg read by the scan
+    ("delta", 1, 512, 20, False),     # 20: paired, 32-wide
+    ("gdn2", 1, 256, 17, False),      # 17: paired, 32-wide
     ("gdn2", 1, 256, 33, False),      # 33: paired, 64-wide, qg / kg / w formed in both
     ("gdn", 1, 256, 33, False),       # 33: paired, 64-wide, Aqk in the state recurrence
     ("delta", 1, 256, 65, False),     # 65: one after the other
@@ -43,7 +45,8 @@ CASES = [  # op, B, T, H, full saving
     ("gdn2", 1, 576, 4, False),       # 4 heads, 9 chunks: affine-step
     ("gdn2", 1, 128, 1, False),       # one head, 2 chunks: paired, 16-wide
     ("gdn", 1, 2048, 12, False),      # 12 heads, 32 chunks: paired, 16-wide
-    ("delta", 1, 2112, 12, False),    # 12 heads, 33 chunks: affine-step
+    ("delta", 1, 2112, 12, False),    # 12 heads, 33 chunks: paired, 16-wide
+    ("delta", 1, 2112, 11, False),    # 11 heads, 33 chunks: affine-step
     ("delta", 8, 256, 16, False),     # 128: the fused sweep
     ("kda", 8, 256, 16, False),       # 128, vector gate
 ]

@@ -173,7 +173,7 @@ def test_side_by_side_rule():
 def test_paired_rule():
     """ops.paired_tile (recompute policy, vector gates: the direct state recurrence beside the
     direct forward scan): the narrowest of 32 / 64 at which each launch holds <= 128
-    work-groups, for 24 <= B*H <= 64."""
+    work-groups, for 17 <= B*H <= 64."""
     from rewy_amd import ops
     V, S = ops.GATE_VECTOR, ops.GATE_SCALAR
     assert ops.paired_tile(2, 32, 128, V) == 64          # GDN2 configs[3]
@@ -185,13 +185,15 @@ def test_paired_rule():
     assert ops.paired_tile(2, 32, 128, S) == 64 and ops.paired_tile(4, 16, 32, S) == 64   # before the fused sweep
     assert ops.paired_tile(2, 16, 32, S) == 32 and ops.paired_tile(1, 48, 64, ops.GATE_NONE) == 64
     assert ops.paired_tile(8, 16, 64, S) == 0
-    # B*H <= 16: 16-wide tiles on rows of <= 8 chunks, <= 32 from B*H = 12, <= 128 at 16
+    # B*H <= 16: 16-wide tiles on rows of <= 8 chunks, of <= 128 from B*H = 12
     assert ops.paired_tile(1, 16, 32, V) == 16 and ops.paired_tile(2, 8, 64, S) == 16
     assert ops.paired_tile(1, 16, 8, ops.GATE_NONE) == 16 and ops.paired_tile(1, 2, 4, ops.GATE_NONE) == 16
     assert ops.paired_tile(1, 16, 129, S) == 0 and ops.paired_tile(1, 15, 32, V) == 16
-    assert ops.paired_tile(1, 16, 128, V) == 16
-    assert ops.paired_tile(1, 12, 33, V) == 0 and ops.paired_tile(1, 8, 16, V) == 0
+    assert ops.paired_tile(1, 16, 128, V) == 16 and ops.paired_tile(1, 12, 128, V) == 16
+    assert ops.paired_tile(1, 12, 129, V) == 0 and ops.paired_tile(1, 8, 16, V) == 0
     assert ops.paired_tile(1, 4, 32, V) == 0 and ops.paired_tile(1, 1, 8, S) == 16
+    # 17 <= B*H < 24: 32-wide tiles
+    assert ops.paired_tile(1, 20, 32, V) == 32 and ops.paired_tile(1, 17, 1024, S) == 32
 
 
 def test_kernel_seams_validate_before_launch():
