@@ -17,7 +17,7 @@ When batch x heads is too small to fill the GPU and the sequence long, the two
 recurrences run instead in affine-step form (after ``fdr_prepare_wu``: w, u and qg, kg or Aqk) (``ops.recurrences``,
 ``fdr_affine_*``): chunk-parallel step matrices, one scan launch carrying both
 recurrences side by side, and a chunk-parallel pass for v_new and dR.
-With 17 <= batch x heads <= 64, and on short rows at batch x heads <= 16, the recompute policy
+With 17 <= batch x heads <= 127, and on short rows at batch x heads <= 16, the recompute policy
 runs the direct backward state recurrence and the direct forward scan side by side in one
 launch (``fdr_paired_recurrences``), at a value-tile width that gives each at most half the
 CUs (``ops.paired_tile``).

@@ -102,6 +102,10 @@ def side_by_side_pays(B, H, NT):
 # at most one work-group per CU.
 PAIRED = True
 PAIRED_MIN_BH = 17
+# ... at 64-wide tiles up to this many work-groups per launch: while one recurrence alone
+# leaves CUs idle the pair still wins, the second launch's work-groups taking the CUs the first
+# leaves (B*H = 72-124: 12-26 % faster); at B*H = 128 each fills the GPU (5 % slower paired)
+PAIRED_MAX_GROUPS = 254
 # ... and at 16-wide tiles for B*H <= 16 (at most 128 work-groups each) on short rows, where
 # the pair (one launch) beats the affine-step form and the direct recurrences one after the
 # other: rows of at most 8 chunks at any such B*H, of at most 128 from B*H = 12
@@ -133,9 +137,10 @@ PAIRED_FORMW = True
 
 def paired_tile(B, H, NT, gate_mode):
     """Value-tile width at which the recompute policy runs ``fwd_h`` and ``state_bwd`` (both
-    direct) side by side, or 0 when it runs them otherwise: for 17 <= B H <= 64, the
-    narrowest of 32 / 64 at which each launch has at most 128 work-groups (the two together
-    one per CU); for B H <= 16, 16-wide tiles on short rows (``PAIRED16_*``).  Measured (MI355X):
+    direct) side by side, or 0 when it runs them otherwise: 32-wide tiles for 17 <= B H <= 32
+    (at most 128 work-groups each, the two together one per CU), 64-wide ones up to B H = 127
+    (``PAIRED_MAX_GROUPS``), and for B H <= 16 16-wide tiles on short rows (``PAIRED16_*``).
+    Measured (MI355X):
     GDN2 B=2 T=8192 H=32 both recurrences 0.451 ms paired at
     64-wide tiles vs 0.544 one after the other at 32-wide; B=2 T=4096 H=16 0.177 (32-wide) vs
     0.231; B=1 T=8192 H=48 0.443 vs 0.543; B=1 T=16384 H=24 0.639 (32-wide) vs 0.905.  The
@@ -156,14 +161,18 @@ def paired_tile(B, H, NT, gate_mode):
     B H = 12, 64 chunks: DeltaNet 160 vs 204, KDA 187 vs 206; 128 chunks: GDN 358 vs 379, KDA 399 vs
     408.  B H = 17-23 at 32-wide tiles, against the recurrences one after the other: B=1 T=2048
     H=20 DeltaNet 118 vs 156 us, GDN 129 vs 179, KDA 136 vs 171, GDN2 153 vs 189; KDA T=4096 H=18
-    259 vs 320."""
+    259 vs 320.  B H = 65-127 at 64-wide tiles (up to 254 work-groups a launch), against the fused
+    sweep or the recurrences one after the other: B=1 T=2048 H=72 DeltaNet 327 vs 444 us, H=96 GDN
+    432 vs 555, H=112 KDA 570 vs 650, H=120 GDN2 645 vs 779, H=124 DeltaNet 464 vs 558; at B H = 128
+    (256 work-groups each) GDN B=8 T=4096 H=16 975 vs 928, KDA B=1 T=4096 H=128 1179 vs 1114."""
     BH = B * H
     if not PAIRED or NT < 1:
         return 0
     if BH >= PAIRED_MIN_BH:
-        for vb in (32, 64):
-            if BH * (V_SUPPORTED // vb) <= 128:
-                return vb
+        if BH * (V_SUPPORTED // 32) <= 128:
+            return 32
+        if BH * (V_SUPPORTED // 64) <= PAIRED_MAX_GROUPS:
+            return 64
         return 0
     if BH * (V_SUPPORTED // 16) <= 128 and (NT <= PAIRED16_SHORT_NT or (BH >= PAIRED16_MID_BH and NT <= PAIRED16_MID_NT)):
         return 16

@@ -1,5 +1,4 @@
-"""The recompute policy's paired direct recurrences (B*H >= 17 where the fused sweep does not
-pay, and B*H <= 16 on short rows): the direct backward state recurrence
+"""The recompute policy's paired direct recurrences (17 <= B*H <= 127, and B*H <= 16 on short rows): the direct backward state recurrence
 (fdr_state_bwd) on the current stream beside the direct forward scan (fdr_fwd_h) on a second stream, both at the value-tile width
 ``ops.paired_tile`` picks (32 at B*H = 32, 64 at B*H = 48, 16 at B*H = 16 with few chunks).  For all four families (the
 scalar / no-gate ones with the state recurrence forming Aqk itself):

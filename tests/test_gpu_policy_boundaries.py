@@ -2,10 +2,9 @@
 
 ``backends.backward`` picks, by batch x heads and chunk count, among the affine-step
 recurrences (few heads), the forward scan beside the segmented state recurrence (few heads,
-long rows), the paired direct recurrences at 32- or 64-wide tiles (17 <= B*H <= 64, with the
-vector gates' in-kernel qg / kg / w at 64-wide tiles) or 16-wide ones (B*H <= 16 on short
-rows), and the fused forward sweep or the
-plain direct recurrences (B*H >= 65).  One case on each side of each switch, odd head counts
+long rows), the paired direct recurrences at 32-wide tiles (17 <= B*H <= 32), 64-wide ones
+(up to B*H = 127, with the vector gates' in-kernel qg / kg / w) or 16-wide ones (B*H <= 16 on
+short rows), and the fused forward sweep or the plain direct recurrences (B*H >= 128).  One case on each side of each switch, odd head counts
 included, every family, both KDA policies: every (batch row, head) pair is independent end to
 end, so two heads of each batch (the first and the last) are checked against the oracle run
 on that head alone, at the reference's acceptance tolerances (validation.py:40-45, :68).  The
@@ -26,8 +25,10 @@ CASES = [  # op, B, T, H, full saving
     ("gdn2", 1, 256, 17, False),      # 17: paired, 32-wide
     ("gdn2", 1, 256, 33, False),      # 33: paired, 64-wide, qg / kg / w formed in both
     ("gdn", 1, 256, 33, False),       # 33: paired, 64-wide, Aqk in the state recurrence
-    ("delta", 1, 256, 65, False),     # 65: one after the other
-    ("kda", 1, 256, 65, False),       # 65: the fused sweep or the direct pair, vector gate
+    ("delta", 1, 256, 65, False),     # 65: paired, 64-wide (130 work-groups a launch)
+    ("kda", 1, 256, 65, False),       # 65: paired, 64-wide, vector gate
+    ("gdn", 1, 256, 127, False),      # 127: paired, 64-wide (254 work-groups a launch)
+    ("gdn2", 2, 256, 64, False),      # 128: one after the other
     ("gdn2", 4, 256, 16, False),      # 64: paired, 64-wide, prepare-free
     ("kda", 4, 256, 16, True),        # full saving at 64
     ("kda", 1, 1024, 4, True),        # full saving, 4 heads, 16 chunks: the direct state recurrence

@@ -173,15 +173,16 @@ def test_side_by_side_rule():
 def test_paired_rule():
     """ops.paired_tile (recompute policy, vector gates: the direct state recurrence beside the
     direct forward scan): the narrowest of 32 / 64 at which each launch holds <= 128
-    work-groups, for 17 <= B*H <= 64."""
+    work-groups (17 <= B*H <= 32), 64-wide ones to B*H = 127, narrow rows at B*H <= 16."""
     from rewy_amd import ops
     V, S = ops.GATE_VECTOR, ops.GATE_SCALAR
     assert ops.paired_tile(2, 32, 128, V) == 64          # GDN2 configs[3]
     assert ops.paired_tile(2, 16, 64, V) == 32 and ops.paired_tile(1, 24, 256, V) == 32
     assert ops.paired_tile(1, 48, 128, V) == 64
     assert ops.paired_tile(1, 16, 512, V) == 0           # few heads, long rows: the side-by-side form
-    assert ops.paired_tile(8, 16, 64, V) == 0            # the fused sweep fills the GPU
-    assert ops.paired_tile(1, 96, 64, V) == 0            # 64-wide tiles would need 192 CUs each
+    assert ops.paired_tile(8, 16, 64, V) == 0            # B*H = 128: one after the other
+    assert ops.paired_tile(1, 96, 64, V) == 64 and ops.paired_tile(1, 127, 64, S) == 64   # launches < 256 groups
+    assert ops.paired_tile(1, 128, 64, V) == 0           # each recurrence fills the GPU
     assert ops.paired_tile(2, 32, 128, S) == 64 and ops.paired_tile(4, 16, 32, S) == 64   # before the fused sweep
     assert ops.paired_tile(2, 16, 32, S) == 32 and ops.paired_tile(1, 48, 64, ops.GATE_NONE) == 64
     assert ops.paired_tile(8, 16, 64, S) == 0
