@@ -1,6 +1,7 @@
-"""The recompute policy's paired direct recurrences (17 <= B*H <= 127, and B*H <= 16 on short rows): the direct backward state recurrence
-(fdr_state_bwd) on the current stream beside the direct forward scan (fdr_fwd_h) on a second stream, both at the value-tile width
-``ops.paired_tile`` picks (32 at B*H = 32, 64 at B*H = 48, 16 at B*H = 16 with few chunks).  For all four families (the
+"""The recompute policy's paired direct recurrences (17 <= B*H <= 127, and B*H <= 16 on short
+rows): the direct backward state recurrence and the direct forward scan side by side in one
+launch (fdr_paired_recurrences), at the value-tile width ``ops.paired_tile`` picks (32 at
+B*H = 32, 64 at B*H = 48, 16 at B*H = 16 with few chunks).  For all four families (the
 scalar / no-gate ones with the state recurrence forming Aqk itself):
 
 * the public autograd backward (recompute policy) against the fp64 oracle at the
