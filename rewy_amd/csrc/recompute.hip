@@ -634,11 +634,14 @@ extern "C" hipError_t fdr_prepare_wu_varlen(const void* q, const void* k, const 
                           qk_heads, scale, stream, cu_seqlens, chunk_indices);
 }
 
+// Value-tile width of the forward scans: as the state recurrence's (the narrowest tile with at
+// most 256 work-groups, 64 beyond); measured alike for fdr_fwd_h and fdr_fwd_h_wy (B*H = 96,
+// T = 4096: fwd_h_wy 327 us at 64-wide vs 524 at 32-wide; B*H = 48: 266 at 32-wide vs 446 at 16).
 static int fwd_default_bv(int B, int H) {
   const int bh = B * H;
-  if (bh * 2 >= 256) return 64;
-  if (bh * 4 >= 256) return 32;
-  return 16;
+  if (bh * 8 <= 256) return 16;
+  if (bh * 4 <= 256) return 32;
+  return 64;
 }
 
 // B rows of T tokens, or (co) B sequences packed along T tokens on 64-token boundaries,

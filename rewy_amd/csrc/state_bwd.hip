@@ -377,13 +377,17 @@ static hipError_t launch_segmented(const void* q, const void* k, const void* w, 
 
 using namespace rewy;
 
-// Value-tile width chosen so that the grid fills the chip: the recurrence is
-// sequential over chunks, so parallelism is B*H*(V/BV) work-groups.
+// Value-tile width: the narrowest at which one launch holds at most 256 work-groups (one
+// round on the CUs; a second round doubles the step chain), 64 beyond.  Measured (KDA state
+// recurrence, T = 4096): B*H <= 32 16-wide fastest (the shortest step chain), 33-64 32-wide
+// (BH = 48: 160 us vs 248 at 16-wide), from 65 64-wide even with CUs left idle (BH = 72: 213 us vs
+// 280 at 32-wide; BH = 200: 445 vs 580): a wider tile shares each chunk's qg / kg / w loads over
+// more value columns.
 static int default_bv(int B, int H) {
   const int bh = B * H;
-  if (bh * 2 >= 256) return 64;
-  if (bh * 4 >= 256) return 32;
-  return 16;
+  if (bh * 8 <= 256) return 16;
+  if (bh * 4 <= 256) return 32;
+  return 64;
 }
 
 // B rows of T tokens, (chunk_off) B sequences packed along T tokens on 64-token boundaries,

@@ -975,13 +975,21 @@ def paired_recurrences(q, k, w, g, gate_mode, dO, scale, v, Akk, value_block, aq
     return (dh, dr, dh0), (h, vnew, None)
 
 
+def default_tile(N, H):
+    """Value-tile width the recurrence kernels take by default for N rows of H heads (the C
+    library's rule): the narrowest of 16 / 32 at which one launch holds at most 256 work-groups,
+    64 beyond."""
+    BH = N * H
+    return 16 if BH * 8 <= 256 else 32 if BH * 4 <= 256 else 64
+
+
 def fwd_h_wy_pays(N, H, gate_mode, varlen=None):
     """Whether ``fwd_h_wy`` beats ``prepare_wu`` + ``fwd_h`` for N rows (sequences) of H heads.
     Each value-tile work-group forms the whole w (and, for a vector gate, every qg / kg / E
-    exponential) of its chunk, so that work is repeated once per value tile of a head.  The
-    default tiles are 64 wide from 2 N H >= 256 work-groups, 32 wide from 4 N H >= 256, else
-    16 wide.  Measured: at 64-wide tiles the sweep wins for every family; at 32-wide ones the
-    scalar / no-gate families still win and the vector gates lose; at 16-wide ones all lose.
+    exponential) of its chunk, so that work is repeated once per value tile of a head (tile
+    widths: ``default_tile``).  Measured: at 64-wide tiles the sweep wins for every family; at
+    32-wide ones the scalar / no-gate families still win and the vector gates lose; at 16-wide
+    ones all lose.
     A packed batch (``varlen``) scans for as long as its longest sequence, which then carries
     the sweep's extra work on every one of its chunks while the pair's ``prepare_wu`` spreads
     it over all chunks: it takes the sweep only when its sequences are near one length
@@ -990,8 +998,8 @@ def fwd_h_wy_pays(N, H, gate_mode, varlen=None):
     if varlen is not None and varlen.max_chunks * varlen.N > 1.5 * varlen.NC:
         return False
     if gate_mode == GATE_VECTOR:
-        return 2 * N * H >= 256
-    return 4 * N * H >= 256
+        return default_tile(N, H) == 64
+    return default_tile(N, H) >= 32
 
 
 def fwd_h_wy(k, v, Akk, g, gate_mode, beta=None, q=None, b=None, w=None, h0=None, want_final=False,
