@@ -88,3 +88,17 @@ def test_check_baseline_detects_stale_library(tmp_path, monkeypatch):
     with pytest.raises(RuntimeError):
         runtime.check_baseline()
     runtime.check_baseline.cache_clear()
+
+
+def test_per_family_compat_modules():
+    """The reference's per-family import paths (src/fast_delta_rule/_compat/{kda,gdn,gdn2,delta}.py)
+    resolve to the optimized operators, with the reference's names."""
+    import inspect
+    from rewy_amd._compat import delta, gdn, gdn2, kda
+    for fn, name, first in ((kda.chunk_kda, "chunk_kda", ["q", "k", "v", "g", "beta"]),
+                            (gdn.chunk_gated_delta_rule, "chunk_gated_delta_rule", ["q", "k", "v", "g", "beta"]),
+                            (gdn.chunk_gdn, "chunk_gated_delta_rule", ["q", "k", "v", "g", "beta"]),
+                            (gdn2.chunk_gdn2, "chunk_gdn2", ["q", "k", "v", "g", "b", "w"]),
+                            (delta.chunk_delta_rule, "chunk_delta_rule", ["q", "k", "v", "beta"])):
+        assert fn.__name__ == name
+        assert list(inspect.signature(fn).parameters)[:len(first)] == first
