@@ -343,6 +343,31 @@ hipError_t fdr_paired_recurrences(const void* q, const void* k, const void* w, c
                                   hipStream_t stream);
 
 /*
+ * The recompute-policy backward of GDN (gate_mode 1) and DeltaNet (gate_mode 0) as one call:
+ * fdr_prepare_wu (w; Aqk too when aqk_in_prepare != 0), fdr_paired_recurrences (value_block
+ * 16, 32 or 64; the state recurrence forms Aqk itself when aqk_in_prepare == 0) and
+ * fdr_chunk_bwd, enqueued on `stream` in that order -- the reference's _scalar backward,
+ * backends/backward.py:96-131 (FLA recompute_w_u_fwd, chunk_gated_delta_rule_fwd_h,
+ * chunk_gated_delta_rule_bwd_dhu, then the chunk stage), with the same bits as the three
+ * entry points called one by one.  This build's own composition (no single counterpart in the
+ * reference): for small batches, where the host time of three calls exceeds the kernels'.
+ * Inputs as those entry points take them (q / k with qk_heads heads, g fp32 [B,T,H] or NULL
+ * for gate_mode 0, beta fp32 [B,T,H], Akk fp32 [B,T,H,64], dht / h0 fp32 or NULL);
+ * outputs dq, dk, dv bf16 [B,T,H,K|V] per value head, dg (gate_mode 1), dbeta, dh0 (may be
+ * NULL) as fdr_chunk_bwd / fdr_state_bwd write them.  workspace: device memory, 256-byte
+ * aligned, of at least fdr_scalar_bwd_workspace_bytes(B, T, H, K, V, chunk) bytes, holding
+ * w, Aqk, dh, dR, h and v_new; two calls in flight at once need two workspaces.  Every
+ * argument rule is checked before the first launch: a rejected call launches nothing.
+ */
+size_t fdr_scalar_bwd_workspace_bytes(int B, int T, int H, int K, int V, int chunk);
+hipError_t fdr_scalar_bwd(const void* q, const void* k, const void* v, const float* g, int gate_mode,
+                          const float* beta, const float* Akk, const void* dO, const float* dht, const float* h0,
+                          void* dq, void* dk, void* dv, float* dg, float* dbeta, float* dh0, void* workspace,
+                          size_t workspace_bytes, float beta_sigmoid, int aqk_in_prepare, int state_v_first, int B,
+                          int T, int H, int qk_heads, int K, int V, int chunk, float scale, int value_block,
+                          hipStream_t stream);
+
+/*
  * The recompute pair fdr_prepare_wu + fdr_fwd_h in one sweep.  Replaces FLA
  * recompute_w_u_fwd(k, v, beta, A, g) -> (w, u) [, qg, kg] followed by
  * chunk_gated_delta_rule_fwd_h(k, w, u, g, initial_state) -> (h, v_new, final), as called at

@@ -27,6 +27,7 @@ SIGNATURES = {
     "fdr_fwd_h": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P],
     "fdr_fwd_h_u": [_P] * 5 + [_I] + [_P] * 8 + [_I] * 9 + [_P],
     "fdr_paired_recurrences": [_P] * 6 + [_I] + [_P] * 15 + [_I] * 9 + [_F, _I, _P],
+    "fdr_scalar_bwd": [_P] * 4 + [_I] + [_P] * 12 + [ctypes.c_size_t, _F] + [_I] * 9 + [_F, _I, _P],
     "fdr_state_bwd_varlen": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
                              _I, _P],
     "fdr_fwd_h_varlen": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
@@ -116,6 +117,8 @@ def load():
         lib.fdr_state_bwd_segmented_workspace_bytes.restype = ctypes.c_size_t
         lib.fdr_chunk_bwd_gate_workspace_bytes.argtypes = [_I, _I, _I]
         lib.fdr_chunk_bwd_gate_workspace_bytes.restype = ctypes.c_size_t
+        lib.fdr_scalar_bwd_workspace_bytes.argtypes = [_I] * 6
+        lib.fdr_scalar_bwd_workspace_bytes.restype = ctypes.c_size_t
         _lib = lib
     return _lib
 

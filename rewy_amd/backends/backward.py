@@ -317,6 +317,14 @@ def _scalar(op, q, k, v, beta, A, scale, initial_state, do, dht, g, beta_sigmoid
     # chip), else by fdr_prepare_wu without Aqk
     inline = vb > 0 or (not affine and (vl is not None or ops.state_form(q.shape[0], v.shape[2],
                                                                           q.shape[1] // ops.CHUNK) == "direct"))
+    if vb and ops.PAIRED_U and ops.PAIRED_ONE_LAUNCH and ops.SCALAR_ONE_CALL:
+        # the paired form below as one library call (fdr_scalar_bwd: the same launches, the same
+        # bits, a third of the host time)
+        out, dh0 = ops.scalar_bwd(q, k, v, g, gate, beta, A, do, scale, vb, vb <= ops.PAIRED_AQK_MAX_VB,
+                                  dht=_f32(dht), h0=_f32(initial_state), want_dh0=initial_state is not None,
+                                  beta_sigmoid=beta_sigmoid, state_v_first=state_v_first)
+        record(op, "optimized_backward")
+        return _group_sum(out, q.shape[2]), dh0
     if inline:
         pre = None
         if not vb and ops.fwd_h_wy_pays(q.shape[0] if vl is None else vl.N, v.shape[2], gate, vl):

@@ -123,6 +123,9 @@ PAIRED_ONE_LAUNCH = True
 PAIRED_AQK_MAX_VB = 32
 # ... with u formed inside the scan (fwd_h_u) instead of written by prepare_wu and read back
 PAIRED_U = True
+# ... and, for GDN / DeltaNet, prepare + paired recurrences + chunk stage as one library call
+# (fdr_scalar_bwd: the same launches and bits, one workspace allocation for the intermediates)
+SCALAR_ONE_CALL = True
 # ... and, vector gates at 64-wide tiles, with qg / kg formed from the raw q / k where each
 # recurrence stages a chunk (fdr_state_bwd_raw_qk, fwd_h_u) instead of written by prepare_wu and
 # read back.  (At 32-wide tiles every one of a head's four value tiles would form them again:
@@ -973,6 +976,51 @@ def paired_recurrences(q, k, w, g, gate_mode, dO, scale, v, Akk, value_block, aq
         CHUNK, float(scale), int(value_block), _lib.stream_handle(dev))
     _lib.check(st, "fdr_paired_recurrences")
     return (dh, dr, dh0), (h, vnew, None)
+
+
+def scalar_bwd(q, k, v, g, gate_mode, beta, Akk, dO, scale, value_block, aqk_in_prepare, dht=None, h0=None,
+               want_dh0=True, beta_sigmoid=0.0, state_v_first=False):
+    """GDN / DeltaNet recompute-policy backward in one library call (fdr_scalar_bwd):
+    ``prepare_wu`` (w, and Aqk with ``aqk_in_prepare``), ``paired_recurrences`` at
+    ``value_block`` and ``chunk_bwd``, with the same bits as those three calls and one
+    allocation for the six intermediates (w, Aqk, dh, dR, h, v_new) instead of six.  Dense rows.
+    Returns (dict(dq, dk, dv [per value head], dg | None, dbeta, db=None, dw=None), dh0 | None)."""
+    B, T, HQ, K = _dims(q)
+    H = v.shape[2]
+    V = V_SUPPORTED
+    dev = q.device
+    bf, f32 = torch.bfloat16, torch.float32
+    if gate_mode not in (GATE_SCALAR, GATE_NONE):
+        raise ValueError("scalar_bwd: gate_mode 0 or 1")
+    if H % HQ:
+        raise ValueError("value heads must be a multiple of q / k heads")
+    _need(q, "q", bf, (B, T, HQ, K), dev)
+    _need(k, "k", bf, (B, T, HQ, K), dev)
+    _need(v, "v", bf, (B, T, H, V), dev)
+    _need(dO, "dO", bf, (B, T, H, V), dev)
+    _need(beta, "beta", f32, (B, T, H), dev)
+    _need(Akk, "Akk", f32, (B, T, H, CHUNK), dev)
+    if gate_mode == GATE_SCALAR:
+        _need(g, "g", f32, (B, T, H), dev)
+    if dht is not None:
+        _need(dht, "dht", f32, (B, H, K, V), dev)
+    if h0 is not None:
+        _need(h0, "h0", f32, (B, H, K, V), dev)
+    lib = _lib.load()
+    ws = torch.empty(lib.fdr_scalar_bwd_workspace_bytes(B, T, H, K, V, CHUNK), device=dev, dtype=torch.uint8)
+    out = dict(dq=torch.empty(B, T, H, K, device=dev, dtype=bf), dk=torch.empty(B, T, H, K, device=dev, dtype=bf),
+               dv=torch.empty(B, T, H, V, device=dev, dtype=bf),
+               dg=torch.empty(B, T, H, device=dev, dtype=f32) if gate_mode == GATE_SCALAR else None,
+               dbeta=torch.empty(B, T, H, device=dev, dtype=f32), db=None, dw=None)
+    dh0 = torch.empty(B, H, K, V, device=dev, dtype=f32) if want_dh0 else None
+    P = _lib.ptr
+    st = lib.fdr_scalar_bwd(P(q), P(k), P(v), P(g), int(gate_mode), P(beta), P(Akk), P(dO), P(dht), P(h0),
+                            P(out["dq"]), P(out["dk"]), P(out["dv"]), P(out["dg"]), P(out["dbeta"]), P(dh0), P(ws),
+                            ws.numel(), float(beta_sigmoid or 0.0), int(bool(aqk_in_prepare)),
+                            int(bool(state_v_first)), B, T, H, HQ, K, V, CHUNK, float(scale), int(value_block),
+                            _lib.stream_handle(dev))
+    _lib.check(st, "fdr_scalar_bwd")
+    return out, dh0
 
 
 def default_tile(N, H):

@@ -6,7 +6,9 @@ scalar / no-gate ones with the state recurrence forming Aqk itself):
 
 * the public autograd backward (recompute policy) against the fp64 oracle at the
   reference's acceptance tolerances (validation.py:40-45, :68);
-* the same gradients, bit for bit, whether the two recurrences run as one launch
+* the same gradients, bit for bit, whether GDN / DeltaNet's three launches are made by one
+  library call (fdr_scalar_bwd, ``ops.SCALAR_ONE_CALL``) or one by one, whether the two
+  recurrences run as one launch
   (fdr_paired_recurrences, ``ops.PAIRED_ONE_LAUNCH``) or as two launches on two streams, as
   the same launches enqueued on one stream, as the two
   recurrences reading the w (``ops.PAIRED_FORMW`` off, GDN2) and the qg / kg (``ops.PAIRED_RAW``
@@ -34,13 +36,15 @@ SHAPES = [(2, 512, 16, 32), (1, 256, 48, 64), (1, 512, 16, 16)]    # B, T, H, th
 
 
 def _count_pairs(monkeypatch):
-    """Count the paired recurrences: one launch (ops.paired_recurrences) or two streams."""
+    """Count the paired recurrences: one launch (ops.paired_recurrences, or inside the one-call
+    GDN / DeltaNet backward ops.scalar_bwd) or two streams."""
     from rewy_amd import ops
     from rewy_amd.backends import backward as bw
     calls = []
-    real_sbs, real_one = bw._side_by_side, ops.paired_recurrences
+    real_sbs, real_one, real_scalar = bw._side_by_side, ops.paired_recurrences, ops.scalar_bwd
     monkeypatch.setattr(bw, "_side_by_side", lambda a, b: (calls.append("streams"), real_sbs(a, b))[1])
     monkeypatch.setattr(ops, "paired_recurrences", lambda *a, **k: (calls.append("one"), real_one(*a, **k))[1])
+    monkeypatch.setattr(ops, "scalar_bwd", lambda *a, **k: (calls.append("one"), real_scalar(*a, **k))[1])
     return calls
 
 
@@ -110,6 +114,13 @@ def test_paired_equals_one_stream_and_policy_off(op, B, T, H, vb, monkeypatch):
     print(f"\n[paired-streams] op={op} B={B} T={T} H={H}", flush=True)
     run = _seam(op, B, T, H)
     got = [x.clone() for x in run()]
+    # GDN / DeltaNet: the one-call backward (fdr_scalar_bwd) against its three launches made
+    # one by one (fdr_prepare_wu, fdr_paired_recurrences, fdr_chunk_bwd)
+    monkeypatch.setattr(ops, "SCALAR_ONE_CALL", False)
+    three = run()
+    torch.cuda.synchronize()
+    for i, (a, r) in enumerate(zip(got, three)):
+        assert torch.equal(a, r), (op, "SCALAR_ONE_CALL", i)
     # the two recurrences as two launches on two streams (fdr_state_bwd*, fdr_fwd_h_u)
     monkeypatch.setattr(ops, "PAIRED_ONE_LAUNCH", False)
     two = run()

@@ -134,3 +134,43 @@ def test_argument_rules():
     args[-2] = 32
     args[22] = 1                                           # raw_qk at 32-wide tiles
     assert lib.fdr_paired_recurrences(*args) != 0
+
+
+@pytest.mark.parametrize("vb", [16, 32, 64])
+@pytest.mark.parametrize("op,HQ", [("gdn", 3), ("delta", 3), ("gdn", 1)])
+def test_one_call_scalar_backward_equals_its_three_launches(op, HQ, vb):
+    """fdr_scalar_bwd (ops.scalar_bwd) against fdr_prepare_wu, fdr_paired_recurrences and
+    fdr_chunk_bwd called one by one, bit for bit: Aqk written by prepare or formed by the state
+    recurrence, V-first states, with and without the initial / final states, beta_sigmoid."""
+    from rewy_amd import ops
+    B, T, H = 2, 320, 3
+    print(f"\n[scalar one call] op={op} HQ={HQ} value_block={vb}", flush=True)
+    d = _inputs(op, B, T, H, HQ, 83)
+    gate = GATE[op]
+    for aqk_pre in (False, True):
+        for vf in (False, True):
+            for with_states, sig in ((True, 0.0), (False, 2.0)):
+                h0 = d["initial_state"] if with_states else None
+                if h0 is not None and vf:
+                    h0 = h0.transpose(-1, -2).contiguous()
+                dht = (d["dht"].transpose(-1, -2).contiguous() if vf else d["dht"]) if with_states else None
+                tag = (op, HQ, vb, aqk_pre, vf, with_states)
+                pre = ops.prepare_wu(d["k"], d["v"], d["Akk"], gate, g=d["gc"], beta=d["beta"], q=d["q"],
+                                     want_aqk=aqk_pre, scale=0.088, want_u=False)
+                (dh, dr, dh0), (h, v_new, _) = ops.paired_recurrences(
+                    d["q"], d["k"], pre["w"], d["gc"], gate, d["dO"], 0.088, d["v"], d["Akk"], vb, aqk=pre.get("Aqk"),
+                    beta=d["beta"], h0=h0, dht=dht, want_dh0=with_states, state_v_first=vf)
+                ref = ops.chunk_bwd(d["q"], d["k"], d["v"], v_new, d["dO"], dr, d["gc"], gate, d["Akk"], h, dh, 0.088,
+                                    beta=d["beta"], beta_sigmoid=sig)
+                got, gdh0 = ops.scalar_bwd(d["q"], d["k"], d["v"], d["gc"], gate, d["beta"], d["Akk"], d["dO"], 0.088,
+                                           vb, aqk_pre, dht=dht, h0=h0, want_dh0=with_states, beta_sigmoid=sig,
+                                           state_v_first=vf)
+                torch.cuda.synchronize()
+                for n in ("dq", "dk", "dv", "dg", "dbeta"):
+                    if ref[n] is None:
+                        assert got[n] is None, (tag, n)
+                        continue
+                    assert torch.equal(got[n], ref[n]), (tag, n, float((got[n].double() - ref[n].double()).abs().max()))
+                assert (gdh0 is None) == (dh0 is None), tag
+                if dh0 is not None:
+                    assert torch.equal(gdh0, dh0), (tag, "dh0")

@@ -121,6 +121,8 @@ def _header_params():
                 kinds.append("F")
             elif prm.startswith("long long"):
                 kinds.append("L")
+            elif prm.startswith("size_t"):
+                kinds.append("Z")
             elif prm.startswith("int"):
                 kinds.append("I")
             else:
@@ -132,7 +134,7 @@ def _header_params():
 def test_ctypes_signatures_match_the_header_parameter_by_parameter():
     import ctypes
     from rewy_amd import _lib
-    kind = {ctypes.c_void_p: "P", ctypes.c_int: "I", ctypes.c_float: "F", ctypes.c_longlong: "L"}
+    kind = {ctypes.c_void_p: "P", ctypes.c_int: "I", ctypes.c_float: "F", ctypes.c_longlong: "L", ctypes.c_size_t: "Z"}
     for name, params in _header_params().items():
         got = [kind[t] for t in _lib.SIGNATURES[name]]
         assert got == params, (name, "".join(got), "".join(params))
@@ -270,6 +272,26 @@ def test_seam_and_pairing_entry_points_reject_bad_arguments_without_touching_the
     assert paired(gate=1, kg=None, w=None) == HIP_ERROR_INVALID_VALUE   # scalar gate: w required
     assert paired(gate=1, kg=None, raw=1) == HIP_ERROR_INVALID_VALUE    # scalar gate: no raw_qk
     assert paired(gate=1, w_gate=fake) == HIP_ERROR_INVALID_VALUE       # w_gate only with the vector gate
+    # fdr_scalar_bwd (q, k, v, g, gate, beta, Akk, dO, dht, h0, dq, dk, dv, dg, dbeta, dh0, workspace,
+    # workspace_bytes, beta_sigmoid, aqk_in_prepare, vf, B, T, H, qk_heads, K, V, chunk, scale, value_block, stream)
+    need = lib.fdr_scalar_bwd_workspace_bytes(1, 128, 2, 128, 128, 64)
+    assert need == 65536 + 65536 + 131072 + 65536 + 131072 + 65536     # w, Aqk, dh, dR, h, v_new
+    assert lib.fdr_scalar_bwd_workspace_bytes(1, 100, 2, 128, 128, 64) == 0
+
+    def scalar(gate=1, g=fake, dg=fake, ws=fake, nbytes=need, sig=0.0, vb=32, T=128, HQ=2):
+        return lib.fdr_scalar_bwd(fake, fake, fake, g, gate, fake, fake, fake, None, None, fake, fake, fake, dg, fake,
+                                  None, ws, nbytes, sig, 1, 0, 1, T, 2, HQ, 128, 128, 64, 1.0, vb, None)
+    assert scalar(gate=2) == HIP_ERROR_INVALID_VALUE                     # GDN / DeltaNet only
+    assert scalar(g=None) == HIP_ERROR_INVALID_VALUE                     # GDN: g required ...
+    assert scalar(gate=0) == HIP_ERROR_INVALID_VALUE                     # ... DeltaNet: none
+    assert scalar(dg=None) == HIP_ERROR_INVALID_VALUE                    # GDN: dg required
+    assert scalar(vb=48) == HIP_ERROR_INVALID_VALUE                      # tile width
+    assert scalar(T=100) == HIP_ERROR_INVALID_VALUE                      # T not whole chunks
+    assert scalar(HQ=3) == HIP_ERROR_INVALID_VALUE                       # q / k heads do not divide H
+    assert scalar(sig=-1.0) == HIP_ERROR_INVALID_VALUE                   # beta_sigmoid >= 0
+    assert scalar(nbytes=need - 1) == HIP_ERROR_INVALID_VALUE            # workspace too small
+    assert scalar(ws=ctypes.c_void_p(320)) == HIP_ERROR_INVALID_VALUE    # workspace not 256-byte aligned
+    assert scalar(ws=None) == HIP_ERROR_INVALID_VALUE
     assert lib.fdr_group_sum(None, None, 16, 2, 2, 64, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fdr_group_sum(None, None, 0, 2, 2, 128, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fdr_gdn2_chunk_bwd_wy(*([None] * 19), 0, 1, 128, 1, 64, 128, 64, 1.0, None) == HIP_ERROR_INVALID_VALUE
