@@ -52,6 +52,16 @@ AFFINE_VALUE_BLOCK = 16
 SEG_MIN_CHUNKS = 256
 SEG_TARGET_GROUPS = 512
 SEG_MIN_LEN = 16
+# ... and from fewer chunks at B*H < 32 (the state recurrence alone, KDA gate, graph replay, us,
+# direct / segmented / affine-step): B*H = 24 96 chunks 197 / 180 / 225, 192 chunks 401 / 338 /
+# 443, 64 chunks 114 / 134 / 149; B*H = 16 96 chunks 157 / 136 / 166, 192 chunks 375 / 229 / 350,
+# 64 chunks 108 / 113 / 104; B*H = 8 128 chunks 203 / 128 / 138, 96 chunks 155 / 117 / 102;
+# B*H = 4 192 chunks 303 / 141 / 160, 128 chunks 204 / 118 / 110; B*H = 32 128 chunks
+# 273 / 286 / 362, 192 chunks 412 / 414 / 546
+SEG_SHORT_MAX_BH = 32
+SEG_SHORT_MIN_CHUNKS = 96           # B*H >= 16
+SEG_NARROW_MIN_CHUNKS = 128         # B*H < 16, with B*H*NT >= SEG_NARROW_MIN_WORK
+SEG_NARROW_MIN_WORK = 768
 
 
 def segments_for(B, H, NT):
@@ -67,6 +77,9 @@ def _state_method(method, B, H, NT):
     if method != "auto":
         return method
     if NT >= SEG_MIN_CHUNKS and 2 * B * H < 256:
+        return "segmented"
+    if B * H < SEG_SHORT_MAX_BH and (NT >= SEG_SHORT_MIN_CHUNKS if B * H >= 16 else
+                                     NT >= SEG_NARROW_MIN_CHUNKS and B * H * NT >= SEG_NARROW_MIN_WORK):
         return "segmented"
     if B * H <= AFFINE_MAX_BH and NT >= AFFINE_STATE_MIN_CHUNKS:
         return "affine"

@@ -33,6 +33,13 @@ CASES = [  # op, B, T, H, full saving
     ("kda", 4, 256, 16, True),        # full saving at 64
     ("kda", 1, 1024, 4, True),        # full saving, 4 heads, 16 chunks: the direct state recurrence
     ("gdn2", 1, 1088, 4, True),       # full saving, 4 heads, 17 chunks: affine-step
+    ("kda", 1, 6144, 16, True),       # full saving, 16 heads, 96 chunks: segmented
+    ("kda", 1, 6080, 16, True),       # ... 95 chunks: affine-step
+    ("kda", 1, 6144, 24, True),       # full saving, 24 heads, 96 chunks: segmented
+    ("gdn2", 1, 6080, 24, True),      # ... 95 chunks: direct
+    ("kda", 1, 8192, 8, True),        # full saving, 8 heads, 128 chunks: segmented
+    ("gdn2", 1, 12288, 4, True),      # full saving, 4 heads, 192 chunks: segmented
+    ("kda", 1, 12224, 4, True),       # ... 191 chunks: affine-step
     ("gdn", 1, 1024, 8, False),       # 8 heads, 16 chunks
     ("kda", 1, 4096, 4, False),       # 4 heads, 64 chunks: affine-step or segmented
     ("gdn2", 1, 2048, 16, False),     # 16 heads, 32 chunks: paired, 16-wide

@@ -87,6 +87,13 @@ def test_state_recurrence_form_routing():
     assert ops._state_method("auto", 1, 4, 128) == "affine"           # the reference's grid, few chunks
     assert ops._state_method("auto", 1, 4, 17) == "affine"
     assert ops._state_method("auto", 1, 16, 16) == "direct"           # short rows: two launches fewer
+    # segmented from fewer chunks below B*H = 32: 96 from B*H = 16, else 128 with B*H*NT >= 768
+    assert ops._state_method("auto", 1, 16, 128) == "segmented"       # the grid's largest case
+    assert ops._state_method("auto", 1, 24, 96) == "segmented" and ops._state_method("auto", 1, 24, 95) == "direct"
+    assert ops._state_method("auto", 1, 16, 95) == "affine" and ops._state_method("auto", 1, 31, 96) == "segmented"
+    assert ops._state_method("auto", 1, 32, 192) == "direct"
+    assert ops._state_method("auto", 1, 8, 128) == "segmented" and ops._state_method("auto", 1, 8, 127) == "affine"
+    assert ops._state_method("auto", 1, 4, 192) == "segmented" and ops._state_method("auto", 1, 4, 191) == "affine"
     assert ops.segments_for(1, 16, 1024) == 8
     assert ops.segments_for(1, 1, 40) == 2                             # segments of >= 16 chunks
     assert ops._state_method("direct", 1, 16, 1024) == "direct"
