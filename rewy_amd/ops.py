@@ -50,6 +50,11 @@ AFFINE_VALUE_BLOCK = 16
 # work-groups leave most of the GPU idle.  Segments are sized so that the per-segment
 # maps fill the chip (P and Q tiles: 4 work-groups per segment-head at 64-wide tiles).
 SEG_MIN_CHUNKS = 256
+# ... up to this B*H (exclusive): from B*H = 48 the direct recurrence at its 64-wide default tiles
+# is faster however long the rows (KDA gate, graph replay, us, direct / segmented: B=1 T=16384
+# H=32 550 / 540, H=48 641 / 896, H=64 649 / 950, H=96 895 / 1746; T=32768 H=40 1254 / 1252,
+# H=80 1743 / 3434)
+SEG_MAX_BH = 48
 SEG_TARGET_GROUPS = 512
 SEG_MIN_LEN = 16
 # ... and from fewer chunks at B*H < 32 (the state recurrence alone, KDA gate, graph replay, us,
@@ -76,7 +81,7 @@ def _state_method(method, B, H, NT):
         raise ValueError('method must be "auto", "direct", "affine" or "segmented"')
     if method != "auto":
         return method
-    if NT >= SEG_MIN_CHUNKS and 2 * B * H < 256:
+    if NT >= SEG_MIN_CHUNKS and B * H < SEG_MAX_BH:
         return "segmented"
     if B * H < SEG_SHORT_MAX_BH and (NT >= SEG_SHORT_MIN_CHUNKS if B * H >= 16 else
                                      NT >= SEG_NARROW_MIN_CHUNKS and B * H * NT >= SEG_NARROW_MIN_WORK):

@@ -40,6 +40,8 @@ CASES = [  # op, B, T, H, full saving
     ("kda", 1, 8192, 8, True),        # full saving, 8 heads, 128 chunks: segmented
     ("gdn2", 1, 12288, 4, True),      # full saving, 4 heads, 192 chunks: segmented
     ("kda", 1, 12224, 4, True),       # ... 191 chunks: affine-step
+    ("gdn2", 1, 16384, 47, True),     # full saving, 47 heads, 256 chunks: segmented
+    ("kda", 1, 16384, 48, True),      # ... 48 heads: direct
     ("gdn", 1, 1024, 8, False),       # 8 heads, 16 chunks
     ("kda", 1, 4096, 4, False),       # 4 heads, 64 chunks: affine-step or segmented
     ("gdn2", 1, 2048, 16, False),     # 16 heads, 32 chunks: paired, 16-wide

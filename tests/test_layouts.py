@@ -92,6 +92,9 @@ def test_state_recurrence_form_routing():
     assert ops._state_method("auto", 1, 24, 96) == "segmented" and ops._state_method("auto", 1, 24, 95) == "direct"
     assert ops._state_method("auto", 1, 16, 95) == "affine" and ops._state_method("auto", 1, 31, 96) == "segmented"
     assert ops._state_method("auto", 1, 32, 192) == "direct"
+    # long rows: segmented below B*H = 48, direct from there
+    assert ops._state_method("auto", 1, 32, 256) == "segmented" and ops._state_method("auto", 1, 47, 512) == "segmented"
+    assert ops._state_method("auto", 1, 48, 256) == "direct" and ops._state_method("auto", 1, 96, 4096) == "direct"
     assert ops._state_method("auto", 1, 8, 128) == "segmented" and ops._state_method("auto", 1, 8, 127) == "affine"
     assert ops._state_method("auto", 1, 4, 192) == "segmented" and ops._state_method("auto", 1, 4, 191) == "affine"
     assert ops.segments_for(1, 16, 1024) == 8
